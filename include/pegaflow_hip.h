@@ -1,0 +1,335 @@
+/*
+ * pegaflow_hip.h — C ABI of the MI355X-native KV-block transfer path.
+ *
+ * This is the seam between an engine/worker layer (the role of
+ * pegaflow-core/src/lib.rs and gpu_worker.rs in the reference) and the
+ * transfer, pinned-memory and completion primitives (the role of
+ * pegaflow-core/src/transfer.rs, pinned_mem.rs and sync_state.rs).  Every
+ * declaration below names the reference interface it replaces.
+ *
+ * Conventions
+ *  - Every entry point returns an int status: PF_OK (0) or a PF_ERR_* code.
+ *    On failure a human-readable message is kept per thread and returned by
+ *    pf_last_error(); messages follow the reference's wording where the
+ *    reference has one (e.g. "Block 3 segment 1 exceeds registered memory").
+ *  - Device and host-mapped addresses are passed as uint64_t; host pointers as
+ *    void*.  No framework types cross this boundary.
+ *  - Device pointers passed in (layer tensors) are borrowed; the library owns
+ *    only the streams, events, staging buffers and pinned allocations it
+ *    creates.
+ *  - Entry points are reentrant.  A pf_xfer context serialises its own work on
+ *    its own streams; use one context per worker thread (the reference runs one
+ *    load thread and one save thread per device, gpu_worker.rs:61-93).
+ */
+#ifndef PEGAFLOW_HIP_H
+#define PEGAFLOW_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------------ */
+/* Status codes.  The engine-level codes mirror EngineError (lib.rs:58-85).   */
+/* ------------------------------------------------------------------------ */
+enum {
+  PF_OK = 0,
+  PF_ERR_INVALID_ARGUMENT = 1,  /* EngineError::InvalidArgument               */
+  PF_ERR_HIP = 2,               /* a HIP runtime call failed                   */
+  PF_ERR_STORAGE = 3,           /* EngineError::Storage (transfer/pool errors) */
+  PF_ERR_INSTANCE_MISSING = 4,  /* EngineError::InstanceMissing                */
+  PF_ERR_WORKER_MISSING = 5,    /* EngineError::WorkerMissing                  */
+  PF_ERR_TOPOLOGY_MISMATCH = 6, /* EngineError::TopologyMismatch               */
+  PF_ERR_INIT = 7,              /* EngineError::CudaInit                       */
+  PF_ERR_LOAD_STATE = 8,        /* LoadStateError (sync_state.rs:46-56)        */
+  PF_ERR_ZERO_SIZE = 9,         /* PinnedMemError::ZeroSize (pinned_mem.rs:72) */
+  PF_ERR_UNSUPPORTED = 10
+};
+
+/* Message of the last failed call on the calling thread ("" if none). */
+const char* pf_last_error(void);
+/* Library version string. */
+const char* pf_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* Layer layout.                                                              */
+/* Replaces KVCacheRegistration (pegaflow-core/src/lib.rs:100-112).           */
+/* ------------------------------------------------------------------------ */
+typedef struct pf_kv_layout {
+  uint64_t data_ptr;         /* device base address of the layer tensor     */
+  uint64_t size_bytes;       /* registered bytes starting at data_ptr       */
+  uint64_t num_blocks;       /* paged blocks in the layer                   */
+  uint64_t bytes_per_block;  /* bytes of one segment of one block           */
+  uint64_t block_size_bytes; /* bytes_per_block * segments                  */
+  uint64_t kv_stride_bytes;  /* distance between K and V segments (0 if 1)  */
+  uint64_t segments;         /* 2 for KV-first, 1 for blocks-first          */
+} pf_kv_layout;
+
+/* Fill *out from the register_context_layer arguments, with the reference's
+ * validation (lib.rs:389-449): zero sizes, missing stride, checked overflow of
+ * the last segment's end, and end > size_bytes are PF_ERR_INVALID_ARGUMENT. */
+int pf_layout_init(uint64_t data_ptr, uint64_t size_bytes, uint64_t num_blocks,
+                   uint64_t bytes_per_block, uint64_t kv_stride_bytes,
+                   uint64_t segments, pf_kv_layout* out);
+
+/* Replaces segment_offset (transfer.rs:18-47): block_idx*bytes_per_block +
+ * segment_idx*kv_stride_bytes, checked; error when segment_idx >= segments,
+ * on overflow, or when offset + bytes_per_block > size_bytes. */
+int pf_segment_offset(const pf_kv_layout* layout, uint64_t block_idx,
+                      uint64_t segment_idx, uint64_t* out_offset);
+
+/* Replaces is_contiguous_layout (transfer.rs:50-52): 1 when segments <= 1 or
+ * kv_stride_bytes == bytes_per_block, else 0. */
+int pf_is_contiguous_layout(const pf_kv_layout* layout);
+
+/* How a layer's blocks are moved, as dispatched in gpu_worker.rs:218-282 and
+ * 326-372: SPLIT = per-segment K list then V list (segments == 2 and
+ * kv_stride_bytes > bytes_per_block); CONTIGUOUS = one block_size_bytes chunk
+ * per block; STRIDED = any other multi-segment layout (save copies each
+ * segment to dst + s*bytes_per_block, load copies block_size_bytes from
+ * segment_offset(block, 0), exactly as the reference does). */
+enum { PF_LAYOUT_SPLIT = 0, PF_LAYOUT_CONTIGUOUS = 1, PF_LAYOUT_STRIDED = 2 };
+int pf_layout_kind(const pf_kv_layout* layout);
+
+/* ------------------------------------------------------------------------ */
+/* Device runtime: devices, streams, events, device memory.                   */
+/* Replaces CudaContext::new / new_stream / record_event / synchronize        */
+/* (gpu_worker.rs:146-150, 286-291; lib.rs:247).                              */
+/* ------------------------------------------------------------------------ */
+typedef void* pf_stream;
+typedef void* pf_event;
+
+int pf_get_device_count(int* count);
+/* hipSetDevice + once-per-device library init (wall-clock rate query).      */
+int pf_init(int device);
+int pf_set_device(int device);
+int pf_get_device(int* device);
+int pf_device_synchronize(void);
+
+/* Non-blocking stream at the default priority. */
+int pf_stream_create(pf_stream* out);
+int pf_stream_destroy(pf_stream stream);
+int pf_stream_synchronize(pf_stream stream);
+int pf_stream_wait_event(pf_stream stream, pf_event event);
+
+/* Timing-capable event. */
+int pf_event_create(pf_event* out);
+int pf_event_destroy(pf_event event);
+int pf_event_record(pf_event event, pf_stream stream);
+int pf_event_synchronize(pf_event event);
+/* *done = 1 when the event has completed, 0 when still pending. */
+int pf_event_query(pf_event event, int* done);
+int pf_event_elapsed_ms(pf_event start, pf_event end, float* ms);
+
+int pf_device_malloc(uint64_t size, uint64_t* out_dev_ptr);
+int pf_device_free(uint64_t dev_ptr);
+int pf_memcpy_h2d(uint64_t dst_dev, const void* src, uint64_t size);
+int pf_memcpy_d2h(void* dst, uint64_t src_dev, uint64_t size);
+int pf_memcpy_d2d(uint64_t dst_dev, uint64_t src_dev, uint64_t size);
+int pf_memset_d8(uint64_t dst_dev, uint8_t value, uint64_t size);
+/* Free and total device memory in bytes. */
+int pf_mem_get_info(uint64_t* free_bytes, uint64_t* total_bytes);
+
+/* ------------------------------------------------------------------------ */
+/* Pinned host memory.                                                        */
+/* Replaces PinnedMemory::{allocate, allocate_hugepages} and Drop              */
+/* (pinned_mem.rs:128-266).  Backed by hipHostMalloc and always mapped for     */
+/* device access, so the transfer kernels can read and write it directly.     */
+/* ------------------------------------------------------------------------ */
+enum {
+  PF_PINNED_DEFAULT = 0,     /* hipHostMallocMapped | Portable             */
+  PF_PINNED_COHERENT = 1,    /* + hipHostMallocCoherent (fine-grained)     */
+  PF_PINNED_NONCOHERENT = 2, /* + hipHostMallocNonCoherent (coarse-grained)*/
+  PF_PINNED_NUMA_USER = 4    /* + hipHostMallocNumaUser (caller's policy)  */
+};
+/* size == 0 is PF_ERR_ZERO_SIZE (pinned_mem.rs:150-152).  *dev_ptr receives
+ * the device-visible address of the allocation (hipHostGetDevicePointer). */
+int pf_pinned_allocate(uint64_t size, uint32_t flags, void** host_ptr,
+                       uint64_t* dev_ptr);
+int pf_pinned_free(void* host_ptr);
+/* Device-visible address of a host pointer inside a pinned allocation. */
+int pf_host_device_pointer(const void* host_ptr, uint64_t* dev_ptr);
+/* Huge page size in bytes parsed from /proc/meminfo ("Hugepagesize: N kB"),
+ * 0 when absent (pinned_mem.rs:33-52). */
+uint64_t pf_huge_page_size(void);
+
+/* ------------------------------------------------------------------------ */
+/* Reference-equivalent DMA primitives (transfer.rs:56-239).                  */
+/* ------------------------------------------------------------------------ */
+/* Synchronous device -> host copy of size bytes from gpu_base+offset.
+ * Replaces copy_gpu_to_cpu (transfer.rs:56-76). */
+int pf_copy_gpu_to_cpu(uint64_t gpu_base, uint64_t offset, void* cpu_buffer,
+                       uint64_t cpu_buffer_len, uint64_t size);
+/* Asynchronous host -> device copy on stream; cpu_buffer_len < size is
+ * "CPU buffer too small: ..." (transfer.rs:89-95).
+ * Replaces copy_cpu_to_gpu_async (transfer.rs:80-113). */
+int pf_copy_cpu_to_gpu_async(uint64_t gpu_base, uint64_t offset,
+                             const void* cpu_buffer, uint64_t cpu_buffer_len,
+                             uint64_t size, pf_stream stream);
+/* Greedy run merging + one async H2D copy per run.  Entry j joins the run
+ * started at i iff gpu_offsets[j] == gpu_offsets[i] + (j-i)*segment_size and
+ * cpu_ptrs[j] == cpu_ptrs[i] + (j-i)*segment_size.  *out_batches receives the
+ * number of copies issued (may be NULL).
+ * Replaces batch_copy_segments_to_gpu (transfer.rs:116-198). */
+int pf_batch_copy_segments_to_gpu(const uint64_t* gpu_offsets,
+                                  const uint64_t* cpu_ptrs, uint64_t count,
+                                  uint64_t segment_size,
+                                  const pf_kv_layout* layout, pf_stream stream,
+                                  uint64_t* out_batches);
+/* Number of copies pf_batch_copy_segments_to_gpu would issue (no copies). */
+uint64_t pf_count_merged_runs(const uint64_t* gpu_offsets,
+                              const uint64_t* cpu_ptrs, uint64_t count,
+                              uint64_t segment_size);
+/* Synchronous copy of one whole block to dst: one chunk of block_size_bytes
+ * when contiguous, else each segment s to dst + s*bytes_per_block.
+ * Replaces copy_block_gpu_to_cpu / copy_gpu_to_cpu_strided
+ * (transfer.rs:201-239). */
+int pf_copy_block_gpu_to_cpu(const pf_kv_layout* layout, uint64_t block_idx,
+                             void* dst);
+
+/* ------------------------------------------------------------------------ */
+/* Batched transfer contexts and kernels (the hot path).                      */
+/* Replace process_save_task / process_load_task (gpu_worker.rs:205-390).     */
+/* ------------------------------------------------------------------------ */
+typedef struct pf_xfer pf_xfer;
+
+/* One block of one layer.  Replaces SaveBlock (gpu_worker.rs:38-44) and
+ * LoadBlock + LayerBlock::{k_ptr, v_ptr} (gpu_worker.rs:25-28,
+ * storage.rs:294-300).  k_host / v_host are host (or host-mapped, or device)
+ * addresses; v_host == 0 means k_host + bytes_per_block, as the reference's
+ * unwrap_or_else fallbacks do (gpu_worker.rs:233-236, 354-356). */
+typedef struct pf_block_xfer {
+  int64_t block_idx;
+  uint64_t k_host;
+  uint64_t v_host;
+} pf_block_xfer;
+
+/* Blocks of one layer.  Replaces LayerLoadData (gpu_worker.rs:19-23) and the
+ * (registration, blocks) pair of SaveTask (gpu_worker.rs:32-36). */
+typedef struct pf_layer_xfer {
+  pf_kv_layout layout;
+  const pf_block_xfer* blocks;
+  uint64_t num_blocks;
+} pf_layer_xfer;
+
+/* Transfer strategies.  All produce identical bytes.
+ *  DMA_REFERENCE: the reference's calls — save = one synchronous D2H copy per
+ *                 segment (gpu_worker.rs:344-371); load = merged runs, one
+ *                 async H2D copy per run (transfer.rs:116-198).
+ *  DMA_BATCHED:   merged runs, async, in both directions; one sync at the end.
+ *  KERNEL:        one gather/scatter kernel per layer moves 16 B per lane
+ *                 directly between the paged layer tensor and the (host-mapped
+ *                 pinned, or device) addresses.
+ *  STAGED:        the kernel runs HBM<->HBM into a packed staging buffer and
+ *                 the host link is crossed by large DMA copies of maximal
+ *                 host-contiguous runs, double-buffered across slices.      */
+enum {
+  PF_MODE_DMA_REFERENCE = 0,
+  PF_MODE_DMA_BATCHED = 1,
+  PF_MODE_KERNEL = 2,
+  PF_MODE_STAGED = 3
+};
+
+/* Create a transfer context on device: its own non-blocking streams, a
+ * device descriptor buffer, and (if staging_bytes > 0) two staging slots of
+ * staging_bytes/2 each for PF_MODE_STAGED. */
+int pf_xfer_create(int device, uint64_t staging_bytes, pf_xfer** out);
+int pf_xfer_destroy(pf_xfer* xfer);
+/* The stream on which the context's gather/scatter kernels run. */
+pf_stream pf_xfer_stream(pf_xfer* xfer);
+/* Wait for all work issued on the context. */
+int pf_xfer_synchronize(pf_xfer* xfer);
+/* Select the kernel's launch shape: threads per workgroup (64..1024, multiple
+ * of 64) and 16-byte loads in flight per lane (1, 2, 4, 8 or 16), optionally
+ * OR-ed with PF_KERNEL_NONTEMPORAL for non-temporal loads and stores.  0 keeps
+ * the current value.  Defaults: 256 threads, 8 loads, temporal accesses. */
+#define PF_KERNEL_NONTEMPORAL 0x100u
+int pf_xfer_set_kernel_shape(pf_xfer* xfer, uint32_t threads, uint32_t unroll);
+/* Number of gather/scatter kernel launches and DMA copies issued by the last
+ * save/load call on this context. */
+int pf_xfer_last_stats(pf_xfer* xfer, uint64_t* kernel_launches,
+                       uint64_t* dma_copies);
+/* Kernel timing: when enabled, every gather/scatter launch is bracketed by
+ * two events on the context's kernel stream.  pf_xfer_last_kernel_ms waits
+ * for the last call's kernels and returns their summed duration and count. */
+int pf_xfer_set_timing(pf_xfer* xfer, int enable);
+int pf_xfer_last_kernel_ms(pf_xfer* xfer, float* ms, uint64_t* launches);
+
+/* Device -> host: for every layer, copy each block's segments to its
+ * k_host/v_host destinations as process_save_task does (gpu_worker.rs:321-390).
+ * Every block_idx must be < num_blocks and pass segment_offset's bound.
+ * Blocking: returns when the bytes are in place. */
+int pf_save_layers(pf_xfer* xfer, const pf_layer_xfer* layers,
+                   uint32_t num_layers, uint32_t mode);
+
+/* Host -> device: for every layer, copy each block's segments from
+ * k_host/v_host into the paged tensor as process_load_task does
+ * (gpu_worker.rs:205-283).  Asynchronous: returns after issuing.  If
+ * layer_events is non-NULL, layer_events[l] is recorded once layer l's bytes
+ * are in place (per-layer completion, which the reference lacks:
+ * worker.py:288-289).  Completion of the whole call is pf_xfer_synchronize or
+ * the last layer's event. */
+int pf_load_layers(pf_xfer* xfer, const pf_layer_xfer* layers,
+                   uint32_t num_layers, uint32_t mode, pf_event* layer_events);
+
+/* ------------------------------------------------------------------------ */
+/* Synthetic data and verification kernels (benchmarks and parity tests).     */
+/* ------------------------------------------------------------------------ */
+/* Fill size_bytes (multiple of 8) at dst_dev with splitmix64 words:
+ * word[i] = mix64(seed + (word_offset + i + 1) * 0x9E3779B97F4A7C15). */
+int pf_fill_random(uint64_t dst_dev, uint64_t size_bytes, uint64_t seed,
+                   uint64_t word_offset, pf_stream stream);
+/* Count 8-byte words at addr that differ from the pf_fill_random formula
+ * (words expected: seed, word_offset...).  Synchronous; addr may be
+ * host-mapped. */
+int pf_verify_random(uint64_t addr, uint64_t size_bytes, uint64_t seed,
+                     uint64_t word_offset, uint64_t* mismatches);
+/* Batched form of pf_verify_random: chunk i (chunk_bytes at addrs[i]) must
+ * hold the words seed, word_offsets[i]... .  Host arrays; synchronous. */
+int pf_verify_random_chunks(const uint64_t* addrs, const uint64_t* word_offsets,
+                            uint64_t n, uint64_t chunk_bytes, uint64_t seed,
+                            uint64_t* mismatches);
+/* Count differing bytes between two device-visible buffers (synchronous). */
+int pf_compare(uint64_t a, uint64_t b, uint64_t size_bytes,
+               uint64_t* mismatches);
+/* Busy-wait on the device wall clock for `microseconds` on stream: a
+ * stand-in for a layer's attention compute in overlap measurements. */
+int pf_spin(pf_stream stream, uint32_t microseconds);
+
+/* ------------------------------------------------------------------------ */
+/* LoadState: cross-process completion word in POSIX shared memory.           */
+/* Replaces sync_state.rs:19-292.  The first 32 bytes are byte-identical to   */
+/* the reference's mapping: a native-endian u64 offset (8) at byte 0, then    */
+/* {u32 magic 0x50464C44, u32 version 1, i64 state} at that offset.           */
+/* A layered state appends an extension record after byte 32:               */
+/* {u32 magic 0x50464C58 ('PFLX'), u32 num_layers, i64 layers_done} so a      */
+/* reader that knows only the reference's record still attaches to it.       */
+/* ------------------------------------------------------------------------ */
+typedef struct pf_load_state pf_load_state;
+enum { PF_LOAD_PENDING = 0, PF_LOAD_SUCCESS = 1, PF_LOAD_ERROR = -1 };
+
+/* LoadState::new (sync_state.rs:125-142): shm "pega_load_<32 hex>". */
+int pf_load_state_create(pf_load_state** out);
+/* Same, with a per-layer completion counter for num_layers layers. */
+int pf_load_state_create_layered(uint32_t num_layers, pf_load_state** out);
+/* LoadState::attach (sync_state.rs:145-155). */
+int pf_load_state_attach(const char* shm_name, pf_load_state** out);
+/* Unmaps; the creator also unlinks the shm name. */
+int pf_load_state_close(pf_load_state* state);
+const char* pf_load_state_name(const pf_load_state* state);
+int64_t pf_load_state_get(const pf_load_state* state);
+void pf_load_state_set_completed(pf_load_state* state);
+void pf_load_state_set_error(pf_load_state* state);
+/* Layered extension: number of layers (0 for a plain state), layers whose
+ * bytes are in place, and the writer's increment (release ordering). */
+uint32_t pf_load_state_num_layers(const pf_load_state* state);
+int64_t pf_load_state_layers_done(const pf_load_state* state);
+void pf_load_state_set_layers_done(pf_load_state* state, int64_t n);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PEGAFLOW_HIP_H */

@@ -1,0 +1,222 @@
+"""ctypes binding of libpegaflow_hip.so (the C ABI in include/pegaflow_hip.h).
+
+The library is loaded from this package directory.  There is no fallback: if
+the library is missing, every entry point raises ``PegaFlowLibraryMissing``
+so the product path can never silently run anything but the HIP code.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libpegaflow_hip.so")
+
+# Status codes (include/pegaflow_hip.h).
+PF_OK = 0
+PF_ERR_INVALID_ARGUMENT = 1
+PF_ERR_HIP = 2
+PF_ERR_STORAGE = 3
+PF_ERR_INSTANCE_MISSING = 4
+PF_ERR_WORKER_MISSING = 5
+PF_ERR_TOPOLOGY_MISMATCH = 6
+PF_ERR_INIT = 7
+PF_ERR_LOAD_STATE = 8
+PF_ERR_ZERO_SIZE = 9
+PF_ERR_UNSUPPORTED = 10
+
+ERROR_NAMES = {
+    PF_ERR_INVALID_ARGUMENT: "invalid argument",
+    PF_ERR_HIP: "HIP error",
+    PF_ERR_STORAGE: "storage error",
+    PF_ERR_INSTANCE_MISSING: "instance missing",
+    PF_ERR_WORKER_MISSING: "worker missing",
+    PF_ERR_TOPOLOGY_MISMATCH: "topology mismatch",
+    PF_ERR_INIT: "failed to initialize",
+    PF_ERR_LOAD_STATE: "LoadState error",
+    PF_ERR_ZERO_SIZE: "zero size",
+    PF_ERR_UNSUPPORTED: "unsupported",
+}
+
+# Transfer modes.
+MODE_DMA_REFERENCE = 0
+MODE_DMA_BATCHED = 1
+MODE_KERNEL = 2
+MODE_STAGED = 3
+MODE_NAMES = {
+    "dma_reference": MODE_DMA_REFERENCE,
+    "dma_batched": MODE_DMA_BATCHED,
+    "kernel": MODE_KERNEL,
+    "staged": MODE_STAGED,
+}
+
+# Layout kinds.
+LAYOUT_SPLIT, LAYOUT_CONTIGUOUS, LAYOUT_STRIDED = 0, 1, 2
+
+# Pinned allocation flags.
+PINNED_DEFAULT = 0
+PINNED_COHERENT = 1
+PINNED_NONCOHERENT = 2
+PINNED_NUMA_USER = 4
+
+KERNEL_NONTEMPORAL = 0x100
+
+LOAD_PENDING, LOAD_SUCCESS, LOAD_ERROR = 0, 1, -1
+
+
+class PegaFlowError(RuntimeError):
+    """A failed C-ABI call: ``code`` is the PF_ERR_* status."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(message)
+        self.code = code
+
+
+class PegaFlowLibraryMissing(ImportError):
+    pass
+
+
+class KVLayout(ctypes.Structure):
+    """pf_kv_layout — KVCacheRegistration (lib.rs:100-112)."""
+
+    _fields_ = [
+        ("data_ptr", ctypes.c_uint64),
+        ("size_bytes", ctypes.c_uint64),
+        ("num_blocks", ctypes.c_uint64),
+        ("bytes_per_block", ctypes.c_uint64),
+        ("block_size_bytes", ctypes.c_uint64),
+        ("kv_stride_bytes", ctypes.c_uint64),
+        ("segments", ctypes.c_uint64),
+    ]
+
+
+class BlockXfer(ctypes.Structure):
+    """pf_block_xfer — SaveBlock / LoadBlock (gpu_worker.rs:25-49)."""
+
+    _fields_ = [
+        ("block_idx", ctypes.c_int64),
+        ("k_host", ctypes.c_uint64),
+        ("v_host", ctypes.c_uint64),
+    ]
+
+
+class LayerXfer(ctypes.Structure):
+    """pf_layer_xfer — LayerLoadData (gpu_worker.rs:19-23)."""
+
+    _fields_ = [
+        ("layout", KVLayout),
+        ("blocks", ctypes.c_void_p),
+        ("num_blocks", ctypes.c_uint64),
+    ]
+
+
+u64 = ctypes.c_uint64
+i64 = ctypes.c_int64
+u32 = ctypes.c_uint32
+i32 = ctypes.c_int
+vp = ctypes.c_void_p
+pu64 = ctypes.POINTER(ctypes.c_uint64)
+pi32 = ctypes.POINTER(ctypes.c_int)
+pvp = ctypes.POINTER(ctypes.c_void_p)
+pl = ctypes.POINTER(KVLayout)
+cs = ctypes.c_char_p
+
+# name -> (restype, argtypes).  Every symbol declared in the header.
+SIGNATURES = {
+    "pf_last_error": (cs, []),
+    "pf_version": (cs, []),
+    "pf_layout_init": (i32, [u64, u64, u64, u64, u64, u64, pl]),
+    "pf_segment_offset": (i32, [pl, u64, u64, pu64]),
+    "pf_is_contiguous_layout": (i32, [pl]),
+    "pf_layout_kind": (i32, [pl]),
+    "pf_get_device_count": (i32, [pi32]),
+    "pf_init": (i32, [i32]),
+    "pf_set_device": (i32, [i32]),
+    "pf_get_device": (i32, [pi32]),
+    "pf_device_synchronize": (i32, []),
+    "pf_stream_create": (i32, [pvp]),
+    "pf_stream_destroy": (i32, [vp]),
+    "pf_stream_synchronize": (i32, [vp]),
+    "pf_stream_wait_event": (i32, [vp, vp]),
+    "pf_event_create": (i32, [pvp]),
+    "pf_event_destroy": (i32, [vp]),
+    "pf_event_record": (i32, [vp, vp]),
+    "pf_event_synchronize": (i32, [vp]),
+    "pf_event_query": (i32, [vp, pi32]),
+    "pf_event_elapsed_ms": (i32, [vp, vp, ctypes.POINTER(ctypes.c_float)]),
+    "pf_device_malloc": (i32, [u64, pu64]),
+    "pf_device_free": (i32, [u64]),
+    "pf_memcpy_h2d": (i32, [u64, vp, u64]),
+    "pf_memcpy_d2h": (i32, [vp, u64, u64]),
+    "pf_memcpy_d2d": (i32, [u64, u64, u64]),
+    "pf_memset_d8": (i32, [u64, ctypes.c_uint8, u64]),
+    "pf_mem_get_info": (i32, [pu64, pu64]),
+    "pf_pinned_allocate": (i32, [u64, u32, pvp, pu64]),
+    "pf_pinned_free": (i32, [vp]),
+    "pf_host_device_pointer": (i32, [vp, pu64]),
+    "pf_huge_page_size": (u64, []),
+    "pf_copy_gpu_to_cpu": (i32, [u64, u64, vp, u64, u64]),
+    "pf_copy_cpu_to_gpu_async": (i32, [u64, u64, vp, u64, u64, vp]),
+    "pf_batch_copy_segments_to_gpu": (i32, [pu64, pu64, u64, u64, pl, vp, pu64]),
+    "pf_count_merged_runs": (u64, [pu64, pu64, u64, u64]),
+    "pf_copy_block_gpu_to_cpu": (i32, [pl, u64, vp]),
+    "pf_xfer_create": (i32, [i32, u64, pvp]),
+    "pf_xfer_destroy": (i32, [vp]),
+    "pf_xfer_stream": (vp, [vp]),
+    "pf_xfer_synchronize": (i32, [vp]),
+    "pf_xfer_set_kernel_shape": (i32, [vp, u32, u32]),
+    "pf_xfer_last_stats": (i32, [vp, pu64, pu64]),
+    "pf_save_layers": (i32, [vp, ctypes.POINTER(LayerXfer), u32, u32]),
+    "pf_load_layers": (i32, [vp, ctypes.POINTER(LayerXfer), u32, u32, pvp]),
+    "pf_fill_random": (i32, [u64, u64, u64, u64, vp]),
+    "pf_verify_random": (i32, [u64, u64, u64, u64, pu64]),
+    "pf_verify_random_chunks": (i32, [pu64, pu64, u64, u64, u64, pu64]),
+    "pf_compare": (i32, [u64, u64, u64, pu64]),
+    "pf_spin": (i32, [vp, u32]),
+    "pf_load_state_create": (i32, [pvp]),
+    "pf_load_state_create_layered": (i32, [u32, pvp]),
+    "pf_load_state_attach": (i32, [cs, pvp]),
+    "pf_load_state_close": (i32, [vp]),
+    "pf_load_state_name": (cs, [vp]),
+    "pf_load_state_get": (i64, [vp]),
+    "pf_load_state_set_completed": (None, [vp]),
+    "pf_load_state_set_error": (None, [vp]),
+    "pf_load_state_num_layers": (u32, [vp]),
+    "pf_load_state_layers_done": (i64, [vp]),
+    "pf_load_state_set_layers_done": (None, [vp, i64]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+def load():
+    """Load and bind the library (once)."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise PegaFlowLibraryMissing(
+                f"{LIB_PATH} is not built; run `python -m pegaflow_amd.build`"
+            )
+        L = ctypes.CDLL(LIB_PATH, mode=os.RTLD_LOCAL | os.RTLD_NOW)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+        return _lib
+
+
+def last_error() -> str:
+    return load().pf_last_error().decode(errors="replace")
+
+
+def check(rc: int, what: str = "") -> None:
+    if rc != PF_OK:
+        msg = last_error()
+        prefix = ERROR_NAMES.get(rc, f"error {rc}")
+        raise PegaFlowError(rc, f"{what + ': ' if what else ''}{prefix}: {msg}")

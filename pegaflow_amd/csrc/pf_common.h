@@ -1,0 +1,94 @@
+// pf_common.h — internal helpers shared by the pegaflow_hip sources.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "../../include/pegaflow_hip.h"
+
+namespace pf {
+
+// Thread-local last-error message (pf_last_error).
+void set_error(const std::string& msg);
+void clear_error();
+int fail(int code, const std::string& msg);
+std::string strf(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+
+// Returns PF_ERR_HIP with "<what> failed: <hip error string>" on error.
+int hip_fail(hipError_t e, const char* what);
+
+#define PF_HIP(call)                                   \
+  do {                                                 \
+    hipError_t pf_e_ = (call);                         \
+    if (pf_e_ != hipSuccess) return ::pf::hip_fail(pf_e_, #call); \
+  } while (0)
+
+// One copy unit for the gather/scatter kernels: `chunk_bytes` bytes from
+// src to dst (device-visible addresses; chunk size is uniform per launch).
+struct ChunkDesc {
+  uint64_t src;
+  uint64_t dst;
+};
+
+// Kernel launchers (pf_kernels.hip).
+hipError_t launch_copy_chunks(const ChunkDesc* d_descs, uint32_t n_chunks,
+                              uint64_t chunk_bytes, bool aligned16,
+                              uint32_t threads, uint32_t unroll,
+                              hipStream_t stream);
+hipError_t launch_fill_random(uint64_t dst, uint64_t size_bytes, uint64_t seed,
+                              uint64_t word_offset, hipStream_t stream);
+hipError_t launch_verify_random(uint64_t addr, uint64_t size_bytes,
+                                uint64_t seed, uint64_t word_offset,
+                                unsigned long long* d_count,
+                                hipStream_t stream);
+hipError_t launch_verify_random_chunks(const uint64_t* d_addrs,
+                                       const uint64_t* d_word_offsets,
+                                       uint64_t n, uint64_t chunk_bytes,
+                                       uint64_t seed,
+                                       unsigned long long* d_count,
+                                       hipStream_t stream);
+hipError_t launch_compare(uint64_t a, uint64_t b, uint64_t size_bytes,
+                          unsigned long long* d_count, hipStream_t stream);
+hipError_t launch_spin(uint64_t ticks, hipStream_t stream);
+
+// Registry of pinned allocations made by pf_pinned_allocate, so that kernels
+// are only ever given host ranges that are mapped for device access.
+void pinned_register(uint64_t base, uint64_t size);
+void pinned_unregister(uint64_t base);
+// True when [addr, addr+len) lies inside one registered pinned allocation;
+// *base/*end receive that allocation's bounds.
+bool pinned_lookup(uint64_t addr, uint64_t len, uint64_t* base, uint64_t* end);
+
+// Address validation for kernel access.  A kernel that touches an unmapped
+// address faults the GPU, so every range a kernel will touch is checked
+// first: it must lie inside one pinned allocation made by pf_pinned_allocate
+// or inside one device allocation.  Results are cached for the lifetime of
+// the object only (allocations may be freed between calls).
+class RangeCache {
+ public:
+  bool check(uint64_t addr, uint64_t len);
+
+ private:
+  bool contains(uint64_t addr, uint64_t len);
+  std::vector<std::pair<uint64_t, uint64_t>> ok_;  // [begin, end)
+  uint64_t last_b_ = 0, last_e_ = 0;
+};
+
+// Layout kind (PF_LAYOUT_*), shared by the transfer paths.
+inline int layout_kind(const pf_kv_layout& l) {
+  if (l.segments == 2 && l.kv_stride_bytes > l.bytes_per_block)
+    return PF_LAYOUT_SPLIT;
+  if (l.segments <= 1 || l.kv_stride_bytes == l.bytes_per_block)
+    return PF_LAYOUT_CONTIGUOUS;
+  return PF_LAYOUT_STRIDED;
+}
+
+// segment_offset with the reference's checks; message set on failure.
+int segment_offset(const pf_kv_layout& l, uint64_t block, uint64_t seg,
+                   uint64_t* out);
+
+}  // namespace pf

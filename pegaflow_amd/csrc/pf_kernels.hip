@@ -1,0 +1,282 @@
+// pf_kernels.hip — gfx950 gather/scatter kernels of the KV-block transfer
+// path, plus the synthetic-data, verification and spin kernels used by the
+// benchmark and the parity tests.
+//
+// The transfer is pure data movement (no contraction, so no MFMA).  A launch
+// moves `n_chunks` chunks of `chunk_bytes` each, described by (src, dst)
+// address pairs in device memory.  Addresses may be HBM (the paged layer
+// tensor, a staging buffer) or host-mapped pinned memory (zero-copy over the
+// host link).  The same kernel therefore serves:
+//   * save:    paged layer tensor -> pinned host (or HBM staging), a gather;
+//   * restore: pinned host (or HBM staging) -> paged layer tensor, a scatter.
+//
+// Work decomposition: a chunk is split into tiles of blockDim.x * UNROLL
+// 16-byte elements.  One workgroup copies one tile: every lane issues UNROLL
+// independent 16-byte loads (global_load_dwordx4) before its UNROLL stores,
+// so each wave keeps UNROLL * 1 KiB in flight — enough to cover HBM latency
+// and, for zero-copy, the much longer host-link read latency.  Consecutive
+// lanes touch consecutive 16-byte words, so every wave instruction covers one
+// contiguous 1 KiB span (fully coalesced).  No LDS: source and destination
+// share the same byte order within a chunk.
+#include <hip/hip_runtime.h>
+
+#include "pf_common.h"
+
+namespace pf {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+// Global-address-space views: the addresses arrive as integers, and without
+// the address space the compiler would emit generic (flat) accesses.
+typedef __attribute__((address_space(1))) u32x4 g_u32x4;
+typedef __attribute__((address_space(1))) uint8_t g_u8;
+typedef __attribute__((address_space(1))) uint64_t g_u64;
+
+template <int UNROLL, bool NT>
+__global__ void __launch_bounds__(1024)
+copy_chunks_v16_kernel(const ChunkDesc* __restrict__ descs,
+                       uint32_t tiles_per_chunk, uint32_t n_tiles,
+                       uint32_t chunk16) {
+  const uint32_t stride = blockDim.x;
+  const uint32_t tile_elems = stride * UNROLL;
+  for (uint32_t t = blockIdx.x; t < n_tiles; t += gridDim.x) {
+    const uint32_t c = t / tiles_per_chunk;
+    const uint32_t tile = t - c * tiles_per_chunk;
+    const ChunkDesc d = descs[c];
+    const g_u32x4* __restrict__ src = reinterpret_cast<const g_u32x4*>(d.src);
+    g_u32x4* __restrict__ dst = reinterpret_cast<g_u32x4*>(d.dst);
+    const uint32_t tile_base = tile * tile_elems;
+    const uint32_t base = tile_base + threadIdx.x;
+    if (tile_base + tile_elems <= chunk16) {
+      u32x4 v[UNROLL];
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) {
+        if constexpr (NT)
+          v[u] = __builtin_nontemporal_load(src + base + u * stride);
+        else
+          v[u] = src[base + u * stride];
+      }
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) {
+        if constexpr (NT)
+          __builtin_nontemporal_store(v[u], dst + base + u * stride);
+        else
+          dst[base + u * stride] = v[u];
+      }
+    } else {
+      // Partial last tile of a chunk: guarded per element.
+      u32x4 v[UNROLL];
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) {
+        const uint32_t e = base + u * stride;
+        if (e < chunk16) v[u] = src[e];
+      }
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) {
+        const uint32_t e = base + u * stride;
+        if (e < chunk16) dst[e] = v[u];
+      }
+    }
+  }
+}
+
+// Fallback for chunks whose addresses or size are not 16-byte aligned.
+__global__ void __launch_bounds__(1024)
+copy_chunks_b1_kernel(const ChunkDesc* __restrict__ descs, uint32_t n_chunks,
+                      uint64_t chunk_bytes) {
+  for (uint32_t c = blockIdx.x; c < n_chunks; c += gridDim.x) {
+    const ChunkDesc d = descs[c];
+    const g_u8* __restrict__ src = reinterpret_cast<const g_u8*>(d.src);
+    g_u8* __restrict__ dst = reinterpret_cast<g_u8*>(d.dst);
+    for (uint64_t i = threadIdx.x; i < chunk_bytes; i += blockDim.x) dst[i] = src[i];
+  }
+}
+
+// Upper bound on workgroups per launch; larger tile counts loop.
+static constexpr uint32_t kMaxGrid = 1u << 20;
+
+template <int UNROLL>
+static hipError_t launch_v16(const ChunkDesc* d_descs, uint32_t tiles_per_chunk,
+                             uint32_t n_tiles, uint32_t chunk16, uint32_t threads,
+                             bool nt, hipStream_t stream) {
+  const uint32_t grid = n_tiles < kMaxGrid ? n_tiles : kMaxGrid;
+  if (nt)
+    hipLaunchKernelGGL((copy_chunks_v16_kernel<UNROLL, true>), dim3(grid),
+                       dim3(threads), 0, stream, d_descs, tiles_per_chunk,
+                       n_tiles, chunk16);
+  else
+    hipLaunchKernelGGL((copy_chunks_v16_kernel<UNROLL, false>), dim3(grid),
+                       dim3(threads), 0, stream, d_descs, tiles_per_chunk,
+                       n_tiles, chunk16);
+  return hipGetLastError();
+}
+
+// `unroll` may carry PF_KERNEL_NONTEMPORAL (0x100) to select non-temporal
+// loads and stores.
+hipError_t launch_copy_chunks(const ChunkDesc* d_descs, uint32_t n_chunks,
+                              uint64_t chunk_bytes, bool aligned16,
+                              uint32_t threads, uint32_t unroll,
+                              hipStream_t stream) {
+  if (n_chunks == 0 || chunk_bytes == 0) return hipSuccess;
+  if (threads == 0 || threads > 1024 || threads % 64 != 0) return hipErrorInvalidValue;
+  const bool nt = (unroll & 0x100u) != 0;
+  unroll &= 0xffu;
+  if (!aligned16) {
+    const uint32_t grid = n_chunks < kMaxGrid ? n_chunks : kMaxGrid;
+    hipLaunchKernelGGL(copy_chunks_b1_kernel, dim3(grid), dim3(threads), 0,
+                       stream, d_descs, n_chunks, chunk_bytes);
+    return hipGetLastError();
+  }
+  const uint64_t chunk16 = chunk_bytes / 16;
+  if (chunk16 > 0xffffffffull) return hipErrorInvalidValue;
+  const uint64_t tile_elems = static_cast<uint64_t>(threads) * unroll;
+  if (tile_elems == 0) return hipErrorInvalidValue;
+  const uint64_t tiles_per_chunk = (chunk16 + tile_elems - 1) / tile_elems;
+  const uint64_t n_tiles = tiles_per_chunk * n_chunks;
+  if (n_tiles > 0xffffffffull) return hipErrorInvalidValue;
+  // Every tile index < n_tiles maps to chunk < n_chunks and element offsets
+  // < tiles_per_chunk * tile_elems; elements >= chunk16 are masked, and the
+  // full-tile path is taken only when the whole tile lies below chunk16.
+  const uint32_t tpc = static_cast<uint32_t>(tiles_per_chunk);
+  const uint32_t nt_ = static_cast<uint32_t>(n_tiles);
+  const uint32_t c16 = static_cast<uint32_t>(chunk16);
+  switch (unroll) {
+    case 1: return launch_v16<1>(d_descs, tpc, nt_, c16, threads, nt, stream);
+    case 2: return launch_v16<2>(d_descs, tpc, nt_, c16, threads, nt, stream);
+    case 4: return launch_v16<4>(d_descs, tpc, nt_, c16, threads, nt, stream);
+    case 8: return launch_v16<8>(d_descs, tpc, nt_, c16, threads, nt, stream);
+    case 16: return launch_v16<16>(d_descs, tpc, nt_, c16, threads, nt, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Synthetic data: splitmix64 words, word[i] = mix64(seed + (off+i+1)*GAMMA).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+static constexpr uint64_t kGamma = 0x9E3779B97F4A7C15ull;
+
+__global__ void __launch_bounds__(256)
+fill_random_kernel(uint64_t* __restrict__ dst, uint64_t n_words, uint64_t seed,
+                   uint64_t word_offset) {
+  const uint64_t step = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+       i < n_words; i += step)
+    dst[i] = mix64(seed + (word_offset + i + 1) * kGamma);
+}
+
+__global__ void __launch_bounds__(256)
+verify_random_kernel(const uint64_t* __restrict__ src, uint64_t n_words,
+                     uint64_t seed, uint64_t word_offset,
+                     unsigned long long* count) {
+  const uint64_t step = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+  unsigned long long bad = 0;
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+       i < n_words; i += step)
+    bad += src[i] != mix64(seed + (word_offset + i + 1) * kGamma);
+  if (bad) atomicAdd(count, bad);
+}
+
+// One workgroup per chunk (grid-stride over chunks).
+__global__ void __launch_bounds__(256)
+verify_random_chunks_kernel(const uint64_t* __restrict__ addrs,
+                            const uint64_t* __restrict__ word_offsets, uint64_t n,
+                            uint64_t chunk_words, uint64_t seed,
+                            unsigned long long* count) {
+  unsigned long long bad = 0;
+  for (uint64_t c = blockIdx.x; c < n; c += gridDim.x) {
+    const g_u64* src = reinterpret_cast<const g_u64*>(addrs[c]);
+    const uint64_t off = word_offsets[c];
+    for (uint64_t i = threadIdx.x; i < chunk_words; i += blockDim.x)
+      bad += src[i] != mix64(seed + (off + i + 1) * kGamma);
+  }
+  if (bad) atomicAdd(count, bad);
+}
+
+__global__ void __launch_bounds__(256)
+compare_kernel(const uint8_t* __restrict__ a, const uint8_t* __restrict__ b,
+               uint64_t n, unsigned long long* count) {
+  const uint64_t step = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+  const uint64_t tid = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  unsigned long long bad = 0;
+  const bool aligned = ((reinterpret_cast<uint64_t>(a) | reinterpret_cast<uint64_t>(b)) & 7) == 0;
+  uint64_t tail_start = 0;
+  if (aligned) {
+    const uint64_t* wa = reinterpret_cast<const uint64_t*>(a);
+    const uint64_t* wb = reinterpret_cast<const uint64_t*>(b);
+    const uint64_t nw = n / 8;
+    for (uint64_t i = tid; i < nw; i += step) {
+      uint64_t x = wa[i] ^ wb[i];
+      for (int k = 0; k < 8; ++k) bad += ((x >> (8 * k)) & 0xff) != 0;
+    }
+    tail_start = nw * 8;
+  }
+  for (uint64_t i = tail_start + tid; i < n; i += step) bad += a[i] != b[i];
+  if (bad) atomicAdd(count, bad);
+}
+
+__global__ void spin_kernel(uint64_t ticks) {
+  if (threadIdx.x == 0) {
+    const uint64_t start = static_cast<uint64_t>(wall_clock64());
+    while (static_cast<uint64_t>(wall_clock64()) - start < ticks)
+      __builtin_amdgcn_s_sleep(4);
+  }
+}
+
+static uint32_t grid_for(uint64_t items, uint32_t threads) {
+  uint64_t g = (items + threads - 1) / threads;
+  if (g > 65536) g = 65536;
+  if (g == 0) g = 1;
+  return static_cast<uint32_t>(g);
+}
+
+hipError_t launch_fill_random(uint64_t dst, uint64_t size_bytes, uint64_t seed,
+                              uint64_t word_offset, hipStream_t stream) {
+  const uint64_t n = size_bytes / 8;
+  hipLaunchKernelGGL(fill_random_kernel, dim3(grid_for(n, 256)), dim3(256), 0,
+                     stream, reinterpret_cast<uint64_t*>(dst), n, seed,
+                     word_offset);
+  return hipGetLastError();
+}
+
+hipError_t launch_verify_random(uint64_t addr, uint64_t size_bytes,
+                                uint64_t seed, uint64_t word_offset,
+                                unsigned long long* d_count,
+                                hipStream_t stream) {
+  const uint64_t n = size_bytes / 8;
+  hipLaunchKernelGGL(verify_random_kernel, dim3(grid_for(n, 256)), dim3(256), 0,
+                     stream, reinterpret_cast<const uint64_t*>(addr), n, seed,
+                     word_offset, d_count);
+  return hipGetLastError();
+}
+
+hipError_t launch_verify_random_chunks(const uint64_t* d_addrs,
+                                       const uint64_t* d_word_offsets,
+                                       uint64_t n, uint64_t chunk_bytes,
+                                       uint64_t seed,
+                                       unsigned long long* d_count,
+                                       hipStream_t stream) {
+  const uint32_t grid = n < 65536 ? static_cast<uint32_t>(n) : 65536u;
+  hipLaunchKernelGGL(verify_random_chunks_kernel, dim3(grid), dim3(256), 0, stream,
+                     d_addrs, d_word_offsets, n, chunk_bytes / 8, seed, d_count);
+  return hipGetLastError();
+}
+
+hipError_t launch_compare(uint64_t a, uint64_t b, uint64_t size_bytes,
+                          unsigned long long* d_count, hipStream_t stream) {
+  hipLaunchKernelGGL(compare_kernel, dim3(grid_for(size_bytes / 8 + 1, 256)),
+                     dim3(256), 0, stream, reinterpret_cast<const uint8_t*>(a),
+                     reinterpret_cast<const uint8_t*>(b), size_bytes, d_count);
+  return hipGetLastError();
+}
+
+hipError_t launch_spin(uint64_t ticks, hipStream_t stream) {
+  hipLaunchKernelGGL(spin_kernel, dim3(1), dim3(64), 0, stream, ticks);
+  return hipGetLastError();
+}
+
+}  // namespace pf

@@ -1,0 +1,258 @@
+// pf_load_state.cpp — LoadState, the cross-process completion word of an
+// asynchronous load (the role of pegaflow-core/src/sync_state.rs).
+//
+// Mapping layout (native endian), identical to the reference for the first
+// 32 bytes so either side can attach to the other's state:
+//   [0, 8)    u64 offset of the record from the mapping start (8 when the
+//             mapping is page aligned)                  sync_state.rs:27-30
+//   offset:   u32 magic 0x50464C44 ('PFLD'), u32 version 1, i64 state
+//             (0 pending, 1 success, -1 error)          sync_state.rs:19-43
+//   mapping size 32 = 8 + sizeof(record) + alignof(record)  sync_state.rs:190-193
+// Layered extension (absent from the reference), at byte 32:
+//   u32 magic 0x50464C58 ('PFLX'), u32 num_layers, i64 layers_done
+// so the per-layer completion of a layer-wise load is visible to a process
+// that polls the shared memory, while a reader of the original record still
+// attaches (it only requires the mapping to hold at least 32 bytes).
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <cerrno>
+#include <cstring>
+#include <random>
+#include <string>
+
+#include "pf_common.h"
+
+using namespace pf;
+
+namespace {
+
+constexpr uint32_t kMagic = 0x50464C44u;  // 'PFLD'
+constexpr uint32_t kVersion = 1;
+constexpr uint32_t kExtMagic = 0x50464C58u;  // 'PFLX'
+constexpr size_t kMetaSize = 8;
+constexpr size_t kRecordSize = 16;
+constexpr size_t kRecordAlign = 8;
+constexpr size_t kAllocSize = kMetaSize + kRecordSize + kRecordAlign;  // 32
+constexpr size_t kExtOffset = kAllocSize;
+constexpr size_t kExtSize = 16;
+
+struct Record {
+  uint32_t magic;
+  uint32_t version;
+  int64_t state;
+};
+static_assert(sizeof(Record) == kRecordSize, "record layout");
+
+struct ExtRecord {
+  uint32_t magic;
+  uint32_t num_layers;
+  int64_t layers_done;
+};
+static_assert(sizeof(ExtRecord) == kExtSize, "extension layout");
+
+std::string random_name() {
+  // "pega_load_" + uuid-v4 in simple (32 lowercase hex) form (sync_state.rs:126).
+  std::random_device rd;
+  uint8_t b[16];
+  for (int i = 0; i < 16; i += 4) {
+    uint32_t r = rd();
+    std::memcpy(b + i, &r, 4);
+  }
+  b[6] = (b[6] & 0x0f) | 0x40;
+  b[8] = (b[8] & 0x3f) | 0x80;
+  static const char* hex = "0123456789abcdef";
+  std::string s = "pega_load_";
+  for (int i = 0; i < 16; ++i) {
+    s.push_back(hex[b[i] >> 4]);
+    s.push_back(hex[b[i] & 15]);
+  }
+  return s;
+}
+
+}  // namespace
+
+struct pf_load_state {
+  std::string name;
+  uint8_t* map = nullptr;
+  size_t len = 0;
+  bool owner = false;
+  Record* rec = nullptr;
+  ExtRecord* ext = nullptr;
+};
+
+namespace {
+
+int create_state(uint32_t num_layers, bool layered, pf_load_state** out) {
+  if (!out) return fail(PF_ERR_INVALID_ARGUMENT, "null output");
+  const size_t size = layered ? kExtOffset + kExtSize : kAllocSize;
+  std::string name;
+  int fd = -1;
+  for (int attempt = 0; attempt < 8 && fd < 0; ++attempt) {
+    name = random_name();
+    fd = shm_open(name.c_str(), O_CREAT | O_EXCL | O_RDWR, S_IRUSR | S_IWUSR);
+    if (fd < 0 && errno != EEXIST) break;
+  }
+  if (fd < 0)
+    return fail(PF_ERR_LOAD_STATE,
+                strf("failed to create shared memory: %s", std::strerror(errno)));
+  if (ftruncate(fd, static_cast<off_t>(size)) != 0) {
+    int err = errno;
+    close(fd);
+    shm_unlink(name.c_str());
+    return fail(PF_ERR_LOAD_STATE,
+                strf("failed to create shared memory: %s", std::strerror(err)));
+  }
+  void* m = mmap(nullptr, size, PROT_READ | PROT_WRITE, MAP_SHARED, fd, 0);
+  close(fd);
+  if (m == MAP_FAILED) {
+    shm_unlink(name.c_str());
+    return fail(PF_ERR_LOAD_STATE,
+                strf("failed to create shared memory: %s", std::strerror(errno)));
+  }
+  uint8_t* base = static_cast<uint8_t*>(m);
+  // init_new_mapping (sync_state.rs:201-242): align base+8 up to the record's
+  // alignment and store the offset in the first 8 bytes.
+  const uintptr_t b = reinterpret_cast<uintptr_t>(base);
+  const uintptr_t aligned = (b + kMetaSize + kRecordAlign - 1) & ~(uintptr_t)(kRecordAlign - 1);
+  const uint64_t offset = aligned - b;
+  std::memcpy(base, &offset, sizeof(offset));
+  auto* st = new pf_load_state();
+  st->name = name;
+  st->map = base;
+  st->len = size;
+  st->owner = true;
+  st->rec = reinterpret_cast<Record*>(base + offset);
+  __atomic_store_n(&st->rec->magic, kMagic, __ATOMIC_RELEASE);
+  __atomic_store_n(&st->rec->version, kVersion, __ATOMIC_RELEASE);
+  __atomic_store_n(&st->rec->state, (int64_t)PF_LOAD_PENDING, __ATOMIC_RELEASE);
+  if (layered) {
+    st->ext = reinterpret_cast<ExtRecord*>(base + kExtOffset);
+    __atomic_store_n(&st->ext->num_layers, num_layers, __ATOMIC_RELEASE);
+    __atomic_store_n(&st->ext->layers_done, (int64_t)0, __ATOMIC_RELEASE);
+    __atomic_store_n(&st->ext->magic, kExtMagic, __ATOMIC_RELEASE);
+  }
+  *out = st;
+  return PF_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int pf_load_state_create(pf_load_state** out) { return create_state(0, false, out); }
+
+int pf_load_state_create_layered(uint32_t num_layers, pf_load_state** out) {
+  return create_state(num_layers, true, out);
+}
+
+// LoadState::attach + attach_mapping + validate_header (sync_state.rs:145-155,
+// 244-292).
+int pf_load_state_attach(const char* shm_name, pf_load_state** out) {
+  if (!shm_name || !out) return fail(PF_ERR_INVALID_ARGUMENT, "null argument");
+  int fd = shm_open(shm_name, O_RDWR, S_IRUSR);
+  if (fd < 0)
+    return fail(PF_ERR_LOAD_STATE,
+                strf("failed to open shared memory: %s", std::strerror(errno)));
+  struct stat sb;
+  if (fstat(fd, &sb) != 0) {
+    int err = errno;
+    close(fd);
+    return fail(PF_ERR_LOAD_STATE, strf("failed to open shared memory: %s", std::strerror(err)));
+  }
+  const size_t len = static_cast<size_t>(sb.st_size);
+  if (len < kAllocSize) {
+    close(fd);
+    return fail(PF_ERR_LOAD_STATE,
+                strf("shared memory too small (actual=%zu bytes, required=%zu bytes)", len,
+                     kAllocSize));
+  }
+  void* m = mmap(nullptr, len, PROT_READ | PROT_WRITE, MAP_SHARED, fd, 0);
+  close(fd);
+  if (m == MAP_FAILED)
+    return fail(PF_ERR_LOAD_STATE,
+                strf("failed to open shared memory: %s", std::strerror(errno)));
+  uint8_t* base = static_cast<uint8_t*>(m);
+  uint64_t offset = 0;
+  std::memcpy(&offset, base, sizeof(offset));
+  auto bail = [&](int code, const std::string& msg) {
+    munmap(m, len);
+    return fail(code, msg);
+  };
+  if (offset < kMetaSize)
+    return bail(PF_ERR_LOAD_STATE,
+                strf("invalid LoadState offset (offset=%llu, len=%zu) recorded in shared memory",
+                     (unsigned long long)offset, len));
+  if (offset > len || len - offset < kRecordSize)
+    return bail(PF_ERR_LOAD_STATE,
+                strf("shared memory too small (actual=%zu bytes, required=%llu bytes)", len,
+                     (unsigned long long)(offset + kRecordSize)));
+  if ((reinterpret_cast<uintptr_t>(base) + offset) % kRecordAlign != 0)
+    return bail(PF_ERR_LOAD_STATE,
+                strf("aligned pointer 0x%llx is not %zu-byte aligned",
+                     (unsigned long long)(reinterpret_cast<uintptr_t>(base) + offset),
+                     kRecordAlign));
+  Record* rec = reinterpret_cast<Record*>(base + offset);
+  const uint32_t magic = __atomic_load_n(&rec->magic, __ATOMIC_ACQUIRE);
+  const uint32_t version = __atomic_load_n(&rec->version, __ATOMIC_ACQUIRE);
+  if (magic != kMagic || version != kVersion)
+    return bail(PF_ERR_LOAD_STATE,
+                strf("invalid LoadState header (magic=0x%x, version=%u, expected magic=0x%x, "
+                     "version=%u)",
+                     magic, version, kMagic, kVersion));
+  auto* st = new pf_load_state();
+  st->name = shm_name;
+  st->map = base;
+  st->len = len;
+  st->owner = false;
+  st->rec = rec;
+  if (len >= kExtOffset + kExtSize) {
+    ExtRecord* ext = reinterpret_cast<ExtRecord*>(base + kExtOffset);
+    if (__atomic_load_n(&ext->magic, __ATOMIC_ACQUIRE) == kExtMagic) st->ext = ext;
+  }
+  *out = st;
+  return PF_OK;
+}
+
+int pf_load_state_close(pf_load_state* st) {
+  if (!st) return PF_OK;
+  if (st->map) munmap(st->map, st->len);
+  if (st->owner) shm_unlink(st->name.c_str());
+  delete st;
+  return PF_OK;
+}
+
+const char* pf_load_state_name(const pf_load_state* st) { return st->name.c_str(); }
+
+int64_t pf_load_state_get(const pf_load_state* st) {
+  return __atomic_load_n(&st->rec->state, __ATOMIC_ACQUIRE);
+}
+
+void pf_load_state_set_completed(pf_load_state* st) {
+  if (st->ext) {
+    const int64_t n = static_cast<int64_t>(__atomic_load_n(&st->ext->num_layers, __ATOMIC_ACQUIRE));
+    __atomic_store_n(&st->ext->layers_done, n, __ATOMIC_RELEASE);
+  }
+  __atomic_store_n(&st->rec->state, (int64_t)PF_LOAD_SUCCESS, __ATOMIC_RELEASE);
+}
+
+void pf_load_state_set_error(pf_load_state* st) {
+  __atomic_store_n(&st->rec->state, (int64_t)PF_LOAD_ERROR, __ATOMIC_RELEASE);
+}
+
+uint32_t pf_load_state_num_layers(const pf_load_state* st) {
+  return st->ext ? __atomic_load_n(&st->ext->num_layers, __ATOMIC_ACQUIRE) : 0;
+}
+
+int64_t pf_load_state_layers_done(const pf_load_state* st) {
+  if (!st->ext) return pf_load_state_get(st) == PF_LOAD_SUCCESS ? 1 : 0;
+  return __atomic_load_n(&st->ext->layers_done, __ATOMIC_ACQUIRE);
+}
+
+void pf_load_state_set_layers_done(pf_load_state* st, int64_t n) {
+  if (st->ext) __atomic_store_n(&st->ext->layers_done, n, __ATOMIC_RELEASE);
+}
+
+}  // extern "C"

@@ -1,0 +1,442 @@
+// pf_runtime.cpp — devices, streams, events, device memory and the pinned
+// host pool backing (the roles of cudarc's CudaContext/CudaStream and of
+// pegaflow-core/src/pinned_mem.rs in the reference).
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <map>
+#include <mutex>
+#include <sstream>
+#include <string>
+
+#include "pf_common.h"
+
+namespace pf {
+
+// ---------------------------------------------------------------------------
+// Pinned allocation registry.
+// ---------------------------------------------------------------------------
+static std::mutex g_pinned_mu;
+static std::map<uint64_t, uint64_t> g_pinned;  // base -> size
+
+void pinned_register(uint64_t base, uint64_t size) {
+  std::lock_guard<std::mutex> lk(g_pinned_mu);
+  g_pinned[base] = size;
+}
+
+void pinned_unregister(uint64_t base) {
+  std::lock_guard<std::mutex> lk(g_pinned_mu);
+  g_pinned.erase(base);
+}
+
+bool pinned_lookup(uint64_t addr, uint64_t len, uint64_t* base, uint64_t* end) {
+  std::lock_guard<std::mutex> lk(g_pinned_mu);
+  auto it = g_pinned.upper_bound(addr);
+  if (it == g_pinned.begin()) return false;
+  --it;
+  uint64_t b = it->first, e = it->first + it->second;
+  if (addr < b || addr + len > e || addr + len < addr) return false;
+  if (base) *base = b;
+  if (end) *end = e;
+  return true;
+}
+
+bool RangeCache::contains(uint64_t a, uint64_t len) {
+  const uint64_t e = a + len;
+  if (e < a) return false;
+  if (a >= last_b_ && e <= last_e_ && last_e_ > last_b_) return true;
+  for (auto& r : ok_)
+    if (a >= r.first && e <= r.second) {
+      last_b_ = r.first;
+      last_e_ = r.second;
+      return true;
+    }
+  return false;
+}
+
+bool RangeCache::check(uint64_t a, uint64_t len) {
+  if (a == 0 || a + len < a) return false;
+  if (contains(a, len)) return true;
+  uint64_t b = 0, e = 0;
+  if (pinned_lookup(a, len, &b, &e)) {
+    ok_.push_back({b, e});
+    last_b_ = b;
+    last_e_ = e;
+    return true;
+  }
+  hipPointerAttribute_t attr;
+  hipError_t err = hipPointerGetAttributes(&attr, reinterpret_cast<void*>(a));
+  if (err != hipSuccess) {
+    (void)hipGetLastError();  // clear the sticky error of the probe
+    return false;
+  }
+  if (attr.type != hipMemoryTypeDevice) return false;
+  hipDeviceptr_t base = nullptr;
+  size_t size = 0;
+  err = hipMemGetAddressRange(&base, &size, reinterpret_cast<hipDeviceptr_t>(a));
+  if (err != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  b = reinterpret_cast<uint64_t>(base);
+  e = b + size;
+  if (a < b || a + len > e) return false;
+  ok_.push_back({b, e});
+  last_b_ = b;
+  last_e_ = e;
+  return true;
+}
+
+static int check_range(uint64_t addr, uint64_t len, const char* what) {
+  RangeCache rc;
+  if (!rc.check(addr, len))
+    return fail(PF_ERR_INVALID_ARGUMENT,
+                strf("%s: range [0x%llx, +%llu) is not inside one device or pinned "
+                     "allocation",
+                     what, (unsigned long long)addr, (unsigned long long)len));
+  return PF_OK;
+}
+
+// Wall-clock rate per device (kHz), cached by pf_init.
+static std::mutex g_dev_mu;
+static std::map<int, int> g_wall_khz;
+
+static int wall_clock_khz() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  {
+    std::lock_guard<std::mutex> lk(g_dev_mu);
+    auto it = g_wall_khz.find(dev);
+    if (it != g_wall_khz.end()) return it->second;
+  }
+  int khz = 0;
+  if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess)
+    khz = 0;
+  std::lock_guard<std::mutex> lk(g_dev_mu);
+  g_wall_khz[dev] = khz;
+  return khz;
+}
+
+}  // namespace pf
+
+using namespace pf;
+
+extern "C" {
+
+int pf_get_device_count(int* count) {
+  PF_HIP(hipGetDeviceCount(count));
+  return PF_OK;
+}
+
+int pf_init(int device) {
+  if (device < 0) return fail(PF_ERR_INVALID_ARGUMENT, "device_id must be >= 0");
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount");
+  if (device >= n)
+    return fail(PF_ERR_INIT, strf("device %d not present (%d devices)", device, n));
+  PF_HIP(hipSetDevice(device));
+  if (wall_clock_khz() <= 0)
+    return fail(PF_ERR_INIT, "hipDeviceAttributeWallClockRate unavailable");
+  return PF_OK;
+}
+
+int pf_set_device(int device) {
+  PF_HIP(hipSetDevice(device));
+  return PF_OK;
+}
+
+int pf_get_device(int* device) {
+  PF_HIP(hipGetDevice(device));
+  return PF_OK;
+}
+
+int pf_device_synchronize(void) {
+  PF_HIP(hipDeviceSynchronize());
+  return PF_OK;
+}
+
+int pf_stream_create(pf_stream* out) {
+  hipStream_t s = nullptr;
+  PF_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  *out = s;
+  return PF_OK;
+}
+
+int pf_stream_destroy(pf_stream stream) {
+  PF_HIP(hipStreamDestroy(static_cast<hipStream_t>(stream)));
+  return PF_OK;
+}
+
+int pf_stream_synchronize(pf_stream stream) {
+  PF_HIP(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+  return PF_OK;
+}
+
+int pf_stream_wait_event(pf_stream stream, pf_event event) {
+  PF_HIP(hipStreamWaitEvent(static_cast<hipStream_t>(stream),
+                            static_cast<hipEvent_t>(event), 0));
+  return PF_OK;
+}
+
+int pf_event_create(pf_event* out) {
+  hipEvent_t e = nullptr;
+  PF_HIP(hipEventCreate(&e));
+  *out = e;
+  return PF_OK;
+}
+
+int pf_event_destroy(pf_event event) {
+  PF_HIP(hipEventDestroy(static_cast<hipEvent_t>(event)));
+  return PF_OK;
+}
+
+int pf_event_record(pf_event event, pf_stream stream) {
+  PF_HIP(hipEventRecord(static_cast<hipEvent_t>(event),
+                        static_cast<hipStream_t>(stream)));
+  return PF_OK;
+}
+
+int pf_event_synchronize(pf_event event) {
+  PF_HIP(hipEventSynchronize(static_cast<hipEvent_t>(event)));
+  return PF_OK;
+}
+
+int pf_event_query(pf_event event, int* done) {
+  hipError_t e = hipEventQuery(static_cast<hipEvent_t>(event));
+  if (e == hipSuccess) {
+    *done = 1;
+    return PF_OK;
+  }
+  if (e == hipErrorNotReady) {
+    *done = 0;
+    return PF_OK;
+  }
+  return hip_fail(e, "hipEventQuery");
+}
+
+int pf_event_elapsed_ms(pf_event start, pf_event end, float* ms) {
+  PF_HIP(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start),
+                             static_cast<hipEvent_t>(end)));
+  return PF_OK;
+}
+
+int pf_device_malloc(uint64_t size, uint64_t* out_dev_ptr) {
+  if (size == 0) return fail(PF_ERR_ZERO_SIZE, "size must be greater than zero");
+  void* p = nullptr;
+  PF_HIP(hipMalloc(&p, size));
+  *out_dev_ptr = reinterpret_cast<uint64_t>(p);
+  return PF_OK;
+}
+
+int pf_device_free(uint64_t dev_ptr) {
+  PF_HIP(hipFree(reinterpret_cast<void*>(dev_ptr)));
+  return PF_OK;
+}
+
+int pf_memcpy_h2d(uint64_t dst_dev, const void* src, uint64_t size) {
+  PF_HIP(hipMemcpy(reinterpret_cast<void*>(dst_dev), src, size,
+                   hipMemcpyHostToDevice));
+  return PF_OK;
+}
+
+int pf_memcpy_d2h(void* dst, uint64_t src_dev, uint64_t size) {
+  PF_HIP(hipMemcpy(dst, reinterpret_cast<const void*>(src_dev), size,
+                   hipMemcpyDeviceToHost));
+  return PF_OK;
+}
+
+int pf_memcpy_d2d(uint64_t dst_dev, uint64_t src_dev, uint64_t size) {
+  PF_HIP(hipMemcpy(reinterpret_cast<void*>(dst_dev),
+                   reinterpret_cast<const void*>(src_dev), size,
+                   hipMemcpyDeviceToDevice));
+  return PF_OK;
+}
+
+int pf_memset_d8(uint64_t dst_dev, uint8_t value, uint64_t size) {
+  PF_HIP(hipMemset(reinterpret_cast<void*>(dst_dev), value, size));
+  return PF_OK;
+}
+
+int pf_mem_get_info(uint64_t* free_bytes, uint64_t* total_bytes) {
+  size_t f = 0, t = 0;
+  PF_HIP(hipMemGetInfo(&f, &t));
+  *free_bytes = f;
+  *total_bytes = t;
+  return PF_OK;
+}
+
+// PinnedMemory::allocate (pinned_mem.rs:128-164).  The reference asks CUDA for
+// write-combined memory; HIP does not implement that flag, so the pool is
+// ordinary pinned memory, always mapped so the transfer kernels can reach it.
+int pf_pinned_allocate(uint64_t size, uint32_t flags, void** host_ptr,
+                       uint64_t* dev_ptr) {
+  if (size == 0) return fail(PF_ERR_ZERO_SIZE, "size must be greater than zero");
+  if (!host_ptr) return fail(PF_ERR_INVALID_ARGUMENT, "null host_ptr");
+  if ((flags & PF_PINNED_COHERENT) && (flags & PF_PINNED_NONCOHERENT))
+    return fail(PF_ERR_INVALID_ARGUMENT, "coherent and non-coherent are exclusive");
+  unsigned hip_flags = hipHostMallocMapped | hipHostMallocPortable;
+  if (flags & PF_PINNED_COHERENT) hip_flags |= hipHostMallocCoherent;
+  if (flags & PF_PINNED_NONCOHERENT) hip_flags |= hipHostMallocNonCoherent;
+  if (flags & PF_PINNED_NUMA_USER) hip_flags |= hipHostMallocNumaUser;
+  void* p = nullptr;
+  hipError_t e = hipHostMalloc(&p, size, hip_flags);
+  if (e != hipSuccess)
+    return fail(PF_ERR_HIP, strf("hipHostMalloc failed: %s (%d)",
+                                 hipGetErrorString(e), static_cast<int>(e)));
+  void* d = nullptr;
+  e = hipHostGetDevicePointer(&d, p, 0);
+  if (e != hipSuccess) {
+    (void)hipHostFree(p);
+    return hip_fail(e, "hipHostGetDevicePointer");
+  }
+  if (d != p) {
+    // The kernels address host memory through the host pointer itself; a
+    // platform that maps it elsewhere is not supported.
+    (void)hipHostFree(p);
+    return fail(PF_ERR_UNSUPPORTED,
+                "pinned memory is not mapped at its host address");
+  }
+  pinned_register(reinterpret_cast<uint64_t>(p), size);
+  *host_ptr = p;
+  if (dev_ptr) *dev_ptr = reinterpret_cast<uint64_t>(d);
+  return PF_OK;
+}
+
+int pf_pinned_free(void* host_ptr) {
+  if (!host_ptr) return PF_OK;
+  pinned_unregister(reinterpret_cast<uint64_t>(host_ptr));
+  PF_HIP(hipHostFree(host_ptr));
+  return PF_OK;
+}
+
+int pf_host_device_pointer(const void* host_ptr, uint64_t* dev_ptr) {
+  void* d = nullptr;
+  PF_HIP(hipHostGetDevicePointer(&d, const_cast<void*>(host_ptr), 0));
+  *dev_ptr = reinterpret_cast<uint64_t>(d);
+  return PF_OK;
+}
+
+// pinned_mem.rs:38-52: "Hugepagesize:       2048 kB" -> bytes.
+uint64_t pf_huge_page_size(void) {
+  std::ifstream f("/proc/meminfo");
+  std::string line;
+  while (std::getline(f, line)) {
+    if (line.rfind("Hugepagesize:", 0) == 0) {
+      std::istringstream ss(line);
+      std::string key, unit;
+      uint64_t kb = 0;
+      if ((ss >> key >> kb >> unit) && unit == "kB") return kb * 1024;
+      return 0;
+    }
+  }
+  return 0;
+}
+
+// ---------------------------------------------------------------------------
+// Synthetic data and verification.
+// ---------------------------------------------------------------------------
+int pf_fill_random(uint64_t dst_dev, uint64_t size_bytes, uint64_t seed,
+                   uint64_t word_offset, pf_stream stream) {
+  if (size_bytes % 8 != 0 || dst_dev % 8 != 0)
+    return fail(PF_ERR_INVALID_ARGUMENT, "fill needs 8-byte aligned size and address");
+  if (size_bytes == 0) return PF_OK;
+  if (int rc = check_range(dst_dev, size_bytes, "fill")) return rc;
+  (void)hipGetLastError();
+  PF_HIP(launch_fill_random(dst_dev, size_bytes, seed, word_offset,
+                            static_cast<hipStream_t>(stream)));
+  return PF_OK;
+}
+
+static int run_count_kernel(int which, uint64_t a, uint64_t b, uint64_t size,
+                            uint64_t seed, uint64_t word_offset,
+                            uint64_t* mismatches) {
+  unsigned long long* d_count = nullptr;
+  PF_HIP(hipMalloc(&d_count, sizeof(unsigned long long)));
+  hipError_t e = hipMemset(d_count, 0, sizeof(unsigned long long));
+  if (e == hipSuccess) {
+    (void)hipGetLastError();
+    e = which == 0 ? launch_verify_random(a, size, seed, word_offset, d_count, nullptr)
+                   : launch_compare(a, b, size, d_count, nullptr);
+  }
+  unsigned long long h = 0;
+  if (e == hipSuccess) e = hipMemcpy(&h, d_count, sizeof(h), hipMemcpyDeviceToHost);
+  (void)hipFree(d_count);
+  if (e != hipSuccess) return hip_fail(e, which == 0 ? "verify kernel" : "compare kernel");
+  *mismatches = h;
+  return PF_OK;
+}
+
+int pf_verify_random(uint64_t addr, uint64_t size_bytes, uint64_t seed,
+                     uint64_t word_offset, uint64_t* mismatches) {
+  if (size_bytes % 8 != 0 || addr % 8 != 0)
+    return fail(PF_ERR_INVALID_ARGUMENT, "verify needs 8-byte aligned size and address");
+  if (size_bytes == 0) {
+    *mismatches = 0;
+    return PF_OK;
+  }
+  if (int rc = check_range(addr, size_bytes, "verify")) return rc;
+  return run_count_kernel(0, addr, 0, size_bytes, seed, word_offset, mismatches);
+}
+
+int pf_verify_random_chunks(const uint64_t* addrs, const uint64_t* word_offsets,
+                            uint64_t n, uint64_t chunk_bytes, uint64_t seed,
+                            uint64_t* mismatches) {
+  if (chunk_bytes % 8 != 0)
+    return fail(PF_ERR_INVALID_ARGUMENT, "verify needs an 8-byte multiple chunk size");
+  for (uint64_t i = 0; i < n; ++i)
+    if (addrs[i] % 8 != 0)
+      return fail(PF_ERR_INVALID_ARGUMENT, "verify needs 8-byte aligned chunk addresses");
+  *mismatches = 0;
+  if (n == 0 || chunk_bytes == 0) return PF_OK;
+  {
+    RangeCache rc;
+    for (uint64_t i = 0; i < n; ++i)
+      if (!rc.check(addrs[i], chunk_bytes))
+        return fail(PF_ERR_INVALID_ARGUMENT,
+                    strf("verify: chunk %llu [0x%llx, +%llu) is not inside one device or "
+                         "pinned allocation",
+                         (unsigned long long)i, (unsigned long long)addrs[i],
+                         (unsigned long long)chunk_bytes));
+  }
+  uint64_t* d = nullptr;
+  unsigned long long* d_count = nullptr;
+  PF_HIP(hipMalloc(&d, 2 * n * sizeof(uint64_t) + sizeof(unsigned long long)));
+  d_count = reinterpret_cast<unsigned long long*>(d + 2 * n);
+  hipError_t e = hipMemcpy(d, addrs, n * sizeof(uint64_t), hipMemcpyHostToDevice);
+  if (e == hipSuccess)
+    e = hipMemcpy(d + n, word_offsets, n * sizeof(uint64_t), hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemset(d_count, 0, sizeof(unsigned long long));
+  if (e == hipSuccess) {
+    (void)hipGetLastError();
+    e = launch_verify_random_chunks(d, d + n, n, chunk_bytes, seed, d_count, nullptr);
+  }
+  unsigned long long h = 0;
+  if (e == hipSuccess) e = hipMemcpy(&h, d_count, sizeof(h), hipMemcpyDeviceToHost);
+  (void)hipFree(d);
+  if (e != hipSuccess) return hip_fail(e, "verify chunks kernel");
+  *mismatches = h;
+  return PF_OK;
+}
+
+int pf_compare(uint64_t a, uint64_t b, uint64_t size_bytes,
+               uint64_t* mismatches) {
+  if (size_bytes == 0) {
+    *mismatches = 0;
+    return PF_OK;
+  }
+  if (int rc = check_range(a, size_bytes, "compare")) return rc;
+  if (int rc = check_range(b, size_bytes, "compare")) return rc;
+  return run_count_kernel(1, a, b, size_bytes, 0, 0, mismatches);
+}
+
+int pf_spin(pf_stream stream, uint32_t microseconds) {
+  int khz = wall_clock_khz();
+  if (khz <= 0) return fail(PF_ERR_INIT, "wall clock rate unknown (call pf_init)");
+  uint64_t ticks = static_cast<uint64_t>(microseconds) * static_cast<uint64_t>(khz) / 1000;
+  (void)hipGetLastError();
+  PF_HIP(launch_spin(ticks, static_cast<hipStream_t>(stream)));
+  return PF_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,791 @@
+// pf_transfer.cpp — the transfer module: reference-equivalent DMA primitives
+// (transfer.rs) and the batched transfer context that replaces the per-call
+// copy loops of gpu_worker.rs with gather/scatter kernels.
+#include <algorithm>
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+#include "pf_common.h"
+
+using namespace pf;
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// Chunk planning.  A layer's transfer is a list of equal-size chunks, each
+// pairing a device address inside the paged layer tensor with an address on
+// the other side (host pinned memory, or any device-visible buffer).
+// ---------------------------------------------------------------------------
+struct Chunk {
+  uint64_t dev;   // address inside the layer tensor
+  uint64_t host;  // address on the host (or staging) side
+};
+
+struct LayerPlan {
+  uint64_t chunk_bytes = 0;
+  std::vector<Chunk> chunks;
+  // The reference merges the K list and the V list of a split layer in two
+  // separate batch_copy_segments_to_gpu calls (gpu_worker.rs:242-256); runs
+  // never cross this index.
+  size_t list_break = 0;
+  // True when the chunks must be copied one after another in list order to
+  // reproduce the reference's result (see needs_order below).
+  bool ordered = false;
+};
+
+// Chunks of distinct blocks never overlap in the layer tensor: split layouts
+// whose V region starts past the K region, and single-segment layouts.  Other
+// registrations (allowed by the reference's validation, never produced by
+// vLLM) can make two blocks' chunks overlap, where the reference's in-order
+// copies decide which bytes win.
+bool device_chunks_disjoint(const pf_kv_layout& l) {
+  const int kind = layout_kind(l);
+  if (kind == PF_LAYOUT_SPLIT) {
+    uint64_t k_end = 0;
+    return !__builtin_mul_overflow(l.num_blocks, l.bytes_per_block, &k_end) &&
+           l.kv_stride_bytes >= k_end;
+  }
+  return kind == PF_LAYOUT_CONTIGUOUS && l.segments <= 1;
+}
+
+// Host-side chunks are pairwise disjoint (checked in O(n) for the usual
+// increasing order, else after sorting a copy).
+bool host_chunks_disjoint(const LayerPlan& p) {
+  bool increasing = true;
+  for (size_t i = 1; i < p.chunks.size() && increasing; ++i)
+    increasing = p.chunks[i].host >= p.chunks[i - 1].host + p.chunk_bytes;
+  if (increasing) return true;
+  std::vector<uint64_t> h(p.chunks.size());
+  for (size_t i = 0; i < h.size(); ++i) h[i] = p.chunks[i].host;
+  std::sort(h.begin(), h.end());
+  for (size_t i = 1; i < h.size(); ++i)
+    if (h[i] < h[i - 1] + p.chunk_bytes) return false;
+  return true;
+}
+
+int plan_layer(const pf_layer_xfer& lx, bool is_save, LayerPlan* out) {
+  const pf_kv_layout& l = lx.layout;
+  if (l.bytes_per_block == 0 || l.segments == 0 || l.num_blocks == 0)
+    return fail(PF_ERR_INVALID_ARGUMENT, "invalid KV cache layout");
+  if (lx.num_blocks > 0 && !lx.blocks)
+    return fail(PF_ERR_INVALID_ARGUMENT, "null block list");
+  const uint64_t seg = l.bytes_per_block;
+  const int kind = layout_kind(l);
+  out->chunks.clear();
+  for (uint64_t i = 0; i < lx.num_blocks; ++i) {
+    if (lx.blocks[i].block_idx < 0)
+      return fail(PF_ERR_INVALID_ARGUMENT,
+                  strf("block index %lld must be >= 0",
+                       (long long)lx.blocks[i].block_idx));
+    if (lx.blocks[i].k_host == 0)
+      return fail(PF_ERR_INVALID_ARGUMENT, "null host address for block");
+  }
+  uint64_t off = 0;
+  if (kind == PF_LAYOUT_SPLIT) {
+    // gpu_worker.rs:226-240 (load) and 334-360 (save): K list, then V list.
+    out->chunk_bytes = seg;
+    out->chunks.reserve(lx.num_blocks * 2);
+    for (uint64_t i = 0; i < lx.num_blocks; ++i) {
+      const pf_block_xfer& b = lx.blocks[i];
+      if (int rc = segment_offset(l, static_cast<uint64_t>(b.block_idx), 0, &off)) return rc;
+      out->chunks.push_back({l.data_ptr + off, b.k_host});
+    }
+    out->list_break = out->chunks.size();
+    for (uint64_t i = 0; i < lx.num_blocks; ++i) {
+      const pf_block_xfer& b = lx.blocks[i];
+      if (int rc = segment_offset(l, static_cast<uint64_t>(b.block_idx), 1, &off)) return rc;
+      out->chunks.push_back({l.data_ptr + off, b.v_host ? b.v_host : b.k_host + seg});
+    }
+    return PF_OK;
+  }
+  if (kind == PF_LAYOUT_STRIDED && is_save) {
+    // copy_gpu_to_cpu_strided (transfer.rs:217-239): segment s of block b to
+    // dst + s * bytes_per_block.
+    out->chunk_bytes = seg;
+    out->chunks.reserve(lx.num_blocks * l.segments);
+    for (uint64_t i = 0; i < lx.num_blocks; ++i) {
+      const pf_block_xfer& b = lx.blocks[i];
+      for (uint64_t s = 0; s < l.segments; ++s) {
+        if (int rc = segment_offset(l, static_cast<uint64_t>(b.block_idx), s, &off)) return rc;
+        out->chunks.push_back({l.data_ptr + off, b.k_host + s * seg});
+      }
+    }
+    out->list_break = out->chunks.size();
+    return PF_OK;
+  }
+  // Whole block of block_size_bytes at segment_offset(b, 0): the contiguous
+  // save (transfer.rs:206-210) and every non-split load (gpu_worker.rs:260-282).
+  const uint64_t bs = l.block_size_bytes;
+  out->chunk_bytes = bs;
+  out->chunks.reserve(lx.num_blocks);
+  for (uint64_t i = 0; i < lx.num_blocks; ++i) {
+    const pf_block_xfer& b = lx.blocks[i];
+    if (int rc = segment_offset(l, static_cast<uint64_t>(b.block_idx), 0, &off)) return rc;
+    uint64_t end = 0;
+    if (__builtin_add_overflow(off, bs, &end) || end > l.size_bytes)
+      return fail(PF_ERR_STORAGE,
+                  strf("Block %lld exceeds registered memory (offset %llu, size "
+                       "%llu, limit %llu)",
+                       (long long)b.block_idx, (unsigned long long)off,
+                       (unsigned long long)bs, (unsigned long long)l.size_bytes));
+    out->chunks.push_back({l.data_ptr + off, b.k_host});
+  }
+  out->list_break = out->chunks.size();
+  return PF_OK;
+}
+
+// Parallel kernels give the reference's bytes only when no two chunks write
+// the same byte.  The reference copies in list order, so for a load that
+// names a block twice the later copy wins: only the last occurrence is kept.
+// Layouts whose blocks can overlap, loads naming a block past num_blocks, and
+// kernel saves to overlapping host ranges are copied in list order instead.
+// (The staged save writes the host side with in-order copies already.)
+void apply_write_policy(const pf_layer_xfer& lx, bool is_save, bool staged, LayerPlan* p) {
+  p->ordered = false;
+  if (p->chunks.empty()) return;
+  if (is_save) {
+    p->ordered = !staged && !host_chunks_disjoint(*p);
+    return;
+  }
+  if (!device_chunks_disjoint(lx.layout)) {
+    p->ordered = true;
+    return;
+  }
+  const uint64_t nb = lx.layout.num_blocks;
+  const size_t n = static_cast<size_t>(lx.num_blocks);
+  std::vector<uint8_t> seen(static_cast<size_t>(nb), 0);
+  std::vector<uint8_t> keep(n, 1);
+  bool any_dup = false;
+  for (size_t i = n; i-- > 0;) {
+    const uint64_t b = static_cast<uint64_t>(lx.blocks[i].block_idx);
+    if (b >= nb) {
+      p->ordered = true;
+      return;
+    }
+    if (seen[b]) {
+      keep[i] = 0;
+      any_dup = true;
+    } else {
+      seen[b] = 1;
+    }
+  }
+  if (!any_dup) return;
+  const size_t per_block = p->chunks.size() / n;  // 2 for split, 1 otherwise
+  std::vector<Chunk> kept;
+  kept.reserve(p->chunks.size());
+  for (size_t part = 0; part < per_block; ++part) {
+    for (size_t i = 0; i < n; ++i)
+      if (keep[i]) kept.push_back(p->chunks[part * n + i]);
+    if (part == 0) p->list_break = kept.size();
+  }
+  p->chunks.swap(kept);
+  if (per_block == 1) p->list_break = p->chunks.size();
+}
+
+// The layer tensor must lie inside one device allocation and each host-side
+// chunk inside one pinned or device allocation (RangeCache, pf_runtime.cpp).
+int check_device_tensor(RangeCache& rc, const pf_kv_layout& l) {
+  if (!rc.check(l.data_ptr, l.size_bytes))
+    return fail(PF_ERR_INVALID_ARGUMENT,
+                strf("layer tensor [0x%llx, +%llu) is not inside one device "
+                     "allocation",
+                     (unsigned long long)l.data_ptr, (unsigned long long)l.size_bytes));
+  return PF_OK;
+}
+
+int check_host_chunks(RangeCache& rc, const LayerPlan& p) {
+  for (const Chunk& c : p.chunks)
+    if (!rc.check(c.host, p.chunk_bytes))
+      return fail(PF_ERR_INVALID_ARGUMENT,
+                  strf("host range [0x%llx, +%llu) is not device-accessible "
+                       "(allocate it with pf_pinned_allocate)",
+                       (unsigned long long)c.host, (unsigned long long)p.chunk_bytes));
+  return PF_OK;
+}
+
+// Greedy run merging of transfer.rs:134-177 over chunks [begin, end): a run
+// grows while the device and host addresses both continue chunk_bytes past
+// the run's start.  Calls fn(first_chunk_index, n_chunks) per run.
+template <class F>
+void for_each_run(const LayerPlan& p, size_t begin, size_t end, F fn) {
+  size_t i = begin;
+  const uint64_t cb = p.chunk_bytes;
+  while (i < end) {
+    size_t n = 1;
+    while (i + n < end && p.chunks[i + n].dev == p.chunks[i].dev + n * cb &&
+           p.chunks[i + n].host == p.chunks[i].host + n * cb)
+      ++n;
+    fn(i, n);
+    i += n;
+  }
+}
+
+bool aligned16(uint64_t v) { return (v & 15u) == 0; }
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Transfer context.
+// ---------------------------------------------------------------------------
+struct pf_xfer {
+  int device = 0;
+  hipStream_t stream = nullptr;  // kernels; DMA for the DMA modes
+  hipStream_t dma = nullptr;     // link-side copies of the staged mode
+  ChunkDesc* d_desc = nullptr;
+  size_t d_cap = 0;
+  ChunkDesc* h_desc = nullptr;
+  size_t h_cap = 0;
+  hipEvent_t desc_uploaded = nullptr;
+  bool desc_inflight = false;
+  uint64_t staging = 0;
+  uint64_t slot_bytes = 0;
+  hipEvent_t slot_ready[2] = {nullptr, nullptr};
+  hipEvent_t slot_free[2] = {nullptr, nullptr};
+  uint32_t threads = 256;
+  uint32_t unroll = 8;
+  uint64_t last_kernels = 0;
+  uint64_t last_dma = 0;
+  bool timing = false;
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> timers;  // one pair per launch
+  std::mutex mu;
+};
+
+namespace {
+
+int ensure_desc_capacity(pf_xfer* x, size_t n) {
+  // The host staging of descriptors may still be read by the previous call's
+  // upload; wait for it before rewriting.
+  if (x->desc_inflight) {
+    PF_HIP(hipEventSynchronize(x->desc_uploaded));
+    x->desc_inflight = false;
+  }
+  if (n > x->h_cap) {
+    size_t cap = 1;
+    while (cap < n) cap <<= 1;
+    if (x->h_desc) PF_HIP(hipHostFree(x->h_desc));
+    x->h_desc = nullptr;
+    x->h_cap = 0;
+    PF_HIP(hipHostMalloc(reinterpret_cast<void**>(&x->h_desc), cap * sizeof(ChunkDesc),
+                         hipHostMallocDefault));
+    x->h_cap = cap;
+  }
+  if (n > x->d_cap) {
+    size_t cap = 1;
+    while (cap < n) cap <<= 1;
+    // Kernels of earlier calls may still read the old buffer.
+    PF_HIP(hipStreamSynchronize(x->stream));
+    if (x->d_desc) PF_HIP(hipFree(x->d_desc));
+    x->d_desc = nullptr;
+    x->d_cap = 0;
+    PF_HIP(hipMalloc(reinterpret_cast<void**>(&x->d_desc), cap * sizeof(ChunkDesc)));
+    x->d_cap = cap;
+  }
+  return PF_OK;
+}
+
+int upload_desc(pf_xfer* x, size_t n) {
+  if (n == 0) return PF_OK;
+  PF_HIP(hipMemcpyAsync(x->d_desc, x->h_desc, n * sizeof(ChunkDesc),
+                        hipMemcpyHostToDevice, x->stream));
+  PF_HIP(hipEventRecord(x->desc_uploaded, x->stream));
+  x->desc_inflight = true;
+  return PF_OK;
+}
+
+int launch(pf_xfer* x, size_t first, size_t n, uint64_t chunk_bytes, bool al16) {
+  if (n == 0) return PF_OK;
+  if (n > 0xffffffffull) return fail(PF_ERR_INVALID_ARGUMENT, "too many chunks");
+  if (chunk_bytes / 16 >= (1ull << 31))
+    return fail(PF_ERR_INVALID_ARGUMENT, "chunk too large");
+  std::pair<hipEvent_t, hipEvent_t>* tm = nullptr;
+  if (x->timing) {
+    if (x->last_kernels >= x->timers.size()) {
+      std::pair<hipEvent_t, hipEvent_t> p{nullptr, nullptr};
+      PF_HIP(hipEventCreate(&p.first));
+      PF_HIP(hipEventCreate(&p.second));
+      x->timers.push_back(p);
+    }
+    tm = &x->timers[x->last_kernels];
+    PF_HIP(hipEventRecord(tm->first, x->stream));
+  }
+  (void)hipGetLastError();
+  hipError_t e = launch_copy_chunks(x->d_desc + first, static_cast<uint32_t>(n),
+                                    chunk_bytes, al16, x->threads, x->unroll,
+                                    x->stream);
+  if (e != hipSuccess) return hip_fail(e, "gather/scatter kernel launch");
+  if (tm) PF_HIP(hipEventRecord(tm->second, x->stream));
+  x->last_kernels++;
+  return PF_OK;
+}
+
+// A staged slice: chunks [begin, end) of one layer packed into one slot.
+struct Slice {
+  uint32_t layer;
+  size_t begin, end;
+  int slot;
+  size_t desc_first;  // descriptors for the slice's kernel
+};
+
+int plan_all(const pf_layer_xfer* layers, uint32_t n, bool is_save,
+             std::vector<LayerPlan>* plans) {
+  plans->resize(n);
+  for (uint32_t i = 0; i < n; ++i)
+    if (int rc = plan_layer(layers[i], is_save, &(*plans)[i])) return rc;
+  return PF_OK;
+}
+
+int check_all_kernel(const pf_layer_xfer* layers, const std::vector<LayerPlan>& plans,
+                     bool host_side) {
+  RangeCache rc;
+  for (size_t i = 0; i < plans.size(); ++i) {
+    if (plans[i].chunks.empty() || plans[i].ordered) continue;
+    if (int r = check_device_tensor(rc, layers[i].layout)) return r;
+    if (host_side)
+      if (int r = check_host_chunks(rc, plans[i])) return r;
+  }
+  return PF_OK;
+}
+
+bool chunks_aligned(const LayerPlan& p) {
+  if (!aligned16(p.chunk_bytes)) return false;
+  for (const Chunk& c : p.chunks)
+    if (!aligned16(c.dev) || !aligned16(c.host)) return false;
+  return true;
+}
+
+// ---- DMA modes ------------------------------------------------------------
+int dma_layer(pf_xfer* x, const LayerPlan& p, bool is_save, bool per_chunk_sync) {
+  hipError_t e = hipSuccess;
+  auto issue = [&](size_t i, size_t n) {
+    if (e != hipSuccess) return;
+    const Chunk& c = p.chunks[i];
+    const uint64_t bytes = n * p.chunk_bytes;
+    if (is_save)
+      e = hipMemcpyAsync(reinterpret_cast<void*>(c.host), reinterpret_cast<void*>(c.dev),
+                         bytes, hipMemcpyDefault, x->stream);
+    else
+      e = hipMemcpyAsync(reinterpret_cast<void*>(c.dev), reinterpret_cast<void*>(c.host),
+                         bytes, hipMemcpyDefault, x->stream);
+    if (e == hipSuccess && per_chunk_sync) e = hipStreamSynchronize(x->stream);
+    x->last_dma++;
+  };
+  if (per_chunk_sync) {
+    // gpu_worker.rs:344-371: one synchronous copy per segment, no merging.
+    for (size_t i = 0; i < p.chunks.size(); ++i) issue(i, 1);
+  } else {
+    for_each_run(p, 0, p.list_break, issue);
+    for_each_run(p, p.list_break, p.chunks.size(), issue);
+  }
+  if (e != hipSuccess)
+    return hip_fail(e, is_save ? "hipMemcpyDtoH" : "hipMemcpyHtoDAsync");
+  return PF_OK;
+}
+
+// ---- staged mode ----------------------------------------------------------
+int plan_slices(pf_xfer* x, const std::vector<LayerPlan>& plans,
+                std::vector<Slice>* slices, size_t* n_desc) {
+  size_t d = 0;
+  int slot = 0;
+  for (uint32_t li = 0; li < plans.size(); ++li) {
+    const LayerPlan& p = plans[li];
+    if (p.chunks.empty() || p.ordered) continue;
+    if (p.chunk_bytes > x->slot_bytes)
+      return fail(PF_ERR_INVALID_ARGUMENT,
+                  strf("staging slot (%llu bytes) smaller than one chunk (%llu)",
+                       (unsigned long long)x->slot_bytes,
+                       (unsigned long long)p.chunk_bytes));
+    const size_t per_slot = static_cast<size_t>(x->slot_bytes / p.chunk_bytes);
+    for (size_t b = 0; b < p.chunks.size(); b += per_slot) {
+      const size_t e = std::min(p.chunks.size(), b + per_slot);
+      slices->push_back({li, b, e, slot, d});
+      d += e - b;
+      slot ^= 1;
+    }
+  }
+  *n_desc = d;
+  return PF_OK;
+}
+
+// Host-contiguous runs inside a slice, packed in the staging slot in chunk
+// order: chunk k of the slice sits at slot + (k - begin) * chunk_bytes.
+template <class F>
+void for_each_host_run(const LayerPlan& p, size_t begin, size_t end, F fn) {
+  size_t i = begin;
+  while (i < end) {
+    size_t n = 1;
+    while (i + n < end && p.chunks[i + n].host == p.chunks[i].host + n * p.chunk_bytes) ++n;
+    fn(i, n);
+    i += n;
+  }
+}
+
+// One staged slice.  Save: the gather kernel packs the slice into the slot,
+// then the link-side stream copies each host-contiguous run out.  Load: the
+// link-side stream copies the runs into the slot, then the scatter kernel
+// places them.  slot_free / slot_ready order the two streams per slot.
+int staged_slice(pf_xfer* x, const std::vector<LayerPlan>& plans, const Slice& s,
+                 bool is_save) {
+  const LayerPlan& p = plans[s.layer];
+  const uint64_t slot_base = x->staging + static_cast<uint64_t>(s.slot) * x->slot_bytes;
+  const bool al16 = aligned16(p.chunk_bytes) && aligned16(slot_base) &&
+                    std::all_of(p.chunks.begin() + s.begin, p.chunks.begin() + s.end,
+                                [](const Chunk& c) { return aligned16(c.dev); });
+  hipError_t e = hipSuccess;
+  auto dma_run = [&](size_t i, size_t n) {
+    if (e != hipSuccess) return;
+    const uint64_t st = slot_base + (i - s.begin) * p.chunk_bytes;
+    const uint64_t bytes = n * p.chunk_bytes;
+    if (is_save)
+      e = hipMemcpyAsync(reinterpret_cast<void*>(p.chunks[i].host),
+                         reinterpret_cast<void*>(st), bytes, hipMemcpyDefault, x->dma);
+    else
+      e = hipMemcpyAsync(reinterpret_cast<void*>(st),
+                         reinterpret_cast<void*>(p.chunks[i].host), bytes,
+                         hipMemcpyDefault, x->dma);
+    x->last_dma++;
+  };
+  if (is_save) {
+    PF_HIP(hipStreamWaitEvent(x->stream, x->slot_free[s.slot], 0));
+    if (int rc = launch(x, s.desc_first, s.end - s.begin, p.chunk_bytes, al16)) return rc;
+    PF_HIP(hipEventRecord(x->slot_ready[s.slot], x->stream));
+    PF_HIP(hipStreamWaitEvent(x->dma, x->slot_ready[s.slot], 0));
+    for_each_host_run(p, s.begin, s.end, dma_run);
+    if (e != hipSuccess) return hip_fail(e, "staged hipMemcpyAsync (D2H)");
+    PF_HIP(hipEventRecord(x->slot_free[s.slot], x->dma));
+  } else {
+    PF_HIP(hipStreamWaitEvent(x->dma, x->slot_free[s.slot], 0));
+    for_each_host_run(p, s.begin, s.end, dma_run);
+    if (e != hipSuccess) return hip_fail(e, "staged hipMemcpyAsync (H2D)");
+    PF_HIP(hipEventRecord(x->slot_ready[s.slot], x->dma));
+    PF_HIP(hipStreamWaitEvent(x->stream, x->slot_ready[s.slot], 0));
+    if (int rc = launch(x, s.desc_first, s.end - s.begin, p.chunk_bytes, al16)) return rc;
+    PF_HIP(hipEventRecord(x->slot_free[s.slot], x->stream));
+  }
+  return PF_OK;
+}
+
+int staged(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<LayerPlan>& plans,
+           bool is_save, pf_event* layer_events) {
+  if (x->staging == 0 || x->slot_bytes == 0)
+    return fail(PF_ERR_INVALID_ARGUMENT, "transfer context has no staging buffer");
+  std::vector<Slice> slices;
+  size_t n_desc = 0;
+  if (int rc = plan_slices(x, plans, &slices, &n_desc)) return rc;
+  {
+    RangeCache rc;
+    for (size_t i = 0; i < plans.size(); ++i)
+      if (!plans[i].chunks.empty() && !plans[i].ordered)
+        if (int r = check_device_tensor(rc, layers[i].layout)) return r;
+  }
+  if (int rc = ensure_desc_capacity(x, n_desc)) return rc;
+  for (const Slice& s : slices) {
+    const LayerPlan& p = plans[s.layer];
+    const uint64_t slot_base = x->staging + static_cast<uint64_t>(s.slot) * x->slot_bytes;
+    for (size_t k = s.begin; k < s.end; ++k) {
+      const uint64_t st = slot_base + (k - s.begin) * p.chunk_bytes;
+      ChunkDesc& d = x->h_desc[s.desc_first + (k - s.begin)];
+      if (is_save) d = {p.chunks[k].dev, st};
+      else d = {st, p.chunks[k].dev};
+    }
+  }
+  if (int rc = upload_desc(x, n_desc)) return rc;
+  size_t si = 0;
+  for (uint32_t li = 0; li < plans.size(); ++li) {
+    if (plans[li].ordered) {
+      if (int rc = dma_layer(x, plans[li], is_save, false)) return rc;
+    }
+    for (; si < slices.size() && slices[si].layer == li; ++si)
+      if (int rc = staged_slice(x, plans, slices[si], is_save)) return rc;
+    if (!is_save && layer_events && layer_events[li])
+      PF_HIP(hipEventRecord(static_cast<hipEvent_t>(layer_events[li]), x->stream));
+  }
+  if (is_save) {
+    PF_HIP(hipStreamSynchronize(x->dma));
+    PF_HIP(hipStreamSynchronize(x->stream));
+  }
+  return PF_OK;
+}
+
+// ---- kernel mode ----------------------------------------------------------
+int kernel_direct(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<LayerPlan>& plans,
+                  bool is_save, pf_event* layer_events) {
+  if (int rc = check_all_kernel(layers, plans, true)) return rc;
+  size_t total = 0;
+  for (const auto& p : plans)
+    if (!p.ordered) total += p.chunks.size();
+  if (int rc = ensure_desc_capacity(x, total)) return rc;
+  size_t d = 0;
+  std::vector<size_t> first(plans.size());
+  for (size_t li = 0; li < plans.size(); ++li) {
+    first[li] = d;
+    if (plans[li].ordered) continue;
+    for (const Chunk& c : plans[li].chunks)
+      x->h_desc[d++] = is_save ? ChunkDesc{c.dev, c.host} : ChunkDesc{c.host, c.dev};
+  }
+  if (int rc = upload_desc(x, total)) return rc;
+  // Without per-layer events, consecutive layers with the same chunk size and
+  // alignment share one launch.
+  size_t li = 0;
+  while (li < plans.size()) {
+    const LayerPlan& p = plans[li];
+    if (p.ordered) {
+      if (int rc = dma_layer(x, p, is_save, false)) return rc;
+      if (layer_events && layer_events[li])
+        PF_HIP(hipEventRecord(static_cast<hipEvent_t>(layer_events[li]), x->stream));
+      ++li;
+      continue;
+    }
+    const bool al = chunks_aligned(p);
+    size_t lj = li + 1;
+    if (!layer_events) {
+      while (lj < plans.size() && !plans[lj].ordered &&
+             plans[lj].chunk_bytes == p.chunk_bytes &&
+             (plans[lj].chunks.empty() || chunks_aligned(plans[lj]) == al))
+        ++lj;
+    }
+    size_t n = 0;
+    for (size_t k = li; k < lj; ++k) n += plans[k].chunks.size();
+    if (int rc = launch(x, first[li], n, p.chunk_bytes, al)) return rc;
+    if (layer_events && layer_events[li])
+      PF_HIP(hipEventRecord(static_cast<hipEvent_t>(layer_events[li]), x->stream));
+    li = lj;
+  }
+  if (is_save) PF_HIP(hipStreamSynchronize(x->stream));
+  return PF_OK;
+}
+
+int run(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, uint32_t mode,
+        bool is_save, pf_event* layer_events) {
+  if (!x) return fail(PF_ERR_INVALID_ARGUMENT, "null transfer context");
+  if (num_layers > 0 && !layers) return fail(PF_ERR_INVALID_ARGUMENT, "null layer list");
+  std::lock_guard<std::mutex> lk(x->mu);
+  x->last_kernels = 0;
+  x->last_dma = 0;
+  PF_HIP(hipSetDevice(x->device));
+  std::vector<LayerPlan> plans;
+  if (int rc = plan_all(layers, num_layers, is_save, &plans)) return rc;
+  switch (mode) {
+    case PF_MODE_DMA_REFERENCE:
+    case PF_MODE_DMA_BATCHED: {
+      const bool per_chunk_sync = is_save && mode == PF_MODE_DMA_REFERENCE;
+      for (uint32_t li = 0; li < num_layers; ++li) {
+        if (int rc = dma_layer(x, plans[li], is_save, per_chunk_sync)) return rc;
+        if (!is_save && layer_events && layer_events[li])
+          PF_HIP(hipEventRecord(static_cast<hipEvent_t>(layer_events[li]), x->stream));
+      }
+      if (is_save) PF_HIP(hipStreamSynchronize(x->stream));
+      return PF_OK;
+    }
+    case PF_MODE_KERNEL:
+      for (uint32_t li = 0; li < num_layers; ++li)
+        apply_write_policy(layers[li], is_save, false, &plans[li]);
+      return kernel_direct(x, layers, plans, is_save, layer_events);
+    case PF_MODE_STAGED:
+      for (uint32_t li = 0; li < num_layers; ++li)
+        apply_write_policy(layers[li], is_save, true, &plans[li]);
+      return staged(x, layers, plans, is_save, layer_events);
+    default:
+      return fail(PF_ERR_INVALID_ARGUMENT, strf("unknown transfer mode %u", mode));
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+// ---------------------------------------------------------------------------
+// transfer.rs primitives.
+// ---------------------------------------------------------------------------
+int pf_copy_gpu_to_cpu(uint64_t gpu_base, uint64_t offset, void* cpu_buffer,
+                       uint64_t cpu_buffer_len, uint64_t size) {
+  if (cpu_buffer_len < size)
+    return fail(PF_ERR_STORAGE, strf("CPU buffer too small: %llu bytes, need %llu bytes",
+                                     (unsigned long long)cpu_buffer_len,
+                                     (unsigned long long)size));
+  hipError_t e = hipMemcpy(cpu_buffer, reinterpret_cast<void*>(gpu_base + offset), size,
+                           hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpyDtoH");
+  return PF_OK;
+}
+
+int pf_copy_cpu_to_gpu_async(uint64_t gpu_base, uint64_t offset, const void* cpu_buffer,
+                             uint64_t cpu_buffer_len, uint64_t size, pf_stream stream) {
+  if (cpu_buffer_len < size)
+    return fail(PF_ERR_STORAGE, strf("CPU buffer too small: %llu bytes, need %llu bytes",
+                                     (unsigned long long)cpu_buffer_len,
+                                     (unsigned long long)size));
+  hipError_t e = hipMemcpyAsync(reinterpret_cast<void*>(gpu_base + offset), cpu_buffer, size,
+                                hipMemcpyHostToDevice, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpyHtoDAsync");
+  return PF_OK;
+}
+
+int pf_batch_copy_segments_to_gpu(const uint64_t* gpu_offsets, const uint64_t* cpu_ptrs,
+                                  uint64_t count, uint64_t segment_size,
+                                  const pf_kv_layout* layout, pf_stream stream,
+                                  uint64_t* out_batches) {
+  uint64_t batches = 0;
+  uint64_t i = 0;
+  while (i < count) {
+    uint64_t n = 1;
+    while (i + n < count && gpu_offsets[i + n] == gpu_offsets[i] + n * segment_size &&
+           cpu_ptrs[i + n] == cpu_ptrs[i] + n * segment_size)
+      ++n;
+    uint64_t total = 0;
+    if (__builtin_mul_overflow(segment_size, n, &total))
+      return fail(PF_ERR_STORAGE, "batch_copy_segments_to_gpu: total_size overflow");
+    int rc = pf_copy_cpu_to_gpu_async(layout->data_ptr, gpu_offsets[i],
+                                      reinterpret_cast<const void*>(cpu_ptrs[i]), total,
+                                      total, stream);
+    if (rc) return rc;
+    ++batches;
+    i += n;
+  }
+  if (out_batches) *out_batches = batches;
+  return PF_OK;
+}
+
+int pf_copy_block_gpu_to_cpu(const pf_kv_layout* layout, uint64_t block_idx, void* dst) {
+  uint64_t off = 0;
+  const pf_kv_layout& l = *layout;
+  if (pf_is_contiguous_layout(layout)) {
+    if (int rc = segment_offset(l, block_idx, 0, &off)) return rc;
+    if (off + l.block_size_bytes > l.size_bytes)
+      return fail(PF_ERR_STORAGE, strf("Block %llu exceeds registered memory",
+                                       (unsigned long long)block_idx));
+    return pf_copy_gpu_to_cpu(l.data_ptr, off, dst, l.block_size_bytes, l.block_size_bytes);
+  }
+  for (uint64_t s = 0; s < l.segments; ++s) {
+    if (int rc = segment_offset(l, block_idx, s, &off)) return rc;
+    uint8_t* d = static_cast<uint8_t*>(dst) + s * l.bytes_per_block;
+    if (int rc = pf_copy_gpu_to_cpu(l.data_ptr, off, d, l.bytes_per_block, l.bytes_per_block))
+      return rc;
+  }
+  return PF_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Transfer contexts.
+// ---------------------------------------------------------------------------
+int pf_xfer_create(int device, uint64_t staging_bytes, pf_xfer** out) {
+  if (!out) return fail(PF_ERR_INVALID_ARGUMENT, "null output");
+  *out = nullptr;
+  if (int rc = pf_init(device)) return rc;
+  pf_xfer* x = new pf_xfer();
+  x->device = device;
+  auto cleanup = [&](int rc) {
+    pf_xfer_destroy(x);
+    return rc;
+  };
+  hipError_t e = hipStreamCreateWithFlags(&x->stream, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&x->dma, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&x->desc_uploaded, hipEventDisableTiming);
+  for (int s = 0; s < 2 && e == hipSuccess; ++s) {
+    e = hipEventCreateWithFlags(&x->slot_ready[s], hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&x->slot_free[s], hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventRecord(x->slot_free[s], x->stream);
+  }
+  if (e != hipSuccess) return cleanup(hip_fail(e, "pf_xfer_create"));
+  if (staging_bytes > 0) {
+    const uint64_t slot = (staging_bytes / 2) & ~uint64_t(255);
+    if (slot == 0) return cleanup(fail(PF_ERR_INVALID_ARGUMENT, "staging buffer too small"));
+    void* p = nullptr;
+    e = hipMalloc(&p, slot * 2);
+    if (e != hipSuccess) return cleanup(hip_fail(e, "hipMalloc(staging)"));
+    x->staging = reinterpret_cast<uint64_t>(p);
+    x->slot_bytes = slot;
+  }
+  e = hipStreamSynchronize(x->stream);
+  if (e != hipSuccess) return cleanup(hip_fail(e, "pf_xfer_create"));
+  *out = x;
+  return PF_OK;
+}
+
+int pf_xfer_destroy(pf_xfer* x) {
+  if (!x) return PF_OK;
+  (void)hipSetDevice(x->device);
+  if (x->stream) (void)hipStreamSynchronize(x->stream);
+  if (x->dma) (void)hipStreamSynchronize(x->dma);
+  if (x->d_desc) (void)hipFree(x->d_desc);
+  if (x->h_desc) (void)hipHostFree(x->h_desc);
+  if (x->staging) (void)hipFree(reinterpret_cast<void*>(x->staging));
+  if (x->desc_uploaded) (void)hipEventDestroy(x->desc_uploaded);
+  for (auto& t : x->timers) {
+    (void)hipEventDestroy(t.first);
+    (void)hipEventDestroy(t.second);
+  }
+  for (int s = 0; s < 2; ++s) {
+    if (x->slot_ready[s]) (void)hipEventDestroy(x->slot_ready[s]);
+    if (x->slot_free[s]) (void)hipEventDestroy(x->slot_free[s]);
+  }
+  if (x->stream) (void)hipStreamDestroy(x->stream);
+  if (x->dma) (void)hipStreamDestroy(x->dma);
+  delete x;
+  return PF_OK;
+}
+
+pf_stream pf_xfer_stream(pf_xfer* x) { return x ? x->stream : nullptr; }
+
+int pf_xfer_synchronize(pf_xfer* x) {
+  if (!x) return fail(PF_ERR_INVALID_ARGUMENT, "null transfer context");
+  PF_HIP(hipStreamSynchronize(x->dma));
+  PF_HIP(hipStreamSynchronize(x->stream));
+  return PF_OK;
+}
+
+int pf_xfer_set_kernel_shape(pf_xfer* x, uint32_t threads, uint32_t unroll) {
+  if (!x) return fail(PF_ERR_INVALID_ARGUMENT, "null transfer context");
+  if (threads && (threads < 64 || threads > 1024 || threads % 64))
+    return fail(PF_ERR_INVALID_ARGUMENT, "threads must be a multiple of 64 in [64, 1024]");
+  const uint32_t u = unroll & 0xffu;
+  if (unroll && u != 1 && u != 2 && u != 4 && u != 8 && u != 16)
+    return fail(PF_ERR_INVALID_ARGUMENT, "unroll must be 1, 2, 4, 8 or 16");
+  if (unroll & ~0x1ffu) return fail(PF_ERR_INVALID_ARGUMENT, "unknown kernel flag");
+  std::lock_guard<std::mutex> lk(x->mu);
+  if (threads) x->threads = threads;
+  if (unroll) x->unroll = unroll;
+  return PF_OK;
+}
+
+int pf_xfer_last_stats(pf_xfer* x, uint64_t* kernel_launches, uint64_t* dma_copies) {
+  if (!x) return fail(PF_ERR_INVALID_ARGUMENT, "null transfer context");
+  if (kernel_launches) *kernel_launches = x->last_kernels;
+  if (dma_copies) *dma_copies = x->last_dma;
+  return PF_OK;
+}
+
+int pf_xfer_set_timing(pf_xfer* x, int enable) {
+  if (!x) return fail(PF_ERR_INVALID_ARGUMENT, "null transfer context");
+  std::lock_guard<std::mutex> lk(x->mu);
+  x->timing = enable != 0;
+  return PF_OK;
+}
+
+int pf_xfer_last_kernel_ms(pf_xfer* x, float* ms, uint64_t* launches) {
+  if (!x || !ms) return fail(PF_ERR_INVALID_ARGUMENT, "null argument");
+  std::lock_guard<std::mutex> lk(x->mu);
+  float total = 0.0f;
+  const uint64_t n = x->timing ? x->last_kernels : 0;
+  for (uint64_t i = 0; i < n && i < x->timers.size(); ++i) {
+    PF_HIP(hipEventSynchronize(x->timers[i].second));
+    float t = 0.0f;
+    PF_HIP(hipEventElapsedTime(&t, x->timers[i].first, x->timers[i].second));
+    total += t;
+  }
+  *ms = total;
+  if (launches) *launches = n;
+  return PF_OK;
+}
+
+int pf_save_layers(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
+                   uint32_t mode) {
+  return run(x, layers, num_layers, mode, true, nullptr);
+}
+
+int pf_load_layers(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
+                   uint32_t mode, pf_event* layer_events) {
+  return run(x, layers, num_layers, mode, false, layer_events);
+}
+
+}  // extern "C"

@@ -1,0 +1,223 @@
+"""Device runtime objects over the C ABI: streams, events, device buffers and
+pinned host buffers, plus the synthetic-data and verification kernels.
+
+These are thin owners of HIP resources created by libpegaflow_hip.so; no
+framework tensors are involved.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import _lib
+from ._lib import check
+
+
+def lib():
+    return _lib.load()
+
+
+def device_count() -> int:
+    n = ctypes.c_int(0)
+    check(lib().pf_get_device_count(ctypes.byref(n)), "pf_get_device_count")
+    return n.value
+
+
+def init(device: int = 0) -> None:
+    check(lib().pf_init(device), "pf_init")
+
+
+def synchronize() -> None:
+    check(lib().pf_device_synchronize(), "pf_device_synchronize")
+
+
+def mem_get_info():
+    f, t = ctypes.c_uint64(), ctypes.c_uint64()
+    check(lib().pf_mem_get_info(ctypes.byref(f), ctypes.byref(t)), "pf_mem_get_info")
+    return f.value, t.value
+
+
+class Stream:
+    """A non-blocking HIP stream at the default priority."""
+
+    def __init__(self, handle=None, owned: bool = True):
+        if handle is None:
+            h = ctypes.c_void_p()
+            check(lib().pf_stream_create(ctypes.byref(h)), "pf_stream_create")
+            handle = h.value
+        self.handle = handle
+        self._owned = owned and handle is not None
+
+    def synchronize(self) -> None:
+        check(lib().pf_stream_synchronize(self.handle), "pf_stream_synchronize")
+
+    def wait_event(self, ev: "Event") -> None:
+        check(lib().pf_stream_wait_event(self.handle, ev.handle), "pf_stream_wait_event")
+
+    def close(self) -> None:
+        if self._owned and self.handle:
+            lib().pf_stream_destroy(self.handle)
+        self.handle = None
+        self._owned = False
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Event:
+    """A timing-capable HIP event."""
+
+    def __init__(self):
+        h = ctypes.c_void_p()
+        check(lib().pf_event_create(ctypes.byref(h)), "pf_event_create")
+        self.handle = h.value
+
+    def record(self, stream: Stream | None = None) -> None:
+        check(lib().pf_event_record(self.handle, stream.handle if stream else None),
+              "pf_event_record")
+
+    def synchronize(self) -> None:
+        check(lib().pf_event_synchronize(self.handle), "pf_event_synchronize")
+
+    def query(self) -> bool:
+        d = ctypes.c_int(0)
+        check(lib().pf_event_query(self.handle, ctypes.byref(d)), "pf_event_query")
+        return bool(d.value)
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = ctypes.c_float()
+        check(lib().pf_event_elapsed_ms(self.handle, end.handle, ctypes.byref(ms)),
+              "pf_event_elapsed_ms")
+        return float(ms.value)
+
+    def close(self) -> None:
+        if self.handle:
+            lib().pf_event_destroy(self.handle)
+        self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class DeviceBuffer:
+    """Device memory from hipMalloc."""
+
+    def __init__(self, nbytes: int):
+        p = ctypes.c_uint64()
+        check(lib().pf_device_malloc(nbytes, ctypes.byref(p)), "pf_device_malloc")
+        self.ptr = p.value
+        self.nbytes = nbytes
+
+    def upload(self, arr: np.ndarray, offset: int = 0) -> None:
+        arr = np.ascontiguousarray(arr)
+        assert offset + arr.nbytes <= self.nbytes
+        check(lib().pf_memcpy_h2d(self.ptr + offset, arr.ctypes.data, arr.nbytes),
+              "pf_memcpy_h2d")
+
+    def download(self, nbytes: int | None = None, offset: int = 0) -> np.ndarray:
+        n = self.nbytes - offset if nbytes is None else nbytes
+        assert offset + n <= self.nbytes
+        out = np.empty(n, np.uint8)
+        check(lib().pf_memcpy_d2h(out.ctypes.data, self.ptr + offset, n), "pf_memcpy_d2h")
+        return out
+
+    def fill_random(self, seed: int, word_offset: int = 0, stream: Stream | None = None,
+                    nbytes: int | None = None, offset: int = 0) -> None:
+        n = self.nbytes - offset if nbytes is None else nbytes
+        check(lib().pf_fill_random(self.ptr + offset, n, seed % 2**64, word_offset,
+                                   stream.handle if stream else None), "pf_fill_random")
+
+    def memset(self, value: int) -> None:
+        check(lib().pf_memset_d8(self.ptr, value, self.nbytes), "pf_memset_d8")
+
+    def close(self) -> None:
+        if self.ptr:
+            lib().pf_device_free(self.ptr)
+        self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class PinnedBuffer:
+    """Pinned host memory from hipHostMalloc, mapped for device access.
+
+    ``array`` is a uint8 numpy view of the allocation; ``ptr`` is both its
+    host address and the address kernels use for zero-copy access.
+    """
+
+    def __init__(self, nbytes: int, flags: int = _lib.PINNED_DEFAULT):
+        h = ctypes.c_void_p()
+        d = ctypes.c_uint64()
+        check(lib().pf_pinned_allocate(nbytes, flags, ctypes.byref(h), ctypes.byref(d)),
+              "pf_pinned_allocate")
+        self.ptr = h.value
+        self.dev_ptr = d.value
+        self.nbytes = nbytes
+        self.array = np.ctypeslib.as_array(
+            ctypes.cast(self.ptr, ctypes.POINTER(ctypes.c_uint8)), shape=(nbytes,))
+
+    def close(self) -> None:
+        if self.ptr:
+            self.array = None
+            lib().pf_pinned_free(self.ptr)
+        self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def fill_random(addr: int, nbytes: int, seed: int, word_offset: int = 0,
+                stream: Stream | None = None) -> None:
+    check(lib().pf_fill_random(addr, nbytes, seed % 2**64, word_offset,
+                               stream.handle if stream else None), "pf_fill_random")
+
+
+def verify_random(addr: int, nbytes: int, seed: int, word_offset: int = 0) -> int:
+    """Count of 8-byte words at addr that differ from the fill formula."""
+    out = ctypes.c_uint64()
+    check(lib().pf_verify_random(addr, nbytes, seed % 2**64, word_offset, ctypes.byref(out)),
+          "pf_verify_random")
+    return out.value
+
+
+def verify_random_chunks(addrs, word_offsets, chunk_bytes: int, seed: int) -> int:
+    """Batched verify: chunk i at addrs[i] must hold words word_offsets[i]..."""
+    a = np.ascontiguousarray(addrs, dtype=np.uint64)
+    w = np.ascontiguousarray(word_offsets, dtype=np.uint64)
+    assert a.shape == w.shape
+    out = ctypes.c_uint64()
+    pu = ctypes.POINTER(ctypes.c_uint64)
+    check(lib().pf_verify_random_chunks(a.ctypes.data_as(pu), w.ctypes.data_as(pu), len(a),
+                                        chunk_bytes, seed % 2**64, ctypes.byref(out)),
+          "pf_verify_random_chunks")
+    return out.value
+
+
+def compare(a: int, b: int, nbytes: int) -> int:
+    """Count of differing bytes between two device-visible buffers."""
+    out = ctypes.c_uint64()
+    check(lib().pf_compare(a, b, nbytes, ctypes.byref(out)), "pf_compare")
+    return out.value
+
+
+def spin(stream: Stream, microseconds: int) -> None:
+    check(lib().pf_spin(stream.handle, microseconds), "pf_spin")
+
+
+def huge_page_size() -> int:
+    return int(lib().pf_huge_page_size())

@@ -1,0 +1,232 @@
+"""The C-ABI library: loads, exports every declared symbol, and its host-side
+logic (layout validation, segment offsets, run merging, LoadState) agrees
+with the oracle and the reference's own unit tests.  No GPU calls here."""
+
+import ctypes
+import os
+import re
+import struct
+
+import numpy as np
+import pytest
+from hypothesis import given, settings, strategies as st
+
+import oracle
+from pegaflow_amd import _lib
+from pegaflow_amd.load_state import LoadState, PyLoadState
+from pegaflow_amd.transfer import (KVCacheRegistration, count_merged_runs, derive_layout,
+                                   is_contiguous_layout, segment_offset)
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "pegaflow_hip.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(pf_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    syms = declared_symbols()
+    assert len(syms) > 50
+    missing = [s for s in syms if not hasattr(lib, s)]
+    assert not missing, missing
+    unbound = [s for s in syms if s not in _lib.SIGNATURES]
+    assert not unbound, unbound
+    assert lib.pf_version().decode().startswith("pegaflow_hip")
+
+
+def test_library_is_gfx950_build():
+    with open(_lib.LIB_PATH, "rb") as fh:
+        blob = fh.read()
+    assert b"gfx950" in blob
+
+
+def _reg(*args):
+    return KVCacheRegistration.create(*args)
+
+
+@settings(max_examples=300, deadline=None)
+@given(st.integers(0, 2**40), st.integers(0, 2**36), st.integers(0, 3000),
+       st.integers(0, 70000), st.integers(0, 2**31), st.integers(0, 3))
+def test_layout_init_matches_oracle(ptr, size, nb, bpb, stride, segs):
+    try:
+        expect = oracle.layout(ptr, size, nb, bpb, stride, segs)
+    except oracle.OracleError:
+        expect = None
+    try:
+        got = _reg(ptr, size, nb, bpb, stride, segs)
+    except _lib.PegaFlowError as e:
+        assert e.code == _lib.PF_ERR_INVALID_ARGUMENT
+        got = None
+    assert (expect is None) == (got is None)
+    if got is not None:
+        assert got.block_size_bytes == expect.block_size_bytes
+        assert got.size_bytes == expect.size_bytes
+
+
+@settings(max_examples=300, deadline=None)
+@given(st.integers(1, 5000), st.integers(1, 70000), st.integers(0, 3), st.integers(1, 2),
+       st.integers(0, 6000), st.integers(0, 2))
+def test_segment_offset_matches_oracle(nb, bpb, pad, segs, block, seg):
+    stride = (nb + pad) * bpb if segs == 2 else 0
+    size = stride + nb * bpb
+    o = oracle.layout(0, size, nb, bpb, stride, segs)
+    r = _reg(0, size, nb, bpb, stride, segs)
+    try:
+        expect = oracle.segment_offset(o, block, seg)
+    except oracle.OracleError as e:
+        expect = str(e)
+    try:
+        got = segment_offset(r, block, seg)
+    except _lib.PegaFlowError as e:
+        got = str(e).split("storage error: ", 1)[1]
+    assert got == expect
+    assert is_contiguous_layout(r) == oracle.is_contiguous(o)
+    assert r.kind == oracle.layout_kind(o)
+
+
+@settings(max_examples=200, deadline=None)
+@given(st.lists(st.tuples(st.integers(0, 3), st.integers(0, 3)), max_size=50))
+def test_merged_runs_match_oracle(steps):
+    seg = 64
+    g, c, x, y = [], [], 0, 10**6
+    for dg, dc in steps:
+        x += dg * seg
+        y += dc * seg
+        g.append(x)
+        c.append(y)
+    assert count_merged_runs(g, c, seg) == len(oracle.merge_runs(g, c, seg))
+
+
+def test_derive_layout_rules():
+    # worker.py:104-115 on vLLM's KV-first [2, nb, bs, h, d] bf16 tensor.
+    shape = (2, 20000, 16, 8, 128)
+    stride = (20000 * 16 * 8 * 128, 16 * 8 * 128, 8 * 128, 128, 1)
+    assert derive_layout(shape, stride, 2) == (20000, 32768, 655_360_000, 2)
+    # Blocks-first MLA latent [8192, 64, 576].
+    assert derive_layout((8192, 64, 576), (64 * 576, 576, 1), 1) == (8192, 36864, 0, 1)
+    # A blocks-first tensor whose first dimension happens to be 2 is taken as
+    # KV-first, exactly as the reference does.
+    assert derive_layout((2, 64, 576), (64 * 576, 576, 1), 2)[3] == 2
+    with pytest.raises(ValueError):
+        derive_layout((4, 0), (0, 1), 2)
+
+
+def test_derive_layout_from_torch_tensor():
+    torch = pytest.importorskip("torch")
+    t = torch.empty((2, 12, 16, 4, 64), dtype=torch.float16)
+    assert derive_layout(t.shape, t.stride(), t.element_size()) == (12, 16 * 4 * 64 * 2,
+                                                                    12 * 16 * 4 * 64 * 2, 2)
+
+
+def test_error_message_is_per_call():
+    with pytest.raises(_lib.PegaFlowError, match="kv_stride_bytes must be > 0"):
+        _reg(0, 1000, 10, 10, 0, 2)
+    assert "kv_stride" in _lib.last_error()
+
+
+# ---------------------------------------------------------------------------
+# LoadState (sync_state.rs:294-340 tests plus the byte layout of :19-43).
+# ---------------------------------------------------------------------------
+def test_load_state_round_trip():
+    st_ = LoadState.new()
+    assert st_.get() == 0
+    name = st_.shm_name()
+    assert re.fullmatch(r"pega_load_[0-9a-f]{32}", name)
+    st_.set_completed()
+    att = LoadState.attach(name)
+    assert att.get() == 1
+    att.set_error()
+    assert st_.get() == -1
+    att.close()
+    st_.close()
+    assert not os.path.exists("/dev/shm/" + name)
+
+
+def test_load_state_byte_layout_matches_reference():
+    st_ = LoadState.new()
+    path = "/dev/shm/" + st_.shm_name()
+    raw = open(path, "rb").read()
+    assert len(raw) == 32
+    off, = struct.unpack_from("<Q", raw, 0)
+    assert off == 8
+    magic, version, state = struct.unpack_from("<IIq", raw, off)
+    assert (magic, version, state) == (0x50464C44, 1, 0)
+    st_.set_completed()
+    assert struct.unpack_from("<q", open(path, "rb").read(), off + 8)[0] == 1
+    st_.close()
+
+
+def _make_shm(name, data: bytes):
+    fd = os.open("/dev/shm/" + name, os.O_CREAT | os.O_RDWR, 0o600)
+    os.write(fd, data)
+    os.close(fd)
+
+
+def test_load_state_attach_rejects_too_small_mapping():
+    name = "pega_test_small_" + os.urandom(8).hex()
+    _make_shm(name, b"\0")
+    try:
+        with pytest.raises(_lib.PegaFlowError, match="shared memory too small"):
+            LoadState.attach(name)
+    finally:
+        os.unlink("/dev/shm/" + name)
+
+
+def test_load_state_attach_rejects_invalid_header():
+    st_ = LoadState.new()
+    path = "/dev/shm/" + st_.shm_name()
+    with open(path, "r+b") as fh:
+        fh.seek(8)
+        fh.write(struct.pack("<I", 0xDEADBEEF))
+    with pytest.raises(_lib.PegaFlowError, match="invalid LoadState header"):
+        LoadState.attach(st_.shm_name())
+    st_.close()
+
+
+def test_load_state_reads_a_reference_written_mapping():
+    # A mapping laid out by the reference's init_new_mapping (offset 8).
+    name = "pega_load_" + os.urandom(16).hex()
+    _make_shm(name, struct.pack("<QIIq", 8, 0x50464C44, 1, -1) + b"\0" * 8)
+    try:
+        st_ = LoadState.attach(name)
+        assert st_.get() == -1 and st_.num_layers() == 0
+        st_.close()
+    finally:
+        os.unlink("/dev/shm/" + name)
+
+
+def test_layered_load_state():
+    p = PyLoadState(num_layers=36)
+    assert p.get_state() == 0 and not p.is_ready() and p.layers_done() == 0
+    srv = LoadState.attach(p.shm_name())
+    assert srv.num_layers() == 36
+    srv.set_layers_done(5)
+    assert p.layers_done() == 5
+    assert p.wait_for_layer(4, timeout_s=1.0)
+    assert not p.wait_for_layer(5, timeout_s=0.01)
+    srv.set_completed()
+    assert p.is_ready() and p.get_state() == 1 and p.layers_done() == 36
+    # The first 32 bytes keep the reference's record.
+    raw = open("/dev/shm/" + p.shm_name(), "rb").read()
+    assert len(raw) == 48
+    assert struct.unpack_from("<QIIq", raw, 0) == (8, 0x50464C44, 1, 1)
+    assert struct.unpack_from("<IIq", raw, 32) == (0x50464C58, 36, 36)
+    srv.close()
+
+
+def test_pinned_zero_size_rejected_without_device():
+    # pinned_mem.rs:285-288: zero size fails before any driver call.
+    h, d = ctypes.c_void_p(), ctypes.c_uint64()
+    rc = _lib.load().pf_pinned_allocate(0, 0, ctypes.byref(h), ctypes.byref(d))
+    assert rc == _lib.PF_ERR_ZERO_SIZE
+
+
+def test_huge_page_size_parse():
+    # pinned_mem.rs:291-306: Hugepagesize is present on Linux and a power of two.
+    from pegaflow_amd.runtime import huge_page_size
+    size = huge_page_size()
+    assert size >= 2 * 1024 * 1024 and size & (size - 1) == 0

@@ -1,0 +1,387 @@
+"""GPU parity of the HIP transfer path against the oracle and golden data.
+
+Every test runs the product path (libpegaflow_hip.so through its C ABI) on
+device 0 and compares bytes:
+  * small shapes: against the CPU oracle on the same seeded inputs, and
+    against the committed golden fixtures;
+  * full BASELINE shapes: through size-independent closed forms — each host
+    chunk and every block of every layer tensor must hold exactly the
+    splitmix64 words of the block it came from (a permutation identity plus
+    "untouched blocks unchanged"), checked on the device.
+All four transfer modes must give identical bytes.
+"""
+
+import hashlib
+import json
+import os
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from pegaflow_amd import _lib
+from pegaflow_amd.runtime import (DeviceBuffer, Event, PinnedBuffer, Stream, spin,
+                                  verify_random_chunks)
+from pegaflow_amd.transfer import (KVCacheRegistration, LayerTransfer, TransferContext,
+                                   block_array)
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+MODES = {"dma_reference": _lib.MODE_DMA_REFERENCE, "dma_batched": _lib.MODE_DMA_BATCHED,
+         "kernel": _lib.MODE_KERNEL, "staged": _lib.MODE_STAGED}
+MiB = 1 << 20
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def ctx(gpu):
+    c = TransferContext(0, staging_bytes=64 * MiB)
+    yield c
+    c.close()
+
+
+class Layers:
+    """Device layer tensors of one shape, filled with seeded random words."""
+
+    def __init__(self, n_layers, num_blocks, bpb, segments, base_seed, pad_blocks=0):
+        self.nb, self.bpb, self.segments = num_blocks, bpb, segments
+        self.kv = (num_blocks + pad_blocks) * bpb if segments == 2 else 0
+        self.size = (self.kv + num_blocks * bpb) if segments == 2 else num_blocks * bpb
+        self.seeds = [oracle.layer_seed(base_seed, l) for l in range(n_layers)]
+        self.bufs = []
+        for l in range(n_layers):
+            b = DeviceBuffer(self.size)
+            b.fill_random(self.seeds[l])
+            self.bufs.append(b)
+        self.regs = [KVCacheRegistration.create(b.ptr, self.size, num_blocks, bpb, self.kv,
+                                                segments) for b in self.bufs]
+
+    def close(self):
+        for b in self.bufs:
+            b.close()
+        self.bufs = []
+
+
+def save_transfers(layers: Layers, ids, host: PinnedBuffer, region_stride=None):
+    """Reference host layout (lib.rs:636-747): per layer a K region then a V
+    region (split), or one region of whole blocks; returns per-layer bases."""
+    n = len(ids)
+    bs = layers.bpb * layers.segments
+    per_layer = n * bs if region_stride is None else region_stride
+    out, bases = [], []
+    for l, reg in enumerate(layers.regs):
+        base = host.ptr + l * per_layer
+        k, v, split = oracle.save_host_layout(oracle.layout(0, reg.size_bytes, reg.num_blocks,
+                                                            reg.bytes_per_block,
+                                                            reg.kv_stride_bytes, reg.segments),
+                                              n, base, base + n * layers.bpb)
+        out.append(LayerTransfer(reg, block_array(ids, k, v if split else None)))
+        bases.append(base)
+    return out, bases
+
+
+def load_transfers(layers: Layers, targets, saved):
+    out = []
+    for reg, lt in zip(layers.regs, saved):
+        b = lt.blocks.copy()
+        b["block_idx"] = np.asarray(targets, np.int64)
+        out.append(LayerTransfer(reg, b))
+    return out
+
+
+def closed_form_host_check(layers: Layers, ids, saved):
+    """Host chunk j of layer l holds the words of block ids[j] (per segment)."""
+    bad = 0
+    for l, lt in enumerate(saved):
+        addrs, offs = [], []
+        for j, b in enumerate(ids):
+            if layers.segments == 2 and layers.kv > layers.bpb:
+                addrs += [int(lt.blocks["k_host"][j]), int(lt.blocks["v_host"][j])]
+                offs += [b * layers.bpb // 8, (layers.kv + b * layers.bpb) // 8]
+            else:
+                addrs.append(int(lt.blocks["k_host"][j]))
+                offs.append(b * layers.bpb * layers.segments // 8)
+        chunk = layers.bpb if layers.segments == 2 else layers.bpb * layers.segments
+        bad += verify_random_chunks(addrs, offs, chunk, layers.seeds[l])
+    return bad
+
+
+def closed_form_tensor_check(layers: Layers, src_of: dict):
+    """Every block b of every layer holds the words of block src_of.get(b, b)."""
+    bad = 0
+    nb, bpb = layers.nb, layers.bpb
+    blocks = np.arange(nb, dtype=np.uint64)
+    src = blocks.copy()
+    for b, s in src_of.items():
+        src[b] = s
+    for l, buf in enumerate(layers.bufs):
+        if layers.segments == 2:
+            addrs = np.concatenate([buf.ptr + blocks * bpb, buf.ptr + layers.kv + blocks * bpb])
+            offs = np.concatenate([src * bpb // 8, (layers.kv + src * bpb) // 8])
+        else:
+            addrs = buf.ptr + blocks * bpb
+            offs = src * bpb // 8
+        bad += verify_random_chunks(addrs, offs, bpb, layers.seeds[l])
+    return bad
+
+
+# ---------------------------------------------------------------------------
+def test_fill_kernel_matches_oracle_words(gpu):
+    buf = DeviceBuffer(1 << 16)
+    buf.fill_random(987654321, word_offset=5)
+    got = buf.download().view(np.uint64)
+    assert np.array_equal(got, oracle.random_words(len(got), 987654321, 5))
+    assert verify_random_chunks([buf.ptr], [5], 1 << 16, 987654321) == 0
+    assert verify_random_chunks([buf.ptr + 8], [5], 64, 987654321) == 8  # shifted: all differ
+    buf.close()
+
+
+@pytest.mark.parametrize("fixture", ["tiny_kvfirst", "tiny_blocks"])
+@pytest.mark.parametrize("mode", list(MODES))
+def test_golden_tiny(ctx, fixture, mode):
+    say(f"[gpu] golden {fixture} mode={mode}")
+    f = np.load(os.path.join(GOLDEN, fixture + ".npz"))
+    nb, bpb, kv, segs = (int(f[k]) for k in ("num_blocks", "bytes_per_block",
+                                             "kv_stride_bytes", "segments"))
+    size = int(f["size_bytes"])
+    kept = [int(b) for b in f["save_ids"] if b >= 0]
+    targets = [int(b) for b in f["load_ids"] if b >= 0]
+    host = PinnedBuffer(1 << 16)
+    for layer in range(2):
+        dev = DeviceBuffer(size)
+        dev.upload(f[f"input_{layer}"])
+        reg = KVCacheRegistration.create(dev.ptr, size, nb, bpb, kv, segs)
+        k, v, split = oracle.save_host_layout(
+            oracle.layout(0, size, nb, bpb, kv, segs), len(kept), host.ptr,
+            host.ptr + len(kept) * bpb)
+        lt = LayerTransfer(reg, block_array(kept, k, v if split else None))
+        host.array[:] = 0
+        ctx.save_layers([lt], MODES[mode])
+        m = len(kept)
+        if split:
+            assert np.array_equal(host.array[: m * bpb], f[f"host_k_{layer}"])
+            assert np.array_equal(host.array[m * bpb: 2 * m * bpb], f[f"host_v_{layer}"])
+        else:
+            assert np.array_equal(host.array[: m * bpb * segs], f[f"host_{layer}"])
+        lt2 = LayerTransfer(reg, block_array(targets, k, v if split else None))
+        ctx.load_layers([lt2], MODES[mode])
+        ctx.synchronize()
+        assert np.array_equal(dev.download(), f[f"restored_{layer}"])
+        dev.close()
+    host.close()
+
+
+@pytest.mark.parametrize("mode", list(MODES))
+def test_gpt2_config1_golden(ctx, mode):
+    """Config 1: GPT-2 shape, 12 fp16 layers [2,512,16,12,64]; 64 random
+    blocks saved, loaded into 64 other random blocks; digests must match."""
+    with open(os.path.join(GOLDEN, "gpt2_config1.json")) as fh:
+        g = json.load(fh)
+    say(f"[gpu] gpt2 config1 mode={mode}")
+    layers = Layers(g["layers"], g["num_blocks"], g["bytes_per_block"], 2, g["base_seed"])
+    assert layers.size == g["size_bytes"]
+    n = len(g["save_ids"])
+    host = PinnedBuffer(g["layers"] * 2 * n * g["bytes_per_block"])
+    saved, bases = save_transfers(layers, g["save_ids"], host)
+    ctx.save_layers(saved, MODES[mode])
+    seg = n * g["bytes_per_block"]
+    for l, base in enumerate(bases):
+        off = base - host.ptr
+        assert hashlib.sha256(host.array[off: off + seg].tobytes()).hexdigest() == \
+            g["host_k_sha256"][l]
+        assert hashlib.sha256(host.array[off + seg: off + 2 * seg].tobytes()).hexdigest() == \
+            g["host_v_sha256"][l]
+    ctx.load_layers(load_transfers(layers, g["load_ids"], saved), MODES[mode])
+    ctx.synchronize()
+    for l, buf in enumerate(layers.bufs):
+        assert hashlib.sha256(buf.download().tobytes()).hexdigest() == g["restored_sha256"][l]
+    layers.close()
+    host.close()
+
+
+def _oracle_roundtrip_case(ctx, mode, nb, bpb, segs, kv, size, save_ids, load_ids,
+                           host_offset=0, seed=3):
+    """Runs save(save_ids) then load(load_ids) on device and on the oracle."""
+    dev = DeviceBuffer(size)
+    dev.fill_random(seed)
+    ref = dev.download()
+    reg = KVCacheRegistration.create(dev.ptr, size, nb, bpb, kv, segs)
+    oreg = oracle.layout(ref.ctypes.data, size, nb, bpb, kv, segs)
+    m = len(save_ids)
+    bs = bpb * segs
+    host = PinnedBuffer(2 * m * bs + 4096)
+    base = host.ptr + host_offset
+    k, v, split = oracle.save_host_layout(oreg, m, base, base + m * bpb)
+    host.array[:] = 0
+    ctx.save_layers([LayerTransfer(reg, block_array(save_ids, k, v if split else None))], mode)
+    got_host = host.array.copy()
+    # Oracle on the CPU copy, with host buffers at the same relative offsets.
+    ohost = np.zeros_like(got_host)
+    obase = ohost.ctypes.data + host_offset
+    ok_, ov, _ = oracle.save_host_layout(oreg, m, obase, obase + m * bpb)
+    oracle.process_save(oreg, ref, save_ids, ok_, ov if split else None)
+    assert np.array_equal(got_host, ohost)
+    ctx.load_layers([LayerTransfer(reg, block_array(load_ids, k, v if split else None))], mode)
+    ctx.synchronize()
+    oracle.process_load(oreg, ref, load_ids, ok_, ov if split else None)
+    assert np.array_equal(dev.download(), ref)
+    dev.close()
+    host.close()
+
+
+@pytest.mark.parametrize("mode", list(MODES))
+def test_edge_cases_vs_oracle(ctx, mode):
+    m = MODES[mode]
+    say(f"[gpu] edge cases mode={mode}")
+    nb, bpb = 40, 256
+    kv = nb * bpb
+    # Every block, in reverse order, loaded in sorted order (maximal merging).
+    _oracle_roundtrip_case(ctx, m, nb, bpb, 2, kv, 2 * kv, list(range(nb))[::-1],
+                           list(range(nb)))
+    # One block.
+    _oracle_roundtrip_case(ctx, m, nb, bpb, 2, kv, 2 * kv, [7], [39])
+    # Duplicate load targets: the later copy wins (in-order semantics).
+    _oracle_roundtrip_case(ctx, m, nb, bpb, 2, kv, 2 * kv, [1, 2, 3, 4], [9, 9, 5, 9])
+    # Host regions at an 8-byte (not 16-byte) offset: unaligned kernel path.
+    _oracle_roundtrip_case(ctx, m, nb, bpb, 2, kv, 2 * kv, [3, 11, 20], [0, 1, 2],
+                           host_offset=8)
+    # Odd segment size (not a multiple of 16).
+    _oracle_roundtrip_case(ctx, m, 30, 24, 2, 30 * 24 + 8, 30 * 24 * 2 + 8, [4, 5, 6],
+                           [20, 0, 29])
+    # Padded split layout (gap between K and V), blocks-first single segment.
+    _oracle_roundtrip_case(ctx, m, nb, bpb, 2, kv + 3 * bpb, 2 * kv + 3 * bpb, [5, 6], [0, 39])
+    _oracle_roundtrip_case(ctx, m, nb, 4608, 1, 0, nb * 4608, [9, 1, 30], [2, 3, 4])
+    # Overlapping split layout (kv_stride < num_blocks * bytes_per_block) and a
+    # strided layout (kv_stride < bytes_per_block): in-order semantics.
+    _oracle_roundtrip_case(ctx, m, 10, 64, 2, 160, 160 + 640, [1, 2, 3], [4, 3, 2])
+    _oracle_roundtrip_case(ctx, m, 10, 64, 2, 32, 9 * 64 + 32 + 64, [2, 5], [3, 4])
+
+
+def test_empty_and_errors(ctx, gpu):
+    say("[gpu] empty and error paths")
+    nb, bpb = 16, 512
+    dev = DeviceBuffer(2 * nb * bpb)
+    reg = KVCacheRegistration.create(dev.ptr, 2 * nb * bpb, nb, bpb, nb * bpb, 2)
+    host = PinnedBuffer(1 << 16)
+    for m in MODES.values():
+        ctx.save_layers([], m)
+        ctx.save_layers([LayerTransfer(reg, block_array([], []))], m)
+        ctx.load_layers([LayerTransfer(reg, block_array([], []))], m)
+    ctx.synchronize()
+    # Out-of-range block: the reference's segment_offset message, before any copy.
+    with pytest.raises(_lib.PegaFlowError, match="exceeds registered memory"):
+        ctx.save_layers([LayerTransfer(reg, block_array([nb], [host.ptr]))], _lib.MODE_KERNEL)
+    with pytest.raises(_lib.PegaFlowError, match="must be >= 0"):
+        ctx.load_layers([LayerTransfer(reg, block_array([-1], [host.ptr]))], _lib.MODE_KERNEL)
+    # Kernel mode refuses host memory that is not mapped for the device.
+    pageable = np.zeros(4 * bpb, np.uint8)
+    with pytest.raises(_lib.PegaFlowError, match="not device-accessible"):
+        ctx.save_layers([LayerTransfer(reg, block_array([0], [pageable.ctypes.data]))],
+                        _lib.MODE_KERNEL)
+    # ...and a "layer tensor" that is not device memory.
+    bad = KVCacheRegistration(data_ptr=pageable.ctypes.data, size_bytes=4 * bpb, num_blocks=2,
+                              bytes_per_block=bpb, block_size_bytes=2 * bpb,
+                              kv_stride_bytes=2 * bpb, segments=2)
+    with pytest.raises(_lib.PegaFlowError, match="not inside one device allocation"):
+        ctx.save_layers([LayerTransfer(bad, block_array([0], [host.ptr]))], _lib.MODE_KERNEL)
+    # DMA modes accept pageable host memory, like cuMemcpy.
+    dev.fill_random(5)
+    ctx.save_layers([LayerTransfer(reg, block_array([3], [pageable.ctypes.data]))],
+                    _lib.MODE_DMA_BATCHED)
+    expect = oracle.random_words(bpb // 8, 5, 3 * bpb // 8).view(np.uint8)
+    assert np.array_equal(pageable[:bpb], expect)
+    # A staged transfer on a context without staging is an error.
+    nostage = TransferContext(0, staging_bytes=0)
+    with pytest.raises(_lib.PegaFlowError, match="no staging buffer"):
+        nostage.save_layers([LayerTransfer(reg, block_array([0], [host.ptr]))],
+                            _lib.MODE_STAGED)
+    nostage.close()
+    dev.close()
+    host.close()
+
+
+@pytest.mark.parametrize("shape", [(256, 1), (256, 2), (256, 4), (512, 8), (1024, 16),
+                                   (64, 8)])
+def test_kernel_shapes_and_nontemporal(ctx, shape):
+    threads, unroll = shape
+    say(f"[gpu] kernel shape threads={threads} unroll={unroll}")
+    for nt in (0, _lib.KERNEL_NONTEMPORAL):
+        ctx.set_kernel_shape(threads, unroll | nt)
+        _oracle_roundtrip_case(ctx, _lib.MODE_KERNEL, 64, 73728, 1, 0, 64 * 73728,
+                               [5, 60, 2, 33], [0, 1, 63, 9], seed=threads + unroll)
+    ctx.set_kernel_shape(256, 8)
+
+
+def _full_size(ctx, n_layers, nb, bpb, segs, n_blocks, save_mode, load_mode, seed=0):
+    layers = Layers(n_layers, nb, bpb, segs, seed)
+    rng = np.random.Generator(np.random.PCG64(seed))
+    ids = rng.choice(nb, n_blocks, replace=False)
+    rest = np.setdiff1d(np.arange(nb), ids)
+    targets = rng.choice(rest, n_blocks, replace=False)
+    host = PinnedBuffer(n_layers * n_blocks * bpb * segs)
+    saved, _ = save_transfers(layers, ids.tolist(), host)
+    ctx.save_layers(saved, save_mode)
+    assert closed_form_host_check(layers, ids.tolist(), saved) == 0
+    ctx.load_layers(load_transfers(layers, targets, saved), load_mode)
+    ctx.synchronize()
+    src_of = {int(t): int(s) for t, s in zip(targets, ids)}
+    assert closed_form_tensor_check(layers, src_of) == 0
+    layers.close()
+    host.close()
+
+
+@pytest.mark.parametrize("save_mode,load_mode", [("kernel", "staged"), ("staged", "kernel"),
+                                                  ("dma_batched", "dma_batched")])
+def test_llama_10k_prefix_full_size(ctx, save_mode, load_mode):
+    """Config 2: 32 bf16 layers [2,20000,16,8,128], 640 random blocks."""
+    say(f"[gpu] llama full size save={save_mode} load={load_mode}")
+    _full_size(ctx, 32, 20000, 32768, 2, 640, MODES[save_mode], MODES[load_mode])
+
+
+@pytest.mark.parametrize("dtype_bytes", [2, 1])
+def test_mla_latent_full_size(ctx, dtype_bytes):
+    """Config 5: 61 layers [8192, 64, 576] (bf16 or fp8 bytes), 128 blocks."""
+    say(f"[gpu] MLA full size dtype_bytes={dtype_bytes}")
+    _full_size(ctx, 61, 8192, 64 * 576 * dtype_bytes, 1, 128, _lib.MODE_KERNEL,
+               _lib.MODE_KERNEL, seed=dtype_bytes)
+
+
+def test_layerwise_load_events_qwen3(ctx):
+    """Config 3 shape: 36 layers [2,16000,16,8,128], 313 blocks, loaded one
+    layer at a time; each layer's event gates a compute kernel on a second
+    stream.  Events complete in layer order and the bytes are exact."""
+    say("[gpu] qwen3 layer-wise events")
+    n_layers, nb, bpb, n = 36, 16000, 32768, 313
+    layers = Layers(n_layers, nb, bpb, 2, 9)
+    rng = np.random.Generator(np.random.PCG64(9))
+    ids = rng.choice(nb, n, replace=False)
+    targets = rng.choice(np.setdiff1d(np.arange(nb), ids), n, replace=False)
+    host = PinnedBuffer(n_layers * n * bpb * 2)
+    saved, _ = save_transfers(layers, ids.tolist(), host)
+    ctx.save_layers(saved, _lib.MODE_KERNEL)
+    compute = Stream()
+    for mode in (_lib.MODE_KERNEL, _lib.MODE_STAGED, _lib.MODE_DMA_BATCHED):
+        evs = [Event() for _ in range(n_layers)]
+        done = [Event() for _ in range(n_layers)]
+        ctx.load_layers(load_transfers(layers, targets, saved), mode, layer_events=evs)
+        for l in range(n_layers):
+            compute.wait_event(evs[l])
+            spin(compute, 50)
+            done[l].record(compute)
+        compute.synchronize()
+        ctx.synchronize()
+        for l in range(1, n_layers):
+            assert evs[l - 1].elapsed_ms(evs[l]) >= 0.0
+        src_of = {int(t): int(s) for t, s in zip(targets, ids)}
+        assert closed_form_tensor_check(layers, src_of) == 0
+        for l in range(n_layers):  # restore the targets for the next mode
+            layers.bufs[l].fill_random(layers.seeds[l])
+    compute.close()
+    layers.close()
+    host.close()
