@@ -1,0 +1,401 @@
+#!/usr/bin/env python3
+"""KV save/restore benchmark of the MI355X transfer path.
+
+Workload (the reference's Llama-3.1-8B 10K-token prefix): 32 bf16 layers of
+[2, 20000, 16, 8, 128] resident in HBM (64 KiB per block per layer), a prefix
+of 640 blocks drawn uniformly at random without replacement.  One step is a
+full save of the prefix to the pinned host pool (in the reference's split
+K/V host layout) followed by a full restore of it into 640 other random
+blocks: P = 1,342,177,280 payload bytes cross the host link in each
+direction.
+
+Printed JSON line (stdout):
+  value            save+restore payload GB/s over the timed steps (2P/step)
+  restore_*        host -> HBM restore: GB/s, ms per prefix, fraction of the
+                   measured host-link peak (best 1 GiB hipMemcpyAsync) and of
+                   PCIe Gen5 x16 (63.0 GB/s)
+  save_*           HBM -> host save, same figures
+  roofline         the device gather kernel (paged layers -> packed HBM
+                   buffer, all 32 layers in one launch): algorithmic bytes 2P
+                   per launch / its HIP-event-timed duration, vs 8 TB/s
+  cpu_baseline     the reference's copy pattern (per-segment save copies,
+                   merged-run restore copies) as host memcpy on this box's
+                   cores, on a bounded sample of the same workload
+Everything else goes to stderr.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import numpy as np
+
+HBM_PEAK_GBPS = 8000.0
+PCIE_GEN5_X16_GBPS = 63.0
+GiB = 1 << 30
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--save-mode", default="kernel",
+                    choices=["dma_reference", "dma_batched", "kernel", "staged"])
+    ap.add_argument("--load-mode", default="kernel",
+                    choices=["dma_reference", "dma_batched", "kernel", "staged"])
+    ap.add_argument("--variants", action="store_true",
+                    help="also time every transfer mode once per direction")
+    ap.add_argument("--sweep", action="store_true",
+                    help="also sweep the gather kernel's launch shape")
+    ap.add_argument("--threads", type=int, default=0, help="kernel workgroup size (0: default)")
+    ap.add_argument("--unroll", type=int, default=0,
+                    help="16-byte loads in flight per lane, +256 for non-temporal (0: default)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample-layers", type=int, default=8)
+    ap.add_argument("--staging-mib", type=int, default=256)
+    ap.add_argument("--seed", type=int, default=0)
+    return ap.parse_args()
+
+
+def timed(fn, reps=1):
+    best = float("inf")
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        best = min(best, time.perf_counter() - t0)
+    return best
+
+
+def link_peaks(pool, scratch, stream):
+    """Best of 10 1-GiB pinned<->device hipMemcpyAsync per direction, and a
+    1-GiB device-to-device copy, each timed with HIP events on its stream
+    (GB/s, decimal; D2D counts read + write)."""
+    from pegaflow_amd import runtime
+
+    dst = runtime.DeviceBuffer(GiB)
+    start, end = runtime.Event(), runtime.Event()
+
+    def best(d, s, bytes_counted):
+        ms = []
+        for _ in range(11):
+            start.record(stream)
+            runtime.memcpy_async(d, s, GiB, stream)
+            end.record(stream)
+            end.synchronize()
+            ms.append(start.elapsed_ms(end))
+        return bytes_counted / (min(ms[1:]) / 1e3) / 1e9
+
+    h2d = best(scratch.ptr, pool.ptr, GiB)
+    d2h = best(pool.ptr, scratch.ptr, GiB)
+    d2d = best(dst.ptr, scratch.ptr, 2 * GiB)
+    dst.close()
+    return h2d, d2h, d2d
+
+
+def duplex(xfer_save, xfer_load, saved, loads, mode, reps=5):
+    """Save of one prefix and restore of another issued together on two
+    transfer contexts (the engine's save and load workers): aggregate payload
+    GB/s with both link directions busy."""
+    ts = []
+    for _ in range(reps + 1):
+        t0 = time.perf_counter()
+        xfer_load.load_layers(loads, mode)   # asynchronous
+        xfer_save.save_layers(saved, mode)   # returns when saved
+        xfer_load.synchronize()
+        ts.append(time.perf_counter() - t0)
+    return min(ts[1:])
+
+
+def cpu_baseline(shape, ids, targets, n_layers, threads, seed):
+    """The reference's CPU-side copy pattern, timed with host memcpy: save =
+    one copy per segment (gpu_worker.rs:344-360), restore = one copy per merged
+    run (transfer.rs:116-198), over host-resident copies of n_layers layers."""
+    import oracle
+    from pegaflow_amd.workload import layer_seed
+
+    n = len(ids)
+    bpb, kv = shape.bytes_per_block, shape.kv_stride_bytes
+    tensors = []
+    for l in range(n_layers):
+        t = np.empty(shape.layer_bytes, np.uint8)
+        oracle.fill_random(t, layer_seed(seed, l))
+        tensors.append(t)
+    pool = np.zeros(n_layers * n * 2 * bpb, np.uint8)
+    ss, sd, sz, ls, ld, lz = [], [], [], [], [], []
+    for l, t in enumerate(tensors):
+        reg = oracle.layout(t.ctypes.data, shape.layer_bytes, shape.num_blocks, bpb, kv,
+                            shape.segments)
+        base = pool.ctypes.data + l * n * 2 * bpb
+        k, v, _ = oracle.save_host_layout(reg, n, base, base + n * bpb)
+        a, b, c = oracle.save_copies(reg, t.ctypes.data, ids, k, v)
+        ss.append(a), sd.append(b), sz.append(c)
+        a, b, c = oracle.load_copies(reg, t.ctypes.data, targets, k, v)
+        ls.append(a), ld.append(b), lz.append(c)
+    save = [np.concatenate(x) for x in (ss, sd, sz)]
+    load = [np.concatenate(x) for x in (ls, ld, lz)]
+    payload = n_layers * n * 2 * bpb
+
+    def run(t):
+        ts, tl = [], []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            oracle.run_copies(*save, nthreads=t)
+            t1 = time.perf_counter()
+            oracle.run_copies(*load, nthreads=t)
+            t2 = time.perf_counter()
+            ts.append(t1 - t0)
+            tl.append(t2 - t1)
+        return statistics.median(ts), statistics.median(tl)
+
+    run(threads)  # warm
+    s_mt, l_mt = run(threads)
+    s_1, l_1 = run(1)
+    return {
+        "value": round(2 * payload / (s_mt + l_mt) / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"{n_layers} of {shape.layers} layers of the same workload "
+                   f"({n} blocks, save then restore, {2 * payload / 1e6:.0f} MB moved), "
+                   "host memory, median of 5"),
+        "save_gbps": round(payload / s_mt / 1e9, 3),
+        "restore_gbps": round(payload / l_mt / 1e9, 3),
+        "single_thread_gbps": round(2 * payload / (s_1 + l_1) / 1e9, 3),
+        "save_copies": int(len(save[0])),
+        "restore_copies": int(len(load[0])),
+    }
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: the KV transfer path has no cross-GPU step "
+              "(each rank moves its own layers over its own host link); run with --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+
+    from pegaflow_amd import _lib, runtime
+    from pegaflow_amd.runtime import DeviceBuffer, PinnedBuffer
+    from pegaflow_amd.transfer import LayerTransfer, TransferContext
+    from pegaflow_amd import workload as wl
+
+    shape = wl.LLAMA3_8B
+    n_blocks = 640
+    runtime.init(0)
+    log(f"[bench] allocating {shape.layers} x {shape.layer_bytes / 1e9:.2f} GB layer tensors")
+    layers = wl.DeviceLayers(shape, base_seed=args.seed)
+    ids, targets = wl.draw_blocks(shape.num_blocks, n_blocks, args.seed)
+    P = wl.payload_bytes(layers.regs, n_blocks)
+    assert P == 1_342_177_280
+    pool = PinnedBuffer(P)
+    gather_buf = DeviceBuffer(P)
+    xfer = TransferContext(0, staging_bytes=args.staging_mib << 20)
+    modes = _lib.MODE_NAMES
+    saved = wl.save_plan(layers.regs, ids, pool.ptr)
+    loads = wl.load_plan(saved, targets)
+
+    log("[bench] host-link and HBM copy peaks")
+    h2d_peak, d2h_peak, d2d_gbps = link_peaks(pool, gather_buf, xfer.stream)
+    log(f"[bench] h2d {h2d_peak:.1f} GB/s, d2h {d2h_peak:.1f} GB/s, d2d {d2d_gbps:.0f} GB/s")
+
+    # Device gather: the same save batch into a packed HBM buffer.
+    gather = wl.save_plan(layers.regs, ids, gather_buf.ptr)
+    xfer.set_timing(True)
+    sweep = {}
+    default_shape = (512, 1 | _lib.KERNEL_NONTEMPORAL)
+    nt_names = {0: "", _lib.KERNEL_NT_LOADS: "_ntl", _lib.KERNEL_NT_STORES: "_nts",
+                _lib.KERNEL_NONTEMPORAL: "_nt"}
+
+    def shape_sweep(label, plan, run, reps, bytes_moved, shapes):
+        for threads, unroll in shapes:
+            xfer.set_kernel_shape(threads, unroll)
+            run(plan)
+            ms = []
+            for _ in range(reps):
+                run(plan)
+                ms.append(xfer.last_kernel_ms()[0])
+            key = f"{label}_t{threads}_u{unroll & 0xff}{nt_names[unroll & 0x300]}"
+            sweep[key] = round(bytes_moved / (min(ms) / 1e3) / 1e9, 1)
+            log(f"[bench] sweep {key}: {min(ms):.4f} ms = {sweep[key]} GB/s")
+        xfer.set_kernel_shape(*default_shape)
+
+    if args.sweep:
+        save_k = lambda plan: xfer.save_layers(plan, _lib.MODE_KERNEL)  # noqa: E731
+        load_k = lambda plan: (xfer.load_layers(plan, _lib.MODE_KERNEL),  # noqa: E731
+                               xfer.synchronize())
+        shape_sweep("gather", gather, save_k, 5, 2 * P,
+                    [(t, u | nt) for t in (256, 512, 768, 1024) for u in (1, 2, 4)
+                     for nt in (0, _lib.KERNEL_NT_LOADS, _lib.KERNEL_NT_STORES,
+                                _lib.KERNEL_NONTEMPORAL)])
+        for grid in (1024, 2048, 4096):
+            xfer.set_max_grid(grid)
+            shape_sweep(f"gather_grid{grid}", gather, save_k, 5, 2 * P, [default_shape])
+        xfer.set_max_grid(0)
+        link_shapes = [(t, u | nt) for t in (256, 512, 1024) for u in (2, 4, 8)
+                       for nt in (0, _lib.KERNEL_NONTEMPORAL)]
+        shape_sweep("zerocopy_restore", loads, load_k, 2, P, link_shapes)
+        shape_sweep("zerocopy_save", saved, save_k, 2, P, link_shapes)
+    if args.threads or args.unroll:
+        xfer.set_kernel_shape(args.threads, args.unroll)
+    xfer.save_layers(gather, _lib.MODE_KERNEL)
+    g_ms, g_launch = [], 0
+    for _ in range(10):
+        xfer.save_layers(gather, _lib.MODE_KERNEL)
+        ms, g_launch = xfer.last_kernel_ms()
+        g_ms.append(ms)
+    gather_ms = sum(g_ms) / len(g_ms)
+    gather_gbps = 2 * P / (gather_ms / 1e3) / 1e9
+    log(f"[bench] device gather {gather_ms:.3f} ms/launch ({g_launch} launch) = "
+        f"{gather_gbps:.0f} GB/s")
+    # Device scatter: the packed HBM buffer back into the target blocks.
+    scatter = wl.load_plan(gather, targets)
+    s_ms = []
+    for _ in range(10):
+        xfer.load_layers(scatter, _lib.MODE_KERNEL)
+        ms, _ = xfer.last_kernel_ms()
+        s_ms.append(ms)
+    scatter_ms = sum(s_ms) / len(s_ms)
+    scatter_gbps = 2 * P / (scatter_ms / 1e3) / 1e9
+
+    variants = {}
+    if args.variants:
+        for name, m in modes.items():
+            reps = 1 if name == "dma_reference" else 3
+            t_s = timed(lambda: xfer.save_layers(saved, m), reps)
+            t_l = timed(lambda: (xfer.load_layers(loads, m), xfer.synchronize()), reps)
+            variants[name] = {"save_gbps": round(P / t_s / 1e9, 2),
+                              "restore_gbps": round(P / t_l / 1e9, 2),
+                              "save_ms": round(t_s * 1e3, 3), "restore_ms": round(t_l * 1e3, 3)}
+            log(f"[bench] variant {name}: {variants[name]}")
+
+    save_mode, load_mode = modes[args.save_mode], modes[args.load_mode]
+    log(f"[bench] steps: save={args.save_mode} restore={args.load_mode} "
+        f"warmup={args.warmup} steps={args.steps}")
+    xfer.set_timing(True)
+    t_save, t_load, k_save, k_load = [], [], [], []
+    for i in range(args.warmup):
+        xfer.save_layers(saved, save_mode)
+        xfer.load_layers(loads, load_mode)
+        xfer.synchronize()
+    runtime.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        a = time.perf_counter()
+        xfer.save_layers(saved, save_mode)
+        k_save.append(xfer.last_kernel_ms()[0])
+        b = time.perf_counter()
+        xfer.load_layers(loads, load_mode)
+        xfer.synchronize()
+        k_load.append(xfer.last_kernel_ms()[0])
+        c = time.perf_counter()
+        t_save.append(b - a)
+        t_load.append(c - b)
+    runtime.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_step = elapsed / args.steps * 1e3
+    value = 2 * P * args.steps / elapsed / 1e9
+    save_s, load_s = statistics.median(t_save), statistics.median(t_load)
+
+    bad_host = wl.verify_saved(layers, saved)
+    bad_dev = wl.verify_restored(layers, ids, targets)
+    log(f"[bench] verify: host mismatches {bad_host}, device mismatches {bad_dev}")
+
+    # Full duplex: a second prefix saved (into a second pool) while the first
+    # is restored, on two contexts as the engine's save and load workers do.
+    pool2 = PinnedBuffer(P)
+    xfer2 = TransferContext(0)
+    saved2 = wl.save_plan(layers.regs, ids, pool2.ptr)
+    t_dup = duplex(xfer2, xfer, saved2, loads, save_mode)
+    bad_dup = wl.verify_saved(layers, saved2) + wl.verify_restored(layers, ids, targets)
+    log(f"[bench] duplex save+restore {t_dup * 1e3:.3f} ms = {2 * P / t_dup / 1e9:.1f} GB/s, "
+        f"mismatches {bad_dup}")
+    bad_host += bad_dup
+    xfer2.close()
+    pool2.close()
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        threads = max(1, min(16, len(os.sched_getaffinity(0))))
+        log(f"[bench] cpu baseline: {args.cpu_sample_layers} layers, {threads} threads")
+        cpu = cpu_baseline(shape, ids, targets, args.cpu_sample_layers, threads, args.seed)
+        log(f"[bench] cpu baseline {cpu}")
+
+    out = {
+        "metric": "KV save/load GB/s + ms per 10K-tok Llama-3-8B prefix (frac of PCIe/HBM peak)",
+        "value": round(value, 3),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u8",
+        "data": "synthetic (seeded splitmix64 random bits in bf16-shaped KV tensors)",
+        "config": {
+            "workload": "llama-3.1-8b 10k-token prefix: 32 x bf16 [2,20000,16,8,128], "
+                        "640 random blocks, save then restore into 640 other blocks",
+            "payload_bytes_per_direction": P,
+            "save_mode": args.save_mode,
+            "restore_mode": args.load_mode,
+            "parallelism": "single gpu",
+        },
+        "restore_gbps": round(P / load_s / 1e9, 3),
+        "restore_ms_per_prefix": round(load_s * 1e3, 3),
+        "restore_frac_of_measured_h2d_peak": round(P / load_s / 1e9 / h2d_peak, 4),
+        "restore_frac_of_pcie_gen5": round(P / load_s / 1e9 / PCIE_GEN5_X16_GBPS, 4),
+        "save_gbps": round(P / save_s / 1e9, 3),
+        "save_ms_per_prefix": round(save_s * 1e3, 3),
+        "save_frac_of_measured_d2h_peak": round(P / save_s / 1e9 / d2h_peak, 4),
+        "save_frac_of_pcie_gen5": round(P / save_s / 1e9 / PCIE_GEN5_X16_GBPS, 4),
+        "restore_kernel_ms": round(statistics.median(k_load), 3) if k_load else None,
+        "save_kernel_ms": round(statistics.median(k_save), 3) if k_save else None,
+        "host_link_peak_gbps": {"h2d": round(h2d_peak, 2), "d2h": round(d2h_peak, 2),
+                                "pcie_gen5_x16": PCIE_GEN5_X16_GBPS},
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gather_gbps, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(gather_gbps / HBM_PEAK_GBPS, 4),
+            "traffic": None,
+            "kernel": "copy_chunks_v16_kernel<1,nt,nt> 512 threads (device gather: 40960 chunks of 32 KiB, 1 launch)",
+            "bytes_per_launch": 2 * P,
+            "ms_per_launch": round(gather_ms, 4),
+        },
+        "device_scatter": {"gbps": round(scatter_gbps, 1), "ms_per_launch": round(scatter_ms, 4),
+                           "frac": round(scatter_gbps / HBM_PEAK_GBPS, 4)},
+        "d2d_memcpy_gbps": round(d2d_gbps, 1),
+        "duplex": {"gbps": round(2 * P / t_dup / 1e9, 3), "ms_per_save_plus_restore":
+                   round(t_dup * 1e3, 3),
+                   "what": "a prefix saved while another is restored (two transfer contexts)"},
+        "bit_exact": bad_host == 0 and bad_dev == 0,
+        "cpu_baseline": cpu,
+    }
+    if variants:
+        out["variants"] = variants
+    if sweep:
+        out["gather_sweep_gbps"] = sweep
+    print(json.dumps(out), flush=True)
+    xfer.close()
+    pool.close()
+    gather_buf.close()
+    layers.close()
+    if not out["bit_exact"]:
+        sys.exit(1)
+
+
+if __name__ == "__main__":
+    main()

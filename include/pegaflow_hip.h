@@ -129,6 +129,8 @@ int pf_memcpy_h2d(uint64_t dst_dev, const void* src, uint64_t size);
 int pf_memcpy_d2h(void* dst, uint64_t src_dev, uint64_t size);
 int pf_memcpy_d2d(uint64_t dst_dev, uint64_t src_dev, uint64_t size);
 int pf_memset_d8(uint64_t dst_dev, uint8_t value, uint64_t size);
+/* hipMemcpyAsync with the direction inferred from the addresses. */
+int pf_memcpy_async(uint64_t dst, uint64_t src, uint64_t size, pf_stream stream);
 /* Free and total device memory in bytes. */
 int pf_mem_get_info(uint64_t* free_bytes, uint64_t* total_bytes);
 
@@ -243,10 +245,17 @@ pf_stream pf_xfer_stream(pf_xfer* xfer);
 int pf_xfer_synchronize(pf_xfer* xfer);
 /* Select the kernel's launch shape: threads per workgroup (64..1024, multiple
  * of 64) and 16-byte loads in flight per lane (1, 2, 4, 8 or 16), optionally
- * OR-ed with PF_KERNEL_NONTEMPORAL for non-temporal loads and stores.  0 keeps
- * the current value.  Defaults: 256 threads, 8 loads, temporal accesses. */
-#define PF_KERNEL_NONTEMPORAL 0x100u
+ * OR-ed with PF_KERNEL_NT_LOADS and/or PF_KERNEL_NT_STORES for non-temporal
+ * (streaming) loads and stores.  0 keeps the current value.  Defaults: 512
+ * threads, 1 load, non-temporal loads and stores (the fastest shape measured
+ * for the HBM gather on MI355X). */
+#define PF_KERNEL_NT_LOADS 0x100u
+#define PF_KERNEL_NT_STORES 0x200u
+#define PF_KERNEL_NONTEMPORAL (PF_KERNEL_NT_LOADS | PF_KERNEL_NT_STORES)
 int pf_xfer_set_kernel_shape(pf_xfer* xfer, uint32_t threads, uint32_t unroll);
+/* Upper bound on workgroups per gather/scatter launch (0 = one workgroup per
+ * tile, the default); with a bound, each workgroup loops over tiles. */
+int pf_xfer_set_max_grid(pf_xfer* xfer, uint32_t max_workgroups);
 /* Number of gather/scatter kernel launches and DMA copies issued by the last
  * save/load call on this context. */
 int pf_xfer_last_stats(pf_xfer* xfer, uint64_t* kernel_launches,

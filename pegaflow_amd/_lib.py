@@ -61,7 +61,9 @@ PINNED_COHERENT = 1
 PINNED_NONCOHERENT = 2
 PINNED_NUMA_USER = 4
 
-KERNEL_NONTEMPORAL = 0x100
+KERNEL_NT_LOADS = 0x100
+KERNEL_NT_STORES = 0x200
+KERNEL_NONTEMPORAL = KERNEL_NT_LOADS | KERNEL_NT_STORES
 
 LOAD_PENDING, LOAD_SUCCESS, LOAD_ERROR = 0, 1, -1
 
@@ -152,6 +154,7 @@ SIGNATURES = {
     "pf_memcpy_d2h": (i32, [vp, u64, u64]),
     "pf_memcpy_d2d": (i32, [u64, u64, u64]),
     "pf_memset_d8": (i32, [u64, ctypes.c_uint8, u64]),
+    "pf_memcpy_async": (i32, [u64, u64, u64, vp]),
     "pf_mem_get_info": (i32, [pu64, pu64]),
     "pf_pinned_allocate": (i32, [u64, u32, pvp, pu64]),
     "pf_pinned_free": (i32, [vp]),
@@ -168,6 +171,9 @@ SIGNATURES = {
     "pf_xfer_synchronize": (i32, [vp]),
     "pf_xfer_set_kernel_shape": (i32, [vp, u32, u32]),
     "pf_xfer_last_stats": (i32, [vp, pu64, pu64]),
+    "pf_xfer_set_max_grid": (i32, [vp, u32]),
+    "pf_xfer_set_timing": (i32, [vp, i32]),
+    "pf_xfer_last_kernel_ms": (i32, [vp, ctypes.POINTER(ctypes.c_float), pu64]),
     "pf_save_layers": (i32, [vp, ctypes.POINTER(LayerXfer), u32, u32]),
     "pf_load_layers": (i32, [vp, ctypes.POINTER(LayerXfer), u32, u32, pvp]),
     "pf_fill_random": (i32, [u64, u64, u64, u64, vp]),

@@ -38,7 +38,7 @@ struct ChunkDesc {
 hipError_t launch_copy_chunks(const ChunkDesc* d_descs, uint32_t n_chunks,
                               uint64_t chunk_bytes, bool aligned16,
                               uint32_t threads, uint32_t unroll,
-                              hipStream_t stream);
+                              uint32_t max_grid, hipStream_t stream);
 hipError_t launch_fill_random(uint64_t dst, uint64_t size_bytes, uint64_t seed,
                               uint64_t word_offset, hipStream_t stream);
 hipError_t launch_verify_random(uint64_t addr, uint64_t size_bytes,

@@ -31,7 +31,26 @@ typedef __attribute__((address_space(1))) u32x4 g_u32x4;
 typedef __attribute__((address_space(1))) uint8_t g_u8;
 typedef __attribute__((address_space(1))) uint64_t g_u64;
 
-template <int UNROLL, bool NT>
+template <bool NT>
+__device__ __forceinline__ u32x4 load16(const g_u32x4* p) {
+  if constexpr (NT)
+    return __builtin_nontemporal_load(p);
+  else
+    return *p;
+}
+
+template <bool NT>
+__device__ __forceinline__ void store16(g_u32x4* p, u32x4 v) {
+  if constexpr (NT)
+    __builtin_nontemporal_store(v, p);
+  else
+    *p = v;
+}
+
+// NTL / NTS select non-temporal (streaming) loads / stores: every byte is
+// touched exactly once, so there is nothing to gain from keeping it in L2 or
+// the MALL, and streaming accesses leave those caches to other traffic.
+template <int UNROLL, bool NTL, bool NTS>
 __global__ void __launch_bounds__(1024)
 copy_chunks_v16_kernel(const ChunkDesc* __restrict__ descs,
                        uint32_t tiles_per_chunk, uint32_t n_tiles,
@@ -46,34 +65,23 @@ copy_chunks_v16_kernel(const ChunkDesc* __restrict__ descs,
     g_u32x4* __restrict__ dst = reinterpret_cast<g_u32x4*>(d.dst);
     const uint32_t tile_base = tile * tile_elems;
     const uint32_t base = tile_base + threadIdx.x;
+    u32x4 v[UNROLL];
     if (tile_base + tile_elems <= chunk16) {
-      u32x4 v[UNROLL];
 #pragma unroll
-      for (int u = 0; u < UNROLL; ++u) {
-        if constexpr (NT)
-          v[u] = __builtin_nontemporal_load(src + base + u * stride);
-        else
-          v[u] = src[base + u * stride];
-      }
+      for (int u = 0; u < UNROLL; ++u) v[u] = load16<NTL>(src + base + u * stride);
 #pragma unroll
-      for (int u = 0; u < UNROLL; ++u) {
-        if constexpr (NT)
-          __builtin_nontemporal_store(v[u], dst + base + u * stride);
-        else
-          dst[base + u * stride] = v[u];
-      }
+      for (int u = 0; u < UNROLL; ++u) store16<NTS>(dst + base + u * stride, v[u]);
     } else {
       // Partial last tile of a chunk: guarded per element.
-      u32x4 v[UNROLL];
 #pragma unroll
       for (int u = 0; u < UNROLL; ++u) {
         const uint32_t e = base + u * stride;
-        if (e < chunk16) v[u] = src[e];
+        if (e < chunk16) v[u] = load16<NTL>(src + e);
       }
 #pragma unroll
       for (int u = 0; u < UNROLL; ++u) {
         const uint32_t e = base + u * stride;
-        if (e < chunk16) dst[e] = v[u];
+        if (e < chunk16) store16<NTS>(dst + e, v[u]);
       }
     }
   }
@@ -94,32 +102,47 @@ copy_chunks_b1_kernel(const ChunkDesc* __restrict__ descs, uint32_t n_chunks,
 // Upper bound on workgroups per launch; larger tile counts loop.
 static constexpr uint32_t kMaxGrid = 1u << 20;
 
+template <int UNROLL, bool NTL, bool NTS>
+static void launch_v16_nt(dim3 grid, dim3 block, hipStream_t stream, const ChunkDesc* d,
+                          uint32_t tpc, uint32_t n_tiles, uint32_t c16) {
+  hipLaunchKernelGGL((copy_chunks_v16_kernel<UNROLL, NTL, NTS>), grid, block, 0, stream, d,
+                     tpc, n_tiles, c16);
+}
+
 template <int UNROLL>
 static hipError_t launch_v16(const ChunkDesc* d_descs, uint32_t tiles_per_chunk,
                              uint32_t n_tiles, uint32_t chunk16, uint32_t threads,
-                             bool nt, hipStream_t stream) {
-  const uint32_t grid = n_tiles < kMaxGrid ? n_tiles : kMaxGrid;
-  if (nt)
-    hipLaunchKernelGGL((copy_chunks_v16_kernel<UNROLL, true>), dim3(grid),
-                       dim3(threads), 0, stream, d_descs, tiles_per_chunk,
-                       n_tiles, chunk16);
-  else
-    hipLaunchKernelGGL((copy_chunks_v16_kernel<UNROLL, false>), dim3(grid),
-                       dim3(threads), 0, stream, d_descs, tiles_per_chunk,
-                       n_tiles, chunk16);
+                             uint32_t nt_flags, uint32_t max_grid, hipStream_t stream) {
+  const uint32_t cap = max_grid ? max_grid : kMaxGrid;
+  const dim3 grid(n_tiles < cap ? n_tiles : cap), block(threads);
+  switch (nt_flags) {
+    case 0:
+      launch_v16_nt<UNROLL, false, false>(grid, block, stream, d_descs, tiles_per_chunk, n_tiles, chunk16);
+      break;
+    case PF_KERNEL_NT_LOADS:
+      launch_v16_nt<UNROLL, true, false>(grid, block, stream, d_descs, tiles_per_chunk, n_tiles, chunk16);
+      break;
+    case PF_KERNEL_NT_STORES:
+      launch_v16_nt<UNROLL, false, true>(grid, block, stream, d_descs, tiles_per_chunk, n_tiles, chunk16);
+      break;
+    default:
+      launch_v16_nt<UNROLL, true, true>(grid, block, stream, d_descs, tiles_per_chunk, n_tiles, chunk16);
+      break;
+  }
   return hipGetLastError();
 }
 
-// `unroll` may carry PF_KERNEL_NONTEMPORAL (0x100) to select non-temporal
-// loads and stores.
+// `unroll` carries the loads in flight per lane (low byte) and the
+// PF_KERNEL_NT_LOADS / PF_KERNEL_NT_STORES flags.
 hipError_t launch_copy_chunks(const ChunkDesc* d_descs, uint32_t n_chunks,
                               uint64_t chunk_bytes, bool aligned16,
                               uint32_t threads, uint32_t unroll,
-                              hipStream_t stream) {
+                              uint32_t max_grid, hipStream_t stream) {
   if (n_chunks == 0 || chunk_bytes == 0) return hipSuccess;
   if (threads == 0 || threads > 1024 || threads % 64 != 0) return hipErrorInvalidValue;
-  const bool nt = (unroll & 0x100u) != 0;
+  const uint32_t nt = unroll & PF_KERNEL_NONTEMPORAL;
   unroll &= 0xffu;
+  if (max_grid > kMaxGrid) max_grid = kMaxGrid;
   if (!aligned16) {
     const uint32_t grid = n_chunks < kMaxGrid ? n_chunks : kMaxGrid;
     hipLaunchKernelGGL(copy_chunks_b1_kernel, dim3(grid), dim3(threads), 0,
@@ -127,7 +150,7 @@ hipError_t launch_copy_chunks(const ChunkDesc* d_descs, uint32_t n_chunks,
     return hipGetLastError();
   }
   const uint64_t chunk16 = chunk_bytes / 16;
-  if (chunk16 > 0xffffffffull) return hipErrorInvalidValue;
+  if (chunk16 >= (1ull << 31)) return hipErrorInvalidValue;
   const uint64_t tile_elems = static_cast<uint64_t>(threads) * unroll;
   if (tile_elems == 0) return hipErrorInvalidValue;
   const uint64_t tiles_per_chunk = (chunk16 + tile_elems - 1) / tile_elems;
@@ -136,15 +159,16 @@ hipError_t launch_copy_chunks(const ChunkDesc* d_descs, uint32_t n_chunks,
   // Every tile index < n_tiles maps to chunk < n_chunks and element offsets
   // < tiles_per_chunk * tile_elems; elements >= chunk16 are masked, and the
   // full-tile path is taken only when the whole tile lies below chunk16.
+  // chunk16 < 2^31 and tile_elems <= 16384 keep tile_base + tile_elems in 32 bits.
   const uint32_t tpc = static_cast<uint32_t>(tiles_per_chunk);
-  const uint32_t nt_ = static_cast<uint32_t>(n_tiles);
+  const uint32_t ntl = static_cast<uint32_t>(n_tiles);
   const uint32_t c16 = static_cast<uint32_t>(chunk16);
   switch (unroll) {
-    case 1: return launch_v16<1>(d_descs, tpc, nt_, c16, threads, nt, stream);
-    case 2: return launch_v16<2>(d_descs, tpc, nt_, c16, threads, nt, stream);
-    case 4: return launch_v16<4>(d_descs, tpc, nt_, c16, threads, nt, stream);
-    case 8: return launch_v16<8>(d_descs, tpc, nt_, c16, threads, nt, stream);
-    case 16: return launch_v16<16>(d_descs, tpc, nt_, c16, threads, nt, stream);
+    case 1: return launch_v16<1>(d_descs, tpc, ntl, c16, threads, nt, max_grid, stream);
+    case 2: return launch_v16<2>(d_descs, tpc, ntl, c16, threads, nt, max_grid, stream);
+    case 4: return launch_v16<4>(d_descs, tpc, ntl, c16, threads, nt, max_grid, stream);
+    case 8: return launch_v16<8>(d_descs, tpc, ntl, c16, threads, nt, max_grid, stream);
+    case 16: return launch_v16<16>(d_descs, tpc, ntl, c16, threads, nt, max_grid, stream);
     default: return hipErrorInvalidValue;
   }
 }

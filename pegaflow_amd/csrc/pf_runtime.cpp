@@ -258,6 +258,12 @@ int pf_memset_d8(uint64_t dst_dev, uint8_t value, uint64_t size) {
   return PF_OK;
 }
 
+int pf_memcpy_async(uint64_t dst, uint64_t src, uint64_t size, pf_stream stream) {
+  PF_HIP(hipMemcpyAsync(reinterpret_cast<void*>(dst), reinterpret_cast<const void*>(src), size,
+                        hipMemcpyDefault, static_cast<hipStream_t>(stream)));
+  return PF_OK;
+}
+
 int pf_mem_get_info(uint64_t* free_bytes, uint64_t* total_bytes) {
   size_t f = 0, t = 0;
   PF_HIP(hipMemGetInfo(&f, &t));

@@ -242,8 +242,13 @@ struct pf_xfer {
   uint64_t slot_bytes = 0;
   hipEvent_t slot_ready[2] = {nullptr, nullptr};
   hipEvent_t slot_free[2] = {nullptr, nullptr};
-  uint32_t threads = 256;
-  uint32_t unroll = 8;
+  // Default launch shape: 512 threads, one non-temporal 16-byte load in flight
+  // per lane, i.e. one 8 KiB tile per workgroup (the fastest HBM gather shape
+  // measured on MI355X; the host-link-bound zero-copy paths are insensitive
+  // to the shape).
+  uint32_t threads = 512;
+  uint32_t unroll = 1 | PF_KERNEL_NONTEMPORAL;
+  uint32_t max_grid = 0;
   uint64_t last_kernels = 0;
   uint64_t last_dma = 0;
   bool timing = false;
@@ -312,7 +317,7 @@ int launch(pf_xfer* x, size_t first, size_t n, uint64_t chunk_bytes, bool al16) 
   (void)hipGetLastError();
   hipError_t e = launch_copy_chunks(x->d_desc + first, static_cast<uint32_t>(n),
                                     chunk_bytes, al16, x->threads, x->unroll,
-                                    x->stream);
+                                    x->max_grid, x->stream);
   if (e != hipSuccess) return hip_fail(e, "gather/scatter kernel launch");
   if (tm) PF_HIP(hipEventRecord(tm->second, x->stream));
   x->last_kernels++;
@@ -741,7 +746,8 @@ int pf_xfer_set_kernel_shape(pf_xfer* x, uint32_t threads, uint32_t unroll) {
   const uint32_t u = unroll & 0xffu;
   if (unroll && u != 1 && u != 2 && u != 4 && u != 8 && u != 16)
     return fail(PF_ERR_INVALID_ARGUMENT, "unroll must be 1, 2, 4, 8 or 16");
-  if (unroll & ~0x1ffu) return fail(PF_ERR_INVALID_ARGUMENT, "unknown kernel flag");
+  if (unroll & ~(0xffu | PF_KERNEL_NONTEMPORAL))
+    return fail(PF_ERR_INVALID_ARGUMENT, "unknown kernel flag");
   std::lock_guard<std::mutex> lk(x->mu);
   if (threads) x->threads = threads;
   if (unroll) x->unroll = unroll;
@@ -752,6 +758,13 @@ int pf_xfer_last_stats(pf_xfer* x, uint64_t* kernel_launches, uint64_t* dma_copi
   if (!x) return fail(PF_ERR_INVALID_ARGUMENT, "null transfer context");
   if (kernel_launches) *kernel_launches = x->last_kernels;
   if (dma_copies) *dma_copies = x->last_dma;
+  return PF_OK;
+}
+
+int pf_xfer_set_max_grid(pf_xfer* x, uint32_t max_workgroups) {
+  if (!x) return fail(PF_ERR_INVALID_ARGUMENT, "null transfer context");
+  std::lock_guard<std::mutex> lk(x->mu);
+  x->max_grid = max_workgroups;
   return PF_OK;
 }
 

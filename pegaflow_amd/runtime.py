@@ -215,6 +215,11 @@ def compare(a: int, b: int, nbytes: int) -> int:
     return out.value
 
 
+def memcpy_async(dst: int, src: int, nbytes: int, stream: Stream) -> None:
+    """hipMemcpyAsync (direction inferred) on stream."""
+    check(lib().pf_memcpy_async(dst, src, nbytes, stream.handle), "pf_memcpy_async")
+
+
 def spin(stream: Stream, microseconds: int) -> None:
     check(lib().pf_spin(stream.handle, microseconds), "pf_spin")
 

@@ -203,6 +203,19 @@ class TransferContext:
               "pf_xfer_last_stats")
         return k.value, d.value
 
+    def set_max_grid(self, max_workgroups: int) -> None:
+        check(lib().pf_xfer_set_max_grid(self.handle, max_workgroups), "pf_xfer_set_max_grid")
+
+    def set_timing(self, enable: bool) -> None:
+        check(lib().pf_xfer_set_timing(self.handle, int(enable)), "pf_xfer_set_timing")
+
+    def last_kernel_ms(self):
+        """(summed kernel ms, launches) of the last call, with timing enabled."""
+        ms, n = ctypes.c_float(), ctypes.c_uint64()
+        check(lib().pf_xfer_last_kernel_ms(self.handle, ctypes.byref(ms), ctypes.byref(n)),
+              "pf_xfer_last_kernel_ms")
+        return float(ms.value), n.value
+
     def save_layers(self, layers: Sequence[LayerTransfer], mode: int = _lib.MODE_KERNEL) -> None:
         """Device -> host for every layer; returns when bytes are in place."""
         arr, keep = _layer_array(layers)

@@ -311,11 +311,24 @@ def test_empty_and_errors(ctx, gpu):
 def test_kernel_shapes_and_nontemporal(ctx, shape):
     threads, unroll = shape
     say(f"[gpu] kernel shape threads={threads} unroll={unroll}")
-    for nt in (0, _lib.KERNEL_NONTEMPORAL):
+    for nt in (0, _lib.KERNEL_NT_LOADS, _lib.KERNEL_NT_STORES, _lib.KERNEL_NONTEMPORAL):
         ctx.set_kernel_shape(threads, unroll | nt)
         _oracle_roundtrip_case(ctx, _lib.MODE_KERNEL, 64, 73728, 1, 0, 64 * 73728,
                                [5, 60, 2, 33], [0, 1, 63, 9], seed=threads + unroll)
-    ctx.set_kernel_shape(256, 8)
+        # Segments that end in a partial tile of every shape.
+        _oracle_roundtrip_case(ctx, _lib.MODE_KERNEL, 20, 16 * 1000, 2, 20 * 16000,
+                               40 * 16000, [3, 19, 0], [5, 6, 7], seed=nt + 1)
+    ctx.set_kernel_shape(512, 1 | _lib.KERNEL_NONTEMPORAL)
+    ctx.set_max_grid(0)
+
+
+def test_capped_grid_loops_over_tiles(ctx):
+    say("[gpu] capped grid")
+    for grid in (1, 7, 256):
+        ctx.set_max_grid(grid)
+        _oracle_roundtrip_case(ctx, _lib.MODE_KERNEL, 64, 32768, 2, 64 * 32768, 128 * 32768,
+                               list(range(0, 64, 3)), list(range(63, -1, -3)), seed=grid)
+    ctx.set_max_grid(0)
 
 
 def _full_size(ctx, n_layers, nb, bpb, segs, n_blocks, save_mode, load_mode, seed=0):
