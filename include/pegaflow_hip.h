@@ -337,6 +337,98 @@ uint32_t pf_load_state_num_layers(const pf_load_state* state);
 int64_t pf_load_state_layers_done(const pf_load_state* state);
 void pf_load_state_set_layers_done(pf_load_state* state, int64_t n);
 
+/* ------------------------------------------------------------------------ */
+/* Pool allocator.  Replaces ScaledOffsetAllocator (allocator.rs:66-171):     */
+/* byte requests rounded up to whole units, 32-bit unit counts.               */
+/* ------------------------------------------------------------------------ */
+typedef struct pf_allocator pf_allocator;
+/* unit_size 0 is "unit size must be greater than zero" (allocator.rs:110). */
+int pf_allocator_create(uint64_t total_bytes, uint64_t unit_size,
+                        pf_allocator** out);
+/* Smallest unit that keeps the unit count within 32 bits (allocator.rs:77-86). */
+int pf_allocator_create_auto(uint64_t total_bytes, pf_allocator** out);
+int pf_allocator_destroy(pf_allocator* a);
+/* *found = 0 when no free region fits (or size_bytes == 0); a request whose
+ * unit count exceeds 32 bits is PF_ERR_INVALID_ARGUMENT (RequestTooLarge). */
+int pf_allocator_allocate(pf_allocator* a, uint64_t size_bytes, int* found,
+                          uint64_t* offset, uint64_t* size);
+int pf_allocator_free(pf_allocator* a, uint64_t offset);
+/* StorageReportBytes plus totals (allocator.rs:157-177). */
+int pf_allocator_report(pf_allocator* a, uint64_t* total_bytes,
+                        uint64_t* free_bytes, uint64_t* largest_free_bytes,
+                        uint64_t* unit_size);
+
+/* ------------------------------------------------------------------------ */
+/* Engine.  Replaces PegaEngine (lib.rs:93-1069) with its StorageEngine       */
+/* (storage.rs) and GpuWorkerPool (gpu_worker.rs).  Names and argument order  */
+/* follow the reference's Python bindings (python/src/lib.rs:122-261).        */
+/* Hash lists are passed as one byte buffer and n+1 offsets: hash i is        */
+/* hash_data[hash_offsets[i] .. hash_offsets[i+1]).                           */
+/* ------------------------------------------------------------------------ */
+typedef struct pf_engine pf_engine;
+enum {
+  PF_POOL_PINNED = 0, /* hipHostMalloc pool, mapped for device access        */
+  PF_POOL_HOST = 1    /* plain host memory: bookkeeping only, no transfers   */
+};
+/* PegaEngine::new_with_pool_size (lib.rs:284-288).  unit_hint 0 = default. */
+int pf_engine_create(uint64_t pool_bytes, uint32_t pool_kind,
+                     uint32_t pinned_flags, uint64_t unit_hint,
+                     pf_engine** out);
+int pf_engine_destroy(pf_engine* e);
+/* Transfer strategies used by saves and loads (default PF_MODE_KERNEL). */
+int pf_engine_set_modes(pf_engine* e, uint32_t save_mode, uint32_t load_mode);
+/* register_context_layer (lib.rs:373-469). */
+int pf_engine_register_context_layer(pf_engine* e, const char* instance_id,
+                                     const char* namespace_, int device_id,
+                                     const char* layer_name, uint64_t data_ptr,
+                                     uint64_t size_bytes, uint64_t num_blocks,
+                                     uint64_t bytes_per_block,
+                                     uint64_t kv_stride_bytes,
+                                     uint64_t segments, uint64_t tp_rank,
+                                     uint64_t tp_size, uint64_t num_layers);
+/* unregister_instance (lib.rs:473-484). */
+int pf_engine_unregister_instance(pf_engine* e, const char* instance_id);
+/* count_prefix_hit_blocks (lib.rs:803-838). */
+int pf_engine_count_prefix_hit_blocks(pf_engine* e, const char* instance_id,
+                                      const uint8_t* hash_data,
+                                      const uint64_t* hash_offsets, uint64_t n,
+                                      uint64_t* hits);
+/* One layer of a save batch: (layer_name, block_ids, block_hashes). */
+typedef struct pf_save_layer {
+  const char* layer_name;
+  const int32_t* block_ids;
+  uint64_t num_blocks;
+  const uint8_t* hash_data;
+  const uint64_t* hash_offsets;
+} pf_save_layer;
+/* batch_save_kv_blocks_from_ipc (lib.rs:497-782): blocking; every layer of
+ * the batch is copied by one batched transfer. */
+int pf_engine_batch_save(pf_engine* e, const char* instance_id,
+                         uint64_t tp_rank, int device_id,
+                         const pf_save_layer* layers, uint32_t num_layers);
+/* batch_load_kv_blocks_multi_layer (lib.rs:957-1069): returns once the load
+ * is queued; completion (and, for a layered LoadState, per-layer progress) is
+ * published in the LoadState named load_state_shm. */
+int pf_engine_batch_load(pf_engine* e, const char* instance_id,
+                         uint64_t tp_rank, int device_id,
+                         const char* load_state_shm,
+                         const char* const* layer_names, uint32_t num_layers,
+                         const int32_t* block_ids, const uint8_t* hash_data,
+                         const uint64_t* hash_offsets, uint64_t n);
+typedef struct pf_engine_stats {
+  uint64_t pool_used_bytes;
+  uint64_t pool_total_bytes;
+  uint64_t sealed_blocks;
+  uint64_t inflight_blocks;
+  uint64_t evicted_blocks;
+  uint64_t saved_bytes;
+  uint64_t loaded_bytes;
+  uint64_t load_failures;
+} pf_engine_stats;
+int pf_engine_stats_get(pf_engine* e, pf_engine_stats* out);
+/* Block until every queued load has finished. */
+int pf_engine_wait_idle(pf_engine* e);
+
 #ifdef __cplusplus
 }
 #endif

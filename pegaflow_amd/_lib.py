@@ -114,6 +114,24 @@ class LayerXfer(ctypes.Structure):
     ]
 
 
+class SaveLayer(ctypes.Structure):
+    """pf_save_layer — one (layer_name, block_ids, block_hashes) of a save batch."""
+
+    _fields_ = [
+        ("layer_name", ctypes.c_char_p),
+        ("block_ids", ctypes.c_void_p),
+        ("num_blocks", ctypes.c_uint64),
+        ("hash_data", ctypes.c_void_p),
+        ("hash_offsets", ctypes.c_void_p),
+    ]
+
+
+class EngineStats(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint64) for n in (
+        "pool_used_bytes", "pool_total_bytes", "sealed_blocks", "inflight_blocks",
+        "evicted_blocks", "saved_bytes", "loaded_bytes", "load_failures")]
+
+
 u64 = ctypes.c_uint64
 i64 = ctypes.c_int64
 u32 = ctypes.c_uint32
@@ -192,6 +210,24 @@ SIGNATURES = {
     "pf_load_state_num_layers": (u32, [vp]),
     "pf_load_state_layers_done": (i64, [vp]),
     "pf_load_state_set_layers_done": (None, [vp, i64]),
+    "pf_allocator_create": (i32, [u64, u64, pvp]),
+    "pf_allocator_create_auto": (i32, [u64, pvp]),
+    "pf_allocator_destroy": (i32, [vp]),
+    "pf_allocator_allocate": (i32, [vp, u64, pi32, pu64, pu64]),
+    "pf_allocator_free": (i32, [vp, u64]),
+    "pf_allocator_report": (i32, [vp, pu64, pu64, pu64, pu64]),
+    "pf_engine_create": (i32, [u64, u32, u32, u64, pvp]),
+    "pf_engine_destroy": (i32, [vp]),
+    "pf_engine_set_modes": (i32, [vp, u32, u32]),
+    "pf_engine_register_context_layer": (i32, [vp, cs, cs, i32, cs, u64, u64, u64, u64, u64,
+                                               u64, u64, u64, u64]),
+    "pf_engine_unregister_instance": (i32, [vp, cs]),
+    "pf_engine_count_prefix_hit_blocks": (i32, [vp, cs, vp, vp, u64, pu64]),
+    "pf_engine_batch_save": (i32, [vp, cs, u64, i32, ctypes.POINTER(SaveLayer), u32]),
+    "pf_engine_batch_load": (i32, [vp, cs, u64, i32, cs, ctypes.POINTER(cs), u32, vp, vp, vp,
+                                   u64]),
+    "pf_engine_stats_get": (i32, [vp, ctypes.POINTER(EngineStats)]),
+    "pf_engine_wait_idle": (i32, [vp]),
 }
 
 _lib = None

@@ -1,0 +1,946 @@
+// pf_engine.cpp — PegaEngine: instances and layer registrations, the pinned
+// block store, and per-device save/load workers (the roles of
+// pegaflow-core/src/{lib,storage,pinned_pool,allocator,gpu_worker}.rs).
+//
+// Save by hash: planning follows lib.rs:553-782 layer by layer (filtering,
+// dedup against sealed and inflight blocks, the split K/V host layout), but
+// all layers of a batch are then copied by one batched transfer
+// (pf_save_layers) instead of one synchronous DMA per segment.
+// Load by hash: lib.rs:957-1069; the device worker runs the transfer with one
+// event per layer and publishes progress in the LoadState as layers land.
+#include "pf_engine.h"
+
+#include <algorithm>
+#include <atomic>
+#include <cstdlib>
+#include <cstring>
+#include <set>
+
+namespace pf {
+
+// ===========================================================================
+// UnitAllocator
+// ===========================================================================
+namespace {
+constexpr uint64_t kU32Max = 0xffffffffull;
+}
+
+int UnitAllocator::create(uint64_t total_bytes, uint64_t unit_size,
+                          std::unique_ptr<UnitAllocator>* out) {
+  if (unit_size == 0) return fail(PF_ERR_INVALID_ARGUMENT, "unit size must be greater than zero");
+  const uint64_t units = total_bytes / unit_size + (total_bytes % unit_size != 0);
+  if (units > kU32Max)
+    return fail(PF_ERR_INVALID_ARGUMENT,
+                strf("capacity %llu bytes with unit %llu overflows u32 backing allocator",
+                     (unsigned long long)total_bytes, (unsigned long long)unit_size));
+  auto a = std::unique_ptr<UnitAllocator>(new UnitAllocator());
+  a->unit_ = unit_size;
+  a->total_units_ = units;
+  a->free_units_ = 0;
+  if (units) a->insert_free(0, units);
+  *out = std::move(a);
+  return PF_OK;
+}
+
+void UnitAllocator::insert_free(uint64_t off, uint64_t units) {
+  free_by_off_[off] = units;
+  free_by_size_.insert({units, off});
+  free_units_ += units;
+}
+
+void UnitAllocator::erase_free(std::map<uint64_t, uint64_t>::iterator it) {
+  auto range = free_by_size_.equal_range(it->second);
+  for (auto s = range.first; s != range.second; ++s)
+    if (s->second == it->first) {
+      free_by_size_.erase(s);
+      break;
+    }
+  free_units_ -= it->second;
+  free_by_off_.erase(it);
+}
+
+int UnitAllocator::allocate(uint64_t size_bytes, bool* found, uint64_t* offset, uint64_t* size) {
+  *found = false;
+  if (size_bytes == 0) return PF_OK;
+  const uint64_t units = size_bytes / unit_ + (size_bytes % unit_ != 0);
+  if (units > kU32Max)
+    return fail(PF_ERR_INVALID_ARGUMENT,
+                strf("request %llu bytes with unit %llu overflows u32 backing allocator",
+                     (unsigned long long)size_bytes, (unsigned long long)unit_));
+  // Best fit; among regions of the best size, the lowest offset.
+  auto s = free_by_size_.lower_bound(units);
+  if (s == free_by_size_.end()) return PF_OK;
+  uint64_t best_units = s->first, best_off = s->second;
+  for (auto t = s; t != free_by_size_.end() && t->first == best_units; ++t)
+    best_off = std::min(best_off, t->second);
+  erase_free(free_by_off_.find(best_off));
+  if (best_units > units) insert_free(best_off + units, best_units - units);
+  used_[best_off] = units;
+  *found = true;
+  *offset = best_off * unit_;
+  *size = units * unit_;
+  return PF_OK;
+}
+
+void UnitAllocator::free(uint64_t offset_bytes) {
+  const uint64_t off = offset_bytes / unit_;
+  auto u = used_.find(off);
+  if (u == used_.end()) return;
+  uint64_t start = off, units = u->second;
+  used_.erase(u);
+  auto next = free_by_off_.find(start + units);
+  if (next != free_by_off_.end()) {
+    units += next->second;
+    erase_free(next);
+  }
+  auto prev = free_by_off_.lower_bound(start);
+  if (prev != free_by_off_.begin()) {
+    --prev;
+    if (prev->first + prev->second == start) {
+      start = prev->first;
+      units += prev->second;
+      erase_free(prev);
+    }
+  }
+  insert_free(start, units);
+}
+
+uint64_t UnitAllocator::largest_free_bytes() const {
+  return free_by_size_.empty() ? 0 : free_by_size_.rbegin()->first * unit_;
+}
+
+// ===========================================================================
+// PinnedPool
+// ===========================================================================
+PoolAllocation::~PoolAllocation() {
+  if (pool) pool->release(offset);
+}
+
+int PinnedPool::create(uint64_t size, uint64_t unit_hint, bool device_backed,
+                       uint32_t pinned_flags, std::shared_ptr<PinnedPool>* out) {
+  if (size == 0) return fail(PF_ERR_ZERO_SIZE, "Pinned memory pool size must be greater than zero");
+  // Units: the reference picks the smallest unit keeping 32-bit unit counts
+  // (or the value-size hint).  Here units are also at least 256 bytes so
+  // every block region starts 16-byte aligned for the vector kernels.
+  uint64_t unit = unit_hint ? unit_hint : (size > kU32Max ? (size + kU32Max - 1) / kU32Max : 1);
+  unit = std::max<uint64_t>(256, (unit + 255) / 256 * 256);
+  std::unique_ptr<UnitAllocator> alloc;
+  if (int rc = UnitAllocator::create(size, unit, &alloc)) return rc;
+  auto p = std::shared_ptr<PinnedPool>(new PinnedPool());
+  p->size_ = alloc->total_bytes();
+  p->device_backed_ = device_backed;
+  if (device_backed) {
+    void* host = nullptr;
+    uint64_t dev = 0;
+    if (int rc = pf_pinned_allocate(p->size_, pinned_flags, &host, &dev)) return rc;
+    p->base_ = static_cast<uint8_t*>(host);
+  } else {
+    const uint64_t rounded = (p->size_ + 4095) / 4096 * 4096;
+    p->base_ = static_cast<uint8_t*>(std::aligned_alloc(4096, rounded));
+    if (!p->base_) return fail(PF_ERR_STORAGE, "host pool allocation failed");
+  }
+  p->alloc_ = std::move(alloc);
+  *out = std::move(p);
+  return PF_OK;
+}
+
+PinnedPool::~PinnedPool() {
+  if (!base_) return;
+  if (device_backed_)
+    pf_pinned_free(base_);
+  else
+    std::free(base_);
+}
+
+std::shared_ptr<PoolAllocation> PinnedPool::allocate(uint64_t size) {
+  bool found = false;
+  uint64_t off = 0, got = 0;
+  {
+    std::lock_guard<std::mutex> lk(mu_);
+    if (alloc_->allocate(size, &found, &off, &got) != PF_OK || !found) return nullptr;
+  }
+  auto a = std::make_shared<PoolAllocation>();
+  a->pool = shared_from_this();
+  a->offset = off;
+  a->size = got;
+  a->ptr = base_ + off;
+  return a;
+}
+
+void PinnedPool::release(uint64_t offset) {
+  std::lock_guard<std::mutex> lk(mu_);
+  alloc_->free(offset);
+}
+
+void PinnedPool::usage(uint64_t* used, uint64_t* total) {
+  std::lock_guard<std::mutex> lk(mu_);
+  *total = alloc_->total_bytes();
+  *used = *total - alloc_->free_bytes();
+}
+
+uint64_t PinnedPool::largest_free() {
+  std::lock_guard<std::mutex> lk(mu_);
+  return alloc_->largest_free_bytes();
+}
+
+// ===========================================================================
+// BlockStore
+// ===========================================================================
+namespace {
+constexpr size_t kReclaimBatch = 64;  // storage.rs:41
+}
+
+size_t BlockStore::evict_lru(size_t max_blocks) {
+  std::vector<std::shared_ptr<SealedBlock>> dropped;
+  {
+    std::lock_guard<std::mutex> lk(cache_mu_);
+    while (dropped.size() < max_blocks && !lru_.empty()) {
+      auto it = cache_.find(lru_.back());
+      dropped.push_back(std::move(it->second.block));
+      cache_.erase(it);
+      lru_.pop_back();
+    }
+    evictions_ += dropped.size();
+  }
+  return dropped.size();  // memory returns to the pool as the handles drop here
+}
+
+std::shared_ptr<PoolAllocation> BlockStore::allocate(uint64_t size) {
+  for (;;) {
+    if (auto a = pool_->allocate(size)) return a;
+    uint64_t largest = pool_->largest_free();
+    while (largest < size) {
+      if (evict_lru(kReclaimBatch) == 0) break;
+      largest = pool_->largest_free();
+    }
+    if (largest < size) return nullptr;
+  }
+}
+
+bool BlockStore::cache_contains(const std::string& key) {
+  std::lock_guard<std::mutex> lk(cache_mu_);
+  return cache_.count(key) != 0;
+}
+
+bool BlockStore::inflight_has_slot(const std::string& key, size_t slot) {
+  std::lock_guard<std::mutex> lk(inflight_mu_);
+  auto it = inflight_.find(key);
+  return it != inflight_.end() && slot < it->second.slots.size() && it->second.slots[slot];
+}
+
+int BlockStore::insert_slot(const std::string& key, size_t slot, std::shared_ptr<LayerBlock> block,
+                            size_t total_slots, bool* inserted) {
+  *inserted = false;
+  if (cache_contains(key)) return PF_OK;
+  std::shared_ptr<SealedBlock> sealed;
+  {
+    std::lock_guard<std::mutex> lk(inflight_mu_);
+    auto it = inflight_.find(key);
+    if (it == inflight_.end()) {
+      InflightBlock ib;
+      ib.slots.resize(total_slots);
+      ib.remaining = total_slots;
+      it = inflight_.emplace(key, std::move(ib)).first;
+    }
+    InflightBlock& ib = it->second;
+    if (slot < ib.slots.size() && ib.slots[slot]) return PF_OK;
+    if (total_slots != ib.slots.size())
+      return fail(PF_ERR_STORAGE, strf("slot count mismatch: expected %zu, got %zu",
+                                       ib.slots.size(), total_slots));
+    if (slot >= ib.slots.size())
+      return fail(PF_ERR_STORAGE,
+                  strf("slot_id %zu out of bounds (%zu slots)", slot, ib.slots.size()));
+    ib.footprint += block->size;
+    ib.slots[slot] = std::move(block);
+    ib.remaining -= 1;
+    if (ib.remaining == 0) {
+      sealed = std::make_shared<SealedBlock>();
+      sealed->slots = std::move(ib.slots);
+      sealed->footprint = ib.footprint;
+      inflight_.erase(it);
+    }
+  }
+  if (sealed) {
+    std::lock_guard<std::mutex> lk(cache_mu_);
+    if (!cache_.count(key)) {
+      lru_.push_front(key);
+      cache_[key] = Entry{std::move(sealed), lru_.begin()};
+    }
+  }
+  *inserted = true;
+  return PF_OK;
+}
+
+int BlockStore::lookup_many(const std::vector<std::string>& keys,
+                            std::vector<std::shared_ptr<SealedBlock>>* out) {
+  std::lock_guard<std::mutex> lk(cache_mu_);
+  out->clear();
+  out->reserve(keys.size());
+  for (size_t i = 0; i < keys.size(); ++i) {
+    auto it = cache_.find(keys[i]);
+    if (it == cache_.end()) {
+      const size_t sep = keys[i].find('\0');
+      return fail(PF_ERR_STORAGE,
+                  strf("missing KV block hash at index %zu (namespace=%s, hash_len=%zu)", i,
+                       keys[i].substr(0, sep).c_str(),
+                       sep == std::string::npos ? keys[i].size() : keys[i].size() - sep - 1));
+    }
+    lru_.splice(lru_.begin(), lru_, it->second.pos);
+    out->push_back(it->second.block);
+  }
+  return PF_OK;
+}
+
+uint64_t BlockStore::sealed_count() {
+  std::lock_guard<std::mutex> lk(cache_mu_);
+  return cache_.size();
+}
+
+uint64_t BlockStore::inflight_count() {
+  std::lock_guard<std::mutex> lk(inflight_mu_);
+  return inflight_.size();
+}
+
+// ===========================================================================
+// Device worker: one save context (used by the calling thread) and one load
+// thread with its own context (gpu_worker.rs:52-201).
+// ===========================================================================
+struct LoadTask {
+  std::vector<std::string> names;
+  std::vector<pf_kv_layout> layouts;
+  std::vector<std::vector<pf_block_xfer>> blocks;
+  std::vector<std::shared_ptr<SealedBlock>> keep;  // host copies stay alive
+  pf_load_state* state = nullptr;
+  uint32_t mode = PF_MODE_KERNEL;
+  uint64_t bytes = 0;
+};
+
+class DeviceWorker {
+ public:
+  static int create(int device, bool with_gpu, std::shared_ptr<DeviceWorker>* out,
+                    std::atomic<uint64_t>* loaded_bytes, std::atomic<uint64_t>* failures);
+  ~DeviceWorker();
+  int save(const std::vector<pf_layer_xfer>& layers, uint32_t mode);
+  int submit(LoadTask&& task);
+  void wait_idle();
+
+ private:
+  void load_loop();
+  int device_ = 0;
+  bool gpu_ = false;
+  pf_xfer* save_x_ = nullptr;
+  pf_xfer* load_x_ = nullptr;
+  std::mutex save_mu_;
+  std::mutex q_mu_;
+  std::condition_variable q_cv_, idle_cv_;
+  std::deque<LoadTask> queue_;
+  size_t busy_ = 0;
+  bool stop_ = false;
+  std::thread thread_;
+  std::vector<hipEvent_t> events_;
+  std::atomic<uint64_t>* loaded_bytes_ = nullptr;
+  std::atomic<uint64_t>* failures_ = nullptr;
+};
+
+int DeviceWorker::create(int device, bool with_gpu, std::shared_ptr<DeviceWorker>* out,
+                         std::atomic<uint64_t>* loaded_bytes, std::atomic<uint64_t>* failures) {
+  auto w = std::make_shared<DeviceWorker>();
+  w->device_ = device;
+  w->gpu_ = with_gpu;
+  w->loaded_bytes_ = loaded_bytes;
+  w->failures_ = failures;
+  if (with_gpu) {
+    if (int rc = pf_xfer_create(device, 0, &w->save_x_))
+      return fail(PF_ERR_INIT, std::string("failed to initialize HIP: ") + pf_last_error());
+    if (int rc = pf_xfer_create(device, 0, &w->load_x_)) {
+      (void)rc;
+      return fail(PF_ERR_INIT, std::string("failed to initialize HIP: ") + pf_last_error());
+    }
+  }
+  w->thread_ = std::thread([p = w.get()] { p->load_loop(); });
+  *out = std::move(w);
+  return PF_OK;
+}
+
+DeviceWorker::~DeviceWorker() {
+  {
+    std::lock_guard<std::mutex> lk(q_mu_);
+    stop_ = true;
+  }
+  q_cv_.notify_all();
+  if (thread_.joinable()) thread_.join();
+  if (gpu_) {
+    (void)hipSetDevice(device_);
+    for (hipEvent_t e : events_) (void)hipEventDestroy(e);
+  }
+  if (save_x_) pf_xfer_destroy(save_x_);
+  if (load_x_) pf_xfer_destroy(load_x_);
+}
+
+int DeviceWorker::save(const std::vector<pf_layer_xfer>& layers, uint32_t mode) {
+  if (!gpu_)
+    return fail(PF_ERR_UNSUPPORTED, "storage error: engine pool is not mapped for a device");
+  std::lock_guard<std::mutex> lk(save_mu_);
+  int rc = pf_save_layers(save_x_, layers.data(), static_cast<uint32_t>(layers.size()), mode);
+  if (rc) return fail(PF_ERR_STORAGE, std::string("storage error: ") + pf_last_error());
+  return PF_OK;
+}
+
+int DeviceWorker::submit(LoadTask&& task) {
+  if (!gpu_)
+    return fail(PF_ERR_UNSUPPORTED, "storage error: engine pool is not mapped for a device");
+  {
+    std::lock_guard<std::mutex> lk(q_mu_);
+    if (stop_)
+      return fail(PF_ERR_STORAGE,
+                  strf("storage error: Load worker channel closed for device %d", device_));
+    queue_.push_back(std::move(task));
+    ++busy_;
+  }
+  q_cv_.notify_one();
+  return PF_OK;
+}
+
+void DeviceWorker::wait_idle() {
+  std::unique_lock<std::mutex> lk(q_mu_);
+  idle_cv_.wait(lk, [this] { return busy_ == 0; });
+}
+
+void DeviceWorker::load_loop() {
+  if (gpu_) (void)hipSetDevice(device_);
+  for (;;) {
+    LoadTask task;
+    {
+      std::unique_lock<std::mutex> lk(q_mu_);
+      q_cv_.wait(lk, [this] { return stop_ || !queue_.empty(); });
+      if (queue_.empty()) return;  // stopping and drained
+      task = std::move(queue_.front());
+      queue_.pop_front();
+    }
+    const size_t L = task.layouts.size();
+    bool ok = true;
+    std::vector<pf_layer_xfer> layers(L);
+    for (size_t l = 0; l < L; ++l)
+      layers[l] = pf_layer_xfer{task.layouts[l], task.blocks[l].data(), task.blocks[l].size()};
+    while (events_.size() < L) {
+      hipEvent_t e = nullptr;
+      if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
+        ok = false;
+        break;
+      }
+      events_.push_back(e);
+    }
+    if (ok && L > 0) {
+      std::vector<pf_event> evs(events_.begin(), events_.begin() + L);
+      ok = pf_load_layers(load_x_, layers.data(), static_cast<uint32_t>(L), task.mode,
+                          evs.data()) == PF_OK;
+      // Per-layer completion: layer l is published as soon as its event fires.
+      for (size_t l = 0; ok && l < L; ++l) {
+        ok = hipEventSynchronize(events_[l]) == hipSuccess;
+        if (ok) pf_load_state_set_layers_done(task.state, static_cast<int64_t>(l + 1));
+      }
+      if (!ok) (void)pf_xfer_synchronize(load_x_);
+    }
+    if (ok) {
+      pf_load_state_set_completed(task.state);
+      loaded_bytes_->fetch_add(task.bytes);
+    } else {
+      pf_load_state_set_error(task.state);
+      failures_->fetch_add(1);
+    }
+    pf_load_state_close(task.state);
+    task.keep.clear();
+    {
+      std::lock_guard<std::mutex> lk(q_mu_);
+      --busy_;
+    }
+    idle_cv_.notify_all();
+  }
+}
+
+// ===========================================================================
+// Instances.
+// ===========================================================================
+struct GpuContext {
+  std::mutex mu;
+  std::unordered_map<std::string, pf_kv_layout> regs;
+  std::shared_ptr<DeviceWorker> worker;
+};
+
+struct Instance {
+  std::string id, ns;
+  size_t num_layers = 0, tp_size = 0;
+  std::mutex layers_mu;
+  std::unordered_map<std::string, size_t> layer_ids;
+  std::vector<std::string> layer_names;
+  std::shared_mutex gpus_mu;
+  std::map<int, std::shared_ptr<GpuContext>> gpus;
+
+  size_t layer_id_or_create(const std::string& name) {
+    std::lock_guard<std::mutex> lk(layers_mu);
+    auto it = layer_ids.find(name);
+    if (it != layer_ids.end()) return it->second;
+    size_t id = layer_names.size();
+    layer_names.push_back(name);
+    layer_ids[name] = id;
+    return id;
+  }
+  bool layer_id(const std::string& name, size_t* out) {
+    std::lock_guard<std::mutex> lk(layers_mu);
+    auto it = layer_ids.find(name);
+    if (it == layer_ids.end()) return false;
+    *out = it->second;
+    return true;
+  }
+  std::shared_ptr<GpuContext> gpu(int device) {
+    std::shared_lock<std::shared_mutex> lk(gpus_mu);
+    auto it = gpus.find(device);
+    return it == gpus.end() ? nullptr : it->second;
+  }
+  // lib.rs:205-219.
+  int slot_index(size_t layer, size_t tp_rank, size_t* out) const {
+    if (layer >= num_layers)
+      return fail(PF_ERR_INVALID_ARGUMENT, strf("invalid argument: layer_id %zu out of range (%zu layers)",
+                                                layer, num_layers));
+    if (tp_rank >= tp_size)
+      return fail(PF_ERR_INVALID_ARGUMENT, strf("invalid argument: tp_rank %zu out of range (tp_size %zu)",
+                                                tp_rank, tp_size));
+    *out = layer * tp_size + tp_rank;
+    return PF_OK;
+  }
+};
+
+std::string block_key(const std::string& ns, const uint8_t* hash, size_t len) {
+  std::string k;
+  k.reserve(ns.size() + 1 + len);
+  k.append(ns);
+  k.push_back('\0');
+  k.append(reinterpret_cast<const char*>(hash), len);
+  return k;
+}
+
+}  // namespace pf
+
+using namespace pf;
+
+struct pf_allocator {
+  std::unique_ptr<UnitAllocator> a;
+};
+
+struct pf_engine {
+  std::shared_mutex mu;
+  std::unordered_map<std::string, std::shared_ptr<Instance>> instances;
+  std::shared_ptr<PinnedPool> pool;
+  std::unique_ptr<BlockStore> store;
+  std::atomic<uint32_t> save_mode{PF_MODE_KERNEL};
+  std::atomic<uint32_t> load_mode{PF_MODE_KERNEL};
+  std::atomic<uint64_t> saved_bytes{0};
+  std::atomic<uint64_t> loaded_bytes{0};
+  std::atomic<uint64_t> load_failures{0};
+};
+
+namespace {
+
+int get_instance(pf_engine* e, const char* id, std::shared_ptr<Instance>* out) {
+  std::shared_lock<std::shared_mutex> lk(e->mu);
+  auto it = e->instances.find(id);
+  if (it == e->instances.end())
+    return fail(PF_ERR_INSTANCE_MISSING, strf("instance %s not found", id));
+  *out = it->second;
+  return PF_OK;
+}
+
+std::vector<std::string> keys_of(const std::string& ns, const uint8_t* data, const uint64_t* offs,
+                                 uint64_t n) {
+  std::vector<std::string> keys(n);
+  for (uint64_t i = 0; i < n; ++i)
+    keys[i] = block_key(ns, data + offs[i], static_cast<size_t>(offs[i + 1] - offs[i]));
+  return keys;
+}
+
+// Host side of one planned layer save.
+struct SavePlan {
+  size_t slot = 0;
+  pf_kv_layout layout{};
+  std::vector<std::string> keys;  // kept hashes, in order
+  std::vector<pf_block_xfer> blocks;
+  std::shared_ptr<PoolAllocation> k_alloc, v_alloc;
+  bool split = false;
+};
+
+}  // namespace
+
+extern "C" {
+
+// ---------------------------------------------------------------------------
+// Allocator.
+// ---------------------------------------------------------------------------
+int pf_allocator_create(uint64_t total_bytes, uint64_t unit_size, pf_allocator** out) {
+  if (!out) return fail(PF_ERR_INVALID_ARGUMENT, "null output");
+  std::unique_ptr<UnitAllocator> a;
+  if (int rc = UnitAllocator::create(total_bytes, unit_size, &a)) return rc;
+  *out = new pf_allocator{std::move(a)};
+  return PF_OK;
+}
+
+int pf_allocator_create_auto(uint64_t total_bytes, pf_allocator** out) {
+  const uint64_t unit = total_bytes > kU32Max ? (total_bytes + kU32Max - 1) / kU32Max : 1;
+  return pf_allocator_create(total_bytes, unit, out);
+}
+
+int pf_allocator_destroy(pf_allocator* a) {
+  delete a;
+  return PF_OK;
+}
+
+int pf_allocator_allocate(pf_allocator* a, uint64_t size_bytes, int* found, uint64_t* offset,
+                          uint64_t* size) {
+  bool f = false;
+  uint64_t o = 0, s = 0;
+  if (int rc = a->a->allocate(size_bytes, &f, &o, &s)) return rc;
+  *found = f ? 1 : 0;
+  if (offset) *offset = o;
+  if (size) *size = s;
+  return PF_OK;
+}
+
+int pf_allocator_free(pf_allocator* a, uint64_t offset) {
+  a->a->free(offset);
+  return PF_OK;
+}
+
+int pf_allocator_report(pf_allocator* a, uint64_t* total_bytes, uint64_t* free_bytes,
+                        uint64_t* largest_free_bytes, uint64_t* unit_size) {
+  if (total_bytes) *total_bytes = a->a->total_bytes();
+  if (free_bytes) *free_bytes = a->a->free_bytes();
+  if (largest_free_bytes) *largest_free_bytes = a->a->largest_free_bytes();
+  if (unit_size) *unit_size = a->a->unit_size();
+  return PF_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Engine.
+// ---------------------------------------------------------------------------
+int pf_engine_create(uint64_t pool_bytes, uint32_t pool_kind, uint32_t pinned_flags,
+                     uint64_t unit_hint, pf_engine** out) {
+  if (!out) return fail(PF_ERR_INVALID_ARGUMENT, "null output");
+  if (pool_kind != PF_POOL_PINNED && pool_kind != PF_POOL_HOST)
+    return fail(PF_ERR_INVALID_ARGUMENT, "unknown pool kind");
+  std::shared_ptr<PinnedPool> pool;
+  if (int rc = PinnedPool::create(pool_bytes, unit_hint, pool_kind == PF_POOL_PINNED, pinned_flags,
+                                  &pool))
+    return rc;
+  auto* e = new pf_engine();
+  e->pool = pool;
+  e->store.reset(new BlockStore(pool));
+  *out = e;
+  return PF_OK;
+}
+
+int pf_engine_destroy(pf_engine* e) {
+  if (!e) return PF_OK;
+  {
+    std::unique_lock<std::shared_mutex> lk(e->mu);
+    e->instances.clear();  // joins the workers after their queued loads
+  }
+  delete e;
+  return PF_OK;
+}
+
+int pf_engine_set_modes(pf_engine* e, uint32_t save_mode, uint32_t load_mode) {
+  if (save_mode > PF_MODE_STAGED || load_mode > PF_MODE_STAGED)
+    return fail(PF_ERR_INVALID_ARGUMENT, "invalid argument: unknown transfer mode");
+  if (save_mode == PF_MODE_STAGED || load_mode == PF_MODE_STAGED)
+    return fail(PF_ERR_INVALID_ARGUMENT,
+                "invalid argument: the engine's workers have no staging buffer");
+  e->save_mode = save_mode;
+  e->load_mode = load_mode;
+  return PF_OK;
+}
+
+// lib.rs:373-469.
+int pf_engine_register_context_layer(pf_engine* e, const char* instance_id, const char* ns,
+                                     int device_id, const char* layer_name, uint64_t data_ptr,
+                                     uint64_t size_bytes, uint64_t num_blocks,
+                                     uint64_t bytes_per_block, uint64_t kv_stride_bytes,
+                                     uint64_t segments, uint64_t tp_rank, uint64_t tp_size,
+                                     uint64_t num_layers) {
+  const std::string layer(layer_name);
+  if (bytes_per_block == 0 || num_blocks == 0 || segments == 0)
+    return fail(PF_ERR_INVALID_ARGUMENT,
+                "invalid argument: invalid KV cache layout for layer " + layer);
+  if (segments > 1 && kv_stride_bytes == 0)
+    return fail(PF_ERR_INVALID_ARGUMENT,
+                "invalid argument: kv_stride_bytes must be > 0 when segments > 1 for layer " + layer);
+  if (device_id < 0) return fail(PF_ERR_INVALID_ARGUMENT, "invalid argument: device_id must be >= 0");
+  pf_kv_layout layout{};
+  if (pf_layout_init(data_ptr, size_bytes, num_blocks, bytes_per_block, kv_stride_bytes, segments,
+                     &layout))
+    return fail(PF_ERR_INVALID_ARGUMENT,
+                std::string("invalid argument: ") + pf_last_error() + " for layer " + layer);
+  std::shared_ptr<Instance> inst;
+  {
+    std::unique_lock<std::shared_mutex> lk(e->mu);
+    auto it = e->instances.find(instance_id);
+    if (it != e->instances.end()) {
+      inst = it->second;
+      if (inst->num_layers != num_layers || inst->tp_size != tp_size)
+        return fail(PF_ERR_TOPOLOGY_MISMATCH,
+                    strf("topology mismatch: instance %s exists with layers=%zu, tp=%zu; "
+                         "requested layers=%llu, tp=%llu",
+                         instance_id, inst->num_layers, inst->tp_size,
+                         (unsigned long long)num_layers, (unsigned long long)tp_size));
+    } else {
+      inst = std::make_shared<Instance>();
+      inst->id = instance_id;
+      inst->ns = ns;
+      inst->num_layers = num_layers;
+      inst->tp_size = tp_size;
+      e->instances[instance_id] = inst;
+    }
+  }
+  // ensure_gpu (lib.rs:221-252): one worker per (instance, device).
+  std::shared_ptr<GpuContext> gpu;
+  {
+    std::unique_lock<std::shared_mutex> lk(inst->gpus_mu);
+    auto it = inst->gpus.find(device_id);
+    if (it == inst->gpus.end()) {
+      auto g = std::make_shared<GpuContext>();
+      if (int rc = DeviceWorker::create(device_id, e->pool->device_backed(), &g->worker,
+                                        &e->loaded_bytes, &e->load_failures))
+        return rc;
+      it = inst->gpus.emplace(device_id, g).first;
+    }
+    gpu = it->second;
+  }
+  inst->layer_id_or_create(layer);
+  std::lock_guard<std::mutex> lk(gpu->mu);
+  gpu->regs[layer] = layout;
+  return PF_OK;
+}
+
+int pf_engine_unregister_instance(pf_engine* e, const char* instance_id) {
+  std::shared_ptr<Instance> removed;
+  {
+    std::unique_lock<std::shared_mutex> lk(e->mu);
+    auto it = e->instances.find(instance_id);
+    if (it == e->instances.end())
+      return fail(PF_ERR_INSTANCE_MISSING, strf("instance %s not found", instance_id));
+    removed = std::move(it->second);
+    e->instances.erase(it);
+  }
+  return PF_OK;  // workers stop when the last reference drops
+}
+
+// lib.rs:803-838.
+int pf_engine_count_prefix_hit_blocks(pf_engine* e, const char* instance_id,
+                                      const uint8_t* hash_data, const uint64_t* hash_offsets,
+                                      uint64_t n, uint64_t* hits) {
+  std::shared_ptr<Instance> inst;
+  if (int rc = get_instance(e, instance_id, &inst)) return rc;
+  uint64_t h = 0;
+  for (uint64_t i = 0; i < n; ++i) {
+    if (!e->store->cache_contains(block_key(inst->ns, hash_data + hash_offsets[i],
+                                            static_cast<size_t>(hash_offsets[i + 1] - hash_offsets[i]))))
+      break;
+    ++h;
+  }
+  *hits = h;
+  return PF_OK;
+}
+
+// lib.rs:497-782.
+int pf_engine_batch_save(pf_engine* e, const char* instance_id, uint64_t tp_rank, int device_id,
+                         const pf_save_layer* layers, uint32_t num_layers) {
+  std::shared_ptr<Instance> inst;
+  if (int rc = get_instance(e, instance_id, &inst)) return rc;
+  auto gpu = inst->gpu(device_id);
+  if (!gpu)
+    return fail(PF_ERR_WORKER_MISSING,
+                strf("device %d not found in instance %s", device_id, instance_id));
+  const size_t total_slots = inst->num_layers * inst->tp_size;
+  std::vector<SavePlan> plans;
+  plans.reserve(num_layers);
+  for (uint32_t li = 0; li < num_layers; ++li) {
+    const pf_save_layer& sl = layers[li];
+    const std::string name(sl.layer_name);
+    size_t layer_id = 0;
+    if (!inst->layer_id(name, &layer_id))
+      return fail(PF_ERR_INVALID_ARGUMENT, "invalid argument: layer " + name + " unknown");
+    pf_kv_layout reg{};
+    {
+      std::lock_guard<std::mutex> lk(gpu->mu);
+      auto it = gpu->regs.find(name);
+      if (it == gpu->regs.end())
+        return fail(PF_ERR_INVALID_ARGUMENT,
+                    "invalid argument: layer " + name + " not registered on device");
+      reg = it->second;
+    }
+    SavePlan plan;
+    if (int rc = inst->slot_index(layer_id, tp_rank, &plan.slot)) return rc;
+    plan.layout = reg;
+    // Filtering and dedup (lib.rs:590-621).
+    std::vector<int64_t> idx;
+    for (uint64_t i = 0; i < sl.num_blocks; ++i) {
+      const int32_t id = sl.block_ids[i];
+      if (id < 0) continue;
+      if (static_cast<uint64_t>(id) >= reg.num_blocks)
+        return fail(PF_ERR_INVALID_ARGUMENT,
+                    strf("invalid argument: block %d out of range for layer %s (%llu blocks "
+                         "registered)",
+                         id, name.c_str(), (unsigned long long)reg.num_blocks));
+      std::string key = block_key(inst->ns, sl.hash_data + sl.hash_offsets[i],
+                                  static_cast<size_t>(sl.hash_offsets[i + 1] - sl.hash_offsets[i]));
+      if (e->store->cache_contains(key) || e->store->inflight_has_slot(key, plan.slot)) continue;
+      idx.push_back(id);
+      plan.keys.push_back(std::move(key));
+    }
+    if (idx.empty()) continue;
+    const uint64_t n = idx.size();
+    plan.split = reg.segments == 2 && reg.kv_stride_bytes > reg.bytes_per_block;
+    plan.blocks.resize(n);
+    if (plan.split) {  // lib.rs:636-679
+      const uint64_t seg = reg.bytes_per_block;
+      plan.k_alloc = e->store->allocate(seg * n);
+      if (!plan.k_alloc)
+        return fail(PF_ERR_STORAGE,
+                    "storage error: pinned pool exhausted while allocating K segment buffer");
+      plan.v_alloc = e->store->allocate(seg * n);
+      if (!plan.v_alloc)
+        return fail(PF_ERR_STORAGE,
+                    "storage error: pinned pool exhausted while allocating V segment buffer");
+      for (uint64_t i = 0; i < n; ++i)
+        plan.blocks[i] = pf_block_xfer{idx[i], reinterpret_cast<uint64_t>(plan.k_alloc->ptr + i * seg),
+                                       reinterpret_cast<uint64_t>(plan.v_alloc->ptr + i * seg)};
+    } else {  // lib.rs:706-747
+      const uint64_t bs = reg.block_size_bytes;
+      plan.k_alloc = e->store->allocate(bs * n);
+      if (!plan.k_alloc)
+        return fail(PF_ERR_STORAGE,
+                    "storage error: pinned pool exhausted while allocating contiguous block buffer");
+      for (uint64_t i = 0; i < n; ++i)
+        plan.blocks[i] =
+            pf_block_xfer{idx[i], reinterpret_cast<uint64_t>(plan.k_alloc->ptr + i * bs), 0};
+    }
+    plans.push_back(std::move(plan));
+  }
+  if (plans.empty()) return PF_OK;
+  std::vector<pf_layer_xfer> xl;
+  xl.reserve(plans.size());
+  for (auto& p : plans) xl.push_back(pf_layer_xfer{p.layout, p.blocks.data(), p.blocks.size()});
+  if (int rc = gpu->worker->save(xl, e->save_mode.load())) return rc;
+  // LayerBlocks and slot insertion once the bytes are in place (lib.rs:687-705, 755-770).
+  uint64_t bytes = 0;
+  for (auto& p : plans) {
+    const uint64_t seg = p.layout.bytes_per_block, bs = p.layout.block_size_bytes;
+    for (size_t i = 0; i < p.keys.size(); ++i) {
+      auto lb = std::make_shared<LayerBlock>();
+      lb->size = bs;
+      lb->k_alloc = p.k_alloc;
+      if (p.split) {
+        lb->k_ptr = p.k_alloc->ptr + i * seg;
+        lb->v_ptr = p.v_alloc->ptr + i * seg;
+        lb->v_alloc = p.v_alloc;
+      } else {
+        lb->k_ptr = p.k_alloc->ptr + i * bs;
+      }
+      bool inserted = false;
+      if (int rc = e->store->insert_slot(p.keys[i], p.slot, std::move(lb), total_slots, &inserted))
+        return fail(rc, std::string("storage error: ") + pf_last_error());
+    }
+    bytes += p.keys.size() * bs;
+  }
+  e->saved_bytes.fetch_add(bytes);
+  return PF_OK;
+}
+
+// lib.rs:957-1069.
+int pf_engine_batch_load(pf_engine* e, const char* instance_id, uint64_t tp_rank, int device_id,
+                         const char* load_state_shm, const char* const* layer_names,
+                         uint32_t num_layers, const int32_t* block_ids, const uint8_t* hash_data,
+                         const uint64_t* hash_offsets, uint64_t n) {
+  pf_load_state* state = nullptr;
+  if (pf_load_state_attach(load_state_shm, &state))
+    return fail(PF_ERR_LOAD_STATE, std::string("storage error: LoadState: ") + pf_last_error());
+  auto bail = [&](int code) {
+    pf_load_state_set_error(state);
+    pf_load_state_close(state);
+    return code;
+  };
+  std::shared_ptr<Instance> inst;
+  if (int rc = get_instance(e, instance_id, &inst)) return bail(rc);
+  auto gpu = inst->gpu(device_id);
+  if (!gpu)
+    return bail(fail(PF_ERR_WORKER_MISSING,
+                     strf("device %d not found in instance %s", device_id, instance_id)));
+  LoadTask task;
+  if (e->store->lookup_many(keys_of(inst->ns, hash_data, hash_offsets, n), &task.keep))
+    return bail(fail(PF_ERR_STORAGE, std::string("storage error: ") + pf_last_error()));
+  bool any = false;
+  for (uint32_t li = 0; li < num_layers; ++li) {
+    const std::string name(layer_names[li]);
+    size_t layer_id = 0, slot = 0;
+    if (!inst->layer_id(name, &layer_id))
+      return bail(fail(PF_ERR_INVALID_ARGUMENT, "invalid argument: layer " + name +
+                                                    " unknown for instance " + instance_id));
+    pf_kv_layout reg{};
+    {
+      std::lock_guard<std::mutex> lk(gpu->mu);
+      auto it = gpu->regs.find(name);
+      if (it == gpu->regs.end())
+        return bail(fail(PF_ERR_INVALID_ARGUMENT,
+                         strf("invalid argument: layer %s not registered on device %d",
+                              name.c_str(), device_id)));
+      reg = it->second;
+    }
+    if (int rc = inst->slot_index(layer_id, tp_rank, &slot)) return bail(rc);
+    std::vector<pf_block_xfer> blocks;
+    for (uint64_t j = 0; j < n; ++j) {
+      if (block_ids[j] < 0) continue;
+      if (slot >= task.keep[j]->slots.size() || !task.keep[j]->slots[slot]) continue;
+      const LayerBlock& lb = *task.keep[j]->slots[slot];
+      blocks.push_back(pf_block_xfer{block_ids[j], reinterpret_cast<uint64_t>(lb.k_ptr),
+                                     reinterpret_cast<uint64_t>(lb.v_ptr)});
+      task.bytes += lb.size;
+    }
+    any = any || !blocks.empty();
+    task.names.push_back(name);
+    task.layouts.push_back(reg);
+    task.blocks.push_back(std::move(blocks));
+  }
+  if (!any) {  // lib.rs:1055-1060
+    pf_load_state_set_completed(state);
+    pf_load_state_close(state);
+    return PF_OK;
+  }
+  task.state = state;
+  task.mode = e->load_mode.load();
+  if (int rc = gpu->worker->submit(std::move(task))) return bail(rc);
+  return PF_OK;
+}
+
+int pf_engine_stats_get(pf_engine* e, pf_engine_stats* out) {
+  e->pool->usage(&out->pool_used_bytes, &out->pool_total_bytes);
+  out->sealed_blocks = e->store->sealed_count();
+  out->inflight_blocks = e->store->inflight_count();
+  out->evicted_blocks = e->store->evictions();
+  out->saved_bytes = e->saved_bytes.load();
+  out->loaded_bytes = e->loaded_bytes.load();
+  out->load_failures = e->load_failures.load();
+  return PF_OK;
+}
+
+int pf_engine_wait_idle(pf_engine* e) {
+  std::vector<std::shared_ptr<DeviceWorker>> workers;
+  {
+    std::shared_lock<std::shared_mutex> lk(e->mu);
+    for (auto& kv : e->instances) {
+      std::shared_lock<std::shared_mutex> g(kv.second->gpus_mu);
+      for (auto& gk : kv.second->gpus) workers.push_back(gk.second->worker);
+    }
+  }
+  for (auto& w : workers) w->wait_idle();
+  return PF_OK;
+}
+
+}  // extern "C"

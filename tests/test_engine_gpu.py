@@ -1,0 +1,266 @@
+"""PegaEngine on the GPU: save by hash, load by hash with LoadState, seal
+visibility across layers and TP ranks, dedup, prefix counting, eviction, and
+per-layer progress — bytes checked against the oracle or in closed form."""
+
+import hashlib
+import sys
+import time
+
+import numpy as np
+import pytest
+
+import oracle
+from pegaflow_amd import _lib
+from pegaflow_amd.engine import PegaEngine
+from pegaflow_amd.load_state import PyLoadState
+from pegaflow_amd.runtime import DeviceBuffer
+from pegaflow_amd.workload import LLAMA3_8B, DeviceLayers, draw_blocks, verify_restored
+
+pytestmark = pytest.mark.gpu
+MiB = 1 << 20
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def h(i, salt=b"blk"):
+    return hashlib.sha256(salt + int(i).to_bytes(8, "little")).digest()
+
+
+def wait(st: PyLoadState, timeout=60.0):
+    t0 = time.monotonic()
+    while not st.is_ready():
+        assert time.monotonic() - t0 < timeout, "load did not complete"
+        time.sleep(0.0005)
+    return st.get_state()
+
+
+class Model:
+    """n_layers KV-first layers [2, nb, ...] on device 0, registered with an
+    engine as instance `inst` (tp_rank of tp_size)."""
+
+    def __init__(self, engine, inst, n_layers, nb, bpb, seed=1, tp_rank=0, tp_size=1,
+                 prefix="layer"):
+        self.nb, self.bpb, self.n_layers = nb, bpb, n_layers
+        self.kv = nb * bpb
+        self.size = 2 * self.kv
+        self.names = [f"{prefix}.{l}" for l in range(n_layers)]
+        self.seeds = [oracle.layer_seed(seed, l) for l in range(n_layers)]
+        self.bufs = []
+        for l in range(n_layers):
+            b = DeviceBuffer(self.size)
+            b.fill_random(self.seeds[l])
+            self.bufs.append(b)
+            engine.register_context_layer(inst, "ns", 0, self.names[l], b.ptr, self.size, nb, bpb,
+                                          self.kv, 2, tp_rank, tp_size, n_layers)
+
+    def host_copies(self):
+        return [b.download() for b in self.bufs]
+
+    def close(self):
+        for b in self.bufs:
+            b.close()
+
+
+def expected_after_load(model, originals, ids, targets):
+    """Oracle: save(ids) then load(targets) on each host copy."""
+    out = []
+    for l, ref in enumerate(originals):
+        ref = ref.copy()
+        reg = oracle.layout(ref.ctypes.data, model.size, model.nb, model.bpb, model.kv, 2)
+        m = len(ids)
+        host = np.zeros(2 * m * model.bpb, np.uint8)
+        k, v, _ = oracle.save_host_layout(reg, m, host.ctypes.data,
+                                          host.ctypes.data + m * model.bpb)
+        oracle.process_save(reg, ref, ids, k, v)
+        oracle.process_load(reg, ref, targets, k, v)
+        out.append(ref)
+    return out
+
+
+@pytest.fixture
+def engine(gpu):
+    e = PegaEngine(pool_size=256 * MiB)
+    yield e
+    e.close()
+
+
+@pytest.mark.parametrize("load_mode", ["kernel", "dma_batched", "dma_reference"])
+def test_save_then_load_by_hash(engine, load_mode):
+    say(f"[gpu] engine save/load by hash load_mode={load_mode}")
+    engine.set_transfer_modes(_lib.MODE_KERNEL, _lib.MODE_NAMES[load_mode])
+    m = Model(engine, "inst", 6, 64, 4096)
+    orig = m.host_copies()
+    ids = [5, 17, 3, 60, 41, 8]
+    hashes = [h(i) for i in ids]
+    engine.batch_save_kv_blocks("inst", 0, 0, [(n, ids, hashes) for n in m.names])
+    assert engine.count_prefix_hit_blocks("inst", hashes) == len(ids)
+    targets = [0, 1, 2, 63, 62, 40]
+    st = PyLoadState(num_layers=m.n_layers)
+    engine.batch_load_kv_blocks("inst", 0, 0, st.shm_name(), m.names, targets, hashes)
+    assert wait(st) == 1
+    assert st.layers_done() == m.n_layers
+    exp = expected_after_load(m, orig, ids, targets)
+    for l in range(m.n_layers):
+        assert np.array_equal(m.bufs[l].download(), exp[l]), f"layer {l}"
+    s = engine.stats()
+    assert s["sealed_blocks"] == len(ids) and s["inflight_blocks"] == 0
+    assert s["saved_bytes"] == s["loaded_bytes"] == m.n_layers * len(ids) * 2 * m.bpb
+    m.close()
+
+
+def test_seal_visibility_dedup_and_prefix(engine):
+    say("[gpu] engine seal visibility / dedup / prefix")
+    m = Model(engine, "inst", 4, 32, 2048)
+    ids = list(range(10))
+    hashes = [h(i) for i in ids]
+    # Half the layers: blocks are inflight, not visible (storage.rs:136-208).
+    engine.batch_save_kv_blocks("inst", 0, 0, [(n, ids, hashes) for n in m.names[:2]])
+    assert engine.count_prefix_hit_blocks("inst", hashes) == 0
+    assert engine.stats()["inflight_blocks"] == 10
+    used = engine.stats()["pool_used_bytes"]
+    # Re-saving the same layers is a no-op (slot already inflight).
+    engine.batch_save_kv_blocks("inst", 0, 0, [(n, ids, hashes) for n in m.names[:2]])
+    assert engine.stats()["pool_used_bytes"] == used
+    engine.batch_save_kv_blocks("inst", 0, 0, [(n, ids, hashes) for n in m.names[2:]])
+    assert engine.count_prefix_hit_blocks("inst", hashes) == 10
+    s = engine.stats()
+    assert s["sealed_blocks"] == 10 and s["inflight_blocks"] == 0
+    # Sealed blocks are skipped entirely.
+    used = s["pool_used_bytes"]
+    engine.batch_save_kv_blocks("inst", 0, 0, [(n, ids, hashes) for n in m.names])
+    assert engine.stats()["pool_used_bytes"] == used
+    # Prefix counting stops at the first miss (lib.rs:803-838).
+    assert engine.count_prefix_hit_blocks("inst", hashes[:3] + [h(99)] + hashes[3:]) == 3
+    # Another namespace sees nothing.
+    engine.register_context_layer("other", "ns2", 0, "x", m.bufs[0].ptr, m.size, m.nb, m.bpb,
+                                  m.kv, 2, 0, 1, 1)
+    assert engine.count_prefix_hit_blocks("other", hashes) == 0
+    m.close()
+
+
+def test_load_missing_hash_fails_whole_call(engine):
+    say("[gpu] engine load with a missing hash")
+    m = Model(engine, "inst", 2, 16, 1024)
+    engine.batch_save_kv_blocks("inst", 0, 0, [(n, [1, 2], [h(1), h(2)]) for n in m.names])
+    st = PyLoadState()
+    with pytest.raises(RuntimeError, match="missing KV block hash at index 1"):
+        engine.batch_load_kv_blocks("inst", 0, 0, st.shm_name(), m.names, [3, 4],
+                                    [h(1), h(7)])
+    assert st.get_state() == -1
+    m.close()
+
+
+def test_tp2_blocks_seal_when_both_ranks_saved(engine):
+    say("[gpu] engine tp_size=2")
+    r0 = Model(engine, "tp", 2, 16, 1024, seed=3, tp_rank=0, tp_size=2, prefix="a")
+    with pytest.raises(RuntimeError, match="topology mismatch"):
+        engine.register_context_layer("tp", "ns", 0, "zz", r0.bufs[0].ptr, r0.size, 16, 1024,
+                                      r0.kv, 2, 0, 2, 3)
+    # The second rank registers the same layer names with its own tensors.
+    r1_bufs = []
+    for l, name in enumerate(r0.names):
+        b = DeviceBuffer(r0.size)
+        b.fill_random(oracle.layer_seed(77, l))
+        r1_bufs.append(b)
+        engine.register_context_layer("tp", "ns", 0, name, b.ptr, r0.size, 16, 1024, r0.kv, 2, 1,
+                                      2, 2)
+    ids, hashes = [4, 9], [h(4), h(9)]
+    # Registration of rank 1 replaced the device-0 registration of these layer
+    # names, as in the reference (one registration per layer name per device).
+    engine.batch_save_kv_blocks("tp", 0, 0, [(n, ids, hashes) for n in r0.names])
+    assert engine.count_prefix_hit_blocks("tp", hashes) == 0  # rank 1 slots missing
+    engine.batch_save_kv_blocks("tp", 1, 0, [(n, ids, hashes) for n in r0.names])
+    assert engine.count_prefix_hit_blocks("tp", hashes) == 2
+    for b in r1_bufs:
+        b.close()
+    r0.close()
+
+
+def test_eviction_under_pool_pressure(gpu):
+    say("[gpu] engine eviction")
+    nb, bpb, layers = 64, 32768, 2
+    per_batch = layers * 8 * 2 * bpb  # 8 blocks, K and V, 2 layers = 1 MiB
+    e = PegaEngine(pool_size=3 * per_batch)
+    m = Model(e, "ev", layers, nb, bpb, seed=5)
+    orig = m.host_copies()
+    batches = [[8 * k + i for i in range(8)] for k in range(4)]
+    for k, ids in enumerate(batches):
+        e.batch_save_kv_blocks("ev", 0, 0, [(n, ids, [h(i) for i in ids]) for n in m.names])
+    s = e.stats()
+    assert s["evicted_blocks"] >= 8
+    # The oldest batch was evicted (LRU); the newest is present.
+    assert e.count_prefix_hit_blocks("ev", [h(i) for i in batches[0]]) == 0
+    assert e.count_prefix_hit_blocks("ev", [h(i) for i in batches[3]]) == 8
+    # Restore the newest batch into other blocks and check the bytes.
+    targets = list(range(40, 48))
+    st = PyLoadState()
+    e.batch_load_kv_blocks("ev", 0, 0, st.shm_name(), m.names, targets,
+                           [h(i) for i in batches[3]])
+    assert wait(st) == 1
+    exp = expected_after_load(m, orig, batches[3], targets)
+    for l in range(layers):
+        assert np.array_equal(m.bufs[l].download(), exp[l])
+    m.close()
+    e.close()
+
+
+def test_layerwise_progress_and_negative_ids(engine):
+    say("[gpu] engine per-layer progress")
+    m = Model(engine, "lw", 8, 256, 32768, seed=11)
+    ids = list(range(0, 200, 2))
+    hashes = [h(i, b"lw") for i in ids]
+    engine.batch_save_kv_blocks("lw", 0, 0, [(n, ids, hashes) for n in m.names])
+    targets = [-1 if i % 10 == 0 else 255 - i // 2 for i in range(len(ids))]
+    st = PyLoadState(num_layers=m.n_layers)
+    engine.batch_load_kv_blocks("lw", 0, 0, st.shm_name(), m.names, targets, hashes)
+    seen = []
+    while not st.is_ready():
+        seen.append(st.layers_done())
+    assert st.get_state() == 1 and st.layers_done() == m.n_layers
+    assert seen == sorted(seen)  # monotonic
+    for l in range(m.n_layers):
+        assert st.wait_for_layer(l, timeout_s=1)
+    kept = [(t, s) for t, s in zip(targets, ids) if t >= 0]
+    src = np.arange(m.nb)
+    for t, s in kept:
+        src[t] = s
+    from pegaflow_amd.runtime import verify_random_chunks
+    blocks = np.arange(m.nb, dtype=np.uint64)
+    for l, b in enumerate(m.bufs):
+        addrs = np.concatenate([b.ptr + blocks * m.bpb, b.ptr + m.kv + blocks * m.bpb])
+        offs = np.concatenate([src.astype(np.uint64) * m.bpb // 8,
+                               (m.kv + src.astype(np.uint64) * m.bpb) // 8])
+        assert verify_random_chunks(addrs, offs, m.bpb, m.seeds[l]) == 0
+    m.close()
+
+
+def test_llama_prefix_through_engine(gpu):
+    """Config 2 through the engine: 32 layers, 640 blocks saved by hash and
+    restored into 640 other blocks; closed-form check of every block."""
+    say("[gpu] engine llama full size")
+    e = PegaEngine(pool_size=1400 * MiB)
+    layers = DeviceLayers(LLAMA3_8B, base_seed=0)
+    names = [f"model.layers.{l}.self_attn" for l in range(LLAMA3_8B.layers)]
+    for name, r in zip(names, layers.regs):
+        e.register_context_layer("llama", "ns", 0, name, r.data_ptr, r.size_bytes, r.num_blocks,
+                                 r.bytes_per_block, r.kv_stride_bytes, r.segments, 0, 1,
+                                 LLAMA3_8B.layers)
+    ids, targets = draw_blocks(LLAMA3_8B.num_blocks, 640, 0)
+    hashes = [h(i, b"llama") for i in ids]
+    t0 = time.perf_counter()
+    e.batch_save_kv_blocks("llama", 0, 0, [(n, ids, hashes) for n in names])
+    t1 = time.perf_counter()
+    assert e.count_prefix_hit_blocks("llama", hashes) == 640
+    st = PyLoadState(num_layers=len(names))
+    t2 = time.perf_counter()
+    e.batch_load_kv_blocks("llama", 0, 0, st.shm_name(), names, targets, hashes)
+    assert wait(st) == 1
+    t3 = time.perf_counter()
+    P = 640 * 32 * 65536
+    say(f"[gpu] engine save {P / (t1 - t0) / 1e9:.1f} GB/s, load {P / (t3 - t2) / 1e9:.1f} GB/s")
+    assert verify_restored(layers, ids, targets) == 0
+    layers.close()
+    e.close()
