@@ -61,6 +61,8 @@ def parse():
     ap.add_argument("--unroll", type=int, default=0,
                     help="16-byte loads in flight per lane, +256 for non-temporal (0: default)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--quick", action="store_true",
+                    help="skip the config 3/4/5 legs (layer-wise, fragmentation, MLA)")
     ap.add_argument("--cpu-sample-layers", type=int, default=8)
     ap.add_argument("--staging-mib", type=int, default=256)
     ap.add_argument("--seed", type=int, default=0)
@@ -114,6 +116,165 @@ def duplex(xfer_save, xfer_load, saved, loads, mode, reps=5):
         xfer_load.synchronize()
         ts.append(time.perf_counter() - t0)
     return min(ts[1:])
+
+
+def leg_layerwise(xfer, seed):
+    """Config 3: Qwen3-8B shape (36 x [2,16000,16,8,128] bf16), 313 random
+    blocks restored one layer at a time; layer l's event gates a 2 ms compute
+    kernel on a second stream.  Overlap efficiency = 36 x 2 ms / total, with
+    the total from the load's first issue to the last compute kernel's end
+    (device events).  The serialized figure gates every compute kernel on the
+    whole load, as a caller without per-layer completion must."""
+    from pegaflow_amd import _lib
+    from pegaflow_amd import workload as wl
+    from pegaflow_amd.runtime import Event, PinnedBuffer, Stream, spin
+
+    shape, n, compute_us = wl.QWEN3_8B, 313, 2000
+    layers = wl.DeviceLayers(shape, base_seed=seed)
+    ids, targets = wl.draw_blocks(shape.num_blocks, n, seed)
+    pool = PinnedBuffer(wl.payload_bytes(layers.regs, n))
+    saved = wl.save_plan(layers.regs, ids, pool.ptr)
+    xfer.save_layers(saved, _lib.MODE_KERNEL)
+    loads = wl.load_plan(saved, targets)
+    compute = Stream()
+    evs = [Event() for _ in range(shape.layers)]
+    start, done = Event(), Event()
+
+    def run(layerwise):
+        start.record(xfer.stream)
+        compute.wait_event(start)
+        xfer.load_layers(loads, _lib.MODE_KERNEL, layer_events=evs)
+        for l in range(shape.layers):
+            compute.wait_event(evs[l] if layerwise else evs[-1])
+            spin(compute, compute_us)
+        done.record(compute)
+        done.synchronize()
+        xfer.synchronize()
+        per_layer = [start.elapsed_ms(evs[0])] + [evs[l - 1].elapsed_ms(evs[l])
+                                                   for l in range(1, shape.layers)]
+        return start.elapsed_ms(done), per_layer
+
+    run(True)
+    total, per_layer = min((run(True) for _ in range(3)), key=lambda r: r[0])
+    serial, _ = min((run(False) for _ in range(2)), key=lambda r: r[0])
+    bad = wl.verify_restored(layers, ids, targets)
+    ideal = shape.layers * compute_us / 1e3
+    out = {
+        "workload": "qwen3-8b 5k-token prefix: 36 x bf16 [2,16000,16,8,128], 313 blocks, "
+                    "layer-wise restore gating a 2 ms compute kernel per layer",
+        "overlap_efficiency": round(ideal / total, 4),
+        "total_ms": round(total, 3),
+        "compute_ms": ideal,
+        "serialized_total_ms": round(serial, 3),
+        "serialized_efficiency": round(ideal / serial, 4),
+        "first_layer_ms": round(per_layer[0], 4),
+        "per_layer_ms_mean": round(sum(per_layer[1:]) / (len(per_layer) - 1), 4),
+        "per_layer_ms_max": round(max(per_layer[1:]), 4),
+        "layer_bytes": n * 2 * shape.bytes_per_block,
+        "bit_exact": bad == 0,
+    }
+    compute.close()
+    pool.close()
+    layers.close()
+    return out
+
+
+def draw_runs(rng, num_blocks, n, mean_run):
+    """n distinct block ids built from runs of consecutive blocks whose
+    lengths are Geometric(1/mean_run) (support >= 1), each run starting at a
+    random free block; mean_run >= n gives one sorted consecutive run."""
+    if mean_run >= n:
+        s = int(rng.integers(0, num_blocks - n + 1))
+        return np.arange(s, s + n, dtype=np.int64)
+    used = np.zeros(num_blocks, bool)
+    out = []
+    while len(out) < n:
+        length = min(int(rng.geometric(1.0 / mean_run)), n - len(out))
+        b = int(rng.integers(0, num_blocks))
+        while used[b]:
+            b = int(rng.integers(0, num_blocks))
+        while length > 0 and b < num_blocks and not used[b]:
+            used[b] = True
+            out.append(b)
+            b += 1
+            length -= 1
+    return np.asarray(out, np.int64)
+
+
+def leg_fragmentation(layers, xfer, seed, dma_requests=8):
+    """Config 4: 64 requests, prefixes of U[1K,16K] tokens (16-token blocks),
+    block ids as geometric runs of mean 1/4/32/640; even requests save, odd
+    requests restore (50/50 interleaved); payload GB/s per transfer mode.  The
+    pinned pool is reused per request (the batch's working set exceeds the
+    20,000-block layer tensors).  The DMA modes issue one copy per run and are
+    timed on the first `dma_requests` requests only."""
+    from pegaflow_amd import _lib
+    from pegaflow_amd import workload as wl
+    from pegaflow_amd.runtime import PinnedBuffer
+
+    shape = layers.shape
+    rng = np.random.Generator(np.random.PCG64(seed + 4))
+    tokens = rng.integers(1024, 16385, 64)
+    n_blocks = [(int(t) + 15) // 16 for t in tokens]
+    pool = PinnedBuffer(max(n_blocks) * shape.layers * 2 * shape.bytes_per_block)
+    out = {}
+    for mean_run in (1, 4, 32, 640):
+        reqs = [draw_runs(rng, shape.num_blocks, nb, mean_run) for nb in n_blocks]
+        row = {}
+        for name, mode in _lib.MODE_NAMES.items():
+            use = reqs if name in ("kernel", "staged") else reqs[:dma_requests]
+            moved, t = 0, 0.0
+            for i, ids in enumerate(use):
+                saved = wl.save_plan(layers.regs, ids, pool.ptr)
+                t0 = time.perf_counter()
+                if i % 2 == 0:
+                    xfer.save_layers(saved, mode)
+                else:
+                    xfer.load_layers(saved, mode)
+                    xfer.synchronize()
+                t += time.perf_counter() - t0
+                moved += wl.payload_bytes(layers.regs, len(ids))
+            row[name] = round(moved / t / 1e9, 2)
+        runs = float(np.mean([1 + np.count_nonzero(np.diff(r) != 1) for r in reqs]))
+        out[f"mean_run_{mean_run}"] = {"gbps": row,
+                                       "measured_mean_run": round(float(np.mean(n_blocks)) / runs, 2)}
+        log(f"[bench] fragmentation mean_run={mean_run}: {row}")
+    pool.close()
+    layers.refill()
+    return {"workload": "64 requests, prefixes U[1K,16K] tokens on llama-3.1-8b layers, "
+                        "save/restore interleaved 50/50", "by_mean_run": out,
+            "dma_modes_timed_on_requests": dma_requests}
+
+
+def leg_mla(xfer, seed):
+    """Config 5: MLA latent, 61 layers [8192, 64, 576] as bf16 and fp8 bytes
+    (one segment per block), 128 random blocks saved then restored into 128
+    other blocks; bit-exact per dtype, payload GB/s per direction."""
+    from pegaflow_amd import _lib
+    from pegaflow_amd import workload as wl
+    from pegaflow_amd.runtime import PinnedBuffer
+
+    out = {}
+    for shape in (wl.MLA_BF16, wl.MLA_FP8):
+        layers = wl.DeviceLayers(shape, base_seed=seed)
+        ids, targets = wl.draw_blocks(shape.num_blocks, 128, seed)
+        P = wl.payload_bytes(layers.regs, 128)
+        pool = PinnedBuffer(P)
+        saved = wl.save_plan(layers.regs, ids, pool.ptr)
+        loads = wl.load_plan(saved, targets)
+        xfer.save_layers(saved, _lib.MODE_KERNEL)
+        xfer.load_layers(loads, _lib.MODE_KERNEL)
+        xfer.synchronize()
+        t_s = timed(lambda: xfer.save_layers(saved, _lib.MODE_KERNEL), 3)
+        t_l = timed(lambda: (xfer.load_layers(loads, _lib.MODE_KERNEL), xfer.synchronize()), 3)
+        bad = wl.verify_saved(layers, saved) + wl.verify_restored(layers, ids, targets)
+        out[shape.name] = {"payload_bytes": P, "save_gbps": round(P / t_s / 1e9, 2),
+                           "restore_gbps": round(P / t_l / 1e9, 2),
+                           "restore_ms": round(t_l * 1e3, 3), "bit_exact": bad == 0}
+        log(f"[bench] {shape.name}: {out[shape.name]}")
+        pool.close()
+        layers.close()
+    return out
 
 
 def cpu_baseline(shape, ids, targets, n_layers, threads, seed):
@@ -324,6 +485,16 @@ def main():
     xfer2.close()
     pool2.close()
 
+    extra = {}
+    if not args.quick:
+        log("[bench] config 3: layer-wise restore (qwen3-8b)")
+        extra["layerwise_qwen3_8b"] = leg_layerwise(xfer, args.seed)
+        log(f"[bench] {extra['layerwise_qwen3_8b']}")
+        log("[bench] config 5: MLA latent bf16 / fp8")
+        extra["mla_latent"] = leg_mla(xfer, args.seed)
+        log("[bench] config 4: fragmentation sweep")
+        extra["fragmentation_llama3_8b"] = leg_fragmentation(layers, xfer, args.seed)
+
     cpu = None
     if not args.no_cpu_baseline:
         threads = max(1, min(16, len(os.sched_getaffinity(0))))
@@ -384,6 +555,7 @@ def main():
         "bit_exact": bad_host == 0 and bad_dev == 0,
         "cpu_baseline": cpu,
     }
+    out.update(extra)
     if variants:
         out["variants"] = variants
     if sweep:

@@ -131,12 +131,18 @@ class DeviceBuffer:
 
     def fill_random(self, seed: int, word_offset: int = 0, stream: Stream | None = None,
                     nbytes: int | None = None, offset: int = 0) -> None:
+        """Fill with splitmix64 words.  Without a stream the fill runs on the
+        null stream and is waited for: the transfer contexts' streams are
+        non-blocking and would not order after it."""
         n = self.nbytes - offset if nbytes is None else nbytes
         check(lib().pf_fill_random(self.ptr + offset, n, seed % 2**64, word_offset,
                                    stream.handle if stream else None), "pf_fill_random")
+        if stream is None:
+            synchronize()
 
     def memset(self, value: int) -> None:
         check(lib().pf_memset_d8(self.ptr, value, self.nbytes), "pf_memset_d8")
+        synchronize()
 
     def close(self) -> None:
         if self.ptr:
@@ -183,8 +189,11 @@ class PinnedBuffer:
 
 def fill_random(addr: int, nbytes: int, seed: int, word_offset: int = 0,
                 stream: Stream | None = None) -> None:
+    """As DeviceBuffer.fill_random: waited for when no stream is given."""
     check(lib().pf_fill_random(addr, nbytes, seed % 2**64, word_offset,
                                stream.handle if stream else None), "pf_fill_random")
+    if stream is None:
+        synchronize()
 
 
 def verify_random(addr: int, nbytes: int, seed: int, word_offset: int = 0) -> int:
