@@ -63,6 +63,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--quick", action="store_true",
                     help="skip the config 3/4/5 legs (layer-wise, fragmentation, MLA)")
+    ap.add_argument("--profile-gather", action="store_true",
+                    help="only run the calibration copy and the device gather (PMC passes)")
     ap.add_argument("--cpu-sample-layers", type=int, default=8)
     ap.add_argument("--staging-mib", type=int, default=256)
     ap.add_argument("--seed", type=int, default=0)
@@ -277,6 +279,54 @@ def leg_mla(xfer, seed):
     return out
 
 
+def profile_gather(seed):
+    """For rocprofv3 --pmc passes: 3 launches of the copy kernel as a plain
+    contiguous 1 GiB device copy (known bytes: 1 GiB read, 1 GiB written),
+    then 3 launches of the Llama prefix device gather (2P algorithmic bytes).
+    The two are told apart by grid size (131,072 vs 163,840 workgroups)."""
+    from pegaflow_amd import _lib, runtime
+    from pegaflow_amd import workload as wl
+    from pegaflow_amd.runtime import DeviceBuffer
+    from pegaflow_amd.transfer import KVCacheRegistration, TransferContext
+
+    runtime.init(0)
+    xfer = TransferContext(0)
+    src, dst = DeviceBuffer(GiB), DeviceBuffer(GiB)
+    src.fill_random(seed + 99)
+    chunk = 32768
+    reg = KVCacheRegistration.create(src.ptr, GiB, GiB // chunk, chunk, 0, 1)
+    plain = wl.save_plan([reg], np.arange(GiB // chunk), dst.ptr)
+    for _ in range(3):
+        xfer.save_layers(plain, _lib.MODE_KERNEL)
+    layers = wl.DeviceLayers(wl.LLAMA3_8B, base_seed=seed)
+    ids, _ = wl.draw_blocks(wl.LLAMA3_8B.num_blocks, 640, seed)
+    P = wl.payload_bytes(layers.regs, 640)
+    gbuf = DeviceBuffer(P)
+    gather = wl.save_plan(layers.regs, ids, gbuf.ptr)
+    for _ in range(3):
+        xfer.save_layers(gather, _lib.MODE_KERNEL)
+    print(json.dumps({"plain_copy_bytes_read": GiB, "plain_copy_bytes_written": GiB,
+                      "gather_algorithmic_bytes": 2 * P,
+                      "plain_workgroups": (GiB // chunk) * 4, "gather_workgroups": 40960 * 4}),
+          flush=True)
+    xfer.close()
+
+
+def read_traffic():
+    """HBM bytes per gather launch from the committed rocprofv3 --pmc summary
+    (profiles/copy_chunks_llama3_8b_prefix_traffic.txt), or None."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        "copy_chunks_llama3_8b_prefix_traffic.txt")
+    try:
+        with open(path) as fh:
+            for line in fh:
+                if line.startswith("traffic_bytes_per_launch"):
+                    return int(line.split("=")[1].strip())
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(shape, ids, targets, n_layers, threads, seed):
     """The reference's CPU-side copy pattern, timed with host memcpy: save =
     one copy per segment (gpu_worker.rs:344-360), restore = one copy per merged
@@ -345,6 +395,9 @@ def main():
               "(each rank moves its own layers over its own host link); run with --gpus 1",
               file=sys.stderr)
         sys.exit(2)
+    if args.profile_gather:
+        profile_gather(args.seed)
+        return
 
     from pegaflow_amd import _lib, runtime
     from pegaflow_amd.runtime import DeviceBuffer, PinnedBuffer
@@ -541,7 +594,7 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(gather_gbps / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": read_traffic(),
             "kernel": "copy_chunks_v16_kernel<1,nt,nt> 512 threads (device gather: 40960 chunks of 32 KiB, 1 launch)",
             "bytes_per_launch": 2 * P,
             "ms_per_launch": round(gather_ms, 4),
