@@ -401,7 +401,7 @@ def main():
 
     from pegaflow_amd import _lib, runtime
     from pegaflow_amd.runtime import DeviceBuffer, PinnedBuffer
-    from pegaflow_amd.transfer import LayerTransfer, TransferContext
+    from pegaflow_amd.transfer import KVCacheRegistration, TransferContext
     from pegaflow_amd import workload as wl
 
     shape = wl.LLAMA3_8B
@@ -439,10 +439,11 @@ def main():
             for _ in range(reps):
                 run(plan)
                 ms.append(xfer.last_kernel_ms()[0])
-            key = f"{label}_t{threads}_u{unroll & 0xff}{nt_names[unroll & 0x300]}"
+            key = (f"{label}_t{threads}_u{unroll & 0xff}{nt_names[unroll & 0x300]}"
+                   f"{'_xcd' if unroll & _lib.KERNEL_XCD_MAJOR else ''}")
             sweep[key] = round(bytes_moved / (min(ms) / 1e3) / 1e9, 1)
             log(f"[bench] sweep {key}: {min(ms):.4f} ms = {sweep[key]} GB/s")
-        xfer.set_kernel_shape(*default_shape)
+        xfer.reset_kernel_shape()
 
     if args.sweep:
         save_k = lambda plan: xfer.save_layers(plan, _lib.MODE_KERNEL)  # noqa: E731
@@ -452,6 +453,18 @@ def main():
                     [(t, u | nt) for t in (256, 512, 768, 1024) for u in (1, 2, 4)
                      for nt in (0, _lib.KERNEL_NT_LOADS, _lib.KERNEL_NT_STORES,
                                 _lib.KERNEL_NONTEMPORAL)])
+        xcd_shapes = [(t, u | _lib.KERNEL_NONTEMPORAL | x) for t in (256, 512, 1024)
+                      for u in (1, 2) for x in (0, _lib.KERNEL_XCD_MAJOR)]
+        shape_sweep("gatherx", gather, save_k, 5, 2 * P, xcd_shapes)
+        scatter_plan = wl.load_plan(gather, targets)
+        shape_sweep("scatter", scatter_plan, load_k, 5, 2 * P, xcd_shapes)
+        # The same kernel as a plain contiguous copy of the packed buffer.
+        creg = KVCacheRegistration.create(gather_buf.ptr, P, P // 32768, 32768, 0, 1)
+        plain_dst = DeviceBuffer(P)
+        plain = wl.save_plan([creg], np.arange(P // 32768), plain_dst.ptr)
+        shape_sweep("plaincopy", plain, save_k, 5, 2 * P, xcd_shapes)
+        plain_dst.close()
+        layers.refill()
         for grid in (1024, 2048, 4096):
             xfer.set_max_grid(grid)
             shape_sweep(f"gather_grid{grid}", gather, save_k, 5, 2 * P, [default_shape])

@@ -246,12 +246,25 @@ int pf_xfer_synchronize(pf_xfer* xfer);
 /* Select the kernel's launch shape: threads per workgroup (64..1024, multiple
  * of 64) and 16-byte loads in flight per lane (1, 2, 4, 8 or 16), optionally
  * OR-ed with PF_KERNEL_NT_LOADS and/or PF_KERNEL_NT_STORES for non-temporal
- * (streaming) loads and stores.  0 keeps the current value.  Defaults: 512
- * threads, 1 load, non-temporal loads and stores (the fastest shape measured
- * for the HBM gather on MI355X). */
+ * (streaming) loads and stores.  0 keeps the current value.  Sets the shape
+ * of both directions; defaults below. */
 #define PF_KERNEL_NT_LOADS 0x100u
 #define PF_KERNEL_NT_STORES 0x200u
 #define PF_KERNEL_NONTEMPORAL (PF_KERNEL_NT_LOADS | PF_KERNEL_NT_STORES)
+/* Give each of the 8 XCDs one contiguous range of tiles instead of the
+ * hardware's round-robin deal (only with an uncapped grid). */
+#define PF_KERNEL_XCD_MAJOR 0x400u
+/* Per-direction defaults (the fastest HBM shapes measured on MI355X):
+ * saves gather 8 KiB tiles in round-robin order, loads scatter 16 KiB tiles
+ * in XCD-major order. */
+#define PF_SAVE_DEFAULT_THREADS 512u
+#define PF_SAVE_DEFAULT_UNROLL (1u | PF_KERNEL_NONTEMPORAL)
+#define PF_LOAD_DEFAULT_THREADS 512u
+#define PF_LOAD_DEFAULT_UNROLL (2u | PF_KERNEL_NONTEMPORAL | PF_KERNEL_XCD_MAJOR)
+/* Shape for one direction only: 0 = saves (gather), 1 = loads (scatter).
+ * pf_xfer_set_kernel_shape sets both. */
+int pf_xfer_set_kernel_shape_dir(pf_xfer* xfer, uint32_t direction,
+                                 uint32_t threads, uint32_t unroll);
 int pf_xfer_set_kernel_shape(pf_xfer* xfer, uint32_t threads, uint32_t unroll);
 /* Upper bound on workgroups per gather/scatter launch (0 = one workgroup per
  * tile, the default); with a bound, each workgroup loops over tiles. */

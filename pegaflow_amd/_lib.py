@@ -64,6 +64,9 @@ PINNED_NUMA_USER = 4
 KERNEL_NT_LOADS = 0x100
 KERNEL_NT_STORES = 0x200
 KERNEL_NONTEMPORAL = KERNEL_NT_LOADS | KERNEL_NT_STORES
+KERNEL_XCD_MAJOR = 0x400
+SAVE_DEFAULT_SHAPE = (512, 1 | KERNEL_NONTEMPORAL)
+LOAD_DEFAULT_SHAPE = (512, 2 | KERNEL_NONTEMPORAL | KERNEL_XCD_MAJOR)
 
 LOAD_PENDING, LOAD_SUCCESS, LOAD_ERROR = 0, 1, -1
 
@@ -190,6 +193,7 @@ SIGNATURES = {
     "pf_xfer_set_kernel_shape": (i32, [vp, u32, u32]),
     "pf_xfer_last_stats": (i32, [vp, pu64, pu64]),
     "pf_xfer_set_max_grid": (i32, [vp, u32]),
+    "pf_xfer_set_kernel_shape_dir": (i32, [vp, u32, u32, u32]),
     "pf_xfer_set_timing": (i32, [vp, i32]),
     "pf_xfer_last_kernel_ms": (i32, [vp, ctypes.POINTER(ctypes.c_float), pu64]),
     "pf_save_layers": (i32, [vp, ctypes.POINTER(LayerXfer), u32, u32]),

@@ -50,14 +50,29 @@ __device__ __forceinline__ void store16(g_u32x4* p, u32x4 v) {
 // NTL / NTS select non-temporal (streaming) loads / stores: every byte is
 // touched exactly once, so there is nothing to gain from keeping it in L2 or
 // the MALL, and streaming accesses leave those caches to other traffic.
+// Workgroup -> tile order.  Workgroups are dealt round-robin to the 8 XCDs
+// (workgroup b runs on XCD b % 8).  With xcd_major set (and one workgroup
+// per tile), XCD x instead takes one contiguous range of tiles:
+//   n = 8q + r tiles; XCD x owns q + (x < r) tiles starting at x*q + min(x, r);
+//   workgroup b = 8i + x handles the i-th of them.
+// The workgroups with b % 8 == x number exactly q + (x < r), so this is a
+// bijection of [0, n).
+__device__ __forceinline__ uint32_t tile_of(uint32_t b, uint32_t n, bool xcd_major) {
+  if (!xcd_major) return b;
+  const uint32_t x = b & 7u, i = b >> 3, q = n >> 3, r = n & 7u;
+  return x * q + (x < r ? x : r) + i;
+}
+
 template <int UNROLL, bool NTL, bool NTS>
 __global__ void __launch_bounds__(1024)
 copy_chunks_v16_kernel(const ChunkDesc* __restrict__ descs,
                        uint32_t tiles_per_chunk, uint32_t n_tiles,
-                       uint32_t chunk16) {
+                       uint32_t chunk16, uint32_t xcd_major) {
   const uint32_t stride = blockDim.x;
   const uint32_t tile_elems = stride * UNROLL;
-  for (uint32_t t = blockIdx.x; t < n_tiles; t += gridDim.x) {
+  const bool remap = xcd_major && gridDim.x == n_tiles;
+  for (uint32_t b = blockIdx.x; b < n_tiles; b += gridDim.x) {
+    const uint32_t t = tile_of(b, n_tiles, remap);
     const uint32_t c = t / tiles_per_chunk;
     const uint32_t tile = t - c * tiles_per_chunk;
     const ChunkDesc d = descs[c];
@@ -104,43 +119,48 @@ static constexpr uint32_t kMaxGrid = 1u << 20;
 
 template <int UNROLL, bool NTL, bool NTS>
 static void launch_v16_nt(dim3 grid, dim3 block, hipStream_t stream, const ChunkDesc* d,
-                          uint32_t tpc, uint32_t n_tiles, uint32_t c16) {
+                          uint32_t tpc, uint32_t n_tiles, uint32_t c16, uint32_t xcd) {
   hipLaunchKernelGGL((copy_chunks_v16_kernel<UNROLL, NTL, NTS>), grid, block, 0, stream, d,
-                     tpc, n_tiles, c16);
+                     tpc, n_tiles, c16, xcd);
 }
 
 template <int UNROLL>
 static hipError_t launch_v16(const ChunkDesc* d_descs, uint32_t tiles_per_chunk,
                              uint32_t n_tiles, uint32_t chunk16, uint32_t threads,
-                             uint32_t nt_flags, uint32_t max_grid, hipStream_t stream) {
+                             uint32_t flags, uint32_t max_grid, hipStream_t stream) {
   const uint32_t cap = max_grid ? max_grid : kMaxGrid;
   const dim3 grid(n_tiles < cap ? n_tiles : cap), block(threads);
-  switch (nt_flags) {
+  const uint32_t xcd = (flags & PF_KERNEL_XCD_MAJOR) ? 1u : 0u;
+  switch (flags & PF_KERNEL_NONTEMPORAL) {
     case 0:
-      launch_v16_nt<UNROLL, false, false>(grid, block, stream, d_descs, tiles_per_chunk, n_tiles, chunk16);
+      launch_v16_nt<UNROLL, false, false>(grid, block, stream, d_descs, tiles_per_chunk, n_tiles,
+                                          chunk16, xcd);
       break;
     case PF_KERNEL_NT_LOADS:
-      launch_v16_nt<UNROLL, true, false>(grid, block, stream, d_descs, tiles_per_chunk, n_tiles, chunk16);
+      launch_v16_nt<UNROLL, true, false>(grid, block, stream, d_descs, tiles_per_chunk, n_tiles,
+                                         chunk16, xcd);
       break;
     case PF_KERNEL_NT_STORES:
-      launch_v16_nt<UNROLL, false, true>(grid, block, stream, d_descs, tiles_per_chunk, n_tiles, chunk16);
+      launch_v16_nt<UNROLL, false, true>(grid, block, stream, d_descs, tiles_per_chunk, n_tiles,
+                                         chunk16, xcd);
       break;
     default:
-      launch_v16_nt<UNROLL, true, true>(grid, block, stream, d_descs, tiles_per_chunk, n_tiles, chunk16);
+      launch_v16_nt<UNROLL, true, true>(grid, block, stream, d_descs, tiles_per_chunk, n_tiles,
+                                        chunk16, xcd);
       break;
   }
   return hipGetLastError();
 }
 
 // `unroll` carries the loads in flight per lane (low byte) and the
-// PF_KERNEL_NT_LOADS / PF_KERNEL_NT_STORES flags.
+// PF_KERNEL_NT_LOADS / PF_KERNEL_NT_STORES / PF_KERNEL_XCD_MAJOR flags.
 hipError_t launch_copy_chunks(const ChunkDesc* d_descs, uint32_t n_chunks,
                               uint64_t chunk_bytes, bool aligned16,
                               uint32_t threads, uint32_t unroll,
                               uint32_t max_grid, hipStream_t stream) {
   if (n_chunks == 0 || chunk_bytes == 0) return hipSuccess;
   if (threads == 0 || threads > 1024 || threads % 64 != 0) return hipErrorInvalidValue;
-  const uint32_t nt = unroll & PF_KERNEL_NONTEMPORAL;
+  const uint32_t flags = unroll & (PF_KERNEL_NONTEMPORAL | PF_KERNEL_XCD_MAJOR);
   unroll &= 0xffu;
   if (max_grid > kMaxGrid) max_grid = kMaxGrid;
   if (!aligned16) {
@@ -164,11 +184,11 @@ hipError_t launch_copy_chunks(const ChunkDesc* d_descs, uint32_t n_chunks,
   const uint32_t ntl = static_cast<uint32_t>(n_tiles);
   const uint32_t c16 = static_cast<uint32_t>(chunk16);
   switch (unroll) {
-    case 1: return launch_v16<1>(d_descs, tpc, ntl, c16, threads, nt, max_grid, stream);
-    case 2: return launch_v16<2>(d_descs, tpc, ntl, c16, threads, nt, max_grid, stream);
-    case 4: return launch_v16<4>(d_descs, tpc, ntl, c16, threads, nt, max_grid, stream);
-    case 8: return launch_v16<8>(d_descs, tpc, ntl, c16, threads, nt, max_grid, stream);
-    case 16: return launch_v16<16>(d_descs, tpc, ntl, c16, threads, nt, max_grid, stream);
+    case 1: return launch_v16<1>(d_descs, tpc, ntl, c16, threads, flags, max_grid, stream);
+    case 2: return launch_v16<2>(d_descs, tpc, ntl, c16, threads, flags, max_grid, stream);
+    case 4: return launch_v16<4>(d_descs, tpc, ntl, c16, threads, flags, max_grid, stream);
+    case 8: return launch_v16<8>(d_descs, tpc, ntl, c16, threads, flags, max_grid, stream);
+    case 16: return launch_v16<16>(d_descs, tpc, ntl, c16, threads, flags, max_grid, stream);
     default: return hipErrorInvalidValue;
   }
 }

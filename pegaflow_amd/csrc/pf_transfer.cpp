@@ -242,12 +242,15 @@ struct pf_xfer {
   uint64_t slot_bytes = 0;
   hipEvent_t slot_ready[2] = {nullptr, nullptr};
   hipEvent_t slot_free[2] = {nullptr, nullptr};
-  // Default launch shape: 512 threads, one non-temporal 16-byte load in flight
-  // per lane, i.e. one 8 KiB tile per workgroup (the fastest HBM gather shape
-  // measured on MI355X; the host-link-bound zero-copy paths are insensitive
-  // to the shape).
-  uint32_t threads = 512;
-  uint32_t unroll = 1 | PF_KERNEL_NONTEMPORAL;
+  // Launch shapes, [0] for saves (gather from the paged tensor) and [1] for
+  // loads (scatter into it), the fastest measured on MI355X for the HBM
+  // paths (the host-link-bound zero-copy paths are insensitive to the shape):
+  //   gather:  512 threads, one non-temporal 16 B load per lane (8 KiB tiles),
+  //            round-robin tile order;
+  //   scatter: 512 threads, two non-temporal loads per lane (16 KiB tiles),
+  //            XCD-major tile order.
+  uint32_t threads[2] = {PF_SAVE_DEFAULT_THREADS, PF_LOAD_DEFAULT_THREADS};
+  uint32_t unroll[2] = {PF_SAVE_DEFAULT_UNROLL, PF_LOAD_DEFAULT_UNROLL};
   uint32_t max_grid = 0;
   uint64_t last_kernels = 0;
   uint64_t last_dma = 0;
@@ -298,8 +301,9 @@ int upload_desc(pf_xfer* x, size_t n) {
   return PF_OK;
 }
 
-int launch(pf_xfer* x, size_t first, size_t n, uint64_t chunk_bytes, bool al16) {
+int launch(pf_xfer* x, size_t first, size_t n, uint64_t chunk_bytes, bool al16, bool is_save) {
   if (n == 0) return PF_OK;
+  const int dir = is_save ? 0 : 1;
   if (n > 0xffffffffull) return fail(PF_ERR_INVALID_ARGUMENT, "too many chunks");
   if (chunk_bytes / 16 >= (1ull << 31))
     return fail(PF_ERR_INVALID_ARGUMENT, "chunk too large");
@@ -316,7 +320,7 @@ int launch(pf_xfer* x, size_t first, size_t n, uint64_t chunk_bytes, bool al16) 
   }
   (void)hipGetLastError();
   hipError_t e = launch_copy_chunks(x->d_desc + first, static_cast<uint32_t>(n),
-                                    chunk_bytes, al16, x->threads, x->unroll,
+                                    chunk_bytes, al16, x->threads[dir], x->unroll[dir],
                                     x->max_grid, x->stream);
   if (e != hipSuccess) return hip_fail(e, "gather/scatter kernel launch");
   if (tm) PF_HIP(hipEventRecord(tm->second, x->stream));
@@ -452,7 +456,7 @@ int staged_slice(pf_xfer* x, const std::vector<LayerPlan>& plans, const Slice& s
   };
   if (is_save) {
     PF_HIP(hipStreamWaitEvent(x->stream, x->slot_free[s.slot], 0));
-    if (int rc = launch(x, s.desc_first, s.end - s.begin, p.chunk_bytes, al16)) return rc;
+    if (int rc = launch(x, s.desc_first, s.end - s.begin, p.chunk_bytes, al16, true)) return rc;
     PF_HIP(hipEventRecord(x->slot_ready[s.slot], x->stream));
     PF_HIP(hipStreamWaitEvent(x->dma, x->slot_ready[s.slot], 0));
     for_each_host_run(p, s.begin, s.end, dma_run);
@@ -464,7 +468,7 @@ int staged_slice(pf_xfer* x, const std::vector<LayerPlan>& plans, const Slice& s
     if (e != hipSuccess) return hip_fail(e, "staged hipMemcpyAsync (H2D)");
     PF_HIP(hipEventRecord(x->slot_ready[s.slot], x->dma));
     PF_HIP(hipStreamWaitEvent(x->stream, x->slot_ready[s.slot], 0));
-    if (int rc = launch(x, s.desc_first, s.end - s.begin, p.chunk_bytes, al16)) return rc;
+    if (int rc = launch(x, s.desc_first, s.end - s.begin, p.chunk_bytes, al16, false)) return rc;
     PF_HIP(hipEventRecord(x->slot_free[s.slot], x->stream));
   }
   return PF_OK;
@@ -551,7 +555,7 @@ int kernel_direct(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<Lay
     }
     size_t n = 0;
     for (size_t k = li; k < lj; ++k) n += plans[k].chunks.size();
-    if (int rc = launch(x, first[li], n, p.chunk_bytes, al)) return rc;
+    if (int rc = launch(x, first[li], n, p.chunk_bytes, al, is_save)) return rc;
     if (layer_events && layer_events[li])
       PF_HIP(hipEventRecord(static_cast<hipEvent_t>(layer_events[li]), x->stream));
     li = lj;
@@ -740,17 +744,24 @@ int pf_xfer_synchronize(pf_xfer* x) {
 }
 
 int pf_xfer_set_kernel_shape(pf_xfer* x, uint32_t threads, uint32_t unroll) {
+  if (int rc = pf_xfer_set_kernel_shape_dir(x, 0, threads, unroll)) return rc;
+  return pf_xfer_set_kernel_shape_dir(x, 1, threads, unroll);
+}
+
+int pf_xfer_set_kernel_shape_dir(pf_xfer* x, uint32_t direction, uint32_t threads,
+                                 uint32_t unroll) {
   if (!x) return fail(PF_ERR_INVALID_ARGUMENT, "null transfer context");
+  if (direction > 1) return fail(PF_ERR_INVALID_ARGUMENT, "direction must be 0 (save) or 1 (load)");
   if (threads && (threads < 64 || threads > 1024 || threads % 64))
     return fail(PF_ERR_INVALID_ARGUMENT, "threads must be a multiple of 64 in [64, 1024]");
   const uint32_t u = unroll & 0xffu;
   if (unroll && u != 1 && u != 2 && u != 4 && u != 8 && u != 16)
     return fail(PF_ERR_INVALID_ARGUMENT, "unroll must be 1, 2, 4, 8 or 16");
-  if (unroll & ~(0xffu | PF_KERNEL_NONTEMPORAL))
+  if (unroll & ~(0xffu | PF_KERNEL_NONTEMPORAL | PF_KERNEL_XCD_MAJOR))
     return fail(PF_ERR_INVALID_ARGUMENT, "unknown kernel flag");
   std::lock_guard<std::mutex> lk(x->mu);
-  if (threads) x->threads = threads;
-  if (unroll) x->unroll = unroll;
+  if (threads) x->threads[direction] = threads;
+  if (unroll) x->unroll[direction] = unroll;
   return PF_OK;
 }
 

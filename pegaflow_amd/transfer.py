@@ -203,6 +203,16 @@ class TransferContext:
               "pf_xfer_last_stats")
         return k.value, d.value
 
+    def set_kernel_shape_dir(self, direction: int, threads: int = 0, unroll: int = 0) -> None:
+        """direction 0 = saves (gather), 1 = loads (scatter)."""
+        check(lib().pf_xfer_set_kernel_shape_dir(self.handle, direction, threads, unroll),
+              "pf_xfer_set_kernel_shape_dir")
+
+    def reset_kernel_shape(self) -> None:
+        """Back to the per-direction defaults."""
+        self.set_kernel_shape_dir(0, *_lib.SAVE_DEFAULT_SHAPE)
+        self.set_kernel_shape_dir(1, *_lib.LOAD_DEFAULT_SHAPE)
+
     def set_max_grid(self, max_workgroups: int) -> None:
         check(lib().pf_xfer_set_max_grid(self.handle, max_workgroups), "pf_xfer_set_max_grid")
 

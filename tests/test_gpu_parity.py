@@ -318,8 +318,20 @@ def test_kernel_shapes_and_nontemporal(ctx, shape):
         # Segments that end in a partial tile of every shape.
         _oracle_roundtrip_case(ctx, _lib.MODE_KERNEL, 20, 16 * 1000, 2, 20 * 16000,
                                40 * 16000, [3, 19, 0], [5, 6, 7], seed=nt + 1)
-    ctx.set_kernel_shape(512, 1 | _lib.KERNEL_NONTEMPORAL)
+    ctx.reset_kernel_shape()
     ctx.set_max_grid(0)
+
+
+@pytest.mark.parametrize("shape", [(512, 1), (256, 2), (64, 1)])
+def test_xcd_major_tile_order(ctx, shape):
+    threads, unroll = shape
+    say(f"[gpu] xcd-major tile order threads={threads} unroll={unroll}")
+    ctx.set_kernel_shape(threads, unroll | _lib.KERNEL_NONTEMPORAL | _lib.KERNEL_XCD_MAJOR)
+    # Tile counts that are and are not multiples of 8.
+    for nb, n in ((64, 13), (64, 64), (40, 7)):
+        _oracle_roundtrip_case(ctx, _lib.MODE_KERNEL, nb, 32768, 2, nb * 32768, 2 * nb * 32768,
+                               list(range(n)), list(range(nb - 1, nb - 1 - n, -1)), seed=n)
+    ctx.reset_kernel_shape()
 
 
 def test_capped_grid_loops_over_tiles(ctx):
