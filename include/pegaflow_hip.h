@@ -158,6 +158,22 @@ int pf_host_device_pointer(const void* host_ptr, uint64_t* dev_ptr);
 uint64_t pf_huge_page_size(void);
 
 /* ------------------------------------------------------------------------ */
+/* Device-memory IPC.  Replaces the CUDA-IPC sharing of layer tensors between */
+/* the inference process and the engine server (torch _share_cuda_ /          */
+/* _new_shared_cuda: ipc_wrapper.py:101-156, registry.rs:144-175).           */
+/* Allocations of 2 GiB or more are refused on both ends.                     */
+/* ------------------------------------------------------------------------ */
+#define PF_IPC_HANDLE_BYTES 64
+#define PF_IPC_MAX_ALLOC_BYTES (1ull << 31)
+/* Handle of the device allocation containing dev_ptr, with its base and size. */
+int pf_ipc_export(uint64_t dev_ptr, uint8_t* handle, uint64_t* alloc_base,
+                  uint64_t* alloc_size);
+/* Maps an exported allocation of alloc_size bytes into this process; *base is
+ * the mapped base address.  The range becomes valid for the kernels. */
+int pf_ipc_open(const uint8_t* handle, uint64_t alloc_size, uint64_t* base);
+int pf_ipc_close(uint64_t base);
+
+/* ------------------------------------------------------------------------ */
 /* Reference-equivalent DMA primitives (transfer.rs:56-239).                  */
 /* ------------------------------------------------------------------------ */
 /* Synchronous device -> host copy of size bytes from gpu_base+offset.

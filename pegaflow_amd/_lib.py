@@ -181,6 +181,9 @@ SIGNATURES = {
     "pf_pinned_free": (i32, [vp]),
     "pf_host_device_pointer": (i32, [vp, pu64]),
     "pf_huge_page_size": (u64, []),
+    "pf_ipc_export": (i32, [u64, vp, pu64, pu64]),
+    "pf_ipc_open": (i32, [vp, u64, pu64]),
+    "pf_ipc_close": (i32, [u64]),
     "pf_copy_gpu_to_cpu": (i32, [u64, u64, vp, u64, u64]),
     "pf_copy_cpu_to_gpu_async": (i32, [u64, u64, vp, u64, u64, vp]),
     "pf_batch_copy_segments_to_gpu": (i32, [pu64, pu64, u64, u64, pl, vp, pu64]),

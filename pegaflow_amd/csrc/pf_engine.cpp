@@ -729,7 +729,16 @@ int pf_engine_unregister_instance(pf_engine* e, const char* instance_id) {
     removed = std::move(it->second);
     e->instances.erase(it);
   }
-  return PF_OK;  // workers stop when the last reference drops
+  // Queued loads still read the instance's layer tensors: let them finish
+  // before the caller may release that memory. The workers themselves stop
+  // when the last reference to the instance drops.
+  std::vector<std::shared_ptr<DeviceWorker>> workers;
+  {
+    std::shared_lock<std::shared_mutex> g(removed->gpus_mu);
+    for (auto& gk : removed->gpus) workers.push_back(gk.second->worker);
+  }
+  for (auto& w : workers) w->wait_idle();
+  return PF_OK;
 }
 
 // lib.rs:803-838.

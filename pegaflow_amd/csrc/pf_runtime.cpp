@@ -41,6 +41,22 @@ bool pinned_lookup(uint64_t addr, uint64_t len, uint64_t* base, uint64_t* end) {
   return true;
 }
 
+// Allocations mapped from another process with pf_ipc_open.
+static std::mutex g_ipc_mu;
+static std::map<uint64_t, uint64_t> g_ipc;  // base -> size
+
+static bool ipc_lookup(uint64_t addr, uint64_t len, uint64_t* base, uint64_t* end) {
+  std::lock_guard<std::mutex> lk(g_ipc_mu);
+  auto it = g_ipc.upper_bound(addr);
+  if (it == g_ipc.begin()) return false;
+  --it;
+  const uint64_t b = it->first, e = it->first + it->second;
+  if (addr < b || addr + len > e || addr + len < addr) return false;
+  *base = b;
+  *end = e;
+  return true;
+}
+
 bool RangeCache::contains(uint64_t a, uint64_t len) {
   const uint64_t e = a + len;
   if (e < a) return false;
@@ -58,7 +74,7 @@ bool RangeCache::check(uint64_t a, uint64_t len) {
   if (a == 0 || a + len < a) return false;
   if (contains(a, len)) return true;
   uint64_t b = 0, e = 0;
-  if (pinned_lookup(a, len, &b, &e)) {
+  if (pinned_lookup(a, len, &b, &e) || ipc_lookup(a, len, &b, &e)) {
     ok_.push_back({b, e});
     last_b_ = b;
     last_e_ = e;
@@ -320,6 +336,75 @@ int pf_host_device_pointer(const void* host_ptr, uint64_t* dev_ptr) {
   void* d = nullptr;
   PF_HIP(hipHostGetDevicePointer(&d, const_cast<void*>(host_ptr), 0));
   *dev_ptr = reinterpret_cast<uint64_t>(d);
+  return PF_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Device-memory IPC.
+// ---------------------------------------------------------------------------
+int pf_ipc_export(uint64_t dev_ptr, uint8_t* handle, uint64_t* alloc_base,
+                  uint64_t* alloc_size) {
+  if (!handle) return fail(PF_ERR_INVALID_ARGUMENT, "null handle buffer");
+  hipPointerAttribute_t attr;
+  hipError_t e = hipPointerGetAttributes(&attr, reinterpret_cast<void*>(dev_ptr));
+  if (e != hipSuccess || attr.type != hipMemoryTypeDevice) {
+    (void)hipGetLastError();
+    return fail(PF_ERR_INVALID_ARGUMENT,
+                strf("0x%llx is not device memory", (unsigned long long)dev_ptr));
+  }
+  hipDeviceptr_t base = nullptr;
+  size_t size = 0;
+  PF_HIP(hipMemGetAddressRange(&base, &size, reinterpret_cast<hipDeviceptr_t>(dev_ptr)));
+  if (size >= PF_IPC_MAX_ALLOC_BYTES)
+    return fail(PF_ERR_UNSUPPORTED,
+                strf("allocation of %zu bytes is too large to share between processes "
+                     "(limit %llu)",
+                     size, (unsigned long long)PF_IPC_MAX_ALLOC_BYTES));
+  hipIpcMemHandle_t h;
+  PF_HIP(hipIpcGetMemHandle(&h, base));
+  std::memcpy(handle, &h, PF_IPC_HANDLE_BYTES);
+  if (alloc_base) *alloc_base = reinterpret_cast<uint64_t>(base);
+  if (alloc_size) *alloc_size = size;
+  return PF_OK;
+}
+
+int pf_ipc_open(const uint8_t* handle, uint64_t alloc_size, uint64_t* base) {
+  if (!handle || !base) return fail(PF_ERR_INVALID_ARGUMENT, "null argument");
+  if (alloc_size == 0 || alloc_size >= PF_IPC_MAX_ALLOC_BYTES)
+    return fail(PF_ERR_UNSUPPORTED,
+                strf("shared allocation size %llu outside (0, %llu)",
+                     (unsigned long long)alloc_size, (unsigned long long)PF_IPC_MAX_ALLOC_BYTES));
+  hipIpcMemHandle_t h;
+  std::memcpy(&h, handle, PF_IPC_HANDLE_BYTES);
+  void* p = nullptr;
+  PF_HIP(hipIpcOpenMemHandle(&p, h, hipIpcMemLazyEnablePeerAccess));
+  // Trust the exporter's size only as far as the mapping goes.
+  hipDeviceptr_t mb = nullptr;
+  size_t ms = 0;
+  if (hipMemGetAddressRange(&mb, &ms, p) == hipSuccess) {
+    if (reinterpret_cast<uint64_t>(mb) != reinterpret_cast<uint64_t>(p) || ms < alloc_size) {
+      (void)hipIpcCloseMemHandle(p);
+      return fail(PF_ERR_INVALID_ARGUMENT,
+                  strf("shared allocation maps %zu bytes, %llu declared", ms,
+                       (unsigned long long)alloc_size));
+    }
+  } else {
+    (void)hipGetLastError();
+  }
+  {
+    std::lock_guard<std::mutex> lk(g_ipc_mu);
+    g_ipc[reinterpret_cast<uint64_t>(p)] = alloc_size;
+  }
+  *base = reinterpret_cast<uint64_t>(p);
+  return PF_OK;
+}
+
+int pf_ipc_close(uint64_t base) {
+  {
+    std::lock_guard<std::mutex> lk(g_ipc_mu);
+    g_ipc.erase(base);
+  }
+  PF_HIP(hipIpcCloseMemHandle(reinterpret_cast<void*>(base)));
   return PF_OK;
 }
 

@@ -1,0 +1,257 @@
+"""The engine server: `pegaflow.Engine` over gRPC in front of PegaEngine.
+
+Mirrors pegaflow-server/src/service.rs:19-405 (RPC semantics and the mapping
+of engine errors to gRPC codes, service.rs:77-88), registry.rs:41-176 (layer
+tensors held per (instance, tp_rank, device), dropped on UnregisterContext)
+and the subset of the CLI (lib.rs:38-113) that concerns this path.
+
+Run: python -m pegaflow_amd.rpc.server --addr 127.0.0.1:50055 --device 0 --pool-size 30gb
+"""
+
+from __future__ import annotations
+
+import argparse
+import logging
+import signal
+import sys
+import threading
+from concurrent import futures
+
+import grpc
+
+from .. import _lib
+from ..engine import PegaEngine
+from ..ipc import OpenedTensor, open_tensor
+from . import proto
+
+log = logging.getLogger("pegaflow.server")
+
+# service.rs:77-88.
+_CODE = {
+    _lib.PF_ERR_INVALID_ARGUMENT: grpc.StatusCode.INVALID_ARGUMENT,
+    _lib.PF_ERR_INSTANCE_MISSING: grpc.StatusCode.FAILED_PRECONDITION,
+    _lib.PF_ERR_WORKER_MISSING: grpc.StatusCode.FAILED_PRECONDITION,
+    _lib.PF_ERR_TOPOLOGY_MISMATCH: grpc.StatusCode.FAILED_PRECONDITION,
+}
+
+
+def parse_memory_size(s: str) -> int:
+    """utils.rs:3-36: a number with an optional kb/mb/gb/tb suffix (1024-based)."""
+    s = s.strip()
+    if "_" in s:
+        raise ValueError(f"Invalid number: '{s}'")
+    boundary = next((i for i, c in enumerate(s) if c.isascii() and c.isalpha()), len(s))
+    num, unit = s[:boundary].strip(), s[boundary:].strip().lower()
+    try:
+        value = float(num)
+    except ValueError:
+        raise ValueError(f"Invalid number: '{num}'") from None
+    if value < 0:
+        raise ValueError("Memory size cannot be negative")
+    mult = {"": 1, "b": 1, "kb": 1 << 10, "mb": 1 << 20, "gb": 1 << 30, "tb": 1 << 40}
+    if unit not in mult:
+        raise ValueError(f"Unknown unit: '{unit}'. Use kb, mb, gb, or tb")
+    return int(value * mult[unit])
+
+
+class TensorRegistry:
+    """Registered layer tensors per context key "instance:tpR:devD"
+    (registry.rs:41-176)."""
+
+    def __init__(self):
+        self._lock = threading.Lock()
+        self._contexts: dict[str, tuple[int, dict[str, OpenedTensor]]] = {}
+
+    @staticmethod
+    def context_key(instance_id: str, tp_rank: int, device_id: int) -> str:
+        return f"{instance_id}:tp{tp_rank}:dev{device_id}"
+
+    def register_layer(self, key: str, layer_name: str, device_id: int,
+                       wrapper_bytes: bytes) -> OpenedTensor:
+        t = open_tensor(wrapper_bytes)
+        with self._lock:
+            dev, tensors = self._contexts.setdefault(key, (t.device_id, {}))
+            if dev != t.device_id:
+                t.close()
+                raise ValueError(f"context {key} is pinned to device {dev} but got {t.device_id}")
+            old = tensors.pop(layer_name, None)
+            tensors[layer_name] = t
+        if old is not None:
+            old.close()
+        return t
+
+    def drop_instance(self, instance_id: str) -> int:
+        prefix = f"{instance_id}:"
+        with self._lock:
+            keys = [k for k in self._contexts if k.startswith(prefix)]
+            dropped = [self._contexts.pop(k)[1] for k in keys]
+        n = 0
+        for tensors in dropped:
+            for t in tensors.values():
+                t.close()
+                n += 1
+        return n
+
+    def clear(self) -> None:
+        with self._lock:
+            dropped = list(self._contexts.values())
+            self._contexts.clear()
+        for _, tensors in dropped:
+            for t in tensors.values():
+                t.close()
+
+
+def _ok():
+    return proto.ResponseStatus(ok=True, message="")
+
+
+class EngineService:
+    """service.rs:133-405."""
+
+    def __init__(self, engine: PegaEngine):
+        self.engine = engine
+        self.registry = TensorRegistry()
+        self.shutdown_event = threading.Event()
+
+    def _abort(self, context, err: Exception):
+        if isinstance(err, _lib.PegaFlowError):
+            context.abort(_CODE.get(err.code, grpc.StatusCode.INTERNAL), str(err))
+        context.abort(grpc.StatusCode.INTERNAL, str(err))
+
+    def RegisterContext(self, req, context):
+        try:
+            t = self.registry.register_layer(
+                TensorRegistry.context_key(req.instance_id, req.tp_rank, req.device_id),
+                req.layer_name, req.device_id, req.wrapper_bytes)
+        except Exception as e:  # the reference's map_py_error (service.rs:90-93)
+            context.abort(grpc.StatusCode.INTERNAL, f"register tensor failed: {e}")
+        try:
+            self.engine.register_context_layer(
+                req.instance_id, req.namespace, t.device_id, req.layer_name, t.data_ptr,
+                t.size_bytes, req.num_blocks, req.bytes_per_block, req.kv_stride_bytes,
+                req.segments, req.tp_rank, req.tp_size, req.num_layers)
+        except Exception as e:
+            self._abort(context, e)
+        return proto.RegisterContextResponse(status=_ok())
+
+    def Save(self, req, context):
+        saves = [(s.layer_name, list(s.block_ids), list(s.block_hashes)) for s in req.saves]
+        try:
+            self.engine.batch_save_kv_blocks(req.instance_id, req.tp_rank, req.device_id, saves)
+        except Exception as e:
+            self._abort(context, e)
+        return proto.SaveResponse(status=_ok())
+
+    def Load(self, req, context):
+        try:
+            self.engine.batch_load_kv_blocks(req.instance_id, req.tp_rank, req.device_id,
+                                             req.load_state_shm, list(req.layer_names),
+                                             list(req.block_ids), list(req.block_hashes))
+        except Exception as e:
+            self._abort(context, e)
+        return proto.LoadResponse(status=_ok())
+
+    def Query(self, req, context):
+        try:
+            hits = self.engine.count_prefix_hit_blocks(req.instance_id, list(req.block_hashes))
+        except Exception as e:
+            self._abort(context, e)
+        return proto.QueryResponse(status=_ok(), hit_blocks=hits,
+                                   prefetch_state=proto.PREFETCH_READY, loading_blocks=0,
+                                   missing_blocks=0)
+
+    def UnregisterContext(self, req, context):
+        # The engine goes first: dropping its last reference to the instance
+        # drains the instance's queued loads, so no transfer still reads a
+        # mapping when the registry closes it below.
+        err = None
+        try:
+            self.engine.unregister_instance(req.instance_id)
+        except Exception as e:
+            err = e
+        removed = self.registry.drop_instance(req.instance_id)
+        if removed:
+            log.info("Dropped %d device tensors for instance %s", removed, req.instance_id)
+        if err is not None:
+            self._abort(context, err)
+        return proto.UnregisterResponse(status=_ok())
+
+    def Shutdown(self, req, context):
+        log.warning("Shutdown requested via RPC")
+        self.shutdown_event.set()
+        return proto.ShutdownResponse(status=_ok())
+
+    def Health(self, req, context):
+        return proto.HealthResponse(status=_ok())
+
+    def handler(self) -> grpc.GenericRpcHandler:
+        methods = {}
+        for rpc, req, resp in proto.METHODS:
+            methods[rpc] = grpc.unary_unary_rpc_method_handler(
+                getattr(self, rpc),
+                request_deserializer=proto.messages[req].FromString,
+                response_serializer=proto.messages[resp].SerializeToString)
+        return grpc.method_handlers_generic_handler(f"{proto.PACKAGE}.{proto.SERVICE}", methods)
+
+
+class Server:
+    """A running engine server (engine + registry + gRPC endpoint)."""
+
+    def __init__(self, addr: str = "127.0.0.1:50055", engine: PegaEngine | None = None,
+                 pool_size: int = 30 << 30, host_pool: bool = False, unit_size_hint: int = 0,
+                 max_workers: int = 16):
+        self.engine = engine or PegaEngine(pool_size=pool_size, host_pool=host_pool,
+                                           unit_size_hint=unit_size_hint)
+        self.service = EngineService(self.engine)
+        self.grpc = grpc.server(futures.ThreadPoolExecutor(max_workers=max_workers),
+                                options=[("grpc.max_receive_message_length", 256 << 20),
+                                         ("grpc.max_send_message_length", 256 << 20)])
+        self.grpc.add_generic_rpc_handlers((self.service.handler(),))
+        self.port = self.grpc.add_insecure_port(addr)
+        if self.port == 0:
+            raise RuntimeError(f"failed to bind {addr}")
+        self.addr = addr.rsplit(":", 1)[0] + f":{self.port}"
+
+    def start(self) -> "Server":
+        self.grpc.start()
+        log.info("pegaflow engine server listening on %s", self.addr)
+        return self
+
+    def wait(self, poll_s: float = 0.2) -> None:
+        while not self.service.shutdown_event.wait(poll_s):
+            pass
+
+    def stop(self, grace: float = 1.0) -> None:
+        self.grpc.stop(grace).wait()
+        self.engine.wait_idle()
+        self.service.registry.clear()
+        self.engine.close()
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(prog="pegaflow-server",
+                                 description="PegaEngine gRPC server (MI355X transfer path)")
+    ap.add_argument("--addr", default="127.0.0.1:50055")
+    ap.add_argument("--device", type=int, default=0)
+    ap.add_argument("--pool-size", type=parse_memory_size, default=parse_memory_size("30gb"))
+    ap.add_argument("--hint-value-size", type=parse_memory_size, default=0,
+                    help="allocation unit of the pinned pool")
+    ap.add_argument("--log-level", default="info")
+    ap.add_argument("--max-workers", type=int, default=16)
+    args = ap.parse_args(argv)
+    logging.basicConfig(level=getattr(logging, args.log_level.upper(), logging.INFO),
+                        format="%(asctime)s %(levelname)s %(name)s: %(message)s")
+    from .. import runtime
+    runtime.init(args.device)
+    server = Server(args.addr, pool_size=args.pool_size, unit_size_hint=args.hint_value_size,
+                    max_workers=args.max_workers).start()
+    for sig in (signal.SIGINT, signal.SIGTERM):
+        signal.signal(sig, lambda *_: server.service.shutdown_event.set())
+    print(f"READY {server.addr}", flush=True)
+    server.wait()
+    server.stop()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -230,3 +230,24 @@ def test_huge_page_size_parse():
     from pegaflow_amd.runtime import huge_page_size
     size = huge_page_size()
     assert size >= 2 * 1024 * 1024 and size & (size - 1) == 0
+
+
+def test_xcd_major_remap_is_a_bijection():
+    """The load kernel's tile order (tile_of in pf_kernels.hip): workgroup b
+    runs on XCD b mod 8 and takes tile x*q + min(x, r) + i.  It must visit
+    every tile of [0, n) exactly once, with XCD x owning one contiguous range
+    of q or q+1 tiles, for every tile count."""
+    for n in range(1, 4097):
+        q, r = n >> 3, n & 7
+        seen = bytearray(n)
+        owner = [[] for _ in range(8)]
+        for b in range(n):
+            x, i = b & 7, b >> 3
+            t = x * q + min(x, r) + i
+            assert 0 <= t < n and not seen[t], (n, b, t)
+            seen[t] = 1
+            owner[x].append(t)
+        for x in range(8):
+            ts = owner[x]
+            assert ts == list(range(ts[0], ts[0] + len(ts))) if ts else True
+            assert len(ts) == q + (1 if x < r else 0)

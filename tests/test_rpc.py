@@ -1,0 +1,207 @@
+"""The `pegaflow.Engine` wire surface on the CPU: schema encodings, the
+tensor-handle record, the server's CLI size parser, and a live in-process
+server over a plain host pool (no transfers).
+
+The reference's own tests for this surface are the parse_memory_size cases
+(pegaflow-server/src/utils.rs:42-57); the encodings below are fixed by the
+field numbers and types of pegaflow-proto/proto/engine.proto:5-115 and the
+protobuf wire format (tag = field << 3 | wire type; packed varints for
+repeated int32; two's-complement 10-byte varints for negative int32).
+"""
+
+import grpc
+import pytest
+
+from pegaflow_amd import ipc
+from pegaflow_amd.engine import PegaEngine
+from pegaflow_amd.load_state import PyLoadState
+from pegaflow_amd.rpc import proto
+from pegaflow_amd.rpc.client import EngineRpcClient
+from pegaflow_amd.rpc.server import Server, TensorRegistry, parse_memory_size
+
+
+# ---------------------------------------------------------------------------
+# Wire encodings.
+# ---------------------------------------------------------------------------
+def test_register_request_encoding():
+    m = proto.RegisterContextRequest(instance_id="a", device_id=1, num_blocks=300, segments=2,
+                                     namespace="ns")
+    # 0a 01 'a' | 10 01 | 28 ac02 (300) | 40 02 | 62 02 'ns'
+    assert m.SerializeToString().hex() == "0a0161100128ac02400262026e73"
+
+
+def test_save_layer_encoding_packs_ids_and_sign_extends():
+    m = proto.SaveLayer(layer_name="l", block_ids=[1, 2, -1], block_hashes=[b"xy"])
+    assert m.SerializeToString().hex() == "0a016c120c0102ffffffffffffffffff011a027879"
+    back = proto.SaveLayer.FromString(bytes.fromhex("0a016c120c0102ffffffffffffffffff011a027879"))
+    assert list(back.block_ids) == [1, 2, -1] and list(back.block_hashes) == [b"xy"]
+
+
+def test_query_response_encoding():
+    m = proto.QueryResponse(hit_blocks=5, prefetch_state=proto.PREFETCH_LOADING)
+    assert m.SerializeToString().hex() == "10051801"
+    # proto3 omits defaults: an all-default status still marks presence.
+    m2 = proto.HealthResponse(status=proto.ResponseStatus(ok=False))
+    assert m2.SerializeToString().hex() == "0a00" and m2.HasField("status")
+
+
+def test_every_field_number_and_service_path():
+    d = proto.LoadRequest.DESCRIPTOR
+    assert [(f.name, f.number) for f in d.fields] == [
+        ("instance_id", 1), ("tp_rank", 2), ("device_id", 3), ("load_state_shm", 4),
+        ("layer_names", 5), ("block_ids", 6), ("block_hashes", 7)]
+    d = proto.RegisterContextRequest.DESCRIPTOR
+    assert [f.number for f in d.fields] == list(range(1, 13))
+    assert proto.method_path("Query") == "/pegaflow.Engine/Query"
+    svc = proto.FILE.services_by_name["Engine"]
+    assert [m.name for m in svc.methods] == ["RegisterContext", "Save", "Load", "Query",
+                                             "UnregisterContext", "Shutdown", "Health"]
+
+
+# ---------------------------------------------------------------------------
+# parse_memory_size: utils.rs:42-57 plus the unit table of utils.rs:22-29.
+# ---------------------------------------------------------------------------
+def test_parse_memory_size_basic():
+    assert parse_memory_size("1024") == 1024
+    assert parse_memory_size("1gb") == 1 << 30
+    assert parse_memory_size("1.5gb") == int(1.5 * 1024 * 1024 * 1024)
+    assert parse_memory_size(" 500MB ") == 500 << 20
+    assert parse_memory_size("1TB") == 1 << 40
+    assert parse_memory_size("512kb") == 512 << 10
+    assert parse_memory_size("7b") == 7
+
+
+def test_parse_memory_size_invalid():
+    for bad in ("", "abc", "-10gb", "10pb", "1_000"):
+        with pytest.raises(ValueError):
+            parse_memory_size(bad)
+
+
+# ---------------------------------------------------------------------------
+# The tensor-handle record.
+# ---------------------------------------------------------------------------
+def test_local_tensor_record_round_trip():
+    rec = ipc.local_tensor(0x7F0000001000, 4096, 3)
+    assert len(rec) == ipc.RECORD_BYTES == 104
+    t = ipc.open_tensor(rec)
+    assert (t.data_ptr, t.size_bytes, t.device_id, t.mapped_base) == (0x7F0000001000, 4096, 3, 0)
+
+
+def test_record_rejections_happen_before_any_device_call():
+    rec = bytearray(ipc.local_tensor(0x1000, 64, 0))
+    with pytest.raises(ValueError, match="must be 104 bytes"):
+        ipc.open_tensor(bytes(rec[:-1]))
+    bad = bytes(b"XXXXXXXX") + bytes(rec[8:])
+    with pytest.raises(ValueError, match="not a pegaflow tensor handle"):
+        ipc.open_tensor(bad)
+    past = ipc._HEAD.pack(ipc.MAGIC_PTR, 0, 0, 100, 64, 64) + bytes(64)
+    with pytest.raises(ValueError, match="extends past"):
+        ipc.open_tensor(past)
+    big = ipc._HEAD.pack(ipc.MAGIC_IPC, 0, 0, 1 << 31, 0, 64) + bytes(64)
+    with pytest.raises(ValueError, match="2 GiB"):
+        ipc.open_tensor(big)
+
+
+def test_registry_keys_and_drop():
+    r = TensorRegistry()
+    k0 = TensorRegistry.context_key("inst", 0, 0)
+    assert k0 == "inst:tp0:dev0"
+    r.register_layer(k0, "l0", 0, ipc.local_tensor(0x1000, 64, 0))
+    r.register_layer(k0, "l0", 0, ipc.local_tensor(0x2000, 64, 0))  # replaces
+    r.register_layer(TensorRegistry.context_key("inst", 1, 0), "l0", 0,
+                     ipc.local_tensor(0x3000, 64, 0))
+    r.register_layer(TensorRegistry.context_key("inst2", 0, 0), "l0", 0,
+                     ipc.local_tensor(0x4000, 64, 0))
+    with pytest.raises(ValueError, match="pinned to device 0"):
+        r.register_layer(k0, "l1", 1, ipc.local_tensor(0x5000, 64, 1))
+    assert r.drop_instance("inst") == 2
+    assert r.drop_instance("inst") == 0
+    assert r.drop_instance("inst2") == 1
+
+
+# ---------------------------------------------------------------------------
+# A live server over a plain host pool.
+# ---------------------------------------------------------------------------
+@pytest.fixture
+def served():
+    srv = Server("127.0.0.1:0", engine=PegaEngine(pool_size=64 << 20, host_pool=True)).start()
+    client = EngineRpcClient(f"http://{srv.addr}")
+    yield srv, client
+    client.close()
+    srv.stop()
+
+
+def _register(client, layer, nb=16, bpb=512, layers=2, inst="i0", tp_size=1, ptr=0x10000):
+    size = 2 * nb * bpb
+    return client.register_context(inst, "ns", 0, tp_size, 0, layers, layer,
+                                   ipc.local_tensor(ptr, size, 0), nb, bpb, nb * bpb, 2)
+
+
+def test_health_and_endpoint(served):
+    srv, client = served
+    assert client.health() == (True, "")
+    assert client.endpoint() == f"http://{srv.addr}"
+
+
+def test_register_query_unregister(served):
+    srv, client = served
+    assert _register(client, "l0") == (True, "")
+    assert _register(client, "l1") == (True, "")
+    q = client.query("i0", [b"a", b"b"])
+    assert q == {"ok": True, "message": "", "hit_blocks": 0, "prefetch_state": "ready",
+                 "loading_blocks": 0, "missing_blocks": 0}
+    assert client.unregister_context("i0") == (True, "")
+    with pytest.raises(RuntimeError, match=r"unregister_context RPC failed: .*FAILED_PRECONDITION"
+                                           r".*instance i0 not found"):
+        client.unregister_context("i0")
+
+
+def test_error_codes_follow_engine_errors(served):
+    srv, client = served
+    _register(client, "l0")
+    with pytest.raises(RuntimeError, match=r"FAILED_PRECONDITION.*topology mismatch"):
+        _register(client, "l2", layers=3)
+    with pytest.raises(RuntimeError, match=r"INVALID_ARGUMENT.*out of range for layer l0"):
+        client.save("i0", 0, 0, [("l0", [16], [b"h"])])
+    with pytest.raises(RuntimeError, match=r"query RPC failed: .*FAILED_PRECONDITION"
+                                           r".*instance zz not found"):
+        client.query("zz", [b"a"])
+    with pytest.raises(RuntimeError, match=r"register_context RPC failed: .*INTERNAL"
+                                           r".*register tensor failed"):
+        client.register_context("i0", "ns", 0, 1, 0, 2, "l9", b"short", 16, 512, 8192, 2)
+    # Negative ids only: nothing to transfer.
+    assert client.save("i0", 0, 0, [("l0", [-1], [b"a"])]) == (True, "")
+
+
+def test_load_failure_reaches_the_load_state(served):
+    srv, client = served
+    _register(client, "l0")
+    st = PyLoadState()
+    with pytest.raises(RuntimeError, match=r"load RPC failed: .*missing KV block hash"):
+        client.load("i0", 0, 0, st.shm_name(), ["l0"], [1], [b"abc"])
+    assert st.get_state() == -1
+    st2 = PyLoadState()
+    assert client.load("i0", 0, 0, st2.shm_name(), ["l0"], [], []) == (True, "")
+    assert st2.get_state() == 1
+
+
+def test_shutdown_sets_the_event(served):
+    srv, client = served
+    assert client.shutdown() == (True, "")
+    assert srv.service.shutdown_event.is_set()
+
+
+def test_client_fails_fast_without_a_server():
+    with pytest.raises(RuntimeError, match="failed to connect to engine server"):
+        EngineRpcClient("http://127.0.0.1:1", connect_timeout_s=0.3)
+
+
+def test_server_speaks_to_a_raw_channel(served):
+    """A client built only from the wire format (as the reference's tonic
+    client is) gets the same answers."""
+    srv, _ = served
+    ch = grpc.insecure_channel(srv.addr)
+    call = ch.unary_unary("/pegaflow.Engine/Health", request_serializer=lambda b: b,
+                          response_deserializer=lambda b: b)
+    assert call(b"", timeout=5) == bytes.fromhex("0a020801")  # status{ok=true}
+    ch.close()

@@ -1,0 +1,159 @@
+"""The `pegaflow.Engine` gRPC path on the GPU: register layer tensors by
+handle, save by hash, overwrite the layers, load by hash through LoadState,
+and check every byte against the oracle — first with the server in this
+process (pointer handles), then with the server in a child process that
+maps the layers through HIP IPC, as a vLLM worker and the reference's
+pegaflow-server do (pegaflow-server/src/registry.rs:144-175)."""
+
+import hashlib
+import os
+import select
+import subprocess
+import sys
+import time
+
+import numpy as np
+import pytest
+
+import oracle
+from pegaflow_amd import ipc
+from pegaflow_amd.engine import PegaEngine
+from pegaflow_amd.load_state import PyLoadState
+from pegaflow_amd.rpc.client import EngineRpcClient
+from pegaflow_amd.rpc.server import Server
+from pegaflow_amd.runtime import DeviceBuffer
+
+pytestmark = pytest.mark.gpu
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+MiB = 1 << 20
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def h(i):
+    return hashlib.sha256(b"rpc" + int(i).to_bytes(8, "little")).digest()
+
+
+def wait(st, timeout=60.0):
+    t0 = time.monotonic()
+    while not st.is_ready():
+        assert time.monotonic() - t0 < timeout, "load did not complete"
+        time.sleep(0.0005)
+    return st.get_state()
+
+
+class Layers:
+    """KV-first layers [2, nb, block] on device 0."""
+
+    def __init__(self, n_layers, nb, bpb, seed):
+        self.nb, self.bpb, self.kv, self.size = nb, bpb, nb * bpb, 2 * nb * bpb
+        self.names = [f"model.layers.{l}.self_attn" for l in range(n_layers)]
+        self.bufs = [DeviceBuffer(self.size) for _ in range(n_layers)]
+        self.fill(seed)
+
+    def fill(self, seed):
+        for l, b in enumerate(self.bufs):
+            b.fill_random(oracle.layer_seed(seed, l))
+
+    def host(self):
+        return [b.download() for b in self.bufs]
+
+    def expected(self, saved_from, clobbered, ids, targets):
+        """Oracle: blocks `ids` of `saved_from` copied to `targets` of `clobbered`."""
+        out = []
+        for src, dst in zip(saved_from, clobbered):
+            src, dst = src.copy(), dst.copy()
+            m = len(ids)
+            host = np.zeros(2 * m * self.bpb, np.uint8)
+            reg_s = oracle.layout(src.ctypes.data, self.size, self.nb, self.bpb, self.kv, 2)
+            k, v, _ = oracle.save_host_layout(reg_s, m, host.ctypes.data,
+                                              host.ctypes.data + m * self.bpb)
+            oracle.process_save(reg_s, src, ids, k, v)
+            reg_d = oracle.layout(dst.ctypes.data, self.size, self.nb, self.bpb, self.kv, 2)
+            oracle.process_load(reg_d, dst, targets, k, v)
+            out.append(dst)
+        return out
+
+    def close(self):
+        for b in self.bufs:
+            b.close()
+
+
+def round_trip(client, layers, handles, inst="vllm-0"):
+    n = len(layers.names)
+    for name, handle in zip(layers.names, handles):
+        assert client.register_context(inst, "llama", 0, 1, 0, n, name, handle, layers.nb,
+                                       layers.bpb, layers.kv, 2) == (True, "")
+    before = layers.host()
+    ids = [7, 0, 33, 12, 63, 20, 21]
+    hashes = [h(i) for i in ids]
+    assert client.save(inst, 0, 0, [(name, ids, hashes) for name in layers.names]) == (True, "")
+    q = client.query(inst, hashes + [h(1000)])
+    assert q["ok"] and q["hit_blocks"] == len(ids) and q["prefetch_state"] == "ready"
+    layers.fill(seed=99)  # what the GPU held is gone
+    clobbered = layers.host()
+    targets = [1, 2, 3, 62, 61, 40, 41]
+    st = PyLoadState(num_layers=n)
+    assert client.load(inst, 0, 0, st.shm_name(), layers.names, targets, hashes) == (True, "")
+    assert wait(st) == 1 and st.layers_done() == n
+    exp = layers.expected(before, clobbered, ids, targets)
+    for l, b in enumerate(layers.bufs):
+        assert np.array_equal(b.download(), exp[l]), f"layer {l}"
+    assert client.unregister_context(inst) == (True, "")
+
+
+def test_in_process_server_round_trip(gpu):
+    say("[gpu] rpc in-process round trip (pointer handles)")
+    srv = Server("127.0.0.1:0", engine=PegaEngine(pool_size=128 * MiB)).start()
+    layers = Layers(4, 64, 16 * 8 * 128 * 2, seed=5)
+    try:
+        with EngineRpcClient(f"http://{srv.addr}") as client:
+            handles = [ipc.local_tensor(b.ptr, layers.size, 0) for b in layers.bufs]
+            round_trip(client, layers, handles)
+    finally:
+        srv.stop()
+        layers.close()
+
+
+def _start_server():
+    cmd = [sys.executable, "-u", "-m", "pegaflow_amd.rpc.server", "--addr", "127.0.0.1:0",
+           "--pool-size", "128mb", "--log-level", "warning"]
+    p = subprocess.Popen(cmd, cwd=ROOT, stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
+                         env=dict(os.environ), text=True)
+    t0 = time.monotonic()
+    seen = []
+    while time.monotonic() - t0 < 90:
+        r, _, _ = select.select([p.stdout], [], [], 1.0)
+        if r:
+            line = p.stdout.readline()
+            if not line:
+                break
+            seen.append(line)
+            if line.startswith("READY "):
+                return p, line.split()[1]
+        if p.poll() is not None:
+            break
+    p.kill()
+    p.wait(10)
+    raise AssertionError("server did not start:\n" + "".join(seen))
+
+
+def test_two_process_ipc_round_trip(gpu):
+    say("[gpu] rpc two-process round trip (HIP IPC handles)")
+    layers = Layers(3, 64, 16 * 8 * 128 * 2, seed=11)
+    assert layers.size < ipc.MAX_ALLOC_BYTES
+    handles = [ipc.export_tensor(b.ptr, layers.size, 0) for b in layers.bufs]
+    p, addr = _start_server()
+    say(f"[gpu] server pid {p.pid} at {addr}")
+    try:
+        with EngineRpcClient(f"http://{addr}", connect_timeout_s=10) as client:
+            round_trip(client, layers, handles)
+            assert client.shutdown() == (True, "")
+        assert p.wait(60) == 0
+    finally:
+        if p.poll() is None:
+            p.kill()
+            p.wait(10)
+        layers.close()
