@@ -62,7 +62,8 @@ def parse():
                     help="16-byte loads in flight per lane, +256 for non-temporal (0: default)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--quick", action="store_true",
-                    help="skip the config 3/4/5 legs (layer-wise, fragmentation, MLA)")
+                    help="skip the config 3/4/5 legs (layer-wise, fragmentation, MLA) and "
+                         "the disk-tier leg")
     ap.add_argument("--profile-gather", action="store_true",
                     help="only run the calibration copy and the device gather (PMC passes)")
     ap.add_argument("--cpu-sample-layers", type=int, default=8)
@@ -277,6 +278,102 @@ def leg_mla(xfer, seed):
         pool.close()
         layers.close()
     return out
+
+
+def fs_type(path):
+    """Filesystem type of the mount that holds path (from /proc/mounts)."""
+    path, best, kind = os.path.realpath(path), "", "unknown"
+    try:
+        with open("/proc/mounts") as f:
+            for line in f:
+                parts = line.split()
+                mnt = parts[1]
+                if (path == mnt or path.startswith(mnt.rstrip("/") + "/")) and len(mnt) > len(best):
+                    best, kind = mnt, parts[2]
+    except OSError:
+        pass
+    return kind
+
+
+def leg_disk(layers, ids, targets, P):
+    """Disk tier (seal_offload.rs) on the Llama prefix: the engine saves the
+    prefix into its pinned pool and writes it to packed files (fsync'd, then
+    dropped from the page cache); a fresh engine on the same directory reads
+    it back into its pool on a prefix query and loads it into HBM."""
+    import hashlib
+    import shutil
+    import tempfile
+
+    from pegaflow_amd import workload as wl
+    from pegaflow_amd.engine import PegaEngine
+    from pegaflow_amd.load_state import PyLoadState
+
+    shape = layers.shape
+    base = os.environ.get("PEGAFLOW_DISK_DIR") or tempfile.gettempdir()
+    st_fs = os.statvfs(base)
+    free = st_fs.f_bavail * st_fs.f_frsize
+    if free < 2 * P:
+        return {"skipped": f"{free / 1e9:.1f} GB free under {base}, need {2 * P / 1e9:.1f}"}
+    root = tempfile.mkdtemp(prefix="pega_disk_", dir=base)
+    names = [f"layer.{l}" for l in range(len(layers.bufs))]
+    hashes = [hashlib.sha256(b"prefix" + int(i).to_bytes(8, "little")).digest() for i in ids]
+    ids_l, targets_l = [int(i) for i in ids], [int(t) for t in targets]
+    io_threads = 8
+
+    def engine():
+        e = PegaEngine(pool_size=P + (256 << 20))
+        e.enable_disk(root, quota_bytes=4 * P, io_threads=io_threads)
+        for name, buf in zip(names, layers.bufs):
+            e.register_context_layer("bench", "llama3-8b", 0, name, buf.ptr, shape.layer_bytes,
+                                     shape.num_blocks, shape.bytes_per_block,
+                                     shape.kv_stride_bytes, shape.segments, 0, 1, len(names))
+        return e
+
+    try:
+        layers.refill()
+        e1 = engine()
+        t0 = time.perf_counter()
+        e1.batch_save_kv_blocks("bench", 0, 0, [(n, ids_l, hashes) for n in names])
+        t1 = time.perf_counter()
+        e1.flush_disk()
+        t2 = time.perf_counter()
+        s1 = e1.disk_stats()
+        e1.close()
+        e2 = engine()
+        t3 = time.perf_counter()
+        q1 = e2.count_prefix_hit_blocks_with_prefetch("bench", hashes)
+        e2.wait_prefetch()
+        t4 = time.perf_counter()
+        q2 = e2.count_prefix_hit_blocks_with_prefetch("bench", hashes)
+        st = PyLoadState(num_layers=len(names))
+        t5 = time.perf_counter()
+        e2.batch_load_kv_blocks("bench", 0, 0, st.shm_name(), names, targets_l, hashes)
+        while not st.is_ready():
+            if time.perf_counter() - t5 > 60:
+                raise RuntimeError("disk-tier restore did not complete within 60 s")
+            time.sleep(0.0002)
+        t6 = time.perf_counter()
+        state = st.get_state()
+        s2 = e2.disk_stats()
+        e2.close()
+        bad = wl.verify_restored(layers, ids, targets)
+    finally:
+        shutil.rmtree(root, ignore_errors=True)
+    return {
+        "what": "llama prefix saved through the engine, written to packed files, read back "
+                "cold by a fresh engine on a prefix query, restored into HBM",
+        "filesystem": fs_type(base),
+        "engine_save_gbps": round(P / (t1 - t0) / 1e9, 3),
+        "write_gbps": round(P / (t2 - t1) / 1e9, 3),
+        "files": s1["files"], "file_bytes": s1["bytes"],
+        "cold_read_gbps": round(P / (t4 - t3) / 1e9, 3),
+        "io_threads": io_threads,
+        "first_query": q1["prefetch_state"],
+        "restore_gbps": round(P / (t6 - t5) / 1e9, 3),
+        "disk_to_hbm_ms": round((t6 - t3) * 1e3, 3),
+        "bit_exact": bad == 0 and state == 1 and q2["hit_blocks"] == len(ids_l)
+                     and s2["prefetched_blocks"] == len(ids_l),
+    }
 
 
 def profile_gather(seed):
@@ -560,6 +657,9 @@ def main():
         extra["mla_latent"] = leg_mla(xfer, args.seed)
         log("[bench] config 4: fragmentation sweep")
         extra["fragmentation_llama3_8b"] = leg_fragmentation(layers, xfer, args.seed)
+        log("[bench] disk tier: offload, cold prefetch, restore")
+        extra["disk_tier_llama3_8b"] = leg_disk(layers, ids, targets, P)
+        log(f"[bench] {extra['disk_tier_llama3_8b']}")
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -458,6 +458,64 @@ int pf_engine_stats_get(pf_engine* e, pf_engine_stats* out);
 /* Block until every queued load has finished. */
 int pf_engine_wait_idle(pf_engine* e);
 
+/* ------------------------------------------------------------------------ */
+/* Disk tier.  Replaces the DFS offload and prefetch of seal_offload.rs and   */
+/* the Redis index behind it (BlockMeta, seal_offload.rs:72-97) with packed   */
+/* files "<root>/<namespace>/<uuid>.bin" plus a "<uuid>.json" sidecar each.   */
+/* ------------------------------------------------------------------------ */
+/* spawn_dfs_offload_task (seal_offload.rs:169-191) with DfsOffloadConfig
+ * (seal_offload.rs:45-69): every block sealed from now on is written to disk
+ * in batches of up to max_pack_blocks; files already under root are indexed.
+ * Enable before the first save.  0 picks the default for max_pack_blocks
+ * (64), max_prefetch_tasks (16) and io_threads (4). */
+int pf_engine_enable_disk(pf_engine* e, const char* root, uint64_t quota_bytes,
+                          uint32_t max_pack_blocks, uint32_t max_prefetch_tasks,
+                          uint32_t io_threads);
+enum {
+  PF_PREFETCH_READY = 0,       /* PrefetchState, engine.proto:66-74 */
+  PF_PREFETCH_LOADING = 1,
+  PF_PREFETCH_PARTIAL_MISS = 2
+};
+typedef struct pf_prefetch_status {
+  int32_t state;
+  uint32_t reserved;
+  uint64_t hit_blocks;
+  uint64_t loading_blocks;
+  uint64_t missing_blocks;
+} pf_prefetch_status;
+/* count_prefix_hit_blocks_async (lib.rs:855-941): cache hits, then blocks
+ * being read; when the first other block is on disk, a background read of
+ * the rest of the prefix starts and the call reports it as loading.  Without
+ * a disk tier: the plain prefix count, state READY. */
+int pf_engine_query_prefetch(pf_engine* e, const char* instance_id,
+                             const uint8_t* hash_data,
+                             const uint64_t* hash_offsets, uint64_t n,
+                             pf_prefetch_status* out);
+/* No counterpart in the reference (tests, benchmarks, orderly shutdown):
+ * block until every queued block is on disk / no disk read is in flight. */
+int pf_engine_disk_flush(pf_engine* e);
+int pf_engine_disk_wait_prefetch(pf_engine* e);
+typedef struct pf_disk_stats {
+  uint64_t files;
+  uint64_t bytes;
+  uint64_t indexed_blocks;
+  uint64_t offloaded_blocks;
+  uint64_t written_bytes;
+  uint64_t prefetched_blocks;
+  uint64_t read_bytes;
+  uint64_t pending_blocks;
+  uint64_t evicted_files;
+  uint64_t failures;
+} pf_disk_stats;
+int pf_engine_disk_stats(pf_engine* e, pf_disk_stats* out);
+/* No counterpart in the reference (inspection for tests and tools): copy the
+ * host bytes of one slot of a cached block, K half then V half, into dst.
+ * *k_bytes / *v_bytes receive the sizes (v 0 for a contiguous slot). */
+int pf_engine_read_block_slot(pf_engine* e, const char* namespace_,
+                              const uint8_t* hash, uint64_t hash_len,
+                              uint64_t slot, uint8_t* dst, uint64_t dst_len,
+                              uint64_t* k_bytes, uint64_t* v_bytes);
+
 #ifdef __cplusplus
 }
 #endif

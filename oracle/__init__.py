@@ -94,6 +94,9 @@ def lib():
         L.or_process_load.argtypes = [pl, u64, ctypes.c_void_p, p64, p64, u64,
                                       p64, cp, sz]
         L.or_fill_random.argtypes = [u64, u64, u64, u64]
+        L.or_pack_blocks.argtypes = [u64, u64, p64, p64, p64, u64, p64]
+        L.or_pack_blocks.restype = u64
+        L.or_unpack_block.argtypes = [u64, u64, ctypes.c_void_p, p64, p64, p64]
         _lib = L
     return _lib
 
@@ -258,3 +261,68 @@ def fill_random(buf: np.ndarray, seed: int, word_offset: int = 0) -> None:
 def layer_seed(base_seed: int, layer: int) -> int:
     """Per-layer seed used by the synthetic workloads."""
     return (base_seed * 0x100000001B3 + layer * 0xD1B54A32D192ED03 + 1) % 2**64
+
+
+# --------------------------------------------------------------------------
+# Packed block files of the disk tier (seal_offload.rs).
+# --------------------------------------------------------------------------
+def pack_blocks(blocks) -> tuple[bytes, list[int]]:
+    """write_packed_file (seal_offload.rs:379-448).  ``blocks`` is a list of
+    blocks, each a list of slots (K bytes, V bytes or None).  Returns the
+    file bytes and each block's offset."""
+    n = len(blocks)
+    s = len(blocks[0]) if n else 0
+    keep = []
+    k = np.zeros(max(n * s, 1), np.uint64)
+    v = np.zeros(max(n * s, 1), np.uint64)
+    size = np.zeros(max(n * s, 1), np.uint64)
+    for b, slots in enumerate(blocks):
+        assert len(slots) == s
+        for j, (kb, vb) in enumerate(slots):
+            ka = np.frombuffer(bytes(kb) or b"\0", np.uint8).copy()
+            keep.append(ka)
+            k[b * s + j] = ka.ctypes.data
+            if vb is None:
+                size[b * s + j] = len(kb)
+            else:
+                assert len(vb) == len(kb)
+                va = np.frombuffer(bytes(vb) or b"\0", np.uint8).copy()
+                keep.append(va)
+                v[b * s + j] = va.ctypes.data
+                size[b * s + j] = 2 * len(kb)
+    offs = np.zeros(max(n, 1), np.uint64)
+    total = lib().or_pack_blocks(n, s, _p64(k), _p64(v), _p64(size), 0, _p64(offs))
+    out = np.zeros(max(total, 1), np.uint8)
+    lib().or_pack_blocks(n, s, _p64(k), _p64(v), _p64(size), out.ctypes.data, _p64(offs))
+    return out[:total].tobytes(), [int(o) for o in offs[:n]]
+
+
+def unpack_block(data: bytes, slots) -> list[tuple[bytes, bytes | None]]:
+    """rebuild_sealed_block (seal_offload.rs:869-909): ``slots`` is the
+    BlockMeta slot list [(is_split, size)]; returns (K, V or None) per slot."""
+    s = len(slots)
+    buf = np.frombuffer(bytes(data) or b"\0", np.uint8).copy()
+    split = np.array([1 if sp else 0 for sp, _ in slots] or [0], np.uint8)
+    size = np.array([sz for _, sz in slots] or [0], np.uint64)
+    k = np.zeros(max(s, 1), np.uint64)
+    v = np.zeros(max(s, 1), np.uint64)
+    lib().or_unpack_block(buf.ctypes.data, s, split.ctypes.data, _p64(size), _p64(k), _p64(v))
+    out = []
+    base = buf.ctypes.data
+    for j, (sp, sz) in enumerate(slots):
+        ko = int(k[j]) - base
+        if sp:
+            vo = int(v[j]) - base
+            out.append((buf[ko:ko + sz // 2].tobytes(), buf[vo:vo + sz // 2].tobytes()))
+        else:
+            out.append((buf[ko:ko + sz].tobytes(), None))
+    return out
+
+
+def block_meta_json(file: str, offset: int, slots, total_slots: int) -> str:
+    """BlockMeta as serde_json renders it (seal_offload.rs:80-97): compact,
+    fields in declaration order."""
+    body = ",".join('{"is_split":%s,"size":%d}' % ("true" if sp else "false", sz)
+                    for sp, sz in slots)
+    return '{"file":"%s","offset":%d,"slots":[%s],"total_slots":%d}' % (
+        file, offset, body, total_slots)

@@ -423,3 +423,40 @@ void or_fill_random(uint64_t dst, uint64_t size_bytes, uint64_t seed,
   for (uint64_t i = 0; i < n; i++)
     w[i] = mix64(seed + (word_offset + i + 1) * 0x9E3779B97F4A7C15ULL);
 }
+
+/* write_packed_file, seal_offload.rs:397-441: per block, per slot, the K half
+ * then the V half when the slot has a V pointer, else the whole slot. */
+uint64_t or_pack_blocks(uint64_t n, uint64_t s, const uint64_t* k,
+                        const uint64_t* v, const uint64_t* size, uint64_t out,
+                        uint64_t* offs) {
+  uint64_t off = 0;
+  for (uint64_t b = 0; b < n; b++) {
+    if (offs) offs[b] = off;
+    for (uint64_t j = 0; j < s; j++) {
+      const uint64_t i = b * s + j;
+      if (v[i]) {
+        const uint64_t half = size[i] / 2;
+        if (out) {
+          memcpy((uint8_t*)(uintptr_t)(out + off), (const void*)(uintptr_t)k[i], half);
+          memcpy((uint8_t*)(uintptr_t)(out + off + half), (const void*)(uintptr_t)v[i], half);
+        }
+        off += 2 * half;
+      } else {
+        if (out) memcpy((uint8_t*)(uintptr_t)(out + off), (const void*)(uintptr_t)k[i], size[i]);
+        off += size[i];
+      }
+    }
+  }
+  return off;
+}
+
+/* rebuild_sealed_block, seal_offload.rs:869-909. */
+void or_unpack_block(uint64_t base, uint64_t s, const uint8_t* is_split,
+                     const uint64_t* size, uint64_t* k, uint64_t* v) {
+  uint64_t off = 0;
+  for (uint64_t j = 0; j < s; j++) {
+    k[j] = base + off;
+    v[j] = is_split[j] ? base + off + size[j] / 2 : 0;
+    off += size[j];
+  }
+}

@@ -116,6 +116,18 @@ int or_process_load(const or_layout* reg, uint64_t dev,
 void or_fill_random(uint64_t dst, uint64_t size_bytes, uint64_t seed,
                     uint64_t word_offset);
 
+/* Packed block file (seal_offload.rs:379-448): n blocks of s slots each,
+ * slot j of block b described by k[b*s+j], v[b*s+j] (0 for a contiguous
+ * slot) and size[b*s+j] (K + V bytes).  Writes the file bytes to out (NULL:
+ * size only) and returns the total size; the block offsets go to offs[n]. */
+uint64_t or_pack_blocks(uint64_t n, uint64_t s, const uint64_t* k,
+                        const uint64_t* v, const uint64_t* size, uint64_t out,
+                        uint64_t* offs);
+/* rebuild_sealed_block (seal_offload.rs:869-909): the K/V addresses of the s
+ * slots of one block read to address base. */
+void or_unpack_block(uint64_t base, uint64_t s, const uint8_t* is_split,
+                     const uint64_t* size, uint64_t* k, uint64_t* v);
+
 #ifdef __cplusplus
 }
 #endif

@@ -135,6 +135,18 @@ class EngineStats(ctypes.Structure):
         "evicted_blocks", "saved_bytes", "loaded_bytes", "load_failures")]
 
 
+class PrefetchStatus(ctypes.Structure):
+    _fields_ = [("state", ctypes.c_int32), ("reserved", ctypes.c_uint32),
+                ("hit_blocks", ctypes.c_uint64), ("loading_blocks", ctypes.c_uint64),
+                ("missing_blocks", ctypes.c_uint64)]
+
+
+class DiskStats(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint64) for n in (
+        "files", "bytes", "indexed_blocks", "offloaded_blocks", "written_bytes",
+        "prefetched_blocks", "read_bytes", "pending_blocks", "evicted_files", "failures")]
+
+
 u64 = ctypes.c_uint64
 i64 = ctypes.c_int64
 u32 = ctypes.c_uint32
@@ -235,6 +247,12 @@ SIGNATURES = {
                                    u64]),
     "pf_engine_stats_get": (i32, [vp, ctypes.POINTER(EngineStats)]),
     "pf_engine_wait_idle": (i32, [vp]),
+    "pf_engine_enable_disk": (i32, [vp, cs, u64, u32, u32, u32]),
+    "pf_engine_query_prefetch": (i32, [vp, cs, vp, vp, u64, ctypes.POINTER(PrefetchStatus)]),
+    "pf_engine_disk_flush": (i32, [vp]),
+    "pf_engine_disk_wait_prefetch": (i32, [vp]),
+    "pf_engine_disk_stats": (i32, [vp, ctypes.POINTER(DiskStats)]),
+    "pf_engine_read_block_slot": (i32, [vp, cs, vp, u64, u64, vp, u64, pu64, pu64]),
 }
 
 _lib = None

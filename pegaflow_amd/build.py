@@ -23,6 +23,7 @@ SOURCES = [
     "pf_transfer.cpp",
     "pf_load_state.cpp",
     "pf_engine.cpp",
+    "pf_disk.cpp",
 ]
 
 # Packed-FP32 instructions are disabled for all device code (this library

@@ -261,14 +261,33 @@ int BlockStore::insert_slot(const std::string& key, size_t slot, std::shared_ptr
     }
   }
   if (sealed) {
-    std::lock_guard<std::mutex> lk(cache_mu_);
-    if (!cache_.count(key)) {
-      lru_.push_front(key);
-      cache_[key] = Entry{std::move(sealed), lru_.begin()};
+    bool fresh = false;
+    {
+      std::lock_guard<std::mutex> lk(cache_mu_);
+      if (!cache_.count(key)) {
+        lru_.push_front(key);
+        cache_[key] = Entry{sealed, lru_.begin()};
+        fresh = true;
+      }
     }
+    if (fresh && seal_hook_) seal_hook_(key, sealed);
   }
   *inserted = true;
   return PF_OK;
+}
+
+bool BlockStore::cache_insert(const std::string& key, std::shared_ptr<SealedBlock> block) {
+  std::lock_guard<std::mutex> lk(cache_mu_);
+  if (cache_.count(key)) return false;
+  lru_.push_front(key);
+  cache_[key] = Entry{std::move(block), lru_.begin()};
+  return true;
+}
+
+std::shared_ptr<SealedBlock> BlockStore::peek(const std::string& key) {
+  std::lock_guard<std::mutex> lk(cache_mu_);
+  auto it = cache_.find(key);
+  return it == cache_.end() ? nullptr : it->second.block;
 }
 
 int BlockStore::lookup_many(const std::vector<std::string>& keys,
@@ -537,6 +556,8 @@ struct pf_engine {
   std::atomic<uint64_t> saved_bytes{0};
   std::atomic<uint64_t> loaded_bytes{0};
   std::atomic<uint64_t> load_failures{0};
+  std::mutex disk_mu;
+  std::unique_ptr<DiskTier> disk;  // declared after store: destroyed before it
 };
 
 namespace {
@@ -643,6 +664,7 @@ int pf_engine_destroy(pf_engine* e) {
     std::unique_lock<std::shared_mutex> lk(e->mu);
     e->instances.clear();  // joins the workers after their queued loads
   }
+  e->disk.reset();  // writes what is queued, then stops its threads
   delete e;
   return PF_OK;
 }
@@ -908,6 +930,15 @@ int pf_engine_batch_load(pf_engine* e, const char* instance_id, uint64_t tp_rank
       if (block_ids[j] < 0) continue;
       if (slot >= task.keep[j]->slots.size() || !task.keep[j]->slots[slot]) continue;
       const LayerBlock& lb = *task.keep[j]->slots[slot];
+      const bool split = reg.segments == 2 && reg.kv_stride_bytes > reg.bytes_per_block;
+      if (lb.size != reg.block_size_bytes || (lb.v_ptr != nullptr) != split)
+        return bail(fail(PF_ERR_STORAGE,
+                         strf("storage error: stored block at index %llu holds %llu %s bytes "
+                              "for layer %s, which is registered with %llu %s bytes per block",
+                              (unsigned long long)j, (unsigned long long)lb.size,
+                              lb.v_ptr ? "split" : "contiguous", name.c_str(),
+                              (unsigned long long)reg.block_size_bytes,
+                              split ? "split" : "contiguous")));
       blocks.push_back(pf_block_xfer{block_ids[j], reinterpret_cast<uint64_t>(lb.k_ptr),
                                      reinterpret_cast<uint64_t>(lb.v_ptr)});
       task.bytes += lb.size;
@@ -936,6 +967,97 @@ int pf_engine_stats_get(pf_engine* e, pf_engine_stats* out) {
   out->saved_bytes = e->saved_bytes.load();
   out->loaded_bytes = e->loaded_bytes.load();
   out->load_failures = e->load_failures.load();
+  return PF_OK;
+}
+
+int pf_engine_enable_disk(pf_engine* e, const char* root, uint64_t quota_bytes,
+                          uint32_t max_pack_blocks, uint32_t max_prefetch_tasks,
+                          uint32_t io_threads) {
+  if (!root) return fail(PF_ERR_INVALID_ARGUMENT, "invalid argument: null disk root");
+  std::lock_guard<std::mutex> lk(e->disk_mu);
+  if (e->disk) return fail(PF_ERR_INVALID_ARGUMENT, "invalid argument: disk tier already enabled");
+  DiskConfig cfg;
+  cfg.root = root;
+  cfg.quota_bytes = quota_bytes;
+  if (max_pack_blocks) cfg.max_pack_blocks = max_pack_blocks;
+  if (max_prefetch_tasks) cfg.max_prefetch_tasks = max_prefetch_tasks;
+  if (io_threads) cfg.io_threads = io_threads;
+  if (int rc = DiskTier::open(cfg, e->store.get(), &e->disk)) return rc;
+  DiskTier* d = e->disk.get();
+  e->store->set_seal_hook(
+      [d](const std::string& k, const std::shared_ptr<SealedBlock>& b) { d->on_seal(k, b); });
+  return PF_OK;
+}
+
+int pf_engine_query_prefetch(pf_engine* e, const char* instance_id, const uint8_t* hash_data,
+                             const uint64_t* hash_offsets, uint64_t n, pf_prefetch_status* out) {
+  if (!out) return fail(PF_ERR_INVALID_ARGUMENT, "invalid argument: null output");
+  *out = pf_prefetch_status{};
+  if (!e->disk) {
+    out->state = PF_PREFETCH_READY;
+    return pf_engine_count_prefix_hit_blocks(e, instance_id, hash_data, hash_offsets, n,
+                                             &out->hit_blocks);
+  }
+  std::shared_ptr<Instance> inst;
+  if (int rc = get_instance(e, instance_id, &inst)) return rc;
+  int state = 0;
+  e->disk->query(keys_of(inst->ns, hash_data, hash_offsets, n), &state, &out->hit_blocks,
+                 &out->loading_blocks, &out->missing_blocks);
+  out->state = state;
+  return PF_OK;
+}
+
+int pf_engine_disk_flush(pf_engine* e) {
+  if (e->disk) e->disk->flush();
+  return PF_OK;
+}
+
+int pf_engine_disk_wait_prefetch(pf_engine* e) {
+  if (e->disk) e->disk->wait_prefetch();
+  return PF_OK;
+}
+
+int pf_engine_disk_stats(pf_engine* e, pf_disk_stats* out) {
+  if (!out) return fail(PF_ERR_INVALID_ARGUMENT, "invalid argument: null output");
+  *out = pf_disk_stats{};
+  if (!e->disk) return PF_OK;
+  const DiskStats s = e->disk->stats();
+  out->files = s.files;
+  out->bytes = s.bytes;
+  out->indexed_blocks = s.indexed_blocks;
+  out->offloaded_blocks = s.offloaded_blocks;
+  out->written_bytes = s.written_bytes;
+  out->prefetched_blocks = s.prefetched_blocks;
+  out->read_bytes = s.read_bytes;
+  out->pending_blocks = s.pending_blocks;
+  out->evicted_files = s.evicted_files;
+  out->failures = s.failures;
+  return PF_OK;
+}
+
+int pf_engine_read_block_slot(pf_engine* e, const char* ns, const uint8_t* hash,
+                              uint64_t hash_len, uint64_t slot, uint8_t* dst, uint64_t dst_len,
+                              uint64_t* k_bytes, uint64_t* v_bytes) {
+  if (!ns || (!hash && hash_len)) return fail(PF_ERR_INVALID_ARGUMENT, "invalid argument: null key");
+  auto sb = e->store->peek(block_key(ns, hash, static_cast<size_t>(hash_len)));
+  if (!sb)
+    return fail(PF_ERR_STORAGE, strf("storage error: block not cached (namespace=%s, hash_len=%llu)",
+                                     ns, (unsigned long long)hash_len));
+  if (slot >= sb->slots.size() || !sb->slots[slot])
+    return fail(PF_ERR_INVALID_ARGUMENT,
+                strf("invalid argument: slot %llu out of range (%zu slots)",
+                     (unsigned long long)slot, sb->slots.size()));
+  const LayerBlock& lb = *sb->slots[slot];
+  const uint64_t k = lb.v_ptr ? lb.size / 2 : lb.size, v = lb.v_ptr ? lb.size / 2 : 0;
+  if (k_bytes) *k_bytes = k;
+  if (v_bytes) *v_bytes = v;
+  if (!dst) return PF_OK;
+  if (dst_len < k + v)
+    return fail(PF_ERR_INVALID_ARGUMENT,
+                strf("invalid argument: slot holds %llu bytes, buffer %llu",
+                     (unsigned long long)(k + v), (unsigned long long)dst_len));
+  std::memcpy(dst, lb.k_ptr, k);
+  if (v) std::memcpy(dst + k, lb.v_ptr, v);
   return PF_OK;
 }
 

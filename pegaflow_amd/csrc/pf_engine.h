@@ -3,9 +3,11 @@
 // pegaflow-core/src/{allocator,pinned_pool,storage,gpu_worker,lib}.rs).
 #pragma once
 
+#include <atomic>
 #include <condition_variable>
 #include <cstdint>
 #include <deque>
+#include <functional>
 #include <list>
 #include <map>
 #include <memory>
@@ -115,7 +117,16 @@ struct InflightBlock {
 
 class BlockStore {
  public:
+  using SealHook = std::function<void(const std::string&, const std::shared_ptr<SealedBlock>&)>;
   explicit BlockStore(std::shared_ptr<PinnedPool> pool) : pool_(std::move(pool)) {}
+  // Called once per block as it seals (the seal notification of
+  // storage.rs:495-504), outside the store's locks.  Set before any save.
+  void set_seal_hook(SealHook h) { seal_hook_ = std::move(h); }
+  // Inserts an already complete block (read back from disk) as the most
+  // recently used entry; false when the key is present already.
+  bool cache_insert(const std::string& key, std::shared_ptr<SealedBlock> block);
+  // A sealed block without touching its recency (inspection).
+  std::shared_ptr<SealedBlock> peek(const std::string& key);
   // Allocation with eviction of least-recently-used sealed blocks in batches
   // of 64 until the largest free region fits (storage.rs:405-433).
   std::shared_ptr<PoolAllocation> allocate(uint64_t size);
@@ -145,7 +156,108 @@ class BlockStore {
   };
   std::unordered_map<std::string, Entry> cache_;
   uint64_t evictions_ = 0;
+  SealHook seal_hook_;
   size_t evict_lru(size_t max_blocks);
+};
+
+// ---------------------------------------------------------------------------
+// Disk tier (seal_offload.rs): sealed blocks are written in batches to packed
+// files "<root>/<namespace>/<uuid>.bin" — per block, per slot, the K half
+// then the V half (or the whole slot when contiguous) — and read back into
+// the pinned pool when a prefix query misses.  The reference indexes blocks
+// in Redis; here each packed file has a sidecar "<uuid>.json" listing its
+// blocks with the reference's BlockMeta JSON, and the index is rebuilt from
+// the sidecars when a tier opens an existing root.
+// ---------------------------------------------------------------------------
+struct DiskSlotMeta {
+  bool is_split = false;
+  uint64_t size = 0;  // K + V bytes of the slot
+};
+
+struct DiskBlockMeta {  // BlockMeta, seal_offload.rs:80-97
+  std::string file;     // "<uuid>.bin"
+  uint64_t offset = 0;  // byte offset of the block inside the file
+  std::vector<DiskSlotMeta> slots;
+  uint64_t total_slots = 0;
+  uint64_t total_size() const {
+    uint64_t s = 0;
+    for (const auto& m : slots) s += m.size;
+    return s;
+  }
+};
+
+// serde_json's compact rendering of BlockMeta.
+std::string block_meta_json(const DiskBlockMeta& m);
+
+struct DiskConfig {
+  std::string root;
+  uint64_t quota_bytes = 50ull << 30;
+  size_t max_pack_blocks = 64;   // seal_offload.rs:61-67
+  size_t max_prefetch_tasks = 16;
+  size_t io_threads = 4;
+};
+
+struct DiskStats {
+  uint64_t files = 0, bytes = 0, indexed_blocks = 0;
+  uint64_t offloaded_blocks = 0, written_bytes = 0;
+  uint64_t prefetched_blocks = 0, read_bytes = 0;
+  uint64_t pending_blocks = 0, evicted_files = 0, failures = 0;
+};
+
+enum PrefetchState : int { kPrefetchReady = 0, kPrefetchLoading = 1, kPrefetchPartialMiss = 2 };
+
+class DiskTier {
+ public:
+  static int open(const DiskConfig& cfg, BlockStore* store, std::unique_ptr<DiskTier>* out);
+  ~DiskTier();
+  // Seal notification: queue the block for the writer thread.
+  void on_seal(const std::string& key, const std::shared_ptr<SealedBlock>& block);
+  // count_prefix_hit_blocks_async (lib.rs:855-941): cache hits, then blocks
+  // being read, then — when the first miss is on disk — a background read of
+  // the rest of the prefix.
+  void query(const std::vector<std::string>& keys, int* state, uint64_t* ready,
+             uint64_t* loading, uint64_t* missing);
+  void flush();          // returns when every queued block is on disk
+  void wait_prefetch();  // returns when no read is in flight
+  DiskStats stats();
+  static std::string dir_name(const std::string& ns);
+
+ private:
+  struct FileEntry {
+    std::string ns_dir, uuid;
+    std::vector<std::string> keys;
+    uint64_t size = 0, seq = 0;
+  };
+  struct ReadJob {
+    std::string path;
+    std::vector<std::pair<std::string, DiskBlockMeta>> blocks;
+    std::shared_ptr<std::atomic<size_t>> parts_left;
+  };
+  DiskConfig cfg_;
+  BlockStore* store_ = nullptr;
+  std::mutex mu_;  // index, files, pending, queues
+  std::condition_variable cv_, idle_cv_;
+  std::unordered_map<std::string, DiskBlockMeta> index_;
+  std::map<std::string, FileEntry> files_;  // uuid -> entry
+  std::map<uint64_t, std::string> by_age_;  // seq -> uuid
+  uint64_t next_seq_ = 0, usage_ = 0;
+  std::deque<std::pair<std::string, std::weak_ptr<SealedBlock>>> write_q_;
+  size_t writing_ = 0;
+  std::unordered_map<std::string, int> pending_;
+  std::deque<ReadJob> read_q_;
+  size_t active_tasks_ = 0, reading_ = 0;
+  bool stop_ = false;
+  DiskStats st_;
+  std::thread writer_;
+  std::vector<std::thread> readers_;
+
+  void rescan();
+  void writer_loop();
+  void reader_loop();
+  int write_packed(const std::string& ns_dir,
+                   const std::vector<std::pair<std::string, std::shared_ptr<SealedBlock>>>& blocks);
+  void enforce_quota_locked();
+  void read_job(ReadJob& job);
 };
 
 }  // namespace pf

@@ -16,9 +16,11 @@ from typing import Iterable, Sequence
 import numpy as np
 
 from . import _lib
-from ._lib import EngineStats, PegaFlowError, SaveLayer
+from ._lib import DiskStats, EngineStats, PegaFlowError, PrefetchStatus, SaveLayer
 
 DEFAULT_PINNED_POOL_BYTES = 30 * 1024 * 1024 * 1024  # lib.rs:56
+DEFAULT_DISK_QUOTA_BYTES = 50 * 1024 * 1024 * 1024  # pegaflow-server/src/lib.rs:106-108
+PREFETCH_STATE_NAMES = {0: "ready", 1: "loading", 2: "partial_miss"}
 
 
 def lib():
@@ -159,6 +161,54 @@ class PegaEngine:
         _raise(lib().pf_engine_batch_load(
             self._h, instance_id.encode(), tp_rank, device_id, load_state_shm.encode(), c_names,
             len(names), ids.ctypes.data, data.ctypes.data, offs.ctypes.data, len(ids)))
+
+    # -- disk tier (seal_offload.rs) -------------------------------------
+    def enable_disk(self, root: str, quota_bytes: int = DEFAULT_DISK_QUOTA_BYTES,
+                    max_pack_blocks: int = 64, max_prefetch_tasks: int = 16,
+                    io_threads: int = 4) -> None:
+        """Write every block sealed from now on to packed files under
+        ``root`` (and index the files already there).  Call before saving."""
+        _raise(lib().pf_engine_enable_disk(self._h, str(root).encode(), quota_bytes,
+                                           max_pack_blocks, max_prefetch_tasks, io_threads))
+
+    def count_prefix_hit_blocks_with_prefetch(self, instance_id: str,
+                                              block_hashes: Sequence[bytes]) -> dict:
+        """count_prefix_hit_blocks_async (lib.rs:855-941): {prefetch_state,
+        hit_blocks, loading_blocks, missing_blocks}; a miss that is on disk
+        starts reading the rest of the prefix into the pinned pool."""
+        data, offs = _hashes(block_hashes)
+        out = PrefetchStatus()
+        _raise(lib().pf_engine_query_prefetch(self._h, instance_id.encode(), data.ctypes.data,
+                                              offs.ctypes.data, len(offs) - 1, ctypes.byref(out)))
+        return {"prefetch_state": PREFETCH_STATE_NAMES[out.state], "state": out.state,
+                "hit_blocks": out.hit_blocks, "loading_blocks": out.loading_blocks,
+                "missing_blocks": out.missing_blocks}
+
+    def flush_disk(self) -> None:
+        """Returns when every block queued for the disk is written."""
+        _raise(lib().pf_engine_disk_flush(self._h))
+
+    def wait_prefetch(self) -> None:
+        """Returns when no disk read is in flight."""
+        _raise(lib().pf_engine_disk_wait_prefetch(self._h))
+
+    def disk_stats(self) -> dict:
+        s = DiskStats()
+        _raise(lib().pf_engine_disk_stats(self._h, ctypes.byref(s)))
+        return {name: getattr(s, name) for name, _ in DiskStats._fields_}
+
+    def read_block_slot(self, namespace: str, block_hash: bytes, slot: int) -> tuple[bytes, bytes]:
+        """(K bytes, V bytes) of one slot of a cached block (V empty when the
+        slot is contiguous)."""
+        h = bytes(block_hash)
+        k, v = ctypes.c_uint64(), ctypes.c_uint64()
+        _raise(lib().pf_engine_read_block_slot(self._h, namespace.encode(), h, len(h), slot,
+                                               None, 0, ctypes.byref(k), ctypes.byref(v)))
+        buf = ctypes.create_string_buffer(k.value + v.value or 1)
+        _raise(lib().pf_engine_read_block_slot(self._h, namespace.encode(), h, len(h), slot, buf,
+                                               len(buf), ctypes.byref(k), ctypes.byref(v)))
+        raw = buf.raw
+        return raw[:k.value], raw[k.value:k.value + v.value]
 
     def stats(self) -> dict:
         s = EngineStats()

@@ -3,7 +3,9 @@
 Mirrors pegaflow-server/src/service.rs:19-405 (RPC semantics and the mapping
 of engine errors to gRPC codes, service.rs:77-88), registry.rs:41-176 (layer
 tensors held per (instance, tp_rank, device), dropped on UnregisterContext)
-and the subset of the CLI (lib.rs:38-113) that concerns this path.
+and the subset of the CLI (lib.rs:38-113) that concerns this path; the disk
+tier's --dfs-root / --dfs-quota (lib.rs:98-112) turn it on directly, since
+its index needs no Redis.
 
 Run: python -m pegaflow_amd.rpc.server --addr 127.0.0.1:50055 --device 0 --pool-size 30gb
 """
@@ -108,8 +110,9 @@ def _ok():
 class EngineService:
     """service.rs:133-405."""
 
-    def __init__(self, engine: PegaEngine):
+    def __init__(self, engine: PegaEngine, disk: bool = False):
         self.engine = engine
+        self.disk = disk  # Query is prefetch-aware when the engine has a disk tier
         self.registry = TensorRegistry()
         self.shutdown_event = threading.Event()
 
@@ -152,7 +155,16 @@ class EngineService:
         return proto.LoadResponse(status=_ok())
 
     def Query(self, req, context):
+        """service.rs:258-330: with a disk tier, a miss that is on disk starts
+        a read into the pinned pool and is reported as loading."""
         try:
+            if self.disk:
+                q = self.engine.count_prefix_hit_blocks_with_prefetch(req.instance_id,
+                                                                      list(req.block_hashes))
+                return proto.QueryResponse(status=_ok(), hit_blocks=q["hit_blocks"],
+                                           prefetch_state=q["state"],
+                                           loading_blocks=q["loading_blocks"],
+                                           missing_blocks=q["missing_blocks"])
             hits = self.engine.count_prefix_hit_blocks(req.instance_id, list(req.block_hashes))
         except Exception as e:
             self._abort(context, e)
@@ -199,10 +211,13 @@ class Server:
 
     def __init__(self, addr: str = "127.0.0.1:50055", engine: PegaEngine | None = None,
                  pool_size: int = 30 << 30, host_pool: bool = False, unit_size_hint: int = 0,
-                 max_workers: int = 16):
+                 max_workers: int = 16, dfs_root: str | None = None,
+                 dfs_quota: int = 50 << 30, dfs_io_threads: int = 4):
         self.engine = engine or PegaEngine(pool_size=pool_size, host_pool=host_pool,
                                            unit_size_hint=unit_size_hint)
-        self.service = EngineService(self.engine)
+        if dfs_root:
+            self.engine.enable_disk(dfs_root, quota_bytes=dfs_quota, io_threads=dfs_io_threads)
+        self.service = EngineService(self.engine, disk=bool(dfs_root))
         self.grpc = grpc.server(futures.ThreadPoolExecutor(max_workers=max_workers),
                                 options=[("grpc.max_receive_message_length", 256 << 20),
                                          ("grpc.max_send_message_length", 256 << 20)])
@@ -238,13 +253,18 @@ def main(argv=None) -> int:
                     help="allocation unit of the pinned pool")
     ap.add_argument("--log-level", default="info")
     ap.add_argument("--max-workers", type=int, default=16)
+    ap.add_argument("--dfs-root", default=None,
+                    help="directory of the disk tier (packed block files); off when absent")
+    ap.add_argument("--dfs-quota", type=parse_memory_size, default=parse_memory_size("50gb"))
+    ap.add_argument("--dfs-io-threads", type=int, default=4)
     args = ap.parse_args(argv)
     logging.basicConfig(level=getattr(logging, args.log_level.upper(), logging.INFO),
                         format="%(asctime)s %(levelname)s %(name)s: %(message)s")
     from .. import runtime
     runtime.init(args.device)
     server = Server(args.addr, pool_size=args.pool_size, unit_size_hint=args.hint_value_size,
-                    max_workers=args.max_workers).start()
+                    max_workers=args.max_workers, dfs_root=args.dfs_root,
+                    dfs_quota=args.dfs_quota, dfs_io_threads=args.dfs_io_threads).start()
     for sig in (signal.SIGINT, signal.SIGTERM):
         signal.signal(sig, lambda *_: server.service.shutdown_event.set())
     print(f"READY {server.addr}", flush=True)

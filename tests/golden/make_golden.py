@@ -18,6 +18,12 @@ Fixtures:
   gpt2_config1.json — the GPT-2-shape workload (12 layers, [2,512,16,12,64]
                       fp16, 64 saved blocks, 64 load targets): block ids and
                       SHA-256 digests of every host region and restored layer.
+  packed_tiny.npz   — packed block files of the disk tier (seal_offload.rs:
+                      379-448): 2 layers x tp 2 KV-first fp16 [2, 8, 2, 2, 4]
+                      layers (4 split slots) and 1 blocks-first layer (one
+                      contiguous slot); the file is the array
+                      [block, slot, K|V, bytes] flattened, with each block's
+                      BlockMeta JSON.
 
 Run: python tests/golden/make_golden.py
 """
@@ -157,8 +163,45 @@ def make_gpt2():
         json.dump(rec, f, indent=1)
 
 
+def make_packed():
+    out = {}
+    # Split: 2 layers x tp 2, slot = layer * 2 + rank; blocks in seal order.
+    nb, bpb, layers, tp = 8, 32, 2, 2
+    kv_stride, size = nb * bpb, 2 * nb * bpb
+    ids = [5, 2, 7]
+    slots = []
+    for l in range(layers):
+        for r in range(tp):
+            buf = random_bytes(size, layer_seed(23 + r, l))
+            out[f"split_input_{l}_{r}"] = buf
+            slots.append(segment_view(buf, nb, bpb, kv_stride, 2))  # [K|V, block, bpb]
+    arr = np.stack([np.stack([sv[:, b, :] for sv in slots]) for b in ids])  # [b, slot, 2, bpb]
+    out["split_ids"] = np.array(ids, np.int32)
+    out["split_file"] = arr.reshape(-1).copy()
+    blk = 2 * bpb * len(slots)
+    out["split_offsets"] = np.arange(len(ids), dtype=np.uint64) * blk
+    out["split_meta"] = np.array([json.dumps(
+        {"file": "00000000-0000-4000-8000-000000000001.bin", "offset": int(o),
+         "slots": [{"is_split": True, "size": 2 * bpb} for _ in slots],
+         "total_slots": len(slots)}, separators=(",", ":")) for o in out["split_offsets"]])
+    # Contiguous: 1 layer, tp 1, blocks-first [6, 64 B].
+    nb, bpb = 6, 64
+    buf = random_bytes(nb * bpb, layer_seed(29, 0))
+    out["contig_input"] = buf
+    ids = [4, 0]
+    out["contig_ids"] = np.array(ids, np.int32)
+    out["contig_file"] = buf.reshape(nb, bpb)[ids].reshape(-1).copy()
+    out["contig_offsets"] = np.arange(len(ids), dtype=np.uint64) * bpb
+    out["contig_meta"] = np.array([json.dumps(
+        {"file": "00000000-0000-4000-8000-000000000002.bin", "offset": int(o),
+         "slots": [{"is_split": False, "size": bpb}], "total_slots": 1},
+        separators=(",", ":")) for o in out["contig_offsets"]])
+    np.savez(os.path.join(HERE, "packed_tiny.npz"), **out)
+
+
 if __name__ == "__main__":
     make_tiny_kvfirst()
     make_tiny_blocks()
     make_gpt2()
+    make_packed()
     print("wrote fixtures to", HERE)
