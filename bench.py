@@ -295,6 +295,60 @@ def fs_type(path):
     return kind
 
 
+def leg_engine(layers, ids, targets, P, reps=4):
+    """The same prefix saved and restored through PegaEngine (by hash, with
+    block-store bookkeeping and a LoadState) instead of the bare transfer
+    context: what a vLLM connector sees."""
+    import hashlib
+
+    from pegaflow_amd import workload as wl
+    from pegaflow_amd.engine import PegaEngine
+    from pegaflow_amd.load_state import PyLoadState
+
+    shape = layers.shape
+    names = [f"layer.{l}" for l in range(len(layers.bufs))]
+    ids_l, targets_l = [int(i) for i in ids], [int(t) for t in targets]
+    e = PegaEngine(pool_size=(reps + 1) * P + (256 << 20))
+    for name, buf in zip(names, layers.bufs):
+        e.register_context_layer("bench", "llama3-8b", 0, name, buf.ptr, shape.layer_bytes,
+                                 shape.num_blocks, shape.bytes_per_block, shape.kv_stride_bytes,
+                                 shape.segments, 0, 1, len(names))
+    layers.refill()
+    save_s, load_s = [], []
+    hashes = None
+    for r in range(reps + 1):  # every save uses new hashes: nothing is deduplicated
+        hashes = [hashlib.sha256(b"engine%d-" % r + int(i).to_bytes(8, "little")).digest()
+                  for i in ids_l]
+        t0 = time.perf_counter()
+        e.batch_save_kv_blocks("bench", 0, 0, [(n, ids_l, hashes) for n in names])
+        save_s.append(time.perf_counter() - t0)
+    bad = 0
+    for r in range(reps + 1):
+        st = PyLoadState(num_layers=len(names))
+        t0 = time.perf_counter()
+        e.batch_load_kv_blocks("bench", 0, 0, st.shm_name(), names, targets_l, hashes)
+        while not st.is_ready():
+            if time.perf_counter() - t0 > 60:
+                raise RuntimeError("engine restore did not complete within 60 s")
+            time.sleep(0.0001)
+        load_s.append(time.perf_counter() - t0)
+        bad += st.get_state() != 1
+    bad += wl.verify_restored(layers, ids, targets)
+    stats = e.stats()
+    e.close()
+    return {
+        "what": "the llama prefix through PegaEngine: save by hash (new hashes each time) and "
+                "load by hash with a layered LoadState, median of the warm calls",
+        "save_gbps": round(P / statistics.median(save_s[1:]) / 1e9, 3),
+        "restore_gbps": round(P / statistics.median(load_s[1:]) / 1e9, 3),
+        "first_save_gbps": round(P / save_s[0] / 1e9, 3),
+        "save_ms": [round(t * 1e3, 2) for t in save_s],
+        "restore_ms": [round(t * 1e3, 2) for t in load_s],
+        "sealed_blocks": stats["sealed_blocks"],
+        "bit_exact": bad == 0,
+    }
+
+
 def leg_disk(layers, ids, targets, P):
     """Disk tier (seal_offload.rs) on the Llama prefix: the engine saves the
     prefix into its pinned pool and writes it to packed files (fsync'd, then
@@ -657,6 +711,9 @@ def main():
         extra["mla_latent"] = leg_mla(xfer, args.seed)
         log("[bench] config 4: fragmentation sweep")
         extra["fragmentation_llama3_8b"] = leg_fragmentation(layers, xfer, args.seed)
+        log("[bench] engine: save and restore by hash")
+        extra["engine_llama3_8b"] = leg_engine(layers, ids, targets, P)
+        log(f"[bench] {extra['engine_llama3_8b']}")
         log("[bench] disk tier: offload, cold prefetch, restore")
         extra["disk_tier_llama3_8b"] = leg_disk(layers, ids, targets, P)
         log(f"[bench] {extra['disk_tier_llama3_8b']}")

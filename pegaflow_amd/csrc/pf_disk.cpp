@@ -437,7 +437,8 @@ DiskTier::~DiskTier() {
       for (auto& b : job.blocks) pending_.erase(b.first);
     read_q_.clear();
   }
-  cv_.notify_all();
+  write_cv_.notify_all();
+  read_cv_.notify_all();
   if (writer_.joinable()) writer_.join();  // the writer drains its queue first
   for (auto& t : readers_)
     if (t.joinable()) t.join();
@@ -522,7 +523,7 @@ void DiskTier::on_seal(const std::string& key, const std::shared_ptr<SealedBlock
     if (stop_ || index_.count(key)) return;  // already on disk
     write_q_.emplace_back(key, block);
   }
-  cv_.notify_all();
+  write_cv_.notify_one();
 }
 
 void DiskTier::writer_loop() {
@@ -530,7 +531,7 @@ void DiskTier::writer_loop() {
     std::vector<std::pair<std::string, std::weak_ptr<SealedBlock>>> batch;
     {
       std::unique_lock<std::mutex> lk(mu_);
-      cv_.wait(lk, [this] { return stop_ || !write_q_.empty(); });
+      write_cv_.wait(lk, [this] { return stop_ || !write_q_.empty(); });
       if (write_q_.empty()) return;  // stopping, and drained
       while (!write_q_.empty() && batch.size() < cfg_.max_pack_blocks) {
         batch.push_back(std::move(write_q_.front()));
@@ -715,7 +716,7 @@ void DiskTier::query(const std::vector<std::string>& keys, int* state, uint64_t*
   *ready = r;
   *loading = l + (n - miss);
   lk.unlock();
-  cv_.notify_all();
+  read_cv_.notify_all();
 }
 
 void DiskTier::reader_loop() {
@@ -723,7 +724,7 @@ void DiskTier::reader_loop() {
     ReadJob job;
     {
       std::unique_lock<std::mutex> lk(mu_);
-      cv_.wait(lk, [this] { return stop_ || !read_q_.empty(); });
+      read_cv_.wait(lk, [this] { return stop_ || !read_q_.empty(); });
       if (stop_ || read_q_.empty()) {
         if (stop_) return;
         continue;

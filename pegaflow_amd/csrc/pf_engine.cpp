@@ -222,57 +222,78 @@ bool BlockStore::cache_contains(const std::string& key) {
   return cache_.count(key) != 0;
 }
 
-bool BlockStore::inflight_has_slot(const std::string& key, size_t slot) {
+void BlockStore::filter_new(const std::vector<const std::string*>& keys, size_t slot,
+                            std::vector<char>* keep) {
+  keep->assign(keys.size(), 1);
+  {
+    std::lock_guard<std::mutex> lk(cache_mu_);
+    for (size_t i = 0; i < keys.size(); ++i)
+      if (cache_.count(*keys[i])) (*keep)[i] = 0;
+  }
   std::lock_guard<std::mutex> lk(inflight_mu_);
-  auto it = inflight_.find(key);
-  return it != inflight_.end() && slot < it->second.slots.size() && it->second.slots[slot];
+  for (size_t i = 0; i < keys.size(); ++i) {
+    if (!(*keep)[i]) continue;
+    auto it = inflight_.find(*keys[i]);
+    if (it != inflight_.end() && slot < it->second.slots.size() && it->second.slots[slot])
+      (*keep)[i] = 0;
+  }
 }
 
-int BlockStore::insert_slot(const std::string& key, size_t slot, std::shared_ptr<LayerBlock> block,
-                            size_t total_slots, bool* inserted) {
-  *inserted = false;
-  if (cache_contains(key)) return PF_OK;
-  std::shared_ptr<SealedBlock> sealed;
+int BlockStore::insert_slots(const std::vector<const std::string*>& keys, size_t slot,
+                             const std::vector<std::shared_ptr<LayerBlock>>& blocks,
+                             size_t total_slots) {
+  std::vector<char> sealed_already(keys.size(), 0);
+  {
+    std::lock_guard<std::mutex> lk(cache_mu_);
+    for (size_t i = 0; i < keys.size(); ++i) sealed_already[i] = cache_.count(*keys[i]) != 0;
+  }
+  std::vector<std::pair<const std::string*, std::shared_ptr<SealedBlock>>> sealed;
   {
     std::lock_guard<std::mutex> lk(inflight_mu_);
-    auto it = inflight_.find(key);
-    if (it == inflight_.end()) {
-      InflightBlock ib;
-      ib.slots.resize(total_slots);
-      ib.remaining = total_slots;
-      it = inflight_.emplace(key, std::move(ib)).first;
-    }
-    InflightBlock& ib = it->second;
-    if (slot < ib.slots.size() && ib.slots[slot]) return PF_OK;
-    if (total_slots != ib.slots.size())
-      return fail(PF_ERR_STORAGE, strf("slot count mismatch: expected %zu, got %zu",
-                                       ib.slots.size(), total_slots));
-    if (slot >= ib.slots.size())
-      return fail(PF_ERR_STORAGE,
-                  strf("slot_id %zu out of bounds (%zu slots)", slot, ib.slots.size()));
-    ib.footprint += block->size;
-    ib.slots[slot] = std::move(block);
-    ib.remaining -= 1;
-    if (ib.remaining == 0) {
-      sealed = std::make_shared<SealedBlock>();
-      sealed->slots = std::move(ib.slots);
-      sealed->footprint = ib.footprint;
-      inflight_.erase(it);
-    }
-  }
-  if (sealed) {
-    bool fresh = false;
-    {
-      std::lock_guard<std::mutex> lk(cache_mu_);
-      if (!cache_.count(key)) {
-        lru_.push_front(key);
-        cache_[key] = Entry{sealed, lru_.begin()};
-        fresh = true;
+    for (size_t i = 0; i < keys.size(); ++i) {
+      if (sealed_already[i]) continue;
+      const std::string& key = *keys[i];
+      auto it = inflight_.find(key);
+      if (it == inflight_.end()) {
+        InflightBlock ib;
+        ib.slots.resize(total_slots);
+        ib.remaining = total_slots;
+        it = inflight_.emplace(key, std::move(ib)).first;
+      }
+      InflightBlock& ib = it->second;
+      if (slot < ib.slots.size() && ib.slots[slot]) continue;
+      if (total_slots != ib.slots.size())
+        return fail(PF_ERR_STORAGE, strf("slot count mismatch: expected %zu, got %zu",
+                                         ib.slots.size(), total_slots));
+      if (slot >= ib.slots.size())
+        return fail(PF_ERR_STORAGE,
+                    strf("slot_id %zu out of bounds (%zu slots)", slot, ib.slots.size()));
+      ib.footprint += blocks[i]->size;
+      ib.slots[slot] = blocks[i];
+      if (--ib.remaining == 0) {
+        auto sb = std::make_shared<SealedBlock>();
+        sb->slots = std::move(ib.slots);
+        sb->footprint = ib.footprint;
+        sealed.emplace_back(&key, std::move(sb));
+        inflight_.erase(it);
       }
     }
-    if (fresh && seal_hook_) seal_hook_(key, sealed);
   }
-  *inserted = true;
+  if (sealed.empty()) return PF_OK;
+  std::vector<char> fresh(sealed.size(), 0);
+  {
+    std::lock_guard<std::mutex> lk(cache_mu_);
+    for (size_t i = 0; i < sealed.size(); ++i) {
+      const std::string& key = *sealed[i].first;
+      if (cache_.count(key)) continue;
+      lru_.push_front(key);
+      cache_[key] = Entry{sealed[i].second, lru_.begin()};
+      fresh[i] = 1;
+    }
+  }
+  if (seal_hook_)
+    for (size_t i = 0; i < sealed.size(); ++i)
+      if (fresh[i]) seal_hook_(*sealed[i].first, sealed[i].second);
   return PF_OK;
 }
 
@@ -583,10 +604,16 @@ std::vector<std::string> keys_of(const std::string& ns, const uint8_t* data, con
 struct SavePlan {
   size_t slot = 0;
   pf_kv_layout layout{};
-  std::vector<std::string> keys;  // kept hashes, in order
+  std::vector<const std::string*> keys;  // kept hashes, in order
   std::vector<pf_block_xfer> blocks;
   std::shared_ptr<PoolAllocation> k_alloc, v_alloc;
   bool split = false;
+};
+
+// The LayerBlocks of one planned layer, in one allocation; each block's
+// handle shares the owner's reference count.
+struct LayerBlockSet {
+  std::vector<LayerBlock> blocks;
 };
 
 }  // namespace
@@ -792,6 +819,27 @@ int pf_engine_batch_save(pf_engine* e, const char* instance_id, uint64_t tp_rank
   const size_t total_slots = inst->num_layers * inst->tp_size;
   std::vector<SavePlan> plans;
   plans.reserve(num_layers);
+  // Keys are built once per distinct hash list: the layers of a batch
+  // normally pass the same one.
+  struct KeyList {
+    const uint8_t* data;
+    const uint64_t* offs;
+    uint64_t n;
+    std::vector<std::string> keys;
+  };
+  std::vector<std::unique_ptr<KeyList>> key_lists;
+  auto keys_for = [&](const pf_save_layer& sl) -> const std::vector<std::string>& {
+    for (auto& kl : key_lists)
+      if (kl->data == sl.hash_data && kl->offs == sl.hash_offsets && kl->n == sl.num_blocks)
+        return kl->keys;
+    key_lists.emplace_back(new KeyList{sl.hash_data, sl.hash_offsets, sl.num_blocks,
+                                       keys_of(inst->ns, sl.hash_data, sl.hash_offsets,
+                                               sl.num_blocks)});
+    return key_lists.back()->keys;
+  };
+  std::vector<const std::string*> cand;
+  std::vector<int64_t> cand_ids;
+  std::vector<char> keep;
   for (uint32_t li = 0; li < num_layers; ++li) {
     const pf_save_layer& sl = layers[li];
     const std::string name(sl.layer_name);
@@ -811,7 +859,9 @@ int pf_engine_batch_save(pf_engine* e, const char* instance_id, uint64_t tp_rank
     if (int rc = inst->slot_index(layer_id, tp_rank, &plan.slot)) return rc;
     plan.layout = reg;
     // Filtering and dedup (lib.rs:590-621).
-    std::vector<int64_t> idx;
+    const std::vector<std::string>& keys = keys_for(sl);
+    cand.clear();
+    cand_ids.clear();
     for (uint64_t i = 0; i < sl.num_blocks; ++i) {
       const int32_t id = sl.block_ids[i];
       if (id < 0) continue;
@@ -820,12 +870,17 @@ int pf_engine_batch_save(pf_engine* e, const char* instance_id, uint64_t tp_rank
                     strf("invalid argument: block %d out of range for layer %s (%llu blocks "
                          "registered)",
                          id, name.c_str(), (unsigned long long)reg.num_blocks));
-      std::string key = block_key(inst->ns, sl.hash_data + sl.hash_offsets[i],
-                                  static_cast<size_t>(sl.hash_offsets[i + 1] - sl.hash_offsets[i]));
-      if (e->store->cache_contains(key) || e->store->inflight_has_slot(key, plan.slot)) continue;
-      idx.push_back(id);
-      plan.keys.push_back(std::move(key));
+      cand.push_back(&keys[i]);
+      cand_ids.push_back(id);
     }
+    e->store->filter_new(cand, plan.slot, &keep);
+    std::vector<int64_t> idx;
+    idx.reserve(cand.size());
+    for (size_t i = 0; i < cand.size(); ++i)
+      if (keep[i]) {
+        idx.push_back(cand_ids[i]);
+        plan.keys.push_back(cand[i]);
+      }
     if (idx.empty()) continue;
     const uint64_t n = idx.size();
     plan.split = reg.segments == 2 && reg.kv_stride_bytes > reg.bytes_per_block;
@@ -856,30 +911,40 @@ int pf_engine_batch_save(pf_engine* e, const char* instance_id, uint64_t tp_rank
     plans.push_back(std::move(plan));
   }
   if (plans.empty()) return PF_OK;
+  // The LayerBlocks, one allocation per layer, ready before the copy.
+  std::vector<std::vector<std::shared_ptr<LayerBlock>>> handles(plans.size());
+  for (size_t pi = 0; pi < plans.size(); ++pi) {
+    const SavePlan& p = plans[pi];
+    const uint64_t seg = p.layout.bytes_per_block, bs = p.layout.block_size_bytes;
+    auto set = std::make_shared<LayerBlockSet>();
+    set->blocks.resize(p.keys.size());
+    for (size_t i = 0; i < p.keys.size(); ++i) {
+      LayerBlock& lb = set->blocks[i];
+      lb.size = bs;
+      lb.k_alloc = p.k_alloc;
+      if (p.split) {
+        lb.k_ptr = p.k_alloc->ptr + i * seg;
+        lb.v_ptr = p.v_alloc->ptr + i * seg;
+        lb.v_alloc = p.v_alloc;
+      } else {
+        lb.k_ptr = p.k_alloc->ptr + i * bs;
+      }
+    }
+    handles[pi].reserve(p.keys.size());
+    for (size_t i = 0; i < p.keys.size(); ++i)
+      handles[pi].emplace_back(set, &set->blocks[i]);  // aliases the set's count
+  }
   std::vector<pf_layer_xfer> xl;
   xl.reserve(plans.size());
   for (auto& p : plans) xl.push_back(pf_layer_xfer{p.layout, p.blocks.data(), p.blocks.size()});
   if (int rc = gpu->worker->save(xl, e->save_mode.load())) return rc;
-  // LayerBlocks and slot insertion once the bytes are in place (lib.rs:687-705, 755-770).
+  // Slot insertion once the bytes are in place (lib.rs:687-705, 755-770).
   uint64_t bytes = 0;
-  for (auto& p : plans) {
-    const uint64_t seg = p.layout.bytes_per_block, bs = p.layout.block_size_bytes;
-    for (size_t i = 0; i < p.keys.size(); ++i) {
-      auto lb = std::make_shared<LayerBlock>();
-      lb->size = bs;
-      lb->k_alloc = p.k_alloc;
-      if (p.split) {
-        lb->k_ptr = p.k_alloc->ptr + i * seg;
-        lb->v_ptr = p.v_alloc->ptr + i * seg;
-        lb->v_alloc = p.v_alloc;
-      } else {
-        lb->k_ptr = p.k_alloc->ptr + i * bs;
-      }
-      bool inserted = false;
-      if (int rc = e->store->insert_slot(p.keys[i], p.slot, std::move(lb), total_slots, &inserted))
-        return fail(rc, std::string("storage error: ") + pf_last_error());
-    }
-    bytes += p.keys.size() * bs;
+  for (size_t pi = 0; pi < plans.size(); ++pi) {
+    const SavePlan& p = plans[pi];
+    if (int rc = e->store->insert_slots(p.keys, p.slot, handles[pi], total_slots))
+      return fail(rc, std::string("storage error: ") + pf_last_error());
+    bytes += p.keys.size() * p.layout.block_size_bytes;
   }
   e->saved_bytes.fetch_add(bytes);
   return PF_OK;

@@ -131,11 +131,15 @@ class BlockStore {
   // of 64 until the largest free region fits (storage.rs:405-433).
   std::shared_ptr<PoolAllocation> allocate(uint64_t size);
   bool cache_contains(const std::string& key);
-  bool inflight_has_slot(const std::string& key, size_t slot);
-  // storage.rs:457-514.  Returns PF_OK and *inserted (false when sealed
-  // already or the slot exists); errors on slot count mismatch / range.
-  int insert_slot(const std::string& key, size_t slot, std::shared_ptr<LayerBlock> block,
-                  size_t total_slots, bool* inserted);
+  // One layer of a save, each lock taken once: keep[i] = 0 when keys[i] is
+  // sealed already or its slot is inflight (lib.rs:590-621).
+  void filter_new(const std::vector<const std::string*>& keys, size_t slot,
+                  std::vector<char>* keep);
+  // storage.rs:457-514 for one layer: slots of sealed blocks and filled
+  // slots are skipped; a block whose last slot arrives moves to the cache
+  // and the seal hook runs for it.  Errors on slot count mismatch / range.
+  int insert_slots(const std::vector<const std::string*>& keys, size_t slot,
+                   const std::vector<std::shared_ptr<LayerBlock>>& blocks, size_t total_slots);
   // storage.rs:529-547: every hash must be sealed; refreshes recency.
   int lookup_many(const std::vector<std::string>& keys,
                   std::vector<std::shared_ptr<SealedBlock>>* out);
@@ -236,7 +240,7 @@ class DiskTier {
   DiskConfig cfg_;
   BlockStore* store_ = nullptr;
   std::mutex mu_;  // index, files, pending, queues
-  std::condition_variable cv_, idle_cv_;
+  std::condition_variable write_cv_, read_cv_, idle_cv_;
   std::unordered_map<std::string, DiskBlockMeta> index_;
   std::map<std::string, FileEntry> files_;  // uuid -> entry
   std::map<uint64_t, std::string> by_age_;  // seq -> uuid

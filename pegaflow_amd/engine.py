@@ -33,11 +33,12 @@ def _raise(rc: int) -> None:
 
 
 def _hashes(block_hashes: Sequence[bytes]):
-    hs = [bytes(h) for h in block_hashes]
-    offs = np.zeros(len(hs) + 1, np.uint64)
-    if hs:
-        offs[1:] = np.cumsum([len(h) for h in hs])
-    data = np.frombuffer(b"".join(hs) or b"\0", np.uint8).copy()
+    """(bytes, offsets): hash i is data[offs[i]:offs[i+1]]."""
+    n = len(block_hashes)
+    offs = np.zeros(n + 1, np.uint64)
+    if n:
+        np.cumsum(np.fromiter(map(len, block_hashes), np.uint64, n), out=offs[1:])
+    data = np.frombuffer(b"".join(block_hashes) or b"\0", np.uint8)
     return data, offs
 
 
@@ -132,15 +133,26 @@ class PegaEngine:
 
     def batch_save_kv_blocks(self, instance_id: str, tp_rank: int, device_id: int,
                              saves: Iterable[tuple[str, Sequence[int], Sequence[bytes]]]) -> None:
-        """Blocking save of (layer_name, block_ids, block_hashes) per layer."""
+        """Blocking save of (layer_name, block_ids, block_hashes) per layer.
+        Lists shared by several layers (the usual case) are packed once."""
         keep, arr = [], []
+        packed_ids, packed_hashes = {}, {}
         for layer_name, block_ids, block_hashes in saves:
-            ids = np.ascontiguousarray(block_ids, dtype=np.int32)
+            ids = packed_ids.get(id(block_ids))
+            if ids is None:
+                ids = np.ascontiguousarray(block_ids, dtype=np.int32)
+                packed_ids[id(block_ids)] = ids
+                keep.append(block_ids)  # keeps id() unique for the whole call
             if len(ids) != len(block_hashes):
                 raise PegaFlowError(_lib.PF_ERR_INVALID_ARGUMENT,
                                     f"invalid argument: block_ids length {len(ids)} does not "
                                     f"match block_hashes {len(block_hashes)}")
-            data, offs = _hashes(block_hashes)
+            hp = packed_hashes.get(id(block_hashes))
+            if hp is None:
+                hp = _hashes(block_hashes)
+                packed_hashes[id(block_hashes)] = hp
+                keep.append(block_hashes)
+            data, offs = hp
             name = layer_name.encode()
             keep += [ids, data, offs, name]
             arr.append(SaveLayer(name, ids.ctypes.data, len(ids), data.ctypes.data,
