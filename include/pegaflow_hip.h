@@ -172,6 +172,15 @@ int pf_ipc_export(uint64_t dev_ptr, uint8_t* handle, uint64_t* alloc_base,
  * the mapped base address.  The range becomes valid for the kernels. */
 int pf_ipc_open(const uint8_t* handle, uint64_t alloc_size, uint64_t* base);
 int pf_ipc_close(uint64_t base);
+/* No counterpart in the reference (its per-layer wait is a no-op,
+ * worker.py:288-289): events another process can record and this one wait
+ * on, for cross-process per-layer completion on the device.  The event is
+ * created with timing disabled and the interprocess flag; its 64-byte handle
+ * is opened in the other process with pf_ipc_event_open (not in the same
+ * process).  Destroy both with pf_event_destroy. */
+int pf_event_create_ipc(pf_event* out);
+int pf_ipc_event_export(pf_event event, uint8_t* handle);
+int pf_ipc_event_open(const uint8_t* handle, pf_event* out);
 
 /* ------------------------------------------------------------------------ */
 /* Reference-equivalent DMA primitives (transfer.rs:56-239).                  */
@@ -365,6 +374,22 @@ void pf_load_state_set_error(pf_load_state* state);
 uint32_t pf_load_state_num_layers(const pf_load_state* state);
 int64_t pf_load_state_layers_done(const pf_load_state* state);
 void pf_load_state_set_layers_done(pf_load_state* state, int64_t n);
+/* Device-side per-layer completion across processes (no counterpart in the
+ * reference).  A layered state created with one interprocess event handle
+ * per layer (num_layers x PF_IPC_HANDLE_BYTES) carries, after the layered
+ * extension at byte 48, {u32 magic 0x50464C45 ('PFLE'), u32 count,
+ * i64 events_recorded} and the handles.  The loader opens the handles,
+ * records layer l's event on its stream after layer l's copy, and then
+ * publishes events_recorded = count; from then on the consumer may make a
+ * stream wait on event l (waiting earlier would see no record). */
+int pf_load_state_create_layered_events(uint32_t num_layers,
+                                        const uint8_t* event_handles,
+                                        pf_load_state** out);
+/* Handles carried by a state (NULL / 0 when none). */
+const uint8_t* pf_load_state_event_handles(const pf_load_state* state,
+                                           uint32_t* count);
+int64_t pf_load_state_events_recorded(const pf_load_state* state);
+void pf_load_state_set_events_recorded(pf_load_state* state, int64_t n);
 
 /* ------------------------------------------------------------------------ */
 /* Pool allocator.  Replaces ScaledOffsetAllocator (allocator.rs:66-171):     */

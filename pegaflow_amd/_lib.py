@@ -181,6 +181,9 @@ SIGNATURES = {
     "pf_event_synchronize": (i32, [vp]),
     "pf_event_query": (i32, [vp, pi32]),
     "pf_event_elapsed_ms": (i32, [vp, vp, ctypes.POINTER(ctypes.c_float)]),
+    "pf_event_create_ipc": (i32, [pvp]),
+    "pf_ipc_event_export": (i32, [vp, vp]),
+    "pf_ipc_event_open": (i32, [vp, pvp]),
     "pf_device_malloc": (i32, [u64, pu64]),
     "pf_device_free": (i32, [u64]),
     "pf_memcpy_h2d": (i32, [u64, vp, u64]),
@@ -229,6 +232,10 @@ SIGNATURES = {
     "pf_load_state_num_layers": (u32, [vp]),
     "pf_load_state_layers_done": (i64, [vp]),
     "pf_load_state_set_layers_done": (None, [vp, i64]),
+    "pf_load_state_create_layered_events": (i32, [u32, vp, pvp]),
+    "pf_load_state_event_handles": (vp, [vp, ctypes.POINTER(ctypes.c_uint32)]),
+    "pf_load_state_events_recorded": (i64, [vp]),
+    "pf_load_state_set_events_recorded": (None, [vp, i64]),
     "pf_allocator_create": (i32, [u64, u64, pvp]),
     "pf_allocator_create_auto": (i32, [u64, pvp]),
     "pf_allocator_destroy": (i32, [vp]),

@@ -1,5 +1,5 @@
 // pf_disk.cpp — the engine's disk tier (pegaflow-core/src/seal_offload.rs):
-// packed block files written from the pinned pool by a writer thread, a
+// packed block files written from the pinned pool by writer threads, a
 // sidecar index per file (in place of Redis), a byte quota that drops the
 // oldest files, and prefetch of a missed prefix back into the pinned pool by
 // reader threads, after which loads take the ordinary restore path.
@@ -22,6 +22,7 @@
 #include <cerrno>
 #include <cstdio>
 #include <cstring>
+#include <chrono>
 #include <random>
 
 #include "pf_engine.h"
@@ -31,6 +32,7 @@ namespace {
 
 constexpr int kMaxIov = 1024;                // IOV_MAX on Linux
 constexpr uint64_t kMaxReadRun = 256ull << 20;  // bytes per preadv run
+constexpr uint64_t kReadJobBytes = 32ull << 20;  // bytes per reader job
 
 std::string to_hex(const uint8_t* p, size_t n) {
   static const char* d = "0123456789abcdef";
@@ -422,9 +424,10 @@ int DiskTier::open(const DiskConfig& cfg, BlockStore* store, std::unique_ptr<Dis
   d->cfg_ = cfg;
   d->store_ = store;
   d->rescan();
-  d->writer_ = std::thread([t = d.get()] { t->writer_loop(); });
-  for (size_t i = 0; i < cfg.io_threads; ++i)
+  for (size_t i = 0; i < cfg.io_threads; ++i) {
+    d->writers_.emplace_back([t = d.get()] { t->writer_loop(); });
     d->readers_.emplace_back([t = d.get()] { t->reader_loop(); });
+  }
   *out = std::move(d);
   return PF_OK;
 }
@@ -439,7 +442,8 @@ DiskTier::~DiskTier() {
   }
   write_cv_.notify_all();
   read_cv_.notify_all();
-  if (writer_.joinable()) writer_.join();  // the writer drains its queue first
+  for (auto& t : writers_)  // the writers drain the queue first
+    if (t.joinable()) t.join();
   for (auto& t : readers_)
     if (t.joinable()) t.join();
 }
@@ -522,8 +526,9 @@ void DiskTier::on_seal(const std::string& key, const std::shared_ptr<SealedBlock
     std::lock_guard<std::mutex> lk(mu_);
     if (stop_ || index_.count(key)) return;  // already on disk
     write_q_.emplace_back(key, block);
+    if (write_q_.size() % cfg_.max_pack_blocks != 0 && write_q_.size() != 1) return;
   }
-  write_cv_.notify_one();
+  write_cv_.notify_one();  // on the first block, and whenever a file's worth is queued
 }
 
 void DiskTier::writer_loop() {
@@ -533,6 +538,13 @@ void DiskTier::writer_loop() {
       std::unique_lock<std::mutex> lk(mu_);
       write_cv_.wait(lk, [this] { return stop_ || !write_q_.empty(); });
       if (write_q_.empty()) return;  // stopping, and drained
+      // Seals arrive in bursts (a save seals its blocks together): linger
+      // briefly so a burst fills whole files instead of a first tiny one.
+      if (!stop_ && write_q_.size() < cfg_.max_pack_blocks)
+        write_cv_.wait_for(lk, std::chrono::milliseconds(2), [this] {
+          return stop_ || write_q_.size() >= cfg_.max_pack_blocks;
+        });
+      if (write_q_.empty()) continue;  // another writer took them
       while (!write_q_.empty() && batch.size() < cfg_.max_pack_blocks) {
         batch.push_back(std::move(write_q_.front()));
         write_q_.pop_front();
@@ -705,11 +717,33 @@ void DiskTier::query(const std::vector<std::string>& keys, int* state, uint64_t*
     job.blocks.emplace_back(k, ix->second);
   }
   if (!jobs.empty()) {
-    ++active_tasks_;
-    auto parts = std::make_shared<std::atomic<size_t>>(jobs.size());
+    // Each file's blocks, in offset order, are cut into jobs of about
+    // kReadJobBytes so that every reader thread has work until the end.
+    std::vector<ReadJob> parts;
     for (auto& kv : jobs) {
-      kv.second.parts_left = parts;
-      read_q_.push_back(std::move(kv.second));
+      auto& bl = kv.second.blocks;
+      std::sort(bl.begin(), bl.end(),
+                [](const auto& a, const auto& b) { return a.second.offset < b.second.offset; });
+      ReadJob cur;
+      uint64_t bytes = 0;
+      for (auto& b : bl) {
+        if (!cur.blocks.empty() && bytes >= kReadJobBytes) {
+          cur.path = kv.second.path;
+          parts.push_back(std::move(cur));
+          cur = ReadJob();
+          bytes = 0;
+        }
+        bytes += b.second.total_size();
+        cur.blocks.push_back(std::move(b));
+      }
+      cur.path = kv.second.path;
+      parts.push_back(std::move(cur));
+    }
+    ++active_tasks_;
+    auto left = std::make_shared<std::atomic<size_t>>(parts.size());
+    for (auto& job : parts) {
+      job.parts_left = left;
+      read_q_.push_back(std::move(job));
     }
   }
   *state = kPrefetchLoading;

@@ -470,17 +470,41 @@ void DeviceWorker::load_loop() {
       }
       events_.push_back(e);
     }
+    // A consumer in another process may have put one interprocess event per
+    // layer in the LoadState: those are recorded instead of the worker's own,
+    // so the consumer's streams can wait on each layer on the device.
+    std::vector<pf_event> ipc_evs;
+    uint32_t n_handles = 0;
+    const uint8_t* handles = pf_load_state_event_handles(task.state, &n_handles);
+    if (ok && handles) {
+      if (n_handles != L) {
+        set_error(strf("storage error: LoadState carries %u layer events for %zu layers",
+                       n_handles, L));
+        ok = false;
+      }
+      for (uint32_t l = 0; ok && l < n_handles; ++l) {
+        pf_event ev = nullptr;
+        ok = pf_ipc_event_open(handles + static_cast<size_t>(l) * PF_IPC_HANDLE_BYTES, &ev) ==
+             PF_OK;
+        if (ok) ipc_evs.push_back(ev);
+      }
+    }
     if (ok && L > 0) {
       std::vector<pf_event> evs(events_.begin(), events_.begin() + L);
+      if (!ipc_evs.empty()) evs = ipc_evs;
       ok = pf_load_layers(load_x_, layers.data(), static_cast<uint32_t>(L), task.mode,
                           evs.data()) == PF_OK;
+      // Every record is on the stream now: a consumer may start waiting.
+      if (ok && !ipc_evs.empty())
+        pf_load_state_set_events_recorded(task.state, static_cast<int64_t>(L));
       // Per-layer completion: layer l is published as soon as its event fires.
       for (size_t l = 0; ok && l < L; ++l) {
-        ok = hipEventSynchronize(events_[l]) == hipSuccess;
+        ok = hipEventSynchronize(static_cast<hipEvent_t>(evs[l])) == hipSuccess;
         if (ok) pf_load_state_set_layers_done(task.state, static_cast<int64_t>(l + 1));
       }
       if (!ok) (void)pf_xfer_synchronize(load_x_);
     }
+    for (pf_event ev : ipc_evs) (void)pf_event_destroy(ev);
     if (ok) {
       pf_load_state_set_completed(task.state);
       loaded_bytes_->fetch_add(task.bytes);

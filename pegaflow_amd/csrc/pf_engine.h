@@ -198,7 +198,7 @@ struct DiskConfig {
   uint64_t quota_bytes = 50ull << 30;
   size_t max_pack_blocks = 64;   // seal_offload.rs:61-67
   size_t max_prefetch_tasks = 16;
-  size_t io_threads = 4;
+  size_t io_threads = 4;  // writer threads and, as many again, reader threads
 };
 
 struct DiskStats {
@@ -214,7 +214,7 @@ class DiskTier {
  public:
   static int open(const DiskConfig& cfg, BlockStore* store, std::unique_ptr<DiskTier>* out);
   ~DiskTier();
-  // Seal notification: queue the block for the writer thread.
+  // Seal notification: queue the block for the writer threads.
   void on_seal(const std::string& key, const std::shared_ptr<SealedBlock>& block);
   // count_prefix_hit_blocks_async (lib.rs:855-941): cache hits, then blocks
   // being read, then — when the first miss is on disk — a background read of
@@ -252,7 +252,7 @@ class DiskTier {
   size_t active_tasks_ = 0, reading_ = 0;
   bool stop_ = false;
   DiskStats st_;
-  std::thread writer_;
+  std::vector<std::thread> writers_;
   std::vector<std::thread> readers_;
 
   void rescan();

@@ -13,6 +13,11 @@
 // so the per-layer completion of a layer-wise load is visible to a process
 // that polls the shared memory, while a reader of the original record still
 // attaches (it only requires the mapping to hold at least 32 bytes).
+// Event block (optional, after the extension), at byte 48:
+//   u32 magic 0x50464C45 ('PFLE'), u32 count, i64 events_recorded, then
+//   count 64-byte interprocess event handles, one per layer; the loader
+//   records layer l's event after layer l's copy and then publishes
+//   events_recorded = count, after which a consumer can wait on the device.
 #include <fcntl.h>
 #include <sys/mman.h>
 #include <sys/stat.h>
@@ -38,6 +43,11 @@ constexpr size_t kRecordAlign = 8;
 constexpr size_t kAllocSize = kMetaSize + kRecordSize + kRecordAlign;  // 32
 constexpr size_t kExtOffset = kAllocSize;
 constexpr size_t kExtSize = 16;
+constexpr uint32_t kEvMagic = 0x50464C45u;  // 'PFLE'
+constexpr size_t kEvOffset = kExtOffset + kExtSize;  // 48
+constexpr size_t kEvSize = 16;
+constexpr size_t kHandleBytes = PF_IPC_HANDLE_BYTES;
+constexpr uint32_t kMaxEvents = 4096;
 
 struct Record {
   uint32_t magic;
@@ -52,6 +62,13 @@ struct ExtRecord {
   int64_t layers_done;
 };
 static_assert(sizeof(ExtRecord) == kExtSize, "extension layout");
+
+struct EvRecord {
+  uint32_t magic;
+  uint32_t count;
+  int64_t recorded;
+};
+static_assert(sizeof(EvRecord) == kEvSize, "event block layout");
 
 std::string random_name() {
   // "pega_load_" + uuid-v4 in simple (32 lowercase hex) form (sync_state.rs:126).
@@ -81,13 +98,19 @@ struct pf_load_state {
   bool owner = false;
   Record* rec = nullptr;
   ExtRecord* ext = nullptr;
+  EvRecord* ev = nullptr;
 };
 
 namespace {
 
-int create_state(uint32_t num_layers, bool layered, pf_load_state** out) {
+int create_state(uint32_t num_layers, bool layered, const uint8_t* handles,
+                 pf_load_state** out) {
   if (!out) return fail(PF_ERR_INVALID_ARGUMENT, "null output");
-  const size_t size = layered ? kExtOffset + kExtSize : kAllocSize;
+  if (handles && (num_layers == 0 || num_layers > kMaxEvents))
+    return fail(PF_ERR_INVALID_ARGUMENT,
+                strf("a LoadState carries 1..%u layer events, got %u", kMaxEvents, num_layers));
+  const size_t size = handles ? kEvOffset + kEvSize + num_layers * kHandleBytes
+                              : layered ? kExtOffset + kExtSize : kAllocSize;
   std::string name;
   int fd = -1;
   for (int attempt = 0; attempt < 8 && fd < 0; ++attempt) {
@@ -134,6 +157,13 @@ int create_state(uint32_t num_layers, bool layered, pf_load_state** out) {
     __atomic_store_n(&st->ext->layers_done, (int64_t)0, __ATOMIC_RELEASE);
     __atomic_store_n(&st->ext->magic, kExtMagic, __ATOMIC_RELEASE);
   }
+  if (handles) {
+    st->ev = reinterpret_cast<EvRecord*>(base + kEvOffset);
+    std::memcpy(base + kEvOffset + kEvSize, handles, num_layers * kHandleBytes);
+    __atomic_store_n(&st->ev->count, num_layers, __ATOMIC_RELEASE);
+    __atomic_store_n(&st->ev->recorded, (int64_t)0, __ATOMIC_RELEASE);
+    __atomic_store_n(&st->ev->magic, kEvMagic, __ATOMIC_RELEASE);
+  }
   *out = st;
   return PF_OK;
 }
@@ -142,10 +172,16 @@ int create_state(uint32_t num_layers, bool layered, pf_load_state** out) {
 
 extern "C" {
 
-int pf_load_state_create(pf_load_state** out) { return create_state(0, false, out); }
+int pf_load_state_create(pf_load_state** out) { return create_state(0, false, nullptr, out); }
 
 int pf_load_state_create_layered(uint32_t num_layers, pf_load_state** out) {
-  return create_state(num_layers, true, out);
+  return create_state(num_layers, true, nullptr, out);
+}
+
+int pf_load_state_create_layered_events(uint32_t num_layers, const uint8_t* event_handles,
+                                        pf_load_state** out) {
+  if (!event_handles) return fail(PF_ERR_INVALID_ARGUMENT, "null event handles");
+  return create_state(num_layers, true, event_handles, out);
 }
 
 // LoadState::attach + attach_mapping + validate_header (sync_state.rs:145-155,
@@ -212,6 +248,13 @@ int pf_load_state_attach(const char* shm_name, pf_load_state** out) {
     ExtRecord* ext = reinterpret_cast<ExtRecord*>(base + kExtOffset);
     if (__atomic_load_n(&ext->magic, __ATOMIC_ACQUIRE) == kExtMagic) st->ext = ext;
   }
+  if (st->ext && len >= kEvOffset + kEvSize) {
+    EvRecord* ev = reinterpret_cast<EvRecord*>(base + kEvOffset);
+    const uint32_t count = __atomic_load_n(&ev->count, __ATOMIC_ACQUIRE);
+    if (__atomic_load_n(&ev->magic, __ATOMIC_ACQUIRE) == kEvMagic && count > 0 &&
+        count <= kMaxEvents && len >= kEvOffset + kEvSize + count * kHandleBytes)
+      st->ev = ev;
+  }
   *out = st;
   return PF_OK;
 }
@@ -253,6 +296,23 @@ int64_t pf_load_state_layers_done(const pf_load_state* st) {
 
 void pf_load_state_set_layers_done(pf_load_state* st, int64_t n) {
   if (st->ext) __atomic_store_n(&st->ext->layers_done, n, __ATOMIC_RELEASE);
+}
+
+const uint8_t* pf_load_state_event_handles(const pf_load_state* st, uint32_t* count) {
+  if (!st->ev) {
+    if (count) *count = 0;
+    return nullptr;
+  }
+  if (count) *count = __atomic_load_n(&st->ev->count, __ATOMIC_ACQUIRE);
+  return reinterpret_cast<const uint8_t*>(st->ev) + kEvSize;
+}
+
+int64_t pf_load_state_events_recorded(const pf_load_state* st) {
+  return st->ev ? __atomic_load_n(&st->ev->recorded, __ATOMIC_ACQUIRE) : 0;
+}
+
+void pf_load_state_set_events_recorded(pf_load_state* st, int64_t n) {
+  if (st->ev) __atomic_store_n(&st->ev->recorded, n, __ATOMIC_RELEASE);
 }
 
 }  // extern "C"

@@ -408,6 +408,35 @@ int pf_ipc_close(uint64_t base) {
   return PF_OK;
 }
 
+int pf_event_create_ipc(pf_event* out) {
+  if (!out) return fail(PF_ERR_INVALID_ARGUMENT, "null output");
+  hipEvent_t e = nullptr;
+  PF_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming | hipEventInterprocess));
+  *out = e;
+  return PF_OK;
+}
+
+int pf_ipc_event_export(pf_event event, uint8_t* handle) {
+  if (!event || !handle) return fail(PF_ERR_INVALID_ARGUMENT, "null argument");
+  static_assert(sizeof(hipIpcEventHandle_t) >= PF_IPC_HANDLE_BYTES, "event handle size");
+  hipIpcEventHandle_t h;
+  std::memset(&h, 0, sizeof(h));
+  PF_HIP(hipIpcGetEventHandle(&h, static_cast<hipEvent_t>(event)));
+  std::memcpy(handle, &h, PF_IPC_HANDLE_BYTES);
+  return PF_OK;
+}
+
+int pf_ipc_event_open(const uint8_t* handle, pf_event* out) {
+  if (!handle || !out) return fail(PF_ERR_INVALID_ARGUMENT, "null argument");
+  hipIpcEventHandle_t h;
+  std::memset(&h, 0, sizeof(h));
+  std::memcpy(&h, handle, PF_IPC_HANDLE_BYTES);
+  hipEvent_t e = nullptr;
+  PF_HIP(hipIpcOpenEventHandle(&e, h));
+  *out = e;
+  return PF_OK;
+}
+
 // pinned_mem.rs:38-52: "Hugepagesize:       2048 kB" -> bytes.
 uint64_t pf_huge_page_size(void) {
   std::ifstream f("/proc/meminfo");

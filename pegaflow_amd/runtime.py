@@ -70,12 +70,35 @@ class Stream:
 
 
 class Event:
-    """A timing-capable HIP event."""
+    """A timing-capable HIP event, or with ``interprocess=True`` one without
+    timing whose handle another process can open (``ipc_handle`` /
+    ``Event.from_ipc_handle``)."""
 
-    def __init__(self):
+    def __init__(self, interprocess: bool = False, _handle=None):
+        if _handle is not None:
+            self.handle = _handle
+            return
         h = ctypes.c_void_p()
-        check(lib().pf_event_create(ctypes.byref(h)), "pf_event_create")
+        if interprocess:
+            check(lib().pf_event_create_ipc(ctypes.byref(h)), "pf_event_create_ipc")
+        else:
+            check(lib().pf_event_create(ctypes.byref(h)), "pf_event_create")
         self.handle = h.value
+
+    def ipc_handle(self) -> bytes:
+        buf = (ctypes.c_uint8 * 64)()
+        check(lib().pf_ipc_event_export(self.handle, buf), "pf_ipc_event_export")
+        return bytes(buf)
+
+    @classmethod
+    def from_ipc_handle(cls, handle: bytes) -> "Event":
+        """Opens an event exported by another process."""
+        if len(handle) != 64:
+            raise ValueError("an event handle is 64 bytes")
+        buf = (ctypes.c_uint8 * 64).from_buffer_copy(handle)
+        h = ctypes.c_void_p()
+        check(lib().pf_ipc_event_open(buf, ctypes.byref(h)), "pf_ipc_event_open")
+        return cls(_handle=h.value)
 
     def record(self, stream: Stream | None = None) -> None:
         check(lib().pf_event_record(self.handle, stream.handle if stream else None),

@@ -236,8 +236,9 @@ def test_xcd_major_remap_is_a_bijection():
     """The load kernel's tile order (tile_of in pf_kernels.hip): workgroup b
     runs on XCD b mod 8 and takes tile x*q + min(x, r) + i.  It must visit
     every tile of [0, n) exactly once, with XCD x owning one contiguous range
-    of q or q+1 tiles, for every tile count."""
-    for n in range(1, 4097):
+    of q or q+1 tiles, for every tile count up to 1024 and some large ones
+    (the Llama gather has 40960 tiles)."""
+    for n in list(range(1, 1025)) + [4096, 4097, 40960, 40967]:
         q, r = n >> 3, n & 7
         seen = bytearray(n)
         owner = [[] for _ in range(8)]
@@ -251,3 +252,36 @@ def test_xcd_major_remap_is_a_bijection():
             ts = owner[x]
             assert ts == list(range(ts[0], ts[0] + len(ts))) if ts else True
             assert len(ts) == q + (1 if x < r else 0)
+
+
+def test_load_state_event_block_layout():
+    """The optional block of per-layer event handles after the layered
+    extension: {'PFLE', count, events_recorded} at byte 48, handles at 64."""
+    from pegaflow_amd.load_state import LoadState, PyLoadState
+
+    handles = [bytes([7 + i]) * 64 for i in range(5)]
+    p = PyLoadState(num_layers=5, layer_events=handles)
+    raw = open("/dev/shm/" + p.shm_name(), "rb").read()
+    assert len(raw) == 64 + 5 * 64
+    assert struct.unpack_from("<QIIq", raw, 0) == (8, 0x50464C44, 1, 0)
+    assert struct.unpack_from("<IIq", raw, 32) == (0x50464C58, 5, 0)
+    assert struct.unpack_from("<IIq", raw, 48) == (0x50464C45, 5, 0)
+    assert raw[64:] == b"".join(handles)
+    srv = LoadState.attach(p.shm_name())
+    assert srv.event_handles() == handles and not p.events_recorded()
+    calls = []
+    # Nothing recorded and the load finished (nothing to load): no device wait.
+    srv.set_completed()
+    assert p.wait_for_layer_on_device(2, calls.append) and calls == []
+    srv.set_events_recorded(5)
+    assert p.events_recorded()
+    assert p.wait_for_layer_on_device(2, calls.append) and calls == [2]
+    srv.close()
+    # A failed load ends the wait without a device wait.
+    q = PyLoadState(num_layers=2, layer_events=handles[:2])
+    LoadState.attach(q.shm_name()).set_error()
+    assert not q.wait_for_layer_on_device(0, calls.append) and calls == [2]
+    # Plain and layered states carry no handles; mismatched lists are refused.
+    assert LoadState.attach(PyLoadState(num_layers=3).shm_name()).event_handles() == []
+    with pytest.raises(ValueError):
+        PyLoadState(num_layers=3, layer_events=handles[:2])

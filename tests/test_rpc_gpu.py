@@ -17,11 +17,12 @@ import pytest
 
 import oracle
 from pegaflow_amd import ipc
+from pegaflow_amd._lib import PegaFlowError
 from pegaflow_amd.engine import PegaEngine
 from pegaflow_amd.load_state import PyLoadState
 from pegaflow_amd.rpc.client import EngineRpcClient
 from pegaflow_amd.rpc.server import Server
-from pegaflow_amd.runtime import DeviceBuffer
+from pegaflow_amd.runtime import DeviceBuffer, Event, Stream, memcpy_async
 
 pytestmark = pytest.mark.gpu
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -156,4 +157,68 @@ def test_two_process_ipc_round_trip(gpu):
         if p.poll() is None:
             p.kill()
             p.wait(10)
+        layers.close()
+
+
+def test_cross_process_layer_events(gpu):
+    """Device-side per-layer completion across processes: this process (the
+    consumer) hands the server one interprocess event per layer in the
+    LoadState; right after the load is queued its own stream waits on each
+    layer's event and snapshots that layer.  Every snapshot must hold the
+    restored bytes, which it could not if a wait returned before the
+    server's copy of its layer had landed (the copies take ~1 ms; the
+    snapshots are queued within microseconds)."""
+    say("[gpu] rpc two-process layer events (device-side per-layer wait)")
+    probe = Event(interprocess=True)
+    try:
+        probe.ipc_handle()
+    except PegaFlowError as err:
+        pytest.skip(f"this runtime cannot export interprocess events ({err})")
+    finally:
+        probe.close()
+    n_layers = 8
+    layers = Layers(n_layers, 256, 16 * 8 * 128 * 2, seed=21)
+    handles = [ipc.export_tensor(b.ptr, layers.size, 0) for b in layers.bufs]
+    events = [Event(interprocess=True) for _ in range(n_layers)]
+    stream = Stream()
+    snaps = [DeviceBuffer(layers.size) for _ in range(n_layers)]
+    p, addr = _start_server()
+    say(f"[gpu] server pid {p.pid} at {addr}")
+    inst = "vllm-ev"
+    try:
+        with EngineRpcClient(f"http://{addr}", connect_timeout_s=10) as client:
+            for name, handle in zip(layers.names, handles):
+                assert client.register_context(inst, "llama", 0, 1, 0, n_layers, name, handle,
+                                               layers.nb, layers.bpb, layers.kv, 2)[0]
+            before = layers.host()
+            ids = list(range(0, 256, 2))
+            hashes = [h(1000 + i) for i in ids]
+            assert client.save(inst, 0, 0, [(n, ids, hashes) for n in layers.names])[0]
+            layers.fill(seed=77)
+            clobbered = layers.host()
+            targets = list(range(1, 256, 2))
+            st = PyLoadState(num_layers=n_layers,
+                             layer_events=[e.ipc_handle() for e in events])
+            assert client.load(inst, 0, 0, st.shm_name(), layers.names, targets, hashes)[0]
+            for l in range(n_layers):
+                assert st.wait_for_layer_on_device(l, lambda i: stream.wait_event(events[i]),
+                                                   timeout_s=30)
+                memcpy_async(snaps[l].ptr, layers.bufs[l].ptr, layers.size, stream)
+            stream.synchronize()
+            assert wait(st) == 1 and st.layers_done() == n_layers
+            exp = layers.expected(before, clobbered, ids, targets)
+            for l in range(n_layers):
+                assert np.array_equal(snaps[l].download(), exp[l]), f"layer {l} snapshot"
+            assert client.unregister_context(inst)[0]
+            assert client.shutdown()[0]
+        assert p.wait(60) == 0
+    finally:
+        if p.poll() is None:
+            p.kill()
+            p.wait(10)
+        for b in snaps:
+            b.close()
+        for e in events:
+            e.close()
+        stream.close()
         layers.close()
