@@ -146,7 +146,7 @@ class BlockStore {
   PinnedPool& pool() { return *pool_; }
   uint64_t sealed_count();
   uint64_t inflight_count();
-  uint64_t evictions() const { return evictions_; }
+  uint64_t evictions() const { return evictions_.load(std::memory_order_relaxed); }
 
  private:
   std::shared_ptr<PinnedPool> pool_;
@@ -159,7 +159,7 @@ class BlockStore {
     std::list<std::string>::iterator pos;
   };
   std::unordered_map<std::string, Entry> cache_;
-  uint64_t evictions_ = 0;
+  std::atomic<uint64_t> evictions_{0};  // written under cache_mu_, read without it
   SealHook seal_hook_;
   size_t evict_lru(size_t max_blocks);
 };

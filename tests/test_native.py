@@ -1,0 +1,77 @@
+"""The engine's host side under sanitizers (CPU only).
+
+tests/native/stress_engine.cpp drives a host-memory engine with a disk tier
+from several threads at once (prefix queries that start prefetches into a
+pool that evicts constantly, prefix counts, byte-checked slot reads,
+statistics, instance churn).  It is built from the library's own sources,
+with the sanitizers on the host code only (no device code runs), twice:
+ThreadSanitizer, and AddressSanitizer with UndefinedBehaviorSanitizer.
+A sanitizer report fails the run through the sanitizer's exit code.
+The reference has no sanitizer runs and a known race of its own
+(lib.rs:608-612).
+"""
+
+import os
+import shutil
+import subprocess
+from concurrent.futures import ThreadPoolExecutor
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+CSRC = os.path.join(ROOT, "pegaflow_amd", "csrc")
+SOURCES = [os.path.join(CSRC, f) for f in (
+    "pf_layout.cpp", "pf_runtime.cpp", "pf_kernels.hip", "pf_transfer.cpp", "pf_load_state.cpp",
+    "pf_engine.cpp", "pf_disk.cpp")] + [os.path.join(ROOT, "tests", "native", "stress_engine.cpp")]
+HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+
+# Host-side sanitizers only: each flag is passed to the host compilation.
+VARIANTS = {
+    "tsan": ("-Xarch_host -fsanitize=thread",
+             {"TSAN_OPTIONS": "halt_on_error=1 exitcode=66 second_deadlock_stack=1"}),
+    "asan": ("-Xarch_host -fsanitize=address -Xarch_host -fsanitize=undefined "
+             "-Xarch_host -fno-sanitize-recover=undefined",
+             {"ASAN_OPTIONS": "exitcode=67 detect_leaks=1",
+              "UBSAN_OPTIONS": "halt_on_error=1 print_stacktrace=1"}),
+}
+
+
+def build(variant: str) -> str:
+    flags = VARIANTS[variant][0].split()
+    out = os.path.join(ROOT, "_build", f"native-{variant}")
+    os.makedirs(out, exist_ok=True)
+    exe = os.path.join(out, "stress_engine")
+    deps = SOURCES + [os.path.join(CSRC, f) for f in os.listdir(CSRC)] + [
+        os.path.join(ROOT, "include", "pegaflow_hip.h"), os.path.abspath(__file__)]
+    newest = max(os.path.getmtime(p) for p in deps)
+    if os.path.exists(exe) and os.path.getmtime(exe) > newest:
+        return exe
+    common = ["-x", "hip", "--offload-arch=gfx950", "-O1", "-g", "-std=c++17",
+              "-fno-omit-frame-pointer", "-Xclang", "-target-feature", "-Xclang",
+              "-packed-fp32-ops", f"-I{os.path.join(ROOT, 'include')}", f"-I{CSRC}", *flags]
+
+    def compile_one(src):
+        obj = os.path.join(out, os.path.basename(src) + ".o")
+        # Only the kernel file needs its device code (the link resolves its
+        # fat binary); the others are compiled for the host alone.
+        host_only = [] if src.endswith(".hip") else ["--offload-host-only"]
+        subprocess.run([HIPCC, *common, *host_only, "-c", src, "-o", obj], check=True,
+                       stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
+        return obj
+
+    with ThreadPoolExecutor(max_workers=4) as pool:
+        objs = list(pool.map(compile_one, SOURCES))
+    subprocess.run([HIPCC, "--offload-arch=gfx950", *flags, "-o", exe, *objs, "-lpthread", "-lrt"],
+                   check=True, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
+    return exe
+
+
+@pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc is not installed")
+@pytest.mark.parametrize("variant", sorted(VARIANTS))
+def test_engine_stress_under_sanitizer(variant, tmp_path):
+    exe = build(variant)
+    env = dict(os.environ, **VARIANTS[variant][1])
+    r = subprocess.run([exe, str(tmp_path / "pega"), "2.0"], env=env, timeout=300,
+                       stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    assert r.returncode == 0, r.stdout[-6000:]
+    assert "bad 0" in r.stdout
