@@ -1,9 +1,9 @@
 """The engine server: `pegaflow.Engine` over gRPC in front of PegaEngine.
 
 Mirrors pegaflow-server/src/service.rs:19-405 (RPC semantics and the mapping
-of engine errors to gRPC codes, service.rs:77-88), registry.rs:41-176 (layer
-tensors held per (instance, tp_rank, device), dropped on UnregisterContext)
-and the subset of the CLI (lib.rs:38-113) that concerns this path; the disk
+of engine errors to gRPC codes, service.rs:77-88); the request logic and the
+tensor registry (registry.rs:41-176) live in ``pegaflow_amd.frontend``; and
+the subset of the CLI (lib.rs:38-113) that concerns this path; the disk
 tier's --dfs-root / --dfs-quota (lib.rs:98-112) turn it on directly, since
 its index needs no Redis.
 
@@ -23,7 +23,7 @@ import grpc
 
 from .. import _lib
 from ..engine import PegaEngine
-from ..ipc import OpenedTensor, open_tensor
+from ..frontend import EngineFrontend, RegisterTensorError, TensorRegistry  # noqa: F401
 from . import proto
 
 log = logging.getLogger("pegaflow.server")
@@ -56,83 +56,33 @@ def parse_memory_size(s: str) -> int:
     return int(value * mult[unit])
 
 
-class TensorRegistry:
-    """Registered layer tensors per context key "instance:tpR:devD"
-    (registry.rs:41-176)."""
-
-    def __init__(self):
-        self._lock = threading.Lock()
-        self._contexts: dict[str, tuple[int, dict[str, OpenedTensor]]] = {}
-
-    @staticmethod
-    def context_key(instance_id: str, tp_rank: int, device_id: int) -> str:
-        return f"{instance_id}:tp{tp_rank}:dev{device_id}"
-
-    def register_layer(self, key: str, layer_name: str, device_id: int,
-                       wrapper_bytes: bytes) -> OpenedTensor:
-        t = open_tensor(wrapper_bytes)
-        with self._lock:
-            dev, tensors = self._contexts.setdefault(key, (t.device_id, {}))
-            if dev != t.device_id:
-                t.close()
-                raise ValueError(f"context {key} is pinned to device {dev} but got {t.device_id}")
-            old = tensors.pop(layer_name, None)
-            tensors[layer_name] = t
-        if old is not None:
-            old.close()
-        return t
-
-    def drop_instance(self, instance_id: str) -> int:
-        prefix = f"{instance_id}:"
-        with self._lock:
-            keys = [k for k in self._contexts if k.startswith(prefix)]
-            dropped = [self._contexts.pop(k)[1] for k in keys]
-        n = 0
-        for tensors in dropped:
-            for t in tensors.values():
-                t.close()
-                n += 1
-        return n
-
-    def clear(self) -> None:
-        with self._lock:
-            dropped = list(self._contexts.values())
-            self._contexts.clear()
-        for _, tensors in dropped:
-            for t in tensors.values():
-                t.close()
-
-
 def _ok():
     return proto.ResponseStatus(ok=True, message="")
 
 
 class EngineService:
-    """service.rs:133-405."""
+    """service.rs:133-405: the gRPC face of an ``EngineFrontend``."""
 
     def __init__(self, engine: PegaEngine, disk: bool = False):
+        self.frontend = EngineFrontend(engine, disk=disk)
         self.engine = engine
-        self.disk = disk  # Query is prefetch-aware when the engine has a disk tier
-        self.registry = TensorRegistry()
+        self.registry = self.frontend.registry
         self.shutdown_event = threading.Event()
 
-    def _abort(self, context, err: Exception):
+    @staticmethod
+    def _abort(context, err: Exception):
+        if isinstance(err, RegisterTensorError):  # map_py_error, service.rs:90-93
+            context.abort(grpc.StatusCode.INTERNAL, str(err))
         if isinstance(err, _lib.PegaFlowError):
             context.abort(_CODE.get(err.code, grpc.StatusCode.INTERNAL), str(err))
         context.abort(grpc.StatusCode.INTERNAL, str(err))
 
     def RegisterContext(self, req, context):
         try:
-            t = self.registry.register_layer(
-                TensorRegistry.context_key(req.instance_id, req.tp_rank, req.device_id),
-                req.layer_name, req.device_id, req.wrapper_bytes)
-        except Exception as e:  # the reference's map_py_error (service.rs:90-93)
-            context.abort(grpc.StatusCode.INTERNAL, f"register tensor failed: {e}")
-        try:
-            self.engine.register_context_layer(
-                req.instance_id, req.namespace, t.device_id, req.layer_name, t.data_ptr,
-                t.size_bytes, req.num_blocks, req.bytes_per_block, req.kv_stride_bytes,
-                req.segments, req.tp_rank, req.tp_size, req.num_layers)
+            self.frontend.register_context(req.instance_id, req.namespace, req.tp_rank,
+                                           req.tp_size, req.device_id, req.num_layers,
+                                           req.layer_name, req.wrapper_bytes, req.num_blocks,
+                                           req.bytes_per_block, req.kv_stride_bytes, req.segments)
         except Exception as e:
             self._abort(context, e)
         return proto.RegisterContextResponse(status=_ok())
@@ -140,16 +90,15 @@ class EngineService:
     def Save(self, req, context):
         saves = [(s.layer_name, list(s.block_ids), list(s.block_hashes)) for s in req.saves]
         try:
-            self.engine.batch_save_kv_blocks(req.instance_id, req.tp_rank, req.device_id, saves)
+            self.frontend.save(req.instance_id, req.tp_rank, req.device_id, saves)
         except Exception as e:
             self._abort(context, e)
         return proto.SaveResponse(status=_ok())
 
     def Load(self, req, context):
         try:
-            self.engine.batch_load_kv_blocks(req.instance_id, req.tp_rank, req.device_id,
-                                             req.load_state_shm, list(req.layer_names),
-                                             list(req.block_ids), list(req.block_hashes))
+            self.frontend.load(req.instance_id, req.tp_rank, req.device_id, req.load_state_shm,
+                               req.layer_names, req.block_ids, req.block_hashes)
         except Exception as e:
             self._abort(context, e)
         return proto.LoadResponse(status=_ok())
@@ -158,34 +107,18 @@ class EngineService:
         """service.rs:258-330: with a disk tier, a miss that is on disk starts
         a read into the pinned pool and is reported as loading."""
         try:
-            if self.disk:
-                q = self.engine.count_prefix_hit_blocks_with_prefetch(req.instance_id,
-                                                                      list(req.block_hashes))
-                return proto.QueryResponse(status=_ok(), hit_blocks=q["hit_blocks"],
-                                           prefetch_state=q["state"],
-                                           loading_blocks=q["loading_blocks"],
-                                           missing_blocks=q["missing_blocks"])
-            hits = self.engine.count_prefix_hit_blocks(req.instance_id, list(req.block_hashes))
+            q = self.frontend.query(req.instance_id, req.block_hashes)
         except Exception as e:
             self._abort(context, e)
-        return proto.QueryResponse(status=_ok(), hit_blocks=hits,
-                                   prefetch_state=proto.PREFETCH_READY, loading_blocks=0,
-                                   missing_blocks=0)
+        return proto.QueryResponse(status=_ok(), hit_blocks=q["hit_blocks"],
+                                   prefetch_state=q["state"], loading_blocks=q["loading_blocks"],
+                                   missing_blocks=q["missing_blocks"])
 
     def UnregisterContext(self, req, context):
-        # The engine goes first: dropping its last reference to the instance
-        # drains the instance's queued loads, so no transfer still reads a
-        # mapping when the registry closes it below.
-        err = None
         try:
-            self.engine.unregister_instance(req.instance_id)
+            self.frontend.unregister(req.instance_id)
         except Exception as e:
-            err = e
-        removed = self.registry.drop_instance(req.instance_id)
-        if removed:
-            log.info("Dropped %d device tensors for instance %s", removed, req.instance_id)
-        if err is not None:
-            self._abort(context, err)
+            self._abort(context, e)
         return proto.UnregisterResponse(status=_ok())
 
     def Shutdown(self, req, context):
@@ -238,8 +171,7 @@ class Server:
 
     def stop(self, grace: float = 1.0) -> None:
         self.grpc.stop(grace).wait()
-        self.engine.wait_idle()
-        self.service.registry.clear()
+        self.service.frontend.close()
         self.engine.close()
 
 
