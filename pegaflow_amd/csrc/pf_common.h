@@ -91,4 +91,11 @@ inline int layout_kind(const pf_kv_layout& l) {
 int segment_offset(const pf_kv_layout& l, uint64_t block, uint64_t seg,
                    uint64_t* out);
 
+// pf_save_layers without its final wait: the copy may still be in flight on
+// the context's stream when this returns; pf_xfer_synchronize completes it.
+// The staged mode still waits.  For callers that overlap host work with the
+// copy and must not use the bytes before the wait.
+int save_layers_begin(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
+                      uint32_t mode);
+
 }  // namespace pf

@@ -12,11 +12,30 @@
 
 #include <algorithm>
 #include <atomic>
+#include <chrono>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <set>
 
 namespace pf {
+
+namespace {
+// Per-call phase timings on stderr when PEGAFLOW_TRACE is set (the role of
+// the reference's tracing spans and per-task GB/s logs, gpu_worker.rs:293-314).
+bool tracing() {
+  static const bool on = [] {
+    const char* v = std::getenv("PEGAFLOW_TRACE");
+    return v && *v && std::strcmp(v, "0") != 0;
+  }();
+  return on;
+}
+
+double us_between(std::chrono::steady_clock::time_point a, std::chrono::steady_clock::time_point b) {
+  return std::chrono::duration<double, std::micro>(b - a).count();
+}
+
+}  // namespace
 
 // ===========================================================================
 // UnitAllocator
@@ -222,79 +241,104 @@ bool BlockStore::cache_contains(const std::string& key) {
   return cache_.count(key) != 0;
 }
 
-void BlockStore::filter_new(const std::vector<const std::string*>& keys, size_t slot,
-                            std::vector<char>* keep) {
-  keep->assign(keys.size(), 1);
+void BlockStore::filter_slots(const std::vector<std::string>& keys,
+                              const std::vector<size_t>& slots,
+                              std::vector<std::vector<char>>* keep) {
+  const size_t n = keys.size();
+  std::vector<char> sealed(n, 0);
   {
     std::lock_guard<std::mutex> lk(cache_mu_);
-    for (size_t i = 0; i < keys.size(); ++i)
-      if (cache_.count(*keys[i])) (*keep)[i] = 0;
+    for (size_t i = 0; i < n; ++i) sealed[i] = cache_.count(keys[i]) != 0;
   }
+  keep->assign(slots.size(), std::vector<char>(n, 1));
   std::lock_guard<std::mutex> lk(inflight_mu_);
-  for (size_t i = 0; i < keys.size(); ++i) {
-    if (!(*keep)[i]) continue;
-    auto it = inflight_.find(*keys[i]);
-    if (it != inflight_.end() && slot < it->second.slots.size() && it->second.slots[slot])
-      (*keep)[i] = 0;
+  for (size_t i = 0; i < n; ++i) {
+    if (sealed[i]) {
+      for (auto& k : *keep) k[i] = 0;
+      continue;
+    }
+    auto it = inflight_.find(keys[i]);
+    if (it == inflight_.end()) continue;
+    const auto& filled = it->second.slots;
+    for (size_t j = 0; j < slots.size(); ++j)
+      if (slots[j] < filled.size() && filled[slots[j]]) (*keep)[j][i] = 0;
   }
 }
 
-int BlockStore::insert_slots(const std::vector<const std::string*>& keys, size_t slot,
-                             const std::vector<std::shared_ptr<LayerBlock>>& blocks,
+int BlockStore::insert_slots(const std::vector<std::string>& keys,
+                             const std::vector<size_t>& slots, std::vector<SlotEntries>& entries,
                              size_t total_slots) {
-  std::vector<char> sealed_already(keys.size(), 0);
+  const size_t n = keys.size();
+  std::vector<char> sealed_already(n, 0);
   {
     std::lock_guard<std::mutex> lk(cache_mu_);
-    for (size_t i = 0; i < keys.size(); ++i) sealed_already[i] = cache_.count(*keys[i]) != 0;
+    for (const auto& layer : entries)
+      for (const auto& e : layer) sealed_already[e.first] = cache_.count(keys[e.first]) != 0;
   }
-  std::vector<std::pair<const std::string*, std::shared_ptr<SealedBlock>>> sealed;
+  std::vector<std::pair<uint32_t, std::shared_ptr<SealedBlock>>> sealed;
+  int err = PF_OK;
   {
     std::lock_guard<std::mutex> lk(inflight_mu_);
-    for (size_t i = 0; i < keys.size(); ++i) {
-      if (sealed_already[i]) continue;
-      const std::string& key = *keys[i];
-      auto it = inflight_.find(key);
-      if (it == inflight_.end()) {
-        InflightBlock ib;
-        ib.slots.resize(total_slots);
-        ib.remaining = total_slots;
-        it = inflight_.emplace(key, std::move(ib)).first;
-      }
-      InflightBlock& ib = it->second;
-      if (slot < ib.slots.size() && ib.slots[slot]) continue;
-      if (total_slots != ib.slots.size())
-        return fail(PF_ERR_STORAGE, strf("slot count mismatch: expected %zu, got %zu",
-                                         ib.slots.size(), total_slots));
-      if (slot >= ib.slots.size())
-        return fail(PF_ERR_STORAGE,
-                    strf("slot_id %zu out of bounds (%zu slots)", slot, ib.slots.size()));
-      ib.footprint += blocks[i]->size;
-      ib.slots[slot] = blocks[i];
-      if (--ib.remaining == 0) {
-        auto sb = std::make_shared<SealedBlock>();
-        sb->slots = std::move(ib.slots);
-        sb->footprint = ib.footprint;
-        sealed.emplace_back(&key, std::move(sb));
-        inflight_.erase(it);
+    std::vector<InflightBlock*> ib(n, nullptr);  // node pointers survive inserts
+    int rc = PF_OK;
+    for (size_t j = 0; j < entries.size() && rc == PF_OK; ++j) {
+      const size_t slot = slots[j];
+      for (auto& e : entries[j]) {
+        const uint32_t i = e.first;
+        if (sealed_already[i]) continue;
+        if (!ib[i]) {
+          auto it = inflight_.find(keys[i]);
+          if (it == inflight_.end()) {
+            InflightBlock fresh;
+            fresh.slots.resize(total_slots);
+            fresh.remaining = total_slots;
+            it = inflight_.emplace(keys[i], std::move(fresh)).first;
+          }
+          ib[i] = &it->second;
+        }
+        InflightBlock& b = *ib[i];
+        if (b.remaining == 0) continue;  // sealed earlier in this call
+        if (slot < b.slots.size() && b.slots[slot]) continue;
+        if (total_slots != b.slots.size()) {
+          rc = fail(PF_ERR_STORAGE, strf("slot count mismatch: expected %zu, got %zu",
+                                         b.slots.size(), total_slots));
+          break;
+        }
+        if (slot >= b.slots.size()) {
+          rc = fail(PF_ERR_STORAGE,
+                    strf("slot_id %zu out of bounds (%zu slots)", slot, b.slots.size()));
+          break;
+        }
+        b.footprint += e.second->size;
+        b.slots[slot] = std::move(e.second);
+        if (--b.remaining == 0) {
+          auto sb = std::make_shared<SealedBlock>();
+          sb->slots = std::move(b.slots);
+          sb->footprint = b.footprint;
+          sealed.emplace_back(i, std::move(sb));
+        }
       }
     }
+    for (const auto& s : sealed) inflight_.erase(keys[s.first]);
+    if (rc != PF_OK && sealed.empty()) return rc;
+    if (rc != PF_OK) err = rc;  // blocks completed before the error still seal
   }
   if (sealed.empty()) return PF_OK;
   std::vector<char> fresh(sealed.size(), 0);
   {
     std::lock_guard<std::mutex> lk(cache_mu_);
-    for (size_t i = 0; i < sealed.size(); ++i) {
-      const std::string& key = *sealed[i].first;
+    for (size_t k = 0; k < sealed.size(); ++k) {
+      const std::string& key = keys[sealed[k].first];
       if (cache_.count(key)) continue;
       lru_.push_front(key);
-      cache_[key] = Entry{sealed[i].second, lru_.begin()};
-      fresh[i] = 1;
+      cache_[key] = Entry{sealed[k].second, lru_.begin()};
+      fresh[k] = 1;
     }
   }
   if (seal_hook_)
-    for (size_t i = 0; i < sealed.size(); ++i)
-      if (fresh[i]) seal_hook_(*sealed[i].first, sealed[i].second);
-  return PF_OK;
+    for (size_t k = 0; k < sealed.size(); ++k)
+      if (fresh[k]) seal_hook_(keys[sealed[k].first], sealed[k].second);
+  return err;
 }
 
 bool BlockStore::cache_insert(const std::string& key, std::shared_ptr<SealedBlock> block) {
@@ -358,6 +402,7 @@ struct LoadTask {
   pf_load_state* state = nullptr;
   uint32_t mode = PF_MODE_KERNEL;
   uint64_t bytes = 0;
+  std::chrono::steady_clock::time_point submitted = std::chrono::steady_clock::now();
 };
 
 class DeviceWorker {
@@ -365,7 +410,10 @@ class DeviceWorker {
   static int create(int device, bool with_gpu, std::shared_ptr<DeviceWorker>* out,
                     std::atomic<uint64_t>* loaded_bytes, std::atomic<uint64_t>* failures);
   ~DeviceWorker();
-  int save(const std::vector<pf_layer_xfer>& layers, uint32_t mode);
+  // Saves the layers; `overlap` runs on the calling thread while the copy is
+  // in flight, and the call returns once the bytes are in place.
+  int save(const std::vector<pf_layer_xfer>& layers, uint32_t mode,
+           const std::function<void()>& overlap);
   int submit(LoadTask&& task);
   void wait_idle();
 
@@ -422,12 +470,20 @@ DeviceWorker::~DeviceWorker() {
   if (load_x_) pf_xfer_destroy(load_x_);
 }
 
-int DeviceWorker::save(const std::vector<pf_layer_xfer>& layers, uint32_t mode) {
+int DeviceWorker::save(const std::vector<pf_layer_xfer>& layers, uint32_t mode,
+                       const std::function<void()>& overlap) {
   if (!gpu_)
     return fail(PF_ERR_UNSUPPORTED, "storage error: engine pool is not mapped for a device");
   std::lock_guard<std::mutex> lk(save_mu_);
-  int rc = pf_save_layers(save_x_, layers.data(), static_cast<uint32_t>(layers.size()), mode);
-  if (rc) return fail(PF_ERR_STORAGE, std::string("storage error: ") + pf_last_error());
+  int rc = save_layers_begin(save_x_, layers.data(), static_cast<uint32_t>(layers.size()), mode);
+  if (rc) {
+    const std::string msg = pf_last_error();
+    (void)pf_xfer_synchronize(save_x_);  // nothing may still read the regions
+    return fail(PF_ERR_STORAGE, "storage error: " + msg);
+  }
+  overlap();
+  if (pf_xfer_synchronize(save_x_))
+    return fail(PF_ERR_STORAGE, std::string("storage error: ") + pf_last_error());
   return PF_OK;
 }
 
@@ -462,6 +518,7 @@ void DeviceWorker::load_loop() {
       task = std::move(queue_.front());
       queue_.pop_front();
     }
+    const auto t_begin = std::chrono::steady_clock::now();
     const size_t L = task.layouts.size();
     bool ok = true;
     std::vector<pf_layer_xfer> layers(L);
@@ -524,6 +581,15 @@ void DeviceWorker::load_loop() {
       if (!ok) (void)pf_xfer_synchronize(load_x_);
     }
     for (pf_event ev : ipc_evs) (void)pf_event_destroy(ev);
+    if (tracing()) {
+      const auto t_end = std::chrono::steady_clock::now();
+      std::fprintf(stderr,
+                   "[pegaflow] load device=%d layers=%zu bytes=%llu queued=%.0fus copy=%.0fus "
+                   "(%.2f GB/s) per_layer=%d ok=%d\n",
+                   device_, L, (unsigned long long)task.bytes, us_between(task.submitted, t_begin),
+                   us_between(t_begin, t_end), task.bytes / us_between(t_begin, t_end) / 1e3,
+                   (int)per_layer, (int)ok);
+    }
     if (ok) {
       pf_load_state_set_completed(task.state);
       loaded_bytes_->fetch_add(task.bytes);
@@ -646,17 +712,19 @@ std::vector<std::string> keys_of(const std::string& ns, const uint8_t* data, con
 // Host side of one planned layer save.
 struct SavePlan {
   size_t slot = 0;
+  size_t group = 0;                // index of the layer's hash list
   pf_kv_layout layout{};
-  std::vector<const std::string*> keys;  // kept hashes, in order
+  std::vector<uint32_t> key_idx;   // kept hashes (indices into the list), in order
   std::vector<pf_block_xfer> blocks;
   std::shared_ptr<PoolAllocation> k_alloc, v_alloc;
   bool split = false;
 };
 
-// The LayerBlocks of one planned layer, in one allocation; each block's
-// handle shares the owner's reference count.
+// The LayerBlocks of one planned layer in one allocation, which also holds
+// the pool regions; each block's handle shares the set's reference count.
 struct LayerBlockSet {
   std::vector<LayerBlock> blocks;
+  std::shared_ptr<PoolAllocation> k_alloc, v_alloc;
 };
 
 }  // namespace
@@ -853,6 +921,7 @@ int pf_engine_count_prefix_hit_blocks(pf_engine* e, const char* instance_id,
 // lib.rs:497-782.
 int pf_engine_batch_save(pf_engine* e, const char* instance_id, uint64_t tp_rank, int device_id,
                          const pf_save_layer* layers, uint32_t num_layers) {
+  const auto t_start = std::chrono::steady_clock::now();
   std::shared_ptr<Instance> inst;
   if (int rc = get_instance(e, instance_id, &inst)) return rc;
   auto gpu = inst->gpu(device_id);
@@ -860,136 +929,155 @@ int pf_engine_batch_save(pf_engine* e, const char* instance_id, uint64_t tp_rank
     return fail(PF_ERR_WORKER_MISSING,
                 strf("device %d not found in instance %s", device_id, instance_id));
   const size_t total_slots = inst->num_layers * inst->tp_size;
-  std::vector<SavePlan> plans;
-  plans.reserve(num_layers);
-  // Keys are built once per distinct hash list: the layers of a batch
-  // normally pass the same one.
-  struct KeyList {
+  // Pass 1: every layer's registration and slot, and its hash list.  The
+  // layers of a batch normally share one list, so keys are built once per
+  // distinct list and the store is consulted once per key, not per layer.
+  struct KeyGroup {
     const uint8_t* data;
     const uint64_t* offs;
     uint64_t n;
     std::vector<std::string> keys;
+    std::vector<size_t> plans;  // the layers that use it
   };
-  std::vector<std::unique_ptr<KeyList>> key_lists;
-  auto keys_for = [&](const pf_save_layer& sl) -> const std::vector<std::string>& {
-    for (auto& kl : key_lists)
-      if (kl->data == sl.hash_data && kl->offs == sl.hash_offsets && kl->n == sl.num_blocks)
-        return kl->keys;
-    key_lists.emplace_back(new KeyList{sl.hash_data, sl.hash_offsets, sl.num_blocks,
-                                       keys_of(inst->ns, sl.hash_data, sl.hash_offsets,
-                                               sl.num_blocks)});
-    return key_lists.back()->keys;
-  };
-  std::vector<const std::string*> cand;
-  std::vector<int64_t> cand_ids;
-  std::vector<char> keep;
+  std::vector<KeyGroup> groups;
+  std::vector<SavePlan> plans(num_layers);
   for (uint32_t li = 0; li < num_layers; ++li) {
     const pf_save_layer& sl = layers[li];
     const std::string name(sl.layer_name);
     size_t layer_id = 0;
     if (!inst->layer_id(name, &layer_id))
       return fail(PF_ERR_INVALID_ARGUMENT, "invalid argument: layer " + name + " unknown");
-    pf_kv_layout reg{};
+    SavePlan& plan = plans[li];
     {
       std::lock_guard<std::mutex> lk(gpu->mu);
       auto it = gpu->regs.find(name);
       if (it == gpu->regs.end())
         return fail(PF_ERR_INVALID_ARGUMENT,
                     "invalid argument: layer " + name + " not registered on device");
-      reg = it->second;
+      plan.layout = it->second;
     }
-    SavePlan plan;
     if (int rc = inst->slot_index(layer_id, tp_rank, &plan.slot)) return rc;
-    plan.layout = reg;
-    // Filtering and dedup (lib.rs:590-621).
-    const std::vector<std::string>& keys = keys_for(sl);
-    cand.clear();
-    cand_ids.clear();
-    for (uint64_t i = 0; i < sl.num_blocks; ++i) {
-      const int32_t id = sl.block_ids[i];
-      if (id < 0) continue;
-      if (static_cast<uint64_t>(id) >= reg.num_blocks)
+    for (uint64_t i = 0; i < sl.num_blocks; ++i)
+      if (sl.block_ids[i] >= 0 && static_cast<uint64_t>(sl.block_ids[i]) >= plan.layout.num_blocks)
         return fail(PF_ERR_INVALID_ARGUMENT,
                     strf("invalid argument: block %d out of range for layer %s (%llu blocks "
                          "registered)",
-                         id, name.c_str(), (unsigned long long)reg.num_blocks));
-      cand.push_back(&keys[i]);
-      cand_ids.push_back(id);
-    }
-    e->store->filter_new(cand, plan.slot, &keep);
-    std::vector<int64_t> idx;
-    idx.reserve(cand.size());
-    for (size_t i = 0; i < cand.size(); ++i)
-      if (keep[i]) {
-        idx.push_back(cand_ids[i]);
-        plan.keys.push_back(cand[i]);
-      }
-    if (idx.empty()) continue;
-    const uint64_t n = idx.size();
-    plan.split = reg.segments == 2 && reg.kv_stride_bytes > reg.bytes_per_block;
-    plan.blocks.resize(n);
-    if (plan.split) {  // lib.rs:636-679
-      const uint64_t seg = reg.bytes_per_block;
-      plan.k_alloc = e->store->allocate(seg * n);
-      if (!plan.k_alloc)
-        return fail(PF_ERR_STORAGE,
-                    "storage error: pinned pool exhausted while allocating K segment buffer");
-      plan.v_alloc = e->store->allocate(seg * n);
-      if (!plan.v_alloc)
-        return fail(PF_ERR_STORAGE,
-                    "storage error: pinned pool exhausted while allocating V segment buffer");
-      for (uint64_t i = 0; i < n; ++i)
-        plan.blocks[i] = pf_block_xfer{idx[i], reinterpret_cast<uint64_t>(plan.k_alloc->ptr + i * seg),
-                                       reinterpret_cast<uint64_t>(plan.v_alloc->ptr + i * seg)};
-    } else {  // lib.rs:706-747
-      const uint64_t bs = reg.block_size_bytes;
-      plan.k_alloc = e->store->allocate(bs * n);
-      if (!plan.k_alloc)
-        return fail(PF_ERR_STORAGE,
-                    "storage error: pinned pool exhausted while allocating contiguous block buffer");
-      for (uint64_t i = 0; i < n; ++i)
-        plan.blocks[i] =
-            pf_block_xfer{idx[i], reinterpret_cast<uint64_t>(plan.k_alloc->ptr + i * bs), 0};
-    }
-    plans.push_back(std::move(plan));
+                         sl.block_ids[i], name.c_str(),
+                         (unsigned long long)plan.layout.num_blocks));
+    size_t g = 0;
+    while (g < groups.size() && !(groups[g].data == sl.hash_data &&
+                                  groups[g].offs == sl.hash_offsets && groups[g].n == sl.num_blocks))
+      ++g;
+    if (g == groups.size())
+      groups.push_back(KeyGroup{sl.hash_data, sl.hash_offsets, sl.num_blocks,
+                                keys_of(inst->ns, sl.hash_data, sl.hash_offsets, sl.num_blocks),
+                                {}});
+    groups[g].plans.push_back(li);
+    plan.group = g;
   }
-  if (plans.empty()) return PF_OK;
-  // The LayerBlocks, one allocation per layer, ready before the copy.
-  std::vector<std::vector<std::shared_ptr<LayerBlock>>> handles(plans.size());
-  for (size_t pi = 0; pi < plans.size(); ++pi) {
-    const SavePlan& p = plans[pi];
-    const uint64_t seg = p.layout.bytes_per_block, bs = p.layout.block_size_bytes;
-    auto set = std::make_shared<LayerBlockSet>();
-    set->blocks.resize(p.keys.size());
-    for (size_t i = 0; i < p.keys.size(); ++i) {
-      LayerBlock& lb = set->blocks[i];
-      lb.size = bs;
-      lb.k_alloc = p.k_alloc;
-      if (p.split) {
-        lb.k_ptr = p.k_alloc->ptr + i * seg;
-        lb.v_ptr = p.v_alloc->ptr + i * seg;
-        lb.v_alloc = p.v_alloc;
-      } else {
-        lb.k_ptr = p.k_alloc->ptr + i * bs;
+  // Pass 2: filtering and dedup (lib.rs:590-621), then the host regions in
+  // the reference's layout.
+  for (const KeyGroup& g : groups) {
+    std::vector<size_t> slots;
+    for (size_t li : g.plans) slots.push_back(plans[li].slot);
+    std::vector<std::vector<char>> keep;
+    e->store->filter_slots(g.keys, slots, &keep);
+    for (size_t j = 0; j < g.plans.size(); ++j) {
+      SavePlan& plan = plans[g.plans[j]];
+      const pf_save_layer& sl = layers[g.plans[j]];
+      std::vector<int64_t> idx;
+      for (uint64_t i = 0; i < sl.num_blocks; ++i)
+        if (sl.block_ids[i] >= 0 && keep[j][i]) {
+          idx.push_back(sl.block_ids[i]);
+          plan.key_idx.push_back(static_cast<uint32_t>(i));
+        }
+      if (idx.empty()) continue;
+      const pf_kv_layout& reg = plan.layout;
+      const uint64_t n = idx.size();
+      plan.split = reg.segments == 2 && reg.kv_stride_bytes > reg.bytes_per_block;
+      plan.blocks.resize(n);
+      if (plan.split) {  // lib.rs:636-679
+        const uint64_t seg = reg.bytes_per_block;
+        plan.k_alloc = e->store->allocate(seg * n);
+        if (!plan.k_alloc)
+          return fail(PF_ERR_STORAGE,
+                      "storage error: pinned pool exhausted while allocating K segment buffer");
+        plan.v_alloc = e->store->allocate(seg * n);
+        if (!plan.v_alloc)
+          return fail(PF_ERR_STORAGE,
+                      "storage error: pinned pool exhausted while allocating V segment buffer");
+        for (uint64_t i = 0; i < n; ++i)
+          plan.blocks[i] =
+              pf_block_xfer{idx[i], reinterpret_cast<uint64_t>(plan.k_alloc->ptr + i * seg),
+                            reinterpret_cast<uint64_t>(plan.v_alloc->ptr + i * seg)};
+      } else {  // lib.rs:706-747
+        const uint64_t bs = reg.block_size_bytes;
+        plan.k_alloc = e->store->allocate(bs * n);
+        if (!plan.k_alloc)
+          return fail(PF_ERR_STORAGE,
+                      "storage error: pinned pool exhausted while allocating contiguous block "
+                      "buffer");
+        for (uint64_t i = 0; i < n; ++i)
+          plan.blocks[i] =
+              pf_block_xfer{idx[i], reinterpret_cast<uint64_t>(plan.k_alloc->ptr + i * bs), 0};
       }
     }
-    handles[pi].reserve(p.keys.size());
-    for (size_t i = 0; i < p.keys.size(); ++i)
-      handles[pi].emplace_back(set, &set->blocks[i]);  // aliases the set's count
   }
   std::vector<pf_layer_xfer> xl;
-  xl.reserve(plans.size());
-  for (auto& p : plans) xl.push_back(pf_layer_xfer{p.layout, p.blocks.data(), p.blocks.size()});
-  if (int rc = gpu->worker->save(xl, e->save_mode.load())) return rc;
-  // Slot insertion once the bytes are in place (lib.rs:687-705, 755-770).
+  for (auto& p : plans)
+    if (!p.blocks.empty()) xl.push_back(pf_layer_xfer{p.layout, p.blocks.data(), p.blocks.size()});
+  if (xl.empty()) return PF_OK;
+  // The LayerBlocks are built while the copy runs; they are published only
+  // after it has completed (lib.rs:687-705, 755-770).
+  std::vector<BlockStore::SlotEntries> entries(plans.size());
+  auto build_handles = [&] {
+    for (size_t pi = 0; pi < plans.size(); ++pi) {
+      const SavePlan& p = plans[pi];
+      if (p.blocks.empty()) continue;
+      const uint64_t seg = p.layout.bytes_per_block, bs = p.layout.block_size_bytes;
+      auto set = std::make_shared<LayerBlockSet>();
+      set->k_alloc = p.k_alloc;
+      set->v_alloc = p.v_alloc;
+      set->blocks.resize(p.key_idx.size());
+      entries[pi].reserve(p.key_idx.size());
+      for (size_t i = 0; i < p.key_idx.size(); ++i) {
+        LayerBlock& lb = set->blocks[i];
+        lb.size = bs;
+        if (p.split) {
+          lb.k_ptr = p.k_alloc->ptr + i * seg;
+          lb.v_ptr = p.v_alloc->ptr + i * seg;
+        } else {
+          lb.k_ptr = p.k_alloc->ptr + i * bs;
+        }
+        entries[pi].emplace_back(p.key_idx[i], std::shared_ptr<LayerBlock>(set, &lb));
+      }
+    }
+  };
+  const auto t_planned = std::chrono::steady_clock::now();
+  if (int rc = gpu->worker->save(xl, e->save_mode.load(), build_handles)) return rc;
+  const auto t_copied = std::chrono::steady_clock::now();
   uint64_t bytes = 0;
-  for (size_t pi = 0; pi < plans.size(); ++pi) {
-    const SavePlan& p = plans[pi];
-    if (int rc = e->store->insert_slots(p.keys, p.slot, handles[pi], total_slots))
+  for (const KeyGroup& g : groups) {
+    std::vector<size_t> slots;
+    std::vector<BlockStore::SlotEntries> ge;
+    for (size_t li : g.plans) {
+      slots.push_back(plans[li].slot);
+      ge.push_back(std::move(entries[li]));
+      bytes += plans[li].key_idx.size() * plans[li].layout.block_size_bytes;
+    }
+    if (int rc = e->store->insert_slots(g.keys, slots, ge, total_slots))
       return fail(rc, std::string("storage error: ") + pf_last_error());
-    bytes += p.keys.size() * p.layout.block_size_bytes;
   }
   e->saved_bytes.fetch_add(bytes);
+  if (tracing()) {
+    const auto t_end = std::chrono::steady_clock::now();
+    std::fprintf(stderr,
+                 "[pegaflow] save instance=%s layers=%u bytes=%llu plan=%.0fus copy=%.0fus "
+                 "publish=%.0fus total=%.0fus (%.2f GB/s)\n",
+                 instance_id, num_layers, (unsigned long long)bytes, us_between(t_start, t_planned),
+                 us_between(t_planned, t_copied), us_between(t_copied, t_end),
+                 us_between(t_start, t_end), bytes / us_between(t_start, t_end) / 1e3);
+  }
   return PF_OK;
 }
 

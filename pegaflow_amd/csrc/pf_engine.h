@@ -131,15 +131,19 @@ class BlockStore {
   // of 64 until the largest free region fits (storage.rs:405-433).
   std::shared_ptr<PoolAllocation> allocate(uint64_t size);
   bool cache_contains(const std::string& key);
-  // One layer of a save, each lock taken once: keep[i] = 0 when keys[i] is
-  // sealed already or its slot is inflight (lib.rs:590-621).
-  void filter_new(const std::vector<const std::string*>& keys, size_t slot,
-                  std::vector<char>* keep);
-  // storage.rs:457-514 for one layer: slots of sealed blocks and filled
-  // slots are skipped; a block whose last slot arrives moves to the cache
-  // and the seal hook runs for it.  Errors on slot count mismatch / range.
-  int insert_slots(const std::vector<const std::string*>& keys, size_t slot,
-                   const std::vector<std::shared_ptr<LayerBlock>>& blocks, size_t total_slots);
+  // The layers of one save that share a hash list, with one lookup per key
+  // in each map: keep[j][i] = 0 when keys[i] is sealed already or its slot
+  // slots[j] is inflight (lib.rs:590-621).
+  void filter_slots(const std::vector<std::string>& keys, const std::vector<size_t>& slots,
+                    std::vector<std::vector<char>>* keep);
+  // storage.rs:457-514 for those layers: entries[j] holds (key index, host
+  // copy) for layer j, stored in slot slots[j].  Slots of sealed blocks and
+  // filled slots are skipped; a block whose last slot arrives moves to the
+  // cache and the seal hook runs for it.  Errors on slot count mismatch or
+  // a slot out of range.
+  using SlotEntries = std::vector<std::pair<uint32_t, std::shared_ptr<LayerBlock>>>;
+  int insert_slots(const std::vector<std::string>& keys, const std::vector<size_t>& slots,
+                   std::vector<SlotEntries>& entries, size_t total_slots);  // moves the copies
   // storage.rs:529-547: every hash must be sealed; refreshes recency.
   int lookup_many(const std::vector<std::string>& keys,
                   std::vector<std::shared_ptr<SealedBlock>>* out);

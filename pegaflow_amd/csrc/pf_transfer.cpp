@@ -518,7 +518,7 @@ int staged(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<LayerPlan>
 
 // ---- kernel mode ----------------------------------------------------------
 int kernel_direct(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<LayerPlan>& plans,
-                  bool is_save, pf_event* layer_events) {
+                  bool is_save, pf_event* layer_events, bool wait_save) {
   if (int rc = check_all_kernel(layers, plans, true)) return rc;
   size_t total = 0;
   for (const auto& p : plans)
@@ -560,12 +560,12 @@ int kernel_direct(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<Lay
       PF_HIP(hipEventRecord(static_cast<hipEvent_t>(layer_events[li]), x->stream));
     li = lj;
   }
-  if (is_save) PF_HIP(hipStreamSynchronize(x->stream));
+  if (is_save && wait_save) PF_HIP(hipStreamSynchronize(x->stream));
   return PF_OK;
 }
 
 int run(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, uint32_t mode,
-        bool is_save, pf_event* layer_events) {
+        bool is_save, pf_event* layer_events, bool wait_save = true) {
   if (!x) return fail(PF_ERR_INVALID_ARGUMENT, "null transfer context");
   if (num_layers > 0 && !layers) return fail(PF_ERR_INVALID_ARGUMENT, "null layer list");
   std::lock_guard<std::mutex> lk(x->mu);
@@ -583,13 +583,13 @@ int run(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, uint32_t m
         if (!is_save && layer_events && layer_events[li])
           PF_HIP(hipEventRecord(static_cast<hipEvent_t>(layer_events[li]), x->stream));
       }
-      if (is_save) PF_HIP(hipStreamSynchronize(x->stream));
+      if (is_save && wait_save) PF_HIP(hipStreamSynchronize(x->stream));
       return PF_OK;
     }
     case PF_MODE_KERNEL:
       for (uint32_t li = 0; li < num_layers; ++li)
         apply_write_policy(layers[li], is_save, false, &plans[li]);
-      return kernel_direct(x, layers, plans, is_save, layer_events);
+      return kernel_direct(x, layers, plans, is_save, layer_events, wait_save);
     case PF_MODE_STAGED:
       for (uint32_t li = 0; li < num_layers; ++li)
         apply_write_policy(layers[li], is_save, true, &plans[li]);
@@ -600,6 +600,11 @@ int run(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, uint32_t m
 }
 
 }  // namespace
+
+int pf::save_layers_begin(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
+                          uint32_t mode) {
+  return run(x, layers, num_layers, mode, true, nullptr, false);
+}
 
 extern "C" {
 
