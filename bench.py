@@ -127,10 +127,14 @@ def leg_layerwise(xfer, seed):
     kernel on a second stream.  Overlap efficiency = 36 x 2 ms / total, with
     the total from the load's first issue to the last compute kernel's end
     (device events).  The serialized figure gates every compute kernel on the
-    whole load, as a caller without per-layer completion must."""
+    whole load, as a caller without per-layer completion must.  The marked
+    figure restores all layers in one launch whose kernel writes a device
+    word per layer, and gates compute kernel l with a bounded device wait on
+    word l."""
     from pegaflow_amd import _lib
     from pegaflow_amd import workload as wl
-    from pegaflow_amd.runtime import Event, PinnedBuffer, Stream, spin
+    from pegaflow_amd.runtime import (DeviceBuffer, Event, PinnedBuffer, Stream, spin,
+                                      stream_wait_word)
 
     shape, n, compute_us = wl.QWEN3_8B, 313, 2000
     layers = wl.DeviceLayers(shape, base_seed=seed)
@@ -157,9 +161,28 @@ def leg_layerwise(xfer, seed):
                                                    for l in range(1, shape.layers)]
         return start.elapsed_ms(done), per_layer
 
+    words = DeviceBuffer(8 * shape.layers)
+    words.memset(0)
+    value = [0]
+
+    def run_marked():
+        value[0] += 1
+        start.record(xfer.stream)
+        compute.wait_event(start)
+        xfer.load_layers_marked(loads, [(words.ptr, value[0], False)], _lib.MODE_KERNEL)
+        for l in range(shape.layers):
+            stream_wait_word(compute, words.ptr + 8 * l, value[0], 10_000_000)
+            spin(compute, compute_us)
+        done.record(compute)
+        done.synchronize()
+        xfer.synchronize()
+        return start.elapsed_ms(done)
+
     run(True)
     total, per_layer = min((run(True) for _ in range(3)), key=lambda r: r[0])
     serial, _ = min((run(False) for _ in range(2)), key=lambda r: r[0])
+    run_marked()
+    marked = min(run_marked() for _ in range(3))
     bad = wl.verify_restored(layers, ids, targets)
     ideal = shape.layers * compute_us / 1e3
     out = {
@@ -170,6 +193,8 @@ def leg_layerwise(xfer, seed):
         "compute_ms": ideal,
         "serialized_total_ms": round(serial, 3),
         "serialized_efficiency": round(ideal / serial, 4),
+        "marked_total_ms": round(marked, 3),
+        "marked_efficiency": round(ideal / marked, 4),
         "first_layer_ms": round(per_layer[0], 4),
         "per_layer_ms_mean": round(sum(per_layer[1:]) / (len(per_layer) - 1), 4),
         "per_layer_ms_max": round(max(per_layer[1:]), 4),
@@ -177,6 +202,7 @@ def leg_layerwise(xfer, seed):
         "bit_exact": bad == 0,
     }
     compute.close()
+    words.close()
     pool.close()
     layers.close()
     return out

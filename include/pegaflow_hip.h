@@ -321,6 +321,50 @@ int pf_save_layers(pf_xfer* xfer, const pf_layer_xfer* layers,
 int pf_load_layers(pf_xfer* xfer, const pf_layer_xfer* layers,
                    uint32_t num_layers, uint32_t mode, pf_event* layer_events);
 
+/* Layer marks: per-layer completion written by the load itself.  No
+ * counterpart in the reference (its per-layer wait is a no-op,
+ * worker.py:288-289; its load syncs once after all layers,
+ * gpu_worker.rs:286-291).  Unlike layer_events, marks do not split a load
+ * from pinned host memory into one launch per layer: in PF_MODE_KERNEL a
+ * single launch covers every such layer and its last workgroup on layer l
+ * writes the marks of layer l.  Layers loaded from device memory (an
+ * HBM-bound copy) get one launch each, followed by their marks; DMA and
+ * staged copies are marked after each layer's copies.
+ *
+ * A signal target is an array of one 8-byte word per layer of the call:
+ * words + 8*l is set to `value` once layer l's bytes are in place.  The
+ * array may be host-mapped pinned memory (host_memory = 1; the host polls
+ * it), device memory of this process, or device memory of another process
+ * mapped with pf_ipc_open (host_memory = 0; a stream waits on it with
+ * pf_stream_wait_word).  Every word is written exactly once per call, empty
+ * layers included; values must be nonzero, and a caller reusing an array
+ * gives each call a larger value than the last, since waiters wait for
+ * word >= value. */
+#define PF_MAX_LAYER_SIGNALS 4
+typedef struct pf_layer_signal {
+  uint64_t words;       /* address of num_layers 8-byte words (8-aligned)  */
+  uint64_t value;       /* nonzero                                        */
+  uint32_t host_memory; /* 1: pinned host memory, 0: device memory        */
+  uint32_t reserved;    /* 0                                              */
+} pf_layer_signal;
+/* pf_load_layers with marks instead of events (1..PF_MAX_LAYER_SIGNALS
+ * targets).  Asynchronous like pf_load_layers. */
+int pf_load_layers_marked(pf_xfer* xfer, const pf_layer_xfer* layers,
+                          uint32_t num_layers, uint32_t mode,
+                          const pf_layer_signal* signals, uint32_t num_signals);
+/* Bounded device-side wait (no counterpart in the reference): work queued on
+ * stream after this call starts once the 8-byte word at `word` (device,
+ * IPC-mapped or pinned host memory) is >= value, or after timeout_us
+ * microseconds (at most 60 s), whichever comes first; the waiting kernel
+ * always ends.  A timeout sets the 4-byte word at timed_out (if nonzero,
+ * device or pinned memory) to 1; the caller clears it beforehand. */
+int pf_stream_wait_word(pf_stream stream, uint64_t word, uint64_t value,
+                        uint32_t timeout_us, uint64_t timed_out);
+/* Host-side wait on a word in pinned host memory: *reached = 1 once the word
+ * is >= value, 0 if timeout_us passed first. */
+int pf_host_wait_word(const uint64_t* word, uint64_t value, uint64_t timeout_us,
+                      int* reached);
+
 /* ------------------------------------------------------------------------ */
 /* Synthetic data and verification kernels (benchmarks and parity tests).     */
 /* ------------------------------------------------------------------------ */
@@ -390,6 +434,36 @@ const uint8_t* pf_load_state_event_handles(const pf_load_state* state,
                                            uint32_t* count);
 int64_t pf_load_state_events_recorded(const pf_load_state* state);
 void pf_load_state_set_events_recorded(pf_load_state* state, int64_t n);
+/* Device-side per-layer completion through layer words (no counterpart in
+ * the reference), for platforms without interprocess events.  The consumer
+ * owns num_layers 8-byte words of device memory and gives them to the loader
+ * in a words block at byte 48 (instead of the event block):
+ * {u32 magic 0x50464C57 ('PFLW'), u32 count, u64 value, u32 kind,
+ * u32 reserved, u64 address, u64 alloc_size, u64 offset, 64-byte handle}.
+ * The loader writes value into word l once layer l's bytes are in place
+ * (pf_load_layers_marked), and into every word when the load fails after it
+ * mapped them; the consumer gates a stream on word l with
+ * pf_stream_wait_word(word_l, value), at any time after the load request.
+ * kind PF_LAYER_WORDS_IPC: the words are at offset inside the allocation of
+ * alloc_size bytes exported as handle (pf_ipc_export); kind
+ * PF_LAYER_WORDS_LOCAL: at address, in the loader's own process. */
+enum { PF_LAYER_WORDS_IPC = 0, PF_LAYER_WORDS_LOCAL = 1 };
+typedef struct pf_layer_words {
+  uint32_t kind;
+  uint32_t reserved; /* 0 */
+  uint64_t value;    /* nonzero; larger than any earlier load's on the same words */
+  uint64_t address;
+  uint64_t alloc_size;
+  uint64_t offset;
+  uint8_t handle[PF_IPC_HANDLE_BYTES];
+} pf_layer_words;
+int pf_load_state_create_layered_words(uint32_t num_layers,
+                                       const pf_layer_words* words,
+                                       pf_load_state** out);
+/* The words block of a state: *count = its layer count (0 when the state has
+ * none, *out untouched). */
+int pf_load_state_layer_words(const pf_load_state* state, pf_layer_words* out,
+                              uint32_t* count);
 
 /* ------------------------------------------------------------------------ */
 /* Pool allocator.  Replaces ScaledOffsetAllocator (allocator.rs:66-171):     */

@@ -117,6 +117,35 @@ class LayerXfer(ctypes.Structure):
     ]
 
 
+class LayerSignal(ctypes.Structure):
+    """pf_layer_signal — one target of a marked load's per-layer completion words."""
+
+    _fields_ = [
+        ("words", ctypes.c_uint64),
+        ("value", ctypes.c_uint64),
+        ("host_memory", ctypes.c_uint32),
+        ("reserved", ctypes.c_uint32),
+    ]
+
+
+MAX_LAYER_SIGNALS = 4
+LAYER_WORDS_IPC, LAYER_WORDS_LOCAL = 0, 1
+
+
+class LayerWords(ctypes.Structure):
+    """pf_layer_words — a consumer's per-layer device words in a LoadState."""
+
+    _fields_ = [
+        ("kind", ctypes.c_uint32),
+        ("reserved", ctypes.c_uint32),
+        ("value", ctypes.c_uint64),
+        ("address", ctypes.c_uint64),
+        ("alloc_size", ctypes.c_uint64),
+        ("offset", ctypes.c_uint64),
+        ("handle", ctypes.c_uint8 * 64),
+    ]
+
+
 class SaveLayer(ctypes.Structure):
     """pf_save_layer — one (layer_name, block_ids, block_hashes) of a save batch."""
 
@@ -216,6 +245,10 @@ SIGNATURES = {
     "pf_xfer_last_kernel_ms": (i32, [vp, ctypes.POINTER(ctypes.c_float), pu64]),
     "pf_save_layers": (i32, [vp, ctypes.POINTER(LayerXfer), u32, u32]),
     "pf_load_layers": (i32, [vp, ctypes.POINTER(LayerXfer), u32, u32, pvp]),
+    "pf_load_layers_marked": (i32, [vp, ctypes.POINTER(LayerXfer), u32, u32,
+                                    ctypes.POINTER(LayerSignal), u32]),
+    "pf_stream_wait_word": (i32, [vp, u64, u64, u32, u64]),
+    "pf_host_wait_word": (i32, [vp, u64, u64, pi32]),
     "pf_fill_random": (i32, [u64, u64, u64, u64, vp]),
     "pf_verify_random": (i32, [u64, u64, u64, u64, pu64]),
     "pf_verify_random_chunks": (i32, [pu64, pu64, u64, u64, u64, pu64]),
@@ -236,6 +269,9 @@ SIGNATURES = {
     "pf_load_state_event_handles": (vp, [vp, ctypes.POINTER(ctypes.c_uint32)]),
     "pf_load_state_events_recorded": (i64, [vp]),
     "pf_load_state_set_events_recorded": (None, [vp, i64]),
+    "pf_load_state_create_layered_words": (i32, [u32, ctypes.POINTER(LayerWords), pvp]),
+    "pf_load_state_layer_words": (i32, [vp, ctypes.POINTER(LayerWords),
+                                        ctypes.POINTER(ctypes.c_uint32)]),
     "pf_allocator_create": (i32, [u64, u64, pvp]),
     "pf_allocator_create_auto": (i32, [u64, pvp]),
     "pf_allocator_destroy": (i32, [vp]),

@@ -34,11 +34,44 @@ struct ChunkDesc {
   uint64_t dst;
 };
 
+// Where a load marks each finished layer: word[layer] of each target is set
+// to that target's value.  Bit i of host_mask: target i is host memory.
+constexpr uint32_t kMaxSignalTargets = PF_MAX_LAYER_SIGNALS;
+struct SignalTargets {
+  uint64_t words[kMaxSignalTargets];
+  uint64_t value[kMaxSignalTargets];
+  uint32_t host_mask;
+  uint32_t count;
+};
+
+// The layers of one marking launch: chunks [chunk_start[g], chunk_start[g+1])
+// of the launch belong to call layer layer[g] (every group non-empty);
+// counters[layer] counts finished tiles and is 0 between launches.
+struct LayerMarks {
+  const uint32_t* chunk_start;  // n + 1 entries, device memory
+  const uint32_t* layer;        // n entries, device memory
+  uint32_t n;
+  uint32_t* counters;
+  SignalTargets targets;
+};
+
+// Layers marked by mark_layers_kernel (passed by value).
+constexpr uint32_t kLayerListMax = 64;
+struct LayerList {
+  uint32_t n;
+  uint32_t ids[kLayerListMax];
+};
+
 // Kernel launchers (pf_kernels.hip).
 hipError_t launch_copy_chunks(const ChunkDesc* d_descs, uint32_t n_chunks,
                               uint64_t chunk_bytes, bool aligned16,
                               uint32_t threads, uint32_t unroll,
-                              uint32_t max_grid, hipStream_t stream);
+                              uint32_t max_grid, const LayerMarks* marks,
+                              hipStream_t stream);
+hipError_t launch_mark_layers(const LayerList& list, const SignalTargets& t,
+                              hipStream_t stream);
+hipError_t launch_wait_word(uint64_t word, uint64_t value, uint64_t max_ticks,
+                            uint64_t timed_out, hipStream_t stream);
 hipError_t launch_fill_random(uint64_t dst, uint64_t size_bytes, uint64_t seed,
                               uint64_t word_offset, hipStream_t stream);
 hipError_t launch_verify_random(uint64_t addr, uint64_t size_bytes,
@@ -97,5 +130,10 @@ int segment_offset(const pf_kv_layout& l, uint64_t block, uint64_t seg,
 // copy and must not use the bytes before the wait.
 int save_layers_begin(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
                       uint32_t mode);
+
+// Writes the signal's value into all num_layers words on the context's
+// stream and waits: releases consumers of a load that failed before its
+// marks were written.
+int mark_all_layers(pf_xfer* x, const pf_layer_signal& signal, uint32_t num_layers);
 
 }  // namespace pf

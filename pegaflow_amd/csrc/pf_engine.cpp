@@ -389,11 +389,6 @@ uint64_t BlockStore::inflight_count() {
 // Device worker: one save context (used by the calling thread) and one load
 // thread with its own context (gpu_worker.rs:52-201).
 // ===========================================================================
-// Smallest load split into per-layer launches for a layered LoadState: 16
-// MiB is about 0.3 ms on a PCIe Gen5 x16 link, below which every layer lands
-// within a fraction of a millisecond anyway.
-constexpr uint64_t kPerLayerMinBytes = 16ull << 20;
-
 struct LoadTask {
   std::vector<std::string> names;
   std::vector<pf_kv_layout> layouts;
@@ -402,6 +397,12 @@ struct LoadTask {
   pf_load_state* state = nullptr;
   uint32_t mode = PF_MODE_KERNEL;
   uint64_t bytes = 0;
+  // A task that only writes a consumer's layer words (a load that failed in
+  // planning or had nothing to copy): queued behind the device's earlier
+  // loads so it cannot end their waits early.
+  bool marks_only = false;
+  pf_layer_words words{};
+  uint32_t n_words = 0;
   std::chrono::steady_clock::time_point submitted = std::chrono::steady_clock::now();
 };
 
@@ -431,9 +432,23 @@ class DeviceWorker {
   bool stop_ = false;
   std::thread thread_;
   std::vector<hipEvent_t> events_;
+  // Per-layer completion of marked loads: one word per layer in pinned host
+  // memory, set to the load's ticket by the copy kernel.
+  uint64_t* host_words_ = nullptr;
+  size_t host_words_cap_ = 0;
+  uint64_t ticket_ = 0;
+  // Consumers' layer words mapped from other processes, by handle (the
+  // mappings are kept for reuse; the oldest is closed beyond kMaxWordMaps).
+  std::deque<std::pair<std::string, uint64_t>> word_maps_;
   std::atomic<uint64_t>* loaded_bytes_ = nullptr;
   std::atomic<uint64_t>* failures_ = nullptr;
+
+  int map_layer_words(const pf_layer_words& w, uint64_t* words);
+  int load_marked(const std::vector<pf_layer_xfer>& layers, uint32_t mode, pf_load_state* st,
+                  uint64_t consumer_words, uint64_t consumer_value);
 };
+
+constexpr size_t kMaxWordMaps = 16;
 
 int DeviceWorker::create(int device, bool with_gpu, std::shared_ptr<DeviceWorker>* out,
                          std::atomic<uint64_t>* loaded_bytes, std::atomic<uint64_t>* failures) {
@@ -462,12 +477,91 @@ DeviceWorker::~DeviceWorker() {
   }
   q_cv_.notify_all();
   if (thread_.joinable()) thread_.join();
+  if (save_x_) pf_xfer_destroy(save_x_);
+  if (load_x_) pf_xfer_destroy(load_x_);
   if (gpu_) {
     (void)hipSetDevice(device_);
     for (hipEvent_t e : events_) (void)hipEventDestroy(e);
+    for (auto& m : word_maps_) (void)pf_ipc_close(m.second);
+    if (host_words_) (void)pf_pinned_free(host_words_);
   }
-  if (save_x_) pf_xfer_destroy(save_x_);
-  if (load_x_) pf_xfer_destroy(load_x_);
+}
+
+// Address of the consumer's layer words in this process.
+int DeviceWorker::map_layer_words(const pf_layer_words& w, uint64_t* words) {
+  if (w.kind == PF_LAYER_WORDS_LOCAL) {
+    *words = w.address;
+    return PF_OK;
+  }
+  std::string key(reinterpret_cast<const char*>(w.handle), PF_IPC_HANDLE_BYTES);
+  key.append(reinterpret_cast<const char*>(&w.alloc_size), sizeof(w.alloc_size));
+  for (auto& m : word_maps_)
+    if (m.first == key) {
+      *words = m.second + w.offset;
+      return PF_OK;
+    }
+  uint64_t base = 0;
+  if (int rc = pf_ipc_open(w.handle, w.alloc_size, &base)) return rc;
+  if (word_maps_.size() >= kMaxWordMaps) {
+    (void)pf_ipc_close(word_maps_.front().second);
+    word_maps_.pop_front();
+  }
+  word_maps_.emplace_back(std::move(key), base);
+  *words = base + w.offset;
+  return PF_OK;
+}
+
+// One launch for every layer (from pinned memory); layer l is published in
+// the LoadState as soon as the kernel has marked it.  The host words are
+// polled in order; a stream that went idle with a word unset means the copy
+// failed.
+int DeviceWorker::load_marked(const std::vector<pf_layer_xfer>& layers, uint32_t mode,
+                              pf_load_state* st, uint64_t consumer_words,
+                              uint64_t consumer_value) {
+  const size_t L = layers.size();
+  if (L > host_words_cap_) {
+    size_t cap = 64;
+    while (cap < L) cap <<= 1;
+    if (host_words_) (void)pf_pinned_free(host_words_);
+    host_words_ = nullptr;
+    host_words_cap_ = 0;
+    void* h = nullptr;
+    uint64_t d = 0;
+    if (int rc = pf_pinned_allocate(cap * 8, PF_PINNED_COHERENT, &h, &d)) return rc;
+    host_words_ = static_cast<uint64_t*>(h);
+    std::memset(host_words_, 0, cap * 8);
+    host_words_cap_ = cap;
+  }
+  const uint64_t ticket = ++ticket_;
+  pf_layer_signal sig[2] = {};
+  sig[0].words = reinterpret_cast<uint64_t>(host_words_);
+  sig[0].value = ticket;
+  sig[0].host_memory = 1;
+  uint32_t n_sig = 1;
+  if (consumer_words) {
+    sig[1].words = consumer_words;
+    sig[1].value = consumer_value;
+    n_sig = 2;
+  }
+  if (int rc = pf_load_layers_marked(load_x_, layers.data(), static_cast<uint32_t>(L), mode,
+                                     sig, n_sig))
+    return rc;
+  hipStream_t stream = static_cast<hipStream_t>(pf_xfer_stream(load_x_));
+  for (size_t l = 0; l < L; ++l) {
+    const uint64_t* w = host_words_ + l;
+    for (uint32_t spins = 0; __atomic_load_n(w, __ATOMIC_ACQUIRE) < ticket; ++spins) {
+      if (spins % 64 == 63) {
+        const hipError_t q = hipStreamQuery(stream);
+        if (q != hipErrorNotReady && __atomic_load_n(w, __ATOMIC_ACQUIRE) < ticket)
+          return fail(PF_ERR_STORAGE,
+                      strf("layer %zu of a marked load was not marked (%s)", l,
+                           hipGetErrorString(q)));
+      }
+      if (spins > 256) std::this_thread::sleep_for(std::chrono::microseconds(10));
+    }
+    pf_load_state_set_layers_done(st, static_cast<int64_t>(l + 1));
+  }
+  return pf_xfer_synchronize(load_x_);
 }
 
 int DeviceWorker::save(const std::vector<pf_layer_xfer>& layers, uint32_t mode,
@@ -518,6 +612,21 @@ void DeviceWorker::load_loop() {
       task = std::move(queue_.front());
       queue_.pop_front();
     }
+    if (task.marks_only) {
+      uint64_t words = 0;
+      if (task.n_words > 0 && map_layer_words(task.words, &words) == PF_OK) {
+        pf_layer_signal all{};
+        all.words = words;
+        all.value = task.words.value;
+        (void)mark_all_layers(load_x_, all, task.n_words);
+      }
+      {
+        std::lock_guard<std::mutex> lk(q_mu_);
+        --busy_;
+      }
+      idle_cv_.notify_all();
+      continue;
+    }
     const auto t_begin = std::chrono::steady_clock::now();
     const size_t L = task.layouts.size();
     bool ok = true;
@@ -551,16 +660,31 @@ void DeviceWorker::load_loop() {
         if (ok) ipc_evs.push_back(ev);
       }
     }
-    // Layer-by-layer launches (each followed by its event) cost a kernel
-    // tail per layer, about 1.6 ms over the 32 layers of a Llama prefix.
-    // They are used only where someone can use a layer early: a layered
-    // LoadState with enough bytes that a layer lands well before the load
-    // ends, or a consumer's interprocess events.  Otherwise one launch
-    // covers every layer and completion is published at its end.
-    const bool per_layer =
-        !ipc_evs.empty() ||
-        (pf_load_state_num_layers(task.state) > 0 && task.bytes >= kPerLayerMinBytes);
-    if (ok && L > 0 && !per_layer) {
+    // A consumer's layer words (device-side gating without interprocess
+    // events) are marked by the same launch as the engine's own host words.
+    pf_layer_words lw{};
+    uint32_t n_words = 0;
+    uint64_t consumer_words = 0;
+    (void)pf_load_state_layer_words(task.state, &lw, &n_words);
+    if (n_words > 0) {
+      if (map_layer_words(lw, &consumer_words) != PF_OK) {
+        ok = false;
+      } else if (n_words != L) {
+        set_error(strf("storage error: LoadState carries words for %u layers, load has %zu",
+                       n_words, L));
+        ok = false;
+      }
+    }
+    // Per-layer completion is published only where someone can use a layer
+    // early: a layered LoadState (marks written by the one launch) or a
+    // consumer's interprocess events (one launch per layer, each followed by
+    // its event).  Otherwise completion is published at the end.
+    const bool marked = ipc_evs.empty() && (pf_load_state_num_layers(task.state) > 0);
+    const bool per_layer = !ipc_evs.empty();
+    if (ok && L > 0 && marked) {
+      ok = load_marked(layers, task.mode, task.state, consumer_words, lw.value) == PF_OK;
+      if (!ok) (void)pf_xfer_synchronize(load_x_);
+    } else if (ok && L > 0 && !per_layer) {
       ok = pf_load_layers(load_x_, layers.data(), static_cast<uint32_t>(L), task.mode,
                           nullptr) == PF_OK &&
            pf_xfer_synchronize(load_x_) == PF_OK;
@@ -581,14 +705,22 @@ void DeviceWorker::load_loop() {
       if (!ok) (void)pf_xfer_synchronize(load_x_);
     }
     for (pf_event ev : ipc_evs) (void)pf_event_destroy(ev);
+    // A failed load still ends the consumer's device waits (the LoadState
+    // says it failed).
+    if (!ok && consumer_words) {
+      pf_layer_signal all{};
+      all.words = consumer_words;
+      all.value = lw.value;
+      (void)mark_all_layers(load_x_, all, n_words);
+    }
     if (tracing()) {
       const auto t_end = std::chrono::steady_clock::now();
       std::fprintf(stderr,
                    "[pegaflow] load device=%d layers=%zu bytes=%llu queued=%.0fus copy=%.0fus "
-                   "(%.2f GB/s) per_layer=%d ok=%d\n",
+                   "(%.2f GB/s) marked=%d per_layer_events=%d ok=%d\n",
                    device_, L, (unsigned long long)task.bytes, us_between(task.submitted, t_begin),
                    us_between(t_begin, t_end), task.bytes / us_between(t_begin, t_end) / 1e3,
-                   (int)per_layer, (int)ok);
+                   (int)marked, (int)per_layer, (int)ok);
     }
     if (ok) {
       pf_load_state_set_completed(task.state);
@@ -1089,14 +1221,27 @@ int pf_engine_batch_load(pf_engine* e, const char* instance_id, uint64_t tp_rank
   pf_load_state* state = nullptr;
   if (pf_load_state_attach(load_state_shm, &state))
     return fail(PF_ERR_LOAD_STATE, std::string("storage error: LoadState: ") + pf_last_error());
+  std::shared_ptr<GpuContext> gpu;
+  // A consumer's layer words are written even when nothing is copied, so
+  // its device waits end; the LoadState says what happened.
+  auto release_words = [&]() {
+    LoadTask marks;
+    marks.marks_only = true;
+    (void)pf_load_state_layer_words(state, &marks.words, &marks.n_words);
+    if (marks.n_words == 0 || !gpu) return;
+    const std::string err = pf_last_error();
+    (void)gpu->worker->submit(std::move(marks));
+    set_error(err);
+  };
   auto bail = [&](int code) {
     pf_load_state_set_error(state);
+    release_words();
     pf_load_state_close(state);
     return code;
   };
   std::shared_ptr<Instance> inst;
   if (int rc = get_instance(e, instance_id, &inst)) return bail(rc);
-  auto gpu = inst->gpu(device_id);
+  gpu = inst->gpu(device_id);
   if (!gpu)
     return bail(fail(PF_ERR_WORKER_MISSING,
                      strf("device %d not found in instance %s", device_id, instance_id)));
@@ -1146,6 +1291,7 @@ int pf_engine_batch_load(pf_engine* e, const char* instance_id, uint64_t tp_rank
   }
   if (!any) {  // lib.rs:1055-1060
     pf_load_state_set_completed(state);
+    release_words();
     pf_load_state_close(state);
     return PF_OK;
   }

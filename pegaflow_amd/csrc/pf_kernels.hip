@@ -63,11 +63,76 @@ __device__ __forceinline__ uint32_t tile_of(uint32_t b, uint32_t n, bool xcd_maj
   return x * q + (x < r ? x : r) + i;
 }
 
-template <int UNROLL, bool NTL, bool NTS>
+// ---------------------------------------------------------------------------
+// Layer completion marks.  A load that covers several layers in one launch
+// can still report each layer as soon as its bytes are in place: every
+// workgroup, after its stores, bumps its layer's tile counter, and the
+// workgroup that brings the counter to the layer's tile count writes the
+// call's value into word[layer] of each signal target (host-mapped pinned
+// memory, device memory, or another process's IPC-mapped device memory).
+//
+// Visibility.  Each XCD has its own L2, so a byte stored by one workgroup is
+// visible to readers on other XCDs only once it has left that L2.  A
+// release fence at agent scope per workgroup would write the whole L2 back
+// every time (measured: 2.2x slower from pinned memory, 40x from HBM).
+// Instead the marking kernel stores its bytes as agent-scope relaxed atomic
+// stores, which write through the L2 to the device's coherence point (the
+// sc1 policy), and waits for every store's acknowledgement (s_waitcnt 0)
+// before the workgroup barrier; only then does one lane bump the counter
+// (an agent-scope atomic).  The finishing workgroup acquires at agent scope,
+// puts the counter back to 0 (ready for the next launch on the stream) and
+// writes the marks as release stores, at system scope for host memory.  A
+// reader that sees word[layer] == value and then acquires, or starts a
+// kernel afterwards, sees every byte of that layer.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void write_marks(const SignalTargets& t, uint32_t layer) {
+  for (uint32_t i = 0; i < t.count; ++i) {
+    uint64_t* w = reinterpret_cast<uint64_t*>(t.words[i]) + layer;
+    if ((t.host_mask >> i) & 1u)
+      __hip_atomic_store(w, t.value[i], __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    else
+      __hip_atomic_store(w, t.value[i], __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// 16 bytes as two agent-coherent (write-through) 8-byte stores.
+__device__ __forceinline__ void store16_coherent(g_u32x4* p, u32x4 v) {
+  g_u64* q = reinterpret_cast<g_u64*>(p);
+  __hip_atomic_store(q, static_cast<uint64_t>(v.x) | (static_cast<uint64_t>(v.y) << 32),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(q + 1, static_cast<uint64_t>(v.z) | (static_cast<uint64_t>(v.w) << 32),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Called by one lane per workgroup once the workgroup's stores of chunk c are
+// acknowledged.  marks.chunk_start[0..n] are the launch-relative first
+// chunks of its layers (increasing, chunk_start[0] == 0 <= c <
+// chunk_start[n]); the search keeps chunk_start[lo] <= c < chunk_start[hi].
+__device__ __forceinline__ void tile_done(const LayerMarks& m, uint32_t c,
+                                          uint32_t tiles_per_chunk) {
+  uint32_t lo = 0, hi = m.n;
+  while (hi - lo > 1) {
+    const uint32_t mid = (lo + hi) >> 1;
+    if (m.chunk_start[mid] <= c) lo = mid;
+    else hi = mid;
+  }
+  const uint32_t layer = m.layer[lo];
+  const uint32_t tiles = (m.chunk_start[lo + 1] - m.chunk_start[lo]) * tiles_per_chunk;
+  uint32_t* cnt = m.counters + layer;
+  const uint32_t prev = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+  if (prev + 1 == tiles) {
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    write_marks(m.targets, layer);
+  }
+}
+
+template <int UNROLL, bool NTL, bool NTS, bool MARK>
 __global__ void __launch_bounds__(1024)
 copy_chunks_v16_kernel(const ChunkDesc* __restrict__ descs,
                        uint32_t tiles_per_chunk, uint32_t n_tiles,
-                       uint32_t chunk16, uint32_t xcd_major) {
+                       uint32_t chunk16, uint32_t xcd_major, LayerMarks marks) {
   const uint32_t stride = blockDim.x;
   const uint32_t tile_elems = stride * UNROLL;
   const bool remap = xcd_major && gridDim.x == n_tiles;
@@ -85,7 +150,10 @@ copy_chunks_v16_kernel(const ChunkDesc* __restrict__ descs,
 #pragma unroll
       for (int u = 0; u < UNROLL; ++u) v[u] = load16<NTL>(src + base + u * stride);
 #pragma unroll
-      for (int u = 0; u < UNROLL; ++u) store16<NTS>(dst + base + u * stride, v[u]);
+      for (int u = 0; u < UNROLL; ++u) {
+        if constexpr (MARK) store16_coherent(dst + base + u * stride, v[u]);
+        else store16<NTS>(dst + base + u * stride, v[u]);
+      }
     } else {
       // Partial last tile of a chunk: guarded per element.
 #pragma unroll
@@ -96,9 +164,41 @@ copy_chunks_v16_kernel(const ChunkDesc* __restrict__ descs,
 #pragma unroll
       for (int u = 0; u < UNROLL; ++u) {
         const uint32_t e = base + u * stride;
-        if (e < chunk16) store16<NTS>(dst + e, v[u]);
+        if (e < chunk16) {
+          if constexpr (MARK) store16_coherent(dst + e, v[u]);
+          else store16<NTS>(dst + e, v[u]);
+        }
       }
     }
+    if constexpr (MARK) {
+      __builtin_amdgcn_s_waitcnt(0);  // every store of this wave acknowledged
+      __syncthreads();
+      if (threadIdx.x == 0) tile_done(marks, c, tiles_per_chunk);
+    }
+  }
+}
+
+// Marks the listed layers (layers with nothing to copy, and layers copied by
+// DMA earlier on the same stream).
+__global__ void mark_layers_kernel(LayerList list, SignalTargets t) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < list.n) write_marks(t, list.ids[i]);
+}
+
+// Bounded device-side wait: lane 0 polls *word until it reaches `value` or
+// `max_ticks` of the device wall clock have passed, so the wave always ends.
+// On a timeout *timed_out (if given) is set to 1.
+__global__ void wait_word_kernel(const uint64_t* word, uint64_t value, uint64_t max_ticks,
+                                 uint32_t* timed_out) {
+  if (threadIdx.x != 0) return;
+  const uint64_t start = static_cast<uint64_t>(wall_clock64());
+  while (__hip_atomic_load(word, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM) < value) {
+    if (static_cast<uint64_t>(wall_clock64()) - start >= max_ticks) {
+      if (timed_out)
+        __hip_atomic_store(timed_out, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      return;
+    }
+    __builtin_amdgcn_s_sleep(2);
   }
 }
 
@@ -119,34 +219,40 @@ static constexpr uint32_t kMaxGrid = 1u << 20;
 
 template <int UNROLL, bool NTL, bool NTS>
 static void launch_v16_nt(dim3 grid, dim3 block, hipStream_t stream, const ChunkDesc* d,
-                          uint32_t tpc, uint32_t n_tiles, uint32_t c16, uint32_t xcd) {
-  hipLaunchKernelGGL((copy_chunks_v16_kernel<UNROLL, NTL, NTS>), grid, block, 0, stream, d,
-                     tpc, n_tiles, c16, xcd);
+                          uint32_t tpc, uint32_t n_tiles, uint32_t c16, uint32_t xcd,
+                          const LayerMarks* marks) {
+  if (marks)
+    hipLaunchKernelGGL((copy_chunks_v16_kernel<UNROLL, NTL, NTS, true>), grid, block, 0,
+                       stream, d, tpc, n_tiles, c16, xcd, *marks);
+  else
+    hipLaunchKernelGGL((copy_chunks_v16_kernel<UNROLL, NTL, NTS, false>), grid, block, 0,
+                       stream, d, tpc, n_tiles, c16, xcd, LayerMarks{});
 }
 
 template <int UNROLL>
 static hipError_t launch_v16(const ChunkDesc* d_descs, uint32_t tiles_per_chunk,
                              uint32_t n_tiles, uint32_t chunk16, uint32_t threads,
-                             uint32_t flags, uint32_t max_grid, hipStream_t stream) {
+                             uint32_t flags, uint32_t max_grid, const LayerMarks* marks,
+                             hipStream_t stream) {
   const uint32_t cap = max_grid ? max_grid : kMaxGrid;
   const dim3 grid(n_tiles < cap ? n_tiles : cap), block(threads);
   const uint32_t xcd = (flags & PF_KERNEL_XCD_MAJOR) ? 1u : 0u;
   switch (flags & PF_KERNEL_NONTEMPORAL) {
     case 0:
       launch_v16_nt<UNROLL, false, false>(grid, block, stream, d_descs, tiles_per_chunk, n_tiles,
-                                          chunk16, xcd);
+                                          chunk16, xcd, marks);
       break;
     case PF_KERNEL_NT_LOADS:
       launch_v16_nt<UNROLL, true, false>(grid, block, stream, d_descs, tiles_per_chunk, n_tiles,
-                                         chunk16, xcd);
+                                         chunk16, xcd, marks);
       break;
     case PF_KERNEL_NT_STORES:
       launch_v16_nt<UNROLL, false, true>(grid, block, stream, d_descs, tiles_per_chunk, n_tiles,
-                                         chunk16, xcd);
+                                         chunk16, xcd, marks);
       break;
     default:
       launch_v16_nt<UNROLL, true, true>(grid, block, stream, d_descs, tiles_per_chunk, n_tiles,
-                                        chunk16, xcd);
+                                        chunk16, xcd, marks);
       break;
   }
   return hipGetLastError();
@@ -154,21 +260,27 @@ static hipError_t launch_v16(const ChunkDesc* d_descs, uint32_t tiles_per_chunk,
 
 // `unroll` carries the loads in flight per lane (low byte) and the
 // PF_KERNEL_NT_LOADS / PF_KERNEL_NT_STORES / PF_KERNEL_XCD_MAJOR flags.
+// `marks` (16-byte path only) makes the kernel mark each layer's completion.
 hipError_t launch_copy_chunks(const ChunkDesc* d_descs, uint32_t n_chunks,
                               uint64_t chunk_bytes, bool aligned16,
                               uint32_t threads, uint32_t unroll,
-                              uint32_t max_grid, hipStream_t stream) {
+                              uint32_t max_grid, const LayerMarks* marks,
+                              hipStream_t stream) {
   if (n_chunks == 0 || chunk_bytes == 0) return hipSuccess;
   if (threads == 0 || threads > 1024 || threads % 64 != 0) return hipErrorInvalidValue;
   const uint32_t flags = unroll & (PF_KERNEL_NONTEMPORAL | PF_KERNEL_XCD_MAJOR);
   unroll &= 0xffu;
   if (max_grid > kMaxGrid) max_grid = kMaxGrid;
   if (!aligned16) {
+    if (marks) return hipErrorInvalidValue;
     const uint32_t grid = n_chunks < kMaxGrid ? n_chunks : kMaxGrid;
     hipLaunchKernelGGL(copy_chunks_b1_kernel, dim3(grid), dim3(threads), 0,
                        stream, d_descs, n_chunks, chunk_bytes);
     return hipGetLastError();
   }
+  if (marks && (marks->n == 0 || !marks->chunk_start || !marks->layer || !marks->counters ||
+                marks->targets.count == 0 || marks->targets.count > kMaxSignalTargets))
+    return hipErrorInvalidValue;
   const uint64_t chunk16 = chunk_bytes / 16;
   if (chunk16 >= (1ull << 31)) return hipErrorInvalidValue;
   const uint64_t tile_elems = static_cast<uint64_t>(threads) * unroll;
@@ -184,13 +296,31 @@ hipError_t launch_copy_chunks(const ChunkDesc* d_descs, uint32_t n_chunks,
   const uint32_t ntl = static_cast<uint32_t>(n_tiles);
   const uint32_t c16 = static_cast<uint32_t>(chunk16);
   switch (unroll) {
-    case 1: return launch_v16<1>(d_descs, tpc, ntl, c16, threads, flags, max_grid, stream);
-    case 2: return launch_v16<2>(d_descs, tpc, ntl, c16, threads, flags, max_grid, stream);
-    case 4: return launch_v16<4>(d_descs, tpc, ntl, c16, threads, flags, max_grid, stream);
-    case 8: return launch_v16<8>(d_descs, tpc, ntl, c16, threads, flags, max_grid, stream);
-    case 16: return launch_v16<16>(d_descs, tpc, ntl, c16, threads, flags, max_grid, stream);
+    case 1: return launch_v16<1>(d_descs, tpc, ntl, c16, threads, flags, max_grid, marks, stream);
+    case 2: return launch_v16<2>(d_descs, tpc, ntl, c16, threads, flags, max_grid, marks, stream);
+    case 4: return launch_v16<4>(d_descs, tpc, ntl, c16, threads, flags, max_grid, marks, stream);
+    case 8: return launch_v16<8>(d_descs, tpc, ntl, c16, threads, flags, max_grid, marks, stream);
+    case 16:
+      return launch_v16<16>(d_descs, tpc, ntl, c16, threads, flags, max_grid, marks, stream);
     default: return hipErrorInvalidValue;
   }
+}
+
+hipError_t launch_mark_layers(const LayerList& list, const SignalTargets& t,
+                              hipStream_t stream) {
+  if (list.n == 0) return hipSuccess;
+  if (list.n > kLayerListMax || t.count == 0 || t.count > kMaxSignalTargets)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(mark_layers_kernel, dim3(1), dim3(kLayerListMax), 0, stream, list, t);
+  return hipGetLastError();
+}
+
+hipError_t launch_wait_word(uint64_t word, uint64_t value, uint64_t max_ticks,
+                            uint64_t timed_out, hipStream_t stream) {
+  hipLaunchKernelGGL(wait_word_kernel, dim3(1), dim3(64), 0, stream,
+                     reinterpret_cast<const uint64_t*>(word), value, max_ticks,
+                     reinterpret_cast<uint32_t*>(timed_out));
+  return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------

@@ -18,6 +18,14 @@
 //   count 64-byte interprocess event handles, one per layer; the loader
 //   records layer l's event after layer l's copy and then publishes
 //   events_recorded = count, after which a consumer can wait on the device.
+// Words block (optional, instead of the event block), at byte 48:
+//   u32 magic 0x50464C57 ('PFLW'), u32 count, u64 value, u32 kind,
+//   u32 reserved, u64 address, u64 alloc_size, u64 offset, 64-byte IPC
+//   memory handle (112 bytes): count 8-byte words of device memory, one per
+//   layer, that the loader sets to value once that layer's bytes are in
+//   place.  kind 0: the words are at offset in the allocation exported as
+//   handle (alloc_size bytes); kind 1: at address in the loader's own
+//   process.
 #include <fcntl.h>
 #include <sys/mman.h>
 #include <sys/stat.h>
@@ -70,6 +78,20 @@ struct EvRecord {
 };
 static_assert(sizeof(EvRecord) == kEvSize, "event block layout");
 
+constexpr uint32_t kWordsMagic = 0x50464C57u;  // 'PFLW'
+struct WordsRecord {
+  uint32_t magic;
+  uint32_t count;
+  uint64_t value;
+  uint32_t kind;
+  uint32_t reserved;
+  uint64_t address;
+  uint64_t alloc_size;
+  uint64_t offset;
+  uint8_t handle[kHandleBytes];
+};
+static_assert(sizeof(WordsRecord) == 112, "words block layout");
+
 std::string random_name() {
   // "pega_load_" + uuid-v4 in simple (32 lowercase hex) form (sync_state.rs:126).
   std::random_device rd;
@@ -99,18 +121,35 @@ struct pf_load_state {
   Record* rec = nullptr;
   ExtRecord* ext = nullptr;
   EvRecord* ev = nullptr;
+  WordsRecord* words = nullptr;
 };
 
 namespace {
 
 int create_state(uint32_t num_layers, bool layered, const uint8_t* handles,
-                 pf_load_state** out) {
+                 const pf_layer_words* words, pf_load_state** out) {
   if (!out) return fail(PF_ERR_INVALID_ARGUMENT, "null output");
   if (handles && (num_layers == 0 || num_layers > kMaxEvents))
     return fail(PF_ERR_INVALID_ARGUMENT,
                 strf("a LoadState carries 1..%u layer events, got %u", kMaxEvents, num_layers));
+  if (words) {
+    if (num_layers == 0 || num_layers > kMaxEvents)
+      return fail(PF_ERR_INVALID_ARGUMENT,
+                  strf("a LoadState carries words for 1..%u layers, got %u", kMaxEvents,
+                       num_layers));
+    if (words->value == 0 || words->kind > PF_LAYER_WORDS_LOCAL || words->reserved != 0 ||
+        (words->kind == PF_LAYER_WORDS_LOCAL ? (words->address & 7u) != 0
+                                             : (words->offset & 7u) != 0 ||
+                                                   words->alloc_size < words->offset ||
+                                                   (words->alloc_size - words->offset) / 8 <
+                                                       num_layers))
+      return fail(PF_ERR_INVALID_ARGUMENT,
+                  "layer words: value must be nonzero, words 8-byte aligned and inside the "
+                  "allocation");
+  }
   const size_t size = handles ? kEvOffset + kEvSize + num_layers * kHandleBytes
-                              : layered ? kExtOffset + kExtSize : kAllocSize;
+                      : words ? kEvOffset + sizeof(WordsRecord)
+                      : layered ? kExtOffset + kExtSize : kAllocSize;
   std::string name;
   int fd = -1;
   for (int attempt = 0; attempt < 8 && fd < 0; ++attempt) {
@@ -164,6 +203,19 @@ int create_state(uint32_t num_layers, bool layered, const uint8_t* handles,
     __atomic_store_n(&st->ev->recorded, (int64_t)0, __ATOMIC_RELEASE);
     __atomic_store_n(&st->ev->magic, kEvMagic, __ATOMIC_RELEASE);
   }
+  if (words) {
+    st->words = reinterpret_cast<WordsRecord*>(base + kEvOffset);
+    WordsRecord* w = st->words;
+    w->count = num_layers;
+    w->value = words->value;
+    w->kind = words->kind;
+    w->reserved = 0;
+    w->address = words->address;
+    w->alloc_size = words->alloc_size;
+    w->offset = words->offset;
+    std::memcpy(w->handle, words->handle, kHandleBytes);
+    __atomic_store_n(&w->magic, kWordsMagic, __ATOMIC_RELEASE);
+  }
   *out = st;
   return PF_OK;
 }
@@ -172,16 +224,24 @@ int create_state(uint32_t num_layers, bool layered, const uint8_t* handles,
 
 extern "C" {
 
-int pf_load_state_create(pf_load_state** out) { return create_state(0, false, nullptr, out); }
+int pf_load_state_create(pf_load_state** out) {
+  return create_state(0, false, nullptr, nullptr, out);
+}
 
 int pf_load_state_create_layered(uint32_t num_layers, pf_load_state** out) {
-  return create_state(num_layers, true, nullptr, out);
+  return create_state(num_layers, true, nullptr, nullptr, out);
 }
 
 int pf_load_state_create_layered_events(uint32_t num_layers, const uint8_t* event_handles,
                                         pf_load_state** out) {
   if (!event_handles) return fail(PF_ERR_INVALID_ARGUMENT, "null event handles");
-  return create_state(num_layers, true, event_handles, out);
+  return create_state(num_layers, true, event_handles, nullptr, out);
+}
+
+int pf_load_state_create_layered_words(uint32_t num_layers, const pf_layer_words* words,
+                                       pf_load_state** out) {
+  if (!words) return fail(PF_ERR_INVALID_ARGUMENT, "null layer words");
+  return create_state(num_layers, true, nullptr, words, out);
 }
 
 // LoadState::attach + attach_mapping + validate_header (sync_state.rs:145-155,
@@ -255,6 +315,12 @@ int pf_load_state_attach(const char* shm_name, pf_load_state** out) {
         count <= kMaxEvents && len >= kEvOffset + kEvSize + count * kHandleBytes)
       st->ev = ev;
   }
+  if (st->ext && len >= kEvOffset + sizeof(WordsRecord)) {
+    WordsRecord* w = reinterpret_cast<WordsRecord*>(base + kEvOffset);
+    if (__atomic_load_n(&w->magic, __ATOMIC_ACQUIRE) == kWordsMagic && w->count > 0 &&
+        w->count <= kMaxEvents && w->value != 0 && w->kind <= PF_LAYER_WORDS_LOCAL)
+      st->words = w;
+  }
   *out = st;
   return PF_OK;
 }
@@ -313,6 +379,25 @@ int64_t pf_load_state_events_recorded(const pf_load_state* st) {
 
 void pf_load_state_set_events_recorded(pf_load_state* st, int64_t n) {
   if (st->ev) __atomic_store_n(&st->ev->recorded, n, __ATOMIC_RELEASE);
+}
+
+int pf_load_state_layer_words(const pf_load_state* st, pf_layer_words* out, uint32_t* count) {
+  if (!st->words) {
+    if (count) *count = 0;
+    return PF_OK;
+  }
+  if (out) {
+    const WordsRecord* w = st->words;
+    out->kind = w->kind;
+    out->reserved = 0;
+    out->value = w->value;
+    out->address = w->address;
+    out->alloc_size = w->alloc_size;
+    out->offset = w->offset;
+    std::memcpy(out->handle, w->handle, kHandleBytes);
+  }
+  if (count) *count = st->words->count;
+  return PF_OK;
 }
 
 }  // extern "C"

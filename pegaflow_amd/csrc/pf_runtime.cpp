@@ -1,6 +1,7 @@
 // pf_runtime.cpp — devices, streams, events, device memory and the pinned
 // host pool backing (the roles of cudarc's CudaContext/CudaStream and of
 // pegaflow-core/src/pinned_mem.rs in the reference).
+#include <chrono>
 #include <cstdio>
 #include <cstring>
 #include <fstream>
@@ -8,6 +9,7 @@
 #include <mutex>
 #include <sstream>
 #include <string>
+#include <thread>
 
 #include "pf_common.h"
 
@@ -548,6 +550,40 @@ int pf_compare(uint64_t a, uint64_t b, uint64_t size_bytes,
   if (int rc = check_range(a, size_bytes, "compare")) return rc;
   if (int rc = check_range(b, size_bytes, "compare")) return rc;
   return run_count_kernel(1, a, b, size_bytes, 0, 0, mismatches);
+}
+
+int pf_stream_wait_word(pf_stream stream, uint64_t word, uint64_t value, uint32_t timeout_us,
+                        uint64_t timed_out) {
+  if ((word & 7u) != 0 || (timed_out & 3u) != 0)
+    return fail(PF_ERR_INVALID_ARGUMENT, "wait word must be 8-byte aligned, timeout flag 4-byte");
+  if (timeout_us > 60u * 1000u * 1000u)
+    return fail(PF_ERR_INVALID_ARGUMENT, "wait timeout above 60 s");
+  if (int rc = check_range(word, 8, "wait word")) return rc;
+  if (timed_out)
+    if (int rc = check_range(timed_out, 4, "wait timeout flag")) return rc;
+  int khz = wall_clock_khz();
+  if (khz <= 0) return fail(PF_ERR_INIT, "wall clock rate unknown (call pf_init)");
+  const uint64_t ticks = static_cast<uint64_t>(timeout_us) * static_cast<uint64_t>(khz) / 1000;
+  (void)hipGetLastError();
+  PF_HIP(launch_wait_word(word, value, ticks, timed_out, static_cast<hipStream_t>(stream)));
+  return PF_OK;
+}
+
+int pf_host_wait_word(const uint64_t* word, uint64_t value, uint64_t timeout_us, int* reached) {
+  if (!word || !reached) return fail(PF_ERR_INVALID_ARGUMENT, "null argument");
+  const auto deadline = std::chrono::steady_clock::now() + std::chrono::microseconds(timeout_us);
+  for (uint32_t spins = 0;; ++spins) {
+    if (__atomic_load_n(word, __ATOMIC_ACQUIRE) >= value) {
+      *reached = 1;
+      return PF_OK;
+    }
+    if (std::chrono::steady_clock::now() >= deadline) {
+      *reached = 0;
+      return PF_OK;
+    }
+    // Spin briefly (a layer lands every few hundred microseconds), then back off.
+    if (spins > 2000) std::this_thread::sleep_for(std::chrono::microseconds(10));
+  }
 }
 
 int pf_spin(pf_stream stream, uint32_t microseconds) {

@@ -256,6 +256,9 @@ struct pf_xfer {
   uint64_t last_dma = 0;
   bool timing = false;
   std::vector<std::pair<hipEvent_t, hipEvent_t>> timers;  // one pair per launch
+  // Per-layer tile counters of marking launches (0 between launches).
+  uint32_t* d_counters = nullptr;
+  size_t counters_cap = 0;
   std::mutex mu;
 };
 
@@ -301,7 +304,8 @@ int upload_desc(pf_xfer* x, size_t n) {
   return PF_OK;
 }
 
-int launch(pf_xfer* x, size_t first, size_t n, uint64_t chunk_bytes, bool al16, bool is_save) {
+int launch(pf_xfer* x, size_t first, size_t n, uint64_t chunk_bytes, bool al16, bool is_save,
+           const LayerMarks* marks = nullptr) {
   if (n == 0) return PF_OK;
   const int dir = is_save ? 0 : 1;
   if (n > 0xffffffffull) return fail(PF_ERR_INVALID_ARGUMENT, "too many chunks");
@@ -321,11 +325,45 @@ int launch(pf_xfer* x, size_t first, size_t n, uint64_t chunk_bytes, bool al16, 
   (void)hipGetLastError();
   hipError_t e = launch_copy_chunks(x->d_desc + first, static_cast<uint32_t>(n),
                                     chunk_bytes, al16, x->threads[dir], x->unroll[dir],
-                                    x->max_grid, x->stream);
+                                    x->max_grid, marks, x->stream);
   if (e != hipSuccess) return hip_fail(e, "gather/scatter kernel launch");
   if (tm) PF_HIP(hipEventRecord(tm->second, x->stream));
   x->last_kernels++;
   return PF_OK;
+}
+
+// Counters for marking launches over num_layers layers, zeroed on the
+// context's stream before first use.
+int ensure_counters(pf_xfer* x, size_t num_layers) {
+  if (num_layers <= x->counters_cap) return PF_OK;
+  size_t cap = 64;
+  while (cap < num_layers) cap <<= 1;
+  PF_HIP(hipStreamSynchronize(x->stream));  // earlier launches may still count
+  if (x->d_counters) PF_HIP(hipFree(x->d_counters));
+  x->d_counters = nullptr;
+  x->counters_cap = 0;
+  PF_HIP(hipMalloc(reinterpret_cast<void**>(&x->d_counters), cap * sizeof(uint32_t)));
+  PF_HIP(hipMemsetAsync(x->d_counters, 0, cap * sizeof(uint32_t), x->stream));
+  x->counters_cap = cap;
+  return PF_OK;
+}
+
+// Marks the given layers on the context's stream (after the work queued so far).
+int mark_layers(pf_xfer* x, const std::vector<uint32_t>& ids, const SignalTargets& t) {
+  for (size_t i = 0; i < ids.size(); i += kLayerListMax) {
+    LayerList list{};
+    list.n = static_cast<uint32_t>(std::min<size_t>(kLayerListMax, ids.size() - i));
+    for (uint32_t k = 0; k < list.n; ++k) list.ids[k] = ids[i + k];
+    (void)hipGetLastError();
+    hipError_t e = launch_mark_layers(list, t, x->stream);
+    if (e != hipSuccess) return hip_fail(e, "layer mark kernel launch");
+  }
+  return PF_OK;
+}
+
+int mark_layer(pf_xfer* x, uint32_t li, const SignalTargets* t) {
+  if (!t) return PF_OK;
+  return mark_layers(x, std::vector<uint32_t>{li}, *t);
 }
 
 // A staged slice: chunks [begin, end) of one layer packed into one slot.
@@ -475,7 +513,7 @@ int staged_slice(pf_xfer* x, const std::vector<LayerPlan>& plans, const Slice& s
 }
 
 int staged(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<LayerPlan>& plans,
-           bool is_save, pf_event* layer_events) {
+           bool is_save, pf_event* layer_events, const SignalTargets* sig) {
   if (x->staging == 0 || x->slot_bytes == 0)
     return fail(PF_ERR_INVALID_ARGUMENT, "transfer context has no staging buffer");
   std::vector<Slice> slices;
@@ -508,6 +546,8 @@ int staged(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<LayerPlan>
       if (int rc = staged_slice(x, plans, slices[si], is_save)) return rc;
     if (!is_save && layer_events && layer_events[li])
       PF_HIP(hipEventRecord(static_cast<hipEvent_t>(layer_events[li]), x->stream));
+    if (!is_save)
+      if (int rc = mark_layer(x, li, sig)) return rc;
   }
   if (is_save) {
     PF_HIP(hipStreamSynchronize(x->dma));
@@ -516,56 +556,132 @@ int staged(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<LayerPlan>
   return PF_OK;
 }
 
+// True when a load's sources (the host side of its chunks) lie in pinned
+// host memory, judged by the first chunk.
+bool host_sourced(const LayerPlan& p, bool is_save) {
+  uint64_t b = 0, e = 0;
+  return !is_save && !p.chunks.empty() &&
+         pinned_lookup(p.chunks[0].host, p.chunk_bytes, &b, &e);
+}
+
 // ---- kernel mode ----------------------------------------------------------
+// One step of a kernel-mode call: a DMA copy of an ordered layer, or one
+// launch over the consecutive layers [li, lj).
+struct Step {
+  size_t li, lj;
+  bool dma;
+  bool aligned;
+  size_t tab = 0;      // marked launch: u32 offset of its table in the aux area
+  uint32_t groups = 0; // marked launch: non-empty layers in it
+};
+
 int kernel_direct(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<LayerPlan>& plans,
-                  bool is_save, pf_event* layer_events, bool wait_save) {
+                  bool is_save, pf_event* layer_events, const SignalTargets* sig,
+                  bool wait_save) {
   if (int rc = check_all_kernel(layers, plans, true)) return rc;
   size_t total = 0;
-  for (const auto& p : plans)
-    if (!p.ordered) total += p.chunks.size();
-  if (int rc = ensure_desc_capacity(x, total)) return rc;
-  size_t d = 0;
   std::vector<size_t> first(plans.size());
   for (size_t li = 0; li < plans.size(); ++li) {
-    first[li] = d;
-    if (plans[li].ordered) continue;
-    for (const Chunk& c : plans[li].chunks)
-      x->h_desc[d++] = is_save ? ChunkDesc{c.dev, c.host} : ChunkDesc{c.host, c.dev};
+    first[li] = total;
+    if (!plans[li].ordered) total += plans[li].chunks.size();
   }
-  if (int rc = upload_desc(x, total)) return rc;
   // Without per-layer events, consecutive layers with the same chunk size and
-  // alignment share one launch.
-  size_t li = 0;
-  while (li < plans.size()) {
+  // alignment share one launch (marks keep per-layer completion inside it).
+  std::vector<Step> steps;
+  std::vector<uint32_t> aux;  // marked launches: chunk_start[n+1], then layer[n]
+  for (size_t li = 0; li < plans.size();) {
     const LayerPlan& p = plans[li];
     if (p.ordered) {
-      if (int rc = dma_layer(x, p, is_save, false)) return rc;
-      if (layer_events && layer_events[li])
-        PF_HIP(hipEventRecord(static_cast<hipEvent_t>(layer_events[li]), x->stream));
+      steps.push_back({li, li + 1, true, false});
       ++li;
       continue;
     }
     const bool al = chunks_aligned(p);
+    // Marks inside the launch cost nothing while the host link is the bound
+    // (sources in pinned memory) but slow an HBM-bound launch; loads from
+    // device memory are split per layer and marked after each launch.
+    const bool host_src = !p.chunks.empty() && host_sourced(p, is_save);
+    const bool per_layer = layer_events || (sig && !p.chunks.empty() && !host_src);
     size_t lj = li + 1;
-    if (!layer_events) {
+    if (!per_layer) {
       while (lj < plans.size() && !plans[lj].ordered &&
              plans[lj].chunk_bytes == p.chunk_bytes &&
-             (plans[lj].chunks.empty() || chunks_aligned(plans[lj]) == al))
+             (plans[lj].chunks.empty() || (chunks_aligned(plans[lj]) == al &&
+                                           (!sig || host_sourced(plans[lj], is_save)))))
         ++lj;
     }
-    size_t n = 0;
-    for (size_t k = li; k < lj; ++k) n += plans[k].chunks.size();
-    if (int rc = launch(x, first[li], n, p.chunk_bytes, al, is_save)) return rc;
-    if (layer_events && layer_events[li])
-      PF_HIP(hipEventRecord(static_cast<hipEvent_t>(layer_events[li]), x->stream));
+    Step st{li, lj, false, al};
+    if (sig && al && !per_layer) {
+      st.tab = aux.size();
+      uint32_t start = 0;
+      std::vector<uint32_t> ids;
+      for (size_t k = li; k < lj; ++k) {
+        if (plans[k].chunks.empty()) continue;
+        aux.push_back(start);
+        ids.push_back(static_cast<uint32_t>(k));
+        start += static_cast<uint32_t>(plans[k].chunks.size());
+      }
+      aux.push_back(start);
+      aux.insert(aux.end(), ids.begin(), ids.end());
+      st.groups = static_cast<uint32_t>(ids.size());
+    }
+    steps.push_back(st);
     li = lj;
+  }
+  if (total > 0xffffffffull) return fail(PF_ERR_INVALID_ARGUMENT, "too many chunks");
+  const size_t aux_desc = (aux.size() * sizeof(uint32_t) + sizeof(ChunkDesc) - 1) /
+                          sizeof(ChunkDesc);
+  if (int rc = ensure_desc_capacity(x, total + aux_desc)) return rc;
+  if (sig)
+    if (int rc = ensure_counters(x, plans.size())) return rc;
+  size_t d = 0;
+  for (size_t li = 0; li < plans.size(); ++li) {
+    if (plans[li].ordered) continue;
+    for (const Chunk& c : plans[li].chunks)
+      x->h_desc[d++] = is_save ? ChunkDesc{c.dev, c.host} : ChunkDesc{c.host, c.dev};
+  }
+  if (!aux.empty()) std::memcpy(x->h_desc + total, aux.data(), aux.size() * sizeof(uint32_t));
+  if (int rc = upload_desc(x, total + aux_desc)) return rc;
+  const uint32_t* d_aux = reinterpret_cast<const uint32_t*>(x->d_desc + total);
+  for (const Step& st : steps) {
+    if (st.dma) {
+      if (int rc = dma_layer(x, plans[st.li], is_save, false)) return rc;
+      if (layer_events && layer_events[st.li])
+        PF_HIP(hipEventRecord(static_cast<hipEvent_t>(layer_events[st.li]), x->stream));
+      if (int rc = mark_layer(x, static_cast<uint32_t>(st.li), sig)) return rc;
+      continue;
+    }
+    size_t n = 0;
+    for (size_t k = st.li; k < st.lj; ++k) n += plans[k].chunks.size();
+    LayerMarks marks{};
+    const bool marked = st.groups > 0;
+    if (marked) {
+      marks.chunk_start = d_aux + st.tab;
+      marks.layer = d_aux + st.tab + st.groups + 1;
+      marks.n = st.groups;
+      marks.counters = x->d_counters;
+      marks.targets = *sig;
+    }
+    if (int rc = launch(x, first[st.li], n, plans[st.li].chunk_bytes, st.aligned, is_save,
+                        marked ? &marks : nullptr))
+      return rc;
+    if (layer_events && layer_events[st.li])
+      PF_HIP(hipEventRecord(static_cast<hipEvent_t>(layer_events[st.li]), x->stream));
+    if (sig) {
+      // Layers the launch did not mark: empty ones, and all of an unaligned launch.
+      std::vector<uint32_t> rest;
+      for (size_t k = st.li; k < st.lj; ++k)
+        if (!marked || plans[k].chunks.empty()) rest.push_back(static_cast<uint32_t>(k));
+      if (int rc = mark_layers(x, rest, *sig)) return rc;
+    }
   }
   if (is_save && wait_save) PF_HIP(hipStreamSynchronize(x->stream));
   return PF_OK;
 }
 
 int run(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, uint32_t mode,
-        bool is_save, pf_event* layer_events, bool wait_save = true) {
+        bool is_save, pf_event* layer_events, bool wait_save = true,
+        const SignalTargets* sig = nullptr) {
   if (!x) return fail(PF_ERR_INVALID_ARGUMENT, "null transfer context");
   if (num_layers > 0 && !layers) return fail(PF_ERR_INVALID_ARGUMENT, "null layer list");
   std::lock_guard<std::mutex> lk(x->mu);
@@ -582,6 +698,8 @@ int run(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, uint32_t m
         if (int rc = dma_layer(x, plans[li], is_save, per_chunk_sync)) return rc;
         if (!is_save && layer_events && layer_events[li])
           PF_HIP(hipEventRecord(static_cast<hipEvent_t>(layer_events[li]), x->stream));
+        if (!is_save)
+          if (int rc = mark_layer(x, li, sig)) return rc;
       }
       if (is_save && wait_save) PF_HIP(hipStreamSynchronize(x->stream));
       return PF_OK;
@@ -589,11 +707,12 @@ int run(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, uint32_t m
     case PF_MODE_KERNEL:
       for (uint32_t li = 0; li < num_layers; ++li)
         apply_write_policy(layers[li], is_save, false, &plans[li]);
-      return kernel_direct(x, layers, plans, is_save, layer_events, wait_save);
+      return kernel_direct(x, layers, plans, is_save, layer_events, is_save ? nullptr : sig,
+                           wait_save);
     case PF_MODE_STAGED:
       for (uint32_t li = 0; li < num_layers; ++li)
         apply_write_policy(layers[li], is_save, true, &plans[li]);
-      return staged(x, layers, plans, is_save, layer_events);
+      return staged(x, layers, plans, is_save, layer_events, sig);
     default:
       return fail(PF_ERR_INVALID_ARGUMENT, strf("unknown transfer mode %u", mode));
   }
@@ -604,6 +723,26 @@ int run(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, uint32_t m
 int pf::save_layers_begin(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
                           uint32_t mode) {
   return run(x, layers, num_layers, mode, true, nullptr, false);
+}
+
+int pf::mark_all_layers(pf_xfer* x, const pf_layer_signal& g, uint32_t num_layers) {
+  if (!x || num_layers == 0) return PF_OK;
+  RangeCache rc;
+  if (g.value == 0 || (g.words & 7u) != 0 ||
+      !rc.check(g.words, static_cast<uint64_t>(num_layers) * 8u))
+    return fail(PF_ERR_INVALID_ARGUMENT, "layer words are not inside one allocation");
+  SignalTargets t{};
+  t.words[0] = g.words;
+  t.value[0] = g.value;
+  t.host_mask = g.host_memory ? 1u : 0u;
+  t.count = 1;
+  std::vector<uint32_t> ids(num_layers);
+  for (uint32_t i = 0; i < num_layers; ++i) ids[i] = i;
+  std::lock_guard<std::mutex> lk(x->mu);
+  PF_HIP(hipSetDevice(x->device));
+  if (int r = mark_layers(x, ids, t)) return r;
+  PF_HIP(hipStreamSynchronize(x->stream));
+  return PF_OK;
 }
 
 extern "C" {
@@ -722,6 +861,7 @@ int pf_xfer_destroy(pf_xfer* x) {
   if (x->stream) (void)hipStreamSynchronize(x->stream);
   if (x->dma) (void)hipStreamSynchronize(x->dma);
   if (x->d_desc) (void)hipFree(x->d_desc);
+  if (x->d_counters) (void)hipFree(x->d_counters);
   if (x->h_desc) (void)hipHostFree(x->h_desc);
   if (x->staging) (void)hipFree(reinterpret_cast<void*>(x->staging));
   if (x->desc_uploaded) (void)hipEventDestroy(x->desc_uploaded);
@@ -815,6 +955,37 @@ int pf_save_layers(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
 int pf_load_layers(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
                    uint32_t mode, pf_event* layer_events) {
   return run(x, layers, num_layers, mode, false, layer_events);
+}
+
+int pf_load_layers_marked(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
+                          uint32_t mode, const pf_layer_signal* signals,
+                          uint32_t num_signals) {
+  if (num_signals == 0 || num_signals > PF_MAX_LAYER_SIGNALS || !signals)
+    return fail(PF_ERR_INVALID_ARGUMENT,
+                strf("a marked load takes 1..%d signal targets, got %u", PF_MAX_LAYER_SIGNALS,
+                     num_signals));
+  SignalTargets t{};
+  RangeCache rc;
+  for (uint32_t i = 0; i < num_signals; ++i) {
+    const pf_layer_signal& g = signals[i];
+    if (g.value == 0 || g.reserved != 0 || g.host_memory > 1 || (g.words & 7u) != 0)
+      return fail(PF_ERR_INVALID_ARGUMENT,
+                  strf("signal target %u: words must be 8-byte aligned, value nonzero, "
+                       "host_memory 0 or 1",
+                       i));
+    // The kernels write these words: they must be mapped for the device.
+    if (num_layers > 0 && !rc.check(g.words, static_cast<uint64_t>(num_layers) * 8u))
+      return fail(PF_ERR_INVALID_ARGUMENT,
+                  strf("signal target %u: [0x%llx, +%llu) is not inside one device, IPC or "
+                       "pinned allocation",
+                       i, (unsigned long long)g.words,
+                       (unsigned long long)num_layers * 8ull));
+    t.words[i] = g.words;
+    t.value[i] = g.value;
+    if (g.host_memory) t.host_mask |= 1u << i;
+  }
+  t.count = num_signals;
+  return run(x, layers, num_layers, mode, false, nullptr, true, &t);
 }
 
 }  // extern "C"

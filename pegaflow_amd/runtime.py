@@ -252,6 +252,24 @@ def memcpy_async(dst: int, src: int, nbytes: int, stream: Stream) -> None:
     check(lib().pf_memcpy_async(dst, src, nbytes, stream.handle), "pf_memcpy_async")
 
 
+def stream_wait_word(stream: Stream, word: int, value: int, timeout_us: int = 10_000_000,
+                     timed_out: int = 0) -> None:
+    """Work queued on ``stream`` afterwards waits until the 8-byte word at
+    ``word`` is >= value, or ``timeout_us`` passes (the 4-byte word at
+    ``timed_out``, if given, is then set to 1)."""
+    check(lib().pf_stream_wait_word(stream.handle, word, value, timeout_us, timed_out),
+          "pf_stream_wait_word")
+
+
+def host_wait_word(word: int, value: int, timeout_us: int = 10_000_000) -> bool:
+    """Wait on the host until the pinned 8-byte word at ``word`` is >= value;
+    False on timeout."""
+    reached = ctypes.c_int()
+    check(lib().pf_host_wait_word(word, value, timeout_us, ctypes.byref(reached)),
+          "pf_host_wait_word")
+    return bool(reached.value)
+
+
 def spin(stream: Stream, microseconds: int) -> None:
     check(lib().pf_spin(stream.handle, microseconds), "pf_spin")
 

@@ -244,6 +244,21 @@ class TransferContext:
         check(lib().pf_load_layers(self.handle, arr, len(layers), mode, evs), "load_layers")
         del keep
 
+    def load_layers_marked(self, layers: Sequence[LayerTransfer], signals,
+                           mode: int = _lib.MODE_KERNEL) -> None:
+        """Host -> device for every layer, asynchronous; ``signals`` is a list of
+        ``(words_addr, value, host_memory)``: once layer l's bytes are in place,
+        the 8-byte word at ``words_addr + 8*l`` of each target holds ``value``."""
+        arr, keep = _layer_array(layers)
+        sig = (_lib.LayerSignal * max(len(signals), 1))()
+        for i, (words, value, host_memory) in enumerate(signals):
+            sig[i].words = words
+            sig[i].value = value
+            sig[i].host_memory = int(bool(host_memory))
+        check(lib().pf_load_layers_marked(self.handle, arr, len(layers), mode, sig,
+                                          len(signals)), "load_layers_marked")
+        del keep
+
     def close(self) -> None:
         if self.handle:
             lib().pf_xfer_destroy(self.handle)

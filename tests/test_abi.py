@@ -285,3 +285,66 @@ def test_load_state_event_block_layout():
     assert LoadState.attach(PyLoadState(num_layers=3).shm_name()).event_handles() == []
     with pytest.raises(ValueError):
         PyLoadState(num_layers=3, layer_events=handles[:2])
+
+
+def _words_record(kind, value, address=0, alloc_size=0, offset=0, handle=b""):
+    w = _lib.LayerWords()
+    w.kind, w.value, w.address, w.alloc_size, w.offset = kind, value, address, alloc_size, offset
+    ctypes.memmove(w.handle, handle.ljust(64, b"\0"), 64)
+    return w
+
+
+class _HostWords:
+    """Stands in for LayerWords (which needs device memory): the record only."""
+
+    def __init__(self, num_layers, record):
+        self.num_layers, self._record = num_layers, record
+
+    def next_load(self):
+        return self._record
+
+
+def test_load_state_words_block_layout():
+    """The optional block of layer words after the layered extension, at byte
+    48: {'PFLW', count, value, kind, 0, address, alloc_size, offset, handle}."""
+    handle = bytes(range(64))
+    rec = _words_record(_lib.LAYER_WORDS_IPC, 9, alloc_size=1 << 21, offset=512, handle=handle)
+    p = PyLoadState(layer_words=_HostWords(6, rec))
+    raw = open("/dev/shm/" + p.shm_name(), "rb").read()
+    assert len(raw) == 48 + 112
+    assert struct.unpack_from("<QIIq", raw, 0) == (8, 0x50464C44, 1, 0)
+    assert struct.unpack_from("<IIq", raw, 32) == (0x50464C58, 6, 0)
+    assert struct.unpack_from("<IIQIIQQQ", raw, 48) == (0x50464C57, 6, 9, 0, 0, 0, 1 << 21, 512)
+    assert raw[96:160] == handle
+    srv = LoadState.attach(p.shm_name())
+    w, n = srv.layer_words()
+    assert n == 6 and w.value == 9 and w.kind == 0 and w.offset == 512
+    assert bytes(w.handle) == handle and srv.event_handles() == []
+    # Words need no "recorded" handshake: the wait is queued at once...
+    calls = []
+    assert p.wait_for_layer_on_device(4, calls.append) and calls == [4]
+    # ...and not at all once the load has failed.
+    srv.set_error()
+    assert not p.wait_for_layer_on_device(1, calls.append) and calls == [4]
+    srv.close()
+    # A local record keeps its address; states without words report none.
+    q = PyLoadState(layer_words=_HostWords(2, _words_record(_lib.LAYER_WORDS_LOCAL, 1,
+                                                            address=0x7000)))
+    w, n = LoadState.attach(q.shm_name()).layer_words()
+    assert n == 2 and w.kind == 1 and w.address == 0x7000
+    assert LoadState.attach(PyLoadState(num_layers=3).shm_name()).layer_words() == (None, 0)
+    ev = PyLoadState(num_layers=1, layer_events=[b"\1" * 64])
+    assert LoadState.attach(ev.shm_name()).layer_words() == (None, 0)
+
+
+@pytest.mark.parametrize("rec,n", [
+    (dict(kind=0, value=0, alloc_size=4096), 2),          # value 0
+    (dict(kind=0, value=1, alloc_size=4096, offset=4), 2),  # misaligned
+    (dict(kind=0, value=1, alloc_size=16, offset=8), 2),  # past the allocation
+    (dict(kind=1, value=1, address=0x1004), 2),           # misaligned address
+    (dict(kind=2, value=1, address=0x1000), 2),           # unknown kind
+    (dict(kind=1, value=1, address=0x1000), 0),           # no layers
+])
+def test_load_state_words_block_rejects(rec, n):
+    with pytest.raises(_lib.PegaFlowError):
+        LoadState.new(n, None, _words_record(**rec))

@@ -264,3 +264,75 @@ def test_llama_prefix_through_engine(gpu):
     assert verify_restored(layers, ids, targets) == 0
     layers.close()
     e.close()
+
+
+def _wait_words(words, value, n, timeout=10.0):
+    """The device words, once all of them hold `value` (written asynchronously
+    by the load thread)."""
+    t0 = time.monotonic()
+    while True:
+        got = words.buf.download().view(np.uint64)[:n]
+        if (got == value).all() or time.monotonic() - t0 > timeout:
+            return got.tolist()
+        time.sleep(0.001)
+
+
+def test_device_words_gate_consumer_per_layer(engine):
+    """A layered load with the consumer's device words (same process): the
+    engine's one marked launch writes word l as layer l lands; a consumer
+    stream waits on each word and snapshots its layer, and every snapshot
+    holds the restored bytes.  A failed load (unknown hash) and an empty load
+    (every id negative) still write every word, so no device wait is left
+    hanging; the LoadState tells them apart."""
+    from pegaflow_amd.load_state import LayerWords
+    from pegaflow_amd.runtime import Stream, memcpy_async
+
+    say("[gpu] engine layer words: device-side per-layer gating")
+    engine.set_transfer_modes(_lib.MODE_KERNEL, _lib.MODE_KERNEL)
+    m = Model(engine, "words", 8, 256, 32768, seed=31)
+    words = LayerWords(m.n_layers, local=True)
+    flag = DeviceBuffer(4 * m.n_layers)
+    snaps = [DeviceBuffer(m.size) for _ in range(m.n_layers)]
+    stream = Stream()
+    try:
+        orig = m.host_copies()
+        ids = list(range(0, 160, 2))
+        hashes = [h(i, b"words") for i in ids]
+        engine.batch_save_kv_blocks("words", 0, 0, [(n, ids, hashes) for n in m.names])
+        targets = list(range(255, 95, -2))
+        exp = expected_after_load(m, orig, ids, targets)
+        for rnd in range(2):  # the same words serve consecutive loads
+            for l, b in enumerate(m.bufs):
+                b.fill_random(m.seeds[l])
+            flag.memset(0)
+            st = PyLoadState(layer_words=words)
+            engine.batch_load_kv_blocks("words", 0, 0, st.shm_name(), m.names, targets, hashes)
+            for l in range(m.n_layers):
+                assert st.wait_for_layer_on_device(
+                    l, lambda i: words.wait_on_device(stream, i, 20_000_000, flag.ptr + 4 * i))
+                memcpy_async(snaps[l].ptr, m.bufs[l].ptr, m.size, stream)
+            stream.synchronize()
+            assert wait(st) == 1 and st.layers_done() == m.n_layers
+            assert not flag.download().any(), f"round {rnd}: a device wait timed out"
+            for l in range(m.n_layers):
+                assert np.array_equal(snaps[l].download(), exp[l]), f"round {rnd} layer {l}"
+        # Unknown hash: the call fails, the state says so, the words are written.
+        st = PyLoadState(layer_words=words)
+        with pytest.raises(_lib.PegaFlowError):
+            engine.batch_load_kv_blocks("words", 0, 0, st.shm_name(), m.names, targets[:2],
+                                        [hashes[0], h(10**6, b"words")])
+        assert st.get_state() == -1
+        assert _wait_words(words, words.value, m.n_layers) == [words.value] * m.n_layers
+        # Nothing to copy: completed at once, words written.
+        st = PyLoadState(layer_words=words)
+        engine.batch_load_kv_blocks("words", 0, 0, st.shm_name(), m.names, [-1, -1],
+                                    hashes[:2])
+        assert wait(st) == 1
+        assert _wait_words(words, words.value, m.n_layers) == [words.value] * m.n_layers
+    finally:
+        stream.close()
+        for b in snaps:
+            b.close()
+        flag.close()
+        words.close()
+        m.close()

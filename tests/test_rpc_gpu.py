@@ -19,7 +19,7 @@ import oracle
 from pegaflow_amd import ipc
 from pegaflow_amd._lib import PegaFlowError
 from pegaflow_amd.engine import PegaEngine
-from pegaflow_amd.load_state import PyLoadState
+from pegaflow_amd.load_state import LayerWords, PyLoadState
 from pegaflow_amd.rpc.client import EngineRpcClient
 from pegaflow_amd.rpc.server import Server
 from pegaflow_amd.runtime import DeviceBuffer, Event, Stream, memcpy_async
@@ -222,3 +222,71 @@ def test_cross_process_layer_events(gpu):
             e.close()
         stream.close()
         layers.close()
+
+
+def test_cross_process_layer_words(gpu):
+    """Device-side per-layer completion across processes without interprocess
+    events: this process (the consumer) shares a few device words through a
+    device-memory IPC handle in the LoadState; the server's copy kernel sets
+    word l when layer l lands, and this process's stream waits on each word
+    and snapshots that layer.  Every snapshot must hold the restored bytes.
+    The same words serve a second load, and a failed load still writes them."""
+    say("[gpu] rpc two-process layer words (device-side per-layer wait)")
+    n_layers = 8
+    layers = Layers(n_layers, 256, 16 * 8 * 128 * 2, seed=23)
+    handles = [ipc.export_tensor(b.ptr, layers.size, 0) for b in layers.bufs]
+    words = LayerWords(n_layers)
+    flag = DeviceBuffer(4 * n_layers)
+    stream = Stream()
+    snaps = [DeviceBuffer(layers.size) for _ in range(n_layers)]
+    p, addr = _start_server()
+    say(f"[gpu] server pid {p.pid} at {addr}")
+    inst = "vllm-words"
+    try:
+        with EngineRpcClient(f"http://{addr}", connect_timeout_s=10) as client:
+            for name, handle in zip(layers.names, handles):
+                assert client.register_context(inst, "llama", 0, 1, 0, n_layers, name, handle,
+                                               layers.nb, layers.bpb, layers.kv, 2)[0]
+            before = layers.host()
+            ids = list(range(0, 256, 2))
+            hashes = [h(2000 + i) for i in ids]
+            assert client.save(inst, 0, 0, [(n, ids, hashes) for n in layers.names])[0]
+            layers.fill(seed=78)
+            clobbered = layers.host()
+            targets = list(range(1, 256, 2))
+            exp = layers.expected(before, clobbered, ids, targets)
+            for rnd in range(2):
+                layers.fill(seed=78)
+                flag.memset(0)
+                st = PyLoadState(layer_words=words)
+                assert client.load(inst, 0, 0, st.shm_name(), layers.names, targets, hashes)[0]
+                for l in range(n_layers):
+                    assert st.wait_for_layer_on_device(
+                        l, lambda i: words.wait_on_device(stream, i, 30_000_000, flag.ptr + 4 * i))
+                    memcpy_async(snaps[l].ptr, layers.bufs[l].ptr, layers.size, stream)
+                stream.synchronize()
+                assert wait(st) == 1 and st.layers_done() == n_layers
+                assert not flag.download().any(), f"round {rnd}: a device wait timed out"
+                for l in range(n_layers):
+                    assert np.array_equal(snaps[l].download(), exp[l]), f"round {rnd} layer {l}"
+            # A load naming an unknown hash fails; its words are still written.
+            st = PyLoadState(layer_words=words)
+            with pytest.raises(RuntimeError, match="missing KV block hash"):
+                client.load(inst, 0, 0, st.shm_name(), layers.names, [1], [h(10**6)])
+            assert st.get_state() == -1
+            t0 = time.monotonic()
+            while (words.buf.download().view(np.uint64) != words.value).any():
+                assert time.monotonic() - t0 < 10, "failed load left its words unset"
+                time.sleep(0.001)
+            assert client.unregister_context(inst)[0]
+            assert client.shutdown()[0]
+        assert p.wait(60) == 0
+    finally:
+        if p.poll() is None:
+            p.kill()
+            p.wait(10)
+        for b in snaps:
+            b.close()
+        flag.close()
+        words.close()
+        stream.close()
