@@ -306,6 +306,41 @@ def leg_mla(xfer, seed):
     return out
 
 
+def leg_tp_rank(xfer, seed):
+    """The Llama prefix as one tensor-parallel rank sees it at TP=8: 32 layers
+    [2,20000,16,1,128] (one kv head, 4 KiB segments), 640 random blocks, save
+    then restore, in the kernel mode and in the reference's call pattern
+    (one synchronous copy per segment for the save, one async copy per merged
+    run for the restore) and merged-run DMA."""
+    from pegaflow_amd import _lib
+    from pegaflow_amd import workload as wl
+    from pegaflow_amd.runtime import PinnedBuffer
+
+    shape, n = wl.LLAMA3_8B_TP8_RANK, 640
+    layers = wl.DeviceLayers(shape, base_seed=seed)
+    ids, targets = wl.draw_blocks(shape.num_blocks, n, seed)
+    P = wl.payload_bytes(layers.regs, n)
+    pool = PinnedBuffer(P)
+    saved = wl.save_plan(layers.regs, ids, pool.ptr)
+    loads = wl.load_plan(saved, targets)
+    out = {"workload": "llama-3.1-8b 10k-token prefix on one TP=8 rank: 32 x bf16 "
+                       "[2,20000,16,1,128], 640 random blocks, save then restore",
+           "payload_bytes": P, "segment_bytes": shape.bytes_per_block}
+    bad = 0
+    for mode, reps in (("kernel", 5), ("dma_batched", 1), ("dma_reference", 1)):
+        m = _lib.MODE_NAMES[mode]
+        t_s = timed(lambda: xfer.save_layers(saved, m), reps)
+        t_l = timed(lambda: (xfer.load_layers(loads, m), xfer.synchronize()), reps)
+        bad += wl.verify_saved(layers, saved) + wl.verify_restored(layers, ids, targets)
+        layers.refill()
+        out[mode] = {"save_gbps": round(P / t_s / 1e9, 2), "restore_gbps": round(P / t_l / 1e9, 2),
+                     "save_ms": round(t_s * 1e3, 3), "restore_ms": round(t_l * 1e3, 3)}
+    out["bit_exact"] = bad == 0
+    pool.close()
+    layers.close()
+    return out
+
+
 def fs_type(path):
     """Filesystem type of the mount that holds path (from /proc/mounts)."""
     path, best, kind = os.path.realpath(path), "", "unknown"
@@ -741,6 +776,9 @@ def main():
         log(f"[bench] {extra['layerwise_qwen3_8b']}")
         log("[bench] config 5: MLA latent bf16 / fp8")
         extra["mla_latent"] = leg_mla(xfer, args.seed)
+        log("[bench] one TP=8 rank of the llama prefix (4 KiB segments)")
+        extra["tp8_rank_llama3_8b"] = leg_tp_rank(xfer, args.seed)
+        log(f"[bench] {extra['tp8_rank_llama3_8b']}")
         log("[bench] config 4: fragmentation sweep")
         extra["fragmentation_llama3_8b"] = leg_fragmentation(layers, xfer, args.seed)
         log("[bench] engine: save and restore by hash")

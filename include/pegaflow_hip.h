@@ -272,22 +272,36 @@ int pf_xfer_synchronize(pf_xfer* xfer);
  * of 64) and 16-byte loads in flight per lane (1, 2, 4, 8 or 16), optionally
  * OR-ed with PF_KERNEL_NT_LOADS and/or PF_KERNEL_NT_STORES for non-temporal
  * (streaming) loads and stores.  0 keeps the current value.  Sets the shape
- * of both directions; defaults below. */
+ * of every route; defaults below. */
 #define PF_KERNEL_NT_LOADS 0x100u
 #define PF_KERNEL_NT_STORES 0x200u
 #define PF_KERNEL_NONTEMPORAL (PF_KERNEL_NT_LOADS | PF_KERNEL_NT_STORES)
 /* Give each of the 8 XCDs one contiguous range of tiles instead of the
  * hardware's round-robin deal (only with an uncapped grid). */
 #define PF_KERNEL_XCD_MAJOR 0x400u
-/* Per-direction defaults (the fastest HBM shapes measured on MI355X):
- * saves gather 8 KiB tiles in round-robin order, loads scatter 16 KiB tiles
- * in XCD-major order. */
+/* Launch shapes are kept per route: the direction, and whether the far side
+ * of the copy is device memory (an HBM-bound gather or scatter) or pinned
+ * host memory (zero-copy over the host link). */
+enum {
+  PF_ROUTE_SAVE_DEVICE = 0, /* paged tensor -> device memory (gather)       */
+  PF_ROUTE_LOAD_DEVICE = 1, /* device memory -> paged tensor (scatter)      */
+  PF_ROUTE_SAVE_HOST = 2,   /* paged tensor -> pinned host memory           */
+  PF_ROUTE_LOAD_HOST = 3    /* pinned host memory -> paged tensor           */
+};
+/* Per-route defaults (the fastest shapes measured on MI355X): HBM gathers
+ * move 8 KiB tiles in round-robin order; scatters 16 KiB tiles in XCD-major
+ * order; zero-copy saves 16 KiB tiles with streaming loads and ordinary
+ * stores into host memory (2% faster than streaming both). */
 #define PF_SAVE_DEFAULT_THREADS 512u
 #define PF_SAVE_DEFAULT_UNROLL (1u | PF_KERNEL_NONTEMPORAL)
 #define PF_LOAD_DEFAULT_THREADS 512u
 #define PF_LOAD_DEFAULT_UNROLL (2u | PF_KERNEL_NONTEMPORAL | PF_KERNEL_XCD_MAJOR)
-/* Shape for one direction only: 0 = saves (gather), 1 = loads (scatter).
- * pf_xfer_set_kernel_shape sets both. */
+#define PF_SAVE_HOST_DEFAULT_THREADS 512u
+#define PF_SAVE_HOST_DEFAULT_UNROLL (2u | PF_KERNEL_NT_LOADS)
+#define PF_LOAD_HOST_DEFAULT_THREADS 512u
+#define PF_LOAD_HOST_DEFAULT_UNROLL (2u | PF_KERNEL_NONTEMPORAL | PF_KERNEL_XCD_MAJOR)
+/* Shape for one route only (PF_ROUTE_*; 0 and 1 are also "saves" and
+ * "loads" of device memory).  pf_xfer_set_kernel_shape sets every route. */
 int pf_xfer_set_kernel_shape_dir(pf_xfer* xfer, uint32_t direction,
                                  uint32_t threads, uint32_t unroll);
 int pf_xfer_set_kernel_shape(pf_xfer* xfer, uint32_t threads, uint32_t unroll);

@@ -67,6 +67,12 @@ KERNEL_NONTEMPORAL = KERNEL_NT_LOADS | KERNEL_NT_STORES
 KERNEL_XCD_MAJOR = 0x400
 SAVE_DEFAULT_SHAPE = (512, 1 | KERNEL_NONTEMPORAL)
 LOAD_DEFAULT_SHAPE = (512, 2 | KERNEL_NONTEMPORAL | KERNEL_XCD_MAJOR)
+SAVE_HOST_DEFAULT_SHAPE = (512, 2 | KERNEL_NT_LOADS)
+LOAD_HOST_DEFAULT_SHAPE = (512, 2 | KERNEL_NONTEMPORAL | KERNEL_XCD_MAJOR)
+# Launch-shape routes (PF_ROUTE_*): direction x where the far side lives.
+ROUTE_SAVE_DEVICE, ROUTE_LOAD_DEVICE, ROUTE_SAVE_HOST, ROUTE_LOAD_HOST = 0, 1, 2, 3
+DEFAULT_SHAPES = {ROUTE_SAVE_DEVICE: SAVE_DEFAULT_SHAPE, ROUTE_LOAD_DEVICE: LOAD_DEFAULT_SHAPE,
+                  ROUTE_SAVE_HOST: SAVE_HOST_DEFAULT_SHAPE, ROUTE_LOAD_HOST: LOAD_HOST_DEFAULT_SHAPE}
 
 LOAD_PENDING, LOAD_SUCCESS, LOAD_ERROR = 0, 1, -1
 

@@ -242,15 +242,17 @@ struct pf_xfer {
   uint64_t slot_bytes = 0;
   hipEvent_t slot_ready[2] = {nullptr, nullptr};
   hipEvent_t slot_free[2] = {nullptr, nullptr};
-  // Launch shapes, [0] for saves (gather from the paged tensor) and [1] for
-  // loads (scatter into it), the fastest measured on MI355X for the HBM
-  // paths (the host-link-bound zero-copy paths are insensitive to the shape):
-  //   gather:  512 threads, one non-temporal 16 B load per lane (8 KiB tiles),
-  //            round-robin tile order;
-  //   scatter: 512 threads, two non-temporal loads per lane (16 KiB tiles),
-  //            XCD-major tile order.
-  uint32_t threads[2] = {PF_SAVE_DEFAULT_THREADS, PF_LOAD_DEFAULT_THREADS};
-  uint32_t unroll[2] = {PF_SAVE_DEFAULT_UNROLL, PF_LOAD_DEFAULT_UNROLL};
+  // Launch shapes per route (PF_ROUTE_*), the fastest measured on MI355X:
+  //   gather into HBM:   512 threads, one non-temporal 16 B load per lane
+  //                      (8 KiB tiles), round-robin tile order;
+  //   scatter:           512 threads, two non-temporal loads per lane (16 KiB
+  //                      tiles), XCD-major tile order;
+  //   save to the host:  512 threads, two streaming loads per lane, ordinary
+  //                      stores into host memory.
+  uint32_t threads[4] = {PF_SAVE_DEFAULT_THREADS, PF_LOAD_DEFAULT_THREADS,
+                         PF_SAVE_HOST_DEFAULT_THREADS, PF_LOAD_HOST_DEFAULT_THREADS};
+  uint32_t unroll[4] = {PF_SAVE_DEFAULT_UNROLL, PF_LOAD_DEFAULT_UNROLL,
+                        PF_SAVE_HOST_DEFAULT_UNROLL, PF_LOAD_HOST_DEFAULT_UNROLL};
   uint32_t max_grid = 0;
   uint64_t last_kernels = 0;
   uint64_t last_dma = 0;
@@ -305,9 +307,9 @@ int upload_desc(pf_xfer* x, size_t n) {
 }
 
 int launch(pf_xfer* x, size_t first, size_t n, uint64_t chunk_bytes, bool al16, bool is_save,
-           const LayerMarks* marks = nullptr) {
+           bool host_side = false, const LayerMarks* marks = nullptr) {
   if (n == 0) return PF_OK;
-  const int dir = is_save ? 0 : 1;
+  const int dir = (is_save ? PF_ROUTE_SAVE_DEVICE : PF_ROUTE_LOAD_DEVICE) + (host_side ? 2 : 0);
   if (n > 0xffffffffull) return fail(PF_ERR_INVALID_ARGUMENT, "too many chunks");
   if (chunk_bytes / 16 >= (1ull << 31))
     return fail(PF_ERR_INVALID_ARGUMENT, "chunk too large");
@@ -556,13 +558,14 @@ int staged(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<LayerPlan>
   return PF_OK;
 }
 
-// True when a load's sources (the host side of its chunks) lie in pinned
-// host memory, judged by the first chunk.
-bool host_sourced(const LayerPlan& p, bool is_save) {
+// True when the host side of a layer's chunks lies in pinned host memory
+// (judged by the first chunk): a zero-copy transfer over the host link.
+bool host_side_pinned(const LayerPlan& p) {
   uint64_t b = 0, e = 0;
-  return !is_save && !p.chunks.empty() &&
-         pinned_lookup(p.chunks[0].host, p.chunk_bytes, &b, &e);
+  return !p.chunks.empty() && pinned_lookup(p.chunks[0].host, p.chunk_bytes, &b, &e);
 }
+
+bool host_sourced(const LayerPlan& p, bool is_save) { return !is_save && host_side_pinned(p); }
 
 // ---- kernel mode ----------------------------------------------------------
 // One step of a kernel-mode call: a DMA copy of an ordered layer, or one
@@ -662,8 +665,15 @@ int kernel_direct(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<Lay
       marks.counters = x->d_counters;
       marks.targets = *sig;
     }
+    // The launch shape follows the first non-empty layer's host side.
+    bool host_side = false;
+    for (size_t k = st.li; k < st.lj; ++k)
+      if (!plans[k].chunks.empty()) {
+        host_side = host_side_pinned(plans[k]);
+        break;
+      }
     if (int rc = launch(x, first[st.li], n, plans[st.li].chunk_bytes, st.aligned, is_save,
-                        marked ? &marks : nullptr))
+                        host_side, marked ? &marks : nullptr))
       return rc;
     if (layer_events && layer_events[st.li])
       PF_HIP(hipEventRecord(static_cast<hipEvent_t>(layer_events[st.li]), x->stream));
@@ -889,14 +899,16 @@ int pf_xfer_synchronize(pf_xfer* x) {
 }
 
 int pf_xfer_set_kernel_shape(pf_xfer* x, uint32_t threads, uint32_t unroll) {
-  if (int rc = pf_xfer_set_kernel_shape_dir(x, 0, threads, unroll)) return rc;
-  return pf_xfer_set_kernel_shape_dir(x, 1, threads, unroll);
+  for (uint32_t r = PF_ROUTE_SAVE_DEVICE; r <= PF_ROUTE_LOAD_HOST; ++r)
+    if (int rc = pf_xfer_set_kernel_shape_dir(x, r, threads, unroll)) return rc;
+  return PF_OK;
 }
 
 int pf_xfer_set_kernel_shape_dir(pf_xfer* x, uint32_t direction, uint32_t threads,
                                  uint32_t unroll) {
   if (!x) return fail(PF_ERR_INVALID_ARGUMENT, "null transfer context");
-  if (direction > 1) return fail(PF_ERR_INVALID_ARGUMENT, "direction must be 0 (save) or 1 (load)");
+  if (direction > PF_ROUTE_LOAD_HOST)
+    return fail(PF_ERR_INVALID_ARGUMENT, "direction must be a route, 0..3 (PF_ROUTE_*)");
   if (threads && (threads < 64 || threads > 1024 || threads % 64))
     return fail(PF_ERR_INVALID_ARGUMENT, "threads must be a multiple of 64 in [64, 1024]");
   const uint32_t u = unroll & 0xffu;

@@ -204,14 +204,16 @@ class TransferContext:
         return k.value, d.value
 
     def set_kernel_shape_dir(self, direction: int, threads: int = 0, unroll: int = 0) -> None:
-        """direction 0 = saves (gather), 1 = loads (scatter)."""
+        """Shape of one route (``_lib.ROUTE_*``): 0 = saves into device memory
+        (gather), 1 = loads from device memory (scatter), 2 = saves into
+        pinned host memory, 3 = loads from pinned host memory."""
         check(lib().pf_xfer_set_kernel_shape_dir(self.handle, direction, threads, unroll),
               "pf_xfer_set_kernel_shape_dir")
 
     def reset_kernel_shape(self) -> None:
-        """Back to the per-direction defaults."""
-        self.set_kernel_shape_dir(0, *_lib.SAVE_DEFAULT_SHAPE)
-        self.set_kernel_shape_dir(1, *_lib.LOAD_DEFAULT_SHAPE)
+        """Back to the per-route defaults."""
+        for route, shape in _lib.DEFAULT_SHAPES.items():
+            self.set_kernel_shape_dir(route, *shape)
 
     def set_max_grid(self, max_workgroups: int) -> None:
         check(lib().pf_xfer_set_max_grid(self.handle, max_workgroups), "pf_xfer_set_max_grid")

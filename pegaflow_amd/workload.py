@@ -49,6 +49,9 @@ class KVShape:
 GPT2 = KVShape("gpt2 fp16 [2,512,16,12,64]", 12, 512, 16 * 12 * 64 * 2, 2)
 LLAMA3_8B = KVShape("llama-3.1-8b bf16 [2,20000,16,8,128]", 32, 20000, 16 * 8 * 128 * 2, 2)
 QWEN3_8B = KVShape("qwen3-8b bf16 [2,16000,16,8,128]", 36, 16000, 16 * 8 * 128 * 2, 2)
+# One tensor-parallel rank of Llama-3.1-8B at TP=8: one kv head, 4 KiB segments.
+LLAMA3_8B_TP8_RANK = KVShape("llama-3.1-8b tp8 rank bf16 [2,20000,16,1,128]", 32, 20000,
+                             16 * 1 * 128 * 2, 2)
 MLA_BF16 = KVShape("mla-latent bf16 [8192,64,576]", 61, 8192, 64 * 576 * 2, 1)
 MLA_FP8 = KVShape("mla-latent fp8 [8192,64,576]", 61, 8192, 64 * 576, 1)
 
@@ -161,6 +164,6 @@ def payload_bytes(regs, n_blocks: int) -> int:
     return sum(n_blocks * r.block_size_bytes for r in regs)
 
 
-__all__ = ["KVShape", "GPT2", "LLAMA3_8B", "QWEN3_8B", "MLA_BF16", "MLA_FP8", "draw_blocks",
+__all__ = ["KVShape", "GPT2", "LLAMA3_8B", "LLAMA3_8B_TP8_RANK", "QWEN3_8B", "MLA_BF16", "MLA_FP8", "draw_blocks",
            "DeviceLayers", "save_plan", "load_plan", "verify_saved", "verify_restored",
            "layer_seed", "payload_bytes", "MiB", "_lib"]

@@ -369,6 +369,14 @@ def test_llama_10k_prefix_full_size(ctx, save_mode, load_mode):
     _full_size(ctx, 32, 20000, 32768, 2, 640, MODES[save_mode], MODES[load_mode])
 
 
+@pytest.mark.parametrize("save_mode,load_mode", [("kernel", "kernel"), ("staged", "dma_batched")])
+def test_llama_tp8_rank_full_size(ctx, save_mode, load_mode):
+    """One TP=8 rank of Llama-3.1-8B: 32 layers [2,20000,16,1,128] (4 KiB
+    segments), 640 random blocks."""
+    say(f"[gpu] llama tp8 rank full size save={save_mode} load={load_mode}")
+    _full_size(ctx, 32, 20000, 4096, 2, 640, MODES[save_mode], MODES[load_mode], seed=8)
+
+
 @pytest.mark.parametrize("dtype_bytes", [2, 1])
 def test_mla_latent_full_size(ctx, dtype_bytes):
     """Config 5: 61 layers [8192, 64, 576] (bf16 or fp8 bytes), 128 blocks."""
