@@ -21,6 +21,10 @@ Printed JSON line (stdout):
   cpu_baseline     the reference's copy pattern (per-segment save copies,
                    merged-run restore copies) as host memcpy on this box's
                    cores, on a bounded sample of the same workload
+  other workloads  (skipped with --quick) layerwise_qwen3_8b, mla_latent,
+                   tp8_rank_llama3_8b, fragmentation_llama3_8b,
+                   engine_llama3_8b, disk_tier_llama3_8b and
+                   pinned_copy_microbench (single-block copy latency)
 Everything else goes to stderr.
 """
 
@@ -178,6 +182,15 @@ def leg_layerwise(xfer, seed):
         xfer.synchronize()
         return start.elapsed_ms(done)
 
+    def run_compute_only():
+        start.record(compute)
+        for _ in range(shape.layers):
+            spin(compute, compute_us)
+        done.record(compute)
+        done.synchronize()
+        return start.elapsed_ms(done)
+
+    compute_only = min(run_compute_only() for _ in range(3))
     run(True)
     total, per_layer = min((run(True) for _ in range(3)), key=lambda r: r[0])
     serial, _ = min((run(False) for _ in range(2)), key=lambda r: r[0])
@@ -191,6 +204,8 @@ def leg_layerwise(xfer, seed):
         "overlap_efficiency": round(ideal / total, 4),
         "total_ms": round(total, 3),
         "compute_ms": ideal,
+        "compute_only_ms": round(compute_only, 3),
+        "overlap_efficiency_vs_compute_only": round(compute_only / total, 4),
         "serialized_total_ms": round(serial, 3),
         "serialized_efficiency": round(ideal / serial, 4),
         "marked_total_ms": round(marked, 3),
@@ -338,6 +353,28 @@ def leg_tp_rank(xfer, seed):
     out["bit_exact"] = bad == 0
     pool.close()
     layers.close()
+    return out
+
+
+def pinned_copy_microbench(iters=2000):
+    """The reference's criterion benchmark of the transfer primitive
+    (pegaflow-core/benches/pinned_copy.rs): one block of 2 x 24 KiB copied
+    from pinned host memory to the device, contiguous and strided (K/V 27
+    blocks apart), as one copy, a copy per segment or a 2D copy, beside the
+    same block through the transfer context.  Latency per block (us)."""
+    import subprocess
+
+    from pegaflow_amd.build import BENCH_PINNED_COPY
+
+    if not os.path.exists(BENCH_PINNED_COPY):
+        raise RuntimeError(f"{BENCH_PINNED_COPY} is not built; run python -m pegaflow_amd.build")
+    log("[bench] pinned_copy microbenchmark (single block, 2 x 24 KiB)")
+    r = subprocess.run([BENCH_PINNED_COPY, str(iters)], capture_output=True, text=True,
+                       timeout=120)
+    if r.returncode != 0:
+        raise RuntimeError(f"bench_pinned_copy failed ({r.returncode}): {r.stderr.strip()}")
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    log(f"[bench] {out}")
     return out
 
 
@@ -617,6 +654,10 @@ def main():
         profile_gather(args.seed)
         return
 
+    # The single-block latency benchmark runs as its own process, before this
+    # one touches the GPU.
+    micro = None if args.quick else pinned_copy_microbench()
+
     from pegaflow_amd import _lib, runtime
     from pegaflow_amd.runtime import DeviceBuffer, PinnedBuffer
     from pegaflow_amd.transfer import KVCacheRegistration, TransferContext
@@ -849,6 +890,8 @@ def main():
         "cpu_baseline": cpu,
     }
     out.update(extra)
+    if micro is not None:
+        out["pinned_copy_microbench"] = micro
     if variants:
         out["variants"] = variants
     if sweep:

@@ -14,6 +14,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libpegaflow_hip.so")
+# Single-block copy latency benchmark (the reference's pinned_copy bench).
+BENCH_PINNED_COPY = os.path.join(HERE, "bench_pinned_copy")
 ARCH = "gfx950"
 
 SOURCES = [
@@ -76,7 +78,23 @@ def build(verbose: bool = False) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, LIB)
+    build_bench(cc, verbose)
     return LIB
+
+
+def build_bench(cc: str, verbose: bool = False) -> str:
+    """bench_pinned_copy, linked against the library next to it."""
+    src = os.path.join(CSRC, "bench_pinned_copy.cpp")
+    tmp = BENCH_PINNED_COPY + ".tmp"
+    cmd = [cc, *HIP_FLAGS, "-x", "hip", src, "-o", tmp, "-L", HERE, "-lpegaflow_hip",
+           "-Wl,-rpath,$ORIGIN", "-Wl,-rpath,/opt/rocm/lib"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed on bench_pinned_copy.cpp:\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, BENCH_PINNED_COPY)
+    return BENCH_PINNED_COPY
 
 
 if __name__ == "__main__":

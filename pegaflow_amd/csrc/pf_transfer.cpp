@@ -234,10 +234,17 @@ struct pf_xfer {
   hipStream_t dma = nullptr;     // link-side copies of the staged mode
   ChunkDesc* d_desc = nullptr;
   size_t d_cap = 0;
+  // Host staging of the descriptors for the upload.
   ChunkDesc* h_desc = nullptr;
   size_t h_cap = 0;
   hipEvent_t desc_uploaded = nullptr;
   bool desc_inflight = false;
+  // Small calls: descriptors the kernels read in place from coherent pinned
+  // memory (kHostDescMax entries), reused only once the stream has drained.
+  ChunkDesc* h_small = nullptr;
+  bool small_inflight = false;
+  // Descriptor base the next launches read: d_desc, or h_small.
+  const ChunkDesc* desc_base = nullptr;
   uint64_t staging = 0;
   uint64_t slot_bytes = 0;
   hipEvent_t slot_ready[2] = {nullptr, nullptr};
@@ -298,12 +305,35 @@ int ensure_desc_capacity(pf_xfer* x, size_t n) {
 }
 
 int upload_desc(pf_xfer* x, size_t n) {
+  x->desc_base = x->d_desc;
   if (n == 0) return PF_OK;
   PF_HIP(hipMemcpyAsync(x->d_desc, x->h_desc, n * sizeof(ChunkDesc),
                         hipMemcpyHostToDevice, x->stream));
   PF_HIP(hipEventRecord(x->desc_uploaded, x->stream));
   x->desc_inflight = true;
   return PF_OK;
+}
+
+// Small calls: a separate copy of the descriptors costs about 12 us before
+// the first kernel can start, more than the kernels of a one-block load
+// take.  Up to this many descriptors the kernels read them in place from
+// coherent pinned memory (one 16-byte read over the host link per
+// workgroup); larger calls upload them, since an HBM-bound launch would feel
+// that read in every workgroup.
+constexpr size_t kHostDescMax = 512;
+
+// The in-place buffer for a call of n descriptors, or null when the call
+// must upload (too many, or the previous in-place call may still be read).
+ChunkDesc* small_desc(pf_xfer* x, size_t n) {
+  if (n > kHostDescMax || !x->h_small) return nullptr;
+  if (x->small_inflight) {
+    if (hipStreamQuery(x->stream) != hipSuccess) {
+      (void)hipGetLastError();  // still running (or an error the sync reports)
+      return nullptr;
+    }
+    x->small_inflight = false;
+  }
+  return x->h_small;
 }
 
 int launch(pf_xfer* x, size_t first, size_t n, uint64_t chunk_bytes, bool al16, bool is_save,
@@ -325,7 +355,7 @@ int launch(pf_xfer* x, size_t first, size_t n, uint64_t chunk_bytes, bool al16, 
     PF_HIP(hipEventRecord(tm->first, x->stream));
   }
   (void)hipGetLastError();
-  hipError_t e = launch_copy_chunks(x->d_desc + first, static_cast<uint32_t>(n),
+  hipError_t e = launch_copy_chunks(x->desc_base + first, static_cast<uint32_t>(n),
                                     chunk_bytes, al16, x->threads[dir], x->unroll[dir],
                                     x->max_grid, marks, x->stream);
   if (e != hipSuccess) return hip_fail(e, "gather/scatter kernel launch");
@@ -634,18 +664,29 @@ int kernel_direct(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<Lay
   if (total > 0xffffffffull) return fail(PF_ERR_INVALID_ARGUMENT, "too many chunks");
   const size_t aux_desc = (aux.size() * sizeof(uint32_t) + sizeof(ChunkDesc) - 1) /
                           sizeof(ChunkDesc);
-  if (int rc = ensure_desc_capacity(x, total + aux_desc)) return rc;
   if (sig)
     if (int rc = ensure_counters(x, plans.size())) return rc;
+  ChunkDesc* hd = small_desc(x, total + aux_desc);
+  if (!hd) {
+    if (int rc = ensure_desc_capacity(x, total + aux_desc)) return rc;
+    hd = x->h_desc;
+  }
   size_t d = 0;
   for (size_t li = 0; li < plans.size(); ++li) {
     if (plans[li].ordered) continue;
     for (const Chunk& c : plans[li].chunks)
-      x->h_desc[d++] = is_save ? ChunkDesc{c.dev, c.host} : ChunkDesc{c.host, c.dev};
+      hd[d++] = is_save ? ChunkDesc{c.dev, c.host} : ChunkDesc{c.host, c.dev};
   }
-  if (!aux.empty()) std::memcpy(x->h_desc + total, aux.data(), aux.size() * sizeof(uint32_t));
-  if (int rc = upload_desc(x, total + aux_desc)) return rc;
-  const uint32_t* d_aux = reinterpret_cast<const uint32_t*>(x->d_desc + total);
+  if (!aux.empty()) std::memcpy(hd + total, aux.data(), aux.size() * sizeof(uint32_t));
+  if (hd == x->h_small) {
+    // Read in place by the launches below; the next in-place call waits for
+    // the stream to drain.
+    x->desc_base = x->h_small;
+    x->small_inflight = true;
+  } else if (int rc = upload_desc(x, total + aux_desc)) {
+    return rc;
+  }
+  const uint32_t* d_aux = reinterpret_cast<const uint32_t*>(x->desc_base + total);
   for (const Step& st : steps) {
     if (st.dma) {
       if (int rc = dma_layer(x, plans[st.li], is_save, false)) return rc;
@@ -844,6 +885,9 @@ int pf_xfer_create(int device, uint64_t staging_bytes, pf_xfer** out) {
   hipError_t e = hipStreamCreateWithFlags(&x->stream, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&x->dma, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipEventCreateWithFlags(&x->desc_uploaded, hipEventDisableTiming);
+  if (e == hipSuccess)
+    e = hipHostMalloc(reinterpret_cast<void**>(&x->h_small), kHostDescMax * sizeof(ChunkDesc),
+                      hipHostMallocMapped | hipHostMallocCoherent);
   for (int s = 0; s < 2 && e == hipSuccess; ++s) {
     e = hipEventCreateWithFlags(&x->slot_ready[s], hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&x->slot_free[s], hipEventDisableTiming);
@@ -873,6 +917,7 @@ int pf_xfer_destroy(pf_xfer* x) {
   if (x->d_desc) (void)hipFree(x->d_desc);
   if (x->d_counters) (void)hipFree(x->d_counters);
   if (x->h_desc) (void)hipHostFree(x->h_desc);
+  if (x->h_small) (void)hipHostFree(x->h_small);
   if (x->staging) (void)hipFree(reinterpret_cast<void*>(x->staging));
   if (x->desc_uploaded) (void)hipEventDestroy(x->desc_uploaded);
   for (auto& t : x->timers) {
