@@ -144,7 +144,9 @@ enum {
   PF_PINNED_DEFAULT = 0,     /* hipHostMallocMapped | Portable             */
   PF_PINNED_COHERENT = 1,    /* + hipHostMallocCoherent (fine-grained)     */
   PF_PINNED_NONCOHERENT = 2, /* + hipHostMallocNonCoherent (coarse-grained)*/
-  PF_PINNED_NUMA_USER = 4    /* + hipHostMallocNumaUser (caller's policy)  */
+  PF_PINNED_NUMA_USER = 4,   /* + hipHostMallocNumaUser (caller's policy)  */
+  PF_PINNED_WRITE_COMBINED = 8 /* + hipHostMallocWriteCombined: the         */
+                               /* reference's pool flag (pinned_mem.rs:159)  */
 };
 /* size == 0 is PF_ERR_ZERO_SIZE (pinned_mem.rs:150-152).  *dev_ptr receives
  * the device-visible address of the allocation (hipHostGetDevicePointer). */

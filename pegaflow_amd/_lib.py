@@ -60,6 +60,7 @@ PINNED_DEFAULT = 0
 PINNED_COHERENT = 1
 PINNED_NONCOHERENT = 2
 PINNED_NUMA_USER = 4
+PINNED_WRITE_COMBINED = 8
 
 KERNEL_NT_LOADS = 0x100
 KERNEL_NT_STORES = 0x200

@@ -303,6 +303,7 @@ int pf_pinned_allocate(uint64_t size, uint32_t flags, void** host_ptr,
   if (flags & PF_PINNED_COHERENT) hip_flags |= hipHostMallocCoherent;
   if (flags & PF_PINNED_NONCOHERENT) hip_flags |= hipHostMallocNonCoherent;
   if (flags & PF_PINNED_NUMA_USER) hip_flags |= hipHostMallocNumaUser;
+  if (flags & PF_PINNED_WRITE_COMBINED) hip_flags |= hipHostMallocWriteCombined;
   void* p = nullptr;
   hipError_t e = hipHostMalloc(&p, size, hip_flags);
   if (e != hipSuccess)
