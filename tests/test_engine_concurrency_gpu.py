@@ -1,0 +1,189 @@
+"""PegaEngine under concurrent use on the GPU.
+
+A saver thread keeps sealing new batches of one instance's blocks while two
+loader threads restore recently sealed batches into disjoint target blocks
+of a second instance (plain and layered LoadStates alternating) and a query
+thread counts prefix hits.  The pool holds only a few batches, so eviction
+runs all the time.
+
+Every load that succeeds must leave its targets holding exactly the source
+blocks' words, checked in closed form on the device.  A load that names a
+hash already evicted must fail cleanly (an error from the call or a -1
+LoadState), never with wrong bytes.  The engine's stats must add up at the
+end.
+"""
+
+import hashlib
+import random
+import sys
+import threading
+import time
+
+import numpy as np
+import pytest
+
+import oracle
+from pegaflow_amd import _lib
+from pegaflow_amd.engine import PegaEngine
+from pegaflow_amd.load_state import PyLoadState
+from pegaflow_amd.runtime import DeviceBuffer, verify_random_chunks
+
+pytestmark = pytest.mark.gpu
+MiB = 1 << 20
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def h(batch, i):
+    return hashlib.sha256(b"conc-%d-" % batch + int(i).to_bytes(8, "little")).digest()
+
+
+class Layers:
+    def __init__(self, n_layers, nb, bpb, seed):
+        self.nb, self.bpb, self.kv, self.size = nb, bpb, nb * bpb, 2 * nb * bpb
+        self.names = [f"layer.{l}" for l in range(n_layers)]
+        self.seeds = [oracle.layer_seed(seed, l) for l in range(n_layers)]
+        self.bufs = [DeviceBuffer(self.size) for _ in range(n_layers)]
+        for b, s in zip(self.bufs, self.seeds):
+            b.fill_random(s)
+
+    def register(self, engine, inst):
+        for name, b in zip(self.names, self.bufs):
+            engine.register_context_layer(inst, "conc", 0, name, b.ptr, self.size, self.nb,
+                                          self.bpb, self.kv, 2, 0, 1, len(self.names))
+
+    def close(self):
+        for b in self.bufs:
+            b.close()
+
+
+def check_targets(dst, src, sources, targets):
+    """Mismatching words: dst block targets[j] must hold src block sources[j]
+    (K and V segments) in every layer."""
+    t = np.asarray(targets, np.uint64)
+    s = np.asarray(sources, np.uint64)
+    bad = 0
+    for l, buf in enumerate(dst.bufs):
+        addrs = np.concatenate([buf.ptr + t * dst.bpb, buf.ptr + dst.kv + t * dst.bpb])
+        offs = np.concatenate([s * src.bpb // 8, (src.kv + s * src.bpb) // 8])
+        bad += verify_random_chunks(addrs, offs, src.bpb, src.seeds[l])
+    return bad
+
+
+def test_concurrent_saves_loads_and_queries(gpu):
+    say("[gpu] engine concurrency: saver, two loaders, a query thread, constant eviction")
+    n_layers, nb, bpb, per_batch = 8, 512, 16384, 32
+    batch_bytes = n_layers * per_batch * 2 * bpb  # 8 MiB
+    e = PegaEngine(pool_size=6 * batch_bytes)      # room for about 6 batches
+    e.set_transfer_modes(_lib.MODE_KERNEL, _lib.MODE_KERNEL)
+    src = Layers(n_layers, nb, bpb, seed=3)
+    dst = Layers(n_layers, nb, bpb, seed=4)
+    src.register(e, "prefill")
+    dst.register(e, "decode")
+    sealed = []            # (batch, source block ids), in sealing order
+    lock = threading.Lock()
+    stop = threading.Event()
+    errors = []
+    stats = {"saves": 0, "loads_ok": 0, "loads_missing": 0, "queries": 0, "words_checked": 0}
+
+    def saver():
+        rng = random.Random(1)
+        batch = 0
+        while not stop.is_set():
+            ids = rng.sample(range(nb), per_batch)
+            hashes = [h(batch, i) for i in ids]
+            e.batch_save_kv_blocks("prefill", 0, 0, [(n, ids, hashes) for n in src.names])
+            with lock:
+                sealed.append((batch, ids))
+                stats["saves"] += 1
+            batch += 1
+
+    def loader(k):
+        rng = random.Random(10 + k)
+        # Loader k owns target blocks [k*256, k*256 + 256) of the decode instance.
+        own = list(range(k * (nb // 2), (k + 1) * (nb // 2)))
+        n = 0
+        while not stop.is_set():
+            with lock:
+                recent = sealed[-4:]
+            if not recent:
+                time.sleep(0.001)
+                continue
+            batch, ids = rng.choice(recent)
+            pick = rng.sample(range(per_batch), 16)
+            sources = [ids[j] for j in pick]
+            hashes = [h(batch, i) for i in sources]
+            targets = rng.sample(own, 16)
+            st = PyLoadState(num_layers=n_layers) if n % 2 else PyLoadState()
+            n += 1
+            try:
+                e.batch_load_kv_blocks("decode", 0, 0, st.shm_name(), dst.names, targets, hashes)
+            except _lib.PegaFlowError as err:
+                assert "missing KV block hash" in str(err), str(err)
+                assert st.get_state() == -1
+                with lock:
+                    stats["loads_missing"] += 1
+                continue
+            t0 = time.monotonic()
+            while not st.is_ready():
+                assert time.monotonic() - t0 < 30, "load did not complete"
+                time.sleep(0.0002)
+            assert st.get_state() == 1
+            if n % 2 == 0:  # layered state: every layer was published
+                assert st.layers_done() == n_layers
+            bad = check_targets(dst, src, sources, targets)
+            assert bad == 0, f"loader {k}: {bad} mismatching words (batch {batch})"
+            with lock:
+                stats["loads_ok"] += 1
+                stats["words_checked"] += n_layers * 16 * 2 * bpb // 8
+
+    def querier():
+        while not stop.is_set():
+            with lock:
+                recent = sealed[-8:]
+            for batch, ids in recent:
+                hits = e.count_prefix_hit_blocks("prefill", [h(batch, i) for i in ids])
+                assert 0 <= hits <= per_batch
+            with lock:
+                stats["queries"] += 1
+            time.sleep(0.0005)
+
+    def guard(fn, *a):
+        try:
+            fn(*a)
+        except BaseException as err:  # report any thread's failure in the test
+            errors.append(err)
+            stop.set()
+
+    threads = [threading.Thread(target=guard, args=(saver,)),
+               threading.Thread(target=guard, args=(loader, 0)),
+               threading.Thread(target=guard, args=(loader, 1)),
+               threading.Thread(target=guard, args=(querier,))]
+    try:
+        for t in threads:
+            t.start()
+        deadline = time.monotonic() + 6.0
+        while time.monotonic() < deadline and not stop.is_set():
+            time.sleep(0.05)
+        stop.set()
+        for t in threads:
+            t.join(60)
+            assert not t.is_alive(), "a worker thread did not stop"
+        if errors:
+            raise errors[0]
+        e.wait_idle()
+        s = e.stats()
+        say(f"[gpu] concurrency: {stats}; engine {s}")
+        assert stats["saves"] >= 10 and stats["loads_ok"] >= 10, stats
+        assert s["evicted_blocks"] > 0, "the pool never filled"
+        assert s["load_failures"] == 0
+        assert s["pool_used_bytes"] <= s["pool_total_bytes"]
+        assert s["loaded_bytes"] == stats["loads_ok"] * n_layers * 16 * 2 * bpb
+    finally:
+        stop.set()
+        e.close()
+        src.close()
+        dst.close()
