@@ -175,7 +175,15 @@ class Server:
         self.engine.close()
 
 
-def main(argv=None) -> int:
+# The reference's default DFS root (pegaflow-server/src/lib.rs:98-104).
+DEFAULT_DFS_ROOT = "/tmp/pega"
+
+
+def parse_args(argv=None):
+    """The reference's CLI (pegaflow-server/src/lib.rs:38-113), so its launch
+    commands run unchanged, plus this server's own options.  Options for
+    parts this server does not have are accepted and reported by
+    unsupported_options()."""
     ap = argparse.ArgumentParser(prog="pegaflow-server",
                                  description="PegaEngine gRPC server (MI355X transfer path)")
     ap.add_argument("--addr", default="127.0.0.1:50055")
@@ -186,12 +194,48 @@ def main(argv=None) -> int:
     ap.add_argument("--log-level", default="info")
     ap.add_argument("--max-workers", type=int, default=16)
     ap.add_argument("--dfs-root", default=None,
-                    help="directory of the disk tier (packed block files); off when absent")
+                    help="directory of the disk tier (packed block files); the tier is on when "
+                         f"this or --redis-url is given (default root {DEFAULT_DFS_ROOT})")
     ap.add_argument("--dfs-quota", type=parse_memory_size, default=parse_memory_size("50gb"))
     ap.add_argument("--dfs-io-threads", type=int, default=4)
+    ap.add_argument("--redis-url", default=None,
+                    help="turns the disk tier on, as in the reference; its index is kept in "
+                         "sidecar files next to the packed files, so Redis itself is not used")
+    ap.add_argument("--dfs-scan-interval-ms", type=int, default=100,
+                    help="accepted for compatibility (quota is enforced after every write)")
+    # Reference options for parts this server does not have.
+    ap.add_argument("--use-hugepages", action="store_true")
+    ap.add_argument("--pre-evict", action="store_true")
+    ap.add_argument("--pre-evict-threshold", type=parse_memory_size,
+                    default=parse_memory_size("5gb"))
+    ap.add_argument("--pre-evict-target", type=parse_memory_size, default=parse_memory_size("8gb"))
+    ap.add_argument("--pre-evict-interval-ms", type=int, default=100)
+    ap.add_argument("--disable-lfu-admission", action="store_true")
+    ap.add_argument("--metrics-otel-endpoint", default="http://127.0.0.1:4321")
+    ap.add_argument("--metrics-period-secs", type=int, default=5)
     args = ap.parse_args(argv)
+    if args.dfs_root is None and args.redis_url:
+        args.dfs_root = DEFAULT_DFS_ROOT
+    return args
+
+
+def unsupported_options(args) -> list[str]:
+    """Reference options given on the command line that change nothing here."""
+    out = []
+    if args.use_hugepages:
+        out.append("--use-hugepages: the pool is hipHostMalloc memory (registering existing "
+                   "huge pages is refused on this platform)")
+    if args.pre_evict:
+        out.append("--pre-evict: blocks are evicted on demand when an allocation does not fit")
+    return out
+
+
+def main(argv=None) -> int:
+    args = parse_args(argv)
     logging.basicConfig(level=getattr(logging, args.log_level.upper(), logging.INFO),
                         format="%(asctime)s %(levelname)s %(name)s: %(message)s")
+    for msg in unsupported_options(args):
+        log.warning("option without effect in this server: %s", msg)
     from .. import runtime
     runtime.init(args.device)
     server = Server(args.addr, pool_size=args.pool_size, unit_size_hint=args.hint_value_size,

@@ -71,6 +71,31 @@ def test_parse_memory_size_basic():
     assert parse_memory_size("7b") == 7
 
 
+def test_cli_accepts_the_reference_launch_command():
+    """Every option of the reference's server (pegaflow-server/src/lib.rs:38-113)
+    parses, with its defaults; --redis-url turns the disk tier on at the
+    reference's default root, and options without effect are reported."""
+    from pegaflow_amd.rpc.server import DEFAULT_DFS_ROOT, parse_args, unsupported_options
+
+    d = parse_args([])
+    assert (d.addr, d.device, d.pool_size, d.log_level) == ("127.0.0.1:50055", 0, 30 << 30, "info")
+    assert d.dfs_root is None and d.dfs_quota == 50 << 30 and unsupported_options(d) == []
+    assert (d.pre_evict_threshold, d.pre_evict_target, d.pre_evict_interval_ms) == \
+        (5 << 30, 8 << 30, 100)
+    a = parse_args(["--addr", "0.0.0.0:50055", "--device", "1", "--pool-size", "10gb",
+                    "--hint-value-size", "64kb", "--use-hugepages", "--pre-evict",
+                    "--pre-evict-threshold", "1gb", "--pre-evict-target", "2gb",
+                    "--pre-evict-interval-ms", "50", "--disable-lfu-admission",
+                    "--metrics-otel-endpoint", "", "--metrics-period-secs", "10",
+                    "--log-level", "debug", "--redis-url", "redis://127.0.0.1:6379",
+                    "--dfs-quota", "1tb", "--dfs-scan-interval-ms", "200"])
+    assert a.pool_size == 10 << 30 and a.hint_value_size == 64 << 10 and a.device == 1
+    assert a.dfs_root == DEFAULT_DFS_ROOT and a.dfs_quota == 1 << 40
+    notes = unsupported_options(a)
+    assert len(notes) == 2 and notes[0].startswith("--use-hugepages")
+    assert parse_args(["--dfs-root", "/mnt/x"]).dfs_root == "/mnt/x"
+
+
 def test_parse_memory_size_invalid():
     for bad in ("", "abc", "-10gb", "10pb", "1_000"):
         with pytest.raises(ValueError):
