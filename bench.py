@@ -23,7 +23,7 @@ Printed JSON line (stdout):
                    cores, on a bounded sample of the same workload
   other workloads  (skipped with --quick) layerwise_qwen3_8b, mla_latent,
                    tp8_rank_llama3_8b, fragmentation_llama3_8b,
-                   engine_llama3_8b, disk_tier_llama3_8b and
+                   engine_llama3_8b, two_process_llama3_8b, disk_tier_llama3_8b and
                    pinned_copy_microbench (single-block copy latency)
 Everything else goes to stderr.
 """
@@ -375,6 +375,110 @@ def pinned_copy_microbench(iters=2000):
         raise RuntimeError(f"bench_pinned_copy failed ({r.returncode}): {r.stderr.strip()}")
     out = json.loads(r.stdout.strip().splitlines()[-1])
     log(f"[bench] {out}")
+    return out
+
+
+def _start_server(pool_bytes):
+    """pegaflow_amd.rpc.server as a child process on an ephemeral port."""
+    import select
+    import subprocess
+
+    cmd = [sys.executable, "-u", "-m", "pegaflow_amd.rpc.server", "--addr", "127.0.0.1:0",
+           "--pool-size", f"{pool_bytes >> 20}mb", "--log-level", "warning"]
+    p = subprocess.Popen(cmd, cwd=os.path.dirname(os.path.abspath(__file__)),
+                         stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    t0, seen = time.monotonic(), []
+    while time.monotonic() - t0 < 120:
+        r, _, _ = select.select([p.stdout], [], [], 1.0)
+        if r:
+            line = p.stdout.readline()
+            if not line:
+                break
+            seen.append(line)
+            if line.startswith("READY "):
+                return p, line.split()[1]
+        if p.poll() is not None:
+            break
+    p.kill()
+    p.wait(10)
+    raise RuntimeError("engine server did not start:\n" + "".join(seen))
+
+
+def leg_two_process(layers, ids, targets, P, reps=4):
+    """The deployment path of the reference: the inference process keeps its
+    layer tensors and talks gRPC to an engine server in another process,
+    which maps the tensors through HIP IPC (registry.rs:144-175).  The
+    inference side saves the prefix by hash (service.rs save), then restores
+    it by hash into other blocks with a LoadState and polls it, as the
+    connector's start_load_kv / get_finished do (worker.py:148-286).  The
+    restore time runs from the Load RPC to the LoadState reading ready."""
+    import hashlib
+
+    from pegaflow_amd import ipc
+    from pegaflow_amd import workload as wl
+    from pegaflow_amd.load_state import PyLoadState
+    from pegaflow_amd.rpc.client import EngineRpcClient
+
+    shape = layers.shape
+    names = [f"model.layers.{l}.self_attn" for l in range(len(layers.bufs))]
+    handles = [ipc.export_tensor(b.ptr, shape.layer_bytes, 0) for b in layers.bufs]
+    ids_l, targets_l = [int(i) for i in ids], [int(t) for t in targets]
+    layers.refill()
+    p, addr = _start_server((reps + 2) * P + (256 << 20))
+    out = {"what": "llama prefix saved and restored by hash through the gRPC engine server in "
+                   "a second process that maps the 32 layer tensors through HIP IPC; restore "
+                   "timed from the Load RPC to the LoadState reading ready, median of the warm "
+                   "calls"}
+    try:
+        with EngineRpcClient(f"http://{addr}", connect_timeout_s=30) as client:
+            t0 = time.perf_counter()
+            for name, handle in zip(names, handles):
+                ok, msg = client.register_context("bench", "llama3-8b", 0, 1, 0, len(names), name,
+                                                  handle, shape.num_blocks,
+                                                  shape.bytes_per_block, shape.kv_stride_bytes,
+                                                  shape.segments)
+                assert ok, msg
+            out["register_ms"] = round((time.perf_counter() - t0) * 1e3, 1)
+            save_ms, hashes = [], None
+            for r in range(reps + 1):
+                hashes = [hashlib.sha256(b"rpc%d-" % r + i.to_bytes(8, "little")).digest()
+                          for i in ids_l]
+                t0 = time.perf_counter()
+                ok, msg = client.save("bench", 0, 0, [(n, ids_l, hashes) for n in names])
+                save_ms.append((time.perf_counter() - t0) * 1e3)
+                assert ok, msg
+            load_ms, first_ms = [], []
+            for layered in (False, True):
+                for r in range(reps + 1):
+                    st = PyLoadState(num_layers=len(names)) if layered else PyLoadState()
+                    t0 = time.perf_counter()
+                    ok, msg = client.load("bench", 0, 0, st.shm_name(), names, targets_l, hashes)
+                    assert ok, msg
+                    t_first = None
+                    while not st.is_ready():
+                        if layered and t_first is None and st.layers_done() >= 1:
+                            t_first = time.perf_counter()
+                        if time.perf_counter() - t0 > 60:
+                            raise RuntimeError("two-process restore did not complete in 60 s")
+                    t1 = time.perf_counter()
+                    assert st.get_state() == 1
+                    (first_ms if layered else load_ms).append(
+                        ((t_first or t1) - t0) * 1e3 if layered else (t1 - t0) * 1e3)
+            bad = wl.verify_restored(layers, ids, targets)
+            ok, msg = client.unregister_context("bench")
+            assert ok, msg
+            client.shutdown()
+        p.wait(60)
+    finally:
+        if p.poll() is None:
+            p.kill()
+            p.wait(10)
+    layers.refill()
+    med = lambda v: statistics.median(v[1:])  # noqa: E731
+    out.update({"save_ms": round(med(save_ms), 2), "save_gbps": round(P / med(save_ms) / 1e6, 2),
+                "restore_ms": round(med(load_ms), 2),
+                "restore_gbps": round(P / med(load_ms) / 1e6, 2),
+                "first_layer_ms": round(med(first_ms), 2), "bit_exact": bad == 0})
     return out
 
 
@@ -825,6 +929,9 @@ def main():
         log("[bench] engine: save and restore by hash")
         extra["engine_llama3_8b"] = leg_engine(layers, ids, targets, P)
         log(f"[bench] {extra['engine_llama3_8b']}")
+        log("[bench] two processes: gRPC engine server mapping the layers by HIP IPC")
+        extra["two_process_llama3_8b"] = leg_two_process(layers, ids, targets, P)
+        log(f"[bench] {extra['two_process_llama3_8b']}")
         log("[bench] disk tier: offload, cold prefetch, restore")
         extra["disk_tier_llama3_8b"] = leg_disk(layers, ids, targets, P)
         log(f"[bench] {extra['disk_tier_llama3_8b']}")

@@ -306,6 +306,17 @@ enum {
  * "loads" of device memory).  pf_xfer_set_kernel_shape sets every route. */
 int pf_xfer_set_kernel_shape_dir(pf_xfer* xfer, uint32_t direction,
                                  uint32_t threads, uint32_t unroll);
+/* Work distribution per route.  0: one workgroup per tile, dealt to the XCDs
+ * by the hardware (best for HBM-bound copies).  N > 0: N persistent
+ * workgroups take tiles from a queue in order (best over the host link,
+ * whose bandwidth the XCDs do not share fairly: the queue keeps tiles, and
+ * a marked load's layers, finishing in order, and few requests in flight
+ * keep the link at its peak).  Marked launches always run queued (at
+ * PF_LOAD_HOST_DEFAULT_GRID when their route says 0).  pf_xfer_set_max_grid
+ * caps both kinds. */
+#define PF_SAVE_HOST_DEFAULT_GRID 32u
+#define PF_LOAD_HOST_DEFAULT_GRID 64u
+int pf_xfer_set_route_grid(pf_xfer* xfer, uint32_t route, uint32_t workgroups);
 int pf_xfer_set_kernel_shape(pf_xfer* xfer, uint32_t threads, uint32_t unroll);
 /* Upper bound on workgroups per gather/scatter launch (0 = one workgroup per
  * tile, the default); with a bound, each workgroup loops over tiles. */

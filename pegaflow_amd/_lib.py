@@ -72,6 +72,9 @@ SAVE_HOST_DEFAULT_SHAPE = (512, 2 | KERNEL_NT_LOADS)
 LOAD_HOST_DEFAULT_SHAPE = (512, 2 | KERNEL_NONTEMPORAL | KERNEL_XCD_MAJOR)
 # Launch-shape routes (PF_ROUTE_*): direction x where the far side lives.
 ROUTE_SAVE_DEVICE, ROUTE_LOAD_DEVICE, ROUTE_SAVE_HOST, ROUTE_LOAD_HOST = 0, 1, 2, 3
+SAVE_HOST_DEFAULT_GRID, LOAD_HOST_DEFAULT_GRID = 32, 64
+DEFAULT_GRIDS = {ROUTE_SAVE_DEVICE: 0, ROUTE_LOAD_DEVICE: 0,
+                 ROUTE_SAVE_HOST: SAVE_HOST_DEFAULT_GRID, ROUTE_LOAD_HOST: LOAD_HOST_DEFAULT_GRID}
 DEFAULT_SHAPES = {ROUTE_SAVE_DEVICE: SAVE_DEFAULT_SHAPE, ROUTE_LOAD_DEVICE: LOAD_DEFAULT_SHAPE,
                   ROUTE_SAVE_HOST: SAVE_HOST_DEFAULT_SHAPE, ROUTE_LOAD_HOST: LOAD_HOST_DEFAULT_SHAPE}
 
@@ -248,6 +251,7 @@ SIGNATURES = {
     "pf_xfer_last_stats": (i32, [vp, pu64, pu64]),
     "pf_xfer_set_max_grid": (i32, [vp, u32]),
     "pf_xfer_set_kernel_shape_dir": (i32, [vp, u32, u32, u32]),
+    "pf_xfer_set_route_grid": (i32, [vp, u32, u32]),
     "pf_xfer_set_timing": (i32, [vp, i32]),
     "pf_xfer_last_kernel_ms": (i32, [vp, ctypes.POINTER(ctypes.c_float), pu64]),
     "pf_save_layers": (i32, [vp, ctypes.POINTER(LayerXfer), u32, u32]),

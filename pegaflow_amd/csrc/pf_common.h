@@ -66,8 +66,16 @@ struct LayerList {
 hipError_t launch_copy_chunks(const ChunkDesc* d_descs, uint32_t n_chunks,
                               uint64_t chunk_bytes, bool aligned16,
                               uint32_t threads, uint32_t unroll,
-                              uint32_t max_grid, const LayerMarks* marks,
-                              hipStream_t stream);
+                              uint32_t max_grid, hipStream_t stream);
+// The queued copy (16-byte aligned chunks only): `grid` persistent
+// workgroups pull tiles from the counter at next_tile, which holds `base`
+// when the launch starts and base + *n_tiles + grid when it ends.  With
+// marks, each finished layer is marked.
+hipError_t launch_copy_chunks_queue(const ChunkDesc* d_descs, uint32_t n_chunks,
+                                    uint64_t chunk_bytes, uint32_t threads, uint32_t unroll,
+                                    uint32_t grid, const LayerMarks* marks,
+                                    uint32_t* next_tile, uint32_t base, uint32_t* n_tiles,
+                                    hipStream_t stream);
 hipError_t launch_mark_layers(const LayerList& list, const SignalTargets& t,
                               hipStream_t stream);
 hipError_t launch_wait_word(uint64_t word, uint64_t value, uint64_t max_ticks,

@@ -128,11 +128,11 @@ __device__ __forceinline__ void tile_done(const LayerMarks& m, uint32_t c,
   }
 }
 
-template <int UNROLL, bool NTL, bool NTS, bool MARK>
+template <int UNROLL, bool NTL, bool NTS>
 __global__ void __launch_bounds__(1024)
 copy_chunks_v16_kernel(const ChunkDesc* __restrict__ descs,
                        uint32_t tiles_per_chunk, uint32_t n_tiles,
-                       uint32_t chunk16, uint32_t xcd_major, LayerMarks marks) {
+                       uint32_t chunk16, uint32_t xcd_major) {
   const uint32_t stride = blockDim.x;
   const uint32_t tile_elems = stride * UNROLL;
   const bool remap = xcd_major && gridDim.x == n_tiles;
@@ -150,10 +150,7 @@ copy_chunks_v16_kernel(const ChunkDesc* __restrict__ descs,
 #pragma unroll
       for (int u = 0; u < UNROLL; ++u) v[u] = load16<NTL>(src + base + u * stride);
 #pragma unroll
-      for (int u = 0; u < UNROLL; ++u) {
-        if constexpr (MARK) store16_coherent(dst + base + u * stride, v[u]);
-        else store16<NTS>(dst + base + u * stride, v[u]);
-      }
+      for (int u = 0; u < UNROLL; ++u) store16<NTS>(dst + base + u * stride, v[u]);
     } else {
       // Partial last tile of a chunk: guarded per element.
 #pragma unroll
@@ -164,6 +161,68 @@ copy_chunks_v16_kernel(const ChunkDesc* __restrict__ descs,
 #pragma unroll
       for (int u = 0; u < UNROLL; ++u) {
         const uint32_t e = base + u * stride;
+        if (e < chunk16) store16<NTS>(dst + e, v[u]);
+      }
+    }
+  }
+}
+
+// Copies over the host link take their tiles from a work queue instead of a
+// fixed workgroup -> tile map.  Workgroups are dealt to the 8 XCDs
+// statically, and when the copy reads or writes host memory the XCDs
+// progress at very different rates (the link is not shared fairly between
+// them): with a fixed map the copy ends when the slowest XCD does, and a
+// marked load's layers land only when the slowest XCD gets to them
+// (measured: the first of 32 Llama layers after half the load).  Here a
+// small persistent grid pulls tile indices from one counter, so the fast
+// XCDs take more tiles and tiles, hence layers, finish in order; with few
+// requests in flight the link also runs closer to its peak (Llama restore
+// 24.1 -> 23.3 ms of kernel time with 64 workgroups).  The counter is
+// never reset: each launch advances it by exactly n_tiles + gridDim.x
+// (every workgroup's last pull fails), and the host passes the value it
+// starts from as `base`.  MARK adds the per-layer completion marks, with
+// agent-coherent stores (see write_marks).
+template <int UNROLL, bool NTL, bool NTS, bool MARK>
+__global__ void __launch_bounds__(1024)
+copy_chunks_queue_kernel(const ChunkDesc* __restrict__ descs, uint32_t tiles_per_chunk,
+                         uint32_t n_tiles, uint32_t chunk16, LayerMarks marks,
+                         uint32_t* next_tile, uint32_t base) {
+  __shared__ uint32_t s_tile;
+  const uint32_t stride = blockDim.x;
+  const uint32_t tile_elems = stride * UNROLL;
+  for (;;) {
+    if (threadIdx.x == 0)
+      s_tile = __hip_atomic_fetch_add(next_tile, 1u, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) - base;
+    __syncthreads();
+    const uint32_t t = s_tile;
+    __syncthreads();  // every lane has read s_tile before it is written again
+    if (t >= n_tiles) break;  // uniform: the queue is empty for every later pull too
+    const uint32_t c = t / tiles_per_chunk;
+    const uint32_t tile = t - c * tiles_per_chunk;
+    const ChunkDesc d = descs[c];
+    const g_u32x4* __restrict__ src = reinterpret_cast<const g_u32x4*>(d.src);
+    g_u32x4* __restrict__ dst = reinterpret_cast<g_u32x4*>(d.dst);
+    const uint32_t tile_base = tile * tile_elems;
+    const uint32_t base_e = tile_base + threadIdx.x;
+    u32x4 v[UNROLL];
+    if (tile_base + tile_elems <= chunk16) {
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) v[u] = load16<NTL>(src + base_e + u * stride);
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) {
+        if constexpr (MARK) store16_coherent(dst + base_e + u * stride, v[u]);
+        else store16<NTS>(dst + base_e + u * stride, v[u]);
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) {
+        const uint32_t e = base_e + u * stride;
+        if (e < chunk16) v[u] = load16<NTL>(src + e);
+      }
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) {
+        const uint32_t e = base_e + u * stride;
         if (e < chunk16) {
           if constexpr (MARK) store16_coherent(dst + e, v[u]);
           else store16<NTS>(dst + e, v[u]);
@@ -219,91 +278,154 @@ static constexpr uint32_t kMaxGrid = 1u << 20;
 
 template <int UNROLL, bool NTL, bool NTS>
 static void launch_v16_nt(dim3 grid, dim3 block, hipStream_t stream, const ChunkDesc* d,
-                          uint32_t tpc, uint32_t n_tiles, uint32_t c16, uint32_t xcd,
-                          const LayerMarks* marks) {
-  if (marks)
-    hipLaunchKernelGGL((copy_chunks_v16_kernel<UNROLL, NTL, NTS, true>), grid, block, 0,
-                       stream, d, tpc, n_tiles, c16, xcd, *marks);
-  else
-    hipLaunchKernelGGL((copy_chunks_v16_kernel<UNROLL, NTL, NTS, false>), grid, block, 0,
-                       stream, d, tpc, n_tiles, c16, xcd, LayerMarks{});
+                          uint32_t tpc, uint32_t n_tiles, uint32_t c16, uint32_t xcd) {
+  hipLaunchKernelGGL((copy_chunks_v16_kernel<UNROLL, NTL, NTS>), grid, block, 0, stream, d,
+                     tpc, n_tiles, c16, xcd);
 }
 
 template <int UNROLL>
 static hipError_t launch_v16(const ChunkDesc* d_descs, uint32_t tiles_per_chunk,
                              uint32_t n_tiles, uint32_t chunk16, uint32_t threads,
-                             uint32_t flags, uint32_t max_grid, const LayerMarks* marks,
-                             hipStream_t stream) {
+                             uint32_t flags, uint32_t max_grid, hipStream_t stream) {
   const uint32_t cap = max_grid ? max_grid : kMaxGrid;
   const dim3 grid(n_tiles < cap ? n_tiles : cap), block(threads);
   const uint32_t xcd = (flags & PF_KERNEL_XCD_MAJOR) ? 1u : 0u;
   switch (flags & PF_KERNEL_NONTEMPORAL) {
     case 0:
       launch_v16_nt<UNROLL, false, false>(grid, block, stream, d_descs, tiles_per_chunk, n_tiles,
-                                          chunk16, xcd, marks);
+                                          chunk16, xcd);
       break;
     case PF_KERNEL_NT_LOADS:
       launch_v16_nt<UNROLL, true, false>(grid, block, stream, d_descs, tiles_per_chunk, n_tiles,
-                                         chunk16, xcd, marks);
+                                         chunk16, xcd);
       break;
     case PF_KERNEL_NT_STORES:
       launch_v16_nt<UNROLL, false, true>(grid, block, stream, d_descs, tiles_per_chunk, n_tiles,
-                                         chunk16, xcd, marks);
+                                         chunk16, xcd);
       break;
     default:
       launch_v16_nt<UNROLL, true, true>(grid, block, stream, d_descs, tiles_per_chunk, n_tiles,
-                                        chunk16, xcd, marks);
+                                        chunk16, xcd);
       break;
   }
   return hipGetLastError();
 }
 
+template <int UNROLL, bool NTL, bool NTS>
+static void launch_queue_nt(dim3 grid, dim3 block, hipStream_t stream, const ChunkDesc* d,
+                            uint32_t tpc, uint32_t n_tiles, uint32_t c16,
+                            const LayerMarks* marks, uint32_t* next, uint32_t base) {
+  if (marks)
+    hipLaunchKernelGGL((copy_chunks_queue_kernel<UNROLL, NTL, NTS, true>), grid, block, 0,
+                       stream, d, tpc, n_tiles, c16, *marks, next, base);
+  else
+    hipLaunchKernelGGL((copy_chunks_queue_kernel<UNROLL, NTL, NTS, false>), grid, block, 0,
+                       stream, d, tpc, n_tiles, c16, LayerMarks{}, next, base);
+}
+
+template <int UNROLL>
+static void launch_queue(dim3 grid, dim3 block, hipStream_t stream, const ChunkDesc* d,
+                         uint32_t tpc, uint32_t n_tiles, uint32_t c16, uint32_t flags,
+                         const LayerMarks* marks, uint32_t* next, uint32_t base) {
+  switch (flags & PF_KERNEL_NONTEMPORAL) {
+    case 0:
+      launch_queue_nt<UNROLL, false, false>(grid, block, stream, d, tpc, n_tiles, c16, marks,
+                                            next, base);
+      break;
+    case PF_KERNEL_NT_LOADS:
+      launch_queue_nt<UNROLL, true, false>(grid, block, stream, d, tpc, n_tiles, c16, marks,
+                                           next, base);
+      break;
+    case PF_KERNEL_NT_STORES:
+      launch_queue_nt<UNROLL, false, true>(grid, block, stream, d, tpc, n_tiles, c16, marks,
+                                           next, base);
+      break;
+    default:
+      launch_queue_nt<UNROLL, true, true>(grid, block, stream, d, tpc, n_tiles, c16, marks,
+                                          next, base);
+      break;
+  }
+}
+
+// Tiles of a launch: every tile index < n_tiles maps to chunk < n_chunks and
+// element offsets < tiles_per_chunk * tile_elems; elements >= chunk16 are
+// masked, and the full-tile path is taken only when the whole tile lies
+// below chunk16.  chunk16 < 2^31 and tile_elems <= 16384 keep
+// tile_base + tile_elems in 32 bits.
+static bool tile_geometry(uint32_t n_chunks, uint64_t chunk_bytes, uint32_t threads,
+                          uint32_t unroll, uint32_t* tpc, uint32_t* n_tiles, uint32_t* c16) {
+  const uint64_t chunk16 = chunk_bytes / 16;
+  if (chunk16 >= (1ull << 31)) return false;
+  const uint64_t tile_elems = static_cast<uint64_t>(threads) * unroll;
+  if (tile_elems == 0) return false;
+  const uint64_t tiles_per_chunk = (chunk16 + tile_elems - 1) / tile_elems;
+  const uint64_t tiles = tiles_per_chunk * n_chunks;
+  if (tiles > 0xffffffffull) return false;
+  *tpc = static_cast<uint32_t>(tiles_per_chunk);
+  *n_tiles = static_cast<uint32_t>(tiles);
+  *c16 = static_cast<uint32_t>(chunk16);
+  return true;
+}
+
 // `unroll` carries the loads in flight per lane (low byte) and the
 // PF_KERNEL_NT_LOADS / PF_KERNEL_NT_STORES / PF_KERNEL_XCD_MAJOR flags.
-// `marks` (16-byte path only) makes the kernel mark each layer's completion.
 hipError_t launch_copy_chunks(const ChunkDesc* d_descs, uint32_t n_chunks,
                               uint64_t chunk_bytes, bool aligned16,
                               uint32_t threads, uint32_t unroll,
-                              uint32_t max_grid, const LayerMarks* marks,
-                              hipStream_t stream) {
+                              uint32_t max_grid, hipStream_t stream) {
   if (n_chunks == 0 || chunk_bytes == 0) return hipSuccess;
   if (threads == 0 || threads > 1024 || threads % 64 != 0) return hipErrorInvalidValue;
   const uint32_t flags = unroll & (PF_KERNEL_NONTEMPORAL | PF_KERNEL_XCD_MAJOR);
   unroll &= 0xffu;
   if (max_grid > kMaxGrid) max_grid = kMaxGrid;
   if (!aligned16) {
-    if (marks) return hipErrorInvalidValue;
     const uint32_t grid = n_chunks < kMaxGrid ? n_chunks : kMaxGrid;
     hipLaunchKernelGGL(copy_chunks_b1_kernel, dim3(grid), dim3(threads), 0,
                        stream, d_descs, n_chunks, chunk_bytes);
     return hipGetLastError();
   }
+  uint32_t tpc = 0, ntl = 0, c16 = 0;
+  if (!tile_geometry(n_chunks, chunk_bytes, threads, unroll, &tpc, &ntl, &c16))
+    return hipErrorInvalidValue;
+  switch (unroll) {
+    case 1: return launch_v16<1>(d_descs, tpc, ntl, c16, threads, flags, max_grid, stream);
+    case 2: return launch_v16<2>(d_descs, tpc, ntl, c16, threads, flags, max_grid, stream);
+    case 4: return launch_v16<4>(d_descs, tpc, ntl, c16, threads, flags, max_grid, stream);
+    case 8: return launch_v16<8>(d_descs, tpc, ntl, c16, threads, flags, max_grid, stream);
+    case 16: return launch_v16<16>(d_descs, tpc, ntl, c16, threads, flags, max_grid, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_copy_chunks_queue(const ChunkDesc* d_descs, uint32_t n_chunks,
+                                    uint64_t chunk_bytes, uint32_t threads, uint32_t unroll,
+                                    uint32_t grid, const LayerMarks* marks,
+                                    uint32_t* next_tile, uint32_t base, uint32_t* n_tiles,
+                                    hipStream_t stream) {
+  *n_tiles = 0;
+  if (n_chunks == 0 || chunk_bytes == 0) return hipSuccess;
+  if (threads == 0 || threads > 1024 || threads % 64 != 0 || grid == 0 || !next_tile)
+    return hipErrorInvalidValue;
   if (marks && (marks->n == 0 || !marks->chunk_start || !marks->layer || !marks->counters ||
                 marks->targets.count == 0 || marks->targets.count > kMaxSignalTargets))
     return hipErrorInvalidValue;
-  const uint64_t chunk16 = chunk_bytes / 16;
-  if (chunk16 >= (1ull << 31)) return hipErrorInvalidValue;
-  const uint64_t tile_elems = static_cast<uint64_t>(threads) * unroll;
-  if (tile_elems == 0) return hipErrorInvalidValue;
-  const uint64_t tiles_per_chunk = (chunk16 + tile_elems - 1) / tile_elems;
-  const uint64_t n_tiles = tiles_per_chunk * n_chunks;
-  if (n_tiles > 0xffffffffull) return hipErrorInvalidValue;
-  // Every tile index < n_tiles maps to chunk < n_chunks and element offsets
-  // < tiles_per_chunk * tile_elems; elements >= chunk16 are masked, and the
-  // full-tile path is taken only when the whole tile lies below chunk16.
-  // chunk16 < 2^31 and tile_elems <= 16384 keep tile_base + tile_elems in 32 bits.
-  const uint32_t tpc = static_cast<uint32_t>(tiles_per_chunk);
-  const uint32_t ntl = static_cast<uint32_t>(n_tiles);
-  const uint32_t c16 = static_cast<uint32_t>(chunk16);
+  const uint32_t flags = unroll & PF_KERNEL_NONTEMPORAL;
+  unroll &= 0xffu;
+  uint32_t tpc = 0, ntiles = 0, c16 = 0;
+  if (!tile_geometry(n_chunks, chunk_bytes, threads, unroll, &tpc, &ntiles, &c16))
+    return hipErrorInvalidValue;
+  if (static_cast<uint64_t>(ntiles) + grid > 0xffffffffull) return hipErrorInvalidValue;
+  const dim3 g(grid), b(threads);
   switch (unroll) {
-    case 1: return launch_v16<1>(d_descs, tpc, ntl, c16, threads, flags, max_grid, marks, stream);
-    case 2: return launch_v16<2>(d_descs, tpc, ntl, c16, threads, flags, max_grid, marks, stream);
-    case 4: return launch_v16<4>(d_descs, tpc, ntl, c16, threads, flags, max_grid, marks, stream);
-    case 8: return launch_v16<8>(d_descs, tpc, ntl, c16, threads, flags, max_grid, marks, stream);
-    case 16:
-      return launch_v16<16>(d_descs, tpc, ntl, c16, threads, flags, max_grid, marks, stream);
+    case 1: launch_queue<1>(g, b, stream, d_descs, tpc, ntiles, c16, flags, marks, next_tile, base); break;
+    case 2: launch_queue<2>(g, b, stream, d_descs, tpc, ntiles, c16, flags, marks, next_tile, base); break;
+    case 4: launch_queue<4>(g, b, stream, d_descs, tpc, ntiles, c16, flags, marks, next_tile, base); break;
+    case 8: launch_queue<8>(g, b, stream, d_descs, tpc, ntiles, c16, flags, marks, next_tile, base); break;
+    case 16: launch_queue<16>(g, b, stream, d_descs, tpc, ntiles, c16, flags, marks, next_tile, base); break;
     default: return hipErrorInvalidValue;
   }
+  *n_tiles = ntiles;
+  return hipGetLastError();
 }
 
 hipError_t launch_mark_layers(const LayerList& list, const SignalTargets& t,

@@ -265,9 +265,16 @@ struct pf_xfer {
   uint64_t last_dma = 0;
   bool timing = false;
   std::vector<std::pair<hipEvent_t, hipEvent_t>> timers;  // one pair per launch
-  // Per-layer tile counters of marking launches (0 between launches).
+  // Per-layer tile counters of marking launches (0 between launches), and
+  // the tile queue of the marking kernel in its own cache line after them:
+  // it only grows, by n_tiles + grid per launch, from next_base.
   uint32_t* d_counters = nullptr;
   size_t counters_cap = 0;
+  uint32_t* d_next = nullptr;
+  uint32_t next_base = 0;
+  // Persistent workgroups of a queued launch per route (0: a fixed
+  // workgroup per tile).  Copies over the host link run queued.
+  uint32_t grid[4] = {0, 0, PF_SAVE_HOST_DEFAULT_GRID, PF_LOAD_HOST_DEFAULT_GRID};
   std::mutex mu;
 };
 
@@ -354,10 +361,26 @@ int launch(pf_xfer* x, size_t first, size_t n, uint64_t chunk_bytes, bool al16, 
     tm = &x->timers[x->last_kernels];
     PF_HIP(hipEventRecord(tm->first, x->stream));
   }
+  // Queued launches: copies over the host link, and every marking launch
+  // (its layers must land in order).  See copy_chunks_queue_kernel.
+  uint32_t qgrid = x->grid[dir];
+  if (marks && qgrid == 0) qgrid = PF_LOAD_HOST_DEFAULT_GRID;
+  if (x->max_grid && qgrid > x->max_grid) qgrid = x->max_grid;
   (void)hipGetLastError();
-  hipError_t e = launch_copy_chunks(x->desc_base + first, static_cast<uint32_t>(n),
-                                    chunk_bytes, al16, x->threads[dir], x->unroll[dir],
-                                    x->max_grid, marks, x->stream);
+  hipError_t e = hipSuccess;
+  if (al16 && qgrid > 0) {
+    if (!x->d_next) return fail(PF_ERR_INVALID_ARGUMENT, "tile queue not allocated");
+    uint32_t n_tiles = 0;
+    e = launch_copy_chunks_queue(x->desc_base + first, static_cast<uint32_t>(n), chunk_bytes,
+                                 x->threads[dir], x->unroll[dir], qgrid, marks, x->d_next,
+                                 x->next_base, &n_tiles, x->stream);
+    if (e == hipSuccess) x->next_base += n_tiles + qgrid;
+  } else if (marks) {
+    return fail(PF_ERR_INVALID_ARGUMENT, "a marking launch needs 16-byte aligned chunks");
+  } else {
+    e = launch_copy_chunks(x->desc_base + first, static_cast<uint32_t>(n), chunk_bytes, al16,
+                           x->threads[dir], x->unroll[dir], x->max_grid, x->stream);
+  }
   if (e != hipSuccess) return hip_fail(e, "gather/scatter kernel launch");
   if (tm) PF_HIP(hipEventRecord(tm->second, x->stream));
   x->last_kernels++;
@@ -373,9 +396,14 @@ int ensure_counters(pf_xfer* x, size_t num_layers) {
   PF_HIP(hipStreamSynchronize(x->stream));  // earlier launches may still count
   if (x->d_counters) PF_HIP(hipFree(x->d_counters));
   x->d_counters = nullptr;
+  x->d_next = nullptr;
   x->counters_cap = 0;
-  PF_HIP(hipMalloc(reinterpret_cast<void**>(&x->d_counters), cap * sizeof(uint32_t)));
-  PF_HIP(hipMemsetAsync(x->d_counters, 0, cap * sizeof(uint32_t), x->stream));
+  // cap counters, then one 256-byte line holding the tile queue.
+  const size_t words = cap + 64;
+  PF_HIP(hipMalloc(reinterpret_cast<void**>(&x->d_counters), words * sizeof(uint32_t)));
+  PF_HIP(hipMemsetAsync(x->d_counters, 0, words * sizeof(uint32_t), x->stream));
+  x->d_next = x->d_counters + cap;
+  x->next_base = 0;
   x->counters_cap = cap;
   return PF_OK;
 }
@@ -664,8 +692,8 @@ int kernel_direct(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<Lay
   if (total > 0xffffffffull) return fail(PF_ERR_INVALID_ARGUMENT, "too many chunks");
   const size_t aux_desc = (aux.size() * sizeof(uint32_t) + sizeof(ChunkDesc) - 1) /
                           sizeof(ChunkDesc);
-  if (sig)
-    if (int rc = ensure_counters(x, plans.size())) return rc;
+  // Counters for marks and the tile queue of queued launches.
+  if (int rc = ensure_counters(x, plans.size())) return rc;
   ChunkDesc* hd = small_desc(x, total + aux_desc);
   if (!hd) {
     if (int rc = ensure_desc_capacity(x, total + aux_desc)) return rc;
@@ -964,6 +992,17 @@ int pf_xfer_set_kernel_shape_dir(pf_xfer* x, uint32_t direction, uint32_t thread
   std::lock_guard<std::mutex> lk(x->mu);
   if (threads) x->threads[direction] = threads;
   if (unroll) x->unroll[direction] = unroll;
+  return PF_OK;
+}
+
+int pf_xfer_set_route_grid(pf_xfer* x, uint32_t route, uint32_t workgroups) {
+  if (!x) return fail(PF_ERR_INVALID_ARGUMENT, "null transfer context");
+  if (route > PF_ROUTE_LOAD_HOST)
+    return fail(PF_ERR_INVALID_ARGUMENT, "route must be 0..3 (PF_ROUTE_*)");
+  if (workgroups > (1u << 20))
+    return fail(PF_ERR_INVALID_ARGUMENT, "at most 2^20 persistent workgroups");
+  std::lock_guard<std::mutex> lk(x->mu);
+  x->grid[route] = workgroups;
   return PF_OK;
 }
 

@@ -210,10 +210,18 @@ class TransferContext:
         check(lib().pf_xfer_set_kernel_shape_dir(self.handle, direction, threads, unroll),
               "pf_xfer_set_kernel_shape_dir")
 
+    def set_route_grid(self, route: int, workgroups: int) -> None:
+        """Persistent workgroups pulling tiles from a queue on this route (0:
+        one workgroup per tile)."""
+        check(lib().pf_xfer_set_route_grid(self.handle, route, workgroups),
+              "pf_xfer_set_route_grid")
+
     def reset_kernel_shape(self) -> None:
-        """Back to the per-route defaults."""
+        """Back to the per-route defaults (shapes and work distribution)."""
         for route, shape in _lib.DEFAULT_SHAPES.items():
             self.set_kernel_shape_dir(route, *shape)
+        for route, grid in _lib.DEFAULT_GRIDS.items():
+            self.set_route_grid(route, grid)
 
     def set_max_grid(self, max_workgroups: int) -> None:
         check(lib().pf_xfer_set_max_grid(self.handle, max_workgroups), "pf_xfer_set_max_grid")

@@ -335,12 +335,41 @@ def test_xcd_major_tile_order(ctx, shape):
 
 
 def test_capped_grid_loops_over_tiles(ctx):
+    """A grid cap makes the fixed-map kernel loop over tiles (device routes:
+    the staged mode's gather and scatter) and shrinks the queued kernel's
+    persistent grid (host routes)."""
     say("[gpu] capped grid")
-    for grid in (1, 7, 256):
-        ctx.set_max_grid(grid)
-        _oracle_roundtrip_case(ctx, _lib.MODE_KERNEL, 64, 32768, 2, 64 * 32768, 128 * 32768,
-                               list(range(0, 64, 3)), list(range(63, -1, -3)), seed=grid)
+    for mode in (_lib.MODE_KERNEL, _lib.MODE_STAGED):
+        for grid in (1, 7, 256):
+            ctx.set_max_grid(grid)
+            _oracle_roundtrip_case(ctx, mode, 64, 32768, 2, 64 * 32768, 128 * 32768,
+                                   list(range(0, 64, 3)), list(range(63, -1, -3)),
+                                   seed=grid + mode)
     ctx.set_max_grid(0)
+
+
+@pytest.mark.parametrize("grid", [0, 1, 3, 32, 64, 5000])
+def test_queued_host_routes(ctx, grid):
+    """Work distribution over the host link: 0 = one workgroup per tile with
+    the hardware's deal; N = N persistent workgroups pulling tiles from the
+    queue, including a single workgroup and more workgroups than tiles.  The
+    queue counter carries over from launch to launch, so several calls and
+    several launches per call (layers of different chunk sizes) must all
+    copy every tile exactly once."""
+    say(f"[gpu] queued host routes grid={grid}")
+    ctx.set_route_grid(_lib.ROUTE_SAVE_HOST, grid)
+    ctx.set_route_grid(_lib.ROUTE_LOAD_HOST, grid)
+    try:
+        for rep in range(2):
+            _oracle_roundtrip_case(ctx, _lib.MODE_KERNEL, 64, 32768, 2, 64 * 32768, 128 * 32768,
+                                   list(range(0, 64, 3)), list(range(63, -1, -3)),
+                                   seed=grid + rep)
+            _oracle_roundtrip_case(ctx, _lib.MODE_KERNEL, 20, 16 * 1000, 2, 20 * 16000,
+                                   40 * 16000, [3, 19, 0], [5, 6, 7], seed=grid + 7)
+            _oracle_roundtrip_case(ctx, _lib.MODE_KERNEL, 64, 73728, 1, 0, 64 * 73728,
+                                   [5, 60, 2, 33], [0, 1, 63, 9], seed=grid + 9)
+    finally:
+        ctx.reset_kernel_shape()
 
 
 def _full_size(ctx, n_layers, nb, bpb, segs, n_blocks, save_mode, load_mode, seed=0):
