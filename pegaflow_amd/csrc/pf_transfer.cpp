@@ -586,6 +586,8 @@ int staged(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<LayerPlan>
         if (int r = check_device_tensor(rc, layers[i].layout)) return r;
   }
   if (int rc = ensure_desc_capacity(x, n_desc)) return rc;
+  // The tile queue, for device routes a caller has set to run queued.
+  if (int rc = ensure_counters(x, plans.size())) return rc;
   for (const Slice& s : slices) {
     const LayerPlan& p = plans[s.layer];
     const uint64_t slot_base = x->staging + static_cast<uint64_t>(s.slot) * x->slot_bytes;

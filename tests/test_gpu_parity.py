@@ -368,6 +368,13 @@ def test_queued_host_routes(ctx, grid):
                                    40 * 16000, [3, 19, 0], [5, 6, 7], seed=grid + 7)
             _oracle_roundtrip_case(ctx, _lib.MODE_KERNEL, 64, 73728, 1, 0, 64 * 73728,
                                    [5, 60, 2, 33], [0, 1, 63, 9], seed=grid + 9)
+        if grid:
+            # Device routes queued too (the staged mode's gather and scatter).
+            ctx.set_route_grid(_lib.ROUTE_SAVE_DEVICE, grid)
+            ctx.set_route_grid(_lib.ROUTE_LOAD_DEVICE, grid)
+            _oracle_roundtrip_case(ctx, _lib.MODE_STAGED, 64, 32768, 2, 64 * 32768,
+                                   128 * 32768, list(range(0, 64, 5)), list(range(63, 0, -5)),
+                                   seed=grid + 11)
     finally:
         ctx.reset_kernel_shape()
 
