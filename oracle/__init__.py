@@ -1,7 +1,7 @@
 """CPU oracle for PegaFlow's KV-block transfer path.
 
-TEST INFRASTRUCTURE ONLY.  This package is the checker for the HIP product
-path (``pegaflow_amd``) and the CPU baseline timed beside it.  Only ``tests/``,
+TEST INFRASTRUCTURE ONLY.  The HIP product path (``pegaflow_amd``) is tested
+against this package, and it is the CPU baseline timed beside it.  Only ``tests/``,
 ``__graft_entry__.smoke()`` and the CPU-baseline leg of ``bench.py`` may import
 it; the product never does.
 

@@ -1,8 +1,8 @@
 /*
  * pf_oracle.c — CPU restatement of PegaFlow's KV-block transfer path.
  *
- * TEST INFRASTRUCTURE ONLY: the checker for the HIP product path and the CPU
- * baseline timed beside it.  Nothing in the product loads this file.
+ * TEST INFRASTRUCTURE ONLY: what the HIP product path is tested against, and
+ * the CPU baseline timed beside it.  Nothing in the product loads this file.
  *
  * Reference: xiaguan/pegaflow (Rust).  The reference cannot be built here (no
  * Rust toolchain, and its cudarc dependency needs CUDA), so this is a

@@ -1,8 +1,8 @@
 /*
  * pf_oracle.h — CPU restatement of PegaFlow's KV-block transfer path.
  *
- * TEST INFRASTRUCTURE ONLY.  This oracle is the checker for the HIP product
- * path and the CPU baseline timed beside it.  Only tests/, the smoke check and
+ * TEST INFRASTRUCTURE ONLY.  The HIP product path is tested against this
+ * oracle, and it is the CPU baseline timed beside it.  Only tests/, the smoke check and
  * the benchmark's CPU-baseline leg may load it; the product never does.
  *
  * Every function restates one piece of the reference (xiaguan/pegaflow) with

@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/pf_oracle.c) before it is trusted as the checker.
+"""Pins the CPU oracle (oracle/pf_oracle.c) before the GPU path is tested against it.
 
 Each check is chosen so that a plausible mistake fails it: closed-form offset
 KATs (a wrong stride or a transposed block/segment index), the reference's
