@@ -1096,10 +1096,18 @@ int pf_engine_batch_save(pf_engine* e, const char* instance_id, uint64_t tp_rank
                          "registered)",
                          sl.block_ids[i], name.c_str(),
                          (unsigned long long)plan.layout.num_blocks));
+    // Same list: the same buffers, or (callers that copy per layer, such as
+    // the gRPC service) equal offsets and bytes.
+    auto same_list = [&](const KeyGroup& kg) {
+      if (kg.n != sl.num_blocks) return false;
+      if (kg.data == sl.hash_data && kg.offs == sl.hash_offsets) return true;
+      const size_t n = static_cast<size_t>(sl.num_blocks);
+      return std::memcmp(kg.offs, sl.hash_offsets, (n + 1) * sizeof(uint64_t)) == 0 &&
+             std::memcmp(kg.data + kg.offs[0], sl.hash_data + sl.hash_offsets[0],
+                         static_cast<size_t>(sl.hash_offsets[n] - sl.hash_offsets[0])) == 0;
+    };
     size_t g = 0;
-    while (g < groups.size() && !(groups[g].data == sl.hash_data &&
-                                  groups[g].offs == sl.hash_offsets && groups[g].n == sl.num_blocks))
-      ++g;
+    while (g < groups.size() && !same_list(groups[g])) ++g;
     if (g == groups.size())
       groups.push_back(KeyGroup{sl.hash_data, sl.hash_offsets, sl.num_blocks,
                                 keys_of(inst->ns, sl.hash_data, sl.hash_offsets, sl.num_blocks),

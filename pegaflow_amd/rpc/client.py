@@ -93,9 +93,20 @@ class EngineRpcClient:
     def save(self, instance_id: str, tp_rank: int, device_id: int, saves):
         """python/src/lib.rs:374-405: `saves` is [(layer_name, block_ids, block_hashes)]."""
         req = proto.SaveRequest(instance_id=instance_id, tp_rank=tp_rank, device_id=device_id)
+        # Lists shared by several layers are converted once.  The cache holds
+        # each list it keys, so an id() cannot be reused within the call.
+        converted = {}
+
+        def once(obj, convert):
+            hit = converted.get(id(obj))
+            if hit is None or hit[0] is not obj:
+                hit = converted[id(obj)] = (obj, convert(obj))
+            return hit[1]
+
         for layer_name, block_ids, block_hashes in saves:
-            req.saves.add(layer_name=layer_name, block_ids=list(block_ids),
-                          block_hashes=[bytes(h) for h in block_hashes])
+            req.saves.add(layer_name=layer_name,
+                          block_ids=once(block_ids, lambda v: [int(i) for i in v]),
+                          block_hashes=once(block_hashes, lambda v: [bytes(h) for h in v]))
         return self._status("save", self._call("Save", "save", req))
 
     def load(self, instance_id: str, tp_rank: int, device_id: int, load_state_shm: str,

@@ -88,7 +88,17 @@ class EngineService:
         return proto.RegisterContextResponse(status=_ok())
 
     def Save(self, req, context):
-        saves = [(s.layer_name, list(s.block_ids), list(s.block_hashes)) for s in req.saves]
+        # Layers of one save usually carry the same ids and hashes: consecutive
+        # equal lists become one list object, which the engine packs and looks
+        # up once.
+        saves, prev = [], None
+        for s in req.saves:
+            if prev is not None and s.block_ids == prev[0] and s.block_hashes == prev[1]:
+                ids, hashes = prev[2], prev[3]
+            else:
+                ids, hashes = list(s.block_ids), list(s.block_hashes)
+                prev = (s.block_ids, s.block_hashes, ids, hashes)
+            saves.append((s.layer_name, ids, hashes))
         try:
             self.frontend.save(req.instance_id, req.tp_rank, req.device_id, saves)
         except Exception as e:

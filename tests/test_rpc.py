@@ -230,3 +230,27 @@ def test_server_speaks_to_a_raw_channel(served):
                           response_deserializer=lambda b: b)
     assert call(b"", timeout=5) == bytes.fromhex("0a020801")  # status{ok=true}
     ch.close()
+
+
+def test_save_request_from_shared_and_generated_lists():
+    """EngineRpcClient.save converts a list shared by several layers once, and
+    a generator of fresh per-layer lists (whose ids Python may reuse) still
+    yields every layer's own values."""
+    from pegaflow_amd.rpc import proto
+    from pegaflow_amd.rpc.client import EngineRpcClient
+
+    c = EngineRpcClient.__new__(EngineRpcClient)
+    sent = []
+    ok = proto.SaveResponse()
+    ok.status.ok = True
+    c._call = lambda rpc, method, req: sent.append(req) or ok
+    ids, hs = [4, 5, 6], [bytes([i]) * 32 for i in range(3)]
+    assert c.save("inst", 0, 0, [("a", ids, hs), ("b", ids, hs)]) == (True, "")
+    gen = ((f"l{i}", [i, i + 1], [bytes([i]) * 32, bytes([i + 1]) * 32]) for i in range(6))
+    assert c.save("inst", 0, 0, gen) == (True, "")
+    first, second = sent
+    assert [list(s.block_ids) for s in first.saves] == [ids, ids]
+    assert [list(s.block_hashes) for s in first.saves] == [hs, hs]
+    assert [list(s.block_ids) for s in second.saves] == [[i, i + 1] for i in range(6)]
+    assert [list(s.block_hashes) for s in second.saves] == \
+        [[bytes([i]) * 32, bytes([i + 1]) * 32] for i in range(6)]
