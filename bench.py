@@ -539,9 +539,33 @@ def leg_engine(layers, ids, targets, P, reps=4):
             bad += st.get_state() != 1
         bad += wl.verify_restored(layers, ids, targets)
         layers.refill()
+    # Small restores (the first 1 and 16 blocks of the prefix, all 32
+    # layers): latency from the call to the LoadState reading ready.
+    # The same through the reference's copy pattern (one async copy per
+    # merged run) for comparison.
+    from pegaflow_amd import _lib
+
+    small = {}
+    for mode, n in (("kernel", 1), ("kernel", 16), ("dma_reference", 1), ("dma_reference", 16)):
+        e.set_transfer_modes(_lib.MODE_KERNEL, _lib.MODE_NAMES[mode])
+        lat = []
+        for r in range(21):
+            st = PyLoadState()
+            t0 = time.perf_counter()
+            e.batch_load_kv_blocks("bench", 0, 0, st.shm_name(), names, targets_l[:n], hashes[:n])
+            while not st.is_ready():
+                if time.perf_counter() - t0 > 10:
+                    raise RuntimeError("small engine restore did not complete within 10 s")
+            lat.append(time.perf_counter() - t0)
+            bad += st.get_state() != 1
+        small[f"{mode}_{n}_blocks_us"] = round(statistics.median(lat[1:]) * 1e6, 1)
+    e.set_transfer_modes(_lib.MODE_KERNEL, _lib.MODE_KERNEL)
+    bad += wl.verify_restored(layers, ids[:16], targets[:16])
+    layers.refill()
     stats = e.stats()
     e.close()
     return {
+        "small_restore_latency": small,
         "what": "the llama prefix through PegaEngine: save by hash (new hashes each time), load "
                 "by hash with a plain LoadState (as the reference's connector) and with a "
                 "layered one (per-layer completion), median of the warm calls",
