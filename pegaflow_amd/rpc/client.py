@@ -15,6 +15,48 @@ _STATE_NAMES = {proto.PREFETCH_READY: "ready", proto.PREFETCH_LOADING: "loading"
                 proto.PREFETCH_PARTIAL_MISS: "partial_miss"}
 
 
+def _varint(n: int) -> bytes:
+    out = bytearray()
+    while True:
+        b, n = n & 0x7F, n >> 7
+        if not n:
+            out.append(b)
+            return bytes(out)
+        out.append(b | 0x80)
+
+
+_SAVES_TAG = _varint((proto.SaveRequest.DESCRIPTOR.fields_by_name["saves"].number << 3) | 2)
+
+
+def encode_save_request(instance_id: str, tp_rank: int, device_id: int, saves) -> bytes:
+    """SaveRequest wire bytes for [(layer_name, block_ids, block_hashes)].
+
+    The layers of a save usually share one id list and one hash list.  Each
+    distinct pair is serialized once and every layer's SaveLayer is its name
+    field followed by those bytes (two serialized parts of one message
+    concatenate into the message with both), so the request costs one
+    encoding of the lists instead of one per layer.  The cache holds each
+    list it keys, so an id() cannot be reused within the call."""
+    parts = [proto.SaveRequest(instance_id=instance_id, tp_rank=tp_rank,
+                               device_id=device_id).SerializeToString()]
+    bodies = {}
+    for layer_name, block_ids, block_hashes in saves:
+        key = (id(block_ids), id(block_hashes))
+        hit = bodies.get(key)
+        if hit is None or hit[0] is not block_ids or hit[1] is not block_hashes:
+            body = proto.SaveLayer(block_ids=[int(i) for i in block_ids],
+                                   block_hashes=[bytes(h) for h in block_hashes])
+            hit = bodies[key] = (block_ids, block_hashes, body.SerializeToString())
+        layer = proto.SaveLayer(layer_name=layer_name).SerializeToString() + hit[2]
+        parts += [_SAVES_TAG, _varint(len(layer)), layer]
+    return b"".join(parts)
+
+
+def _serialize(request) -> bytes:
+    """Requests are messages, or wire bytes already encoded."""
+    return request if isinstance(request, bytes) else request.SerializeToString()
+
+
 def _target(endpoint: str) -> str:
     for scheme in ("http://", "https://"):
         if endpoint.startswith(scheme):
@@ -44,7 +86,7 @@ class EngineRpcClient:
                                f"no answer within {connect_timeout_s} s") from None
         self._stubs = {
             rpc: self._channel.unary_unary(proto.method_path(rpc),
-                                           request_serializer=proto.messages[req].SerializeToString,
+                                           request_serializer=_serialize,
                                            response_deserializer=proto.messages[resp].FromString)
             for rpc, req, resp in proto.METHODS}
 
@@ -92,21 +134,7 @@ class EngineRpcClient:
 
     def save(self, instance_id: str, tp_rank: int, device_id: int, saves):
         """python/src/lib.rs:374-405: `saves` is [(layer_name, block_ids, block_hashes)]."""
-        req = proto.SaveRequest(instance_id=instance_id, tp_rank=tp_rank, device_id=device_id)
-        # Lists shared by several layers are converted once.  The cache holds
-        # each list it keys, so an id() cannot be reused within the call.
-        converted = {}
-
-        def once(obj, convert):
-            hit = converted.get(id(obj))
-            if hit is None or hit[0] is not obj:
-                hit = converted[id(obj)] = (obj, convert(obj))
-            return hit[1]
-
-        for layer_name, block_ids, block_hashes in saves:
-            req.saves.add(layer_name=layer_name,
-                          block_ids=once(block_ids, lambda v: [int(i) for i in v]),
-                          block_hashes=once(block_hashes, lambda v: [bytes(h) for h in v]))
+        req = encode_save_request(instance_id, tp_rank, device_id, saves)
         return self._status("save", self._call("Save", "save", req))
 
     def load(self, instance_id: str, tp_rank: int, device_id: int, load_state_shm: str,

@@ -90,14 +90,22 @@ class EngineService:
     def Save(self, req, context):
         # Layers of one save usually carry the same ids and hashes: consecutive
         # equal lists become one list object, which the engine packs and looks
-        # up once.
+        # up once.  Equality is judged on the wire bytes: a layer equals the
+        # previous one when its encoding is its name field followed by the
+        # previous layer's list bytes (fields are encoded in field order).
+        # Equal bytes imply equal lists; an encoding that differs only falls
+        # back to converting that layer's lists.
         saves, prev = [], None
         for s in req.saves:
-            if prev is not None and s.block_ids == prev[0] and s.block_hashes == prev[1]:
-                ids, hashes = prev[2], prev[3]
+            blob = s.SerializeToString()
+            name = proto.SaveLayer(layer_name=s.layer_name).SerializeToString()
+            if (prev is not None and blob.startswith(name)
+                    and memoryview(blob)[len(name):] == prev[0]):
+                ids, hashes = prev[1], prev[2]
             else:
                 ids, hashes = list(s.block_ids), list(s.block_hashes)
-                prev = (s.block_ids, s.block_hashes, ids, hashes)
+                body = blob[len(name):] if blob.startswith(name) else None
+                prev = (body, ids, hashes) if body is not None else None
             saves.append((s.layer_name, ids, hashes))
         try:
             self.frontend.save(req.instance_id, req.tp_rank, req.device_id, saves)

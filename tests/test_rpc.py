@@ -248,9 +248,45 @@ def test_save_request_from_shared_and_generated_lists():
     assert c.save("inst", 0, 0, [("a", ids, hs), ("b", ids, hs)]) == (True, "")
     gen = ((f"l{i}", [i, i + 1], [bytes([i]) * 32, bytes([i + 1]) * 32]) for i in range(6))
     assert c.save("inst", 0, 0, gen) == (True, "")
-    first, second = sent
+    first, second = (proto.SaveRequest.FromString(r) for r in sent)
+    assert first.instance_id == "inst" and [s.layer_name for s in first.saves] == ["a", "b"]
     assert [list(s.block_ids) for s in first.saves] == [ids, ids]
     assert [list(s.block_hashes) for s in first.saves] == [hs, hs]
     assert [list(s.block_ids) for s in second.saves] == [[i, i + 1] for i in range(6)]
     assert [list(s.block_hashes) for s in second.saves] == \
         [[bytes([i]) * 32, bytes([i + 1]) * 32] for i in range(6)]
+
+
+def test_save_request_encoding_matches_the_message():
+    """The client's pre-encoded SaveRequest is byte-identical to the message
+    built field by field, for shared, distinct and empty lists; the service
+    hands equal consecutive lists to the engine as one object."""
+    from pegaflow_amd.rpc import proto
+    from pegaflow_amd.rpc.client import encode_save_request
+    from pegaflow_amd.rpc.server import EngineService
+
+    ids, hs = [7, -1, 300000], [bytes([i]) * 32 for i in range(3)]
+    other = [1, 2, 3]
+    saves = [("a", ids, hs), ("", ids, hs), ("c" * 200, other, hs), ("d", ids, hs),
+             ("e", [], [])]
+    ref = proto.SaveRequest(instance_id="inst", tp_rank=2, device_id=1)
+    for n, i, h in saves:
+        ref.saves.add(layer_name=n, block_ids=i, block_hashes=h)
+    wire = encode_save_request("inst", 2, 1, saves)
+    assert wire == ref.SerializeToString()
+    assert proto.SaveRequest.FromString(wire) == ref
+
+    got = {}
+
+    class Frontend:
+        def save(self, *a):
+            got["saves"] = a[3]
+
+    svc = EngineService.__new__(EngineService)
+    svc.frontend = Frontend()
+    svc.Save(proto.SaveRequest.FromString(wire), None)
+    out = got["saves"]
+    assert [(n, list(i), list(h)) for n, i, h in out] == [(n, i, h) for n, i, h in saves]
+    assert out[1][1] is out[0][1] and out[1][2] is out[0][2]   # "" after "a": shared
+    assert out[2][1] is not out[1][1]                           # other ids
+    assert out[3][1] is not out[2][1]                           # changes back
