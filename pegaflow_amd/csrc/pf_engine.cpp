@@ -275,17 +275,51 @@ int BlockStore::insert_slots(const std::vector<std::string>& keys,
     for (const auto& layer : entries)
       for (const auto& e : layer) sealed_already[e.first] = cache_.count(keys[e.first]) != 0;
   }
+  // The usual save brings every slot of its blocks in one call (all layers
+  // of a single-rank instance), each layer naming the same keys.  Such a
+  // block seals here directly, without passing through the inflight map,
+  // unless an earlier call left part of it there.
+  bool whole = total_slots > 0 && entries.size() == total_slots;
+  if (whole) {
+    std::vector<char> seen(total_slots, 0);
+    for (size_t sl : slots) {
+      if (sl >= total_slots || seen[sl]) {
+        whole = false;
+        break;
+      }
+      seen[sl] = 1;
+    }
+  }
+  for (size_t j = 1; whole && j < entries.size(); ++j) {
+    whole = entries[j].size() == entries[0].size();
+    for (size_t k = 0; whole && k < entries[j].size(); ++k)
+      whole = entries[j][k].first == entries[0][k].first;
+  }
   std::vector<std::pair<uint32_t, std::shared_ptr<SealedBlock>>> sealed;
   int err = PF_OK;
   {
     std::lock_guard<std::mutex> lk(inflight_mu_);
+    if (whole) {
+      for (size_t k = 0; k < entries[0].size(); ++k) {
+        const uint32_t i = entries[0][k].first;
+        if (sealed_already[i] || inflight_.count(keys[i])) continue;  // general path below
+        auto sb = std::make_shared<SealedBlock>();
+        sb->slots.resize(total_slots);
+        for (size_t j = 0; j < entries.size(); ++j) {
+          sb->footprint += entries[j][k].second->size;
+          sb->slots[slots[j]] = std::move(entries[j][k].second);  // leaves it empty
+        }
+        sealed.emplace_back(i, std::move(sb));
+      }
+    }
+    const size_t n_direct = sealed.size();  // never entered the inflight map
     std::vector<InflightBlock*> ib(n, nullptr);  // node pointers survive inserts
     int rc = PF_OK;
     for (size_t j = 0; j < entries.size() && rc == PF_OK; ++j) {
       const size_t slot = slots[j];
       for (auto& e : entries[j]) {
         const uint32_t i = e.first;
-        if (sealed_already[i]) continue;
+        if (sealed_already[i] || !e.second) continue;  // sealed above, or nothing
         if (!ib[i]) {
           auto it = inflight_.find(keys[i]);
           if (it == inflight_.end()) {
@@ -319,7 +353,7 @@ int BlockStore::insert_slots(const std::vector<std::string>& keys,
         }
       }
     }
-    for (const auto& s : sealed) inflight_.erase(keys[s.first]);
+    for (size_t k = n_direct; k < sealed.size(); ++k) inflight_.erase(keys[sealed[k].first]);
     if (rc != PF_OK && sealed.empty()) return rc;
     if (rc != PF_OK) err = rc;  // blocks completed before the error still seal
   }

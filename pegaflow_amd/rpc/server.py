@@ -88,27 +88,13 @@ class EngineService:
         return proto.RegisterContextResponse(status=_ok())
 
     def Save(self, req, context):
-        # Layers of one save usually carry the same ids and hashes: consecutive
-        # equal lists become one list object, which the engine packs and looks
-        # up once.  Equality is judged on the wire bytes: a layer equals the
-        # previous one when its encoding is its name field followed by the
-        # previous layer's list bytes (fields are encoded in field order).
-        # Equal bytes imply equal lists; an encoding that differs only falls
-        # back to converting that layer's lists.
-        saves, prev = [], None
-        for s in req.saves:
-            blob = s.SerializeToString()
-            name = proto.SaveLayer(layer_name=s.layer_name).SerializeToString()
-            if (prev is not None and blob.startswith(name)
-                    and memoryview(blob)[len(name):] == prev[0]):
-                ids, hashes = prev[1], prev[2]
-            else:
-                ids, hashes = list(s.block_ids), list(s.block_hashes)
-                body = blob[len(name):] if blob.startswith(name) else None
-                prev = (body, ids, hashes) if body is not None else None
-            saves.append((s.layer_name, ids, hashes))
+        # The request arrives decoded by proto.decode_save_request: layers
+        # that carry the same ids and hashes share one list object, which
+        # the engine packs and looks up once.
+        if not isinstance(req, proto.DecodedSave):
+            req = proto.decoded_save(req)
         try:
-            self.frontend.save(req.instance_id, req.tp_rank, req.device_id, saves)
+            self.frontend.save(req.instance_id, req.tp_rank, req.device_id, req.saves)
         except Exception as e:
             self._abort(context, e)
         return proto.SaveResponse(status=_ok())
@@ -152,7 +138,8 @@ class EngineService:
         for rpc, req, resp in proto.METHODS:
             methods[rpc] = grpc.unary_unary_rpc_method_handler(
                 getattr(self, rpc),
-                request_deserializer=proto.messages[req].FromString,
+                request_deserializer=(proto.decode_save_request if rpc == "Save"
+                                      else proto.messages[req].FromString),
                 response_serializer=proto.messages[resp].SerializeToString)
         return grpc.method_handlers_generic_handler(f"{proto.PACKAGE}.{proto.SERVICE}", methods)
 

@@ -284,9 +284,62 @@ def test_save_request_encoding_matches_the_message():
 
     svc = EngineService.__new__(EngineService)
     svc.frontend = Frontend()
-    svc.Save(proto.SaveRequest.FromString(wire), None)
-    out = got["saves"]
-    assert [(n, list(i), list(h)) for n, i, h in out] == [(n, i, h) for n, i, h in saves]
-    assert out[1][1] is out[0][1] and out[1][2] is out[0][2]   # "" after "a": shared
-    assert out[2][1] is not out[1][1]                           # other ids
-    assert out[3][1] is not out[2][1]                           # changes back
+    for req in (proto.decode_save_request(wire), proto.SaveRequest.FromString(wire)):
+        svc.Save(req, None)
+        out = got["saves"]
+        assert [(n, list(i), list(h)) for n, i, h in out] == [(n, i, h) for n, i, h in saves]
+        assert out[1][1] is out[0][1] and out[1][2] is out[0][2]   # "" after "a": shared
+        assert out[2][1] is not out[1][1]                           # other ids
+        assert out[3][1] is not out[2][1]                           # changes back
+
+
+def _ld(field, payload):
+    """One length-delimited record."""
+    from pegaflow_amd.rpc.client import _varint
+    return _varint(field << 3 | 2) + _varint(len(payload)) + payload
+
+
+def test_save_request_decoder_matches_the_full_parse():
+    """decode_save_request gives what the full parse gives, for the
+    canonical encoding and for encodings it does not take apart itself
+    (unpacked ids, the name after the lists, a second name record, unknown
+    fields, negative ids); malformed bytes fail as the full parse does."""
+    from google.protobuf.message import DecodeError
+
+    from pegaflow_amd.rpc import proto
+    from pegaflow_amd.rpc.client import _varint, encode_save_request
+
+    def expect(wire):
+        m = proto.SaveRequest.FromString(wire)
+        d = proto.decode_save_request(wire)
+        assert (d.instance_id, d.tp_rank, d.device_id) == (m.instance_id, m.tp_rank, m.device_id)
+        assert [(n, list(i), list(h)) for n, i, h in d.saves] == \
+            [(s.layer_name, list(s.block_ids), list(s.block_hashes)) for s in m.saves]
+        return d
+
+    hs = [b"x" * 32, b"y" * 32]
+    canon = encode_save_request("i", 1, 2, [("a", [3, -4], hs), ("b", [3, -4], hs)])
+    d = expect(canon)
+    assert d.saves[0][1] is d.saves[1][1]
+    assert proto._decode_save_fast(canon) == d  # taken apart without the full parse
+    head = proto.SaveRequest(instance_id="i", tp_rank=1, device_id=2).SerializeToString()
+    lists = proto.SaveLayer(block_ids=[3, -4], block_hashes=hs).SerializeToString()
+    unpacked = b"".join(_varint(2 << 3) + _varint(v & (2**64 - 1)) for v in (3, -4))
+    hashes = b"".join(_ld(3, h) for h in hs)
+    variants = [
+        head + _ld(4, _ld(1, b"a") + unpacked + hashes),           # ids not packed
+        head + _ld(4, lists + _ld(1, b"a")),                         # name after the lists
+        head + _ld(4, _ld(1, b"a") + lists + _ld(1, b"z")),          # second name wins
+        head + _ld(4, _ld(1, b"a") + lists + _ld(1, b"")),           # ... also when empty
+        head + _ld(4, _ld(1, b"a") + lists) + _varint(9 << 3) + _varint(7),  # unknown field
+        _ld(4, _ld(1, b"a") + lists) + head,                         # header last
+        head + _ld(4, b""),                                          # an empty layer
+    ]
+    for w in variants:
+        expect(w)
+    assert proto.decode_save_request(variants[3]).saves[0][0] == ""
+    for bad in (canon[:-3], head + _ld(4, _ld(1, b"\xff\xfe") + lists), b"\x22\xff"):
+        with pytest.raises(DecodeError):
+            proto.SaveRequest.FromString(bad)
+        with pytest.raises(DecodeError):
+            proto.decode_save_request(bad)
