@@ -269,11 +269,15 @@ int BlockStore::insert_slots(const std::vector<std::string>& keys,
                              const std::vector<size_t>& slots, std::vector<SlotEntries>& entries,
                              size_t total_slots) {
   const size_t n = keys.size();
-  std::vector<char> sealed_already(n, 0);
+  // Keys sealed before this call (each key looked up once, not once per
+  // layer that carries it).
+  std::vector<char> sealed_already(n, 0), named(n, 0);
+  for (const auto& layer : entries)
+    for (const auto& e : layer) named[e.first] = 1;
   {
     std::lock_guard<std::mutex> lk(cache_mu_);
-    for (const auto& layer : entries)
-      for (const auto& e : layer) sealed_already[e.first] = cache_.count(keys[e.first]) != 0;
+    for (size_t i = 0; i < n; ++i)
+      if (named[i]) sealed_already[i] = cache_.count(keys[i]) != 0;
   }
   // The usual save brings every slot of its blocks in one call (all layers
   // of a single-rank instance), each layer naming the same keys.  Such a
