@@ -29,12 +29,21 @@ class RegisterTensorError(RuntimeError):
     service.rs:90-93)."""
 
 
+class _Refused(Exception):
+    """The engine refused a registration (carries the engine's error)."""
+
+    def __init__(self, cause: BaseException):
+        super().__init__(str(cause))
+        self.cause = cause
+
+
 class TensorRegistry:
     """Registered layer tensors per context key "instance:tpR:devD"
     (registry.rs:41-176)."""
 
     def __init__(self):
         self._lock = threading.Lock()
+        self._reg_lock = threading.Lock()  # one registration at a time
         self._contexts: dict[str, tuple[int, dict[str, OpenedTensor]]] = {}
 
     @staticmethod
@@ -42,18 +51,43 @@ class TensorRegistry:
         return f"{instance_id}:tp{tp_rank}:dev{device_id}"
 
     def register_layer(self, key: str, layer_name: str, device_id: int,
-                       wrapper_bytes: bytes) -> OpenedTensor:
-        t = open_tensor(wrapper_bytes)
-        with self._lock:
-            dev, tensors = self._contexts.setdefault(key, (t.device_id, {}))
-            if dev != t.device_id:
+                       wrapper_bytes: bytes, commit=None, drain=None) -> OpenedTensor:
+        """Opens the handle and makes it the layer's tensor.
+
+        ``commit(t)`` (the engine's registration of the new address) runs
+        before the registry changes: if it raises, the new handle is closed,
+        the old one stays, and the error comes back as ``_Refused``.  A
+        replaced handle is closed only after ``drain()``, so transfers queued
+        on the old mapping finish before it is unmapped."""
+        with self._reg_lock:
+            t = open_tensor(wrapper_bytes)
+            try:
+                with self._lock:
+                    dev = self._contexts.get(key, (t.device_id, None))[0]
+                if dev != t.device_id:
+                    raise ValueError(f"context {key} is pinned to device {dev} but got "
+                                     f"{t.device_id}")
+                if commit is not None:
+                    try:
+                        commit(t)
+                    except Exception as e:
+                        raise _Refused(e) from None
+            except BaseException:
                 t.close()
-                raise ValueError(f"context {key} is pinned to device {dev} but got {t.device_id}")
-            old = tensors.pop(layer_name, None)
-            tensors[layer_name] = t
-        if old is not None:
-            old.close()
-        return t
+                raise
+            with self._lock:
+                _, tensors = self._contexts.setdefault(key, (t.device_id, {}))
+                old = tensors.pop(layer_name, None)
+                tensors[layer_name] = t
+            if old is not None:
+                if drain is not None:
+                    drain()
+                old.close()
+            return t
+
+    def tensor(self, key: str, layer_name: str) -> OpenedTensor | None:
+        with self._lock:
+            return self._contexts.get(key, (None, {}))[1].get(layer_name)
 
     def drop_instance(self, instance_id: str) -> int:
         prefix = f"{instance_id}:"
@@ -90,16 +124,24 @@ class EngineFrontend:
                          device_id: int, num_layers: int, layer_name: str, wrapper_bytes: bytes,
                          num_blocks: int, bytes_per_block: int, kv_stride_bytes: int,
                          segments: int) -> None:
-        """service.rs:140-186."""
+        """service.rs:140-186.  A layer registered again gets the new
+        mapping in the engine before the old mapping is closed, and the old one
+        is closed only once the engine's queued loads have drained; a
+        registration the engine refuses leaves the old mapping in place."""
+        def commit(t):
+            self.engine.register_context_layer(instance_id, namespace, t.device_id, layer_name,
+                                               t.data_ptr, t.size_bytes, num_blocks,
+                                               bytes_per_block, kv_stride_bytes, segments,
+                                               tp_rank, tp_size, num_layers)
+
         try:
-            t = self.registry.register_layer(
+            self.registry.register_layer(
                 TensorRegistry.context_key(instance_id, tp_rank, device_id), layer_name,
-                device_id, bytes(wrapper_bytes))
+                device_id, bytes(wrapper_bytes), commit=commit, drain=self.engine.wait_idle)
+        except _Refused as e:
+            raise e.cause from None
         except Exception as e:
             raise RegisterTensorError(f"register tensor failed: {e}") from None
-        self.engine.register_context_layer(instance_id, namespace, t.device_id, layer_name,
-                                           t.data_ptr, t.size_bytes, num_blocks, bytes_per_block,
-                                           kv_stride_bytes, segments, tp_rank, tp_size, num_layers)
 
     def save(self, instance_id: str, tp_rank: int, device_id: int, saves) -> None:
         self.engine.batch_save_kv_blocks(instance_id, tp_rank, device_id, saves)

@@ -12,7 +12,7 @@ repeated int32; two's-complement 10-byte varints for negative int32).
 import grpc
 import pytest
 
-from pegaflow_amd import ipc
+from pegaflow_amd import _lib, ipc
 from pegaflow_amd.engine import PegaEngine
 from pegaflow_amd.load_state import PyLoadState
 from pegaflow_amd.rpc import proto
@@ -142,6 +142,50 @@ def test_registry_keys_and_drop():
     assert r.drop_instance("inst") == 2
     assert r.drop_instance("inst") == 0
     assert r.drop_instance("inst2") == 1
+
+
+def test_reregistration_keeps_the_mapping_the_engine_uses(monkeypatch):
+    """A layer registered again: the engine gets the new address first, the
+    old mapping is closed only after the engine's queued loads drained, and a
+    registration the engine refuses closes the new mapping and keeps the
+    old one (the engine still points there)."""
+    from pegaflow_amd import frontend as fe
+
+    events = []
+
+    class Mapping:
+        def __init__(self, addr):
+            self.data_ptr, self.size_bytes, self.device_id = addr, 64, 0
+
+        def close(self):
+            events.append(("close", self.data_ptr))
+
+    monkeypatch.setattr(fe, "open_tensor", lambda raw: Mapping(int(raw)))
+
+    class Engine:
+        refuse = False
+
+        def register_context_layer(self, inst, ns, dev, name, ptr, *rest):
+            if self.refuse:
+                raise _lib.PegaFlowError(_lib.PF_ERR_TOPOLOGY_MISMATCH, "topology mismatch")
+            events.append(("engine", ptr))
+
+        def wait_idle(self):
+            events.append(("drain",))
+
+    eng = Engine()
+    f = fe.EngineFrontend(eng)
+    args = ("inst", "ns", 0, 1, 0, 2, "l0")
+    f.register_context(*args, b"4096", 16, 512, 8192, 2)
+    f.register_context(*args, b"8192", 16, 512, 8192, 2)
+    assert events == [("engine", 4096), ("engine", 8192), ("drain",), ("close", 4096)]
+    events.clear()
+    eng.refuse = True
+    with pytest.raises(_lib.PegaFlowError, match="topology mismatch"):
+        f.register_context(*args, b"12288", 16, 512, 8192, 2)
+    assert events == [("close", 12288)]
+    key = TensorRegistry.context_key("inst", 0, 0)
+    assert f.registry.tensor(key, "l0").data_ptr == 8192
 
 
 # ---------------------------------------------------------------------------
