@@ -371,10 +371,12 @@ int ensure_desc_capacity(pf_xfer* x, size_t n) {
   return PF_OK;
 }
 
-int upload_desc(pf_xfer* x, size_t n) {
-  x->desc_base = x->d_desc;
+// Copies descriptors [off, off + n) of the host staging to the same place in
+// device memory; the next launches read from there.
+int upload_desc(pf_xfer* x, size_t n, size_t off = 0) {
+  x->desc_base = x->d_desc + off;
   if (n == 0) return PF_OK;
-  PF_HIP(hipMemcpyAsync(x->d_desc, x->h_desc, n * sizeof(ChunkDesc),
+  PF_HIP(hipMemcpyAsync(x->d_desc + off, x->h_desc + off, n * sizeof(ChunkDesc),
                         hipMemcpyHostToDevice, x->stream));
   PF_HIP(hipEventRecord(x->desc_uploaded, x->stream));
   x->desc_inflight = true;
@@ -713,9 +715,12 @@ struct Step {
   uint32_t groups = 0; // marked launch: non-empty layers in it
 };
 
+// desc_off > 0: a later part of one pipelined call.  Its descriptors go
+// after the earlier parts' (whose copies may still read theirs), in room
+// the caller has reserved, and never in place.
 int kernel_direct(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<LayerPlan>& plans,
                   bool is_save, pf_event* layer_events, const SignalTargets* sig,
-                  bool wait_save) {
+                  bool wait_save, size_t desc_off = 0) {
   if (int rc = check_all_kernel(layers, plans, true)) return rc;
   size_t total = 0;
   std::vector<size_t> first(plans.size());
@@ -771,8 +776,12 @@ int kernel_direct(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<Lay
                           sizeof(ChunkDesc);
   // Counters for marks and the tile queue of queued launches.
   if (int rc = ensure_counters(x, plans.size())) return rc;
-  ChunkDesc* hd = small_desc(x, total + aux_desc);
-  if (!hd) {
+  ChunkDesc* hd = desc_off ? nullptr : small_desc(x, total + aux_desc);
+  if (desc_off) {
+    if (desc_off + total + aux_desc > x->h_cap || desc_off + total + aux_desc > x->d_cap)
+      return fail(PF_ERR_INVALID_ARGUMENT, "descriptor room not reserved");
+    hd = x->h_desc + desc_off;
+  } else if (!hd) {
     if (int rc = ensure_desc_capacity(x, total + aux_desc)) return rc;
     hd = x->h_desc;
   }
@@ -788,7 +797,7 @@ int kernel_direct(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<Lay
     // the stream to drain.
     x->desc_base = x->h_small;
     x->small_inflight = true;
-  } else if (int rc = upload_desc(x, total + aux_desc)) {
+  } else if (int rc = upload_desc(x, total + aux_desc, desc_off)) {
     return rc;
   }
   const uint32_t* d_aux = reinterpret_cast<const uint32_t*>(x->desc_base + total);
@@ -835,6 +844,51 @@ int kernel_direct(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<Lay
   return PF_OK;
 }
 
+// Layers in the first part of a pipelined call, or 0 for a call issued
+// whole: calls of at least 8 layers and kPipelineMinChunks chunks (of the
+// order of the chunk counts whose planning takes ~0.1 ms) start with an
+// eighth of their layers.
+constexpr uint64_t kPipelineMinChunks = 16384;
+
+uint32_t pipeline_head(const pf_layer_xfer* layers, uint32_t num_layers) {
+  if (num_layers < 8) return 0;
+  uint64_t chunks = 0;
+  for (uint32_t i = 0; i < num_layers; ++i)
+    chunks += layers[i].num_blocks * (layers[i].layout.segments ? layers[i].layout.segments : 1);
+  return chunks >= kPipelineMinChunks ? num_layers / 8 : 0;
+}
+
+int kernel_pipelined(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
+                     uint32_t head, bool is_save, bool wait_save) {
+  std::vector<LayerPlan> first, rest;
+  if (int rc = plan_all(layers, head, is_save, &first)) return rc;
+  for (uint32_t li = 0; li < head; ++li)
+    apply_write_policy(layers[li], is_save, false, &first[li]);
+  // Room for every descriptor of the call, reserved before the first part
+  // is uploaded: growing the buffers later would wait for the first copy.
+  uint64_t bound = 1;
+  for (uint32_t i = 0; i < num_layers; ++i)
+    bound += layers[i].num_blocks * (layers[i].layout.segments ? layers[i].layout.segments : 1);
+  if (int rc = ensure_desc_capacity(x, static_cast<size_t>(bound))) return rc;
+  size_t n_first = 0;
+  for (const LayerPlan& p : first)
+    if (!p.ordered) n_first += p.chunks.size();
+  if (int rc = kernel_direct(x, layers, first, is_save, nullptr, nullptr, false)) return rc;
+  int rc = plan_all(layers + head, num_layers - head, is_save, &rest);
+  if (rc == PF_OK) {
+    for (uint32_t li = head; li < num_layers; ++li)
+      apply_write_policy(layers[li], is_save, false, &rest[li - head]);
+    // The first part may have read its descriptors in place (h_small); the
+    // second always uploads, after the first part's.
+    rc = kernel_direct(x, layers + head, rest, is_save, nullptr, nullptr, wait_save,
+                       n_first > 0 ? n_first : 1);
+  }
+  // On an error nothing of the call is left in flight: the caller may free
+  // or reuse the host side at once.
+  if (rc != PF_OK) (void)hipStreamSynchronize(x->stream);
+  return rc;
+}
+
 int run(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, uint32_t mode,
         bool is_save, pf_event* layer_events, bool wait_save = true,
         const SignalTargets* sig = nullptr) {
@@ -845,6 +899,13 @@ int run(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, uint32_t m
   x->last_dma = 0;
   PF_HIP(hipSetDevice(x->device));
   std::vector<LayerPlan> plans;
+  if (mode == PF_MODE_KERNEL && !layer_events && !sig) {
+    // A large call: its first layers are planned and launched before the
+    // rest are planned, so the planning of the rest (about 3 ns a chunk)
+    // overlaps their copy.
+    const uint32_t head = pipeline_head(layers, num_layers);
+    if (head > 0) return kernel_pipelined(x, layers, num_layers, head, is_save, wait_save);
+  }
   if (int rc = plan_all(layers, num_layers, is_save, &plans)) return rc;
   switch (mode) {
     case PF_MODE_DMA_REFERENCE:

@@ -263,6 +263,65 @@ def test_edge_cases_vs_oracle(ctx, mode):
     _oracle_roundtrip_case(ctx, m, 10, 64, 2, 32, 9 * 64 + 32 + 64, [2, 5], [3, 4])
 
 
+def test_pipelined_multi_layer_calls_vs_oracle(ctx):
+    """Calls of at least 8 layers and 16384 chunks are issued in two parts
+    (the first layers launched before the rest are planned).  16 layers of
+    1024 blocks, one with overlapping K/V regions (copied in list order),
+    loads naming blocks more than once (the later copy wins): every byte
+    against the oracle.  A planning error in the second part fails the call
+    with the reference's message and leaves nothing in flight."""
+    say("[gpu] pipelined multi-layer calls vs oracle")
+    L, nb, bpb, m = 16, 1100, 256, 1024
+    rng = np.random.Generator(np.random.PCG64(11))
+    host = PinnedBuffer(L * 2 * m * bpb)
+    ohost = np.zeros(L * 2 * m * bpb, np.uint8)
+    devs, refs, regs, oregs, saves, loads, osaves = [], [], [], [], [], [], []
+    for l in range(L):
+        kv = nb * bpb // 2 if l == 5 else nb * bpb
+        size = kv + nb * bpb
+        dev = DeviceBuffer(size)
+        dev.fill_random(100 + l)
+        ref = dev.download()
+        reg = KVCacheRegistration.create(dev.ptr, size, nb, bpb, kv, 2)
+        oreg = oracle.layout(ref.ctypes.data, size, nb, bpb, kv, 2)
+        save_ids = rng.choice(nb, m, replace=False).tolist()
+        load_ids = rng.choice(nb, m, replace=True).tolist()
+        base, obase = host.ptr + l * 2 * m * bpb, ohost.ctypes.data + l * 2 * m * bpb
+        k, v, split = oracle.save_host_layout(oreg, m, base, base + m * bpb)
+        ok_, ov, _ = oracle.save_host_layout(oreg, m, obase, obase + m * bpb)
+        saves.append(LayerTransfer(reg, block_array(save_ids, k, v if split else None)))
+        loads.append(LayerTransfer(reg, block_array(load_ids, k, v if split else None)))
+        osaves.append((oreg, ref, save_ids, load_ids, ok_, ov if split else None))
+        devs.append(dev)
+    host.array[:] = 0
+    ctx.save_layers(saves, _lib.MODE_KERNEL)
+    for oreg, ref, save_ids, _, ok_, ov in osaves:
+        oracle.process_save(oreg, ref, save_ids, ok_, ov)
+    assert np.array_equal(host.array, ohost)
+    ctx.load_layers(loads, _lib.MODE_KERNEL)
+    ctx.synchronize()
+    for dev, (oreg, ref, _, load_ids, ok_, ov) in zip(devs, osaves):
+        oracle.process_load(oreg, ref, load_ids, ok_, ov)
+        assert np.array_equal(dev.download(), ref)
+    # An out-of-range block in the last layer: found after the first part
+    # was launched.
+    bad = list(loads)
+    b = bad[-1].blocks.copy()
+    b["block_idx"][7] = nb
+    bad[-1] = LayerTransfer(bad[-1].registration, b)
+    for fn in (ctx.load_layers, ctx.save_layers):
+        with pytest.raises(_lib.PegaFlowError, match="exceeds registered memory"):
+            fn(bad, _lib.MODE_KERNEL)
+        ctx.stream.synchronize()
+    ctx.load_layers(loads, _lib.MODE_KERNEL)
+    ctx.synchronize()
+    for dev, (_, ref, _, _, _, _) in zip(devs, osaves):
+        assert np.array_equal(dev.download(), ref)
+    for dev in devs:
+        dev.close()
+    host.close()
+
+
 def test_empty_and_errors(ctx, gpu):
     say("[gpu] empty and error paths")
     nb, bpb = 16, 512
