@@ -299,6 +299,9 @@ struct pf_xfer {
   size_t h_cap = 0;
   hipEvent_t desc_uploaded = nullptr;
   bool desc_inflight = false;
+  // Pipelined calls: recorded on the kernel stream before the call's first
+  // part, i.e. once every earlier launch (a reader of the descriptors) ended.
+  hipEvent_t parts_ready = nullptr;
   // Small calls: descriptors the kernels read in place from coherent pinned
   // memory (kHostDescMax entries), reused only once the stream has drained.
   ChunkDesc* h_small = nullptr;
@@ -372,13 +375,26 @@ int ensure_desc_capacity(pf_xfer* x, size_t n) {
 }
 
 // Copies descriptors [off, off + n) of the host staging to the same place in
-// device memory; the next launches read from there.
+// device memory; the next launches read from there.  A later part of a
+// pipelined call (off > 0) copies on the link-side stream, so the copy runs
+// under the earlier part's kernel instead of between the two kernels, and
+// the kernel stream waits for it.
 int upload_desc(pf_xfer* x, size_t n, size_t off = 0) {
   x->desc_base = x->d_desc + off;
   if (n == 0) return PF_OK;
+  hipStream_t s = off ? x->dma : x->stream;
+  if (off) {
+    // Not before earlier calls' kernels are done with this region, nor
+    // before the first part's own upload (desc_uploaded, if it uploaded),
+    // which the next call's reuse of the staging waits for through the
+    // event recorded below.
+    PF_HIP(hipStreamWaitEvent(s, x->parts_ready, 0));
+    PF_HIP(hipStreamWaitEvent(s, x->desc_uploaded, 0));
+  }
   PF_HIP(hipMemcpyAsync(x->d_desc + off, x->h_desc + off, n * sizeof(ChunkDesc),
-                        hipMemcpyHostToDevice, x->stream));
-  PF_HIP(hipEventRecord(x->desc_uploaded, x->stream));
+                        hipMemcpyHostToDevice, s));
+  PF_HIP(hipEventRecord(x->desc_uploaded, s));
+  if (off) PF_HIP(hipStreamWaitEvent(x->stream, x->desc_uploaded, 0));
   x->desc_inflight = true;
   return PF_OK;
 }
@@ -845,17 +861,26 @@ int kernel_direct(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<Lay
 }
 
 // Layers in the first part of a pipelined call, or 0 for a call issued
-// whole: calls of at least 8 layers and kPipelineMinChunks chunks (of the
-// order of the chunk counts whose planning takes ~0.1 ms) start with an
-// eighth of their layers.
+// whole.  Copies over the host link of at least 8 layers and
+// kPipelineMinChunks chunks (of the order of the chunk counts whose planning
+// takes ~0.1 ms) start with an eighth of their layers: that part's copy
+// (2.9 ms for a Llama prefix, 0.37 ms for one tensor-parallel rank's) hides
+// the planning of the rest, and one more launch boundary costs under 1%.
+// Copies between device buffers, HBM-bound at about 0.05 ms for such a
+// first part, are issued whole, as one launch.
 constexpr uint64_t kPipelineMinChunks = 16384;
 
 uint32_t pipeline_head(const pf_layer_xfer* layers, uint32_t num_layers) {
   if (num_layers < 8) return 0;
   uint64_t chunks = 0;
-  for (uint32_t i = 0; i < num_layers; ++i)
+  const pf_block_xfer* first = nullptr;
+  for (uint32_t i = 0; i < num_layers; ++i) {
     chunks += layers[i].num_blocks * (layers[i].layout.segments ? layers[i].layout.segments : 1);
-  return chunks >= kPipelineMinChunks ? num_layers / 8 : 0;
+    if (!first && layers[i].num_blocks > 0 && layers[i].blocks) first = layers[i].blocks;
+  }
+  uint64_t b = 0, e = 0;
+  if (chunks < kPipelineMinChunks || !first || !pinned_lookup(first->k_host, 1, &b, &e)) return 0;
+  return num_layers / 8;
 }
 
 int kernel_pipelined(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
@@ -870,6 +895,7 @@ int kernel_pipelined(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layer
   for (uint32_t i = 0; i < num_layers; ++i)
     bound += layers[i].num_blocks * (layers[i].layout.segments ? layers[i].layout.segments : 1);
   if (int rc = ensure_desc_capacity(x, static_cast<size_t>(bound))) return rc;
+  PF_HIP(hipEventRecord(x->parts_ready, x->stream));
   size_t n_first = 0;
   for (const LayerPlan& p : first)
     if (!p.ordered) n_first += p.chunks.size();
@@ -1051,6 +1077,7 @@ int pf_xfer_create(int device, uint64_t staging_bytes, pf_xfer** out) {
   hipError_t e = hipStreamCreateWithFlags(&x->stream, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&x->dma, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipEventCreateWithFlags(&x->desc_uploaded, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&x->parts_ready, hipEventDisableTiming);
   if (e == hipSuccess)
     e = hipHostMalloc(reinterpret_cast<void**>(&x->h_small), kHostDescMax * sizeof(ChunkDesc),
                       hipHostMallocMapped | hipHostMallocCoherent);
@@ -1086,6 +1113,7 @@ int pf_xfer_destroy(pf_xfer* x) {
   if (x->h_small) (void)hipHostFree(x->h_small);
   if (x->staging) (void)hipFree(reinterpret_cast<void*>(x->staging));
   if (x->desc_uploaded) (void)hipEventDestroy(x->desc_uploaded);
+  if (x->parts_ready) (void)hipEventDestroy(x->parts_ready);
   for (auto& t : x->timers) {
     (void)hipEventDestroy(t.first);
     (void)hipEventDestroy(t.second);

@@ -303,6 +303,23 @@ def test_pipelined_multi_layer_calls_vs_oracle(ctx):
     for dev, (oreg, ref, _, load_ids, ok_, ov) in zip(devs, osaves):
         oracle.process_load(oreg, ref, load_ids, ok_, ov)
         assert np.array_equal(dev.download(), ref)
+    # Three pipelined loads back to back, without waiting in between: each
+    # call's descriptors must not be overwritten while an earlier call's
+    # copies still read them.
+    loads2, ids2 = [], []
+    for lt in loads:
+        b = lt.blocks.copy()
+        ids = rng.choice(nb, m, replace=True)
+        b["block_idx"] = ids
+        loads2.append(LayerTransfer(lt.registration, b))
+        ids2.append(ids.tolist())
+    for batch in (loads, loads2, loads):
+        ctx.load_layers(batch, _lib.MODE_KERNEL)
+    ctx.synchronize()
+    for l, (dev, (oreg, ref, _, load_ids, ok_, ov)) in enumerate(zip(devs, osaves)):
+        for ids in (load_ids, ids2[l], load_ids):
+            oracle.process_load(oreg, ref, ids, ok_, ov)
+        assert np.array_equal(dev.download(), ref)
     # An out-of-range block in the last layer: found after the first part
     # was launched.
     bad = list(loads)
