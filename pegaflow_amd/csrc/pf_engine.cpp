@@ -214,10 +214,10 @@ size_t BlockStore::evict_lru(size_t max_blocks) {
   {
     std::lock_guard<std::mutex> lk(cache_mu_);
     while (dropped.size() < max_blocks && !lru_.empty()) {
-      auto it = cache_.find(lru_.back());
+      auto it = cache_.find(*lru_.back());
+      lru_.pop_back();
       dropped.push_back(std::move(it->second.block));
       cache_.erase(it);
-      lru_.pop_back();
     }
     evictions_ += dropped.size();
   }
@@ -265,25 +265,11 @@ void BlockStore::filter_slots(const std::vector<std::string>& keys,
   }
 }
 
-int BlockStore::insert_slots(const std::vector<std::string>& keys,
-                             const std::vector<size_t>& slots, std::vector<SlotEntries>& entries,
-                             size_t total_slots) {
-  const size_t n = keys.size();
-  // Keys sealed before this call (each key looked up once, not once per
-  // layer that carries it).
-  std::vector<char> sealed_already(n, 0), named(n, 0);
-  for (const auto& layer : entries)
-    for (const auto& e : layer) named[e.first] = 1;
-  {
-    std::lock_guard<std::mutex> lk(cache_mu_);
-    for (size_t i = 0; i < n; ++i)
-      if (named[i]) sealed_already[i] = cache_.count(keys[i]) != 0;
-  }
-  // The usual save brings every slot of its blocks in one call (all layers
-  // of a single-rank instance), each layer naming the same keys.  Such a
-  // block seals here directly, without passing through the inflight map,
-  // unless an earlier call left part of it there.
-  bool whole = total_slots > 0 && entries.size() == total_slots;
+BlockStore::Prepared BlockStore::prepare_whole(const std::vector<size_t>& slots,
+                                               std::vector<SlotEntries>& entries,
+                                               size_t total_slots) {
+  Prepared out;
+  bool whole = total_slots > 0 && entries.size() == total_slots && slots.size() == total_slots;
   if (whole) {
     std::vector<char> seen(total_slots, 0);
     for (size_t sl : slots) {
@@ -299,23 +285,57 @@ int BlockStore::insert_slots(const std::vector<std::string>& keys,
     for (size_t k = 0; whole && k < entries[j].size(); ++k)
       whole = entries[j][k].first == entries[0][k].first;
   }
+  if (!whole) return out;
+  out.reserve(entries[0].size());
+  for (size_t k = 0; k < entries[0].size(); ++k) {
+    auto sb = std::make_shared<SealedBlock>();
+    sb->slots.resize(total_slots);
+    for (size_t j = 0; j < entries.size(); ++j) {
+      sb->footprint += entries[j][k].second->size;
+      sb->slots[slots[j]] = std::move(entries[j][k].second);  // leaves it empty
+    }
+    out.emplace_back(entries[0][k].first, std::move(sb));
+  }
+  return out;
+}
+
+int BlockStore::insert_slots(const std::vector<std::string>& keys,
+                             const std::vector<size_t>& slots, std::vector<SlotEntries>& entries,
+                             size_t total_slots, Prepared* prepared) {
+  Prepared own;
+  if (!prepared) {
+    own = prepare_whole(slots, entries, total_slots);
+    prepared = &own;
+  }
+  const size_t n = keys.size();
+  // Keys sealed before this call (each key looked up once, not once per
+  // layer that carries it).
+  std::vector<char> sealed_already(n, 0), named(n, 0);
+  for (const auto& layer : entries)
+    for (const auto& e : layer) named[e.first] = 1;
+  for (const auto& p : *prepared) named[p.first] = 1;
+  {
+    std::lock_guard<std::mutex> lk(cache_mu_);
+    for (size_t i = 0; i < n; ++i)
+      if (named[i]) sealed_already[i] = cache_.count(keys[i]) != 0;
+  }
   std::vector<std::pair<uint32_t, std::shared_ptr<SealedBlock>>> sealed;
   int err = PF_OK;
   {
     std::lock_guard<std::mutex> lk(inflight_mu_);
-    if (whole) {
-      for (size_t k = 0; k < entries[0].size(); ++k) {
-        const uint32_t i = entries[0][k].first;
-        if (sealed_already[i] || inflight_.count(keys[i])) continue;  // general path below
-        auto sb = std::make_shared<SealedBlock>();
-        sb->slots.resize(total_slots);
-        for (size_t j = 0; j < entries.size(); ++j) {
-          sb->footprint += entries[j][k].second->size;
-          sb->slots[slots[j]] = std::move(entries[j][k].second);  // leaves it empty
-        }
-        sealed.emplace_back(i, std::move(sb));
+    // Complete blocks seal directly, unless an earlier call left part of
+    // the block in flight: then its slots go back to the general path.
+    for (auto& p : *prepared) {
+      const uint32_t i = p.first;
+      if (sealed_already[i]) continue;
+      if (inflight_.count(keys[i])) {
+        for (size_t j = 0; j < entries.size(); ++j)
+          entries[j].emplace_back(i, std::move(p.second->slots[slots[j]]));
+        continue;
       }
+      sealed.emplace_back(i, std::move(p.second));
     }
+    prepared->clear();
     const size_t n_direct = sealed.size();  // never entered the inflight map
     std::vector<InflightBlock*> ib(n, nullptr);  // node pointers survive inserts
     int rc = PF_OK;
@@ -366,10 +386,10 @@ int BlockStore::insert_slots(const std::vector<std::string>& keys,
   {
     std::lock_guard<std::mutex> lk(cache_mu_);
     for (size_t k = 0; k < sealed.size(); ++k) {
-      const std::string& key = keys[sealed[k].first];
-      if (cache_.count(key)) continue;
-      lru_.push_front(key);
-      cache_[key] = Entry{sealed[k].second, lru_.begin()};
+      auto ins = cache_.try_emplace(keys[sealed[k].first]);
+      if (!ins.second) continue;  // sealed already
+      lru_.push_front(&ins.first->first);
+      ins.first->second = Entry{sealed[k].second, lru_.begin()};
       fresh[k] = 1;
     }
   }
@@ -381,9 +401,10 @@ int BlockStore::insert_slots(const std::vector<std::string>& keys,
 
 bool BlockStore::cache_insert(const std::string& key, std::shared_ptr<SealedBlock> block) {
   std::lock_guard<std::mutex> lk(cache_mu_);
-  if (cache_.count(key)) return false;
-  lru_.push_front(key);
-  cache_[key] = Entry{std::move(block), lru_.begin()};
+  auto ins = cache_.try_emplace(key);
+  if (!ins.second) return false;
+  lru_.push_front(&ins.first->first);
+  ins.first->second = Entry{std::move(block), lru_.begin()};
   return true;
 }
 
@@ -1208,6 +1229,12 @@ int pf_engine_batch_save(pf_engine* e, const char* instance_id, uint64_t tp_rank
   // The LayerBlocks are built while the copy runs; they are published only
   // after it has completed (lib.rs:687-705, 755-770).
   std::vector<BlockStore::SlotEntries> entries(plans.size());
+  struct GroupSeal {
+    std::vector<size_t> slots;
+    std::vector<BlockStore::SlotEntries> entries;
+    BlockStore::Prepared prepared;
+  };
+  std::vector<GroupSeal> seals(groups.size());
   auto build_handles = [&] {
     for (size_t pi = 0; pi < plans.size(); ++pi) {
       const SavePlan& p = plans[pi];
@@ -1230,20 +1257,27 @@ int pf_engine_batch_save(pf_engine* e, const char* instance_id, uint64_t tp_rank
         entries[pi].emplace_back(p.key_idx[i], std::shared_ptr<LayerBlock>(set, &lb));
       }
     }
+    // Per hash list, the slots it fills and, when they are all of its
+    // blocks' slots, the complete blocks, ready to publish.
+    for (size_t gi = 0; gi < groups.size(); ++gi) {
+      GroupSeal& gs = seals[gi];
+      for (size_t li : groups[gi].plans) {
+        gs.slots.push_back(plans[li].slot);
+        gs.entries.push_back(std::move(entries[li]));
+      }
+      gs.prepared = BlockStore::prepare_whole(gs.slots, gs.entries, total_slots);
+    }
   };
   const auto t_planned = std::chrono::steady_clock::now();
   if (int rc = gpu->worker->save(xl, e->save_mode.load(), build_handles)) return rc;
   const auto t_copied = std::chrono::steady_clock::now();
   uint64_t bytes = 0;
-  for (const KeyGroup& g : groups) {
-    std::vector<size_t> slots;
-    std::vector<BlockStore::SlotEntries> ge;
-    for (size_t li : g.plans) {
-      slots.push_back(plans[li].slot);
-      ge.push_back(std::move(entries[li]));
+  for (size_t gi = 0; gi < groups.size(); ++gi) {
+    for (size_t li : groups[gi].plans)
       bytes += plans[li].key_idx.size() * plans[li].layout.block_size_bytes;
-    }
-    if (int rc = e->store->insert_slots(g.keys, slots, ge, total_slots))
+    GroupSeal& gs = seals[gi];
+    if (int rc = e->store->insert_slots(groups[gi].keys, gs.slots, gs.entries, total_slots,
+                                        &gs.prepared))
       return fail(rc, std::string("storage error: ") + pf_last_error());
   }
   e->saved_bytes.fetch_add(bytes);

@@ -142,8 +142,19 @@ class BlockStore {
   // cache and the seal hook runs for it.  Errors on slot count mismatch or
   // a slot out of range.
   using SlotEntries = std::vector<std::pair<uint32_t, std::shared_ptr<LayerBlock>>>;
+  using Prepared = std::vector<std::pair<uint32_t, std::shared_ptr<SealedBlock>>>;
+  // When the call brings every slot of its blocks (entries[j] for slot
+  // slots[j], all naming the same keys in the same order), the complete
+  // blocks built from them, moving the layer blocks out of `entries`;
+  // otherwise nothing.  Touches no state of the store, so it can run while
+  // the copy is in flight.
+  static Prepared prepare_whole(const std::vector<size_t>& slots,
+                                std::vector<SlotEntries>& entries, size_t total_slots);
+  // Publishes the copies (moves them): blocks in `prepared` seal directly
+  // unless an earlier call left part of them in flight.
   int insert_slots(const std::vector<std::string>& keys, const std::vector<size_t>& slots,
-                   std::vector<SlotEntries>& entries, size_t total_slots);  // moves the copies
+                   std::vector<SlotEntries>& entries, size_t total_slots,
+                   Prepared* prepared = nullptr);
   // storage.rs:529-547: every hash must be sealed; refreshes recency.
   int lookup_many(const std::vector<std::string>& keys,
                   std::vector<std::shared_ptr<SealedBlock>>* out);
@@ -157,10 +168,12 @@ class BlockStore {
   std::mutex inflight_mu_;
   std::unordered_map<std::string, InflightBlock> inflight_;
   std::mutex cache_mu_;
-  std::list<std::string> lru_;  // front = most recent
+  // Recency order, front = most recent; each element points at its key in
+  // cache_ (unordered_map nodes, hence keys, stay put until erased).
+  std::list<const std::string*> lru_;
   struct Entry {
     std::shared_ptr<SealedBlock> block;
-    std::list<std::string>::iterator pos;
+    std::list<const std::string*>::iterator pos;
   };
   std::unordered_map<std::string, Entry> cache_;
   std::atomic<uint64_t> evictions_{0};  // written under cache_mu_, read without it
