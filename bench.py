@@ -17,7 +17,9 @@ Printed JSON line (stdout):
   save_*           HBM -> host save, same figures
   roofline         the device gather kernel (paged layers -> packed HBM
                    buffer, all 32 layers in one launch): algorithmic bytes 2P
-                   per launch / its HIP-event-timed duration, vs 8 TB/s
+                   per launch / its HIP-event-timed duration, vs 8 TB/s; also
+                   the same kernel on a plain contiguous copy of 2P bytes
+                   (plain_copy_gbps) and the gather's fraction of that
   cpu_baseline     the reference's copy pattern (per-segment save copies,
                    merged-run restore copies) as host memcpy on this box's
                    cores, on a bounded sample of the same workload
@@ -872,6 +874,20 @@ def main():
     gather_gbps = 2 * P / (gather_ms / 1e3) / 1e9
     log(f"[bench] device gather {gather_ms:.3f} ms/launch ({g_launch} launch) = "
         f"{gather_gbps:.0f} GB/s")
+    # The same kernel and launch shape as a plain contiguous copy of the
+    # packed buffer (2P bytes moved, 32 KiB chunks in address order): the
+    # copy ceiling the gather's random chunk order is held against.
+    creg = KVCacheRegistration.create(gather_buf.ptr, P, P // 32768, 32768, 0, 1)
+    plain_dst = DeviceBuffer(P)
+    plain = wl.save_plan([creg], np.arange(P // 32768), plain_dst.ptr)
+    xfer.save_layers(plain, _lib.MODE_KERNEL)
+    p_ms = []
+    for _ in range(5):
+        xfer.save_layers(plain, _lib.MODE_KERNEL)
+        p_ms.append(xfer.last_kernel_ms()[0])
+    plain_dst.close()
+    plain_gbps = 2 * P / (sum(p_ms) / len(p_ms) / 1e3) / 1e9
+    log(f"[bench] plain contiguous copy, same kernel: {plain_gbps:.0f} GB/s")
     # Device scatter: the packed HBM buffer back into the target blocks.
     scatter = wl.load_plan(gather, targets)
     s_ms = []
@@ -1010,6 +1026,8 @@ def main():
             "kernel": "copy_chunks_v16_kernel<1,nt,nt> 512 threads (device gather: 40960 chunks of 32 KiB, 1 launch)",
             "bytes_per_launch": 2 * P,
             "ms_per_launch": round(gather_ms, 4),
+            "plain_copy_gbps": round(plain_gbps, 1),
+            "frac_of_plain_copy": round(gather_gbps / plain_gbps, 4),
         },
         "device_scatter": {"gbps": round(scatter_gbps, 1), "ms_per_launch": round(scatter_ms, 4),
                            "frac": round(scatter_gbps / HBM_PEAK_GBPS, 4)},
