@@ -316,6 +316,8 @@ _lock = threading.Lock()
 def load():
     """Load and bind the library (once)."""
     global _lib
+    if _lib is not None:  # bound already: no lock on the per-call path
+        return _lib
     with _lock:
         if _lib is not None:
             return _lib
