@@ -1,0 +1,140 @@
+// blockstore_test.cpp — the block store's sealing rules, on the host (no GPU),
+// built by tests/test_native.py from the library's own sources.
+//
+// A block seals when every one of its slots (layer x tensor-parallel rank)
+// has arrived (storage.rs:160-193, 457-514): a slot already present keeps
+// its first copy, a block sealed earlier is not replaced, and one call may
+// bring a whole block at once.  Checked here through BlockStore directly:
+//   1. a call bringing every slot of its blocks (slots in a permuted order);
+//   2. a block partly in flight from an earlier call, completed by a call
+//      that brings all slots (the earlier copies win);
+//   3. a block sealed earlier, saved again (unchanged);
+//   4. one key named twice in a call (the first occurrence seals);
+//   5. a slot count that differs from the block's in flight (an error).
+// Exit status 0 and "ok" on success; the first failed check is printed.
+#include <cstdio>
+#include <cstdlib>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "pf_engine.h"
+
+using namespace pf;
+
+namespace {
+
+int failures = 0;
+
+void expect(bool cond, const char* what) {
+  if (!cond) {
+    std::printf("FAILED: %s\n", what);
+    ++failures;
+  }
+}
+
+// One layer block per (slot, key) with a recognisable address.
+std::shared_ptr<LayerBlock> block(uint64_t tag) {
+  auto b = std::make_shared<LayerBlock>();
+  b->k_ptr = reinterpret_cast<uint8_t*>(tag);
+  b->size = 64;
+  return b;
+}
+
+uint64_t tag_of(const std::shared_ptr<LayerBlock>& b) {
+  return b ? reinterpret_cast<uint64_t>(b->k_ptr) : 0;
+}
+
+// entries[j] for slot slots[j]: every key index in `idx`, tagged
+// call * 1000 + slot * 10 + key index.
+std::vector<BlockStore::SlotEntries> entries_for(const std::vector<size_t>& slots,
+                                                 const std::vector<uint32_t>& idx, int call) {
+  std::vector<BlockStore::SlotEntries> e(slots.size());
+  for (size_t j = 0; j < slots.size(); ++j)
+    for (uint32_t i : idx) e[j].emplace_back(i, block(call * 1000 + slots[j] * 10 + i + 1));
+  return e;
+}
+
+}  // namespace
+
+int main() {
+  std::shared_ptr<PinnedPool> pool;
+  if (PinnedPool::create(1 << 20, 0, false, 0, &pool)) {
+    std::printf("FAILED: pool: %s\n", pf_last_error());
+    return 1;
+  }
+  BlockStore store(pool);
+  const size_t total = 4;
+  // Keys as the engine builds them: namespace, a zero byte, the hash.
+  auto key = [](int i) { return std::string("ns") + '\0' + "hash" + std::to_string(i); };
+  const std::vector<std::string> keys = {key(0), key(1), key(2), key(3)};
+
+  // 1. Every slot of keys 0 and 1 in one call, slots in a permuted order.
+  {
+    std::vector<size_t> slots = {2, 0, 3, 1};
+    auto e = entries_for(slots, {0, 1}, 1);
+    expect(store.insert_slots(keys, slots, e, total) == PF_OK, "whole call");
+    for (uint32_t i : {0u, 1u}) {
+      auto sb = store.peek(keys[i]);
+      expect(sb && sb->slots.size() == total, "whole call seals its blocks");
+      if (!sb) continue;
+      for (size_t s = 0; s < total; ++s)
+        expect(tag_of(sb->slots[s]) == 1000 + s * 10 + i + 1, "slot s holds the copy for slot s");
+      expect(sb->footprint == total * 64, "footprint");
+    }
+    expect(store.inflight_count() == 0, "nothing left in flight");
+  }
+  // 2. Key 2: slots 0 and 1 first (in flight), then a call with all slots.
+  {
+    std::vector<size_t> half = {0, 1};
+    auto e = entries_for(half, {2}, 2);
+    expect(store.insert_slots(keys, half, e, total) == PF_OK, "partial call");
+    expect(!store.peek(keys[2]) && store.inflight_count() == 1, "partial block stays in flight");
+    std::vector<size_t> all = {0, 1, 2, 3};
+    auto e2 = entries_for(all, {2}, 3);
+    expect(store.insert_slots(keys, all, e2, total) == PF_OK, "completing call");
+    auto sb = store.peek(keys[2]);
+    expect(sb != nullptr && store.inflight_count() == 0, "completed block seals");
+    if (sb) {
+      expect(tag_of(sb->slots[0]) == 2000 + 0 + 3 && tag_of(sb->slots[1]) == 2000 + 10 + 3,
+             "slots present in flight keep their first copy");
+      expect(tag_of(sb->slots[2]) == 3000 + 20 + 3 && tag_of(sb->slots[3]) == 3000 + 30 + 3,
+             "missing slots come from the completing call");
+      expect(sb->footprint == total * 64, "footprint counts every slot once");
+    }
+  }
+  // 3. Key 1 saved again: the sealed block is not replaced.
+  {
+    auto before = store.peek(keys[1]);
+    std::vector<size_t> all = {0, 1, 2, 3};
+    auto e = entries_for(all, {1}, 4);
+    expect(store.insert_slots(keys, all, e, total) == PF_OK, "save of a sealed key");
+    expect(store.peek(keys[1]) == before, "sealed block unchanged");
+  }
+  // 4. Key 3 named twice (indices 3 and 4 of the call's key list).
+  {
+    std::vector<std::string> dup = keys;
+    dup.push_back(keys[3]);
+    std::vector<size_t> all = {0, 1, 2, 3};
+    auto e = entries_for(all, {3, 4}, 5);
+    expect(store.insert_slots(dup, all, e, total) == PF_OK, "duplicate key");
+    auto sb = store.peek(keys[3]);
+    expect(sb && tag_of(sb->slots[0]) == 5000 + 0 + 3 + 1, "first occurrence seals");
+    expect(store.sealed_count() == 4, "four keys sealed");
+  }
+  // 5. A block in flight with 4 slots, then a call that counts 5.
+  {
+    const std::vector<std::string> k5 = {key(5)};
+    std::vector<size_t> one = {0};
+    auto e = entries_for(one, {0}, 6);
+    expect(store.insert_slots(k5, one, e, total) == PF_OK, "partial call (4 slots)");
+    std::vector<size_t> other = {1};
+    auto e2 = entries_for(other, {0}, 7);
+    expect(store.insert_slots(k5, other, e2, total + 1) != PF_OK, "slot count mismatch refused");
+    expect(std::string(pf_last_error()).find("slot count mismatch") != std::string::npos,
+           "the reference's message");
+  }
+  if (failures) return 1;
+  std::printf("ok\n");
+  return 0;
+}

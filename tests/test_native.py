@@ -20,9 +20,10 @@ import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CSRC = os.path.join(ROOT, "pegaflow_amd", "csrc")
-SOURCES = [os.path.join(CSRC, f) for f in (
+LIB_SOURCES = [os.path.join(CSRC, f) for f in (
     "pf_layout.cpp", "pf_runtime.cpp", "pf_kernels.hip", "pf_transfer.cpp", "pf_load_state.cpp",
-    "pf_engine.cpp", "pf_disk.cpp")] + [os.path.join(ROOT, "tests", "native", "stress_engine.cpp")]
+    "pf_engine.cpp", "pf_disk.cpp")]
+NATIVE = os.path.join(ROOT, "tests", "native")
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 
 # Host-side sanitizers only: each flag is passed to the host compilation.
@@ -36,11 +37,12 @@ VARIANTS = {
 }
 
 
-def build(variant: str) -> str:
+def build(variant: str, main: str = "stress_engine") -> str:
     flags = VARIANTS[variant][0].split()
     out = os.path.join(ROOT, "_build", f"native-{variant}")
     os.makedirs(out, exist_ok=True)
-    exe = os.path.join(out, "stress_engine")
+    exe = os.path.join(out, main)
+    SOURCES = LIB_SOURCES + [os.path.join(NATIVE, main + ".cpp")]
     deps = SOURCES + [os.path.join(CSRC, f) for f in os.listdir(CSRC)] + [
         os.path.join(ROOT, "include", "pegaflow_hip.h"), os.path.abspath(__file__)]
     newest = max(os.path.getmtime(p) for p in deps)
@@ -75,3 +77,16 @@ def test_engine_stress_under_sanitizer(variant, tmp_path):
                        stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     assert r.returncode == 0, r.stdout[-6000:]
     assert "bad 0" in r.stdout
+
+
+@pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc is not installed")
+def test_block_store_sealing_rules():
+    """tests/native/blockstore_test.cpp under AddressSanitizer+UBSan: whole
+    calls, blocks completed across calls (first copies win), sealed blocks
+    not replaced, a key named twice, and a slot count mismatch."""
+    exe = build("asan", "blockstore_test")
+    env = dict(os.environ, **VARIANTS["asan"][1])
+    r = subprocess.run([exe], env=env, timeout=120, stdout=subprocess.PIPE,
+                       stderr=subprocess.STDOUT, text=True)
+    assert r.returncode == 0, r.stdout[-6000:]
+    assert r.stdout.strip().endswith("ok")
