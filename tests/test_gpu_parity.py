@@ -206,8 +206,10 @@ def test_gpt2_config1_golden(ctx, mode):
 
 
 def _oracle_roundtrip_case(ctx, mode, nb, bpb, segs, kv, size, save_ids, load_ids,
-                           host_offset=0, seed=3):
-    """Runs save(save_ids) then load(load_ids) on device and on the oracle."""
+                           host_offset=0, seed=3, load_error=None):
+    """Runs save(save_ids) then load(load_ids) on device and on the oracle.
+    With ``load_error`` (a message pattern) the load must fail with it on
+    both, leaving the device bytes as they were."""
     dev = DeviceBuffer(size)
     dev.fill_random(seed)
     ref = dev.download()
@@ -227,6 +229,17 @@ def _oracle_roundtrip_case(ctx, mode, nb, bpb, segs, kv, size, save_ids, load_id
     ok_, ov, _ = oracle.save_host_layout(oreg, m, obase, obase + m * bpb)
     oracle.process_save(oreg, ref, save_ids, ok_, ov if split else None)
     assert np.array_equal(got_host, ohost)
+    if load_error is not None:
+        with pytest.raises(_lib.PegaFlowError, match=load_error):
+            ctx.load_layers([LayerTransfer(reg, block_array(load_ids, k, v if split else None))],
+                            mode)
+        ctx.synchronize()
+        with pytest.raises(oracle.OracleError, match=load_error):
+            oracle.process_load(oreg, ref, load_ids, ok_, ov if split else None)
+        assert np.array_equal(dev.download(), ref)
+        dev.close()
+        host.close()
+        return
     ctx.load_layers([LayerTransfer(reg, block_array(load_ids, k, v if split else None))], mode)
     ctx.synchronize()
     oracle.process_load(oreg, ref, load_ids, ok_, ov if split else None)
@@ -261,6 +274,52 @@ def test_edge_cases_vs_oracle(ctx, mode):
     # strided layout (kv_stride < bytes_per_block): in-order semantics.
     _oracle_roundtrip_case(ctx, m, 10, 64, 2, 160, 160 + 640, [1, 2, 3], [4, 3, 2])
     _oracle_roundtrip_case(ctx, m, 10, 64, 2, 32, 9 * 64 + 32 + 64, [2, 5], [3, 4])
+
+
+def _random_case(rng):
+    """A random layer layout of every kind validation accepts (split,
+    padded split, overlapping split, strided, contiguous two-segment,
+    blocks-first), random save ids and load ids with repeats."""
+    nb = int(rng.integers(1, 120))
+    bpb = int(rng.choice([16, 24, 48, 256, 4096, 32768]))
+    kind = rng.choice(["split", "padded", "overlap", "strided", "contig2", "single"])
+    if kind == "single":
+        segs, kv, size = 1, 0, nb * bpb
+    elif kind == "contig2":
+        segs, kv, size = 2, bpb, (nb + 1) * bpb
+    elif kind == "strided":
+        # The smallest size validation accepts, or room for whole blocks.
+        segs, kv = 2, max(8, (bpb // 2) // 8 * 8)
+        size = (nb - 1) * bpb + kv + bpb if rng.integers(2) else (nb + 1) * bpb
+    elif kind == "overlap":
+        segs, kv = 2, max(bpb, (nb * bpb // 2) // 8 * 8)
+        size = kv + nb * bpb
+    else:
+        segs, kv = 2, nb * bpb + (int(rng.integers(1, 4)) * bpb if kind == "padded" else 0)
+        size = kv + nb * bpb
+    m = int(rng.integers(1, nb + 1))
+    save_ids = rng.choice(nb, m, replace=False).tolist()
+    load_ids = rng.choice(nb, m, replace=True).tolist()
+    return kind, nb, bpb, segs, kv, size, save_ids, load_ids
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_layouts_vs_oracle(ctx, seed):
+    """Seeded random layouts, ids and host offsets, every mode: the device
+    bytes and the host regions equal the oracle's after save then load.  A
+    whole-block load of a strided layout's last block at the smallest valid
+    size would write past the tensor: both refuse it."""
+    rng = np.random.Generator(np.random.PCG64(1000 + seed))
+    for case in range(4):
+        kind, nb, bpb, segs, kv, size, save_ids, load_ids = _random_case(rng)
+        off = int(rng.choice([0, 8, 16, 4096]))
+        past = kind == "strided" and any((b + 2) * bpb > size for b in load_ids)
+        err = f"Block {max(load_ids)} exceeds registered memory" if past else None
+        for name, m in MODES.items():
+            say(f"[gpu] random seed={seed} case={case} {kind} nb={nb} bpb={bpb} kv={kv} "
+                f"size={size} m={len(save_ids)} off={off} mode={name} error={past}")
+            _oracle_roundtrip_case(ctx, m, nb, bpb, segs, kv, size, save_ids, load_ids,
+                                   host_offset=off, seed=seed * 10 + case, load_error=err)
 
 
 def test_pipelined_multi_layer_calls_vs_oracle(ctx):
