@@ -733,10 +733,16 @@ struct Step {
 
 // desc_off > 0: a later part of one pipelined call.  Its descriptors go
 // after the earlier parts' (whose copies may still read theirs), in room
-// the caller has reserved, and never in place.
+// the caller has reserved, and never in place.  layer_base: the call-wide
+// index of plans[0] (marks and their counters are per call-wide layer).
+// *used (if given): the descriptor slots of d_desc from desc_off on that
+// this call's launches read (chunks, then the marks' tables), 0 when they
+// read in place.
 int kernel_direct(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<LayerPlan>& plans,
                   bool is_save, pf_event* layer_events, const SignalTargets* sig,
-                  bool wait_save, size_t desc_off = 0) {
+                  bool wait_save, size_t desc_off = 0, uint32_t layer_base = 0,
+                  size_t* used = nullptr) {
+  if (used) *used = 0;
   if (int rc = check_all_kernel(layers, plans, true)) return rc;
   size_t total = 0;
   std::vector<size_t> first(plans.size());
@@ -777,7 +783,7 @@ int kernel_direct(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<Lay
       for (size_t k = li; k < lj; ++k) {
         if (plans[k].chunks.empty()) continue;
         aux.push_back(start);
-        ids.push_back(static_cast<uint32_t>(k));
+        ids.push_back(static_cast<uint32_t>(layer_base + k));
         start += static_cast<uint32_t>(plans[k].chunks.size());
       }
       aux.push_back(start);
@@ -791,7 +797,7 @@ int kernel_direct(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<Lay
   const size_t aux_desc = (aux.size() * sizeof(uint32_t) + sizeof(ChunkDesc) - 1) /
                           sizeof(ChunkDesc);
   // Counters for marks and the tile queue of queued launches.
-  if (int rc = ensure_counters(x, plans.size())) return rc;
+  if (int rc = ensure_counters(x, layer_base + plans.size())) return rc;
   ChunkDesc* hd = desc_off ? nullptr : small_desc(x, total + aux_desc);
   if (desc_off) {
     if (desc_off + total + aux_desc > x->h_cap || desc_off + total + aux_desc > x->d_cap)
@@ -813,8 +819,9 @@ int kernel_direct(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<Lay
     // the stream to drain.
     x->desc_base = x->h_small;
     x->small_inflight = true;
-  } else if (int rc = upload_desc(x, total + aux_desc, desc_off)) {
-    return rc;
+  } else {
+    if (int rc = upload_desc(x, total + aux_desc, desc_off)) return rc;
+    if (used) *used = total + aux_desc;
   }
   const uint32_t* d_aux = reinterpret_cast<const uint32_t*>(x->desc_base + total);
   for (const Step& st : steps) {
@@ -822,7 +829,7 @@ int kernel_direct(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<Lay
       if (int rc = dma_layer(x, plans[st.li], is_save, false)) return rc;
       if (layer_events && layer_events[st.li])
         PF_HIP(hipEventRecord(static_cast<hipEvent_t>(layer_events[st.li]), x->stream));
-      if (int rc = mark_layer(x, static_cast<uint32_t>(st.li), sig)) return rc;
+      if (int rc = mark_layer(x, static_cast<uint32_t>(layer_base + st.li), sig)) return rc;
       continue;
     }
     size_t n = 0;
@@ -852,7 +859,8 @@ int kernel_direct(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<Lay
       // Layers the launch did not mark: empty ones, and all of an unaligned launch.
       std::vector<uint32_t> rest;
       for (size_t k = st.li; k < st.lj; ++k)
-        if (!marked || plans[k].chunks.empty()) rest.push_back(static_cast<uint32_t>(k));
+        if (!marked || plans[k].chunks.empty())
+          rest.push_back(static_cast<uint32_t>(layer_base + k));
       if (int rc = mark_layers(x, rest, *sig)) return rc;
     }
   }
@@ -884,30 +892,33 @@ uint32_t pipeline_head(const pf_layer_xfer* layers, uint32_t num_layers) {
 }
 
 int kernel_pipelined(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
-                     uint32_t head, bool is_save, bool wait_save) {
+                     uint32_t head, bool is_save, bool wait_save, const SignalTargets* sig) {
   std::vector<LayerPlan> first, rest;
   if (int rc = plan_all(layers, head, is_save, &first)) return rc;
   for (uint32_t li = 0; li < head; ++li)
     apply_write_policy(layers[li], is_save, false, &first[li]);
-  // Room for every descriptor of the call, reserved before the first part
-  // is uploaded: growing the buffers later would wait for the first copy.
-  uint64_t bound = 1;
+  // Room for every descriptor of the call and both parts' mark tables
+  // (at most 2L+1 words each), reserved before the first part is uploaded:
+  // growing the buffers later would wait for the first copy.
+  uint64_t bound = 1 + 2 * ((2ull * num_layers + 1) * sizeof(uint32_t) / sizeof(ChunkDesc) + 1);
   for (uint32_t i = 0; i < num_layers; ++i)
     bound += layers[i].num_blocks * (layers[i].layout.segments ? layers[i].layout.segments : 1);
   if (int rc = ensure_desc_capacity(x, static_cast<size_t>(bound))) return rc;
+  if (int rc = ensure_counters(x, num_layers)) return rc;  // marks of both parts
   PF_HIP(hipEventRecord(x->parts_ready, x->stream));
+  // The second part's descriptors go after everything the first part's
+  // launches read: its chunks and its mark tables.
   size_t n_first = 0;
-  for (const LayerPlan& p : first)
-    if (!p.ordered) n_first += p.chunks.size();
-  if (int rc = kernel_direct(x, layers, first, is_save, nullptr, nullptr, false)) return rc;
+  if (int rc = kernel_direct(x, layers, first, is_save, nullptr, sig, false, 0, 0, &n_first))
+    return rc;
   int rc = plan_all(layers + head, num_layers - head, is_save, &rest);
   if (rc == PF_OK) {
     for (uint32_t li = head; li < num_layers; ++li)
       apply_write_policy(layers[li], is_save, false, &rest[li - head]);
     // The first part may have read its descriptors in place (h_small); the
     // second always uploads, after the first part's.
-    rc = kernel_direct(x, layers + head, rest, is_save, nullptr, nullptr, wait_save,
-                       n_first > 0 ? n_first : 1);
+    rc = kernel_direct(x, layers + head, rest, is_save, nullptr, sig, wait_save,
+                       n_first > 0 ? n_first : 1, head);
   }
   // On an error nothing of the call is left in flight: the caller may free
   // or reuse the host side at once.
@@ -925,12 +936,14 @@ int run(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, uint32_t m
   x->last_dma = 0;
   PF_HIP(hipSetDevice(x->device));
   std::vector<LayerPlan> plans;
-  if (mode == PF_MODE_KERNEL && !layer_events && !sig) {
+  if (mode == PF_MODE_KERNEL && !layer_events) {
     // A large call: its first layers are planned and launched before the
     // rest are planned, so the planning of the rest (about 3 ns a chunk)
-    // overlaps their copy.
+    // overlaps their copy.  Marks carry call-wide layer indices.
     const uint32_t head = pipeline_head(layers, num_layers);
-    if (head > 0) return kernel_pipelined(x, layers, num_layers, head, is_save, wait_save);
+    if (head > 0)
+      return kernel_pipelined(x, layers, num_layers, head, is_save, wait_save,
+                              is_save ? nullptr : sig);
   }
   if (int rc = plan_all(layers, num_layers, is_save, &plans)) return rc;
   switch (mode) {

@@ -133,6 +133,54 @@ def test_marked_load_mixed_layers_vs_oracle(ctx, mode):
         dev_words.close()
 
 
+def test_pipelined_marked_load_vs_oracle(ctx):
+    """A marked load large enough to be issued in two parts (16 layers,
+    about 30K chunks from pinned memory): the second part's marks use the
+    call-wide layer index, so every word of both targets holds the value,
+    twice in a row (the tile counters return to zero), with an empty layer
+    and an in-order (overlapping) layer in the second part; bytes against
+    the oracle.  Three copy launches: layers 0-1, 2-11, 13-15 (layer 12 is
+    copied in order by DMA); issued whole it would be two."""
+    say("[gpu] pipelined marked load vs oracle")
+    rng = np.random.Generator(np.random.PCG64(77))
+    nb, bpb, m = 1100, 256, 1024
+    cases = []
+    for l in range(16):
+        if l == 12:
+            cases.append(Case(10, bpb, 2, 1280, 1280 + 2560, [1, 2, 3], [4, 3, 2], 500 + l))
+        elif l == 9:
+            cases.append(Case(nb, bpb, 2, nb * bpb, 2 * nb * bpb, [], [], 500 + l))
+        else:
+            cases.append(Case(nb, bpb, 2, nb * bpb, 2 * nb * bpb,
+                              rng.choice(nb, m, replace=False).tolist(),
+                              rng.choice(nb, m, replace=True).tolist(), 500 + l))
+    L = len(cases)
+    host_words = PinnedBuffer(8 * L)
+    dev_words = DeviceBuffer(8 * L)
+    dev_words.memset(0)
+    host_words.array[:] = 0
+    try:
+        for c in cases:
+            c.save(ctx, _lib.MODE_KERNEL)
+        for value in (5, 6):
+            ctx.load_layers_marked([c.load_transfer() for c in cases],
+                                   [(host_words.ptr, value, True), (dev_words.ptr, value, False)],
+                                   _lib.MODE_KERNEL)
+            ctx.synchronize()
+            assert ctx.last_stats()[0] == 3, f"copy launches {ctx.last_stats()[0]}"
+            hw = host_words.array.view(np.uint64)
+            dw = dev_words.download().view(np.uint64)
+            assert hw.tolist() == [value] * L, f"host marks {hw.tolist()}"
+            assert dw.tolist() == [value] * L, f"device marks {dw.tolist()}"
+            for c in cases:
+                c.check_load()
+    finally:
+        for c in cases:
+            c.close()
+        host_words.close()
+        dev_words.close()
+
+
 def test_marked_load_rejects_bad_targets(ctx):
     say("[gpu] marked load argument checks")
     c = Case(16, 512, 2, 16 * 512, 2 * 16 * 512, [1], [2], 3)
