@@ -140,13 +140,19 @@ def test_pipelined_marked_load_vs_oracle(ctx):
     twice in a row (the tile counters return to zero), with an empty layer
     and an in-order (overlapping) layer in the second part; bytes against
     the oracle.  Three copy launches: layers 0-1, 2-11, 13-15 (layer 12 is
-    copied in order by DMA); issued whole it would be two."""
+    copied in order by DMA); issued whole it would be two.  The first part
+    (2 x 32 MiB) is still running when the second part's descriptors are
+    uploaded, so they must not overlap the first part's mark tables."""
     say("[gpu] pipelined marked load vs oracle")
     rng = np.random.Generator(np.random.PCG64(77))
     nb, bpb, m = 1100, 256, 1024
     cases = []
     for l in range(16):
-        if l == 12:
+        if l < 2:  # the first part: 32 MiB per layer, still copying while the rest is issued
+            cases.append(Case(600, 32768, 2, 600 * 32768, 2 * 600 * 32768,
+                              rng.choice(600, 512, replace=False).tolist(),
+                              rng.choice(600, 512, replace=True).tolist(), 500 + l))
+        elif l == 12:
             cases.append(Case(10, bpb, 2, 1280, 1280 + 2560, [1, 2, 3], [4, 3, 2], 500 + l))
         elif l == 9:
             cases.append(Case(nb, bpb, 2, nb * bpb, 2 * nb * bpb, [], [], 500 + l))
