@@ -5,7 +5,8 @@ device 0 and compares bytes:
   * small shapes: against the CPU oracle on the same seeded inputs, and
     against the committed golden fixtures;
   * full workload shapes (Llama-3.1-8B prefix, its TP=8 rank, MLA
-    latent): through size-independent closed forms — each host chunk and every block of every layer tensor must hold exactly the
+    latent): through size-independent closed forms — each host chunk
+    and every block of every layer tensor must hold exactly the
     splitmix64 words of the block it came from (a permutation identity plus
     "untouched blocks unchanged"), checked on the device.
 All four transfer modes must give identical bytes.
