@@ -517,12 +517,9 @@ int DeviceWorker::create(int device, bool with_gpu, std::shared_ptr<DeviceWorker
   w->loaded_bytes_ = loaded_bytes;
   w->failures_ = failures;
   if (with_gpu) {
-    if (int rc = pf_xfer_create(device, 0, &w->save_x_))
+    if (pf_xfer_create(device, 0, &w->save_x_) != PF_OK ||
+        pf_xfer_create(device, 0, &w->load_x_) != PF_OK)
       return fail(PF_ERR_INIT, std::string("failed to initialize HIP: ") + pf_last_error());
-    if (int rc = pf_xfer_create(device, 0, &w->load_x_)) {
-      (void)rc;
-      return fail(PF_ERR_INIT, std::string("failed to initialize HIP: ") + pf_last_error());
-    }
   }
   w->thread_ = std::thread([p = w.get()] { p->load_loop(); });
   *out = std::move(w);
