@@ -7,7 +7,6 @@ import os
 import re
 import struct
 
-import numpy as np
 import pytest
 from hypothesis import given, settings, strategies as st
 
