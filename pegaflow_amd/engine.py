@@ -105,6 +105,7 @@ class PegaEngine:
         _raise(lib().pf_engine_create(pool_size, kind, pinned_flags, unit_size_hint,
                                       ctypes.byref(h)))
         self._h = h.value
+        self._name_arrays = {}  # tuple of layer names -> C array of their bytes
 
     def set_transfer_modes(self, save_mode: int = _lib.MODE_KERNEL,
                            load_mode: int = _lib.MODE_KERNEL) -> None:
@@ -168,11 +169,20 @@ class PegaEngine:
         """Queues a multi-layer load; completion is published in the LoadState."""
         ids = np.ascontiguousarray(block_ids, dtype=np.int32)
         data, offs = _hashes(block_hashes)
-        names = [n.encode() for n in layer_names]
-        c_names = (ctypes.c_char_p * max(len(names), 1))(*names)
+        # A connector names the same layers on every load: their C array is
+        # built once (the bytes objects it points into are kept with it).
+        key = tuple(layer_names)
+        c_names = self._name_arrays.get(key)
+        if c_names is None:
+            names = [n.encode() for n in key]
+            c_names = (ctypes.c_char_p * max(len(names), 1))(*names)
+            c_names._keep = names
+            if len(self._name_arrays) >= 64:
+                self._name_arrays.clear()
+            self._name_arrays[key] = c_names
         _raise(lib().pf_engine_batch_load(
             self._h, instance_id.encode(), tp_rank, device_id, load_state_shm.encode(), c_names,
-            len(names), ids.ctypes.data, data.ctypes.data, offs.ctypes.data, len(ids)))
+            len(key), ids.ctypes.data, data.ctypes.data, offs.ctypes.data, len(ids)))
 
     # -- disk tier (seal_offload.rs) -------------------------------------
     def enable_disk(self, root: str, quota_bytes: int = DEFAULT_DISK_QUOTA_BYTES,
