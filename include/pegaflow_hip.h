@@ -360,10 +360,11 @@ int pf_load_layers(pf_xfer* xfer, const pf_layer_xfer* layers,
  *
  * A signal target is an array of one 8-byte word per layer of the call:
  * words + 8*l is set to `value` once layer l's bytes are in place.  The
- * array may be host-mapped pinned memory (host_memory = 1; the host polls
- * it), device memory of this process, or device memory of another process
- * mapped with pf_ipc_open (host_memory = 0; a stream waits on it with
- * pf_stream_wait_word).  Every word is written exactly once per call, empty
+ * array may be host-mapped pinned memory (host_memory = 1, the host polls
+ * it; an array inside a pf_pinned_allocate allocation is treated so even
+ * when the flag is 0), device memory of this process, or device memory of
+ * another process mapped with pf_ipc_open (host_memory = 0; a stream waits
+ * on it with pf_stream_wait_word).  Every word is written exactly once per call, empty
  * layers included; values must be nonzero, and a caller reusing an array
  * gives each call a larger value than the last, since waiters wait for
  * word >= value. */

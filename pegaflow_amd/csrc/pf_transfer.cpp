@@ -1257,7 +1257,11 @@ int pf_load_layers_marked(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_
                        (unsigned long long)num_layers * 8ull));
     t.words[i] = g.words;
     t.value[i] = g.value;
-    if (g.host_memory) t.host_mask |= 1u << i;
+    // Words in pinned host memory get system-scope stores even when the
+    // caller did not say so: the host has to see them.
+    uint64_t pb = 0, pe = 0;
+    if (g.host_memory || (num_layers > 0 && pinned_lookup(g.words, 8, &pb, &pe)))
+      t.host_mask |= 1u << i;
   }
   t.count = num_signals;
   return run(x, layers, num_layers, mode, false, nullptr, true, &t);
