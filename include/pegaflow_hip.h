@@ -352,9 +352,10 @@ int pf_load_layers(pf_xfer* xfer, const pf_layer_xfer* layers,
  * counterpart in the reference (its per-layer wait is a no-op,
  * worker.py:288-289; its load syncs once after all layers,
  * gpu_worker.rs:286-291).  Unlike layer_events, marks do not split a load
- * from pinned host memory into one launch per layer: in PF_MODE_KERNEL a
- * single launch covers every such layer and its last workgroup on layer l
- * writes the marks of layer l.  Layers loaded from device memory (an
+ * from pinned host memory into one launch per layer: in PF_MODE_KERNEL one
+ * launch covers every such layer (two for a large call, whose first eighth
+ * of layers is launched before the rest is planned) and its last workgroup
+ * on layer l writes the marks of layer l.  Layers loaded from device memory (an
  * HBM-bound copy) get one launch each, followed by their marks; DMA and
  * staged copies are marked after each layer's copies.
  *
