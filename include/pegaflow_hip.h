@@ -344,7 +344,8 @@ int pf_save_layers(pf_xfer* xfer, const pf_layer_xfer* layers,
  * layer_events is non-NULL, layer_events[l] is recorded once layer l's bytes
  * are in place (per-layer completion, which the reference lacks:
  * worker.py:288-289).  Completion of the whole call is pf_xfer_synchronize or
- * the last layer's event. */
+ * the last layer's event.  A save or load that fails returns with none of
+ * its copies (or marks) still in flight. */
 int pf_load_layers(pf_xfer* xfer, const pf_layer_xfer* layers,
                    uint32_t num_layers, uint32_t mode, pf_event* layer_events);
 

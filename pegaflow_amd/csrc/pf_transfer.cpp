@@ -930,6 +930,11 @@ int kernel_pipelined(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layer
   return rc;
 }
 
+int run_locked(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, uint32_t mode,
+               bool is_save, pf_event* layer_events, bool wait_save, const SignalTargets* sig);
+
+// One transfer call.  A call that fails part-way returns with none of its
+// copies in flight, so the caller may reuse or free the buffers at once.
 int run(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, uint32_t mode,
         bool is_save, pf_event* layer_events, bool wait_save = true,
         const SignalTargets* sig = nullptr) {
@@ -939,6 +944,16 @@ int run(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, uint32_t m
   x->last_kernels = 0;
   x->last_dma = 0;
   PF_HIP(hipSetDevice(x->device));
+  const int rc = run_locked(x, layers, num_layers, mode, is_save, layer_events, wait_save, sig);
+  if (rc != PF_OK) {
+    (void)hipStreamSynchronize(x->dma);
+    (void)hipStreamSynchronize(x->stream);
+  }
+  return rc;
+}
+
+int run_locked(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, uint32_t mode,
+               bool is_save, pf_event* layer_events, bool wait_save, const SignalTargets* sig) {
   std::vector<LayerPlan> plans;
   if (mode == PF_MODE_KERNEL && !layer_events) {
     // A large call: its first layers are planned and launched before the
