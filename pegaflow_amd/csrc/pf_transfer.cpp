@@ -920,14 +920,7 @@ int kernel_pipelined(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layer
     rc = kernel_direct(x, layers + head, rest, is_save, nullptr, sig, wait_save,
                        n_first > 0 ? n_first : 1, head);
   }
-  // On an error nothing of the call is left in flight (copies, or the
-  // second part's descriptor upload): the caller may free or reuse the host
-  // side at once.
-  if (rc != PF_OK) {
-    (void)hipStreamSynchronize(x->dma);
-    (void)hipStreamSynchronize(x->stream);
-  }
-  return rc;
+  return rc;  // on an error, run() drains both streams (copies and the upload)
 }
 
 int run_locked(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, uint32_t mode,
