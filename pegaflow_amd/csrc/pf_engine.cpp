@@ -1344,11 +1344,12 @@ int pf_engine_batch_load(pf_engine* e, const char* instance_id, uint64_t tp_rank
     }
     if (int rc = inst->slot_index(layer_id, tp_rank, &slot)) return bail(rc);
     std::vector<pf_block_xfer> blocks;
+    blocks.reserve(static_cast<size_t>(n));
+    const bool split = reg.segments == 2 && reg.kv_stride_bytes > reg.bytes_per_block;
     for (uint64_t j = 0; j < n; ++j) {
       if (block_ids[j] < 0) continue;
       if (slot >= task.keep[j]->slots.size() || !task.keep[j]->slots[slot]) continue;
       const LayerBlock& lb = *task.keep[j]->slots[slot];
-      const bool split = reg.segments == 2 && reg.kv_stride_bytes > reg.bytes_per_block;
       if (lb.size != reg.block_size_bytes || (lb.v_ptr != nullptr) != split)
         return bail(fail(PF_ERR_STORAGE,
                          strf("storage error: stored block at index %llu holds %llu %s bytes "
