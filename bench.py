@@ -23,6 +23,10 @@ Printed JSON line (stdout):
   cpu_baseline     the reference's copy pattern (per-segment save copies,
                    merged-run restore copies) as host memcpy on this box's
                    cores, on a bounded sample of the same workload
+  variants         the same prefix in every transfer mode: the reference's
+                   copy pattern (dma_reference), merged-run async copies
+                   (dma_batched), the zero-copy kernel and the staged mode
+                   (skipped with --quick unless --variants)
   other workloads  (skipped with --quick) layerwise_qwen3_8b, mla_latent,
                    tp8_rank_llama3_8b, fragmentation_llama3_8b,
                    engine_llama3_8b, two_process_llama3_8b, disk_tier_llama3_8b and
@@ -60,7 +64,7 @@ def parse():
     ap.add_argument("--load-mode", default="kernel",
                     choices=["dma_reference", "dma_batched", "kernel", "staged"])
     ap.add_argument("--variants", action="store_true",
-                    help="also time every transfer mode once per direction")
+                    help="also time every transfer mode with --quick (always done without it)")
     ap.add_argument("--sweep", action="store_true",
                     help="also sweep the gather kernel's launch shape")
     ap.add_argument("--threads", type=int, default=0, help="kernel workgroup size (0: default)")
@@ -899,7 +903,7 @@ def main():
     scatter_gbps = 2 * P / (scatter_ms / 1e3) / 1e9
 
     variants = {}
-    if args.variants:
+    if args.variants or not args.quick:
         for name, m in modes.items():
             reps = 1 if name == "dma_reference" else 3
             t_s = timed(lambda: xfer.save_layers(saved, m), reps)
