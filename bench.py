@@ -27,7 +27,7 @@ Printed JSON line (stdout):
                    copy pattern (dma_reference), merged-run async copies
                    (dma_batched), the zero-copy kernel and the staged mode
                    (skipped with --quick unless --variants)
-  other workloads  (skipped with --quick) layerwise_qwen3_8b, mla_latent,
+  other workloads  (skipped with --quick) gpt2_config1, layerwise_qwen3_8b, mla_latent,
                    tp8_rank_llama3_8b, fragmentation_llama3_8b,
                    engine_llama3_8b, two_process_llama3_8b, disk_tier_llama3_8b and
                    pinned_copy_microbench (single-block copy latency)
@@ -324,6 +324,39 @@ def leg_mla(xfer, seed):
         log(f"[bench] {shape.name}: {out[shape.name]}")
         pool.close()
         layers.close()
+    return out
+
+
+def leg_gpt2(xfer, seed):
+    """Config 1: GPT-2 shape, 12 fp16 layers [2,512,16,12,64], 64 random
+    blocks saved then restored into 64 other blocks (36 MiB each way), in the
+    kernel mode and in the reference's call pattern; bit-exact."""
+    from pegaflow_amd import _lib
+    from pegaflow_amd import workload as wl
+    from pegaflow_amd.runtime import PinnedBuffer
+
+    shape = wl.GPT2
+    layers = wl.DeviceLayers(shape, base_seed=seed)
+    ids, targets = wl.draw_blocks(shape.num_blocks, 64, seed)
+    P = wl.payload_bytes(layers.regs, 64)
+    pool = PinnedBuffer(P)
+    saved = wl.save_plan(layers.regs, ids, pool.ptr)
+    loads = wl.load_plan(saved, targets)
+    out = {"workload": shape.name + ", 64 random blocks", "payload_bytes": P}
+    bad = 0
+    for name, mode in (("kernel", _lib.MODE_KERNEL), ("dma_reference", _lib.MODE_DMA_REFERENCE)):
+        xfer.save_layers(saved, mode)
+        xfer.load_layers(loads, mode)
+        xfer.synchronize()
+        t_s = timed(lambda: xfer.save_layers(saved, mode), 5)
+        t_l = timed(lambda: (xfer.load_layers(loads, mode), xfer.synchronize()), 5)
+        bad += wl.verify_saved(layers, saved) + wl.verify_restored(layers, ids, targets)
+        out[name] = {"save_gbps": round(P / t_s / 1e9, 2), "restore_gbps": round(P / t_l / 1e9, 2),
+                     "save_ms": round(t_s * 1e3, 3), "restore_ms": round(t_l * 1e3, 3)}
+    out["bit_exact"] = bad == 0
+    log(f"[bench] gpt2: {out}")
+    pool.close()
+    layers.close()
     return out
 
 
@@ -773,7 +806,20 @@ def cpu_baseline(shape, ids, targets, n_layers, threads, seed):
         "single_thread_gbps": round(2 * payload / (s_1 + l_1) / 1e9, 3),
         "save_copies": int(len(save[0])),
         "restore_copies": int(len(load[0])),
+        "cpu_model": _cpu_model(),
+        "host_cpus": os.cpu_count(),
     }
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def main():
@@ -960,6 +1006,8 @@ def main():
 
     extra = {}
     if not args.quick:
+        log("[bench] config 1: gpt2 shape")
+        extra["gpt2_config1"] = leg_gpt2(xfer, args.seed)
         log("[bench] config 3: layer-wise restore (qwen3-8b)")
         extra["layerwise_qwen3_8b"] = leg_layerwise(xfer, args.seed)
         log(f"[bench] {extra['layerwise_qwen3_8b']}")
