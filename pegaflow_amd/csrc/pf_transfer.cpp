@@ -892,7 +892,8 @@ uint32_t pipeline_head(const pf_layer_xfer* layers, uint32_t num_layers) {
 }
 
 int kernel_pipelined(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
-                     uint32_t head, bool is_save, bool wait_save, const SignalTargets* sig) {
+                     uint32_t head, bool is_save, bool wait_save, const SignalTargets* sig,
+                     pf_event* layer_events) {
   std::vector<LayerPlan> first, rest;
   if (int rc = plan_all(layers, head, is_save, &first)) return rc;
   for (uint32_t li = 0; li < head; ++li)
@@ -909,7 +910,8 @@ int kernel_pipelined(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layer
   // The second part's descriptors go after everything the first part's
   // launches read: its chunks and its mark tables.
   size_t n_first = 0;
-  if (int rc = kernel_direct(x, layers, first, is_save, nullptr, sig, false, 0, 0, &n_first))
+  if (int rc = kernel_direct(x, layers, first, is_save, layer_events, sig, false, 0, 0,
+                             &n_first))
     return rc;
   int rc = plan_all(layers + head, num_layers - head, is_save, &rest);
   if (rc == PF_OK) {
@@ -917,8 +919,8 @@ int kernel_pipelined(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layer
       apply_write_policy(layers[li], is_save, false, &rest[li - head]);
     // The first part may have read its descriptors in place (h_small); the
     // second always uploads, after the first part's.
-    rc = kernel_direct(x, layers + head, rest, is_save, nullptr, sig, wait_save,
-                       n_first > 0 ? n_first : 1, head);
+    rc = kernel_direct(x, layers + head, rest, is_save, layer_events ? layer_events + head : nullptr,
+                       sig, wait_save, n_first > 0 ? n_first : 1, head);
   }
   return rc;  // on an error, run() drains both streams (copies and the upload)
 }
@@ -948,14 +950,15 @@ int run(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, uint32_t m
 int run_locked(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, uint32_t mode,
                bool is_save, pf_event* layer_events, bool wait_save, const SignalTargets* sig) {
   std::vector<LayerPlan> plans;
-  if (mode == PF_MODE_KERNEL && !layer_events) {
+  if (mode == PF_MODE_KERNEL) {
     // A large call: its first layers are planned and launched before the
     // rest are planned, so the planning of the rest (about 3 ns a chunk)
-    // overlaps their copy.  Marks carry call-wide layer indices.
+    // overlaps their copy.  Marks carry call-wide layer indices; per-layer
+    // events stay with their layers.
     const uint32_t head = pipeline_head(layers, num_layers);
     if (head > 0)
       return kernel_pipelined(x, layers, num_layers, head, is_save, wait_save,
-                              is_save ? nullptr : sig);
+                              is_save ? nullptr : sig, is_save ? nullptr : layer_events);
   }
   if (int rc = plan_all(layers, num_layers, is_save, &plans)) return rc;
   switch (mode) {
