@@ -91,6 +91,7 @@ int pf_is_contiguous_layout(const pf_kv_layout* layout);
  * segment to dst + s*bytes_per_block, load copies block_size_bytes from
  * segment_offset(block, 0), exactly as the reference does). */
 enum { PF_LAYOUT_SPLIT = 0, PF_LAYOUT_CONTIGUOUS = 1, PF_LAYOUT_STRIDED = 2 };
+/* -1 for a null layout. */
 int pf_layout_kind(const pf_kv_layout* layout);
 
 /* ------------------------------------------------------------------------ */
@@ -188,6 +189,8 @@ int pf_ipc_event_open(const uint8_t* handle, pf_event* out);
 /* Reference-equivalent DMA primitives (transfer.rs:56-239).                  */
 /* ------------------------------------------------------------------------ */
 /* Synchronous device -> host copy of size bytes from gpu_base+offset.
+ * cpu_buffer_len < size is "CPU buffer too small: ..." (the reference takes a
+ * slice and leaves the check to its callers, which pass size == len).
  * Replaces copy_gpu_to_cpu (transfer.rs:56-76). */
 int pf_copy_gpu_to_cpu(uint64_t gpu_base, uint64_t offset, void* cpu_buffer,
                        uint64_t cpu_buffer_len, uint64_t size);
@@ -212,7 +215,11 @@ uint64_t pf_count_merged_runs(const uint64_t* gpu_offsets,
                               const uint64_t* cpu_ptrs, uint64_t count,
                               uint64_t segment_size);
 /* Synchronous copy of one whole block to dst: one chunk of block_size_bytes
- * when contiguous, else each segment s to dst + s*bytes_per_block.
+ * when contiguous, else each segment s to dst + s*bytes_per_block.  Errors of
+ * segment_offset are returned as they are; a contiguous whole block that
+ * ends past size_bytes is "Block b exceeds registered memory (offset o,
+ * size block_size_bytes, limit size_bytes)" (the reference bounds only the
+ * first segment there and would read past the tensor).
  * Replaces copy_block_gpu_to_cpu / copy_gpu_to_cpu_strided
  * (transfer.rs:201-239). */
 int pf_copy_block_gpu_to_cpu(const pf_kv_layout* layout, uint64_t block_idx,
@@ -459,9 +466,21 @@ void pf_load_state_set_layers_done(pf_load_state* state, int64_t n);
 int pf_load_state_create_layered_events(uint32_t num_layers,
                                         const uint8_t* event_handles,
                                         pf_load_state** out);
+/* The in-process variant of the event block (no counterpart in the
+ * reference): num_layers events of the loader's own process (pf_event_create
+ * or pf_event_create_ipc), whose addresses fill the handle slots (8 bytes,
+ * then zeros) under magic 0x50464C4C ('PFLL').  The loader records them as
+ * it records opened handles, one launch per layer, then publishes
+ * events_recorded.  For an engine in the consumer's process, and for
+ * runtimes that cannot export interprocess events. */
+int pf_load_state_create_layered_local_events(uint32_t num_layers,
+                                              const pf_event* events,
+                                              pf_load_state** out);
 /* Handles carried by a state (NULL / 0 when none). */
 const uint8_t* pf_load_state_event_handles(const pf_load_state* state,
                                            uint32_t* count);
+/* 1 when the state's event block holds in-process event addresses. */
+int pf_load_state_events_local(const pf_load_state* state);
 int64_t pf_load_state_events_recorded(const pf_load_state* state);
 void pf_load_state_set_events_recorded(pf_load_state* state, int64_t n);
 /* Device-side per-layer completion through layer words (no counterpart in

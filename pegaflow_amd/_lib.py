@@ -278,6 +278,8 @@ SIGNATURES = {
     "pf_load_state_set_layers_done": (None, [vp, i64]),
     "pf_load_state_create_layered_events": (i32, [u32, vp, pvp]),
     "pf_load_state_event_handles": (vp, [vp, ctypes.POINTER(ctypes.c_uint32)]),
+    "pf_load_state_create_layered_local_events": (i32, [u32, ctypes.POINTER(vp), vp]),
+    "pf_load_state_events_local": (i32, [vp]),
     "pf_load_state_events_recorded": (i64, [vp]),
     "pf_load_state_set_events_recorded": (None, [vp, i64]),
     "pf_load_state_create_layered_words": (i32, [u32, ctypes.POINTER(LayerWords), pvp]),

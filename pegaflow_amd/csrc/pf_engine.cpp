@@ -697,12 +697,15 @@ void DeviceWorker::load_loop() {
       }
       events_.push_back(e);
     }
-    // A consumer in another process may have put one interprocess event per
-    // layer in the LoadState: those are recorded instead of the worker's own,
-    // so the consumer's streams can wait on each layer on the device.
+    // A consumer may have put one event per layer in the LoadState: those
+    // are recorded instead of the worker's own, so the consumer's streams
+    // can wait on each layer on the device.  Interprocess handles (a
+    // consumer in another process) are opened here and closed after the
+    // load; in-process events are the consumer's own and recorded as given.
     std::vector<pf_event> ipc_evs;
     uint32_t n_handles = 0;
     const uint8_t* handles = pf_load_state_event_handles(task.state, &n_handles);
+    const bool local_evs = pf_load_state_events_local(task.state) != 0;
     if (ok && handles) {
       if (n_handles != L) {
         set_error(strf("storage error: LoadState carries %u layer events for %zu layers",
@@ -710,9 +713,17 @@ void DeviceWorker::load_loop() {
         ok = false;
       }
       for (uint32_t l = 0; ok && l < n_handles; ++l) {
+        const uint8_t* slot = handles + static_cast<size_t>(l) * PF_IPC_HANDLE_BYTES;
         pf_event ev = nullptr;
-        ok = pf_ipc_event_open(handles + static_cast<size_t>(l) * PF_IPC_HANDLE_BYTES, &ev) ==
-             PF_OK;
+        if (local_evs) {
+          uint64_t a = 0;
+          std::memcpy(&a, slot, sizeof(a));
+          ev = reinterpret_cast<pf_event>(a);
+          ok = ev != nullptr;
+          if (!ok) set_error(strf("storage error: null event for layer %u", l));
+        } else {
+          ok = pf_ipc_event_open(slot, &ev) == PF_OK;
+        }
         if (ok) ipc_evs.push_back(ev);
       }
     }
@@ -760,7 +771,8 @@ void DeviceWorker::load_loop() {
       }
       if (!ok) (void)pf_xfer_synchronize(load_x_);
     }
-    for (pf_event ev : ipc_evs) (void)pf_event_destroy(ev);
+    if (!local_evs)
+      for (pf_event ev : ipc_evs) (void)pf_event_destroy(ev);
     // A failed load still ends the consumer's device waits (the LoadState
     // says it failed).
     if (!ok && consumer_words) {

@@ -117,11 +117,18 @@ int pf_segment_offset(const pf_kv_layout* layout, uint64_t block_idx,
 }
 
 int pf_is_contiguous_layout(const pf_kv_layout* layout) {
+  if (!layout) {
+    fail(PF_ERR_INVALID_ARGUMENT, "null layout");
+    return 0;
+  }
   return layout->segments <= 1 ||
          layout->kv_stride_bytes == layout->bytes_per_block;
 }
 
-int pf_layout_kind(const pf_kv_layout* layout) { return layout_kind(*layout); }
+int pf_layout_kind(const pf_kv_layout* layout) {
+  if (!layout) return fail(PF_ERR_INVALID_ARGUMENT, "null layout"), -1;
+  return layout_kind(*layout);
+}
 
 // transfer.rs:134-177: a run grows while both the device offset and the host
 // address continue exactly `segment_size` past the run's start.

@@ -18,6 +18,9 @@
 //   count 64-byte interprocess event handles, one per layer; the loader
 //   records layer l's event after layer l's copy and then publishes
 //   events_recorded = count, after which a consumer can wait on the device.
+//   Magic 0x50464C4C ('PFLL') marks the in-process variant: each 64-byte
+//   slot holds the address of an event of the loader's own process in its
+//   first 8 bytes (zeros after), recorded as it is.
 // Words block (optional, instead of the event block), at byte 48:
 //   u32 magic 0x50464C57 ('PFLW'), u32 count, u64 value, u32 kind,
 //   u32 reserved, u64 address, u64 alloc_size, u64 offset, 64-byte IPC
@@ -52,7 +55,8 @@ constexpr size_t kRecordAlign = 8;
 constexpr size_t kAllocSize = kMetaSize + kRecordSize + kRecordAlign;  // 32
 constexpr size_t kExtOffset = kAllocSize;
 constexpr size_t kExtSize = 16;
-constexpr uint32_t kEvMagic = 0x50464C45u;  // 'PFLE'
+constexpr uint32_t kEvMagic = 0x50464C45u;       // 'PFLE'
+constexpr uint32_t kEvLocalMagic = 0x50464C4Cu;  // 'PFLL'
 constexpr size_t kEvOffset = kExtOffset + kExtSize;  // 48
 constexpr size_t kEvSize = 16;
 constexpr size_t kHandleBytes = PF_IPC_HANDLE_BYTES;
@@ -129,13 +133,14 @@ struct pf_load_state {
   Record* rec = nullptr;
   ExtRecord* ext = nullptr;
   EvRecord* ev = nullptr;
+  bool ev_local = false;  // the event block holds in-process event addresses
   WordsRecord* words = nullptr;
 };
 
 namespace {
 
 int create_state(uint32_t num_layers, bool layered, const uint8_t* handles,
-                 const pf_layer_words* words, pf_load_state** out) {
+                 const pf_layer_words* words, pf_load_state** out, bool local_events = false) {
   if (!out) return fail(PF_ERR_INVALID_ARGUMENT, "null output");
   if (handles && (num_layers == 0 || num_layers > kMaxEvents))
     return fail(PF_ERR_INVALID_ARGUMENT,
@@ -209,7 +214,8 @@ int create_state(uint32_t num_layers, bool layered, const uint8_t* handles,
     std::memcpy(base + kEvOffset + kEvSize, handles, num_layers * kHandleBytes);
     __atomic_store_n(&st->ev->count, num_layers, __ATOMIC_RELEASE);
     __atomic_store_n(&st->ev->recorded, (int64_t)0, __ATOMIC_RELEASE);
-    __atomic_store_n(&st->ev->magic, kEvMagic, __ATOMIC_RELEASE);
+    st->ev_local = local_events;
+    __atomic_store_n(&st->ev->magic, local_events ? kEvLocalMagic : kEvMagic, __ATOMIC_RELEASE);
   }
   if (words) {
     st->words = reinterpret_cast<WordsRecord*>(base + kEvOffset);
@@ -244,6 +250,22 @@ int pf_load_state_create_layered_events(uint32_t num_layers, const uint8_t* even
                                         pf_load_state** out) {
   if (!event_handles) return fail(PF_ERR_INVALID_ARGUMENT, "null event handles");
   return create_state(num_layers, true, event_handles, nullptr, out);
+}
+
+int pf_load_state_create_layered_local_events(uint32_t num_layers, const pf_event* events,
+                                              pf_load_state** out) {
+  if (!events) return fail(PF_ERR_INVALID_ARGUMENT, "null events");
+  if (num_layers == 0 || num_layers > kMaxEvents)
+    return fail(PF_ERR_INVALID_ARGUMENT,
+                strf("a LoadState carries 1..%u layer events, got %u", kMaxEvents, num_layers));
+  std::string slots(static_cast<size_t>(num_layers) * kHandleBytes, '\0');
+  for (uint32_t l = 0; l < num_layers; ++l) {
+    if (!events[l]) return fail(PF_ERR_INVALID_ARGUMENT, strf("null event for layer %u", l));
+    const uint64_t a = reinterpret_cast<uint64_t>(events[l]);
+    std::memcpy(&slots[static_cast<size_t>(l) * kHandleBytes], &a, sizeof(a));
+  }
+  return create_state(num_layers, true, reinterpret_cast<const uint8_t*>(slots.data()), nullptr,
+                      out, true);
 }
 
 int pf_load_state_create_layered_words(uint32_t num_layers, const pf_layer_words* words,
@@ -319,9 +341,12 @@ int pf_load_state_attach(const char* shm_name, pf_load_state** out) {
   if (st->ext && len >= kEvOffset + kEvSize) {
     EvRecord* ev = reinterpret_cast<EvRecord*>(base + kEvOffset);
     const uint32_t count = __atomic_load_n(&ev->count, __ATOMIC_ACQUIRE);
-    if (__atomic_load_n(&ev->magic, __ATOMIC_ACQUIRE) == kEvMagic && count > 0 &&
-        count <= kMaxEvents && len >= kEvOffset + kEvSize + count * kHandleBytes)
+    const uint32_t magic = __atomic_load_n(&ev->magic, __ATOMIC_ACQUIRE);
+    if ((magic == kEvMagic || magic == kEvLocalMagic) && count > 0 && count <= kMaxEvents &&
+        len >= kEvOffset + kEvSize + count * kHandleBytes) {
       st->ev = ev;
+      st->ev_local = magic == kEvLocalMagic;
+    }
   }
   if (st->ext && len >= kEvOffset + sizeof(WordsRecord)) {
     WordsRecord* w = reinterpret_cast<WordsRecord*>(base + kEvOffset);
@@ -380,6 +405,8 @@ const uint8_t* pf_load_state_event_handles(const pf_load_state* st, uint32_t* co
   if (count) *count = __atomic_load_n(&st->ev->count, __ATOMIC_ACQUIRE);
   return reinterpret_cast<const uint8_t*>(st->ev) + kEvSize;
 }
+
+int pf_load_state_events_local(const pf_load_state* st) { return st->ev && st->ev_local ? 1 : 0; }
 
 int64_t pf_load_state_events_recorded(const pf_load_state* st) {
   return st->ev ? __atomic_load_n(&st->ev->recorded, __ATOMIC_ACQUIRE) : 0;

@@ -1023,6 +1023,7 @@ extern "C" {
 // ---------------------------------------------------------------------------
 int pf_copy_gpu_to_cpu(uint64_t gpu_base, uint64_t offset, void* cpu_buffer,
                        uint64_t cpu_buffer_len, uint64_t size) {
+  if (!cpu_buffer && size > 0) return fail(PF_ERR_INVALID_ARGUMENT, "null CPU buffer");
   if (cpu_buffer_len < size)
     return fail(PF_ERR_STORAGE, strf("CPU buffer too small: %llu bytes, need %llu bytes",
                                      (unsigned long long)cpu_buffer_len,
@@ -1035,6 +1036,7 @@ int pf_copy_gpu_to_cpu(uint64_t gpu_base, uint64_t offset, void* cpu_buffer,
 
 int pf_copy_cpu_to_gpu_async(uint64_t gpu_base, uint64_t offset, const void* cpu_buffer,
                              uint64_t cpu_buffer_len, uint64_t size, pf_stream stream) {
+  if (!cpu_buffer && size > 0) return fail(PF_ERR_INVALID_ARGUMENT, "null CPU buffer");
   if (cpu_buffer_len < size)
     return fail(PF_ERR_STORAGE, strf("CPU buffer too small: %llu bytes, need %llu bytes",
                                      (unsigned long long)cpu_buffer_len,
@@ -1049,6 +1051,10 @@ int pf_batch_copy_segments_to_gpu(const uint64_t* gpu_offsets, const uint64_t* c
                                   uint64_t count, uint64_t segment_size,
                                   const pf_kv_layout* layout, pf_stream stream,
                                   uint64_t* out_batches) {
+  if (out_batches) *out_batches = 0;
+  if (!layout) return fail(PF_ERR_INVALID_ARGUMENT, "null layout");
+  if (count > 0 && (!gpu_offsets || !cpu_ptrs))
+    return fail(PF_ERR_INVALID_ARGUMENT, "null transfer list");
   uint64_t batches = 0;
   uint64_t i = 0;
   while (i < count) {
@@ -1062,6 +1068,8 @@ int pf_batch_copy_segments_to_gpu(const uint64_t* gpu_offsets, const uint64_t* c
     int rc = pf_copy_cpu_to_gpu_async(layout->data_ptr, gpu_offsets[i],
                                       reinterpret_cast<const void*>(cpu_ptrs[i]), total,
                                       total, stream);
+    // Copies already issued stay queued on the stream, as in the reference.
+    if (out_batches) *out_batches = batches;
     if (rc) return rc;
     ++batches;
     i += n;
@@ -1071,13 +1079,22 @@ int pf_batch_copy_segments_to_gpu(const uint64_t* gpu_offsets, const uint64_t* c
 }
 
 int pf_copy_block_gpu_to_cpu(const pf_kv_layout* layout, uint64_t block_idx, void* dst) {
+  if (!layout) return fail(PF_ERR_INVALID_ARGUMENT, "null layout");
+  if (!dst) return fail(PF_ERR_INVALID_ARGUMENT, "null destination");
   uint64_t off = 0;
   const pf_kv_layout& l = *layout;
   if (pf_is_contiguous_layout(layout)) {
     if (int rc = segment_offset(l, block_idx, 0, &off)) return rc;
-    if (off + l.block_size_bytes > l.size_bytes)
-      return fail(PF_ERR_STORAGE, strf("Block %llu exceeds registered memory",
-                                       (unsigned long long)block_idx));
+    // The reference bounds only the first segment here (transfer.rs:206-208)
+    // and would read past the tensor for a whole block that does not fit.
+    uint64_t end = 0;
+    if (__builtin_add_overflow(off, l.block_size_bytes, &end) || end > l.size_bytes)
+      return fail(PF_ERR_STORAGE,
+                  strf("Block %llu exceeds registered memory (offset %llu, size %llu, "
+                       "limit %llu)",
+                       (unsigned long long)block_idx, (unsigned long long)off,
+                       (unsigned long long)l.block_size_bytes,
+                       (unsigned long long)l.size_bytes));
     return pf_copy_gpu_to_cpu(l.data_ptr, off, dst, l.block_size_bytes, l.block_size_bytes);
   }
   for (uint64_t s = 0; s < l.segments; ++s) {

@@ -39,6 +39,15 @@ class LoadState:
             check(lib().pf_load_state_create_layered_words(num_layers, ctypes.byref(layer_words),
                                                            ctypes.byref(h)),
                   "failed to create LoadState")
+        elif event_handles is not None and all(hasattr(e, "handle") for e in event_handles):
+            # In-process events (runtime.Event): their addresses, for an
+            # engine in this process.
+            if num_layers is None or len(event_handles) != num_layers:
+                raise ValueError("one event per layer is required")
+            arr = (ctypes.c_void_p * num_layers)(*[e.handle for e in event_handles])
+            check(lib().pf_load_state_create_layered_local_events(num_layers, arr,
+                                                                  ctypes.byref(h)),
+                  "failed to create LoadState")
         elif event_handles is not None:
             handles = b"".join(bytes(e) for e in event_handles)
             if num_layers is None or len(event_handles) != num_layers or \
@@ -95,6 +104,10 @@ class LoadState:
 
     def events_recorded(self) -> int:
         return int(lib().pf_load_state_events_recorded(self._h))
+
+    def events_local(self) -> bool:
+        """True when the event block holds in-process event addresses."""
+        return bool(lib().pf_load_state_events_local(self._h))
 
     def layer_words(self):
         """(pf_layer_words, layer count) of the words block, or (None, 0)."""
@@ -190,7 +203,8 @@ class PyLoadState:
     (``wait_for_layer_on_device``):
       * ``layer_events``: one 64-byte interprocess event handle per layer
         (e.g. ``torch.cuda.Event(interprocess=True).ipc_handle()``), recorded
-        by the loader after each layer;
+        by the loader after each layer; or, for an engine in this process,
+        one ``runtime.Event`` per layer, recorded as they are;
       * ``layer_words``: a ``LayerWords`` whose words the loader's copy kernel
         sets per layer (for runtimes that cannot share events)."""
 

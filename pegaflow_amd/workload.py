@@ -66,6 +66,76 @@ def draw_blocks(num_blocks: int, n: int, seed: int = 0):
     return ids.astype(np.int64), targets.astype(np.int64)
 
 
+def draw_runs(rng, num_blocks: int, n: int, mean_run: float, exclude=None) -> np.ndarray:
+    """n distinct block ids built from runs of consecutive blocks whose
+    lengths are Geometric(1/mean_run) (support >= 1), each run starting at a
+    random free block and stopping early at a used block or the tensor's end.
+    mean_run >= n gives one sorted consecutive run at a random free window.
+    ``exclude``: a bool mask of num_blocks blocks that may not be drawn.
+    Ids are returned in draw order (the reference never sorts)."""
+    used = np.zeros(num_blocks, bool) if exclude is None else np.array(exclude, bool)
+    if used.shape != (num_blocks,):
+        raise ValueError("exclude must be a mask of num_blocks entries")
+    if n > num_blocks - int(used.sum()):
+        raise ValueError(f"cannot draw {n} distinct blocks: {num_blocks - int(used.sum())} free")
+    if mean_run >= n:
+        # Start positions s whose window [s, s + n) holds no used block.
+        c = np.concatenate([[0], np.cumsum(used, dtype=np.int64)])
+        starts = np.flatnonzero(c[n:] - c[:-n] == 0)
+        if len(starts) == 0:
+            raise ValueError(f"no free window of {n} consecutive blocks")
+        s = int(starts[int(rng.integers(0, len(starts)))])
+        return np.arange(s, s + n, dtype=np.int64)
+    out = []
+    while len(out) < n:
+        length = min(int(rng.geometric(1.0 / mean_run)), n - len(out))
+        b = int(rng.integers(0, num_blocks))
+        while used[b]:
+            b = int(rng.integers(0, num_blocks))
+        while length > 0 and b < num_blocks and not used[b]:
+            used[b] = True
+            out.append(b)
+            b += 1
+            length -= 1
+    return np.asarray(out, np.int64)
+
+
+def run_count(ids) -> int:
+    """Maximal runs of consecutive increasing ids (1 + breaks)."""
+    ids = np.asarray(ids, np.int64)
+    return 0 if len(ids) == 0 else 1 + int(np.count_nonzero(np.diff(ids) != 1))
+
+
+def fragmentation_requests(num_blocks: int, mean_run: float, seed: int = 0,
+                           n_requests: int = 64, min_tokens: int = 1024,
+                           max_tokens: int = 16384, block_tokens: int = 16):
+    """The fragmentation sweep's batch: n_requests prefixes of U[min_tokens,
+    max_tokens] tokens (ceil(tokens / block_tokens) blocks each).  Each
+    request is (ids, targets): the blocks it saves, drawn as geometric runs
+    of mean ``mean_run``, and the blocks it restores that batch into, a
+    second draw of the same kind disjoint from ``ids``.  Each request saves
+    and then restores the same bytes, so saves and restores alternate 50/50.
+    mean_run >= SORTED_MEAN_RUN (640, the 10K-token prefix's block count)
+    stands for fully sorted ids: one consecutive run per request, whatever
+    its length.  The same seed gives the same token counts for every
+    mean_run."""
+    tok_rng = np.random.Generator(np.random.PCG64(seed + 4))
+    tokens = tok_rng.integers(min_tokens, max_tokens + 1, n_requests)
+    rng = np.random.Generator(np.random.PCG64([seed + 4, int(round(mean_run * 1000))]))
+    m = float("inf") if mean_run >= SORTED_MEAN_RUN else mean_run
+    out = []
+    for t in tokens:
+        nb = (int(t) + block_tokens - 1) // block_tokens
+        ids = draw_runs(rng, num_blocks, nb, m)
+        mask = np.zeros(num_blocks, bool)
+        mask[ids] = True
+        out.append((ids, draw_runs(rng, num_blocks, nb, m, exclude=mask)))
+    return out
+
+
+SORTED_MEAN_RUN = 640
+
+
 class DeviceLayers:
     """One device tensor per layer, filled with seeded random words."""
 
@@ -121,12 +191,16 @@ def load_plan(saved: list[LayerTransfer], targets) -> list[LayerTransfer]:
     return out
 
 
-def verify_saved(layers: DeviceLayers, saved: list[LayerTransfer]) -> int:
-    """Mismatching words in the host regions of a save batch (0 = exact)."""
+def verify_saved(layers: DeviceLayers, saved: list[LayerTransfer], src_of=None) -> int:
+    """Mismatching words in the host regions of a save batch (0 = exact).
+    ``src_of`` (optional, one entry per block): block b currently holds the
+    words block src_of[b] was filled with (after earlier restores)."""
     bad = 0
     for l, lt in enumerate(saved):
         reg = lt.registration
         ids = lt.blocks["block_idx"].astype(np.uint64)
+        if src_of is not None:
+            ids = np.asarray(src_of, np.uint64)[ids.astype(np.int64)]
         bpb = reg.bytes_per_block
         if reg.is_split:
             addrs = np.concatenate([lt.blocks["k_host"], lt.blocks["v_host"]])
@@ -142,11 +216,20 @@ def verify_restored(layers: DeviceLayers, ids, targets) -> int:
     """Mismatching words over every block of every layer after restoring the
     blocks saved from `ids` into `targets` (0 = exact, untouched blocks
     included)."""
+    src = np.arange(layers.shape.num_blocks, dtype=np.uint64)
+    src[np.asarray(targets, np.int64)] = np.asarray(ids, np.uint64)
+    return verify_blocks(layers, src)
+
+
+def verify_blocks(layers: DeviceLayers, src_of) -> int:
+    """Mismatching words over every block of every layer: block b must hold
+    the words block src_of[b] was filled with (0 = exact)."""
     shape = layers.shape
     nb, bpb = shape.num_blocks, shape.bytes_per_block
     blocks = np.arange(nb, dtype=np.uint64)
-    src = blocks.copy()
-    src[np.asarray(targets, np.int64)] = np.asarray(ids, np.uint64)
+    src = np.asarray(src_of, np.uint64)
+    if src.shape != (nb,):
+        raise ValueError("src_of needs one entry per block")
     bad = 0
     for l, buf in enumerate(layers.bufs):
         if shape.segments == 2:
@@ -165,5 +248,6 @@ def payload_bytes(regs, n_blocks: int) -> int:
 
 
 __all__ = ["KVShape", "GPT2", "LLAMA3_8B", "LLAMA3_8B_TP8_RANK", "QWEN3_8B", "MLA_BF16", "MLA_FP8", "draw_blocks",
+           "draw_runs", "run_count", "fragmentation_requests",
            "DeviceLayers", "save_plan", "load_plan", "verify_saved", "verify_restored",
-           "layer_seed", "payload_bytes", "MiB", "_lib"]
+           "verify_blocks", "layer_seed", "payload_bytes", "MiB", "_lib"]

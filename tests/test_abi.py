@@ -286,6 +286,37 @@ def test_load_state_event_block_layout():
         PyLoadState(num_layers=3, layer_events=handles[:2])
 
 
+def test_load_state_local_event_block_layout():
+    """The in-process variant of the event block: {'PFLL', count,
+    events_recorded} at byte 48, then per layer a 64-byte slot holding the
+    event's address and zeros; an attacher sees it as local."""
+    from types import SimpleNamespace
+
+    from pegaflow_amd.load_state import LoadState, PyLoadState
+
+    evs = [SimpleNamespace(handle=0x7F0000001000 + 0x40 * i) for i in range(3)]
+    p = PyLoadState(num_layers=3, layer_events=evs)
+    raw = open("/dev/shm/" + p.shm_name(), "rb").read()
+    assert len(raw) == 64 + 3 * 64
+    assert struct.unpack_from("<IIq", raw, 32) == (0x50464C58, 3, 0)
+    assert struct.unpack_from("<IIq", raw, 48) == (0x50464C4C, 3, 0)
+    for i, e in enumerate(evs):
+        slot = raw[64 + 64 * i: 128 + 64 * i]
+        assert struct.unpack_from("<Q", slot)[0] == e.handle and slot[8:] == bytes(56)
+    srv = LoadState.attach(p.shm_name())
+    assert srv.events_local() and p.inner.events_local()
+    assert len(srv.event_handles()) == 3
+    srv.set_events_recorded(3)
+    calls = []
+    assert p.wait_for_layer_on_device(1, calls.append) and calls == [1]
+    srv.close()
+    # An IPC event block is not local; a null event is refused.
+    q = PyLoadState(num_layers=1, layer_events=[b"\x01" * 64])
+    assert not LoadState.attach(q.shm_name()).events_local()
+    with pytest.raises(_lib.PegaFlowError, match="null event for layer 1"):
+        PyLoadState(num_layers=2, layer_events=[evs[0], SimpleNamespace(handle=0)])
+
+
 def _words_record(kind, value, address=0, alloc_size=0, offset=0, handle=b""):
     w = _lib.LayerWords()
     w.kind, w.value, w.address, w.alloc_size, w.offset = kind, value, address, alloc_size, offset
@@ -347,3 +378,86 @@ def test_load_state_words_block_layout():
 def test_load_state_words_block_rejects(rec, n):
     with pytest.raises(_lib.PegaFlowError):
         LoadState.new(n, None, _words_record(**rec))
+
+
+# ---------------------------------------------------------------------------
+# The transfer.rs primitives' error paths, which return before any HIP call.
+# ---------------------------------------------------------------------------
+def _last_error():
+    return _lib.load().pf_last_error().decode()
+
+
+def test_copy_primitives_buffer_too_small():
+    """copy_cpu_to_gpu_async refuses a CPU buffer shorter than the copy with
+    the reference's message (transfer.rs:89-95); copy_gpu_to_cpu does too."""
+    lib = _lib.load()
+    buf = (ctypes.c_uint8 * 100)()
+    rc = lib.pf_copy_cpu_to_gpu_async(0x1000, 0, ctypes.addressof(buf), 100, 101, None)
+    assert rc == _lib.PF_ERR_STORAGE
+    assert _last_error() == "CPU buffer too small: 100 bytes, need 101 bytes"
+    rc = lib.pf_copy_gpu_to_cpu(0x1000, 64, ctypes.addressof(buf), 99, 100)
+    assert rc == _lib.PF_ERR_STORAGE
+    assert _last_error() == "CPU buffer too small: 99 bytes, need 100 bytes"
+    rc = lib.pf_copy_cpu_to_gpu_async(0x1000, 0, None, 0, 16, None)
+    assert rc == _lib.PF_ERR_INVALID_ARGUMENT and _last_error() == "null CPU buffer"
+
+
+def test_batch_copy_segments_argument_errors():
+    lib = _lib.load()
+    pu = ctypes.POINTER(ctypes.c_uint64)
+    g = (ctypes.c_uint64 * 2)(0, 64)
+    c = (ctypes.c_uint64 * 2)(0x10000, 0x10040)
+    out = ctypes.c_uint64(7)
+    rc = lib.pf_batch_copy_segments_to_gpu(ctypes.cast(g, pu), ctypes.cast(c, pu), 2, 64, None,
+                                           None, ctypes.byref(out))
+    assert rc == _lib.PF_ERR_INVALID_ARGUMENT and _last_error() == "null layout"
+    assert out.value == 0
+    reg = _reg(0x100000, 1 << 20, 64, 4096, 64 * 4096 // 2, 2).to_c()
+    rc = lib.pf_batch_copy_segments_to_gpu(None, None, 2, 64, ctypes.byref(reg), None,
+                                           ctypes.byref(out))
+    assert rc == _lib.PF_ERR_INVALID_ARGUMENT and _last_error() == "null transfer list"
+    # An empty list issues nothing (transfer.rs:122-126).
+    rc = lib.pf_batch_copy_segments_to_gpu(None, None, 0, 64, ctypes.byref(reg), None,
+                                           ctypes.byref(out))
+    assert rc == _lib.PF_OK and out.value == 0
+    # segment_size * run length overflowing is the reference's error.
+    big = (ctypes.c_uint64 * 2)(0, 1 << 63)
+    bigc = (ctypes.c_uint64 * 2)(0x10000, 0x10000 + (1 << 63))
+    rc = lib.pf_batch_copy_segments_to_gpu(ctypes.cast(big, pu), ctypes.cast(bigc, pu), 2,
+                                           1 << 63, ctypes.byref(reg), None, ctypes.byref(out))
+    assert rc == _lib.PF_ERR_STORAGE
+    assert _last_error() == "batch_copy_segments_to_gpu: total_size overflow"
+
+
+def test_copy_block_gpu_to_cpu_errors_from_segment_offset():
+    """copy_block_gpu_to_cpu passes segment_offset's errors up unchanged
+    (transfer.rs:207, 227), for contiguous and strided layouts; a contiguous
+    whole block past the tensor gets the same offset/size/limit detail."""
+    lib = _lib.load()
+    dst = (ctypes.c_uint8 * 8192)()
+    # Split KV-first layout (not contiguous): block 128's first segment
+    # already starts at the end of the tensor.
+    split = _reg(0x100000, 2 * 64 * 4096, 64, 4096, 64 * 4096, 2)
+    rc = lib.pf_copy_block_gpu_to_cpu(ctypes.byref(split.to_c()), 128, ctypes.addressof(dst))
+    assert rc == _lib.PF_ERR_STORAGE
+    assert _last_error() == ("Block 128 segment 0 exceeds registered memory "
+                             "(offset 524288, size 4096, limit 524288)")
+    # Single-segment (contiguous) layout.
+    single = _reg(0x100000, 10 * 4096, 10, 4096, 0, 1)
+    rc = lib.pf_copy_block_gpu_to_cpu(ctypes.byref(single.to_c()), 10, ctypes.addressof(dst))
+    assert rc == _lib.PF_ERR_STORAGE
+    assert _last_error() == ("Block 10 segment 0 exceeds registered memory "
+                             "(offset 40960, size 4096, limit 40960)")
+    # Contiguous two-segment layout (kv_stride == bytes_per_block) at the
+    # smallest size validation accepts, (num_blocks + 1) segments: block 10's
+    # first segment passes segment_offset, its whole block does not fit.
+    contig2 = _reg(0x100000, 11 * 4096, 10, 4096, 4096, 2)
+    assert is_contiguous_layout(contig2)
+    assert segment_offset(contig2, 10, 0) == 40960
+    rc = lib.pf_copy_block_gpu_to_cpu(ctypes.byref(contig2.to_c()), 10, ctypes.addressof(dst))
+    assert rc == _lib.PF_ERR_STORAGE
+    assert _last_error() == ("Block 10 exceeds registered memory "
+                             "(offset 40960, size 8192, limit 45056)")
+    rc = lib.pf_copy_block_gpu_to_cpu(None, 0, ctypes.addressof(dst))
+    assert rc == _lib.PF_ERR_INVALID_ARGUMENT and _last_error() == "null layout"
+    assert lib.pf_layout_kind(None) == -1

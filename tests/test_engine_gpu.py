@@ -141,6 +141,59 @@ def test_seal_visibility_dedup_and_prefix(engine):
     m.close()
 
 
+def _expect_per_layer(model, orig, pairs_per_layer):
+    """Oracle: for each layer, save the listed source blocks and load them
+    into the listed targets (pairs_per_layer[l] = (sources, targets))."""
+    out = []
+    for l, ref in enumerate(orig):
+        src, dst = pairs_per_layer[l]
+        out.append(expected_after_load(model, [ref], src, dst)[0])
+    return out
+
+
+def test_duplicate_hash_in_one_save_keeps_first(engine):
+    """One save batch names a hash twice with different blocks.  Both are
+    copied, the first occurrence fills the slot and the second is dropped
+    (lib.rs:590-621; storage.rs:182, 466-471): the whole-batch path."""
+    say("[gpu] engine duplicate hash in one save (whole batch)")
+    m = Model(engine, "dup", 4, 32, 2048, seed=12)
+    orig = m.host_copies()
+    ids, hashes = [3, 7, 12], [h(1), h(2), h(1)]
+    engine.batch_save_kv_blocks("dup", 0, 0, [(n, ids, hashes) for n in m.names])
+    s = engine.stats()
+    assert s["sealed_blocks"] == 2 and s["inflight_blocks"] == 0
+    st = PyLoadState()
+    engine.batch_load_kv_blocks("dup", 0, 0, st.shm_name(), m.names, [20, 21], [h(1), h(2)])
+    assert wait(st) == 1
+    exp = _expect_per_layer(m, orig, [([3, 7], [20, 21])] * m.n_layers)
+    for l in range(m.n_layers):
+        assert np.array_equal(m.bufs[l].download(), exp[l]), f"layer {l}"
+    m.close()
+
+
+def test_duplicate_hash_slot_by_slot_keeps_first(engine):
+    """The same rule when an earlier call left the block partly in flight,
+    which sends the batch through the slot-by-slot path: layer 0's slot
+    keeps the earlier call's block, the other layers the first occurrence."""
+    say("[gpu] engine duplicate hash in one save (slot by slot)")
+    m = Model(engine, "dup2", 4, 32, 2048, seed=13)
+    orig = m.host_copies()
+    engine.batch_save_kv_blocks("dup2", 0, 0, [(m.names[0], [5], [h(1)])])
+    assert engine.stats()["inflight_blocks"] == 1
+    ids, hashes = [3, 7, 12], [h(1), h(2), h(1)]
+    engine.batch_save_kv_blocks("dup2", 0, 0, [(n, ids, hashes) for n in m.names])
+    s = engine.stats()
+    assert s["sealed_blocks"] == 2 and s["inflight_blocks"] == 0
+    st = PyLoadState(num_layers=m.n_layers)
+    engine.batch_load_kv_blocks("dup2", 0, 0, st.shm_name(), m.names, [20, 21], [h(1), h(2)])
+    assert wait(st) == 1
+    exp = _expect_per_layer(m, orig, [([5, 7], [20, 21])] +
+                            [([3, 7], [20, 21])] * (m.n_layers - 1))
+    for l in range(m.n_layers):
+        assert np.array_equal(m.bufs[l].download(), exp[l]), f"layer {l}"
+    m.close()
+
+
 def test_load_missing_hash_fails_whole_call(engine):
     say("[gpu] engine load with a missing hash")
     m = Model(engine, "inst", 2, 16, 1024)
