@@ -170,3 +170,25 @@ def test_loads_complete_and_layers_can_be_awaited():
     assert w.get_finished(set()) == (None, {"r3"})
     assert w.start_load_kv(ConnectorMetadata()) is None
     w.shutdown()
+
+
+def test_request_reopened_by_later_saves_waits_for_them():
+    """A request whose first step's saves completed, then saves again in a
+    later step, is sent only once those later saves are processed, also when
+    the scheduler reports it finished in between."""
+    c = RecordingClient()
+    w = make(c, num_layers=2)
+    w.register_kv_caches({f"l{i}": kv_first(0x1000 * (i + 1)) for i in range(2)})
+    meta = ConnectorMetadata(save_intents={"r": SaveIntent((1,), (b"a",))})
+    for name in ("l0", "l1"):
+        w.save_kv_layer(meta, name)
+    w.drain_saves()
+    meta2 = ConnectorMetadata(save_intents={"r": SaveIntent((2,), (b"b",))})
+    w.save_kv_layer(meta2, "l0")
+    w.drain_saves()
+    assert w.get_finished({"r"}) == (None, None)  # layer l1 of the second step pending
+    w.save_kv_layer(meta2, "l1")
+    w.drain_saves()
+    assert w.get_finished(set()) == ({"r"}, None)  # finished earlier, now saved
+    assert w.get_finished({"r"}) == (None, None)  # reported once
+    w.shutdown()

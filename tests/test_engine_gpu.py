@@ -389,3 +389,56 @@ def test_device_words_gate_consumer_per_layer(engine):
         flag.close()
         words.close()
         m.close()
+
+
+def test_local_layer_events_gate_consumer_per_layer(engine):
+    """The engine's per-layer-event branch run in one process: the consumer
+    puts one of its own events per layer in the LoadState (the in-process
+    variant of the interprocess event block).  The load thread issues one
+    launch per layer, records layer l's event after it, publishes
+    events_recorded once every record is queued, then layers_done as the
+    events fire.  A consumer stream waits on each event and snapshots its
+    layer at once; every snapshot must hold the restored bytes.  The same
+    events serve a second load; a failed load ends without a device wait."""
+    from pegaflow_amd.runtime import Event, Stream, memcpy_async
+
+    say("[gpu] engine local layer events: device-side per-layer gating")
+    engine.set_transfer_modes(_lib.MODE_KERNEL, _lib.MODE_KERNEL)
+    m = Model(engine, "levents", 8, 256, 32768, seed=37)
+    evs = [Event() for _ in range(m.n_layers)]
+    snaps = [DeviceBuffer(m.size) for _ in range(m.n_layers)]
+    stream = Stream()
+    try:
+        orig = m.host_copies()
+        ids = list(range(1, 161, 2))
+        hashes = [h(i, b"levents") for i in ids]
+        engine.batch_save_kv_blocks("levents", 0, 0, [(n, ids, hashes) for n in m.names])
+        targets = list(range(254, 94, -2))
+        exp = expected_after_load(m, orig, ids, targets)
+        for rnd in range(2):
+            for l, b in enumerate(m.bufs):
+                b.fill_random(m.seeds[l])
+            st = PyLoadState(num_layers=m.n_layers, layer_events=evs)
+            assert st.inner.events_local()
+            engine.batch_load_kv_blocks("levents", 0, 0, st.shm_name(), m.names, targets,
+                                        hashes)
+            for l in range(m.n_layers):
+                assert st.wait_for_layer_on_device(l, lambda i: stream.wait_event(evs[i]))
+                memcpy_async(snaps[l].ptr, m.bufs[l].ptr, m.size, stream)
+            stream.synchronize()
+            assert wait(st) == 1
+            assert st.events_recorded() and st.layers_done() == m.n_layers
+            for l in range(m.n_layers):
+                assert np.array_equal(snaps[l].download(), exp[l]), f"round {rnd} layer {l}"
+        # An unknown hash fails the call before any record: no device wait.
+        st = PyLoadState(num_layers=m.n_layers, layer_events=evs)
+        with pytest.raises(_lib.PegaFlowError):
+            engine.batch_load_kv_blocks("levents", 0, 0, st.shm_name(), m.names, targets[:2],
+                                        [hashes[0], h(10**6, b"levents")])
+        calls = []
+        assert not st.wait_for_layer_on_device(0, calls.append) and calls == []
+    finally:
+        stream.close()
+        for s in snaps:
+            s.close()
+        m.close()
