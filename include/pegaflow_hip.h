@@ -356,6 +356,26 @@ int pf_save_layers(pf_xfer* xfer, const pf_layer_xfer* layers,
 int pf_load_layers(pf_xfer* xfer, const pf_layer_xfer* layers,
                    uint32_t num_layers, uint32_t mode, pf_event* layer_events);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory: code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc.  pf_load_layers in PF_MODE_KERNEL without events, with
+ * the same bytes, issued on the caller's stream (NULL: the current device's
+ * null stream) instead of a transfer context's.  The chunk descriptors and
+ * the tile queue live in a static device array of the library (one copy per
+ * device, 256 B + PF_NOALLOC_MAX_CHUNKS x 16 B = 1 MiB + 256 B, held until
+ * the process ends); nothing is allocated on the device or in pinned memory.
+ * A call of more than PF_NOALLOC_MAX_CHUNKS chunks (segments, or whole
+ * blocks for single-segment layouts, summed over layers) fails with
+ * PF_ERR_INVALID_ARGUMENT before anything is issued.  Asynchronous: returns
+ * after issuing; stream order serialises calls on one stream, and the array
+ * keeps the last call's descriptors.  Calls on one device that overlap on
+ * different streams race on the shared array: the caller orders them.
+ * Layers whose copies must run in list order use async DMA copies on the
+ * stream, as pf_load_layers does. */
+#define PF_NOALLOC_MAX_CHUNKS 65536
+int pf_load_layers_noalloc(pf_stream stream, const pf_layer_xfer* layers,
+                           uint32_t num_layers);
+
 /* Layer marks: per-layer completion written by the load itself.  No
  * counterpart in the reference (its per-layer wait is a no-op,
  * worker.py:288-289; its load syncs once after all layers,

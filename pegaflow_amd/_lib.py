@@ -56,6 +56,8 @@ MODE_NAMES = {
 LAYOUT_SPLIT, LAYOUT_CONTIGUOUS, LAYOUT_STRIDED = 0, 1, 2
 
 # Pinned allocation flags.
+# Chunks one pf_load_layers_noalloc call may plan (its static scratch).
+NOALLOC_MAX_CHUNKS = 65536
 PINNED_DEFAULT = 0
 PINNED_COHERENT = 1
 PINNED_NONCOHERENT = 2
@@ -256,6 +258,7 @@ SIGNATURES = {
     "pf_xfer_last_kernel_ms": (i32, [vp, ctypes.POINTER(ctypes.c_float), pu64]),
     "pf_save_layers": (i32, [vp, ctypes.POINTER(LayerXfer), u32, u32]),
     "pf_load_layers": (i32, [vp, ctypes.POINTER(LayerXfer), u32, u32, pvp]),
+    "pf_load_layers_noalloc": (i32, [vp, ctypes.POINTER(LayerXfer), u32]),
     "pf_load_layers_marked": (i32, [vp, ctypes.POINTER(LayerXfer), u32, u32,
                                     ctypes.POINTER(LayerSignal), u32]),
     "pf_stream_wait_word": (i32, [vp, u64, u64, u32, u64]),

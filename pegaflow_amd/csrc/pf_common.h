@@ -4,6 +4,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <cstdint>
+#include <mutex>
 #include <string>
 #include <utility>
 #include <vector>
@@ -131,6 +132,22 @@ inline int layout_kind(const pf_kv_layout& l) {
 // segment_offset with the reference's checks; message set on failure.
 int segment_offset(const pf_kv_layout& l, uint64_t block, uint64_t seg,
                    uint64_t* out);
+
+// Static device scratch of pf_load_layers_noalloc (one copy per device,
+// held until the process ends): the tile queue's counter in the first 256
+// bytes, then up to PF_NOALLOC_MAX_CHUNKS chunk descriptors.
+constexpr uint64_t kNoAllocQueueBytes = 256;
+constexpr uint64_t kNoAllocScratchBytes =
+    kNoAllocQueueBytes + PF_NOALLOC_MAX_CHUNKS * sizeof(ChunkDesc);
+struct NoAllocScratch {
+  uint64_t base = 0;        // device address of the device's copy of the array
+  uint32_t next_base = 0;   // where the tile counter stands after the last launch
+  std::mutex mu;            // host-side bookkeeping of calls on this device
+};
+// The device's scratch.  The array's address is looked up once per device,
+// with that device current (pf_init does it; a first call on a device that
+// pf_init never saw does it then).
+int noalloc_scratch(int device, NoAllocScratch** out);
 
 // pf_save_layers without its final wait: the copy may still be in flight on
 // the context's stream when this returns; pf_xfer_synchronize completes it.

@@ -6,10 +6,13 @@
 #include <cstring>
 #include <fstream>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <sstream>
 #include <string>
 #include <thread>
+
+#include <hip/hip_runtime.h>
 
 #include "pf_common.h"
 
@@ -135,6 +138,42 @@ static int wall_clock_khz() {
   return khz;
 }
 
+// ---------------------------------------------------------------------------
+// Static device scratch of pf_load_layers_noalloc.  Host code never uses the
+// array's name as an address (in host code it names a host-side stand-in):
+// hipGetSymbolAddress gives each device's own copy, and that address is what
+// the entry point hands to copies and kernels.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+static std::mutex g_scratch_mu;
+static std::map<int, std::unique_ptr<NoAllocScratch>> g_scratch;
+
+int noalloc_scratch(int device, NoAllocScratch** out) {
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  auto it = g_scratch.find(device);
+  if (it != g_scratch.end()) {
+    *out = it->second.get();
+    return PF_OK;
+  }
+  int prev = 0;
+  PF_HIP(hipGetDevice(&prev));
+  if (prev != device) PF_HIP(hipSetDevice(device));
+  void* ptr = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (prev != device) (void)hipSetDevice(prev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+  if (!ptr) return fail(PF_ERR_INIT, "no device address for the scratch array");
+  auto sc = std::make_unique<NoAllocScratch>();
+  sc->base = reinterpret_cast<uint64_t>(ptr);
+  // The array is zero when the code object is loaded: the tile counter
+  // starts at 0, and every launch advances it by a count the host tracks.
+  sc->next_base = 0;
+  *out = sc.get();
+  g_scratch.emplace(device, std::move(sc));
+  return PF_OK;
+}
+
 }  // namespace pf
 
 using namespace pf;
@@ -156,7 +195,8 @@ int pf_init(int device) {
   PF_HIP(hipSetDevice(device));
   if (wall_clock_khz() <= 0)
     return fail(PF_ERR_INIT, "hipDeviceAttributeWallClockRate unavailable");
-  return PF_OK;
+  NoAllocScratch* sc = nullptr;
+  return noalloc_scratch(device, &sc);
 }
 
 int pf_set_device(int device) {

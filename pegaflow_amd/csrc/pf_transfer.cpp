@@ -421,13 +421,52 @@ ChunkDesc* small_desc(pf_xfer* x, size_t n) {
   return x->h_small;
 }
 
+// One gather/scatter launch of the n chunks at descs on `stream`.  With
+// qgrid > 0 (16-byte aligned chunks only) it runs queued: qgrid persistent
+// workgroups pull tiles from the counter at `next`, which holds *next_base
+// when the launch starts; *next_base is advanced past the launch.  Otherwise
+// one workgroup per tile (at most max_grid workgroups, 0 = no cap).
+hipError_t issue_copy(hipStream_t stream, const ChunkDesc* descs, size_t n, uint64_t chunk_bytes,
+                      bool al16, uint32_t threads, uint32_t unroll, uint32_t qgrid,
+                      uint32_t max_grid, const LayerMarks* marks, uint32_t* next,
+                      uint32_t* next_base) {
+  (void)hipGetLastError();
+  if (!(al16 && qgrid > 0))
+    return launch_copy_chunks(descs, static_cast<uint32_t>(n), chunk_bytes, al16, threads, unroll,
+                              max_grid, stream);
+  // Chunks smaller than a tile (e.g. 4 KiB segments of one tensor-parallel
+  // rank) get workgroups sized to the chunk, and proportionally more of
+  // them, so each pull moves a whole chunk with every lane busy and the
+  // bytes in flight stay the same (measured: 4 KiB-segment save 53.9 ->
+  // 55.6 GB/s).
+  const uint64_t u = unroll & 0xffu;
+  const uint64_t want = ((chunk_bytes / 16 + u - 1) / u + 63) / 64 * 64;
+  if (u > 0 && want < threads) {
+    const uint32_t t2 = static_cast<uint32_t>(want < 64 ? 64 : want);
+    const uint64_t g2 = static_cast<uint64_t>(qgrid) * threads / t2;
+    qgrid = static_cast<uint32_t>(g2 < (1u << 16) ? g2 : (1u << 16));
+    if (max_grid && qgrid > max_grid) qgrid = max_grid;
+    threads = t2;
+  }
+  uint32_t n_tiles = 0;
+  const hipError_t e =
+      launch_copy_chunks_queue(descs, static_cast<uint32_t>(n), chunk_bytes, threads, unroll,
+                               qgrid, marks, next, *next_base, &n_tiles, stream);
+  if (e == hipSuccess) *next_base += n_tiles + qgrid;
+  return e;
+}
+
+int check_launch_size(size_t n, uint64_t chunk_bytes) {
+  if (n > 0xffffffffull) return fail(PF_ERR_INVALID_ARGUMENT, "too many chunks");
+  if (chunk_bytes / 16 >= (1ull << 31)) return fail(PF_ERR_INVALID_ARGUMENT, "chunk too large");
+  return PF_OK;
+}
+
 int launch(pf_xfer* x, size_t first, size_t n, uint64_t chunk_bytes, bool al16, bool is_save,
            bool host_side = false, const LayerMarks* marks = nullptr) {
   if (n == 0) return PF_OK;
   const int dir = (is_save ? PF_ROUTE_SAVE_DEVICE : PF_ROUTE_LOAD_DEVICE) + (host_side ? 2 : 0);
-  if (n > 0xffffffffull) return fail(PF_ERR_INVALID_ARGUMENT, "too many chunks");
-  if (chunk_bytes / 16 >= (1ull << 31))
-    return fail(PF_ERR_INVALID_ARGUMENT, "chunk too large");
+  if (int rc = check_launch_size(n, chunk_bytes)) return rc;
   std::pair<hipEvent_t, hipEvent_t>* tm = nullptr;
   if (x->timing) {
     if (x->last_kernels >= x->timers.size()) {
@@ -444,36 +483,13 @@ int launch(pf_xfer* x, size_t first, size_t n, uint64_t chunk_bytes, bool al16, 
   uint32_t qgrid = x->grid[dir];
   if (marks && qgrid == 0) qgrid = PF_LOAD_HOST_DEFAULT_GRID;
   if (x->max_grid && qgrid > x->max_grid) qgrid = x->max_grid;
-  (void)hipGetLastError();
-  hipError_t e = hipSuccess;
-  if (al16 && qgrid > 0) {
-    if (!x->d_next) return fail(PF_ERR_INVALID_ARGUMENT, "tile queue not allocated");
-    // Chunks smaller than a tile (e.g. 4 KiB segments of one tensor-parallel
-    // rank) get workgroups sized to the chunk, and proportionally more of
-    // them, so each pull moves a whole chunk with every lane busy and the
-    // bytes in flight stay the same (measured: 4 KiB-segment save 53.9 ->
-    // 55.6 GB/s).
-    uint32_t threads = x->threads[dir];
-    const uint64_t u = x->unroll[dir] & 0xffu;
-    const uint64_t want = ((chunk_bytes / 16 + u - 1) / u + 63) / 64 * 64;
-    if (u > 0 && want < threads) {
-      const uint32_t t2 = static_cast<uint32_t>(want < 64 ? 64 : want);
-      const uint64_t g2 = static_cast<uint64_t>(qgrid) * threads / t2;
-      qgrid = static_cast<uint32_t>(g2 < (1u << 16) ? g2 : (1u << 16));
-      if (x->max_grid && qgrid > x->max_grid) qgrid = x->max_grid;
-      threads = t2;
-    }
-    uint32_t n_tiles = 0;
-    e = launch_copy_chunks_queue(x->desc_base + first, static_cast<uint32_t>(n), chunk_bytes,
-                                 threads, x->unroll[dir], qgrid, marks, x->d_next,
-                                 x->next_base, &n_tiles, x->stream);
-    if (e == hipSuccess) x->next_base += n_tiles + qgrid;
-  } else if (marks) {
+  if (al16 && qgrid > 0 && !x->d_next)
+    return fail(PF_ERR_INVALID_ARGUMENT, "tile queue not allocated");
+  if (marks && !(al16 && qgrid > 0))
     return fail(PF_ERR_INVALID_ARGUMENT, "a marking launch needs 16-byte aligned chunks");
-  } else {
-    e = launch_copy_chunks(x->desc_base + first, static_cast<uint32_t>(n), chunk_bytes, al16,
-                           x->threads[dir], x->unroll[dir], x->max_grid, x->stream);
-  }
+  const hipError_t e = issue_copy(x->stream, x->desc_base + first, n, chunk_bytes, al16,
+                                  x->threads[dir], x->unroll[dir], qgrid, x->max_grid, marks,
+                                  x->d_next, &x->next_base);
   if (e != hipSuccess) return hip_fail(e, "gather/scatter kernel launch");
   if (tm) PF_HIP(hipEventRecord(tm->second, x->stream));
   x->last_kernels++;
@@ -555,7 +571,10 @@ bool chunks_aligned(const LayerPlan& p) {
 }
 
 // ---- DMA modes ------------------------------------------------------------
-int dma_layer(pf_xfer* x, const LayerPlan& p, bool is_save, bool per_chunk_sync) {
+// The copies of one layer as DMA calls on `stream`, in list order; *issued
+// counts them.
+int dma_copies(hipStream_t stream, const LayerPlan& p, bool is_save, bool per_chunk_sync,
+               uint64_t* issued) {
   hipError_t e = hipSuccess;
   auto issue = [&](size_t i, size_t n) {
     if (e != hipSuccess) return;
@@ -563,12 +582,12 @@ int dma_layer(pf_xfer* x, const LayerPlan& p, bool is_save, bool per_chunk_sync)
     const uint64_t bytes = n * p.chunk_bytes;
     if (is_save)
       e = hipMemcpyAsync(reinterpret_cast<void*>(c.host), reinterpret_cast<void*>(c.dev),
-                         bytes, hipMemcpyDefault, x->stream);
+                         bytes, hipMemcpyDefault, stream);
     else
       e = hipMemcpyAsync(reinterpret_cast<void*>(c.dev), reinterpret_cast<void*>(c.host),
-                         bytes, hipMemcpyDefault, x->stream);
-    if (e == hipSuccess && per_chunk_sync) e = hipStreamSynchronize(x->stream);
-    x->last_dma++;
+                         bytes, hipMemcpyDefault, stream);
+    if (e == hipSuccess && per_chunk_sync) e = hipStreamSynchronize(stream);
+    ++*issued;
   };
   if (per_chunk_sync) {
     // gpu_worker.rs:344-371: one synchronous copy per segment, no merging.
@@ -580,6 +599,10 @@ int dma_layer(pf_xfer* x, const LayerPlan& p, bool is_save, bool per_chunk_sync)
   if (e != hipSuccess)
     return hip_fail(e, is_save ? "hipMemcpyDtoH" : "hipMemcpyHtoDAsync");
   return PF_OK;
+}
+
+int dma_layer(pf_xfer* x, const LayerPlan& p, bool is_save, bool per_chunk_sync) {
+  return dma_copies(x->stream, p, is_save, per_chunk_sync, &x->last_dma);
 }
 
 // ---- staged mode ----------------------------------------------------------
@@ -1104,6 +1127,106 @@ int pf_copy_block_gpu_to_cpu(const pf_kv_layout* layout, uint64_t block_idx, voi
       return rc;
   }
   return PF_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Loads that allocate nothing: the plan of pf_load_layers in PF_MODE_KERNEL,
+// with its descriptors and tile queue in the library's static device scratch
+// (pf_runtime.cpp) and its work on the caller's stream.
+// ---------------------------------------------------------------------------
+int pf_load_layers_noalloc(pf_stream stream, const pf_layer_xfer* layers, uint32_t num_layers) {
+  if (num_layers > 0 && !layers) return fail(PF_ERR_INVALID_ARGUMENT, "null layer list");
+  // Chunks the call plans (duplicates included): two per block of a split
+  // layer, one per block otherwise.  Checked before planning, so nothing is
+  // issued and the planning buffers below stay bounded.
+  uint64_t planned = 0;
+  for (uint32_t i = 0; i < num_layers; ++i)
+    planned += layers[i].num_blocks * (layout_kind(layers[i].layout) == PF_LAYOUT_SPLIT ? 2 : 1);
+  if (planned > PF_NOALLOC_MAX_CHUNKS)
+    return fail(PF_ERR_INVALID_ARGUMENT,
+                strf("pf_load_layers_noalloc: %llu chunks exceed the %u-chunk scratch",
+                     (unsigned long long)planned, (unsigned)PF_NOALLOC_MAX_CHUNKS));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int dev = 0;
+  if (s) PF_HIP(hipStreamGetDevice(s, &dev));
+  else PF_HIP(hipGetDevice(&dev));
+  NoAllocScratch* sc = nullptr;
+  if (int rc = noalloc_scratch(dev, &sc)) return rc;
+  // Host-side planning buffers, kept by the thread for its later calls.
+  thread_local std::vector<LayerPlan> plans;
+  thread_local std::vector<ChunkDesc> descs;
+  if (plans.size() < num_layers) plans.resize(num_layers);
+  size_t total = 0;
+  RangeCache ranges;
+  for (uint32_t i = 0; i < num_layers; ++i) {
+    LayerPlan& p = plans[i];
+    if (int rc = plan_layer(layers[i], false, &p)) return rc;
+    apply_write_policy(layers[i], false, false, &p);
+    if (p.chunks.empty() || p.ordered) continue;
+    if (int rc = check_device_tensor(ranges, layers[i].layout)) return rc;
+    if (int rc = check_host_chunks(ranges, p)) return rc;
+    total += p.chunks.size();
+  }
+  descs.resize(total);
+  size_t d = 0;
+  for (uint32_t i = 0; i < num_layers; ++i)
+    if (!plans[i].ordered)
+      for (const Chunk& c : plans[i].chunks) descs[d++] = ChunkDesc{c.host, c.dev};
+
+  std::lock_guard<std::mutex> lk(sc->mu);
+  int prev = 0;
+  PF_HIP(hipGetDevice(&prev));
+  if (prev != dev) PF_HIP(hipSetDevice(dev));
+  ChunkDesc* d_desc = reinterpret_cast<ChunkDesc*>(sc->base + kNoAllocQueueBytes);
+  uint32_t* next = reinterpret_cast<uint32_t*>(sc->base);
+  auto issue = [&]() -> int {
+    // A pageable source: the call returns once the bytes have been taken,
+    // so the thread's buffer may be refilled by its next call.
+    if (total > 0)
+      PF_HIP(hipMemcpyAsync(d_desc, descs.data(), total * sizeof(ChunkDesc),
+                            hipMemcpyHostToDevice, s));
+    size_t first = 0;
+    uint64_t dma = 0;
+    for (uint32_t li = 0; li < num_layers;) {
+      const LayerPlan& p = plans[li];
+      if (p.ordered) {
+        if (int rc = dma_copies(s, p, false, false, &dma)) return rc;
+        ++li;
+        continue;
+      }
+      if (p.chunks.empty()) {
+        ++li;
+        continue;
+      }
+      // Consecutive layers of the same chunk size and alignment share one
+      // launch, whose shape follows its first layer's host side.
+      const bool al = chunks_aligned(p);
+      size_t n = p.chunks.size();
+      uint32_t lj = li + 1;
+      while (lj < num_layers && !plans[lj].ordered &&
+             (plans[lj].chunks.empty() ||
+              (plans[lj].chunk_bytes == p.chunk_bytes && chunks_aligned(plans[lj]) == al))) {
+        n += plans[lj].chunks.size();
+        ++lj;
+      }
+      const bool host = host_side_pinned(p);
+      if (int rc = check_launch_size(n, p.chunk_bytes)) return rc;
+      const hipError_t e = issue_copy(
+          s, d_desc + first, n, p.chunk_bytes, al,
+          host ? PF_LOAD_HOST_DEFAULT_THREADS : PF_LOAD_DEFAULT_THREADS,
+          host ? PF_LOAD_HOST_DEFAULT_UNROLL : PF_LOAD_DEFAULT_UNROLL,
+          host ? PF_LOAD_HOST_DEFAULT_GRID : 0, 0, nullptr, next, &sc->next_base);
+      if (e != hipSuccess) return hip_fail(e, "gather/scatter kernel launch");
+      first += n;
+      li = lj;
+    }
+    return PF_OK;
+  };
+  const int rc = issue();
+  // A call that failed part-way leaves nothing in flight.
+  if (rc != PF_OK) (void)hipStreamSynchronize(s);
+  if (prev != dev) (void)hipSetDevice(prev);
+  return rc;
 }
 
 // ---------------------------------------------------------------------------

@@ -180,6 +180,16 @@ def _layer_array(layers: Sequence[LayerTransfer]):
     return arr, keep
 
 
+def load_layers_noalloc(layers: Sequence[LayerTransfer], stream: Stream | None = None) -> None:
+    """pf_load_layers_noalloc: the kernel-mode load of ``layers`` on ``stream``
+    (the current device's null stream when None) with no device allocation;
+    asynchronous.  At most ``_lib.NOALLOC_MAX_CHUNKS`` chunks per call."""
+    arr, keep = _layer_array(layers)
+    check(lib().pf_load_layers_noalloc(stream.handle if stream is not None else None, arr,
+                                       len(layers)), "load_layers_noalloc")
+    del keep
+
+
 class TransferContext:
     """A pf_xfer: per-worker streams, descriptor buffers and staging slots."""
 

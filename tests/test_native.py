@@ -24,6 +24,8 @@ LIB_SOURCES = [os.path.join(CSRC, f) for f in (
     "pf_layout.cpp", "pf_runtime.cpp", "pf_kernels.hip", "pf_transfer.cpp", "pf_load_state.cpp",
     "pf_engine.cpp", "pf_disk.cpp")]
 NATIVE = os.path.join(ROOT, "tests", "native")
+# C++ sources that define device variables.
+DEVICE_CPP = {"pf_runtime.cpp"}
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 
 # Host-side sanitizers only: each flag is passed to the host compilation.
@@ -54,9 +56,11 @@ def build(variant: str, main: str = "stress_engine") -> str:
 
     def compile_one(src):
         obj = os.path.join(out, os.path.basename(src) + ".o")
-        # Only the kernel file needs its device code (the link resolves its
-        # fat binary); the others are compiled for the host alone.
-        host_only = [] if src.endswith(".hip") else ["--offload-host-only"]
+        # Only the files with device code (the kernels, and the runtime's
+        # static scratch array) need their device pass (the link resolves
+        # their fat binaries); the others are compiled for the host alone.
+        device = src.endswith(".hip") or os.path.basename(src) in DEVICE_CPP
+        host_only = [] if device else ["--offload-host-only"]
         subprocess.run([HIPCC, *common, *host_only, "-c", src, "-o", obj], check=True,
                        stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
         return obj
