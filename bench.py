@@ -15,14 +15,21 @@ Printed JSON line (stdout):
                    measured host-link peak (best 1 GiB hipMemcpyAsync) and of
                    PCIe Gen5 x16 (63.0 GB/s)
   save_*           HBM -> host save, same figures
-  roofline         the device gather kernel (paged layers -> packed HBM
-                   buffer, all 32 layers in one launch): algorithmic bytes 2P
-                   per launch / its HIP-event-timed duration, vs 8 TB/s; also
-                   the same kernel on a plain contiguous copy of 2P bytes
-                   (plain_copy_gbps) and the gather's fraction of that
+  roofline         the timed step's dominant kernel, the zero-copy save
+                   (paged HBM -> pinned host over the host link): P per call /
+                   its kernel time (HIP events on the context's stream), vs
+                   PCIe Gen5 x16 and vs the measured D2H peak; the restore
+                   kernel beside it; traffic from the committed rocprofv3
+                   summary it names (traffic_source)
+  device_gather    the HBM-bound gather of the staged mode (paged layers ->
+                   packed HBM buffer, all 32 layers in one launch): 2P per
+                   launch / its duration, vs 8 TB/s; also the same kernel on
+                   a plain contiguous copy of 2P bytes and its fraction
+  device_scatter   the staged mode's scatter (packed HBM -> paged layers)
   cpu_baseline     the reference's copy pattern (per-segment save copies,
-                   merged-run restore copies) as host memcpy on this box's
-                   cores, on a bounded sample of the same workload
+                   merged-run restore copies) as host memcpy, one thread per
+                   physical core of the GPU's NUMA node, on a bounded sample
+                   of the same workload, byte-checked
   variants         the same prefix in every transfer mode: the reference's
                    copy pattern (dma_reference), merged-run async copies
                    (dma_batched), the zero-copy kernel and the staged mode
@@ -74,8 +81,15 @@ def parse():
     ap.add_argument("--quick", action="store_true",
                     help="skip the config 3/4/5 legs (layer-wise, fragmentation, MLA) and "
                          "the disk-tier leg")
-    ap.add_argument("--profile-gather", action="store_true",
-                    help="only run the calibration copy and the device gather (PMC passes)")
+    ap.add_argument("--profile", choices=["gather", "scatter", "zerocopy"],
+                    help="only run the calibration copy and one kernel's launches (PMC passes)")
+    ap.add_argument("--profile-gather", action="store_const", const="gather", dest="profile",
+                    help="same as --profile gather")
+    ap.add_argument("--sweep-scatter", action="store_true",
+                    help="also sweep the device scatter's launch shape and chunk order")
+    ap.add_argument("--duplex-study", action="store_true",
+                    help="also time each link direction against a plain DMA copy the other way, "
+                         "and the two queued kernels' grids in duplex")
     ap.add_argument("--cpu-sample-layers", type=int, default=8)
     ap.add_argument("--staging-mib", type=int, default=256)
     ap.add_argument("--seed", type=int, default=0)
@@ -129,6 +143,76 @@ def duplex(xfer_save, xfer_load, saved, loads, mode, reps=5):
         xfer_load.synchronize()
         ts.append(time.perf_counter() - t0)
     return min(ts[1:])
+
+
+def duplex_study(xfer_load, xfer_save, saved, loads, pool, pool2, dev_buf, P, reps=4):
+    """Which direction loses bandwidth when both link directions are busy.
+    Each case runs a save and a restore of P bytes at once and reports the
+    aggregate payload GB/s and each side's own time (HIP events on its
+    stream): the two queued kernels (as the engine's workers run them), each
+    kernel against a plain DMA copy of P contiguous bytes the other way, the
+    two DMA copies, and the kernels with other persistent-grid sizes."""
+    from pegaflow_amd import _lib, runtime
+    from pegaflow_amd.runtime import Event, Stream
+
+    dma = Stream()
+    evs = [Event() for _ in range(4)]
+
+    def kernel_save(s0, s1):
+        s0.record(xfer_save.stream)
+        xfer_save.save_layers(saved, _lib.MODE_KERNEL)
+        s1.record(xfer_save.stream)
+
+    def kernel_restore(s0, s1):
+        s0.record(xfer_load.stream)
+        xfer_load.load_layers(loads, _lib.MODE_KERNEL)
+        s1.record(xfer_load.stream)
+
+    def dma_save(s0, s1):  # device -> pinned host, one contiguous copy
+        s0.record(dma)
+        runtime.memcpy_async(pool2.ptr, dev_buf.ptr, P, dma)
+        s1.record(dma)
+
+    def dma_restore(s0, s1):  # pinned host -> device, one contiguous copy
+        s0.record(dma)
+        runtime.memcpy_async(dev_buf.ptr, pool.ptr, P, dma)
+        s1.record(dma)
+
+    def case(restore, save):
+        best = None
+        for _ in range(reps + 1):
+            t0 = time.perf_counter()
+            restore(evs[0], evs[1])   # asynchronous issue first, as the engine's load thread
+            save(evs[2], evs[3])
+            xfer_load.synchronize()
+            xfer_save.synchronize()
+            dma.synchronize()
+            wall = time.perf_counter() - t0
+            r = (wall, evs[0].elapsed_ms(evs[1]), evs[2].elapsed_ms(evs[3]))
+            best = r if best is None or r[0] < best[0] else best
+        wall, r_ms, s_ms = best
+        return {"gbps": round(2 * P / wall / 1e9, 2), "restore_gbps": round(P / r_ms / 1e6, 2),
+                "save_gbps": round(P / s_ms / 1e6, 2)}
+
+    out = {"kernel_restore+kernel_save": case(kernel_restore, kernel_save),
+           "kernel_restore+dma_save": case(kernel_restore, dma_save),
+           "dma_restore+kernel_save": case(dma_restore, kernel_save)}
+    # The DMA pair needs two streams: the restore on the load context's.
+    def dma_restore_ctx(s0, s1):
+        s0.record(xfer_load.stream)
+        runtime.memcpy_async(dev_buf.ptr, pool.ptr, P, xfer_load.stream)
+        s1.record(xfer_load.stream)
+    out["dma_restore+dma_save"] = case(dma_restore_ctx, dma_save)
+    for gs, gr in ((16, 64), (32, 32), (32, 128), (64, 64), (24, 48)):
+        xfer_save.set_route_grid(_lib.ROUTE_SAVE_HOST, gs)
+        xfer_load.set_route_grid(_lib.ROUTE_LOAD_HOST, gr)
+        out[f"kernels_grid_save{gs}_restore{gr}"] = case(kernel_restore, kernel_save)
+    xfer_save.set_route_grid(_lib.ROUTE_SAVE_HOST, _lib.SAVE_HOST_DEFAULT_GRID)
+    xfer_load.set_route_grid(_lib.ROUTE_LOAD_HOST, _lib.LOAD_HOST_DEFAULT_GRID)
+    dma.close()
+    for k, v in out.items():
+        log(f"[bench] duplex study {k}: {v}")
+    return out
 
 
 def leg_layerwise(xfer, seed):
@@ -229,71 +313,68 @@ def leg_layerwise(xfer, seed):
     return out
 
 
-def draw_runs(rng, num_blocks, n, mean_run):
-    """n distinct block ids built from runs of consecutive blocks whose
-    lengths are Geometric(1/mean_run) (support >= 1), each run starting at a
-    random free block; mean_run >= n gives one sorted consecutive run."""
-    if mean_run >= n:
-        s = int(rng.integers(0, num_blocks - n + 1))
-        return np.arange(s, s + n, dtype=np.int64)
-    used = np.zeros(num_blocks, bool)
-    out = []
-    while len(out) < n:
-        length = min(int(rng.geometric(1.0 / mean_run)), n - len(out))
-        b = int(rng.integers(0, num_blocks))
-        while used[b]:
-            b = int(rng.integers(0, num_blocks))
-        while length > 0 and b < num_blocks and not used[b]:
-            used[b] = True
-            out.append(b)
-            b += 1
-            length -= 1
-    return np.asarray(out, np.int64)
-
-
 def leg_fragmentation(layers, xfer, seed, dma_requests=8):
-    """Config 4: 64 requests, prefixes of U[1K,16K] tokens (16-token blocks),
-    block ids as geometric runs of mean 1/4/32/640; even requests save, odd
-    requests restore (50/50 interleaved); payload GB/s per transfer mode.  The
-    pinned pool is reused per request (the batch's working set exceeds the
-    20,000-block layer tensors).  The DMA modes issue one copy per run and are
-    timed on the first `dma_requests` requests only."""
+    """Config 4: 64 requests, prefixes of U[1K,16K] tokens (16-token blocks)
+    on the Llama layers, block ids as contiguous runs of geometric length
+    with mean 1, 4 or 32, or fully sorted (640).  Each request saves its
+    blocks to the pinned pool and then restores those bytes into a second
+    draw of the same kind, so saves and restores alternate 50/50 and every
+    restore is checkable.  Outside the timed calls, the host regions are
+    checked after every save and every block of every layer after each
+    mean's batch, tracking which block's words each block holds.  Kernel and
+    staged modes run all 64 requests; the DMA modes, about 20x slower, the
+    first ``dma_requests``, and every mode is also reported on those same
+    first requests."""
     from pegaflow_amd import _lib
     from pegaflow_amd import workload as wl
     from pegaflow_amd.runtime import PinnedBuffer
 
     shape = layers.shape
-    rng = np.random.Generator(np.random.PCG64(seed + 4))
-    tokens = rng.integers(1024, 16385, 64)
-    n_blocks = [(int(t) + 15) // 16 for t in tokens]
-    pool = PinnedBuffer(max(n_blocks) * shape.layers * 2 * shape.bytes_per_block)
-    out = {}
-    for mean_run in (1, 4, 32, 640):
-        reqs = [draw_runs(rng, shape.num_blocks, nb, mean_run) for nb in n_blocks]
-        row = {}
+    pool = PinnedBuffer(1024 * shape.layers * 2 * shape.bytes_per_block)
+    out, bad = {}, 0
+    for mean_run in (1, 4, 32, wl.SORTED_MEAN_RUN):
+        reqs = wl.fragmentation_requests(shape.num_blocks, mean_run, seed=seed)
+        layers.refill()
+        src_of = np.arange(shape.num_blocks, dtype=np.int64)
+        row, row_first = {}, {}
         for name, mode in _lib.MODE_NAMES.items():
             use = reqs if name in ("kernel", "staged") else reqs[:dma_requests]
-            moved, t = 0, 0.0
-            for i, ids in enumerate(use):
+            moved = t = moved_first = t_first = 0.0
+            for i, (ids, targets) in enumerate(use):
                 saved = wl.save_plan(layers.regs, ids, pool.ptr)
+                loads = wl.load_plan(saved, targets)
                 t0 = time.perf_counter()
-                if i % 2 == 0:
-                    xfer.save_layers(saved, mode)
-                else:
-                    xfer.load_layers(saved, mode)
-                    xfer.synchronize()
-                t += time.perf_counter() - t0
-                moved += wl.payload_bytes(layers.regs, len(ids))
+                xfer.save_layers(saved, mode)
+                t1 = time.perf_counter()
+                bad += wl.verify_saved(layers, saved, src_of)
+                t2 = time.perf_counter()
+                xfer.load_layers(loads, mode)
+                xfer.synchronize()
+                t3 = time.perf_counter()
+                src_of[targets] = src_of[ids]
+                nbytes = 2 * wl.payload_bytes(layers.regs, len(ids))
+                moved += nbytes
+                t += (t1 - t0) + (t3 - t2)
+                if i < dma_requests:
+                    moved_first += nbytes
+                    t_first += (t1 - t0) + (t3 - t2)
             row[name] = round(moved / t / 1e9, 2)
-        runs = float(np.mean([1 + np.count_nonzero(np.diff(r) != 1) for r in reqs]))
-        out[f"mean_run_{mean_run}"] = {"gbps": row,
-                                       "measured_mean_run": round(float(np.mean(n_blocks)) / runs, 2)}
-        log(f"[bench] fragmentation mean_run={mean_run}: {row}")
+            row_first[name] = round(moved_first / t_first / 1e9, 2)
+        bad += wl.verify_blocks(layers, src_of)
+        runs = float(np.mean([wl.run_count(ids) for ids, _ in reqs]))
+        blocks = float(np.mean([len(ids) for ids, _ in reqs]))
+        out[f"mean_run_{mean_run}"] = {
+            "gbps": row, f"gbps_first_{dma_requests}_requests": row_first,
+            "measured_mean_run": round(blocks / runs, 2)}
+        log(f"[bench] fragmentation mean_run={mean_run}: {row}; first {dma_requests}: "
+            f"{row_first}")
     pool.close()
     layers.refill()
-    return {"workload": "64 requests, prefixes U[1K,16K] tokens on llama-3.1-8b layers, "
-                        "save/restore interleaved 50/50", "by_mean_run": out,
-            "dma_modes_timed_on_requests": dma_requests}
+    return {"workload": "64 requests, prefixes U[1K,16K] tokens on llama-3.1-8b layers, each "
+                        "saving its blocks and restoring them into a second draw (saves and "
+                        "restores 50/50); GB/s = save + restore payload / their time",
+            "by_mean_run": out, "dma_modes_timed_on_requests": dma_requests,
+            "bit_exact": bad == 0}
 
 
 def leg_mla(xfer, seed):
@@ -486,13 +567,14 @@ def leg_two_process(layers, ids, targets, P, reps=4):
                 ok, msg = client.save("bench", 0, 0, [(n, ids_l, hashes) for n in names])
                 save_ms.append((time.perf_counter() - t0) * 1e3)
                 assert ok, msg
-            load_ms, first_ms = [], []
+            load_ms, first_ms, rpc_ms = [], [], []
             for layered in (False, True):
                 for r in range(reps + 1):
                     st = PyLoadState(num_layers=len(names)) if layered else PyLoadState()
                     t0 = time.perf_counter()
                     ok, msg = client.load("bench", 0, 0, st.shm_name(), names, targets_l, hashes)
                     assert ok, msg
+                    rpc_ms.append((time.perf_counter() - t0) * 1e3)
                     t_first = None
                     while not st.is_ready():
                         if layered and t_first is None and st.layers_done() >= 1:
@@ -517,7 +599,9 @@ def leg_two_process(layers, ids, targets, P, reps=4):
     out.update({"save_ms": round(med(save_ms), 2), "save_gbps": round(P / med(save_ms) / 1e6, 2),
                 "restore_ms": round(med(load_ms), 2),
                 "restore_gbps": round(P / med(load_ms) / 1e6, 2),
-                "first_layer_ms": round(med(first_ms), 2), "bit_exact": bad == 0})
+                "first_layer_ms": round(med(first_ms), 2),
+                "load_rpc_return_ms": round(statistics.median(rpc_ms), 3),
+                "bit_exact": bad == 0})
     return out
 
 
@@ -701,14 +785,21 @@ def leg_disk(layers, ids, targets, P):
     }
 
 
-def profile_gather(seed):
-    """For rocprofv3 --pmc passes: 3 launches of the copy kernel as a plain
-    contiguous 1 GiB device copy (known bytes: 1 GiB read, 1 GiB written),
-    then 3 launches of the Llama prefix device gather (2P algorithmic bytes).
-    The two are told apart by grid size (131,072 vs 163,840 workgroups)."""
+def profile_kernels(kind, seed):
+    """For rocprofv3 --pmc passes.  Every mode first runs the copy kernel 3
+    times as a plain contiguous 1 GiB device copy (known bytes: 1 GiB read,
+    1 GiB written: the counters' calibration), then 3 launches of:
+      gather:   the Llama prefix paged -> packed HBM buffer (2P algorithmic
+                bytes per launch);
+      scatter:  the packed HBM buffer -> 640 other blocks of the paged
+                tensors (2P);
+      zerocopy: the prefix saved to pinned host memory, then restored from
+                it (P over the host link per call; each call is two
+                launches, its first eighth of layers, then the rest).
+    Kernels are told apart by grid size (printed)."""
     from pegaflow_amd import _lib, runtime
     from pegaflow_amd import workload as wl
-    from pegaflow_amd.runtime import DeviceBuffer
+    from pegaflow_amd.runtime import DeviceBuffer, PinnedBuffer
     from pegaflow_amd.transfer import KVCacheRegistration, TransferContext
 
     runtime.init(0)
@@ -720,43 +811,142 @@ def profile_gather(seed):
     plain = wl.save_plan([reg], np.arange(GiB // chunk), dst.ptr)
     for _ in range(3):
         xfer.save_layers(plain, _lib.MODE_KERNEL)
+    src.close()
+    dst.close()
     layers = wl.DeviceLayers(wl.LLAMA3_8B, base_seed=seed)
-    ids, _ = wl.draw_blocks(wl.LLAMA3_8B.num_blocks, 640, seed)
+    ids, targets = wl.draw_blocks(wl.LLAMA3_8B.num_blocks, 640, seed)
     P = wl.payload_bytes(layers.regs, 640)
-    gbuf = DeviceBuffer(P)
-    gather = wl.save_plan(layers.regs, ids, gbuf.ptr)
-    for _ in range(3):
+    info = {"plain_copy_bytes_read": GiB, "plain_copy_bytes_written": GiB,
+            "plain_workgroups": (GiB // chunk) * 4, "kind": kind}
+    if kind in ("gather", "scatter"):
+        gbuf = DeviceBuffer(P)
+        gather = wl.save_plan(layers.regs, ids, gbuf.ptr)
         xfer.save_layers(gather, _lib.MODE_KERNEL)
-    print(json.dumps({"plain_copy_bytes_read": GiB, "plain_copy_bytes_written": GiB,
-                      "gather_algorithmic_bytes": 2 * P,
-                      "plain_workgroups": (GiB // chunk) * 4, "gather_workgroups": 40960 * 4}),
-          flush=True)
+        plan = gather if kind == "gather" else wl.load_plan(gather, targets)
+        for _ in range(3):
+            if kind == "gather":
+                xfer.save_layers(plan, _lib.MODE_KERNEL)
+            else:
+                xfer.load_layers(plan, _lib.MODE_KERNEL)
+                xfer.synchronize()
+        ok = (wl.verify_saved(layers, gather) == 0 if kind == "gather"
+              else wl.verify_restored(layers, ids, targets) == 0)
+        info.update({f"{kind}_algorithmic_bytes": 2 * P,
+                     f"{kind}_workgroups": 40960 * (4 if kind == "gather" else 2),
+                     "bit_exact": ok})
+        gbuf.close()
+    else:
+        pool = PinnedBuffer(P)
+        saved = wl.save_plan(layers.regs, ids, pool.ptr)
+        loads = wl.load_plan(saved, targets)
+        for _ in range(3):
+            xfer.save_layers(saved, _lib.MODE_KERNEL)
+        for _ in range(3):
+            xfer.load_layers(loads, _lib.MODE_KERNEL)
+            xfer.synchronize()
+        info.update({"zerocopy_link_bytes_per_call": P,
+                     "bit_exact": wl.verify_saved(layers, saved) == 0 and
+                     wl.verify_restored(layers, ids, targets) == 0})
+        pool.close()
+    print(json.dumps(info), flush=True)
+    layers.close()
     xfer.close()
 
 
-def read_traffic():
-    """HBM bytes per gather launch from the committed rocprofv3 --pmc summary
-    (profiles/copy_chunks_llama3_8b_prefix_traffic.txt), or None."""
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                        "copy_chunks_llama3_8b_prefix_traffic.txt")
+def read_traffic(name):
+    """HBM bytes per launch from a committed rocprofv3 --pmc summary under
+    profiles/ (its "traffic_bytes_per_launch = N" line), with the file's
+    name, or (None, None)."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", name)
     try:
         with open(path) as fh:
             for line in fh:
                 if line.startswith("traffic_bytes_per_launch"):
-                    return int(line.split("=")[1].strip())
+                    return int(line.split("=")[1].strip()), "profiles/" + name
     except OSError:
         pass
-    return None
+    return None, None
 
 
-def cpu_baseline(shape, ids, targets, n_layers, threads, seed):
+def _cpulist(text):
+    """CPU ids of a sysfs cpulist ("0-7,16-23")."""
+    out = set()
+    for part in text.strip().split(","):
+        if part:
+            a, _, b = part.partition("-")
+            out.update(range(int(a), int(b or a) + 1))
+    return out
+
+
+def _read(path, default=""):
+    try:
+        with open(path) as f:
+            return f.read().strip()
+    except OSError:
+        return default
+
+
+def host_cores_near_gpu(device=0):
+    """The GPU's NUMA node (from its PCI address) and one CPU per physical
+    core of that node that this process may run on (its affinity mask), as
+    the CPU baseline's threads.  Falls back to the whole affinity mask when
+    the node is unknown or shares no CPU with it."""
+    from pegaflow_amd import runtime
+
+    try:
+        bdf = runtime.pci_bus_id(device)
+    except Exception:  # noqa: BLE001 - no device here: no node to be near
+        bdf = "unknown"
+    node = int(_read(f"/sys/bus/pci/devices/{bdf}/numa_node", "-1") or -1)
+    allowed = os.sched_getaffinity(0)
+    node_cpus = _cpulist(_read(f"/sys/devices/system/node/node{node}/cpulist")) if node >= 0 \
+        else set()
+    cpus = sorted(node_cpus & allowed) or sorted(allowed)
+    cores = {}
+    for c in cpus:
+        topo = f"/sys/devices/system/cpu/cpu{c}/topology"
+        cores.setdefault((_read(f"{topo}/physical_package_id"), _read(f"{topo}/core_id", str(c))),
+                         c)
+    return {"pci_bus_id": bdf, "numa_node": node, "node_cpus": len(node_cpus),
+            "allowed_cpus": len(allowed), "cores": sorted(cores.values())}
+
+
+def cpu_model() -> str:
+    """The CPU's model name as lscpu reports it (its BIOS name too when the
+    two differ), else /proc/cpuinfo's."""
+    import subprocess
+
+    names = []
+    try:
+        text = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in text.splitlines():
+            key, _, val = line.partition(":")
+            if key.strip() in ("Model name", "BIOS Model name") and val.strip() not in names:
+                names.append(val.strip())
+    except (OSError, subprocess.SubprocessError):
+        pass
+    if not names:
+        for line in _read("/proc/cpuinfo").splitlines():
+            if line.startswith("model name"):
+                names.append(line.split(":", 1)[1].strip())
+                break
+    return " / ".join(names) or "unknown"
+
+
+def cpu_baseline(shape, ids, targets, n_layers, seed, device=0):
     """The reference's CPU-side copy pattern, timed with host memcpy: save =
     one copy per segment (gpu_worker.rs:344-360), restore = one copy per merged
-    run (transfer.rs:116-198), over host-resident copies of n_layers layers."""
+    run (transfer.rs:116-198), over host-resident copies of n_layers layers,
+    on one thread per physical core of the GPU's NUMA node and on one thread.
+    The threaded result is compared byte for byte with the single-thread
+    result and checked in closed form (pool regions = source segments in
+    save order, target blocks = source blocks, source words = the fill)."""
     import oracle
     from pegaflow_amd.workload import layer_seed
 
-    n = len(ids)
+    near = host_cores_near_gpu(device)
+    threads = max(1, len(near["cores"]))
+    n, nb = len(ids), shape.num_blocks
     bpb, kv = shape.bytes_per_block, shape.kv_stride_bytes
     tensors = []
     for l in range(n_layers):
@@ -766,8 +956,7 @@ def cpu_baseline(shape, ids, targets, n_layers, threads, seed):
     pool = np.zeros(n_layers * n * 2 * bpb, np.uint8)
     ss, sd, sz, ls, ld, lz = [], [], [], [], [], []
     for l, t in enumerate(tensors):
-        reg = oracle.layout(t.ctypes.data, shape.layer_bytes, shape.num_blocks, bpb, kv,
-                            shape.segments)
+        reg = oracle.layout(t.ctypes.data, shape.layer_bytes, nb, bpb, kv, shape.segments)
         base = pool.ctypes.data + l * n * 2 * bpb
         k, v, _ = oracle.save_host_layout(reg, n, base, base + n * bpb)
         a, b, c = oracle.save_copies(reg, t.ctypes.data, ids, k, v)
@@ -790,9 +979,29 @@ def cpu_baseline(shape, ids, targets, n_layers, threads, seed):
             tl.append(t2 - t1)
         return statistics.median(ts), statistics.median(tl)
 
+    def targets_of(t):
+        return t.reshape(2, nb, bpb)[:, targets]
+
     run(threads)  # warm
     s_mt, l_mt = run(threads)
+    pool_mt = pool.copy()
+    tgt_mt = [targets_of(t) for t in tensors]
+    pool[:] = 0
+    for t in tensors:
+        t.reshape(2, nb, bpb)[:, targets] = 0
     s_1, l_1 = run(1)
+    bad = int(np.count_nonzero(pool != pool_mt))
+    bad += sum(int(np.count_nonzero(targets_of(t) != m)) for t, m in zip(tensors, tgt_mt))
+    for l, t in enumerate(tensors):
+        segs = t.reshape(2, nb, bpb)
+        region = pool[l * n * 2 * bpb:(l + 1) * n * 2 * bpb].reshape(2, n, bpb)
+        src = segs[:, ids]
+        bad += int(np.count_nonzero(region != src)) + int(np.count_nonzero(segs[:, targets] != src))
+        for j in ids[:4]:
+            for sg in range(2):
+                off = sg * kv + int(j) * bpb
+                want = oracle.random_words(bpb // 8, layer_seed(seed, l), off // 8)
+                bad += int(np.count_nonzero(t[off:off + bpb].view(np.uint64) != want))
     return {
         "value": round(2 * payload / (s_mt + l_mt) / 1e9, 3),
         "unit": "GB/s",
@@ -806,20 +1015,13 @@ def cpu_baseline(shape, ids, targets, n_layers, threads, seed):
         "single_thread_gbps": round(2 * payload / (s_1 + l_1) / 1e9, 3),
         "save_copies": int(len(save[0])),
         "restore_copies": int(len(load[0])),
-        "cpu_model": _cpu_model(),
+        "bit_exact": bad == 0,
+        "threads": ("one per physical core of the GPU's NUMA node in this process's CPU set"
+                    if near["node_cpus"] else "one per physical core in this process's CPU set"),
+        "numa": {k: v for k, v in near.items() if k != "cores"},
+        "cpu_model": cpu_model(),
         "host_cpus": os.cpu_count(),
     }
-
-
-def _cpu_model() -> str:
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
-    except OSError:
-        pass
-    return "unknown"
 
 
 def main():
@@ -830,8 +1032,8 @@ def main():
               "(each rank moves its own layers over its own host link); run with --gpus 1",
               file=sys.stderr)
         sys.exit(2)
-    if args.profile_gather:
-        profile_gather(args.seed)
+    if args.profile:
+        profile_kernels(args.profile, args.seed)
         return
 
     # The single-block latency benchmark runs as its own process, before this
@@ -947,6 +1149,21 @@ def main():
         s_ms.append(ms)
     scatter_ms = sum(s_ms) / len(s_ms)
     scatter_gbps = 2 * P / (scatter_ms / 1e3) / 1e9
+    if args.sweep_scatter:
+        load_k = lambda plan: (xfer.load_layers(plan, _lib.MODE_KERNEL),  # noqa: E731
+                               xfer.synchronize())
+        scatter_shapes = [(t, u | nt | x) for t in (256, 512, 1024) for u in (1, 2, 4)
+                          for nt in (0, _lib.KERNEL_NT_LOADS, _lib.KERNEL_NT_STORES,
+                                     _lib.KERNEL_NONTEMPORAL)
+                          for x in (0, _lib.KERNEL_XCD_MAJOR)]
+        shape_sweep("scatter", scatter, load_k, 5, 2 * P, scatter_shapes)
+        # The same chunks with each layer's blocks in destination order.
+        dst_sorted = []
+        for lt in scatter:
+            b = lt.blocks[np.argsort(lt.blocks["block_idx"], kind="stable")]
+            dst_sorted.append(type(lt)(lt.registration, b))
+        shape_sweep("scatter_dstsorted", dst_sorted, load_k, 5, 2 * P, scatter_shapes)
+        layers.refill()
 
     variants = {}
     if args.variants or not args.quick:
@@ -1001,6 +1218,8 @@ def main():
     log(f"[bench] duplex save+restore {t_dup * 1e3:.3f} ms = {2 * P / t_dup / 1e9:.1f} GB/s, "
         f"mismatches {bad_dup}")
     bad_host += bad_dup
+    if args.duplex_study:
+        extra_duplex = duplex_study(xfer, xfer2, saved2, loads, pool, pool2, gather_buf, P)
     xfer2.close()
     pool2.close()
 
@@ -1028,11 +1247,18 @@ def main():
         extra["disk_tier_llama3_8b"] = leg_disk(layers, ids, targets, P)
         log(f"[bench] {extra['disk_tier_llama3_8b']}")
 
+    k_save_ms, k_load_ms = statistics.median(k_save), statistics.median(k_load)
+    link_save_gbps = P / (k_save_ms / 1e3) / 1e9
+    link_restore_gbps = P / (k_load_ms / 1e3) / 1e9
+    save_traffic, save_traffic_src = read_traffic("copy_chunks_llama3_8b_zerocopy_traffic.txt")
+    gather_traffic, gather_traffic_src = read_traffic("copy_chunks_llama3_8b_prefix_traffic.txt")
+    scatter_traffic, scatter_traffic_src = read_traffic(
+        "copy_chunks_llama3_8b_scatter_traffic.txt")
+
     cpu = None
     if not args.no_cpu_baseline:
-        threads = max(1, min(16, len(os.sched_getaffinity(0))))
-        log(f"[bench] cpu baseline: {args.cpu_sample_layers} layers, {threads} threads")
-        cpu = cpu_baseline(shape, ids, targets, args.cpu_sample_layers, threads, args.seed)
+        log(f"[bench] cpu baseline: {args.cpu_sample_layers} layers")
+        cpu = cpu_baseline(shape, ids, targets, args.cpu_sample_layers, args.seed)
         log(f"[bench] cpu baseline {cpu}")
 
     out = {
@@ -1064,29 +1290,67 @@ def main():
         "save_ms_per_prefix": round(save_s * 1e3, 3),
         "save_frac_of_measured_d2h_peak": round(P / save_s / 1e9 / d2h_peak, 4),
         "save_frac_of_pcie_gen5": round(P / save_s / 1e9 / PCIE_GEN5_X16_GBPS, 4),
-        "restore_kernel_ms": round(statistics.median(k_load), 3) if k_load else None,
-        "save_kernel_ms": round(statistics.median(k_save), 3) if k_save else None,
+        "restore_kernel_ms": round(k_load_ms, 3),
+        "save_kernel_ms": round(k_save_ms, 3),
         "host_link_peak_gbps": {"h2d": round(h2d_peak, 2), "d2h": round(d2h_peak, 2),
                                 "pcie_gen5_x16": PCIE_GEN5_X16_GBPS},
+        # The timed step is two host-link kernels; the save, the longer of
+        # the two, is the dominant kernel.  Achieved = P per call / the
+        # call's kernel time (HIP events on the context's stream around
+        # each launch, summed over the call's two launches).
         "roofline": {
+            "bound": "pcie",
+            "kernel": "copy_chunks_queue_kernel<2,nt-loads> 512 threads x 32 persistent "
+                      "workgroups (zero-copy save: 40,960 chunks of 32 KiB, paged HBM -> "
+                      "pinned host, 2 launches per call)",
+            "achieved": round(link_save_gbps, 2),
+            "peak": PCIE_GEN5_X16_GBPS,
+            "unit": "GB/s",
+            "frac": round(link_save_gbps / PCIE_GEN5_X16_GBPS, 4),
+            "measured_peak": round(d2h_peak, 2),
+            "frac_of_measured_peak": round(link_save_gbps / d2h_peak, 4),
+            "bytes_per_call": P,
+            "ms_per_call": round(k_save_ms, 4),
+            "traffic": save_traffic,
+            "traffic_source": save_traffic_src,
+            "restore": {
+                "kernel": "copy_chunks_queue_kernel<2,nt,nt> 512 threads x 64 persistent "
+                          "workgroups (zero-copy restore, pinned host -> paged HBM)",
+                "achieved": round(link_restore_gbps, 2),
+                "frac": round(link_restore_gbps / PCIE_GEN5_X16_GBPS, 4),
+                "measured_peak": round(h2d_peak, 2),
+                "frac_of_measured_peak": round(link_restore_gbps / h2d_peak, 4),
+                "ms_per_call": round(k_load_ms, 4),
+            },
+        },
+        # The HBM-bound kernels of the staged mode, timed outside the steps.
+        "device_gather": {
             "bound": "hbm",
             "achieved": round(gather_gbps, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(gather_gbps / HBM_PEAK_GBPS, 4),
-            "traffic": read_traffic(),
-            "kernel": "copy_chunks_v16_kernel<1,nt,nt> 512 threads (device gather: 40960 chunks of 32 KiB, 1 launch)",
+            "traffic": gather_traffic,
+            "traffic_source": gather_traffic_src,
+            "kernel": "copy_chunks_v16_kernel<1,nt,nt> 512 threads (device gather: 40960 "
+                      "chunks of 32 KiB, 1 launch)",
             "bytes_per_launch": 2 * P,
             "ms_per_launch": round(gather_ms, 4),
             "plain_copy_gbps": round(plain_gbps, 1),
             "frac_of_plain_copy": round(gather_gbps / plain_gbps, 4),
         },
-        "device_scatter": {"gbps": round(scatter_gbps, 1), "ms_per_launch": round(scatter_ms, 4),
-                           "frac": round(scatter_gbps / HBM_PEAK_GBPS, 4)},
+        "device_scatter": {"bound": "hbm", "achieved": round(scatter_gbps, 1),
+                           "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                           "frac": round(scatter_gbps / HBM_PEAK_GBPS, 4),
+                           "traffic": scatter_traffic, "traffic_source": scatter_traffic_src,
+                           "kernel": "copy_chunks_v16_kernel<2,nt,nt> 512 threads, XCD-major "
+                                     "tile order (device scatter: packed HBM -> 640 blocks)",
+                           "bytes_per_launch": 2 * P, "ms_per_launch": round(scatter_ms, 4)},
         "d2d_memcpy_gbps": round(d2d_gbps, 1),
         "duplex": {"gbps": round(2 * P / t_dup / 1e9, 3), "ms_per_save_plus_restore":
                    round(t_dup * 1e3, 3),
-                   "what": "a prefix saved while another is restored (two transfer contexts)"},
+                   "what": "a prefix saved while another is restored (two transfer contexts)",
+                   **({"study": extra_duplex} if args.duplex_study else {})},
         "bit_exact": bad_host == 0 and bad_dev == 0,
         "cpu_baseline": cpu,
     }

@@ -134,6 +134,11 @@ int pf_memset_d8(uint64_t dst_dev, uint8_t value, uint64_t size);
 int pf_memcpy_async(uint64_t dst, uint64_t src, uint64_t size, pf_stream stream);
 /* Free and total device memory in bytes. */
 int pf_mem_get_info(uint64_t* free_bytes, uint64_t* total_bytes);
+/* PCI address of the device, "dddd:bb:dd.f" (lower case, NUL-terminated in
+ * len bytes), to find its NUMA node under /sys/bus/pci/devices (no
+ * counterpart in the reference; the pinned pool's NUMA placement and the
+ * benchmark's host-thread count use it). */
+int pf_device_pci_bus_id(int device, char* buf, int len);
 
 /* ------------------------------------------------------------------------ */
 /* Pinned host memory.                                                        */

@@ -232,6 +232,7 @@ SIGNATURES = {
     "pf_memcpy_d2d": (i32, [u64, u64, u64]),
     "pf_memset_d8": (i32, [u64, ctypes.c_uint8, u64]),
     "pf_memcpy_async": (i32, [u64, u64, u64, vp]),
+    "pf_device_pci_bus_id": (i32, [i32, ctypes.c_char_p, i32]),
     "pf_mem_get_info": (i32, [pu64, pu64]),
     "pf_pinned_allocate": (i32, [u64, u32, pvp, pu64]),
     "pf_pinned_free": (i32, [vp]),

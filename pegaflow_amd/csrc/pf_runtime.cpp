@@ -199,6 +199,14 @@ int pf_init(int device) {
   return noalloc_scratch(device, &sc);
 }
 
+int pf_device_pci_bus_id(int device, char* buf, int len) {
+  if (!buf || len < 13) return fail(PF_ERR_INVALID_ARGUMENT, "buffer too small for a PCI id");
+  PF_HIP(hipDeviceGetPCIBusId(buf, len, device));
+  for (int i = 0; i < len && buf[i]; ++i)
+    if (buf[i] >= 'A' && buf[i] <= 'F') buf[i] = static_cast<char>(buf[i] - 'A' + 'a');
+  return PF_OK;
+}
+
 int pf_set_device(int device) {
   PF_HIP(hipSetDevice(device));
   return PF_OK;

@@ -33,6 +33,13 @@ def synchronize() -> None:
     check(lib().pf_device_synchronize(), "pf_device_synchronize")
 
 
+def pci_bus_id(device: int = 0) -> str:
+    """The device's PCI address, "dddd:bb:dd.f"."""
+    buf = ctypes.create_string_buffer(64)
+    check(lib().pf_device_pci_bus_id(device, buf, len(buf)), "pf_device_pci_bus_id")
+    return buf.value.decode()
+
+
 def mem_get_info():
     f, t = ctypes.c_uint64(), ctypes.c_uint64()
     check(lib().pf_mem_get_info(ctypes.byref(f), ctypes.byref(t)), "pf_mem_get_info")
