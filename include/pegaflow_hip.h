@@ -293,6 +293,13 @@ int pf_xfer_synchronize(pf_xfer* xfer);
 /* Give each of the 8 XCDs one contiguous range of tiles instead of the
  * hardware's round-robin deal (only with an uncapped grid). */
 #define PF_KERNEL_XCD_MAJOR 0x400u
+/* Scatters only (PF_ROUTE_LOAD_DEVICE): choose the shape on evidence.  The
+ * context times two candidate shapes, 512 threads with 2 loads per lane in
+ * XCD-major order and 512 threads with 1 load per lane in round-robin order
+ * (both non-temporal), twice each on its first scatters of at least 64 MiB,
+ * and keeps the faster.  Which one wins depends on where the destination
+ * tensors lie in HBM.  The other bits of the value are then ignored. */
+#define PF_KERNEL_AUTO 0x800u
 /* Launch shapes are kept per route: the direction, and whether the far side
  * of the copy is device memory (an HBM-bound gather or scatter) or pinned
  * host memory (zero-copy over the host link). */
@@ -303,21 +310,28 @@ enum {
   PF_ROUTE_LOAD_HOST = 3    /* pinned host memory -> paged tensor           */
 };
 /* Per-route defaults (the fastest shapes measured on MI355X): HBM gathers
- * move 8 KiB tiles in round-robin order; scatters 16 KiB tiles in XCD-major
- * order; zero-copy saves 16 KiB tiles with streaming loads and ordinary
- * stores into host memory (2% faster than streaming both). */
+ * move 8 KiB tiles in round-robin order; scatters choose on evidence
+ * (PF_KERNEL_AUTO); zero-copy saves 16 KiB tiles with streaming loads and
+ * ordinary stores into host memory (2% faster than streaming both). */
 #define PF_SAVE_DEFAULT_THREADS 512u
 #define PF_SAVE_DEFAULT_UNROLL (1u | PF_KERNEL_NONTEMPORAL)
 #define PF_LOAD_DEFAULT_THREADS 512u
-#define PF_LOAD_DEFAULT_UNROLL (2u | PF_KERNEL_NONTEMPORAL | PF_KERNEL_XCD_MAJOR)
+#define PF_LOAD_DEFAULT_UNROLL (2u | PF_KERNEL_NONTEMPORAL | PF_KERNEL_XCD_MAJOR | PF_KERNEL_AUTO)
 #define PF_SAVE_HOST_DEFAULT_THREADS 512u
 #define PF_SAVE_HOST_DEFAULT_UNROLL (2u | PF_KERNEL_NT_LOADS)
 #define PF_LOAD_HOST_DEFAULT_THREADS 512u
 #define PF_LOAD_HOST_DEFAULT_UNROLL (2u | PF_KERNEL_NONTEMPORAL | PF_KERNEL_XCD_MAJOR)
 /* Shape for one route only (PF_ROUTE_*; 0 and 1 are also "saves" and
- * "loads" of device memory).  pf_xfer_set_kernel_shape sets every route. */
+ * "loads" of device memory).  pf_xfer_set_kernel_shape sets every route.
+ * Setting the scatter route's shape restarts its choice when the new value
+ * carries PF_KERNEL_AUTO, and ends it otherwise. */
 int pf_xfer_set_kernel_shape_dir(pf_xfer* xfer, uint32_t direction,
                                  uint32_t threads, uint32_t unroll);
+/* The shape a route's next fixed-map launch uses: the route's setting, or for
+ * a scatter route on PF_KERNEL_AUTO the chosen candidate once both have been
+ * timed (*decided = 1), else the first candidate (*decided = 0). */
+int pf_xfer_route_shape(pf_xfer* xfer, uint32_t route, uint32_t* threads,
+                        uint32_t* unroll, int* decided);
 /* Work distribution per route.  0: one workgroup per tile, dealt to the XCDs
  * by the hardware (best for HBM-bound copies).  N > 0: N persistent
  * workgroups take tiles from a queue in order (best over the host link,

@@ -68,8 +68,10 @@ KERNEL_NT_LOADS = 0x100
 KERNEL_NT_STORES = 0x200
 KERNEL_NONTEMPORAL = KERNEL_NT_LOADS | KERNEL_NT_STORES
 KERNEL_XCD_MAJOR = 0x400
+# Scatter route only: time two candidate shapes, keep the faster.
+KERNEL_AUTO = 0x800
 SAVE_DEFAULT_SHAPE = (512, 1 | KERNEL_NONTEMPORAL)
-LOAD_DEFAULT_SHAPE = (512, 2 | KERNEL_NONTEMPORAL | KERNEL_XCD_MAJOR)
+LOAD_DEFAULT_SHAPE = (512, 2 | KERNEL_NONTEMPORAL | KERNEL_XCD_MAJOR | KERNEL_AUTO)
 SAVE_HOST_DEFAULT_SHAPE = (512, 2 | KERNEL_NT_LOADS)
 LOAD_HOST_DEFAULT_SHAPE = (512, 2 | KERNEL_NONTEMPORAL | KERNEL_XCD_MAJOR)
 # Launch-shape routes (PF_ROUTE_*): direction x where the far side lives.
@@ -254,6 +256,8 @@ SIGNATURES = {
     "pf_xfer_last_stats": (i32, [vp, pu64, pu64]),
     "pf_xfer_set_max_grid": (i32, [vp, u32]),
     "pf_xfer_set_kernel_shape_dir": (i32, [vp, u32, u32, u32]),
+    "pf_xfer_route_shape": (i32, [vp, u32, ctypes.POINTER(u32), ctypes.POINTER(u32),
+                                  ctypes.POINTER(i32)]),
     "pf_xfer_set_route_grid": (i32, [vp, u32, u32]),
     "pf_xfer_set_timing": (i32, [vp, i32]),
     "pf_xfer_last_kernel_ms": (i32, [vp, ctypes.POINTER(ctypes.c_float), pu64]),

@@ -226,6 +226,15 @@ class TransferContext:
         check(lib().pf_xfer_set_route_grid(self.handle, route, workgroups),
               "pf_xfer_set_route_grid")
 
+    def route_shape(self, route: int):
+        """(threads, unroll, decided): the shape the route's next fixed-map
+        launch uses (for an automatic scatter route, the chosen candidate once
+        decided)."""
+        t, u, d = ctypes.c_uint32(), ctypes.c_uint32(), ctypes.c_int()
+        check(lib().pf_xfer_route_shape(self.handle, route, ctypes.byref(t), ctypes.byref(u),
+                                        ctypes.byref(d)), "pf_xfer_route_shape")
+        return t.value, u.value, bool(d.value)
+
     def reset_kernel_shape(self) -> None:
         """Back to the per-route defaults (shapes and work distribution)."""
         for route, shape in _lib.DEFAULT_SHAPES.items():

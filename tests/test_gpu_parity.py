@@ -590,3 +590,49 @@ def test_layerwise_load_events_qwen3(ctx):
     compute.close()
     layers.close()
     host.close()
+
+
+def test_scatter_shape_chosen_on_evidence(ctx):
+    """The scatter route times its two candidate shapes on a context's first
+    scatters of at least 64 MiB (two each) and keeps the faster: every call's
+    bytes are exact whichever shape ran, the choice is made after the trials,
+    an explicit shape ends it and the defaults start it again."""
+    say("[gpu] scatter shape chosen on evidence")
+    n_layers, nb, bpb, n = 8, 4000, 32768, 640
+    layers = Layers(n_layers, nb, bpb, 2, 21)
+    rng = np.random.Generator(np.random.PCG64(21))
+    ids = rng.choice(nb, n, replace=False)
+    targets = rng.choice(np.setdiff1d(np.arange(nb), ids), n, replace=False)
+    stage = DeviceBuffer(n_layers * n * 2 * bpb)  # 335 MB: one launch per call
+    x = TransferContext(0)
+    try:
+        saved, _ = save_transfers(layers, ids.tolist(), stage)
+        x.save_layers(saved, _lib.MODE_KERNEL)
+        assert closed_form_host_check(layers, ids.tolist(), saved) == 0
+        scatter = load_transfers(layers, targets, saved)
+        src_of = {int(t): int(s) for t, s in zip(targets, ids)}
+        assert x.route_shape(_lib.ROUTE_LOAD_DEVICE)[2] is False
+        for call in range(6):
+            x.load_layers(scatter, _lib.MODE_KERNEL)
+            x.synchronize()
+            assert closed_form_tensor_check(layers, src_of) == 0, f"call {call}"
+            for l in range(n_layers):
+                layers.bufs[l].fill_random(layers.seeds[l])
+        threads, unroll, decided = x.route_shape(_lib.ROUTE_LOAD_DEVICE)
+        assert decided and (threads, unroll) in (
+            (512, 2 | _lib.KERNEL_NONTEMPORAL | _lib.KERNEL_XCD_MAJOR),
+            (512, 1 | _lib.KERNEL_NONTEMPORAL))
+        say(f"[gpu] scatter shape chosen: {threads} threads, unroll {unroll:#x}")
+        x.set_kernel_shape_dir(_lib.ROUTE_LOAD_DEVICE, 256, 1)
+        assert x.route_shape(_lib.ROUTE_LOAD_DEVICE) == (256, 1, True)
+        x.load_layers(scatter, _lib.MODE_KERNEL)
+        x.synchronize()
+        assert closed_form_tensor_check(layers, src_of) == 0
+        x.reset_kernel_shape()
+        assert x.route_shape(_lib.ROUTE_LOAD_DEVICE)[2] is False
+        with pytest.raises(_lib.PegaFlowError, match="scatter route only"):
+            x.set_kernel_shape_dir(_lib.ROUTE_SAVE_DEVICE, 512, 1 | _lib.KERNEL_AUTO)
+    finally:
+        x.close()
+        stage.close()
+        layers.close()
