@@ -90,6 +90,8 @@ def parse():
     ap.add_argument("--duplex-study", action="store_true",
                     help="also time each link direction against a plain DMA copy the other way, "
                          "and the two queued kernels' grids in duplex")
+    ap.add_argument("--pinned-flags", type=int, default=0,
+                    help="PF_PINNED_* flags of the pinned pools (0: mapped, portable)")
     ap.add_argument("--cpu-sample-layers", type=int, default=8)
     ap.add_argument("--staging-mib", type=int, default=256)
     ap.add_argument("--seed", type=int, default=0)
@@ -203,6 +205,20 @@ def duplex_study(xfer_load, xfer_save, saved, loads, pool, pool2, dev_buf, P, re
         runtime.memcpy_async(dev_buf.ptr, pool.ptr, P, xfer_load.stream)
         s1.record(xfer_load.stream)
     out["dma_restore+dma_save"] = case(dma_restore_ctx, dma_save)
+
+    def staged_save(s0, s1):
+        s0.record(xfer_save.stream)
+        xfer_save.save_layers(saved, _lib.MODE_STAGED)
+        s1.record(xfer_save.stream)
+
+    def staged_restore(s0, s1):
+        s0.record(xfer_load.stream)
+        xfer_load.load_layers(loads, _lib.MODE_STAGED)
+        s1.record(xfer_load.stream)
+
+    out["staged_restore+staged_save"] = case(staged_restore, staged_save)
+    out["staged_restore+kernel_save"] = case(staged_restore, kernel_save)
+    out["kernel_restore+staged_save"] = case(kernel_restore, staged_save)
     for gs, gr in ((16, 64), (32, 32), (32, 128), (64, 64), (24, 48)):
         xfer_save.set_route_grid(_lib.ROUTE_SAVE_HOST, gs)
         xfer_load.set_route_grid(_lib.ROUTE_LOAD_HOST, gr)
@@ -1053,7 +1069,7 @@ def main():
     ids, targets = wl.draw_blocks(shape.num_blocks, n_blocks, args.seed)
     P = wl.payload_bytes(layers.regs, n_blocks)
     assert P == 1_342_177_280
-    pool = PinnedBuffer(P)
+    pool = PinnedBuffer(P, args.pinned_flags)
     gather_buf = DeviceBuffer(P)
     xfer = TransferContext(0, staging_bytes=args.staging_mib << 20)
     modes = _lib.MODE_NAMES
@@ -1216,8 +1232,8 @@ def main():
 
     # Full duplex: a second prefix saved (into a second pool) while the first
     # is restored, on two contexts as the engine's save and load workers do.
-    pool2 = PinnedBuffer(P)
-    xfer2 = TransferContext(0)
+    pool2 = PinnedBuffer(P, args.pinned_flags)
+    xfer2 = TransferContext(0, staging_bytes=(args.staging_mib << 20) if args.duplex_study else 0)
     saved2 = wl.save_plan(layers.regs, ids, pool2.ptr)
     t_dup = duplex(xfer2, xfer, saved2, loads, save_mode)
     bad_dup = wl.verify_saved(layers, saved2) + wl.verify_restored(layers, ids, targets)
