@@ -46,6 +46,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import shutil
 import statistics
 import sys
 import time
@@ -514,13 +515,13 @@ def pinned_copy_microbench(iters=2000):
     return out
 
 
-def _start_server(pool_bytes):
+def _start_server(pool_bytes, *extra):
     """pegaflow_amd.rpc.server as a child process on an ephemeral port."""
     import select
     import subprocess
 
     cmd = [sys.executable, "-u", "-m", "pegaflow_amd.rpc.server", "--addr", "127.0.0.1:0",
-           "--pool-size", f"{pool_bytes >> 20}mb", "--log-level", "warning"]
+           "--pool-size", f"{pool_bytes >> 20}mb", "--log-level", "warning", *extra]
     p = subprocess.Popen(cmd, cwd=os.path.dirname(os.path.abspath(__file__)),
                          stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     t0, seen = time.monotonic(), []
@@ -542,13 +543,17 @@ def _start_server(pool_bytes):
 
 def leg_two_process(layers, ids, targets, P, reps=4):
     """The deployment path of the reference: the inference process keeps its
-    layer tensors and talks gRPC to an engine server in another process,
-    which maps the tensors through HIP IPC (registry.rs:144-175).  The
-    inference side saves the prefix by hash (service.rs save), then restores
-    it by hash into other blocks with a LoadState and polls it, as the
-    connector's start_load_kv / get_finished do (worker.py:148-286).  The
-    restore time runs from the Load RPC to the LoadState reading ready."""
+    layer tensors and talks to an engine server in another process, which
+    maps the tensors through HIP IPC (registry.rs:144-175).  The inference
+    side saves the prefix by hash (service.rs save), then restores it by hash
+    into other blocks with a LoadState and polls it, as the connector's
+    start_load_kv / get_finished do (worker.py:148-286).  The restore time
+    runs from the Load request to the LoadState reading ready; the first
+    layer from the request to layer 0 reading done in a layered LoadState.
+    Measured over gRPC, and over the server's native endpoint for the same
+    requests (--fast-socket)."""
     import hashlib
+    import tempfile
 
     from pegaflow_amd import ipc
     from pegaflow_amd import workload as wl
@@ -560,11 +565,50 @@ def leg_two_process(layers, ids, targets, P, reps=4):
     handles = [ipc.export_tensor(b.ptr, shape.layer_bytes, 0) for b in layers.bufs]
     ids_l, targets_l = [int(i) for i in ids], [int(t) for t in targets]
     layers.refill()
-    p, addr = _start_server((reps + 2) * P + (256 << 20))
-    out = {"what": "llama prefix saved and restored by hash through the gRPC engine server in "
-                   "a second process that maps the 32 layer tensors through HIP IPC; restore "
-                   "timed from the Load RPC to the LoadState reading ready, median of the warm "
-                   "calls"}
+    sock = os.path.join(tempfile.mkdtemp(prefix="pega_bench_"), "engine.sock")
+    p, addr = _start_server((reps + 2) * P + (256 << 20), "--fast-socket", sock)
+    out = {"what": "llama prefix saved and restored by hash through the engine server in a "
+                   "second process that maps the 32 layer tensors through HIP IPC; restore "
+                   "timed from the Load request to the LoadState reading ready, median of the "
+                   "warm calls; over gRPC, and over the server's native endpoint (fast_path)"}
+    med = lambda v: statistics.median(v[1:])  # noqa: E731
+
+    def measure(client, tag):
+        save_ms, hashes = [], None
+        for r in range(reps + 1):
+            hashes = [hashlib.sha256(tag + b"%d-" % r + i.to_bytes(8, "little")).digest()
+                      for i in ids_l]
+            t0 = time.perf_counter()
+            ok, msg = client.save("bench", 0, 0, [(n, ids_l, hashes) for n in names])
+            save_ms.append((time.perf_counter() - t0) * 1e3)
+            assert ok, msg
+        load_ms, first_ms, rpc_ms = [], [], []
+        for layered in (False, True):
+            for r in range(reps + 1):
+                st = PyLoadState(num_layers=len(names)) if layered else PyLoadState()
+                t0 = time.perf_counter()
+                ok, msg = client.load("bench", 0, 0, st.shm_name(), names, targets_l, hashes)
+                assert ok, msg
+                rpc_ms.append((time.perf_counter() - t0) * 1e3)
+                t_first = None
+                while not st.is_ready():
+                    if layered and t_first is None and st.layers_done() >= 1:
+                        t_first = time.perf_counter()
+                    if time.perf_counter() - t0 > 60:
+                        raise RuntimeError("two-process restore did not complete in 60 s")
+                t1 = time.perf_counter()
+                assert st.get_state() == 1
+                (first_ms if layered else load_ms).append(
+                    ((t_first or t1) - t0) * 1e3 if layered else (t1 - t0) * 1e3)
+        bad = wl.verify_restored(layers, ids, targets)
+        layers.refill()
+        return {"save_ms": round(med(save_ms), 2), "save_gbps": round(P / med(save_ms) / 1e6, 2),
+                "restore_ms": round(med(load_ms), 2),
+                "restore_gbps": round(P / med(load_ms) / 1e6, 2),
+                "first_layer_ms": round(med(first_ms), 3),
+                "load_request_return_ms": round(statistics.median(rpc_ms), 3),
+                "bit_exact": bad == 0}
+
     try:
         with EngineRpcClient(f"http://{addr}", connect_timeout_s=30) as client:
             t0 = time.perf_counter()
@@ -575,33 +619,10 @@ def leg_two_process(layers, ids, targets, P, reps=4):
                                                   shape.segments)
                 assert ok, msg
             out["register_ms"] = round((time.perf_counter() - t0) * 1e3, 1)
-            save_ms, hashes = [], None
-            for r in range(reps + 1):
-                hashes = [hashlib.sha256(b"rpc%d-" % r + i.to_bytes(8, "little")).digest()
-                          for i in ids_l]
-                t0 = time.perf_counter()
-                ok, msg = client.save("bench", 0, 0, [(n, ids_l, hashes) for n in names])
-                save_ms.append((time.perf_counter() - t0) * 1e3)
-                assert ok, msg
-            load_ms, first_ms, rpc_ms = [], [], []
-            for layered in (False, True):
-                for r in range(reps + 1):
-                    st = PyLoadState(num_layers=len(names)) if layered else PyLoadState()
-                    t0 = time.perf_counter()
-                    ok, msg = client.load("bench", 0, 0, st.shm_name(), names, targets_l, hashes)
-                    assert ok, msg
-                    rpc_ms.append((time.perf_counter() - t0) * 1e3)
-                    t_first = None
-                    while not st.is_ready():
-                        if layered and t_first is None and st.layers_done() >= 1:
-                            t_first = time.perf_counter()
-                        if time.perf_counter() - t0 > 60:
-                            raise RuntimeError("two-process restore did not complete in 60 s")
-                    t1 = time.perf_counter()
-                    assert st.get_state() == 1
-                    (first_ms if layered else load_ms).append(
-                        ((t_first or t1) - t0) * 1e3 if layered else (t1 - t0) * 1e3)
-            bad = wl.verify_restored(layers, ids, targets)
+            out.update(measure(client, b"rpc"))
+            with EngineRpcClient(f"http://{addr}", connect_timeout_s=30,
+                                 fast_socket=sock) as fast:
+                out["fast_path"] = measure(fast, b"fast")
             ok, msg = client.unregister_context("bench")
             assert ok, msg
             client.shutdown()
@@ -610,14 +631,8 @@ def leg_two_process(layers, ids, targets, P, reps=4):
         if p.poll() is None:
             p.kill()
             p.wait(10)
-    layers.refill()
-    med = lambda v: statistics.median(v[1:])  # noqa: E731
-    out.update({"save_ms": round(med(save_ms), 2), "save_gbps": round(P / med(save_ms) / 1e6, 2),
-                "restore_ms": round(med(load_ms), 2),
-                "restore_gbps": round(P / med(load_ms) / 1e6, 2),
-                "first_layer_ms": round(med(first_ms), 2),
-                "load_rpc_return_ms": round(statistics.median(rpc_ms), 3),
-                "bit_exact": bad == 0})
+        shutil.rmtree(os.path.dirname(sock), ignore_errors=True)
+    out["bit_exact"] = out["bit_exact"] and out["fast_path"]["bit_exact"]
     return out
 
 
@@ -726,7 +741,6 @@ def leg_disk(layers, ids, targets, P):
     dropped from the page cache); a fresh engine on the same directory reads
     it back into its pool on a prefix query and loads it into HBM."""
     import hashlib
-    import shutil
     import tempfile
 
     from pegaflow_amd import workload as wl

@@ -646,6 +646,28 @@ int pf_engine_stats_get(pf_engine* e, pf_engine_stats* out);
 int pf_engine_wait_idle(pf_engine* e);
 
 /* ------------------------------------------------------------------------ */
+/* Native endpoint for the per-step requests (no counterpart in the          */
+/* reference, whose server is native: service.rs:133-405).  Serves Load,     */
+/* Save and Health for an engine from the library's own threads on a         */
+/* Unix-domain socket, bypassing a Python gRPC stack.  Frames, little endian: */
+/* request = u32 length of what follows, u8 method, then the engine.proto    */
+/* LoadRequest / SaveRequest bytes (none for Health); reply = u32 length,    */
+/* u8 status (PF_OK or PF_ERR_*), then the error message.  Requests mean     */
+/* what the gRPC service's Load and Save mean (service.rs:184-250).          */
+/* ------------------------------------------------------------------------ */
+enum { PF_FAST_LOAD = 1, PF_FAST_SAVE = 2, PF_FAST_HEALTH = 3 };
+#define PF_FAST_MAX_FRAME (256u << 20)
+typedef struct pf_fastpath pf_fastpath;
+/* Listens on socket_path (a stale socket file there is replaced; the file is
+ * created mode 0600 and removed at stop). */
+int pf_fastpath_start(pf_engine* engine, const char* socket_path,
+                      pf_fastpath** out);
+/* Stops listening, closes every connection and waits for their threads. */
+int pf_fastpath_stop(pf_fastpath* fastpath);
+/* Requests served so far. */
+uint64_t pf_fastpath_served(const pf_fastpath* fastpath);
+
+/* ------------------------------------------------------------------------ */
 /* Disk tier.  Replaces the DFS offload and prefetch of seal_offload.rs and   */
 /* the Redis index behind it (BlockMeta, seal_offload.rs:72-97) with packed   */
 /* files "<root>/<namespace>/<uuid>.bin" plus a "<uuid>.json" sidecar each.   */

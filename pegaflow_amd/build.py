@@ -26,6 +26,7 @@ SOURCES = [
     "pf_load_state.cpp",
     "pf_engine.cpp",
     "pf_disk.cpp",
+    "pf_fastpath.cpp",
 ]
 
 # Packed-FP32 instructions are disabled for all device code (this library

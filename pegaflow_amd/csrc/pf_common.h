@@ -3,7 +3,9 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <chrono>
 #include <cstdint>
+#include <functional>
 #include <mutex>
 #include <string>
 #include <utility>
@@ -18,6 +20,14 @@ void set_error(const std::string& msg);
 void clear_error();
 int fail(int code, const std::string& msg);
 std::string strf(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+
+// Per-call phase timings on stderr when PEGAFLOW_TRACE is set (the role of
+// the reference's tracing spans and per-task GB/s logs, gpu_worker.rs:293-314);
+// absolute times are CLOCK_MONOTONIC microseconds, comparable across the
+// processes of one host.
+bool tracing();
+double mono_us(std::chrono::steady_clock::time_point t);
+long thread_minor_faults();  // of the calling thread, for traces
 
 // Returns PF_ERR_HIP with "<what> failed: <hip error string>" on error.
 int hip_fail(hipError_t e, const char* what);
@@ -155,6 +165,29 @@ int noalloc_scratch(int device, NoAllocScratch** out);
 // copy and must not use the bytes before the wait.
 int save_layers_begin(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
                       uint32_t mode);
+
+// Layers [head, num_layers) of a load whose block lists another thread is
+// still building.  In kernel mode the call plans and issues layers
+// [0, head) first, then calls ready(), which returns PF_OK once every later
+// entry of the call's layer array holds its blocks (an error fails the call,
+// with the first part drained), and issues the rest; descriptor room for
+// the later layers is reserved beforehand from max_blocks, a bound on each
+// one's block count.  In the other modes, or with head 0, ready() is called
+// before anything is issued.
+struct PendingLayers {
+  uint32_t head = 0;
+  uint64_t max_blocks = 0;
+  std::function<int()> ready;
+};
+// A load whose later layers are pending: layer_events as pf_load_layers',
+// signals as pf_load_layers_marked's (num_signals 0: no marks).
+int load_layers_pending(pf_xfer* x, pf_layer_xfer* layers, uint32_t num_layers, uint32_t mode,
+                        pf_event* layer_events, const pf_layer_signal* signals,
+                        uint32_t num_signals, const PendingLayers& pending);
+// The leading layers that a kernel-mode call over the host link of
+// num_layers layers and `chunks` chunks in all plans and issues before
+// planning the rest (0: the call is planned whole).
+uint32_t pipeline_head_layers(uint32_t num_layers, uint64_t chunks);
 
 // Writes the signal's value into all num_layers words on the context's
 // stream and waits: releases consumers of a load that failed before its

@@ -385,6 +385,7 @@ std::shared_ptr<SealedBlock> rebuild(const std::shared_ptr<PoolAllocation>& allo
     off += sm.size;
   }
   sb->footprint = off;
+  sb->index();
   return sb;
 }
 

@@ -103,10 +103,27 @@ struct LayerBlock {
   std::shared_ptr<PoolAllocation> v_alloc;
 };
 
+// One slot of a sealed block as a load reads it (size 0: no slot).
+struct SlotView {
+  const uint8_t* k_ptr = nullptr;
+  const uint8_t* v_ptr = nullptr;
+  uint64_t size = 0;
+};
+
 // All slots (layer x tp_rank) of one block hash, immutable once sealed.
+// `views` repeats each slot's pointers and size in one contiguous array,
+// built by index() when the block seals, so a load naming hundreds of blocks
+// and dozens of layers reads them in order instead of chasing one pointer
+// per (block, layer).
 struct SealedBlock {
   std::vector<std::shared_ptr<LayerBlock>> slots;
+  std::vector<SlotView> views;
   uint64_t footprint = 0;
+  void index() {
+    views.assign(slots.size(), SlotView{});
+    for (size_t s = 0; s < slots.size(); ++s)
+      if (slots[s]) views[s] = SlotView{slots[s]->k_ptr, slots[s]->v_ptr, slots[s]->size};
+  }
 };
 
 struct InflightBlock {

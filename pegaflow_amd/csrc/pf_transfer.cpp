@@ -362,6 +362,10 @@ struct pf_xfer {
   // The scatter route's choice between kScatterShapes (-1: still timing).
   ScatterTrial trials[2];
   int scatter_choice = -1;
+  // Per-layer plans of the call in progress (under mu), kept with their
+  // capacity for the next call: a call plans tens of thousands of chunks,
+  // and fresh buffers each time cost page faults before the first launch.
+  std::vector<LayerPlan> plans, plans_rest;
   std::mutex mu;
 };
 
@@ -990,6 +994,14 @@ int kernel_direct(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<Lay
 // first part, are issued whole, as one launch.
 constexpr uint64_t kPipelineMinChunks = 16384;
 
+}  // namespace
+
+uint32_t pf::pipeline_head_layers(uint32_t num_layers, uint64_t chunks) {
+  return num_layers < 8 || chunks < kPipelineMinChunks ? 0 : num_layers / 8;
+}
+
+namespace {
+
 uint32_t pipeline_head(const pf_layer_xfer* layers, uint32_t num_layers) {
   if (num_layers < 8) return 0;
   uint64_t chunks = 0;
@@ -999,14 +1011,17 @@ uint32_t pipeline_head(const pf_layer_xfer* layers, uint32_t num_layers) {
     if (!first && layers[i].num_blocks > 0 && layers[i].blocks) first = layers[i].blocks;
   }
   uint64_t b = 0, e = 0;
-  if (chunks < kPipelineMinChunks || !first || !pinned_lookup(first->k_host, 1, &b, &e)) return 0;
-  return num_layers / 8;
+  if (!first || !pinned_lookup(first->k_host, 1, &b, &e)) return 0;
+  return pipeline_head_layers(num_layers, chunks);
 }
 
+// pending: the layers from `head` on are filled in by pending->ready(),
+// called once the first part is issued.
 int kernel_pipelined(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
                      uint32_t head, bool is_save, bool wait_save, const SignalTargets* sig,
-                     pf_event* layer_events) {
-  std::vector<LayerPlan> first, rest;
+                     pf_event* layer_events, const PendingLayers* pending = nullptr) {
+  std::vector<LayerPlan>& first = x->plans;
+  std::vector<LayerPlan>& rest = x->plans_rest;
   if (int rc = plan_all(layers, head, is_save, &first)) return rc;
   for (uint32_t li = 0; li < head; ++li)
     apply_write_policy(layers[li], is_save, false, &first[li]);
@@ -1015,7 +1030,8 @@ int kernel_pipelined(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layer
   // growing the buffers later would wait for the first copy.
   uint64_t bound = 1 + 2 * ((2ull * num_layers + 1) * sizeof(uint32_t) / sizeof(ChunkDesc) + 1);
   for (uint32_t i = 0; i < num_layers; ++i)
-    bound += layers[i].num_blocks * (layers[i].layout.segments ? layers[i].layout.segments : 1);
+    bound += (pending && i >= head ? pending->max_blocks : layers[i].num_blocks) *
+             (layers[i].layout.segments ? layers[i].layout.segments : 1);
   if (int rc = ensure_desc_capacity(x, static_cast<size_t>(bound))) return rc;
   if (int rc = ensure_counters(x, num_layers)) return rc;  // marks of both parts
   PF_HIP(hipEventRecord(x->parts_ready, x->stream));
@@ -1025,6 +1041,8 @@ int kernel_pipelined(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layer
   if (int rc = kernel_direct(x, layers, first, is_save, layer_events, sig, false, 0, 0,
                              &n_first))
     return rc;
+  if (pending)
+    if (int rc = pending->ready()) return rc;
   int rc = plan_all(layers + head, num_layers - head, is_save, &rest);
   if (rc == PF_OK) {
     for (uint32_t li = head; li < num_layers; ++li)
@@ -1038,20 +1056,22 @@ int kernel_pipelined(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layer
 }
 
 int run_locked(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, uint32_t mode,
-               bool is_save, pf_event* layer_events, bool wait_save, const SignalTargets* sig);
+               bool is_save, pf_event* layer_events, bool wait_save, const SignalTargets* sig,
+               const PendingLayers* pending);
 
 // One transfer call.  A call that fails part-way returns with none of its
 // copies in flight, so the caller may reuse or free the buffers at once.
 int run(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, uint32_t mode,
         bool is_save, pf_event* layer_events, bool wait_save = true,
-        const SignalTargets* sig = nullptr) {
+        const SignalTargets* sig = nullptr, const PendingLayers* pending = nullptr) {
   if (!x) return fail(PF_ERR_INVALID_ARGUMENT, "null transfer context");
   if (num_layers > 0 && !layers) return fail(PF_ERR_INVALID_ARGUMENT, "null layer list");
   std::lock_guard<std::mutex> lk(x->mu);
   x->last_kernels = 0;
   x->last_dma = 0;
   PF_HIP(hipSetDevice(x->device));
-  const int rc = run_locked(x, layers, num_layers, mode, is_save, layer_events, wait_save, sig);
+  const int rc =
+      run_locked(x, layers, num_layers, mode, is_save, layer_events, wait_save, sig, pending);
   if (rc != PF_OK) {
     (void)hipStreamSynchronize(x->dma);
     (void)hipStreamSynchronize(x->stream);
@@ -1060,18 +1080,22 @@ int run(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, uint32_t m
 }
 
 int run_locked(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, uint32_t mode,
-               bool is_save, pf_event* layer_events, bool wait_save, const SignalTargets* sig) {
-  std::vector<LayerPlan> plans;
+               bool is_save, pf_event* layer_events, bool wait_save, const SignalTargets* sig,
+               const PendingLayers* pending) {
+  std::vector<LayerPlan>& plans = x->plans;
   if (mode == PF_MODE_KERNEL) {
     // A large call: its first layers are planned and launched before the
     // rest are planned, so the planning of the rest (about 3 ns a chunk)
     // overlaps their copy.  Marks carry call-wide layer indices; per-layer
     // events stay with their layers.
-    const uint32_t head = pipeline_head(layers, num_layers);
-    if (head > 0)
+    const uint32_t head = pending ? pending->head : pipeline_head(layers, num_layers);
+    if (head > 0 && head < num_layers)
       return kernel_pipelined(x, layers, num_layers, head, is_save, wait_save,
-                              is_save ? nullptr : sig, is_save ? nullptr : layer_events);
+                              is_save ? nullptr : sig, is_save ? nullptr : layer_events,
+                              pending);
   }
+  if (pending)
+    if (int rc = pending->ready()) return rc;
   if (int rc = plan_all(layers, num_layers, is_save, &plans)) return rc;
   switch (mode) {
     case PF_MODE_DMA_REFERENCE:
@@ -1099,6 +1123,42 @@ int run_locked(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, uin
     default:
       return fail(PF_ERR_INVALID_ARGUMENT, strf("unknown transfer mode %u", mode));
   }
+}
+
+// A marked load's signal targets, checked: 1..PF_MAX_LAYER_SIGNALS of them,
+// each with num_layers words the device may write.
+int signal_targets(const pf_layer_signal* signals, uint32_t num_signals, uint32_t num_layers,
+                   SignalTargets* out) {
+  if (num_signals == 0 || num_signals > PF_MAX_LAYER_SIGNALS || !signals)
+    return fail(PF_ERR_INVALID_ARGUMENT,
+                strf("a marked load takes 1..%d signal targets, got %u", PF_MAX_LAYER_SIGNALS,
+                     num_signals));
+  SignalTargets& t = *out;
+  RangeCache rc;
+  for (uint32_t i = 0; i < num_signals; ++i) {
+    const pf_layer_signal& g = signals[i];
+    if (g.value == 0 || g.reserved != 0 || g.host_memory > 1 || (g.words & 7u) != 0)
+      return fail(PF_ERR_INVALID_ARGUMENT,
+                  strf("signal target %u: words must be 8-byte aligned, value nonzero, "
+                       "host_memory 0 or 1",
+                       i));
+    // The kernels write these words: they must be mapped for the device.
+    if (num_layers > 0 && !rc.check(g.words, static_cast<uint64_t>(num_layers) * 8u))
+      return fail(PF_ERR_INVALID_ARGUMENT,
+                  strf("signal target %u: [0x%llx, +%llu) is not inside one device, IPC or "
+                       "pinned allocation",
+                       i, (unsigned long long)g.words,
+                       (unsigned long long)num_layers * 8ull));
+    t.words[i] = g.words;
+    t.value[i] = g.value;
+    // Words in pinned host memory get system-scope stores even when the
+    // caller did not say so: the host has to see them.
+    uint64_t pb = 0, pe = 0;
+    if (g.host_memory || (num_layers > 0 && pinned_lookup(g.words, 8, &pb, &pe)))
+      t.host_mask |= 1u << i;
+  }
+  t.count = num_signals;
+  return PF_OK;
 }
 
 }  // namespace
@@ -1506,36 +1566,23 @@ int pf_load_layers(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
 int pf_load_layers_marked(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
                           uint32_t mode, const pf_layer_signal* signals,
                           uint32_t num_signals) {
-  if (num_signals == 0 || num_signals > PF_MAX_LAYER_SIGNALS || !signals)
-    return fail(PF_ERR_INVALID_ARGUMENT,
-                strf("a marked load takes 1..%d signal targets, got %u", PF_MAX_LAYER_SIGNALS,
-                     num_signals));
   SignalTargets t{};
-  RangeCache rc;
-  for (uint32_t i = 0; i < num_signals; ++i) {
-    const pf_layer_signal& g = signals[i];
-    if (g.value == 0 || g.reserved != 0 || g.host_memory > 1 || (g.words & 7u) != 0)
-      return fail(PF_ERR_INVALID_ARGUMENT,
-                  strf("signal target %u: words must be 8-byte aligned, value nonzero, "
-                       "host_memory 0 or 1",
-                       i));
-    // The kernels write these words: they must be mapped for the device.
-    if (num_layers > 0 && !rc.check(g.words, static_cast<uint64_t>(num_layers) * 8u))
-      return fail(PF_ERR_INVALID_ARGUMENT,
-                  strf("signal target %u: [0x%llx, +%llu) is not inside one device, IPC or "
-                       "pinned allocation",
-                       i, (unsigned long long)g.words,
-                       (unsigned long long)num_layers * 8ull));
-    t.words[i] = g.words;
-    t.value[i] = g.value;
-    // Words in pinned host memory get system-scope stores even when the
-    // caller did not say so: the host has to see them.
-    uint64_t pb = 0, pe = 0;
-    if (g.host_memory || (num_layers > 0 && pinned_lookup(g.words, 8, &pb, &pe)))
-      t.host_mask |= 1u << i;
-  }
-  t.count = num_signals;
+  if (int rc = signal_targets(signals, num_signals, num_layers, &t)) return rc;
   return run(x, layers, num_layers, mode, false, nullptr, true, &t);
 }
 
 }  // extern "C"
+
+namespace pf {
+
+int load_layers_pending(pf_xfer* x, pf_layer_xfer* layers, uint32_t num_layers, uint32_t mode,
+                        pf_event* layer_events, const pf_layer_signal* signals,
+                        uint32_t num_signals, const PendingLayers& pending) {
+  SignalTargets t{};
+  if (num_signals > 0)
+    if (int rc = signal_targets(signals, num_signals, num_layers, &t)) return rc;
+  return run(x, layers, num_layers, mode, false, layer_events, true,
+             num_signals > 0 ? &t : nullptr, &pending);
+}
+
+}  // namespace pf

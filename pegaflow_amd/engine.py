@@ -166,8 +166,14 @@ class PegaEngine:
     def batch_load_kv_blocks(self, instance_id: str, tp_rank: int, device_id: int,
                              load_state_shm: str, layer_names: Sequence[str],
                              block_ids: Sequence[int], block_hashes: Sequence[bytes]) -> None:
-        """Queues a multi-layer load; completion is published in the LoadState."""
+        """Queues a multi-layer load; completion is published in the LoadState.
+        As in the reference (lib.rs:1008-1043), every hash is looked up and
+        ids pair with hashes up to the shorter list: extra hashes get id -1
+        (skipped), extra ids are dropped."""
         ids = np.ascontiguousarray(block_ids, dtype=np.int32)
+        if len(ids) != len(block_hashes):
+            ids = np.concatenate([ids[:len(block_hashes)],
+                                  np.full(max(0, len(block_hashes) - len(ids)), -1, np.int32)])
         data, offs = _hashes(block_hashes)
         # A connector names the same layers on every load: their C array is
         # built once (the bytes objects it points into are kept with it).
@@ -240,7 +246,28 @@ class PegaEngine:
     def wait_idle(self) -> None:
         _raise(lib().pf_engine_wait_idle(self._h))
 
+    # -- native endpoint for Load / Save (no counterpart in the reference) --
+    def start_fast_path(self, socket_path: str) -> None:
+        """Serves this engine's Load, Save and Health requests on a
+        Unix-domain socket from native threads (pf_fastpath_start): the
+        requests in engine.proto's encoding, without the Python gRPC stack.
+        Stopped by stop_fast_path or close."""
+        if getattr(self, "_fast", None):
+            raise RuntimeError("fast path already started")
+        h = ctypes.c_void_p()
+        _raise(lib().pf_fastpath_start(self._h, socket_path.encode(), ctypes.byref(h)))
+        self._fast = h.value
+
+    def stop_fast_path(self) -> None:
+        if getattr(self, "_fast", None):
+            lib().pf_fastpath_stop(self._fast)
+        self._fast = None
+
+    def fast_path_served(self) -> int:
+        return int(lib().pf_fastpath_served(self._fast)) if getattr(self, "_fast", None) else 0
+
     def close(self) -> None:
+        self.stop_fast_path()
         if self._h:
             lib().pf_engine_destroy(self._h)
         self._h = None

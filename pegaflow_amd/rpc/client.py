@@ -7,6 +7,11 @@ and a dict for query — so a connector written against it runs unchanged.
 
 from __future__ import annotations
 
+import operator
+import socket
+import struct
+import threading
+
 import grpc
 
 from . import proto
@@ -28,6 +33,38 @@ def _varint(n: int) -> bytes:
 _SAVES_TAG = _varint((proto.SaveRequest.DESCRIPTOR.fields_by_name["saves"].number << 3) | 2)
 
 
+def _ids_part(msg_cls, block_ids) -> bytes:
+    """The packed int32 block_ids field of `msg_cls` alone.  The message
+    takes ints and numpy integers as they are; other integer-like values
+    (bools) are converted first, and non-integers raise TypeError."""
+    if not isinstance(block_ids, (list, tuple)) and not hasattr(block_ids, "__array__"):
+        block_ids = list(block_ids)  # an iterator is read once
+    try:
+        return msg_cls(block_ids=block_ids).SerializeToString()
+    except TypeError:
+        return msg_cls(block_ids=[operator.index(i) for i in block_ids]).SerializeToString()
+
+
+def _hashes_part(msg_cls, block_hashes) -> bytes:
+    """The repeated bytes block_hashes field of `msg_cls` alone.  Hashes of
+    one length under 128 bytes (a one-byte length) share the two-byte
+    tag + length prefix, so the field is one join of the hashes; any other
+    list is serialized by the message."""
+    if not isinstance(block_hashes, (list, tuple)):
+        block_hashes = list(block_hashes)
+    if not block_hashes:
+        return b""
+    try:
+        size = len(block_hashes[0])
+        if size < 128 and set(map(len, block_hashes)) == {size}:
+            field = msg_cls.DESCRIPTOR.fields_by_name["block_hashes"].number
+            prefix = bytes(((field << 3) | 2, size))
+            return prefix + prefix.join(block_hashes)
+    except TypeError:
+        pass
+    return msg_cls(block_hashes=[bytes(h) for h in block_hashes]).SerializeToString()
+
+
 def encode_save_request(instance_id: str, tp_rank: int, device_id: int, saves) -> bytes:
     """SaveRequest wire bytes for [(layer_name, block_ids, block_hashes)].
 
@@ -44,12 +81,76 @@ def encode_save_request(instance_id: str, tp_rank: int, device_id: int, saves) -
         key = (id(block_ids), id(block_hashes))
         hit = bodies.get(key)
         if hit is None or hit[0] is not block_ids or hit[1] is not block_hashes:
-            body = proto.SaveLayer(block_ids=[int(i) for i in block_ids],
-                                   block_hashes=[bytes(h) for h in block_hashes])
-            hit = bodies[key] = (block_ids, block_hashes, body.SerializeToString())
+            body = (_ids_part(proto.SaveLayer, block_ids) +
+                    _hashes_part(proto.SaveLayer, block_hashes))
+            hit = bodies[key] = (block_ids, block_hashes, body)
         layer = proto.SaveLayer(layer_name=layer_name).SerializeToString() + hit[2]
         parts += [_SAVES_TAG, _varint(len(layer)), layer]
     return b"".join(parts)
+
+
+_LAYER_NAMES_CACHE: dict = {}
+
+
+def encode_load_request(instance_id: str, tp_rank: int, device_id: int, load_state_shm: str,
+                        layer_names, block_ids, block_hashes) -> bytes:
+    """LoadRequest wire bytes.  A connector names the same layers on every
+    load, so the layer-name field is serialized once per name list (cached)
+    and concatenated with the rest (serialized parts of one message
+    concatenate into the message with all the fields)."""
+    names = tuple(layer_names)
+    named = _LAYER_NAMES_CACHE.get(names)
+    if named is None:
+        if len(_LAYER_NAMES_CACHE) >= 64:
+            _LAYER_NAMES_CACHE.clear()
+        named = _LAYER_NAMES_CACHE[names] = proto.LoadRequest(
+            layer_names=list(names)).SerializeToString()
+    head = proto.LoadRequest(instance_id=instance_id, tp_rank=tp_rank, device_id=device_id,
+                             load_state_shm=load_state_shm).SerializeToString()
+    return (head + named + _ids_part(proto.LoadRequest, block_ids) +
+            _hashes_part(proto.LoadRequest, block_hashes))
+
+
+# Engine status -> the gRPC status the service reports it as (service.rs:77-88).
+_STATUS_NAMES = {1: "INVALID_ARGUMENT", 4: "FAILED_PRECONDITION", 5: "FAILED_PRECONDITION",
+                 6: "FAILED_PRECONDITION"}
+
+
+class FastChannel:
+    """A connection to a server's native endpoint (pf_fastpath_start): Load,
+    Save and Health requests in engine.proto's encoding, framed as u32
+    length + u8 method, answered with u32 length + u8 status + message.
+    One request at a time per channel (a lock)."""
+
+    def __init__(self, path: str, timeout_s: float | None = None):
+        self._sock = socket.socket(socket.AF_UNIX, socket.SOCK_STREAM)
+        self._sock.settimeout(timeout_s)
+        try:
+            self._sock.connect(path)
+        except OSError as e:
+            self._sock.close()
+            raise RuntimeError(f"failed to connect to the fast endpoint {path}: {e}") from None
+        self._lock = threading.Lock()
+
+    def _recv(self, n: int) -> bytes:
+        out = bytearray()
+        while len(out) < n:
+            chunk = self._sock.recv(n - len(out))
+            if not chunk:
+                raise RuntimeError("fast endpoint closed the connection")
+            out += chunk
+        return bytes(out)
+
+    def call(self, method: int, payload: bytes = b"") -> tuple[int, str]:
+        frame = struct.pack("<IB", len(payload) + 1, method) + payload
+        with self._lock:
+            self._sock.sendall(frame)
+            length, status = struct.unpack("<IB", self._recv(5))
+            message = self._recv(length - 1).decode("utf-8", "replace")
+        return status, message
+
+    def close(self) -> None:
+        self._sock.close()
 
 
 def _serialize(request) -> bytes:
@@ -69,8 +170,14 @@ class EngineRpcClient:
     does not answer within `connect_timeout_s`.  `endpoint` is
     "http://host:port" or "host:port"."""
 
+    _fast: FastChannel | None = None  # the native endpoint's connection, if any
+
     def __init__(self, endpoint: str | None = None, timeout_s: float | None = None,
-                 connect_timeout_s: float = 2.0):
+                 connect_timeout_s: float = 2.0, fast_socket: str | None = None):
+        """``fast_socket`` (no counterpart in the reference): the server's
+        native endpoint (pegaflow-server --fast-socket); load, save and health
+        then go there, with the same results and errors, and everything else
+        over gRPC."""
         self._endpoint = endpoint or "http://127.0.0.1:50055"
         self.timeout_s = timeout_s
         self._channel = grpc.insecure_channel(
@@ -89,9 +196,30 @@ class EngineRpcClient:
                                            request_serializer=_serialize,
                                            response_deserializer=proto.messages[resp].FromString)
             for rpc, req, resp in proto.METHODS}
+        if fast_socket:
+            try:
+                self._fast = FastChannel(fast_socket, timeout_s)
+            except RuntimeError:
+                self._channel.close()
+                raise
 
     def close(self) -> None:
+        if self._fast is not None:
+            self._fast.close()
         self._channel.close()
+
+    def _fast_call(self, method: str, method_id: int, payload: bytes = b""):
+        """(ok, message) from the native endpoint; engine errors raise as the
+        gRPC path raises them."""
+        try:
+            status, message = self._fast.call(method_id, payload)
+        except OSError as e:
+            raise RuntimeError(f"{method} RPC failed: {e}") from None
+        if status == 0:
+            return True, ""
+        code = _STATUS_NAMES.get(status, "INTERNAL")
+        raise RuntimeError(f"{method} RPC failed: status: StatusCode.{code}, "
+                           f"message: {message!r}")
 
     def __enter__(self):
         return self
@@ -117,6 +245,8 @@ class EngineRpcClient:
         return self._endpoint
 
     def health(self):
+        if self._fast is not None:
+            return self._fast_call("health", 3)
         return self._status("health", self._call("Health", "health", proto.HealthRequest()))
 
     def register_context(self, instance_id: str, namespace: str, tp_rank: int, tp_size: int,
@@ -135,15 +265,17 @@ class EngineRpcClient:
     def save(self, instance_id: str, tp_rank: int, device_id: int, saves):
         """python/src/lib.rs:374-405: `saves` is [(layer_name, block_ids, block_hashes)]."""
         req = encode_save_request(instance_id, tp_rank, device_id, saves)
+        if self._fast is not None:
+            return self._fast_call("save", 2, req)
         return self._status("save", self._call("Save", "save", req))
 
     def load(self, instance_id: str, tp_rank: int, device_id: int, load_state_shm: str,
              layer_names, block_ids, block_hashes):
         """python/src/lib.rs:417-446."""
-        req = proto.LoadRequest(instance_id=instance_id, tp_rank=tp_rank, device_id=device_id,
-                                load_state_shm=load_state_shm, layer_names=list(layer_names),
-                                block_ids=list(block_ids),
-                                block_hashes=[bytes(h) for h in block_hashes])
+        req = encode_load_request(instance_id, tp_rank, device_id, load_state_shm, layer_names,
+                                  block_ids, block_hashes)
+        if self._fast is not None:
+            return self._fast_call("load", 1, req)
         return self._status("load", self._call("Load", "load", req))
 
     def query(self, instance_id: str, block_hashes):

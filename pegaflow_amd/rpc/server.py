@@ -150,11 +150,16 @@ class Server:
     def __init__(self, addr: str = "127.0.0.1:50055", engine: PegaEngine | None = None,
                  pool_size: int = 30 << 30, host_pool: bool = False, unit_size_hint: int = 0,
                  max_workers: int = 16, dfs_root: str | None = None,
-                 dfs_quota: int = 50 << 30, dfs_io_threads: int = 4):
+                 dfs_quota: int = 50 << 30, dfs_io_threads: int = 4,
+                 fast_socket: str | None = None):
         self.engine = engine or PegaEngine(pool_size=pool_size, host_pool=host_pool,
                                            unit_size_hint=unit_size_hint)
         if dfs_root:
             self.engine.enable_disk(dfs_root, quota_bytes=dfs_quota, io_threads=dfs_io_threads)
+        # Load, Save and Health also on a native Unix-socket endpoint.
+        self.fast_socket = fast_socket
+        if fast_socket:
+            self.engine.start_fast_path(fast_socket)
         self.service = EngineService(self.engine, disk=bool(dfs_root))
         self.grpc = grpc.server(futures.ThreadPoolExecutor(max_workers=max_workers),
                                 options=[("grpc.max_receive_message_length", 256 << 20),
@@ -175,6 +180,7 @@ class Server:
             pass
 
     def stop(self, grace: float = 1.0) -> None:
+        self.engine.stop_fast_path()
         self.grpc.stop(grace).wait()
         self.service.frontend.close()
         self.engine.close()
@@ -198,6 +204,9 @@ def parse_args(argv=None):
                     help="allocation unit of the pinned pool")
     ap.add_argument("--log-level", default="info")
     ap.add_argument("--max-workers", type=int, default=16)
+    ap.add_argument("--fast-socket", default=None,
+                    help="also serve Load, Save and Health natively on this Unix-domain "
+                         "socket path (EngineRpcClient(fast_socket=...))")
     ap.add_argument("--dfs-root", default=None,
                     help="directory of the disk tier (packed block files); the tier is on when "
                          f"this or --redis-url is given (default root {DEFAULT_DFS_ROOT})")
@@ -245,7 +254,8 @@ def main(argv=None) -> int:
     runtime.init(args.device)
     server = Server(args.addr, pool_size=args.pool_size, unit_size_hint=args.hint_value_size,
                     max_workers=args.max_workers, dfs_root=args.dfs_root,
-                    dfs_quota=args.dfs_quota, dfs_io_threads=args.dfs_io_threads).start()
+                    dfs_quota=args.dfs_quota, dfs_io_threads=args.dfs_io_threads,
+                    fast_socket=args.fast_socket).start()
     for sig in (signal.SIGINT, signal.SIGTERM):
         signal.signal(sig, lambda *_: server.service.shutdown_event.set())
     print(f"READY {server.addr}", flush=True)

@@ -42,7 +42,7 @@ class Model:
     engine as instance `inst` (tp_rank of tp_size)."""
 
     def __init__(self, engine, inst, n_layers, nb, bpb, seed=1, tp_rank=0, tp_size=1,
-                 prefix="layer"):
+                 prefix="layer", total_layers=None):
         self.nb, self.bpb, self.n_layers = nb, bpb, n_layers
         self.kv = nb * bpb
         self.size = 2 * self.kv
@@ -54,7 +54,8 @@ class Model:
             b.fill_random(self.seeds[l])
             self.bufs.append(b)
             engine.register_context_layer(inst, "ns", 0, self.names[l], b.ptr, self.size, nb, bpb,
-                                          self.kv, 2, tp_rank, tp_size, n_layers)
+                                          self.kv, 2, tp_rank, tp_size,
+                                          total_layers or n_layers)
 
     def host_copies(self):
         return [b.download() for b in self.bufs]
@@ -442,3 +443,91 @@ def test_local_layer_events_gate_consumer_per_layer(engine):
         for s in snaps:
             s.close()
         m.close()
+
+
+@pytest.mark.parametrize("completion", ["plain", "layered", "events"])
+def test_split_load_matches_oracle(engine, completion):
+    """A load of 8 layers x 1024 split blocks (16384 chunks) is split: the
+    lists of its first two layers are submitted while the others are built,
+    and the transfer issues them once they are published.  Bytes against the
+    oracle for each way the load thread publishes completion."""
+    from pegaflow_amd.runtime import Event, Stream
+
+    say(f"[gpu] engine split load ({completion})")
+    engine.set_transfer_modes(_lib.MODE_KERNEL, _lib.MODE_KERNEL)
+    m = Model(engine, "split", 8, 2100, 1024, seed=41)
+    evs = [Event() for _ in range(m.n_layers)] if completion == "events" else None
+    stream = Stream() if completion == "events" else None
+    try:
+        orig = m.host_copies()
+        perm = np.random.default_rng(41).permutation(2100)
+        ids, targets = [int(i) for i in perm[:1024]], [int(i) for i in perm[1024:2048]]
+        hashes = [h(i, b"split") for i in ids]
+        engine.batch_save_kv_blocks("split", 0, 0, [(n, ids, hashes) for n in m.names])
+        exp = expected_after_load(m, orig, ids, targets)
+        for l, b in enumerate(m.bufs):
+            b.fill_random(m.seeds[l])
+        if completion == "plain":
+            st = PyLoadState()
+        elif completion == "layered":
+            st = PyLoadState(num_layers=m.n_layers)
+        else:
+            st = PyLoadState(num_layers=m.n_layers, layer_events=evs)
+        engine.batch_load_kv_blocks("split", 0, 0, st.shm_name(), m.names, targets, hashes)
+        if completion == "events":
+            for l in range(m.n_layers):
+                assert st.wait_for_layer_on_device(l, lambda i: stream.wait_event(evs[i]))
+            stream.synchronize()
+        assert wait(st) == 1
+        if completion != "plain":
+            assert st.layers_done() == m.n_layers
+        got = m.host_copies()
+        for l in range(m.n_layers):
+            assert np.array_equal(got[l], exp[l]), f"layer {l}"
+    finally:
+        if stream is not None:
+            stream.close()
+        m.close()
+
+
+def test_split_load_error_in_later_layers(engine):
+    """A split load whose later layer is registered with another block size
+    than the stored blocks hold: the call fails with the size message after
+    the first layer was submitted, the LoadState reads failed, the later
+    layers' destinations are untouched and the load thread serves the next
+    load (the first layer may have been copied already)."""
+    say("[gpu] engine split load: error in a later layer")
+    engine.set_transfer_modes(_lib.MODE_KERNEL, _lib.MODE_KERNEL)
+    a = Model(engine, "splita", 8, 2100, 2048, seed=43)
+    b = odd = None
+    try:
+        ids = list(range(1024))
+        hashes = [h(i, b"splite") for i in ids]
+        engine.batch_save_kv_blocks("splita", 0, 0, [(n, ids, hashes) for n in a.names])
+        # Instance b shares the namespace; its layer 7 holds 1024-byte halves.
+        # With 4096-byte blocks the first part is layer 0 alone.
+        b = Model(engine, "splitb", 7, 2100, 2048, seed=44, prefix="b", total_layers=8)
+        odd = DeviceBuffer(2 * 2100 * 1024)
+        odd.fill_random(45)
+        engine.register_context_layer("splitb", "ns", 0, "b.7", odd.ptr, 2 * 2100 * 1024, 2100,
+                                      1024, 2100 * 1024, 2, 0, 1, 8)
+        names = b.names + ["b.7"]
+        before = [x.download() for x in b.bufs[1:]] + [odd.download()]
+        targets = list(range(1024, 2048))
+        st = PyLoadState(num_layers=8)
+        with pytest.raises(RuntimeError, match="holds 4096 split bytes for layer b.7, which is "
+                                               "registered with 2048 split bytes"):
+            engine.batch_load_kv_blocks("splitb", 0, 0, st.shm_name(), names, targets, hashes)
+        assert wait(st) == -1
+        after = [x.download() for x in b.bufs[1:]] + [odd.download()]
+        assert all(np.array_equal(x, y) for x, y in zip(before, after))
+        # The worker is free: a load of the matching layers completes.
+        st = PyLoadState()
+        engine.batch_load_kv_blocks("splitb", 0, 0, st.shm_name(), b.names, targets, hashes)
+        assert wait(st) == 1
+    finally:
+        a.close()
+        if b is not None:
+            b.close()
+        if odd is not None:
+            odd.close()

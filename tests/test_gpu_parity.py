@@ -22,7 +22,7 @@ import pytest
 
 import oracle
 from pegaflow_amd import _lib
-from pegaflow_amd.runtime import (DeviceBuffer, Event, PinnedBuffer, Stream, spin,
+from pegaflow_amd.runtime import (DeviceBuffer, Event, PinnedBuffer, Stream, memcpy_async, spin,
                                   verify_random_chunks)
 from pegaflow_amd.transfer import (KVCacheRegistration, LayerTransfer, TransferContext,
                                    block_array)
@@ -571,22 +571,36 @@ def test_layerwise_load_events_qwen3(ctx):
     saved, _ = save_transfers(layers, ids.tolist(), host)
     ctx.save_layers(saved, _lib.MODE_KERNEL)
     compute = Stream()
+    # Layer l is copied on the compute stream right after its wait: an event
+    # recorded for the wrong layer, or before its layer's copy, leaves a
+    # snapshot without all of its restored blocks.
+    snaps = [DeviceBuffer(layers.size) for _ in range(n_layers)]
+    bpb, kv = layers.bpb, layers.kv
     for mode in (_lib.MODE_KERNEL, _lib.MODE_STAGED, _lib.MODE_DMA_BATCHED):
         evs = [Event() for _ in range(n_layers)]
         done = [Event() for _ in range(n_layers)]
         ctx.load_layers(load_transfers(layers, targets, saved), mode, layer_events=evs)
         for l in range(n_layers):
             compute.wait_event(evs[l])
+            memcpy_async(snaps[l].ptr, layers.bufs[l].ptr, layers.size, compute)
             spin(compute, 50)
             done[l].record(compute)
         compute.synchronize()
         ctx.synchronize()
         for l in range(1, n_layers):
             assert evs[l - 1].elapsed_ms(evs[l]) >= 0.0
+        t64, s64 = targets.astype(np.uint64), ids.astype(np.uint64)
+        for l in range(n_layers):
+            addrs = np.concatenate([snaps[l].ptr + t64 * bpb, snaps[l].ptr + kv + t64 * bpb])
+            offs = np.concatenate([s64 * bpb // 8, (kv + s64 * bpb) // 8])
+            assert verify_random_chunks(addrs, offs, bpb, layers.seeds[l]) == 0, \
+                f"mode {mode}: layer {l}'s snapshot after its event misses restored bytes"
         src_of = {int(t): int(s) for t, s in zip(targets, ids)}
         assert closed_form_tensor_check(layers, src_of) == 0
         for l in range(n_layers):  # restore the targets for the next mode
             layers.bufs[l].fill_random(layers.seeds[l])
+    for b in snaps:
+        b.close()
     compute.close()
     layers.close()
     host.close()

@@ -9,6 +9,8 @@ protobuf wire format (tag = field << 3 | wire type; packed varints for
 repeated int32; two's-complement 10-byte varints for negative int32).
 """
 
+import os
+
 import grpc
 import pytest
 
@@ -387,3 +389,137 @@ def test_save_request_decoder_matches_the_full_parse():
             proto.SaveRequest.FromString(bad)
         with pytest.raises(DecodeError):
             proto.decode_save_request(bad)
+
+
+# ---------------------------------------------------------------------------
+# The native endpoint for Load, Save and Health (pf_fastpath_start).
+# ---------------------------------------------------------------------------
+@pytest.fixture
+def served_fast(tmp_path):
+    path = str(tmp_path / "pf.sock")
+    srv = Server("127.0.0.1:0", engine=PegaEngine(pool_size=64 << 20, host_pool=True),
+                 fast_socket=path).start()
+    slow = EngineRpcClient(f"http://{srv.addr}")
+    fast = EngineRpcClient(f"http://{srv.addr}", fast_socket=path)
+    yield srv, slow, fast, path
+    fast.close()
+    slow.close()
+    srv.stop()
+    assert not os.path.exists(path)  # removed at stop
+
+
+def _error(fn):
+    with pytest.raises(RuntimeError) as e:
+        fn()
+    return str(e.value)
+
+
+def test_fast_path_gives_the_grpc_results_and_errors(served_fast):
+    srv, slow, fast, _ = served_fast
+    assert fast.health() == (True, "")
+    _register(slow, "l0")
+    _register(slow, "l1")
+    cases = [
+        lambda c: c.save("i0", 0, 0, [("l0", [16], [b"h"])]),                 # id out of range
+        lambda c: c.save("i0", 0, 0, [("l0", [1, 2], [b"h"])]),               # length mismatch
+        lambda c: c.save("i0", 0, 0, [("l1", [3], [b"h"])]),                  # host pool
+        lambda c: c.save("zz", 0, 0, [("l0", [1], [b"h"])]),                  # no instance
+        lambda c: c.save("i0", 0, 0, [("nope", [1], [b"h"])]),                # unknown layer
+        lambda c: c.load("zz", 0, 0, PyLoadState().shm_name(), ["l0"], [1], [b"a"]),
+        lambda c: c.load("i0", 0, 0, PyLoadState().shm_name(), ["l0"], [1], [b"abc"]),
+        # More hashes than ids: every hash is still looked up (lib.rs:1008-1011).
+        lambda c: c.load("i0", 0, 0, PyLoadState().shm_name(), ["l0"], [], [b"abc"]),
+        lambda c: c.load("i0", 0, 0, "pega_load_missing", ["l0"], [1], [b"a"]),
+    ]
+    for i, case in enumerate(cases):
+        want = _error(lambda: case(slow))
+        assert _error(lambda: case(fast)) == want, f"case {i}: {want}"
+    assert "INVALID_ARGUMENT" in _error(lambda: cases[0](fast))
+    assert "block_ids length 2 does not match block_hashes 1" in _error(lambda: cases[1](fast))
+    assert "FAILED_PRECONDITION" in _error(lambda: cases[3](fast))
+    # Negative ids only, and an empty load: nothing to do, the same on both.
+    assert fast.save("i0", 0, 0, [("l0", [-1], [b"a"])]) == (True, "")
+    st = PyLoadState()
+    assert fast.load("i0", 0, 0, st.shm_name(), ["l0"], [], []) == (True, "")
+    assert st.get_state() == 1
+    st = PyLoadState()
+    with pytest.raises(RuntimeError, match="missing KV block hash"):
+        fast.load("i0", 0, 0, st.shm_name(), ["l0"], [1], [b"abc"])
+    assert st.get_state() == -1  # the failure reaches the LoadState
+    assert srv.engine.fast_path_served() >= len(cases) + 4
+
+
+def _varint(n):
+    n &= (1 << 64) - 1
+    out = bytearray()
+    while True:
+        b, n = n & 0x7F, n >> 7
+        if not n:
+            out.append(b)
+            return bytes(out)
+        out.append(b | 0x80)
+
+
+def _field(num, wt, payload):
+    if wt == 0:
+        return _varint(num << 3) + _varint(payload)
+    return _varint(num << 3 | wt) + (_varint(len(payload)) + payload if wt == 2 else payload)
+
+
+def _raw(path, method, payload, raw_len=None):
+    import socket
+    import struct
+
+    s = socket.socket(socket.AF_UNIX, socket.SOCK_STREAM)
+    s.settimeout(10)
+    s.connect(path)
+    n = len(payload) + 1 if raw_len is None else raw_len
+    s.sendall(struct.pack("<IB", n, method) + payload)
+    hdr = b""
+    while len(hdr) < 5:
+        chunk = s.recv(5 - len(hdr))
+        if not chunk:
+            s.close()
+            return None
+        hdr += chunk
+    length, status = struct.unpack("<IB", hdr)
+    msg = b""
+    while len(msg) < length - 1:
+        msg += s.recv(length - 1 - len(msg))
+    s.close()
+    return status, msg.decode()
+
+
+def test_fast_path_decodes_every_encoding(served_fast):
+    """Hand-built requests: fields out of order, ids packed and unpacked,
+    negative ids as 10-byte varints, unknown fields of every wire type; and
+    malformed, unknown and oversized requests get error replies."""
+    srv, slow, fast, path = served_fast
+    _register(slow, "l0")
+    _register(slow, "l1")
+    layer = (_field(3, 2, b"h1") + _field(2, 0, 5) + _field(2, 0, -3) + _field(1, 2, b"l0") +
+             _field(3, 2, b"h2") + _field(3, 2, b"h3") + _field(2, 2, _varint(16)) +
+             _field(9, 0, 7) + _field(10, 1, b"\0" * 8) + _field(11, 5, b"\0" * 4))
+    req = _field(4, 2, layer) + _field(3, 0, 0) + _field(1, 2, b"i0") + _field(2, 0, 0)
+    status, msg = _raw(path, 2, req)
+    # ids [5, -3, 16]: the negative id is skipped, 16 is out of range on l0.
+    assert status == 1 and msg == "invalid argument: block 16 out of range for layer l0 " \
+                                  "(16 blocks registered)"
+    load = (_field(7, 2, b"zz") + _field(5, 2, b"l1") + _field(1, 2, b"i0") +
+            _field(6, 2, _varint(1) + _varint(-2)) + _field(4, 2, b"pega_load_x") +
+            _field(12, 2, b"ignored"))
+    status, msg = _raw(path, 1, load)
+    assert status != 0 and "LoadState" in msg  # decoded through to the shm attach
+    st = PyLoadState()
+    load = (_field(5, 2, b"l1") + _field(1, 2, b"i0") + _field(7, 2, b"a") +
+            _field(6, 0, 3) + _field(4, 2, st.shm_name().encode()) + _field(7, 2, b"b"))
+    status, msg = _raw(path, 1, load)
+    assert status == 3 and "missing KV block hash at index 0" in msg
+    assert st.get_state() == -1
+    # Malformed: a length running past the message, a group wire type.
+    assert _raw(path, 2, _field(1, 2, b"i0")[:-1]) == (1, "malformed SaveRequest")
+    assert _raw(path, 1, _varint(1 << 3 | 3)) == (1, "malformed LoadRequest")
+    assert _raw(path, 9, b"") == (1, "unknown method 9")
+    status, msg = _raw(path, 1, b"", raw_len=(256 << 20) + 2)
+    assert status == 1 and "exceeds" in msg
+    assert fast.health() == (True, "")  # the endpoint still serves

@@ -118,9 +118,9 @@ def test_in_process_server_round_trip(gpu):
         layers.close()
 
 
-def _start_server():
+def _start_server(*extra):
     cmd = [sys.executable, "-u", "-m", "pegaflow_amd.rpc.server", "--addr", "127.0.0.1:0",
-           "--pool-size", "128mb", "--log-level", "warning"]
+           "--pool-size", "128mb", "--log-level", "warning", *extra]
     p = subprocess.Popen(cmd, cwd=ROOT, stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
                          env=dict(os.environ), text=True)
     t0 = time.monotonic()
@@ -153,6 +153,29 @@ def test_two_process_ipc_round_trip(gpu):
             round_trip(client, layers, handles)
             assert client.shutdown() == (True, "")
         assert p.wait(60) == 0
+    finally:
+        if p.poll() is None:
+            p.kill()
+            p.wait(10)
+        layers.close()
+
+
+def test_two_process_round_trip_over_the_native_endpoint(gpu, tmp_path):
+    """The same round trip with save, load and health over the server's
+    native endpoint (--fast-socket), registration and queries over gRPC."""
+    say("[gpu] rpc two-process round trip over the native endpoint")
+    layers = Layers(3, 64, 16 * 8 * 128 * 2, seed=13)
+    handles = [ipc.export_tensor(b.ptr, layers.size, 0) for b in layers.bufs]
+    sock = str(tmp_path / "pegaflow.sock")
+    p, addr = _start_server("--fast-socket", sock)
+    say(f"[gpu] server pid {p.pid} at {addr}, {sock}")
+    try:
+        with EngineRpcClient(f"http://{addr}", connect_timeout_s=10, fast_socket=sock) as client:
+            assert client.health() == (True, "")
+            round_trip(client, layers, handles)
+            assert client.shutdown() == (True, "")
+        assert p.wait(60) == 0
+        assert not os.path.exists(sock)
     finally:
         if p.poll() is None:
             p.kill()
