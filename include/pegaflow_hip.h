@@ -666,6 +666,13 @@ int pf_fastpath_start(pf_engine* engine, const char* socket_path,
 int pf_fastpath_stop(pf_fastpath* fastpath);
 /* Requests served so far. */
 uint64_t pf_fastpath_served(const pf_fastpath* fastpath);
+/* One request in the same encoding (method PF_FAST_*, the message bytes
+ * without the frame), served on the calling thread: what the endpoint does
+ * with a frame, for a server that receives the bytes itself (the gRPC
+ * service's Load and Save, service.rs:184-250).  A request that does not
+ * decode fails with PF_ERR_INVALID_ARGUMENT. */
+int pf_engine_serve_request(pf_engine* engine, uint32_t method,
+                            const uint8_t* request, uint64_t size);
 
 /* ------------------------------------------------------------------------ */
 /* Disk tier.  Replaces the DFS offload and prefetch of seal_offload.rs and   */

@@ -315,6 +315,7 @@ SIGNATURES = {
     "pf_fastpath_start": (i32, [vp, ctypes.c_char_p, pvp]),
     "pf_fastpath_stop": (i32, [vp]),
     "pf_fastpath_served": (u64, [vp]),
+    "pf_engine_serve_request": (i32, [vp, u32, ctypes.c_char_p, u64]),
     "pf_engine_stats_get": (i32, [vp, ctypes.POINTER(EngineStats)]),
     "pf_engine_wait_idle": (i32, [vp]),
     "pf_engine_enable_disk": (i32, [vp, cs, u64, u32, u32, u32]),

@@ -117,10 +117,44 @@ bool read_int32s(Wire& w, uint32_t wt, std::vector<int32_t>* out) {
   return true;
 }
 
+// UTF-8 as RFC 3629 defines it: no overlong forms, no surrogates, nothing
+// above U+10FFFF.  A proto3 string field must hold it (a decoder refuses the
+// message otherwise, as prost and protobuf's own parsers do).
+bool valid_utf8(const uint8_t* p, size_t n) {
+  size_t i = 0;
+  while (i < n) {
+    const uint8_t c = p[i];
+    if (c < 0x80) {
+      ++i;
+      continue;
+    }
+    size_t len = 0;
+    uint8_t lo = 0x80, hi = 0xBF;  // allowed range of the second byte
+    if (c >= 0xC2 && c <= 0xDF) {
+      len = 2;
+    } else if (c >= 0xE0 && c <= 0xEF) {
+      len = 3;
+      if (c == 0xE0) lo = 0xA0;  // overlong
+      if (c == 0xED) hi = 0x9F;  // surrogates
+    } else if (c >= 0xF0 && c <= 0xF4) {
+      len = 4;
+      if (c == 0xF0) lo = 0x90;  // overlong
+      if (c == 0xF4) hi = 0x8F;  // above U+10FFFF
+    } else {
+      return false;
+    }
+    if (n - i < len || p[i + 1] < lo || p[i + 1] > hi) return false;
+    for (size_t k = 2; k < len; ++k)
+      if ((p[i + k] & 0xC0) != 0x80) return false;
+    i += len;
+  }
+  return true;
+}
+
 bool read_string(Wire& w, uint32_t wt, std::string* out) {
   const uint8_t* p = nullptr;
   size_t n = 0;
-  if (wt != 2 || !w.bytes(&p, &n)) return false;
+  if (wt != 2 || !w.bytes(&p, &n) || !valid_utf8(p, n)) return false;
   out->assign(reinterpret_cast<const char*>(p), n);
   return true;
 }
@@ -145,7 +179,7 @@ struct Hashes {
 // engine.proto LoadRequest (fields as in pegaflow_amd/rpc/proto.py).
 struct LoadReq {
   std::string instance_id, load_state_shm;
-  uint64_t tp_rank = 0, device_id = 0;
+  uint64_t tp_rank = 0, device_id = 0;  // uint32 and int32 fields: truncated at use
   std::vector<std::string> layer_names;
   std::vector<int32_t> block_ids;
   Hashes hashes;
@@ -241,7 +275,7 @@ int serve_load(pf_engine* e, const uint8_t* p, size_t n) {
   std::vector<const char*> names;
   names.reserve(r.layer_names.size());
   for (const std::string& s : r.layer_names) names.push_back(s.c_str());
-  return pf_engine_batch_load(e, r.instance_id.c_str(), r.tp_rank,
+  return pf_engine_batch_load(e, r.instance_id.c_str(), static_cast<uint32_t>(r.tp_rank),
                               static_cast<int>(static_cast<int32_t>(r.device_id)),
                               r.load_state_shm.c_str(), names.data(),
                               static_cast<uint32_t>(names.size()), r.block_ids.data(),
@@ -261,7 +295,7 @@ int serve_save(pf_engine* e, const uint8_t* p, size_t n) {
     layers.push_back(pf_save_layer{s.layer_name.c_str(), s.block_ids.data(), s.block_ids.size(),
                                    s.hashes.data.data(), s.hashes.offs.data()});
   }
-  return pf_engine_batch_save(e, r.instance_id.c_str(), r.tp_rank,
+  return pf_engine_batch_save(e, r.instance_id.c_str(), static_cast<uint32_t>(r.tp_rank),
                               static_cast<int>(static_cast<int32_t>(r.device_id)), layers.data(),
                               static_cast<uint32_t>(layers.size()));
 }
@@ -337,14 +371,7 @@ void serve_connection(pf_fastpath* f, int fd) {
     buf.resize(len);
     if (!read_full(fd, buf.data(), len)) break;
     const uint8_t method = buf[0];
-    clear_error();
-    int rc = PF_OK;
-    switch (method) {
-      case PF_FAST_LOAD: rc = serve_load(f->engine, buf.data() + 1, len - 1); break;
-      case PF_FAST_SAVE: rc = serve_save(f->engine, buf.data() + 1, len - 1); break;
-      case PF_FAST_HEALTH: break;
-      default: rc = fail(PF_ERR_INVALID_ARGUMENT, strf("unknown method %u", method)); break;
-    }
+    const int rc = pf_engine_serve_request(f->engine, method, buf.data() + 1, len - 1);
     f->served.fetch_add(1, std::memory_order_relaxed);
     const auto t_reply = std::chrono::steady_clock::now();
     if (!reply(fd, rc, rc == PF_OK ? std::string() : std::string(pf_last_error()))) break;
@@ -382,6 +409,19 @@ void accept_loop(pf_fastpath* f) {
 }  // namespace
 
 extern "C" {
+
+int pf_engine_serve_request(pf_engine* engine, uint32_t method, const uint8_t* request,
+                            uint64_t size) {
+  if (!engine) return fail(PF_ERR_INVALID_ARGUMENT, "null engine");
+  if (size > 0 && !request) return fail(PF_ERR_INVALID_ARGUMENT, "null request");
+  clear_error();
+  switch (method) {
+    case PF_FAST_LOAD: return serve_load(engine, request, static_cast<size_t>(size));
+    case PF_FAST_SAVE: return serve_save(engine, request, static_cast<size_t>(size));
+    case PF_FAST_HEALTH: return PF_OK;
+    default: return fail(PF_ERR_INVALID_ARGUMENT, strf("unknown method %u", method));
+  }
+}
 
 int pf_fastpath_start(pf_engine* engine, const char* socket_path, pf_fastpath** out) {
   if (!engine || !socket_path || !out) return fail(PF_ERR_INVALID_ARGUMENT, "null argument");

@@ -266,6 +266,12 @@ class PegaEngine:
     def fast_path_served(self) -> int:
         return int(lib().pf_fastpath_served(self._fast)) if getattr(self, "_fast", None) else 0
 
+    def serve_request(self, method: int, request: bytes) -> None:
+        """One Load or Save request (method FAST_LOAD / FAST_SAVE) in
+        engine.proto's encoding, decoded and served natively on this thread,
+        as the fast path serves a frame (pf_engine_serve_request)."""
+        _raise(lib().pf_engine_serve_request(self._h, method, request, len(request)))
+
     def close(self) -> None:
         self.stop_fast_path()
         if self._h:

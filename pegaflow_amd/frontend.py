@@ -146,6 +146,10 @@ class EngineFrontend:
     def save(self, instance_id: str, tp_rank: int, device_id: int, saves) -> None:
         self.engine.batch_save_kv_blocks(instance_id, tp_rank, device_id, saves)
 
+    def serve(self, method: int, request: bytes) -> None:
+        """A Load or Save request as its wire bytes, decoded by the engine."""
+        self.engine.serve_request(method, request)
+
     def load(self, instance_id: str, tp_rank: int, device_id: int, load_state_shm: str,
              layer_names, block_ids, block_hashes) -> None:
         self.engine.batch_load_kv_blocks(instance_id, tp_rank, device_id, load_state_shm,

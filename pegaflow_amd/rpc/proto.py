@@ -11,7 +11,6 @@ from __future__ import annotations
 
 from typing import NamedTuple
 
-from google.protobuf.message import DecodeError
 from google.protobuf import descriptor_pb2, descriptor_pool, message_factory
 
 PACKAGE = "pegaflow"
@@ -122,14 +121,10 @@ def method_path(rpc: str) -> str:
     return f"/{PACKAGE}.{SERVICE}/{rpc}"
 
 
-# ---- SaveRequest decoding for the service ----------------------------------
-# A save carries every layer's copy of the same ids and hashes (about 23 KB
-# per Llama layer).  The service splits the request into its top-level
-# records, compares each layer's list bytes with the previous layer's, and
-# parses only the distinct ones, so equal lists become one shared list
-# object and the request costs one parse of the lists instead of one per
-# layer.  Anything unusual (fields out of order, unpacked ids, an unknown
-# wire type) falls back to the full parse, which decides validity.
+# ---- SaveRequest as the engine takes it ------------------------------------
+# A save carries every layer's copy of the same ids and hashes.  A decoded
+# request handed to the service object keeps equal neighbouring lists as one
+# shared list object, which the engine packs and looks up once.
 
 
 class DecodedSave(NamedTuple):
@@ -137,76 +132,6 @@ class DecodedSave(NamedTuple):
     tp_rank: int
     device_id: int
     saves: list  # [(layer_name, block_ids, block_hashes)], equal neighbours shared
-
-
-class _NotCanonical(Exception):
-    pass
-
-
-def _varint(buf, pos: int):
-    result = shift = 0
-    while True:
-        if pos >= len(buf) or shift > 63:
-            raise _NotCanonical
-        b = buf[pos]
-        pos += 1
-        result |= (b & 0x7F) << shift
-        if not b & 0x80:
-            return result, pos
-        shift += 7
-
-
-def _records(buf):
-    """(field, wire type, start, value start, end) of each top-level record."""
-    pos, n = 0, len(buf)
-    while pos < n:
-        start = pos
-        tag, pos = _varint(buf, pos)
-        wt, vstart = tag & 7, pos
-        if wt == 0:
-            _, pos = _varint(buf, pos)
-        elif wt == 1:
-            pos += 8
-        elif wt == 2:
-            ln, vstart = _varint(buf, pos)
-            pos = vstart + ln
-        elif wt == 5:
-            pos += 4
-        else:
-            raise _NotCanonical
-        if pos > n:
-            raise _NotCanonical
-        yield tag >> 3, wt, start, vstart, pos
-
-
-def _decode_save_fast(data: bytes) -> DecodedSave:
-    data = bytes(data)  # byte-string slices compare with memcmp
-    header, layers = [], []
-    for field, wt, start, vstart, end in _records(data):
-        if field == 4 and wt == 2:
-            layers.append(data[vstart:end])
-        else:
-            header.append(data[start:end])
-    head = SaveRequest.FromString(b"".join(header))
-    saves, prev_body, prev = [], None, None
-    for layer in layers:
-        name, body = "", layer
-        if len(layer) and layer[0] == 0x0A:  # layer_name, field 1, first
-            ln, p = _varint(layer, 1)
-            if p + ln > len(layer):
-                raise _NotCanonical
-            name = layer[p:p + ln].decode("utf-8")
-            body = layer[p + ln:]
-        if prev_body is None or body != prev_body:
-            # The list bytes must be exactly the canonical encoding of the
-            # lists alone (no second layer_name, nothing reordered), so that
-            # name + lists is what the full parse would give.
-            m = SaveLayer.FromString(body)
-            if m.SerializeToString() != body:
-                raise _NotCanonical
-            prev_body, prev = body, (list(m.block_ids), list(m.block_hashes))
-        saves.append((name, prev[0], prev[1]))
-    return DecodedSave(head.instance_id, head.tp_rank, head.device_id, saves)
 
 
 def decoded_save(msg) -> DecodedSave:
@@ -219,11 +144,3 @@ def decoded_save(msg) -> DecodedSave:
         prev = (ids, hashes)
         saves.append((s.layer_name, ids, hashes))
     return DecodedSave(msg.instance_id, msg.tp_rank, msg.device_id, saves)
-
-
-def decode_save_request(data: bytes) -> DecodedSave:
-    """The service's request deserializer for Save."""
-    try:
-        return _decode_save_fast(data)
-    except (_NotCanonical, UnicodeDecodeError, DecodeError):
-        return decoded_save(SaveRequest.FromString(data))  # exact semantics, or its error

@@ -87,22 +87,31 @@ class EngineService:
             self._abort(context, e)
         return proto.RegisterContextResponse(status=_ok())
 
+    # Save and Load arrive as their wire bytes (registered without a
+    # deserializer) and are decoded by the engine itself, as on its native
+    # endpoint.  A decoded message (a caller of the service object) takes the
+    # Python path: layers that carry the same ids and hashes share one list
+    # object, which the engine packs and looks up once.
     def Save(self, req, context):
-        # The request arrives decoded by proto.decode_save_request: layers
-        # that carry the same ids and hashes share one list object, which
-        # the engine packs and looks up once.
-        if not isinstance(req, proto.DecodedSave):
-            req = proto.decoded_save(req)
         try:
-            self.frontend.save(req.instance_id, req.tp_rank, req.device_id, req.saves)
+            if isinstance(req, bytes):
+                self.frontend.serve(_lib.FAST_SAVE, req)
+            else:
+                if not isinstance(req, proto.DecodedSave):
+                    req = proto.decoded_save(req)
+                self.frontend.save(req.instance_id, req.tp_rank, req.device_id, req.saves)
         except Exception as e:
             self._abort(context, e)
         return proto.SaveResponse(status=_ok())
 
     def Load(self, req, context):
         try:
-            self.frontend.load(req.instance_id, req.tp_rank, req.device_id, req.load_state_shm,
-                               req.layer_names, req.block_ids, req.block_hashes)
+            if isinstance(req, bytes):
+                self.frontend.serve(_lib.FAST_LOAD, req)
+            else:
+                self.frontend.load(req.instance_id, req.tp_rank, req.device_id,
+                                   req.load_state_shm, req.layer_names, req.block_ids,
+                                   req.block_hashes)
         except Exception as e:
             self._abort(context, e)
         return proto.LoadResponse(status=_ok())
@@ -138,7 +147,7 @@ class EngineService:
         for rpc, req, resp in proto.METHODS:
             methods[rpc] = grpc.unary_unary_rpc_method_handler(
                 getattr(self, rpc),
-                request_deserializer=(proto.decode_save_request if rpc == "Save"
+                request_deserializer=(None if rpc in ("Save", "Load")
                                       else proto.messages[req].FromString),
                 response_serializer=proto.messages[resp].SerializeToString)
         return grpc.method_handlers_generic_handler(f"{proto.PACKAGE}.{proto.SERVICE}", methods)

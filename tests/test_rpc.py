@@ -330,7 +330,7 @@ def test_save_request_encoding_matches_the_message():
 
     svc = EngineService.__new__(EngineService)
     svc.frontend = Frontend()
-    for req in (proto.decode_save_request(wire), proto.SaveRequest.FromString(wire)):
+    for req in (proto.SaveRequest.FromString(wire),):
         svc.Save(req, None)
         out = got["saves"]
         assert [(n, list(i), list(h)) for n, i, h in out] == [(n, i, h) for n, i, h in saves]
@@ -345,50 +345,88 @@ def _ld(field, payload):
     return _varint(field << 3 | 2) + _varint(len(payload)) + payload
 
 
-def test_save_request_decoder_matches_the_full_parse():
-    """decode_save_request gives what the full parse gives, for the
-    canonical encoding and for encodings it does not take apart itself
-    (unpacked ids, the name after the lists, a second name record, unknown
-    fields, negative ids); malformed bytes fail as the full parse does."""
+def test_engine_decoder_matches_the_full_parse(served_fast):
+    """The engine's request decoder (gRPC Save and Load, the native
+    endpoint) gives what protobuf's full parse gives (the service's Python
+    path) for the canonical encoding and for unpacked ids, the name after
+    the lists, a second name record (the last wins), unknown fields, the
+    header last and an empty layer: each variant's result or error text is
+    the same, and the error names the layer that was decoded.  Malformed
+    bytes (truncated, a name that is not UTF-8, a string with the wrong wire
+    type, a bad length) fail on both."""
     from google.protobuf.message import DecodeError
 
     from pegaflow_amd.rpc import proto
-    from pegaflow_amd.rpc.client import _varint, encode_save_request
+    from pegaflow_amd.rpc.client import _STATUS_NAMES
+    from pegaflow_amd.rpc.client import _varint as varint
 
-    def expect(wire):
-        m = proto.SaveRequest.FromString(wire)
-        d = proto.decode_save_request(wire)
-        assert (d.instance_id, d.tp_rank, d.device_id) == (m.instance_id, m.tp_rank, m.device_id)
-        assert [(n, list(i), list(h)) for n, i, h in d.saves] == \
-            [(s.layer_name, list(s.block_ids), list(s.block_hashes)) for s in m.saves]
-        return d
+    srv, slow, _, path = served_fast
+    _register(slow, "l0")
+    _register(slow, "l1")
+
+    def python_path(method, msg_cls, wire):
+        got = []
+
+        class Context:
+            def abort(self, code, detail):
+                got.append((code.name, detail))
+                raise RuntimeError(detail)
+
+        handler = srv.service.Save if method == 2 else srv.service.Load
+        try:
+            handler(msg_cls.FromString(wire), Context())
+        except RuntimeError:
+            pass
+        return got[0] if got else ("OK", "")
+
+    def native(method, wire):
+        status, msg = _raw(path, method, wire)
+        return ("OK", "") if status == 0 else (_STATUS_NAMES.get(status, "INTERNAL"), msg)
 
     hs = [b"x" * 32, b"y" * 32]
-    canon = encode_save_request("i", 1, 2, [("a", [3, -4], hs), ("b", [3, -4], hs)])
-    d = expect(canon)
-    assert d.saves[0][1] is d.saves[1][1]
-    assert proto._decode_save_fast(canon) == d  # taken apart without the full parse
-    head = proto.SaveRequest(instance_id="i", tp_rank=1, device_id=2).SerializeToString()
-    lists = proto.SaveLayer(block_ids=[3, -4], block_hashes=hs).SerializeToString()
-    unpacked = b"".join(_varint(2 << 3) + _varint(v & (2**64 - 1)) for v in (3, -4))
+    head = proto.SaveRequest(instance_id="i0", tp_rank=0, device_id=0).SerializeToString()
+    lists = proto.SaveLayer(block_ids=[5, 16], block_hashes=hs).SerializeToString()  # 16: out of range
+    unpacked = b"".join(varint(2 << 3) + varint(v & (2**64 - 1)) for v in (5, 16))
     hashes = b"".join(_ld(3, h) for h in hs)
-    variants = [
-        head + _ld(4, _ld(1, b"a") + unpacked + hashes),           # ids not packed
-        head + _ld(4, lists + _ld(1, b"a")),                         # name after the lists
-        head + _ld(4, _ld(1, b"a") + lists + _ld(1, b"z")),          # second name wins
-        head + _ld(4, _ld(1, b"a") + lists + _ld(1, b"")),           # ... also when empty
-        head + _ld(4, _ld(1, b"a") + lists) + _varint(9 << 3) + _varint(7),  # unknown field
-        _ld(4, _ld(1, b"a") + lists) + head,                         # header last
-        head + _ld(4, b""),                                          # an empty layer
+    saves = [
+        head + _ld(4, _ld(1, b"l0") + lists),                          # canonical
+        head + _ld(4, _ld(1, b"l0") + unpacked + hashes),              # ids not packed
+        head + _ld(4, lists + _ld(1, b"l1")),                          # name after the lists
+        head + _ld(4, _ld(1, b"l0") + lists + _ld(1, b"l1")),          # second name wins
+        head + _ld(4, _ld(1, b"l1") + lists + _ld(1, b"")),            # ... also when empty
+        head + _ld(4, _ld(1, b"l0") + lists) + varint(9 << 3) + varint(7),  # unknown field
+        _ld(4, _ld(1, b"l1") + lists) + head,                          # header last
+        head + _ld(4, b""),                                            # an empty layer
+        head + _ld(4, _ld(1, b"l0") + _ld(2, varint(5)) + _ld(3, b"a")),  # a good one
     ]
-    for w in variants:
-        expect(w)
-    assert proto.decode_save_request(variants[3]).saves[0][0] == ""
-    for bad in (canon[:-3], head + _ld(4, _ld(1, b"\xff\xfe") + lists), b"\x22\xff"):
+    outcomes = []
+    for i, w in enumerate(saves):
+        want = python_path(2, proto.SaveRequest, w)
+        assert native(2, w) == want, f"save variant {i}: {want}"
+        outcomes.append(want)
+    assert "layer l0" in outcomes[0][1] and "layer l1" in outcomes[3][1]
+    assert outcomes[8] == ("OK", "") or outcomes[8][0] != "INVALID_ARGUMENT"
+    lhead = proto.LoadRequest(instance_id="i0", tp_rank=0, device_id=0,
+                              load_state_shm="pega_load_none").SerializeToString()
+    loads = [
+        lhead + _ld(5, b"l0") + _ld(7, b"abc"),                        # missing shm, then hash
+        _ld(7, b"abc") + _ld(5, b"zz") + lhead,                        # header last
+        lhead + _ld(5, b"l0") + varint(6 << 3) + varint(3) + _ld(7, b"a"),  # unpacked id
+    ]
+    for i, w in enumerate(loads):
+        want = python_path(1, proto.LoadRequest, w)
+        assert native(1, w) == want, f"load variant {i}: {want}"
+    canon = saves[0]
+    bad = [canon[:-3], head + _ld(4, _ld(1, b"\xff\xfe") + lists), b"\x22\xff"]
+    for i, w in enumerate(bad):
         with pytest.raises(DecodeError):
-            proto.SaveRequest.FromString(bad)
-        with pytest.raises(DecodeError):
-            proto.decode_save_request(bad)
+            proto.SaveRequest.FromString(w)
+        assert native(2, w) == ("INVALID_ARGUMENT", "malformed SaveRequest"), f"bad {i}"
+    # A known field with another wire type: the reference server's decoder
+    # (prost) refuses the message, as the engine's does; protobuf's Python
+    # parser keeps the record as an unknown field instead.
+    assert native(2, head + _ld(4, varint(1 << 3) + varint(7))) == \
+        ("INVALID_ARGUMENT", "malformed SaveRequest")
 
 
 # ---------------------------------------------------------------------------
@@ -414,8 +452,43 @@ def _error(fn):
     return str(e.value)
 
 
+class _Decoded:
+    """The service object called with decoded messages (its Python path, as
+    a caller of the service object takes it), errors formatted as the
+    client formats an RPC error.  Over gRPC the server hands Load and Save
+    to the engine's own decoder instead."""
+
+    def __init__(self, svc):
+        self.svc = svc
+
+    @staticmethod
+    def _run(method, handler, req):
+        class Context:
+            def abort(self, code, detail):
+                raise RuntimeError(f"{method} RPC failed: status: {code}, message: {detail!r}")
+
+        handler(req, Context())
+        return True, ""
+
+    def save(self, *args):
+        from pegaflow_amd.rpc import proto
+        from pegaflow_amd.rpc.client import encode_save_request
+        req = proto.SaveRequest.FromString(encode_save_request(*args))
+        return self._run("save", self.svc.Save, req)
+
+    def load(self, *args):
+        from pegaflow_amd.rpc import proto
+        from pegaflow_amd.rpc.client import encode_load_request
+        req = proto.LoadRequest.FromString(encode_load_request(*args))
+        return self._run("load", self.svc.Load, req)
+
+
 def test_fast_path_gives_the_grpc_results_and_errors(served_fast):
+    """Each request gives the same result and error text three ways: over
+    gRPC and over the native endpoint (both decoded by the engine) and
+    through the service's Python path for decoded messages."""
     srv, slow, fast, _ = served_fast
+    decoded = _Decoded(srv.service)
     assert fast.health() == (True, "")
     _register(slow, "l0")
     _register(slow, "l1")
@@ -432,7 +505,8 @@ def test_fast_path_gives_the_grpc_results_and_errors(served_fast):
         lambda c: c.load("i0", 0, 0, "pega_load_missing", ["l0"], [1], [b"a"]),
     ]
     for i, case in enumerate(cases):
-        want = _error(lambda: case(slow))
+        want = _error(lambda: case(decoded))
+        assert _error(lambda: case(slow)) == want, f"case {i}: {want}"
         assert _error(lambda: case(fast)) == want, f"case {i}: {want}"
     assert "INVALID_ARGUMENT" in _error(lambda: cases[0](fast))
     assert "block_ids length 2 does not match block_hashes 1" in _error(lambda: cases[1](fast))
