@@ -45,7 +45,10 @@ enum {
   PF_ERR_INIT = 7,              /* EngineError::CudaInit                       */
   PF_ERR_LOAD_STATE = 8,        /* LoadStateError (sync_state.rs:46-56)        */
   PF_ERR_ZERO_SIZE = 9,         /* PinnedMemError::ZeroSize (pinned_mem.rs:72) */
-  PF_ERR_UNSUPPORTED = 10
+  PF_ERR_UNSUPPORTED = 10,
+  PF_ERR_MALFORMED = 11         /* a request that does not decode; the gRPC    */
+                                /* service answers INTERNAL, as gRPC servers  */
+                                /* do for a message that does not parse       */
 };
 
 /* Message of the last failed call on the calling thread ("" if none). */
@@ -670,7 +673,7 @@ uint64_t pf_fastpath_served(const pf_fastpath* fastpath);
  * without the frame), served on the calling thread: what the endpoint does
  * with a frame, for a server that receives the bytes itself (the gRPC
  * service's Load and Save, service.rs:184-250).  A request that does not
- * decode fails with PF_ERR_INVALID_ARGUMENT. */
+ * decode fails with PF_ERR_MALFORMED. */
 int pf_engine_serve_request(pf_engine* engine, uint32_t method,
                             const uint8_t* request, uint64_t size);
 

@@ -26,6 +26,7 @@ PF_ERR_INIT = 7
 PF_ERR_LOAD_STATE = 8
 PF_ERR_ZERO_SIZE = 9
 PF_ERR_UNSUPPORTED = 10
+PF_ERR_MALFORMED = 11
 
 ERROR_NAMES = {
     PF_ERR_INVALID_ARGUMENT: "invalid argument",
@@ -38,6 +39,7 @@ ERROR_NAMES = {
     PF_ERR_LOAD_STATE: "LoadState error",
     PF_ERR_ZERO_SIZE: "zero size",
     PF_ERR_UNSUPPORTED: "unsupported",
+    PF_ERR_MALFORMED: "malformed request",
 }
 
 # Transfer modes.

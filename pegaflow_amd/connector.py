@@ -218,8 +218,9 @@ class WorkerConnector:
         processed.  A request finished while it has no save activity is not
         tracked.  Unlike the reference, a step's new layer saves reopen a
         request whose earlier saves completed but were not yet reported, so
-        it is not handed back while those saves are still queued.  Every load whose LoadState is ready, failed or not,
-        reports its requests as received."""
+        it is not handed back while those saves are still queued.  Every
+        load whose LoadState is ready, failed or not, reports its requests
+        as received."""
         with self._lock:
             for rid in finished_req_ids:
                 progress = self._saves.get(rid)

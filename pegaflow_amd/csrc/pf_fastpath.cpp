@@ -267,7 +267,7 @@ bool decode_save(const uint8_t* p, size_t n, SaveReq* r) {
 // ---------------------------------------------------------------------------
 int serve_load(pf_engine* e, const uint8_t* p, size_t n) {
   LoadReq r;
-  if (!decode_load(p, n, &r)) return fail(PF_ERR_INVALID_ARGUMENT, "malformed LoadRequest");
+  if (!decode_load(p, n, &r)) return fail(PF_ERR_MALFORMED, "malformed LoadRequest");
   // lib.rs:1008-1043: every hash is looked up; ids pair with hashes up to
   // the shorter list (extra hashes get id -1, skipped; extra ids dropped).
   const size_t nh = r.hashes.size();
@@ -284,7 +284,7 @@ int serve_load(pf_engine* e, const uint8_t* p, size_t n) {
 
 int serve_save(pf_engine* e, const uint8_t* p, size_t n) {
   SaveReq r;
-  if (!decode_save(p, n, &r)) return fail(PF_ERR_INVALID_ARGUMENT, "malformed SaveRequest");
+  if (!decode_save(p, n, &r)) return fail(PF_ERR_MALFORMED, "malformed SaveRequest");
   std::vector<pf_save_layer> layers;
   layers.reserve(r.saves.size());
   for (const SaveLayerReq& s : r.saves) {

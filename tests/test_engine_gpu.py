@@ -155,7 +155,7 @@ def _expect_per_layer(model, orig, pairs_per_layer):
 def test_duplicate_hash_in_one_save_keeps_first(engine):
     """One save batch names a hash twice with different blocks.  Both are
     copied, the first occurrence fills the slot and the second is dropped
-    (lib.rs:590-621; storage.rs:182, 466-471): the whole-batch path."""
+    (lib.rs:590-621; storage.rs:181-184, 483-486): the whole-batch path."""
     say("[gpu] engine duplicate hash in one save (whole batch)")
     m = Model(engine, "dup", 4, 32, 2048, seed=12)
     orig = m.host_copies()

@@ -421,12 +421,20 @@ def test_engine_decoder_matches_the_full_parse(served_fast):
     for i, w in enumerate(bad):
         with pytest.raises(DecodeError):
             proto.SaveRequest.FromString(w)
-        assert native(2, w) == ("INVALID_ARGUMENT", "malformed SaveRequest"), f"bad {i}"
+        assert native(2, w) == ("INTERNAL", "malformed SaveRequest"), f"bad {i}"
     # A known field with another wire type: the reference server's decoder
     # (prost) refuses the message, as the engine's does; protobuf's Python
     # parser keeps the record as an unknown field instead.
     assert native(2, head + _ld(4, varint(1 << 3) + varint(7))) == \
-        ("INVALID_ARGUMENT", "malformed SaveRequest")
+        ("INTERNAL", "malformed SaveRequest")
+    # Over gRPC the same bytes fail as a message that does not parse.
+    from pegaflow_amd.rpc.client import _serialize
+    stub = slow._channel.unary_unary(proto.method_path("Save"), request_serializer=_serialize,
+                                     response_deserializer=proto.SaveResponse.FromString)
+    with pytest.raises(grpc.RpcError) as err:
+        stub(bad[0], timeout=10)
+    assert err.value.code() == grpc.StatusCode.INTERNAL
+    assert err.value.details() == "malformed SaveRequest"
 
 
 # ---------------------------------------------------------------------------
@@ -591,8 +599,8 @@ def test_fast_path_decodes_every_encoding(served_fast):
     assert status == 3 and "missing KV block hash at index 0" in msg
     assert st.get_state() == -1
     # Malformed: a length running past the message, a group wire type.
-    assert _raw(path, 2, _field(1, 2, b"i0")[:-1]) == (1, "malformed SaveRequest")
-    assert _raw(path, 1, _varint(1 << 3 | 3)) == (1, "malformed LoadRequest")
+    assert _raw(path, 2, _field(1, 2, b"i0")[:-1]) == (11, "malformed SaveRequest")
+    assert _raw(path, 1, _varint(1 << 3 | 3)) == (11, "malformed LoadRequest")
     assert _raw(path, 9, b"") == (1, "unknown method 9")
     status, msg = _raw(path, 1, b"", raw_len=(256 << 20) + 2)
     assert status == 1 and "exceeds" in msg
