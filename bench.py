@@ -148,6 +148,90 @@ def duplex(xfer_save, xfer_load, saved, loads, mode, reps=5):
     return min(ts[1:])
 
 
+def duplex_threads(xfer_save, xfer_load, saved, loads, mode, reps=5):
+    """As duplex, with the restore issued from a second thread, as the
+    engine's load thread does (a staged restore on the copy engines returns
+    once its copies are done)."""
+    import threading
+
+    ts = []
+    for _ in range(reps + 1):
+        t0 = time.perf_counter()
+        th = threading.Thread(target=lambda: (xfer_load.load_layers(loads, mode),
+                                              xfer_load.synchronize()))
+        th.start()
+        xfer_save.save_layers(saved, mode)
+        th.join()
+        ts.append(time.perf_counter() - t0)
+    return min(ts[1:])
+
+
+def leg_interference(layers, saved, loads, P, reps=3):
+    """How much each transfer mode slows a kernel running beside it: a plain
+    256 MiB device-to-device copy by the chunk kernel, launched back to back
+    from the main thread (its kernel time by HIP events) while a thread saves
+    or restores the Llama prefix.  Shader reads and writes of host memory
+    (the zero-copy kernel) hold up the memory traffic of every other kernel;
+    the staged mode's copies run on the copy engines."""
+    import threading
+
+    from pegaflow_amd import _lib
+    from pegaflow_amd.runtime import DeviceBuffer
+    from pegaflow_amd.transfer import KVCacheRegistration, TransferContext
+    from pegaflow_amd import workload as wl
+
+    vb = 256 << 20
+    vsrc, vdst = DeviceBuffer(vb), DeviceBuffer(vb)
+    xv = TransferContext(0)
+    creg = KVCacheRegistration.create(vsrc.ptr, vb, vb // 32768, 32768, 0, 1)
+    vplan = wl.save_plan([creg], np.arange(vb // 32768), vdst.ptr)
+    xv.set_timing(True)
+    xt = TransferContext(0, staging_bytes=256 << 20)
+
+    def victim():
+        xv.save_layers(vplan, _lib.MODE_KERNEL)
+        return xv.last_kernel_ms()[0]
+
+    for _ in range(3):
+        victim()
+    solo = statistics.median([victim() for _ in range(20)])
+    out = {"victim": "256 MiB device-to-device copy (chunk kernel, 512 threads)",
+           "victim_solo_ms": round(solo, 4)}
+    ops = {
+        "kernel_save": lambda: xt.save_layers(saved, _lib.MODE_KERNEL),
+        "staged_save": lambda: xt.save_layers(saved, _lib.MODE_STAGED),
+        "kernel_restore": lambda: (xt.load_layers(loads, _lib.MODE_KERNEL), xt.synchronize()),
+        "staged_restore": lambda: (xt.load_layers(loads, _lib.MODE_STAGED), xt.synchronize()),
+    }
+    for name, op in ops.items():
+        op()
+        t_op, times = [], []
+
+        def worker():
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                op()
+                t_op.append(time.perf_counter() - t0)
+
+        th = threading.Thread(target=worker)
+        th.start()
+        time.sleep(0.002)
+        while th.is_alive():
+            times.append(victim())
+        th.join()
+        times = times[1:-1] if len(times) > 3 else times
+        med = statistics.median(times)
+        out[name] = {"victim_ms": round(med, 4), "slowdown": round(med / solo, 2),
+                     "victim_launches": len(times),
+                     "transfer_gbps": round(P / statistics.median(t_op) / 1e9, 2)}
+        log(f"[bench] interference {name}: {out[name]}")
+    xt.close()
+    xv.close()
+    vsrc.close()
+    vdst.close()
+    return out
+
+
 def duplex_study(xfer_load, xfer_save, saved, loads, pool, pool2, dev_buf, P, reps=4):
     """Which direction loses bandwidth when both link directions are busy.
     Each case runs a save and a restore of P bytes at once and reports the
@@ -664,20 +748,27 @@ def leg_engine(layers, ids, targets, P, reps=4):
     shape = layers.shape
     names = [f"layer.{l}" for l in range(len(layers.bufs))]
     ids_l, targets_l = [int(i) for i in ids], [int(t) for t in targets]
-    e = PegaEngine(pool_size=(reps + 1) * P + (256 << 20))
+    e = PegaEngine(pool_size=2 * (reps + 1) * P + (256 << 20))
     for name, buf in zip(names, layers.bufs):
         e.register_context_layer("bench", "llama3-8b", 0, name, buf.ptr, shape.layer_bytes,
                                  shape.num_blocks, shape.bytes_per_block, shape.kv_stride_bytes,
                                  shape.segments, 0, 1, len(names))
     layers.refill()
-    save_s, load_s = [], []
+    from pegaflow_amd import _lib
+
+    save_s, load_s, ksave_s = [], [], []
     hashes = None
-    for r in range(reps + 1):  # every save uses new hashes: nothing is deduplicated
+    # The engine's default modes (saves staged on the copy engines, loads by
+    # the zero-copy kernel), then saves by the kernel for comparison.
+    for r in range(2 * (reps + 1)):  # every save uses new hashes: nothing is deduplicated
+        if r == reps + 1:
+            e.set_transfer_modes(_lib.MODE_KERNEL, _lib.MODE_KERNEL)
         hashes = [hashlib.sha256(b"engine%d-" % r + int(i).to_bytes(8, "little")).digest()
                   for i in ids_l]
         t0 = time.perf_counter()
         e.batch_save_kv_blocks("bench", 0, 0, [(n, ids_l, hashes) for n in names])
-        save_s.append(time.perf_counter() - t0)
+        (save_s if r <= reps else ksave_s).append(time.perf_counter() - t0)
+    e.set_transfer_modes()
     bad = 0
     layered_s = []
     for layered, out in ((False, load_s), (True, layered_s)):
@@ -697,8 +788,6 @@ def leg_engine(layers, ids, targets, P, reps=4):
     # layers): latency from the call to the LoadState reading ready.
     # The same through the reference's copy pattern (one async copy per
     # merged run) for comparison.
-    from pegaflow_amd import _lib
-
     small = {}
     for mode, n in (("kernel", 1), ("kernel", 16), ("dma_reference", 1), ("dma_reference", 16)):
         e.set_transfer_modes(_lib.MODE_KERNEL, _lib.MODE_NAMES[mode])
@@ -713,7 +802,7 @@ def leg_engine(layers, ids, targets, P, reps=4):
             lat.append(time.perf_counter() - t0)
             bad += st.get_state() != 1
         small[f"{mode}_{n}_blocks_us"] = round(statistics.median(lat[1:]) * 1e6, 1)
-    e.set_transfer_modes(_lib.MODE_KERNEL, _lib.MODE_KERNEL)
+    e.set_transfer_modes()
     bad += wl.verify_restored(layers, ids[:16], targets[:16])
     layers.refill()
     stats = e.stats()
@@ -722,12 +811,17 @@ def leg_engine(layers, ids, targets, P, reps=4):
         "small_restore_latency": small,
         "what": "the llama prefix through PegaEngine: save by hash (new hashes each time), load "
                 "by hash with a plain LoadState (as the reference's connector) and with a "
-                "layered one (per-layer completion), median of the warm calls",
+                "layered one (per-layer completion), median of the warm calls; the engine's "
+                "default modes (saves staged on the copy engines, loads by the zero-copy "
+                "kernel), and kernel saves for comparison",
+        "save_mode": "auto (staged)",
         "save_gbps": round(P / statistics.median(save_s[1:]) / 1e9, 3),
+        "kernel_save_gbps": round(P / statistics.median(ksave_s[1:]) / 1e9, 3),
         "restore_gbps": round(P / statistics.median(load_s[1:]) / 1e9, 3),
         "restore_layered_gbps": round(P / statistics.median(layered_s[1:]) / 1e9, 3),
         "first_save_gbps": round(P / save_s[0] / 1e9, 3),
         "save_ms": [round(t * 1e3, 2) for t in save_s],
+        "kernel_save_ms": [round(t * 1e3, 2) for t in ksave_s],
         "restore_ms": [round(t * 1e3, 2) for t in load_s],
         "restore_layered_ms": [round(t * 1e3, 2) for t in layered_s],
         "sealed_blocks": stats["sealed_blocks"],
@@ -1256,7 +1350,17 @@ def main():
     bad_dup = wl.verify_saved(layers, saved2) + wl.verify_restored(layers, ids, targets)
     log(f"[bench] duplex save+restore {t_dup * 1e3:.3f} ms = {2 * P / t_dup / 1e9:.1f} GB/s, "
         f"mismatches {bad_dup}")
+    # The staged pair on the copy engines (one engine each way), the restore
+    # from a second thread as the engine's load thread issues it.
+    xfer_s = TransferContext(0, staging_bytes=args.staging_mib << 20)
+    t_dup_staged = duplex_threads(xfer_s, xfer, saved2, loads, _lib.MODE_STAGED)
+    xfer_s.close()
+    bad_dup += wl.verify_saved(layers, saved2) + wl.verify_restored(layers, ids, targets)
+    log(f"[bench] duplex staged save+restore {t_dup_staged * 1e3:.3f} ms = "
+        f"{2 * P / t_dup_staged / 1e9:.1f} GB/s, mismatches {bad_dup}")
     bad_host += bad_dup
+    log("[bench] interference: a device copy kernel beside each transfer mode")
+    interference = leg_interference(layers, saved, loads, P)
     if args.duplex_study:
         extra_duplex = duplex_study(xfer, xfer2, saved2, loads, pool, pool2, gather_buf, P)
     xfer2.close()
@@ -1390,6 +1494,11 @@ def main():
                                      "packed HBM -> 640 blocks)",
                            "bytes_per_launch": 2 * P, "ms_per_launch": round(scatter_ms, 4)},
         "d2d_memcpy_gbps": round(d2d_gbps, 1),
+        "interference": interference,
+        "duplex_staged": {"gbps": round(2 * P / t_dup_staged / 1e9, 3),
+                          "ms_per_save_plus_restore": round(t_dup_staged * 1e3, 3),
+                          "what": "as duplex, both staged on the copy engines, the restore "
+                                  "issued from a second thread"},
         "duplex": {"gbps": round(2 * P / t_dup / 1e9, 3), "ms_per_save_plus_restore":
                    round(t_dup * 1e3, 3),
                    "what": "a prefix saved while another is restored (two transfer contexts)",

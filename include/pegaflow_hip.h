@@ -266,22 +266,40 @@ typedef struct pf_layer_xfer {
  *  KERNEL:        one gather/scatter kernel per layer moves 16 B per lane
  *                 directly between the paged layer tensor and the (host-mapped
  *                 pinned, or device) addresses.
- *  STAGED:        the kernel runs HBM<->HBM into a packed staging buffer and
- *                 the host link is crossed by large DMA copies of maximal
- *                 host-contiguous runs, double-buffered across slices.      */
+ *  STAGED:        the kernel runs HBM<->HBM between the paged tensor and
+ *                 packed staging slots, and the host link is crossed only by
+ *                 DMA copies of host-contiguous runs; the call is cut into
+ *                 slices that may span layers.  With the host side in pinned
+ *                 memory the copies run on the device's preferred copy
+ *                 engine for their direction, driven from the calling
+ *                 thread (a load returns once its copies are done and its
+ *                 last kernels are issued); otherwise through HIP, slices
+ *                 alternating between the context's two streams.  Unlike
+ *                 KERNEL, it leaves kernels running beside it at their
+ *                 speed: shader reads and writes of host memory hold up
+ *                 every other kernel's memory traffic (a bf16 GEMM in
+ *                 another process ran 29x slower beside a KERNEL save of the
+ *                 Llama prefix, 1.03x beside a STAGED one).
+ *  AUTO:          STAGED when the context has staging and the call's
+ *                 host-contiguous runs average at least 1 MiB (long enough
+ *                 for DMA copies to run at the link's speed), else KERNEL.
+ *                 No counterpart in the reference (its calls are DMA). */
 enum {
   PF_MODE_DMA_REFERENCE = 0,
   PF_MODE_DMA_BATCHED = 1,
   PF_MODE_KERNEL = 2,
-  PF_MODE_STAGED = 3
+  PF_MODE_STAGED = 3,
+  PF_MODE_AUTO = 4
 };
 
-/* Create a transfer context on device: its own non-blocking streams, a
+/* Create a transfer context on device: its own two non-blocking streams, a
  * device descriptor buffer, and (if staging_bytes > 0) two staging slots of
- * staging_bytes/2 each for PF_MODE_STAGED. */
+ * staging_bytes/2 each for PF_MODE_STAGED, one per stream. */
 int pf_xfer_create(int device, uint64_t staging_bytes, pf_xfer** out);
 int pf_xfer_destroy(pf_xfer* xfer);
-/* The stream on which the context's gather/scatter kernels run. */
+/* The context's first stream: the kernel mode's launches run on it, and every
+ * load's work (on both streams in the staged mode) is ordered before what is
+ * queued on it afterwards. */
 pf_stream pf_xfer_stream(pf_xfer* xfer);
 /* Wait for all work issued on the context. */
 int pf_xfer_synchronize(pf_xfer* xfer);
@@ -350,6 +368,13 @@ int pf_xfer_set_kernel_shape(pf_xfer* xfer, uint32_t threads, uint32_t unroll);
 /* Upper bound on workgroups per gather/scatter launch (0 = one workgroup per
  * tile, the default); with a bound, each workgroup loops over tiles. */
 int pf_xfer_set_max_grid(pf_xfer* xfer, uint32_t max_workgroups);
+/* Largest staged slice per direction, in bytes (0 keeps the current value);
+ * slices are further capped by the staging slot.  Smaller load slices land
+ * a layer sooner; the defaults are the smallest that keep each direction's
+ * DMA copies at the link's speed. */
+#define PF_STAGED_SAVE_SLICE_DEFAULT (128ull << 20)
+#define PF_STAGED_LOAD_SLICE_DEFAULT (16ull << 20)
+int pf_xfer_set_staged_slices(pf_xfer* xfer, uint64_t save_bytes, uint64_t load_bytes);
 /* Number of gather/scatter kernel launches and DMA copies issued by the last
  * save/load call on this context. */
 int pf_xfer_last_stats(pf_xfer* xfer, uint64_t* kernel_launches,
@@ -369,7 +394,8 @@ int pf_save_layers(pf_xfer* xfer, const pf_layer_xfer* layers,
 
 /* Host -> device: for every layer, copy each block's segments from
  * k_host/v_host into the paged tensor as process_load_task does
- * (gpu_worker.rs:205-283).  Asynchronous: returns after issuing.  If
+ * (gpu_worker.rs:205-283).  Asynchronous: returns after issuing (a STAGED
+ * load on the copy engines: once its copies are done).  If
  * layer_events is non-NULL, layer_events[l] is recorded once layer l's bytes
  * are in place (per-layer completion, which the reference lacks:
  * worker.py:288-289).  Completion of the whole call is pf_xfer_synchronize or
@@ -594,7 +620,12 @@ int pf_engine_create(uint64_t pool_bytes, uint32_t pool_kind,
                      uint32_t pinned_flags, uint64_t unit_hint,
                      pf_engine** out);
 int pf_engine_destroy(pf_engine* e);
-/* Transfer strategies used by saves and loads (default PF_MODE_KERNEL). */
+/* Transfer strategies used by saves and loads.  Defaults: saves
+ * PF_MODE_AUTO (a save batch's host regions are long runs, so saves run
+ * staged and leave the device's other kernels at their speed), loads
+ * PF_MODE_KERNEL (the link's full rate and the first layer soonest).  The
+ * workers' contexts have staging for every mode.  An AUTO load is resolved
+ * from its first layer's block list. */
 int pf_engine_set_modes(pf_engine* e, uint32_t save_mode, uint32_t load_mode);
 /* register_context_layer (lib.rs:373-469). */
 int pf_engine_register_context_layer(pf_engine* e, const char* instance_id,

@@ -47,11 +47,13 @@ MODE_DMA_REFERENCE = 0
 MODE_DMA_BATCHED = 1
 MODE_KERNEL = 2
 MODE_STAGED = 3
+MODE_AUTO = 4
 MODE_NAMES = {
     "dma_reference": MODE_DMA_REFERENCE,
     "dma_batched": MODE_DMA_BATCHED,
     "kernel": MODE_KERNEL,
     "staged": MODE_STAGED,
+    "auto": MODE_AUTO,
 }
 
 # Layout kinds.
@@ -260,6 +262,7 @@ SIGNATURES = {
     "pf_xfer_set_kernel_shape": (i32, [vp, u32, u32]),
     "pf_xfer_last_stats": (i32, [vp, pu64, pu64]),
     "pf_xfer_set_max_grid": (i32, [vp, u32]),
+    "pf_xfer_set_staged_slices": (i32, [vp, u64, u64]),
     "pf_xfer_set_kernel_shape_dir": (i32, [vp, u32, u32, u32]),
     "pf_xfer_route_shape": (i32, [vp, u32, ctypes.POINTER(u32), ctypes.POINTER(u32),
                                   ctypes.POINTER(i32)]),

@@ -72,7 +72,8 @@ def build(verbose: bool = False) -> str:
         objs.append(obj)
     tmp = LIB + ".tmp"
     cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs,
-           "-Wl,-rpath,/opt/rocm/lib", "-Wl,--no-undefined", "-lpthread", "-lrt"]
+           "-Wl,-rpath,/opt/rocm/lib", "-Wl,--no-undefined", "-L/opt/rocm/lib",
+           "-lhsa-runtime64", "-lpthread", "-lrt"]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)

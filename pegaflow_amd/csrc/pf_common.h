@@ -115,6 +115,34 @@ void pinned_unregister(uint64_t base);
 // *base/*end receive that allocation's bounds.
 bool pinned_lookup(uint64_t addr, uint64_t len, uint64_t* base, uint64_t* end);
 
+// DMA copies over the host link on chosen copy engines (pf_runtime.cpp).  The
+// HIP runtime gives each copy an engine of its own choosing, and the 16
+// engines of an MI355X move host data at very different rates (measured,
+// 1 GiB each: device to host 57.1 GB/s on engines 0-3, 7-13 GB/s on the
+// others; host to device 57.6 down to 28 GB/s), so a process whose copies
+// land on a slow engine moves them at a fraction of the link's speed.
+// These copies use the runtime's preferred engine for each direction, a
+// different one for each direction where it allows.
+//
+// A signal counts a batch's copies still in flight (0: none).
+struct EngineSignal {
+  uint64_t handle = 0;
+};
+// True when the device's engines for both directions are known.
+bool engine_copies_available(int device);
+int engine_signal_create(EngineSignal* s);  // value 0
+void engine_signal_destroy(EngineSignal* s);
+// Adds n to the count before n copies are submitted against the signal.
+void engine_signal_add(EngineSignal* s, int64_t n);
+// One copy of `bytes` on the device's engine for the direction (d2h: device
+// to host).  The host side must lie in pinned memory.  On success the
+// signal drops by one when the copy is done; on failure it is dropped here.
+int engine_copy(int device, bool d2h, uint64_t dst, uint64_t src, uint64_t bytes,
+                EngineSignal* s);
+// Waits until the signal reads 0 (an error after kEngineWaitSeconds).
+constexpr int kEngineWaitSeconds = 60;
+int engine_signal_wait(EngineSignal* s);
+
 // Address validation for kernel access.  A kernel that touches an unmapped
 // address faults the GPU, so every range a kernel will touch is checked
 // first: it must lie inside one pinned allocation made by pf_pinned_allocate
@@ -188,6 +216,12 @@ int load_layers_pending(pf_xfer* x, pf_layer_xfer* layers, uint32_t num_layers, 
 // num_layers layers and `chunks` chunks in all plans and issues before
 // planning the rest (0: the call is planned whole).
 uint32_t pipeline_head_layers(uint32_t num_layers, uint64_t chunks);
+
+// The mode a call in `mode` runs in on context x: PF_MODE_AUTO resolved
+// against the layers' host-side runs and the context's staging; other modes
+// unchanged.
+uint32_t resolve_mode(const pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
+                      uint32_t mode);
 
 // Writes the signal's value into all num_layers words on the context's
 // stream and waits: releases consumers of a load that failed before its

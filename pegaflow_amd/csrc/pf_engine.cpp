@@ -528,6 +528,10 @@ class DeviceWorker {
            const std::function<void()>& overlap);
   int submit(LoadTask&& task);
   void wait_idle();
+  // The mode a load in `mode` would run in on this device's load context.
+  uint32_t resolve_load_mode(uint32_t mode, const pf_layer_xfer* layers, uint32_t n) const {
+    return load_x_ ? resolve_mode(load_x_, layers, n, mode) : PF_MODE_KERNEL;
+  }
   // Hands a new task the block lists of a finished one (cleared, capacity
   // kept), so building a task allocates nothing new in steady state.
   void take_spares(LoadTask* task);
@@ -579,6 +583,12 @@ constexpr size_t kMaxWordMaps = 16;
 // defaults, 32 + 64).
 constexpr uint32_t kLoadGridAlone = 32;
 
+// Staging of the workers' transfer contexts (two slots each): the save
+// context's slots hold the staged mode's largest save slice, the load
+// context's twice its load slice (0.375 GiB of HBM per device in all).
+constexpr uint64_t kSaveStagingBytes = 2 * PF_STAGED_SAVE_SLICE_DEFAULT;
+constexpr uint64_t kLoadStagingBytes = 4 * PF_STAGED_LOAD_SLICE_DEFAULT;
+
 int DeviceWorker::create(int device, bool with_gpu, std::shared_ptr<DeviceWorker>* out,
                          std::atomic<uint64_t>* loaded_bytes, std::atomic<uint64_t>* failures) {
   auto w = std::make_shared<DeviceWorker>();
@@ -587,8 +597,8 @@ int DeviceWorker::create(int device, bool with_gpu, std::shared_ptr<DeviceWorker
   w->loaded_bytes_ = loaded_bytes;
   w->failures_ = failures;
   if (with_gpu) {
-    if (pf_xfer_create(device, 0, &w->save_x_) != PF_OK ||
-        pf_xfer_create(device, 0, &w->load_x_) != PF_OK)
+    if (pf_xfer_create(device, kSaveStagingBytes, &w->save_x_) != PF_OK ||
+        pf_xfer_create(device, kLoadStagingBytes, &w->load_x_) != PF_OK)
       return fail(PF_ERR_INIT, std::string("failed to initialize HIP: ") + pf_last_error());
   }
   w->thread_ = std::thread([p = w.get()] { p->load_loop(); });
@@ -1022,7 +1032,12 @@ struct pf_engine {
   std::unordered_map<std::string, std::shared_ptr<Instance>> instances;
   std::shared_ptr<PinnedPool> pool;
   std::unique_ptr<BlockStore> store;
-  std::atomic<uint32_t> save_mode{PF_MODE_KERNEL};
+  // Saves run staged (PF_MODE_AUTO: copy-engine DMA for a save batch's
+  // regions), leaving the device's other kernels at their speed: a zero-copy
+  // save held a bf16 GEMM in another process to 1/29th of its speed while it
+  // ran.  Loads, on the request's path, run the zero-copy kernel: the
+  // link's full rate and the first layer soonest, at 2.4x on such a GEMM.
+  std::atomic<uint32_t> save_mode{PF_MODE_AUTO};
   std::atomic<uint32_t> load_mode{PF_MODE_KERNEL};
   std::atomic<uint64_t> saved_bytes{0};
   std::atomic<uint64_t> loaded_bytes{0};
@@ -1163,11 +1178,8 @@ int pf_engine_destroy(pf_engine* e) {
 }
 
 int pf_engine_set_modes(pf_engine* e, uint32_t save_mode, uint32_t load_mode) {
-  if (save_mode > PF_MODE_STAGED || load_mode > PF_MODE_STAGED)
+  if (save_mode > PF_MODE_AUTO || load_mode > PF_MODE_AUTO)
     return fail(PF_ERR_INVALID_ARGUMENT, "invalid argument: unknown transfer mode");
-  if (save_mode == PF_MODE_STAGED || load_mode == PF_MODE_STAGED)
-    return fail(PF_ERR_INVALID_ARGUMENT,
-                "invalid argument: the engine's workers have no staging buffer");
   e->save_mode = save_mode;
   e->load_mode = load_mode;
   return PF_OK;
@@ -1577,6 +1589,15 @@ int pf_engine_batch_load(pf_engine* e, const char* instance_id, uint64_t tp_rank
   // still fails the call and the LoadState, but the first layers may have
   // been copied by then.
   task.mode = e->load_mode.load();
+  if (task.mode == PF_MODE_AUTO && num_layers > 0) {
+    // Blocks saved together lie alike in every layer: the first layer's
+    // list decides, so a load resolved to the kernel mode is still split.
+    std::vector<pf_block_xfer> probe;
+    uint64_t probe_bytes = 0;
+    if (int rc = build(0, 1, &probe, &probe_bytes)) return bail(rc);
+    const pf_layer_xfer lx{refs[0].reg, probe.data(), probe.size()};
+    task.mode = gpu->worker->resolve_load_mode(PF_MODE_AUTO, &lx, 1);
+  }
   uint64_t chunks = 0;
   for (const LayerRef& r : refs) chunks += n * (r.split ? 2 : 1);
   uint32_t head = 0;

@@ -13,6 +13,8 @@
 #include <thread>
 
 #include <hip/hip_runtime.h>
+#include <hsa/hsa.h>
+#include <hsa/hsa_ext_amd.h>
 
 #include "pf_common.h"
 
@@ -171,6 +173,161 @@ int noalloc_scratch(int device, NoAllocScratch** out) {
   sc->next_base = 0;
   *out = sc.get();
   g_scratch.emplace(device, std::move(sc));
+  return PF_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Copy engines.
+// ---------------------------------------------------------------------------
+struct EngineDevice {
+  bool ok = false;
+  hsa_agent_t gpu{}, cpu{};
+  uint32_t engine[2] = {0, 0};  // [0]: device to host, [1]: host to device
+};
+
+static std::mutex g_engine_mu;
+static std::map<int, EngineDevice> g_engines;
+
+namespace {
+
+struct AgentSearch {
+  uint32_t bdf = 0, domain = 0;
+  bool gpu_found = false, cpu_found = false;
+  hsa_agent_t gpu{}, cpu{};
+};
+
+hsa_status_t visit_agent(hsa_agent_t a, void* arg) {
+  AgentSearch* s = static_cast<AgentSearch*>(arg);
+  hsa_device_type_t t;
+  if (hsa_agent_get_info(a, HSA_AGENT_INFO_DEVICE, &t) != HSA_STATUS_SUCCESS)
+    return HSA_STATUS_SUCCESS;
+  if (t == HSA_DEVICE_TYPE_CPU && !s->cpu_found) {
+    s->cpu = a;
+    s->cpu_found = true;
+  }
+  if (t == HSA_DEVICE_TYPE_GPU && !s->gpu_found) {
+    uint32_t bdf = 0, domain = 0;
+    if (hsa_agent_get_info(a, static_cast<hsa_agent_info_t>(HSA_AMD_AGENT_INFO_BDFID), &bdf) ==
+            HSA_STATUS_SUCCESS &&
+        hsa_agent_get_info(a, static_cast<hsa_agent_info_t>(HSA_AMD_AGENT_INFO_DOMAIN),
+                           &domain) == HSA_STATUS_SUCCESS &&
+        bdf == s->bdf && domain == s->domain) {
+      s->gpu = a;
+      s->gpu_found = true;
+    }
+  }
+  return HSA_STATUS_SUCCESS;
+}
+
+uint32_t lowest_bit(uint32_t m) { return m & (~m + 1u); }
+
+// The device's agents (matched by PCI address) and engine choice.
+EngineDevice discover_engines(int device) {
+  EngineDevice d;
+  char bus[64] = {0};
+  unsigned dom = 0, b = 0, dv = 0, fn = 0;
+  if (hipDeviceGetPCIBusId(bus, sizeof(bus), device) != hipSuccess ||
+      std::sscanf(bus, "%x:%x:%x.%x", &dom, &b, &dv, &fn) != 4) {
+    (void)hipGetLastError();
+    return d;
+  }
+  // HIP has initialized the HSA runtime already; this holds a reference of
+  // the library's own (never released: engine copies may run until exit).
+  if (hsa_init() != HSA_STATUS_SUCCESS) return d;
+  AgentSearch s;
+  s.bdf = (b << 8) | (dv << 3) | fn;
+  s.domain = dom;
+  if (hsa_iterate_agents(visit_agent, &s) != HSA_STATUS_SUCCESS || !s.gpu_found) return d;
+  hsa_agent_t near{};
+  if (hsa_agent_get_info(s.gpu, static_cast<hsa_agent_info_t>(HSA_AMD_AGENT_INFO_NEAREST_CPU),
+                         &near) == HSA_STATUS_SUCCESS &&
+      near.handle != 0) {
+    s.cpu = near;
+    s.cpu_found = true;
+  }
+  if (!s.cpu_found) return d;
+  uint32_t d2h = 0, h2d = 0;
+  if (hsa_amd_memory_get_preferred_copy_engine(s.cpu, s.gpu, &d2h) != HSA_STATUS_SUCCESS ||
+      hsa_amd_memory_get_preferred_copy_engine(s.gpu, s.cpu, &h2d) != HSA_STATUS_SUCCESS ||
+      d2h == 0 || h2d == 0)
+    return d;
+  d.engine[1] = lowest_bit(h2d);
+  // Saves and loads run at once: give them different engines where the
+  // preferred sets allow.
+  const uint32_t other = d2h & ~d.engine[1];
+  d.engine[0] = lowest_bit(other ? other : d2h);
+  d.gpu = s.gpu;
+  d.cpu = s.cpu;
+  d.ok = true;
+  return d;
+}
+
+const EngineDevice* engines_of(int device) {
+  std::lock_guard<std::mutex> lk(g_engine_mu);
+  auto it = g_engines.find(device);
+  if (it == g_engines.end()) it = g_engines.emplace(device, discover_engines(device)).first;
+  return it->second.ok ? &it->second : nullptr;
+}
+
+hsa_signal_t sig_of(const EngineSignal* s) { return hsa_signal_t{s->handle}; }
+
+}  // namespace
+
+bool engine_copies_available(int device) { return engines_of(device) != nullptr; }
+
+int engine_signal_create(EngineSignal* s) {
+  hsa_signal_t h{};
+  if (hsa_signal_create(0, 0, nullptr, &h) != HSA_STATUS_SUCCESS)
+    return fail(PF_ERR_HIP, "hsa_signal_create failed");
+  s->handle = h.handle;
+  return PF_OK;
+}
+
+void engine_signal_destroy(EngineSignal* s) {
+  if (s->handle) (void)hsa_signal_destroy(sig_of(s));
+  s->handle = 0;
+}
+
+void engine_signal_add(EngineSignal* s, int64_t n) { hsa_signal_add_screlease(sig_of(s), n); }
+
+int engine_copy(int device, bool d2h, uint64_t dst, uint64_t src, uint64_t bytes,
+                EngineSignal* s) {
+  const EngineDevice* d = engines_of(device);
+  hsa_status_t r = HSA_STATUS_ERROR;
+  if (d) {
+    const hsa_agent_t dst_agent = d2h ? d->cpu : d->gpu;
+    const hsa_agent_t src_agent = d2h ? d->gpu : d->cpu;
+    r = hsa_amd_memory_async_copy_on_engine(
+        reinterpret_cast<void*>(dst), dst_agent, reinterpret_cast<const void*>(src), src_agent,
+        bytes, 0, nullptr, sig_of(s),
+        static_cast<hsa_amd_sdma_engine_id_t>(d->engine[d2h ? 0 : 1]), false);
+  }
+  if (r != HSA_STATUS_SUCCESS) {
+    hsa_signal_subtract_screlease(sig_of(s), 1);
+    return fail(PF_ERR_HIP, strf("copy engine refused a %s copy of %llu bytes (%d)",
+                                 d2h ? "device-to-host" : "host-to-device",
+                                 (unsigned long long)bytes, static_cast<int>(r)));
+  }
+  return PF_OK;
+}
+
+int engine_signal_wait(EngineSignal* s) {
+  const hsa_signal_t h = sig_of(s);
+  // Each wait is bounded to about 0.1 s (in system timestamp ticks) so the
+  // deadline below is checked.
+  static const uint64_t hint = [] {
+    uint64_t hz = 0;
+    if (hsa_system_get_info(HSA_SYSTEM_INFO_TIMESTAMP_FREQUENCY, &hz) != HSA_STATUS_SUCCESS ||
+        hz == 0)
+      hz = 1000000000ull;
+    return hz / 10;
+  }();
+  const auto t0 = std::chrono::steady_clock::now();
+  while (hsa_signal_wait_scacquire(h, HSA_SIGNAL_CONDITION_EQ, 0, hint,
+                                   HSA_WAIT_STATE_BLOCKED) != 0) {
+    if (std::chrono::steady_clock::now() - t0 > std::chrono::seconds(kEngineWaitSeconds))
+      return fail(PF_ERR_HIP, strf("copy engine copies not done after %d s", kEngineWaitSeconds));
+  }
   return PF_OK;
 }
 

@@ -298,6 +298,9 @@ constexpr uint32_t kScatterShapes[2][2] = {
 constexpr int kScatterTrialsPerShape = 2;
 constexpr uint64_t kScatterTrialMinBytes = 64ull << 20;  // time only launches this large
 
+// Staging slots of a staged call on the copy engines, at most.
+constexpr int kEngineSlots = 8;
+
 struct ScatterTrial {
   hipEvent_t start = nullptr, stop = nullptr;
   uint64_t bytes = 0;       // bytes of the launch being timed
@@ -327,12 +330,26 @@ struct pf_xfer {
   // memory (kHostDescMax entries), reused only once the stream has drained.
   ChunkDesc* h_small = nullptr;
   bool small_inflight = false;
+  // The upload kernel's own descriptor, read in place: [0] for a call's
+  // first part, [1] for a pipelined call's second part.
+  ChunkDesc* h_boot = nullptr;
   // Descriptor base the next launches read: d_desc, or h_small.
   const ChunkDesc* desc_base = nullptr;
+  // Staging for PF_MODE_STAGED: one slot per lane (stream, then dma), each
+  // slot_bytes long, the first at `staging`.
   uint64_t staging = 0;
   uint64_t slot_bytes = 0;
-  hipEvent_t slot_ready[2] = {nullptr, nullptr};
-  hipEvent_t slot_free[2] = {nullptr, nullptr};
+  // Largest staged slice per direction (0: save, 1: load), capped by slot_bytes.
+  uint64_t staged_slice[2] = {PF_STAGED_SAVE_SLICE_DEFAULT, PF_STAGED_LOAD_SLICE_DEFAULT};
+  // Recorded on a lane for the other lane to wait on (one per lane).
+  hipEvent_t lane_mark[2] = {nullptr, nullptr};
+  // Staged copies on the copy engines (when the device's are known): one
+  // completion signal and one kernel-done event per staging slot, and the
+  // end of the last staged call's kernels on the context's stream.
+  bool engine_ok = false;
+  EngineSignal eng_sig[kEngineSlots];
+  hipEvent_t eng_ev[kEngineSlots] = {};
+  hipEvent_t staging_free = nullptr;
   // Launch shapes per route (PF_ROUTE_*), the fastest measured on MI355X:
   //   gather into HBM:   512 threads, one non-temporal 16 B load per lane
   //                      (8 KiB tiles), round-robin tile order;
@@ -384,14 +401,17 @@ int ensure_desc_capacity(pf_xfer* x, size_t n) {
     if (x->h_desc) PF_HIP(hipHostFree(x->h_desc));
     x->h_desc = nullptr;
     x->h_cap = 0;
+    // Read in place by the upload kernel: mapped, and uncached on the device
+    // (rewritten by the host between calls).
     PF_HIP(hipHostMalloc(reinterpret_cast<void**>(&x->h_desc), cap * sizeof(ChunkDesc),
-                         hipHostMallocDefault));
+                         hipHostMallocMapped | hipHostMallocCoherent));
     x->h_cap = cap;
   }
   if (n > x->d_cap) {
     size_t cap = 1;
     while (cap < n) cap <<= 1;
     // Kernels of earlier calls may still read the old buffer.
+    PF_HIP(hipStreamSynchronize(x->dma));
     PF_HIP(hipStreamSynchronize(x->stream));
     if (x->d_desc) PF_HIP(hipFree(x->d_desc));
     x->d_desc = nullptr;
@@ -401,6 +421,9 @@ int ensure_desc_capacity(pf_xfer* x, size_t n) {
   }
   return PF_OK;
 }
+
+// Workgroup size of the descriptor upload kernel (4 KiB tiles).
+constexpr uint32_t kDescUploadThreads = 256;
 
 // Copies descriptors [off, off + n) of the host staging to the same place in
 // device memory; the next launches read from there.  A later part of a
@@ -419,8 +442,18 @@ int upload_desc(pf_xfer* x, size_t n, size_t off = 0) {
     PF_HIP(hipStreamWaitEvent(s, x->parts_ready, 0));
     PF_HIP(hipStreamWaitEvent(s, x->desc_uploaded, 0));
   }
-  PF_HIP(hipMemcpyAsync(x->d_desc + off, x->h_desc + off, n * sizeof(ChunkDesc),
-                        hipMemcpyHostToDevice, s));
+  // Copied by the chunk kernel, which reads the host staging in place (one
+  // boot descriptor per part of a call, itself read in place), not by a DMA
+  // copy: the process's DMA copies to the device share an engine queue, so a
+  // staged restore's 1.25 GiB of copies held a concurrent save's 640 KiB
+  // upload, and with it the whole save, for 28 ms.
+  ChunkDesc* boot = x->h_boot + (off ? 1 : 0);
+  *boot = ChunkDesc{reinterpret_cast<uint64_t>(x->h_desc + off),
+                    reinterpret_cast<uint64_t>(x->d_desc + off)};
+  (void)hipGetLastError();
+  const hipError_t e = launch_copy_chunks(boot, 1, n * sizeof(ChunkDesc), true,
+                                          kDescUploadThreads, 1, 0, s);
+  if (e != hipSuccess) return hip_fail(e, "descriptor upload kernel launch");
   PF_HIP(hipEventRecord(x->desc_uploaded, s));
   if (off) PF_HIP(hipStreamWaitEvent(x->stream, x->desc_uploaded, 0));
   x->desc_inflight = true;
@@ -542,8 +575,10 @@ int check_launch_size(size_t n, uint64_t chunk_bytes) {
 }
 
 int launch(pf_xfer* x, size_t first, size_t n, uint64_t chunk_bytes, bool al16, bool is_save,
-           bool host_side = false, const LayerMarks* marks = nullptr) {
+           bool host_side = false, const LayerMarks* marks = nullptr,
+           hipStream_t stream = nullptr) {
   if (n == 0) return PF_OK;
+  if (!stream) stream = x->stream;
   const int dir = (is_save ? PF_ROUTE_SAVE_DEVICE : PF_ROUTE_LOAD_DEVICE) + (host_side ? 2 : 0);
   if (int rc = check_launch_size(n, chunk_bytes)) return rc;
   std::pair<hipEvent_t, hipEvent_t>* tm = nullptr;
@@ -555,7 +590,7 @@ int launch(pf_xfer* x, size_t first, size_t n, uint64_t chunk_bytes, bool al16, 
       x->timers.push_back(p);
     }
     tm = &x->timers[x->last_kernels];
-    PF_HIP(hipEventRecord(tm->first, x->stream));
+    PF_HIP(hipEventRecord(tm->first, stream));
   }
   // Queued launches: copies over the host link, and every marking launch
   // (its layers must land in order).  See copy_chunks_queue_kernel.
@@ -572,19 +607,19 @@ int launch(pf_xfer* x, size_t first, size_t n, uint64_t chunk_bytes, bool al16, 
     const int pick = scatter_pick(x, static_cast<uint64_t>(n) * chunk_bytes, &trial);
     threads = kScatterShapes[pick][0];
     unroll = kScatterShapes[pick][1];
-    if (trial) PF_HIP(hipEventRecord(trial->start, x->stream));
+    if (trial) PF_HIP(hipEventRecord(trial->start, stream));
   }
   unroll &= ~PF_KERNEL_AUTO;
-  const hipError_t e = issue_copy(x->stream, x->desc_base + first, n, chunk_bytes, al16,
+  const hipError_t e = issue_copy(stream, x->desc_base + first, n, chunk_bytes, al16,
                                   threads, unroll, qgrid, x->max_grid, marks, x->d_next,
                                   &x->next_base);
   if (e != hipSuccess) return hip_fail(e, "gather/scatter kernel launch");
   if (trial) {
-    PF_HIP(hipEventRecord(trial->stop, x->stream));
+    PF_HIP(hipEventRecord(trial->stop, stream));
     trial->bytes = static_cast<uint64_t>(n) * chunk_bytes;
     trial->pending = true;
   }
-  if (tm) PF_HIP(hipEventRecord(tm->second, x->stream));
+  if (tm) PF_HIP(hipEventRecord(tm->second, stream));
   x->last_kernels++;
   return PF_OK;
 }
@@ -595,7 +630,8 @@ int ensure_counters(pf_xfer* x, size_t num_layers) {
   if (num_layers <= x->counters_cap) return PF_OK;
   size_t cap = 64;
   while (cap < num_layers) cap <<= 1;
-  PF_HIP(hipStreamSynchronize(x->stream));  // earlier launches may still count
+  PF_HIP(hipStreamSynchronize(x->dma));  // earlier launches may still count
+  PF_HIP(hipStreamSynchronize(x->stream));
   if (x->d_counters) PF_HIP(hipFree(x->d_counters));
   x->d_counters = nullptr;
   x->d_next = nullptr;
@@ -611,13 +647,15 @@ int ensure_counters(pf_xfer* x, size_t num_layers) {
 }
 
 // Marks the given layers on the context's stream (after the work queued so far).
-int mark_layers(pf_xfer* x, const std::vector<uint32_t>& ids, const SignalTargets& t) {
+int mark_layers(pf_xfer* x, const std::vector<uint32_t>& ids, const SignalTargets& t,
+                hipStream_t stream = nullptr) {
+  if (!stream) stream = x->stream;
   for (size_t i = 0; i < ids.size(); i += kLayerListMax) {
     LayerList list{};
     list.n = static_cast<uint32_t>(std::min<size_t>(kLayerListMax, ids.size() - i));
     for (uint32_t k = 0; k < list.n; ++k) list.ids[k] = ids[i + k];
     (void)hipGetLastError();
-    hipError_t e = launch_mark_layers(list, t, x->stream);
+    hipError_t e = launch_mark_layers(list, t, stream);
     if (e != hipSuccess) return hip_fail(e, "layer mark kernel launch");
   }
   return PF_OK;
@@ -627,14 +665,6 @@ int mark_layer(pf_xfer* x, uint32_t li, const SignalTargets* t) {
   if (!t) return PF_OK;
   return mark_layers(x, std::vector<uint32_t>{li}, *t);
 }
-
-// A staged slice: chunks [begin, end) of one layer packed into one slot.
-struct Slice {
-  uint32_t layer;
-  size_t begin, end;
-  int slot;
-  size_t desc_first;  // descriptors for the slice's kernel
-};
 
 int plan_all(const pf_layer_xfer* layers, uint32_t n, bool is_save,
              std::vector<LayerPlan>* plans) {
@@ -699,131 +729,484 @@ int dma_layer(pf_xfer* x, const LayerPlan& p, bool is_save, bool per_chunk_sync)
 }
 
 // ---- staged mode ----------------------------------------------------------
-int plan_slices(pf_xfer* x, const std::vector<LayerPlan>& plans,
-                std::vector<Slice>* slices, size_t* n_desc) {
-  size_t d = 0;
-  int slot = 0;
+// The host link is crossed only by DMA copies of host-contiguous runs; the
+// chunk kernel moves the paged side between the layer tensors and a packed
+// staging slot in HBM.  Host-memory traffic issued by shaders (the zero-copy
+// kernels) holds up the memory traffic of every other kernel on the device
+// while it runs: measured from another process, a bf16 8192^3 GEMM ran 29x
+// slower beside a zero-copy save of the Llama prefix and 2.4x slower beside
+// a zero-copy restore, against 1.03x beside this mode.
+//
+// A call's chunks are cut, in layer order, into slices of at most the
+// direction's slice size; a slice may span layers, but not an ordered layer
+// (copied in place, in list order) or a change of chunk size.  Consecutive
+// slices alternate between the context's two lanes (its two streams), each
+// lane owning one staging slot: a slice's copies and kernel run in order on
+// its lane, so the lane's next slice refills the slot only once the kernel
+// has read it, with no wait across streams, while the other lane's copies
+// keep the link busy.  (On one stream each copy starts about 10 us after the
+// previous one ends: 8 MiB copies moved 53.7 GB/s host to device on one
+// stream, 57.4 GB/s alternating over two.)
+struct Piece {
+  uint32_t layer;
+  size_t begin, end;  // chunks [begin, end) of the layer's plan
+};
+
+struct StagedStep {
+  size_t piece_begin = 0, piece_end = 0;  // pieces[piece_begin, piece_end)
+  uint64_t chunk_bytes = 0;
+  size_t n_chunks = 0;
+  size_t desc_first = 0;
+  int64_t ordered_layer = -1;  // >= 0: this step is that layer's in-place copies
+  int lane = 0;
+};
+
+struct StagedPlan {
+  std::vector<StagedStep> steps;
+  std::vector<Piece> pieces;
+  // Per layer: the step after which its bytes are in place (-1: before any).
+  std::vector<int64_t> done_at;
+  size_t n_desc = 0;
+};
+
+int plan_staged(const pf_xfer* x, const std::vector<LayerPlan>& plans, bool is_save,
+                StagedPlan* sp) {
+  const uint64_t cap = std::min(x->slot_bytes, x->staged_slice[is_save ? 0 : 1]);
+  sp->steps.clear();
+  sp->pieces.clear();
+  sp->done_at.assign(plans.size(), -1);
+  sp->n_desc = 0;
+  StagedStep cur;
+  uint64_t cur_bytes = 0;
+  auto close = [&]() {
+    if (cur.n_chunks > 0) {
+      cur.piece_end = sp->pieces.size();
+      cur.desc_first = sp->n_desc;
+      sp->n_desc += cur.n_chunks;
+      sp->steps.push_back(cur);
+    }
+    cur = StagedStep{};
+    cur.piece_begin = sp->pieces.size();
+    cur_bytes = 0;
+  };
   for (uint32_t li = 0; li < plans.size(); ++li) {
     const LayerPlan& p = plans[li];
-    if (p.chunks.empty() || p.ordered) continue;
+    if (p.ordered) {
+      close();
+      StagedStep st;
+      st.piece_begin = st.piece_end = sp->pieces.size();
+      st.ordered_layer = li;
+      sp->steps.push_back(st);
+      sp->done_at[li] = static_cast<int64_t>(sp->steps.size()) - 1;
+      continue;
+    }
+    if (p.chunks.empty()) {
+      // In place once everything before it is: after the open slice, if any.
+      sp->done_at[li] = static_cast<int64_t>(sp->steps.size()) - (cur.n_chunks > 0 ? 0 : 1);
+      continue;
+    }
     if (p.chunk_bytes > x->slot_bytes)
       return fail(PF_ERR_INVALID_ARGUMENT,
                   strf("staging slot (%llu bytes) smaller than one chunk (%llu)",
                        (unsigned long long)x->slot_bytes,
                        (unsigned long long)p.chunk_bytes));
-    const size_t per_slot = static_cast<size_t>(x->slot_bytes / p.chunk_bytes);
-    for (size_t b = 0; b < p.chunks.size(); b += per_slot) {
-      const size_t e = std::min(p.chunks.size(), b + per_slot);
-      slices->push_back({li, b, e, slot, d});
-      d += e - b;
-      slot ^= 1;
+    if (cur.n_chunks > 0 && cur.chunk_bytes != p.chunk_bytes) close();
+    // A slice holds at least one chunk, even one larger than the slice size.
+    const uint64_t lcap = std::max(cap, p.chunk_bytes);
+    size_t i = 0;
+    while (i < p.chunks.size()) {
+      const size_t room = static_cast<size_t>((lcap - cur_bytes) / p.chunk_bytes);
+      if (room == 0) {
+        close();
+        continue;
+      }
+      const size_t take = std::min(room, p.chunks.size() - i);
+      cur.chunk_bytes = p.chunk_bytes;
+      sp->pieces.push_back({li, i, i + take});
+      cur.n_chunks += take;
+      cur_bytes += take * p.chunk_bytes;
+      i += take;
     }
+    sp->done_at[li] = static_cast<int64_t>(sp->steps.size());  // the open slice
   }
-  *n_desc = d;
+  close();
+  if (sp->n_desc > 0xffffffffull) return fail(PF_ERR_INVALID_ARGUMENT, "too many chunks");
   return PF_OK;
 }
 
-// Host-contiguous runs inside a slice, packed in the staging slot in chunk
-// order: chunk k of the slice sits at slot + (k - begin) * chunk_bytes.
+// A staged save may copy its slices out on both lanes only when no two of its
+// host-side chunks overlap: the reference's in-order copies decide which
+// bytes an overlap keeps, and one lane keeps that order.  Checked per layer,
+// then across layers by their spans (sorting every chunk only when spans of
+// different layers interleave).
+bool save_hosts_disjoint(const std::vector<LayerPlan>& plans) {
+  std::vector<std::pair<uint64_t, uint64_t>> spans;
+  for (const LayerPlan& p : plans) {
+    if (p.chunks.empty()) continue;
+    if (!host_chunks_disjoint(p)) return false;
+    uint64_t lo = p.chunks[0].host, hi = p.chunks[0].host;
+    for (const Chunk& c : p.chunks) {
+      lo = std::min(lo, c.host);
+      hi = std::max(hi, c.host);
+    }
+    spans.push_back({lo, hi + p.chunk_bytes});
+  }
+  std::sort(spans.begin(), spans.end());
+  bool interleaved = false;
+  for (size_t i = 1; i < spans.size() && !interleaved; ++i)
+    interleaved = spans[i].first < spans[i - 1].second;
+  if (!interleaved) return true;
+  std::vector<std::pair<uint64_t, uint64_t>> all;
+  for (const LayerPlan& p : plans)
+    for (const Chunk& c : p.chunks) all.push_back({c.host, c.host + p.chunk_bytes});
+  std::sort(all.begin(), all.end());
+  for (size_t i = 1; i < all.size(); ++i)
+    if (all[i].first < all[i - 1].second) return false;
+  return true;
+}
+
+// Calls fn(chunk, k) for the chunks of a staged step in order, k counting
+// from 0 (the chunk's place in the slot).
 template <class F>
-void for_each_host_run(const LayerPlan& p, size_t begin, size_t end, F fn) {
-  size_t i = begin;
-  while (i < end) {
-    size_t n = 1;
-    while (i + n < end && p.chunks[i + n].host == p.chunks[i].host + n * p.chunk_bytes) ++n;
-    fn(i, n);
-    i += n;
+void for_each_step_chunk(const std::vector<LayerPlan>& plans, const StagedPlan& sp,
+                         const StagedStep& st, F fn) {
+  size_t k = 0;
+  for (size_t pi = st.piece_begin; pi < st.piece_end; ++pi) {
+    const Piece& pc = sp.pieces[pi];
+    const LayerPlan& p = plans[pc.layer];
+    for (size_t i = pc.begin; i < pc.end; ++i) fn(p.chunks[i], k++);
   }
 }
 
-// One staged slice.  Save: the gather kernel packs the slice into the slot,
-// then the link-side stream copies each host-contiguous run out.  Load: the
-// link-side stream copies the runs into the slot, then the scatter kernel
-// places them.  slot_free / slot_ready order the two streams per slot.
-int staged_slice(pf_xfer* x, const std::vector<LayerPlan>& plans, const Slice& s,
-                 bool is_save) {
-  const LayerPlan& p = plans[s.layer];
-  const uint64_t slot_base = x->staging + static_cast<uint64_t>(s.slot) * x->slot_bytes;
-  const bool al16 = aligned16(p.chunk_bytes) && aligned16(slot_base) &&
-                    std::all_of(p.chunks.begin() + s.begin, p.chunks.begin() + s.end,
-                                [](const Chunk& c) { return aligned16(c.dev); });
-  hipError_t e = hipSuccess;
-  auto dma_run = [&](size_t i, size_t n) {
-    if (e != hipSuccess) return;
-    const uint64_t st = slot_base + (i - s.begin) * p.chunk_bytes;
-    const uint64_t bytes = n * p.chunk_bytes;
-    if (is_save)
-      e = hipMemcpyAsync(reinterpret_cast<void*>(p.chunks[i].host),
-                         reinterpret_cast<void*>(st), bytes, hipMemcpyDefault, x->dma);
-    else
-      e = hipMemcpyAsync(reinterpret_cast<void*>(st),
-                         reinterpret_cast<void*>(p.chunks[i].host), bytes,
-                         hipMemcpyDefault, x->dma);
-    x->last_dma++;
+// Waits for every copy-engine copy the context has in flight.
+int engine_drain(pf_xfer* x) {
+  if (!x->engine_ok) return PF_OK;
+  int rc = PF_OK;
+  for (EngineSignal& s : x->eng_sig)
+    if (int r = engine_signal_wait(&s)) rc = r;
+  return rc;
+}
+
+// True when every host-side chunk of the staged layers lies in pinned memory
+// (the copy engines read and write it directly); checked per layer by its
+// span first.
+bool hosts_pinned(const std::vector<LayerPlan>& plans) {
+  for (const LayerPlan& p : plans) {
+    if (p.chunks.empty() || p.ordered) continue;
+    uint64_t lo = p.chunks[0].host, hi = p.chunks[0].host;
+    for (const Chunk& c : p.chunks) {
+      lo = std::min(lo, c.host);
+      hi = std::max(hi, c.host);
+    }
+    uint64_t b = 0, e = 0;
+    if (hi + p.chunk_bytes >= hi && pinned_lookup(lo, hi + p.chunk_bytes - lo, &b, &e)) continue;
+    for (const Chunk& c : p.chunks)
+      if (!pinned_lookup(c.host, p.chunk_bytes, &b, &e)) return false;
+  }
+  return true;
+}
+
+// The staged mode with its copies on the device's copy engines, driven from
+// the calling thread.  An engine runs its copies in submission order, one
+// after another, so keeping the next slice's copy queued behind the running
+// one keeps the link busy: a save gathers a slice into its slot, waits for
+// the gather and queues the slot's copies; a load queues the copies of the
+// first slots and, as each slot's copies complete, scatters it and queues
+// the copies that refill it once the scatter is done.  Every kernel runs on
+// the context's stream.  A load returns once its copies are done and its
+// last kernels are issued, with its layer events and marks recorded.
+int staged_engine(pf_xfer* x, const std::vector<LayerPlan>& plans, StagedPlan& sp,
+                  bool is_save, pf_event* layer_events, const SignalTargets* sig,
+                  bool wait_save) {
+  // Slots: as many as the staging holds of the largest slice (at least one).
+  uint64_t stride = 0;
+  std::vector<size_t> slice_of(sp.steps.size(), SIZE_MAX);
+  size_t n_slices = 0;
+  for (size_t si = 0; si < sp.steps.size(); ++si) {
+    const StagedStep& st = sp.steps[si];
+    if (st.ordered_layer >= 0) continue;
+    slice_of[si] = n_slices++;
+    stride = std::max(stride, st.n_chunks * st.chunk_bytes);
+  }
+  stride = (stride + 255) & ~uint64_t(255);
+  size_t n_slots = 1;
+  if (stride > 0)
+    n_slots = static_cast<size_t>(
+        std::max<uint64_t>(1, std::min<uint64_t>(kEngineSlots, 2 * x->slot_bytes / stride)));
+  auto slot_base = [&](size_t j) {
+    return x->staging + static_cast<uint64_t>(j % n_slots) * stride;
+  };
+  ChunkDesc* hd = small_desc(x, sp.n_desc);
+  if (!hd) {
+    if (int rc = ensure_desc_capacity(x, sp.n_desc)) return rc;
+    hd = x->h_desc;
+  }
+  for (size_t si = 0; si < sp.steps.size(); ++si) {
+    const StagedStep& st = sp.steps[si];
+    if (st.ordered_layer >= 0) continue;
+    const uint64_t slot = slot_base(slice_of[si]);
+    for_each_step_chunk(plans, sp, st, [&](const Chunk& c, size_t k) {
+      const uint64_t at = slot + k * st.chunk_bytes;
+      hd[st.desc_first + k] = is_save ? ChunkDesc{c.dev, at} : ChunkDesc{at, c.dev};
+    });
+  }
+  if (hd == x->h_small) {
+    x->desc_base = x->h_small;
+    x->small_inflight = true;
+  } else if (int rc = upload_desc(x, sp.n_desc)) {
+    return rc;
+  }
+  // The host-contiguous runs of a slice, each one engine copy.
+  auto queue_copies = [&](size_t si) -> int {
+    const StagedStep& st = sp.steps[si];
+    const size_t j = slice_of[si];
+    EngineSignal* es = &x->eng_sig[j % n_slots];
+    const uint64_t slot = slot_base(j), cb = st.chunk_bytes;
+    uint64_t run_host = 0, run_at = 0, run_bytes = 0;
+    int rc = PF_OK;
+    auto flush = [&]() {
+      if (run_bytes == 0 || rc != PF_OK) return;
+      engine_signal_add(es, 1);
+      rc = is_save ? engine_copy(x->device, true, run_host, run_at, run_bytes, es)
+                   : engine_copy(x->device, false, run_at, run_host, run_bytes, es);
+      x->last_dma++;
+    };
+    for_each_step_chunk(plans, sp, st, [&](const Chunk& c, size_t k) {
+      if (run_bytes > 0 && c.host == run_host + run_bytes) {
+        run_bytes += cb;
+        return;
+      }
+      flush();
+      run_host = c.host;
+      run_at = slot + k * cb;
+      run_bytes = cb;
+    });
+    flush();
+    return rc;
+  };
+  auto kernel = [&](size_t si) -> int {
+    const StagedStep& st = sp.steps[si];
+    const uint64_t slot = slot_base(slice_of[si]);
+    bool al16 = aligned16(st.chunk_bytes) && aligned16(slot);
+    for_each_step_chunk(plans, sp, st,
+                        [&](const Chunk& c, size_t) { al16 = al16 && aligned16(c.dev); });
+    return launch(x, st.desc_first, st.n_chunks, st.chunk_bytes, al16, is_save);
+  };
+  // Kernels of slot s done (waited for on the host).
+  auto kernels_done = [&](size_t s) -> int {
+    PF_HIP(hipEventRecord(x->eng_ev[s], x->stream));
+    PF_HIP(hipEventSynchronize(x->eng_ev[s]));
+    return PF_OK;
   };
   if (is_save) {
-    PF_HIP(hipStreamWaitEvent(x->stream, x->slot_free[s.slot], 0));
-    if (int rc = launch(x, s.desc_first, s.end - s.begin, p.chunk_bytes, al16, true)) return rc;
-    PF_HIP(hipEventRecord(x->slot_ready[s.slot], x->stream));
-    PF_HIP(hipStreamWaitEvent(x->dma, x->slot_ready[s.slot], 0));
-    for_each_host_run(p, s.begin, s.end, dma_run);
-    if (e != hipSuccess) return hip_fail(e, "staged hipMemcpyAsync (D2H)");
-    PF_HIP(hipEventRecord(x->slot_free[s.slot], x->dma));
-  } else {
-    PF_HIP(hipStreamWaitEvent(x->dma, x->slot_free[s.slot], 0));
-    for_each_host_run(p, s.begin, s.end, dma_run);
-    if (e != hipSuccess) return hip_fail(e, "staged hipMemcpyAsync (H2D)");
-    PF_HIP(hipEventRecord(x->slot_ready[s.slot], x->dma));
-    PF_HIP(hipStreamWaitEvent(x->stream, x->slot_ready[s.slot], 0));
-    if (int rc = launch(x, s.desc_first, s.end - s.begin, p.chunk_bytes, al16, false)) return rc;
-    PF_HIP(hipEventRecord(x->slot_free[s.slot], x->stream));
+    for (size_t si = 0; si < sp.steps.size(); ++si) {
+      const size_t s = slice_of[si] % n_slots;
+      // The slot's previous copies (of this call or an earlier one) are done.
+      if (int rc = engine_signal_wait(&x->eng_sig[s])) return rc;
+      if (int rc = kernel(si)) return rc;
+      if (int rc = kernels_done(s)) return rc;
+      if (int rc = queue_copies(si)) return rc;
+    }
+    if (wait_save) return engine_drain(x);
+    return PF_OK;
+  }
+  size_t next_layer = 0;
+  auto complete = [&](int64_t step) -> int {
+    std::vector<uint32_t> ids;
+    while (next_layer < plans.size() && sp.done_at[next_layer] == step)
+      ids.push_back(static_cast<uint32_t>(next_layer++));
+    if (ids.empty()) return PF_OK;
+    for (uint32_t li : ids)
+      if (layer_events && layer_events[li])
+        PF_HIP(hipEventRecord(static_cast<hipEvent_t>(layer_events[li]), x->stream));
+    if (sig)
+      if (int rc = mark_layers(x, ids, *sig)) return rc;
+    return PF_OK;
+  };
+  if (int rc = complete(-1)) return rc;
+  // The first slots' copies, then each slot refilled after its scatter.
+  std::vector<size_t> slice_steps;
+  for (size_t si = 0; si < sp.steps.size(); ++si)
+    if (slice_of[si] != SIZE_MAX) slice_steps.push_back(si);
+  size_t queued = 0;
+  for (; queued < slice_steps.size() && queued < n_slots; ++queued)
+    if (int rc = queue_copies(slice_steps[queued])) return rc;
+  for (size_t si = 0; si < sp.steps.size(); ++si) {
+    const StagedStep& st = sp.steps[si];
+    if (st.ordered_layer >= 0) {
+      if (int rc = dma_layer(x, plans[static_cast<size_t>(st.ordered_layer)], false, false))
+        return rc;
+    } else {
+      const size_t s = slice_of[si] % n_slots;
+      if (int rc = engine_signal_wait(&x->eng_sig[s])) return rc;
+      if (int rc = kernel(si)) return rc;
+      if (queued < slice_steps.size()) {
+        if (int rc = kernels_done(s)) return rc;
+        if (int rc = queue_copies(slice_steps[queued++])) return rc;
+      }
+    }
+    if (int rc = complete(static_cast<int64_t>(si))) return rc;
   }
   return PF_OK;
 }
 
 int staged(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<LayerPlan>& plans,
-           bool is_save, pf_event* layer_events, const SignalTargets* sig) {
+           bool is_save, pf_event* layer_events, const SignalTargets* sig, bool wait_save) {
   if (x->staging == 0 || x->slot_bytes == 0)
     return fail(PF_ERR_INVALID_ARGUMENT, "transfer context has no staging buffer");
-  std::vector<Slice> slices;
-  size_t n_desc = 0;
-  if (int rc = plan_slices(x, plans, &slices, &n_desc)) return rc;
+  StagedPlan sp;
+  if (int rc = plan_staged(x, plans, is_save, &sp)) return rc;
   {
     RangeCache rc;
     for (size_t i = 0; i < plans.size(); ++i)
       if (!plans[i].chunks.empty() && !plans[i].ordered)
         if (int r = check_device_tensor(rc, layers[i].layout)) return r;
   }
-  if (int rc = ensure_desc_capacity(x, n_desc)) return rc;
-  // The tile queue, for device routes a caller has set to run queued.
-  if (int rc = ensure_counters(x, plans.size())) return rc;
-  for (const Slice& s : slices) {
-    const LayerPlan& p = plans[s.layer];
-    const uint64_t slot_base = x->staging + static_cast<uint64_t>(s.slot) * x->slot_bytes;
-    for (size_t k = s.begin; k < s.end; ++k) {
-      const uint64_t st = slot_base + (k - s.begin) * p.chunk_bytes;
-      ChunkDesc& d = x->h_desc[s.desc_first + (k - s.begin)];
-      if (is_save) d = {p.chunks[k].dev, st};
-      else d = {st, p.chunks[k].dev};
-    }
+  // Nothing of an earlier staged call may still use the slots.
+  if (int rc = engine_drain(x)) return rc;
+  if (x->engine_ok && hosts_pinned(plans)) {
+    if (int rc = ensure_counters(x, plans.size())) return rc;  // queued device routes
+    PF_HIP(hipEventSynchronize(x->staging_free));
+    const int rc = staged_engine(x, plans, sp, is_save, layer_events, sig, wait_save);
+    PF_HIP(hipEventRecord(x->staging_free, x->stream));
+    return rc;
   }
-  if (int rc = upload_desc(x, n_desc)) return rc;
-  size_t si = 0;
-  for (uint32_t li = 0; li < plans.size(); ++li) {
-    if (plans[li].ordered) {
-      if (int rc = dma_layer(x, plans[li], is_save, false)) return rc;
-    }
-    for (; si < slices.size() && slices[si].layer == li; ++si)
-      if (int rc = staged_slice(x, plans, slices[si], is_save)) return rc;
-    if (!is_save && layer_events && layer_events[li])
-      PF_HIP(hipEventRecord(static_cast<hipEvent_t>(layer_events[li]), x->stream));
-    if (!is_save)
-      if (int rc = mark_layer(x, li, sig)) return rc;
+  // One lane when the kernel launches run queued (they share one tile
+  // counter, so they must not overlap) or when a save's order matters.
+  const int route = is_save ? PF_ROUTE_SAVE_DEVICE : PF_ROUTE_LOAD_DEVICE;
+  const int lanes = (x->grid[route] > 0 || (is_save && !save_hosts_disjoint(plans))) ? 1 : 2;
+  hipStream_t lane_s[2] = {x->stream, x->dma};
+  {
+    int k = 0;
+    for (StagedStep& st : sp.steps)
+      st.lane = st.ordered_layer >= 0 ? 0 : (k++ % lanes);
   }
-  if (is_save) {
+  if (int rc = ensure_counters(x, plans.size())) return rc;  // queued device routes
+  ChunkDesc* hd = small_desc(x, sp.n_desc);
+  if (!hd) {
+    if (int rc = ensure_desc_capacity(x, sp.n_desc)) return rc;
+    hd = x->h_desc;
+  }
+  for (const StagedStep& st : sp.steps) {
+    if (st.ordered_layer >= 0) continue;
+    const uint64_t slot = x->staging + static_cast<uint64_t>(st.lane) * x->slot_bytes;
+    for_each_step_chunk(plans, sp, st, [&](const Chunk& c, size_t k) {
+      const uint64_t at = slot + k * st.chunk_bytes;
+      hd[st.desc_first + k] = is_save ? ChunkDesc{c.dev, at} : ChunkDesc{at, c.dev};
+    });
+  }
+  if (hd == x->h_small) {
+    x->desc_base = x->h_small;
+    x->small_inflight = true;
+  } else if (int rc = upload_desc(x, sp.n_desc)) {
+    return rc;
+  }
+  // pending[l]: lane l has work the other lane has not waited for.
+  bool pending[2] = {false, false};
+  auto join = [&](int to, int from) -> int {
+    if (!pending[from]) return PF_OK;
+    PF_HIP(hipEventRecord(x->lane_mark[from], lane_s[from]));
+    PF_HIP(hipStreamWaitEvent(lane_s[to], x->lane_mark[from], 0));
+    pending[from] = false;
+    return PF_OK;
+  };
+  // Lane 1 starts after the descriptors are uploaded and after everything
+  // earlier calls left on the context's stream.
+  pending[0] = true;
+  if (lanes == 2)
+    if (int rc = join(1, 0)) return rc;
+  pending[0] = false;
+  // Load completion of the layers done after step s (s = -1: before any), on
+  // lane `to`: once every step so far is done, then in layer order.
+  size_t next_layer = 0;
+  auto complete = [&](int64_t s, int to) -> int {
+    if (is_save) return PF_OK;
+    std::vector<uint32_t> ids;
+    while (next_layer < plans.size() && sp.done_at[next_layer] == s)
+      ids.push_back(static_cast<uint32_t>(next_layer++));
+    if (ids.empty()) return PF_OK;
+    if (int rc = join(to, 1 - to)) return rc;
+    for (uint32_t li : ids)
+      if (layer_events && layer_events[li])
+        PF_HIP(hipEventRecord(static_cast<hipEvent_t>(layer_events[li]), lane_s[to]));
+    if (sig)
+      if (int rc = mark_layers(x, ids, *sig, lane_s[to])) return rc;
+    // A later layer's completion on the other lane comes after these.
+    pending[to] = true;
+    return PF_OK;
+  };
+  if (int rc = complete(-1, 0)) return rc;
+  hipError_t e = hipSuccess;
+  for (size_t si = 0; si < sp.steps.size(); ++si) {
+    const StagedStep& st = sp.steps[si];
+    const int L = st.lane;
+    if (st.ordered_layer >= 0) {
+      // In place, after everything before it, and before anything after it.
+      if (int rc = join(0, 1)) return rc;
+      if (int rc = dma_layer(x, plans[static_cast<size_t>(st.ordered_layer)], is_save, false))
+        return rc;
+      pending[0] = true;
+      if (lanes == 2)
+        if (int rc = join(1, 0)) return rc;
+    } else {
+      const uint64_t slot = x->staging + static_cast<uint64_t>(L) * x->slot_bytes;
+      const uint64_t cb = st.chunk_bytes;
+      bool al16 = aligned16(cb) && aligned16(slot);
+      for_each_step_chunk(plans, sp, st,
+                          [&](const Chunk& c, size_t) { al16 = al16 && aligned16(c.dev); });
+      // The host-contiguous runs of the step, each one DMA copy to or from
+      // its place in the slot.
+      auto copy_runs = [&]() {
+        uint64_t run_host = 0, run_at = 0, run_bytes = 0;
+        auto flush = [&]() {
+          if (run_bytes == 0 || e != hipSuccess) return;
+          if (is_save)
+            e = hipMemcpyAsync(reinterpret_cast<void*>(run_host),
+                               reinterpret_cast<void*>(run_at), run_bytes, hipMemcpyDefault,
+                               lane_s[L]);
+          else
+            e = hipMemcpyAsync(reinterpret_cast<void*>(run_at),
+                               reinterpret_cast<void*>(run_host), run_bytes, hipMemcpyDefault,
+                               lane_s[L]);
+          x->last_dma++;
+        };
+        for_each_step_chunk(plans, sp, st, [&](const Chunk& c, size_t k) {
+          if (run_bytes > 0 && c.host == run_host + run_bytes) {
+            run_bytes += cb;
+            return;
+          }
+          flush();
+          run_host = c.host;
+          run_at = slot + k * cb;
+          run_bytes = cb;
+        });
+        flush();
+      };
+      if (is_save) {
+        if (int rc = launch(x, st.desc_first, st.n_chunks, cb, al16, true, false, nullptr,
+                            lane_s[L]))
+          return rc;
+        copy_runs();
+        if (e != hipSuccess) return hip_fail(e, "staged hipMemcpyAsync (D2H)");
+      } else {
+        copy_runs();
+        if (e != hipSuccess) return hip_fail(e, "staged hipMemcpyAsync (H2D)");
+        if (int rc = launch(x, st.desc_first, st.n_chunks, cb, al16, false, false, nullptr,
+                            lane_s[L]))
+          return rc;
+      }
+      pending[L] = true;
+    }
+    if (int rc = complete(static_cast<int64_t>(si), L)) return rc;
+  }
+  if (is_save && wait_save) {
     PF_HIP(hipStreamSynchronize(x->dma));
     PF_HIP(hipStreamSynchronize(x->stream));
+    return PF_OK;
   }
+  // The context's stream ends after all of the call's work.
+  if (int rc = join(0, 1)) return rc;
+  PF_HIP(hipEventRecord(x->staging_free, x->stream));
   return PF_OK;
 }
 
@@ -1075,14 +1458,62 @@ int run(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, uint32_t m
   if (rc != PF_OK) {
     (void)hipStreamSynchronize(x->dma);
     (void)hipStreamSynchronize(x->stream);
+    const std::string msg = pf_last_error();
+    (void)engine_drain(x);
+    (void)fail(rc, msg);  // the call's own error
   }
   return rc;
 }
+
+// PF_MODE_AUTO: the staged mode when the context has staging and the host
+// side's contiguous runs (in list order, as the staged mode copies them)
+// average at least kAutoMinRunBytes, else the kernel mode.  A DMA copy costs
+// about 10 us to issue and start, so 1 MiB runs (18 us on the link) keep the
+// link busy from the context's two streams; a restore of blocks saved
+// together (one host region per layer and segment) is one run per region.
+constexpr uint64_t kAutoMinRunBytes = 1ull << 20;
+
+uint32_t auto_mode(const pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers) {
+  if (x->staging == 0 || x->slot_bytes == 0) return PF_MODE_KERNEL;
+  uint64_t bytes = 0, runs = 0;
+  for (uint32_t li = 0; li < num_layers; ++li) {
+    const pf_layer_xfer& lx = layers[li];
+    if (lx.num_blocks == 0 || !lx.blocks) continue;
+    const pf_kv_layout& l = lx.layout;
+    const bool split = layout_kind(l) == PF_LAYOUT_SPLIT;
+    const uint64_t seg = l.bytes_per_block;
+    const uint64_t step = split ? seg : l.block_size_bytes;
+    if (step == 0 || step > x->slot_bytes) return PF_MODE_KERNEL;
+    const pf_block_xfer* b = lx.blocks;
+    runs += 1;
+    for (uint64_t j = 1; j < lx.num_blocks; ++j)
+      if (b[j].k_host != b[j - 1].k_host + step) ++runs;
+    bytes += lx.num_blocks * step;
+    if (split) {
+      auto v = [&](uint64_t j) { return b[j].v_host ? b[j].v_host : b[j].k_host + seg; };
+      runs += 1;
+      for (uint64_t j = 1; j < lx.num_blocks; ++j)
+        if (v(j) != v(j - 1) + seg) ++runs;
+      bytes += lx.num_blocks * seg;
+    }
+  }
+  return runs > 0 && bytes / runs >= kAutoMinRunBytes ? PF_MODE_STAGED : PF_MODE_KERNEL;
+}
+
+}  // namespace
+
+uint32_t pf::resolve_mode(const pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
+                          uint32_t mode) {
+  return mode == PF_MODE_AUTO ? auto_mode(x, layers, num_layers) : mode;
+}
+
+namespace {
 
 int run_locked(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, uint32_t mode,
                bool is_save, pf_event* layer_events, bool wait_save, const SignalTargets* sig,
                const PendingLayers* pending) {
   std::vector<LayerPlan>& plans = x->plans;
+  if (mode == PF_MODE_AUTO) mode = auto_mode(x, layers, num_layers);
   if (mode == PF_MODE_KERNEL) {
     // A large call: its first layers are planned and launched before the
     // rest are planned, so the planning of the rest (about 3 ns a chunk)
@@ -1119,7 +1550,7 @@ int run_locked(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, uin
     case PF_MODE_STAGED:
       for (uint32_t li = 0; li < num_layers; ++li)
         apply_write_policy(layers[li], is_save, true, &plans[li]);
-      return staged(x, layers, plans, is_save, layer_events, sig);
+      return staged(x, layers, plans, is_save, layer_events, sig, wait_save);
     default:
       return fail(PF_ERR_INVALID_ARGUMENT, strf("unknown transfer mode %u", mode));
   }
@@ -1398,10 +1829,21 @@ int pf_xfer_create(int device, uint64_t staging_bytes, pf_xfer** out) {
   if (e == hipSuccess)
     e = hipHostMalloc(reinterpret_cast<void**>(&x->h_small), kHostDescMax * sizeof(ChunkDesc),
                       hipHostMallocMapped | hipHostMallocCoherent);
-  for (int s = 0; s < 2 && e == hipSuccess; ++s) {
-    e = hipEventCreateWithFlags(&x->slot_ready[s], hipEventDisableTiming);
-    if (e == hipSuccess) e = hipEventCreateWithFlags(&x->slot_free[s], hipEventDisableTiming);
-    if (e == hipSuccess) e = hipEventRecord(x->slot_free[s], x->stream);
+  if (e == hipSuccess)
+    e = hipHostMalloc(reinterpret_cast<void**>(&x->h_boot), 2 * sizeof(ChunkDesc),
+                      hipHostMallocMapped | hipHostMallocCoherent);
+  for (int s = 0; s < 2 && e == hipSuccess; ++s)
+    e = hipEventCreateWithFlags(&x->lane_mark[s], hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&x->staging_free, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventRecord(x->staging_free, x->stream);
+  if (e == hipSuccess && staging_bytes > 0 && engine_copies_available(device)) {
+    for (int s = 0; s < kEngineSlots && e == hipSuccess; ++s)
+      e = hipEventCreateWithFlags(&x->eng_ev[s], hipEventDisableTiming);
+    int rc = PF_OK;
+    for (int s = 0; s < kEngineSlots && e == hipSuccess && rc == PF_OK; ++s)
+      rc = engine_signal_create(&x->eng_sig[s]);
+    if (rc != PF_OK) return cleanup(rc);
+    x->engine_ok = e == hipSuccess;
   }
   if (e != hipSuccess) return cleanup(hip_fail(e, "pf_xfer_create"));
   if (staging_bytes > 0) {
@@ -1424,10 +1866,16 @@ int pf_xfer_destroy(pf_xfer* x) {
   (void)hipSetDevice(x->device);
   if (x->stream) (void)hipStreamSynchronize(x->stream);
   if (x->dma) (void)hipStreamSynchronize(x->dma);
+  (void)engine_drain(x);
+  for (EngineSignal& s : x->eng_sig) engine_signal_destroy(&s);
+  for (hipEvent_t ev : x->eng_ev)
+    if (ev) (void)hipEventDestroy(ev);
+  if (x->staging_free) (void)hipEventDestroy(x->staging_free);
   if (x->d_desc) (void)hipFree(x->d_desc);
   if (x->d_counters) (void)hipFree(x->d_counters);
   if (x->h_desc) (void)hipHostFree(x->h_desc);
   if (x->h_small) (void)hipHostFree(x->h_small);
+  if (x->h_boot) (void)hipHostFree(x->h_boot);
   if (x->staging) (void)hipFree(reinterpret_cast<void*>(x->staging));
   if (x->desc_uploaded) (void)hipEventDestroy(x->desc_uploaded);
   if (x->parts_ready) (void)hipEventDestroy(x->parts_ready);
@@ -1435,10 +1883,8 @@ int pf_xfer_destroy(pf_xfer* x) {
     (void)hipEventDestroy(t.first);
     (void)hipEventDestroy(t.second);
   }
-  for (int s = 0; s < 2; ++s) {
-    if (x->slot_ready[s]) (void)hipEventDestroy(x->slot_ready[s]);
-    if (x->slot_free[s]) (void)hipEventDestroy(x->slot_free[s]);
-  }
+  for (int s = 0; s < 2; ++s)
+    if (x->lane_mark[s]) (void)hipEventDestroy(x->lane_mark[s]);
   for (ScatterTrial& t : x->trials) {
     if (t.start) (void)hipEventDestroy(t.start);
     if (t.stop) (void)hipEventDestroy(t.stop);
@@ -1455,7 +1901,7 @@ int pf_xfer_synchronize(pf_xfer* x) {
   if (!x) return fail(PF_ERR_INVALID_ARGUMENT, "null transfer context");
   PF_HIP(hipStreamSynchronize(x->dma));
   PF_HIP(hipStreamSynchronize(x->stream));
-  return PF_OK;
+  return engine_drain(x);
 }
 
 int pf_xfer_set_kernel_shape(pf_xfer* x, uint32_t threads, uint32_t unroll) {
@@ -1527,6 +1973,14 @@ int pf_xfer_set_max_grid(pf_xfer* x, uint32_t max_workgroups) {
   if (!x) return fail(PF_ERR_INVALID_ARGUMENT, "null transfer context");
   std::lock_guard<std::mutex> lk(x->mu);
   x->max_grid = max_workgroups;
+  return PF_OK;
+}
+
+int pf_xfer_set_staged_slices(pf_xfer* x, uint64_t save_bytes, uint64_t load_bytes) {
+  if (!x) return fail(PF_ERR_INVALID_ARGUMENT, "null transfer context");
+  std::lock_guard<std::mutex> lk(x->mu);
+  if (save_bytes) x->staged_slice[0] = save_bytes;
+  if (load_bytes) x->staged_slice[1] = load_bytes;
   return PF_OK;
 }
 

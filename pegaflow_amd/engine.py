@@ -107,8 +107,8 @@ class PegaEngine:
         self._h = h.value
         self._name_arrays = {}  # tuple of layer names -> C array of their bytes
 
-    def set_transfer_modes(self, save_mode: int = _lib.MODE_KERNEL,
-                           load_mode: int = _lib.MODE_KERNEL) -> None:
+    def set_transfer_modes(self, save_mode: int = _lib.MODE_AUTO,
+                           load_mode: int = _lib.MODE_AUTO) -> None:
         _raise(lib().pf_engine_set_modes(self._h, save_mode, load_mode))
 
     def register_context_layer(self, instance_id: str, namespace: str, device_id: int,

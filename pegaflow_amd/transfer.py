@@ -242,6 +242,11 @@ class TransferContext:
         for route, grid in _lib.DEFAULT_GRIDS.items():
             self.set_route_grid(route, grid)
 
+    def set_staged_slices(self, save_bytes: int = 0, load_bytes: int = 0) -> None:
+        """Largest staged slice per direction (0 keeps the current value)."""
+        check(lib().pf_xfer_set_staged_slices(self.handle, save_bytes, load_bytes),
+              "pf_xfer_set_staged_slices")
+
     def set_max_grid(self, max_workgroups: int) -> None:
         check(lib().pf_xfer_set_max_grid(self.handle, max_workgroups), "pf_xfer_set_max_grid")
 

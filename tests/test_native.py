@@ -67,7 +67,8 @@ def build(variant: str, main: str = "stress_engine") -> str:
 
     with ThreadPoolExecutor(max_workers=4) as pool:
         objs = list(pool.map(compile_one, SOURCES))
-    subprocess.run([HIPCC, "--offload-arch=gfx950", *flags, "-o", exe, *objs, "-lpthread", "-lrt"],
+    subprocess.run([HIPCC, "--offload-arch=gfx950", *flags, "-o", exe, *objs, "-L/opt/rocm/lib",
+                    "-lhsa-runtime64", "-lpthread", "-lrt"],
                    check=True, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
     return exe
 

@@ -1,0 +1,230 @@
+"""GPU parity of the staged mode's slicing, and of PF_MODE_AUTO's choice.
+
+The staged mode cuts a call's chunks, in layer order, into slices that may
+span layers and alternate between the context's two streams.  These tests
+shrink the slices to a few chunks so that slices cross layer boundaries,
+chunk-size changes, empty layers and layers copied in place in list order,
+and compare every byte with the oracle (each layer's save and load restated
+on the host, in the reference's order).
+"""
+
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from pegaflow_amd import _lib
+from pegaflow_amd.runtime import DeviceBuffer, Event, PinnedBuffer
+from pegaflow_amd.transfer import KVCacheRegistration, LayerTransfer, TransferContext, block_array
+
+pytestmark = pytest.mark.gpu
+MiB = 1 << 20
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+class Layer:
+    """One layer tensor with its oracle copy; host regions at given offsets
+    of a pinned buffer shared by the call's layers (and the same offsets of a
+    numpy buffer for the oracle)."""
+
+    def __init__(self, nb, bpb, segs, kv, size, seed):
+        self.dev = DeviceBuffer(size)
+        self.dev.fill_random(seed)
+        self.ref = self.dev.download()
+        self.reg = KVCacheRegistration.create(self.dev.ptr, size, nb, bpb, kv, segs)
+        self.oreg = oracle.layout(self.ref.ctypes.data, size, nb, bpb, kv, segs)
+        self.bpb = bpb
+
+    def place(self, ids, host, ohost, off):
+        """The reference's host layout for `ids` at byte `off` of both buffers."""
+        n = len(ids)
+        self.k, self.v, self.split = oracle.save_host_layout(
+            self.oreg, n, host.ptr + off, host.ptr + off + n * self.bpb)
+        self.ok_, self.ov, _ = oracle.save_host_layout(
+            self.oreg, n, ohost.ctypes.data + off, ohost.ctypes.data + off + n * self.bpb)
+        self.save_ids = list(ids)
+
+    def transfer(self, ids):
+        return LayerTransfer(self.reg, block_array(ids, self.k, self.v if self.split else None))
+
+    def oracle_save(self):
+        oracle.process_save(self.oreg, self.ref, self.save_ids, self.ok_,
+                            self.ov if self.split else None)
+
+    def oracle_load(self, ids):
+        oracle.process_load(self.oreg, self.ref, ids, self.ok_, self.ov if self.split else None)
+
+    def close(self):
+        self.dev.close()
+
+
+def _mixed_layers(seed):
+    """Split layers of two segment sizes, an empty one, an overlapping layout
+    (its loads are copied in place, in list order), a blocks-first layer and
+    an unaligned one; with their save and load ids."""
+    nb, bpb = 40, 256
+    kv = nb * bpb
+    specs = [
+        ((nb, bpb, 2, kv, 2 * kv), [3, 9, 27, 1, 30, 31, 32], [0, 5, 39, 12, 13, 14, 15]),
+        ((nb, bpb, 2, kv, 2 * kv), list(range(nb))[::-1], list(range(nb))),
+        ((nb, bpb, 2, kv, 2 * kv), [], []),
+        ((nb, 512, 2, nb * 512, 2 * nb * 512), [4, 5, 6, 7, 8], [9, 9, 1, 2, 9]),
+        ((10, 64, 2, 160, 160 + 640), [1, 2, 3], [4, 3, 2]),
+        ((nb, 4608, 1, 0, nb * 4608), [9, 1, 30, 2], [2, 3, 4, 5]),
+        ((30, 24, 2, 30 * 24 + 8, 30 * 24 * 2 + 8), [4, 5, 6], [20, 0, 29]),
+        ((nb, bpb, 2, kv, 2 * kv), [11, 12, 13], [13, 12, 11]),
+    ]
+    layers = [Layer(*shape, seed + i) for i, (shape, _, _) in enumerate(specs)]
+    return layers, [s for _, s, _ in specs], [l for _, _, l in specs]
+
+
+def _place_all(layers, save_ids, gap=0):
+    """Host regions of all layers one after another, `gap` bytes apart (a gap
+    that is not a multiple of 16 leaves later regions unaligned)."""
+    regions = [2 * max(len(ids), 1) * L.bpb for L, ids in zip(layers, save_ids)]
+    size = sum(regions) + gap * len(regions)
+    host = PinnedBuffer(size)
+    ohost = np.zeros(size, np.uint8)
+    off = 0
+    for L, ids, r in zip(layers, save_ids, regions):
+        L.place(ids, host, ohost, off)
+        off += r + gap
+    return host, ohost
+
+
+@pytest.mark.parametrize("slices", [(3000, 5000), (1, 1), (65536, 2048)])
+def test_staged_slices_across_layers_vs_oracle(gpu, slices):
+    """One staged save, then one staged load with per-layer events, of eight
+    mixed layers, with slices of a few chunks (or one chunk each): host
+    regions and every layer tensor equal the oracle's; the layer events
+    complete in layer order.  A second load of the same call with layer marks
+    sets every layer's word."""
+    say(f"[gpu] staged slices across layers, slice caps {slices}")
+    ctx = TransferContext(0, staging_bytes=64 * 1024)
+    ctx.set_staged_slices(*slices)
+    layers, save_ids, load_ids = _mixed_layers(70)
+    host, ohost = _place_all(layers, save_ids, gap=8)
+    words = PinnedBuffer(8 * len(layers))
+    try:
+        host.array[:] = 0
+        ctx.save_layers([L.transfer(ids) for L, ids in zip(layers, save_ids)], _lib.MODE_STAGED)
+        for L in layers:
+            L.oracle_save()
+        assert np.array_equal(host.array, ohost), "host regions differ from the oracle"
+        evs = [Event() for _ in layers]
+        ctx.load_layers([L.transfer(ids) for L, ids in zip(layers, load_ids)], _lib.MODE_STAGED,
+                        layer_events=evs)
+        ctx.synchronize()
+        for i in range(1, len(evs)):
+            assert evs[i - 1].elapsed_ms(evs[i]) >= 0.0, f"layer {i} completed before {i - 1}"
+        for L, ids in zip(layers, load_ids):
+            L.oracle_load(ids)
+            assert np.array_equal(L.dev.download(), L.ref), "layer differs from the oracle"
+        # The same load again, marked: its bytes are unchanged (the oracle
+        # already holds them) and every word is set.
+        words.array[:] = 0
+        ctx.load_layers_marked([L.transfer(ids) for L, ids in zip(layers, load_ids)],
+                               [(words.ptr, 7, True)], _lib.MODE_STAGED)
+        ctx.synchronize()
+        assert words.array.view(np.uint64).tolist() == [7] * len(layers)
+        for L in layers:
+            assert np.array_equal(L.dev.download(), L.ref)
+    finally:
+        for L in layers:
+            L.close()
+        host.close()
+        words.close()
+        ctx.close()
+
+
+def test_staged_save_overlapping_hosts_keeps_list_order(gpu):
+    """Host destinations that overlap across layers (layer 1's region starts
+    inside layer 0's V region): the staged save copies in list order, as the
+    reference does, so the later copy's bytes are kept.  The third layer
+    names one block twice (two host chunks with the same bytes)."""
+    say("[gpu] staged save, overlapping host destinations")
+    ctx = TransferContext(0, staging_bytes=64 * 1024)
+    ctx.set_staged_slices(1024, 1024)
+    nb, bpb = 32, 256
+    kv = nb * bpb
+    layers = [Layer(nb, bpb, 2, kv, 2 * kv, 90 + i) for i in range(3)]
+    ids = [[1, 2, 3, 4], [5, 6, 7, 8], [9, 9, 10, 11]]
+    size = 16 * bpb * 3
+    host = PinnedBuffer(size)
+    ohost = np.zeros(size, np.uint8)
+    layers[0].place(ids[0], host, ohost, 0)
+    layers[1].place(ids[1], host, ohost, 6 * bpb)          # inside layer 0's V region
+    layers[2].place(ids[2], host, ohost, 20 * bpb)
+    try:
+        host.array[:] = 0
+        ctx.save_layers([L.transfer(i) for L, i in zip(layers, ids)], _lib.MODE_STAGED)
+        for L in layers:
+            L.oracle_save()
+        assert np.array_equal(host.array, ohost)
+    finally:
+        for L in layers:
+            L.close()
+        host.close()
+        ctx.close()
+
+
+def test_auto_mode_follows_host_runs(gpu):
+    """PF_MODE_AUTO runs staged (DMA copies over the link) when the host side
+    lies in long contiguous runs, as a save batch's regions do, and runs the
+    zero-copy kernels when the host chunks are scattered; bytes are exact
+    either way."""
+    say("[gpu] auto mode follows host runs")
+    ctx = TransferContext(0, staging_bytes=64 * MiB)
+    nb, bpb, n, n_layers = 256, 32768, 64, 4
+    kv = nb * bpb
+    layers = [Layer(nb, bpb, 2, kv, 2 * kv, 120 + i) for i in range(n_layers)]
+    rng = np.random.Generator(np.random.PCG64(12))
+    ids = rng.choice(nb, n, replace=False).tolist()
+    targets = rng.choice(np.setdiff1d(np.arange(nb), ids), n, replace=False).tolist()
+    hosts = []
+    try:
+        for scattered in (False, True):
+            host = PinnedBuffer(n_layers * 2 * n * bpb)
+            hosts.append(host)
+            ohost = np.zeros(host.nbytes, np.uint8)
+            for i, L in enumerate(layers):
+                L.place(ids, host, ohost, i * 2 * n * bpb)
+            if scattered:  # each layer's K and V chunks in a shuffled order
+                for L in layers:
+                    perm = rng.permutation(n)
+                    L.k, L.ok_ = L.k[perm], L.ok_[perm]
+                    L.v, L.ov = L.v[perm], L.ov[perm]
+            host.array[:] = 0
+            ctx.save_layers([L.transfer(ids) for L in layers], _lib.MODE_AUTO)
+            _, dma = ctx.last_stats()
+            assert (dma == 0) == scattered, f"save: {dma} DMA copies (scattered={scattered})"
+            for L in layers:
+                L.oracle_save()
+            assert np.array_equal(host.array, ohost)
+            ctx.load_layers([L.transfer(targets) for L in layers], _lib.MODE_AUTO)
+            ctx.synchronize()
+            _, dma = ctx.last_stats()
+            assert (dma == 0) == scattered, f"load: {dma} DMA copies (scattered={scattered})"
+            for L in layers:
+                L.oracle_load(targets)
+                assert np.array_equal(L.dev.download(), L.ref)
+        # Without staging, AUTO is the kernel mode (the same load again: the
+        # targets already hold these bytes).
+        plain = TransferContext(0)
+        plain.load_layers([L.transfer(targets) for L in layers], _lib.MODE_AUTO)
+        plain.synchronize()
+        assert plain.last_stats()[1] == 0
+        plain.close()
+        for L in layers:
+            assert np.array_equal(L.dev.download(), L.ref)
+    finally:
+        for L in layers:
+            L.close()
+        for h in hosts:
+            h.close()
+        ctx.close()
