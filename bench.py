@@ -91,6 +91,8 @@ def parse():
     ap.add_argument("--duplex-study", action="store_true",
                     help="also time each link direction against a plain DMA copy the other way, "
                          "and the two queued kernels' grids in duplex")
+    ap.add_argument("--interference-study", action="store_true",
+                    help="only run the cross-process interference study (one JSON line)")
     ap.add_argument("--pinned-flags", type=int, default=0,
                     help="PF_PINNED_* flags of the pinned pools (0: mapped, portable)")
     ap.add_argument("--cpu-sample-layers", type=int, default=8)
@@ -230,6 +232,155 @@ def leg_interference(layers, saved, loads, P, reps=3):
     vsrc.close()
     vdst.close()
     return out
+
+
+STUDY_PHASES = ["idle", "kernel_save", "staged_save", "kernel_restore", "staged_restore"]
+
+
+def _study_transfer(go, done, ready, out):
+    """Transfer process of the interference study: each phase saves or
+    restores the Llama prefix six times while the victim process measures."""
+    from pegaflow_amd import _lib, runtime
+    from pegaflow_amd import workload as wl
+    from pegaflow_amd.runtime import PinnedBuffer
+    from pegaflow_amd.transfer import TransferContext
+
+    runtime.init(0)
+    layers = wl.DeviceLayers(wl.LLAMA3_8B, base_seed=0)
+    ids, targets = wl.draw_blocks(wl.LLAMA3_8B.num_blocks, 640, 0)
+    P = wl.payload_bytes(layers.regs, 640)
+    pool = PinnedBuffer(P)
+    x = TransferContext(0, staging_bytes=256 << 20)
+    saved = wl.save_plan(layers.regs, ids, pool.ptr)
+    loads = wl.load_plan(saved, targets)
+    ops = {
+        "idle": lambda: time.sleep(0.024),
+        "kernel_save": lambda: x.save_layers(saved, _lib.MODE_KERNEL),
+        "staged_save": lambda: x.save_layers(saved, _lib.MODE_STAGED),
+        "kernel_restore": lambda: (x.load_layers(loads, _lib.MODE_KERNEL), x.synchronize()),
+        "staged_restore": lambda: (x.load_layers(loads, _lib.MODE_STAGED), x.synchronize()),
+    }
+    for name in STUDY_PHASES:
+        ops[name]()
+    ready.set()
+    gbps = {}
+    for name in STUDY_PHASES:
+        go.wait()
+        go.clear()
+        t = []
+        for _ in range(6):
+            t0 = time.perf_counter()
+            ops[name]()
+            t.append(time.perf_counter() - t0)
+        gbps[name] = round(P / statistics.median(t) / 1e9, 2)
+        done.set()
+    gbps.pop("idle")
+    out.put(gbps)
+
+
+def _study_victim(go, done, ready, kind, out):
+    """Victim process: launches its work back to back through each phase of
+    the transfer process and reports the median duration."""
+    if kind == "gemm_bf16_8192":
+        import torch  # initialized here, in a process that never loads the library
+
+        a = torch.randn(8192, 8192, device="cuda", dtype=torch.bfloat16)
+        b = torch.randn(8192, 8192, device="cuda", dtype=torch.bfloat16)
+        c = torch.empty(8192, 8192, device="cuda", dtype=torch.bfloat16)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+        def victim():
+            e0.record()
+            torch.mm(a, b, out=c)
+            e1.record()
+            e1.synchronize()
+            return e0.elapsed_time(e1)
+    else:
+        from pegaflow_amd import _lib, runtime
+        from pegaflow_amd import workload as wl
+        from pegaflow_amd.runtime import DeviceBuffer, Event, PinnedBuffer, Stream
+        from pegaflow_amd.transfer import KVCacheRegistration, TransferContext
+
+        runtime.init(0)
+        if kind == "hbm_copy_256MiB":
+            vb = 256 << 20
+            vsrc, vdst = DeviceBuffer(vb), DeviceBuffer(vb)
+            xv = TransferContext(0)
+            creg = KVCacheRegistration.create(vsrc.ptr, vb, vb // 32768, 32768, 0, 1)
+            vplan = wl.save_plan([creg], np.arange(vb // 32768), vdst.ptr)
+            xv.set_timing(True)
+
+            def victim():
+                xv.save_layers(vplan, _lib.MODE_KERNEL)
+                return xv.last_kernel_ms()[0]
+        else:
+            h, d = PinnedBuffer(1 << 20), DeviceBuffer(1 << 20)
+            st, ev = Stream(), Event()
+
+            def victim():
+                t0 = time.perf_counter()
+                if kind == "copy_64KiB_h2d":
+                    runtime.memcpy_async(d.ptr, h.ptr, 65536, st)
+                else:
+                    runtime.memcpy_async(h.ptr, d.ptr, 65536, st)
+                ev.record(st)
+                ev.synchronize()
+                return (time.perf_counter() - t0) * 1e3
+    for _ in range(5):
+        victim()
+    ready.wait()
+    base = None
+    res = {}
+    for name in STUDY_PHASES:
+        times = []
+        go.set()
+        time.sleep(0.003)
+        while not done.is_set():
+            times.append(victim())
+            time.sleep(0.0005 if kind.startswith("copy") else 0)
+        done.clear()
+        times = times[1:-1] if len(times) > 3 else times
+        med = statistics.median(times)
+        base = med if base is None else base
+        res[name] = {"median_ms": round(med, 4), "slowdown": round(med / base, 2),
+                     "n": len(times)}
+    out.put(res)
+
+
+def interference_study():
+    """Cross-process interference (the engine server beside a vLLM worker):
+    for each victim, a transfer process saves and restores the Llama prefix
+    in each mode while a victim process runs its work back to back.  Prints
+    one JSON line."""
+    import multiprocessing as mp
+
+    ctx = mp.get_context("spawn")
+    victims = ["hbm_copy_256MiB", "gemm_bf16_8192", "copy_64KiB_h2d", "copy_64KiB_d2h"]
+    try:
+        import torch  # noqa: F401  (the GEMM victim needs it)
+    except ImportError:
+        victims.remove("gemm_bf16_8192")
+    result = {"metric": "interference of each transfer mode with work in another process",
+              "transfer": "llama-3.1-8b 10k-token prefix (32 x [2,20000,16,8,128] bf16, "
+                          "640 blocks), six calls per phase",
+              "victims": {}}
+    for kind in victims:
+        log(f"[bench] interference study: victim {kind}")
+        go, done, ready = ctx.Event(), ctx.Event(), ctx.Event()
+        out, tout = ctx.Queue(), ctx.Queue()
+        pt = ctx.Process(target=_study_transfer, args=(go, done, ready, tout))
+        pv = ctx.Process(target=_study_victim, args=(go, done, ready, kind, out))
+        pt.start()
+        pv.start()
+        res = out.get(timeout=300)
+        res["transfer_gbps"] = tout.get(timeout=60)
+        pv.join(60)
+        pt.join(60)
+        if pt.exitcode != 0 or pv.exitcode != 0:
+            raise RuntimeError(f"interference study processes exited {pt.exitcode}, "
+                               f"{pv.exitcode}")
+        result["victims"][kind] = res
+    print(json.dumps(result), flush=True)
 
 
 def duplex_study(xfer_load, xfer_save, saved, loads, pool, pool2, dev_buf, P, reps=4):
@@ -594,6 +745,24 @@ def pinned_copy_microbench(iters=2000):
                        timeout=120)
     if r.returncode != 0:
         raise RuntimeError(f"bench_pinned_copy failed ({r.returncode}): {r.stderr.strip()}")
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    log(f"[bench] {out}")
+    return out
+
+
+def copy_engine_rates():
+    """Host-link GB/s of each of the device's copy engines per direction (one
+    1 GiB copy each, best of 3), and the engines the staged mode uses."""
+    import subprocess
+
+    from pegaflow_amd.build import BENCH_COPY_ENGINES
+
+    if not os.path.exists(BENCH_COPY_ENGINES):
+        raise RuntimeError(f"{BENCH_COPY_ENGINES} is not built; run python -m pegaflow_amd.build")
+    log("[bench] copy engines: 1 GiB per engine and direction")
+    r = subprocess.run([BENCH_COPY_ENGINES], capture_output=True, text=True, timeout=180)
+    if r.returncode != 0:
+        raise RuntimeError(f"bench_copy_engines failed ({r.returncode}): {r.stderr.strip()}")
     out = json.loads(r.stdout.strip().splitlines()[-1])
     log(f"[bench] {out}")
     return out
@@ -1159,10 +1328,14 @@ def main():
     if args.profile:
         profile_kernels(args.profile, args.seed)
         return
+    if args.interference_study:
+        interference_study()
+        return
 
     # The single-block latency benchmark runs as its own process, before this
     # one touches the GPU.
     micro = None if args.quick else pinned_copy_microbench()
+    engines = None if args.quick else copy_engine_rates()
 
     from pegaflow_amd import _lib, runtime
     from pegaflow_amd.runtime import DeviceBuffer, PinnedBuffer
@@ -1495,6 +1668,7 @@ def main():
                            "bytes_per_launch": 2 * P, "ms_per_launch": round(scatter_ms, 4)},
         "d2d_memcpy_gbps": round(d2d_gbps, 1),
         "interference": interference,
+        **({"copy_engines": engines} if engines else {}),
         "duplex_staged": {"gbps": round(2 * P / t_dup_staged / 1e9, 3),
                           "ms_per_save_plus_restore": round(t_dup_staged * 1e3, 3),
                           "what": "as duplex, both staged on the copy engines, the restore "

@@ -368,6 +368,12 @@ int pf_xfer_set_kernel_shape(pf_xfer* xfer, uint32_t threads, uint32_t unroll);
 /* Upper bound on workgroups per gather/scatter launch (0 = one workgroup per
  * tile, the default); with a bound, each workgroup loops over tiles. */
 int pf_xfer_set_max_grid(pf_xfer* xfer, uint32_t max_workgroups);
+/* The copy engines (one HSA SDMA engine id bit each, from
+ * hsa_amd_sdma_engine_id_t) the staged mode's copies run on for `device`:
+ * device to host, then host to device; both 0 when they are not known (the
+ * staged mode then copies through HIP).  No counterpart in the reference
+ * (its copies are cuMemcpy calls); bench_copy_engines measures each engine. */
+int pf_copy_engines(int device, uint32_t* d2h_engine, uint32_t* h2d_engine);
 /* Largest staged slice per direction, in bytes (0 keeps the current value);
  * slices are further capped by the staging slot.  Smaller load slices land
  * a layer sooner; the defaults are the smallest that keep each direction's

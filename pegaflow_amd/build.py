@@ -16,6 +16,8 @@ CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libpegaflow_hip.so")
 # Single-block copy latency benchmark (the reference's pinned_copy bench).
 BENCH_PINNED_COPY = os.path.join(HERE, "bench_pinned_copy")
+# Host-link bandwidth of each copy engine.
+BENCH_COPY_ENGINES = os.path.join(HERE, "bench_copy_engines")
 ARCH = "gfx950"
 
 SOURCES = [
@@ -84,19 +86,21 @@ def build(verbose: bool = False) -> str:
     return LIB
 
 
-def build_bench(cc: str, verbose: bool = False) -> str:
-    """bench_pinned_copy, linked against the library next to it."""
-    src = os.path.join(CSRC, "bench_pinned_copy.cpp")
-    tmp = BENCH_PINNED_COPY + ".tmp"
-    cmd = [cc, *HIP_FLAGS, "-x", "hip", src, "-o", tmp, "-L", HERE, "-lpegaflow_hip",
-           "-Wl,-rpath,$ORIGIN", "-Wl,-rpath,/opt/rocm/lib"]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"hipcc failed on bench_pinned_copy.cpp:\n{r.stdout}\n{r.stderr}")
-    os.replace(tmp, BENCH_PINNED_COPY)
-    return BENCH_PINNED_COPY
+def build_bench(cc: str, verbose: bool = False) -> None:
+    """The benchmark binaries, linked against the library next to them."""
+    for name, out in (("bench_pinned_copy.cpp", BENCH_PINNED_COPY),
+                      ("bench_copy_engines.cpp", BENCH_COPY_ENGINES)):
+        src = os.path.join(CSRC, name)
+        tmp = out + ".tmp"
+        cmd = [cc, *HIP_FLAGS, "-x", "hip", src, "-o", tmp, "-L", HERE, "-lpegaflow_hip",
+               "-Wl,-rpath,$ORIGIN", "-Wl,-rpath,/opt/rocm/lib", "-L/opt/rocm/lib",
+               "-lhsa-runtime64"]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"hipcc failed on {name}:\n{r.stdout}\n{r.stderr}")
+        os.replace(tmp, out)
 
 
 if __name__ == "__main__":

@@ -130,6 +130,8 @@ struct EngineSignal {
 };
 // True when the device's engines for both directions are known.
 bool engine_copies_available(int device);
+// The engine id bits in use for each direction (false, and 0, when unknown).
+bool engine_ids(int device, uint32_t* d2h, uint32_t* h2d);
 int engine_signal_create(EngineSignal* s);  // value 0
 void engine_signal_destroy(EngineSignal* s);
 // Adds n to the count before n copies are submitted against the signal.

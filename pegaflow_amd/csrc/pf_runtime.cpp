@@ -275,6 +275,13 @@ hsa_signal_t sig_of(const EngineSignal* s) { return hsa_signal_t{s->handle}; }
 
 bool engine_copies_available(int device) { return engines_of(device) != nullptr; }
 
+bool engine_ids(int device, uint32_t* d2h, uint32_t* h2d) {
+  const EngineDevice* d = engines_of(device);
+  *d2h = d ? d->engine[0] : 0;
+  *h2d = d ? d->engine[1] : 0;
+  return d != nullptr;
+}
+
 int engine_signal_create(EngineSignal* s) {
   hsa_signal_t h{};
   if (hsa_signal_create(0, 0, nullptr, &h) != HSA_STATUS_SUCCESS)
@@ -802,3 +809,10 @@ int pf_spin(pf_stream stream, uint32_t microseconds) {
 }
 
 }  // extern "C"
+
+int pf_copy_engines(int device, uint32_t* d2h_engine, uint32_t* h2d_engine) {
+  if (!d2h_engine || !h2d_engine) return pf::fail(PF_ERR_INVALID_ARGUMENT, "null output");
+  if (int rc = pf_init(device)) return rc;
+  (void)pf::engine_ids(device, d2h_engine, h2d_engine);
+  return PF_OK;
+}

@@ -40,6 +40,14 @@ def pci_bus_id(device: int = 0) -> str:
     return buf.value.decode()
 
 
+def copy_engines(device: int = 0):
+    """(d2h, h2d): the copy-engine id bits the staged mode's copies use on
+    the device (0, 0 when unknown)."""
+    d, h = ctypes.c_uint32(), ctypes.c_uint32()
+    check(lib().pf_copy_engines(device, ctypes.byref(d), ctypes.byref(h)), "pf_copy_engines")
+    return d.value, h.value
+
+
 def mem_get_info():
     f, t = ctypes.c_uint64(), ctypes.c_uint64()
     check(lib().pf_mem_get_info(ctypes.byref(f), ctypes.byref(t)), "pf_mem_get_info")

@@ -15,7 +15,7 @@ import pytest
 
 import oracle
 from pegaflow_amd import _lib
-from pegaflow_amd.runtime import DeviceBuffer, Event, PinnedBuffer
+from pegaflow_amd.runtime import DeviceBuffer, Event, PinnedBuffer, copy_engines
 from pegaflow_amd.transfer import KVCacheRegistration, LayerTransfer, TransferContext, block_array
 
 pytestmark = pytest.mark.gpu
@@ -83,12 +83,25 @@ def _mixed_layers(seed):
     return layers, [s for _, s, _ in specs], [l for _, _, l in specs]
 
 
-def _place_all(layers, save_ids, gap=0):
+class PageableBuffer:
+    """Ordinary (pageable) host memory with PinnedBuffer's fields: staged
+    copies to and from it go through HIP, not the copy engines."""
+
+    def __init__(self, nbytes):
+        self.array = np.zeros(nbytes, np.uint8)
+        self.ptr = self.array.ctypes.data
+        self.nbytes = nbytes
+
+    def close(self):
+        self.array = None
+
+
+def _place_all(layers, save_ids, gap=0, pinned=True):
     """Host regions of all layers one after another, `gap` bytes apart (a gap
     that is not a multiple of 16 leaves later regions unaligned)."""
     regions = [2 * max(len(ids), 1) * L.bpb for L, ids in zip(layers, save_ids)]
     size = sum(regions) + gap * len(regions)
-    host = PinnedBuffer(size)
+    host = PinnedBuffer(size) if pinned else PageableBuffer(size)
     ohost = np.zeros(size, np.uint8)
     off = 0
     for L, ids, r in zip(layers, save_ids, regions):
@@ -97,18 +110,20 @@ def _place_all(layers, save_ids, gap=0):
     return host, ohost
 
 
-@pytest.mark.parametrize("slices", [(3000, 5000), (1, 1), (65536, 2048)])
-def test_staged_slices_across_layers_vs_oracle(gpu, slices):
+@pytest.mark.parametrize("slices,pinned", [((3000, 5000), True), ((1, 1), True),
+                                           ((65536, 2048), True), ((3000, 5000), False)])
+def test_staged_slices_across_layers_vs_oracle(gpu, slices, pinned):
     """One staged save, then one staged load with per-layer events, of eight
     mixed layers, with slices of a few chunks (or one chunk each): host
     regions and every layer tensor equal the oracle's; the layer events
     complete in layer order.  A second load of the same call with layer marks
-    sets every layer's word."""
-    say(f"[gpu] staged slices across layers, slice caps {slices}")
+    sets every layer's word.  Pinned host regions take the copy engines;
+    pageable ones HIP's copies over the context's two streams."""
+    say(f"[gpu] staged slices across layers, slice caps {slices}, pinned={pinned}")
     ctx = TransferContext(0, staging_bytes=64 * 1024)
     ctx.set_staged_slices(*slices)
     layers, save_ids, load_ids = _mixed_layers(70)
-    host, ohost = _place_all(layers, save_ids, gap=8)
+    host, ohost = _place_all(layers, save_ids, gap=8, pinned=pinned)
     words = PinnedBuffer(8 * len(layers))
     try:
         host.array[:] = 0
@@ -228,3 +243,13 @@ def test_auto_mode_follows_host_runs(gpu):
         for h in hosts:
             h.close()
         ctx.close()
+
+
+def test_copy_engines_known(gpu):
+    """The staged mode's copies use one copy engine per direction, different
+    engines for the two directions (so a save and a load can run at once)."""
+    d2h, h2d = copy_engines(0)
+    say(f"[gpu] copy engines: d2h {d2h:#x}, h2d {h2d:#x}")
+    assert d2h and h2d, "no copy engines known for device 0"
+    assert d2h & (d2h - 1) == 0 and h2d & (h2d - 1) == 0, "one engine per direction"
+    assert d2h != h2d
