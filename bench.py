@@ -387,9 +387,11 @@ def duplex_study(xfer_load, xfer_save, saved, loads, pool, pool2, dev_buf, P, re
     """Which direction loses bandwidth when both link directions are busy.
     Each case runs a save and a restore of P bytes at once and reports the
     aggregate payload GB/s and each side's own time (HIP events on its
-    stream): the two queued kernels (as the engine's workers run them), each
+    stream; for a staged side on the copy engines, from its first kernel to
+    the context's stream after the call): the two queued kernels, each
     kernel against a plain DMA copy of P contiguous bytes the other way, the
-    two DMA copies, and the kernels with other persistent-grid sizes."""
+    two DMA copies, the staged pairs, and the kernels with other
+    persistent-grid sizes."""
     from pegaflow_amd import _lib, runtime
     from pegaflow_amd.runtime import Event, Stream
 
@@ -416,12 +418,19 @@ def duplex_study(xfer_load, xfer_save, saved, loads, pool, pool2, dev_buf, P, re
         runtime.memcpy_async(dev_buf.ptr, pool.ptr, P, dma)
         s1.record(dma)
 
+    import threading
+
     def case(restore, save):
         best = None
         for _ in range(reps + 1):
             t0 = time.perf_counter()
-            restore(evs[0], evs[1])   # asynchronous issue first, as the engine's load thread
+            # The restore issued from a second thread, as the engine's load
+            # thread issues it (a staged restore on the copy engines returns
+            # once its copies are done).
+            th = threading.Thread(target=restore, args=(evs[0], evs[1]))
+            th.start()
             save(evs[2], evs[3])
+            th.join()
             xfer_load.synchronize()
             xfer_save.synchronize()
             dma.synchronize()
