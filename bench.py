@@ -926,7 +926,7 @@ def leg_engine(layers, ids, targets, P, reps=4):
     shape = layers.shape
     names = [f"layer.{l}" for l in range(len(layers.bufs))]
     ids_l, targets_l = [int(i) for i in ids], [int(t) for t in targets]
-    e = PegaEngine(pool_size=2 * (reps + 1) * P + (256 << 20))
+    e = PegaEngine(pool_size=(reps + 1) * P + (256 << 20))
     for name, buf in zip(names, layers.bufs):
         e.register_context_layer("bench", "llama3-8b", 0, name, buf.ptr, shape.layer_bytes,
                                  shape.num_blocks, shape.bytes_per_block, shape.kv_stride_bytes,

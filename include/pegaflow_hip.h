@@ -368,18 +368,21 @@ int pf_xfer_set_kernel_shape(pf_xfer* xfer, uint32_t threads, uint32_t unroll);
 /* Upper bound on workgroups per gather/scatter launch (0 = one workgroup per
  * tile, the default); with a bound, each workgroup loops over tiles. */
 int pf_xfer_set_max_grid(pf_xfer* xfer, uint32_t max_workgroups);
-/* The copy engines (one HSA SDMA engine id bit each, from
- * hsa_amd_sdma_engine_id_t) the staged mode's copies run on for `device`:
- * device to host, then host to device; both 0 when they are not known (the
- * staged mode then copies through HIP).  No counterpart in the reference
+/* The copy engines (HSA SDMA engine id bits, from hsa_amd_sdma_engine_id_t)
+ * the staged mode's copies run on for `device`: device to host, then host to
+ * device; one each, different where the device allows (the environment
+ * variable PEGAFLOW_COPY_ENGINES="<d2h>,<h2d>" names others, one or two bits
+ * each, slices alternating between two); both 0 when they are not known
+ * (the staged mode then copies through HIP).  No counterpart in the reference
  * (its copies are cuMemcpy calls); bench_copy_engines measures each engine. */
 int pf_copy_engines(int device, uint32_t* d2h_engine, uint32_t* h2d_engine);
 /* Largest staged slice per direction, in bytes (0 keeps the current value);
- * slices are further capped by the staging slot.  Smaller load slices land
- * a layer sooner; the defaults are the smallest that keep each direction's
- * DMA copies at the link's speed. */
+ * slices are further capped by the staging slot.  A load's slices start at
+ * 8 MiB (or the load size, if smaller) and double, so its first layer lands
+ * early; each copy-engine command costs about 10 us besides its bytes, which
+ * 64 MiB slices amortize to 1%. */
 #define PF_STAGED_SAVE_SLICE_DEFAULT (128ull << 20)
-#define PF_STAGED_LOAD_SLICE_DEFAULT (16ull << 20)
+#define PF_STAGED_LOAD_SLICE_DEFAULT (64ull << 20)
 int pf_xfer_set_staged_slices(pf_xfer* xfer, uint64_t save_bytes, uint64_t load_bytes);
 /* Number of gather/scatter kernel launches and DMA copies issued by the last
  * save/load call on this context. */

@@ -121,8 +121,8 @@ bool pinned_lookup(uint64_t addr, uint64_t len, uint64_t* base, uint64_t* end);
 // 1 GiB each: device to host 57.1 GB/s on engines 0-3, 7-13 GB/s on the
 // others; host to device 57.6 down to 28 GB/s), so a process whose copies
 // land on a slow engine moves them at a fraction of the link's speed.
-// These copies use the runtime's preferred engine for each direction, a
-// different one for each direction where it allows.
+// These copies use the runtime's preferred engines for each direction,
+// different ones for each direction where it allows.
 //
 // A signal counts a batch's copies still in flight (0: none).
 struct EngineSignal {
@@ -130,17 +130,19 @@ struct EngineSignal {
 };
 // True when the device's engines for both directions are known.
 bool engine_copies_available(int device);
-// The engine id bits in use for each direction (false, and 0, when unknown).
+// The engine id bits in use for each direction, one or two each (false,
+// and 0, when unknown).
 bool engine_ids(int device, uint32_t* d2h, uint32_t* h2d);
 int engine_signal_create(EngineSignal* s);  // value 0
 void engine_signal_destroy(EngineSignal* s);
 // Adds n to the count before n copies are submitted against the signal.
 void engine_signal_add(EngineSignal* s, int64_t n);
-// One copy of `bytes` on the device's engine for the direction (d2h: device
-// to host).  The host side must lie in pinned memory.  On success the
-// signal drops by one when the copy is done; on failure it is dropped here.
+// One copy of `bytes` on one of the device's engines for the direction (d2h:
+// device to host; `lane` alternates between the direction's two engines).
+// The host side must lie in pinned memory.  On success the signal drops by
+// one when the copy is done; on failure it is dropped here.
 int engine_copy(int device, bool d2h, uint64_t dst, uint64_t src, uint64_t bytes,
-                EngineSignal* s);
+                EngineSignal* s, unsigned lane);
 // Waits until the signal reads 0 (an error after kEngineWaitSeconds).
 constexpr int kEngineWaitSeconds = 60;
 int engine_signal_wait(EngineSignal* s);

@@ -583,11 +583,10 @@ constexpr size_t kMaxWordMaps = 16;
 // defaults, 32 + 64).
 constexpr uint32_t kLoadGridAlone = 32;
 
-// Staging of the workers' transfer contexts (two slots each): the save
-// context's slots hold the staged mode's largest save slice, the load
-// context's twice its load slice (0.375 GiB of HBM per device in all).
+// Staging of the workers' transfer contexts: two slots each of the staged
+// mode's largest slice (0.375 GiB of HBM per device in all).
 constexpr uint64_t kSaveStagingBytes = 2 * PF_STAGED_SAVE_SLICE_DEFAULT;
-constexpr uint64_t kLoadStagingBytes = 4 * PF_STAGED_LOAD_SLICE_DEFAULT;
+constexpr uint64_t kLoadStagingBytes = 2 * PF_STAGED_LOAD_SLICE_DEFAULT;
 
 int DeviceWorker::create(int device, bool with_gpu, std::shared_ptr<DeviceWorker>* out,
                          std::atomic<uint64_t>* loaded_bytes, std::atomic<uint64_t>* failures) {

@@ -246,10 +246,11 @@ def test_auto_mode_follows_host_runs(gpu):
 
 
 def test_copy_engines_known(gpu):
-    """The staged mode's copies use one copy engine per direction, different
-    engines for the two directions (so a save and a load can run at once)."""
+    """The staged mode's copies use one or two copy engines per direction,
+    different engines for the two directions (so a save and a load can run
+    at once)."""
     d2h, h2d = copy_engines(0)
     say(f"[gpu] copy engines: d2h {d2h:#x}, h2d {h2d:#x}")
     assert d2h and h2d, "no copy engines known for device 0"
-    assert d2h & (d2h - 1) == 0 and h2d & (h2d - 1) == 0, "one engine per direction"
-    assert d2h != h2d
+    assert bin(d2h).count("1") <= 2 and bin(h2d).count("1") <= 2
+    assert d2h & h2d == 0
