@@ -1010,6 +1010,12 @@ int staged_engine(pf_xfer* x, const std::vector<LayerPlan>& plans, StagedPlan& s
   };
   if (is_save) {
     for (size_t si = 0; si < sp.steps.size(); ++si) {
+      if (sp.steps[si].ordered_layer >= 0) {  // not produced for saves; copied in place
+        if (int rc = dma_layer(x, plans[static_cast<size_t>(sp.steps[si].ordered_layer)], true,
+                               false))
+          return rc;
+        continue;
+      }
       const size_t s = slice_of[si] % n_slots;
       // The slot's previous copies (of this call or an earlier one) are done.
       if (int rc = engine_signal_wait(&x->eng_sig[s])) return rc;

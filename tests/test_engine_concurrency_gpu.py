@@ -4,7 +4,9 @@ A saver thread keeps sealing new batches of one instance's blocks while two
 loader threads restore recently sealed batches into disjoint target blocks
 of a second instance (plain and layered LoadStates alternating) and a query
 thread counts prefix hits.  The pool holds only a few batches, so eviction
-runs all the time.
+runs all the time.  It runs with the zero-copy kernels both ways, with saves
+staged on the copy engines beside kernel loads, and with both directions
+staged.
 
 Every load that succeeds must leave its targets holding exactly the source
 blocks' words, checked in closed form on the device.  A load that names a
@@ -73,12 +75,19 @@ def check_targets(dst, src, sources, targets):
     return bad
 
 
-def test_concurrent_saves_loads_and_queries(gpu):
-    say("[gpu] engine concurrency: saver, two loaders, a query thread, constant eviction")
+# (save mode, load mode): the zero-copy kernels both ways; saves staged on the
+# copy engines beside kernel loads; both directions staged.
+MODES = [("kernel", "kernel"), ("staged", "kernel"), ("staged", "staged")]
+
+
+@pytest.mark.parametrize("save_mode,load_mode", MODES)
+def test_concurrent_saves_loads_and_queries(gpu, save_mode, load_mode):
+    say(f"[gpu] engine concurrency ({save_mode} saves, {load_mode} loads): saver, two loaders, "
+        "a query thread, constant eviction")
     n_layers, nb, bpb, per_batch = 8, 512, 16384, 32
     batch_bytes = n_layers * per_batch * 2 * bpb  # 8 MiB
     e = PegaEngine(pool_size=6 * batch_bytes)      # room for about 6 batches
-    e.set_transfer_modes(_lib.MODE_KERNEL, _lib.MODE_KERNEL)
+    e.set_transfer_modes(_lib.MODE_NAMES[save_mode], _lib.MODE_NAMES[load_mode])
     src = Layers(n_layers, nb, bpb, seed=3)
     dst = Layers(n_layers, nb, bpb, seed=4)
     src.register(e, "prefill")
