@@ -934,34 +934,88 @@ def leg_engine(layers, ids, targets, P, reps=4):
     layers.refill()
     from pegaflow_amd import _lib
 
-    save_s, load_s, ksave_s = [], [], []
+    save_s, ksave_s = [], []
     hashes = None
-    # The engine's default modes (saves staged on the copy engines, loads by
-    # the zero-copy kernel), then saves by the kernel for comparison.
+    # The engine's default modes (saves and loads staged on the copy
+    # engines), then saves by the kernel for comparison.
     for r in range(2 * (reps + 1)):  # every save uses new hashes: nothing is deduplicated
         if r == reps + 1:
-            e.set_transfer_modes(_lib.MODE_KERNEL, _lib.MODE_KERNEL)
+            e.set_transfer_modes(_lib.MODE_KERNEL, _lib.MODE_AUTO)
         hashes = [hashlib.sha256(b"engine%d-" % r + int(i).to_bytes(8, "little")).digest()
                   for i in ids_l]
         t0 = time.perf_counter()
         e.batch_save_kv_blocks("bench", 0, 0, [(n, ids_l, hashes) for n in names])
         (save_s if r <= reps else ksave_s).append(time.perf_counter() - t0)
-    e.set_transfer_modes()
     bad = 0
-    layered_s = []
-    for layered, out in ((False, load_s), (True, layered_s)):
-        for r in range(reps + 1):
-            st = PyLoadState(num_layers=len(names)) if layered else PyLoadState()
-            t0 = time.perf_counter()
-            e.batch_load_kv_blocks("bench", 0, 0, st.shm_name(), names, targets_l, hashes)
-            while not st.is_ready():
-                if time.perf_counter() - t0 > 60:
-                    raise RuntimeError("engine restore did not complete within 60 s")
-                time.sleep(0.0001)
-            out.append(time.perf_counter() - t0)
-            bad += st.get_state() != 1
+
+    def restore(layered):
+        """One load of the prefix by hash: (seconds to ready, to layer 0 done)."""
+        st = PyLoadState(num_layers=len(names)) if layered else PyLoadState()
+        t0 = time.perf_counter()
+        e.batch_load_kv_blocks("bench", 0, 0, st.shm_name(), names, targets_l, hashes)
+        t_first = None
+        while not st.is_ready():
+            if layered and t_first is None and st.layers_done() >= 1:
+                t_first = time.perf_counter()
+            if time.perf_counter() - t0 > 60:
+                raise RuntimeError("engine restore did not complete within 60 s")
+        t1 = time.perf_counter()
+        if st.get_state() != 1:
+            raise RuntimeError("engine restore failed")
+        return t1 - t0, (t_first or t1) - t0
+
+    loads = {}
+    for mode in ("auto", "kernel"):
+        e.set_transfer_modes(_lib.MODE_AUTO, _lib.MODE_NAMES[mode])
+        for layered in (False, True):
+            runs = [restore(layered) for _ in range(reps + 1)]
+            loads[(mode, layered)] = runs
+            bad += wl.verify_restored(layers, ids, targets)
+            layers.refill()
+    e.set_transfer_modes()
+    # Duplex: a save of a new batch and a restore of the last one at once,
+    # from two threads (the reference's save and load workers).
+    import threading
+
+    duplex_s = []
+    for r in range(reps + 1):
+        new = [hashlib.sha256(b"duplex%d-" % r + int(i).to_bytes(8, "little")).digest()
+               for i in ids_l]
+        go = threading.Barrier(3)
+        ends, errs = {}, []
+
+        def saver():
+            try:
+                go.wait()
+                e.batch_save_kv_blocks("bench", 0, 0, [(n, ids_l, new) for n in names])
+                ends["save"] = time.perf_counter()
+            except BaseException as err:  # reported below
+                errs.append(err)
+
+        def loader():
+            try:
+                go.wait()
+                restore(False)
+                ends["load"] = time.perf_counter()
+            except BaseException as err:  # reported below
+                errs.append(err)
+
+        ts = [threading.Thread(target=saver), threading.Thread(target=loader)]
+        for t in ts:
+            t.start()
+        go.wait()
+        t0 = time.perf_counter()
+        for t in ts:
+            t.join(120)
+        if errs:
+            raise errs[0]
+        duplex_s.append(max(ends.values()) - t0)
         bad += wl.verify_restored(layers, ids, targets)
         layers.refill()
+        hashes = new  # the next round restores what this one saved
+    restore(False)  # the last duplex save, restored and checked
+    bad += wl.verify_restored(layers, ids, targets)
+    layers.refill()
     # Small restores (the first 1 and 16 blocks of the prefix, all 32
     # layers): latency from the call to the LoadState reading ready.
     # The same through the reference's copy pattern (one async copy per
@@ -985,23 +1039,32 @@ def leg_engine(layers, ids, targets, P, reps=4):
     layers.refill()
     stats = e.stats()
     e.close()
+    med = lambda v: statistics.median(v[1:])  # noqa: E731
+    gbps = lambda runs: round(P / med([t for t, _ in runs]) / 1e9, 3)  # noqa: E731
     return {
         "small_restore_latency": small,
         "what": "the llama prefix through PegaEngine: save by hash (new hashes each time), load "
                 "by hash with a plain LoadState (as the reference's connector) and with a "
-                "layered one (per-layer completion), median of the warm calls; the engine's "
-                "default modes (saves staged on the copy engines, loads by the zero-copy "
-                "kernel), and kernel saves for comparison",
+                "layered one (per-layer completion; first layer from the call to layer 0 "
+                "reading done), median of the warm calls; the engine's default modes (auto: "
+                "saves and loads staged on the copy engines), kernel saves and loads for "
+                "comparison, and a save and a restore at once from two threads (duplex)",
         "save_mode": "auto (staged)",
+        "load_mode": "auto (staged)",
         "save_gbps": round(P / statistics.median(save_s[1:]) / 1e9, 3),
         "kernel_save_gbps": round(P / statistics.median(ksave_s[1:]) / 1e9, 3),
-        "restore_gbps": round(P / statistics.median(load_s[1:]) / 1e9, 3),
-        "restore_layered_gbps": round(P / statistics.median(layered_s[1:]) / 1e9, 3),
+        "restore_gbps": gbps(loads[("auto", False)]),
+        "restore_layered_gbps": gbps(loads[("auto", True)]),
+        "first_layer_ms": round(med([f for _, f in loads[("auto", True)]]) * 1e3, 3),
+        "kernel_restore_gbps": gbps(loads[("kernel", False)]),
+        "kernel_first_layer_ms": round(med([f for _, f in loads[("kernel", True)]]) * 1e3, 3),
+        "duplex_gbps": round(2 * P / med(duplex_s) / 1e9, 3),
         "first_save_gbps": round(P / save_s[0] / 1e9, 3),
         "save_ms": [round(t * 1e3, 2) for t in save_s],
         "kernel_save_ms": [round(t * 1e3, 2) for t in ksave_s],
-        "restore_ms": [round(t * 1e3, 2) for t in load_s],
-        "restore_layered_ms": [round(t * 1e3, 2) for t in layered_s],
+        "restore_ms": [round(t * 1e3, 2) for t, _ in loads[("auto", False)]],
+        "kernel_restore_ms": [round(t * 1e3, 2) for t, _ in loads[("kernel", False)]],
+        "duplex_ms": [round(t * 1e3, 2) for t in duplex_s],
         "sealed_blocks": stats["sealed_blocks"],
         "bit_exact": bad == 0,
     }

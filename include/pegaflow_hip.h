@@ -378,7 +378,8 @@ int pf_xfer_set_max_grid(pf_xfer* xfer, uint32_t max_workgroups);
 int pf_copy_engines(int device, uint32_t* d2h_engine, uint32_t* h2d_engine);
 /* Largest staged slice per direction, in bytes (0 keeps the current value);
  * slices are further capped by the staging slot.  A load's slices start at
- * 8 MiB (or the load size, if smaller) and double, so its first layer lands
+ * an eighth of its largest slice (at most 8 MiB) and double, each of the
+ * first layers ending its last slice meanwhile, so the first layers land
  * early; each copy-engine command costs about 10 us besides its bytes, which
  * 64 MiB slices amortize to 1%. */
 #define PF_STAGED_SAVE_SLICE_DEFAULT (128ull << 20)
@@ -629,12 +630,14 @@ int pf_engine_create(uint64_t pool_bytes, uint32_t pool_kind,
                      uint32_t pinned_flags, uint64_t unit_hint,
                      pf_engine** out);
 int pf_engine_destroy(pf_engine* e);
-/* Transfer strategies used by saves and loads.  Defaults: saves
- * PF_MODE_AUTO (a save batch's host regions are long runs, so saves run
- * staged and leave the device's other kernels at their speed), loads
- * PF_MODE_KERNEL (the link's full rate and the first layer soonest).  The
- * workers' contexts have staging for every mode.  An AUTO load is resolved
- * from its first layer's block list. */
+/* Transfer strategies used by saves and loads.  Defaults: PF_MODE_AUTO both
+ * ways: a save batch's host regions, and a load of blocks saved together,
+ * are long runs, so they run staged on the copy engines and leave the
+ * device's other kernels at their speed; a load of a few scattered blocks
+ * takes the kernel.  A load whose LoadState carries per-layer events runs
+ * the kernel mode instead of the staged one (its events are recorded at
+ * issue).  The workers' contexts have staging for every mode.  An AUTO load
+ * is resolved from its first layer's block list. */
 int pf_engine_set_modes(pf_engine* e, uint32_t save_mode, uint32_t load_mode);
 /* register_context_layer (lib.rs:373-469). */
 int pf_engine_register_context_layer(pf_engine* e, const char* instance_id,

@@ -517,6 +517,67 @@ struct LoadTask {
   std::shared_ptr<LaterLayers> later;
 };
 
+// A thread that runs one job at a time for the load thread: the issue of a
+// staged load, whose call drives the copy engines slice by slice and returns
+// only once its copies are done, while the load thread publishes each layer
+// as its mark lands.
+class Issuer {
+ public:
+  Issuer() : thread_([this] { loop(); }) {}
+  ~Issuer() {
+    {
+      std::lock_guard<std::mutex> lk(mu_);
+      stop_ = true;
+    }
+    cv_.notify_all();
+    thread_.join();
+  }
+  // Starts `job`; the previous job must have been waited for.
+  void start(std::function<int()> job) {
+    {
+      std::lock_guard<std::mutex> lk(mu_);
+      job_ = std::move(job);
+      finished_.store(false, std::memory_order_relaxed);
+    }
+    cv_.notify_all();
+  }
+  // True once the job has returned.
+  bool finished() const { return finished_.load(std::memory_order_acquire); }
+  // Waits for the job; its result, with its error message set on this thread.
+  int wait() {
+    std::unique_lock<std::mutex> lk(mu_);
+    cv_.wait(lk, [this] { return finished(); });
+    return rc_ == PF_OK ? PF_OK : fail(rc_, msg_);
+  }
+
+ private:
+  void loop() {
+    std::unique_lock<std::mutex> lk(mu_);
+    for (;;) {
+      cv_.wait(lk, [this] { return stop_ || job_; });
+      if (!job_) return;
+      std::function<int()> job = std::move(job_);
+      job_ = nullptr;
+      lk.unlock();
+      const int rc = job();
+      std::string msg = rc == PF_OK ? std::string() : std::string(pf_last_error());
+      lk.lock();
+      rc_ = rc;
+      msg_ = std::move(msg);
+      finished_.store(true, std::memory_order_release);
+      cv_.notify_all();
+    }
+  }
+  std::mutex mu_;
+  std::condition_variable cv_;
+  std::function<int()> job_;
+  std::atomic<bool> finished_{true};
+  int rc_ = PF_OK;
+  std::string msg_;
+  bool stop_ = false;
+  std::thread thread_;  // last: started once the members above exist
+};
+
 class DeviceWorker {
  public:
   static int create(int device, bool with_gpu, std::shared_ptr<DeviceWorker>* out,
@@ -565,6 +626,7 @@ class DeviceWorker {
   // shares the host link with them (see kLoadGridAlone).
   std::atomic<int> saves_running_{0};
   std::vector<std::shared_ptr<SealedBlock>> spare_keep_;  // under q_mu_
+  std::unique_ptr<Issuer> issuer_;  // staged marked loads (with a device)
 
   int map_layer_words(const pf_layer_words& w, uint64_t* words);
   int load_marked(std::vector<pf_layer_xfer>& layers, uint32_t mode, pf_load_state* st,
@@ -599,6 +661,7 @@ int DeviceWorker::create(int device, bool with_gpu, std::shared_ptr<DeviceWorker
     if (pf_xfer_create(device, kSaveStagingBytes, &w->save_x_) != PF_OK ||
         pf_xfer_create(device, kLoadStagingBytes, &w->load_x_) != PF_OK)
       return fail(PF_ERR_INIT, std::string("failed to initialize HIP: ") + pf_last_error());
+    w->issuer_.reset(new Issuer());
   }
   w->thread_ = std::thread([p = w.get()] { p->load_loop(); });
   *out = std::move(w);
@@ -612,6 +675,7 @@ DeviceWorker::~DeviceWorker() {
   }
   q_cv_.notify_all();
   if (thread_.joinable()) thread_.join();
+  issuer_.reset();
   if (save_x_) pf_xfer_destroy(save_x_);
   if (load_x_) pf_xfer_destroy(load_x_);
   if (gpu_) {
@@ -679,10 +743,24 @@ int DeviceWorker::load_marked(std::vector<pf_layer_xfer>& layers, uint32_t mode,
     n_sig = 2;
   }
   const auto t0 = std::chrono::steady_clock::now();
-  if (int rc = pending ? load_layers_pending(load_x_, layers.data(), static_cast<uint32_t>(L),
-                                             mode, nullptr, sig, n_sig, *pending)
-                       : pf_load_layers_marked(load_x_, layers.data(), static_cast<uint32_t>(L),
-                                               mode, sig, n_sig))
+  auto issue = [&]() -> int {
+    return pending ? load_layers_pending(load_x_, layers.data(), static_cast<uint32_t>(L), mode,
+                                         nullptr, sig, n_sig, *pending)
+                   : pf_load_layers_marked(load_x_, layers.data(), static_cast<uint32_t>(L), mode,
+                                           sig, n_sig);
+  };
+  // A staged load returns only once its copies are done: it is issued from
+  // the issuer thread while this one publishes its layers as they land.
+  // Every return below waits for the issue first (it uses the task's lists).
+  struct Join {
+    Issuer* issuer;
+    ~Join() {
+      if (issuer) (void)issuer->wait();
+    }
+  } join{mode == PF_MODE_STAGED ? issuer_.get() : nullptr};
+  if (join.issuer)
+    join.issuer->start(issue);
+  else if (int rc = issue())
     return rc;
   const auto t_issued = std::chrono::steady_clock::now();
   auto t_first = t_issued;
@@ -690,7 +768,13 @@ int DeviceWorker::load_marked(std::vector<pf_layer_xfer>& layers, uint32_t mode,
   for (size_t l = 0; l < L; ++l) {
     const uint64_t* w = host_words_ + l;
     for (uint32_t spins = 0; __atomic_load_n(w, __ATOMIC_ACQUIRE) < ticket; ++spins) {
-      if (spins % 64 == 63) {
+      // While a staged load is still issuing, its copies are in flight.
+      if (spins % 64 == 63 && join.issuer && join.issuer->finished()) {
+        Issuer* done = join.issuer;
+        join.issuer = nullptr;
+        if (int rc = done->wait()) return rc;
+      }
+      if (spins % 64 == 63 && !join.issuer) {
         const hipError_t q = hipStreamQuery(stream);
         if (q != hipErrorNotReady && __atomic_load_n(w, __ATOMIC_ACQUIRE) < ticket)
           return fail(PF_ERR_STORAGE,
@@ -701,6 +785,11 @@ int DeviceWorker::load_marked(std::vector<pf_layer_xfer>& layers, uint32_t mode,
     }
     pf_load_state_set_layers_done(st, static_cast<int64_t>(l + 1));
     if (l == 0) t_first = std::chrono::steady_clock::now();
+  }
+  if (join.issuer) {
+    Issuer* done = join.issuer;
+    join.issuer = nullptr;
+    if (int rc = done->wait()) return rc;
   }
   if (tracing())
     std::fprintf(stderr, "[pegaflow] marked load at=%.0fus issue=%.0fus first_layer=%.0fus\n",
@@ -874,6 +963,10 @@ void DeviceWorker::load_loop() {
     // its event).  Otherwise completion is published at the end.
     const bool marked = ipc_evs.empty() && (pf_load_state_num_layers(task.state) > 0);
     const bool per_layer = !ipc_evs.empty();
+    // A consumer's events are recorded at issue by the kernel mode; a staged
+    // load would record each only as its layer lands, after the consumer
+    // was told that every record is on the stream.
+    if (per_layer && task.mode == PF_MODE_STAGED) task.mode = PF_MODE_KERNEL;
     if (ok && L > 0 && marked) {
       ok = load_marked(layers, task.mode, task.state, consumer_words, lw.value, pending.get()) ==
            PF_OK;
@@ -1031,13 +1124,17 @@ struct pf_engine {
   std::unordered_map<std::string, std::shared_ptr<Instance>> instances;
   std::shared_ptr<PinnedPool> pool;
   std::unique_ptr<BlockStore> store;
-  // Saves run staged (PF_MODE_AUTO: copy-engine DMA for a save batch's
-  // regions), leaving the device's other kernels at their speed: a zero-copy
-  // save held a bf16 GEMM in another process to 1/29th of its speed while it
-  // ran.  Loads, on the request's path, run the zero-copy kernel: the
-  // link's full rate and the first layer soonest, at 2.4x on such a GEMM.
+  // Saves and loads of long host runs (PF_MODE_AUTO) run staged, their
+  // link traffic on the copy engines, leaving the device's other kernels at
+  // their speed: beside a zero-copy save a bf16 GEMM in another process ran
+  // at 1/29th of its speed, beside a zero-copy restore at 1/2.4th.  A staged
+  // load lands its first layer as soon as the kernel's (its first layer is
+  // sliced and copied while the rest is planned), and a staged save and
+  // load at once share the link (94 GB/s) where a zero-copy restore starves
+  // a staged save (59 GB/s).  Loads of short runs (a few blocks) take the
+  // kernel.
   std::atomic<uint32_t> save_mode{PF_MODE_AUTO};
-  std::atomic<uint32_t> load_mode{PF_MODE_KERNEL};
+  std::atomic<uint32_t> load_mode{PF_MODE_AUTO};
   std::atomic<uint64_t> saved_bytes{0};
   std::atomic<uint64_t> loaded_bytes{0};
   std::atomic<uint64_t> load_failures{0};
@@ -1576,7 +1673,7 @@ int pf_engine_batch_load(pf_engine* e, const char* instance_id, uint64_t tp_rank
     }
     return PF_OK;
   };
-  // A large kernel-mode load is split: the lists of its first layers are
+  // A large kernel-mode or staged load is split: the lists of its first layers are
   // built and submitted, and this thread builds the rest while the load
   // thread copies those, so the first layers do not wait for the whole plan
   // (40-170 us for 640 blocks x 32 layers, varying with the core this thread
@@ -1600,7 +1697,8 @@ int pf_engine_batch_load(pf_engine* e, const char* instance_id, uint64_t tp_rank
   uint64_t chunks = 0;
   for (const LayerRef& r : refs) chunks += n * (r.split ? 2 : 1);
   uint32_t head = 0;
-  if (task.mode == PF_MODE_KERNEL && pipeline_head_layers(num_layers, chunks) > 0) {
+  if ((task.mode == PF_MODE_KERNEL || task.mode == PF_MODE_STAGED) &&
+      pipeline_head_layers(num_layers, chunks) > 0) {
     constexpr uint64_t kHeadBytesPerLaterEntry = 500;
     uint64_t head_bytes = 0;
     for (head = 0; head + 1 < num_layers; ) {

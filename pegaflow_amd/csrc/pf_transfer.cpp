@@ -2,6 +2,8 @@
 // (transfer.rs) and the batched transfer context that replaces the per-call
 // copy loops of gpu_worker.rs with gather/scatter kernels.
 #include <algorithm>
+#include <chrono>
+#include <cstdio>
 #include <cstring>
 #include <mutex>
 #include <vector>
@@ -769,76 +771,127 @@ struct StagedPlan {
   size_t n_desc = 0;
 };
 
-// A load's first slice, at most; later slices double up to the load slice
-// size.  Each copy-engine command costs about 10 us besides its bytes (80 x
-// 16 MiB host-to-device copies on one engine moved 55.5 GB/s, 20 x 64 MiB
-// 57.0), so slices grow to amortize it while the first layer lands early.
+// A load's first slice is an eighth of the load slice size, at most 8 MiB;
+// later slices double up to the load slice size.  Each copy-engine command
+// costs about 10 us besides its bytes (80 x 16 MiB host-to-device copies on
+// one engine moved 55.5 GB/s, 20 x 64 MiB 57.0), so slices grow to amortize
+// it while the first layer lands early.
 constexpr uint64_t kStagedLoadFirstSlice = 8ull << 20;
 
-int plan_staged(const pf_xfer* x, const std::vector<LayerPlan>& plans, bool is_save,
-                StagedPlan* sp) {
-  const uint64_t max_cap = std::min(x->slot_bytes, x->staged_slice[is_save ? 0 : 1]);
-  uint64_t cap = is_save ? max_cap : std::min(max_cap, kStagedLoadFirstSlice);
-  sp->steps.clear();
-  sp->pieces.clear();
-  sp->done_at.assign(plans.size(), -1);
-  sp->n_desc = 0;
-  StagedStep cur;
-  uint64_t cur_bytes = 0;
-  auto close = [&]() {
-    if (cur.n_chunks > 0) {
-      cur.piece_end = sp->pieces.size();
-      cur.desc_first = sp->n_desc;
-      sp->n_desc += cur.n_chunks;
-      sp->steps.push_back(cur);
-      cap = std::min(max_cap, 2 * cap);
-    }
-    cur = StagedStep{};
-    cur.piece_begin = sp->pieces.size();
-    cur_bytes = 0;
-  };
-  for (uint32_t li = 0; li < plans.size(); ++li) {
-    const LayerPlan& p = plans[li];
-    if (p.ordered) {
-      close();
-      StagedStep st;
-      st.piece_begin = st.piece_end = sp->pieces.size();
-      st.ordered_layer = li;
-      sp->steps.push_back(st);
-      sp->done_at[li] = static_cast<int64_t>(sp->steps.size()) - 1;
-      continue;
-    }
-    if (p.chunks.empty()) {
-      // In place once everything before it is: after the open slice, if any.
-      sp->done_at[li] = static_cast<int64_t>(sp->steps.size()) - (cur.n_chunks > 0 ? 0 : 1);
-      continue;
-    }
-    if (p.chunk_bytes > x->slot_bytes)
-      return fail(PF_ERR_INVALID_ARGUMENT,
-                  strf("staging slot (%llu bytes) smaller than one chunk (%llu)",
-                       (unsigned long long)x->slot_bytes,
-                       (unsigned long long)p.chunk_bytes));
-    if (cur.n_chunks > 0 && cur.chunk_bytes != p.chunk_bytes) close();
-    // A slice holds at least one chunk, even one larger than the slice size.
-    const uint64_t lcap = std::max(cap, p.chunk_bytes);
-    size_t i = 0;
-    while (i < p.chunks.size()) {
-      const size_t room = static_cast<size_t>((lcap - cur_bytes) / p.chunk_bytes);
-      if (room == 0) {
+// done_at of a layer not sliced yet.
+constexpr int64_t kNotSliced = INT64_MIN;
+
+// Cuts the chunks of a call's layers into slices, in layer order, a range of
+// layers at a time (a pipelined load slices its first layer, queues its
+// copies, and slices the rest while they run).  Plans are indexed by the
+// call's layer numbers.
+class StagedPlanner {
+ public:
+  StagedPlanner(const pf_xfer* x, bool is_save, size_t num_layers, StagedPlan* sp)
+      : sp_(sp),
+        is_save_(is_save),
+        slot_bytes_(x->slot_bytes),
+        max_cap_(std::min(x->slot_bytes, x->staged_slice[is_save ? 0 : 1])) {
+    cap_ = is_save ? max_cap_
+                   : std::max<uint64_t>(1, std::min(kStagedLoadFirstSlice, max_cap_ / 8));
+    sp_->steps.clear();
+    sp_->pieces.clear();
+    sp_->done_at.assign(num_layers, kNotSliced);
+    sp_->n_desc = 0;
+  }
+
+  // Slices layers [begin, end), after those sliced so far.
+  int add(const std::vector<LayerPlan>& plans, uint32_t begin, uint32_t end) {
+    for (uint32_t li = begin; li < end; ++li) {
+      const LayerPlan& p = plans[li];
+      if (p.ordered) {
         close();
+        StagedStep st;
+        st.piece_begin = st.piece_end = sp_->pieces.size();
+        st.ordered_layer = li;
+        sp_->steps.push_back(st);
+        sp_->done_at[li] = static_cast<int64_t>(sp_->steps.size()) - 1;
         continue;
       }
-      const size_t take = std::min(room, p.chunks.size() - i);
-      cur.chunk_bytes = p.chunk_bytes;
-      sp->pieces.push_back({li, i, i + take});
-      cur.n_chunks += take;
-      cur_bytes += take * p.chunk_bytes;
-      i += take;
+      if (p.chunks.empty()) {
+        // In place once everything before it is: after the open slice, if any.
+        sp_->done_at[li] = static_cast<int64_t>(sp_->steps.size()) - (cur_.n_chunks > 0 ? 0 : 1);
+        continue;
+      }
+      if (p.chunk_bytes > slot_bytes_)
+        return fail(PF_ERR_INVALID_ARGUMENT,
+                    strf("staging slot (%llu bytes) smaller than one chunk (%llu)",
+                         (unsigned long long)slot_bytes_, (unsigned long long)p.chunk_bytes));
+      if (cur_.n_chunks > 0 && cur_.chunk_bytes != p.chunk_bytes) close();
+      size_t i = 0;
+      while (i < p.chunks.size()) {
+        // A slice holds at least one chunk, even one larger than the slice size.
+        const uint64_t lcap = std::max(cap_, p.chunk_bytes);
+        const size_t room = static_cast<size_t>((lcap - cur_bytes_) / p.chunk_bytes);
+        if (room == 0) {
+          close();
+          continue;
+        }
+        const size_t take = std::min(room, p.chunks.size() - i);
+        cur_.chunk_bytes = p.chunk_bytes;
+        sp_->pieces.push_back({li, i, i + take});
+        cur_.n_chunks += take;
+        cur_bytes_ += take * p.chunk_bytes;
+        i += take;
+      }
+      sp_->done_at[li] = static_cast<int64_t>(sp_->steps.size());  // the open slice
+      // A load's layer ends its last slice while slices still grow (its
+      // first layers) and once that slice is half full, so the layer lands
+      // without waiting for the next one's bytes.
+      if (!is_save_ && (cap_ < max_cap_ || 2 * cur_bytes_ >= cap_)) close();
     }
-    sp->done_at[li] = static_cast<int64_t>(sp->steps.size());  // the open slice
+    return PF_OK;
   }
-  close();
-  if (sp->n_desc > 0xffffffffull) return fail(PF_ERR_INVALID_ARGUMENT, "too many chunks");
+
+  // Closes the open slice: the steps so far are final.
+  int cut() {
+    close();
+    if (sp_->n_desc > 0xffffffffull) return fail(PF_ERR_INVALID_ARGUMENT, "too many chunks");
+    return PF_OK;
+  }
+
+ private:
+  void close() {
+    if (cur_.n_chunks > 0) {
+      cur_.piece_end = sp_->pieces.size();
+      cur_.desc_first = sp_->n_desc;
+      sp_->n_desc += cur_.n_chunks;
+      sp_->steps.push_back(cur_);
+      cap_ = std::min(max_cap_, 2 * cap_);
+    }
+    cur_ = StagedStep{};
+    cur_.piece_begin = sp_->pieces.size();
+    cur_bytes_ = 0;
+  }
+
+  StagedPlan* sp_;
+  bool is_save_;
+  uint64_t slot_bytes_, max_cap_, cap_ = 0, cur_bytes_ = 0;
+  StagedStep cur_;
+};
+
+// Plans layers [begin, end) of a staged call into plans[begin, end).
+int plan_range(const pf_layer_xfer* layers, uint32_t begin, uint32_t end, bool is_save,
+               std::vector<LayerPlan>* plans) {
+  for (uint32_t li = begin; li < end; ++li) {
+    if (int rc = plan_layer(layers[li], is_save, &(*plans)[li])) return rc;
+    apply_write_policy(layers[li], is_save, true, &(*plans)[li]);
+  }
+  return PF_OK;
+}
+
+// The device tensors of layers [begin, end) that the staged kernels touch.
+int check_devices(const pf_layer_xfer* layers, const std::vector<LayerPlan>& plans,
+                  uint32_t begin, uint32_t end) {
+  RangeCache rc;
+  for (uint32_t li = begin; li < end; ++li)
+    if (!plans[li].chunks.empty() && !plans[li].ordered)
+      if (int r = check_device_tensor(rc, layers[li].layout)) return r;
   return PF_OK;
 }
 
@@ -886,6 +939,26 @@ void for_each_step_chunk(const std::vector<LayerPlan>& plans, const StagedPlan& 
   }
 }
 
+// PEGAFLOW_TRACE: microseconds from the start of a staged call to each of
+// its steps (slices queued and completed, layers completed), printed as one
+// line when the call ends.
+struct StagedTrace {
+  bool on = tracing();
+  std::chrono::steady_clock::time_point t0 = std::chrono::steady_clock::now();
+  std::string line;
+  void mark(const char* what, size_t i) {
+    if (!on) return;
+    const double us =
+        std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count();
+    line += strf(" %s%zu=%.0f", what, i, us);
+  }
+  void print(bool is_save) {
+    if (on)
+      std::fprintf(stderr, "[pegaflow] staged %s at=%.0fus%s\n", is_save ? "save" : "load",
+                   mono_us(t0), line.c_str());
+  }
+};
+
 // Waits for every copy-engine copy the context has in flight.
 int engine_drain(pf_xfer* x) {
   if (!x->engine_ok) return PF_OK;
@@ -895,11 +968,12 @@ int engine_drain(pf_xfer* x) {
   return rc;
 }
 
-// True when every host-side chunk of the staged layers lies in pinned memory
-// (the copy engines read and write it directly); checked per layer by its
-// span first.
-bool hosts_pinned(const std::vector<LayerPlan>& plans) {
-  for (const LayerPlan& p : plans) {
+// True when every host-side chunk of the staged layers [begin, end) lies in
+// pinned memory (the copy engines read and write it directly); checked per
+// layer by its span first.
+bool hosts_pinned(const std::vector<LayerPlan>& plans, uint32_t begin, uint32_t end) {
+  for (uint32_t li = begin; li < end; ++li) {
+    const LayerPlan& p = plans[li];
     if (p.chunks.empty() || p.ordered) continue;
     uint64_t lo = p.chunks[0].host, hi = p.chunks[0].host;
     for (const Chunk& c : p.chunks) {
@@ -914,6 +988,15 @@ bool hosts_pinned(const std::vector<LayerPlan>& plans) {
   return true;
 }
 
+// Pinned host memory, by the allocation found last.
+struct PinnedCache {
+  uint64_t b = 0, e = 0;
+  bool covers(uint64_t a, uint64_t n) {
+    if (a >= b && a + n >= a && a + n <= e) return true;
+    return pinned_lookup(a, n, &b, &e);
+  }
+};
+
 // The staged mode with its copies on the device's copy engines, driven from
 // the calling thread.  An engine runs its copies in submission order, one
 // after another, so keeping the next slice's copy queued behind the running
@@ -923,19 +1006,26 @@ bool hosts_pinned(const std::vector<LayerPlan>& plans) {
 // the copies that refill it once the scatter is done.  Every kernel runs on
 // the context's stream.  A load returns once its copies are done and its
 // last kernels are issued, with its layer events and marks recorded.
-int staged_engine(pf_xfer* x, const std::vector<LayerPlan>& plans, StagedPlan& sp,
-                  bool is_save, pf_event* layer_events, const SignalTargets* sig,
-                  bool wait_save) {
-  // Slots: as many as the staging holds of the largest slice (at least one).
-  uint64_t stride = 0;
-  std::vector<size_t> slice_of(sp.steps.size(), SIZE_MAX);
-  size_t n_slices = 0;
-  for (size_t si = 0; si < sp.steps.size(); ++si) {
-    const StagedStep& st = sp.steps[si];
-    if (st.ordered_layer >= 0) continue;
-    slice_of[si] = n_slices++;
-    stride = std::max(stride, st.n_chunks * st.chunk_bytes);
-  }
+//
+// A pipelined load (head < num_layers) has planned and sliced only its
+// first `head` layers on entry.  Once their first copies are queued it takes
+// the rest of its layers (pending->ready(), when they were still being
+// listed), plans and slices them and uploads their descriptors while those
+// copies run.  Host runs outside pinned memory are copied through HIP, each
+// waited for before the next is queued.
+int staged_engine(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
+                  std::vector<LayerPlan>& plans, StagedPlanner& planner, StagedPlan& sp,
+                  uint32_t head, const PendingLayers* pending, bool is_save,
+                  pf_event* layer_events, const SignalTargets* sig, bool wait_save,
+                  StagedTrace& tr) {
+  const bool piped = head < num_layers;
+  // Slots: as many as the staging holds of the largest slice (at least one);
+  // a pipelined load's later slices are not known yet, so its slots are the
+  // staging's two.
+  uint64_t stride = piped ? x->slot_bytes : 0;
+  if (!piped)
+    for (const StagedStep& st : sp.steps)
+      if (st.ordered_layer < 0) stride = std::max<uint64_t>(stride, st.n_chunks * st.chunk_bytes);
   stride = (stride + 255) & ~uint64_t(255);
   size_t n_slots = 1;
   if (stride > 0)
@@ -944,26 +1034,64 @@ int staged_engine(pf_xfer* x, const std::vector<LayerPlan>& plans, StagedPlan& s
   auto slot_base = [&](size_t j) {
     return x->staging + static_cast<uint64_t>(j % n_slots) * stride;
   };
-  ChunkDesc* hd = small_desc(x, sp.n_desc);
+  // Per step its slice number (SIZE_MAX: copied in place); per slice its step.
+  std::vector<size_t> slice_of, slice_steps;
+  auto index = [&]() {
+    for (size_t si = slice_of.size(); si < sp.steps.size(); ++si) {
+      if (sp.steps[si].ordered_layer >= 0) {
+        slice_of.push_back(SIZE_MAX);
+      } else {
+        slice_of.push_back(slice_steps.size());
+        slice_steps.push_back(si);
+      }
+    }
+  };
+  index();
+  ChunkDesc* hd = piped ? nullptr : small_desc(x, sp.n_desc);
   if (!hd) {
-    if (int rc = ensure_desc_capacity(x, sp.n_desc)) return rc;
+    // Room for every descriptor of the call, reserved before the first part
+    // is uploaded: growing the buffers later would wait for its copies.
+    uint64_t bound = sp.n_desc;
+    if (piped) {
+      bound = 0;
+      for (uint32_t li = 0; li < num_layers; ++li)
+        bound += (pending && li >= head ? pending->max_blocks : layers[li].num_blocks) *
+                 (layers[li].layout.segments ? layers[li].layout.segments : 1);
+    }
+    if (int rc = ensure_desc_capacity(x, static_cast<size_t>(bound))) return rc;
     hd = x->h_desc;
+    // A later part's upload waits for everything the stream holds so far.
+    if (piped) PF_HIP(hipEventRecord(x->parts_ready, x->stream));
   }
-  for (size_t si = 0; si < sp.steps.size(); ++si) {
-    const StagedStep& st = sp.steps[si];
-    if (st.ordered_layer >= 0) continue;
-    const uint64_t slot = slot_base(slice_of[si]);
-    for_each_step_chunk(plans, sp, st, [&](const Chunk& c, size_t k) {
-      const uint64_t at = slot + k * st.chunk_bytes;
-      hd[st.desc_first + k] = is_save ? ChunkDesc{c.dev, at} : ChunkDesc{at, c.dev};
-    });
-  }
-  if (hd == x->h_small) {
-    x->desc_base = x->h_small;
-    x->small_inflight = true;
-  } else if (int rc = upload_desc(x, sp.n_desc)) {
-    return rc;
-  }
+  // Descriptors of the steps not written yet, then uploaded (launches index
+  // them from the start of the device copy).
+  size_t written = 0, uploaded = 0;
+  auto publish = [&]() -> int {
+    for (size_t si = written; si < sp.steps.size(); ++si) {
+      const StagedStep& st = sp.steps[si];
+      if (st.ordered_layer >= 0) continue;
+      const uint64_t slot = slot_base(slice_of[si]);
+      for_each_step_chunk(plans, sp, st, [&](const Chunk& c, size_t k) {
+        const uint64_t at = slot + k * st.chunk_bytes;
+        hd[st.desc_first + k] = is_save ? ChunkDesc{c.dev, at} : ChunkDesc{at, c.dev};
+      });
+    }
+    written = sp.steps.size();
+    if (hd == x->h_small) {
+      x->desc_base = x->h_small;
+      x->small_inflight = true;
+      return PF_OK;
+    }
+    if (sp.n_desc > uploaded) {
+      if (int rc = upload_desc(x, sp.n_desc - uploaded, uploaded)) return rc;
+      uploaded = sp.n_desc;
+    }
+    x->desc_base = x->d_desc;
+    return PF_OK;
+  };
+  if (int rc = publish()) return rc;
+  tr.mark("desc", sp.n_desc);
+  PinnedCache pinned;
   // The host-contiguous runs of a slice, each one engine copy.
   auto queue_copies = [&](size_t si) -> int {
     const StagedStep& st = sp.steps[si];
@@ -974,12 +1102,25 @@ int staged_engine(pf_xfer* x, const std::vector<LayerPlan>& plans, StagedPlan& s
     int rc = PF_OK;
     auto flush = [&]() {
       if (run_bytes == 0 || rc != PF_OK) return;
-      engine_signal_add(es, 1);
-      rc = is_save ? engine_copy(x->device, true, run_host, run_at, run_bytes, es,
-                                 static_cast<unsigned>(j))
-                   : engine_copy(x->device, false, run_at, run_host, run_bytes, es,
-                                 static_cast<unsigned>(j));
       x->last_dma++;
+      if (pinned.covers(run_host, run_bytes)) {
+        engine_signal_add(es, 1);
+        rc = is_save ? engine_copy(x->device, true, run_host, run_at, run_bytes, es,
+                                   static_cast<unsigned>(j))
+                     : engine_copy(x->device, false, run_at, run_host, run_bytes, es,
+                                   static_cast<unsigned>(j));
+        return;
+      }
+      hipError_t e =
+          is_save ? hipMemcpyAsync(reinterpret_cast<void*>(run_host),
+                                   reinterpret_cast<void*>(run_at), run_bytes, hipMemcpyDefault,
+                                   x->dma)
+                  : hipMemcpyAsync(reinterpret_cast<void*>(run_at),
+                                   reinterpret_cast<void*>(run_host), run_bytes, hipMemcpyDefault,
+                                   x->dma);
+      if (e == hipSuccess) e = hipStreamSynchronize(x->dma);
+      if (e != hipSuccess)
+        rc = hip_fail(e, is_save ? "staged hipMemcpyAsync (D2H)" : "staged hipMemcpyAsync (H2D)");
     };
     for_each_step_chunk(plans, sp, st, [&](const Chunk& c, size_t k) {
       if (run_bytes > 0 && c.host == run_host + run_bytes) {
@@ -992,6 +1133,7 @@ int staged_engine(pf_xfer* x, const std::vector<LayerPlan>& plans, StagedPlan& s
       run_bytes = cb;
     });
     flush();
+    tr.mark("q", j);
     return rc;
   };
   auto kernel = [&](size_t si) -> int {
@@ -1026,6 +1168,26 @@ int staged_engine(pf_xfer* x, const std::vector<LayerPlan>& plans, StagedPlan& s
     if (wait_save) return engine_drain(x);
     return PF_OK;
   }
+  // The first slots' copies; a pipelined load's other layers meanwhile.
+  size_t queued = 0;
+  auto queue_free_slots = [&]() -> int {
+    for (; queued < slice_steps.size() && queued < n_slots; ++queued)
+      if (int rc = queue_copies(slice_steps[queued])) return rc;
+    return PF_OK;
+  };
+  if (int rc = queue_free_slots()) return rc;
+  if (piped) {
+    if (pending)
+      if (int rc = pending->ready()) return rc;
+    if (int rc = plan_range(layers, head, num_layers, false, &plans)) return rc;
+    if (int rc = check_devices(layers, plans, head, num_layers)) return rc;
+    if (int rc = planner.add(plans, head, num_layers)) return rc;
+    if (int rc = planner.cut()) return rc;
+    index();
+    if (int rc = publish()) return rc;
+    tr.mark("rest", sp.n_desc);
+    if (int rc = queue_free_slots()) return rc;
+  }
   size_t next_layer = 0;
   auto complete = [&](int64_t step) -> int {
     std::vector<uint32_t> ids;
@@ -1037,16 +1199,11 @@ int staged_engine(pf_xfer* x, const std::vector<LayerPlan>& plans, StagedPlan& s
         PF_HIP(hipEventRecord(static_cast<hipEvent_t>(layer_events[li]), x->stream));
     if (sig)
       if (int rc = mark_layers(x, ids, *sig)) return rc;
+    tr.mark("L", ids.back());
     return PF_OK;
   };
   if (int rc = complete(-1)) return rc;
-  // The first slots' copies, then each slot refilled after its scatter.
-  std::vector<size_t> slice_steps;
-  for (size_t si = 0; si < sp.steps.size(); ++si)
-    if (slice_of[si] != SIZE_MAX) slice_steps.push_back(si);
-  size_t queued = 0;
-  for (; queued < slice_steps.size() && queued < n_slots; ++queued)
-    if (int rc = queue_copies(slice_steps[queued])) return rc;
+  // Each slot refilled after its scatter.
   for (size_t si = 0; si < sp.steps.size(); ++si) {
     const StagedStep& st = sp.steps[si];
     if (st.ordered_layer >= 0) {
@@ -1055,6 +1212,7 @@ int staged_engine(pf_xfer* x, const std::vector<LayerPlan>& plans, StagedPlan& s
     } else {
       const size_t s = slice_of[si] % n_slots;
       if (int rc = engine_signal_wait(&x->eng_sig[s])) return rc;
+      tr.mark("c", slice_of[si]);
       if (int rc = kernel(si)) return rc;
       if (queued < slice_steps.size()) {
         if (int rc = kernels_done(s)) return rc;
@@ -1066,25 +1224,45 @@ int staged_engine(pf_xfer* x, const std::vector<LayerPlan>& plans, StagedPlan& s
   return PF_OK;
 }
 
-int staged(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<LayerPlan>& plans,
-           bool is_save, pf_event* layer_events, const SignalTargets* sig, bool wait_save) {
+uint32_t pipeline_head(const pf_layer_xfer* layers, uint32_t num_layers);
+
+// A staged call.  `pending`: layers from pending->head on are listed once
+// pending->ready() returns.
+int staged(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, bool is_save,
+           pf_event* layer_events, const SignalTargets* sig, bool wait_save,
+           const PendingLayers* pending) {
   if (x->staging == 0 || x->slot_bytes == 0)
     return fail(PF_ERR_INVALID_ARGUMENT, "transfer context has no staging buffer");
-  StagedPlan sp;
-  if (int rc = plan_staged(x, plans, is_save, &sp)) return rc;
-  {
-    RangeCache rc;
-    for (size_t i = 0; i < plans.size(); ++i)
-      if (!plans[i].chunks.empty() && !plans[i].ordered)
-        if (int r = check_device_tensor(rc, layers[i].layout)) return r;
+  StagedTrace tr;
+  std::vector<LayerPlan>& plans = x->plans;
+  plans.resize(num_layers);
+  // Layers planned before the first copies: all, or a pipelined load's
+  // first layer (the layers listed so far, when the rest are pending).
+  uint32_t head = pending ? pending->head : num_layers;
+  if (!pending && !is_save && x->engine_ok && pipeline_head(layers, num_layers) > 0) head = 1;
+  if (int rc = plan_range(layers, 0, head, is_save, &plans)) return rc;
+  const bool engines = x->engine_ok && hosts_pinned(plans, 0, head);
+  if (head < num_layers && !engines) {
+    if (pending)
+      if (int rc = pending->ready()) return rc;
+    if (int rc = plan_range(layers, head, num_layers, is_save, &plans)) return rc;
+    head = num_layers;
   }
+  StagedPlan sp;
+  StagedPlanner planner(x, is_save, num_layers, &sp);
+  if (int rc = planner.add(plans, 0, head)) return rc;
+  if (int rc = planner.cut()) return rc;
+  if (int rc = check_devices(layers, plans, 0, head)) return rc;
   // Nothing of an earlier staged call may still use the slots.
   if (int rc = engine_drain(x)) return rc;
-  if (x->engine_ok && hosts_pinned(plans)) {
-    if (int rc = ensure_counters(x, plans.size())) return rc;  // queued device routes
+  if (engines) {
+    if (int rc = ensure_counters(x, num_layers)) return rc;  // queued device routes
     PF_HIP(hipEventSynchronize(x->staging_free));
-    const int rc = staged_engine(x, plans, sp, is_save, layer_events, sig, wait_save);
+    tr.mark("start", sp.steps.size());
+    const int rc = staged_engine(x, layers, num_layers, plans, planner, sp, head, pending,
+                                 is_save, layer_events, sig, wait_save, tr);
     PF_HIP(hipEventRecord(x->staging_free, x->stream));
+    tr.print(is_save);
     return rc;
   }
   // One lane when the kernel launches run queued (they share one tile
@@ -1117,21 +1295,21 @@ int staged(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<LayerPlan>
   } else if (int rc = upload_desc(x, sp.n_desc)) {
     return rc;
   }
-  // pending[l]: lane l has work the other lane has not waited for.
-  bool pending[2] = {false, false};
+  // lane_open[l]: lane l has work the other lane has not waited for.
+  bool lane_open[2] = {false, false};
   auto join = [&](int to, int from) -> int {
-    if (!pending[from]) return PF_OK;
+    if (!lane_open[from]) return PF_OK;
     PF_HIP(hipEventRecord(x->lane_mark[from], lane_s[from]));
     PF_HIP(hipStreamWaitEvent(lane_s[to], x->lane_mark[from], 0));
-    pending[from] = false;
+    lane_open[from] = false;
     return PF_OK;
   };
   // Lane 1 starts after the descriptors are uploaded and after everything
   // earlier calls left on the context's stream.
-  pending[0] = true;
+  lane_open[0] = true;
   if (lanes == 2)
     if (int rc = join(1, 0)) return rc;
-  pending[0] = false;
+  lane_open[0] = false;
   // Load completion of the layers done after step s (s = -1: before any), on
   // lane `to`: once every step so far is done, then in layer order.
   size_t next_layer = 0;
@@ -1148,7 +1326,7 @@ int staged(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<LayerPlan>
     if (sig)
       if (int rc = mark_layers(x, ids, *sig, lane_s[to])) return rc;
     // A later layer's completion on the other lane comes after these.
-    pending[to] = true;
+    lane_open[to] = true;
     return PF_OK;
   };
   if (int rc = complete(-1, 0)) return rc;
@@ -1161,7 +1339,7 @@ int staged(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<LayerPlan>
       if (int rc = join(0, 1)) return rc;
       if (int rc = dma_layer(x, plans[static_cast<size_t>(st.ordered_layer)], is_save, false))
         return rc;
-      pending[0] = true;
+      lane_open[0] = true;
       if (lanes == 2)
         if (int rc = join(1, 0)) return rc;
     } else {
@@ -1211,7 +1389,7 @@ int staged(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<LayerPlan>
                             lane_s[L]))
           return rc;
       }
-      pending[L] = true;
+      lane_open[L] = true;
     }
     if (int rc = complete(static_cast<int64_t>(si), L)) return rc;
   }
@@ -1541,6 +1719,8 @@ int run_locked(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, uin
                               is_save ? nullptr : sig, is_save ? nullptr : layer_events,
                               pending);
   }
+  if (mode == PF_MODE_STAGED)
+    return staged(x, layers, num_layers, is_save, layer_events, sig, wait_save, pending);
   if (pending)
     if (int rc = pending->ready()) return rc;
   if (int rc = plan_all(layers, num_layers, is_save, &plans)) return rc;
@@ -1563,10 +1743,6 @@ int run_locked(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, uin
         apply_write_policy(layers[li], is_save, false, &plans[li]);
       return kernel_direct(x, layers, plans, is_save, layer_events, is_save ? nullptr : sig,
                            wait_save);
-    case PF_MODE_STAGED:
-      for (uint32_t li = 0; li < num_layers; ++li)
-        apply_write_policy(layers[li], is_save, true, &plans[li]);
-      return staged(x, layers, plans, is_save, layer_events, sig, wait_save);
     default:
       return fail(PF_ERR_INVALID_ARGUMENT, strf("unknown transfer mode %u", mode));
   }

@@ -88,10 +88,12 @@ def engine(gpu):
     e.close()
 
 
-@pytest.mark.parametrize("load_mode", ["kernel", "dma_batched", "dma_reference"])
-def test_save_then_load_by_hash(engine, load_mode):
-    say(f"[gpu] engine save/load by hash load_mode={load_mode}")
-    engine.set_transfer_modes(_lib.MODE_KERNEL, _lib.MODE_NAMES[load_mode])
+@pytest.mark.parametrize("save_mode,load_mode", [
+    ("kernel", "kernel"), ("kernel", "dma_batched"), ("kernel", "dma_reference"),
+    ("staged", "staged"), ("auto", "auto")])
+def test_save_then_load_by_hash(engine, save_mode, load_mode):
+    say(f"[gpu] engine save/load by hash save_mode={save_mode} load_mode={load_mode}")
+    engine.set_transfer_modes(_lib.MODE_NAMES[save_mode], _lib.MODE_NAMES[load_mode])
     m = Model(engine, "inst", 6, 64, 4096)
     orig = m.host_copies()
     ids = [5, 17, 3, 60, 41, 8]
@@ -445,16 +447,19 @@ def test_local_layer_events_gate_consumer_per_layer(engine):
         m.close()
 
 
+@pytest.mark.parametrize("mode", ["kernel", "staged"])
 @pytest.mark.parametrize("completion", ["plain", "layered", "events"])
-def test_split_load_matches_oracle(engine, completion):
+def test_split_load_matches_oracle(engine, completion, mode):
     """A load of 8 layers x 1024 split blocks (16384 chunks) is split: the
     lists of its first two layers are submitted while the others are built,
     and the transfer issues them once they are published.  Bytes against the
-    oracle for each way the load thread publishes completion."""
+    oracle for each way the load thread publishes completion, by the kernel
+    and staged (a load with per-layer events runs the kernel mode either
+    way)."""
     from pegaflow_amd.runtime import Event, Stream
 
-    say(f"[gpu] engine split load ({completion})")
-    engine.set_transfer_modes(_lib.MODE_KERNEL, _lib.MODE_KERNEL)
+    say(f"[gpu] engine split load ({completion}, {mode})")
+    engine.set_transfer_modes(_lib.MODE_KERNEL, _lib.MODE_NAMES[mode])
     m = Model(engine, "split", 8, 2100, 1024, seed=41)
     evs = [Event() for _ in range(m.n_layers)] if completion == "events" else None
     stream = Stream() if completion == "events" else None
@@ -490,14 +495,15 @@ def test_split_load_matches_oracle(engine, completion):
         m.close()
 
 
-def test_split_load_error_in_later_layers(engine):
+@pytest.mark.parametrize("mode", ["kernel", "staged"])
+def test_split_load_error_in_later_layers(engine, mode):
     """A split load whose later layer is registered with another block size
     than the stored blocks hold: the call fails with the size message after
     the first layer was submitted, the LoadState reads failed, the later
     layers' destinations are untouched and the load thread serves the next
     load (the first layer may have been copied already)."""
-    say("[gpu] engine split load: error in a later layer")
-    engine.set_transfer_modes(_lib.MODE_KERNEL, _lib.MODE_KERNEL)
+    say(f"[gpu] engine split load: error in a later layer ({mode})")
+    engine.set_transfer_modes(_lib.MODE_KERNEL, _lib.MODE_NAMES[mode])
     a = Model(engine, "splita", 8, 2100, 2048, seed=43)
     b = odd = None
     try:

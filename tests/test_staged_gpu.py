@@ -157,6 +157,74 @@ def test_staged_slices_across_layers_vs_oracle(gpu, slices, pinned):
         ctx.close()
 
 
+def test_staged_pipelined_load_vs_oracle(gpu):
+    """A staged load large enough to be pipelined (9 layers, 19,606 chunks):
+    its first layer is sliced and its copies queued before the other layers
+    are planned.  After the first layer come an empty layer, a layer copied
+    in place in list order, and a layer whose host region is ordinary
+    (pageable) memory, copied through HIP run by run; slices start small and
+    grow.  Bytes against the oracle, per-layer events in layer order, and
+    every layer's mark set by a second, marked load."""
+    say("[gpu] staged pipelined load, mixed later layers")
+    ctx = TransferContext(0, staging_bytes=64 * 1024)
+    nb, bpb = 2048, 256
+    kv = nb * bpb
+    rng = np.random.Generator(np.random.PCG64(31))
+    specs = []  # (layer shape, save ids, load ids, host region pageable)
+    for i in range(9):
+        if i == 3:
+            specs.append(((nb, bpb, 2, kv, 2 * kv), [], [], False))
+        elif i == 5:
+            specs.append(((10, 64, 2, 160, 160 + 640), [1, 2, 3], [4, 3, 2], False))
+        else:
+            specs.append(((nb, bpb, 2, kv, 2 * kv), rng.permutation(nb)[:1400].tolist(),
+                          rng.permutation(nb)[:1400].tolist(), i == 7))
+    layers = [Layer(*shape, 200 + i) for i, (shape, _, _, _) in enumerate(specs)]
+    regions = [2 * max(len(save), 1) * L.bpb for L, (_, save, _, _) in zip(layers, specs)]
+    pinned = PinnedBuffer(sum(regions))
+    opinned = np.zeros(pinned.nbytes, np.uint8)
+    pageable = PageableBuffer(regions[7])
+    opage = np.zeros(pageable.nbytes, np.uint8)
+    words = PinnedBuffer(8 * len(layers))
+    off = 0
+    for L, (_, save, _, paged), r in zip(layers, specs, regions):
+        if paged:
+            L.place(save, pageable, opage, 0)
+        else:
+            L.place(save, pinned, opinned, off)
+            off += r
+    loads = lambda: [L.transfer(ids) for L, (_, _, ids, _) in zip(layers, specs)]  # noqa: E731
+    try:
+        pinned.array[:] = 0
+        ctx.save_layers([L.transfer(save) for L, (_, save, _, _) in zip(layers, specs)],
+                        _lib.MODE_STAGED)
+        for L in layers:
+            L.oracle_save()
+        assert np.array_equal(pinned.array, opinned), "pinned host regions differ"
+        assert np.array_equal(pageable.array, opage), "pageable host region differs"
+        evs = [Event() for _ in layers]
+        ctx.load_layers(loads(), _lib.MODE_STAGED, layer_events=evs)
+        ctx.synchronize()
+        for i in range(1, len(evs)):
+            assert evs[i - 1].elapsed_ms(evs[i]) >= 0.0, f"layer {i} completed before {i - 1}"
+        for i, (L, (_, _, ids, _)) in enumerate(zip(layers, specs)):
+            L.oracle_load(ids)
+            assert np.array_equal(L.dev.download(), L.ref), f"layer {i} differs from the oracle"
+        words.array[:] = 0
+        ctx.load_layers_marked(loads(), [(words.ptr, 9, True)], _lib.MODE_STAGED)
+        ctx.synchronize()
+        assert words.array.view(np.uint64).tolist() == [9] * len(layers)
+        for L in layers:
+            assert np.array_equal(L.dev.download(), L.ref)
+    finally:
+        for L in layers:
+            L.close()
+        pinned.close()
+        pageable.close()
+        words.close()
+        ctx.close()
+
+
 def test_staged_save_overlapping_hosts_keeps_list_order(gpu):
     """Host destinations that overlap across layers (layer 1's region starts
     inside layer 0's V region): the staged save copies in list order, as the
