@@ -82,7 +82,7 @@ def parse():
     ap.add_argument("--quick", action="store_true",
                     help="skip the config 3/4/5 legs (layer-wise, fragmentation, MLA) and "
                          "the disk-tier leg")
-    ap.add_argument("--profile", choices=["gather", "scatter", "zerocopy"],
+    ap.add_argument("--profile", choices=["gather", "scatter", "scatter_sets", "zerocopy"],
                     help="only run the calibration copy and one kernel's launches (PMC passes)")
     ap.add_argument("--profile-gather", action="store_const", const="gather", dest="profile",
                     help="same as --profile gather")
@@ -1158,6 +1158,11 @@ def profile_kernels(kind, seed):
                 bytes per launch);
       scatter:  the packed HBM buffer -> 640 other blocks of the paged
                 tensors (2P);
+      scatter_sets: two sets of the 32 layer tensors (42 GB each), A and B:
+                gathers from A, A, B, B, then scatters into A, B, A, B in
+                round-robin order (512 threads, 1 load per lane) and
+                A, B, A, B in XCD-major order (2 loads per lane), then one
+                more into A, which is checked;
       zerocopy: the prefix saved to pinned host memory, then restored from
                 it (P over the host link per call; each call is two
                 launches, its first eighth of layers, then the rest).
@@ -1200,6 +1205,31 @@ def profile_kernels(kind, seed):
                      f"{kind}_workgroups": 40960 * (4 if kind == "gather" else 2),
                      "bit_exact": ok})
         gbuf.close()
+    elif kind == "scatter_sets":
+        other = wl.DeviceLayers(wl.LLAMA3_8B, base_seed=seed + 1)
+        gbuf = DeviceBuffer(P)
+        gather = wl.save_plan(layers.regs, ids, gbuf.ptr)
+        xfer.save_layers(gather, _lib.MODE_KERNEL)
+        gather_b = wl.save_plan(other.regs, ids, gbuf.ptr)
+        for plan in (gather, gather, gather_b, gather_b):
+            xfer.save_layers(plan, _lib.MODE_KERNEL)
+        xfer.save_layers(gather, _lib.MODE_KERNEL)  # the packed buffer holds set A's blocks
+        # Set B receives set A's packed bytes: its targets are not checked.
+        into = [wl.load_plan(gather, targets), wl.load_plan(gather_b, targets)]
+        nt = _lib.KERNEL_NONTEMPORAL
+        for shape in ((512, 1 | nt), (512, 2 | nt | _lib.KERNEL_XCD_MAJOR)):
+            xfer.set_kernel_shape_dir(_lib.ROUTE_LOAD_DEVICE, *shape)
+            for r in range(4):
+                xfer.load_layers(into[r % 2], _lib.MODE_KERNEL)
+                xfer.synchronize()
+        xfer.load_layers(into[0], _lib.MODE_KERNEL)
+        xfer.synchronize()
+        info.update({"scatter_algorithmic_bytes": 2 * P,
+                     "order": "gather A, A, B, B, A; scatter round-robin A, B, A, B; "
+                              "XCD-major A, B, A, B; A",
+                     "bit_exact": wl.verify_restored(layers, ids, targets) == 0})
+        gbuf.close()
+        other.close()
     else:
         pool = PinnedBuffer(P)
         saved = wl.save_plan(layers.regs, ids, pool.ptr)
