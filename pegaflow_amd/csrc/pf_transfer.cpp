@@ -741,7 +741,10 @@ int dma_layer(pf_xfer* x, const LayerPlan& p, bool is_save, bool per_chunk_sync)
 //
 // A call's chunks are cut, in layer order, into slices of at most the
 // direction's slice size; a slice may span layers, but not an ordered layer
-// (copied in place, in list order) or a change of chunk size.  Consecutive
+// (copied in place, in list order) or a change of chunk size, and a load's
+// layer ends its last slice while slices grow and once it is half full
+// (StagedPlanner).  With pinned host memory and known copy engines the
+// slices' copies run on the engines (staged_engine).  Otherwise consecutive
 // slices alternate between the context's two lanes (its two streams), each
 // lane owning one staging slot: a slice's copies and kernel run in order on
 // its lane, so the lane's next slice refills the slot only once the kernel
