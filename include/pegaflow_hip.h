@@ -721,6 +721,39 @@ int pf_engine_serve_request(pf_engine* engine, uint32_t method,
                             const uint8_t* request, uint64_t size);
 
 /* ------------------------------------------------------------------------ */
+/* Native gRPC server for the Engine service (service.rs:133-405, served by  */
+/* the reference from Rust with tonic): engine.proto over HTTP/2 without     */
+/* TLS, as an insecure gRPC channel connects.  Load and Health are served on */
+/* the connection's thread and Save on a worker thread, by the engine's own  */
+/* decoder of the request bytes (pf_engine_serve_request), with engine       */
+/* errors mapped to gRPC codes as service.rs:77-88 does.  The other RPCs go  */
+/* to the caller's handler.                                                  */
+/* ------------------------------------------------------------------------ */
+typedef struct pf_grpc_server pf_grpc_server;
+typedef struct pf_grpc_call pf_grpc_call;
+/* Called on one of the server's threads with the RPC's name within the
+ * service ("RegisterContext", "Query", ...) and its request message bytes;
+ * answers with pf_grpc_reply before returning (a call left unanswered fails
+ * with INTERNAL). */
+typedef void (*pf_grpc_handler)(void* ctx, pf_grpc_call* call, const char* method,
+                                const uint8_t* request, uint64_t size);
+/* Listens on address "host:port" (an IPv6 host in brackets; port 0: a free
+ * port, see pf_grpc_port).  handler may be null: the other RPCs then fail
+ * with UNIMPLEMENTED. */
+int pf_grpc_start(pf_engine* engine, const char* address, pf_grpc_handler handler,
+                  void* ctx, pf_grpc_server** out);
+int pf_grpc_port(const pf_grpc_server* server);
+/* Requests dispatched so far. */
+uint64_t pf_grpc_served(const pf_grpc_server* server);
+/* The answer to a call handed to the handler, once: gRPC status 0 with the
+ * response message bytes, or an error status with its message. */
+int pf_grpc_reply(pf_grpc_call* call, uint32_t status, const char* message,
+                  const uint8_t* response, uint64_t size);
+/* Stops listening, closes every connection and waits for the server's
+ * threads; handler calls already running finish first. */
+int pf_grpc_stop(pf_grpc_server* server);
+
+/* ------------------------------------------------------------------------ */
 /* Disk tier.  Replaces the DFS offload and prefetch of seal_offload.rs and   */
 /* the Redis index behind it (BlockMeta, seal_offload.rs:72-97) with packed   */
 /* files "<root>/<namespace>/<uuid>.bin" plus a "<uuid>.json" sidecar each.   */

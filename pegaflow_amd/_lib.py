@@ -207,6 +207,8 @@ pi32 = ctypes.POINTER(ctypes.c_int)
 pvp = ctypes.POINTER(ctypes.c_void_p)
 pl = ctypes.POINTER(KVLayout)
 cs = ctypes.c_char_p
+# pf_grpc_handler: (ctx, call, method, request bytes, size).
+GRPC_HANDLER = ctypes.CFUNCTYPE(None, vp, vp, cs, ctypes.POINTER(ctypes.c_uint8), u64)
 
 # name -> (restype, argtypes).  Every symbol declared in the header.
 SIGNATURES = {
@@ -322,6 +324,11 @@ SIGNATURES = {
     "pf_fastpath_stop": (i32, [vp]),
     "pf_fastpath_served": (u64, [vp]),
     "pf_engine_serve_request": (i32, [vp, u32, ctypes.c_char_p, u64]),
+    "pf_grpc_start": (i32, [vp, cs, GRPC_HANDLER, vp, pvp]),
+    "pf_grpc_port": (i32, [vp]),
+    "pf_grpc_served": (u64, [vp]),
+    "pf_grpc_reply": (i32, [vp, u32, cs, cs, u64]),
+    "pf_grpc_stop": (i32, [vp]),
     "pf_engine_stats_get": (i32, [vp, ctypes.POINTER(EngineStats)]),
     "pf_engine_wait_idle": (i32, [vp]),
     "pf_engine_enable_disk": (i32, [vp, cs, u64, u32, u32, u32]),

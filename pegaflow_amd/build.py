@@ -29,6 +29,8 @@ SOURCES = [
     "pf_engine.cpp",
     "pf_disk.cpp",
     "pf_fastpath.cpp",
+    "pf_hpack.cpp",
+    "pf_grpc.cpp",
 ]
 
 # Packed-FP32 instructions are disabled for all device code (this library

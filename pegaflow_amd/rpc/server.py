@@ -13,6 +13,7 @@ Run: python -m pegaflow_amd.rpc.server --addr 127.0.0.1:50055 --device 0 --pool-
 from __future__ import annotations
 
 import argparse
+import ctypes
 import logging
 import signal
 import sys
@@ -20,6 +21,7 @@ import threading
 from concurrent import futures
 
 import grpc
+from google.protobuf.message import DecodeError
 
 from .. import _lib
 from ..engine import PegaEngine
@@ -153,14 +155,74 @@ class EngineService:
         return grpc.method_handlers_generic_handler(f"{proto.PACKAGE}.{proto.SERVICE}", methods)
 
 
+class _Abort(Exception):
+    def __init__(self, code: grpc.StatusCode, details: str):
+        super().__init__(details)
+        self.code, self.details = code, details
+
+
+class _CallContext:
+    """What the service's handlers use of a grpc.ServicerContext."""
+
+    def abort(self, code, details):
+        raise _Abort(code, details)
+
+
+class NativeGrpc:
+    """The Engine service on the library's native gRPC server
+    (pf_grpc_start): Load, Save and Health are served by the engine on the
+    server's own threads; the other RPCs reach ``service`` through a
+    callback, with the same results, codes and messages as on grpcio."""
+
+    def __init__(self, engine: PegaEngine, service: EngineService, addr: str):
+        self._methods = {rpc: (getattr(service, rpc), proto.messages[req])
+                         for rpc, req, _ in proto.METHODS}
+        self._lib = _lib.load()
+        self._cb = _lib.GRPC_HANDLER(self._handle)  # kept alive with the server
+        h = ctypes.c_void_p()
+        rc = self._lib.pf_grpc_start(engine._h, addr.encode(), self._cb, None, ctypes.byref(h))
+        if rc != _lib.PF_OK:
+            raise RuntimeError(f"failed to bind {addr}: {_lib.last_error()}")
+        self._h = h.value
+        self.port = int(self._lib.pf_grpc_port(self._h))
+
+    def _handle(self, _ctx, call, method, request, size):
+        # Nothing may escape a ctypes callback: every outcome is a reply.
+        out, status, msg = b"", 0, None
+        try:
+            fn, req_cls = self._methods[method.decode()]
+            req = req_cls.FromString(ctypes.string_at(request, size) if size else b"")
+            out = fn(req, _CallContext()).SerializeToString()
+        except KeyError:
+            status, msg = grpc.StatusCode.UNIMPLEMENTED.value[0], "Method not found!"
+        except DecodeError:
+            status, msg = grpc.StatusCode.INTERNAL.value[0], "Exception deserializing request!"
+        except _Abort as a:
+            status, msg = a.code.value[0], a.details
+        except Exception as e:  # noqa: BLE001 - reported to the caller as INTERNAL
+            status, msg = grpc.StatusCode.INTERNAL.value[0], str(e) or type(e).__name__
+        self._lib.pf_grpc_reply(call, status, msg.encode() if msg else None, out, len(out))
+
+    def served(self) -> int:
+        return int(self._lib.pf_grpc_served(self._h)) if self._h else 0
+
+    def stop(self) -> None:
+        if self._h:
+            self._lib.pf_grpc_stop(self._h)
+        self._h = None
+
+
 class Server:
-    """A running engine server (engine + registry + gRPC endpoint)."""
+    """A running engine server (engine + registry + gRPC endpoint).
+
+    grpc_impl "native" (the default) serves gRPC from the library's own
+    HTTP/2 server (NativeGrpc); "python" from grpcio's server."""
 
     def __init__(self, addr: str = "127.0.0.1:50055", engine: PegaEngine | None = None,
                  pool_size: int = 30 << 30, host_pool: bool = False, unit_size_hint: int = 0,
                  max_workers: int = 16, dfs_root: str | None = None,
                  dfs_quota: int = 50 << 30, dfs_io_threads: int = 4,
-                 fast_socket: str | None = None):
+                 fast_socket: str | None = None, grpc_impl: str = "native"):
         self.engine = engine or PegaEngine(pool_size=pool_size, host_pool=host_pool,
                                            unit_size_hint=unit_size_hint)
         if dfs_root:
@@ -170,18 +232,27 @@ class Server:
         if fast_socket:
             self.engine.start_fast_path(fast_socket)
         self.service = EngineService(self.engine, disk=bool(dfs_root))
-        self.grpc = grpc.server(futures.ThreadPoolExecutor(max_workers=max_workers),
-                                options=[("grpc.max_receive_message_length", 256 << 20),
-                                         ("grpc.max_send_message_length", 256 << 20)])
-        self.grpc.add_generic_rpc_handlers((self.service.handler(),))
-        self.port = self.grpc.add_insecure_port(addr)
-        if self.port == 0:
-            raise RuntimeError(f"failed to bind {addr}")
+        self.grpc = self.native = None
+        if grpc_impl == "native":
+            self.native = NativeGrpc(self.engine, self.service, addr)
+            self.port = self.native.port
+        elif grpc_impl == "python":
+            self.grpc = grpc.server(futures.ThreadPoolExecutor(max_workers=max_workers),
+                                    options=[("grpc.max_receive_message_length", 256 << 20),
+                                             ("grpc.max_send_message_length", 256 << 20)])
+            self.grpc.add_generic_rpc_handlers((self.service.handler(),))
+            self.port = self.grpc.add_insecure_port(addr)
+            if self.port == 0:
+                raise RuntimeError(f"failed to bind {addr}")
+        else:
+            raise ValueError(f"unknown gRPC implementation {grpc_impl!r}")
+        self.grpc_impl = grpc_impl
         self.addr = addr.rsplit(":", 1)[0] + f":{self.port}"
 
     def start(self) -> "Server":
-        self.grpc.start()
-        log.info("pegaflow engine server listening on %s", self.addr)
+        if self.grpc is not None:
+            self.grpc.start()
+        log.info("pegaflow engine server listening on %s (%s gRPC)", self.addr, self.grpc_impl)
         return self
 
     def wait(self, poll_s: float = 0.2) -> None:
@@ -190,7 +261,10 @@ class Server:
 
     def stop(self, grace: float = 1.0) -> None:
         self.engine.stop_fast_path()
-        self.grpc.stop(grace).wait()
+        if self.native is not None:
+            self.native.stop()
+        if self.grpc is not None:
+            self.grpc.stop(grace).wait()
         self.service.frontend.close()
         self.engine.close()
 
@@ -212,7 +286,11 @@ def parse_args(argv=None):
     ap.add_argument("--hint-value-size", type=parse_memory_size, default=0,
                     help="allocation unit of the pinned pool")
     ap.add_argument("--log-level", default="info")
-    ap.add_argument("--max-workers", type=int, default=16)
+    ap.add_argument("--max-workers", type=int, default=16,
+                    help="worker threads of the python gRPC server")
+    ap.add_argument("--grpc-impl", choices=("native", "python"), default="native",
+                    help="serve gRPC from the library's native HTTP/2 server (default) or "
+                         "from grpcio's")
     ap.add_argument("--fast-socket", default=None,
                     help="also serve Load, Save and Health natively on this Unix-domain "
                          "socket path (EngineRpcClient(fast_socket=...))")
@@ -264,7 +342,7 @@ def main(argv=None) -> int:
     server = Server(args.addr, pool_size=args.pool_size, unit_size_hint=args.hint_value_size,
                     max_workers=args.max_workers, dfs_root=args.dfs_root,
                     dfs_quota=args.dfs_quota, dfs_io_threads=args.dfs_io_threads,
-                    fast_socket=args.fast_socket).start()
+                    fast_socket=args.fast_socket, grpc_impl=args.grpc_impl).start()
     for sig in (signal.SIGINT, signal.SIGTERM):
         signal.signal(sig, lambda *_: server.service.shutdown_event.set())
     print(f"READY {server.addr}", flush=True)

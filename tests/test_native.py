@@ -22,7 +22,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CSRC = os.path.join(ROOT, "pegaflow_amd", "csrc")
 LIB_SOURCES = [os.path.join(CSRC, f) for f in (
     "pf_layout.cpp", "pf_runtime.cpp", "pf_kernels.hip", "pf_transfer.cpp", "pf_load_state.cpp",
-    "pf_engine.cpp", "pf_disk.cpp", "pf_fastpath.cpp")]
+    "pf_engine.cpp", "pf_disk.cpp", "pf_fastpath.cpp", "pf_hpack.cpp", "pf_grpc.cpp")]
 NATIVE = os.path.join(ROOT, "tests", "native")
 # C++ sources that define device variables.
 DEVICE_CPP = {"pf_runtime.cpp"}
@@ -90,6 +90,20 @@ def test_block_store_sealing_rules():
     calls, blocks completed across calls (first copies win), sealed blocks
     not replaced, a key named twice, and a slot count mismatch."""
     exe = build("asan", "blockstore_test")
+    env = dict(os.environ, **VARIANTS["asan"][1])
+    r = subprocess.run([exe], env=env, timeout=120, stdout=subprocess.PIPE,
+                       stderr=subprocess.STDOUT, text=True)
+    assert r.returncode == 0, r.stdout[-6000:]
+    assert r.stdout.strip().endswith("ok")
+
+
+@pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc is not installed")
+def test_hpack_decoder_rfc7541_examples():
+    """tests/native/hpack_test.cpp under AddressSanitizer+UBSan: the native
+    gRPC server's HPACK decoder against RFC 7541 Appendix C (integers, three
+    requests with and without Huffman coding through one dynamic table) and
+    malformed blocks."""
+    exe = build("asan", "hpack_test")
     env = dict(os.environ, **VARIANTS["asan"][1])
     r = subprocess.run([exe], env=env, timeout=120, stdout=subprocess.PIPE,
                        stderr=subprocess.STDOUT, text=True)

@@ -193,9 +193,10 @@ def test_reregistration_keeps_the_mapping_the_engine_uses(monkeypatch):
 # ---------------------------------------------------------------------------
 # A live server over a plain host pool.
 # ---------------------------------------------------------------------------
-@pytest.fixture
-def served():
-    srv = Server("127.0.0.1:0", engine=PegaEngine(pool_size=64 << 20, host_pool=True)).start()
+@pytest.fixture(params=["native", "python"])
+def served(request):
+    srv = Server("127.0.0.1:0", engine=PegaEngine(pool_size=64 << 20, host_pool=True),
+                 grpc_impl=request.param).start()
     client = EngineRpcClient(f"http://{srv.addr}")
     yield srv, client
     client.close()
@@ -440,11 +441,11 @@ def test_engine_decoder_matches_the_full_parse(served_fast):
 # ---------------------------------------------------------------------------
 # The native endpoint for Load, Save and Health (pf_fastpath_start).
 # ---------------------------------------------------------------------------
-@pytest.fixture
-def served_fast(tmp_path):
+@pytest.fixture(params=["native", "python"])
+def served_fast(tmp_path, request):
     path = str(tmp_path / "pf.sock")
     srv = Server("127.0.0.1:0", engine=PegaEngine(pool_size=64 << 20, host_pool=True),
-                 fast_socket=path).start()
+                 fast_socket=path, grpc_impl=request.param).start()
     slow = EngineRpcClient(f"http://{srv.addr}")
     fast = EngineRpcClient(f"http://{srv.addr}", fast_socket=path)
     yield srv, slow, fast, path
