@@ -378,7 +378,7 @@ int pf_xfer_set_max_grid(pf_xfer* xfer, uint32_t max_workgroups);
 int pf_copy_engines(int device, uint32_t* d2h_engine, uint32_t* h2d_engine);
 /* Largest staged slice per direction, in bytes (0 keeps the current value);
  * slices are further capped by the staging slot.  A load's slices start at
- * an eighth of its largest slice (at most 8 MiB) and double, each of the
+ * a quarter of its largest slice (at most 16 MiB) and double, each of the
  * first layers ending its last slice meanwhile, so the first layers land
  * early; each copy-engine command costs about 10 us besides its bytes, which
  * 64 MiB slices amortize to 1%. */

@@ -143,9 +143,11 @@ void engine_signal_add(EngineSignal* s, int64_t n);
 // one when the copy is done; on failure it is dropped here.
 int engine_copy(int device, bool d2h, uint64_t dst, uint64_t src, uint64_t bytes,
                 EngineSignal* s, unsigned lane);
-// Waits until the signal reads 0 (an error after kEngineWaitSeconds).
+// Waits until the signal reads 0 (an error after kEngineWaitSeconds):
+// asleep until the copy's completion interrupt, or, with spin, polling the
+// signal (about 25 us sooner, for a core kept busy meanwhile).
 constexpr int kEngineWaitSeconds = 60;
-int engine_signal_wait(EngineSignal* s);
+int engine_signal_wait(EngineSignal* s, bool spin = false);
 
 // Address validation for kernel access.  A kernel that touches an unmapped
 // address faults the GPU, so every range a kernel will touch is checked

@@ -347,8 +347,18 @@ int engine_copy(int device, bool d2h, uint64_t dst, uint64_t src, uint64_t bytes
   return PF_OK;
 }
 
-int engine_signal_wait(EngineSignal* s) {
+int engine_signal_wait(EngineSignal* s, bool spin) {
   const hsa_signal_t h = sig_of(s);
+  if (spin) {
+    const auto t0 = std::chrono::steady_clock::now();
+    for (uint32_t i = 1; hsa_signal_load_scacquire(h) != 0; ++i) {
+      if ((i & 1023) == 0 &&
+          std::chrono::steady_clock::now() - t0 > std::chrono::seconds(kEngineWaitSeconds))
+        return fail(PF_ERR_HIP,
+                    strf("copy engine copies not done after %d s", kEngineWaitSeconds));
+    }
+    return PF_OK;
+  }
   // Each wait is bounded to about 0.1 s (in system timestamp ticks) so the
   // deadline below is checked.
   static const uint64_t hint = [] {

@@ -352,6 +352,8 @@ struct pf_xfer {
   EngineSignal eng_sig[kEngineSlots];
   hipEvent_t eng_ev[kEngineSlots] = {};
   hipEvent_t staging_free = nullptr;
+  // End of a pipelined staged load's first layer, copied by the kernel.
+  hipEvent_t head_done = nullptr;
   // Launch shapes per route (PF_ROUTE_*), the fastest measured on MI355X:
   //   gather into HBM:   512 threads, one non-temporal 16 B load per lane
   //                      (8 KiB tiles), round-robin tile order;
@@ -774,12 +776,13 @@ struct StagedPlan {
   size_t n_desc = 0;
 };
 
-// A load's first slice is an eighth of the load slice size, at most 8 MiB;
+// A load's first slice is a quarter of the load slice size, at most 16 MiB;
 // later slices double up to the load slice size.  Each copy-engine command
-// costs about 10 us besides its bytes (80 x 16 MiB host-to-device copies on
+// costs about 11 us besides its bytes (80 x 16 MiB host-to-device copies on
 // one engine moved 55.5 GB/s, 20 x 64 MiB 57.0), so slices grow to amortize
-// it while the first layer lands early.
-constexpr uint64_t kStagedLoadFirstSlice = 8ull << 20;
+// it while the first layer lands early (the Llama prefix's 40 MiB first
+// layer is two copies, 16 + 24 MiB).
+constexpr uint64_t kStagedLoadFirstSlice = 16ull << 20;
 
 // done_at of a layer not sliced yet.
 constexpr int64_t kNotSliced = INT64_MIN;
@@ -796,7 +799,7 @@ class StagedPlanner {
         slot_bytes_(x->slot_bytes),
         max_cap_(std::min(x->slot_bytes, x->staged_slice[is_save ? 0 : 1])) {
     cap_ = is_save ? max_cap_
-                   : std::max<uint64_t>(1, std::min(kStagedLoadFirstSlice, max_cap_ / 8));
+                   : std::max<uint64_t>(1, std::min(kStagedLoadFirstSlice, max_cap_ / 4));
     sp_->steps.clear();
     sp_->pieces.clear();
     sp_->done_at.assign(num_layers, kNotSliced);
@@ -850,6 +853,9 @@ class StagedPlanner {
     }
     return PF_OK;
   }
+
+  // Descriptors of the slices start at index n (before any slice).
+  void start_descriptors_at(size_t n) { sp_->n_desc = n; }
 
   // Closes the open slice: the steps so far are final.
   int cut() {
@@ -1016,9 +1022,13 @@ struct PinnedCache {
 // listed), plans and slices them and uploads their descriptors while those
 // copies run.  Host runs outside pinned memory are copied through HIP, each
 // waited for before the next is queued.
+int kernel_direct(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<LayerPlan>& plans,
+                  bool is_save, pf_event* layer_events, const SignalTargets* sig,
+                  bool wait_save, size_t desc_off, uint32_t layer_base, size_t* used);
+
 int staged_engine(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
                   std::vector<LayerPlan>& plans, StagedPlanner& planner, StagedPlan& sp,
-                  uint32_t head, const PendingLayers* pending, bool is_save,
+                  uint32_t head, bool kernel_head, const PendingLayers* pending, bool is_save,
                   pf_event* layer_events, const SignalTargets* sig, bool wait_save,
                   StagedTrace& tr) {
   const bool piped = head < num_layers;
@@ -1055,8 +1065,8 @@ int staged_engine(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
     // Room for every descriptor of the call, reserved before the first part
     // is uploaded: growing the buffers later would wait for its copies.
     uint64_t bound = sp.n_desc;
-    if (piped) {
-      bound = 0;
+    if (piped) {  // with the first layer's mark tables, when the kernel copies it
+      bound = 1 + 2 * ((2ull * num_layers + 1) * sizeof(uint32_t) / sizeof(ChunkDesc) + 1);
       for (uint32_t li = 0; li < num_layers; ++li)
         bound += (pending && li >= head ? pending->max_blocks : layers[li].num_blocks) *
                  (layers[li].layout.segments ? layers[li].layout.segments : 1);
@@ -1092,6 +1102,20 @@ int staged_engine(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
     x->desc_base = x->d_desc;
     return PF_OK;
   };
+  if (kernel_head) {
+    // The first layers by the zero-copy kernel (marked, with their events),
+    // the slices' descriptors after the kernel's.
+    std::vector<LayerPlan>& hp = x->plans_rest;
+    hp.resize(head);
+    for (uint32_t li = 0; li < head; ++li) std::swap(hp[li], plans[li]);
+    size_t used = 0;
+    if (int rc = kernel_direct(x, layers, hp, false, layer_events, sig, false, 0, 0, &used))
+      return rc;
+    PF_HIP(hipEventRecord(x->head_done, x->stream));
+    uploaded = std::max<size_t>(used, 1);
+    planner.start_descriptors_at(uploaded);
+    tr.mark("head", used);
+  }
   if (int rc = publish()) return rc;
   tr.mark("desc", sp.n_desc);
   PinnedCache pinned;
@@ -1189,9 +1213,11 @@ int staged_engine(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
     index();
     if (int rc = publish()) return rc;
     tr.mark("rest", sp.n_desc);
+    // The copy engine starts once the kernel is done with the link.
+    if (kernel_head) PF_HIP(hipEventSynchronize(x->head_done));
     if (int rc = queue_free_slots()) return rc;
   }
-  size_t next_layer = 0;
+  size_t next_layer = kernel_head ? head : 0;  // the kernel completes its own layers
   auto complete = [&](int64_t step) -> int {
     std::vector<uint32_t> ids;
     while (next_layer < plans.size() && sp.done_at[next_layer] == step)
@@ -1214,7 +1240,10 @@ int staged_engine(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
         return rc;
     } else {
       const size_t s = slice_of[si] % n_slots;
-      if (int rc = engine_signal_wait(&x->eng_sig[s])) return rc;
+      // The first layer's slices are waited for by polling: the interrupt
+      // wake costs about 25 us, and the first layer gates its consumer.
+      const bool first_layer = !kernel_head && static_cast<int64_t>(si) <= sp.done_at[0];
+      if (int rc = engine_signal_wait(&x->eng_sig[s], first_layer)) return rc;
       tr.mark("c", slice_of[si]);
       if (int rc = kernel(si)) return rc;
       if (queued < slice_steps.size()) {
@@ -1251,10 +1280,22 @@ int staged(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, bool is
     if (int rc = plan_range(layers, head, num_layers, is_save, &plans)) return rc;
     head = num_layers;
   }
+  // A pipelined load whose caller waits layer by layer (marks or per-layer
+  // events) copies its first layer with the zero-copy kernel, which has the
+  // link at full rate from the call's start (the Llama prefix's first layer
+  // in place 0.87 ms after an engine load's call, against 0.97 ms through
+  // the copy engine), and the rest staged once it is done: its 0.74 ms of
+  // shader traffic over the host link is the only part of the load that
+  // slows the device's other kernels.  A load completed as a whole stays
+  // staged throughout.
+  const bool kernel_head = engines && !is_save && head > 0 && head < num_layers &&
+                           (sig != nullptr || layer_events != nullptr);
   StagedPlan sp;
   StagedPlanner planner(x, is_save, num_layers, &sp);
-  if (int rc = planner.add(plans, 0, head)) return rc;
-  if (int rc = planner.cut()) return rc;
+  if (!kernel_head) {
+    if (int rc = planner.add(plans, 0, head)) return rc;
+    if (int rc = planner.cut()) return rc;
+  }
   if (int rc = check_devices(layers, plans, 0, head)) return rc;
   // Nothing of an earlier staged call may still use the slots.
   if (int rc = engine_drain(x)) return rc;
@@ -1262,8 +1303,8 @@ int staged(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, bool is
     if (int rc = ensure_counters(x, num_layers)) return rc;  // queued device routes
     PF_HIP(hipEventSynchronize(x->staging_free));
     tr.mark("start", sp.steps.size());
-    const int rc = staged_engine(x, layers, num_layers, plans, planner, sp, head, pending,
-                                 is_save, layer_events, sig, wait_save, tr);
+    const int rc = staged_engine(x, layers, num_layers, plans, planner, sp, head, kernel_head,
+                                 pending, is_save, layer_events, sig, wait_save, tr);
     PF_HIP(hipEventRecord(x->staging_free, x->stream));
     tr.print(is_save);
     return rc;
@@ -2030,6 +2071,7 @@ int pf_xfer_create(int device, uint64_t staging_bytes, pf_xfer** out) {
   for (int s = 0; s < 2 && e == hipSuccess; ++s)
     e = hipEventCreateWithFlags(&x->lane_mark[s], hipEventDisableTiming);
   if (e == hipSuccess) e = hipEventCreateWithFlags(&x->staging_free, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&x->head_done, hipEventDisableTiming);
   if (e == hipSuccess) e = hipEventRecord(x->staging_free, x->stream);
   if (e == hipSuccess && staging_bytes > 0 && engine_copies_available(device)) {
     for (int s = 0; s < kEngineSlots && e == hipSuccess; ++s)
@@ -2066,6 +2108,7 @@ int pf_xfer_destroy(pf_xfer* x) {
   for (hipEvent_t ev : x->eng_ev)
     if (ev) (void)hipEventDestroy(ev);
   if (x->staging_free) (void)hipEventDestroy(x->staging_free);
+  if (x->head_done) (void)hipEventDestroy(x->head_done);
   if (x->d_desc) (void)hipFree(x->d_desc);
   if (x->d_counters) (void)hipFree(x->d_counters);
   if (x->h_desc) (void)hipHostFree(x->h_desc);

@@ -159,12 +159,13 @@ def test_staged_slices_across_layers_vs_oracle(gpu, slices, pinned):
 
 def test_staged_pipelined_load_vs_oracle(gpu):
     """A staged load large enough to be pipelined (9 layers, 19,606 chunks):
-    its first layer is sliced and its copies queued before the other layers
+    its first layer is copied (by the zero-copy kernel when the caller waits
+    layer by layer, else sliced onto the copy engine) before the other layers
     are planned.  After the first layer come an empty layer, a layer copied
     in place in list order, and a layer whose host region is ordinary
     (pageable) memory, copied through HIP run by run; slices start small and
-    grow.  Bytes against the oracle, per-layer events in layer order, and
-    every layer's mark set by a second, marked load."""
+    grow.  Bytes against the oracle for a load with per-layer events (in
+    layer order), a marked load (every layer's mark set) and a plain one."""
     say("[gpu] staged pipelined load, mixed later layers")
     ctx = TransferContext(0, staging_bytes=64 * 1024)
     nb, bpb = 2048, 256
@@ -216,6 +217,16 @@ def test_staged_pipelined_load_vs_oracle(gpu):
         assert words.array.view(np.uint64).tolist() == [9] * len(layers)
         for L in layers:
             assert np.array_equal(L.dev.download(), L.ref)
+        # A load completed as a whole (no events, no marks) is staged for
+        # every layer, the first included: into refilled tensors.
+        for i, L in enumerate(layers):
+            L.dev.fill_random(300 + i)
+            L.ref[:] = L.dev.download()  # in place: the oracle's layout points here
+        ctx.load_layers(loads(), _lib.MODE_STAGED)
+        ctx.synchronize()
+        for i, (L, (_, _, ids, _)) in enumerate(zip(layers, specs)):
+            L.oracle_load(ids)
+            assert np.array_equal(L.dev.download(), L.ref), f"plain load: layer {i} differs"
     finally:
         for L in layers:
             L.close()
