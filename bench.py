@@ -803,7 +803,7 @@ def _start_server(pool_bytes, *extra):
     raise RuntimeError("engine server did not start:\n" + "".join(seen))
 
 
-def leg_two_process(layers, ids, targets, P, reps=4):
+def leg_two_process(layers, ids, targets, P, reps=4, server_args=()):
     """The deployment path of the reference: the inference process keeps its
     layer tensors and talks to an engine server in another process, which
     maps the tensors through HIP IPC (registry.rs:144-175).  The inference
@@ -828,7 +828,7 @@ def leg_two_process(layers, ids, targets, P, reps=4):
     ids_l, targets_l = [int(i) for i in ids], [int(t) for t in targets]
     layers.refill()
     sock = os.path.join(tempfile.mkdtemp(prefix="pega_bench_"), "engine.sock")
-    p, addr = _start_server((reps + 2) * P + (256 << 20), "--fast-socket", sock)
+    p, addr = _start_server((reps + 2) * P + (256 << 20), "--fast-socket", sock, *server_args)
     out = {"what": "llama prefix saved and restored by hash through the engine server in a "
                    "second process that maps the 32 layer tensors through HIP IPC; restore "
                    "timed from the Load request to the LoadState reading ready, median of the "

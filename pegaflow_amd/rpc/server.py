@@ -222,11 +222,15 @@ class Server:
                  pool_size: int = 30 << 30, host_pool: bool = False, unit_size_hint: int = 0,
                  max_workers: int = 16, dfs_root: str | None = None,
                  dfs_quota: int = 50 << 30, dfs_io_threads: int = 4,
-                 fast_socket: str | None = None, grpc_impl: str = "native"):
+                 fast_socket: str | None = None, grpc_impl: str = "native",
+                 save_mode: int | None = None, load_mode: int | None = None):
         self.engine = engine or PegaEngine(pool_size=pool_size, host_pool=host_pool,
                                            unit_size_hint=unit_size_hint)
         if dfs_root:
             self.engine.enable_disk(dfs_root, quota_bytes=dfs_quota, io_threads=dfs_io_threads)
+        if save_mode is not None or load_mode is not None:
+            self.engine.set_transfer_modes(_lib.MODE_AUTO if save_mode is None else save_mode,
+                                           _lib.MODE_AUTO if load_mode is None else load_mode)
         # Load, Save and Health also on a native Unix-socket endpoint.
         self.fast_socket = fast_socket
         if fast_socket:
@@ -288,6 +292,12 @@ def parse_args(argv=None):
     ap.add_argument("--log-level", default="info")
     ap.add_argument("--max-workers", type=int, default=16,
                     help="worker threads of the python gRPC server")
+    ap.add_argument("--save-mode", choices=sorted(_lib.MODE_NAMES), default="auto",
+                    help="transfer mode of saves (auto: staged on the copy engines for long "
+                         "host runs)")
+    ap.add_argument("--load-mode", choices=sorted(_lib.MODE_NAMES), default="auto",
+                    help="transfer mode of loads (auto: staged for long host runs; kernel: "
+                         "the zero-copy kernel throughout)")
     ap.add_argument("--grpc-impl", choices=("native", "python"), default="native",
                     help="serve gRPC from the library's native HTTP/2 server (default) or "
                          "from grpcio's")
@@ -342,7 +352,9 @@ def main(argv=None) -> int:
     server = Server(args.addr, pool_size=args.pool_size, unit_size_hint=args.hint_value_size,
                     max_workers=args.max_workers, dfs_root=args.dfs_root,
                     dfs_quota=args.dfs_quota, dfs_io_threads=args.dfs_io_threads,
-                    fast_socket=args.fast_socket, grpc_impl=args.grpc_impl).start()
+                    fast_socket=args.fast_socket, grpc_impl=args.grpc_impl,
+                    save_mode=_lib.MODE_NAMES[args.save_mode],
+                    load_mode=_lib.MODE_NAMES[args.load_mode]).start()
     for sig in (signal.SIGINT, signal.SIGTERM):
         signal.signal(sig, lambda *_: server.service.shutdown_event.set())
     print(f"READY {server.addr}", flush=True)
