@@ -109,3 +109,18 @@ def test_hpack_decoder_rfc7541_examples():
                        stderr=subprocess.STDOUT, text=True)
     assert r.returncode == 0, r.stdout[-6000:]
     assert r.stdout.strip().endswith("ok")
+
+
+@pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc is not installed")
+@pytest.mark.parametrize("variant", sorted(VARIANTS))
+def test_grpc_server_under_sanitizer(variant):
+    """tests/native/grpc_stress.cpp: the native gRPC server with 4 raw HTTP/2
+    clients keeping 4 requests in flight each (replies from the connection's
+    thread and from the handler on worker threads), PINGs, and a stop with
+    the connections open, under each sanitizer."""
+    exe = build(variant, "grpc_stress")
+    env = dict(os.environ, **VARIANTS[variant][1])
+    r = subprocess.run([exe], env=env, timeout=300, stdout=subprocess.PIPE,
+                       stderr=subprocess.STDOUT, text=True)
+    assert r.returncode == 0, r.stdout[-6000:]
+    assert r.stdout.strip().endswith("ok")
