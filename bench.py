@@ -832,7 +832,8 @@ def leg_two_process(layers, ids, targets, P, reps=4, server_args=()):
     out = {"what": "llama prefix saved and restored by hash through the engine server in a "
                    "second process that maps the 32 layer tensors through HIP IPC; restore "
                    "timed from the Load request to the LoadState reading ready, median of the "
-                   "warm calls; over gRPC, and over the server's native endpoint (fast_path)"}
+                   "warm calls; over gRPC (the library's native HTTP/2 server), and over the "
+                   "server's native Unix-socket endpoint (fast_path); engine default modes"}
     med = lambda v: statistics.median(v[1:])  # noqa: E731
 
     def measure(client, tag):
