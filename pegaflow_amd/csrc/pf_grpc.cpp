@@ -39,23 +39,13 @@
 #include <vector>
 
 #include "pf_common.h"
+#include "pf_h2.h"
 #include "pf_hpack.h"
 
 using namespace pf;
+using namespace pf::h2;
 
 namespace {
-
-// Frame types, flags, settings and error codes (RFC 9113 6, 7).
-enum : uint8_t {
-  kData = 0, kHeaders = 1, kPriority = 2, kRstStream = 3, kSettings = 4, kPushPromise = 5,
-  kPing = 6, kGoaway = 7, kWindowUpdate = 8, kContinuation = 9
-};
-constexpr uint8_t kEndStream = 0x1, kAck = 0x1, kEndHeaders = 0x4, kPadded = 0x8,
-                  kPriorityFlag = 0x20;
-enum : uint32_t {
-  kProtocolError = 1, kFlowControlError = 3, kFrameSizeError = 6, kRefusedStream = 7,
-  kCompressionError = 9
-};
 
 // gRPC status codes (grpc/status.h).
 enum : uint32_t {
@@ -70,73 +60,9 @@ constexpr uint32_t kMaxStreams = 1024;
 constexpr uint64_t kWindowRefill = 64ull << 20;  // connection window given back per
 constexpr size_t kWorkers = 8;
 
-const char kPreface[] = "PRI * HTTP/2.0\r\n\r\nSM\r\n\r\n";
 const std::string kServicePrefix = "/pegaflow.Engine/";
 // LoadResponse / SaveResponse / HealthResponse { status: ResponseStatus { ok: true } }.
 const uint8_t kOkResponse[] = {0x0a, 0x02, 0x08, 0x01};
-
-void put32(std::string* s, uint32_t v) {
-  for (int sh = 24; sh >= 0; sh -= 8) s->push_back(static_cast<char>((v >> sh) & 0xff));
-}
-
-void frame(std::string* out, uint8_t type, uint8_t flags, uint32_t sid, const void* p,
-           size_t n) {
-  out->push_back(static_cast<char>((n >> 16) & 0xff));
-  out->push_back(static_cast<char>((n >> 8) & 0xff));
-  out->push_back(static_cast<char>(n & 0xff));
-  out->push_back(static_cast<char>(type));
-  out->push_back(static_cast<char>(flags));
-  put32(out, sid & 0x7fffffffu);
-  out->append(static_cast<const char*>(p), n);
-}
-
-// HPACK integer with an N-bit prefix, the prefix's other bits `first`.
-void hp_int(std::string* s, uint8_t first, int prefix, uint64_t v) {
-  const uint64_t mask = (1u << prefix) - 1;
-  if (v < mask) {
-    s->push_back(static_cast<char>(first | v));
-    return;
-  }
-  s->push_back(static_cast<char>(first | mask));
-  v -= mask;
-  while (v >= 0x80) {
-    s->push_back(static_cast<char>((v & 0x7f) | 0x80));
-    v >>= 7;
-  }
-  s->push_back(static_cast<char>(v));
-}
-
-void hp_string(std::string* s, const std::string& v) {
-  hp_int(s, 0x00, 7, v.size());  // no Huffman coding
-  s->append(v);
-}
-
-// Literal header field without indexing: by static name index, or new name.
-void hp_field(std::string* s, uint32_t name_index, const std::string& value) {
-  hp_int(s, 0x00, 4, name_index);
-  hp_string(s, value);
-}
-void hp_field(std::string* s, const std::string& name, const std::string& value) {
-  s->push_back(0x00);
-  hp_string(s, name);
-  hp_string(s, value);
-}
-
-// grpc-message: bytes outside 0x20-0x7e, and '%', percent-encoded.
-std::string percent_encode(const std::string& m) {
-  static const char* hexd = "0123456789ABCDEF";
-  std::string out;
-  for (unsigned char c : m) {
-    if (c >= 0x20 && c <= 0x7e && c != '%') {
-      out.push_back(static_cast<char>(c));
-    } else {
-      out.push_back('%');
-      out.push_back(hexd[c >> 4]);
-      out.push_back(hexd[c & 15]);
-    }
-  }
-  return out;
-}
 
 // service.rs:77-88.
 uint32_t grpc_code(int rc) {
@@ -375,7 +301,7 @@ bool Conn::reply(uint32_t sid, uint32_t status, const std::string& message, cons
 }
 
 void Conn::run() {
-  char pre[sizeof(kPreface) - 1];
+  char pre[kPrefaceLen];
   if (read_exact(pre, sizeof(pre)) && std::memcmp(pre, kPreface, sizeof(pre)) == 0) {
     std::string out, s;
     const uint16_t ids[3] = {0x3, 0x4, 0x5};  // max streams, initial window, max frame
