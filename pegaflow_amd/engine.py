@@ -109,6 +109,10 @@ class PegaEngine:
 
     def set_transfer_modes(self, save_mode: int = _lib.MODE_AUTO,
                            load_mode: int = _lib.MODE_AUTO) -> None:
+        """Transfer modes of saves and loads (pf_engine_set_modes); the
+        defaults (AUTO both ways) run a save batch, and a load of blocks
+        saved together, staged on the copy engines, and a load of a few
+        scattered blocks by the zero-copy kernel."""
         _raise(lib().pf_engine_set_modes(self._h, save_mode, load_mode))
 
     def register_context_layer(self, instance_id: str, namespace: str, device_id: int,

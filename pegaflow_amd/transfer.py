@@ -243,7 +243,9 @@ class TransferContext:
             self.set_route_grid(route, grid)
 
     def set_staged_slices(self, save_bytes: int = 0, load_bytes: int = 0) -> None:
-        """Largest staged slice per direction (0 keeps the current value)."""
+        """Largest staged slice per direction (0 keeps the current value;
+        pf_xfer_set_staged_slices).  A load's slices start at a quarter of
+        its largest and double."""
         check(lib().pf_xfer_set_staged_slices(self.handle, save_bytes, load_bytes),
               "pf_xfer_set_staged_slices")
 
