@@ -485,9 +485,16 @@ def leg_layerwise(xfer, seed):
     whole load, as a caller without per-layer completion must.  The marked
     figure restores all layers in one launch whose kernel writes a device
     word per layer, and gates compute kernel l with a bounded device wait on
-    word l."""
+    word l.  The engine figure restores the same blocks by hash through
+    PegaEngine in its default modes (staged on the copy engines, its first
+    layer by the kernel) with a layered LoadState carrying device layer
+    words, compute kernel l gated on word l."""
+    import hashlib
+
     from pegaflow_amd import _lib
     from pegaflow_amd import workload as wl
+    from pegaflow_amd.engine import PegaEngine
+    from pegaflow_amd.load_state import LayerWords, PyLoadState
     from pegaflow_amd.runtime import (DeviceBuffer, Event, PinnedBuffer, Stream, spin,
                                       stream_wait_word)
 
@@ -548,6 +555,42 @@ def leg_layerwise(xfer, seed):
     run_marked()
     marked = min(run_marked() for _ in range(3))
     bad = wl.verify_restored(layers, ids, targets)
+    layers.refill()
+    # Through the engine, default modes, gated on device layer words.
+    eng = PegaEngine(pool_size=wl.payload_bytes(layers.regs, n) + (256 << 20))
+    names = [f"layer.{l}" for l in range(shape.layers)]
+    for name, r in zip(names, layers.regs):
+        eng.register_context_layer("lw", "qwen3", 0, name, r.data_ptr, r.size_bytes, r.num_blocks,
+                                   r.bytes_per_block, r.kv_stride_bytes, r.segments, 0, 1,
+                                   shape.layers)
+    ids_l, tg_l = [int(i) for i in ids], [int(t) for t in targets]
+    hashes = [hashlib.sha256(b"qwen3-%d" % i).digest() for i in ids_l]
+    eng.batch_save_kv_blocks("lw", 0, 0, [(nm, ids_l, hashes) for nm in names])
+    lw = LayerWords(shape.layers, local=True)
+    timed_out = DeviceBuffer(4 * shape.layers)
+
+    def run_engine():
+        timed_out.memset(0)
+        st = PyLoadState(layer_words=lw)
+        start.record(compute)
+        eng.batch_load_kv_blocks("lw", 0, 0, st.shm_name(), names, tg_l, hashes)
+        for l in range(shape.layers):
+            lw.wait_on_device(compute, l, 10_000_000, timed_out.ptr + 4 * l)
+            spin(compute, compute_us)
+        done.record(compute)
+        done.synchronize()
+        while not st.is_ready():
+            time.sleep(0.0001)
+        if st.get_state() != 1 or timed_out.download().any():
+            raise RuntimeError("engine layer-wise restore failed or a device wait timed out")
+        return start.elapsed_ms(done)
+
+    run_engine()
+    engine_total = min(run_engine() for _ in range(3))
+    bad += wl.verify_restored(layers, ids, targets)
+    eng.close()
+    lw.close()
+    timed_out.close()
     ideal = shape.layers * compute_us / 1e3
     out = {
         "workload": "qwen3-8b 5k-token prefix: 36 x bf16 [2,16000,16,8,128], 313 blocks, "
@@ -561,6 +604,8 @@ def leg_layerwise(xfer, seed):
         "serialized_efficiency": round(ideal / serial, 4),
         "marked_total_ms": round(marked, 3),
         "marked_efficiency": round(ideal / marked, 4),
+        "engine_total_ms": round(engine_total, 3),
+        "engine_efficiency": round(ideal / engine_total, 4),
         "first_layer_ms": round(per_layer[0], 4),
         "per_layer_ms_mean": round(sum(per_layer[1:]) / (len(per_layer) - 1), 4),
         "per_layer_ms_max": round(max(per_layer[1:]), 4),
