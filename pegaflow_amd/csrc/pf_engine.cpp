@@ -517,14 +517,14 @@ struct LoadTask {
   std::shared_ptr<LaterLayers> later;
 };
 
-// A thread that runs one job at a time for the load thread: the issue of a
-// staged load, whose call drives the copy engines slice by slice and returns
-// only once its copies are done, while the load thread publishes each layer
-// as its mark lands.
-class Issuer {
+// A thread that runs one job at a time for the load thread: publishing each
+// layer of a staged load as its mark lands, while the load thread issues the
+// load, whose call drives the copy engines slice by slice and returns only
+// once its copies are done.
+class Publisher {
  public:
-  Issuer() : thread_([this] { loop(); }) {}
-  ~Issuer() {
+  Publisher() : thread_([this] { loop(); }) {}
+  ~Publisher() {
     {
       std::lock_guard<std::mutex> lk(mu_);
       stop_ = true;
@@ -552,6 +552,9 @@ class Issuer {
 
  private:
   void loop() {
+    // Its polls sleep 10 us between reads, as the load thread's do: without
+    // the load thread's timer slack (1 us) each sleep lasts about 60 us.
+    (void)prctl(PR_SET_TIMERSLACK, 1000UL, 0, 0, 0);
     std::unique_lock<std::mutex> lk(mu_);
     for (;;) {
       cv_.wait(lk, [this] { return stop_ || job_; });
@@ -626,7 +629,7 @@ class DeviceWorker {
   // shares the host link with them (see kLoadGridAlone).
   std::atomic<int> saves_running_{0};
   std::vector<std::shared_ptr<SealedBlock>> spare_keep_;  // under q_mu_
-  std::unique_ptr<Issuer> issuer_;  // staged marked loads (with a device)
+  std::unique_ptr<Publisher> publisher_;  // staged marked loads' layers (with a device)
 
   int map_layer_words(const pf_layer_words& w, uint64_t* words);
   int load_marked(std::vector<pf_layer_xfer>& layers, uint32_t mode, pf_load_state* st,
@@ -661,7 +664,7 @@ int DeviceWorker::create(int device, bool with_gpu, std::shared_ptr<DeviceWorker
     if (pf_xfer_create(device, kSaveStagingBytes, &w->save_x_) != PF_OK ||
         pf_xfer_create(device, kLoadStagingBytes, &w->load_x_) != PF_OK)
       return fail(PF_ERR_INIT, std::string("failed to initialize HIP: ") + pf_last_error());
-    w->issuer_.reset(new Issuer());
+    w->publisher_.reset(new Publisher());
   }
   w->thread_ = std::thread([p = w.get()] { p->load_loop(); });
   *out = std::move(w);
@@ -675,7 +678,7 @@ DeviceWorker::~DeviceWorker() {
   }
   q_cv_.notify_all();
   if (thread_.joinable()) thread_.join();
-  issuer_.reset();
+  publisher_.reset();
   if (save_x_) pf_xfer_destroy(save_x_);
   if (load_x_) pf_xfer_destroy(load_x_);
   if (gpu_) {
@@ -749,51 +752,54 @@ int DeviceWorker::load_marked(std::vector<pf_layer_xfer>& layers, uint32_t mode,
                    : pf_load_layers_marked(load_x_, layers.data(), static_cast<uint32_t>(L), mode,
                                            sig, n_sig);
   };
-  // A staged load returns only once its copies are done: it is issued from
-  // the issuer thread while this one publishes its layers as they land.
-  // Every return below waits for the issue first (it uses the task's lists).
-  struct Join {
-    Issuer* issuer;
-    ~Join() {
-      if (issuer) (void)issuer->wait();
-    }
-  } join{mode == PF_MODE_STAGED ? issuer_.get() : nullptr};
-  if (join.issuer)
-    join.issuer->start(issue);
-  else if (int rc = issue())
-    return rc;
-  const auto t_issued = std::chrono::steady_clock::now();
-  auto t_first = t_issued;
   hipStream_t stream = static_cast<hipStream_t>(pf_xfer_stream(load_x_));
-  for (size_t l = 0; l < L; ++l) {
-    const uint64_t* w = host_words_ + l;
-    for (uint32_t spins = 0; __atomic_load_n(w, __ATOMIC_ACQUIRE) < ticket; ++spins) {
-      // While a staged load is still issuing, its copies are in flight.
-      if (spins % 64 == 63 && join.issuer && join.issuer->finished()) {
-        Issuer* done = join.issuer;
-        join.issuer = nullptr;
-        if (int rc = done->wait()) return rc;
+  // Publishes each layer in the LoadState as its word lands.  `issuing`
+  // reads 1 while a staged call still runs on another thread (its copies
+  // are in flight meanwhile, whatever the stream says) and 2 once it failed;
+  // otherwise a stream gone idle with a word unset means the copy failed.
+  std::atomic<int> issuing{0};
+  auto t_first = t0;
+  auto publish = [&]() -> int {
+    for (size_t l = 0; l < L; ++l) {
+      const uint64_t* w = host_words_ + l;
+      for (uint32_t spins = 0; __atomic_load_n(w, __ATOMIC_ACQUIRE) < ticket; ++spins) {
+        if (spins % 64 == 63) {
+          const int state = issuing.load(std::memory_order_acquire);
+          if (state == 2) return PF_ERR_STORAGE;  // the issuing thread reports why
+          if (state == 0) {
+            const hipError_t q = hipStreamQuery(stream);
+            if (q != hipErrorNotReady && __atomic_load_n(w, __ATOMIC_ACQUIRE) < ticket)
+              return fail(PF_ERR_STORAGE,
+                          strf("layer %zu of a marked load was not marked (%s)", l,
+                               hipGetErrorString(q)));
+          }
+        }
+        if (spins > 256) std::this_thread::sleep_for(std::chrono::microseconds(10));
       }
-      if (spins % 64 == 63 && !join.issuer) {
-        const hipError_t q = hipStreamQuery(stream);
-        if (q != hipErrorNotReady && __atomic_load_n(w, __ATOMIC_ACQUIRE) < ticket)
-          return fail(PF_ERR_STORAGE,
-                      strf("layer %zu of a marked load was not marked (%s)", l,
-                           hipGetErrorString(q)));
-      }
-      if (spins > 256) std::this_thread::sleep_for(std::chrono::microseconds(10));
+      pf_load_state_set_layers_done(st, static_cast<int64_t>(l + 1));
+      if (l == 0) t_first = std::chrono::steady_clock::now();
     }
-    pf_load_state_set_layers_done(st, static_cast<int64_t>(l + 1));
-    if (l == 0) t_first = std::chrono::steady_clock::now();
-  }
-  if (join.issuer) {
-    Issuer* done = join.issuer;
-    join.issuer = nullptr;
-    if (int rc = done->wait()) return rc;
+    return PF_OK;
+  };
+  if (mode == PF_MODE_STAGED && publisher_) {
+    // A staged load returns only once its copies are done.  It is issued on
+    // this thread at once, and the publisher thread publishes its layers as
+    // they land (that thread's wake-up overlaps the first layer's copy).
+    issuing.store(1, std::memory_order_release);
+    publisher_->start(publish);
+    const int rc = issue();
+    const std::string msg = rc == PF_OK ? std::string() : std::string(pf_last_error());
+    issuing.store(rc == PF_OK ? 0 : 2, std::memory_order_release);
+    const int prc = publisher_->wait();  // it reads this call's locals
+    if (rc) return fail(rc, msg);
+    if (prc) return prc;
+  } else {
+    if (int rc = issue()) return rc;
+    if (int rc = publish()) return rc;
   }
   if (tracing())
-    std::fprintf(stderr, "[pegaflow] marked load at=%.0fus issue=%.0fus first_layer=%.0fus\n",
-                 mono_us(t0), us_between(t0, t_issued), us_between(t0, t_first));
+    std::fprintf(stderr, "[pegaflow] marked load at=%.0fus first_layer=%.0fus\n", mono_us(t0),
+                 us_between(t0, t_first));
   return pf_xfer_synchronize(load_x_);
 }
 
