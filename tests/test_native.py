@@ -124,3 +124,19 @@ def test_grpc_server_under_sanitizer(variant):
                        stderr=subprocess.STDOUT, text=True)
     assert r.returncode == 0, r.stdout[-6000:]
     assert r.stdout.strip().endswith("ok")
+
+
+@pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc is not installed")
+def test_staged_slicing_rules():
+    """tests/native/staged_plan_test.cpp under AddressSanitizer+UBSan: the
+    staged mode's slices for a Llama-3-8B prefix load and save and a
+    tensor-parallel rank's load (sizes worked out by hand), empty, in-place
+    and oversized layers, and 3000 random calls against the rules every cut
+    keeps (each chunk once in order, slice sizes, contiguous descriptors,
+    layers done in order with their last slice)."""
+    exe = build("asan", "staged_plan_test")
+    env = dict(os.environ, **VARIANTS["asan"][1])
+    r = subprocess.run([exe], env=env, timeout=120, stdout=subprocess.PIPE,
+                       stderr=subprocess.STDOUT, text=True)
+    assert r.returncode == 0, r.stdout[-6000:]
+    assert r.stdout.strip().endswith("ok")
