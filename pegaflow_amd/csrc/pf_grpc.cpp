@@ -26,6 +26,7 @@
 #include <unistd.h>
 
 #include <atomic>
+#include <chrono>
 #include <condition_variable>
 #include <cstdio>
 #include <cstring>
@@ -153,6 +154,7 @@ class Conn : public std::enable_shared_from_this<Conn> {
     std::string path, content_type, encoding;
     std::string data;     // request body (length-prefixed messages)
     bool headers_done = false, end_after_block = false, rejected = false;
+    std::chrono::steady_clock::time_point opened;  // its first HEADERS frame
   };
   void run();
   bool handle(uint8_t type, uint8_t flags, uint32_t sid, std::string& payload);
@@ -220,9 +222,23 @@ struct Server {
   std::atomic<uint64_t> served{0};
 
   void accept_loop();
+  // `data`: the request's one length-prefixed message (5 bytes of prefix).
   void dispatch(const std::shared_ptr<Conn>& c, uint32_t sid, const std::string& path,
-                std::string&& body);
+                std::string&& data, std::chrono::steady_clock::time_point opened);
 };
+
+// With PEGAFLOW_TRACE set: when a request's stream opened, its body was
+// complete, its handling began, and its reply was sent (monotonic us).
+void trace_request(const std::string& method, size_t bytes,
+                   std::chrono::steady_clock::time_point opened,
+                   std::chrono::steady_clock::time_point received,
+                   std::chrono::steady_clock::time_point started) {
+  std::fprintf(stderr,
+               "[pegaflow] grpc request method=%s bytes=%zu opened=%.0fus received=%.0fus "
+               "started=%.0fus replied=%.0fus\n",
+               method.c_str(), bytes, mono_us(opened), mono_us(received), mono_us(started),
+               mono_us(std::chrono::steady_clock::now()));
+}
 
 bool Conn::read_exact(void* p, size_t n) {
   char* q = static_cast<char*>(p);
@@ -421,6 +437,7 @@ bool Conn::handle(uint8_t type, uint8_t flags, uint32_t sid, std::string& payloa
         }
         last_sid_ = sid;
         it = streams_.emplace(sid, Stream()).first;
+        if (tracing()) it->second.opened = std::chrono::steady_clock::now();
       }
       // A second block on a stream is the client's trailers: decoded (the
       // table must stay in step) and otherwise ignored.
@@ -604,35 +621,41 @@ void Conn::complete(uint32_t sid, Stream&& st) {
           nullptr, 0);
     return;
   }
-  srv_->dispatch(shared_from_this(), sid, st.path, std::string(st.data, 5));
+  srv_->dispatch(shared_from_this(), sid, st.path, std::move(st.data), st.opened);
 }
 
 void Server::dispatch(const std::shared_ptr<Conn>& c, uint32_t sid, const std::string& path,
-                      std::string&& body) {
+                      std::string&& data, std::chrono::steady_clock::time_point opened) {
   served.fetch_add(1);
+  const bool trace = tracing();
+  const auto received = trace ? std::chrono::steady_clock::now() : opened;
   if (path.compare(0, kServicePrefix.size(), kServicePrefix) != 0) {
     c->reply(sid, kUnimplemented, "Method not found!", nullptr, 0);
     return;
   }
   const std::string method = path.substr(kServicePrefix.size());
-  const auto* req = reinterpret_cast<const uint8_t*>(body.data());
+  const auto* req = reinterpret_cast<const uint8_t*>(data.data()) + 5;
+  const size_t size = data.size() - 5;
   if (method == "Load" || method == "Health") {
-    const int rc = method == "Load"
-                       ? pf_engine_serve_request(engine, PF_FAST_LOAD, req, body.size())
-                       : PF_OK;
+    const int rc = method == "Load" ? pf_engine_serve_request(engine, PF_FAST_LOAD, req, size)
+                                    : PF_OK;
     std::string msg = rc == PF_OK ? std::string() : std::string(pf_last_error());
     // On the connection's thread the reply may not wait for window updates
     // (that thread reads them); a worker sends it if the windows are short.
     if (!c->reply_rc(sid, rc, msg, false))
       workers->post([c, sid, rc, msg] { c->reply_rc(sid, rc, msg); });
+    if (trace) trace_request(method, size, opened, received, received);
     return;
   }
+  auto job = std::make_shared<std::string>(std::move(data));
   if (method == "Save") {
-    auto job = std::make_shared<std::string>(std::move(body));
-    workers->post([this, c, sid, job] {
+    workers->post([this, c, sid, job, trace, opened, received] {
+      const auto started = std::chrono::steady_clock::now();
       const int rc = pf_engine_serve_request(
-          engine, PF_FAST_SAVE, reinterpret_cast<const uint8_t*>(job->data()), job->size());
+          engine, PF_FAST_SAVE, reinterpret_cast<const uint8_t*>(job->data()) + 5,
+          job->size() - 5);
       c->reply_rc(sid, rc, rc == PF_OK ? std::string() : std::string(pf_last_error()));
+      if (trace) trace_request("Save", job->size() - 5, opened, received, started);
     });
     return;
   }
@@ -640,13 +663,12 @@ void Server::dispatch(const std::shared_ptr<Conn>& c, uint32_t sid, const std::s
     c->reply(sid, kUnimplemented, "Method not found!", nullptr, 0);
     return;
   }
-  auto job = std::make_shared<std::string>(std::move(body));
   workers->post([this, c, sid, job, method] {
     pf_grpc_call call;
     call.conn = c;
     call.sid = sid;
-    fallback(ctx, &call, method.c_str(), reinterpret_cast<const uint8_t*>(job->data()),
-             job->size());
+    fallback(ctx, &call, method.c_str(), reinterpret_cast<const uint8_t*>(job->data()) + 5,
+             job->size() - 5);
     if (!call.replied) c->reply(sid, kInternal, "the handler sent no reply", nullptr, 0);
   });
 }

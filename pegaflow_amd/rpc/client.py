@@ -84,8 +84,8 @@ def encode_save_request(instance_id: str, tp_rank: int, device_id: int, saves) -
             body = (_ids_part(proto.SaveLayer, block_ids) +
                     _hashes_part(proto.SaveLayer, block_hashes))
             hit = bodies[key] = (block_ids, block_hashes, body)
-        layer = proto.SaveLayer(layer_name=layer_name).SerializeToString() + hit[2]
-        parts += [_SAVES_TAG, _varint(len(layer)), layer]
+        name = proto.SaveLayer(layer_name=layer_name).SerializeToString()
+        parts += [_SAVES_TAG, _varint(len(name) + len(hit[2])), name, hit[2]]
     return b"".join(parts)
 
 

@@ -197,6 +197,78 @@ def test_duplicate_hash_slot_by_slot_keeps_first(engine):
     m.close()
 
 
+def _save_request(inst, layers):
+    """SaveRequest wire bytes; each layer is (name, ids, hashes) or raw
+    SaveLayer bytes."""
+    from pegaflow_amd.rpc import proto
+
+    out = proto.SaveRequest(instance_id=inst, tp_rank=0, device_id=0).SerializeToString()
+    for layer in layers:
+        if not isinstance(layer, bytes):
+            name, ids, hashes = layer
+            layer = proto.SaveLayer(layer_name=name, block_ids=ids,
+                                    block_hashes=hashes).SerializeToString()
+        out += b"\x22" + _varint(len(layer)) + layer  # field 4, length-delimited
+    return out
+
+
+def _varint(n):
+    out = bytearray()
+    while True:
+        b, n = n & 0x7F, n >> 7
+        out.append(b | (0x80 if n else 0))
+        if not n:
+            return bytes(out)
+
+
+def test_save_requests_share_repeated_lists(engine):
+    """The request decoder shares a layer's id and hash lists with the
+    previous layer's when their bytes are equal (the whole message after the
+    name, or either field alone), and decodes them otherwise: reversed lists,
+    a layer with an unknown field first and its name last, ids that differ
+    under shared hashes.  Every (hash, layer) slot must hold the block that
+    layer's own lists name."""
+    from pegaflow_amd.rpc import proto
+
+    say("[gpu] engine save requests with shared and distinct per-layer lists")
+    m = Model(engine, "req", 6, 64, 2048, seed=21)
+    orig = m.host_copies()
+    H = [h(i, b"req") for i in range(8)]
+    A = [5, 17, 3, 60, 41, 8, 22, 30]
+    B = [1, 2, 9, 10, 33, 34, 50, 63]
+    odd = (b"\x48\x01" +  # field 9, varint: skipped
+           proto.SaveLayer(block_ids=B, block_hashes=H).SerializeToString() +
+           proto.SaveLayer(layer_name=m.names[3]).SerializeToString())
+    req = _save_request("req", [
+        (m.names[0], A, H),
+        (m.names[1], A, H),              # the same bytes after the name
+        (m.names[2], B[::-1], H[::-1]),  # both lists differ
+        odd,                             # name last: decoded in full
+        (m.names[4], A, H),              # hashes equal to the layer before's
+        (m.names[5], B, H),              # hashes shared along the chain
+    ])
+    engine.serve_request(_lib.FAST_SAVE, req)
+    want_ids = [A, A, B, B, A, B]
+    # A second request whose layers are all alike.
+    H2 = [h(i, b"req2") for i in range(5)]
+    C = [11, 12, 13, 14, 15]
+    engine.serve_request(_lib.FAST_SAVE, _save_request("req", [(n, C, H2) for n in m.names]))
+    assert engine.stats()["sealed_blocks"] == len(H) + len(H2)
+    for hashes, per_layer in ((H, want_ids), (H2, [C] * m.n_layers)):
+        for l in range(m.n_layers):
+            for i, hh in enumerate(hashes):
+                b = per_layer[l][i]
+                k, v = engine.read_block_slot("ns", hh, l)
+                assert k == orig[l][b * m.bpb:(b + 1) * m.bpb].tobytes(), f"layer {l} block {i} K"
+                assert v == orig[l][m.kv + b * m.bpb:m.kv + (b + 1) * m.bpb].tobytes(), \
+                    f"layer {l} block {i} V"
+    # A layer whose lists differ in length is refused as the reference does.
+    bad = _save_request("req", [(m.names[0], A, H), (m.names[1], A[:3], H)])
+    with pytest.raises(RuntimeError, match="block_ids length 3 does not match block_hashes 8"):
+        engine.serve_request(_lib.FAST_SAVE, bad)
+    m.close()
+
+
 def test_load_missing_hash_fails_whole_call(engine):
     say("[gpu] engine load with a missing hash")
     m = Model(engine, "inst", 2, 16, 1024)
