@@ -533,12 +533,15 @@ def _full_size(ctx, n_layers, nb, bpb, segs, n_blocks, save_mode, load_mode, see
     host.close()
 
 
-@pytest.mark.parametrize("save_mode,load_mode", [("kernel", "staged"), ("staged", "kernel"),
+@pytest.mark.parametrize("save_mode,load_mode", [("kernel", "kernel"), ("kernel", "staged"),
+                                                  ("staged", "kernel"), ("auto", "auto"),
                                                   ("dma_batched", "dma_batched")])
 def test_llama_10k_prefix_full_size(ctx, save_mode, load_mode):
-    """Config 2: 32 bf16 layers [2,20000,16,8,128], 640 random blocks."""
+    """Config 2: 32 bf16 layers [2,20000,16,8,128], 640 random blocks; the
+    bench's own pairing (zero-copy save, zero-copy restore) first."""
     say(f"[gpu] llama full size save={save_mode} load={load_mode}")
-    _full_size(ctx, 32, 20000, 32768, 2, 640, MODES[save_mode], MODES[load_mode])
+    _full_size(ctx, 32, 20000, 32768, 2, 640, _lib.MODE_NAMES[save_mode],
+               _lib.MODE_NAMES[load_mode])
 
 
 @pytest.mark.parametrize("save_mode,load_mode", [("kernel", "kernel"), ("staged", "dma_batched")])
