@@ -1691,11 +1691,13 @@ int pf_engine_batch_load(pf_engine* e, const char* instance_id, uint64_t tp_rank
   // still fails the call and the LoadState, but the first layers may have
   // been copied by then.
   task.mode = e->load_mode.load();
-  if (task.mode == PF_MODE_AUTO && num_layers > 0) {
+  // Layer 0's list when built early (AUTO), kept as the task's.
+  std::vector<pf_block_xfer> probe;
+  uint64_t probe_bytes = 0;
+  const bool probed = task.mode == PF_MODE_AUTO && num_layers > 0;
+  if (probed) {
     // Blocks saved together lie alike in every layer: the first layer's
     // list decides, so a load resolved to the kernel mode is still split.
-    std::vector<pf_block_xfer> probe;
-    uint64_t probe_bytes = 0;
     if (int rc = build(0, 1, &probe, &probe_bytes)) return bail(rc);
     const pf_layer_xfer lx{refs[0].reg, probe.data(), probe.size()};
     task.mode = gpu->worker->resolve_load_mode(PF_MODE_AUTO, &lx, 1);
@@ -1713,7 +1715,13 @@ int pf_engine_batch_load(pf_engine* e, const char* instance_id, uint64_t tp_rank
     }
   }
   task.blocks.resize(num_layers);
-  if (int rc = build(0, head ? head : num_layers, task.blocks.data(), &task.bytes))
+  uint32_t from = 0;
+  if (probed) {
+    task.blocks[0] = std::move(probe);
+    task.bytes += probe_bytes;
+    from = 1;
+  }
+  if (int rc = build(from, head ? head : num_layers, task.blocks.data() + from, &task.bytes))
     return bail(rc);
   bool any = false;
   for (uint32_t li = 0; li < (head ? head : num_layers); ++li)
