@@ -84,9 +84,17 @@ def encode_save_request(instance_id: str, tp_rank: int, device_id: int, saves) -
             body = (_ids_part(proto.SaveLayer, block_ids) +
                     _hashes_part(proto.SaveLayer, block_hashes))
             hit = bodies[key] = (block_ids, block_hashes, body)
-        name = proto.SaveLayer(layer_name=layer_name).SerializeToString()
+        name = _NAME_FIELDS.get(layer_name)
+        if name is None:  # a connector names the same layers every step
+            if len(_NAME_FIELDS) >= 4096:
+                _NAME_FIELDS.clear()
+            name = _NAME_FIELDS[layer_name] = proto.SaveLayer(
+                layer_name=layer_name).SerializeToString()
         parts += [_SAVES_TAG, _varint(len(name) + len(hit[2])), name, hit[2]]
     return b"".join(parts)
+
+
+_NAME_FIELDS: dict = {}  # layer name -> its SaveLayer name field, serialized
 
 
 _LAYER_NAMES_CACHE: dict = {}
