@@ -400,6 +400,23 @@ def test_engine_decoder_matches_the_full_parse(served_fast):
         head + _ld(4, b""),                                            # an empty layer
         head + _ld(4, _ld(1, b"l0") + _ld(2, varint(5)) + _ld(3, b"a")),  # a good one
     ]
+    # Several layers: the decoder shares a layer's lists with the previous
+    # layer's when their bytes are equal, and must still see every layer's own.
+    def layer(name, ids, hl=hs, name_last=False):
+        body = proto.SaveLayer(block_ids=ids, block_hashes=hl).SerializeToString()
+        return _ld(4, body + _ld(1, name) if name_last else _ld(1, name) + body)
+
+    mixed = b"".join(_ld(3, h) + varint(2 << 3) + varint(v) for h, v in zip(hs, (1, 2)))
+    saves += [
+        head + layer(b"l0", [1, 2]) + layer(b"l1", [1, 2]) + layer(b"l0", [1, 16]),
+        head + layer(b"l0", [1, 2]) + layer(b"l1", [1]),                  # fewer ids
+        head + layer(b"l0", [1, 2]) + layer(b"l1", [1, 2], hs[:1]),       # fewer hashes
+        head + layer(b"l0", [1, 2]) + layer(b"l1", [1, 2], name_last=True) +
+        layer(b"l1", [1, 2]) + layer(b"l0", [3, 16]),                     # after a name-last one
+        head + _ld(4, _ld(1, b"l0") + mixed) + _ld(4, _ld(1, b"l1") + mixed) +
+        layer(b"l1", [1, 2, 3]),                                          # interleaved lists
+        head + layer(b"l0", [2, 1], hs[::-1]) + layer(b"l1", [1, 2]) + layer(b"l1", [16, 2]),
+    ]
     outcomes = []
     for i, w in enumerate(saves):
         want = python_path(2, proto.SaveRequest, w)
