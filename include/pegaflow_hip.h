@@ -188,7 +188,10 @@ int pf_ipc_close(uint64_t base);
  * on, for cross-process per-layer completion on the device.  The event is
  * created with timing disabled and the interprocess flag; its 64-byte handle
  * is opened in the other process with pf_ipc_event_open (not in the same
- * process).  Destroy both with pf_event_destroy. */
+ * process).  Destroy both with pf_event_destroy.  A runtime that refuses to
+ * export interprocess events (probed once per process) makes
+ * pf_event_create_ipc fail with PF_ERR_UNSUPPORTED; cross-process waits then
+ * use layer words (pf_load_state_create_layered_words). */
 int pf_event_create_ipc(pf_event* out);
 int pf_ipc_event_export(pf_event event, uint8_t* handle);
 int pf_ipc_event_open(const uint8_t* handle, pf_event* out);
@@ -360,7 +363,9 @@ int pf_xfer_route_shape(pf_xfer* xfer, uint32_t route, uint32_t* threads,
  * a marked load's layers, finishing in order, and few requests in flight
  * keep the link at its peak).  Marked launches always run queued (at
  * PF_LOAD_HOST_DEFAULT_GRID when their route says 0).  pf_xfer_set_max_grid
- * caps both kinds. */
+ * caps both kinds.  Every route may run queued: the staged mode's two
+ * streams each have a queue of their own, and a queued launch leaves its
+ * queue empty. */
 #define PF_SAVE_HOST_DEFAULT_GRID 32u
 #define PF_LOAD_HOST_DEFAULT_GRID 64u
 int pf_xfer_set_route_grid(pf_xfer* xfer, uint32_t route, uint32_t workgroups);
@@ -376,6 +381,12 @@ int pf_xfer_set_max_grid(pf_xfer* xfer, uint32_t max_workgroups);
  * (the staged mode then copies through HIP).  No counterpart in the reference
  * (its copies are cuMemcpy calls); bench_copy_engines measures each engine. */
 int pf_copy_engines(int device, uint32_t* d2h_engine, uint32_t* h2d_engine);
+/* Chooses the copy engines of the staged mode on `device`, per direction a
+ * mask of one or two engine id bits (0 keeps that direction's choice), from
+ * those the runtime reports available (else PF_ERR_INVALID_ARGUMENT); copies
+ * issued afterwards use them.  PF_ERR_UNSUPPORTED when the device's engines
+ * are not known.  No counterpart in the reference. */
+int pf_set_copy_engines(int device, uint32_t d2h_engines, uint32_t h2d_engines);
 /* Largest staged slice per direction, in bytes (0 keeps the current value);
  * slices are further capped by the staging slot.  A load's slices start at
  * a quarter of its largest slice (at most 16 MiB) and double, each of the
@@ -415,8 +426,11 @@ int pf_load_layers(pf_xfer* xfer, const pf_layer_xfer* layers,
                    uint32_t num_layers, uint32_t mode, pf_event* layer_events);
 
 /* No counterpart in the reference.  For callers that cannot allocate device
- * memory: code under HIP graph capture, tight serving loops, harnesses that
- * forbid hipMalloc.  pf_load_layers in PF_MODE_KERNEL without events, with
+ * memory: tight serving loops and harnesses that forbid hipMalloc.  Not for
+ * HIP graph capture: the scratch below is shared by every call on a device,
+ * so a replayed graph would copy the blocks of whichever call ran last; on a
+ * stream that is capturing, the call fails with PF_ERR_UNSUPPORTED before
+ * anything is issued.  pf_load_layers in PF_MODE_KERNEL without events, with
  * the same bytes, issued on the caller's stream (NULL: the current device's
  * null stream) instead of a transfer context's.  The chunk descriptors and
  * the tile queue live in a static device array of the library (one copy per
@@ -540,7 +554,10 @@ void pf_load_state_set_layers_done(pf_load_state* state, int64_t n);
  * i64 events_recorded} and the handles.  The loader opens the handles,
  * records layer l's event on its stream after layer l's copy, and then
  * publishes events_recorded = count; from then on the consumer may make a
- * stream wait on event l (waiting earlier would see no record). */
+ * stream wait on event l (waiting earlier would see no record).  Where the
+ * runtime refuses to export interprocess events (as pf_event_create_ipc
+ * reports) this fails with PF_ERR_UNSUPPORTED; with no device present the
+ * handles are kept as opaque bytes. */
 int pf_load_state_create_layered_events(uint32_t num_layers,
                                         const uint8_t* event_handles,
                                         pf_load_state** out);

@@ -266,6 +266,7 @@ SIGNATURES = {
     "pf_xfer_set_max_grid": (i32, [vp, u32]),
     "pf_xfer_set_staged_slices": (i32, [vp, u64, u64]),
     "pf_copy_engines": (i32, [i32, ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint32)]),
+    "pf_set_copy_engines": (i32, [i32, u32, u32]),
     "pf_xfer_set_kernel_shape_dir": (i32, [vp, u32, u32, u32]),
     "pf_xfer_route_shape": (i32, [vp, u32, ctypes.POINTER(u32), ctypes.POINTER(u32),
                                   ctypes.POINTER(i32)]),

@@ -79,14 +79,14 @@ hipError_t launch_copy_chunks(const ChunkDesc* d_descs, uint32_t n_chunks,
                               uint32_t threads, uint32_t unroll,
                               uint32_t max_grid, hipStream_t stream);
 // The queued copy (16-byte aligned chunks only): `grid` persistent
-// workgroups pull tiles from the counter at next_tile, which holds `base`
-// when the launch starts and base + *n_tiles + grid when it ends.  With
-// marks, each finished layer is marked.
+// workgroups pull tiles from the two-word queue at `queue` (device memory),
+// which holds 0, 0 when the launch starts and again when it ends.  Launches
+// that may run at the same time need separate queues.  With marks, each
+// finished layer is marked.
 hipError_t launch_copy_chunks_queue(const ChunkDesc* d_descs, uint32_t n_chunks,
                                     uint64_t chunk_bytes, uint32_t threads, uint32_t unroll,
                                     uint32_t grid, const LayerMarks* marks,
-                                    uint32_t* next_tile, uint32_t base, uint32_t* n_tiles,
-                                    hipStream_t stream);
+                                    uint32_t* queue, uint32_t* n_tiles, hipStream_t stream);
 hipError_t launch_mark_layers(const LayerList& list, const SignalTargets& t,
                               hipStream_t stream);
 hipError_t launch_wait_word(uint64_t word, uint64_t value, uint64_t max_ticks,
@@ -133,6 +133,9 @@ bool engine_copies_available(int device);
 // The engine id bits in use for each direction, one or two each (false,
 // and 0, when unknown).
 bool engine_ids(int device, uint32_t* d2h, uint32_t* h2d);
+// Sets the engines of either direction (a mask of one or two engine id
+// bits; 0 keeps that direction's); copies issued afterwards use them.
+int set_engine_ids(int device, uint32_t d2h, uint32_t h2d);
 int engine_signal_create(EngineSignal* s);  // value 0
 void engine_signal_destroy(EngineSignal* s);
 // Adds n to the count before n copies are submitted against the signal.
@@ -164,6 +167,13 @@ class RangeCache {
   uint64_t last_b_ = 0, last_e_ = 0;
 };
 
+// Whether this process's runtime exports interprocess events: 1 yes, 0 no
+// (it refuses hipIpcGetEventHandle; *why then holds its error), -1 no device
+// to ask.  Probed once, on the current device, with one throwaway event.
+int ipc_events_supported(std::string* why = nullptr);
+// PF_ERR_UNSUPPORTED (message set) where ipc_events_supported says 0.
+int refuse_ipc_events();
+
 // Layout kind (PF_LAYOUT_*), shared by the transfer paths.
 inline int layout_kind(const pf_kv_layout& l) {
   if (l.segments == 2 && l.kv_stride_bytes > l.bytes_per_block)
@@ -178,14 +188,13 @@ int segment_offset(const pf_kv_layout& l, uint64_t block, uint64_t seg,
                    uint64_t* out);
 
 // Static device scratch of pf_load_layers_noalloc (one copy per device,
-// held until the process ends): the tile queue's counter in the first 256
-// bytes, then up to PF_NOALLOC_MAX_CHUNKS chunk descriptors.
+// held until the process ends): the tile queue in the first 256 bytes, then
+// up to PF_NOALLOC_MAX_CHUNKS chunk descriptors.
 constexpr uint64_t kNoAllocQueueBytes = 256;
 constexpr uint64_t kNoAllocScratchBytes =
     kNoAllocQueueBytes + PF_NOALLOC_MAX_CHUNKS * sizeof(ChunkDesc);
 struct NoAllocScratch {
   uint64_t base = 0;        // device address of the device's copy of the array
-  uint32_t next_base = 0;   // where the tile counter stands after the last launch
   std::mutex mu;            // host-side bookkeeping of calls on this device
 };
 // The device's scratch.  The array's address is looked up once per device,

@@ -177,27 +177,43 @@ copy_chunks_v16_kernel(const ChunkDesc* __restrict__ descs,
 // small persistent grid pulls tile indices from one counter, so the fast
 // XCDs take more tiles and tiles, hence layers, finish in order; with few
 // requests in flight the link also runs closer to its peak (Llama restore
-// 24.1 -> 23.3 ms of kernel time with 64 workgroups).  The counter is
-// never reset: each launch advances it by exactly n_tiles + gridDim.x
-// (every workgroup's last pull fails), and the host passes the value it
-// starts from as `base`.  MARK adds the per-layer completion marks, with
-// agent-coherent stores (see write_marks).
+// 24.1 -> 23.3 ms of kernel time with 64 workgroups).
+//
+// The queue is two words, queue[0] the next tile and queue[1] the
+// workgroups that have left, both 0 when a launch starts.  A workgroup
+// leaves after a pull past the last tile, and counts itself out with an
+// acquire-release add; the last one out has seen every workgroup's final
+// pull, so it puts both words back to 0.  The launch therefore leaves the
+// queue as it found it, whatever the host knows of earlier launches: a
+// replayed graph or a launch on another stream after this one finds 0.
+// Launches that run at the same time need queues of their own.  MARK adds
+// the per-layer completion marks, with agent-coherent stores (see
+// write_marks).
 template <int UNROLL, bool NTL, bool NTS, bool MARK>
 __global__ void __launch_bounds__(1024)
 copy_chunks_queue_kernel(const ChunkDesc* __restrict__ descs, uint32_t tiles_per_chunk,
                          uint32_t n_tiles, uint32_t chunk16, LayerMarks marks,
-                         uint32_t* next_tile, uint32_t base) {
+                         uint32_t* queue) {
   __shared__ uint32_t s_tile;
   const uint32_t stride = blockDim.x;
   const uint32_t tile_elems = stride * UNROLL;
   for (;;) {
     if (threadIdx.x == 0)
-      s_tile = __hip_atomic_fetch_add(next_tile, 1u, __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT) - base;
+      s_tile = __hip_atomic_fetch_add(queue, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     const uint32_t t = s_tile;
     __syncthreads();  // every lane has read s_tile before it is written again
-    if (t >= n_tiles) break;  // uniform: the queue is empty for every later pull too
+    if (t >= n_tiles) {  // uniform: the queue is empty for every later pull too
+      if (threadIdx.x == 0) {
+        const uint32_t out = __hip_atomic_fetch_add(queue + 1, 1u, __ATOMIC_ACQ_REL,
+                                                    __HIP_MEMORY_SCOPE_AGENT);
+        if (out + 1 == gridDim.x) {
+          __hip_atomic_store(queue, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(queue + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+      break;
+    }
     const uint32_t c = t / tiles_per_chunk;
     const uint32_t tile = t - c * tiles_per_chunk;
     const ChunkDesc d = descs[c];
@@ -314,35 +330,35 @@ static hipError_t launch_v16(const ChunkDesc* d_descs, uint32_t tiles_per_chunk,
 template <int UNROLL, bool NTL, bool NTS>
 static void launch_queue_nt(dim3 grid, dim3 block, hipStream_t stream, const ChunkDesc* d,
                             uint32_t tpc, uint32_t n_tiles, uint32_t c16,
-                            const LayerMarks* marks, uint32_t* next, uint32_t base) {
+                            const LayerMarks* marks, uint32_t* queue) {
   if (marks)
     hipLaunchKernelGGL((copy_chunks_queue_kernel<UNROLL, NTL, NTS, true>), grid, block, 0,
-                       stream, d, tpc, n_tiles, c16, *marks, next, base);
+                       stream, d, tpc, n_tiles, c16, *marks, queue);
   else
     hipLaunchKernelGGL((copy_chunks_queue_kernel<UNROLL, NTL, NTS, false>), grid, block, 0,
-                       stream, d, tpc, n_tiles, c16, LayerMarks{}, next, base);
+                       stream, d, tpc, n_tiles, c16, LayerMarks{}, queue);
 }
 
 template <int UNROLL>
 static void launch_queue(dim3 grid, dim3 block, hipStream_t stream, const ChunkDesc* d,
                          uint32_t tpc, uint32_t n_tiles, uint32_t c16, uint32_t flags,
-                         const LayerMarks* marks, uint32_t* next, uint32_t base) {
+                         const LayerMarks* marks, uint32_t* queue) {
   switch (flags & PF_KERNEL_NONTEMPORAL) {
     case 0:
       launch_queue_nt<UNROLL, false, false>(grid, block, stream, d, tpc, n_tiles, c16, marks,
-                                            next, base);
+                                            queue);
       break;
     case PF_KERNEL_NT_LOADS:
       launch_queue_nt<UNROLL, true, false>(grid, block, stream, d, tpc, n_tiles, c16, marks,
-                                           next, base);
+                                           queue);
       break;
     case PF_KERNEL_NT_STORES:
       launch_queue_nt<UNROLL, false, true>(grid, block, stream, d, tpc, n_tiles, c16, marks,
-                                           next, base);
+                                           queue);
       break;
     default:
       launch_queue_nt<UNROLL, true, true>(grid, block, stream, d, tpc, n_tiles, c16, marks,
-                                          next, base);
+                                          queue);
       break;
   }
 }
@@ -400,11 +416,10 @@ hipError_t launch_copy_chunks(const ChunkDesc* d_descs, uint32_t n_chunks,
 hipError_t launch_copy_chunks_queue(const ChunkDesc* d_descs, uint32_t n_chunks,
                                     uint64_t chunk_bytes, uint32_t threads, uint32_t unroll,
                                     uint32_t grid, const LayerMarks* marks,
-                                    uint32_t* next_tile, uint32_t base, uint32_t* n_tiles,
-                                    hipStream_t stream) {
+                                    uint32_t* queue, uint32_t* n_tiles, hipStream_t stream) {
   *n_tiles = 0;
   if (n_chunks == 0 || chunk_bytes == 0) return hipSuccess;
-  if (threads == 0 || threads > 1024 || threads % 64 != 0 || grid == 0 || !next_tile)
+  if (threads == 0 || threads > 1024 || threads % 64 != 0 || grid == 0 || !queue)
     return hipErrorInvalidValue;
   if (marks && (marks->n == 0 || !marks->chunk_start || !marks->layer || !marks->counters ||
                 marks->targets.count == 0 || marks->targets.count > kMaxSignalTargets))
@@ -415,13 +430,14 @@ hipError_t launch_copy_chunks_queue(const ChunkDesc* d_descs, uint32_t n_chunks,
   if (!tile_geometry(n_chunks, chunk_bytes, threads, unroll, &tpc, &ntiles, &c16))
     return hipErrorInvalidValue;
   if (static_cast<uint64_t>(ntiles) + grid > 0xffffffffull) return hipErrorInvalidValue;
+  if (grid > kMaxGrid) return hipErrorInvalidValue;
   const dim3 g(grid), b(threads);
   switch (unroll) {
-    case 1: launch_queue<1>(g, b, stream, d_descs, tpc, ntiles, c16, flags, marks, next_tile, base); break;
-    case 2: launch_queue<2>(g, b, stream, d_descs, tpc, ntiles, c16, flags, marks, next_tile, base); break;
-    case 4: launch_queue<4>(g, b, stream, d_descs, tpc, ntiles, c16, flags, marks, next_tile, base); break;
-    case 8: launch_queue<8>(g, b, stream, d_descs, tpc, ntiles, c16, flags, marks, next_tile, base); break;
-    case 16: launch_queue<16>(g, b, stream, d_descs, tpc, ntiles, c16, flags, marks, next_tile, base); break;
+    case 1: launch_queue<1>(g, b, stream, d_descs, tpc, ntiles, c16, flags, marks, queue); break;
+    case 2: launch_queue<2>(g, b, stream, d_descs, tpc, ntiles, c16, flags, marks, queue); break;
+    case 4: launch_queue<4>(g, b, stream, d_descs, tpc, ntiles, c16, flags, marks, queue); break;
+    case 8: launch_queue<8>(g, b, stream, d_descs, tpc, ntiles, c16, flags, marks, queue); break;
+    case 16: launch_queue<16>(g, b, stream, d_descs, tpc, ntiles, c16, flags, marks, queue); break;
     default: return hipErrorInvalidValue;
   }
   *n_tiles = ntiles;

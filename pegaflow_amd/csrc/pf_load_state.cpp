@@ -249,6 +249,14 @@ int pf_load_state_create_layered(uint32_t num_layers, pf_load_state** out) {
 int pf_load_state_create_layered_events(uint32_t num_layers, const uint8_t* event_handles,
                                         pf_load_state** out) {
   if (!event_handles) return fail(PF_ERR_INVALID_ARGUMENT, "null event handles");
+  // Where this runtime cannot export interprocess events no loader could be
+  // handed real ones: refused up front rather than at the loader's open.
+  // Without a device the handles are opaque bytes, kept as given.
+  std::string why;
+  if (ipc_events_supported(&why) == 0)
+    return fail(PF_ERR_UNSUPPORTED,
+                "a LoadState of interprocess event handles: this runtime cannot export "
+                "interprocess events (" + why + "); use layer words instead");
   return create_state(num_layers, true, event_handles, nullptr, out);
 }
 

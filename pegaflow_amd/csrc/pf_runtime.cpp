@@ -169,9 +169,8 @@ int noalloc_scratch(int device, NoAllocScratch** out) {
   if (!ptr) return fail(PF_ERR_INIT, "no device address for the scratch array");
   auto sc = std::make_unique<NoAllocScratch>();
   sc->base = reinterpret_cast<uint64_t>(ptr);
-  // The array is zero when the code object is loaded: the tile counter
-  // starts at 0, and every launch advances it by a count the host tracks.
-  sc->next_base = 0;
+  // The array is zero when the code object is loaded, so the tile queue
+  // starts empty, and every queued launch leaves it empty.
   *out = sc.get();
   g_scratch.emplace(device, std::move(sc));
   return PF_OK;
@@ -291,24 +290,63 @@ EngineDevice discover_engines(int device) {
   return d;
 }
 
-const EngineDevice* engines_of(int device) {
+// The device's engines (discovered on first use), copied under the lock:
+// pf_set_copy_engines may change the choice while copies are issued.
+bool engines_of(int device, EngineDevice* out) {
   std::lock_guard<std::mutex> lk(g_engine_mu);
   auto it = g_engines.find(device);
   if (it == g_engines.end()) it = g_engines.emplace(device, discover_engines(device)).first;
-  return it->second.ok ? &it->second : nullptr;
+  if (!it->second.ok) return false;
+  *out = it->second;
+  return true;
 }
 
 hsa_signal_t sig_of(const EngineSignal* s) { return hsa_signal_t{s->handle}; }
 
 }  // namespace
 
-bool engine_copies_available(int device) { return engines_of(device) != nullptr; }
+bool engine_copies_available(int device) {
+  EngineDevice d;
+  return engines_of(device, &d);
+}
 
 bool engine_ids(int device, uint32_t* d2h, uint32_t* h2d) {
-  const EngineDevice* d = engines_of(device);
-  *d2h = d ? (d->engine[0][0] | d->engine[0][1]) : 0;
-  *h2d = d ? (d->engine[1][0] | d->engine[1][1]) : 0;
-  return d != nullptr;
+  EngineDevice d;
+  const bool ok = engines_of(device, &d);
+  *d2h = ok ? (d.engine[0][0] | d.engine[0][1]) : 0;
+  *h2d = ok ? (d.engine[1][0] | d.engine[1][1]) : 0;
+  return ok;
+}
+
+int set_engine_ids(int device, uint32_t d2h, uint32_t h2d) {
+  EngineDevice d;
+  if (!engines_of(device, &d))
+    return fail(PF_ERR_UNSUPPORTED, "the device's copy engines are not known");
+  uint32_t avail[2] = {0, 0};
+  (void)hsa_amd_memory_copy_engine_status(d.cpu, d.gpu, &avail[0]);
+  (void)hsa_amd_memory_copy_engine_status(d.gpu, d.cpu, &avail[1]);
+  const uint32_t mask[2] = {d2h, h2d};
+  for (int dir = 0; dir < 2; ++dir) {
+    const uint32_t m = mask[dir];
+    if (m == 0) continue;
+    if (__builtin_popcount(m) > 2)
+      return fail(PF_ERR_INVALID_ARGUMENT,
+                  strf("copy engine mask 0x%x: one or two engine bits per direction", m));
+    if (m & ~avail[dir])
+      return fail(PF_ERR_INVALID_ARGUMENT,
+                  strf("copy engine mask 0x%x: the runtime reports only 0x%x available %s", m,
+                       avail[dir], dir == 0 ? "device to host" : "host to device"));
+  }
+  std::lock_guard<std::mutex> lk(g_engine_mu);
+  EngineDevice& e = g_engines[device];
+  for (int dir = 0; dir < 2; ++dir) {
+    const uint32_t m = mask[dir];
+    if (m == 0) continue;
+    const uint32_t a = lowest_bit(m), b = lowest_bit(m & ~a);
+    e.engine[dir][0] = a;
+    e.engine[dir][1] = b ? b : a;
+  }
+  return PF_OK;
 }
 
 int engine_signal_create(EngineSignal* s) {
@@ -328,15 +366,15 @@ void engine_signal_add(EngineSignal* s, int64_t n) { hsa_signal_add_screlease(si
 
 int engine_copy(int device, bool d2h, uint64_t dst, uint64_t src, uint64_t bytes,
                 EngineSignal* s, unsigned lane) {
-  const EngineDevice* d = engines_of(device);
+  EngineDevice d;
   hsa_status_t r = HSA_STATUS_ERROR;
-  if (d) {
-    const hsa_agent_t dst_agent = d2h ? d->cpu : d->gpu;
-    const hsa_agent_t src_agent = d2h ? d->gpu : d->cpu;
+  if (engines_of(device, &d)) {
+    const hsa_agent_t dst_agent = d2h ? d.cpu : d.gpu;
+    const hsa_agent_t src_agent = d2h ? d.gpu : d.cpu;
     r = hsa_amd_memory_async_copy_on_engine(
         reinterpret_cast<void*>(dst), dst_agent, reinterpret_cast<const void*>(src), src_agent,
         bytes, 0, nullptr, sig_of(s),
-        static_cast<hsa_amd_sdma_engine_id_t>(d->engine[d2h ? 0 : 1][lane & 1]), false);
+        static_cast<hsa_amd_sdma_engine_id_t>(d.engine[d2h ? 0 : 1][lane & 1]), false);
   }
   if (r != HSA_STATUS_SUCCESS) {
     hsa_signal_subtract_screlease(sig_of(s), 1);
@@ -375,6 +413,42 @@ int engine_signal_wait(EngineSignal* s, bool spin) {
       return fail(PF_ERR_HIP, strf("copy engine copies not done after %d s", kEngineWaitSeconds));
   }
   return PF_OK;
+}
+
+int ipc_events_supported(std::string* why) {
+  static std::once_flag once;
+  static int supported = -1;
+  static std::string reason;
+  std::call_once(once, [] {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0) {
+      (void)hipGetLastError();
+      return;
+    }
+    hipEvent_t e = nullptr;
+    hipError_t r = hipEventCreateWithFlags(&e, hipEventDisableTiming | hipEventInterprocess);
+    if (r == hipSuccess) {
+      hipIpcEventHandle_t h;
+      std::memset(&h, 0, sizeof(h));
+      r = hipIpcGetEventHandle(&h, e);
+      (void)hipEventDestroy(e);
+    }
+    (void)hipGetLastError();
+    supported = r == hipSuccess ? 1 : 0;
+    if (r != hipSuccess) reason = strf("hipIpcGetEventHandle: %s", hipGetErrorString(r));
+  });
+  if (why) *why = reason;
+  return supported;
+}
+
+// An interprocess event this runtime cannot export would leave its consumer
+// waiting on a handle that never arrives; the event is refused instead.
+int refuse_ipc_events() {
+  std::string why;
+  if (ipc_events_supported(&why) != 0) return PF_OK;
+  return fail(PF_ERR_UNSUPPORTED,
+              "interprocess events are not supported by this runtime (" + why +
+                  "); wait on layer words instead (pf_load_state_create_layered_words)");
 }
 
 }  // namespace pf
@@ -664,6 +738,7 @@ int pf_ipc_close(uint64_t base) {
 
 int pf_event_create_ipc(pf_event* out) {
   if (!out) return fail(PF_ERR_INVALID_ARGUMENT, "null output");
+  if (int rc = refuse_ipc_events()) return rc;
   hipEvent_t e = nullptr;
   PF_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming | hipEventInterprocess));
   *out = e;
@@ -854,4 +929,9 @@ int pf_copy_engines(int device, uint32_t* d2h_engine, uint32_t* h2d_engine) {
   if (int rc = pf_init(device)) return rc;
   (void)pf::engine_ids(device, d2h_engine, h2d_engine);
   return PF_OK;
+}
+
+int pf_set_copy_engines(int device, uint32_t d2h_engines, uint32_t h2d_engines) {
+  if (int rc = pf_init(device)) return rc;
+  return pf::set_engine_ids(device, d2h_engines, h2d_engines);
 }

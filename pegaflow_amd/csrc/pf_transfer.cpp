@@ -355,12 +355,12 @@ struct pf_xfer {
   bool timing = false;
   std::vector<std::pair<hipEvent_t, hipEvent_t>> timers;  // one pair per launch
   // Per-layer tile counters of marking launches (0 between launches), and
-  // the tile queue of the marking kernel in its own cache line after them:
-  // it only grows, by n_tiles + grid per launch, from next_base.
+  // after them one tile queue per lane (kernel stream, link-side stream),
+  // each in a 256-byte line of its own: queued launches on the two lanes
+  // may run at the same time.
   uint32_t* d_counters = nullptr;
   size_t counters_cap = 0;
-  uint32_t* d_next = nullptr;
-  uint32_t next_base = 0;
+  uint32_t* d_queue[2] = {nullptr, nullptr};
   // Persistent workgroups of a queued launch per route (0: a fixed
   // workgroup per tile).  Copies over the host link run queued.
   uint32_t grid[4] = {0, 0, PF_SAVE_HOST_DEFAULT_GRID, PF_LOAD_HOST_DEFAULT_GRID};
@@ -472,13 +472,12 @@ ChunkDesc* small_desc(pf_xfer* x, size_t n) {
 
 // One gather/scatter launch of the n chunks at descs on `stream`.  With
 // qgrid > 0 (16-byte aligned chunks only) it runs queued: qgrid persistent
-// workgroups pull tiles from the counter at `next`, which holds *next_base
-// when the launch starts; *next_base is advanced past the launch.  Otherwise
-// one workgroup per tile (at most max_grid workgroups, 0 = no cap).
+// workgroups pull tiles from the queue at `queue`, which no launch that may
+// overlap this one uses.  Otherwise one workgroup per tile (at most max_grid
+// workgroups, 0 = no cap).
 hipError_t issue_copy(hipStream_t stream, const ChunkDesc* descs, size_t n, uint64_t chunk_bytes,
                       bool al16, uint32_t threads, uint32_t unroll, uint32_t qgrid,
-                      uint32_t max_grid, const LayerMarks* marks, uint32_t* next,
-                      uint32_t* next_base) {
+                      uint32_t max_grid, const LayerMarks* marks, uint32_t* queue) {
   (void)hipGetLastError();
   if (!(al16 && qgrid > 0))
     return launch_copy_chunks(descs, static_cast<uint32_t>(n), chunk_bytes, al16, threads, unroll,
@@ -498,11 +497,8 @@ hipError_t issue_copy(hipStream_t stream, const ChunkDesc* descs, size_t n, uint
     threads = t2;
   }
   uint32_t n_tiles = 0;
-  const hipError_t e =
-      launch_copy_chunks_queue(descs, static_cast<uint32_t>(n), chunk_bytes, threads, unroll,
-                               qgrid, marks, next, *next_base, &n_tiles, stream);
-  if (e == hipSuccess) *next_base += n_tiles + qgrid;
-  return e;
+  return launch_copy_chunks_queue(descs, static_cast<uint32_t>(n), chunk_bytes, threads, unroll,
+                                  qgrid, marks, queue, &n_tiles, stream);
 }
 
 // Reads back finished scatter trials; once every candidate has been timed
@@ -585,7 +581,9 @@ int launch(pf_xfer* x, size_t first, size_t n, uint64_t chunk_bytes, bool al16, 
   uint32_t qgrid = x->grid[dir];
   if (marks && qgrid == 0) qgrid = PF_LOAD_HOST_DEFAULT_GRID;
   if (x->max_grid && qgrid > x->max_grid) qgrid = x->max_grid;
-  if (al16 && qgrid > 0 && !x->d_next)
+  // Each lane's launches run in its stream's order; the two lanes overlap.
+  uint32_t* queue = x->d_queue[stream == x->dma ? 1 : 0];
+  if (al16 && qgrid > 0 && !queue)
     return fail(PF_ERR_INVALID_ARGUMENT, "tile queue not allocated");
   if (marks && !(al16 && qgrid > 0))
     return fail(PF_ERR_INVALID_ARGUMENT, "a marking launch needs 16-byte aligned chunks");
@@ -599,8 +597,7 @@ int launch(pf_xfer* x, size_t first, size_t n, uint64_t chunk_bytes, bool al16, 
   }
   unroll &= ~PF_KERNEL_AUTO;
   const hipError_t e = issue_copy(stream, x->desc_base + first, n, chunk_bytes, al16,
-                                  threads, unroll, qgrid, x->max_grid, marks, x->d_next,
-                                  &x->next_base);
+                                  threads, unroll, qgrid, x->max_grid, marks, queue);
   if (e != hipSuccess) return hip_fail(e, "gather/scatter kernel launch");
   if (trial) {
     PF_HIP(hipEventRecord(trial->stop, stream));
@@ -622,14 +619,15 @@ int ensure_counters(pf_xfer* x, size_t num_layers) {
   PF_HIP(hipStreamSynchronize(x->stream));
   if (x->d_counters) PF_HIP(hipFree(x->d_counters));
   x->d_counters = nullptr;
-  x->d_next = nullptr;
+  x->d_queue[0] = x->d_queue[1] = nullptr;
   x->counters_cap = 0;
-  // cap counters, then one 256-byte line holding the tile queue.
-  const size_t words = cap + 64;
+  // cap counters, then one 256-byte line per lane holding its tile queue.
+  const size_t words = cap + 128;
   PF_HIP(hipMalloc(reinterpret_cast<void**>(&x->d_counters), words * sizeof(uint32_t)));
   PF_HIP(hipMemsetAsync(x->d_counters, 0, words * sizeof(uint32_t), x->stream));
-  x->d_next = x->d_counters + cap;
-  x->next_base = 0;
+  PF_HIP(hipStreamSynchronize(x->stream));  // the link-side lane's first launch finds 0 too
+  x->d_queue[0] = x->d_counters + cap;
+  x->d_queue[1] = x->d_counters + cap + 64;
   x->counters_cap = cap;
   return PF_OK;
 }
@@ -1818,6 +1816,15 @@ int pf_load_layers_noalloc(pf_stream stream, const pf_layer_xfer* layers, uint32
                 strf("pf_load_layers_noalloc: %llu chunks exceed the %u-chunk scratch",
                      (unsigned long long)planned, (unsigned)PF_NOALLOC_MAX_CHUNKS));
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // Not under graph capture: the scratch holds whatever descriptors the last
+  // call on the device left, so a replayed graph would copy another call's
+  // blocks.  Refused before anything is issued.
+  hipStreamCaptureStatus capturing = hipStreamCaptureStatusNone;
+  PF_HIP(hipStreamIsCapturing(s, &capturing));
+  if (capturing != hipStreamCaptureStatusNone)
+    return fail(PF_ERR_UNSUPPORTED,
+                "pf_load_layers_noalloc: the stream is capturing a graph; the shared "
+                "scratch cannot hold a captured call's descriptors");
   int dev = 0;
   if (s) PF_HIP(hipStreamGetDevice(s, &dev));
   else PF_HIP(hipGetDevice(&dev));
@@ -1849,7 +1856,7 @@ int pf_load_layers_noalloc(pf_stream stream, const pf_layer_xfer* layers, uint32
   PF_HIP(hipGetDevice(&prev));
   if (prev != dev) PF_HIP(hipSetDevice(dev));
   ChunkDesc* d_desc = reinterpret_cast<ChunkDesc*>(sc->base + kNoAllocQueueBytes);
-  uint32_t* next = reinterpret_cast<uint32_t*>(sc->base);
+  uint32_t* queue = reinterpret_cast<uint32_t*>(sc->base);
   auto issue = [&]() -> int {
     // A pageable source: the call returns once the bytes have been taken,
     // so the thread's buffer may be refilled by its next call.
@@ -1886,7 +1893,7 @@ int pf_load_layers_noalloc(pf_stream stream, const pf_layer_xfer* layers, uint32
           s, d_desc + first, n, p.chunk_bytes, al,
           host ? PF_LOAD_HOST_DEFAULT_THREADS : PF_LOAD_DEFAULT_THREADS,
           host ? PF_LOAD_HOST_DEFAULT_UNROLL : (PF_LOAD_DEFAULT_UNROLL & ~PF_KERNEL_AUTO),
-          host ? PF_LOAD_HOST_DEFAULT_GRID : 0, 0, nullptr, next, &sc->next_base);
+          host ? PF_LOAD_HOST_DEFAULT_GRID : 0, 0, nullptr, queue);
       if (e != hipSuccess) return hip_fail(e, "gather/scatter kernel launch");
       first += n;
       li = lj;

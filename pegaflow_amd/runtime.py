@@ -48,6 +48,12 @@ def copy_engines(device: int = 0):
     return d.value, h.value
 
 
+def set_copy_engines(device: int = 0, d2h: int = 0, h2d: int = 0) -> None:
+    """Chooses the staged mode's copy engines on the device: per direction a
+    mask of one or two engine id bits (0 keeps that direction's choice)."""
+    check(lib().pf_set_copy_engines(device, d2h, h2d), "pf_set_copy_engines")
+
+
 def mem_get_info():
     f, t = ctypes.c_uint64(), ctypes.c_uint64()
     check(lib().pf_mem_get_info(ctypes.byref(f), ctypes.byref(t)), "pf_mem_get_info")

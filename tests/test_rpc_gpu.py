@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 
 import oracle
-from pegaflow_amd import ipc
+from pegaflow_amd import _lib, ipc
 from pegaflow_amd._lib import PegaFlowError
 from pegaflow_amd.engine import PegaEngine
 from pegaflow_amd.load_state import LayerWords, PyLoadState
@@ -183,6 +183,36 @@ def test_two_process_round_trip_over_the_native_endpoint(gpu, tmp_path):
         layers.close()
 
 
+def _ipc_events_supported():
+    try:
+        probe = Event(interprocess=True)
+    except PegaFlowError as err:
+        assert err.code == _lib.PF_ERR_UNSUPPORTED, err
+        return False
+    try:
+        probe.ipc_handle()
+    finally:
+        probe.close()
+    return True
+
+
+def test_interprocess_events_fail_fast(gpu):
+    """Where the runtime refuses to export interprocess events, both ways in
+    fail up front with PF_ERR_UNSUPPORTED: creating such an event, and
+    creating a LoadState that carries event handles (no loader could be
+    handed real ones).  Where it exports them, both succeed."""
+    say("[gpu] interprocess events: fail fast or work")
+    handles = [bytes([1 + i]) * 64 for i in range(2)]
+    if _ipc_events_supported():
+        PyLoadState(num_layers=2, layer_events=handles)
+        return
+    with pytest.raises(PegaFlowError, match="cannot export interprocess events") as ei:
+        PyLoadState(num_layers=2, layer_events=handles)
+    assert ei.value.code == _lib.PF_ERR_UNSUPPORTED
+    # Layer words, the cross-process substitute, are unaffected.
+    PyLoadState(num_layers=2)
+
+
 def test_cross_process_layer_events(gpu):
     """Device-side per-layer completion across processes: this process (the
     consumer) hands the server one interprocess event per layer in the
@@ -192,13 +222,9 @@ def test_cross_process_layer_events(gpu):
     server's copy of its layer had landed (the copies take ~1 ms; the
     snapshots are queued within microseconds)."""
     say("[gpu] rpc two-process layer events (device-side per-layer wait)")
-    probe = Event(interprocess=True)
-    try:
-        probe.ipc_handle()
-    except PegaFlowError as err:
-        pytest.skip(f"this runtime cannot export interprocess events ({err})")
-    finally:
-        probe.close()
+    if not _ipc_events_supported():
+        pytest.skip("this runtime cannot export interprocess events "
+                    "(pf_event_create_ipc: PF_ERR_UNSUPPORTED)")
     n_layers = 8
     layers = Layers(n_layers, 256, 16 * 8 * 128 * 2, seed=21)
     handles = [ipc.export_tensor(b.ptr, layers.size, 0) for b in layers.bufs]

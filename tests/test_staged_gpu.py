@@ -110,18 +110,26 @@ def _place_all(layers, save_ids, gap=0, pinned=True):
     return host, ohost
 
 
-@pytest.mark.parametrize("slices,pinned", [((3000, 5000), True), ((1, 1), True),
-                                           ((65536, 2048), True), ((3000, 5000), False)])
-def test_staged_slices_across_layers_vs_oracle(gpu, slices, pinned):
+@pytest.mark.parametrize("slices,pinned,grid", [((3000, 5000), True, 0), ((1, 1), True, 0),
+                                                ((65536, 2048), True, 0),
+                                                ((3000, 5000), False, 0),
+                                                ((3000, 5000), False, 3),
+                                                ((1, 1), False, 2)])
+def test_staged_slices_across_layers_vs_oracle(gpu, slices, pinned, grid):
     """One staged save, then one staged load with per-layer events, of eight
     mixed layers, with slices of a few chunks (or one chunk each): host
     regions and every layer tensor equal the oracle's; the layer events
     complete in layer order.  A second load of the same call with layer marks
     sets every layer's word.  Pinned host regions take the copy engines;
-    pageable ones HIP's copies over the context's two streams."""
-    say(f"[gpu] staged slices across layers, slice caps {slices}, pinned={pinned}")
+    pageable ones HIP's copies over the context's two streams.  grid > 0
+    runs the device routes' kernels queued, on both streams at once."""
+    say(f"[gpu] staged slices across layers, slice caps {slices}, pinned={pinned}, "
+        f"device-route grid {grid}")
     ctx = TransferContext(0, staging_bytes=64 * 1024)
     ctx.set_staged_slices(*slices)
+    if grid:
+        ctx.set_route_grid(_lib.ROUTE_SAVE_DEVICE, grid)
+        ctx.set_route_grid(_lib.ROUTE_LOAD_DEVICE, grid)
     layers, save_ids, load_ids = _mixed_layers(70)
     host, ohost = _place_all(layers, save_ids, gap=8, pinned=pinned)
     words = PinnedBuffer(8 * len(layers))
@@ -154,6 +162,45 @@ def test_staged_slices_across_layers_vs_oracle(gpu, slices, pinned):
             L.close()
         host.close()
         words.close()
+        ctx.close()
+
+
+def test_staged_two_lanes_queued_vs_oracle(gpu):
+    """Four split layers [2, 512, 16, 8, 128] from pageable memory, 200 random
+    blocks each, staged in 1 MiB slices over the context's two streams with
+    both device routes queued on 16 workgroups: each stream's kernels pull
+    tiles from a queue of their own while the other stream's run, and every
+    byte of the save and of the load equals the oracle's."""
+    say("[gpu] staged save/load over two lanes, queued device routes")
+    nb, bpb = 512, 32768
+    rng = np.random.Generator(np.random.PCG64(31))
+    layers = [Layer(nb, bpb, 2, nb * bpb, 2 * nb * bpb, 300 + i) for i in range(4)]
+    save_ids = [rng.choice(nb, 200, replace=False).tolist() for _ in layers]
+    load_ids = [rng.choice(nb, 200, replace=False).tolist() for _ in layers]
+    host, ohost = _place_all(layers, save_ids, pinned=False)
+    ctx = TransferContext(0, staging_bytes=4 * MiB)
+    ctx.set_staged_slices(MiB, MiB)
+    ctx.set_route_grid(_lib.ROUTE_SAVE_DEVICE, 16)
+    ctx.set_route_grid(_lib.ROUTE_LOAD_DEVICE, 16)
+    try:
+        for rnd in range(2):
+            ctx.save_layers([L.transfer(ids) for L, ids in zip(layers, save_ids)],
+                            _lib.MODE_STAGED)
+            for L in layers:
+                L.oracle_save()
+            assert np.array_equal(host.array, ohost), f"round {rnd}: host regions differ"
+            ctx.load_layers([L.transfer(ids) for L, ids in zip(layers, load_ids)],
+                            _lib.MODE_STAGED)
+            ctx.synchronize()
+            for L, ids in zip(layers, load_ids):
+                L.oracle_load(ids)
+                assert np.array_equal(L.dev.download(), L.ref), f"round {rnd}: layer differs"
+            launches, copies = ctx.last_stats()
+            assert launches > 2 and copies > 2
+    finally:
+        for L in layers:
+            L.close()
+        host.close()
         ctx.close()
 
 

@@ -13,8 +13,12 @@ point, compared byte for byte on the device.
     cases are also checked against the oracle.
   * The scratch's limit: exactly PF_NOALLOC_MAX_CHUNKS chunks pass, one more
     is refused before anything is issued.
+  * Graph capture: on a stream that is capturing, the call is refused with
+    PF_ERR_UNSUPPORTED before anything is issued (the shared scratch cannot
+    hold a captured call's descriptors), and the stream works afterwards.
 """
 
+import ctypes
 import sys
 
 import numpy as np
@@ -184,6 +188,52 @@ def test_scratch_limit(ctx):
                                    pool.ptr + 1025 * bpb, bpb), stream)
     stream.synchronize()
     assert t.mismatches() == 0  # nothing was issued
+    stream.close()
+    pool.close()
+    t.close()
+
+
+def _hip():
+    """The HIP runtime the library itself is linked against."""
+    h = ctypes.CDLL("libamdhip64.so.7")
+    h.hipStreamBeginCapture.argtypes = [ctypes.c_void_p, ctypes.c_int]
+    h.hipStreamEndCapture.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)]
+    h.hipGraphDestroy.argtypes = [ctypes.c_void_p]
+    return h
+
+
+def test_graph_capture_is_refused(ctx):
+    """A call on a capturing stream fails with PF_ERR_UNSUPPORTED and leaves
+    nothing in the graph; the same call after the capture ends restores the
+    same bytes as pf_load_layers."""
+    say("[gpu] noalloc under graph capture")
+    nb, bpb = 64, 4096
+    t = Twins(1, nb, bpb, seed=11)
+    targets = np.array([4, 17, 33, 2], dtype=np.int64)
+    n = len(targets)
+    pool = PinnedBuffer(2 * n * bpb)
+    oracle.fill_random(pool.array, 123)
+    stream = Stream()
+    hip = _hip()
+    relaxed = 2  # hipStreamCaptureModeRelaxed
+    assert hip.hipStreamBeginCapture(stream.handle, relaxed) == 0
+    graph = ctypes.c_void_p()
+    try:
+        with pytest.raises(_lib.PegaFlowError, match="capturing a graph") as ei:
+            load_layers_noalloc(_loads(t.regs(t.x), targets, pool.ptr, pool.ptr + n * bpb, bpb),
+                                stream)
+        assert ei.value.code == _lib.PF_ERR_UNSUPPORTED
+    finally:
+        assert hip.hipStreamEndCapture(stream.handle, ctypes.byref(graph)) == 0
+        if graph.value:
+            hip.hipGraphDestroy(graph)
+    stream.synchronize()
+    assert t.mismatches() == 0  # nothing was issued
+    load_layers_noalloc(_loads(t.regs(t.x), targets, pool.ptr, pool.ptr + n * bpb, bpb), stream)
+    stream.synchronize()
+    ctx.load_layers(_loads(t.regs(t.y), targets, pool.ptr, pool.ptr + n * bpb, bpb))
+    ctx.synchronize()
+    assert t.mismatches() == 0
     stream.close()
     pool.close()
     t.close()
