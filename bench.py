@@ -44,6 +44,7 @@ Everything else goes to stderr.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import shutil
@@ -93,6 +94,14 @@ def parse():
                          "and the two queued kernels' grids in duplex")
     ap.add_argument("--interference-study", action="store_true",
                     help="only run the cross-process interference study (one JSON line)")
+    ap.add_argument("--study-engines", default="",
+                    help="with --interference-study: staged phases only, once per copy-engine "
+                         "pair, e.g. '0x2:0x1,0x8:0x4' (device-to-host mask:host-to-device mask)")
+    ap.add_argument("--leg", choices=["gpt2", "layerwise", "mla", "tp8", "fragmentation",
+                                      "engine", "two_process", "disk"],
+                    help="only run this one workload and print its JSON")
+    ap.add_argument("--study-victims", default="",
+                    help="with --interference-study: comma-separated victims (default: all)")
     ap.add_argument("--pinned-flags", type=int, default=0,
                     help="PF_PINNED_* flags of the pinned pools (0: mapped, portable)")
     ap.add_argument("--cpu-sample-layers", type=int, default=8)
@@ -237,9 +246,24 @@ def leg_interference(layers, saved, loads, P, reps=3):
 STUDY_PHASES = ["idle", "kernel_save", "staged_save", "kernel_restore", "staged_restore"]
 
 
-def _study_transfer(go, done, ready, out):
+def study_phases(engines: str):
+    """The study's phases: every mode, or with engine pairs ('d2h:h2d,...')
+    the idle phase and then the staged save and restore on each pair, named
+    '<mode>@<d2h>:<h2d>'."""
+    if not engines:
+        return list(STUDY_PHASES)
+    phases = ["idle"]
+    for pair in engines.split(","):
+        d2h, h2d = (int(v, 0) for v in pair.split(":"))
+        phases += [f"staged_save@{d2h:#x}:{h2d:#x}", f"staged_restore@{d2h:#x}:{h2d:#x}"]
+    return phases
+
+
+def _study_transfer(go, done, ready, out, phases):
     """Transfer process of the interference study: each phase saves or
-    restores the Llama prefix six times while the victim process measures."""
+    restores the Llama prefix six times while the victim process measures.
+    A phase '<mode>@<d2h>:<h2d>' first moves the staged copies to that pair
+    of copy engines."""
     from pegaflow_amd import _lib, runtime
     from pegaflow_amd import workload as wl
     from pegaflow_amd.runtime import PinnedBuffer
@@ -260,17 +284,26 @@ def _study_transfer(go, done, ready, out):
         "kernel_restore": lambda: (x.load_layers(loads, _lib.MODE_KERNEL), x.synchronize()),
         "staged_restore": lambda: (x.load_layers(loads, _lib.MODE_STAGED), x.synchronize()),
     }
-    for name in STUDY_PHASES:
-        ops[name]()
+    default_engines = runtime.copy_engines(0)
+
+    def engines_for(name):
+        if "@" not in name:
+            return default_engines
+        return tuple(int(v, 0) for v in name.split("@")[1].split(":"))
+
+    for name in phases:
+        runtime.set_copy_engines(0, *engines_for(name))
+        ops[name.split("@")[0]]()
     ready.set()
     gbps = {}
-    for name in STUDY_PHASES:
+    for name in phases:
+        runtime.set_copy_engines(0, *engines_for(name))
         go.wait()
         go.clear()
         t = []
         for _ in range(6):
             t0 = time.perf_counter()
-            ops[name]()
+            ops[name.split("@")[0]]()
             t.append(time.perf_counter() - t0)
         gbps[name] = round(P / statistics.median(t) / 1e9, 2)
         done.set()
@@ -278,7 +311,7 @@ def _study_transfer(go, done, ready, out):
     out.put(gbps)
 
 
-def _study_victim(go, done, ready, kind, out):
+def _study_victim(go, done, ready, kind, out, phases):
     """Victim process: launches its work back to back through each phase of
     the transfer process and reports the median duration."""
     if kind == "gemm_bf16_8192":
@@ -331,7 +364,7 @@ def _study_victim(go, done, ready, kind, out):
     ready.wait()
     base = None
     res = {}
-    for name in STUDY_PHASES:
+    for name in phases:
         times = []
         go.set()
         time.sleep(0.003)
@@ -347,29 +380,34 @@ def _study_victim(go, done, ready, kind, out):
     out.put(res)
 
 
-def interference_study():
+def interference_study(engines: str = "", victim_list: str = ""):
     """Cross-process interference (the engine server beside a vLLM worker):
     for each victim, a transfer process saves and restores the Llama prefix
-    in each mode while a victim process runs its work back to back.  Prints
-    one JSON line."""
+    in each mode (or staged on each given copy-engine pair) while a victim
+    process runs its work back to back.  Prints one JSON line."""
     import multiprocessing as mp
 
     ctx = mp.get_context("spawn")
     victims = ["hbm_copy_256MiB", "gemm_bf16_8192", "copy_64KiB_h2d", "copy_64KiB_d2h"]
-    try:
-        import torch  # noqa: F401  (the GEMM victim needs it)
-    except ImportError:
-        victims.remove("gemm_bf16_8192")
+    if victim_list:
+        victims = [v for v in victim_list.split(",") if v]
+    if "gemm_bf16_8192" in victims:
+        try:
+            import torch  # noqa: F401  (the GEMM victim needs it)
+        except ImportError:
+            victims.remove("gemm_bf16_8192")
+    phases = study_phases(engines)
     result = {"metric": "interference of each transfer mode with work in another process",
               "transfer": "llama-3.1-8b 10k-token prefix (32 x [2,20000,16,8,128] bf16, "
                           "640 blocks), six calls per phase",
+              "phases": phases,
               "victims": {}}
     for kind in victims:
         log(f"[bench] interference study: victim {kind}")
         go, done, ready = ctx.Event(), ctx.Event(), ctx.Event()
         out, tout = ctx.Queue(), ctx.Queue()
-        pt = ctx.Process(target=_study_transfer, args=(go, done, ready, tout))
-        pv = ctx.Process(target=_study_victim, args=(go, done, ready, kind, out))
+        pt = ctx.Process(target=_study_transfer, args=(go, done, ready, tout, phases))
+        pv = ctx.Process(target=_study_victim, args=(go, done, ready, kind, out, phases))
         pt.start()
         pv.start()
         res = out.get(timeout=300)
@@ -476,10 +514,100 @@ def duplex_study(xfer_load, xfer_save, saved, loads, pool, pool2, dev_buf, P, re
     return out
 
 
-def leg_layerwise(xfer, seed):
+class GemmLayer:
+    """A bf16 GEMM (fp32 accumulation) sized to about `target_ms` alone,
+    queued on one of the library's streams: the per-layer compute of a
+    layer-wise restore, in place of a spin kernel, so that the restore
+    competes with it for CUs and HBM as a model's layers would.  It runs
+    through rocBLAS from /opt/rocm, on the HIP runtime this library is built
+    against (torch's wheel carries a HIP runtime of its own, which cannot
+    share a process with another).  [8192, K] x [K, 8192], column-major,
+    with K calibrated in multiples of 512; operands of N(0, 1) values."""
+
+    OP_N, BF16, F32 = 111, 168, 151  # rocblas_operation_none, rocblas_datatype_*
+
+    def __init__(self, stream, target_ms=2.0):
+        from pegaflow_amd.runtime import DeviceBuffer, Event
+
+        vp, i32 = ctypes.c_void_p, ctypes.c_int
+        lib = ctypes.CDLL("librocblas.so.5")
+        lib.rocblas_create_handle.argtypes = [ctypes.POINTER(vp)]
+        lib.rocblas_set_stream.argtypes = [vp, vp]
+        lib.rocblas_destroy_handle.argtypes = [vp]
+        lib.rocblas_gemm_ex.argtypes = [vp, i32, i32, i32, i32, i32, vp, vp, i32, i32, vp, i32,
+                                        i32, vp, vp, i32, i32, vp, i32, i32, i32, i32, i32,
+                                        ctypes.c_uint32]
+        self.lib, self.stream = lib, stream
+        self.handle = vp()
+        self._check(lib.rocblas_create_handle(ctypes.byref(self.handle)), "create_handle")
+        self._check(lib.rocblas_set_stream(self.handle, stream.handle), "set_stream")
+        self.alpha, self.beta = ctypes.c_float(1.0), ctypes.c_float(0.0)
+        self.m = 8192
+        self.e0, self.e1 = Event(), Event()
+        self._DeviceBuffer = DeviceBuffer
+        self.a = self.b = self.c = None
+        k = 20480
+        for _ in range(2):
+            self._alloc(k)
+            ms = self.time_alone(5)
+            k = max(512, int(round(k * target_ms / ms / 512)) * 512)
+        self._alloc(k)
+        self.alone_ms = self.time_alone(10)
+
+    @staticmethod
+    def _check(rc, what):
+        if rc != 0:
+            raise RuntimeError(f"rocblas_{what} failed with status {rc}")
+
+    def _bf16(self, n, seed):
+        """n bf16 values of N(0, 1): the top half of each float32."""
+        f = np.random.Generator(np.random.PCG64(seed)).standard_normal(n, dtype=np.float32)
+        return (f.view(np.uint32) >> 16).astype(np.uint16).view(np.uint8)
+
+    def _alloc(self, k):
+        self._free()
+        m = self.m
+        self.k = k
+        self.a, self.b = self._DeviceBuffer(2 * m * k), self._DeviceBuffer(2 * k * m)
+        self.c = self._DeviceBuffer(2 * m * m)
+        self.a.upload(self._bf16(m * k, 1))
+        self.b.upload(self._bf16(k * m, 2))
+
+    def _free(self):
+        for buf in (self.a, self.b, self.c):
+            if buf is not None:
+                buf.close()
+        self.a = self.b = self.c = None
+
+    def __call__(self):
+        m, k = self.m, self.k
+        self._check(self.lib.rocblas_gemm_ex(
+            self.handle, self.OP_N, self.OP_N, m, m, k, ctypes.byref(self.alpha),
+            self.a.ptr, self.BF16, m, self.b.ptr, self.BF16, k, ctypes.byref(self.beta),
+            self.c.ptr, self.BF16, m, self.c.ptr, self.BF16, m, self.F32, 0, 0, 0), "gemm_ex")
+
+    def time_alone(self, reps):
+        times = []
+        for _ in range(reps + 1):
+            self.e0.record(self.stream)
+            self()
+            self.e1.record(self.stream)
+            self.e1.synchronize()
+            times.append(self.e0.elapsed_ms(self.e1))
+        return statistics.median(times[1:])
+
+    def close(self):
+        self.stream.synchronize()
+        self._free()
+        if self.handle:
+            self.lib.rocblas_destroy_handle(self.handle)
+        self.handle = None
+
+
+def leg_layerwise(xfer, seed, gemm=True):
     """Config 3: Qwen3-8B shape (36 x [2,16000,16,8,128] bf16), 313 random
-    blocks restored one layer at a time; layer l's event gates a 2 ms compute
-    kernel on a second stream.  Overlap efficiency = 36 x 2 ms / total, with
+    blocks restored one layer at a time; layer l's completion gates layer l's
+    compute on a second stream.  Overlap efficiency = 36 x 2 ms / total, with
     the total from the load's first issue to the last compute kernel's end
     (device events).  The serialized figure gates every compute kernel on the
     whole load, as a caller without per-layer completion must.  The marked
@@ -488,7 +616,13 @@ def leg_layerwise(xfer, seed):
     word l.  The engine figure restores the same blocks by hash through
     PegaEngine in its default modes (staged on the copy engines, its first
     layer by the kernel) with a layered LoadState carrying device layer
-    words, compute kernel l gated on word l."""
+    words, compute kernel l gated on word l.
+
+    The compute is first a 2 ms spin kernel (one lane, no memory traffic: an
+    upper bound on overlap), then (``*_gemm`` keys) a bf16 GEMM calibrated
+    to about 2 ms alone, which shares CUs and HBM with the restore: its
+    efficiency is the 36 GEMMs' time back to back over the gated total, and
+    its slowdown the mean gated GEMM's time over the GEMM's time alone."""
     import hashlib
 
     from pegaflow_amd import _lib
@@ -507,7 +641,22 @@ def leg_layerwise(xfer, seed):
     loads = wl.load_plan(saved, targets)
     compute = Stream()
     evs = [Event() for _ in range(shape.layers)]
+    g0 = [Event() for _ in range(shape.layers)]
+    g1 = [Event() for _ in range(shape.layers)]
     start, done = Event(), Event()
+
+    def spin_work():
+        spin(compute, compute_us)
+
+    work = [spin_work]  # the per-layer compute of the runs below
+
+    def layer_work(l):
+        g0[l].record(compute)
+        work[0]()
+        g1[l].record(compute)
+
+    def work_ms():
+        return statistics.mean(g0[l].elapsed_ms(g1[l]) for l in range(shape.layers))
 
     def run(layerwise):
         start.record(xfer.stream)
@@ -515,13 +664,13 @@ def leg_layerwise(xfer, seed):
         xfer.load_layers(loads, _lib.MODE_KERNEL, layer_events=evs)
         for l in range(shape.layers):
             compute.wait_event(evs[l] if layerwise else evs[-1])
-            spin(compute, compute_us)
+            layer_work(l)
         done.record(compute)
         done.synchronize()
         xfer.synchronize()
         per_layer = [start.elapsed_ms(evs[0])] + [evs[l - 1].elapsed_ms(evs[l])
                                                    for l in range(1, shape.layers)]
-        return start.elapsed_ms(done), per_layer
+        return start.elapsed_ms(done), per_layer, work_ms()
 
     words = DeviceBuffer(8 * shape.layers)
     words.memset(0)
@@ -534,26 +683,53 @@ def leg_layerwise(xfer, seed):
         xfer.load_layers_marked(loads, [(words.ptr, value[0], False)], _lib.MODE_KERNEL)
         for l in range(shape.layers):
             stream_wait_word(compute, words.ptr + 8 * l, value[0], 10_000_000)
-            spin(compute, compute_us)
+            layer_work(l)
         done.record(compute)
         done.synchronize()
         xfer.synchronize()
-        return start.elapsed_ms(done)
+        return start.elapsed_ms(done), work_ms()
 
     def run_compute_only():
         start.record(compute)
-        for _ in range(shape.layers):
-            spin(compute, compute_us)
+        for l in range(shape.layers):
+            layer_work(l)
         done.record(compute)
         done.synchronize()
         return start.elapsed_ms(done)
 
     compute_only = min(run_compute_only() for _ in range(3))
     run(True)
-    total, per_layer = min((run(True) for _ in range(3)), key=lambda r: r[0])
-    serial, _ = min((run(False) for _ in range(2)), key=lambda r: r[0])
+    total, per_layer, _ = min((run(True) for _ in range(3)), key=lambda r: r[0])
+    serial, _, _ = min((run(False) for _ in range(2)), key=lambda r: r[0])
     run_marked()
-    marked = min(run_marked() for _ in range(3))
+    marked, _ = min(run_marked() for _ in range(3))
+    gemm_res = {}
+    gl = None
+    if gemm:
+        gl = GemmLayer(compute)
+        work[0] = gl
+        gemm_only = min(run_compute_only() for _ in range(3))
+        run(True)
+        g_total, g_per_layer, g_ms = min((run(True) for _ in range(3)), key=lambda r: r[0])
+        run_marked()
+        gm_total, gm_ms = min(run_marked() for _ in range(3))
+        gemm_res = {
+            "gemm_shape": f"bf16 [{gl.m},{gl.k}] x [{gl.k},{gl.m}]",
+            "gemm_alone_ms": round(gl.alone_ms, 4),
+            "gemm_only_total_ms": round(gemm_only, 3),
+            "events_gemm": {"total_ms": round(g_total, 3),
+                            "efficiency": round(gemm_only / g_total, 4),
+                            "gemm_ms_mean": round(g_ms, 4),
+                            "gemm_slowdown": round(g_ms / gl.alone_ms, 3),
+                            "first_layer_ms": round(g_per_layer[0], 4),
+                            "per_layer_ms_mean": round(sum(g_per_layer[1:]) /
+                                                       (len(g_per_layer) - 1), 4)},
+            "marked_gemm": {"total_ms": round(gm_total, 3),
+                            "efficiency": round(gemm_only / gm_total, 4),
+                            "gemm_ms_mean": round(gm_ms, 4),
+                            "gemm_slowdown": round(gm_ms / gl.alone_ms, 3)},
+        }
+        work[0] = spin_work
     bad = wl.verify_restored(layers, ids, targets)
     layers.refill()
     # Through the engine, default modes, gated on device layer words.
@@ -576,17 +752,28 @@ def leg_layerwise(xfer, seed):
         eng.batch_load_kv_blocks("lw", 0, 0, st.shm_name(), names, tg_l, hashes)
         for l in range(shape.layers):
             lw.wait_on_device(compute, l, 10_000_000, timed_out.ptr + 4 * l)
-            spin(compute, compute_us)
+            layer_work(l)
         done.record(compute)
         done.synchronize()
         while not st.is_ready():
             time.sleep(0.0001)
         if st.get_state() != 1 or timed_out.download().any():
             raise RuntimeError("engine layer-wise restore failed or a device wait timed out")
-        return start.elapsed_ms(done)
+        return start.elapsed_ms(done), work_ms()
 
     run_engine()
-    engine_total = min(run_engine() for _ in range(3))
+    engine_total, _ = min(run_engine() for _ in range(3))
+    if gl is not None:
+        work[0] = gl
+        run_engine()
+        ge_total, ge_ms = min(run_engine() for _ in range(3))
+        gemm_res["engine_gemm"] = {"total_ms": round(ge_total, 3),
+                                   "efficiency": round(gemm_res["gemm_only_total_ms"] / ge_total,
+                                                       4),
+                                   "gemm_ms_mean": round(ge_ms, 4),
+                                   "gemm_slowdown": round(ge_ms / gl.alone_ms, 3)}
+        work[0] = spin_work
+        gl.close()
     bad += wl.verify_restored(layers, ids, targets)
     eng.close()
     lw.close()
@@ -610,6 +797,7 @@ def leg_layerwise(xfer, seed):
         "per_layer_ms_mean": round(sum(per_layer[1:]) / (len(per_layer) - 1), 4),
         "per_layer_ms_max": round(max(per_layer[1:]), 4),
         "layer_bytes": n * 2 * shape.bytes_per_block,
+        **gemm_res,
         "bit_exact": bad == 0,
     }
     compute.close()
@@ -857,10 +1045,8 @@ def leg_two_process(layers, ids, targets, P, reps=4, server_args=()):
     start_load_kv / get_finished do (worker.py:148-286).  The restore time
     runs from the Load request to the LoadState reading ready; the first
     layer from the request to layer 0 reading done in a layered LoadState.
-    Measured over gRPC, and over the server's native endpoint for the same
-    requests (--fast-socket)."""
+    Measured over gRPC (the library's native HTTP/2 server)."""
     import hashlib
-    import tempfile
 
     from pegaflow_amd import ipc
     from pegaflow_amd import workload as wl
@@ -872,13 +1058,12 @@ def leg_two_process(layers, ids, targets, P, reps=4, server_args=()):
     handles = [ipc.export_tensor(b.ptr, shape.layer_bytes, 0) for b in layers.bufs]
     ids_l, targets_l = [int(i) for i in ids], [int(t) for t in targets]
     layers.refill()
-    sock = os.path.join(tempfile.mkdtemp(prefix="pega_bench_"), "engine.sock")
-    p, addr = _start_server((reps + 2) * P + (256 << 20), "--fast-socket", sock, *server_args)
+    p, addr = _start_server((reps + 2) * P + (256 << 20), *server_args)
     out = {"what": "llama prefix saved and restored by hash through the engine server in a "
                    "second process that maps the 32 layer tensors through HIP IPC; restore "
                    "timed from the Load request to the LoadState reading ready, median of the "
-                   "warm calls; over gRPC (the library's native HTTP/2 server), and over the "
-                   "server's native Unix-socket endpoint (fast_path); engine default modes"}
+                   "warm calls; over gRPC (the library's native HTTP/2 server); engine "
+                   "default modes"}
     med = lambda v: statistics.median(v[1:])  # noqa: E731
 
     def measure(client, tag):
@@ -928,9 +1113,6 @@ def leg_two_process(layers, ids, targets, P, reps=4, server_args=()):
                 assert ok, msg
             out["register_ms"] = round((time.perf_counter() - t0) * 1e3, 1)
             out.update(measure(client, b"rpc"))
-            with EngineRpcClient(f"http://{addr}", connect_timeout_s=30,
-                                 fast_socket=sock) as fast:
-                out["fast_path"] = measure(fast, b"fast")
             ok, msg = client.unregister_context("bench")
             assert ok, msg
             client.shutdown()
@@ -939,8 +1121,6 @@ def leg_two_process(layers, ids, targets, P, reps=4, server_args=()):
         if p.poll() is None:
             p.kill()
             p.wait(10)
-        shutil.rmtree(os.path.dirname(sock), ignore_errors=True)
-    out["bit_exact"] = out["bit_exact"] and out["fast_path"]["bit_exact"]
     return out
 
 
@@ -1465,6 +1645,35 @@ def cpu_baseline(shape, ids, targets, n_layers, seed, device=0):
     }
 
 
+def run_leg(args):
+    """One workload on its own (--leg): its JSON object on stdout."""
+    from pegaflow_amd import runtime
+    from pegaflow_amd.transfer import TransferContext
+    from pegaflow_amd import workload as wl
+
+    runtime.init(0)
+    xfer = TransferContext(0, staging_bytes=args.staging_mib << 20)
+    simple = {"gpt2": leg_gpt2, "layerwise": leg_layerwise, "mla": leg_mla, "tp8": leg_tp_rank}
+    if args.leg in simple:
+        out = simple[args.leg](xfer, args.seed)
+    else:
+        shape = wl.LLAMA3_8B
+        layers = wl.DeviceLayers(shape, base_seed=args.seed)
+        ids, targets = wl.draw_blocks(shape.num_blocks, 640, args.seed)
+        P = wl.payload_bytes(layers.regs, 640)
+        if args.leg == "fragmentation":
+            out = leg_fragmentation(layers, xfer, args.seed)
+        elif args.leg == "engine":
+            out = leg_engine(layers, ids, targets, P)
+        elif args.leg == "two_process":
+            out = leg_two_process(layers, ids, targets, P)
+        else:
+            out = leg_disk(layers, ids, targets, P)
+        layers.close()
+    xfer.close()
+    print(json.dumps({args.leg: out}), flush=True)
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -1477,7 +1686,10 @@ def main():
         profile_kernels(args.profile, args.seed)
         return
     if args.interference_study:
-        interference_study()
+        interference_study(args.study_engines, args.study_victims)
+        return
+    if args.leg:
+        run_leg(args)
         return
 
     # The single-block latency benchmark runs as its own process, before this

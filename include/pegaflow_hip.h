@@ -273,8 +273,9 @@ typedef struct pf_layer_xfer {
  *                 packed staging slots, and the host link is crossed only by
  *                 DMA copies of host-contiguous runs; the call is cut into
  *                 slices that may span layers.  With the host side in pinned
- *                 memory the copies run on the device's preferred copy
- *                 engine for their direction, driven from the calling
+ *                 memory the copies run on a fast copy engine per
+ *                 direction that the runtime's own copies do not use
+ *                 (pf_copy_engines), driven from the calling
  *                 thread (a load returns once its copies are done and its
  *                 last kernels are issued); otherwise through HIP, slices
  *                 alternating between the context's two streams.  Unlike
@@ -375,11 +376,15 @@ int pf_xfer_set_kernel_shape(pf_xfer* xfer, uint32_t threads, uint32_t unroll);
 int pf_xfer_set_max_grid(pf_xfer* xfer, uint32_t max_workgroups);
 /* The copy engines (HSA SDMA engine id bits, from hsa_amd_sdma_engine_id_t)
  * the staged mode's copies run on for `device`: device to host, then host to
- * device; one each, different where the device allows (the environment
- * variable PEGAFLOW_COPY_ENGINES="<d2h>,<h2d>" names others, one or two bits
- * each, slices alternating between two); both 0 when they are not known
- * (the staged mode then copies through HIP).  No counterpart in the reference
- * (its copies are cuMemcpy calls); bench_copy_engines measures each engine. */
+ * device; one each, different where the device allows.  By default two of
+ * the four fast engines (0-3 on MI355X) that the runtime's own copies do not
+ * use (hipMemcpyAsync takes the lowest engine of each preferred set), so a
+ * model's small copies beside a staged transfer do not queue behind its
+ * slices; the environment variable PEGAFLOW_COPY_ENGINES="<d2h>,<h2d>" or
+ * pf_set_copy_engines names others, one or two bits each, slices alternating
+ * between two.  Both 0 when they are not known (the staged mode then copies
+ * through HIP).  No counterpart in the reference (its copies are cuMemcpy
+ * calls); bench_copy_engines measures each engine. */
 int pf_copy_engines(int device, uint32_t* d2h_engine, uint32_t* h2d_engine);
 /* Chooses the copy engines of the staged mode on `device`, per direction a
  * mask of one or two engine id bits (0 keeps that direction's choice), from
@@ -709,31 +714,19 @@ int pf_engine_stats_get(pf_engine* e, pf_engine_stats* out);
 int pf_engine_wait_idle(pf_engine* e);
 
 /* ------------------------------------------------------------------------ */
-/* Native endpoint for the per-step requests (no counterpart in the          */
-/* reference, whose server is native: service.rs:133-405).  Serves Load,     */
-/* Save and Health for an engine from the library's own threads on a         */
-/* Unix-domain socket, bypassing a Python gRPC stack.  Frames, little endian: */
-/* request = u32 length of what follows, u8 method, then the engine.proto    */
-/* LoadRequest / SaveRequest bytes (none for Health); reply = u32 length,    */
-/* u8 status (PF_OK or PF_ERR_*), then the error message.  Requests mean     */
-/* what the gRPC service's Load and Save mean (service.rs:184-250).          */
+/* The engine's decoder of the Engine service's request bytes (no           */
+/* counterpart in the reference, whose tonic service decodes with prost:    */
+/* service.rs:184-250).  Requests mean what the gRPC service's Load and Save */
+/* mean.                                                                     */
 /* ------------------------------------------------------------------------ */
-enum { PF_FAST_LOAD = 1, PF_FAST_SAVE = 2, PF_FAST_HEALTH = 3 };
-#define PF_FAST_MAX_FRAME (256u << 20)
-typedef struct pf_fastpath pf_fastpath;
-/* Listens on socket_path (a stale socket file there is replaced; the file is
- * created mode 0600 and removed at stop). */
-int pf_fastpath_start(pf_engine* engine, const char* socket_path,
-                      pf_fastpath** out);
-/* Stops listening, closes every connection and waits for their threads. */
-int pf_fastpath_stop(pf_fastpath* fastpath);
-/* Requests served so far. */
-uint64_t pf_fastpath_served(const pf_fastpath* fastpath);
-/* One request in the same encoding (method PF_FAST_*, the message bytes
- * without the frame), served on the calling thread: what the endpoint does
- * with a frame, for a server that receives the bytes itself (the gRPC
- * service's Load and Save, service.rs:184-250).  A request that does not
- * decode fails with PF_ERR_MALFORMED. */
+enum { PF_REQUEST_LOAD = 1, PF_REQUEST_SAVE = 2, PF_REQUEST_HEALTH = 3 };
+/* Largest request message the native gRPC server accepts. */
+#define PF_REQUEST_MAX_BYTES (256u << 20)
+/* One request (method PF_REQUEST_*; the engine.proto LoadRequest or
+ * SaveRequest message bytes, none for Health), served on the calling
+ * thread, for a server that receives the bytes itself (the native gRPC
+ * server's Load and Save).  A request that does not decode fails with
+ * PF_ERR_MALFORMED. */
 int pf_engine_serve_request(pf_engine* engine, uint32_t method,
                             const uint8_t* request, uint64_t size);
 

@@ -60,9 +60,9 @@ MODE_NAMES = {
 LAYOUT_SPLIT, LAYOUT_CONTIGUOUS, LAYOUT_STRIDED = 0, 1, 2
 
 # Pinned allocation flags.
-# Methods of the native endpoint (pf_fastpath_start).
-FAST_LOAD, FAST_SAVE, FAST_HEALTH = 1, 2, 3
-FAST_MAX_FRAME = 256 << 20
+# Request methods of pf_engine_serve_request (PF_REQUEST_*).
+REQUEST_LOAD, REQUEST_SAVE, REQUEST_HEALTH = 1, 2, 3
+REQUEST_MAX_BYTES = 256 << 20
 # Chunks one pf_load_layers_noalloc call may plan (its static scratch).
 NOALLOC_MAX_CHUNKS = 65536
 PINNED_DEFAULT = 0
@@ -321,9 +321,6 @@ SIGNATURES = {
     "pf_engine_batch_save": (i32, [vp, cs, u64, i32, ctypes.POINTER(SaveLayer), u32]),
     "pf_engine_batch_load": (i32, [vp, cs, u64, i32, cs, ctypes.POINTER(cs), u32, vp, vp, vp,
                                    u64]),
-    "pf_fastpath_start": (i32, [vp, ctypes.c_char_p, pvp]),
-    "pf_fastpath_stop": (i32, [vp]),
-    "pf_fastpath_served": (u64, [vp]),
     "pf_engine_serve_request": (i32, [vp, u32, ctypes.c_char_p, u64]),
     "pf_grpc_start": (i32, [vp, cs, GRPC_HANDLER, vp, pvp]),
     "pf_grpc_port": (i32, [vp]),

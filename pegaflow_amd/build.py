@@ -28,7 +28,7 @@ SOURCES = [
     "pf_load_state.cpp",
     "pf_engine.cpp",
     "pf_disk.cpp",
-    "pf_fastpath.cpp",
+    "pf_requests.cpp",
     "pf_hpack.cpp",
     "pf_grpc.cpp",
 ]

@@ -392,7 +392,7 @@ bool Conn::handle(uint8_t type, uint8_t flags, uint32_t sid, std::string& payloa
       if (it == streams_.end() || !it->second.headers_done) return true;  // reset or unknown
       Stream& st = it->second;
       if (!st.rejected) {
-        if (st.data.size() + n > PF_FAST_MAX_FRAME + 5ull) {
+        if (st.data.size() + n > PF_REQUEST_MAX_BYTES + 5ull) {
           st.rejected = true;
           st.data.clear();
           st.data.shrink_to_fit();
@@ -597,7 +597,7 @@ bool Conn::headers_complete(uint32_t sid, Stream& st) {
 void Conn::complete(uint32_t sid, Stream&& st) {
   if (st.rejected) {
     reply(sid, kResourceExhausted,
-          strf("Received message larger than max (limit %u bytes)", PF_FAST_MAX_FRAME), nullptr,
+          strf("Received message larger than max (limit %u bytes)", PF_REQUEST_MAX_BYTES), nullptr,
           0);
     return;
   }
@@ -637,7 +637,7 @@ void Server::dispatch(const std::shared_ptr<Conn>& c, uint32_t sid, const std::s
   const auto* req = reinterpret_cast<const uint8_t*>(data.data()) + 5;
   const size_t size = data.size() - 5;
   if (method == "Load" || method == "Health") {
-    const int rc = method == "Load" ? pf_engine_serve_request(engine, PF_FAST_LOAD, req, size)
+    const int rc = method == "Load" ? pf_engine_serve_request(engine, PF_REQUEST_LOAD, req, size)
                                     : PF_OK;
     std::string msg = rc == PF_OK ? std::string() : std::string(pf_last_error());
     // On the connection's thread the reply may not wait for window updates
@@ -652,7 +652,7 @@ void Server::dispatch(const std::shared_ptr<Conn>& c, uint32_t sid, const std::s
     workers->post([this, c, sid, job, trace, opened, received] {
       const auto started = std::chrono::steady_clock::now();
       const int rc = pf_engine_serve_request(
-          engine, PF_FAST_SAVE, reinterpret_cast<const uint8_t*>(job->data()) + 5,
+          engine, PF_REQUEST_SAVE, reinterpret_cast<const uint8_t*>(job->data()) + 5,
           job->size() - 5);
       c->reply_rc(sid, rc, rc == PF_OK ? std::string() : std::string(pf_last_error()));
       if (trace) trace_request("Save", job->size() - 5, opened, received, started);

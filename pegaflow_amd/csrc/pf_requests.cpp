@@ -1,35 +1,14 @@
-// pf_fastpath.cpp — a native endpoint for the engine's per-step requests.
-//
-// The Engine gRPC service runs in Python (pegaflow_amd/rpc/server.py), and a
-// Load through grpcio costs about 0.7 ms end to end on the MI355X box's host
-// (0.4 ms for an empty Health call): as long as the copy of a whole Llama
-// layer.  The reference serves the same RPCs from Rust (tonic,
-// pegaflow-server/src/service.rs:133-405).  This endpoint serves Load, Save
-// and Health from the library's own threads on a Unix-domain socket, with
-// each request in the Engine service's protobuf encoding (engine.proto
-// LoadRequest / SaveRequest), so a client in the inference process can skip
-// the Python stack for the requests it makes every step.  Registration,
-// queries and the rest stay on gRPC.
-//
-// Framing, little endian:
-//   request: u32 length of what follows, u8 method (PF_FAST_*), message bytes
-//   reply:   u32 length of what follows, u8 status (PF_OK or a PF_ERR_*
-//            code), the error message (empty on success)
-// A frame longer than PF_FAST_MAX_FRAME, or one that does not parse, gets an
-// error reply; a connection that sends a truncated frame is closed.
-#include <poll.h>
-#include <sys/socket.h>
-#include <sys/stat.h>
-#include <sys/un.h>
-#include <unistd.h>
+// pf_requests.cpp — the engine's own decoder of the Engine service's Load
+// and Save request bytes (engine.proto LoadRequest / SaveRequest), served on
+// the calling thread: the native gRPC server (pf_grpc.cpp) hands each Load
+// and Save message to pf_engine_serve_request, which decodes it and calls
+// the engine as the reference's service does (service.rs:184-250).  Every
+// read is bounds-checked; a message that does not decode fails with
+// PF_ERR_MALFORMED.
 
-#include <atomic>
-#include <cerrno>
 #include <cstdio>
 #include <cstring>
-#include <mutex>
 #include <string>
-#include <thread>
 #include <vector>
 
 #include "pf_common.h"
@@ -403,112 +382,6 @@ int serve_save(pf_engine* e, const uint8_t* p, size_t n) {
                               static_cast<uint32_t>(layers.size()));
 }
 
-bool read_full(int fd, void* buf, size_t n) {
-  uint8_t* p = static_cast<uint8_t*>(buf);
-  while (n > 0) {
-    const ssize_t r = ::recv(fd, p, n, 0);
-    if (r > 0) {
-      p += r;
-      n -= static_cast<size_t>(r);
-    } else if (r < 0 && errno == EINTR) {
-      continue;
-    } else {
-      return false;
-    }
-  }
-  return true;
-}
-
-bool write_full(int fd, const void* buf, size_t n) {
-  const uint8_t* p = static_cast<const uint8_t*>(buf);
-  while (n > 0) {
-    const ssize_t r = ::send(fd, p, n, MSG_NOSIGNAL);
-    if (r > 0) {
-      p += r;
-      n -= static_cast<size_t>(r);
-    } else if (r < 0 && errno == EINTR) {
-      continue;
-    } else {
-      return false;
-    }
-  }
-  return true;
-}
-
-bool reply(int fd, int status, const std::string& msg) {
-  std::string out(5 + msg.size(), '\0');
-  const uint32_t len = static_cast<uint32_t>(1 + msg.size());
-  std::memcpy(&out[0], &len, 4);  // little endian on this platform
-  out[4] = static_cast<char>(status);
-  std::memcpy(&out[5], msg.data(), msg.size());
-  return write_full(fd, out.data(), out.size());
-}
-
-}  // namespace
-
-struct pf_fastpath {
-  pf_engine* engine = nullptr;
-  std::string path;
-  int listen_fd = -1;
-  int stop_pipe[2] = {-1, -1};
-  std::thread acceptor;
-  std::mutex mu;
-  std::vector<std::thread> conns;  // joined at stop (clients connect once each)
-  std::vector<int> conn_fds;       // open connections
-  std::atomic<uint64_t> served{0};
-};
-
-namespace {
-
-void serve_connection(pf_fastpath* f, int fd) {
-  std::vector<uint8_t> buf;
-  for (;;) {
-    uint32_t len = 0;
-    if (!read_full(fd, &len, 4) || len == 0) break;
-    if (len > PF_FAST_MAX_FRAME + 1u) {
-      (void)reply(fd, PF_ERR_INVALID_ARGUMENT,
-                  strf("request of %u bytes exceeds %u", len, (unsigned)PF_FAST_MAX_FRAME));
-      break;  // the rest of the frame cannot be skipped reliably
-    }
-    const auto t_recv = std::chrono::steady_clock::now();
-    buf.resize(len);
-    if (!read_full(fd, buf.data(), len)) break;
-    const uint8_t method = buf[0];
-    const int rc = pf_engine_serve_request(f->engine, method, buf.data() + 1, len - 1);
-    f->served.fetch_add(1, std::memory_order_relaxed);
-    const auto t_reply = std::chrono::steady_clock::now();
-    if (!reply(fd, rc, rc == PF_OK ? std::string() : std::string(pf_last_error()))) break;
-    if (tracing())
-      std::fprintf(stderr, "[pegaflow] fast request method=%u bytes=%u at=%.0fus reply=%.0fus\n",
-                   method, len, mono_us(t_recv), mono_us(t_reply));
-  }
-  // Off the list before the close, so stop() never shuts down a descriptor
-  // number the process has reused.
-  std::lock_guard<std::mutex> lk(f->mu);
-  for (size_t i = 0; i < f->conn_fds.size(); ++i)
-    if (f->conn_fds[i] == fd) {
-      f->conn_fds[i] = f->conn_fds.back();
-      f->conn_fds.pop_back();
-      break;
-    }
-  ::close(fd);
-}
-
-void accept_loop(pf_fastpath* f) {
-  pollfd fds[2] = {{f->listen_fd, POLLIN, 0}, {f->stop_pipe[0], POLLIN, 0}};
-  for (;;) {
-    const int r = ::poll(fds, 2, -1);
-    if (r < 0 && errno == EINTR) continue;
-    if (r < 0 || (fds[1].revents & (POLLIN | POLLHUP | POLLERR))) return;
-    if (!(fds[0].revents & POLLIN)) continue;
-    const int c = ::accept(f->listen_fd, nullptr, nullptr);
-    if (c < 0) continue;
-    std::lock_guard<std::mutex> lk(f->mu);
-    f->conn_fds.push_back(c);
-    f->conns.emplace_back(serve_connection, f, c);
-  }
-}
-
 }  // namespace
 
 extern "C" {
@@ -519,70 +392,11 @@ int pf_engine_serve_request(pf_engine* engine, uint32_t method, const uint8_t* r
   if (size > 0 && !request) return fail(PF_ERR_INVALID_ARGUMENT, "null request");
   clear_error();
   switch (method) {
-    case PF_FAST_LOAD: return serve_load(engine, request, static_cast<size_t>(size));
-    case PF_FAST_SAVE: return serve_save(engine, request, static_cast<size_t>(size));
-    case PF_FAST_HEALTH: return PF_OK;
+    case PF_REQUEST_LOAD: return serve_load(engine, request, static_cast<size_t>(size));
+    case PF_REQUEST_SAVE: return serve_save(engine, request, static_cast<size_t>(size));
+    case PF_REQUEST_HEALTH: return PF_OK;
     default: return fail(PF_ERR_INVALID_ARGUMENT, strf("unknown method %u", method));
   }
-}
-
-int pf_fastpath_start(pf_engine* engine, const char* socket_path, pf_fastpath** out) {
-  if (!engine || !socket_path || !out) return fail(PF_ERR_INVALID_ARGUMENT, "null argument");
-  *out = nullptr;
-  sockaddr_un addr{};
-  addr.sun_family = AF_UNIX;
-  if (std::strlen(socket_path) == 0 || std::strlen(socket_path) >= sizeof(addr.sun_path))
-    return fail(PF_ERR_INVALID_ARGUMENT,
-                strf("socket path must be 1..%zu bytes", sizeof(addr.sun_path) - 1));
-  std::strncpy(addr.sun_path, socket_path, sizeof(addr.sun_path) - 1);
-  auto* f = new pf_fastpath();
-  f->engine = engine;
-  f->path = socket_path;
-  auto bail = [&](const std::string& what) {
-    const int err = errno;
-    if (f->listen_fd >= 0) ::close(f->listen_fd);
-    if (f->stop_pipe[0] >= 0) ::close(f->stop_pipe[0]);
-    if (f->stop_pipe[1] >= 0) ::close(f->stop_pipe[1]);
-    delete f;
-    return fail(PF_ERR_INVALID_ARGUMENT, what + ": " + std::strerror(err));
-  };
-  if (::pipe(f->stop_pipe) != 0) return bail("pipe");
-  f->listen_fd = ::socket(AF_UNIX, SOCK_STREAM | SOCK_CLOEXEC, 0);
-  if (f->listen_fd < 0) return bail("socket");
-  // A stale socket file from an earlier server is replaced; anything else at
-  // the path is left alone and the bind fails.
-  struct stat st{};
-  if (::lstat(socket_path, &st) == 0 && S_ISSOCK(st.st_mode)) ::unlink(socket_path);
-  if (::bind(f->listen_fd, reinterpret_cast<sockaddr*>(&addr), sizeof(addr)) != 0)
-    return bail(std::string("bind ") + socket_path);
-  (void)::chmod(socket_path, 0600);
-  if (::listen(f->listen_fd, 64) != 0) return bail("listen");
-  f->acceptor = std::thread(accept_loop, f);
-  *out = f;
-  return PF_OK;
-}
-
-int pf_fastpath_stop(pf_fastpath* f) {
-  if (!f) return PF_OK;
-  const char b = 1;
-  (void)!::write(f->stop_pipe[1], &b, 1);
-  if (f->acceptor.joinable()) f->acceptor.join();
-  {
-    std::lock_guard<std::mutex> lk(f->mu);
-    for (int fd : f->conn_fds) ::shutdown(fd, SHUT_RDWR);
-  }
-  for (std::thread& t : f->conns)
-    if (t.joinable()) t.join();
-  ::close(f->listen_fd);
-  ::close(f->stop_pipe[0]);
-  ::close(f->stop_pipe[1]);
-  ::unlink(f->path.c_str());
-  delete f;
-  return PF_OK;
-}
-
-uint64_t pf_fastpath_served(const pf_fastpath* f) {
-  return f ? f->served.load(std::memory_order_relaxed) : 0;
 }
 
 }  // extern "C"

@@ -256,15 +256,33 @@ EngineDevice discover_engines(int device) {
   uint32_t avail_d2h = 0, avail_h2d = 0;
   (void)hsa_amd_memory_copy_engine_status(s.cpu, s.gpu, &avail_d2h);
   (void)hsa_amd_memory_copy_engine_status(s.gpu, s.cpu, &avail_h2d);
-  // Saves and loads run at once: give them different engines where the
-  // preferred sets allow.
-  const uint32_t h0 = lowest_bit(h2d);
-  const uint32_t d2h_rest = d2h & ~h0;
-  const uint32_t d0 = lowest_bit(d2h_rest ? d2h_rest : d2h);
-  // One engine per direction.  A second one per direction was measured and
-  // dropped: two device-to-host engines saved the Llama prefix at 45 GB/s
-  // against 56 on one, and with four engines busy a save and a restore at
-  // once fell from 95 to 66 GB/s.
+  // The model's own copies (hipMemcpyAsync, in this process or in the
+  // serving process beside it) run on the lowest engine of each preferred
+  // set: measured on MI355X, a staged save on engine 1 slowed a 64 KiB
+  // device-to-host hipMemcpyAsync every 0.5 ms 8.3x and fell to 26 GB/s
+  // itself, and any staged copy on engine 0 slowed a 64 KiB host-to-device
+  // one 6x; on engines 2 and 3 both stayed within 1.25x and the staged
+  // copies at 56 GB/s.  So the staged copies take the fast engines the
+  // runtime's copies do not use: engines 0-3 move 57 GB/s each way, the
+  // others 7-51 GB/s.  One engine per direction, different for the two
+  // directions, so a save and a load run at once.  A second engine per
+  // direction was measured and dropped: two device-to-host engines saved
+  // the Llama prefix at 45 GB/s against 56 on one, and with four engines
+  // busy a save and a restore at once fell from 95 to 66 GB/s.
+  constexpr uint32_t kFastEngines = 0xF;
+  const uint32_t runtime_own = lowest_bit(d2h) | lowest_bit(h2d);
+  const uint32_t spare = kFastEngines & ~runtime_own & avail_d2h & avail_h2d;
+  uint32_t d0 = 0, h0 = 0;
+  if (spare) {
+    d0 = 1u << (31 - __builtin_clz(spare));  // the highest spare engine
+    const uint32_t rest = spare & ~d0;
+    h0 = rest ? lowest_bit(rest) : d0;
+  } else {
+    // No spare fast engine: the preferred ones, different where they allow.
+    h0 = lowest_bit(h2d);
+    const uint32_t d2h_rest = d2h & ~h0;
+    d0 = lowest_bit(d2h_rest ? d2h_rest : d2h);
+  }
   d.engine[0][0] = d.engine[0][1] = d0;
   d.engine[1][0] = d.engine[1][1] = h0;
   // PEGAFLOW_COPY_ENGINES="<d2h>,<h2d>" (engine id bit masks, one or two

@@ -250,34 +250,13 @@ class PegaEngine:
     def wait_idle(self) -> None:
         _raise(lib().pf_engine_wait_idle(self._h))
 
-    # -- native endpoint for Load / Save (no counterpart in the reference) --
-    def start_fast_path(self, socket_path: str) -> None:
-        """Serves this engine's Load, Save and Health requests on a
-        Unix-domain socket from native threads (pf_fastpath_start): the
-        requests in engine.proto's encoding, without the Python gRPC stack.
-        Stopped by stop_fast_path or close."""
-        if getattr(self, "_fast", None):
-            raise RuntimeError("fast path already started")
-        h = ctypes.c_void_p()
-        _raise(lib().pf_fastpath_start(self._h, socket_path.encode(), ctypes.byref(h)))
-        self._fast = h.value
-
-    def stop_fast_path(self) -> None:
-        if getattr(self, "_fast", None):
-            lib().pf_fastpath_stop(self._fast)
-        self._fast = None
-
-    def fast_path_served(self) -> int:
-        return int(lib().pf_fastpath_served(self._fast)) if getattr(self, "_fast", None) else 0
-
     def serve_request(self, method: int, request: bytes) -> None:
-        """One Load or Save request (method FAST_LOAD / FAST_SAVE) in
+        """One Load or Save request (method REQUEST_LOAD / REQUEST_SAVE) in
         engine.proto's encoding, decoded and served natively on this thread,
-        as the fast path serves a frame (pf_engine_serve_request)."""
+        as the native gRPC server serves one (pf_engine_serve_request)."""
         _raise(lib().pf_engine_serve_request(self._h, method, request, len(request)))
 
     def close(self) -> None:
-        self.stop_fast_path()
         if self._h:
             lib().pf_engine_destroy(self._h)
         self._h = None

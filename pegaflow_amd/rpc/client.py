@@ -8,9 +8,6 @@ and a dict for query — so a connector written against it runs unchanged.
 from __future__ import annotations
 
 import operator
-import socket
-import struct
-import threading
 
 import grpc
 
@@ -119,48 +116,6 @@ def encode_load_request(instance_id: str, tp_rank: int, device_id: int, load_sta
             _hashes_part(proto.LoadRequest, block_hashes))
 
 
-# Engine status -> the gRPC status the service reports it as (service.rs:77-88).
-_STATUS_NAMES = {1: "INVALID_ARGUMENT", 4: "FAILED_PRECONDITION", 5: "FAILED_PRECONDITION",
-                 6: "FAILED_PRECONDITION"}
-
-
-class FastChannel:
-    """A connection to a server's native endpoint (pf_fastpath_start): Load,
-    Save and Health requests in engine.proto's encoding, framed as u32
-    length + u8 method, answered with u32 length + u8 status + message.
-    One request at a time per channel (a lock)."""
-
-    def __init__(self, path: str, timeout_s: float | None = None):
-        self._sock = socket.socket(socket.AF_UNIX, socket.SOCK_STREAM)
-        self._sock.settimeout(timeout_s)
-        try:
-            self._sock.connect(path)
-        except OSError as e:
-            self._sock.close()
-            raise RuntimeError(f"failed to connect to the fast endpoint {path}: {e}") from None
-        self._lock = threading.Lock()
-
-    def _recv(self, n: int) -> bytes:
-        out = bytearray()
-        while len(out) < n:
-            chunk = self._sock.recv(n - len(out))
-            if not chunk:
-                raise RuntimeError("fast endpoint closed the connection")
-            out += chunk
-        return bytes(out)
-
-    def call(self, method: int, payload: bytes = b"") -> tuple[int, str]:
-        frame = struct.pack("<IB", len(payload) + 1, method) + payload
-        with self._lock:
-            self._sock.sendall(frame)
-            length, status = struct.unpack("<IB", self._recv(5))
-            message = self._recv(length - 1).decode("utf-8", "replace")
-        return status, message
-
-    def close(self) -> None:
-        self._sock.close()
-
-
 def _serialize(request) -> bytes:
     """Requests are messages, or wire bytes already encoded."""
     return request if isinstance(request, bytes) else request.SerializeToString()
@@ -178,14 +133,8 @@ class EngineRpcClient:
     does not answer within `connect_timeout_s`.  `endpoint` is
     "http://host:port" or "host:port"."""
 
-    _fast: FastChannel | None = None  # the native endpoint's connection, if any
-
     def __init__(self, endpoint: str | None = None, timeout_s: float | None = None,
-                 connect_timeout_s: float = 2.0, fast_socket: str | None = None):
-        """``fast_socket`` (no counterpart in the reference): the server's
-        native endpoint (pegaflow-server --fast-socket); load, save and health
-        then go there, with the same results and errors, and everything else
-        over gRPC."""
+                 connect_timeout_s: float = 2.0):
         self._endpoint = endpoint or "http://127.0.0.1:50055"
         self.timeout_s = timeout_s
         self._channel = grpc.insecure_channel(
@@ -204,30 +153,9 @@ class EngineRpcClient:
                                            request_serializer=_serialize,
                                            response_deserializer=proto.messages[resp].FromString)
             for rpc, req, resp in proto.METHODS}
-        if fast_socket:
-            try:
-                self._fast = FastChannel(fast_socket, timeout_s)
-            except RuntimeError:
-                self._channel.close()
-                raise
 
     def close(self) -> None:
-        if self._fast is not None:
-            self._fast.close()
         self._channel.close()
-
-    def _fast_call(self, method: str, method_id: int, payload: bytes = b""):
-        """(ok, message) from the native endpoint; engine errors raise as the
-        gRPC path raises them."""
-        try:
-            status, message = self._fast.call(method_id, payload)
-        except OSError as e:
-            raise RuntimeError(f"{method} RPC failed: {e}") from None
-        if status == 0:
-            return True, ""
-        code = _STATUS_NAMES.get(status, "INTERNAL")
-        raise RuntimeError(f"{method} RPC failed: status: StatusCode.{code}, "
-                           f"message: {message!r}")
 
     def __enter__(self):
         return self
@@ -253,8 +181,6 @@ class EngineRpcClient:
         return self._endpoint
 
     def health(self):
-        if self._fast is not None:
-            return self._fast_call("health", 3)
         return self._status("health", self._call("Health", "health", proto.HealthRequest()))
 
     def register_context(self, instance_id: str, namespace: str, tp_rank: int, tp_size: int,
@@ -273,8 +199,6 @@ class EngineRpcClient:
     def save(self, instance_id: str, tp_rank: int, device_id: int, saves):
         """python/src/lib.rs:374-405: `saves` is [(layer_name, block_ids, block_hashes)]."""
         req = encode_save_request(instance_id, tp_rank, device_id, saves)
-        if self._fast is not None:
-            return self._fast_call("save", 2, req)
         return self._status("save", self._call("Save", "save", req))
 
     def load(self, instance_id: str, tp_rank: int, device_id: int, load_state_shm: str,
@@ -282,8 +206,6 @@ class EngineRpcClient:
         """python/src/lib.rs:417-446."""
         req = encode_load_request(instance_id, tp_rank, device_id, load_state_shm, layer_names,
                                   block_ids, block_hashes)
-        if self._fast is not None:
-            return self._fast_call("load", 1, req)
         return self._status("load", self._call("Load", "load", req))
 
     def query(self, instance_id: str, block_hashes):

@@ -97,7 +97,7 @@ class EngineService:
     def Save(self, req, context):
         try:
             if isinstance(req, bytes):
-                self.frontend.serve(_lib.FAST_SAVE, req)
+                self.frontend.serve(_lib.REQUEST_SAVE, req)
             else:
                 if not isinstance(req, proto.DecodedSave):
                     req = proto.decoded_save(req)
@@ -109,7 +109,7 @@ class EngineService:
     def Load(self, req, context):
         try:
             if isinstance(req, bytes):
-                self.frontend.serve(_lib.FAST_LOAD, req)
+                self.frontend.serve(_lib.REQUEST_LOAD, req)
             else:
                 self.frontend.load(req.instance_id, req.tp_rank, req.device_id,
                                    req.load_state_shm, req.layer_names, req.block_ids,
@@ -222,7 +222,7 @@ class Server:
                  pool_size: int = 30 << 30, host_pool: bool = False, unit_size_hint: int = 0,
                  max_workers: int = 16, dfs_root: str | None = None,
                  dfs_quota: int = 50 << 30, dfs_io_threads: int = 4,
-                 fast_socket: str | None = None, grpc_impl: str = "native",
+                 grpc_impl: str = "native",
                  save_mode: int | None = None, load_mode: int | None = None):
         self.engine = engine or PegaEngine(pool_size=pool_size, host_pool=host_pool,
                                            unit_size_hint=unit_size_hint)
@@ -231,10 +231,6 @@ class Server:
         if save_mode is not None or load_mode is not None:
             self.engine.set_transfer_modes(_lib.MODE_AUTO if save_mode is None else save_mode,
                                            _lib.MODE_AUTO if load_mode is None else load_mode)
-        # Load, Save and Health also on a native Unix-socket endpoint.
-        self.fast_socket = fast_socket
-        if fast_socket:
-            self.engine.start_fast_path(fast_socket)
         self.service = EngineService(self.engine, disk=bool(dfs_root))
         self.grpc = self.native = None
         if grpc_impl == "native":
@@ -264,7 +260,6 @@ class Server:
             pass
 
     def stop(self, grace: float = 1.0) -> None:
-        self.engine.stop_fast_path()
         if self.native is not None:
             self.native.stop()
         if self.grpc is not None:
@@ -301,9 +296,6 @@ def parse_args(argv=None):
     ap.add_argument("--grpc-impl", choices=("native", "python"), default="native",
                     help="serve gRPC from the library's native HTTP/2 server (default) or "
                          "from grpcio's")
-    ap.add_argument("--fast-socket", default=None,
-                    help="also serve Load, Save and Health natively on this Unix-domain "
-                         "socket path (EngineRpcClient(fast_socket=...))")
     ap.add_argument("--dfs-root", default=None,
                     help="directory of the disk tier (packed block files); the tier is on when "
                          f"this or --redis-url is given (default root {DEFAULT_DFS_ROOT})")
@@ -352,7 +344,7 @@ def main(argv=None) -> int:
     server = Server(args.addr, pool_size=args.pool_size, unit_size_hint=args.hint_value_size,
                     max_workers=args.max_workers, dfs_root=args.dfs_root,
                     dfs_quota=args.dfs_quota, dfs_io_threads=args.dfs_io_threads,
-                    fast_socket=args.fast_socket, grpc_impl=args.grpc_impl,
+                    grpc_impl=args.grpc_impl,
                     save_mode=_lib.MODE_NAMES[args.save_mode],
                     load_mode=_lib.MODE_NAMES[args.load_mode]).start()
     for sig in (signal.SIGINT, signal.SIGTERM):

@@ -247,12 +247,12 @@ def test_save_requests_share_repeated_lists(engine):
         (m.names[4], A, H),              # hashes equal to the layer before's
         (m.names[5], B, H),              # hashes shared along the chain
     ])
-    engine.serve_request(_lib.FAST_SAVE, req)
+    engine.serve_request(_lib.REQUEST_SAVE, req)
     want_ids = [A, A, B, B, A, B]
     # A second request whose layers are all alike.
     H2 = [h(i, b"req2") for i in range(5)]
     C = [11, 12, 13, 14, 15]
-    engine.serve_request(_lib.FAST_SAVE, _save_request("req", [(n, C, H2) for n in m.names]))
+    engine.serve_request(_lib.REQUEST_SAVE, _save_request("req", [(n, C, H2) for n in m.names]))
     assert engine.stats()["sealed_blocks"] == len(H) + len(H2)
     for hashes, per_layer in ((H, want_ids), (H2, [C] * m.n_layers)):
         for l in range(m.n_layers):
@@ -265,7 +265,7 @@ def test_save_requests_share_repeated_lists(engine):
     # A layer whose lists differ in length is refused as the reference does.
     bad = _save_request("req", [(m.names[0], A, H), (m.names[1], A[:3], H)])
     with pytest.raises(RuntimeError, match="block_ids length 3 does not match block_hashes 8"):
-        engine.serve_request(_lib.FAST_SAVE, bad)
+        engine.serve_request(_lib.REQUEST_SAVE, bad)
     m.close()
 
 

@@ -22,7 +22,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CSRC = os.path.join(ROOT, "pegaflow_amd", "csrc")
 LIB_SOURCES = [os.path.join(CSRC, f) for f in (
     "pf_layout.cpp", "pf_runtime.cpp", "pf_kernels.hip", "pf_transfer.cpp", "pf_load_state.cpp",
-    "pf_engine.cpp", "pf_disk.cpp", "pf_fastpath.cpp", "pf_hpack.cpp", "pf_grpc.cpp")]
+    "pf_engine.cpp", "pf_disk.cpp", "pf_requests.cpp", "pf_hpack.cpp", "pf_grpc.cpp")]
 NATIVE = os.path.join(ROOT, "tests", "native")
 # C++ sources that define device variables.
 DEVICE_CPP = {"pf_runtime.cpp"}

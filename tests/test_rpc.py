@@ -346,9 +346,9 @@ def _ld(field, payload):
     return _varint(field << 3 | 2) + _varint(len(payload)) + payload
 
 
-def test_engine_decoder_matches_the_full_parse(served_fast):
-    """The engine's request decoder (gRPC Save and Load, the native
-    endpoint) gives what protobuf's full parse gives (the service's Python
+def test_engine_decoder_matches_the_full_parse(served):
+    """The engine's request decoder (the native gRPC server's Save and Load,
+    pf_engine_serve_request) gives what protobuf's full parse gives (the service's Python
     path) for the canonical encoding and for unpacked ids, the name after
     the lists, a second name record (the last wins), unknown fields, the
     header last and an empty layer: each variant's result or error text is
@@ -358,10 +358,9 @@ def test_engine_decoder_matches_the_full_parse(served_fast):
     from google.protobuf.message import DecodeError
 
     from pegaflow_amd.rpc import proto
-    from pegaflow_amd.rpc.client import _STATUS_NAMES
     from pegaflow_amd.rpc.client import _varint as varint
 
-    srv, slow, _, path = served_fast
+    srv, slow = served
     _register(slow, "l0")
     _register(slow, "l1")
 
@@ -381,7 +380,7 @@ def test_engine_decoder_matches_the_full_parse(served_fast):
         return got[0] if got else ("OK", "")
 
     def native(method, wire):
-        status, msg = _raw(path, method, wire)
+        status, msg = _serve(srv.engine, method, wire)
         return ("OK", "") if status == 0 else (_STATUS_NAMES.get(status, "INTERNAL"), msg)
 
     hs = [b"x" * 32, b"y" * 32]
@@ -456,20 +455,19 @@ def test_engine_decoder_matches_the_full_parse(served_fast):
 
 
 # ---------------------------------------------------------------------------
-# The native endpoint for Load, Save and Health (pf_fastpath_start).
+# The engine's decoder of request bytes (pf_engine_serve_request), which the
+# native gRPC server hands Load and Save to.
 # ---------------------------------------------------------------------------
-@pytest.fixture(params=["native", "python"])
-def served_fast(tmp_path, request):
-    path = str(tmp_path / "pf.sock")
-    srv = Server("127.0.0.1:0", engine=PegaEngine(pool_size=64 << 20, host_pool=True),
-                 fast_socket=path, grpc_impl=request.param).start()
-    slow = EngineRpcClient(f"http://{srv.addr}")
-    fast = EngineRpcClient(f"http://{srv.addr}", fast_socket=path)
-    yield srv, slow, fast, path
-    fast.close()
-    slow.close()
-    srv.stop()
-    assert not os.path.exists(path)  # removed at stop
+# Engine status -> the gRPC status the service reports it as (service.rs:77-88).
+_STATUS_NAMES = {1: "INVALID_ARGUMENT", 4: "FAILED_PRECONDITION", 5: "FAILED_PRECONDITION",
+                 6: "FAILED_PRECONDITION"}
+
+
+def _serve(engine, method, payload):
+    """(status, error message) of one request through the engine's decoder."""
+    from pegaflow_amd._lib import last_error, load
+    rc = load().pf_engine_serve_request(engine._h, method, payload, len(payload))
+    return rc, ("" if rc == 0 else last_error())
 
 
 def _error(fn):
@@ -509,13 +507,13 @@ class _Decoded:
         return self._run("load", self.svc.Load, req)
 
 
-def test_fast_path_gives_the_grpc_results_and_errors(served_fast):
-    """Each request gives the same result and error text three ways: over
-    gRPC and over the native endpoint (both decoded by the engine) and
-    through the service's Python path for decoded messages."""
-    srv, slow, fast, _ = served_fast
+def test_grpc_gives_the_service_results_and_errors(served):
+    """Each request gives the same result and error text over gRPC (native:
+    decoded by the engine; python: by protobuf) and through the service's
+    Python path for decoded messages."""
+    srv, slow = served
     decoded = _Decoded(srv.service)
-    assert fast.health() == (True, "")
+    assert slow.health() == (True, "")
     _register(slow, "l0")
     _register(slow, "l1")
     cases = [
@@ -533,20 +531,18 @@ def test_fast_path_gives_the_grpc_results_and_errors(served_fast):
     for i, case in enumerate(cases):
         want = _error(lambda: case(decoded))
         assert _error(lambda: case(slow)) == want, f"case {i}: {want}"
-        assert _error(lambda: case(fast)) == want, f"case {i}: {want}"
-    assert "INVALID_ARGUMENT" in _error(lambda: cases[0](fast))
-    assert "block_ids length 2 does not match block_hashes 1" in _error(lambda: cases[1](fast))
-    assert "FAILED_PRECONDITION" in _error(lambda: cases[3](fast))
+    assert "INVALID_ARGUMENT" in _error(lambda: cases[0](slow))
+    assert "block_ids length 2 does not match block_hashes 1" in _error(lambda: cases[1](slow))
+    assert "FAILED_PRECONDITION" in _error(lambda: cases[3](slow))
     # Negative ids only, and an empty load: nothing to do, the same on both.
-    assert fast.save("i0", 0, 0, [("l0", [-1], [b"a"])]) == (True, "")
+    assert slow.save("i0", 0, 0, [("l0", [-1], [b"a"])]) == (True, "")
     st = PyLoadState()
-    assert fast.load("i0", 0, 0, st.shm_name(), ["l0"], [], []) == (True, "")
+    assert slow.load("i0", 0, 0, st.shm_name(), ["l0"], [], []) == (True, "")
     assert st.get_state() == 1
     st = PyLoadState()
     with pytest.raises(RuntimeError, match="missing KV block hash"):
-        fast.load("i0", 0, 0, st.shm_name(), ["l0"], [1], [b"abc"])
+        slow.load("i0", 0, 0, st.shm_name(), ["l0"], [1], [b"abc"])
     assert st.get_state() == -1  # the failure reaches the LoadState
-    assert srv.engine.fast_path_served() >= len(cases) + 4
 
 
 def _varint(n):
@@ -566,60 +562,36 @@ def _field(num, wt, payload):
     return _varint(num << 3 | wt) + (_varint(len(payload)) + payload if wt == 2 else payload)
 
 
-def _raw(path, method, payload, raw_len=None):
-    import socket
-    import struct
-
-    s = socket.socket(socket.AF_UNIX, socket.SOCK_STREAM)
-    s.settimeout(10)
-    s.connect(path)
-    n = len(payload) + 1 if raw_len is None else raw_len
-    s.sendall(struct.pack("<IB", n, method) + payload)
-    hdr = b""
-    while len(hdr) < 5:
-        chunk = s.recv(5 - len(hdr))
-        if not chunk:
-            s.close()
-            return None
-        hdr += chunk
-    length, status = struct.unpack("<IB", hdr)
-    msg = b""
-    while len(msg) < length - 1:
-        msg += s.recv(length - 1 - len(msg))
-    s.close()
-    return status, msg.decode()
-
-
-def test_fast_path_decodes_every_encoding(served_fast):
-    """Hand-built requests: fields out of order, ids packed and unpacked,
-    negative ids as 10-byte varints, unknown fields of every wire type; and
-    malformed, unknown and oversized requests get error replies."""
-    srv, slow, fast, path = served_fast
+def test_decoder_handles_every_encoding(served):
+    """Hand-built requests through the engine's decoder: fields out of order,
+    ids packed and unpacked, negative ids as 10-byte varints, unknown fields
+    of every wire type; and malformed and unknown requests are errors."""
+    srv, slow = served
+    eng = srv.engine
     _register(slow, "l0")
     _register(slow, "l1")
     layer = (_field(3, 2, b"h1") + _field(2, 0, 5) + _field(2, 0, -3) + _field(1, 2, b"l0") +
              _field(3, 2, b"h2") + _field(3, 2, b"h3") + _field(2, 2, _varint(16)) +
              _field(9, 0, 7) + _field(10, 1, b"\0" * 8) + _field(11, 5, b"\0" * 4))
     req = _field(4, 2, layer) + _field(3, 0, 0) + _field(1, 2, b"i0") + _field(2, 0, 0)
-    status, msg = _raw(path, 2, req)
+    status, msg = _serve(eng, 2, req)
     # ids [5, -3, 16]: the negative id is skipped, 16 is out of range on l0.
     assert status == 1 and msg == "invalid argument: block 16 out of range for layer l0 " \
                                   "(16 blocks registered)"
     load = (_field(7, 2, b"zz") + _field(5, 2, b"l1") + _field(1, 2, b"i0") +
             _field(6, 2, _varint(1) + _varint(-2)) + _field(4, 2, b"pega_load_x") +
             _field(12, 2, b"ignored"))
-    status, msg = _raw(path, 1, load)
+    status, msg = _serve(eng, 1, load)
     assert status != 0 and "LoadState" in msg  # decoded through to the shm attach
     st = PyLoadState()
     load = (_field(5, 2, b"l1") + _field(1, 2, b"i0") + _field(7, 2, b"a") +
             _field(6, 0, 3) + _field(4, 2, st.shm_name().encode()) + _field(7, 2, b"b"))
-    status, msg = _raw(path, 1, load)
+    status, msg = _serve(eng, 1, load)
     assert status == 3 and "missing KV block hash at index 0" in msg
     assert st.get_state() == -1
     # Malformed: a length running past the message, a group wire type.
-    assert _raw(path, 2, _field(1, 2, b"i0")[:-1]) == (11, "malformed SaveRequest")
-    assert _raw(path, 1, _varint(1 << 3 | 3)) == (11, "malformed LoadRequest")
-    assert _raw(path, 9, b"") == (1, "unknown method 9")
-    status, msg = _raw(path, 1, b"", raw_len=(256 << 20) + 2)
-    assert status == 1 and "exceeds" in msg
-    assert fast.health() == (True, "")  # the endpoint still serves
+    assert _serve(eng, 2, _field(1, 2, b"i0")[:-1]) == (11, "malformed SaveRequest")
+    assert _serve(eng, 1, _varint(1 << 3 | 3)) == (11, "malformed LoadRequest")
+    assert _serve(eng, 9, b"") == (1, "unknown method 9")
+    assert _serve(eng, 3, b"") == (0, "")  # Health
+    assert slow.health() == (True, "")

@@ -160,22 +160,20 @@ def test_two_process_ipc_round_trip(gpu):
         layers.close()
 
 
-def test_two_process_round_trip_over_the_native_endpoint(gpu, tmp_path):
-    """The same round trip with save, load and health over the server's
-    native endpoint (--fast-socket), registration and queries over gRPC."""
-    say("[gpu] rpc two-process round trip over the native endpoint")
+def test_two_process_round_trip_over_grpcio(gpu):
+    """The same round trip against a server whose gRPC endpoint is grpcio's
+    (--grpc-impl python) instead of the library's own HTTP/2 server."""
+    say("[gpu] rpc two-process round trip, grpcio server")
     layers = Layers(3, 64, 16 * 8 * 128 * 2, seed=13)
     handles = [ipc.export_tensor(b.ptr, layers.size, 0) for b in layers.bufs]
-    sock = str(tmp_path / "pegaflow.sock")
-    p, addr = _start_server("--fast-socket", sock)
-    say(f"[gpu] server pid {p.pid} at {addr}, {sock}")
+    p, addr = _start_server("--grpc-impl", "python")
+    say(f"[gpu] server pid {p.pid} at {addr}")
     try:
-        with EngineRpcClient(f"http://{addr}", connect_timeout_s=10, fast_socket=sock) as client:
+        with EngineRpcClient(f"http://{addr}", connect_timeout_s=10) as client:
             assert client.health() == (True, "")
             round_trip(client, layers, handles)
             assert client.shutdown() == (True, "")
         assert p.wait(60) == 0
-        assert not os.path.exists(sock)
     finally:
         if p.poll() is None:
             p.kill()

@@ -380,3 +380,49 @@ def test_copy_engines_known(gpu):
     assert d2h and h2d, "no copy engines known for device 0"
     assert bin(d2h).count("1") <= 2 and bin(h2d).count("1") <= 2
     assert d2h & h2d == 0
+    # Not the engines hipMemcpyAsync uses on MI355X (engine 0 host to device,
+    # engine 1 device to host), and among the fast engines 0-3.
+    assert (d2h | h2d) & 0x3 == 0 and (d2h | h2d) & ~0xF == 0
+
+
+def test_set_copy_engines(gpu):
+    """pf_set_copy_engines moves the staged copies to other engines (a staged
+    save and load over them stay bit-exact against the oracle); masks of
+    more than two engines, or of engines the runtime does not offer, are
+    refused; 0 keeps a direction's choice."""
+    from pegaflow_amd.runtime import set_copy_engines
+
+    say("[gpu] set copy engines")
+    d2h, h2d = copy_engines(0)
+    try:
+        set_copy_engines(0, 0x1, 0x2)
+        assert copy_engines(0) == (0x1, 0x2)
+        set_copy_engines(0, 0, 0x8)
+        assert copy_engines(0) == (0x1, 0x8)
+        with pytest.raises(_lib.PegaFlowError, match="one or two engine bits"):
+            set_copy_engines(0, 0x7, 0)
+        with pytest.raises(_lib.PegaFlowError, match="available"):
+            set_copy_engines(0, 1 << 30, 0)
+        layers, save_ids, load_ids = _mixed_layers(90)
+        host, ohost = _place_all(layers, save_ids)
+        ctx = TransferContext(0, staging_bytes=4 * MiB)
+        try:
+            ctx.save_layers([L.transfer(ids) for L, ids in zip(layers, save_ids)],
+                            _lib.MODE_STAGED)
+            for L in layers:
+                L.oracle_save()
+            assert np.array_equal(host.array, ohost)
+            ctx.load_layers([L.transfer(ids) for L, ids in zip(layers, load_ids)],
+                            _lib.MODE_STAGED)
+            ctx.synchronize()
+            for L, ids in zip(layers, load_ids):
+                L.oracle_load(ids)
+                assert np.array_equal(L.dev.download(), L.ref)
+        finally:
+            for L in layers:
+                L.close()
+            host.close()
+            ctx.close()
+    finally:
+        set_copy_engines(0, d2h, h2d)
+    assert copy_engines(0) == (d2h, h2d)
