@@ -89,6 +89,9 @@ def parse():
                     help="same as --profile gather")
     ap.add_argument("--sweep-scatter", action="store_true",
                     help="also sweep the device scatter's launch shape and chunk order")
+    ap.add_argument("--scatter-spread", action="store_true",
+                    help="also time the device scatter and gather with the 640 blocks spread "
+                         "over all 20,000, a narrower range, or consecutive")
     ap.add_argument("--duplex-study", action="store_true",
                     help="also time each link direction against a plain DMA copy the other way, "
                          "and the two queued kernels' grids in duplex")
@@ -622,7 +625,8 @@ def leg_layerwise(xfer, seed, gemm=True):
     upper bound on overlap), then (``*_gemm`` keys) a bf16 GEMM calibrated
     to about 2 ms alone, which shares CUs and HBM with the restore: its
     efficiency is the 36 GEMMs' time back to back over the gated total, and
-    its slowdown the mean gated GEMM's time over the GEMM's time alone."""
+    its slowdown the mean gated GEMM's time over its time back to back (HIP
+    events around each GEMM in both)."""
     import hashlib
 
     from pegaflow_amd import _lib
@@ -649,13 +653,18 @@ def leg_layerwise(xfer, seed, gemm=True):
         spin(compute, compute_us)
 
     work = [spin_work]  # the per-layer compute of the runs below
+    timed = [False]  # events around each layer's compute (the GEMM runs only)
 
     def layer_work(l):
-        g0[l].record(compute)
+        if timed[0]:
+            g0[l].record(compute)
         work[0]()
-        g1[l].record(compute)
+        if timed[0]:
+            g1[l].record(compute)
 
     def work_ms():
+        if not timed[0]:
+            return 0.0
         return statistics.mean(g0[l].elapsed_ms(g1[l]) for l in range(shape.layers))
 
     def run(layerwise):
@@ -708,28 +717,32 @@ def leg_layerwise(xfer, seed, gemm=True):
     if gemm:
         gl = GemmLayer(compute)
         work[0] = gl
+        timed[0] = True
         gemm_only = min(run_compute_only() for _ in range(3))
+        gemm_b2b = work_ms()  # one GEMM's time, back to back with the others
         run(True)
         g_total, g_per_layer, g_ms = min((run(True) for _ in range(3)), key=lambda r: r[0])
         run_marked()
         gm_total, gm_ms = min(run_marked() for _ in range(3))
         gemm_res = {
-            "gemm_shape": f"bf16 [{gl.m},{gl.k}] x [{gl.k},{gl.m}]",
+            "gemm_shape": f"bf16 [{gl.m},{gl.k}] x [{gl.k},{gl.m}] (rocBLAS)",
             "gemm_alone_ms": round(gl.alone_ms, 4),
+            "gemm_back_to_back_ms": round(gemm_b2b, 4),
             "gemm_only_total_ms": round(gemm_only, 3),
             "events_gemm": {"total_ms": round(g_total, 3),
                             "efficiency": round(gemm_only / g_total, 4),
                             "gemm_ms_mean": round(g_ms, 4),
-                            "gemm_slowdown": round(g_ms / gl.alone_ms, 3),
+                            "gemm_slowdown": round(g_ms / gemm_b2b, 3),
                             "first_layer_ms": round(g_per_layer[0], 4),
                             "per_layer_ms_mean": round(sum(g_per_layer[1:]) /
                                                        (len(g_per_layer) - 1), 4)},
             "marked_gemm": {"total_ms": round(gm_total, 3),
                             "efficiency": round(gemm_only / gm_total, 4),
                             "gemm_ms_mean": round(gm_ms, 4),
-                            "gemm_slowdown": round(gm_ms / gl.alone_ms, 3)},
+                            "gemm_slowdown": round(gm_ms / gemm_b2b, 3)},
         }
         work[0] = spin_work
+        timed[0] = False
     bad = wl.verify_restored(layers, ids, targets)
     layers.refill()
     # Through the engine, default modes, gated on device layer words.
@@ -765,14 +778,16 @@ def leg_layerwise(xfer, seed, gemm=True):
     engine_total, _ = min(run_engine() for _ in range(3))
     if gl is not None:
         work[0] = gl
+        timed[0] = True
         run_engine()
         ge_total, ge_ms = min(run_engine() for _ in range(3))
         gemm_res["engine_gemm"] = {"total_ms": round(ge_total, 3),
                                    "efficiency": round(gemm_res["gemm_only_total_ms"] / ge_total,
                                                        4),
                                    "gemm_ms_mean": round(ge_ms, 4),
-                                   "gemm_slowdown": round(ge_ms / gl.alone_ms, 3)}
+                                   "gemm_slowdown": round(ge_ms / gemm_b2b, 3)}
         work[0] = spin_work
+        timed[0] = False
         gl.close()
     bad += wl.verify_restored(layers, ids, targets)
     eng.close()
@@ -1645,6 +1660,55 @@ def cpu_baseline(shape, ids, targets, n_layers, seed, device=0):
     }
 
 
+def scatter_spread(xfer, layers, gather_buf, ids, targets, seed, reps=6):
+    """The device scatter (packed HBM -> the blocks of 32 layers) and the
+    device gather (the blocks -> packed HBM) of 640 blocks, with the blocks
+    drawn ever closer together: uniformly from all 20,000 (the workload),
+    the same sorted, from the first 2,000, the first 640 in a random order,
+    and the first 640 in order.  Every case moves the same 2P bytes in the
+    same 40,960 chunks of 32 KiB with the same launch; only where the random
+    side's chunks lie in memory changes.  Median kernel time of `reps`
+    launches each (HIP events on the context's stream)."""
+    from pegaflow_amd import _lib
+    from pegaflow_amd import workload as wl
+
+    n = len(ids)
+    rng = np.random.Generator(np.random.PCG64(seed + 7))
+    cases = {
+        "all_20000_random": np.asarray(targets),
+        "all_20000_sorted": np.sort(np.asarray(targets)),
+        "first_2000_random": rng.choice(2000, n, replace=False),
+        "first_640_permuted": rng.permutation(n),
+        "first_640_in_order": np.arange(n),
+    }
+    P2 = 2 * wl.payload_bytes(layers.regs, n)
+    gather_ids = wl.save_plan(layers.regs, ids, gather_buf.ptr)
+    xfer.set_timing(True)
+    out = {}
+    for name, blocks in cases.items():
+        row = {}
+        for kind in ("scatter", "gather"):
+            plan = (wl.load_plan(gather_ids, blocks) if kind == "scatter"
+                    else wl.save_plan(layers.regs, blocks, gather_buf.ptr))
+
+            def go():
+                if kind == "scatter":
+                    xfer.load_layers(plan, _lib.MODE_KERNEL)
+                    xfer.synchronize()
+                else:
+                    xfer.save_layers(plan, _lib.MODE_KERNEL)
+                return xfer.last_kernel_ms()[0]
+
+            go()
+            ms = statistics.median(go() for _ in range(reps))
+            row[kind] = {"ms": round(ms, 4), "gbps": round(P2 / ms / 1e6, 1),
+                         "frac": round(P2 / ms / 1e6 / HBM_PEAK_GBPS, 4)}
+        out[name] = row
+        log(f"[bench] scatter spread {name}: {row}")
+    layers.refill()
+    return out
+
+
 def run_leg(args):
     """One workload on its own (--leg): its JSON object on stdout."""
     from pegaflow_amd import runtime
@@ -1827,6 +1891,9 @@ def main():
             dst_sorted.append(type(lt)(lt.registration, b))
         shape_sweep("scatter_dstsorted", dst_sorted, load_k, 5, 2 * P, scatter_shapes)
         layers.refill()
+
+    spread = scatter_spread(xfer, layers, gather_buf, ids, targets, args.seed) \
+        if args.scatter_spread else None
 
     variants = {}
     if args.variants or not args.quick:
@@ -2047,6 +2114,8 @@ def main():
         out["variants"] = variants
     if sweep:
         out["gather_sweep_gbps"] = sweep
+    if spread:
+        out["scatter_spread"] = spread
     print(json.dumps(out), flush=True)
     xfer.close()
     pool.close()
