@@ -222,6 +222,11 @@ struct PendingLayers {
   uint64_t max_blocks = 0;
   std::function<int()> ready;
 };
+// save_layers_begin for a save whose later layers are pending: in the
+// kernel and staged modes the first `head` layers' copies start before
+// ready() is called; the other modes call it before anything is issued.
+int save_layers_pending_begin(pf_xfer* x, pf_layer_xfer* layers, uint32_t num_layers,
+                              uint32_t mode, const PendingLayers& pending);
 // A load whose later layers are pending: layer_events as pf_load_layers',
 // signals as pf_load_layers_marked's (num_signals 0: no marks).
 int load_layers_pending(pf_xfer* x, pf_layer_xfer* layers, uint32_t num_layers, uint32_t mode,

@@ -262,11 +262,13 @@ void BlockStore::filter_slots(const std::vector<std::string>& keys,
   }
   keep->assign(slots.size(), std::vector<char>(n, 1));
   std::lock_guard<std::mutex> lk(inflight_mu_);
+  const bool none_inflight = inflight_.empty();  // the common case: no lookups
   for (size_t i = 0; i < n; ++i) {
     if (sealed[i]) {
       for (auto& k : *keep) k[i] = 0;
       continue;
     }
+    if (none_inflight) continue;
     auto it = inflight_.find(keys[i]);
     if (it == inflight_.end()) continue;
     const auto& filled = it->second.slots;
@@ -319,13 +321,16 @@ int BlockStore::insert_slots(const std::vector<std::string>& keys,
     prepared = &own;
   }
   const size_t n = keys.size();
-  // Keys sealed before this call (each key looked up once, not once per
-  // layer that carries it).
+  // Keys sealed before this call, among those of the slot entries (each key
+  // looked up once, not once per layer that carries it).  Complete blocks
+  // need no lookup here: the cache insert below skips a key sealed
+  // meanwhile.
   std::vector<char> sealed_already(n, 0), named(n, 0);
+  bool any_named = false;
   for (const auto& layer : entries)
-    for (const auto& e : layer) named[e.first] = 1;
-  for (const auto& p : *prepared) named[p.first] = 1;
-  {
+    for (const auto& e : layer)
+      if (e.second) named[e.first] = any_named = true;  // not moved into a complete block
+  if (any_named) {
     std::lock_guard<std::mutex> lk(cache_mu_);
     for (size_t i = 0; i < n; ++i)
       if (named[i]) sealed_already[i] = cache_.count(keys[i]) != 0;
@@ -336,10 +341,10 @@ int BlockStore::insert_slots(const std::vector<std::string>& keys,
     std::lock_guard<std::mutex> lk(inflight_mu_);
     // Complete blocks seal directly, unless an earlier call left part of
     // the block in flight: then its slots go back to the general path.
+    const bool none_inflight = inflight_.empty();
     for (auto& p : *prepared) {
       const uint32_t i = p.first;
-      if (sealed_already[i]) continue;
-      if (inflight_.count(keys[i])) {
+      if (!none_inflight && inflight_.count(keys[i])) {
         for (size_t j = 0; j < entries.size(); ++j)
           entries[j].emplace_back(i, std::move(p.second->slots[slots[j]]));
         continue;
@@ -587,14 +592,20 @@ class DeviceWorker {
                     std::atomic<uint64_t>* loaded_bytes, std::atomic<uint64_t>* failures);
   ~DeviceWorker();
   // Saves the layers; `overlap` runs on the calling thread while the copy is
-  // in flight, and the call returns once the bytes are in place.
-  int save(const std::vector<pf_layer_xfer>& layers, uint32_t mode,
-           const std::function<void()>& overlap);
+  // in flight, and the call returns once the bytes are in place.  With
+  // `pending`, layers from pending->head on are listed by pending->ready(),
+  // which the transfer calls on this thread once the first ones are issued.
+  int save(std::vector<pf_layer_xfer>& layers, uint32_t mode,
+           const std::function<void()>& overlap, const PendingLayers* pending = nullptr);
   int submit(LoadTask&& task);
   void wait_idle();
   // The mode a load in `mode` would run in on this device's load context.
   uint32_t resolve_load_mode(uint32_t mode, const pf_layer_xfer* layers, uint32_t n) const {
     return load_x_ ? resolve_mode(load_x_, layers, n, mode) : PF_MODE_KERNEL;
+  }
+  // The same for a save on this device's save context.
+  uint32_t resolve_save_mode(uint32_t mode, const pf_layer_xfer* layers, uint32_t n) const {
+    return save_x_ ? resolve_mode(save_x_, layers, n, mode) : PF_MODE_KERNEL;
   }
   // Hands a new task the block lists of a finished one (cleared, capacity
   // kept), so building a task allocates nothing new in steady state.
@@ -803,8 +814,8 @@ int DeviceWorker::load_marked(std::vector<pf_layer_xfer>& layers, uint32_t mode,
   return pf_xfer_synchronize(load_x_);
 }
 
-int DeviceWorker::save(const std::vector<pf_layer_xfer>& layers, uint32_t mode,
-                       const std::function<void()>& overlap) {
+int DeviceWorker::save(std::vector<pf_layer_xfer>& layers, uint32_t mode,
+                       const std::function<void()>& overlap, const PendingLayers* pending) {
   if (!gpu_)
     return fail(PF_ERR_UNSUPPORTED, "storage error: engine pool is not mapped for a device");
   std::lock_guard<std::mutex> lk(save_mu_);
@@ -813,7 +824,9 @@ int DeviceWorker::save(const std::vector<pf_layer_xfer>& layers, uint32_t mode,
     explicit Running(std::atomic<int>& c) : n(c) { n.fetch_add(1); }
     ~Running() { n.fetch_sub(1); }
   } running(saves_running_);
-  int rc = save_layers_begin(save_x_, layers.data(), static_cast<uint32_t>(layers.size()), mode);
+  const uint32_t n = static_cast<uint32_t>(layers.size());
+  int rc = pending ? save_layers_pending_begin(save_x_, layers.data(), n, mode, *pending)
+                   : save_layers_begin(save_x_, layers.data(), n, mode);
   if (rc) {
     const std::string msg = pf_last_error();
     (void)pf_xfer_synchronize(save_x_);  // nothing may still read the regions
@@ -1186,6 +1199,7 @@ struct SavePlan {
   size_t slot = 0;
   size_t group = 0;                // index of the layer's hash list
   pf_kv_layout layout{};
+  std::vector<int64_t> ids;        // kept block ids, in order
   std::vector<uint32_t> key_idx;   // kept hashes (indices into the list), in order
   std::vector<pf_block_xfer> blocks;
   std::shared_ptr<PoolAllocation> k_alloc, v_alloc;
@@ -1452,8 +1466,8 @@ int pf_engine_batch_save(pf_engine* e, const char* instance_id, uint64_t tp_rank
     groups[g].plans.push_back(li);
     plan.group = g;
   }
-  // Pass 2: filtering and dedup (lib.rs:590-621), then the host regions in
-  // the reference's layout.
+  // Pass 2: filtering and dedup (lib.rs:590-621): each layer's kept block
+  // ids, in order.
   for (const KeyGroup& g : groups) {
     std::vector<size_t> slots;
     for (size_t li : g.plans) slots.push_back(plans[li].slot);
@@ -1462,48 +1476,114 @@ int pf_engine_batch_save(pf_engine* e, const char* instance_id, uint64_t tp_rank
     for (size_t j = 0; j < g.plans.size(); ++j) {
       SavePlan& plan = plans[g.plans[j]];
       const pf_save_layer& sl = layers[g.plans[j]];
-      std::vector<int64_t> idx;
       for (uint64_t i = 0; i < sl.num_blocks; ++i)
         if (sl.block_ids[i] >= 0 && keep[j][i]) {
-          idx.push_back(sl.block_ids[i]);
+          plan.ids.push_back(sl.block_ids[i]);
           plan.key_idx.push_back(static_cast<uint32_t>(i));
         }
-      if (idx.empty()) continue;
-      const pf_kv_layout& reg = plan.layout;
-      const uint64_t n = idx.size();
-      plan.split = reg.segments == 2 && reg.kv_stride_bytes > reg.bytes_per_block;
-      plan.blocks.resize(n);
-      if (plan.split) {  // lib.rs:636-679
-        const uint64_t seg = reg.bytes_per_block;
-        plan.k_alloc = e->store->allocate(seg * n);
-        if (!plan.k_alloc)
-          return fail(PF_ERR_STORAGE,
-                      "storage error: pinned pool exhausted while allocating K segment buffer");
-        plan.v_alloc = e->store->allocate(seg * n);
-        if (!plan.v_alloc)
-          return fail(PF_ERR_STORAGE,
-                      "storage error: pinned pool exhausted while allocating V segment buffer");
-        for (uint64_t i = 0; i < n; ++i)
-          plan.blocks[i] =
-              pf_block_xfer{idx[i], reinterpret_cast<uint64_t>(plan.k_alloc->ptr + i * seg),
-                            reinterpret_cast<uint64_t>(plan.v_alloc->ptr + i * seg)};
-      } else {  // lib.rs:706-747
-        const uint64_t bs = reg.block_size_bytes;
-        plan.k_alloc = e->store->allocate(bs * n);
-        if (!plan.k_alloc)
-          return fail(PF_ERR_STORAGE,
-                      "storage error: pinned pool exhausted while allocating contiguous block "
-                      "buffer");
-        for (uint64_t i = 0; i < n; ++i)
-          plan.blocks[i] =
-              pf_block_xfer{idx[i], reinterpret_cast<uint64_t>(plan.k_alloc->ptr + i * bs), 0};
-      }
     }
   }
-  std::vector<pf_layer_xfer> xl;
-  for (auto& p : plans)
-    if (!p.blocks.empty()) xl.push_back(pf_layer_xfer{p.layout, p.blocks.data(), p.blocks.size()});
-  if (xl.empty()) return PF_OK;
+  // The host regions in the reference's layout, one layer at a time.
+  auto place = [&](SavePlan& plan) -> int {
+    const pf_kv_layout& reg = plan.layout;
+    const uint64_t n = plan.ids.size();
+    plan.split = reg.segments == 2 && reg.kv_stride_bytes > reg.bytes_per_block;
+    plan.blocks.resize(n);
+    if (plan.split) {  // lib.rs:636-679
+      const uint64_t seg = reg.bytes_per_block;
+      plan.k_alloc = e->store->allocate(seg * n);
+      if (!plan.k_alloc)
+        return fail(PF_ERR_STORAGE,
+                    "storage error: pinned pool exhausted while allocating K segment buffer");
+      plan.v_alloc = e->store->allocate(seg * n);
+      if (!plan.v_alloc)
+        return fail(PF_ERR_STORAGE,
+                    "storage error: pinned pool exhausted while allocating V segment buffer");
+      for (uint64_t i = 0; i < n; ++i)
+        plan.blocks[i] =
+            pf_block_xfer{plan.ids[i], reinterpret_cast<uint64_t>(plan.k_alloc->ptr + i * seg),
+                          reinterpret_cast<uint64_t>(plan.v_alloc->ptr + i * seg)};
+    } else {  // lib.rs:706-747
+      const uint64_t bs = reg.block_size_bytes;
+      plan.k_alloc = e->store->allocate(bs * n);
+      if (!plan.k_alloc)
+        return fail(PF_ERR_STORAGE,
+                    "storage error: pinned pool exhausted while allocating contiguous block "
+                    "buffer");
+      for (uint64_t i = 0; i < n; ++i)
+        plan.blocks[i] =
+            pf_block_xfer{plan.ids[i], reinterpret_cast<uint64_t>(plan.k_alloc->ptr + i * bs), 0};
+    }
+    return PF_OK;
+  };
+  // The layers with blocks to copy, in call order.
+  std::vector<size_t> order;
+  uint64_t chunks = 0, max_blocks = 0;
+  for (size_t pi = 0; pi < plans.size(); ++pi) {
+    const SavePlan& p = plans[pi];
+    if (p.ids.empty()) continue;
+    order.push_back(pi);
+    const bool split = p.layout.segments == 2 && p.layout.kv_stride_bytes > p.layout.bytes_per_block;
+    chunks += p.ids.size() * (split ? 2 : 1);
+    max_blocks = std::max<uint64_t>(max_blocks, p.ids.size());
+  }
+  if (order.empty()) return PF_OK;
+  // A large save is pipelined as loads are: the first layers' regions and
+  // lists are made, their copy starts, and the rest are made meanwhile
+  // (pool allocations, which may evict, and the block lists: about 0.1 ms
+  // for the Llama prefix, off the copy's start).  The reference likewise
+  // allocates each layer's regions just before that layer's copy
+  // (lib.rs:636-747 inside the per-layer loop).
+  uint32_t mode = e->save_mode.load();
+  if (int rc = place(plans[order[0]])) return rc;
+  if (mode == PF_MODE_AUTO) {  // the first layer's host runs decide (auto_mode)
+    const SavePlan& p0 = plans[order[0]];
+    const pf_layer_xfer lx{p0.layout, p0.blocks.data(), p0.blocks.size()};
+    mode = gpu->worker->resolve_save_mode(PF_MODE_AUTO, &lx, 1);
+  }
+  const uint32_t nl = static_cast<uint32_t>(order.size());
+  uint32_t head = nl;
+  if ((mode == PF_MODE_KERNEL || mode == PF_MODE_STAGED) && pipeline_head_layers(nl, chunks) > 0) {
+    // As many leading layers as it takes for their copy to outlast making
+    // the rest (about 10 ns per later block entry, in which the link moves
+    // about 500 bytes): one layer for the Llama prefix.
+    constexpr uint64_t kHeadBytesPerLaterEntry = 500;
+    uint64_t head_bytes = 0;
+    for (head = 0; head + 1 < nl;) {
+      head_bytes += plans[order[head++]].layout.block_size_bytes;
+      if (head_bytes >= (nl - head) * kHeadBytesPerLaterEntry) break;
+    }
+  }
+  for (uint32_t k = 1; k < head; ++k)
+    if (int rc = place(plans[order[k]])) return rc;
+  std::vector<pf_layer_xfer> xl(nl);
+  auto list = [&](uint32_t k) {
+    const SavePlan& p = plans[order[k]];
+    xl[k] = pf_layer_xfer{p.layout, p.blocks.data(), p.blocks.size()};
+  };
+  for (uint32_t k = 0; k < head; ++k) list(k);
+  for (uint32_t k = head; k < nl; ++k) xl[k] = pf_layer_xfer{plans[order[k]].layout, nullptr, 0};
+  // The later layers, made while the first ones copy.  A failure (the pool
+  // exhausted) fails the call after the first layers' copy drained, with
+  // nothing published, as a failure before any copy would.
+  bool rest_made = head == nl;
+  int rest_rc = PF_OK;
+  std::string rest_error;
+  PendingLayers pending;
+  pending.head = head;
+  pending.max_blocks = max_blocks;
+  pending.ready = [&]() -> int {
+    for (uint32_t k = head; k < nl; ++k) {
+      if (int rc = place(plans[order[k]])) {
+        rest_rc = rc;
+        rest_error = pf_last_error();
+        return rc;
+      }
+      list(k);
+    }
+    rest_made = true;
+    return PF_OK;
+  };
   // The LayerBlocks are built while the copy runs; they are published only
   // after it has completed (lib.rs:687-705, 755-770).
   std::vector<BlockStore::SlotEntries> entries(plans.size());
@@ -1547,7 +1627,12 @@ int pf_engine_batch_save(pf_engine* e, const char* instance_id, uint64_t tp_rank
     }
   };
   const auto t_planned = std::chrono::steady_clock::now();
-  if (int rc = gpu->worker->save(xl, e->save_mode.load(), build_handles)) return rc;
+  if (int rc = gpu->worker->save(xl, mode, build_handles, head < nl ? &pending : nullptr)) {
+    if (rest_rc != PF_OK) return fail(rest_rc, rest_error);  // its own message
+    return rc;
+  }
+  if (!rest_made)  // every transfer mode lists the later layers before it returns
+    return fail(PF_ERR_STORAGE, "storage error: the later layers of a save were not planned");
   const auto t_copied = std::chrono::steady_clock::now();
   uint64_t bytes = 0;
   for (size_t gi = 0; gi < groups.size(); ++gi) {

@@ -1030,19 +1030,33 @@ int staged_engine(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
     return PF_OK;
   };
   if (is_save) {
-    for (size_t si = 0; si < sp.steps.size(); ++si) {
-      if (sp.steps[si].ordered_layer >= 0) {  // not produced for saves; copied in place
-        if (int rc = dma_layer(x, plans[static_cast<size_t>(sp.steps[si].ordered_layer)], true,
-                               false))
-          return rc;
-        continue;
-      }
+    auto save_step = [&](size_t si) -> int {
+      if (sp.steps[si].ordered_layer >= 0)  // not produced for saves; copied in place
+        return dma_layer(x, plans[static_cast<size_t>(sp.steps[si].ordered_layer)], true, false);
       const size_t s = slice_of[si] % n_slots;
       // The slot's previous copies (of this call or an earlier one) are done.
       if (int rc = engine_signal_wait(&x->eng_sig[s])) return rc;
       if (int rc = kernel(si)) return rc;
       if (int rc = kernels_done(s)) return rc;
-      if (int rc = queue_copies(si)) return rc;
+      return queue_copies(si);
+    };
+    size_t si = 0;
+    for (; si < sp.steps.size(); ++si)
+      if (int rc = save_step(si)) return rc;
+    if (piped) {
+      // The first layers' copies run on the engine while the rest is
+      // listed and planned.
+      if (pending)
+        if (int rc = pending->ready()) return rc;
+      if (int rc = plan_range(layers, head, num_layers, true, &plans)) return rc;
+      if (int rc = check_devices(layers, plans, head, num_layers)) return rc;
+      if (int rc = planner.add(plans, head, num_layers)) return rc;
+      if (int rc = planner.cut()) return rc;
+      index();
+      if (int rc = publish()) return rc;
+      tr.mark("rest", sp.n_desc);
+      for (; si < sp.steps.size(); ++si)
+        if (int rc = save_step(si)) return rc;
     }
     if (wait_save) return engine_drain(x);
     return PF_OK;
@@ -1120,10 +1134,13 @@ int staged(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, bool is
   StagedTrace tr;
   std::vector<LayerPlan>& plans = x->plans;
   plans.resize(num_layers);
-  // Layers planned before the first copies: all, or a pipelined load's
-  // first layer (the layers listed so far, when the rest are pending).
+  // Layers planned before the first copies: all, or a pipelined call's
+  // first layer (the layers listed so far, when the rest are pending).  A
+  // save's first copy then starts after planning and gathering 1 of the
+  // Llama prefix's 32 layers (40 MiB) instead of all 40,960 chunks and a
+  // full slice, and the rest is planned under that copy.
   uint32_t head = pending ? pending->head : num_layers;
-  if (!pending && !is_save && x->engine_ok && pipeline_head(layers, num_layers) > 0) head = 1;
+  if (!pending && x->engine_ok && pipeline_head(layers, num_layers) > 0) head = 1;
   if (int rc = plan_range(layers, 0, head, is_save, &plans)) return rc;
   const bool engines = x->engine_ok && hosts_pinned(plans, 0, head);
   if (head < num_layers && !engines) {
@@ -1162,10 +1179,10 @@ int staged(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, bool is
     tr.print(is_save);
     return rc;
   }
-  // One lane when the kernel launches run queued (they share one tile
-  // counter, so they must not overlap) or when a save's order matters.
-  const int route = is_save ? PF_ROUTE_SAVE_DEVICE : PF_ROUTE_LOAD_DEVICE;
-  const int lanes = (x->grid[route] > 0 || (is_save && !save_hosts_disjoint(plans))) ? 1 : 2;
+  // One lane when a save's order matters (host regions that overlap must
+  // be written in list order); otherwise slices alternate between the two
+  // streams, each with a tile queue of its own for queued launches.
+  const int lanes = (is_save && !save_hosts_disjoint(plans)) ? 1 : 2;
   hipStream_t lane_s[2] = {x->stream, x->dma};
   {
     int k = 0;
@@ -2128,6 +2145,11 @@ int pf_load_layers_marked(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_
 }  // extern "C"
 
 namespace pf {
+
+int save_layers_pending_begin(pf_xfer* x, pf_layer_xfer* layers, uint32_t num_layers,
+                              uint32_t mode, const PendingLayers& pending) {
+  return run(x, layers, num_layers, mode, true, nullptr, false, nullptr, &pending);
+}
 
 int load_layers_pending(pf_xfer* x, pf_layer_xfer* layers, uint32_t num_layers, uint32_t mode,
                         pf_event* layer_events, const pf_layer_signal* signals,

@@ -141,27 +141,28 @@ class PegaEngine:
         """Blocking save of (layer_name, block_ids, block_hashes) per layer.
         Lists shared by several layers (the usual case) are packed once."""
         keep, arr = [], []
+        # Each list packed once, with its address (numpy's ctypes.data costs
+        # microseconds per access: 96 of them were 0.2 ms of a 32-layer save).
         packed_ids, packed_hashes = {}, {}
         for layer_name, block_ids, block_hashes in saves:
-            ids = packed_ids.get(id(block_ids))
-            if ids is None:
+            pi = packed_ids.get(id(block_ids))
+            if pi is None:
                 ids = np.ascontiguousarray(block_ids, dtype=np.int32)
-                packed_ids[id(block_ids)] = ids
-                keep.append(block_ids)  # keeps id() unique for the whole call
-            if len(ids) != len(block_hashes):
+                pi = packed_ids[id(block_ids)] = (ids, ids.ctypes.data, len(ids))
+                keep += [block_ids, ids]  # keeps id() unique for the whole call
+            _, ids_ptr, n_ids = pi
+            if n_ids != len(block_hashes):
                 raise PegaFlowError(_lib.PF_ERR_INVALID_ARGUMENT,
-                                    f"invalid argument: block_ids length {len(ids)} does not "
+                                    f"invalid argument: block_ids length {n_ids} does not "
                                     f"match block_hashes {len(block_hashes)}")
             hp = packed_hashes.get(id(block_hashes))
             if hp is None:
-                hp = _hashes(block_hashes)
-                packed_hashes[id(block_hashes)] = hp
-                keep.append(block_hashes)
-            data, offs = hp
+                data, offs = _hashes(block_hashes)
+                hp = packed_hashes[id(block_hashes)] = (data.ctypes.data, offs.ctypes.data)
+                keep += [block_hashes, data, offs]
             name = layer_name.encode()
-            keep += [ids, data, offs, name]
-            arr.append(SaveLayer(name, ids.ctypes.data, len(ids), data.ctypes.data,
-                                 offs.ctypes.data))
+            keep.append(name)
+            arr.append(SaveLayer(name, ids_ptr, n_ids, hp[0], hp[1]))
         c_arr = (SaveLayer * max(len(arr), 1))(*arr)
         _raise(lib().pf_engine_batch_save(self._h, instance_id.encode(), tp_rank, device_id,
                                           c_arr, len(arr)))

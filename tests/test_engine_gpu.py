@@ -609,3 +609,70 @@ def test_split_load_error_in_later_layers(engine, mode):
             b.close()
         if odd is not None:
             odd.close()
+
+
+@pytest.mark.parametrize("save_mode", ["kernel", "staged", "auto"])
+def test_pipelined_save_matches_oracle(engine, save_mode):
+    """A save of 8 layers x 1024 split blocks (16,384 chunks) is pipelined:
+    the regions and lists of its first layers are made and their copy
+    started before the others are made.  A first save of half the blocks,
+    then a save of all of them (the saved half filtered out, so the kept
+    lists differ from the ids); every block restored into other blocks
+    equals the oracle's, and the store holds all 1024 blocks sealed."""
+    say(f"[gpu] engine pipelined save ({save_mode})")
+    engine.set_transfer_modes(_lib.MODE_NAMES[save_mode], _lib.MODE_KERNEL)
+    m = Model(engine, "psave", 8, 2100, 1024, seed=51)
+    try:
+        orig = m.host_copies()
+        perm = np.random.default_rng(51).permutation(2100)
+        ids, targets = [int(i) for i in perm[:1024]], [int(i) for i in perm[1024:2048]]
+        hashes = [h(i, b"psave") for i in ids]
+        engine.batch_save_kv_blocks("psave", 0, 0,
+                                    [(n, ids[::2], hashes[::2]) for n in m.names])
+        engine.batch_save_kv_blocks("psave", 0, 0, [(n, ids, hashes) for n in m.names])
+        assert engine.count_prefix_hit_blocks("psave", hashes) == 1024
+        s = engine.stats()
+        assert s["sealed_blocks"] == 1024 and s["inflight_blocks"] == 0
+        st = PyLoadState()
+        engine.batch_load_kv_blocks("psave", 0, 0, st.shm_name(), m.names, targets, hashes)
+        assert wait(st) == 1
+        exp = expected_after_load(m, orig, ids, targets)
+        got = m.host_copies()
+        for l in range(m.n_layers):
+            assert np.array_equal(got[l], exp[l]), f"layer {l}"
+    finally:
+        m.close()
+
+
+@pytest.mark.parametrize("save_mode", ["kernel", "staged"])
+def test_pipelined_save_pool_exhausted_in_later_layer(gpu, save_mode):
+    """A pipelined save whose pool holds its first layers' regions but not
+    the rest: the call fails with the pool's message once the first
+    layers' copy has drained, nothing is published, and a save that fits
+    then completes and restores correctly."""
+    say(f"[gpu] engine pipelined save, pool exhausted in a later layer ({save_mode})")
+    e = PegaEngine(pool_size=5 * MiB)  # 2 MiB per layer of 1024 split 1 KiB blocks
+    e.set_transfer_modes(_lib.MODE_NAMES[save_mode], _lib.MODE_KERNEL)
+    m = Model(e, "pex", 8, 2100, 1024, seed=53)
+    try:
+        orig = m.host_copies()
+        ids = list(range(1024))
+        hashes = [h(i, b"pex") for i in ids]
+        with pytest.raises(RuntimeError, match="pinned pool exhausted while allocating"):
+            e.batch_save_kv_blocks("pex", 0, 0, [(n, ids, hashes) for n in m.names])
+        s = e.stats()
+        assert s["sealed_blocks"] == 0 and s["inflight_blocks"] == 0
+        assert s["pool_used_bytes"] == 0
+        assert e.count_prefix_hit_blocks("pex", hashes) == 0
+        small, tg = ids[:200], list(range(1500, 1700))
+        e.batch_save_kv_blocks("pex", 0, 0, [(n, small, hashes[:200]) for n in m.names])
+        st = PyLoadState()
+        e.batch_load_kv_blocks("pex", 0, 0, st.shm_name(), m.names, tg, hashes[:200])
+        assert wait(st) == 1
+        exp = expected_after_load(m, orig, small, tg)
+        got = m.host_copies()
+        for l in range(m.n_layers):
+            assert np.array_equal(got[l], exp[l]), f"layer {l}"
+    finally:
+        m.close()
+        e.close()
