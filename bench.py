@@ -108,7 +108,7 @@ def parse():
     ap.add_argument("--pinned-flags", type=int, default=0,
                     help="PF_PINNED_* flags of the pinned pools (0: mapped, portable)")
     ap.add_argument("--cpu-sample-layers", type=int, default=8)
-    ap.add_argument("--staging-mib", type=int, default=256)
+    ap.add_argument("--staging-mib", type=int, default=512)
     ap.add_argument("--seed", type=int, default=0)
     return ap.parse_args()
 

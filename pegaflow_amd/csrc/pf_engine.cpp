@@ -298,7 +298,7 @@ BlockStore::Prepared BlockStore::prepare_whole(const std::vector<size_t>& slots,
       whole = entries[j][k].first == entries[0][k].first;
   }
   if (!whole) return out;
-  out.reserve(entries[0].size());
+  out.blocks.reserve(entries[0].size());
   for (size_t k = 0; k < entries[0].size(); ++k) {
     auto sb = std::make_shared<SealedBlock>();
     sb->slots.resize(total_slots);
@@ -307,9 +307,20 @@ BlockStore::Prepared BlockStore::prepare_whole(const std::vector<size_t>& slots,
       sb->slots[slots[j]] = std::move(entries[j][k].second);  // leaves it empty
     }
     sb->index();
-    out.emplace_back(entries[0][k].first, std::move(sb));
+    out.blocks.emplace_back(entries[0][k].first, std::move(sb));
   }
   return out;
+}
+
+void BlockStore::stage_nodes(const std::vector<std::string>& keys, Prepared* p) {
+  p->nodes.reserve(p->blocks.size());
+  for (const auto& b : p->blocks) {
+    auto ins = p->nodes.try_emplace(keys[b.first]);
+    if (!ins.second) continue;  // a key named twice keeps its first block
+    p->order.push_front(&ins.first->first);
+    ins.first->second = Entry{b.second, p->order.begin()};
+  }
+  p->staged = true;
 }
 
 int BlockStore::insert_slots(const std::vector<std::string>& keys,
@@ -337,22 +348,30 @@ int BlockStore::insert_slots(const std::vector<std::string>& keys,
   }
   std::vector<std::pair<uint32_t, std::shared_ptr<SealedBlock>>> sealed;
   int err = PF_OK;
+  size_t n_direct = 0;  // sealed[0, n_direct): complete blocks that never entered the inflight map
   {
     std::lock_guard<std::mutex> lk(inflight_mu_);
     // Complete blocks seal directly, unless an earlier call left part of
     // the block in flight: then its slots go back to the general path.
     const bool none_inflight = inflight_.empty();
-    for (auto& p : *prepared) {
+    for (auto& p : prepared->blocks) {
       const uint32_t i = p.first;
       if (!none_inflight && inflight_.count(keys[i])) {
         for (size_t j = 0; j < entries.size(); ++j)
           entries[j].emplace_back(i, std::move(p.second->slots[slots[j]]));
+        if (prepared->staged) {  // its staged node, if it is the key's, goes too
+          auto it = prepared->nodes.find(keys[i]);
+          if (it != prepared->nodes.end() && it->second.block == p.second) {
+            prepared->order.erase(it->second.pos);
+            prepared->nodes.erase(it);
+          }
+        }
         continue;
       }
       sealed.emplace_back(i, std::move(p.second));
     }
-    prepared->clear();
-    const size_t n_direct = sealed.size();  // never entered the inflight map
+    prepared->blocks.clear();
+    n_direct = sealed.size();
     std::vector<InflightBlock*> ib(n, nullptr);  // node pointers survive inserts
     int rc = PF_OK;
     for (size_t j = 0; j < entries.size() && rc == PF_OK; ++j) {
@@ -402,7 +421,21 @@ int BlockStore::insert_slots(const std::vector<std::string>& keys,
   std::vector<char> fresh(sealed.size(), 0);
   {
     std::lock_guard<std::mutex> lk(cache_mu_);
-    for (size_t k = 0; k < sealed.size(); ++k) {
+    size_t k = 0;
+    if (prepared->staged) {
+      // The complete blocks' nodes move in whole (no allocation or hashing
+      // under the lock); those whose key was sealed meanwhile stay behind.
+      cache_.merge(prepared->nodes);
+      for (auto& left : prepared->nodes) prepared->order.erase(left.second.pos);
+      lru_.splice(lru_.begin(), prepared->order);
+      if (seal_hook_)
+        for (; k < n_direct; ++k) {
+          auto it = cache_.find(keys[sealed[k].first]);
+          fresh[k] = it != cache_.end() && it->second.block == sealed[k].second;
+        }
+      k = n_direct;
+    }
+    for (; k < sealed.size(); ++k) {
       auto ins = cache_.try_emplace(keys[sealed[k].first]);
       if (!ins.second) continue;  // sealed already
       lru_.push_front(&ins.first->first);
@@ -410,6 +443,7 @@ int BlockStore::insert_slots(const std::vector<std::string>& keys,
       fresh[k] = 1;
     }
   }
+  prepared->nodes.clear();  // blocks sealed by another call meanwhile
   if (seal_hook_)
     for (size_t k = 0; k < sealed.size(); ++k)
       if (fresh[k]) seal_hook_(keys[sealed[k].first], sealed[k].second);
@@ -660,7 +694,7 @@ constexpr size_t kMaxWordMaps = 16;
 constexpr uint32_t kLoadGridAlone = 32;
 
 // Staging of the workers' transfer contexts: two slots each of the staged
-// mode's largest slice (0.375 GiB of HBM per device in all).
+// mode's largest slice (1 GiB of HBM per device in all).
 constexpr uint64_t kSaveStagingBytes = 2 * PF_STAGED_SAVE_SLICE_DEFAULT;
 constexpr uint64_t kLoadStagingBytes = 2 * PF_STAGED_LOAD_SLICE_DEFAULT;
 
@@ -1624,6 +1658,7 @@ int pf_engine_batch_save(pf_engine* e, const char* instance_id, uint64_t tp_rank
         gs.entries.push_back(std::move(entries[li]));
       }
       gs.prepared = BlockStore::prepare_whole(gs.slots, gs.entries, total_slots);
+      BlockStore::stage_nodes(groups[gi].keys, &gs.prepared);
     }
   };
   const auto t_planned = std::chrono::steady_clock::now();

@@ -159,7 +159,19 @@ class BlockStore {
   // cache and the seal hook runs for it.  Errors on slot count mismatch or
   // a slot out of range.
   using SlotEntries = std::vector<std::pair<uint32_t, std::shared_ptr<LayerBlock>>>;
-  using Prepared = std::vector<std::pair<uint32_t, std::shared_ptr<SealedBlock>>>;
+  struct Entry {
+    std::shared_ptr<SealedBlock> block;
+    std::list<const std::string*>::iterator pos;
+  };
+  struct Prepared {
+    // Complete blocks (key index, block), in the call's order.
+    std::vector<std::pair<uint32_t, std::shared_ptr<SealedBlock>>> blocks;
+    // Their cache nodes, made ahead of the lock by stage_nodes: the first
+    // block of each key with its recency element (front = most recent).
+    std::unordered_map<std::string, Entry> nodes;
+    std::list<const std::string*> order;
+    bool staged = false;
+  };
   // When the call brings every slot of its blocks (entries[j] for slot
   // slots[j], all naming the same keys in the same order), the complete
   // blocks built from them, moving the layer blocks out of `entries`;
@@ -167,6 +179,10 @@ class BlockStore {
   // the copy is in flight.
   static Prepared prepare_whole(const std::vector<size_t>& slots,
                                 std::vector<SlotEntries>& entries, size_t total_slots);
+  // Makes the cache nodes of prepared blocks (key copies, hashing, the
+  // recency elements), so that publishing them is a merge and a splice
+  // under the lock.  Touches no state of the store.
+  static void stage_nodes(const std::vector<std::string>& keys, Prepared* prepared);
   // Publishes the copies (moves them): blocks in `prepared` seal directly
   // unless an earlier call left part of them in flight.
   int insert_slots(const std::vector<std::string>& keys, const std::vector<size_t>& slots,
@@ -179,6 +195,8 @@ class BlockStore {
   uint64_t sealed_count();
   uint64_t inflight_count();
   uint64_t evictions() const { return evictions_.load(std::memory_order_relaxed); }
+  // Evicts up to max_blocks least-recently-used sealed blocks; the count.
+  size_t evict_lru(size_t max_blocks);
 
  private:
   std::shared_ptr<PinnedPool> pool_;
@@ -188,14 +206,9 @@ class BlockStore {
   // Recency order, front = most recent; each element points at its key in
   // cache_ (unordered_map nodes, hence keys, stay put until erased).
   std::list<const std::string*> lru_;
-  struct Entry {
-    std::shared_ptr<SealedBlock> block;
-    std::list<const std::string*>::iterator pos;
-  };
   std::unordered_map<std::string, Entry> cache_;
   std::atomic<uint64_t> evictions_{0};  // written under cache_mu_, read without it
   SealHook seal_hook_;
-  size_t evict_lru(size_t max_blocks);
 };
 
 // ---------------------------------------------------------------------------

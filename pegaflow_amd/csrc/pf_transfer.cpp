@@ -286,6 +286,8 @@ constexpr uint64_t kScatterTrialMinBytes = 64ull << 20;  // time only launches t
 
 // Staging slots of a staged call on the copy engines, at most.
 constexpr int kEngineSlots = 8;
+// Largest slice of a staged load that reports each layer's completion.
+constexpr uint64_t kLayeredLoadSlice = 64ull << 20;
 
 struct ScatterTrial {
   hipEvent_t start = nullptr, stop = nullptr;
@@ -1159,9 +1161,14 @@ int staged(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, bool is
   // staged throughout.
   const bool kernel_head = engines && !is_save && head > 0 && head < num_layers &&
                            (sig != nullptr || layer_events != nullptr);
+  // A load waited for layer by layer (marks or per-layer events) keeps its
+  // slices at most kLayeredLoadSlice, so each Llama layer (40 MiB) is a copy
+  // of its own and lands on its own; larger slices would join 3-4 layers in
+  // one copy.  Other calls take the context's slice sizes.
+  uint64_t slice = x->staged_slice[is_save ? 0 : 1];
+  if (!is_save && (sig || layer_events)) slice = std::min(slice, kLayeredLoadSlice);
   StagedPlan sp;
-  StagedPlanner planner(x->slot_bytes, x->staged_slice[is_save ? 0 : 1], is_save, num_layers,
-                        &sp);
+  StagedPlanner planner(x->slot_bytes, slice, is_save, num_layers, &sp);
   if (!kernel_head) {
     if (int rc = planner.add(plans, 0, head)) return rc;
     if (int rc = planner.cut()) return rc;

@@ -10,7 +10,12 @@
 //      that brings all slots (the earlier copies win);
 //   3. a block sealed earlier, saved again (unchanged);
 //   4. one key named twice in a call (the first occurrence seals);
-//   5. a slot count that differs from the block's in flight (an error).
+//   5. a slot count that differs from the block's in flight (an error);
+//   6. the engine's own publishing of a whole call, with the cache nodes
+//      made ahead (prepare_whole + stage_nodes, as a save does while its
+//      copy runs): a fresh key, a key sealed meanwhile, a key an earlier call
+//      left in flight, a key named twice; then the recency order those
+//      blocks took, read through eviction.
 // Exit status 0 and "ok" on success; the first failed check is printed.
 #include <cstdio>
 #include <cstdlib>
@@ -133,6 +138,45 @@ int main() {
     expect(store.insert_slots(k5, other, e2, total + 1) != PF_OK, "slot count mismatch refused");
     expect(std::string(pf_last_error()).find("slot count mismatch") != std::string::npos,
            "the reference's message");
+  }
+  // 6. Staged publishing.  Keys 10-13: 10 fresh, 11 sealed by another call
+  //    after this one was prepared, 12 left in flight (slot 0) by an earlier
+  //    call, and 10 named again as index 4.
+  {
+    std::vector<std::string> k6 = {key(10), key(11), key(12), key(13), key(10)};
+    const std::vector<size_t> one = {0};
+    auto early = entries_for(one, {2}, 8);
+    expect(store.insert_slots(k6, one, early, total) == PF_OK, "earlier partial call");
+    const std::vector<size_t> all = {3, 1, 0, 2};
+    auto e = entries_for(all, {0, 1, 2, 3, 4}, 9);
+    BlockStore::Prepared prep = BlockStore::prepare_whole(all, e, total);
+    expect(prep.blocks.size() == 5, "five complete blocks prepared");
+    BlockStore::stage_nodes(k6, &prep);
+    expect(prep.nodes.size() == 4 && prep.order.size() == 4, "one node per distinct key");
+    auto other = entries_for(all, {1}, 10);  // key 11 seals through another call
+    expect(store.insert_slots(k6, all, other, total) == PF_OK, "another call seals key 11");
+    auto sealed11 = store.peek(k6[1]);
+    const uint64_t before = store.sealed_count();
+    expect(store.insert_slots(k6, all, e, total, &prep) == PF_OK, "staged publish");
+    expect(store.sealed_count() == before + 3, "keys 10, 12 and 13 sealed");
+    expect(store.peek(k6[1]) == sealed11, "the block sealed meanwhile stays");
+    auto b10 = store.peek(k6[0]);
+    expect(b10 && tag_of(b10->slots[3]) == 9000 + 30 + 0 + 1, "a key named twice keeps its first");
+    auto b12 = store.peek(k6[2]);
+    expect(b12 && tag_of(b12->slots[0]) == 8000 + 0 + 2 + 1 &&
+               tag_of(b12->slots[1]) == 9000 + 10 + 2 + 1,
+           "the in-flight key keeps its earlier slot and takes the rest");
+    expect(store.inflight_count() == 1, "only key 5 of check 5 is left in flight");
+    expect(prep.nodes.empty() && prep.blocks.empty(), "the prepared call is consumed");
+    // Recency: evicting all but three leaves the three most recent: key 12
+    // (sealed through the in-flight path, last), then 13 and 10 (the staged
+    // nodes, most recent first).
+    const uint64_t n = store.sealed_count();
+    expect(store.evict_lru(n - 3) == n - 3, "eviction");
+    expect(store.peek(k6[2]) && store.peek(k6[3]) && store.peek(k6[0]),
+           "the staged and completed blocks are the most recent");
+    expect(store.evict_lru(1) == 1 && !store.peek(k6[0]) && store.peek(k6[3]),
+           "key 10, staged first, is the older of the staged two");
   }
   if (failures) return 1;
   std::printf("ok\n");
