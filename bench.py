@@ -7,7 +7,9 @@ of 640 blocks drawn uniformly at random without replacement.  One step is a
 full save of the prefix to the pinned host pool (in the reference's split
 K/V host layout) followed by a full restore of it into 640 other random
 blocks: P = 1,342,177,280 payload bytes cross the host link in each
-direction.
+direction.  By default the save runs in PF_MODE_AUTO (staged: an HBM gather
+and copy-engine DMA, the engine's deployed mode) and the restore by the
+zero-copy kernel (--save-mode / --load-mode change them).
 
 Printed JSON line (stdout):
   value            save+restore payload GB/s over the timed steps (2P/step)
@@ -15,12 +17,12 @@ Printed JSON line (stdout):
                    measured host-link peak (best 1 GiB hipMemcpyAsync) and of
                    PCIe Gen5 x16 (63.0 GB/s)
   save_*           HBM -> host save, same figures
-  roofline         the timed step's dominant kernel, the zero-copy save
-                   (paged HBM -> pinned host over the host link): P per call /
+  roofline         the timed step's dominant kernel, the zero-copy restore
+                   (pinned host -> paged HBM over the host link): P per call /
                    its kernel time (HIP events on the context's stream), vs
-                   PCIe Gen5 x16 and vs the measured D2H peak; the restore
-                   kernel beside it; traffic from the committed rocprofv3
-                   summary it names (traffic_source)
+                   PCIe Gen5 x16 and vs the measured H2D peak; the save beside
+                   it (staged: its link rate by wall clock); traffic from the
+                   committed rocprofv3 summary it names (traffic_source)
   device_gather    the HBM-bound gather of the staged mode (paged layers ->
                    packed HBM buffer, all 32 layers in one launch): 2P per
                    launch / its duration, vs 8 TB/s; also the same kernel on
@@ -70,10 +72,10 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--save-mode", default="kernel",
-                    choices=["dma_reference", "dma_batched", "kernel", "staged"])
+    ap.add_argument("--save-mode", default="auto",
+                    choices=["dma_reference", "dma_batched", "kernel", "staged", "auto"])
     ap.add_argument("--load-mode", default="kernel",
-                    choices=["dma_reference", "dma_batched", "kernel", "staged"])
+                    choices=["dma_reference", "dma_batched", "kernel", "staged", "auto"])
     ap.add_argument("--variants", action="store_true",
                     help="also time every transfer mode with --quick (always done without it)")
     ap.add_argument("--sweep", action="store_true",
@@ -1491,15 +1493,14 @@ def profile_kernels(kind, seed):
     xfer.close()
 
 
-def read_traffic(name):
-    """HBM bytes per launch from a committed rocprofv3 --pmc summary under
-    profiles/ (its "traffic_bytes_per_launch = N" line), with the file's
-    name, or (None, None)."""
+def read_traffic(name, key="traffic_bytes_per_launch"):
+    """Memory traffic in bytes from a committed rocprofv3 --pmc summary under
+    profiles/ (its "<key> = N" line), with the file's name, or (None, None)."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", name)
     try:
         with open(path) as fh:
             for line in fh:
-                if line.startswith("traffic_bytes_per_launch"):
+                if line.startswith(key + " ") or line.startswith(key + "="):
                     return int(line.split("=")[1].strip()), "profiles/" + name
     except OSError:
         pass
@@ -1993,9 +1994,46 @@ def main():
         log(f"[bench] {extra['disk_tier_llama3_8b']}")
 
     k_save_ms, k_load_ms = statistics.median(k_save), statistics.median(k_load)
-    link_save_gbps = P / (k_save_ms / 1e3) / 1e9
-    link_restore_gbps = P / (k_load_ms / 1e3) / 1e9
-    save_traffic, save_traffic_src = read_traffic("copy_chunks_llama3_8b_zerocopy_traffic.txt")
+    # The step's dominant kernel: a side whose host-link bytes a kernel moves
+    # (the zero-copy kernel) spends about its whole call in that kernel; a
+    # staged side's kernels are its HBM gather or scatter, a few percent of
+    # the call, and its link bytes are copy-engine DMA.
+    zc_file = "copy_chunks_llama3_8b_zerocopy_traffic.txt"
+    sides = {
+        "save": {"kernel_ms": k_save_ms, "wall_s": save_s, "peak": d2h_peak,
+                 "zero_copy": k_save_ms > 0.5 * save_s * 1e3,
+                 "traffic": read_traffic(zc_file, "save_traffic_bytes_per_call"),
+                 "kernel": "copy_chunks_queue_kernel<2,nt-loads> 512 threads x 32 persistent "
+                           "workgroups (zero-copy save: 40,960 chunks of 32 KiB, paged HBM -> "
+                           "pinned host, 2 launches per call)"},
+        "restore": {"kernel_ms": k_load_ms, "wall_s": load_s, "peak": h2d_peak,
+                    "zero_copy": k_load_ms > 0.5 * load_s * 1e3,
+                    "traffic": read_traffic(zc_file, "restore_traffic_bytes_per_call"),
+                    "kernel": "copy_chunks_queue_kernel<2,nt,nt> 512 threads x 64 persistent "
+                              "workgroups (zero-copy restore: 40,960 chunks of 32 KiB, pinned "
+                              "host -> paged HBM, 2 launches per call)"},
+    }
+
+    def side_entry(name):
+        sd = sides[name]
+        if sd["zero_copy"]:
+            gbps = P / (sd["kernel_ms"] / 1e3) / 1e9
+            return {"kernel": sd["kernel"], "achieved": round(gbps, 2),
+                    "frac": round(gbps / PCIE_GEN5_X16_GBPS, 4),
+                    "measured_peak": round(sd["peak"], 2),
+                    "frac_of_measured_peak": round(gbps / sd["peak"], 4),
+                    "ms_per_call": round(sd["kernel_ms"], 4),
+                    "traffic": sd["traffic"][0], "traffic_source": sd["traffic"][1]}
+        gbps = P / sd["wall_s"] / 1e9
+        return {"mode": "staged: HBM gather/scatter kernels on the device, the host-link "
+                        "bytes by copy-engine DMA (wall clock)",
+                "link_gbps": round(gbps, 2), "frac": round(gbps / PCIE_GEN5_X16_GBPS, 4),
+                "measured_peak": round(sd["peak"], 2),
+                "frac_of_measured_peak": round(gbps / sd["peak"], 4),
+                "hbm_kernel_ms_per_call": round(sd["kernel_ms"], 4)}
+
+    zc_sides = [n for n in ("save", "restore") if sides[n]["zero_copy"]]
+    dominant = max(zc_sides, key=lambda n: sides[n]["kernel_ms"]) if zc_sides else None
     gather_traffic, gather_traffic_src = read_traffic("copy_chunks_llama3_8b_prefix_traffic.txt")
     scatter_traffic, scatter_traffic_src = read_traffic(
         "copy_chunks_llama3_8b_scatter_traffic.txt")
@@ -2039,35 +2077,15 @@ def main():
         "save_kernel_ms": round(k_save_ms, 3),
         "host_link_peak_gbps": {"h2d": round(h2d_peak, 2), "d2h": round(d2h_peak, 2),
                                 "pcie_gen5_x16": PCIE_GEN5_X16_GBPS},
-        # The timed step is two host-link kernels; the save, the longer of
-        # the two, is the dominant kernel.  Achieved = P per call / the
-        # call's kernel time (HIP events on the context's stream around
-        # each launch, summed over the call's two launches).
-        "roofline": {
-            "bound": "pcie",
-            "kernel": "copy_chunks_queue_kernel<2,nt-loads> 512 threads x 32 persistent "
-                      "workgroups (zero-copy save: 40,960 chunks of 32 KiB, paged HBM -> "
-                      "pinned host, 2 launches per call)",
-            "achieved": round(link_save_gbps, 2),
-            "peak": PCIE_GEN5_X16_GBPS,
-            "unit": "GB/s",
-            "frac": round(link_save_gbps / PCIE_GEN5_X16_GBPS, 4),
-            "measured_peak": round(d2h_peak, 2),
-            "frac_of_measured_peak": round(link_save_gbps / d2h_peak, 4),
-            "bytes_per_call": P,
-            "ms_per_call": round(k_save_ms, 4),
-            "traffic": save_traffic,
-            "traffic_source": save_traffic_src,
-            "restore": {
-                "kernel": "copy_chunks_queue_kernel<2,nt,nt> 512 threads x 64 persistent "
-                          "workgroups (zero-copy restore, pinned host -> paged HBM)",
-                "achieved": round(link_restore_gbps, 2),
-                "frac": round(link_restore_gbps / PCIE_GEN5_X16_GBPS, 4),
-                "measured_peak": round(h2d_peak, 2),
-                "frac_of_measured_peak": round(link_restore_gbps / h2d_peak, 4),
-                "ms_per_call": round(k_load_ms, 4),
-            },
-        },
+        # The step's dominant kernel (the zero-copy side with the longer
+        # kernel time): achieved = P per call / the call's kernel time (HIP
+        # events on the context's stream around each launch, summed over the
+        # call's two launches); the other side as a sub-entry.
+        "roofline": ({"bound": "pcie", "peak": PCIE_GEN5_X16_GBPS, "unit": "GB/s",
+                      "bytes_per_call": P, "side": dominant, **side_entry(dominant),
+                      ("restore" if dominant == "save" else "save"):
+                          side_entry("restore" if dominant == "save" else "save")}
+                     if dominant else None),
         # The HBM-bound kernels of the staged mode, timed outside the steps.
         "device_gather": {
             "bound": "hbm",
@@ -2109,6 +2127,8 @@ def main():
         "bit_exact": bad_host == 0 and bad_dev == 0,
         "cpu_baseline": cpu,
     }
+    if out["roofline"] is None:  # no zero-copy side: the staged mode's HBM kernel
+        out["roofline"] = dict(out["device_scatter"], side="device scatter (staged restore)")
     out.update(extra)
     if micro is not None:
         out["pinned_copy_microbench"] = micro

@@ -58,6 +58,10 @@ constexpr uint32_t kMaxFrame = (1u << 24) - 1;  // SETTINGS_MAX_FRAME_SIZE we ad
 constexpr int64_t kMaxWindow = 0x7fffffff;       // our windows: as large as allowed
 constexpr size_t kMaxHeaderBlock = 1 << 20;
 constexpr uint32_t kMaxStreams = 1024;
+// Request bytes one connection may hold at once, over all its streams (two
+// of the largest requests); a stream that would pass it is answered
+// RESOURCE_EXHAUSTED, as a single oversized request is.
+constexpr uint64_t kMaxConnBuffered = 2ull * PF_REQUEST_MAX_BYTES + 10;
 constexpr uint64_t kWindowRefill = 64ull << 20;  // connection window given back per
 constexpr size_t kWorkers = 8;
 
@@ -197,6 +201,10 @@ class Conn : public std::enable_shared_from_this<Conn> {
   std::unordered_map<uint32_t, Stream> streams_;
   uint32_t last_sid_ = 0, continuation_of_ = 0;
   uint64_t consumed_ = 0;
+  uint64_t buffered_ = 0;  // bytes of request bodies held in streams_
+  // Drops a stream's body from the count (before the stream is erased or
+  // its body handed on).
+  void unbuffer(Stream& st) { buffered_ -= st.data.size(); }
 };
 
 }  // namespace
@@ -392,15 +400,19 @@ bool Conn::handle(uint8_t type, uint8_t flags, uint32_t sid, std::string& payloa
       if (it == streams_.end() || !it->second.headers_done) return true;  // reset or unknown
       Stream& st = it->second;
       if (!st.rejected) {
-        if (st.data.size() + n > PF_REQUEST_MAX_BYTES + 5ull) {
+        if (st.data.size() + n > PF_REQUEST_MAX_BYTES + 5ull ||
+            buffered_ + n > kMaxConnBuffered) {
+          unbuffer(st);
           st.rejected = true;
           st.data.clear();
           st.data.shrink_to_fit();
         } else {
           st.data.append(payload, off, n);
+          buffered_ += n;
         }
       }
       if (flags & kEndStream) {
+        unbuffer(st);
         Stream done = std::move(st);
         streams_.erase(it);
         complete(sid, std::move(done));
@@ -443,6 +455,10 @@ bool Conn::handle(uint8_t type, uint8_t flags, uint32_t sid, std::string& payloa
       // table must stay in step) and otherwise ignored.
       Stream& st = it->second;
       st.block.append(payload, off, n);
+      if (st.block.size() > kMaxHeaderBlock) {
+        goaway(kProtocolError);
+        return false;
+      }
       st.end_after_block = (flags & kEndStream) != 0;
       if (!(flags & kEndHeaders)) {
         continuation_of_ = sid;
@@ -524,18 +540,55 @@ bool Conn::handle(uint8_t type, uint8_t flags, uint32_t sid, std::string& payloa
       const int64_t inc = ((uint32_t(uint8_t(payload[0])) & 0x7f) << 24) |
                           (uint32_t(uint8_t(payload[1])) << 16) |
                           (uint32_t(uint8_t(payload[2])) << 8) | uint8_t(payload[3]);
-      std::lock_guard<std::mutex> lk(wmu_);
+      bool bad_window = false;
+      // RFC 9113 6.9: an increment of 0, or one that takes a window past
+      // 2^31-1, is an error (of the connection, or of the stream).
       if (sid == 0) {
-        conn_window_ += inc;
+        std::lock_guard<std::mutex> lk(wmu_);
+        if (inc == 0 || conn_window_ + inc > kMaxWindow) {
+          bad_window = true;
+        } else {
+          conn_window_ += inc;
+          wcv_.notify_all();
+        }
       } else {
-        auto it = live_.find(sid);
-        if (it != live_.end()) it->second += inc;
+        bool reset = false;
+        {
+          std::lock_guard<std::mutex> lk(wmu_);
+          auto it = live_.find(sid);
+          if (it != live_.end()) {
+            if (inc == 0 || it->second + inc > kMaxWindow) {
+              live_.erase(it);
+              std::string out, p;
+              put32(&p, inc == 0 ? kProtocolError : kFlowControlError);
+              frame(&out, kRstStream, 0, sid, p.data(), p.size());
+              (void)send_locked(out);
+              reset = true;
+            } else {
+              it->second += inc;
+            }
+          }
+          wcv_.notify_all();
+        }
+        if (reset) {
+          auto st = streams_.find(sid);
+          if (st != streams_.end()) {
+            unbuffer(st->second);
+            streams_.erase(st);
+          }
+        }
       }
-      wcv_.notify_all();
+      if (bad_window) {
+        goaway(inc == 0 ? kProtocolError : kFlowControlError);
+        return false;
+      }
       return true;
     }
     case kRstStream: {
-      streams_.erase(sid);
+      if (auto st = streams_.find(sid); st != streams_.end()) {
+        unbuffer(st->second);
+        streams_.erase(st);
+      }
       std::lock_guard<std::mutex> lk(wmu_);
       live_.erase(sid);
       wcv_.notify_all();
@@ -562,6 +615,7 @@ bool Conn::headers_complete(uint32_t sid, Stream& st) {
   st.block.clear();
   if (st.headers_done) {  // trailers
     if (st.end_after_block) {
+      unbuffer(st);
       Stream done = std::move(st);
       streams_.erase(sid);
       complete(sid, std::move(done));

@@ -168,3 +168,67 @@ def test_clients_breaking_the_protocol_do_not_disturb_others(native):
     for _ in range(20):
         with EngineRpcClient(f"http://{native.addr}") as client:
             assert client.health() == (True, "")
+
+
+def _goaway_code(host, port, frames_after_settings):
+    """The error code of the server's GOAWAY after the preface, our SETTINGS
+    and the given bytes; the connection must then close."""
+    s = socket.create_connection((host, port))
+    try:
+        s.sendall(PREFACE + _frame(4, 0, 0) + frames_after_settings)
+        got, closed = _read_until_closed(s)
+        assert closed
+        goaways = [f for f in _frames(got) if f[0] == 7]
+        assert goaways, "no GOAWAY"
+        return int.from_bytes(goaways[0][3][4:8], "big")
+    finally:
+        s.close()
+
+
+def test_per_connection_limits(native):
+    """A header block over 1 MiB in a single HEADERS frame is refused as one
+    spread over CONTINUATION frames is (PROTOCOL_ERROR); a WINDOW_UPDATE that
+    takes the connection's window past 2^31-1 is a FLOW_CONTROL_ERROR, and an
+    increment of 0 a PROTOCOL_ERROR (RFC 9113 6.9); the server keeps serving
+    other clients."""
+    host, port = native.addr.rsplit(":", 1)
+    port = int(port)
+    big = b"\x00" + bytes([0x7f]) + b"\x81\x80\x40" + b"x" * (1 << 20)  # a literal > 1 MiB
+    assert _goaway_code(host, port, _frame(1, 0x4 | 0x1, 1, big)) == 1
+    assert _goaway_code(host, port, _frame(8, 0, 0, struct.pack(">I", 0x7fffffff))) == 3
+    assert _goaway_code(host, port, _frame(8, 0, 0, struct.pack(">I", 0))) == 1
+    with EngineRpcClient(f"http://{native.addr}") as client:
+        assert client.health() == (True, "")
+
+
+def _literal(name, value):
+    """An HPACK literal header field without indexing, new name (short)."""
+    return bytes([0, len(name)]) + name + bytes([len(value)]) + value
+
+
+def test_stream_window_overflow_resets_only_that_stream(native):
+    """A WINDOW_UPDATE taking one open stream's window past 2^31-1 resets
+    that stream (RST_STREAM FLOW_CONTROL_ERROR); the connection goes on (a
+    PING is still answered)."""
+    host, port = native.addr.rsplit(":", 1)
+    block = b"".join(_literal(n, v) for n, v in (
+        (b":method", b"POST"), (b":scheme", b"http"), (b":path", b"/pegaflow.Engine/Health"),
+        (b":authority", b"x"), (b"content-type", b"application/grpc"), (b"te", b"trailers")))
+    s = socket.create_connection((host, int(port)))
+    try:
+        s.sendall(PREFACE + _frame(4, 0, 0) + _frame(1, 0x4, 1, block) +  # headers, no end
+                  _frame(8, 0, 1, struct.pack(">I", 0x7fffffff)) + _frame(6, 0, 0, b"pingpong"))
+        s.settimeout(5)
+        got, t0 = b"", time.monotonic()
+        while time.monotonic() - t0 < 5:
+            frames = _frames(got)
+            if any(f[0] == 6 and f[1] == 1 for f in frames):
+                break
+            got += s.recv(65536)
+        frames = _frames(got)
+        rst = [f for f in frames if f[0] == 3 and f[2] == 1]
+        assert rst and int.from_bytes(rst[0][3], "big") == 3
+        assert any(f[0] == 6 and f[1] == 1 and f[3] == b"pingpong" for f in frames)
+        assert not any(f[0] == 7 for f in frames)  # no GOAWAY
+    finally:
+        s.close()
