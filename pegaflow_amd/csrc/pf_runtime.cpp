@@ -286,7 +286,7 @@ EngineDevice discover_engines(int device) {
   d.engine[0][0] = d.engine[0][1] = d0;
   d.engine[1][0] = d.engine[1][1] = h0;
   // PEGAFLOW_COPY_ENGINES="<d2h>,<h2d>" (engine id bit masks, one or two
-  // bits each, e.g. "0x2,0x1") overrides the choice; masks the runtime does
+  // bits each, e.g. "0x8,0x4") overrides the choice; masks the runtime does
   // not report available are ignored.
   if (const char* env = std::getenv("PEGAFLOW_COPY_ENGINES")) {
     unsigned long m[2] = {0, 0};

@@ -205,14 +205,16 @@ def test_staged_two_lanes_queued_vs_oracle(gpu):
 
 
 def test_staged_pipelined_load_vs_oracle(gpu):
-    """A staged load large enough to be pipelined (9 layers, 19,606 chunks):
-    its first layer is copied (by the zero-copy kernel when the caller waits
-    layer by layer, else sliced onto the copy engine) before the other layers
-    are planned.  After the first layer come an empty layer, a layer copied
+    """A staged save and load large enough to be pipelined (9 layers, 19,606
+    chunks).  The save slices its first layer onto the copy engine and plans
+    the rest under that copy; the load copies its first layer (by the
+    zero-copy kernel when the caller waits layer by layer, else sliced onto
+    the copy engine) before the other layers are planned.  After the first layer come an empty layer, a layer copied
     in place in list order, and a layer whose host region is ordinary
     (pageable) memory, copied through HIP run by run; slices start small and
-    grow.  Bytes against the oracle for a load with per-layer events (in
-    layer order), a marked load (every layer's mark set) and a plain one."""
+    grow.  Bytes against the oracle for the save (pinned and pageable host
+    regions), a load with per-layer events (in layer order), a marked load
+    (every layer's mark set) and a plain one."""
     say("[gpu] staged pipelined load, mixed later layers")
     ctx = TransferContext(0, staging_bytes=64 * 1024)
     nb, bpb = 2048, 256
