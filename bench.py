@@ -957,9 +957,10 @@ def leg_gpt2(xfer, seed):
 def leg_tp_rank(xfer, seed):
     """The Llama prefix as one tensor-parallel rank sees it at TP=8: 32 layers
     [2,20000,16,1,128] (one kv head, 4 KiB segments), 640 random blocks, save
-    then restore, in the kernel mode and in the reference's call pattern
-    (one synchronous copy per segment for the save, one async copy per merged
-    run for the restore) and merged-run DMA."""
+    then restore, in the kernel mode, the staged mode and AUTO (the engine's
+    default), in the reference's call pattern (one synchronous copy per
+    segment for the save, one async copy per merged run for the restore) and
+    merged-run DMA."""
     from pegaflow_amd import _lib
     from pegaflow_amd import workload as wl
     from pegaflow_amd.runtime import PinnedBuffer
@@ -975,7 +976,8 @@ def leg_tp_rank(xfer, seed):
                        "[2,20000,16,1,128], 640 random blocks, save then restore",
            "payload_bytes": P, "segment_bytes": shape.bytes_per_block}
     bad = 0
-    for mode, reps in (("kernel", 5), ("dma_batched", 1), ("dma_reference", 1)):
+    for mode, reps in (("kernel", 5), ("staged", 5), ("auto", 5), ("dma_batched", 1),
+                       ("dma_reference", 1)):
         m = _lib.MODE_NAMES[mode]
         t_s = timed(lambda: xfer.save_layers(saved, m), reps)
         t_l = timed(lambda: (xfer.load_layers(loads, m), xfer.synchronize()), reps)

@@ -1582,10 +1582,13 @@ int pf_engine_batch_save(pf_engine* e, const char* instance_id, uint64_t tp_rank
     // the rest (about 10 ns per later block entry, in which the link moves
     // about 500 bytes): one layer for the Llama prefix.
     constexpr uint64_t kHeadBytesPerLaterEntry = 500;
-    uint64_t head_bytes = 0;
+    uint64_t later_entries = 0, head_bytes = 0;
+    for (size_t pi : order) later_entries += plans[pi].ids.size();
     for (head = 0; head + 1 < nl;) {
-      head_bytes += plans[order[head++]].layout.block_size_bytes;
-      if (head_bytes >= (nl - head) * kHeadBytesPerLaterEntry) break;
+      const SavePlan& p = plans[order[head++]];
+      head_bytes += p.ids.size() * p.layout.block_size_bytes;
+      later_entries -= p.ids.size();
+      if (head_bytes >= later_entries * kHeadBytesPerLaterEntry) break;
     }
   }
   for (uint32_t k = 1; k < head; ++k)
