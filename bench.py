@@ -1608,9 +1608,12 @@ def cpu_baseline(shape, ids, targets, n_layers, seed, device=0):
     load = [np.concatenate(x) for x in (ls, ld, lz)]
     payload = n_layers * n * 2 * bpb
 
-    def run(t):
+    # Passes are repeated for at least `seconds` (and 5 passes); the median
+    # pass is reported.
+    def run(t, seconds):
         ts, tl = [], []
-        for _ in range(5):
+        start = time.perf_counter()
+        while len(ts) < 5 or (time.perf_counter() - start < seconds and len(ts) < 5000):
             t0 = time.perf_counter()
             oracle.run_copies(*save, nthreads=t)
             t1 = time.perf_counter()
@@ -1618,19 +1621,19 @@ def cpu_baseline(shape, ids, targets, n_layers, seed, device=0):
             t2 = time.perf_counter()
             ts.append(t1 - t0)
             tl.append(t2 - t1)
-        return statistics.median(ts), statistics.median(tl)
+        return statistics.median(ts), statistics.median(tl), len(ts), time.perf_counter() - start
 
     def targets_of(t):
         return t.reshape(2, nb, bpb)[:, targets]
 
-    run(threads)  # warm
-    s_mt, l_mt = run(threads)
+    run(threads, 0)  # warm
+    s_mt, l_mt, reps_mt, secs_mt = run(threads, 6.0)
     pool_mt = pool.copy()
     tgt_mt = [targets_of(t) for t in tensors]
     pool[:] = 0
     for t in tensors:
         t.reshape(2, nb, bpb)[:, targets] = 0
-    s_1, l_1 = run(1)
+    s_1, l_1, reps_1, secs_1 = run(1, 4.0)
     bad = int(np.count_nonzero(pool != pool_mt))
     bad += sum(int(np.count_nonzero(targets_of(t) != m)) for t, m in zip(tensors, tgt_mt))
     for l, t in enumerate(tensors):
@@ -1649,8 +1652,9 @@ def cpu_baseline(shape, ids, targets, n_layers, seed, device=0):
         "cores": threads,
         "kind": "port",
         "sample": (f"{n_layers} of {shape.layers} layers of the same workload "
-                   f"({n} blocks, save then restore, {2 * payload / 1e6:.0f} MB moved), "
-                   "host memory, median of 5"),
+                   f"({n} blocks, save then restore, {2 * payload / 1e6:.0f} MB moved per "
+                   f"pass), host memory; median pass of {reps_mt} over {secs_mt:.1f} s on "
+                   f"{threads} threads, of {reps_1} over {secs_1:.1f} s on one"),
         "save_gbps": round(payload / s_mt / 1e9, 3),
         "restore_gbps": round(payload / l_mt / 1e9, 3),
         "single_thread_gbps": round(2 * payload / (s_1 + l_1) / 1e9, 3),
