@@ -28,8 +28,10 @@ from pegaflow_amd.transfer import (KVCacheRegistration, LayerTransfer, TransferC
 
 pytestmark = pytest.mark.gpu
 
+# AUTO picks the kernel or the staged mode per call from the host side's
+# run lengths, so it meets both choices across the run lengths below.
 MODES = {"dma_reference": _lib.MODE_DMA_REFERENCE, "dma_batched": _lib.MODE_DMA_BATCHED,
-         "kernel": _lib.MODE_KERNEL, "staged": _lib.MODE_STAGED}
+         "kernel": _lib.MODE_KERNEL, "staged": _lib.MODE_STAGED, "auto": _lib.MODE_AUTO}
 MEANS = (1, 4, 32, 640)
 
 
