@@ -101,6 +101,9 @@ def parse():
                          "and the two queued kernels' grids in duplex")
     ap.add_argument("--interference-study", action="store_true",
                     help="only run the cross-process interference study (one JSON line)")
+    ap.add_argument("--first-layer-study", action="store_true",
+                    help="only run the first-layer study: layer-by-layer restores beside a "
+                         "GEMM in another process (one JSON line)")
     ap.add_argument("--study-engines", default="",
                     help="with --interference-study: staged phases only, once per copy-engine "
                          "pair, e.g. '0x2:0x1,0x8:0x4' (device-to-host mask:host-to-device mask)")
@@ -426,6 +429,156 @@ def interference_study(engines: str = "", victim_list: str = ""):
                                f"{pv.exitcode}")
         result["victims"][kind] = res
     print(json.dumps(result), flush=True)
+
+
+def _first_layer_victim(go, stop, ready, count):
+    """GEMM process of the first-layer study: bf16 8192^3 products back to
+    back, two per synchronization, counted in `count`."""
+    import torch  # initialized here, in a process that never loads the library
+
+    a = torch.randn(8192, 8192, device="cuda", dtype=torch.bfloat16)
+    b = torch.randn(8192, 8192, device="cuda", dtype=torch.bfloat16)
+    c = torch.empty(8192, 8192, device="cuda", dtype=torch.bfloat16)
+    for _ in range(3):
+        torch.mm(a, b, out=c)
+    torch.cuda.synchronize()
+    ready.set()
+    go.wait()
+    while not stop.is_set():
+        torch.mm(a, b, out=c)
+        torch.mm(a, b, out=c)
+        torch.cuda.synchronize()
+        with count.get_lock():
+            count.value += 2
+
+
+def first_layer_study(reps=10):
+    """Layer-by-layer restores of the Llama prefix beside bf16 8192^3 GEMMs
+    that another process runs back to back.  Each restore marks its layers
+    in pinned host memory; this process polls layer 0's mark while another
+    thread issues the load (a staged load returns once its copies are done).
+    Variants, interleaved, `reps` loads each: the staged mode with its first
+    layer by the zero-copy kernel (the default) or by the copy engines
+    (pf_xfer_set_staged_head), the kernel mode, and whole loads of both
+    modes.  Reports per variant the first layer's latency from the call, the
+    load's rate, and the GEMM's rate during the variant's loads against its
+    rate alone; then the same loads on an idle device.  One JSON line."""
+    import multiprocessing as mp
+    import threading
+
+    from pegaflow_amd import _lib, runtime
+    from pegaflow_amd import workload as wl
+    from pegaflow_amd.runtime import PinnedBuffer
+    from pegaflow_amd.transfer import TransferContext
+
+    ctx = mp.get_context("spawn")
+    go, stop, ready = ctx.Event(), ctx.Event(), ctx.Event()
+    count = ctx.Value("l", 0)
+    victim = ctx.Process(target=_first_layer_victim, args=(go, stop, ready, count))
+    victim.start()
+    runtime.init(0)
+    shape = wl.LLAMA3_8B
+    layers = wl.DeviceLayers(shape, base_seed=0)
+    ids, targets = wl.draw_blocks(shape.num_blocks, 640, 0)
+    P = wl.payload_bytes(layers.regs, 640)
+    pool = PinnedBuffer(P)
+    x_kernel_head = TransferContext(0, staging_bytes=512 << 20)
+    x_engine_head = TransferContext(0, staging_bytes=512 << 20)
+    x_engine_head.set_staged_head(_lib.STAGED_HEAD_ENGINE)
+    saved = wl.save_plan(layers.regs, ids, pool.ptr)
+    loads = wl.load_plan(saved, targets)
+    x_kernel_head.save_layers(saved, _lib.MODE_KERNEL)
+    words = PinnedBuffer(8 * len(loads))
+    wv = words.array.view(np.uint64)
+    wv[:] = 0
+    serial = [0]
+
+    def marked(x, mode):
+        serial[0] += 1
+        val = serial[0]
+        th = threading.Thread(target=lambda: x.load_layers_marked(
+            loads, [(words.ptr, val, True)], mode))
+        t0 = time.perf_counter()
+        th.start()
+        while wv[0] != val:
+            time.sleep(0)  # lets the issuing thread take the GIL
+        t1 = time.perf_counter()
+        th.join()
+        x.synchronize()
+        t2 = time.perf_counter()
+        if any(int(w) != val for w in wv):
+            raise RuntimeError("a layer's mark is missing after the load")
+        return t1 - t0, t2 - t0
+
+    def whole(x, mode):
+        t0 = time.perf_counter()
+        x.load_layers(loads, mode)
+        x.synchronize()
+        return None, time.perf_counter() - t0
+
+    variants = {
+        "staged_first_layer_by_kernel": lambda: marked(x_kernel_head, _lib.MODE_STAGED),
+        "staged_first_layer_by_copy_engine": lambda: marked(x_engine_head, _lib.MODE_STAGED),
+        "kernel": lambda: marked(x_kernel_head, _lib.MODE_KERNEL),
+        "staged_whole_load": lambda: whole(x_kernel_head, _lib.MODE_STAGED),
+        "kernel_whole_load": lambda: whole(x_kernel_head, _lib.MODE_KERNEL),
+    }
+    for f in variants.values():
+        f()
+    ready.wait()
+    go.set()
+    time.sleep(0.3)
+    c0, t0 = count.value, time.perf_counter()
+    time.sleep(1.5)
+    solo_rate = (count.value - c0) / (time.perf_counter() - t0)
+    runs = {k: {"first": [], "load": [], "gemms": 0, "secs": 0.0} for k in variants}
+    for _ in range(reps):
+        for name, f in variants.items():
+            r = runs[name]
+            c0, t0 = count.value, time.perf_counter()
+            first, load = f()
+            r["secs"] += time.perf_counter() - t0
+            r["gemms"] += count.value - c0
+            if first is not None:
+                r["first"].append(first * 1e3)
+            r["load"].append(load)
+    stop.set()
+    victim.join(60)
+    if victim.exitcode != 0:
+        raise RuntimeError(f"GEMM process exited {victim.exitcode}")
+    beside = {}
+    for name, r in runs.items():
+        e = {"load_gbps": round(P / statistics.median(r["load"]) / 1e9, 2),
+             "gemm_slowdown": round(solo_rate / (r["gemms"] / r["secs"]), 3),
+             "gemms": r["gemms"]}
+        if r["first"]:
+            e.update(first_layer_ms=round(statistics.median(r["first"]), 3),
+                     first_layer_ms_min=round(min(r["first"]), 3),
+                     first_layer_ms_max=round(max(r["first"]), 3))
+        beside[name] = e
+    idle = {}
+    for name, f in variants.items():
+        got = [f() for _ in range(5)]
+        e = {"load_gbps": round(P / statistics.median([g[1] for g in got]) / 1e9, 2)}
+        if got[0][0] is not None:
+            e["first_layer_ms"] = round(statistics.median([g[0] for g in got]) * 1e3, 3)
+        idle[name] = e
+    bad = wl.verify_restored(layers, ids, targets)
+    print(json.dumps({
+        "metric": "first layer of a layer-by-layer restore beside a GEMM in another process",
+        "transfer": "llama-3.1-8b 10k-token prefix (32 x [2,20000,16,8,128] bf16, 640 blocks), "
+                    "each layer marked in pinned host memory",
+        "gemm": "bf16 8192^3 torch.mm back to back, two per synchronization",
+        "gemm_alone_ms": round(1e3 / solo_rate, 3),
+        "loads_per_variant": reps,
+        "beside_gemm": beside,
+        "idle": idle,
+        "bit_exact": bad == 0}), flush=True)
+    for x in (x_kernel_head, x_engine_head):
+        x.close()
+    words.close()
+    pool.close()
+    layers.close()
 
 
 def duplex_study(xfer_load, xfer_save, saved, loads, pool, pool2, dev_buf, P, reps=4):
@@ -1760,6 +1913,9 @@ def main():
         return
     if args.interference_study:
         interference_study(args.study_engines, args.study_victims)
+        return
+    if args.first_layer_study:
+        first_layer_study()
         return
     if args.leg:
         run_leg(args)

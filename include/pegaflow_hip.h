@@ -404,6 +404,23 @@ int pf_set_copy_engines(int device, uint32_t d2h_engines, uint32_t h2d_engines);
 #define PF_STAGED_SAVE_SLICE_DEFAULT (256ull << 20)
 #define PF_STAGED_LOAD_SLICE_DEFAULT (256ull << 20)
 int pf_xfer_set_staged_slices(pf_xfer* xfer, uint64_t save_bytes, uint64_t load_bytes);
+/* How a staged load whose caller waits layer by layer (marks or per-layer
+ * events) copies its first layer: PF_STAGED_HEAD_KERNEL (the default) by the
+ * zero-copy kernel, PF_STAGED_HEAD_ENGINE through the copy engines as the
+ * rest.  The kernel lands the first layer earliest; the copy engine keeps
+ * the whole load off the CUs.  Measured on the Llama-3.1-8B prefix beside a
+ * bf16 8192^3 GEMM run back to back by another process (bench.py
+ * --first-layer-study): the kernel head lands the first layer 1.43 ms after
+ * the call, the load runs at 50.0 GB/s and the GEMM 1.11x slower; the
+ * copy-engine head 3.09 ms (its scatter waits for CUs), 55.0 GB/s and 1.03x.
+ * On an idle device: 0.96 and 1.02 ms, 55.8 GB/s both.  The environment
+ * variable PEGAFLOW_STAGED_HEAD=engine makes the copy engines the default of
+ * contexts created afterwards, the engine's included.  Other routes:
+ * PF_ERR_INVALID_ARGUMENT.  No counterpart in the reference (its loads are
+ * one cuMemcpyHtoDAsync per run). */
+#define PF_STAGED_HEAD_KERNEL 0u
+#define PF_STAGED_HEAD_ENGINE 1u
+int pf_xfer_set_staged_head(pf_xfer* xfer, uint32_t route);
 /* Number of gather/scatter kernel launches and DMA copies issued by the last
  * save/load call on this context. */
 int pf_xfer_last_stats(pf_xfer* xfer, uint64_t* kernel_launches,

@@ -48,6 +48,10 @@ MODE_DMA_BATCHED = 1
 MODE_KERNEL = 2
 MODE_STAGED = 3
 MODE_AUTO = 4
+
+# First layer of a layer-by-layer staged load (pf_xfer_set_staged_head).
+STAGED_HEAD_KERNEL = 0
+STAGED_HEAD_ENGINE = 1
 MODE_NAMES = {
     "dma_reference": MODE_DMA_REFERENCE,
     "dma_batched": MODE_DMA_BATCHED,
@@ -271,6 +275,7 @@ SIGNATURES = {
     "pf_xfer_route_shape": (i32, [vp, u32, ctypes.POINTER(u32), ctypes.POINTER(u32),
                                   ctypes.POINTER(i32)]),
     "pf_xfer_set_route_grid": (i32, [vp, u32, u32]),
+    "pf_xfer_set_staged_head": (i32, [vp, u32]),
     "pf_xfer_set_timing": (i32, [vp, i32]),
     "pf_xfer_last_kernel_ms": (i32, [vp, ctypes.POINTER(ctypes.c_float), pu64]),
     "pf_save_layers": (i32, [vp, ctypes.POINTER(LayerXfer), u32, u32]),

@@ -140,6 +140,10 @@ class StagedPlanner {
   // Descriptors of the slices start at index n (before any slice).
   void start_descriptors_at(size_t n) { sp_->n_desc = n; }
 
+  // The largest slice this planner makes of chunks up to `chunk` bytes: the
+  // slice cap, or one chunk when a chunk is larger.
+  uint64_t max_slice_bytes(uint64_t chunk) const { return std::max(max_cap_, chunk); }
+
   // Closes the open slice: the steps so far are final.
   int cut() {
     close();

@@ -4,6 +4,7 @@
 #include <algorithm>
 #include <chrono>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <vector>
@@ -329,6 +330,8 @@ struct pf_xfer {
   uint64_t slot_bytes = 0;
   // Largest staged slice per direction (0: save, 1: load), capped by slot_bytes.
   uint64_t staged_slice[2] = {PF_STAGED_SAVE_SLICE_DEFAULT, PF_STAGED_LOAD_SLICE_DEFAULT};
+  // A layer-by-layer staged load's first layer: PF_STAGED_HEAD_KERNEL or _ENGINE.
+  uint32_t staged_head = PF_STAGED_HEAD_KERNEL;
   // Recorded on a lane for the other lane to wait on (one per lane).
   hipEvent_t lane_mark[2] = {nullptr, nullptr};
   // Staged copies on the copy engines (when the device's are known): one
@@ -886,13 +889,24 @@ int staged_engine(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
                   pf_event* layer_events, const SignalTargets* sig, bool wait_save,
                   StagedTrace& tr) {
   const bool piped = head < num_layers;
-  // Slots: as many as the staging holds of the largest slice (at least one);
-  // a pipelined load's later slices are not known yet, so its slots are the
-  // staging's two.
-  uint64_t stride = piped ? x->slot_bytes : 0;
-  if (!piped)
+  // Slots: as many as the staging holds of the largest slice (at least one).
+  // A pipelined call's later slices are not known yet; each is at most the
+  // planner's cap or one chunk (a block or a segment of its layer's layout),
+  // so a load waited for layer by layer (64 MiB slices) keeps 8 slices in
+  // flight in 512 MiB of staging, not 2: each slice's scatter then has time
+  // to finish before its slot is needed again, also when the device's CUs
+  // are busy with other work.
+  uint64_t stride = 0;
+  if (piped) {
+    uint64_t chunk = 0;
+    for (uint32_t li = 0; li < num_layers; ++li)
+      chunk = std::max({chunk, layers[li].layout.block_size_bytes,
+                        layers[li].layout.bytes_per_block});
+    stride = std::min(x->slot_bytes, planner.max_slice_bytes(chunk));
+  } else {
     for (const StagedStep& st : sp.steps)
       if (st.ordered_layer < 0) stride = std::max<uint64_t>(stride, st.n_chunks * st.chunk_bytes);
+  }
   stride = (stride + 255) & ~uint64_t(255);
   size_t n_slots = 1;
   if (stride > 0)
@@ -1155,11 +1169,16 @@ int staged(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, bool is
   // events) copies its first layer with the zero-copy kernel, which has the
   // link at full rate from the call's start (the Llama prefix's first layer
   // in place 0.87 ms after an engine load's call, against 0.97 ms through
-  // the copy engine), and the rest staged once it is done: its 0.74 ms of
-  // shader traffic over the host link is the only part of the load that
-  // slows the device's other kernels.  A load completed as a whole stays
-  // staged throughout.
-  const bool kernel_head = engines && !is_save && head > 0 && head < num_layers &&
+  // the copy engine; beside a GEMM that holds every CU, 1.43 against 3.09
+  // ms, the engine's layer also waiting for CUs for its scatter), and the
+  // rest staged once it is done: its 0.74 ms of shader traffic over the host
+  // link is the only part of the load that slows the device's other kernels
+  // (that GEMM 1.11x during the load, against 1.03x; the load 50.0 against
+  // 55.0 GB/s).  The context's staged_head may send the first layer through
+  // the copy engines too.  A load completed as a whole stays staged
+  // throughout.
+  const bool kernel_head = x->staged_head == PF_STAGED_HEAD_KERNEL && engines && !is_save &&
+                           head > 0 && head < num_layers &&
                            (sig != nullptr || layer_events != nullptr);
   // A load waited for layer by layer (marks or per-layer events) keeps its
   // slices at most kLayeredLoadSlice, so each Llama layer (40 MiB) is a copy
@@ -1940,6 +1959,10 @@ int pf_xfer_create(int device, uint64_t staging_bytes, pf_xfer** out) {
   if (int rc = pf_init(device)) return rc;
   pf_xfer* x = new pf_xfer();
   x->device = device;
+  // PEGAFLOW_STAGED_HEAD=engine: new contexts (the engine's included) copy a
+  // layer-by-layer staged load's first layer through the copy engines.
+  if (const char* head = std::getenv("PEGAFLOW_STAGED_HEAD"))
+    if (std::strcmp(head, "engine") == 0) x->staged_head = PF_STAGED_HEAD_ENGINE;
   auto cleanup = [&](int rc) {
     pf_xfer_destroy(x);
     return rc;
@@ -2105,6 +2128,15 @@ int pf_xfer_set_staged_slices(pf_xfer* x, uint64_t save_bytes, uint64_t load_byt
   std::lock_guard<std::mutex> lk(x->mu);
   if (save_bytes) x->staged_slice[0] = save_bytes;
   if (load_bytes) x->staged_slice[1] = load_bytes;
+  return PF_OK;
+}
+
+int pf_xfer_set_staged_head(pf_xfer* x, uint32_t route) {
+  if (!x) return fail(PF_ERR_INVALID_ARGUMENT, "null transfer context");
+  if (route != PF_STAGED_HEAD_KERNEL && route != PF_STAGED_HEAD_ENGINE)
+    return fail(PF_ERR_INVALID_ARGUMENT, strf("unknown staged head route %u", route));
+  std::lock_guard<std::mutex> lk(x->mu);
+  x->staged_head = route;
   return PF_OK;
 }
 

@@ -249,6 +249,12 @@ class TransferContext:
         check(lib().pf_xfer_set_staged_slices(self.handle, save_bytes, load_bytes),
               "pf_xfer_set_staged_slices")
 
+    def set_staged_head(self, route: int) -> None:
+        """How a staged load waited for layer by layer copies its first layer:
+        _lib.STAGED_HEAD_KERNEL (zero-copy kernel, the default) or
+        _lib.STAGED_HEAD_ENGINE (copy engines; pf_xfer_set_staged_head)."""
+        check(lib().pf_xfer_set_staged_head(self.handle, route), "pf_xfer_set_staged_head")
+
     def set_max_grid(self, max_workgroups: int) -> None:
         check(lib().pf_xfer_set_max_grid(self.handle, max_workgroups), "pf_xfer_set_max_grid")
 

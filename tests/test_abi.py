@@ -37,6 +37,34 @@ def test_library_exports_every_declared_symbol():
     assert lib.pf_version().decode().startswith("pegaflow_hip")
 
 
+def header_constants():
+    """Every integer #define and enum value of the header, by name."""
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    raw = dict(re.findall(r"^#define (PF_[A-Z0-9_]+) (.+)$", text, flags=re.M))
+    raw.update(re.findall(r"(PF_[A-Z0-9_]+) = (-?[^,}\n]+)", text))
+    values = {}
+    for _ in range(4):  # definitions that use other definitions
+        for name, expr in raw.items():
+            e = re.sub(r"(0x[0-9a-fA-F]+|\d+)(ull|u)\b", r"\1", expr.strip())
+            e = re.sub(r"PF_[A-Z0-9_]+", lambda m: str(values.get(m.group(0), "?")), e)
+            if re.fullmatch(r"-?[0-9a-fx()|<+ ]+", e):
+                values[name] = eval(e)  # digits and | << + only
+    return values
+
+
+def test_python_constants_match_the_header():
+    values = header_constants()
+    assert len(values) > 60, sorted(values)
+    checked = 0
+    for name, value in values.items():
+        for attr in (name, name[3:]):
+            if hasattr(_lib, attr) and isinstance(getattr(_lib, attr), int):
+                assert getattr(_lib, attr) == value, (attr, getattr(_lib, attr), value)
+                checked += 1
+    assert checked > 30
+    assert _lib.STAGED_HEAD_ENGINE == values["PF_STAGED_HEAD_ENGINE"]
+
+
 def test_library_is_gfx950_build():
     with open(_lib.LIB_PATH, "rb") as fh:
         blob = fh.read()

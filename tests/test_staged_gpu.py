@@ -204,19 +204,30 @@ def test_staged_two_lanes_queued_vs_oracle(gpu):
         ctx.close()
 
 
-def test_staged_pipelined_load_vs_oracle(gpu):
+@pytest.mark.parametrize("head,staging,load_slice", [
+    ("kernel", 64 * 1024, 0), ("engine", 64 * 1024, 0),
+    ("kernel", 4 * MiB, 128 * 1024), ("engine", 4 * MiB, 128 * 1024)])
+def test_staged_pipelined_load_vs_oracle(gpu, head, staging, load_slice):
     """A staged save and load large enough to be pipelined (9 layers, 19,606
     chunks).  The save slices its first layer onto the copy engine and plans
-    the rest under that copy; the load copies its first layer (by the
-    zero-copy kernel when the caller waits layer by layer, else sliced onto
-    the copy engine) before the other layers are planned.  After the first layer come an empty layer, a layer copied
+    the rest under that copy; the load copies its first layer (when the
+    caller waits layer by layer: by the zero-copy kernel, or sliced onto the
+    copy engine with the context's head route set so; else sliced onto the
+    copy engine) before the other layers are planned.  With 64 KiB of
+    staging the copies go through two 32 KiB slots; with 4 MiB and 128 KiB
+    load slices, a load waited for layer by layer keeps 8 slots of 128 KiB.  After the first layer come an empty layer, a layer copied
     in place in list order, and a layer whose host region is ordinary
     (pageable) memory, copied through HIP run by run; slices start small and
     grow.  Bytes against the oracle for the save (pinned and pageable host
     regions), a load with per-layer events (in layer order), a marked load
     (every layer's mark set) and a plain one."""
-    say("[gpu] staged pipelined load, mixed later layers")
-    ctx = TransferContext(0, staging_bytes=64 * 1024)
+    say(f"[gpu] staged pipelined load, mixed later layers, first layer by {head}, "
+        f"staging {staging}, load slices {load_slice or 'default'}")
+    ctx = TransferContext(0, staging_bytes=staging)
+    ctx.set_staged_slices(0, load_slice)
+    with pytest.raises(_lib.PegaFlowError, match="unknown staged head route 2"):
+        ctx.set_staged_head(2)
+    ctx.set_staged_head(_lib.STAGED_HEAD_KERNEL if head == "kernel" else _lib.STAGED_HEAD_ENGINE)
     nb, bpb = 2048, 256
     kv = nb * bpb
     rng = np.random.Generator(np.random.PCG64(31))
@@ -283,6 +294,60 @@ def test_staged_pipelined_load_vs_oracle(gpu):
         pageable.close()
         words.close()
         ctx.close()
+
+
+def test_staged_head_route_from_setting_and_environment(gpu, monkeypatch):
+    """The first layer's route of a layer-by-layer staged load: the default
+    context copies it by the kernel, a context set to the copy engines and
+    one created under PEGAFLOW_STAGED_HEAD=engine copy it by DMA (more DMA
+    copies for the same load, the same count for both).  Every context's
+    load is checked against the oracle."""
+    say("[gpu] staged head route: default, set, environment")
+    nb, bpb = 2048, 256
+    kv = nb * bpb
+    rng = np.random.Generator(np.random.PCG64(57))
+    specs = [(rng.permutation(nb)[:1000].tolist(), rng.permutation(nb)[:1000].tolist())
+             for _ in range(9)]  # 18,000 chunks: pipelined
+    layers = [Layer(nb, bpb, 2, kv, 2 * kv, 500 + i) for i in range(9)]
+    host, ohost = _place_all(layers, [save for save, _ in specs])
+    words = PinnedBuffer(8 * len(layers))
+    ctxs = []
+    try:
+        plain = TransferContext(0, staging_bytes=4 * MiB)
+        ctxs.append(plain)
+        plain.save_layers([L.transfer(save) for L, (save, _) in zip(layers, specs)],
+                          _lib.MODE_KERNEL)
+        for L in layers:
+            L.oracle_save()
+        assert np.array_equal(host.array, ohost)
+        set_engine = TransferContext(0, staging_bytes=4 * MiB)
+        ctxs.append(set_engine)
+        set_engine.set_staged_head(_lib.STAGED_HEAD_ENGINE)
+        monkeypatch.setenv("PEGAFLOW_STAGED_HEAD", "engine")
+        from_env = TransferContext(0, staging_bytes=4 * MiB)
+        ctxs.append(from_env)
+        monkeypatch.delenv("PEGAFLOW_STAGED_HEAD")
+        dma = []
+        for k, ctx in enumerate(ctxs):
+            words.array[:] = 0
+            ctx.load_layers_marked([L.transfer(load) for L, (_, load) in zip(layers, specs)],
+                                   [(words.ptr, k + 1, True)], _lib.MODE_STAGED)
+            ctx.synchronize()
+            dma.append(ctx.last_stats()[1])
+            assert words.array.view(np.uint64).tolist() == [k + 1] * len(layers)
+            for i, (L, (_, load)) in enumerate(zip(layers, specs)):
+                if k == 0:
+                    L.oracle_load(load)
+                assert np.array_equal(L.dev.download(), L.ref), f"context {k}: layer {i}"
+        say(f"[gpu] DMA copies: default {dma[0]}, set {dma[1]}, environment {dma[2]}")
+        assert dma[0] < dma[1] == dma[2], dma
+    finally:
+        for c in ctxs:
+            c.close()
+        for L in layers:
+            L.close()
+        host.close()
+        words.close()
 
 
 def test_staged_save_overlapping_hosts_keeps_list_order(gpu):
