@@ -7,6 +7,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
+#include <thread>
 #include <vector>
 
 #include "pf_common.h"
@@ -970,6 +971,8 @@ int staged_engine(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
     x->desc_base = x->d_desc;
     return PF_OK;
   };
+  uint64_t head_bytes = 0;
+  std::chrono::steady_clock::time_point head_start;
   if (kernel_head) {
     // The first layers by the zero-copy kernel (marked, with their events),
     // the slices' descriptors after the kernel's.
@@ -977,6 +980,8 @@ int staged_engine(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
     hp.resize(head);
     for (uint32_t li = 0; li < head; ++li) std::swap(hp[li], plans[li]);
     size_t used = 0;
+    for (uint32_t li = 0; li < head; ++li) head_bytes += hp[li].chunks.size() * hp[li].chunk_bytes;
+    head_start = std::chrono::steady_clock::now();
     if (int rc = kernel_direct(x, layers, hp, false, layer_events, sig, false, 0, 0, &used))
       return rc;
     PF_HIP(hipEventRecord(x->head_done, x->stream));
@@ -1095,8 +1100,23 @@ int staged_engine(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
     index();
     if (int rc = publish()) return rc;
     tr.mark("rest", sp.n_desc);
-    // The copy engine starts once the kernel is done with the link.
-    if (kernel_head) PF_HIP(hipEventSynchronize(x->head_done));
+    // The copy engine starts once the kernel is done with the link, or once
+    // the kernel has had the time its bytes take on the link at 40 GB/s:
+    // a kernel slowed by other work holding the CUs leaves the link idle
+    // (beside a GEMM the Llama prefix's first layer took 2.2 ms by the
+    // kernel, and the engine waited throughout).  On an idle device the
+    // kernel ends first and has the link to itself.
+    if (kernel_head) {
+      const auto limit = head_start + std::chrono::microseconds(100 + head_bytes / 40000);
+      for (;;) {
+        const hipError_t q = hipEventQuery(x->head_done);
+        if (q == hipSuccess) break;
+        if (q != hipErrorNotReady) return hip_fail(q, "first-layer kernel");
+        if (std::chrono::steady_clock::now() >= limit) break;
+        std::this_thread::yield();
+      }
+      tr.mark("engine", 0);
+    }
     if (int rc = queue_free_slots()) return rc;
   }
   size_t next_layer = kernel_head ? head : 0;  // the kernel completes its own layers
@@ -1128,10 +1148,18 @@ int staged_engine(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
       if (int rc = engine_signal_wait(&x->eng_sig[s], first_layer)) return rc;
       tr.mark("c", slice_of[si]);
       if (int rc = kernel(si)) return rc;
-      if (queued < slice_steps.size()) {
-        if (int rc = kernels_done(s)) return rc;
+      // The slot is refilled once its scatter is done (waited for on the
+      // host); the layers the slice completes are marked behind the scatter
+      // on the stream first, so a mark does not wait for that host wait
+      // (beside a GEMM a scatter waits for CUs for up to a millisecond).
+      const bool refill = queued < slice_steps.size();
+      if (refill) PF_HIP(hipEventRecord(x->eng_ev[s], x->stream));
+      if (int rc = complete(static_cast<int64_t>(si))) return rc;
+      if (refill) {
+        PF_HIP(hipEventSynchronize(x->eng_ev[s]));
         if (int rc = queue_copies(slice_steps[queued++])) return rc;
       }
+      continue;
     }
     if (int rc = complete(static_cast<int64_t>(si))) return rc;
   }
@@ -1169,14 +1197,13 @@ int staged(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, bool is
   // events) copies its first layer with the zero-copy kernel, which has the
   // link at full rate from the call's start (the Llama prefix's first layer
   // in place 0.87 ms after an engine load's call, against 0.97 ms through
-  // the copy engine; beside a GEMM that holds every CU, 1.43 against 3.09
+  // the copy engine; beside a GEMM that holds every CU, 1.35 against 2.89
   // ms, the engine's layer also waiting for CUs for its scatter), and the
-  // rest staged once it is done: its 0.74 ms of shader traffic over the host
-  // link is the only part of the load that slows the device's other kernels
-  // (that GEMM 1.11x during the load, against 1.03x; the load 50.0 against
-  // 55.0 GB/s).  The context's staged_head may send the first layer through
-  // the copy engines too.  A load completed as a whole stays staged
-  // throughout.
+  // rest staged: its 0.74 ms of shader traffic over the host link is the
+  // only part of the load that slows the device's other kernels (that GEMM
+  // 1.09x during the load, against 1.06x).  The context's staged_head may
+  // send the first layer through the copy engines too.  A load completed as
+  // a whole stays staged throughout.
   const bool kernel_head = x->staged_head == PF_STAGED_HEAD_KERNEL && engines && !is_save &&
                            head > 0 && head < num_layers &&
                            (sig != nullptr || layer_events != nullptr);
