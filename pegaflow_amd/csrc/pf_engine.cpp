@@ -1125,10 +1125,10 @@ struct Instance {
     std::lock_guard<std::mutex> lk(layers_mu);
     auto it = layer_ids.find(name);
     if (it != layer_ids.end()) return it->second;
-    size_t id = layer_names.size();
+    const size_t next = layer_names.size();
     layer_names.push_back(name);
-    layer_ids[name] = id;
-    return id;
+    layer_ids[name] = next;
+    return next;
   }
   bool layer_id(const std::string& name, size_t* out) {
     std::lock_guard<std::mutex> lk(layers_mu);

@@ -349,11 +349,11 @@ int pf_load_state_attach(const char* shm_name, pf_load_state** out) {
   if (st->ext && len >= kEvOffset + kEvSize) {
     EvRecord* ev = reinterpret_cast<EvRecord*>(base + kEvOffset);
     const uint32_t count = __atomic_load_n(&ev->count, __ATOMIC_ACQUIRE);
-    const uint32_t magic = __atomic_load_n(&ev->magic, __ATOMIC_ACQUIRE);
-    if ((magic == kEvMagic || magic == kEvLocalMagic) && count > 0 && count <= kMaxEvents &&
+    const uint32_t ev_magic = __atomic_load_n(&ev->magic, __ATOMIC_ACQUIRE);
+    if ((ev_magic == kEvMagic || ev_magic == kEvLocalMagic) && count > 0 && count <= kMaxEvents &&
         len >= kEvOffset + kEvSize + count * kHandleBytes) {
       st->ev = ev;
-      st->ev_local = magic == kEvLocalMagic;
+      st->ev_local = ev_magic == kEvLocalMagic;
     }
   }
   if (st->ext && len >= kEvOffset + sizeof(WordsRecord)) {
