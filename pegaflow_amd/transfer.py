@@ -167,16 +167,37 @@ class LayerTransfer:
     registration: KVCacheRegistration
     blocks: np.ndarray  # BLOCK_DTYPE
 
+    def __getstate__(self):  # the cached C struct points into this process
+        state = dict(self.__dict__)
+        state.pop("_c", None)
+        return state
+
+
+def _layer_c(lt: LayerTransfer):
+    """The layer's pf_layer_xfer and the block array it points into, made
+    once per (registration, blocks array) pair and kept on the object: a
+    caller that passes the same layers each step (a worker's registered
+    layers) pays the marshalling once.  The array is held with the struct,
+    so the pointer stays valid; its contents may change between calls."""
+    c = lt.__dict__.get("_c")
+    if c is not None and c[0] is lt.blocks and c[1] is lt.registration:
+        return c[2], c[3]
+    b = np.ascontiguousarray(lt.blocks, dtype=BLOCK_DTYPE)
+    x = LayerXfer()
+    x.layout = lt.registration.to_c()
+    x.blocks = b.ctypes.data if len(b) else None
+    x.num_blocks = len(b)
+    lt.__dict__["_c"] = (lt.blocks, lt.registration, x, b)
+    return x, b
+
 
 def _layer_array(layers: Sequence[LayerTransfer]):
     arr = (LayerXfer * max(len(layers), 1))()
     keep = []
     for i, lt in enumerate(layers):
-        b = np.ascontiguousarray(lt.blocks, dtype=BLOCK_DTYPE)
+        x, b = _layer_c(lt)
+        arr[i] = x
         keep.append(b)
-        arr[i].layout = lt.registration.to_c()
-        arr[i].blocks = b.ctypes.data if len(b) else None
-        arr[i].num_blocks = len(b)
     return arr, keep
 
 

@@ -7,6 +7,7 @@ import os
 import re
 import struct
 
+import numpy as np
 import pytest
 from hypothesis import given, settings, strategies as st
 
@@ -489,3 +490,36 @@ def test_copy_block_gpu_to_cpu_errors_from_segment_offset():
     rc = lib.pf_copy_block_gpu_to_cpu(None, 0, ctypes.addressof(dst))
     assert rc == _lib.PF_ERR_INVALID_ARGUMENT and _last_error() == "null layout"
     assert lib.pf_layout_kind(None) == -1
+
+
+def test_layer_array_reuses_and_refreshes_the_c_structs():
+    """_layer_array makes each layer's pf_layer_xfer once per (registration,
+    blocks array) and reuses it; a new blocks array or registration rebuilds
+    it, in-place edits of the array are seen through the same pointer, and a
+    pickled layer leaves the struct behind."""
+    import pickle
+
+    from pegaflow_amd import transfer as T
+
+    reg = _reg(0x10000, 2 * 16 * 64, 16, 64, 16 * 64, 2)
+    lt = T.LayerTransfer(reg, T.block_array([1, 2, 3], [0x9000, 0x9040, 0x9080]))
+    arr, keep = T._layer_array([lt, lt])
+    first = arr[0].blocks
+    assert arr[1].blocks == first and arr[0].num_blocks == 3
+    assert arr[0].layout.num_blocks == 16 and arr[0].layout.kv_stride_bytes == 16 * 64
+    arr2, _ = T._layer_array([lt])
+    assert arr2[0].blocks == first  # reused
+    lt.blocks["block_idx"][0] = 7  # in place: the same memory
+    assert np.frombuffer((ctypes.c_int64 * 1).from_address(first), np.int64)[0] == 7
+    lt.blocks = T.block_array([4, 5], [0xA000, 0xA040])
+    arr3, keep3 = T._layer_array([lt])
+    assert arr3[0].num_blocks == 2 and arr3[0].blocks == keep3[0].ctypes.data != first
+    reg2 = _reg(0x20000, 2 * 8 * 64, 8, 64, 8 * 64, 2)
+    lt.registration = reg2
+    arr4, _ = T._layer_array([lt])
+    assert arr4[0].layout.data_ptr == 0x20000 and arr4[0].layout.num_blocks == 8
+    back = pickle.loads(pickle.dumps(lt))
+    assert "_c" not in back.__dict__
+    assert back.registration == reg2 and back.blocks.tolist() == lt.blocks.tolist()
+    arr5, keep5 = T._layer_array([back])
+    assert arr5[0].blocks == keep5[0].ctypes.data
