@@ -63,12 +63,13 @@ MODE_NAMES = {
 # Layout kinds.
 LAYOUT_SPLIT, LAYOUT_CONTIGUOUS, LAYOUT_STRIDED = 0, 1, 2
 
-# Pinned allocation flags.
 # Request methods of pf_engine_serve_request (PF_REQUEST_*).
 REQUEST_LOAD, REQUEST_SAVE, REQUEST_HEALTH = 1, 2, 3
 REQUEST_MAX_BYTES = 256 << 20
 # Chunks one pf_load_layers_noalloc call may plan (its static scratch).
 NOALLOC_MAX_CHUNKS = 65536
+
+# Pinned allocation flags.
 PINNED_DEFAULT = 0
 PINNED_COHERENT = 1
 PINNED_NONCOHERENT = 2
