@@ -462,7 +462,8 @@ def first_layer_study(reps=10):
     (pf_xfer_set_staged_head), the kernel mode, and whole loads of both
     modes.  Reports per variant the first layer's latency from the call, the
     load's rate, and the GEMM's rate during the variant's loads against its
-    rate alone; then the same loads on an idle device.  One JSON line."""
+    rate alone; then the same loads on an idle device.  Every load's bytes
+    are checked on the device.  One JSON line."""
     import multiprocessing as mp
     import threading
 
@@ -531,10 +532,15 @@ def first_layer_study(reps=10):
     c0, t0 = count.value, time.perf_counter()
     time.sleep(1.5)
     solo_rate = (count.value - c0) / (time.perf_counter() - t0)
+    # Every load is checked: the tensors are refilled first (each target
+    # block then holds its own words, not the ones the load must bring), and
+    # every block of every layer is verified after it, outside the timing.
     runs = {k: {"first": [], "load": [], "gemms": 0, "secs": 0.0} for k in variants}
+    bad = checked = 0
     for _ in range(reps):
         for name, f in variants.items():
             r = runs[name]
+            layers.refill()
             c0, t0 = count.value, time.perf_counter()
             first, load = f()
             r["secs"] += time.perf_counter() - t0
@@ -542,6 +548,8 @@ def first_layer_study(reps=10):
             if first is not None:
                 r["first"].append(first * 1e3)
             r["load"].append(load)
+            bad += wl.verify_restored(layers, ids, targets)
+            checked += 1
     stop.set()
     victim.join(60)
     if victim.exitcode != 0:
@@ -558,12 +566,16 @@ def first_layer_study(reps=10):
         beside[name] = e
     idle = {}
     for name, f in variants.items():
-        got = [f() for _ in range(5)]
+        got = []
+        for _ in range(5):
+            layers.refill()
+            got.append(f())
+            bad += wl.verify_restored(layers, ids, targets)
+            checked += 1
         e = {"load_gbps": round(P / statistics.median([g[1] for g in got]) / 1e9, 2)}
         if got[0][0] is not None:
             e["first_layer_ms"] = round(statistics.median([g[0] for g in got]) * 1e3, 3)
         idle[name] = e
-    bad = wl.verify_restored(layers, ids, targets)
     print(json.dumps({
         "metric": "first layer of a layer-by-layer restore beside a GEMM in another process",
         "transfer": "llama-3.1-8b 10k-token prefix (32 x [2,20000,16,8,128] bf16, 640 blocks), "
@@ -573,6 +585,7 @@ def first_layer_study(reps=10):
         "loads_per_variant": reps,
         "beside_gemm": beside,
         "idle": idle,
+        "loads_checked": checked,
         "bit_exact": bad == 0}), flush=True)
     for x in (x_kernel_head, x_engine_head):
         x.close()

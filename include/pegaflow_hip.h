@@ -410,10 +410,11 @@ int pf_xfer_set_staged_slices(pf_xfer* xfer, uint64_t save_bytes, uint64_t load_
  * rest.  The kernel lands the first layer earliest; the copy engine keeps
  * the whole load off the CUs.  Measured on the Llama-3.1-8B prefix beside a
  * bf16 8192^3 GEMM run back to back by another process (bench.py
- * --first-layer-study): the kernel head lands the first layer 1.35 ms after
- * the call, the load runs at 54.1 GB/s and the GEMM 1.09x slower; the
- * copy-engine head 2.89 ms (its scatter waits for CUs), 53.5 GB/s and 1.06x.
- * On an idle device: 0.99 and 1.00 ms, 55.8 and 55.9 GB/s.  The environment
+ * --first-layer-study, two runs): the kernel head lands the first layer
+ * 1.35-1.55 ms after the call, the load runs at 52.9-54.1 GB/s and the GEMM
+ * 1.06-1.09x slower; the copy-engine head 2.35-2.89 ms (its scatter waits
+ * for CUs), 53.2-53.5 GB/s and 1.05-1.06x.  On an idle device both land it
+ * in 0.91-1.00 ms and load at 55.7-56.0 GB/s.  The environment
  * variable PEGAFLOW_STAGED_HEAD=engine makes the copy engines the default of
  * contexts created afterwards, the engine's included.  Other routes:
  * PF_ERR_INVALID_ARGUMENT.  No counterpart in the reference (its loads are

@@ -1197,11 +1197,11 @@ int staged(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, bool is
   // events) copies its first layer with the zero-copy kernel, which has the
   // link at full rate from the call's start (the Llama prefix's first layer
   // in place 0.87 ms after an engine load's call, against 0.97 ms through
-  // the copy engine; beside a GEMM that holds every CU, 1.35 against 2.89
-  // ms, the engine's layer also waiting for CUs for its scatter), and the
-  // rest staged: its 0.74 ms of shader traffic over the host link is the
-  // only part of the load that slows the device's other kernels (that GEMM
-  // 1.09x during the load, against 1.06x).  The context's staged_head may
+  // the copy engine; beside a GEMM that holds every CU, 1.35-1.55 against
+  // 2.35-2.89 ms, the engine's layer also waiting for CUs for its scatter),
+  // and the rest staged: its 0.74 ms of shader traffic over the host link is
+  // the only part of the load that slows the device's other kernels (that
+  // GEMM 1.06-1.09x during the load, against 1.05-1.06x).  The context's staged_head may
   // send the first layer through the copy engines too.  A load completed as
   // a whole stays staged throughout.
   const bool kernel_head = x->staged_head == PF_STAGED_HEAD_KERNEL && engines && !is_save &&
