@@ -173,6 +173,37 @@ def test_engine_indexes_and_prefetches_fixture_files(golden_root, g):
     e.close()
 
 
+def test_prefetch_of_page_sized_slots(tmp_path):
+    """Blocks whose slot halves are 4 KiB (as a bf16 head of 16 tokens x 128
+    dims is), packed by the oracle: five adjacent blocks are one read run
+    into five pool allocations, and every slot holds the file's bytes."""
+    rng = np.random.default_rng(7)
+    seg, n_blocks, n_slots = 4096, 5, 2
+    blocks = [[(rng.bytes(seg), rng.bytes(seg)) for _ in range(n_slots)]
+              for _ in range(n_blocks)]
+    data, offs = oracle.pack_blocks(blocks)
+    assert all(o % 4096 == 0 for o in offs)
+    uuid = "00000000-0000-4000-8000-000000000003"
+    metas = [json.dumps({"file": uuid + ".bin", "offset": o,
+                         "slots": [{"is_split": True, "size": 2 * seg}] * n_slots,
+                         "total_slots": n_slots}, separators=(",", ":")) for o in offs]
+    hs = [h(i, b"aligned") for i in range(n_blocks)]
+    root = str(tmp_path / "pega")
+    write_packed(root, "llama", "llama", uuid, data, metas, hs)
+    e = engine_on(root)
+    reg(e, "vllm", "llama", 2, 1, nb=8, bpb=seg)
+    q = e.count_prefix_hit_blocks_with_prefetch("vllm", hs)
+    assert q["prefetch_state"] == "loading"
+    e.wait_prefetch()
+    assert e.count_prefix_hit_blocks("vllm", hs) == n_blocks
+    for b in range(n_blocks):
+        for slot in range(n_slots):
+            assert e.read_block_slot("llama", hs[b], slot) == blocks[b][slot]
+    s = e.disk_stats()
+    assert (s["prefetched_blocks"], s["read_bytes"], s["failures"]) == (n_blocks, len(data), 0)
+    e.close()
+
+
 def test_query_states_follow_the_reference(golden_root):
     root, hs = golden_root
     e = engine_on(root)
