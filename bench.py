@@ -104,6 +104,9 @@ def parse():
     ap.add_argument("--first-layer-study", action="store_true",
                     help="only run the first-layer study: layer-by-layer restores beside a "
                          "GEMM in another process (one JSON line)")
+    ap.add_argument("--cu-masks", default="",
+                    help="with --first-layer-study: also run the staged variants on contexts "
+                         "masked to these compute units per XCD, e.g. '1,2,4'")
     ap.add_argument("--study-engines", default="",
                     help="with --interference-study: staged phases only, once per copy-engine "
                          "pair, e.g. '0x2:0x1,0x8:0x4' (device-to-host mask:host-to-device mask)")
@@ -452,7 +455,7 @@ def _first_layer_victim(go, stop, ready, count):
             count.value += 2
 
 
-def first_layer_study(reps=10):
+def first_layer_study(reps=10, cu_masks=()):
     """Layer-by-layer restores of the Llama prefix beside bf16 8192^3 GEMMs
     that another process runs back to back.  Each restore marks its layers
     in pinned host memory; this process polls layer 0's mark while another
@@ -460,17 +463,19 @@ def first_layer_study(reps=10):
     Variants, interleaved, `reps` loads each: the staged mode with its first
     layer by the zero-copy kernel (the default) or by the copy engines
     (pf_xfer_set_staged_head), the kernel mode, and whole loads of both
-    modes.  Reports per variant the first layer's latency from the call, the
-    load's rate, and the GEMM's rate during the variant's loads against its
-    rate alone; then the same loads on an idle device.  Every load's bytes
-    are checked on the device.  One JSON line."""
+    modes; with `cu_masks`, the three staged variants again on contexts
+    whose kernels run on k compute units of each XCD, for each k.  Reports
+    per variant the first layer's latency from the call, the load's rate,
+    and the GEMM's rate during the variant's loads against its rate alone;
+    then the same loads on an idle device.  Every load's bytes are checked
+    on the device.  One JSON line."""
     import multiprocessing as mp
     import threading
 
     from pegaflow_amd import _lib, runtime
     from pegaflow_amd import workload as wl
     from pegaflow_amd.runtime import PinnedBuffer
-    from pegaflow_amd.transfer import TransferContext
+    from pegaflow_amd.transfer import TransferContext, cu_mask_per_xcd
 
     ctx = mp.get_context("spawn")
     go, stop, ready = ctx.Event(), ctx.Event(), ctx.Event()
@@ -524,6 +529,21 @@ def first_layer_study(reps=10):
         "staged_whole_load": lambda: whole(x_kernel_head, _lib.MODE_STAGED),
         "kernel_whole_load": lambda: whole(x_kernel_head, _lib.MODE_KERNEL),
     }
+    masked = []
+    for k in cu_masks:
+        xk = TransferContext(0, staging_bytes=512 << 20)
+        xk.set_cu_mask(cu_mask_per_xcd(k))
+        xe = TransferContext(0, staging_bytes=512 << 20)
+        xe.set_cu_mask(cu_mask_per_xcd(k))
+        xe.set_staged_head(_lib.STAGED_HEAD_ENGINE)
+        masked += [xk, xe]
+        variants.update({
+            f"staged_first_layer_by_kernel_{k}_cus_per_xcd":
+                lambda xk=xk: marked(xk, _lib.MODE_STAGED),
+            f"staged_first_layer_by_copy_engine_{k}_cus_per_xcd":
+                lambda xe=xe: marked(xe, _lib.MODE_STAGED),
+            f"staged_whole_load_{k}_cus_per_xcd": lambda xk=xk: whole(xk, _lib.MODE_STAGED),
+        })
     for f in variants.values():
         f()
     ready.wait()
@@ -583,11 +603,12 @@ def first_layer_study(reps=10):
         "gemm": "bf16 8192^3 torch.mm back to back, two per synchronization",
         "gemm_alone_ms": round(1e3 / solo_rate, 3),
         "loads_per_variant": reps,
+        "cu_masks_per_xcd": list(cu_masks),
         "beside_gemm": beside,
         "idle": idle,
         "loads_checked": checked,
         "bit_exact": bad == 0}), flush=True)
-    for x in (x_kernel_head, x_engine_head):
+    for x in [x_kernel_head, x_engine_head] + masked:
         x.close()
     words.close()
     pool.close()
@@ -1928,7 +1949,7 @@ def main():
         interference_study(args.study_engines, args.study_victims)
         return
     if args.first_layer_study:
-        first_layer_study()
+        first_layer_study(cu_masks=[int(k) for k in args.cu_masks.split(",") if k])
         return
     if args.leg:
         run_leg(args)

@@ -422,6 +422,22 @@ int pf_xfer_set_staged_slices(pf_xfer* xfer, uint64_t save_bytes, uint64_t load_
 #define PF_STAGED_HEAD_KERNEL 0u
 #define PF_STAGED_HEAD_ENGINE 1u
 int pf_xfer_set_staged_head(pf_xfer* xfer, uint32_t route);
+/* Compute units the context's kernels run on.  Bit b of `mask` (word b/32,
+ * bit b%32) enables the device's CU b; the runtime deals the bits to the
+ * XCDs round-robin, so bit b is on XCD b mod (number of XCDs) — on MI355X
+ * bits 0-7 are one CU on each of the 8 XCDs, the next 8 a second CU of
+ * each.  `words` = 0 restores unmasked streams.  A mask that leaves an XCD
+ * without a CU is refused (PF_ERR_INVALID_ARGUMENT): every launch is split
+ * across the XCDs, and that XCD's share would never run.  The call waits for
+ * the context's work, then replaces its two streams: a stream handle taken
+ * from pf_xfer_stream before the call is no longer valid after it.  Masked
+ * streams are ordered with the null stream.  PEGAFLOW_CUS_PER_XCD=<k> masks
+ * every context created afterwards (the engine's included) to k CUs per
+ * XCD.  No counterpart in the reference (its copies run on DMA engines). */
+int pf_xfer_set_cu_mask(pf_xfer* xfer, const uint32_t* mask, uint32_t words);
+/* Fills `mask` (`words` words) with k CUs on each XCD of `device`: bits 0
+ * to k*(number of XCDs)-1. */
+int pf_cu_mask_per_xcd(int device, uint32_t cus_per_xcd, uint32_t* mask, uint32_t words);
 /* Number of gather/scatter kernel launches and DMA copies issued by the last
  * save/load call on this context. */
 int pf_xfer_last_stats(pf_xfer* xfer, uint64_t* kernel_launches,

@@ -277,6 +277,8 @@ SIGNATURES = {
                                   ctypes.POINTER(i32)]),
     "pf_xfer_set_route_grid": (i32, [vp, u32, u32]),
     "pf_xfer_set_staged_head": (i32, [vp, u32]),
+    "pf_xfer_set_cu_mask": (i32, [vp, ctypes.POINTER(ctypes.c_uint32), u32]),
+    "pf_cu_mask_per_xcd": (i32, [i32, u32, ctypes.POINTER(ctypes.c_uint32), u32]),
     "pf_xfer_set_timing": (i32, [vp, i32]),
     "pf_xfer_last_kernel_ms": (i32, [vp, ctypes.POINTER(ctypes.c_float), pu64]),
     "pf_save_layers": (i32, [vp, ctypes.POINTER(LayerXfer), u32, u32]),

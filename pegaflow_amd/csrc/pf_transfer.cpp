@@ -1977,6 +1977,60 @@ int pf_load_layers_noalloc(pf_stream stream, const pf_layer_xfer* layers, uint32
   return rc;
 }
 
+namespace {
+
+// Bit b of a stream's CU mask enables compute unit b of the device in the
+// runtime's numbering, which deals the bits to the XCDs round-robin: bit b
+// is on XCD b mod n_xcd (measured on MI355X by recording each workgroup's
+// XCC_ID and HW_ID: bits 0-7 are one CU on each of the 8 XCDs, the next 8 a
+// second CU of each, in its next shader engine).  Every launch is split
+// across all XCDs, so a mask that leaves an XCD without a CU would leave
+// that XCD's share of every launch waiting forever: refused.
+int check_cu_mask(int device, const uint32_t* mask, uint32_t words) {
+  int cus = 0, xcds = 0;
+  PF_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
+  PF_HIP(hipDeviceGetAttribute(&xcds, hipDeviceAttributeNumberOfXccs, device));
+  if (xcds <= 0) xcds = 1;
+  std::vector<int> per_xcd(static_cast<size_t>(xcds), 0);
+  for (uint32_t b = 0; b < words * 32u && b < static_cast<uint32_t>(cus); ++b)
+    if (mask[b / 32] >> (b % 32) & 1u) ++per_xcd[b % static_cast<uint32_t>(xcds)];
+  for (int i = 0; i < xcds; ++i)
+    if (per_xcd[static_cast<size_t>(i)] == 0)
+      return fail(PF_ERR_INVALID_ARGUMENT,
+                  strf("CU mask leaves XCD %d without a compute unit (bit b of the mask is "
+                       "on XCD b mod %d, bits below %d count)",
+                       i, xcds, cus));
+  return PF_OK;
+}
+
+// (Re)creates the context's two streams: plain non-blocking ones, or
+// CU-masked ones (HIP creates those as blocking streams: they also order
+// with the null stream).
+int create_lane_streams(pf_xfer* x, const uint32_t* mask, uint32_t words) {
+  if (words) {  // bits past the device's CUs are dropped
+    int cus = 0;
+    PF_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, x->device));
+    words = std::min(words, static_cast<uint32_t>(cus + 31) / 32u);
+  }
+  hipStream_t s[2] = {nullptr, nullptr};
+  hipError_t e = hipSuccess;
+  for (int i = 0; i < 2 && e == hipSuccess; ++i)
+    e = words ? hipExtStreamCreateWithCUMask(&s[i], words, mask)
+              : hipStreamCreateWithFlags(&s[i], hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    for (hipStream_t t : s)
+      if (t) (void)hipStreamDestroy(t);
+    return hip_fail(e, words ? "hipExtStreamCreateWithCUMask" : "hipStreamCreateWithFlags");
+  }
+  if (x->stream) (void)hipStreamDestroy(x->stream);
+  if (x->dma) (void)hipStreamDestroy(x->dma);
+  x->stream = s[0];
+  x->dma = s[1];
+  return PF_OK;
+}
+
+}  // namespace
+
 // ---------------------------------------------------------------------------
 // Transfer contexts.
 // ---------------------------------------------------------------------------
@@ -1994,9 +2048,18 @@ int pf_xfer_create(int device, uint64_t staging_bytes, pf_xfer** out) {
     pf_xfer_destroy(x);
     return rc;
   };
-  hipError_t e = hipStreamCreateWithFlags(&x->stream, hipStreamNonBlocking);
-  if (e == hipSuccess) e = hipStreamCreateWithFlags(&x->dma, hipStreamNonBlocking);
-  if (e == hipSuccess) e = hipEventCreateWithFlags(&x->desc_uploaded, hipEventDisableTiming);
+  // PEGAFLOW_CUS_PER_XCD=<k>: new contexts (the engine's included) run
+  // their kernels on k compute units of each XCD (pf_cu_mask_per_xcd).
+  if (const char* k = std::getenv("PEGAFLOW_CUS_PER_XCD")) {
+    uint32_t mask[64];
+    const unsigned long cus = std::strtoul(k, nullptr, 10);
+    int rc = pf_cu_mask_per_xcd(device, static_cast<uint32_t>(cus), mask, 64);
+    if (rc == PF_OK) rc = create_lane_streams(x, mask, 64);
+    if (rc != PF_OK) return cleanup(rc);
+  } else if (int rc = create_lane_streams(x, nullptr, 0)) {
+    return cleanup(rc);
+  }
+  hipError_t e = hipEventCreateWithFlags(&x->desc_uploaded, hipEventDisableTiming);
   if (e == hipSuccess) e = hipEventCreateWithFlags(&x->parts_ready, hipEventDisableTiming);
   if (e == hipSuccess)
     e = hipHostMalloc(reinterpret_cast<void**>(&x->h_small), kHostDescMax * sizeof(ChunkDesc),
@@ -2165,6 +2228,40 @@ int pf_xfer_set_staged_head(pf_xfer* x, uint32_t route) {
   std::lock_guard<std::mutex> lk(x->mu);
   x->staged_head = route;
   return PF_OK;
+}
+
+int pf_cu_mask_per_xcd(int device, uint32_t cus_per_xcd, uint32_t* mask, uint32_t words) {
+  if (!mask || words == 0) return fail(PF_ERR_INVALID_ARGUMENT, "null or empty mask");
+  int cus = 0, xcds = 0;
+  PF_HIP(hipSetDevice(device));
+  PF_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
+  PF_HIP(hipDeviceGetAttribute(&xcds, hipDeviceAttributeNumberOfXccs, device));
+  if (xcds <= 0) xcds = 1;
+  const uint64_t bits = uint64_t(cus_per_xcd) * uint64_t(xcds);
+  if (cus_per_xcd == 0 || bits > static_cast<uint64_t>(cus))
+    return fail(PF_ERR_INVALID_ARGUMENT,
+                strf("%u CUs per XCD: the device has %d CUs on %d XCDs", cus_per_xcd, cus, xcds));
+  if (bits > uint64_t(words) * 32u)
+    return fail(PF_ERR_INVALID_ARGUMENT, strf("a mask of %u words holds fewer than %llu bits",
+                                              words, static_cast<unsigned long long>(bits)));
+  for (uint32_t w = 0; w < words; ++w) mask[w] = 0;
+  for (uint64_t b = 0; b < bits; ++b) mask[b / 32] |= 1u << (b % 32);
+  return PF_OK;
+}
+
+int pf_xfer_set_cu_mask(pf_xfer* x, const uint32_t* mask, uint32_t words) {
+  if (!x) return fail(PF_ERR_INVALID_ARGUMENT, "null transfer context");
+  if (words && !mask) return fail(PF_ERR_INVALID_ARGUMENT, "null mask");
+  if (words > 64) return fail(PF_ERR_INVALID_ARGUMENT, "a CU mask has at most 64 words");
+  std::lock_guard<std::mutex> lk(x->mu);
+  PF_HIP(hipSetDevice(x->device));
+  if (words)
+    if (int rc = check_cu_mask(x->device, mask, words)) return rc;
+  // Everything issued on the old streams ends first.
+  PF_HIP(hipStreamSynchronize(x->dma));
+  PF_HIP(hipStreamSynchronize(x->stream));
+  if (int rc = engine_drain(x)) return rc;
+  return create_lane_streams(x, mask, words);
 }
 
 int pf_xfer_set_timing(pf_xfer* x, int enable) {

@@ -211,6 +211,14 @@ def load_layers_noalloc(layers: Sequence[LayerTransfer], stream: Stream | None =
     del keep
 
 
+def cu_mask_per_xcd(cus_per_xcd: int, device: int = 0, words: int = 8):
+    """A CU mask with `cus_per_xcd` compute units on each XCD of `device`
+    (pf_cu_mask_per_xcd), as a list of 32-bit words."""
+    arr = (ctypes.c_uint32 * words)()
+    check(lib().pf_cu_mask_per_xcd(device, cus_per_xcd, arr, words), "pf_cu_mask_per_xcd")
+    return list(arr)
+
+
 class TransferContext:
     """A pf_xfer: per-worker streams, descriptor buffers and staging slots."""
 
@@ -275,6 +283,16 @@ class TransferContext:
         _lib.STAGED_HEAD_KERNEL (zero-copy kernel, the default) or
         _lib.STAGED_HEAD_ENGINE (copy engines; pf_xfer_set_staged_head)."""
         check(lib().pf_xfer_set_staged_head(self.handle, route), "pf_xfer_set_staged_head")
+
+    def set_cu_mask(self, mask=None) -> None:
+        """Compute units this context's kernels run on (pf_xfer_set_cu_mask):
+        a sequence of 32-bit words, bit b enabling CU b (on XCD b mod the
+        XCD count), or None for unmasked streams.  Waits for the context's
+        work and replaces its streams, `self.stream` included."""
+        words = list(mask or [])
+        arr = (ctypes.c_uint32 * max(1, len(words)))(*words)
+        check(lib().pf_xfer_set_cu_mask(self.handle, arr, len(words)), "pf_xfer_set_cu_mask")
+        self.stream = Stream(lib().pf_xfer_stream(self.handle), owned=False)
 
     def set_max_grid(self, max_workgroups: int) -> None:
         check(lib().pf_xfer_set_max_grid(self.handle, max_workgroups), "pf_xfer_set_max_grid")

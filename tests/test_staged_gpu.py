@@ -493,3 +493,109 @@ def test_set_copy_engines(gpu):
     finally:
         set_copy_engines(0, d2h, h2d)
     assert copy_engines(0) == (d2h, h2d)
+
+
+@pytest.mark.parametrize("per_xcd", [1, 4])
+def test_cu_masked_context_vs_oracle(gpu, per_xcd):
+    """A context whose streams run on `per_xcd` compute units of each XCD:
+    kernel and staged saves, and loads with per-layer events and with marks,
+    of the mixed layers and of four [2, 512, 16, 8, 128] layers with 200
+    random blocks each, equal the oracle byte for byte.  Unmasking the
+    context afterwards keeps it working."""
+    from pegaflow_amd.transfer import cu_mask_per_xcd
+
+    say(f"[gpu] CU-masked context, {per_xcd} CUs per XCD")
+    mask = cu_mask_per_xcd(per_xcd)
+    assert sum(bin(w).count("1") for w in mask) == 8 * per_xcd
+    ctx = TransferContext(0, staging_bytes=4 * MiB)
+    ctx.set_cu_mask(mask)
+    mixed, mixed_save, mixed_load = _mixed_layers(110)
+    nb, bpb = 512, 32768
+    rng = np.random.Generator(np.random.PCG64(per_xcd))
+    big = [Layer(nb, bpb, 2, nb * bpb, 2 * nb * bpb, 120 + i) for i in range(4)]
+    layers = mixed + big
+    save_ids = mixed_save + [rng.choice(nb, 200, replace=False).tolist() for _ in big]
+    load_ids = mixed_load + [rng.choice(nb, 200, replace=False).tolist() for _ in big]
+    host, ohost = _place_all(layers, save_ids)
+    words = PinnedBuffer(8 * len(layers))
+    try:
+        for rnd, mode in enumerate((_lib.MODE_KERNEL, _lib.MODE_STAGED)):
+            if rnd == 1 and per_xcd == 4:
+                ctx.set_cu_mask(None)  # the staged round on unmasked streams
+            host.array[:] = 0
+            ctx.save_layers([L.transfer(ids) for L, ids in zip(layers, save_ids)], mode)
+            ctx.synchronize()
+            for L in layers:
+                L.oracle_save()
+            assert np.array_equal(host.array, ohost), f"mode {mode}: host regions differ"
+            evs = [Event() for _ in layers]
+            ctx.load_layers([L.transfer(ids) for L, ids in zip(layers, load_ids)], mode,
+                            layer_events=evs)
+            ctx.synchronize()
+            for i, (L, ids) in enumerate(zip(layers, load_ids)):
+                L.oracle_load(ids)
+                assert np.array_equal(L.dev.download(), L.ref), f"mode {mode}: layer {i} differs"
+            words.array[:] = 0
+            ctx.load_layers_marked([L.transfer(ids) for L, ids in zip(layers, load_ids)],
+                                   [(words.ptr, 5 + rnd, True)], mode)
+            ctx.synchronize()
+            assert words.array.view(np.uint64).tolist() == [5 + rnd] * len(layers)
+            for L in layers:
+                assert np.array_equal(L.dev.download(), L.ref)
+    finally:
+        for L in layers:
+            L.close()
+        host.close()
+        words.close()
+        ctx.close()
+
+
+def test_cu_mask_refusals(gpu, monkeypatch):
+    """Masks that would leave an XCD without a compute unit are refused
+    before any stream is replaced (the context keeps working); so are 0 CUs
+    per XCD and more than the device has.  PEGAFLOW_CUS_PER_XCD masks new
+    contexts, and a bad value fails their creation."""
+    from pegaflow_amd.transfer import cu_mask_per_xcd
+
+    say("[gpu] CU mask refusals")
+    ctx = TransferContext(0, staging_bytes=MiB)
+    try:
+        with pytest.raises(_lib.PegaFlowError, match="leaves XCD 1 without a compute unit"):
+            ctx.set_cu_mask([1, 0, 0, 0, 0, 0, 0, 0])
+        with pytest.raises(_lib.PegaFlowError, match="leaves XCD 0 without a compute unit"):
+            ctx.set_cu_mask([0xFEFEFEFE] * 8)
+        with pytest.raises(_lib.PegaFlowError, match="CUs per XCD"):
+            cu_mask_per_xcd(0)
+        with pytest.raises(_lib.PegaFlowError, match="CUs per XCD"):
+            cu_mask_per_xcd(10_000)
+        with pytest.raises(_lib.PegaFlowError, match="fewer than"):
+            cu_mask_per_xcd(8, words=1)
+        layers, save_ids, load_ids = _mixed_layers(130)
+        host, ohost = _place_all(layers, save_ids)
+        try:
+            ctx.save_layers([L.transfer(ids) for L, ids in zip(layers, save_ids)],
+                            _lib.MODE_KERNEL)
+            ctx.synchronize()
+            for L in layers:
+                L.oracle_save()
+            assert np.array_equal(host.array, ohost)
+            monkeypatch.setenv("PEGAFLOW_CUS_PER_XCD", "2")
+            masked = TransferContext(0, staging_bytes=MiB)
+            try:
+                masked.load_layers([L.transfer(ids) for L, ids in zip(layers, load_ids)],
+                                   _lib.MODE_STAGED)
+                masked.synchronize()
+                for L, ids in zip(layers, load_ids):
+                    L.oracle_load(ids)
+                    assert np.array_equal(L.dev.download(), L.ref)
+            finally:
+                masked.close()
+            monkeypatch.setenv("PEGAFLOW_CUS_PER_XCD", "0")
+            with pytest.raises(_lib.PegaFlowError, match="CUs per XCD"):
+                TransferContext(0, staging_bytes=MiB)
+        finally:
+            for L in layers:
+                L.close()
+            host.close()
+    finally:
+        ctx.close()
