@@ -461,8 +461,8 @@ def first_layer_study(reps=10, cu_masks=()):
     in pinned host memory; this process polls layer 0's mark while another
     thread issues the load (a staged load returns once its copies are done).
     Variants, interleaved, `reps` loads each: the staged mode with its first
-    layer by the zero-copy kernel (the default) or by the copy engines
-    (pf_xfer_set_staged_head), the kernel mode, and whole loads of both
+    layer by the zero-copy kernel or by the copy engines (the default;
+    pf_xfer_set_staged_head), the kernel mode, and whole loads of both
     modes; with `cu_masks`, the three staged variants again on contexts
     whose kernels run on k compute units of each XCD, for each k.  Reports
     per variant the first layer's latency from the call, the load's rate,
@@ -489,6 +489,7 @@ def first_layer_study(reps=10, cu_masks=()):
     P = wl.payload_bytes(layers.regs, 640)
     pool = PinnedBuffer(P)
     x_kernel_head = TransferContext(0, staging_bytes=512 << 20)
+    x_kernel_head.set_staged_head(_lib.STAGED_HEAD_KERNEL)
     x_engine_head = TransferContext(0, staging_bytes=512 << 20)
     x_engine_head.set_staged_head(_lib.STAGED_HEAD_ENGINE)
     saved = wl.save_plan(layers.regs, ids, pool.ptr)
@@ -533,6 +534,7 @@ def first_layer_study(reps=10, cu_masks=()):
     for k in cu_masks:
         xk = TransferContext(0, staging_bytes=512 << 20)
         xk.set_cu_mask(cu_mask_per_xcd(k))
+        xk.set_staged_head(_lib.STAGED_HEAD_KERNEL)
         xe = TransferContext(0, staging_bytes=512 << 20)
         xe.set_cu_mask(cu_mask_per_xcd(k))
         xe.set_staged_head(_lib.STAGED_HEAD_ENGINE)

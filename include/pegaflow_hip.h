@@ -405,20 +405,22 @@ int pf_set_copy_engines(int device, uint32_t d2h_engines, uint32_t h2d_engines);
 #define PF_STAGED_LOAD_SLICE_DEFAULT (256ull << 20)
 int pf_xfer_set_staged_slices(pf_xfer* xfer, uint64_t save_bytes, uint64_t load_bytes);
 /* How a staged load whose caller waits layer by layer (marks or per-layer
- * events) copies its first layer: PF_STAGED_HEAD_KERNEL (the default) by the
- * zero-copy kernel, PF_STAGED_HEAD_ENGINE through the copy engines as the
- * rest.  The kernel lands the first layer earliest; the copy engine keeps
- * the whole load off the CUs.  Measured on the Llama-3.1-8B prefix beside a
- * bf16 8192^3 GEMM run back to back by another process (bench.py
- * --first-layer-study, two runs): the kernel head lands the first layer
- * 1.35-1.55 ms after the call, the load runs at 52.9-54.1 GB/s and the GEMM
- * 1.06-1.09x slower; the copy-engine head 2.35-2.89 ms (its scatter waits
- * for CUs), 53.2-53.5 GB/s and 1.05-1.06x.  On an idle device both land it
- * in 0.91-1.00 ms and load at 55.7-56.0 GB/s.  The environment
- * variable PEGAFLOW_STAGED_HEAD=engine makes the copy engines the default of
- * contexts created afterwards, the engine's included.  Other routes:
- * PF_ERR_INVALID_ARGUMENT.  No counterpart in the reference (its loads are
- * one cuMemcpyHtoDAsync per run). */
+ * events) copies its first layer: PF_STAGED_HEAD_ENGINE (the default)
+ * through the copy engines as one copy, then one scatter kernel that marks
+ * the layer itself; PF_STAGED_HEAD_KERNEL by the zero-copy kernel.  Beside a
+ * GEMM whose workgroups fill every CU, each kernel of the load waits for one
+ * of the GEMM's kernels to end, so either route lands the layer after one
+ * such wait.  Measured on the Llama-3.1-8B prefix beside a bf16 8192^3 GEMM
+ * run back to back by another process (bench.py --first-layer-study, two
+ * runs): the copy-engine route lands the first layer 1.58-1.66 ms after the
+ * call, the load runs at 52.8-53.8 GB/s and the GEMM 1.04x slower; the
+ * kernel route 1.57-1.62 ms, 52.9-53.5 GB/s and 1.05x (its 0.74 ms of shader
+ * traffic over the host link also slows every other kernel's memory
+ * traffic).  On an idle device both land it in 0.93-0.96 ms.  The
+ * environment variable PEGAFLOW_STAGED_HEAD=kernel (or =engine) sets the
+ * route of contexts created afterwards, the engine's included.  Other
+ * routes: PF_ERR_INVALID_ARGUMENT.  No counterpart in the reference (its
+ * loads are one cuMemcpyHtoDAsync per run). */
 #define PF_STAGED_HEAD_KERNEL 0u
 #define PF_STAGED_HEAD_ENGINE 1u
 int pf_xfer_set_staged_head(pf_xfer* xfer, uint32_t route);

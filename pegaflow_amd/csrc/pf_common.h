@@ -87,6 +87,12 @@ hipError_t launch_copy_chunks_queue(const ChunkDesc* d_descs, uint32_t n_chunks,
                                     uint64_t chunk_bytes, uint32_t threads, uint32_t unroll,
                                     uint32_t grid, const LayerMarks* marks,
                                     uint32_t* queue, uint32_t* n_tiles, hipStream_t stream);
+// A marked copy between device buffers with a fixed workgroup -> tile map
+// (16-byte aligned chunks): each finished layer of `marks` is marked.
+hipError_t launch_copy_chunks_marked(const ChunkDesc* d_descs, uint32_t n_chunks,
+                                     uint64_t chunk_bytes, uint32_t threads, uint32_t unroll,
+                                     uint32_t grid, const LayerMarks& marks,
+                                     hipStream_t stream);
 hipError_t launch_mark_layers(const LayerList& list, const SignalTargets& t,
                               hipStream_t stream);
 hipError_t launch_wait_word(uint64_t word, uint64_t value, uint64_t max_ticks,

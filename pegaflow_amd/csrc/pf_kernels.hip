@@ -128,6 +128,85 @@ __device__ __forceinline__ void tile_done(const LayerMarks& m, uint32_t c,
   }
 }
 
+// The group (launch layer) of chunk c: chunk_start[g] <= c < chunk_start[g+1].
+__device__ __forceinline__ uint32_t group_of(const LayerMarks& m, uint32_t c) {
+  uint32_t lo = 0, hi = m.n;
+  while (hi - lo > 1) {
+    const uint32_t mid = (lo + hi) >> 1;
+    if (m.chunk_start[mid] <= c) lo = mid;
+    else hi = mid;
+  }
+  return lo;
+}
+
+// tile_done for k tiles of group g at once.
+__device__ __forceinline__ void tiles_done(const LayerMarks& m, uint32_t g, uint32_t k,
+                                           uint32_t tiles_per_chunk) {
+  const uint32_t layer = m.layer[g];
+  const uint32_t tiles = (m.chunk_start[g + 1] - m.chunk_start[g]) * tiles_per_chunk;
+  uint32_t* cnt = m.counters + layer;
+  const uint32_t prev = __hip_atomic_fetch_add(cnt, k, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+  if (prev + k == tiles) {
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    write_marks(m.targets, layer);
+  }
+}
+
+// A marked copy between device buffers (the staged load's scatter of a
+// slice whose layers it reports itself): a fixed map like
+// copy_chunks_v16_kernel, with the marking protocol above.  Workgroup w
+// copies tiles w, w + grid, ..., which run through the launch's layers in
+// order, and adds the tiles it finished of a layer to that layer's counter
+// once, when it moves on to the next layer or ends, not once per tile: one
+// counter takes one add at a time, and per-tile adds (2,560 for a 40 MiB
+// layer, in a queued launch) held such a copy at a fraction of HBM rate.
+// The flush condition depends only on the tile index, so it is uniform
+// across the workgroup and its barrier is reached by every lane.
+template <int UNROLL, bool NTL>
+__global__ void __launch_bounds__(1024)
+copy_chunks_marked_kernel(const ChunkDesc* __restrict__ descs, uint32_t tiles_per_chunk,
+                          uint32_t n_tiles, uint32_t chunk16, LayerMarks marks) {
+  const uint32_t stride = blockDim.x;
+  const uint32_t tile_elems = stride * UNROLL;
+  uint32_t group = 0, done = 0;
+  for (uint32_t t = blockIdx.x; t < n_tiles; t += gridDim.x) {
+    const uint32_t c = t / tiles_per_chunk;
+    const uint32_t g = group_of(marks, c);
+    if (done > 0 && g != group) {
+      __builtin_amdgcn_s_waitcnt(0);  // every store of this wave acknowledged
+      __syncthreads();
+      if (threadIdx.x == 0) tiles_done(marks, group, done, tiles_per_chunk);
+      done = 0;
+    }
+    group = g;
+    const uint32_t tile = t - c * tiles_per_chunk;
+    const ChunkDesc d = descs[c];
+    const g_u32x4* __restrict__ src = reinterpret_cast<const g_u32x4*>(d.src);
+    g_u32x4* __restrict__ dst = reinterpret_cast<g_u32x4*>(d.dst);
+    const uint32_t tile_base = tile * tile_elems;
+    const uint32_t base = tile_base + threadIdx.x;
+    u32x4 v[UNROLL];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const uint32_t e = base + u * stride;
+      if (e < chunk16) v[u] = load16<NTL>(src + e);
+    }
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const uint32_t e = base + u * stride;
+      if (e < chunk16) store16_coherent(dst + e, v[u]);
+    }
+    ++done;
+  }
+  if (done > 0) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) tiles_done(marks, group, done, tiles_per_chunk);
+  }
+}
+
 template <int UNROLL, bool NTL, bool NTS>
 __global__ void __launch_bounds__(1024)
 copy_chunks_v16_kernel(const ChunkDesc* __restrict__ descs,
@@ -441,6 +520,43 @@ hipError_t launch_copy_chunks_queue(const ChunkDesc* d_descs, uint32_t n_chunks,
     default: return hipErrorInvalidValue;
   }
   *n_tiles = ntiles;
+  return hipGetLastError();
+}
+
+template <int UNROLL>
+static void launch_marked(dim3 g, dim3 b, hipStream_t stream, bool ntl, const ChunkDesc* d,
+                          uint32_t tpc, uint32_t ntiles, uint32_t c16, const LayerMarks& m) {
+  if (ntl)
+    hipLaunchKernelGGL((copy_chunks_marked_kernel<UNROLL, true>), g, b, 0, stream, d, tpc,
+                       ntiles, c16, m);
+  else
+    hipLaunchKernelGGL((copy_chunks_marked_kernel<UNROLL, false>), g, b, 0, stream, d, tpc,
+                       ntiles, c16, m);
+}
+
+hipError_t launch_copy_chunks_marked(const ChunkDesc* d_descs, uint32_t n_chunks,
+                                     uint64_t chunk_bytes, uint32_t threads, uint32_t unroll,
+                                     uint32_t grid, const LayerMarks& marks,
+                                     hipStream_t stream) {
+  if (n_chunks == 0 || chunk_bytes == 0) return hipSuccess;
+  if (threads == 0 || threads > 1024 || threads % 64 != 0 || grid == 0 || grid > kMaxGrid)
+    return hipErrorInvalidValue;
+  if (marks.n == 0 || !marks.chunk_start || !marks.layer || !marks.counters ||
+      marks.targets.count == 0 || marks.targets.count > kMaxSignalTargets)
+    return hipErrorInvalidValue;
+  const bool ntl = (unroll & PF_KERNEL_NT_LOADS) != 0;
+  unroll &= 0xffu;
+  uint32_t tpc = 0, ntiles = 0, c16 = 0;
+  if (!tile_geometry(n_chunks, chunk_bytes, threads, unroll, &tpc, &ntiles, &c16))
+    return hipErrorInvalidValue;
+  if (static_cast<uint64_t>(ntiles) + grid > 0xffffffffull) return hipErrorInvalidValue;
+  const dim3 g(grid < ntiles ? grid : ntiles), b(threads);
+  switch (unroll) {
+    case 1: launch_marked<1>(g, b, stream, ntl, d_descs, tpc, ntiles, c16, marks); break;
+    case 2: launch_marked<2>(g, b, stream, ntl, d_descs, tpc, ntiles, c16, marks); break;
+    case 4: launch_marked<4>(g, b, stream, ntl, d_descs, tpc, ntiles, c16, marks); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

@@ -137,6 +137,17 @@ class StagedPlanner {
     return PF_OK;
   }
 
+  // A load waited for layer by layer starts with a slice that holds its
+  // first layer whole (up to the largest slice size): that layer is then one
+  // copy and one scatter, and each kernel on the way to it can wait for a
+  // whole kernel of other work holding every CU (a GEMM whose workgroups
+  // fill the register files).  Later slices double from there.  Before any
+  // layer is added.
+  void start_with_layer(uint64_t bytes) {
+    if (!is_save_ && sp_->steps.empty() && cur_.n_chunks == 0)
+      cap_ = std::max(cap_, std::min(max_cap_, bytes));
+  }
+
   // Descriptors of the slices start at index n (before any slice).
   void start_descriptors_at(size_t n) { sp_->n_desc = n; }
 

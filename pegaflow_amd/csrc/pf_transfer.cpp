@@ -6,6 +6,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <deque>
 #include <mutex>
 #include <thread>
 #include <vector>
@@ -290,6 +291,19 @@ constexpr uint64_t kScatterTrialMinBytes = 64ull << 20;  // time only launches t
 constexpr int kEngineSlots = 8;
 // Largest slice of a staged load that reports each layer's completion.
 constexpr uint64_t kLayeredLoadSlice = 64ull << 20;
+// A marked staged load's first slice marks up to kHeadTableLayers whole
+// layers from inside its scatter; their table (chunk starts, then layer
+// ids, as uint32) takes kHeadTableDescs descriptor slots.
+constexpr uint32_t kHeadTableLayers = 8;
+constexpr size_t kHeadTableDescs =
+    ((2 * kHeadTableLayers + 1) * sizeof(uint32_t) + sizeof(ChunkDesc) - 1) / sizeof(ChunkDesc);
+// Shape of that scatter (copy_chunks_marked_kernel): 512 threads, two
+// non-temporal 16-byte loads per lane (16 KiB tiles), at most 512
+// workgroups, so each takes several tiles and adds to its layer's counter
+// once per layer.
+constexpr uint32_t kMarkedScatterThreads = 512;
+constexpr uint32_t kMarkedScatterUnroll = 2u | PF_KERNEL_NT_LOADS;
+constexpr uint32_t kMarkedScatterGrid = 512;
 
 struct ScatterTrial {
   hipEvent_t start = nullptr, stop = nullptr;
@@ -331,8 +345,8 @@ struct pf_xfer {
   uint64_t slot_bytes = 0;
   // Largest staged slice per direction (0: save, 1: load), capped by slot_bytes.
   uint64_t staged_slice[2] = {PF_STAGED_SAVE_SLICE_DEFAULT, PF_STAGED_LOAD_SLICE_DEFAULT};
-  // A layer-by-layer staged load's first layer: PF_STAGED_HEAD_KERNEL or _ENGINE.
-  uint32_t staged_head = PF_STAGED_HEAD_KERNEL;
+  // A layer-by-layer staged load's first layer: PF_STAGED_HEAD_ENGINE or _KERNEL.
+  uint32_t staged_head = PF_STAGED_HEAD_ENGINE;
   // Recorded on a lane for the other lane to wait on (one per lane).
   hipEvent_t lane_mark[2] = {nullptr, nullptr};
   // Staged copies on the copy engines (when the device's are known): one
@@ -615,6 +629,34 @@ int launch(pf_xfer* x, size_t first, size_t n, uint64_t chunk_bytes, bool al16, 
   return PF_OK;
 }
 
+// A marked copy between device buffers (16-byte aligned chunks) on the
+// context's stream with a fixed workgroup -> tile map: the staged load's
+// scatter of a slice whose layers it marks itself.
+int launch_marked_scatter(pf_xfer* x, size_t first, size_t n, uint64_t chunk_bytes,
+                          const LayerMarks& m) {
+  if (n == 0) return PF_OK;
+  if (int rc = check_launch_size(n, chunk_bytes)) return rc;
+  std::pair<hipEvent_t, hipEvent_t>* tm = nullptr;
+  if (x->timing) {
+    if (x->last_kernels >= x->timers.size()) {
+      std::pair<hipEvent_t, hipEvent_t> p{nullptr, nullptr};
+      PF_HIP(hipEventCreate(&p.first));
+      PF_HIP(hipEventCreate(&p.second));
+      x->timers.push_back(p);
+    }
+    tm = &x->timers[x->last_kernels];
+    PF_HIP(hipEventRecord(tm->first, x->stream));
+  }
+  (void)hipGetLastError();
+  const hipError_t e = launch_copy_chunks_marked(
+      x->desc_base + first, static_cast<uint32_t>(n), chunk_bytes, kMarkedScatterThreads,
+      kMarkedScatterUnroll, kMarkedScatterGrid, m, x->stream);
+  if (e != hipSuccess) return hip_fail(e, "marked scatter kernel launch");
+  if (tm) PF_HIP(hipEventRecord(tm->second, x->stream));
+  x->last_kernels++;
+  return PF_OK;
+}
+
 // Counters for marking launches over num_layers layers, zeroed on the
 // context's stream before first use.
 int ensure_counters(pf_xfer* x, size_t num_layers) {
@@ -886,9 +928,9 @@ int kernel_direct(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<Lay
 
 int staged_engine(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
                   std::vector<LayerPlan>& plans, StagedPlanner& planner, StagedPlan& sp,
-                  uint32_t head, bool kernel_head, const PendingLayers* pending, bool is_save,
-                  pf_event* layer_events, const SignalTargets* sig, bool wait_save,
-                  StagedTrace& tr) {
+                  uint32_t head, bool kernel_head, bool head_table, const PendingLayers* pending,
+                  bool is_save, pf_event* layer_events, const SignalTargets* sig,
+                  bool wait_save, StagedTrace& tr) {
   const bool piped = head < num_layers;
   // Slots: as many as the staging holds of the largest slice (at least one).
   // A pipelined call's later slices are not known yet; each is at most the
@@ -989,6 +1031,31 @@ int staged_engine(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
     planner.start_descriptors_at(uploaded);
     tr.mark("head", used);
   }
+  // The first slice's scatter marks the layers it holds whole (head_table:
+  // their table is at descriptor 0), so the first layer lands after one
+  // kernel instead of a scatter and a marking kernel.
+  std::vector<uint32_t> fused;
+  if (head_table && !slice_steps.empty()) {
+    const StagedStep& st0 = sp.steps[slice_steps[0]];
+    std::vector<uint32_t> tab(1, 0);
+    bool ok = aligned16(st0.chunk_bytes) && aligned16(slot_base(0));
+    for (size_t pi = st0.piece_begin; pi < st0.piece_end && ok; ++pi) {
+      const Piece& pc = sp.pieces[pi];
+      const LayerPlan& p = plans[pc.layer];
+      ok = pc.begin == 0 && pc.end == p.chunks.size();
+      for (size_t i = pc.begin; i < pc.end && ok; ++i) ok = aligned16(p.chunks[i].dev);
+      if (ok) {
+        fused.push_back(pc.layer);
+        tab.push_back(tab.back() + static_cast<uint32_t>(pc.end - pc.begin));
+      }
+    }
+    if (!ok || fused.size() > kHeadTableLayers) {
+      fused.clear();
+    } else {
+      tab.insert(tab.end(), fused.begin(), fused.end());
+      std::memcpy(hd, tab.data(), tab.size() * sizeof(uint32_t));
+    }
+  }
   if (int rc = publish()) return rc;
   tr.mark("desc", sp.n_desc);
   PinnedCache pinned;
@@ -1042,6 +1109,16 @@ int staged_engine(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
     bool al16 = aligned16(st.chunk_bytes) && aligned16(slot);
     for_each_step_chunk(plans, sp, st,
                         [&](const Chunk& c, size_t) { al16 = al16 && aligned16(c.dev); });
+    if (slice_of[si] == 0 && !fused.empty()) {
+      const uint32_t* tab = reinterpret_cast<const uint32_t*>(x->desc_base);
+      LayerMarks m{};
+      m.chunk_start = tab;
+      m.layer = tab + fused.size() + 1;
+      m.n = static_cast<uint32_t>(fused.size());
+      m.counters = x->d_counters;
+      m.targets = *sig;
+      return launch_marked_scatter(x, st.desc_first, st.n_chunks, st.chunk_bytes, m);
+    }
     return launch(x, st.desc_first, st.n_chunks, st.chunk_bytes, al16, is_save);
   };
   // Kernels of slot s done (waited for on the host).
@@ -1125,43 +1202,77 @@ int staged_engine(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
     while (next_layer < plans.size() && sp.done_at[next_layer] == step)
       ids.push_back(static_cast<uint32_t>(next_layer++));
     if (ids.empty()) return PF_OK;
+    const uint32_t last = ids.back();
     for (uint32_t li : ids)
       if (layer_events && layer_events[li])
         PF_HIP(hipEventRecord(static_cast<hipEvent_t>(layer_events[li]), x->stream));
-    if (sig)
-      if (int rc = mark_layers(x, ids, *sig)) return rc;
-    tr.mark("L", ids.back());
+    if (sig) {
+      // Layers the first slice's scatter marked itself are left out.
+      if (!fused.empty() && !slice_steps.empty() && step == static_cast<int64_t>(slice_steps[0]))
+        ids.erase(std::remove_if(ids.begin(), ids.end(),
+                                 [&](uint32_t li) {
+                                   return std::find(fused.begin(), fused.end(), li) !=
+                                          fused.end();
+                                 }),
+                  ids.end());
+      if (!ids.empty())
+        if (int rc = mark_layers(x, ids, *sig)) return rc;
+    }
+    tr.mark("L", last);
     return PF_OK;
   };
   if (int rc = complete(-1)) return rc;
-  // Each slot refilled after its scatter.
+  // A slot is refilled once its scatter is done.  Scattered slices wait for
+  // that in order, and the host waits for the oldest one only when the next
+  // slice to scatter has not been queued yet: beside other work holding
+  // every CU a scatter can wait a whole kernel of that work (up to a
+  // millisecond), and the slices behind it are scattered and marked
+  // meanwhile.  Slice `queued` reuses the slot of the oldest waiting slice,
+  // queued - n_slots.
+  std::deque<size_t> scattered;
+  auto refill = [&](bool block) -> int {
+    while (!scattered.empty() && queued < slice_steps.size()) {
+      const size_t s = scattered.front() % n_slots;
+      if (block) {
+        PF_HIP(hipEventSynchronize(x->eng_ev[s]));
+        block = false;
+      } else {
+        const hipError_t q = hipEventQuery(x->eng_ev[s]);
+        if (q == hipErrorNotReady) break;
+        if (q != hipSuccess) return hip_fail(q, "staged scatter");
+      }
+      scattered.pop_front();
+      if (int rc = queue_copies(slice_steps[queued++])) return rc;
+    }
+    return PF_OK;
+  };
   for (size_t si = 0; si < sp.steps.size(); ++si) {
     const StagedStep& st = sp.steps[si];
     if (st.ordered_layer >= 0) {
       if (int rc = dma_layer(x, plans[static_cast<size_t>(st.ordered_layer)], false, false))
         return rc;
-    } else {
-      const size_t s = slice_of[si] % n_slots;
-      // The first layer's slices are waited for by polling: the interrupt
-      // wake costs about 25 us, and the first layer gates its consumer.
-      const bool first_layer = !kernel_head && static_cast<int64_t>(si) <= sp.done_at[0];
-      if (int rc = engine_signal_wait(&x->eng_sig[s], first_layer)) return rc;
-      tr.mark("c", slice_of[si]);
-      if (int rc = kernel(si)) return rc;
-      // The slot is refilled once its scatter is done (waited for on the
-      // host); the layers the slice completes are marked behind the scatter
-      // on the stream first, so a mark does not wait for that host wait
-      // (beside a GEMM a scatter waits for CUs for up to a millisecond).
-      const bool refill = queued < slice_steps.size();
-      if (refill) PF_HIP(hipEventRecord(x->eng_ev[s], x->stream));
       if (int rc = complete(static_cast<int64_t>(si))) return rc;
-      if (refill) {
-        PF_HIP(hipEventSynchronize(x->eng_ev[s]));
-        if (int rc = queue_copies(slice_steps[queued++])) return rc;
-      }
       continue;
     }
+    const size_t j = slice_of[si], s = j % n_slots;
+    while (j >= queued) {
+      if (scattered.empty())  // cannot happen: slice queued - n_slots was scattered
+        return fail(PF_ERR_STORAGE, "staged load: a slice's slot was never freed");
+      if (int rc = refill(true)) return rc;
+    }
+    // The first layer's slices are waited for by polling: the interrupt
+    // wake costs about 25 us, and the first layer gates its consumer.
+    const bool first_layer = !kernel_head && static_cast<int64_t>(si) <= sp.done_at[0];
+    if (int rc = engine_signal_wait(&x->eng_sig[s], first_layer)) return rc;
+    tr.mark("c", j);
+    if (int rc = kernel(si)) return rc;
+    if (queued < slice_steps.size()) {
+      PF_HIP(hipEventRecord(x->eng_ev[s], x->stream));
+      scattered.push_back(j);
+    }
+    // The layers the slice completes are marked behind its scatter.
     if (int rc = complete(static_cast<int64_t>(si))) return rc;
+    if (int rc = refill(false)) return rc;
   }
   return PF_OK;
 }
@@ -1194,16 +1305,16 @@ int staged(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, bool is
     head = num_layers;
   }
   // A pipelined load whose caller waits layer by layer (marks or per-layer
-  // events) copies its first layer with the zero-copy kernel, which has the
-  // link at full rate from the call's start (the Llama prefix's first layer
-  // in place 0.87 ms after an engine load's call, against 0.97 ms through
-  // the copy engine; beside a GEMM that holds every CU, 1.35-1.55 against
-  // 2.35-2.89 ms, the engine's layer also waiting for CUs for its scatter),
-  // and the rest staged: its 0.74 ms of shader traffic over the host link is
-  // the only part of the load that slows the device's other kernels (that
-  // GEMM 1.06-1.09x during the load, against 1.05-1.06x).  The context's staged_head may
-  // send the first layer through the copy engines too.  A load completed as
-  // a whole stays staged throughout.
+  // events) copies its first layer through the copy engines by default, as
+  // one copy (the planner's first slice holds it whole) and one scatter that
+  // marks it itself: beside a GEMM whose workgroups fill every CU's
+  // registers, each kernel of ours waits for one of the GEMM's kernels to
+  // end, so the layer lands after one such wait (the Llama prefix's first
+  // layer 1.58-1.66 ms after the call, 0.93-0.96 ms idle), and the load
+  // makes no shader traffic over the host link (the GEMM 1.04x slower while
+  // it runs).  The context's staged_head may send the first layer by the
+  // zero-copy kernel instead (1.57-1.62 ms beside that GEMM, 0.95 ms idle,
+  // the GEMM 1.05x).  A load completed as a whole stays staged throughout.
   const bool kernel_head = x->staged_head == PF_STAGED_HEAD_KERNEL && engines && !is_save &&
                            head > 0 && head < num_layers &&
                            (sig != nullptr || layer_events != nullptr);
@@ -1215,6 +1326,18 @@ int staged(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, bool is
   if (!is_save && (sig || layer_events)) slice = std::min(slice, kLayeredLoadSlice);
   StagedPlan sp;
   StagedPlanner planner(x->slot_bytes, slice, is_save, num_layers, &sp);
+  if (!is_save && (sig || layer_events) && !kernel_head) {
+    for (uint32_t li = 0; li < head; ++li)
+      if (!plans[li].ordered && !plans[li].chunks.empty()) {
+        planner.start_with_layer(plans[li].chunks.size() * plans[li].chunk_bytes);
+        break;
+      }
+  }
+  // A marked load through the copy engines marks the layers of its first
+  // slice from inside that slice's scatter; their table goes before the
+  // slices' descriptors.
+  const bool head_table = !is_save && sig && !kernel_head && engines;
+  if (head_table) planner.start_descriptors_at(kHeadTableDescs);
   if (!kernel_head) {
     if (int rc = planner.add(plans, 0, head)) return rc;
     if (int rc = planner.cut()) return rc;
@@ -1227,7 +1350,7 @@ int staged(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, bool is
     PF_HIP(hipEventSynchronize(x->staging_free));
     tr.mark("start", sp.steps.size());
     const int rc = staged_engine(x, layers, num_layers, plans, planner, sp, head, kernel_head,
-                                 pending, is_save, layer_events, sig, wait_save, tr);
+                                 head_table, pending, is_save, layer_events, sig, wait_save, tr);
     PF_HIP(hipEventRecord(x->staging_free, x->stream));
     tr.print(is_save);
     return rc;
@@ -2040,10 +2163,13 @@ int pf_xfer_create(int device, uint64_t staging_bytes, pf_xfer** out) {
   if (int rc = pf_init(device)) return rc;
   pf_xfer* x = new pf_xfer();
   x->device = device;
-  // PEGAFLOW_STAGED_HEAD=engine: new contexts (the engine's included) copy a
-  // layer-by-layer staged load's first layer through the copy engines.
-  if (const char* head = std::getenv("PEGAFLOW_STAGED_HEAD"))
+  // PEGAFLOW_STAGED_HEAD=kernel (or =engine): new contexts (the engine's
+  // included) copy a layer-by-layer staged load's first layer by the
+  // zero-copy kernel (or through the copy engines, the default).
+  if (const char* head = std::getenv("PEGAFLOW_STAGED_HEAD")) {
+    if (std::strcmp(head, "kernel") == 0) x->staged_head = PF_STAGED_HEAD_KERNEL;
     if (std::strcmp(head, "engine") == 0) x->staged_head = PF_STAGED_HEAD_ENGINE;
+  }
   auto cleanup = [&](int rc) {
     pf_xfer_destroy(x);
     return rc;

@@ -280,8 +280,8 @@ class TransferContext:
 
     def set_staged_head(self, route: int) -> None:
         """How a staged load waited for layer by layer copies its first layer:
-        _lib.STAGED_HEAD_KERNEL (zero-copy kernel, the default) or
-        _lib.STAGED_HEAD_ENGINE (copy engines; pf_xfer_set_staged_head)."""
+        _lib.STAGED_HEAD_ENGINE (copy engines, the default) or
+        _lib.STAGED_HEAD_KERNEL (zero-copy kernel; pf_xfer_set_staged_head)."""
         check(lib().pf_xfer_set_staged_head(self.handle, route), "pf_xfer_set_staged_head")
 
     def set_cu_mask(self, mask=None) -> None:

@@ -2,7 +2,9 @@
 // (no GPU), built by tests/test_native.py from the library's own sources:
 //   * a Llama-3-8B prefix load (32 layers of 40 MiB, 64 MiB load slices,
 //     128 MiB slots): the first layer in 16 + 24 MiB, every later layer one
-//     40 MiB slice; the same with the first layer left to the kernel;
+//     40 MiB slice; waited for layer by layer, every layer one slice; the
+//     same with the first layer left to the kernel; Qwen3-8B and oversized
+//     first layers waited for layer by layer;
 //   * its save: 128 MiB slices spanning layers, ten of them;
 //   * a tensor-parallel rank's load (5 MiB layers): the first two layers
 //     alone while slices grow, then seven layers a slice;
@@ -56,11 +58,13 @@ struct Call {
 };
 
 Call plan(std::vector<LayerPlan> plans, uint64_t slot, uint64_t slice, bool is_save,
-          uint32_t head, bool kernel_head = false, size_t desc_start = 0) {
+          uint32_t head, bool kernel_head = false, size_t desc_start = 0,
+          uint64_t first_layer = 0) {
   Call c;
   c.plans = std::move(plans);
   const uint32_t n = static_cast<uint32_t>(c.plans.size());
   StagedPlanner pl(slot, slice, is_save, n, &c.sp);
+  if (first_layer) pl.start_with_layer(first_layer);
   if (!kernel_head) {
     if ((c.rc = pl.add(c.plans, 0, head)) != PF_OK) return c;
     if ((c.rc = pl.cut()) != PF_OK) return c;
@@ -97,10 +101,12 @@ std::string spans(const StagedPlan& sp) {
 
 // Every rule a cut must keep (loads: slice sizes double from the first).
 void check_rules(const Call& c, uint64_t slot, uint64_t slice, bool is_save, uint32_t head,
-                 bool kernel_head, size_t desc_start, const std::string& what) {
+                 bool kernel_head, size_t desc_start, const std::string& what,
+                 uint64_t first_layer = 0) {
   const StagedPlan& sp = c.sp;
   const uint64_t max_cap = std::min(slot, slice);
   uint64_t cap = is_save ? max_cap : std::max<uint64_t>(1, std::min(16 * MiB, max_cap / 4));
+  if (!is_save) cap = std::max(cap, std::min(max_cap, first_layer));
   const uint32_t first = kernel_head ? head : 0;
   // Each chunk once, in order: walk the pieces against the plans.
   uint32_t li = first;
@@ -209,6 +215,27 @@ int main() {
     check_rules(c, slot, 64 * MiB, false, 1, false, 0, "llama load");
   }
   {
+    // Waited for layer by layer: the first layer one slice of its own.
+    const Call c = plan(llama(32, 40 * MiB), slot, 64 * MiB, false, 1, false, 0, 40 * MiB);
+    std::string want;
+    for (int l = 0; l < 32; ++l) want += "40 ";
+    expect(c.rc == PF_OK && sizes(c.sp) == want, "llama layered load: " + sizes(c.sp));
+    expect(c.sp.done_at[0] == 0 && c.sp.done_at[31] == 31, "llama layered load done_at");
+    check_rules(c, slot, 64 * MiB, false, 1, false, 0, "llama layered load", 40 * MiB);
+    // Qwen3-8B's 313 blocks (19.56 MiB layers): the first two layers alone
+    // while slices grow, then two layers a slice.
+    const uint64_t q = 313 * 2 * (32 << 10);
+    const Call qw = plan(llama(36, q), slot, 64 * MiB, false, 1, false, 0, q);
+    expect(qw.rc == PF_OK && spans(qw.sp).rfind("0 1 2-3 4-5 ", 0) == 0,
+           "qwen3 layered load: " + spans(qw.sp));
+    check_rules(qw, slot, 64 * MiB, false, 1, false, 0, "qwen3 layered load", q);
+    // A first layer larger than the largest slice: slices of that size.
+    const Call big = plan(llama(4, 100 * MiB), slot, 64 * MiB, false, 1, false, 0, 100 * MiB);
+    expect(big.rc == PF_OK && sizes(big.sp).rfind("64 36 64 36 ", 0) == 0,
+           "large-layer layered load: " + sizes(big.sp));
+    check_rules(big, slot, 64 * MiB, false, 1, false, 0, "large-layer layered load", 100 * MiB);
+  }
+  {
     const Call c = plan(llama(32, 40 * MiB), slot, 64 * MiB, false, 1, true, 40);
     std::string want = "16 24 ";
     for (int l = 2; l < 32; ++l) want += "40 ";
@@ -288,14 +315,21 @@ int main() {
     bool too_big = false;
     for (uint32_t l = kh ? head : 0; l < n; ++l)
       too_big = too_big || (!v[l].ordered && !v[l].chunks.empty() && v[l].chunk_bytes > slot_t);
-    const Call c = plan(v, slot_t, slice_t, is_save, head, kh, ds);
+    // A load waited for layer by layer starts with its first layer's bytes
+    // (as the transfer code passes them: the first non-empty layer copied
+    // through the staging).
+    uint64_t first = 0;
+    if (!is_save && !kh && rng() % 2 == 0)
+      for (uint32_t l = 0; l < head && first == 0; ++l)
+        if (!v[l].ordered && !v[l].chunks.empty()) first = v[l].chunks.size() * v[l].chunk_bytes;
+    const Call c = plan(v, slot_t, slice_t, is_save, head, kh, ds, first);
     const std::string what = "random call " + std::to_string(t);
     if (too_big) {
       expect(c.rc == PF_ERR_INVALID_ARGUMENT, what + ": oversized chunk accepted");
       continue;
     }
     expect(c.rc == PF_OK, what + ": refused");
-    if (c.rc == PF_OK) check_rules(c, slot_t, slice_t, is_save, head, kh, ds, what);
+    if (c.rc == PF_OK) check_rules(c, slot_t, slice_t, is_save, head, kh, ds, what, first);
   }
   if (failures) return 1;
   std::printf("ok\n");

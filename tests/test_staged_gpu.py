@@ -298,10 +298,11 @@ def test_staged_pipelined_load_vs_oracle(gpu, head, staging, load_slice):
 
 def test_staged_head_route_from_setting_and_environment(gpu, monkeypatch):
     """The first layer's route of a layer-by-layer staged load: the default
-    context copies it by the kernel, a context set to the copy engines and
-    one created under PEGAFLOW_STAGED_HEAD=engine copy it by DMA (more DMA
-    copies for the same load, the same count for both).  Every context's
-    load is checked against the oracle."""
+    context copies it through the copy engines, a context set to the kernel
+    and one created under PEGAFLOW_STAGED_HEAD=kernel copy it by the
+    zero-copy kernel (fewer DMA copies for the same load, the same count for
+    both); PEGAFLOW_STAGED_HEAD=engine gives the default's count.  Every
+    context's load is checked against the oracle."""
     say("[gpu] staged head route: default, set, environment")
     nb, bpb = 2048, 256
     kv = nb * bpb
@@ -320,12 +321,13 @@ def test_staged_head_route_from_setting_and_environment(gpu, monkeypatch):
         for L in layers:
             L.oracle_save()
         assert np.array_equal(host.array, ohost)
-        set_engine = TransferContext(0, staging_bytes=4 * MiB)
-        ctxs.append(set_engine)
-        set_engine.set_staged_head(_lib.STAGED_HEAD_ENGINE)
+        set_kernel = TransferContext(0, staging_bytes=4 * MiB)
+        ctxs.append(set_kernel)
+        set_kernel.set_staged_head(_lib.STAGED_HEAD_KERNEL)
+        monkeypatch.setenv("PEGAFLOW_STAGED_HEAD", "kernel")
+        ctxs.append(TransferContext(0, staging_bytes=4 * MiB))
         monkeypatch.setenv("PEGAFLOW_STAGED_HEAD", "engine")
-        from_env = TransferContext(0, staging_bytes=4 * MiB)
-        ctxs.append(from_env)
+        ctxs.append(TransferContext(0, staging_bytes=4 * MiB))
         monkeypatch.delenv("PEGAFLOW_STAGED_HEAD")
         dma = []
         for k, ctx in enumerate(ctxs):
@@ -339,8 +341,9 @@ def test_staged_head_route_from_setting_and_environment(gpu, monkeypatch):
                 if k == 0:
                     L.oracle_load(load)
                 assert np.array_equal(L.dev.download(), L.ref), f"context {k}: layer {i}"
-        say(f"[gpu] DMA copies: default {dma[0]}, set {dma[1]}, environment {dma[2]}")
-        assert dma[0] < dma[1] == dma[2], dma
+        say(f"[gpu] DMA copies: default {dma[0]}, set to the kernel {dma[1]}, environment "
+            f"kernel {dma[2]}, environment engine {dma[3]}")
+        assert dma[0] > dma[1] == dma[2] and dma[3] == dma[0], dma
     finally:
         for c in ctxs:
             c.close()
