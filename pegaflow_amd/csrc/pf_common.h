@@ -66,6 +66,19 @@ struct LayerMarks {
   SignalTargets targets;
 };
 
+// The layers of one marked scatter of a staged slice (passed by value, so
+// the kernel reads them from its arguments): chunks [chunk_start[g],
+// chunk_start[g+1]) of the launch belong to call layer layer[g], for g < n
+// (every group non-empty, n <= kSliceMarkLayers).
+constexpr uint32_t kSliceMarkLayers = 8;
+struct SliceMarks {
+  uint32_t n;
+  uint32_t chunk_start[kSliceMarkLayers + 1];
+  uint32_t layer[kSliceMarkLayers];
+  uint32_t* counters;
+  SignalTargets targets;
+};
+
 // Layers marked by mark_layers_kernel (passed by value).
 constexpr uint32_t kLayerListMax = 64;
 struct LayerList {
@@ -91,7 +104,7 @@ hipError_t launch_copy_chunks_queue(const ChunkDesc* d_descs, uint32_t n_chunks,
 // (16-byte aligned chunks): each finished layer of `marks` is marked.
 hipError_t launch_copy_chunks_marked(const ChunkDesc* d_descs, uint32_t n_chunks,
                                      uint64_t chunk_bytes, uint32_t threads, uint32_t unroll,
-                                     uint32_t grid, const LayerMarks& marks,
+                                     uint32_t grid, const SliceMarks& marks,
                                      hipStream_t stream);
 hipError_t launch_mark_layers(const LayerList& list, const SignalTargets& t,
                               hipStream_t stream);

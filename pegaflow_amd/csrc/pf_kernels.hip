@@ -128,22 +128,20 @@ __device__ __forceinline__ void tile_done(const LayerMarks& m, uint32_t c,
   }
 }
 
-// The group (launch layer) of chunk c: chunk_start[g] <= c < chunk_start[g+1].
-__device__ __forceinline__ uint32_t group_of(const LayerMarks& m, uint32_t c) {
-  uint32_t lo = 0, hi = m.n;
-  while (hi - lo > 1) {
-    const uint32_t mid = (lo + hi) >> 1;
-    if (m.chunk_start[mid] <= c) lo = mid;
-    else hi = mid;
-  }
-  return lo;
-}
-
-// tile_done for k tiles of group g at once.
-__device__ __forceinline__ void tiles_done(const LayerMarks& m, uint32_t g, uint32_t k,
-                                           uint32_t tiles_per_chunk) {
-  const uint32_t layer = m.layer[g];
-  const uint32_t tiles = (m.chunk_start[g + 1] - m.chunk_start[g]) * tiles_per_chunk;
+// tile_done for k tiles of group g of a slice's marks at once.  The group
+// table lives in the kernel's arguments; it is read with constant indices
+// only, so it stays in scalar registers.
+__device__ __forceinline__ void slice_tiles_done(const SliceMarks& m, uint32_t g, uint32_t k,
+                                                 uint32_t tiles_per_chunk) {
+  uint32_t layer = 0, first = 0, end = 0;
+#pragma unroll
+  for (uint32_t i = 0; i < kSliceMarkLayers; ++i)
+    if (i == g) {
+      layer = m.layer[i];
+      first = m.chunk_start[i];
+      end = m.chunk_start[i + 1];
+    }
+  const uint32_t tiles = (end - first) * tiles_per_chunk;
   uint32_t* cnt = m.counters + layer;
   const uint32_t prev = __hip_atomic_fetch_add(cnt, k, __ATOMIC_RELAXED,
                                                __HIP_MEMORY_SCOPE_AGENT);
@@ -152,6 +150,15 @@ __device__ __forceinline__ void tiles_done(const LayerMarks& m, uint32_t g, uint
     __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     write_marks(m.targets, layer);
   }
+}
+
+// The group of chunk c: the last g < n with chunk_start[g] <= c.
+__device__ __forceinline__ uint32_t slice_group_of(const SliceMarks& m, uint32_t c) {
+  uint32_t g = 0;
+#pragma unroll
+  for (uint32_t i = 1; i < kSliceMarkLayers; ++i)
+    if (i < m.n && m.chunk_start[i] <= c) g = i;
+  return g;
 }
 
 // A marked copy between device buffers (the staged load's scatter of a
@@ -167,17 +174,17 @@ __device__ __forceinline__ void tiles_done(const LayerMarks& m, uint32_t g, uint
 template <int UNROLL, bool NTL>
 __global__ void __launch_bounds__(1024)
 copy_chunks_marked_kernel(const ChunkDesc* __restrict__ descs, uint32_t tiles_per_chunk,
-                          uint32_t n_tiles, uint32_t chunk16, LayerMarks marks) {
+                          uint32_t n_tiles, uint32_t chunk16, SliceMarks marks) {
   const uint32_t stride = blockDim.x;
   const uint32_t tile_elems = stride * UNROLL;
   uint32_t group = 0, done = 0;
   for (uint32_t t = blockIdx.x; t < n_tiles; t += gridDim.x) {
     const uint32_t c = t / tiles_per_chunk;
-    const uint32_t g = group_of(marks, c);
+    const uint32_t g = slice_group_of(marks, c);
     if (done > 0 && g != group) {
       __builtin_amdgcn_s_waitcnt(0);  // every store of this wave acknowledged
       __syncthreads();
-      if (threadIdx.x == 0) tiles_done(marks, group, done, tiles_per_chunk);
+      if (threadIdx.x == 0) slice_tiles_done(marks, group, done, tiles_per_chunk);
       done = 0;
     }
     group = g;
@@ -203,7 +210,7 @@ copy_chunks_marked_kernel(const ChunkDesc* __restrict__ descs, uint32_t tiles_pe
   if (done > 0) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (threadIdx.x == 0) tiles_done(marks, group, done, tiles_per_chunk);
+    if (threadIdx.x == 0) slice_tiles_done(marks, group, done, tiles_per_chunk);
   }
 }
 
@@ -525,7 +532,7 @@ hipError_t launch_copy_chunks_queue(const ChunkDesc* d_descs, uint32_t n_chunks,
 
 template <int UNROLL>
 static void launch_marked(dim3 g, dim3 b, hipStream_t stream, bool ntl, const ChunkDesc* d,
-                          uint32_t tpc, uint32_t ntiles, uint32_t c16, const LayerMarks& m) {
+                          uint32_t tpc, uint32_t ntiles, uint32_t c16, const SliceMarks& m) {
   if (ntl)
     hipLaunchKernelGGL((copy_chunks_marked_kernel<UNROLL, true>), g, b, 0, stream, d, tpc,
                        ntiles, c16, m);
@@ -536,14 +543,17 @@ static void launch_marked(dim3 g, dim3 b, hipStream_t stream, bool ntl, const Ch
 
 hipError_t launch_copy_chunks_marked(const ChunkDesc* d_descs, uint32_t n_chunks,
                                      uint64_t chunk_bytes, uint32_t threads, uint32_t unroll,
-                                     uint32_t grid, const LayerMarks& marks,
+                                     uint32_t grid, const SliceMarks& marks,
                                      hipStream_t stream) {
   if (n_chunks == 0 || chunk_bytes == 0) return hipSuccess;
   if (threads == 0 || threads > 1024 || threads % 64 != 0 || grid == 0 || grid > kMaxGrid)
     return hipErrorInvalidValue;
-  if (marks.n == 0 || !marks.chunk_start || !marks.layer || !marks.counters ||
-      marks.targets.count == 0 || marks.targets.count > kMaxSignalTargets)
+  if (marks.n == 0 || marks.n > kSliceMarkLayers || !marks.counters ||
+      marks.targets.count == 0 || marks.targets.count > kMaxSignalTargets ||
+      marks.chunk_start[0] != 0 || marks.chunk_start[marks.n] != n_chunks)
     return hipErrorInvalidValue;
+  for (uint32_t g = 0; g < marks.n; ++g)
+    if (marks.chunk_start[g + 1] <= marks.chunk_start[g]) return hipErrorInvalidValue;
   const bool ntl = (unroll & PF_KERNEL_NT_LOADS) != 0;
   unroll &= 0xffu;
   uint32_t tpc = 0, ntiles = 0, c16 = 0;

@@ -291,13 +291,8 @@ constexpr uint64_t kScatterTrialMinBytes = 64ull << 20;  // time only launches t
 constexpr int kEngineSlots = 8;
 // Largest slice of a staged load that reports each layer's completion.
 constexpr uint64_t kLayeredLoadSlice = 64ull << 20;
-// A marked staged load's first slice marks up to kHeadTableLayers whole
-// layers from inside its scatter; their table (chunk starts, then layer
-// ids, as uint32) takes kHeadTableDescs descriptor slots.
-constexpr uint32_t kHeadTableLayers = 8;
-constexpr size_t kHeadTableDescs =
-    ((2 * kHeadTableLayers + 1) * sizeof(uint32_t) + sizeof(ChunkDesc) - 1) / sizeof(ChunkDesc);
-// Shape of that scatter (copy_chunks_marked_kernel): 512 threads, two
+// Shape of a marked staged load's scatter that marks its slice's layers
+// itself (copy_chunks_marked_kernel): 512 threads, two
 // non-temporal 16-byte loads per lane (16 KiB tiles), at most 512
 // workgroups, so each takes several tiles and adds to its layer's counter
 // once per layer.
@@ -633,7 +628,7 @@ int launch(pf_xfer* x, size_t first, size_t n, uint64_t chunk_bytes, bool al16, 
 // context's stream with a fixed workgroup -> tile map: the staged load's
 // scatter of a slice whose layers it marks itself.
 int launch_marked_scatter(pf_xfer* x, size_t first, size_t n, uint64_t chunk_bytes,
-                          const LayerMarks& m) {
+                          const SliceMarks& m) {
   if (n == 0) return PF_OK;
   if (int rc = check_launch_size(n, chunk_bytes)) return rc;
   std::pair<hipEvent_t, hipEvent_t>* tm = nullptr;
@@ -928,7 +923,7 @@ int kernel_direct(pf_xfer* x, const pf_layer_xfer* layers, const std::vector<Lay
 
 int staged_engine(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
                   std::vector<LayerPlan>& plans, StagedPlanner& planner, StagedPlan& sp,
-                  uint32_t head, bool kernel_head, bool head_table, const PendingLayers* pending,
+                  uint32_t head, bool kernel_head, bool slice_marks, const PendingLayers* pending,
                   bool is_save, pf_event* layer_events, const SignalTargets* sig,
                   bool wait_save, StagedTrace& tr) {
   const bool piped = head < num_layers;
@@ -1031,31 +1026,6 @@ int staged_engine(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
     planner.start_descriptors_at(uploaded);
     tr.mark("head", used);
   }
-  // The first slice's scatter marks the layers it holds whole (head_table:
-  // their table is at descriptor 0), so the first layer lands after one
-  // kernel instead of a scatter and a marking kernel.
-  std::vector<uint32_t> fused;
-  if (head_table && !slice_steps.empty()) {
-    const StagedStep& st0 = sp.steps[slice_steps[0]];
-    std::vector<uint32_t> tab(1, 0);
-    bool ok = aligned16(st0.chunk_bytes) && aligned16(slot_base(0));
-    for (size_t pi = st0.piece_begin; pi < st0.piece_end && ok; ++pi) {
-      const Piece& pc = sp.pieces[pi];
-      const LayerPlan& p = plans[pc.layer];
-      ok = pc.begin == 0 && pc.end == p.chunks.size();
-      for (size_t i = pc.begin; i < pc.end && ok; ++i) ok = aligned16(p.chunks[i].dev);
-      if (ok) {
-        fused.push_back(pc.layer);
-        tab.push_back(tab.back() + static_cast<uint32_t>(pc.end - pc.begin));
-      }
-    }
-    if (!ok || fused.size() > kHeadTableLayers) {
-      fused.clear();
-    } else {
-      tab.insert(tab.end(), fused.begin(), fused.end());
-      std::memcpy(hd, tab.data(), tab.size() * sizeof(uint32_t));
-    }
-  }
   if (int rc = publish()) return rc;
   tr.mark("desc", sp.n_desc);
   PinnedCache pinned;
@@ -1103,21 +1073,36 @@ int staged_engine(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
     tr.mark("q", j);
     return rc;
   };
+  // Per call layer: marked by its slice's scatter.
+  std::vector<char> self_marked(slice_marks ? num_layers : 0, 0);
   auto kernel = [&](size_t si) -> int {
     const StagedStep& st = sp.steps[si];
     const uint64_t slot = slot_base(slice_of[si]);
     bool al16 = aligned16(st.chunk_bytes) && aligned16(slot);
     for_each_step_chunk(plans, sp, st,
                         [&](const Chunk& c, size_t) { al16 = al16 && aligned16(c.dev); });
-    if (slice_of[si] == 0 && !fused.empty()) {
-      const uint32_t* tab = reinterpret_cast<const uint32_t*>(x->desc_base);
-      LayerMarks m{};
-      m.chunk_start = tab;
-      m.layer = tab + fused.size() + 1;
-      m.n = static_cast<uint32_t>(fused.size());
-      m.counters = x->d_counters;
-      m.targets = *sig;
-      return launch_marked_scatter(x, st.desc_first, st.n_chunks, st.chunk_bytes, m);
+    // A slice that holds each of its layers whole marks them from inside
+    // its scatter: beside other work filling every CU, each kernel of ours
+    // waits for one of that work's kernels to end, so the layers land after
+    // one such wait instead of two (a scatter, then a marking kernel).
+    if (slice_marks && al16 && st.piece_end - st.piece_begin <= kSliceMarkLayers) {
+      SliceMarks m{};
+      bool whole = true;
+      for (size_t pi = st.piece_begin; pi < st.piece_end && whole; ++pi) {
+        const Piece& pc = sp.pieces[pi];
+        whole = pc.begin == 0 && pc.end == plans[pc.layer].chunks.size();
+        m.layer[m.n] = pc.layer;
+        m.chunk_start[m.n + 1] = m.chunk_start[m.n] + static_cast<uint32_t>(pc.end - pc.begin);
+        ++m.n;
+      }
+      if (whole) {
+        m.counters = x->d_counters;
+        m.targets = *sig;
+        if (int rc = launch_marked_scatter(x, st.desc_first, st.n_chunks, st.chunk_bytes, m))
+          return rc;
+        for (uint32_t g = 0; g < m.n; ++g) self_marked[m.layer[g]] = 1;
+        return PF_OK;
+      }
     }
     return launch(x, st.desc_first, st.n_chunks, st.chunk_bytes, al16, is_save);
   };
@@ -1207,14 +1192,12 @@ int staged_engine(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
       if (layer_events && layer_events[li])
         PF_HIP(hipEventRecord(static_cast<hipEvent_t>(layer_events[li]), x->stream));
     if (sig) {
-      // Layers the first slice's scatter marked itself are left out.
-      if (!fused.empty() && !slice_steps.empty() && step == static_cast<int64_t>(slice_steps[0]))
-        ids.erase(std::remove_if(ids.begin(), ids.end(),
-                                 [&](uint32_t li) {
-                                   return std::find(fused.begin(), fused.end(), li) !=
-                                          fused.end();
-                                 }),
-                  ids.end());
+      // Layers a slice's scatter marked itself are left out.
+      ids.erase(std::remove_if(ids.begin(), ids.end(),
+                               [&](uint32_t li) {
+                                 return li < self_marked.size() && self_marked[li] != 0;
+                               }),
+                ids.end());
       if (!ids.empty())
         if (int rc = mark_layers(x, ids, *sig)) return rc;
     }
@@ -1333,11 +1316,9 @@ int staged(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, bool is
         break;
       }
   }
-  // A marked load through the copy engines marks the layers of its first
-  // slice from inside that slice's scatter; their table goes before the
-  // slices' descriptors.
-  const bool head_table = !is_save && sig && !kernel_head && engines;
-  if (head_table) planner.start_descriptors_at(kHeadTableDescs);
+  // A marked load through the copy engines marks the layers a slice holds
+  // whole from inside that slice's scatter.
+  const bool slice_marks = !is_save && sig && engines;
   if (!kernel_head) {
     if (int rc = planner.add(plans, 0, head)) return rc;
     if (int rc = planner.cut()) return rc;
@@ -1350,7 +1331,7 @@ int staged(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, bool is
     PF_HIP(hipEventSynchronize(x->staging_free));
     tr.mark("start", sp.steps.size());
     const int rc = staged_engine(x, layers, num_layers, plans, planner, sp, head, kernel_head,
-                                 head_table, pending, is_save, layer_events, sig, wait_save, tr);
+                                 slice_marks, pending, is_save, layer_events, sig, wait_save, tr);
     PF_HIP(hipEventRecord(x->staging_free, x->stream));
     tr.print(is_save);
     return rc;
