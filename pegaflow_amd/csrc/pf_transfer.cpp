@@ -1206,12 +1206,15 @@ int staged_engine(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
   };
   if (int rc = complete(-1)) return rc;
   // A slot is refilled once its scatter is done.  Scattered slices wait for
-  // that in order, and the host waits for the oldest one only when the next
-  // slice to scatter has not been queued yet: beside other work holding
-  // every CU a scatter can wait a whole kernel of that work (up to a
-  // millisecond), and the slices behind it are scattered and marked
-  // meanwhile.  Slice `queued` reuses the slot of the oldest waiting slice,
-  // queued - n_slots.
+  // that in order.  The host waits for the oldest one when the engine would
+  // otherwise be left with only the copy it is running (two slots: each
+  // refill must be queued while the other slot's copy runs), or when the
+  // next slice to scatter has not been queued yet; with more slots in
+  // flight it refills whatever scatters have ended and moves on: beside
+  // other work holding every CU a scatter can wait a whole kernel of that
+  // work (up to a millisecond), and the slices behind it are scattered and
+  // marked meanwhile.  Slice `queued` reuses the slot of the oldest waiting
+  // slice, queued - n_slots.
   std::deque<size_t> scattered;
   auto refill = [&](bool block) -> int {
     while (!scattered.empty() && queued < slice_steps.size()) {
@@ -1255,7 +1258,8 @@ int staged_engine(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
     }
     // The layers the slice completes are marked behind its scatter.
     if (int rc = complete(static_cast<int64_t>(si))) return rc;
-    if (int rc = refill(false)) return rc;
+    const bool engine_short = queued < slice_steps.size() && queued <= j + 2;
+    if (int rc = refill(engine_short)) return rc;
   }
   return PF_OK;
 }
