@@ -69,12 +69,16 @@ struct LayerMarks {
 // The layers of one marked scatter of a staged slice (passed by value, so
 // the kernel reads them from its arguments): chunks [chunk_start[g],
 // chunk_start[g+1]) of the launch belong to call layer layer[g], for g < n
-// (every group non-empty, n <= kSliceMarkLayers).
+// (every group non-empty, n <= kSliceMarkLayers).  tiles[g] is the layer's
+// tile count over all the launches that copy it (a layer may span slices:
+// counters[layer] adds up across them and the launch that reaches the count
+// marks the layer), or 0 for a layer marked otherwise (not counted).
 constexpr uint32_t kSliceMarkLayers = 8;
 struct SliceMarks {
   uint32_t n;
   uint32_t chunk_start[kSliceMarkLayers + 1];
   uint32_t layer[kSliceMarkLayers];
+  uint32_t tiles[kSliceMarkLayers];
   uint32_t* counters;
   SignalTargets targets;
 };

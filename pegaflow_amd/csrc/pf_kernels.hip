@@ -128,20 +128,19 @@ __device__ __forceinline__ void tile_done(const LayerMarks& m, uint32_t c,
   }
 }
 
-// tile_done for k tiles of group g of a slice's marks at once.  The group
-// table lives in the kernel's arguments; it is read with constant indices
-// only, so it stays in scalar registers.
-__device__ __forceinline__ void slice_tiles_done(const SliceMarks& m, uint32_t g, uint32_t k,
-                                                 uint32_t tiles_per_chunk) {
-  uint32_t layer = 0, first = 0, end = 0;
+// tile_done for k tiles of group g of a slice's marks at once, counted
+// toward the layer's tiles over all its launches.  The group table lives in
+// the kernel's arguments; it is read with constant indices only, so it
+// stays in scalar registers.
+__device__ __forceinline__ void slice_tiles_done(const SliceMarks& m, uint32_t g, uint32_t k) {
+  uint32_t layer = 0, tiles = 0;
 #pragma unroll
   for (uint32_t i = 0; i < kSliceMarkLayers; ++i)
     if (i == g) {
       layer = m.layer[i];
-      first = m.chunk_start[i];
-      end = m.chunk_start[i + 1];
+      tiles = m.tiles[i];
     }
-  const uint32_t tiles = (end - first) * tiles_per_chunk;
+  if (tiles == 0) return;  // marked by another kernel
   uint32_t* cnt = m.counters + layer;
   const uint32_t prev = __hip_atomic_fetch_add(cnt, k, __ATOMIC_RELAXED,
                                                __HIP_MEMORY_SCOPE_AGENT);
@@ -184,7 +183,7 @@ copy_chunks_marked_kernel(const ChunkDesc* __restrict__ descs, uint32_t tiles_pe
     if (done > 0 && g != group) {
       __builtin_amdgcn_s_waitcnt(0);  // every store of this wave acknowledged
       __syncthreads();
-      if (threadIdx.x == 0) slice_tiles_done(marks, group, done, tiles_per_chunk);
+      if (threadIdx.x == 0) slice_tiles_done(marks, group, done);
       done = 0;
     }
     group = g;
@@ -210,7 +209,7 @@ copy_chunks_marked_kernel(const ChunkDesc* __restrict__ descs, uint32_t tiles_pe
   if (done > 0) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (threadIdx.x == 0) slice_tiles_done(marks, group, done, tiles_per_chunk);
+    if (threadIdx.x == 0) slice_tiles_done(marks, group, done);
   }
 }
 
@@ -552,13 +551,18 @@ hipError_t launch_copy_chunks_marked(const ChunkDesc* d_descs, uint32_t n_chunks
       marks.targets.count == 0 || marks.targets.count > kMaxSignalTargets ||
       marks.chunk_start[0] != 0 || marks.chunk_start[marks.n] != n_chunks)
     return hipErrorInvalidValue;
-  for (uint32_t g = 0; g < marks.n; ++g)
-    if (marks.chunk_start[g + 1] <= marks.chunk_start[g]) return hipErrorInvalidValue;
   const bool ntl = (unroll & PF_KERNEL_NT_LOADS) != 0;
   unroll &= 0xffu;
   uint32_t tpc = 0, ntiles = 0, c16 = 0;
   if (!tile_geometry(n_chunks, chunk_bytes, threads, unroll, &tpc, &ntiles, &c16))
     return hipErrorInvalidValue;
+  // Groups in chunk order, each counting at least its own tiles.
+  for (uint32_t g = 0; g < marks.n; ++g)
+    if (marks.chunk_start[g + 1] <= marks.chunk_start[g] ||
+        (marks.tiles[g] != 0 &&
+         static_cast<uint64_t>(marks.tiles[g]) <
+             static_cast<uint64_t>(marks.chunk_start[g + 1] - marks.chunk_start[g]) * tpc))
+      return hipErrorInvalidValue;
   if (static_cast<uint64_t>(ntiles) + grid > 0xffffffffull) return hipErrorInvalidValue;
   const dim3 g(grid < ntiles ? grid : ntiles), b(threads);
   switch (unroll) {

@@ -1073,35 +1073,60 @@ int staged_engine(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
     tr.mark("q", j);
     return rc;
   };
-  // Per call layer: marked by its slice's scatter.
-  std::vector<char> self_marked(slice_marks ? num_layers : 0, 0);
+  // A marked load's layers are marked by the scatters of their slices where
+  // every slice holding a piece of the layer can run the marking kernel
+  // (16-byte aligned, at most kSliceMarkLayers layers): the layer's counter
+  // adds up over those launches.  Per call layer: 1 so, 0 marked by a
+  // marking kernel after its last slice, -1 not decided yet (decided at its
+  // first slice, when every slice holding it is known).
+  std::vector<signed char> self_marked(slice_marks ? num_layers : 0, -1);
+  auto markable = [&](size_t si) {
+    const StagedStep& st = sp.steps[si];
+    if (st.ordered_layer >= 0 || st.piece_end - st.piece_begin > kSliceMarkLayers ||
+        !aligned16(st.chunk_bytes) || !aligned16(slot_base(slice_of[si])))
+      return false;
+    bool al = true;
+    for_each_step_chunk(plans, sp, st, [&](const Chunk& c, size_t) { al = al && aligned16(c.dev); });
+    return al;
+  };
+  const uint64_t marked_tile = uint64_t(kMarkedScatterThreads) * (kMarkedScatterUnroll & 0xffu);
   auto kernel = [&](size_t si) -> int {
     const StagedStep& st = sp.steps[si];
     const uint64_t slot = slot_base(slice_of[si]);
     bool al16 = aligned16(st.chunk_bytes) && aligned16(slot);
     for_each_step_chunk(plans, sp, st,
                         [&](const Chunk& c, size_t) { al16 = al16 && aligned16(c.dev); });
-    // A slice that holds each of its layers whole marks them from inside
-    // its scatter: beside other work filling every CU, each kernel of ours
-    // waits for one of that work's kernels to end, so the layers land after
-    // one such wait instead of two (a scatter, then a marking kernel).
-    if (slice_marks && al16 && st.piece_end - st.piece_begin <= kSliceMarkLayers) {
+    // A slice's scatter marks the layers it completes: beside other work
+    // filling every CU, each kernel of ours waits for one of that work's
+    // kernels to end, so a layer lands after one such wait instead of two (a
+    // scatter, then a marking kernel).
+    if (slice_marks) {
+      for (size_t pi = st.piece_begin; pi < st.piece_end; ++pi) {
+        const uint32_t li = sp.pieces[pi].layer;
+        if (self_marked[li] >= 0) continue;
+        bool ok = true;  // this slice is the layer's first
+        for (size_t k = si; ok && static_cast<int64_t>(k) <= sp.done_at[li]; ++k)
+          ok = markable(k);
+        self_marked[li] = ok ? 1 : 0;
+      }
       SliceMarks m{};
-      bool whole = true;
-      for (size_t pi = st.piece_begin; pi < st.piece_end && whole; ++pi) {
+      bool counts = false;
+      for (size_t pi = st.piece_begin; pi < st.piece_end && m.n < kSliceMarkLayers; ++pi) {
         const Piece& pc = sp.pieces[pi];
-        whole = pc.begin == 0 && pc.end == plans[pc.layer].chunks.size();
+        const LayerPlan& p = plans[pc.layer];
         m.layer[m.n] = pc.layer;
         m.chunk_start[m.n + 1] = m.chunk_start[m.n] + static_cast<uint32_t>(pc.end - pc.begin);
+        if (self_marked[pc.layer] == 1) {
+          const uint64_t tpc = (p.chunk_bytes / 16 + marked_tile - 1) / marked_tile;
+          m.tiles[m.n] = static_cast<uint32_t>(p.chunks.size() * tpc);
+          counts = true;
+        }
         ++m.n;
       }
-      if (whole) {
+      if (counts) {
         m.counters = x->d_counters;
         m.targets = *sig;
-        if (int rc = launch_marked_scatter(x, st.desc_first, st.n_chunks, st.chunk_bytes, m))
-          return rc;
-        for (uint32_t g = 0; g < m.n; ++g) self_marked[m.layer[g]] = 1;
-        return PF_OK;
+        return launch_marked_scatter(x, st.desc_first, st.n_chunks, st.chunk_bytes, m);
       }
     }
     return launch(x, st.desc_first, st.n_chunks, st.chunk_bytes, al16, is_save);
@@ -1192,10 +1217,10 @@ int staged_engine(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
       if (layer_events && layer_events[li])
         PF_HIP(hipEventRecord(static_cast<hipEvent_t>(layer_events[li]), x->stream));
     if (sig) {
-      // Layers a slice's scatter marked itself are left out.
+      // Layers their slices' scatters marked are left out.
       ids.erase(std::remove_if(ids.begin(), ids.end(),
                                [&](uint32_t li) {
-                                 return li < self_marked.size() && self_marked[li] != 0;
+                                 return li < self_marked.size() && self_marked[li] == 1;
                                }),
                 ids.end());
       if (!ids.empty())
@@ -1334,8 +1359,18 @@ int staged(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, bool is
     if (int rc = ensure_counters(x, num_layers)) return rc;  // queued device routes
     PF_HIP(hipEventSynchronize(x->staging_free));
     tr.mark("start", sp.steps.size());
-    const int rc = staged_engine(x, layers, num_layers, plans, planner, sp, head, kernel_head,
-                                 slice_marks, pending, is_save, layer_events, sig, wait_save, tr);
+    int rc = staged_engine(x, layers, num_layers, plans, planner, sp, head, kernel_head,
+                           slice_marks, pending, is_save, layer_events, sig, wait_save, tr);
+    // A layer's tile counter adds up over the scatters of its slices; a call
+    // that stopped between two of them leaves counts behind.  Once its
+    // kernels have ended they are cleared, so the next marked call starts
+    // from 0.
+    if (rc != PF_OK && slice_marks) {
+      const hipError_t e1 = hipStreamSynchronize(x->stream);
+      const hipError_t e2 =
+          e1 == hipSuccess ? hipMemset(x->d_counters, 0, num_layers * sizeof(uint32_t)) : e1;
+      if (e2 != hipSuccess) (void)hipGetLastError();
+    }
     PF_HIP(hipEventRecord(x->staging_free, x->stream));
     tr.print(is_save);
     return rc;

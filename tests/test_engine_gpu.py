@@ -599,10 +599,15 @@ def test_split_load_error_in_later_layers(engine, mode):
         assert wait(st) == -1
         after = [x.download() for x in b.bufs[1:]] + [odd.download()]
         assert all(np.array_equal(x, y) for x, y in zip(before, after))
-        # The worker is free: a load of the matching layers completes.
+        # The worker is free: a load of the matching layers completes, and so
+        # does one that reports each layer (its marks count from 0 again).
         st = PyLoadState()
         engine.batch_load_kv_blocks("splitb", 0, 0, st.shm_name(), b.names, targets, hashes)
         assert wait(st) == 1
+        st = PyLoadState(num_layers=len(b.names))
+        engine.batch_load_kv_blocks("splitb", 0, 0, st.shm_name(), b.names, targets, hashes)
+        assert wait(st) == 1
+        assert st.layers_done() == len(b.names)
     finally:
         a.close()
         if b is not None:

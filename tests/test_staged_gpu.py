@@ -602,3 +602,58 @@ def test_cu_mask_refusals(gpu, monkeypatch):
             host.close()
     finally:
         ctx.close()
+
+
+def test_marked_slices_mixed_routes_vs_oracle(gpu):
+    """A marked staged load whose slices take both marking routes: 16 small
+    layers (one slice holds more of them than a scatter can mark itself, so
+    they and the large layer whose first piece shares that slice are marked
+    by a marking kernel), then large layers spanning several 64 KiB slices
+    (each marked by the scatters of its slices, its tile count adding up over
+    them; some of those slices also finish the previous layer).  Every
+    layer's word is set and every byte equals the oracle; a second load (new
+    value, into refilled tensors) marks every layer again: no count is left
+    over from the first."""
+    say("[gpu] marked staged load: scatter-marked and kernel-marked layers")
+    # 256-byte segments throughout, so chunk size never closes a slice:
+    # slices of 64 KiB (256 chunks).  Layers 0 and 1 alone (slices growing),
+    # layers 2-15 (1 KiB each) with the first 200 chunks of layer 16 in one
+    # slice of 15 pieces, then layer 16's 1 MiB over 15 more slices, the
+    # last shared with layer 17's start, and likewise for 17 and 18.
+    nb, big_nb = 96, 2100
+    small = [(nb, 256, 2, nb * 256, 2 * nb * 256) for _ in range(16)]
+    big = [(big_nb, 256, 2, big_nb * 256, 2 * big_nb * 256) for _ in range(3)]
+    layers = [Layer(*shape, 900 + i) for i, shape in enumerate(small + big)]
+    rng = np.random.Generator(np.random.PCG64(91))
+    save_ids = [([5, 9] if i < 16 else rng.permutation(big_nb)[:2048].tolist())
+                for i in range(len(layers))]
+    load_ids = [([1, 2] if i < 16 else rng.permutation(big_nb)[:2048].tolist())
+                for i in range(len(layers))]
+    host, ohost = _place_all(layers, save_ids)
+    ctx = TransferContext(0, staging_bytes=4 * MiB)
+    ctx.set_staged_slices(0, 64 * 1024)
+    words = PinnedBuffer(8 * len(layers))
+    try:
+        ctx.save_layers([L.transfer(ids) for L, ids in zip(layers, save_ids)], _lib.MODE_STAGED)
+        ctx.synchronize()
+        for L in layers:
+            L.oracle_save()
+        assert np.array_equal(host.array, ohost), "host regions differ from the oracle"
+        for value in (21, 22):
+            for i, (L, ids) in enumerate(zip(layers, load_ids)):
+                L.dev.fill_random(value * 100 + i)
+                L.ref[:] = L.dev.download()  # in place: the oracle's layout points here
+                L.oracle_load(ids)
+            words.array[:] = 0
+            ctx.load_layers_marked([L.transfer(ids) for L, ids in zip(layers, load_ids)],
+                                   [(words.ptr, value, True)], _lib.MODE_STAGED)
+            ctx.synchronize()
+            assert words.array.view(np.uint64).tolist() == [value] * len(layers)
+            for i, L in enumerate(layers):
+                assert np.array_equal(L.dev.download(), L.ref), f"load {value}: layer {i}"
+    finally:
+        for L in layers:
+            L.close()
+        host.close()
+        words.close()
+        ctx.close()
