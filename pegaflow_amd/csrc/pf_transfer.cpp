@@ -292,13 +292,21 @@ constexpr int kEngineSlots = 8;
 // Largest slice of a staged load that reports each layer's completion.
 constexpr uint64_t kLayeredLoadSlice = 64ull << 20;
 // Shape of a marked staged load's scatter that marks its slice's layers
-// itself (copy_chunks_marked_kernel): 512 threads, two
-// non-temporal 16-byte loads per lane (16 KiB tiles), at most 512
-// workgroups, so each takes several tiles and adds to its layer's counter
-// once per layer.
+// itself (copy_chunks_marked_kernel): 512 threads, up to four non-temporal
+// 16-byte loads per lane (a 32 KiB chunk is one tile), 128 workgroups.
+// Each workgroup ends each of its layers with a release fence that writes
+// its XCD's L2 back, so fewer, busier workgroups win: measured on 40 MiB
+// layers of 32 KiB chunks, 24.8 us per layer with 128 workgroups and four
+// loads per lane, 25.1 with 256, 32 with 512, 73 with 1,280, 108 with one
+// workgroup per 8 KiB tile, 46 with 64.
 constexpr uint32_t kMarkedScatterThreads = 512;
-constexpr uint32_t kMarkedScatterUnroll = 2u | PF_KERNEL_NT_LOADS;
-constexpr uint32_t kMarkedScatterGrid = 512;
+constexpr uint32_t kMarkedScatterGrid = 128;
+// Loads per lane for chunks of chunk_bytes: the tile covers a chunk of up to
+// 32 KiB, or 32 KiB of a larger one.
+static uint32_t marked_unroll(uint64_t chunk_bytes) {
+  const uint64_t c16 = chunk_bytes / 16;
+  return c16 >= 4u * kMarkedScatterThreads ? 4u : c16 >= 2u * kMarkedScatterThreads ? 2u : 1u;
+}
 
 struct ScatterTrial {
   hipEvent_t start = nullptr, stop = nullptr;
@@ -645,7 +653,7 @@ int launch_marked_scatter(pf_xfer* x, size_t first, size_t n, uint64_t chunk_byt
   (void)hipGetLastError();
   const hipError_t e = launch_copy_chunks_marked(
       x->desc_base + first, static_cast<uint32_t>(n), chunk_bytes, kMarkedScatterThreads,
-      kMarkedScatterUnroll, kMarkedScatterGrid, m, x->stream);
+      marked_unroll(chunk_bytes) | PF_KERNEL_NT_LOADS, kMarkedScatterGrid, m, x->stream);
   if (e != hipSuccess) return hip_fail(e, "marked scatter kernel launch");
   if (tm) PF_HIP(hipEventRecord(tm->second, x->stream));
   x->last_kernels++;
@@ -1089,7 +1097,6 @@ int staged_engine(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
     for_each_step_chunk(plans, sp, st, [&](const Chunk& c, size_t) { al = al && aligned16(c.dev); });
     return al;
   };
-  const uint64_t marked_tile = uint64_t(kMarkedScatterThreads) * (kMarkedScatterUnroll & 0xffu);
   auto kernel = [&](size_t si) -> int {
     const StagedStep& st = sp.steps[si];
     const uint64_t slot = slot_base(slice_of[si]);
@@ -1117,7 +1124,8 @@ int staged_engine(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers,
         m.layer[m.n] = pc.layer;
         m.chunk_start[m.n + 1] = m.chunk_start[m.n] + static_cast<uint32_t>(pc.end - pc.begin);
         if (self_marked[pc.layer] == 1) {
-          const uint64_t tpc = (p.chunk_bytes / 16 + marked_tile - 1) / marked_tile;
+          const uint64_t tile = uint64_t(kMarkedScatterThreads) * marked_unroll(p.chunk_bytes);
+          const uint64_t tpc = (p.chunk_bytes / 16 + tile - 1) / tile;
           m.tiles[m.n] = static_cast<uint32_t>(p.chunks.size() * tpc);
           counts = true;
         }
