@@ -411,12 +411,12 @@ int pf_xfer_set_staged_slices(pf_xfer* xfer, uint64_t save_bytes, uint64_t load_
  * GEMM whose workgroups fill every CU, each kernel of the load waits for one
  * of the GEMM's kernels to end, so either route lands the layer after one
  * such wait.  Measured on the Llama-3.1-8B prefix beside a bf16 8192^3 GEMM
- * run back to back by another process (bench.py --first-layer-study, two
- * runs): the copy-engine route lands the first layer 1.58-1.66 ms after the
- * call, the load runs at 52.8-53.8 GB/s and the GEMM 1.04x slower; the
- * kernel route 1.57-1.62 ms, 52.9-53.5 GB/s and 1.05x (its 0.74 ms of shader
- * traffic over the host link also slows every other kernel's memory
- * traffic).  On an idle device both land it in 0.93-0.96 ms.  The
+ * run back to back by another process (bench.py --first-layer-study, four
+ * runs): the copy-engine route lands the first layer 1.57-1.65 ms after the
+ * call, the load runs at 54.2-55.7 GB/s and the GEMM 1.01-1.04x slower; the
+ * kernel route 1.50-1.58 ms, 53.3-53.6 GB/s and 1.04-1.06x (its 0.74 ms of
+ * shader traffic over the host link also slows every other kernel's memory
+ * traffic).  On an idle device both land it in 0.93-1.02 ms.  The
  * environment variable PEGAFLOW_STAGED_HEAD=kernel (or =engine) sets the
  * route of contexts created afterwards, the engine's included.  Other
  * routes: PF_ERR_INVALID_ARGUMENT.  No counterpart in the reference (its

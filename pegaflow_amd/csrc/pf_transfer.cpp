@@ -1330,11 +1330,12 @@ int staged(pf_xfer* x, const pf_layer_xfer* layers, uint32_t num_layers, bool is
   // marks it itself: beside a GEMM whose workgroups fill every CU's
   // registers, each kernel of ours waits for one of the GEMM's kernels to
   // end, so the layer lands after one such wait (the Llama prefix's first
-  // layer 1.58-1.66 ms after the call, 0.93-0.96 ms idle), and the load
-  // makes no shader traffic over the host link (the GEMM 1.04x slower while
-  // it runs).  The context's staged_head may send the first layer by the
-  // zero-copy kernel instead (1.57-1.62 ms beside that GEMM, 0.95 ms idle,
-  // the GEMM 1.05x).  A load completed as a whole stays staged throughout.
+  // layer 1.57-1.65 ms after the call, 0.93-0.98 ms idle), and the load
+  // makes no shader traffic over the host link (the GEMM 1.01-1.04x slower
+  // while it runs).  The context's staged_head may send the first layer by
+  // the zero-copy kernel instead (1.50-1.58 ms beside that GEMM, 0.94-1.02
+  // ms idle, the GEMM 1.04-1.06x).  A load completed as a whole stays staged
+  // throughout.
   const bool kernel_head = x->staged_head == PF_STAGED_HEAD_KERNEL && engines && !is_save &&
                            head > 0 && head < num_layers &&
                            (sig != nullptr || layer_events != nullptr);
