@@ -16,6 +16,7 @@ end.
 """
 
 import hashlib
+import os
 import random
 import sys
 import threading
@@ -174,7 +175,8 @@ def test_concurrent_saves_loads_and_queries(gpu, save_mode, load_mode):
     try:
         for t in threads:
             t.start()
-        deadline = time.monotonic() + 6.0
+        # PEGAFLOW_SOAK_SECONDS lengthens the run (6 s by default).
+        deadline = time.monotonic() + float(os.environ.get("PEGAFLOW_SOAK_SECONDS", "6"))
         while time.monotonic() < deadline and not stop.is_set():
             time.sleep(0.05)
         stop.set()
