@@ -2388,7 +2388,6 @@ int pf_xfer_set_staged_head(pf_xfer* x, uint32_t route) {
 int pf_cu_mask_per_xcd(int device, uint32_t cus_per_xcd, uint32_t* mask, uint32_t words) {
   if (!mask || words == 0) return fail(PF_ERR_INVALID_ARGUMENT, "null or empty mask");
   int cus = 0, xcds = 0;
-  PF_HIP(hipSetDevice(device));
   PF_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
   PF_HIP(hipDeviceGetAttribute(&xcds, hipDeviceAttributeNumberOfXccs, device));
   if (xcds <= 0) xcds = 1;
