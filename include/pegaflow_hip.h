@@ -747,8 +747,28 @@ typedef struct pf_engine_stats {
   uint64_t saved_bytes;
   uint64_t loaded_bytes;
   uint64_t load_failures;
+  uint64_t admission_rejections; /* new blocks TinyLFU refused (cache.rs:84-92) */
+  uint64_t pre_evicted_blocks;   /* blocks the pre-eviction monitor evicted    */
 } pf_engine_stats;
 int pf_engine_stats_get(pf_engine* e, pf_engine_stats* out);
+/* Storage policy (replaces StorageConfig and PreEvictConfig, storage.rs:43-111,
+ * and TinyLfuCache's sizing, cache.rs:33-47).
+ *  - lfu_admission: TinyLFU admission of newly sealed blocks and of blocks read
+ *    back from disk (cache.rs:71-95): each is recorded in a count-min sketch,
+ *    and refused when its estimate is below that of the least recently used
+ *    block; lookup hits are recorded too.  The sketch is sized for
+ *    pool_bytes / value_size_hint entries (value_size_hint 0: 128 MiB, as the
+ *    reference's default).  Off by default here; the reference turns it on by
+ *    default, where its 128 MiB sizing for KV blocks of a few MiB makes the
+ *    sketch's collisions decide (replayed on the host: 9-17% of new 2 MiB
+ *    blocks refused under a save/load mix).
+ *  - pre_evict: a thread that every interval_ms evicts least-recently-used
+ *    blocks while the pool's free bytes are below threshold_bytes, until
+ *    target_bytes are free (storage.rs:646-688).  0 stops it.
+ * May be called again at any time; admission restarts with an empty sketch. */
+int pf_engine_set_storage_policy(pf_engine* e, int lfu_admission, uint64_t value_size_hint,
+                                 int pre_evict, uint64_t threshold_bytes,
+                                 uint64_t target_bytes, uint32_t interval_ms);
 /* Block until every queued load has finished. */
 int pf_engine_wait_idle(pf_engine* e);
 

@@ -187,7 +187,8 @@ class SaveLayer(ctypes.Structure):
 class EngineStats(ctypes.Structure):
     _fields_ = [(n, ctypes.c_uint64) for n in (
         "pool_used_bytes", "pool_total_bytes", "sealed_blocks", "inflight_blocks",
-        "evicted_blocks", "saved_bytes", "loaded_bytes", "load_failures")]
+        "evicted_blocks", "saved_bytes", "loaded_bytes", "load_failures",
+        "admission_rejections", "pre_evicted_blocks")]
 
 
 class PrefetchStatus(ctypes.Structure):
@@ -322,6 +323,7 @@ SIGNATURES = {
     "pf_engine_create": (i32, [u64, u32, u32, u64, pvp]),
     "pf_engine_destroy": (i32, [vp]),
     "pf_engine_set_modes": (i32, [vp, u32, u32]),
+    "pf_engine_set_storage_policy": (i32, [vp, i32, u64, i32, u64, u64, u32]),
     "pf_engine_register_context_layer": (i32, [vp, cs, cs, i32, cs, u64, u64, u64, u64, u64,
                                                u64, u64, u64, u64]),
     "pf_engine_unregister_instance": (i32, [vp, cs]),

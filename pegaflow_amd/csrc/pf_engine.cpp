@@ -19,6 +19,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <random>
 #include <set>
 
 namespace pf {
@@ -217,6 +218,8 @@ uint64_t PinnedPool::largest_free() {
 // ===========================================================================
 namespace {
 constexpr size_t kReclaimBatch = 64;  // storage.rs:41
+// Value size assumed by TinyLFU's sizing when no hint is given (cache.rs:14).
+constexpr uint64_t kLfuDefaultValueBytes = 128ull << 20;
 }
 
 size_t BlockStore::evict_lru(size_t max_blocks) {
@@ -232,6 +235,41 @@ size_t BlockStore::evict_lru(size_t max_blocks) {
     evictions_ += dropped.size();
   }
   return dropped.size();  // memory returns to the pool as the handles drop here
+}
+
+size_t BlockStore::evict_bytes(uint64_t bytes, uint64_t* freed) {
+  std::vector<std::shared_ptr<SealedBlock>> dropped;
+  uint64_t total = 0;
+  {
+    std::lock_guard<std::mutex> lk(cache_mu_);
+    while (total < bytes && !lru_.empty()) {
+      auto it = cache_.find(*lru_.back());
+      lru_.pop_back();
+      total += it->second.block->footprint;
+      dropped.push_back(std::move(it->second.block));
+      cache_.erase(it);
+    }
+    evictions_ += dropped.size();
+  }
+  if (freed) *freed = total;
+  return dropped.size();
+}
+
+void BlockStore::set_admission(uint64_t items, uint64_t seed) {
+  std::lock_guard<std::mutex> lk(cache_mu_);
+  lfu_.reset(items ? new TinyLfu(items, seed) : nullptr);
+}
+
+// cache.rs:71-95: the key is recorded whatever the outcome, then refused
+// when it is colder than the least recently used entry.
+bool BlockStore::admit(const std::string& key) {
+  if (!lfu_) return true;
+  lfu_->incr(key);
+  if (!lru_.empty() && lfu_->get(key) < lfu_->get(*lru_.back())) {
+    ++rejections_;
+    return false;
+  }
+  return true;
 }
 
 std::shared_ptr<PoolAllocation> BlockStore::allocate(uint64_t size) {
@@ -422,9 +460,10 @@ int BlockStore::insert_slots(const std::vector<std::string>& keys,
   {
     std::lock_guard<std::mutex> lk(cache_mu_);
     size_t k = 0;
-    if (prepared->staged) {
+    if (prepared->staged && !lfu_) {
       // The complete blocks' nodes move in whole (no allocation or hashing
       // under the lock); those whose key was sealed meanwhile stay behind.
+      // With admission on, every block goes through it, in order, below.
       cache_.merge(prepared->nodes);
       for (auto& left : prepared->nodes) prepared->order.erase(left.second.pos);
       lru_.splice(lru_.begin(), prepared->order);
@@ -435,8 +474,18 @@ int BlockStore::insert_slots(const std::vector<std::string>& keys,
         }
       k = n_direct;
     }
+    // A key named twice in the call is offered once (its first block), as
+    // the reference skips the second occurrence's slots before its cache.
+    std::vector<char> offered;
+    if (lfu_) offered.assign(n, 0);
     for (; k < sealed.size(); ++k) {
-      auto ins = cache_.try_emplace(keys[sealed[k].first]);
+      const std::string& key = keys[sealed[k].first];
+      if (lfu_) {
+        if (offered[sealed[k].first] || cache_.count(key)) continue;
+        offered[sealed[k].first] = 1;
+        if (!admit(key)) continue;
+      }
+      auto ins = cache_.try_emplace(key);
       if (!ins.second) continue;  // sealed already
       lru_.push_front(&ins.first->first);
       ins.first->second = Entry{sealed[k].second, lru_.begin()};
@@ -452,6 +501,7 @@ int BlockStore::insert_slots(const std::vector<std::string>& keys,
 
 bool BlockStore::cache_insert(const std::string& key, std::shared_ptr<SealedBlock> block) {
   std::lock_guard<std::mutex> lk(cache_mu_);
+  if (cache_.count(key) || !admit(key)) return false;
   auto ins = cache_.try_emplace(key);
   if (!ins.second) return false;
   lru_.push_front(&ins.first->first);
@@ -480,6 +530,7 @@ int BlockStore::lookup_many(const std::vector<std::string>& keys,
                        sep == std::string::npos ? keys[i].size() : keys[i].size() - sep - 1));
     }
     lru_.splice(lru_.begin(), lru_, it->second.pos);
+    if (lfu_) lfu_->incr(keys[i]);  // a hit is recorded (cache.rs:59-67)
     out->push_back(it->second.block);
   }
   return PF_OK;
@@ -1193,6 +1244,13 @@ struct pf_engine {
   std::atomic<uint64_t> load_failures{0};
   std::mutex disk_mu;
   std::unique_ptr<DiskTier> disk;  // declared after store: destroyed before it
+  // Pre-eviction monitor (storage.rs:646-688), when configured.
+  std::mutex policy_mu;  // serializes pf_engine_set_storage_policy
+  std::thread pre_evict;
+  std::mutex pre_mu;
+  std::condition_variable pre_cv;
+  bool pre_stop = false;
+  std::atomic<uint64_t> pre_evicted{0};
 };
 
 namespace {
@@ -1316,14 +1374,66 @@ int pf_engine_create(uint64_t pool_bytes, uint32_t pool_kind, uint32_t pinned_fl
   return PF_OK;
 }
 
+namespace {
+
+void stop_pre_evict(pf_engine* e) {
+  if (!e->pre_evict.joinable()) return;
+  {
+    std::lock_guard<std::mutex> lk(e->pre_mu);
+    e->pre_stop = true;
+  }
+  e->pre_cv.notify_all();
+  e->pre_evict.join();
+  e->pre_stop = false;
+}
+
+}  // namespace
+
 int pf_engine_destroy(pf_engine* e) {
   if (!e) return PF_OK;
+  stop_pre_evict(e);
   {
     std::unique_lock<std::shared_mutex> lk(e->mu);
     e->instances.clear();  // joins the workers after their queued loads
   }
   e->disk.reset();  // writes what is queued, then stops its threads
   delete e;
+  return PF_OK;
+}
+
+// storage.rs:43-111, 346-398 and cache.rs:33-47: admission sized by the
+// value-size hint, and the pre-eviction monitor's thread.
+int pf_engine_set_storage_policy(pf_engine* e, int lfu_admission, uint64_t value_size_hint,
+                                 int pre_evict, uint64_t threshold_bytes, uint64_t target_bytes,
+                                 uint32_t interval_ms) {
+  if (!e) return fail(PF_ERR_INVALID_ARGUMENT, "invalid argument: null engine");
+  if (pre_evict && interval_ms == 0)
+    return fail(PF_ERR_INVALID_ARGUMENT, "invalid argument: pre-eviction interval of 0 ms");
+  std::lock_guard<std::mutex> policy(e->policy_mu);
+  uint64_t used = 0, total = 0;
+  e->pool->usage(&used, &total);
+  const uint64_t per_value = value_size_hint ? value_size_hint : kLfuDefaultValueBytes;
+  e->store->set_admission(lfu_admission ? std::max<uint64_t>(1, total / per_value) : 0,
+                          std::random_device{}() ^ (uint64_t(std::random_device{}()) << 32));
+  stop_pre_evict(e);
+  if (pre_evict) {
+    e->pre_evict = std::thread([e, threshold_bytes, target_bytes, interval_ms]() {
+      std::unique_lock<std::mutex> lk(e->pre_mu);
+      for (;;) {
+        if (e->pre_cv.wait_for(lk, std::chrono::milliseconds(interval_ms),
+                               [e] { return e->pre_stop; }))
+          return;
+        uint64_t used_now = 0, total_now = 0;
+        e->pool->usage(&used_now, &total_now);
+        const uint64_t free_now = total_now > used_now ? total_now - used_now : 0;
+        if (free_now >= threshold_bytes) continue;
+        const uint64_t need = target_bytes > free_now ? target_bytes - free_now : 0;
+        lk.unlock();
+        e->pre_evicted += e->store->evict_bytes(need, nullptr);
+        lk.lock();
+      }
+    });
+  }
   return PF_OK;
 }
 
@@ -1907,6 +2017,8 @@ int pf_engine_stats_get(pf_engine* e, pf_engine_stats* out) {
   out->saved_bytes = e->saved_bytes.load();
   out->loaded_bytes = e->loaded_bytes.load();
   out->load_failures = e->load_failures.load();
+  out->admission_rejections = e->store->admission_rejections();
+  out->pre_evicted_blocks = e->pre_evicted.load();
   return PF_OK;
 }
 

@@ -19,6 +19,7 @@
 #include <vector>
 
 #include "pf_common.h"
+#include "pf_lfu.h"
 
 namespace pf {
 
@@ -92,7 +93,7 @@ class PinnedPool : public std::enable_shared_from_this<PinnedPool> {
 };
 
 // ---------------------------------------------------------------------------
-// Block store (storage.rs:136-687, without TinyLFU admission).
+// Block store (storage.rs:136-687; TinyLFU admission, cache.rs, opt-in).
 // ---------------------------------------------------------------------------
 // Host copy of one (block, slot): LayerBlock (storage.rs:249-310).
 struct LayerBlock {
@@ -197,8 +198,22 @@ class BlockStore {
   uint64_t evictions() const { return evictions_.load(std::memory_order_relaxed); }
   // Evicts up to max_blocks least-recently-used sealed blocks; the count.
   size_t evict_lru(size_t max_blocks);
+  // Evicts least-recently-used sealed blocks until their footprints add up
+  // to `bytes` or the cache is empty (storage.rs:610-644); the count, and
+  // the bytes in *freed.
+  size_t evict_bytes(uint64_t bytes, uint64_t* freed);
+  // TinyLFU admission (cache.rs:28-241) for a cache of `items` expected
+  // entries, its sketch's row hashes seeded from `seed`; 0 items turns it
+  // off (plain LRU inserts, the default here).  With it on, a newly sealed
+  // block, or one read back from disk, is recorded and then refused when
+  // its estimate is below that of the least recently used entry, and every
+  // lookup hit is recorded.
+  void set_admission(uint64_t items, uint64_t seed);
+  uint64_t admission_rejections() const { return rejections_.load(std::memory_order_relaxed); }
 
  private:
+  // Whether a key not in the cache enters it (caller holds cache_mu_).
+  bool admit(const std::string& key);
   std::shared_ptr<PinnedPool> pool_;
   std::mutex inflight_mu_;
   std::unordered_map<std::string, InflightBlock> inflight_;
@@ -208,6 +223,8 @@ class BlockStore {
   std::list<const std::string*> lru_;
   std::unordered_map<std::string, Entry> cache_;
   std::atomic<uint64_t> evictions_{0};  // written under cache_mu_, read without it
+  std::unique_ptr<TinyLfu> lfu_;        // under cache_mu_; null: admission off
+  std::atomic<uint64_t> rejections_{0};  // written under cache_mu_
   SealHook seal_hook_;
 };
 

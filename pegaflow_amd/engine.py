@@ -107,6 +107,20 @@ class PegaEngine:
         self._h = h.value
         self._name_arrays = {}  # tuple of layer names -> C array of their bytes
 
+    def set_storage_policy(self, lfu_admission: bool = False, value_size_hint: int = 0,
+                           pre_evict: bool = False, pre_evict_threshold: int = 5 << 30,
+                           pre_evict_target: int = 8 << 30,
+                           pre_evict_interval_ms: int = 100) -> None:
+        """The reference's StorageConfig (storage.rs:43-111;
+        pf_engine_set_storage_policy): TinyLFU admission of new blocks, its
+        sketch sized for pool / value_size_hint entries (0: 128 MiB per
+        value), and the pre-eviction monitor (evict least-recently-used
+        blocks while fewer than pre_evict_threshold bytes are free, until
+        pre_evict_target are).  Both off by default here."""
+        _raise(lib().pf_engine_set_storage_policy(
+            self._h, int(bool(lfu_admission)), value_size_hint, int(bool(pre_evict)),
+            pre_evict_threshold, pre_evict_target, pre_evict_interval_ms))
+
     def set_transfer_modes(self, save_mode: int = _lib.MODE_AUTO,
                            load_mode: int = _lib.MODE_AUTO) -> None:
         """Transfer modes of saves and loads (pf_engine_set_modes); the

@@ -223,9 +223,16 @@ class Server:
                  max_workers: int = 16, dfs_root: str | None = None,
                  dfs_quota: int = 50 << 30, dfs_io_threads: int = 4,
                  grpc_impl: str = "native",
-                 save_mode: int | None = None, load_mode: int | None = None):
+                 save_mode: int | None = None, load_mode: int | None = None,
+                 lfu_admission: bool = False, pre_evict: bool = False,
+                 pre_evict_threshold: int = 5 << 30, pre_evict_target: int = 8 << 30,
+                 pre_evict_interval_ms: int = 100):
         self.engine = engine or PegaEngine(pool_size=pool_size, host_pool=host_pool,
                                            unit_size_hint=unit_size_hint)
+        if lfu_admission or pre_evict:
+            self.engine.set_storage_policy(lfu_admission, unit_size_hint, pre_evict,
+                                           pre_evict_threshold, pre_evict_target,
+                                           pre_evict_interval_ms)
         if dfs_root:
             self.engine.enable_disk(dfs_root, quota_bytes=dfs_quota, io_threads=dfs_io_threads)
         if save_mode is not None or load_mode is not None:
@@ -283,7 +290,8 @@ def parse_args(argv=None):
     ap.add_argument("--device", type=int, default=0)
     ap.add_argument("--pool-size", type=parse_memory_size, default=parse_memory_size("30gb"))
     ap.add_argument("--hint-value-size", type=parse_memory_size, default=0,
-                    help="allocation unit of the pinned pool")
+                    help="allocation unit of the pinned pool, and the value size TinyLFU "
+                         "admission is sized for (128 MiB when not given)")
     ap.add_argument("--log-level", default="info")
     ap.add_argument("--max-workers", type=int, default=16,
                     help="worker threads of the python gRPC server")
@@ -306,14 +314,21 @@ def parse_args(argv=None):
                          "sidecar files next to the packed files, so Redis itself is not used")
     ap.add_argument("--dfs-scan-interval-ms", type=int, default=100,
                     help="accepted for compatibility (quota is enforced after every write)")
-    # Reference options for parts this server does not have.
-    ap.add_argument("--use-hugepages", action="store_true")
-    ap.add_argument("--pre-evict", action="store_true")
+    ap.add_argument("--pre-evict", action="store_true",
+                    help="evict least-recently-used blocks in the background while fewer than "
+                         "--pre-evict-threshold bytes of the pool are free")
     ap.add_argument("--pre-evict-threshold", type=parse_memory_size,
                     default=parse_memory_size("5gb"))
     ap.add_argument("--pre-evict-target", type=parse_memory_size, default=parse_memory_size("8gb"))
     ap.add_argument("--pre-evict-interval-ms", type=int, default=100)
-    ap.add_argument("--disable-lfu-admission", action="store_true")
+    ap.add_argument("--lfu-admission", action="store_true",
+                    help="TinyLFU admission of new blocks, as the reference's server runs by "
+                         "default (off here: sized for 128 MiB values, it refuses blocks by "
+                         "sketch collisions; see --hint-value-size)")
+    ap.add_argument("--disable-lfu-admission", action="store_true",
+                    help="accepted for compatibility: admission is off unless --lfu-admission")
+    # Reference options for parts this server does not have.
+    ap.add_argument("--use-hugepages", action="store_true")
     ap.add_argument("--metrics-otel-endpoint", default="http://127.0.0.1:4321")
     ap.add_argument("--metrics-period-secs", type=int, default=5)
     args = ap.parse_args(argv)
@@ -328,8 +343,6 @@ def unsupported_options(args) -> list[str]:
     if args.use_hugepages:
         out.append("--use-hugepages: the pool is hipHostMalloc memory (registering existing "
                    "huge pages is refused on this platform)")
-    if args.pre_evict:
-        out.append("--pre-evict: blocks are evicted on demand when an allocation does not fit")
     return out
 
 
@@ -346,7 +359,11 @@ def main(argv=None) -> int:
                     dfs_quota=args.dfs_quota, dfs_io_threads=args.dfs_io_threads,
                     grpc_impl=args.grpc_impl,
                     save_mode=_lib.MODE_NAMES[args.save_mode],
-                    load_mode=_lib.MODE_NAMES[args.load_mode]).start()
+                    load_mode=_lib.MODE_NAMES[args.load_mode],
+                    lfu_admission=args.lfu_admission and not args.disable_lfu_admission,
+                    pre_evict=args.pre_evict, pre_evict_threshold=args.pre_evict_threshold,
+                    pre_evict_target=args.pre_evict_target,
+                    pre_evict_interval_ms=args.pre_evict_interval_ms).start()
     for sig in (signal.SIGINT, signal.SIGTERM):
         signal.signal(sig, lambda *_: server.service.shutdown_event.set())
     print(f"READY {server.addr}", flush=True)

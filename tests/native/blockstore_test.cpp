@@ -15,7 +15,14 @@
 //      made ahead (prepare_whole + stage_nodes, as a save does while its
 //      copy runs): a fresh key, a key sealed meanwhile, a key an earlier call
 //      left in flight, a key named twice; then the recency order those
-//      blocks took, read through eviction.
+//      blocks took, read through eviction;
+//   7. TinyLFU admission (cache.rs:71-95): a new key colder than the least
+//      recently used entry is refused, one as warm is let in, lookup hits
+//      warm a key, blocks read back from disk go through it too, and with
+//      admission off every key enters;
+//   8. eviction by bytes (storage.rs:610-644, the pre-eviction monitor's
+//      step): least recently used blocks until their footprints reach the
+//      request.
 // Exit status 0 and "ok" on success; the first failed check is printed.
 #include <cstdio>
 #include <cstdlib>
@@ -177,6 +184,56 @@ int main() {
            "the staged and completed blocks are the most recent");
     expect(store.evict_lru(1) == 1 && !store.peek(k6[0]) && store.peek(k6[3]),
            "key 10, staged first, is the older of the staged two");
+  }
+  // 7. Admission, on a store of its own.
+  {
+    BlockStore lfu(pool);
+    lfu.set_admission(1000, 7);  // a wide sketch: no collisions among these keys
+    std::vector<std::string> k7 = {key(20), key(21), key(22)};
+    std::vector<size_t> all = {0, 1, 2, 3};
+    auto seal = [&](uint32_t i, int call) {
+      auto e = entries_for(all, {i}, call);
+      return lfu.insert_slots(k7, all, e, total);
+    };
+    std::vector<std::shared_ptr<SealedBlock>> got;
+    expect(seal(0, 20) == PF_OK && lfu.sealed_count() == 1, "the first key enters an empty cache");
+    expect(lfu.lookup_many({k7[0]}, &got) == PF_OK && lfu.lookup_many({k7[0]}, &got) == PF_OK,
+           "two hits");
+    // Key 20 is the least recently used entry, recorded three times; key 21,
+    // recorded once, is colder: refused, and a lookup of it misses.
+    expect(seal(1, 21) == PF_OK && lfu.sealed_count() == 1 && lfu.admission_rejections() == 1,
+           "a colder key is refused");
+    expect(lfu.lookup_many({k7[1]}, &got) != PF_OK, "a refused key is not in the cache");
+    expect(lfu.inflight_count() == 0, "a refused block does not stay in flight");
+    // Offered again it is recorded again: twice is still colder, three
+    // times as warm as key 20 (3): let in.
+    expect(seal(1, 22) == PF_OK && lfu.sealed_count() == 1, "still colder");
+    expect(seal(1, 23) == PF_OK && lfu.sealed_count() == 2 && lfu.admission_rejections() == 2,
+           "as warm as the least recently used entry: let in");
+    // A block read back from disk is offered the same way.  Key 20 is now
+    // the least recently used entry (3 records); key 22 has none yet.
+    auto sb = std::make_shared<SealedBlock>();
+    sb->slots.resize(total);
+    expect(!lfu.cache_insert(k7[2], sb) && lfu.admission_rejections() == 3,
+           "a cold block from disk is refused");
+    lfu.set_admission(0, 0);
+    expect(lfu.cache_insert(k7[2], sb) && lfu.sealed_count() == 3, "admission off: it enters");
+  }
+  // 8. Eviction by bytes.  Every block of check 7's store layout holds four
+  // 64-byte slots (256 bytes of footprint).
+  {
+    BlockStore ev(pool);
+    std::vector<std::string> k8;
+    for (int i = 0; i < 6; ++i) k8.push_back(key(30 + i));
+    std::vector<size_t> all = {0, 1, 2, 3};
+    auto e = entries_for(all, {0, 1, 2, 3, 4, 5}, 30);
+    expect(ev.insert_slots(k8, all, e, total) == PF_OK && ev.sealed_count() == 6, "six blocks");
+    uint64_t freed = 0;
+    expect(ev.evict_bytes(600, &freed) == 3 && freed == 768, "three blocks free 768 >= 600 bytes");
+    expect(!ev.peek(k8[0]) && !ev.peek(k8[2]) && ev.peek(k8[3]), "the oldest three went");
+    expect(ev.evict_bytes(1 << 20, &freed) == 3 && freed == 768 && ev.sealed_count() == 0,
+           "a request past the cache empties it");
+    expect(ev.evict_bytes(0, &freed) == 0 && freed == 0, "nothing asked, nothing evicted");
   }
   if (failures) return 1;
   std::printf("ok\n");

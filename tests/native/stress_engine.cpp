@@ -4,8 +4,9 @@
 // A host-memory pool engine (no GPU, no HIP call) with a disk tier over packed
 // files written here: several threads query prefixes (starting prefetches that
 // allocate from a pool small enough to evict constantly), count prefixes, read
-// cached slots and check every byte, read statistics, and register and
-// unregister an instance, all at once.  Exit status 0 = every byte read back
+// cached slots and check every byte, read statistics, register and
+// unregister an instance, and turn TinyLFU admission and the pre-eviction
+// monitor on and off, all at once.  Exit status 0 = every byte read back
 // was right and the engine shut down cleanly; a sanitizer report fails the run
 // through its own exit code.
 #include <sys/stat.h>
@@ -186,6 +187,14 @@ int main(int argc, char** argv) {
     pf_engine_disk_stats(e, &ds);
     if (es.pool_used_bytes > es.pool_total_bytes) bad.fetch_add(1);
   }));
+  threads.emplace_back(until_stop([&, on = false]() mutable {  // storage policy churn
+    // TinyLFU admission and a 1 ms pre-eviction monitor (keeping 30 of the
+    // 40 blocks' room free once fewer than 20 are), on and off in turn.
+    on = !on;
+    if (pf_engine_set_storage_policy(e, on, 4096, on, 20 * kBlockBytes, 30 * kBlockBytes, 1))
+      bad.fetch_add(1);
+    std::this_thread::sleep_for(std::chrono::milliseconds(3));
+  }));
   threads.emplace_back(until_stop([&] {  // instance churn
     if (reg(e, "c") == PF_OK) {
       Hashes hs;
@@ -198,6 +207,7 @@ int main(int argc, char** argv) {
   std::this_thread::sleep_for(std::chrono::duration<double>(seconds));
   stop.store(true);
   for (auto& t : threads) t.join();
+  pf_engine_set_storage_policy(e, 0, 0, 0, 0, 0, 0);
   pf_engine_disk_wait_prefetch(e);
   pf_disk_stats ds{};
   pf_engine_disk_stats(e, &ds);

@@ -681,3 +681,94 @@ def test_pipelined_save_pool_exhausted_in_later_layer(gpu, save_mode):
     finally:
         m.close()
         e.close()
+
+
+def test_tinylfu_admission_refuses_colder_blocks(gpu):
+    """With TinyLFU admission on (set_storage_policy, cache.rs:71-95; a
+    sketch sized wide through the value-size hint), a batch saved after the
+    least recently used batch has been loaded twice is colder than it and is
+    refused: its hashes are not counted, loading them fails, and the
+    refusals are counted.  Saved twice more it is as warm and enters; every
+    byte it loads then equals the oracle's.  Admission off: a colder batch
+    enters at once."""
+    say("[gpu] engine TinyLFU admission")
+    e = PegaEngine(pool_size=64 * MiB)
+    m = Model(e, "lfu", 2, 64, 4096, seed=61)
+    try:
+        e.set_storage_policy(lfu_admission=True, value_size_hint=4096)
+        orig = m.host_copies()
+        a_ids, b_ids = [1, 2, 3], [10, 11, 12]
+        a_h, b_h = [h(i, b"lfuA") for i in a_ids], [h(i, b"lfuB") for i in b_ids]
+        e.batch_save_kv_blocks("lfu", 0, 0, [(n, a_ids, a_h) for n in m.names])
+        for _ in range(2):
+            st = PyLoadState()
+            e.batch_load_kv_blocks("lfu", 0, 0, st.shm_name(), m.names, [40, 41, 42], a_h)
+            assert wait(st) == 1
+        e.batch_save_kv_blocks("lfu", 0, 0, [(n, b_ids, b_h) for n in m.names])
+        assert e.count_prefix_hit_blocks("lfu", b_h) == 0
+        assert e.stats()["admission_rejections"] == 3
+        st = PyLoadState()
+        with pytest.raises(RuntimeError, match="missing KV block hash at index 0"):
+            e.batch_load_kv_blocks("lfu", 0, 0, st.shm_name(), m.names, [50, 51, 52], b_h)
+        assert st.get_state() == -1
+        # Recorded on every offer: the third offer is as warm as batch A.
+        e.batch_save_kv_blocks("lfu", 0, 0, [(n, b_ids, b_h) for n in m.names])
+        assert e.count_prefix_hit_blocks("lfu", b_h) == 0
+        e.batch_save_kv_blocks("lfu", 0, 0, [(n, b_ids, b_h) for n in m.names])
+        assert e.count_prefix_hit_blocks("lfu", b_h) == 3
+        assert e.stats()["admission_rejections"] == 6
+        st = PyLoadState()
+        e.batch_load_kv_blocks("lfu", 0, 0, st.shm_name(), m.names, [50, 51, 52], b_h)
+        assert wait(st) == 1
+        exp = expected_after_load(m, orig, a_ids, [40, 41, 42])
+        exp = expected_after_load(m, exp, b_ids, [50, 51, 52])
+        got = m.host_copies()
+        for l in range(m.n_layers):
+            assert np.array_equal(got[l], exp[l]), f"layer {l}"
+        # Admission off: a new, colder batch enters at once.
+        e.set_storage_policy(lfu_admission=False)
+        c_h = [h(i, b"lfuC") for i in b_ids]
+        e.batch_save_kv_blocks("lfu", 0, 0, [(n, b_ids, c_h) for n in m.names])
+        assert e.count_prefix_hit_blocks("lfu", c_h) == 3
+    finally:
+        e.close()
+        m.close()
+
+
+def test_pre_eviction_keeps_free_space(gpu):
+    """The pre-eviction monitor (storage.rs:646-688): once the pool's free
+    bytes fall below the threshold, it evicts least-recently-used blocks
+    until the target is free; the oldest batches go first and the newest
+    stays loadable."""
+    say("[gpu] engine pre-eviction")
+    e = PegaEngine(pool_size=8 * MiB)
+    m = Model(e, "pre", 2, 256, 4096, seed=62)
+    try:
+        # 8 batches of 16 blocks x 2 layers x 8 KiB = 256 KiB each: 2 MiB.
+        batches = [([b * 16 + i for i in range(16)], [h(b * 16 + i, b"pre") for i in range(16)])
+                   for b in range(8)]
+        for ids, hs in batches:
+            e.batch_save_kv_blocks("pre", 0, 0, [(n, ids, hs) for n in m.names])
+        s = e.stats()
+        free = s["pool_total_bytes"] - s["pool_used_bytes"]
+        assert s["sealed_blocks"] == 128 and free < 7 * MiB
+        e.set_storage_policy(pre_evict=True, pre_evict_threshold=7 * MiB,
+                             pre_evict_target=7 * MiB + 512 * 1024, pre_evict_interval_ms=10)
+        t0 = time.monotonic()
+        while e.stats()["pre_evicted_blocks"] == 0:
+            assert time.monotonic() - t0 < 10, "the monitor evicted nothing"
+            time.sleep(0.01)
+        time.sleep(0.05)
+        e.set_storage_policy()  # stops the monitor
+        s = e.stats()
+        assert s["pool_total_bytes"] - s["pool_used_bytes"] >= 7 * MiB + 512 * 1024
+        assert s["pre_evicted_blocks"] == s["evicted_blocks"] > 0
+        assert e.count_prefix_hit_blocks("pre", batches[0][1]) == 0
+        assert e.count_prefix_hit_blocks("pre", batches[-1][1]) == 16
+        st = PyLoadState()
+        e.batch_load_kv_blocks("pre", 0, 0, st.shm_name(), m.names,
+                               list(range(200, 216)), batches[-1][1])
+        assert wait(st) == 1
+    finally:
+        e.close()
+        m.close()

@@ -173,3 +173,18 @@ def test_load_errors_set_the_load_state(engine):
     assert st3.get_state() == 1
     with pytest.raises(RuntimeError, match="failed to open shared memory"):
         engine.batch_load_kv_blocks("i0", 0, 0, "pega_load_does_not_exist", ["l0"], [], [])
+
+
+def test_storage_policy_settings(engine):
+    """set_storage_policy (StorageConfig, storage.rs:43-111): admission and
+    the pre-eviction monitor turn on and off again; a monitor without an
+    interval is refused; the stats carry their counters (0 on an engine
+    that has stored nothing)."""
+    engine.set_storage_policy(lfu_admission=True, value_size_hint=4096)
+    engine.set_storage_policy(pre_evict=True, pre_evict_threshold=1 << 20,
+                              pre_evict_target=2 << 20, pre_evict_interval_ms=5)
+    with pytest.raises(RuntimeError, match="pre-eviction interval of 0 ms"):
+        engine.set_storage_policy(pre_evict=True, pre_evict_interval_ms=0)
+    engine.set_storage_policy()
+    s = engine.stats()
+    assert s["admission_rejections"] == 0 and s["pre_evicted_blocks"] == 0

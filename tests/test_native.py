@@ -85,10 +85,24 @@ def test_engine_stress_under_sanitizer(variant, tmp_path):
 
 
 @pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc is not installed")
+def test_tinylfu_sketch_rules():
+    """tests/native/lfu_test.cpp under AddressSanitizer+UBSan: the sketch's
+    sizing as cache.rs computes it, the count-min property against exact
+    counts, halving at the window's end, saturation at 255."""
+    exe = build("asan", "lfu_test")
+    env = dict(os.environ, **VARIANTS["asan"][1])
+    r = subprocess.run([exe], env=env, timeout=120, stdout=subprocess.PIPE,
+                       stderr=subprocess.STDOUT, text=True)
+    assert r.returncode == 0, r.stdout[-6000:]
+    assert r.stdout.strip().endswith("ok")
+
+
+@pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc is not installed")
 def test_block_store_sealing_rules():
     """tests/native/blockstore_test.cpp under AddressSanitizer+UBSan: whole
     calls, blocks completed across calls (first copies win), sealed blocks
-    not replaced, a key named twice, and a slot count mismatch."""
+    not replaced, a key named twice, a slot count mismatch, TinyLFU
+    admission and eviction by bytes."""
     exe = build("asan", "blockstore_test")
     env = dict(os.environ, **VARIANTS["asan"][1])
     r = subprocess.run([exe], env=env, timeout=120, stdout=subprocess.PIPE,

@@ -94,7 +94,10 @@ def test_cli_accepts_the_reference_launch_command():
     assert a.pool_size == 10 << 30 and a.hint_value_size == 64 << 10 and a.device == 1
     assert a.dfs_root == DEFAULT_DFS_ROOT and a.dfs_quota == 1 << 40
     notes = unsupported_options(a)
-    assert len(notes) == 2 and notes[0].startswith("--use-hugepages")
+    assert len(notes) == 1 and notes[0].startswith("--use-hugepages")
+    assert a.pre_evict and (a.pre_evict_threshold, a.pre_evict_target) == (1 << 30, 2 << 30)
+    assert a.disable_lfu_admission and not a.lfu_admission and not d.lfu_admission
+    assert parse_args(["--lfu-admission"]).lfu_admission
     assert parse_args(["--dfs-root", "/mnt/x"]).dfs_root == "/mnt/x"
 
 
