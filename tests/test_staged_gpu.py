@@ -634,6 +634,7 @@ def test_marked_slices_mixed_routes_vs_oracle(gpu):
     ctx.set_staged_slices(0, 64 * 1024)
     words = PinnedBuffer(8 * len(layers))
     try:
+        host.array[:] = 0  # gaps and empty layers' regions are never written
         ctx.save_layers([L.transfer(ids) for L, ids in zip(layers, save_ids)], _lib.MODE_STAGED)
         ctx.synchronize()
         for L in layers:
@@ -642,6 +643,81 @@ def test_marked_slices_mixed_routes_vs_oracle(gpu):
         for value in (21, 22):
             for i, (L, ids) in enumerate(zip(layers, load_ids)):
                 L.dev.fill_random(value * 100 + i)
+                L.ref[:] = L.dev.download()  # in place: the oracle's layout points here
+                L.oracle_load(ids)
+            words.array[:] = 0
+            ctx.load_layers_marked([L.transfer(ids) for L, ids in zip(layers, load_ids)],
+                                   [(words.ptr, value, True)], _lib.MODE_STAGED)
+            ctx.synchronize()
+            assert words.array.view(np.uint64).tolist() == [value] * len(layers)
+            for i, L in enumerate(layers):
+                assert np.array_equal(L.dev.download(), L.ref), f"load {value}: layer {i}"
+    finally:
+        for L in layers:
+            L.close()
+        host.close()
+        words.close()
+        ctx.close()
+
+
+def _fuzz_layers(rng, seed):
+    """1-20 layers of random kinds: split K/V of 16-byte aligned segments (the
+    common case), blocks-first single segments, padded K/V gaps, overlapping
+    K/V (copied in place, in list order) and unaligned segments; random save
+    and load ids (some layers empty)."""
+    specs = []
+    for _ in range(int(rng.integers(1, 21))):
+        nb = int(rng.integers(4, 64))
+        kind = rng.choice(["split", "split", "split", "single", "padded", "overlap", "unaligned"])
+        if kind == "unaligned":
+            bpb = int(rng.choice([24, 40, 72]))
+        else:
+            bpb = int(rng.choice([64, 256, 1024, 4096, 8192]))
+        if kind == "single":
+            shape = (nb, bpb, 1, 0, nb * bpb)
+        elif kind == "padded":
+            kv = nb * bpb + 16 * int(rng.integers(1, 9))
+            shape = (nb, bpb, 2, kv, kv + nb * bpb)
+        elif kind == "overlap":
+            kv = (nb * bpb) // 2
+            shape = (nb, bpb, 2, kv, kv + nb * bpb)
+        else:
+            shape = (nb, bpb, 2, nb * bpb, 2 * nb * bpb)
+        m = 0 if rng.random() < 0.1 else int(rng.integers(1, nb + 1))
+        save = rng.choice(nb, m, replace=False).tolist()
+        load = rng.choice(nb, m, replace=False).tolist()
+        specs.append((shape, save, load))
+    layers = [Layer(*shape, seed * 100 + i) for i, (shape, _, _) in enumerate(specs)]
+    return layers, [s for _, s, _ in specs], [l for _, _, l in specs]
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_staged_marked_fuzz_vs_oracle(gpu, seed):
+    """Seeded random calls through the staged mode with per-layer marks:
+    random layers (see _fuzz_layers) with random load slice caps from one
+    chunk to 256 KiB, so slices hold many layers, parts of layers, or a
+    chunk each, and their scatters mark layers themselves, across slices,
+    or leave them to the marking kernel.  After a staged save, two marked
+    loads (into refilled tensors) must set every layer's word and leave
+    every byte as the oracle does."""
+    rng = np.random.Generator(np.random.PCG64(4000 + seed))
+    layers, save_ids, load_ids = _fuzz_layers(rng, seed)
+    cap = int(rng.choice([1, 512, 4096, 16 * 1024, 64 * 1024, 256 * 1024]))
+    say(f"[gpu] staged marked fuzz seed={seed}: {len(layers)} layers, load slice cap {cap}")
+    host, ohost = _place_all(layers, save_ids, gap=16 * int(rng.integers(0, 3)))
+    ctx = TransferContext(0, staging_bytes=4 * MiB)
+    ctx.set_staged_slices(0, cap)
+    words = PinnedBuffer(8 * len(layers))
+    try:
+        host.array[:] = 0  # gaps and empty layers' regions are never written
+        ctx.save_layers([L.transfer(ids) for L, ids in zip(layers, save_ids)], _lib.MODE_STAGED)
+        ctx.synchronize()
+        for L in layers:
+            L.oracle_save()
+        assert np.array_equal(host.array, ohost), "host regions differ from the oracle"
+        for value in (31, 32):
+            for i, (L, ids) in enumerate(zip(layers, load_ids)):
+                L.dev.fill_random(seed * 1000 + value * 50 + i)
                 L.ref[:] = L.dev.download()  # in place: the oracle's layout points here
                 L.oracle_load(ids)
             words.array[:] = 0
