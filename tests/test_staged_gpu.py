@@ -691,26 +691,29 @@ def _fuzz_layers(rng, seed):
     return layers, [s for _, s, _ in specs], [l for _, _, l in specs]
 
 
+@pytest.mark.parametrize("mode", ["staged", "kernel", "auto"])
 @pytest.mark.parametrize("seed", range(8))
-def test_staged_marked_fuzz_vs_oracle(gpu, seed):
-    """Seeded random calls through the staged mode with per-layer marks:
-    random layers (see _fuzz_layers) with random load slice caps from one
-    chunk to 256 KiB, so slices hold many layers, parts of layers, or a
-    chunk each, and their scatters mark layers themselves, across slices,
-    or leave them to the marking kernel.  After a staged save, two marked
-    loads (into refilled tensors) must set every layer's word and leave
-    every byte as the oracle does."""
+def test_staged_marked_fuzz_vs_oracle(gpu, seed, mode):
+    """Seeded random calls with per-layer marks: random layers (see
+    _fuzz_layers) with random load slice caps from one chunk to 256 KiB.  In
+    the staged mode slices hold many layers, parts of layers, or a chunk
+    each, and their scatters mark layers themselves, across slices, or leave
+    them to the marking kernel; the kernel mode marks from inside its
+    launches; AUTO picks either per call.  After a save in the same mode,
+    two marked loads (into refilled tensors) must set every layer's word and
+    leave every byte as the oracle does."""
     rng = np.random.Generator(np.random.PCG64(4000 + seed))
     layers, save_ids, load_ids = _fuzz_layers(rng, seed)
     cap = int(rng.choice([1, 512, 4096, 16 * 1024, 64 * 1024, 256 * 1024]))
-    say(f"[gpu] staged marked fuzz seed={seed}: {len(layers)} layers, load slice cap {cap}")
+    say(f"[gpu] marked fuzz seed={seed} mode={mode}: {len(layers)} layers, load slice cap {cap}")
+    m = _lib.MODE_NAMES[mode]
     host, ohost = _place_all(layers, save_ids, gap=16 * int(rng.integers(0, 3)))
     ctx = TransferContext(0, staging_bytes=4 * MiB)
     ctx.set_staged_slices(0, cap)
     words = PinnedBuffer(8 * len(layers))
     try:
         host.array[:] = 0  # gaps and empty layers' regions are never written
-        ctx.save_layers([L.transfer(ids) for L, ids in zip(layers, save_ids)], _lib.MODE_STAGED)
+        ctx.save_layers([L.transfer(ids) for L, ids in zip(layers, save_ids)], m)
         ctx.synchronize()
         for L in layers:
             L.oracle_save()
@@ -722,7 +725,7 @@ def test_staged_marked_fuzz_vs_oracle(gpu, seed):
                 L.oracle_load(ids)
             words.array[:] = 0
             ctx.load_layers_marked([L.transfer(ids) for L, ids in zip(layers, load_ids)],
-                                   [(words.ptr, value, True)], _lib.MODE_STAGED)
+                                   [(words.ptr, value, True)], m)
             ctx.synchronize()
             assert words.array.view(np.uint64).tolist() == [value] * len(layers)
             for i, L in enumerate(layers):
