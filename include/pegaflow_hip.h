@@ -500,8 +500,13 @@ int pf_load_layers_noalloc(pf_stream stream, const pf_layer_xfer* layers,
  * launch covers every such layer (two for a large call, whose first eighth
  * of layers is launched before the rest is planned) and its last workgroup
  * on layer l writes the marks of layer l.  Layers loaded from device memory (an
- * HBM-bound copy) get one launch each, followed by their marks; DMA and
- * staged copies are marked after each layer's copies.
+ * HBM-bound copy) get one launch each, followed by their marks; DMA copies
+ * are marked after each layer's copies.  In PF_MODE_STAGED (and AUTO when it
+ * stages) each slice's scatter marks the layers it completes, counting a
+ * layer's tiles over the slices that hold it, so a layer lands after one
+ * kernel; layers in slices that cannot carry them (more than 8 layers,
+ * unaligned chunks) are marked by a separate kernel after their last
+ * slice. 
  *
  * A signal target is an array of one 8-byte word per layer of the call:
  * words + 8*l is set to `value` once layer l's bytes are in place.  The
