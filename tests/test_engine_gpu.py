@@ -772,3 +772,29 @@ def test_pre_eviction_keeps_free_space(gpu):
     finally:
         e.close()
         m.close()
+
+
+def test_engine_on_cu_masked_contexts(gpu, monkeypatch):
+    """PEGAFLOW_CUS_PER_XCD masks the contexts the engine creates: a save
+    and a layer-by-layer load through them (staged, each slice's scatter on
+    2 CUs per XCD) equal the oracle, every layer published."""
+    say("[gpu] engine on CU-masked contexts")
+    monkeypatch.setenv("PEGAFLOW_CUS_PER_XCD", "2")
+    e = PegaEngine(pool_size=64 * MiB)
+    m = Model(e, "cum", 4, 256, 8192, seed=63)
+    try:
+        orig = m.host_copies()
+        ids = list(range(0, 200, 3))
+        targets = list(range(1, 200, 3))
+        hashes = [h(i, b"cum") for i in ids]
+        e.batch_save_kv_blocks("cum", 0, 0, [(n, ids, hashes) for n in m.names])
+        st = PyLoadState(num_layers=m.n_layers)
+        e.batch_load_kv_blocks("cum", 0, 0, st.shm_name(), m.names, targets, hashes)
+        assert wait(st) == 1 and st.layers_done() == m.n_layers
+        exp = expected_after_load(m, orig, ids, targets)
+        got = m.host_copies()
+        for l in range(m.n_layers):
+            assert np.array_equal(got[l], exp[l]), f"layer {l}"
+    finally:
+        e.close()
+        m.close()
