@@ -222,6 +222,16 @@ constexpr size_t kReclaimBatch = 64;  // storage.rs:41
 constexpr uint64_t kLfuDefaultValueBytes = 128ull << 20;
 }
 
+// Evicted blocks return their memory to the pool as their handles drop,
+// after the cache lock is released.  Until then `releasing_` counts the
+// eviction, so an allocation that finds the cache empty meanwhile waits for
+// that memory instead of reporting the pool exhausted.
+void BlockStore::drop_evicted(std::vector<std::shared_ptr<SealedBlock>>* dropped) {
+  if (dropped->empty()) return;
+  dropped->clear();
+  releasing_.fetch_sub(1, std::memory_order_release);
+}
+
 size_t BlockStore::evict_lru(size_t max_blocks) {
   std::vector<std::shared_ptr<SealedBlock>> dropped;
   {
@@ -233,8 +243,11 @@ size_t BlockStore::evict_lru(size_t max_blocks) {
       cache_.erase(it);
     }
     evictions_ += dropped.size();
+    if (!dropped.empty()) releasing_.fetch_add(1, std::memory_order_relaxed);
   }
-  return dropped.size();  // memory returns to the pool as the handles drop here
+  const size_t n = dropped.size();
+  drop_evicted(&dropped);
+  return n;
 }
 
 size_t BlockStore::evict_bytes(uint64_t bytes, uint64_t* freed) {
@@ -250,9 +263,12 @@ size_t BlockStore::evict_bytes(uint64_t bytes, uint64_t* freed) {
       cache_.erase(it);
     }
     evictions_ += dropped.size();
+    if (!dropped.empty()) releasing_.fetch_add(1, std::memory_order_relaxed);
   }
+  const size_t n = dropped.size();
+  drop_evicted(&dropped);
   if (freed) *freed = total;
-  return dropped.size();
+  return n;
 }
 
 void BlockStore::set_admission(uint64_t items, uint64_t seed) {
@@ -280,7 +296,16 @@ std::shared_ptr<PoolAllocation> BlockStore::allocate(uint64_t size) {
       if (evict_lru(kReclaimBatch) == 0) break;
       largest = pool_->largest_free();
     }
-    if (largest < size) return nullptr;
+    if (largest >= size) continue;
+    // The cache is empty.  Another thread's eviction (the pre-eviction
+    // monitor, another save) may still be returning memory: wait for it.
+    // Once none is, whatever they returned is visible to one more attempt;
+    // memory still taken is held by loads or saves in progress.
+    if (releasing_.load(std::memory_order_acquire) > 0) {
+      std::this_thread::yield();
+      continue;
+    }
+    return pool_->allocate(size);
   }
 }
 

@@ -146,7 +146,9 @@ class BlockStore {
   // A sealed block without touching its recency (inspection).
   std::shared_ptr<SealedBlock> peek(const std::string& key);
   // Allocation with eviction of least-recently-used sealed blocks in batches
-  // of 64 until the largest free region fits (storage.rs:405-433).
+  // of 64 until the largest free region fits (storage.rs:405-433).  With the
+  // cache empty it waits for memory that other threads' evictions are still
+  // returning; null when the rest is held by loads and saves in progress.
   std::shared_ptr<PoolAllocation> allocate(uint64_t size);
   bool cache_contains(const std::string& key);
   // The layers of one save that share a hash list, with one lookup per key
@@ -214,6 +216,9 @@ class BlockStore {
  private:
   // Whether a key not in the cache enters it (caller holds cache_mu_).
   bool admit(const std::string& key);
+  // Drops an eviction's blocks (their memory returns to the pool) and ends
+  // its count in releasing_.
+  void drop_evicted(std::vector<std::shared_ptr<SealedBlock>>* dropped);
   std::shared_ptr<PinnedPool> pool_;
   std::mutex inflight_mu_;
   std::unordered_map<std::string, InflightBlock> inflight_;
@@ -225,6 +230,9 @@ class BlockStore {
   std::atomic<uint64_t> evictions_{0};  // written under cache_mu_, read without it
   std::unique_ptr<TinyLfu> lfu_;        // under cache_mu_; null: admission off
   std::atomic<uint64_t> rejections_{0};  // written under cache_mu_
+  // Evictions whose blocks are out of the cache but whose memory may not
+  // be back in the pool yet (raised under cache_mu_).
+  std::atomic<uint32_t> releasing_{0};
   SealHook seal_hook_;
 };
 

@@ -22,11 +22,16 @@
 //      admission off every key enters;
 //   8. eviction by bytes (storage.rs:610-644, the pre-eviction monitor's
 //      step): least recently used blocks until their footprints reach the
-//      request.
+//      request;
+//   9. allocation racing a monitor thread's evictions: no allocation fails
+//      while memory the monitor took out of the cache is still returning.
 // Exit status 0 and "ok" on success; the first failed check is printed.
+#include <atomic>
+#include <chrono>
 #include <cstdio>
 #include <cstdlib>
 #include <memory>
+#include <thread>
 #include <string>
 #include <vector>
 
@@ -234,6 +239,74 @@ int main() {
     expect(ev.evict_bytes(1 << 20, &freed) == 3 && freed == 768 && ev.sealed_count() == 0,
            "a request past the cache empties it");
     expect(ev.evict_bytes(0, &freed) == 0 && freed == 0, "nothing asked, nothing evicted");
+  }
+  // 9. Eviction racing allocation.  A saver thread fills a pool of its own
+  // with sealed blocks (eight 8 KiB blocks sharing one 64 KiB allocation
+  // per call), while a monitor thread, as the pre-eviction monitor does,
+  // evicts whenever little is free.  Nothing but the cache and the saver's
+  // own current allocation holds pool memory, so every allocation must
+  // succeed, including one made while the monitor is still returning the
+  // memory of blocks it has just taken out of the cache; and once the
+  // cache is emptied, no memory may stay in use.  Run with admission off
+  // and on (refused blocks must return their memory too).
+  for (int lfu_on = 0; lfu_on < 2; ++lfu_on) {
+    std::shared_ptr<PinnedPool> small;
+    if (PinnedPool::create(1 << 20, 0, false, 0, &small)) {
+      std::printf("FAILED: pool: %s\n", pf_last_error());
+      return 1;
+    }
+    BlockStore race(small);
+    if (lfu_on) race.set_admission(128, 9);
+    std::atomic<bool> stop{false};
+    std::atomic<uint64_t> failed{0}, calls{0}, monitor_evicted{0};
+    std::thread monitor([&] {
+      while (!stop.load()) {
+        uint64_t used = 0, total_bytes = 0;
+        small->usage(&used, &total_bytes);
+        if (total_bytes - used < (128u << 10)) monitor_evicted += race.evict_bytes(~0ull, nullptr);
+      }
+    });
+    std::vector<size_t> one = {0};
+    std::vector<std::shared_ptr<SealedBlock>> hits;
+    const auto until = std::chrono::steady_clock::now() + std::chrono::milliseconds(1000);
+    for (uint32_t call = 0; std::chrono::steady_clock::now() < until; ++call) {
+      auto a = race.allocate(64u << 10);
+      if (!a) {
+        ++failed;
+        continue;
+      }
+      std::vector<std::string> keys;
+      std::vector<BlockStore::SlotEntries> e(1);
+      for (uint32_t i = 0; i < 8; ++i) {
+        keys.push_back(key(1000000 + static_cast<int>(call * 8 + i)));
+        auto b = std::make_shared<LayerBlock>();
+        b->k_ptr = a->ptr + i * (8u << 10);
+        b->size = 8u << 10;
+        b->k_alloc = a;
+        e[0].emplace_back(i, std::move(b));
+      }
+      a.reset();
+      if (race.insert_slots(keys, one, e, 1) != PF_OK) ++failed;
+      // Some hits, so admission has warm entries to weigh new keys against.
+      if (call % 3 == 0) (void)race.lookup_many({keys[0]}, &hits);
+      hits.clear();
+      ++calls;
+    }
+    stop = true;
+    monitor.join();
+    race.evict_bytes(~0ull, nullptr);
+    uint64_t used = 0, total_bytes = 0;
+    small->usage(&used, &total_bytes);
+    std::printf("eviction race (admission %s): %llu calls, %llu blocks evicted by the monitor, "
+                "%llu refused, %llu failed, %llu bytes in use after evicting everything\n",
+                lfu_on ? "on" : "off", (unsigned long long)calls.load(),
+                (unsigned long long)monitor_evicted.load(),
+                (unsigned long long)race.admission_rejections(),
+                (unsigned long long)failed.load(), (unsigned long long)used);
+    expect(calls.load() > 1000 && monitor_evicted.load() > 0, "the race ran");
+    expect(!lfu_on || race.admission_rejections() > 0, "admission refused some blocks");
+    expect(failed.load() == 0, "no allocation fails while evicted memory is returning");
+    expect(used == 0, "every evicted or refused block returned its memory");
   }
   if (failures) return 1;
   std::printf("ok\n");

@@ -5,14 +5,15 @@ loader threads restore recently sealed batches into disjoint target blocks
 of a second instance (plain and layered LoadStates alternating) and a query
 thread counts prefix hits.  The pool holds only a few batches, so eviction
 runs all the time.  It runs with the zero-copy kernels both ways, with saves
-staged on the copy engines beside kernel loads, and with both directions
-staged.
+staged on the copy engines beside kernel loads, with both directions staged,
+and in the engine's default modes with TinyLFU admission and the
+pre-eviction monitor on.
 
 Every load that succeeds must leave its targets holding exactly the source
 blocks' words, checked in closed form on the device.  A load that names a
 hash already evicted must fail cleanly (an error from the call or a -1
 LoadState), never with wrong bytes.  The engine's stats must add up at the
-end.
+end, and once every block is evicted the pool must be empty.
 """
 
 import hashlib
@@ -76,19 +77,30 @@ def check_targets(dst, src, sources, targets):
     return bad
 
 
-# (save mode, load mode): the zero-copy kernels both ways; saves staged on the
-# copy engines beside kernel loads; both directions staged.
-MODES = [("kernel", "kernel"), ("staged", "kernel"), ("staged", "staged")]
+# (save mode, load mode, storage policy): the zero-copy kernels both ways;
+# saves staged on the copy engines beside kernel loads; both directions
+# staged; and AUTO both ways with TinyLFU admission and a pre-eviction
+# monitor that wakes every millisecond, so blocks are refused and dropped
+# by a thread of the engine's own while loads hold them.
+MODES = [("kernel", "kernel", False), ("staged", "kernel", False), ("staged", "staged", False),
+         ("auto", "auto", True)]
 
 
-@pytest.mark.parametrize("save_mode,load_mode", MODES)
-def test_concurrent_saves_loads_and_queries(gpu, save_mode, load_mode):
-    say(f"[gpu] engine concurrency ({save_mode} saves, {load_mode} loads): saver, two loaders, "
-        "a query thread, constant eviction")
+@pytest.mark.parametrize("save_mode,load_mode,policy", MODES,
+                         ids=[f"{a}-{b}{'-policy' if c else ''}" for a, b, c in MODES])
+def test_concurrent_saves_loads_and_queries(gpu, save_mode, load_mode, policy):
+    say(f"[gpu] engine concurrency ({save_mode} saves, {load_mode} loads, storage policy "
+        f"{'on' if policy else 'off'}): saver, two loaders, a query thread, constant eviction")
     n_layers, nb, bpb, per_batch = 8, 512, 16384, 32
     batch_bytes = n_layers * per_batch * 2 * bpb  # 8 MiB
     e = PegaEngine(pool_size=6 * batch_bytes)      # room for about 6 batches
     e.set_transfer_modes(_lib.MODE_NAMES[save_mode], _lib.MODE_NAMES[load_mode])
+    if policy:
+        # Admission sized for one entry per block; the monitor keeps two
+        # batches' bytes free once fewer than one batch's are.
+        e.set_storage_policy(lfu_admission=True, value_size_hint=n_layers * 2 * bpb,
+                             pre_evict=True, pre_evict_threshold=batch_bytes,
+                             pre_evict_target=2 * batch_bytes, pre_evict_interval_ms=1)
     src = Layers(n_layers, nb, bpb, seed=3)
     dst = Layers(n_layers, nb, bpb, seed=4)
     src.register(e, "prefill")
@@ -190,6 +202,22 @@ def test_concurrent_saves_loads_and_queries(gpu, save_mode, load_mode):
         say(f"[gpu] concurrency: {stats}; engine {s}")
         assert stats["saves"] >= 10 and stats["loads_ok"] >= 10, stats
         assert s["evicted_blocks"] > 0, "the pool never filled"
+        if policy:
+            assert s["pre_evicted_blocks"] > 0, "the monitor never ran"
+            assert s["pre_evicted_blocks"] <= s["evicted_blocks"]
+        # With every block evicted (a monitor asked to free more than the
+        # pool holds, then stopped), nothing may keep pool memory.
+        everything = s["pool_total_bytes"] + 1
+        e.set_storage_policy(pre_evict=True, pre_evict_threshold=everything,
+                             pre_evict_target=everything, pre_evict_interval_ms=1)
+        t0 = time.monotonic()
+        while e.stats()["sealed_blocks"] and time.monotonic() - t0 < 10:
+            time.sleep(0.005)
+        e.set_storage_policy()  # joins the monitor
+        s = e.stats()
+        say(f"[gpu] after evicting everything: {s}")
+        assert s["sealed_blocks"] == 0 and s["inflight_blocks"] == 0, s
+        assert s["pool_used_bytes"] == 0, s
         assert s["load_failures"] == 0
         assert s["pool_used_bytes"] <= s["pool_total_bytes"]
         assert s["loaded_bytes"] == stats["loads_ok"] * n_layers * 16 * 2 * bpb

@@ -98,13 +98,15 @@ def test_tinylfu_sketch_rules():
 
 
 @pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc is not installed")
-def test_block_store_sealing_rules():
-    """tests/native/blockstore_test.cpp under AddressSanitizer+UBSan: whole
-    calls, blocks completed across calls (first copies win), sealed blocks
-    not replaced, a key named twice, a slot count mismatch, TinyLFU
-    admission and eviction by bytes."""
-    exe = build("asan", "blockstore_test")
-    env = dict(os.environ, **VARIANTS["asan"][1])
+@pytest.mark.parametrize("variant", sorted(VARIANTS))
+def test_block_store_sealing_rules(variant):
+    """tests/native/blockstore_test.cpp under AddressSanitizer+UBSan and
+    under ThreadSanitizer: whole calls, blocks completed across calls (first
+    copies win), sealed blocks not replaced, a key named twice, a slot count
+    mismatch, TinyLFU admission, eviction by bytes, and allocations racing a
+    monitor thread's evictions."""
+    exe = build(variant, "blockstore_test")
+    env = dict(os.environ, **VARIANTS[variant][1])
     r = subprocess.run([exe], env=env, timeout=120, stdout=subprocess.PIPE,
                        stderr=subprocess.STDOUT, text=True)
     assert r.returncode == 0, r.stdout[-6000:]
