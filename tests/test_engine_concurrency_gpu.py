@@ -1,8 +1,9 @@
 """PegaEngine under concurrent use on the GPU.
 
-A saver thread keeps sealing new batches of one instance's blocks while two
-loader threads restore recently sealed batches into disjoint target blocks
-of a second instance (plain and layered LoadStates alternating) and a query
+Two saver threads keep sealing new batches of blocks, each from an instance
+of its own (two save workers evicting from one pool), while two loader
+threads restore recently sealed batches into disjoint target blocks of a
+third instance (plain and layered LoadStates alternating) and a query
 thread counts prefix hits.  The pool holds only a few batches, so eviction
 runs all the time.  It runs with the zero-copy kernels both ways, with saves
 staged on the copy engines beside kernel loads, with both directions staged,
@@ -90,7 +91,7 @@ MODES = [("kernel", "kernel", False), ("staged", "kernel", False), ("staged", "s
                          ids=[f"{a}-{b}{'-policy' if c else ''}" for a, b, c in MODES])
 def test_concurrent_saves_loads_and_queries(gpu, save_mode, load_mode, policy):
     say(f"[gpu] engine concurrency ({save_mode} saves, {load_mode} loads, storage policy "
-        f"{'on' if policy else 'off'}): saver, two loaders, a query thread, constant eviction")
+        f"{'on' if policy else 'off'}): two savers, two loaders, a query thread, constant eviction")
     n_layers, nb, bpb, per_batch = 8, 512, 16384, 32
     batch_bytes = n_layers * per_batch * 2 * bpb  # 8 MiB
     e = PegaEngine(pool_size=6 * batch_bytes)      # room for about 6 batches
@@ -101,27 +102,29 @@ def test_concurrent_saves_loads_and_queries(gpu, save_mode, load_mode, policy):
         e.set_storage_policy(lfu_admission=True, value_size_hint=n_layers * 2 * bpb,
                              pre_evict=True, pre_evict_threshold=batch_bytes,
                              pre_evict_target=2 * batch_bytes, pre_evict_interval_ms=1)
-    src = Layers(n_layers, nb, bpb, seed=3)
+    srcs = [Layers(n_layers, nb, bpb, seed=3), Layers(n_layers, nb, bpb, seed=5)]
     dst = Layers(n_layers, nb, bpb, seed=4)
-    src.register(e, "prefill")
+    for k, src in enumerate(srcs):
+        src.register(e, f"prefill{k}")
     dst.register(e, "decode")
-    sealed = []            # (batch, source block ids), in sealing order
+    sealed = []            # (saver, batch, source block ids), in sealing order
     lock = threading.Lock()
     stop = threading.Event()
     errors = []
     stats = {"saves": 0, "loads_ok": 0, "loads_missing": 0, "queries": 0, "words_checked": 0}
 
-    def saver():
-        rng = random.Random(1)
-        batch = 0
+    def saver(k):
+        rng = random.Random(1 + k)
+        src = srcs[k]
+        batch = k  # saver k's batches are k, k + 2, ...: hashes differ between savers
         while not stop.is_set():
             ids = rng.sample(range(nb), per_batch)
             hashes = [h(batch, i) for i in ids]
-            e.batch_save_kv_blocks("prefill", 0, 0, [(n, ids, hashes) for n in src.names])
+            e.batch_save_kv_blocks(f"prefill{k}", 0, 0, [(n, ids, hashes) for n in src.names])
             with lock:
-                sealed.append((batch, ids))
+                sealed.append((k, batch, ids))
                 stats["saves"] += 1
-            batch += 1
+            batch += 2
 
     def loader(k):
         rng = random.Random(10 + k)
@@ -134,7 +137,7 @@ def test_concurrent_saves_loads_and_queries(gpu, save_mode, load_mode, policy):
             if not recent:
                 time.sleep(0.001)
                 continue
-            batch, ids = rng.choice(recent)
+            ks, batch, ids = rng.choice(recent)
             pick = rng.sample(range(per_batch), 16)
             sources = [ids[j] for j in pick]
             hashes = [h(batch, i) for i in sources]
@@ -156,7 +159,7 @@ def test_concurrent_saves_loads_and_queries(gpu, save_mode, load_mode, policy):
             assert st.get_state() == 1
             if n % 2 == 0:  # layered state: every layer was published
                 assert st.layers_done() == n_layers
-            bad = check_targets(dst, src, sources, targets)
+            bad = check_targets(dst, srcs[ks], sources, targets)
             assert bad == 0, f"loader {k}: {bad} mismatching words (batch {batch})"
             with lock:
                 stats["loads_ok"] += 1
@@ -166,8 +169,8 @@ def test_concurrent_saves_loads_and_queries(gpu, save_mode, load_mode, policy):
         while not stop.is_set():
             with lock:
                 recent = sealed[-8:]
-            for batch, ids in recent:
-                hits = e.count_prefix_hit_blocks("prefill", [h(batch, i) for i in ids])
+            for ks, batch, ids in recent:
+                hits = e.count_prefix_hit_blocks(f"prefill{ks}", [h(batch, i) for i in ids])
                 assert 0 <= hits <= per_batch
             with lock:
                 stats["queries"] += 1
@@ -180,7 +183,8 @@ def test_concurrent_saves_loads_and_queries(gpu, save_mode, load_mode, policy):
             errors.append(err)
             stop.set()
 
-    threads = [threading.Thread(target=guard, args=(saver,)),
+    threads = [threading.Thread(target=guard, args=(saver, 0)),
+               threading.Thread(target=guard, args=(saver, 1)),
                threading.Thread(target=guard, args=(loader, 0)),
                threading.Thread(target=guard, args=(loader, 1)),
                threading.Thread(target=guard, args=(querier,))]
@@ -224,5 +228,6 @@ def test_concurrent_saves_loads_and_queries(gpu, save_mode, load_mode, policy):
     finally:
         stop.set()
         e.close()
-        src.close()
+        for src in srcs:
+            src.close()
         dst.close()
