@@ -1,0 +1,209 @@
+"""Seeded fuzz of PegaEngine's save and load by hash on the GPU.
+
+Each seed builds an engine with a source instance and a target instance in
+one namespace (random layer count, layout and segment size, some segment
+sizes not 16-byte multiples), then runs a random sequence of calls, each in
+transfer modes drawn at random:
+- saves of a random subset of layers, each layer with a list of its own or
+  all sharing one, naming negative ids, hashes named twice, hashes sealed
+  before and hashes an earlier call left part-way in flight;
+- the source tensors refilled with new bits after every save, so a slot
+  that keeps an earlier copy shows it;
+- loads of random hashes into random targets of a random subset of layers,
+  with negative and repeated targets and plain or layered LoadStates; some
+  name a hash that is not sealed and must fail as a whole, writing nothing.
+
+After every load each target tensor is compared byte for byte with a model
+of the reference's rules:
+- save (lib.rs:553-782, storage.rs:457-514): negative ids are skipped; a
+  hash sealed before the call, or a slot already filled, is skipped; within
+  one layer's list the first occurrence of a hash fills its slot; a block
+  seals once every layer's slot has arrived;
+- load (lib.rs:957-1069): every hash must be sealed or the call fails;
+  negative ids are skipped; blocks are written in list order, so a target
+  named twice ends with the later block.
+At the end the engine's sealed and in-flight block counts must match the
+model's.
+"""
+
+import hashlib
+import random
+import sys
+
+import numpy as np
+import pytest
+
+from pegaflow_amd import _lib
+from pegaflow_amd.engine import PegaEngine
+from pegaflow_amd.load_state import PyLoadState
+from pegaflow_amd.runtime import DeviceBuffer
+
+pytestmark = pytest.mark.gpu
+MiB = 1 << 20
+
+LAYOUTS = ("kv_first", "kv_first_padded", "blocks_first")
+SEGMENT_BYTES = (512, 1040, 4096, 16384, 200)   # one K or V segment (KV-first)
+BLOCK_BYTES = (1024, 2080, 8192, 32768, 400)    # one whole block (blocks-first)
+MODES = ("kernel", "staged", "auto", "dma_batched", "dma_reference")
+NB = 48
+HASHES = 24
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+class Tensors:
+    """One instance's layers on device 0, registered with the engine."""
+
+    def __init__(self, engine, inst, n_layers, layout, seg, seed):
+        self.layout = layout
+        if layout == "blocks_first":
+            self.bpb, self.kv, self.segments = seg, 0, 1
+            self.size = NB * seg
+        else:
+            pad = 4096 if layout == "kv_first_padded" else 0
+            self.bpb, self.kv, self.segments = seg, NB * seg + pad, 2
+            self.size = self.kv + NB * seg
+        self.names = [f"layer.{l}" for l in range(n_layers)]
+        self.bufs = [DeviceBuffer(self.size) for _ in range(n_layers)]
+        self.refill(seed)
+        for name, b in zip(self.names, self.bufs):
+            engine.register_context_layer(inst, "fuzz", 0, name, b.ptr, self.size, NB, self.bpb,
+                                          self.kv, self.segments, 0, 1, n_layers)
+
+    def refill(self, seed):
+        for l, b in enumerate(self.bufs):
+            b.fill_random(seed * 1000 + l)
+
+    def download(self):
+        return [b.download() for b in self.bufs]
+
+    def slot(self, arr, b):
+        """The bytes a save copies for block b of one layer."""
+        s = self.bpb
+        if self.segments == 1:
+            return arr[b * s:(b + 1) * s].copy()
+        v = self.kv + b * s
+        return np.concatenate([arr[b * s:(b + 1) * s], arr[v:v + s]])
+
+    def put(self, arr, b, data):
+        """What a load of `data` into block b writes into one layer."""
+        s = self.bpb
+        if self.segments == 1:
+            arr[b * s:(b + 1) * s] = data
+        else:
+            v = self.kv + b * s
+            arr[b * s:(b + 1) * s] = data[:s]
+            arr[v:v + s] = data[s:]
+
+    def close(self):
+        for b in self.bufs:
+            b.close()
+
+
+def h(seed, j):
+    return hashlib.sha256(b"fuzz-%d-%d" % (seed, j)).digest()
+
+
+def rand_ids(rng, n):
+    return [-1 if rng.random() < 0.1 else rng.randrange(NB) for _ in range(n)]
+
+
+@pytest.mark.parametrize("seed", range(48))
+def test_engine_calls_vs_model(gpu, seed):
+    rng = random.Random(seed)
+    n_layers = rng.randint(1, 5)
+    layout = LAYOUTS[seed % len(LAYOUTS)]
+    seg = rng.choice(BLOCK_BYTES if layout == "blocks_first" else SEGMENT_BYTES)
+    say(f"[gpu] engine fuzz seed={seed}: {n_layers} layers, {layout}, {seg} B segments")
+    e = PegaEngine(pool_size=64 * MiB)
+    src = Tensors(e, "src", n_layers, layout, seg, seed=seed * 7 + 1)
+    dst = Tensors(e, "dst", n_layers, layout, seg, seed=seed * 7 + 2)
+    pool = [h(seed, j) for j in range(HASHES)]
+    sealed = {}     # hash -> per-layer slot bytes
+    inflight = {}   # hash -> {layer: slot bytes}
+    expect = dst.download()
+    calls = {"saves": 0, "loads": 0, "failed_loads": 0}
+    try:
+        for step in range(40):
+            save_mode, load_mode = rng.choice(MODES), rng.choice(MODES)
+            e.set_transfer_modes(_lib.MODE_NAMES[save_mode], _lib.MODE_NAMES[load_mode])
+            if rng.random() < 0.5 or not sealed:
+                # A save of a random subset of layers.
+                layers = rng.sample(range(n_layers), rng.randint(1, n_layers))
+                shared = rng.random() < 0.5
+                n = rng.randint(1, 12)
+                one = (rand_ids(rng, n), [rng.choice(pool) for _ in range(n)])
+                lists = {l: one if shared else (rand_ids(rng, n), [rng.choice(pool)
+                                                                   for _ in range(n)])
+                         for l in layers}
+                host = src.download()
+                fresh = {}
+                for l in layers:
+                    ids, hashes = lists[l]
+                    named = set()
+                    for b, k in zip(ids, hashes):
+                        if b < 0 or k in sealed or k in named:
+                            continue
+                        named.add(k)
+                        if l in inflight.get(k, {}):
+                            continue
+                        fresh.setdefault(k, {})[l] = src.slot(host[l], b)
+                for k, slots in fresh.items():
+                    inflight.setdefault(k, {}).update(slots)
+                    if len(inflight[k]) == n_layers:
+                        sealed[k] = [inflight[k][l] for l in range(n_layers)]
+                        del inflight[k]
+                e.batch_save_kv_blocks("src", 0, 0, [(src.names[l], lists[l][0], lists[l][1])
+                                                     for l in layers])
+                src.refill(seed * 7 + 100 + step)
+                calls["saves"] += 1
+                continue
+            # A load of a random subset of layers.
+            names_idx = rng.sample(range(n_layers), rng.randint(1, n_layers))
+            n = rng.randint(1, 10)
+            known = list(sealed)
+            hashes = [rng.choice(known) for _ in range(n)]
+            missing = rng.random() < 0.15 and len(sealed) < HASHES
+            if missing:
+                hashes[rng.randrange(n)] = rng.choice([k for k in pool if k not in sealed])
+            targets = rand_ids(rng, n)
+            layered = rng.random() < 0.5
+            st = PyLoadState(num_layers=len(names_idx)) if layered else PyLoadState()
+            names = [dst.names[l] for l in names_idx]
+            try:
+                e.batch_load_kv_blocks("dst", 0, 0, st.shm_name(), names, targets, hashes)
+                raised = None
+            except _lib.PegaFlowError as err:
+                raised = err
+            if missing:
+                assert raised is not None and "missing KV block hash" in str(raised), raised
+                assert st.get_state() == -1
+                calls["failed_loads"] += 1
+            else:
+                assert raised is None, raised
+                e.wait_idle()
+                assert st.is_ready() and st.get_state() == 1
+                if layered:
+                    assert st.layers_done() == len(names_idx)
+                for l in names_idx:
+                    for t, k in zip(targets, hashes):
+                        if t >= 0:
+                            dst.put(expect[l], t, sealed[k][l])
+                calls["loads"] += 1
+            got = dst.download()
+            for l in range(n_layers):
+                assert np.array_equal(got[l], expect[l]), (
+                    f"step {step}: layer {l} differs after a load in {load_mode} mode "
+                    f"(targets {targets})")
+        s = e.stats()
+        say(f"[gpu] engine fuzz seed={seed}: {calls}, model {len(sealed)} sealed / "
+            f"{len(inflight)} in flight; engine {s['sealed_blocks']} / {s['inflight_blocks']}")
+        assert s["sealed_blocks"] == len(sealed) and s["inflight_blocks"] == len(inflight), s
+        assert s["evicted_blocks"] == 0 and s["load_failures"] == 0, s
+    finally:
+        e.close()
+        src.close()
+        dst.close()
