@@ -2,8 +2,10 @@
 
 Each seed builds an engine with a source instance and a target instance in
 one namespace (random layer count, layout and segment size, some segment
-sizes not 16-byte multiples), then runs a random sequence of calls, each in
-transfer modes drawn at random:
+sizes not 16-byte multiples; a third of the seeds with two tensor-parallel
+ranks, registered on the one device with the same tensors), then runs a
+random sequence of calls, each by a random rank and in transfer modes drawn
+at random:
 - saves of a random subset of layers, each layer with a list of its own or
   all sharing one, naming negative ids, hashes named twice, hashes sealed
   before and hashes an earlier call left part-way in flight;
@@ -18,10 +20,10 @@ of the reference's rules:
 - save (lib.rs:553-782, storage.rs:457-514): negative ids are skipped; a
   hash sealed before the call, or a slot already filled, is skipped; within
   one layer's list the first occurrence of a hash fills its slot; a block
-  seals once every layer's slot has arrived;
+  seals once the slot of every layer and rank has arrived;
 - load (lib.rs:957-1069): every hash must be sealed or the call fails;
-  negative ids are skipped; blocks are written in list order, so a target
-  named twice ends with the later block.
+  negative ids are skipped; a rank loads its own slots; blocks are written
+  in list order, so a target named twice ends with the later block.
 At the end the engine's sealed and in-flight block counts must match the
 model's.
 """
@@ -57,7 +59,7 @@ def say(*a):
 class Tensors:
     """One instance's layers on device 0, registered with the engine."""
 
-    def __init__(self, engine, inst, n_layers, layout, seg, seed):
+    def __init__(self, engine, inst, n_layers, layout, seg, seed, tp):
         self.layout = layout
         if layout == "blocks_first":
             self.bpb, self.kv, self.segments = seg, 0, 1
@@ -69,9 +71,12 @@ class Tensors:
         self.names = [f"layer.{l}" for l in range(n_layers)]
         self.bufs = [DeviceBuffer(self.size) for _ in range(n_layers)]
         self.refill(seed)
-        for name, b in zip(self.names, self.bufs):
-            engine.register_context_layer(inst, "fuzz", 0, name, b.ptr, self.size, NB, self.bpb,
-                                          self.kv, self.segments, 0, 1, n_layers)
+        # Every rank registers the same tensors: one device holds one
+        # registration per layer name (the last), as in the reference.
+        for rank in range(tp):
+            for name, b in zip(self.names, self.bufs):
+                engine.register_context_layer(inst, "fuzz", 0, name, b.ptr, self.size, NB,
+                                              self.bpb, self.kv, self.segments, rank, tp, n_layers)
 
     def refill(self, seed):
         for l, b in enumerate(self.bufs):
@@ -111,25 +116,27 @@ def rand_ids(rng, n):
     return [-1 if rng.random() < 0.1 else rng.randrange(NB) for _ in range(n)]
 
 
-@pytest.mark.parametrize("seed", range(48))
+@pytest.mark.parametrize("seed", range(72))
 def test_engine_calls_vs_model(gpu, seed):
     rng = random.Random(seed)
     n_layers = rng.randint(1, 5)
+    tp = 2 if seed >= 48 else 1
     layout = LAYOUTS[seed % len(LAYOUTS)]
     seg = rng.choice(BLOCK_BYTES if layout == "blocks_first" else SEGMENT_BYTES)
-    say(f"[gpu] engine fuzz seed={seed}: {n_layers} layers, {layout}, {seg} B segments")
+    say(f"[gpu] engine fuzz seed={seed}: {n_layers} layers, tp {tp}, {layout}, {seg} B segments")
     e = PegaEngine(pool_size=64 * MiB)
-    src = Tensors(e, "src", n_layers, layout, seg, seed=seed * 7 + 1)
-    dst = Tensors(e, "dst", n_layers, layout, seg, seed=seed * 7 + 2)
+    src = Tensors(e, "src", n_layers, layout, seg, seed * 7 + 1, tp)
+    dst = Tensors(e, "dst", n_layers, layout, seg, seed * 7 + 2, tp)
     pool = [h(seed, j) for j in range(HASHES)]
-    sealed = {}     # hash -> per-layer slot bytes
-    inflight = {}   # hash -> {layer: slot bytes}
+    sealed = {}     # hash -> {(layer, rank): slot bytes}
+    inflight = {}   # hash -> {(layer, rank): slot bytes}
     expect = dst.download()
     calls = {"saves": 0, "loads": 0, "failed_loads": 0}
     try:
         for step in range(40):
             save_mode, load_mode = rng.choice(MODES), rng.choice(MODES)
             e.set_transfer_modes(_lib.MODE_NAMES[save_mode], _lib.MODE_NAMES[load_mode])
+            rank = rng.randrange(tp)
             if rng.random() < 0.5 or not sealed:
                 # A save of a random subset of layers.
                 layers = rng.sample(range(n_layers), rng.randint(1, n_layers))
@@ -148,16 +155,15 @@ def test_engine_calls_vs_model(gpu, seed):
                         if b < 0 or k in sealed or k in named:
                             continue
                         named.add(k)
-                        if l in inflight.get(k, {}):
+                        if (l, rank) in inflight.get(k, {}):
                             continue
-                        fresh.setdefault(k, {})[l] = src.slot(host[l], b)
+                        fresh.setdefault(k, {})[(l, rank)] = src.slot(host[l], b)
                 for k, slots in fresh.items():
                     inflight.setdefault(k, {}).update(slots)
-                    if len(inflight[k]) == n_layers:
-                        sealed[k] = [inflight[k][l] for l in range(n_layers)]
-                        del inflight[k]
-                e.batch_save_kv_blocks("src", 0, 0, [(src.names[l], lists[l][0], lists[l][1])
-                                                     for l in layers])
+                    if len(inflight[k]) == n_layers * tp:
+                        sealed[k] = inflight.pop(k)
+                e.batch_save_kv_blocks("src", rank, 0, [(src.names[l], lists[l][0], lists[l][1])
+                                                        for l in layers])
                 src.refill(seed * 7 + 100 + step)
                 calls["saves"] += 1
                 continue
@@ -174,7 +180,7 @@ def test_engine_calls_vs_model(gpu, seed):
             st = PyLoadState(num_layers=len(names_idx)) if layered else PyLoadState()
             names = [dst.names[l] for l in names_idx]
             try:
-                e.batch_load_kv_blocks("dst", 0, 0, st.shm_name(), names, targets, hashes)
+                e.batch_load_kv_blocks("dst", rank, 0, st.shm_name(), names, targets, hashes)
                 raised = None
             except _lib.PegaFlowError as err:
                 raised = err
@@ -191,7 +197,7 @@ def test_engine_calls_vs_model(gpu, seed):
                 for l in names_idx:
                     for t, k in zip(targets, hashes):
                         if t >= 0:
-                            dst.put(expect[l], t, sealed[k][l])
+                            dst.put(expect[l], t, sealed[k][(l, rank)])
                 calls["loads"] += 1
             got = dst.download()
             for l in range(n_layers):
