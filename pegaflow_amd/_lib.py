@@ -328,7 +328,8 @@ SIGNATURES = {
                                                u64, u64, u64, u64]),
     "pf_engine_unregister_instance": (i32, [vp, cs]),
     "pf_engine_count_prefix_hit_blocks": (i32, [vp, cs, vp, vp, u64, pu64]),
-    "pf_engine_batch_save": (i32, [vp, cs, u64, i32, ctypes.POINTER(SaveLayer), u32]),
+    # The layers: the address of a pf_save_layer array (SaveLayer's layout).
+    "pf_engine_batch_save": (i32, [vp, cs, u64, i32, vp, u32]),
     "pf_engine_batch_load": (i32, [vp, cs, u64, i32, cs, ctypes.POINTER(cs), u32, vp, vp, vp,
                                    u64]),
     "pf_engine_serve_request": (i32, [vp, u32, ctypes.c_char_p, u64]),

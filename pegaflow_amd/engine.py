@@ -10,13 +10,14 @@ point the reference exposes only through its gRPC service
 
 from __future__ import annotations
 
+import array
 import ctypes
 from typing import Iterable, Sequence
 
 import numpy as np
 
 from . import _lib
-from ._lib import DiskStats, EngineStats, PegaFlowError, PrefetchStatus, SaveLayer
+from ._lib import DiskStats, EngineStats, PegaFlowError, PrefetchStatus
 
 DEFAULT_PINNED_POOL_BYTES = 30 * 1024 * 1024 * 1024  # lib.rs:56
 DEFAULT_DISK_QUOTA_BYTES = 50 * 1024 * 1024 * 1024  # pegaflow-server/src/lib.rs:106-108
@@ -35,11 +36,23 @@ def _raise(rc: int) -> None:
 def _hashes(block_hashes: Sequence[bytes]):
     """(bytes, offsets): hash i is data[offs[i]:offs[i+1]]."""
     n = len(block_hashes)
+    data = np.frombuffer(b"".join(block_hashes) or b"\0", np.uint8)
+    lengths = set(map(len, block_hashes))
+    if len(lengths) == 1 and (step := lengths.pop()) > 0:  # the usual case: one length
+        return data, np.arange(0, (n + 1) * step, step, dtype=np.uint64)
     offs = np.zeros(n + 1, np.uint64)
     if n:
         np.cumsum(np.fromiter(map(len, block_hashes), np.uint64, n), out=offs[1:])
-    data = np.frombuffer(b"".join(block_hashes) or b"\0", np.uint8)
     return data, offs
+
+
+def _block_ids(block_ids: Sequence[int]):
+    """(keep-alive object, address, count) of block_ids as int32."""
+    if isinstance(block_ids, np.ndarray):
+        ids = np.ascontiguousarray(block_ids, dtype=np.int32)
+        return ids, ids.ctypes.data, len(ids)
+    ids = array.array("i", block_ids)  # C int: 32 bits on this platform
+    return ids, ids.buffer_info()[0], len(ids)
 
 
 class ScaledOffsetAllocator:
@@ -106,6 +119,7 @@ class PegaEngine:
                                       ctypes.byref(h)))
         self._h = h.value
         self._name_arrays = {}  # tuple of layer names -> C array of their bytes
+        self._save_names = {}   # layer name -> (its bytes, their address)
 
     def set_storage_policy(self, lfu_admission: bool = False, value_size_hint: int = 0,
                            pre_evict: bool = False, pre_evict_threshold: int = 5 << 30,
@@ -154,16 +168,20 @@ class PegaEngine:
                              saves: Iterable[tuple[str, Sequence[int], Sequence[bytes]]]) -> None:
         """Blocking save of (layer_name, block_ids, block_hashes) per layer.
         Lists shared by several layers (the usual case) are packed once."""
-        keep, arr = [], []
+        keep, words = [], []
         # Each list packed once, with its address (numpy's ctypes.data costs
         # microseconds per access: 96 of them were 0.2 ms of a 32-layer save).
+        # The pf_save_layer array is built as its 64-bit words (name, ids,
+        # count, hash bytes, hash offsets): one ctypes structure per layer
+        # cost more than the rest of a 32-layer save's marshalling.
         packed_ids, packed_hashes = {}, {}
+        names = self._save_names
+        n_layers = 0
         for layer_name, block_ids, block_hashes in saves:
             pi = packed_ids.get(id(block_ids))
             if pi is None:
-                ids = np.ascontiguousarray(block_ids, dtype=np.int32)
-                pi = packed_ids[id(block_ids)] = (ids, ids.ctypes.data, len(ids))
-                keep += [block_ids, ids]  # keeps id() unique for the whole call
+                pi = packed_ids[id(block_ids)] = _block_ids(block_ids)
+                keep += [block_ids, pi[0]]  # keeps id() unique for the whole call
             _, ids_ptr, n_ids = pi
             if n_ids != len(block_hashes):
                 raise PegaFlowError(_lib.PF_ERR_INVALID_ARGUMENT,
@@ -174,12 +192,19 @@ class PegaEngine:
                 data, offs = _hashes(block_hashes)
                 hp = packed_hashes[id(block_hashes)] = (data.ctypes.data, offs.ctypes.data)
                 keep += [block_hashes, data, offs]
-            name = layer_name.encode()
-            keep.append(name)
-            arr.append(SaveLayer(name, ids_ptr, n_ids, hp[0], hp[1]))
-        c_arr = (SaveLayer * max(len(arr), 1))(*arr)
+            name = names.get(layer_name)
+            if name is None:
+                if len(names) >= 4096:
+                    names.clear()
+                b = layer_name.encode()
+                name = names[layer_name] = (b, ctypes.cast(ctypes.c_char_p(b),
+                                                           ctypes.c_void_p).value)
+            keep.append(name[0])
+            words += (name[1], ids_ptr, n_ids, hp[0], hp[1])
+            n_layers += 1
+        c_arr = array.array("Q", words or [0] * 5)
         _raise(lib().pf_engine_batch_save(self._h, instance_id.encode(), tp_rank, device_id,
-                                          c_arr, len(arr)))
+                                          c_arr.buffer_info()[0], n_layers))
         del keep
 
     def batch_load_kv_blocks(self, instance_id: str, tp_rank: int, device_id: int,

@@ -3,11 +3,14 @@ reference's allocator.rs tests plus a model check) and the engine's
 registration / validation / lookup rules (lib.rs:303-484, 803-838) on an
 engine whose pool is plain host memory."""
 
+import ctypes
+
+import numpy as np
 import pytest
 from hypothesis import given, settings, strategies as st
 
 from pegaflow_amd import _lib
-from pegaflow_amd.engine import PegaEngine, ScaledOffsetAllocator
+from pegaflow_amd.engine import PegaEngine, ScaledOffsetAllocator, _block_ids, _hashes
 from pegaflow_amd.load_state import PyLoadState
 
 GiB = 1 << 30
@@ -154,6 +157,40 @@ def test_save_errors_before_any_transfer(engine):
         engine.batch_save_kv_blocks("i0", 0, 0, [("l0", [1], [b"h"])])
     assert ei.value.code == _lib.PF_ERR_UNSUPPORTED
     assert engine.stats()["pool_used_bytes"] == 0  # the failed save released its regions
+
+
+def test_save_marshalling(engine):
+    """A save's layer array is built as pf_save_layer's 64-bit words: each
+    layer reaches the engine with its own name, ids and hashes (the errors
+    name the second layer), from lists or numpy ids; hashes of one length
+    get arithmetic offsets, mixed lengths their running sums."""
+    assert ctypes.sizeof(_lib.SaveLayer) == 40
+    assert [getattr(_lib.SaveLayer, f).offset for f, _ in _lib.SaveLayer._fields_] == \
+        [0, 8, 16, 24, 32]
+    data, offs = _hashes([b"ab", b"cd", b"ef"])
+    assert bytes(data) == b"abcdef" and offs.tolist() == [0, 2, 4, 6]
+    data, offs = _hashes([b"a", b"bcd", b""])
+    assert bytes(data) == b"abcd" and offs.tolist() == [0, 1, 4, 4]
+    data, offs = _hashes([b"", b""])
+    assert offs.tolist() == [0, 0, 0]
+    data, offs = _hashes([])
+    assert offs.tolist() == [0]
+    for ids in ([3, -1, 7], np.array([3, -1, 7], np.int64)):
+        keep, addr, n = _block_ids(ids)
+        assert n == 3 and (ctypes.c_int32 * 3).from_address(addr)[:] == [3, -1, 7]
+    reg(engine, "l0")
+    reg(engine, "l1")
+    with pytest.raises(RuntimeError, match="block 17 out of range for layer l1"):
+        engine.batch_save_kv_blocks("i0", 0, 0, [("l0", [-1], [b"h"]),
+                                                 ("l1", np.array([17]), [b"hh"])])
+    with pytest.raises(RuntimeError, match="layer zz unknown"):
+        engine.batch_save_kv_blocks("i0", 0, 0, [("l0", [-1, -2], [b"a", b"bcd"]),
+                                                 ("zz", [0], [b"h"])])
+    # Negative ids only, hashes of mixed lengths, and an empty batch: no copy.
+    engine.batch_save_kv_blocks("i0", 0, 0, [("l0", np.array([-1, -2]), [b"a", b"bcd"]),
+                                             ("l1", [-3], [b"xyz"])])
+    engine.batch_save_kv_blocks("i0", 0, 0, [])
+    assert engine.stats()["pool_used_bytes"] == 0
 
 
 def test_load_errors_set_the_load_state(engine):
