@@ -214,10 +214,10 @@ class PegaEngine:
         As in the reference (lib.rs:1008-1043), every hash is looked up and
         ids pair with hashes up to the shorter list: extra hashes get id -1
         (skipped), extra ids are dropped."""
-        ids = np.ascontiguousarray(block_ids, dtype=np.int32)
-        if len(ids) != len(block_hashes):
-            ids = np.concatenate([ids[:len(block_hashes)],
-                                  np.full(max(0, len(block_hashes) - len(ids)), -1, np.int32)])
+        count = len(block_hashes)
+        if len(block_ids) != count:
+            block_ids = list(block_ids)[:count] + [-1] * max(0, count - len(block_ids))
+        ids, ids_ptr, _ = _block_ids(block_ids)
         data, offs = _hashes(block_hashes)
         # A connector names the same layers on every load: their C array is
         # built once (the bytes objects it points into are kept with it).
@@ -232,7 +232,8 @@ class PegaEngine:
             self._name_arrays[key] = c_names
         _raise(lib().pf_engine_batch_load(
             self._h, instance_id.encode(), tp_rank, device_id, load_state_shm.encode(), c_names,
-            len(key), ids.ctypes.data, data.ctypes.data, offs.ctypes.data, len(ids)))
+            len(key), ids_ptr, data.ctypes.data, offs.ctypes.data, count))
+        del ids
 
     # -- disk tier (seal_offload.rs) -------------------------------------
     def enable_disk(self, root: str, quota_bytes: int = DEFAULT_DISK_QUOTA_BYTES,

@@ -269,6 +269,39 @@ def test_save_requests_share_repeated_lists(engine):
     m.close()
 
 
+def test_load_pairs_ids_with_hashes_up_to_the_shorter_list(engine):
+    """lib.rs:1008-1043 pairs ids with hashes as zip does: extra hashes get no
+    target, extra ids are dropped; every hash is still looked up, so an
+    unpaired hash must be sealed too."""
+    say("[gpu] engine load pairs ids and hashes up to the shorter list")
+    m = Model(engine, "zip", 2, 32, 2048, seed=21)
+    orig = m.host_copies()
+    ids = [3, 7, 12, 20]
+    hashes = [h(i, b"zip") for i in ids]
+    engine.batch_save_kv_blocks("zip", 0, 0, [(n, ids, hashes) for n in m.names])
+    st = PyLoadState()  # two targets for four hashes
+    engine.batch_load_kv_blocks("zip", 0, 0, st.shm_name(), m.names, [30, 31], hashes)
+    assert wait(st) == 1
+    exp = _expect_per_layer(m, orig, [([3, 7], [30, 31])] * m.n_layers)
+    for l in range(m.n_layers):
+        assert np.array_equal(m.bufs[l].download(), exp[l]), f"layer {l}"
+    st = PyLoadState()  # four targets for two hashes
+    engine.batch_load_kv_blocks("zip", 0, 0, st.shm_name(), m.names, [28, 29, 0, 1],
+                                hashes[2:])
+    assert wait(st) == 1
+    exp = _expect_per_layer(m, exp, [([12, 20], [28, 29])] * m.n_layers)
+    for l in range(m.n_layers):
+        assert np.array_equal(m.bufs[l].download(), exp[l]), f"layer {l}"
+    st = PyLoadState()
+    with pytest.raises(RuntimeError, match="missing KV block hash at index 1"):
+        engine.batch_load_kv_blocks("zip", 0, 0, st.shm_name(), m.names, [30],
+                                    [hashes[0], h(99, b"zip")])
+    assert st.get_state() == -1
+    for l in range(m.n_layers):
+        assert np.array_equal(m.bufs[l].download(), exp[l]), f"layer {l} written by a failed load"
+    m.close()
+
+
 def test_load_missing_hash_fails_whole_call(engine):
     say("[gpu] engine load with a missing hash")
     m = Model(engine, "inst", 2, 16, 1024)
