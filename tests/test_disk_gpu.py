@@ -41,11 +41,16 @@ def wait(st, timeout=60.0):
 
 
 class Layers:
-    """n_layers x tp_size KV-first layers on device 0 (slot = layer*tp + rank)."""
+    """n_layers x tp_size layers on device 0 (slot = layer*tp + rank):
+    KV-first (two segments of bpb bytes per block) or blocks-first (one
+    segment of bpb bytes, packed whole)."""
 
-    def __init__(self, n_layers, tp, nb, bpb, seed):
+    def __init__(self, n_layers, tp, nb, bpb, seed, segments=2):
         self.n_layers, self.tp, self.nb, self.bpb = n_layers, tp, nb, bpb
-        self.kv, self.size = nb * bpb, 2 * nb * bpb
+        self.segments = segments
+        self.kv = nb * bpb if segments == 2 else 0
+        self.size = nb * bpb * segments
+        self.slot_bytes = bpb * segments
         self.names = [f"model.layers.{l}.self_attn" for l in range(n_layers)]
         self.bufs = {(l, r): DeviceBuffer(self.size) for l in range(n_layers) for r in range(tp)}
         self.fill(seed)
@@ -62,7 +67,8 @@ class Layers:
         for l in range(self.n_layers):
             b = self.bufs[(l, rank)]
             engine.register_context_layer(inst, ns, 0, self.names[l], b.ptr, self.size, self.nb,
-                                          self.bpb, self.kv, 2, rank, self.tp, self.n_layers)
+                                          self.bpb, self.kv, self.segments, rank, self.tp,
+                                          self.n_layers)
 
     def host(self):
         return {k: b.download() for k, b in self.bufs.items()}
@@ -71,12 +77,15 @@ class Layers:
         """Per block: the (K, V) of every slot, from the oracle's save path."""
         per = {}
         m = len(ids)
+        split = self.segments == 2
         for key, buf in host.items():
             buf = buf.copy()
-            reg = oracle.layout(buf.ctypes.data, self.size, self.nb, self.bpb, self.kv, 2)
-            region = np.zeros(2 * m * self.bpb, np.uint8)
-            k, v, _ = oracle.save_host_layout(reg, m, region.ctypes.data,
-                                              region.ctypes.data + m * self.bpb)
+            reg = oracle.layout(buf.ctypes.data, self.size, self.nb, self.bpb, self.kv,
+                                self.segments)
+            region = np.zeros(m * self.slot_bytes, np.uint8)
+            k, v, is_split = oracle.save_host_layout(reg, m, region.ctypes.data,
+                                                     region.ctypes.data + m * self.bpb)
+            assert is_split == split
             oracle.process_save(reg, buf, ids, k, v)
             per[key] = region
         out = []
@@ -86,7 +95,8 @@ class Layers:
                 for r in range(self.tp):
                     reg_ = per[(l, r)]
                     slots.append((reg_[j * self.bpb:(j + 1) * self.bpb].tobytes(),
-                                  reg_[(m + j) * self.bpb:(m + j + 1) * self.bpb].tobytes()))
+                                  reg_[(m + j) * self.bpb:(m + j + 1) * self.bpb].tobytes()
+                                  if split else None))
             out.append(slots)
         return out
 
@@ -95,12 +105,14 @@ class Layers:
         m = len(ids)
         for key in self.bufs:
             src, dst = before[key].copy(), clobbered[key].copy()
-            region = np.zeros(2 * m * self.bpb, np.uint8)
-            reg_s = oracle.layout(src.ctypes.data, self.size, self.nb, self.bpb, self.kv, 2)
+            region = np.zeros(m * self.slot_bytes, np.uint8)
+            reg_s = oracle.layout(src.ctypes.data, self.size, self.nb, self.bpb, self.kv,
+                                  self.segments)
             k, v, _ = oracle.save_host_layout(reg_s, m, region.ctypes.data,
                                               region.ctypes.data + m * self.bpb)
             oracle.process_save(reg_s, src, ids, k, v)
-            reg_d = oracle.layout(dst.ctypes.data, self.size, self.nb, self.bpb, self.kv, 2)
+            reg_d = oracle.layout(dst.ctypes.data, self.size, self.nb, self.bpb, self.kv,
+                                  self.segments)
             oracle.process_load(reg_d, dst, targets, k, v)
             out[key] = dst
         return out
@@ -137,11 +149,13 @@ def check_files(root, ns, hashes, want_slots):
     assert seen == set(range(len(hashes)))
 
 
-@pytest.mark.parametrize("tp", [1, 2])
-def test_offload_restart_prefetch_load(gpu, tmp_path, tp):
-    say(f"[gpu] disk tier offload -> restart -> prefetch -> load tp={tp}")
+@pytest.mark.parametrize("tp,segments", [(1, 2), (2, 2), (1, 1)],
+                         ids=["kv_first-tp1", "kv_first-tp2", "blocks_first-tp1"])
+def test_offload_restart_prefetch_load(gpu, tmp_path, tp, segments):
+    say(f"[gpu] disk tier offload -> restart -> prefetch -> load tp={tp} segments={segments}")
     root = str(tmp_path / "pega")
-    layers = Layers(4, tp, 64, 4096, seed=17 + tp)
+    layers = Layers(4, tp, 64, 4096 * (3 - segments), seed=17 + tp + (10 if segments == 1 else 0),
+                    segments=segments)
     ids = [5, 17, 3, 60, 41, 8, 9, 10, 11, 12]
     hashes = [h(i + 100 * tp) for i in ids]
     try:
@@ -153,7 +167,7 @@ def test_offload_restart_prefetch_load(gpu, tmp_path, tp):
             e1.batch_save_kv_blocks("inst", r, 0, [(n, ids, hashes) for n in layers.names])
         e1.flush_disk()
         s = e1.disk_stats()
-        slot_bytes = 2 * layers.bpb
+        slot_bytes = layers.slot_bytes
         assert s["offloaded_blocks"] == len(ids) and s["failures"] == 0
         assert s["written_bytes"] == len(ids) * 4 * tp * slot_bytes == s["bytes"]
         assert s["files"] >= 3  # at most 4 blocks per file
